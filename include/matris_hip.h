@@ -1,0 +1,163 @@
+/*
+ * matris_hip.h -- C ABI of the MI355X (gfx950) MatRIS efsm hot path.
+ *
+ * Library: matris_amd/csrc/libmatris_hip.so (hipcc --offload-arch=gfx950).
+ *
+ * Conventions (every entry point):
+ *   - returns 0 on success, a hipError_t value (> 0) on a HIP failure, or a negative
+ *     MATRIS_E_* code when an argument is rejected before any launch;
+ *   - all array pointers are DEVICE pointers unless the parameter name ends in `_host`;
+ *   - nothing here allocates or frees device memory: callers pass outputs and, where
+ *     stated, a workspace of the size the matching *_workspace_bytes() call returns;
+ *   - kernels are enqueued on `stream` (a hipStream_t) and are not synchronised;
+ *   - feature rows are fp32, 128 wide, row-major and contiguous unless a leading
+ *     dimension is given; graph indices are int32.
+ *
+ * Each declaration names the reference interface it replaces (paths relative to the
+ * HPC-AI-Team/MatRIS tree).
+ */
+#ifndef MATRIS_HIP_H
+#define MATRIS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MATRIS_E_ARG (-1001)       /* invalid size / pointer argument            */
+#define MATRIS_E_CAPACITY (-1002)  /* per-atom neighbour capacity exceeded        */
+#define MATRIS_E_IMAGES (-1003)    /* periodic image range beyond +-511           */
+#define MATRIS_E_UNPAIRED (-1004)  /* a directed edge has no reverse partner      */
+#define MATRIS_E_ORDER (-1005)     /* edges not in canonical (center, neighbor, image) order */
+
+/* Library version / build identification (for tests: "is the HIP path loaded"). */
+const char *matris_version(void);
+
+/* ------------------------------------------------------------------------------------
+ * Graph construction (rows G1-G5)
+ * ------------------------------------------------------------------------------------ */
+
+/* G1: periodic radius graph.  Replaces pymatgen Structure.get_neighbor_list(r, sites,
+ * numerical_tol) as called at matris/graph/converter.py:85-87.  Edges (i, j, n) with
+ * tol < |r_j + n.L - r_i| <= cutoff, emitted in canonical order (i, j, n0, n1, n2
+ * ascending), all decisions in fp64 with a fixed evaluation order.
+ * The structure is periodic along all three axes (a pymatgen Structure always is; the
+ * calculator pads non-periodic axes, matris/applications/base.py:70-93).
+ * Two phases: count (per-atom counts and their exclusive scan row_ptr[n+1]) then fill.
+ *   frac [n,3] fp64 (device); lattice_host [3][3] fp64, rows are lattice vectors;
+ *   grid_host[3] = cells per axis, search_host[3] = cell reach per axis (from
+ *   matris_radius_graph_plan); workspace of matris_radius_graph_workspace_bytes(). */
+int matris_radius_graph_plan(const double *lattice_host, double cutoff, int *grid_host, int *search_host);
+size_t matris_radius_graph_workspace_bytes(int64_t n, const int *grid_host);
+int matris_radius_graph_count(int64_t n, const double *frac, const double *lattice_host, double cutoff, double tol,
+                              const int *grid_host, const int *search_host, int32_t *row_count, int64_t *row_ptr,
+                              void *workspace, size_t workspace_bytes, void *stream);
+int matris_radius_graph_fill(int64_t n, const double *lattice_host, double cutoff, double tol, const int *grid_host,
+                             const int *search_host, const int64_t *row_ptr, int32_t *center, int32_t *neighbor,
+                             int32_t *image, double *dist, void *workspace, size_t workspace_bytes, void *stream);
+
+/* G3/G4: directed -> undirected pairing.  Replaces create_graph()
+ * (matris/graph/fast_converter_libraries/create_graph.c:100-219) and the Python
+ * Graph.add_edge / adjacency_list / undirected2directed (matris/graph/radiusgraph.py:
+ * 298-410, 489-496) for edge lists in canonical order (as emitted by G1; checked).
+ * Outputs: rev[E] (index of the reverse edge), d2u[E], u2d[E_u] (first directed edge),
+ * u_second[E_u] (second directed edge); *n_undirected_host receives E_u (one readback).
+ * workspace: matris_pair_edges_workspace_bytes(E). */
+size_t matris_pair_edges_workspace_bytes(int64_t n_edges);
+int matris_pair_edges(int64_t n_atoms, int64_t n_edges, const int32_t *center, const int32_t *neighbor,
+                      const int32_t *image, const int64_t *row_ptr, int32_t *rev, int32_t *d2u, int32_t *u2d,
+                      int32_t *u_second, int64_t *n_undirected_host, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* G5: bond -> angle line graph.  Replaces Graph.line_graph_adjacency_list(cutoff)
+ * (matris/graph/radiusgraph.py:412-487): bonds with length <= cutoff (inclusive) as
+ * first bond, partners with length < cutoff (strict), rows [center, u1, DE1, u2, DE2].
+ * angle_ptr[E_u+1] is the exclusive scan of per-bond angle counts, i.e. the CSR of the
+ * angles grouped by u1 (rows are emitted sorted by u1).
+ * count: fills angle_ptr and *n_angles_host (one readback).  fill: writes line_graph. */
+size_t matris_line_graph_workspace_bytes(int64_t n_atoms, int64_t n_undirected);
+int matris_line_graph_count(int64_t n_atoms, int64_t n_edges, int64_t n_undirected, const int32_t *center,
+                            const int32_t *neighbor, const double *dist, const int64_t *row_ptr,
+                            const int32_t *u2d, const int32_t *u_second, double cutoff, int32_t *angle_ptr,
+                            int64_t *n_angles_host, void *workspace, size_t workspace_bytes, void *stream);
+int matris_line_graph_fill(int64_t n_atoms, int64_t n_edges, int64_t n_undirected, const int32_t *center,
+                           const int32_t *neighbor, const double *dist, const int64_t *row_ptr,
+                           const int32_t *d2u, const int32_t *u2d, const int32_t *u_second, double cutoff,
+                           const int32_t *angle_ptr, int32_t *line_graph, void *stream);
+
+/* CSR of rows grouped by an int32 key (stable: rows ascending within each segment).
+ * Used for every gather's backward (the deterministic replacement of index_add_,
+ * matris/model/functions.py:156-157) and for the source side of the segment softmax
+ * (functions.py:110-123).  keys may be strided (key of row r = keys[r * key_stride]).
+ * workspace: matris_csr_workspace_bytes(n_rows, n_segments). */
+size_t matris_csr_workspace_bytes(int64_t n_rows, int64_t n_segments);
+int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t n_segments,
+                     int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------------------
+ * Segmented reductions and gathers (row M3)
+ * ------------------------------------------------------------------------------------ */
+
+/* out[s, :] = (accumulate ? out[s, :] : 0) + scale * sum_{i in [rowptr[s], rowptr[s+1])}
+ *             x[(perm ? perm[i] : i) * ldx + col_off + :128]
+ * Replaces aggregate() / GraphPooling (matris/model/functions.py:129-160, 340-365):
+ * index_add_ with average=False (scale 1) or the d2u mean (scale 0.5), summed in
+ * CSR order -- deterministic, no atomics. */
+int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *rowptr, const int32_t *perm,
+                   int64_t n_seg, float scale, int accumulate, float *out, void *stream);
+
+/* out[r, :] = (accumulate ? out[r, :] : 0) + scale * src[idx ? idx[r] : r, :]
+ * torch.index_select(x, 0, idx) (interaction_block.py:96-100) and the backward of a
+ * segment sum. */
+int matris_gather_rows(const float *src, const int32_t *idx, int64_t n_rows, float scale, int accumulate,
+                       float *out, void *stream);
+
+/* ------------------------------------------------------------------------------------
+ * Segment attention (rows M2 + M4 / M5): Dimwise_softmax by target and by source,
+ * alpha * e' and both segment sums, fused.  Replaces interaction_block.py:113-134 with
+ * functions.py:97-160.
+ *   alpha_t / alpha_s: logits, row r at (alpha_idx ? alpha_idx[r] : r) * lda;
+ *   e [R,128]; target CSR (t_ptr, t_perm|NULL), source CSR (s_ptr, s_perm|NULL),
+ *   both over n_seg segments.
+ * fwd writes y_t, y_s [n_seg,128] and the per-segment log-sum-exp lse_t, lse_s
+ * [n_seg,128] needed by the backward.
+ * bwd (input gradients only): given g_yt, g_ys, writes g_alpha_t, g_alpha_s [R,128]
+ * (per row r, before any alpha_idx reduction) and g_e [R,128];
+ * t_idx[R], s_idx[R] are the target / source segment of each row. */
+int matris_attn_fwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s, int64_t lda,
+                    const int32_t *alpha_idx, const float *e, const int32_t *t_ptr, const int32_t *t_perm,
+                    const int32_t *s_ptr, const int32_t *s_perm, float *y_t, float *y_s, float *lse_t,
+                    float *lse_s, void *stream);
+int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s, int64_t lda,
+                    const int32_t *alpha_idx, const float *e, const int32_t *t_idx, const int32_t *s_idx,
+                    const float *y_t, const float *y_s, const float *lse_t, const float *lse_s, const float *g_yt,
+                    const float *g_ys, float *g_alpha_t, float *g_alpha_s, float *g_e, void *stream);
+
+/* ------------------------------------------------------------------------------------
+ * Fused gated MLP on MFMA (row M1).  Replaces GatedMLP.forward
+ * (matris/model/functions.py:297-311) with its MLP / RMSNorm / FusedSiLU / FusedSigmoid
+ * parts (functions.py:163-242, 10-36; op/fused_silu_op.py; op/fuse_sigmoid_op.py) and
+ * the torch.cat of gathered rows that feeds it (interaction_block.py:96-107, 232-254).
+ *   input row m = concat_j src_j[(src_idx_j ? src_idx_j[m] : m), 0:128], j < n_src
+ *   (n_src in {1..4}, K = 128 n_src); src_host / src_idx_host are host arrays of n_src
+ *   device pointers (an index pointer may be NULL for the identity);
+ *   w1 [256, K] = [mlp_core.layers.0.weight; mlp_gate.layers.0.weight], b1 [256];
+ *   w2 [256, 128] = [mlp_core.layers.3.weight; mlp_gate.layers.3.weight], b2 [256];
+ *   norm_c / norm_g [128] = core_norm.weight / gate_norm.weight, RMSNorm eps.
+ * fwd writes out [M,128]; save_p / save_z [M,256] (layer-1 pre-activation and layer-2
+ * output, both halves) when non-NULL -- the backward needs them.
+ * bwd (input gradients only) reads g_out [M,128], p, z and the transposed weights
+ * w1t [K,256], w2t [128,256] (w2t[k][n] = w2[n][k]); writes g_x [M,K]. */
+int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
+                    const float *w1, const float *b1, const float *w2, const float *b2, const float *norm_c,
+                    const float *norm_g, float eps, float *out, float *save_p, float *save_z, void *stream);
+int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const float *w1t,
+                    const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MATRIS_HIP_H */

@@ -1,0 +1,385 @@
+// Fused gated MLP (GatedMLP with RMSNorm, SiLU core, sigmoid gate) on gfx950 MFMA.
+//
+//   x    = concat_j src_j[idx_j[m]]                         [BM, K]   (gathered on load)
+//   p    = x W1^T + b1                                      [BM, 256] (core | gate)
+//   h    = SiLU(p)
+//   z    = [h_c W2c^T + b2c | h_g W2g^T + b2g]              [BM, 256]
+//   out  = SiLU(RMS(z_c) * w_c) * sigmoid(RMS(z_g) * w_g)   [BM, 128]
+//
+// Work-group = 4 wave64s, BM = 64 rows.  GEMM1 streams K in 32-wide chunks through LDS
+// (X chunk gathered row by row, W1 chunk), register-prefetching the next chunk while
+// the current one feeds v_mfma_f32_32x32x2f32; each wave owns 64 output columns (a 2x2
+// grid of 32x32 tiles).  h never leaves LDS: GEMM2 reads it as the A operand, RMSNorm
+// reductions go through cross-lane shuffles plus a 64-row LDS exchange, and the
+// core * gate product is formed through LDS.  p and z are written for the backward.
+//
+// Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
+// from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
+// tiling, with the transposed weights as B operands.
+#include "common.h"
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+#define BM 64
+#define BK 32
+#define LDX 36   // LDS row stride (floats) of the X chunk
+#define LDW 36   // LDS row stride of the W1 chunk
+#define LDH 260  // LDS row stride of the [64, 256] h / gradient tiles
+
+struct GmlpSrc {
+    const float *ptr[4];
+    const int32_t *idx[4];
+};
+
+__device__ __forceinline__ v16f mfma32(float a, float b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigm_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float dsilu_f(float x) {
+    float s = sigm_f(x);
+    return s * (1.0f + x * (1.0f - s));
+}
+
+// Row of accumulator register i of a 32x32 tile for lane half h.
+__device__ __forceinline__ int acc_row(int i, int h) { return (i >> 2) * 8 + h * 4 + (i & 3); }
+
+// acc[rt][ct] += A[rt*32.., k] * B[k, ct*32..] for a 32-wide K chunk.  A rows are read
+// from LDS at a_base + row * lda; B columns are row n of a [n][k] array at
+// b_base + n * ldb (LDS or global).  Lane half h consumes columns 16h .. 16h+15.
+template <int NRT, int NCT>
+__device__ __forceinline__ void mfma_chunk(v16f (&acc)[NRT][NCT], const float *a_base, int lda, const float *b_base,
+                                           int ldb, int lane) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 a[NRT], b[NCT];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+            a[rt] = *reinterpret_cast<const float4 *>(a_base + (rt * 32 + l32) * lda + 16 * h + 4 * q);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+            b[ct] = *reinterpret_cast<const float4 *>(b_base + (int64_t)(ct * 32 + l32) * ldb + 16 * h + 4 * q);
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                acc[rt][ct] = mfma32(a[rt].x, b[ct].x, acc[rt][ct]);
+                acc[rt][ct] = mfma32(a[rt].y, b[ct].y, acc[rt][ct]);
+                acc[rt][ct] = mfma32(a[rt].z, b[ct].z, acc[rt][ct]);
+                acc[rt][ct] = mfma32(a[rt].w, b[ct].w, acc[rt][ct]);
+            }
+    }
+}
+
+template <int NRT, int NCT>
+__device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
+}
+
+// ------------------------------------------------------------------------------------
+// forward
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src,
+                                                          const float *__restrict__ W1, const float *__restrict__ b1,
+                                                          const float *__restrict__ W2, const float *__restrict__ b2,
+                                                          const float *__restrict__ norm_c,
+                                                          const float *__restrict__ norm_g, float eps,
+                                                          float *__restrict__ out, float *__restrict__ save_p,
+                                                          float *__restrict__ save_z) {
+    __shared__ __align__(16) float smem[BM * LDH];
+    __shared__ float red[4 * BM];
+    float *Xs = smem;
+    float *Ws = smem + BM * LDX;
+    float *Hs = smem;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const int K = nsrc * MATRIS_D;
+
+    // gather assignment: thread -> (row xr, 8 columns at xc) of each X chunk
+    const int xr = tid >> 2, xc = (tid & 3) * 8;
+    const int64_t grow = m0 + xr;
+    const bool xvalid = grow < M;
+    int64_t srow[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (j < nsrc && xvalid) srow[j] = src.idx[j] ? (int64_t)src.idx[j][grow] : grow;
+
+    float4 xreg[2], wreg[8];
+    auto load_chunk = [&](int kc) {
+        const int j = kc >> 7, cc = kc & 127;
+        const float *sp = src.ptr[0];
+        int64_t sr = srow[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q)
+            if (j == q) { sp = src.ptr[q]; sr = srow[q]; }
+        if (xvalid) {
+            const float4 *xp = reinterpret_cast<const float4 *>(sp + sr * MATRIS_D + cc + xc);
+            xreg[0] = xp[0];
+            xreg[1] = xp[1];
+        } else {
+            xreg[0] = xreg[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const float4 *wp = reinterpret_cast<const float4 *>(W1 + (int64_t)tid * K + kc);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wreg[q] = wp[q];
+    };
+
+    v16f acc[2][2];
+    zero_acc(acc);
+    load_chunk(0);
+    for (int kc = 0; kc < K; kc += BK) {
+        __syncthreads();
+        *reinterpret_cast<float4 *>(Xs + xr * LDX + xc) = xreg[0];
+        *reinterpret_cast<float4 *>(Xs + xr * LDX + xc + 4) = xreg[1];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) *reinterpret_cast<float4 *>(Ws + tid * LDW + 4 * q) = wreg[q];
+        __syncthreads();
+        if (kc + BK < K) load_chunk(kc + BK);
+        mfma_chunk<2, 2>(acc, Xs, LDX, Ws + (wave * 64) * LDW, LDW, lane);
+    }
+    __syncthreads();  // all waves are done with Xs / Ws before Hs overwrites them
+
+    // GEMM1 epilogue: bias, save p, SiLU into LDS
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const int col = wave * 64 + ct * 32 + l32;
+        const float bias = b1[col];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = rt * 32 + acc_row(i, h);
+                const float p = acc[rt][ct][i] + bias;
+                if (save_p && m0 + row < M) save_p[(m0 + row) * 256 + col] = p;
+                Hs[row * LDH + col] = silu_f(p);
+            }
+    }
+    __syncthreads();
+
+    // GEMM2: wave w -> z columns [64w, 64w+64); block = w/2 (0 core, 1 gate)
+    const int blk = wave >> 1;
+    zero_acc(acc);
+#pragma unroll
+    for (int kc = 0; kc < MATRIS_D; kc += BK)
+        mfma_chunk<2, 2>(acc, Hs + blk * MATRIS_D + kc, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D + kc, MATRIS_D,
+                         lane);
+
+    // bias, save z, per-row sum of squares over this wave's 64 columns
+    float zsq[2][16];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) zsq[rt][i] = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const int col = wave * 64 + ct * 32 + l32;
+        const float bias = b2[col];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = rt * 32 + acc_row(i, h);
+                const float z = acc[rt][ct][i] + bias;
+                acc[rt][ct][i] = z;
+                if (save_z && m0 + row < M) save_z[(m0 + row) * 256 + col] = z;
+                zsq[rt][i] += z * z;
+            }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float v = half_sum(zsq[rt][i]);
+            if (l32 == 0) red[wave * BM + rt * 32 + acc_row(i, h)] = v;
+        }
+    __syncthreads();  // red complete; every wave is past GEMM2 (Hs free)
+
+    const float *nw = blk ? norm_g : norm_c;
+    float act[2][2][16];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = rt * 32 + acc_row(i, h);
+            const float ss = red[wave * BM + row] + red[(wave ^ 1) * BM + row];
+            const float rinv = rsqrtf(ss * (1.0f / MATRIS_D) + eps);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int lc = (wave & 1) * 64 + ct * 32 + l32;  // column inside the block
+                const float a = acc[rt][ct][i] * rinv * nw[lc];
+                act[rt][ct][i] = blk ? sigm_f(a) : silu_f(a);
+            }
+        }
+    // gate -> LDS (reusing the h tile), then core * gate
+    float *Gs = smem;
+    if (blk == 1) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = rt * 32 + acc_row(i, h);
+                    const int lc = (wave & 1) * 64 + ct * 32 + l32;
+                    Gs[row * LDH + lc] = act[rt][ct][i];
+                }
+    }
+    __syncthreads();
+    if (blk == 0) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = rt * 32 + acc_row(i, h);
+                    const int lc = (wave & 1) * 64 + ct * 32 + l32;
+                    if (m0 + row < M) out[(m0 + row) * MATRIS_D + lc] = act[rt][ct][i] * Gs[row * LDH + lc];
+                }
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// backward
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, const float *__restrict__ g_out,
+                                                          const float *__restrict__ P, const float *__restrict__ Z,
+                                                          const float *__restrict__ W1t,
+                                                          const float *__restrict__ W2t,
+                                                          const float *__restrict__ norm_c,
+                                                          const float *__restrict__ norm_g, float eps,
+                                                          float *__restrict__ g_x) {
+    __shared__ __align__(16) float G[BM * LDH];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+
+    // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g)
+    for (int rr = 0; rr < BM / 4; ++rr) {
+        const int row = wave * (BM / 4) + rr;
+        const int64_t m = m0 + row;
+        float gz[4] = {0.f, 0.f, 0.f, 0.f};  // core l, core l+64, gate l, gate l+64
+        if (m < M) {
+            const float *zr = Z + m * 256;
+            float zc0 = zr[lane], zc1 = zr[lane + 64], zg0 = zr[128 + lane], zg1 = zr[192 + lane];
+            float go0 = g_out[m * MATRIS_D + lane], go1 = g_out[m * MATRIS_D + lane + 64];
+            float rc = rsqrtf(wave_sum(zc0 * zc0 + zc1 * zc1) * (1.0f / MATRIS_D) + eps);
+            float rg = rsqrtf(wave_sum(zg0 * zg0 + zg1 * zg1) * (1.0f / MATRIS_D) + eps);
+            float wc0 = norm_c[lane], wc1 = norm_c[lane + 64], wg0 = norm_g[lane], wg1 = norm_g[lane + 64];
+            float nc0 = zc0 * rc, nc1 = zc1 * rc, ng0 = zg0 * rg, ng1 = zg1 * rg;
+            float ac0 = nc0 * wc0, ac1 = nc1 * wc1, ag0 = ng0 * wg0, ag1 = ng1 * wg1;
+            float sc0 = sigm_f(ac0), sc1 = sigm_f(ac1);
+            float core0 = ac0 * sc0, core1 = ac1 * sc1;
+            float gate0 = sigm_f(ag0), gate1 = sigm_f(ag1);
+            float gnc0 = go0 * gate0 * (sc0 * (1.f + ac0 * (1.f - sc0))) * wc0;
+            float gnc1 = go1 * gate1 * (sc1 * (1.f + ac1 * (1.f - sc1))) * wc1;
+            float gng0 = go0 * core0 * (gate0 * (1.f - gate0)) * wg0;
+            float gng1 = go1 * core1 * (gate1 * (1.f - gate1)) * wg1;
+            float dc = wave_sum(gnc0 * nc0 + gnc1 * nc1) * (1.0f / MATRIS_D);
+            float dg = wave_sum(gng0 * ng0 + gng1 * ng1) * (1.0f / MATRIS_D);
+            gz[0] = (gnc0 - nc0 * dc) * rc;
+            gz[1] = (gnc1 - nc1 * dc) * rc;
+            gz[2] = (gng0 - ng0 * dg) * rg;
+            gz[3] = (gng1 - ng1 * dg) * rg;
+        }
+        G[row * LDH + lane] = gz[0];
+        G[row * LDH + lane + 64] = gz[1];
+        G[row * LDH + 128 + lane] = gz[2];
+        G[row * LDH + 192 + lane] = gz[3];
+    }
+    __syncthreads();
+
+    // phase 2: g_h = g_z W2 (block diagonal); wave w -> columns [64w, 64w+64)
+    const int blk = wave >> 1;
+    v16f acc[2][2];
+    zero_acc(acc);
+#pragma unroll
+    for (int kc = 0; kc < MATRIS_D; kc += BK)
+        mfma_chunk<2, 2>(acc, G + blk * MATRIS_D + kc, LDH,
+                         W2t + (int64_t)((wave & 1) * 64) * 256 + blk * MATRIS_D + kc, 256, lane);
+    // g_p = g_h * SiLU'(p)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const int col = wave * 64 + ct * 32 + l32;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = rt * 32 + acc_row(i, h);
+                const float p = (m0 + row < M) ? P[(m0 + row) * 256 + col] : 0.f;
+                acc[rt][ct][i] *= dsilu_f(p);
+            }
+    }
+    __syncthreads();  // every wave is done reading g_z
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const int col = wave * 64 + ct * 32 + l32;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) G[(rt * 32 + acc_row(i, h)) * LDH + col] = acc[rt][ct][i];
+    }
+    __syncthreads();
+
+    // phase 3: g_x = g_p W1 over 128-column blocks; wave w -> 32 columns of each block
+    for (int cb = 0; cb < K; cb += MATRIS_D) {
+        v16f a2[2][1];
+        zero_acc(a2);
+        const int col0 = cb + wave * 32;
+#pragma unroll 2
+        for (int kc = 0; kc < 256; kc += BK)
+            mfma_chunk<2, 1>(a2, G + kc, LDH, W1t + (int64_t)col0 * 256 + kc, 256, lane);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = rt * 32 + acc_row(i, h);
+                if (m0 + row < M) g_x[(m0 + row) * K + col0 + l32] = a2[rt][0][i];
+            }
+    }
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host,
+                               const int32_t *const *src_idx_host, const float *w1, const float *b1, const float *w2,
+                               const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
+                               float *save_p, float *save_z, void *stream) {
+    if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1 || !b1 || !w2 || !b2 || !norm_c || !norm_g || !out)
+        return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    GmlpSrc s;
+    for (int j = 0; j < 4; ++j) {
+        s.ptr[j] = j < n_src ? src_host[j] : nullptr;
+        s.idx[j] = (j < n_src && src_idx_host) ? src_idx_host[j] : nullptr;
+        if (j < n_src && (!s.ptr[j] || !aligned16(s.ptr[j]))) return MATRIS_E_ARG;
+    }
+    if (!aligned16(w1) || !aligned16(w2)) return MATRIS_E_ARG;
+    gmlp_fwd_kernel<<<matris_blocks(m, BM), 256, 0, (hipStream_t)stream>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g,
+                                                                         eps, out, save_p, save_z);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const float *w1t,
+                               const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x,
+                               void *stream) {
+    if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1t || !w2t ||
+        !norm_c || !norm_g || !g_x)
+        return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    if (!aligned16(w1t) || !aligned16(w2t)) return MATRIS_E_ARG;
+    gmlp_bwd_kernel<<<matris_blocks(m, BM), 256, 0, (hipStream_t)stream>>>(m, k, g_out, p, z, w1t, w2t, norm_c,
+                                                                         norm_g, eps, g_x);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}

@@ -1,0 +1,105 @@
+"""process_graphs on the device (row P1): batching, strain, edge geometry and the CSR
+groupings every gather / segment kernel needs.
+
+Mirrors matris/model/processgraph.py:6-245 (same keys and meaning).  Differences by
+design: no host-side per-graph offset tensors, no [E, 3G] block-diagonal image matrix
+(each edge reads its own graph's lattice), no bincount syncs; the groupings are stable
+CSR structures built by matris_csr_build.
+"""
+from __future__ import annotations
+
+import torch
+
+from .ops import Grouping
+
+
+def _sorted(x: torch.Tensor) -> bool:
+    return x.numel() < 2 or bool((x[1:] >= x[:-1]).all().item())
+
+
+def process_graphs(graphs, compute_stress: bool = True) -> dict:
+    device = graphs[0].lattice.device
+    dtype = graphs[0].lattice.dtype
+    G = len(graphs)
+    n_atoms = [int(g.atomic_number.shape[0]) for g in graphs]
+    n_dir = [int(g.atom_graph.shape[0]) for g in graphs]
+    n_und = [int(g.undirected2directed.shape[0]) for g in graphs]
+    n_ang = [int(g.line_graph.shape[0]) if len(g.line_graph) else 0 for g in graphs]
+    N, E, U, A = sum(n_atoms), sum(n_dir), sum(n_und), sum(n_ang)
+    canonical = all(g.meta.get("canonical", False) for g in graphs)
+
+    a_off = u_off = d_off = 0
+    ag, d2u, u2d, lgs, carts, lats, imgs = [], [], [], [], [], [], []
+    for g, na, nd, nu, nl in zip(graphs, n_atoms, n_dir, n_und, n_ang):
+        ag.append(g.atom_graph.to(torch.int32) + a_off)
+        d2u.append(g.directed2undirected.to(torch.int32) + u_off)
+        u2d.append(g.undirected2directed.to(torch.int32) + d_off)
+        if nl:
+            off = torch.tensor([a_off, u_off, d_off, u_off, d_off], dtype=torch.int32, device=device)
+            lgs.append(g.line_graph.to(torch.int32) + off)
+        frac = g.atom_frac_coord.detach()
+        lat = g.lattice.detach()
+        carts.append(frac @ lat)  # processgraph.py:87
+        lats.append(lat)
+        imgs.append(g.neighbor_image)
+        a_off += na
+        u_off += nu
+        d_off += nd
+
+    atom_graph = torch.cat(ag, 0)
+    tgt32 = atom_graph[:, 0].contiguous()
+    src32 = atom_graph[:, 1].contiguous()
+    tgt, src = tgt32.long(), src32.long()
+    d2u32 = torch.cat(d2u, 0).contiguous()
+    u2d32 = torch.cat(u2d, 0).contiguous()
+    lattice = torch.cat(lats, 0)  # [3G, 3]
+    cart = torch.cat(carts, 0)
+    image = torch.cat(imgs, 0)
+    counts = torch.tensor(n_atoms, device=device)
+    atom_segment = torch.repeat_interleave(torch.arange(G, device=device), counts)
+    lat3 = lattice.reshape(G, 3, 3)
+    volumes = torch.einsum("ni,ni->n", lat3[:, 0], torch.linalg.cross(lat3[:, 1], lat3[:, 2]))[:, None, None]
+
+    # strain trick (processgraph.py:169-189)
+    cart.requires_grad_(True)
+    strains = None
+    if compute_stress:
+        strains = torch.zeros((G, 3, 3), dtype=dtype, device=device, requires_grad=True)
+        sym = 0.5 * (strains + strains.transpose(-1, -2))
+        cart = cart + torch.bmm(cart.unsqueeze(1), sym[atom_segment]).squeeze(1)
+        lat3 = lat3 + torch.matmul(lat3, sym)
+        lattice = lat3.reshape(-1, 3)
+
+    # edge geometry (processgraph.py:192-199); image . lattice of the edge's own graph
+    if G == 1:
+        shift = image @ lattice
+    else:
+        edge_graph = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_dir, device=device))
+        shift = torch.bmm(image.unsqueeze(1), lat3[edge_graph]).squeeze(1)
+    vec = cart[tgt] - (cart[src] + shift)
+    length = torch.norm(vec, dim=1)
+    unit = vec / length[:, None]
+
+    out = dict(atomic_numbers=torch.cat([g.atomic_number for g in graphs], 0), edge_lengths=length,
+               unit_edge_vectors=unit, atom_segment=atom_segment, atoms_per_graph=n_atoms,
+               directed2undirected=d2u32.long(), undirected2directed=u2d32.long(), volumes=volumes,
+               lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
+               n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
+    out["grp_d2u"] = Grouping.build(d2u32, U, sorted_rows=False)
+    out["atom_graph_dict"] = dict(
+        atom_graph=atom_graph, target_index=tgt, source_index=src,
+        grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32)),
+        grp_src=Grouping.build(src32, N))
+    lgd: dict = {}
+    if A:
+        lg = torch.cat(lgs, 0)
+        cols = [lg[:, k].contiguous() for k in range(5)]
+        lgd = dict(line_graph=lg[:, [0, 1, 3]], atom_list=cols[0].long(), target_index=cols[1].long(),
+                   source_index=cols[3].long(), target_DE_index=cols[2].long(), source_DE_index=cols[4].long(),
+                   grp_tgt=Grouping.build(cols[1], U, sorted_rows=True),
+                   grp_src=Grouping.build(cols[3], U),
+                   grp_atom=Grouping.build(cols[0], N))
+    else:
+        lgd = dict(line_graph=torch.zeros(0, 3, dtype=torch.int64, device=device))
+    out["line_graph_dict"] = lgd
+    return out

@@ -1,0 +1,595 @@
+"""MatRIS on MI355X: the reference module tree (same class names, attribute names,
+construction order and state_dict keys, so `torch.manual_seed(s)` gives the reference's
+weights and a reference checkpoint loads unchanged) whose forward runs the gfx950
+kernels of libmatris_hip.so:
+
+  gated MLPs (every GatedMLP, with its input concatenation)  -> matris_gmlp_fwd / _bwd
+  Dimwise_softmax x2 + alpha * e' + both aggregations         -> matris_attn_fwd / _bwd
+  aggregate(), index_select and their backward scatters      -> matris_seg_sum / _gather_rows
+  graph construction                                          -> GraphConverter (G1-G5 kernels)
+
+Plain dense layers (edge/three-body embeddings, W_s / W_t projections, FFNs, heads) are
+library GEMMs (hipBLASLt through torch); elementwise glue is torch on the device.
+Forces and stress come from torch.autograd.grad exactly as in the reference
+(readout.py:202-217); every custom op supplies its own input-gradient kernel.
+
+Reference: matris/model/model.py, interaction_block.py, feature_embed.py, functions.py,
+readout.py, basis_function.py.
+"""
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from ..config import EV_A3_TO_GPA
+from ..graph.converter import GraphConverter
+from . import ops
+from .batch import process_graphs
+
+
+# ------------------------------------------------------------------------------------
+# primitives (functions.py)
+# ------------------------------------------------------------------------------------
+class FusedSiLU(nn.Module):
+    """functions.py:10-22 (the activation inside the fused kernels; F.silu elsewhere)."""
+
+    def forward(self, x):
+        return F.silu(x)
+
+
+class FusedSigmoid(nn.Module):
+    """functions.py:24-36."""
+
+    def forward(self, x):
+        return torch.sigmoid(x)
+
+
+def get_activation(name: str) -> nn.Module:
+    """functions.py:38-55."""
+    table = {"relu": nn.ReLU, "silu": FusedSiLU, "gelu": nn.GELU, "softplus": nn.Softplus, "sigmoid": FusedSigmoid,
+             "tanh": nn.Tanh}
+    if name.lower() not in table:
+        raise NotImplementedError(f"Activation '{name}' is not implemented. Supported activations: {list(table)}")
+    return table[name.lower()]()
+
+
+def get_normalization(name: str, dim: int | None = None) -> nn.Module | None:
+    """functions.py:57-68 (LayerNorm / RMSNorm / BatchNorm1d construction consumes no RNG)."""
+    if name is None:
+        return None
+    name = name.lower()
+    if name == "layer":
+        return nn.LayerNorm(dim)
+    if name == "rms":
+        return nn.RMSNorm(dim)
+    if name == "batch":
+        return nn.BatchNorm1d(dim)
+    raise KeyError(name)
+
+
+class SwishLayer(nn.Module):
+    """functions.py:70-95."""
+
+    def __init__(self, input_dim: int = 128, output_dim: int = 128, bias: bool = True):
+        super().__init__()
+        self.linear = nn.Linear(input_dim, output_dim, bias=bias)
+        self.act = get_activation("silu")
+
+    def forward(self, x):
+        return self.act(self.linear(x))
+
+
+class MLP(nn.Module):
+    """functions.py:163-242."""
+
+    def __init__(self, input_dim=128, hidden_dim=(128, 128), output_dim=128, dropout=0.0, activation="silu",
+                 bias=True, use_fp16=False):
+        super().__init__()
+        if not 0.0 <= dropout < 1.0:
+            raise ValueError(f"Dropout rate must be in [0.0, 1.0), got {dropout}")
+        self.use_fp16 = use_fp16
+        act = get_activation(activation)
+        layers: list[nn.Module] = []
+        if hidden_dim in (None, 0):
+            layers += [nn.Dropout(dropout), nn.Linear(input_dim, output_dim, bias=bias)]
+        elif isinstance(hidden_dim, int):
+            layers += [nn.Linear(input_dim, hidden_dim, bias=bias), act, nn.Dropout(dropout),
+                       nn.Linear(hidden_dim, output_dim, bias=bias)]
+        elif isinstance(hidden_dim, Sequence):
+            layers += [nn.Linear(input_dim, hidden_dim[0], bias=bias), act]
+            for i in range(len(hidden_dim) - 1):
+                layers += [nn.Dropout(dropout), nn.Linear(hidden_dim[i], hidden_dim[i + 1], bias=bias), act]
+            layers += [nn.Dropout(dropout), nn.Linear(hidden_dim[-1], output_dim, bias=bias)]
+        else:
+            raise TypeError(f"hidden_dim must be an integer, sequence of integers, or None, got "
+                            f"{type(hidden_dim).__name__}")
+        self.layers = nn.Sequential(*layers)
+
+    def forward(self, x):
+        return self.layers(x)
+
+
+class GatedMLP(nn.Module):
+    """functions.py:245-311.  `fused(sources)` runs the whole block -- gathers, concat,
+    two MLPs, RMSNorm, SiLU, sigmoid, product -- in matris_gmlp_fwd."""
+
+    def __init__(self, input_dim=128, hidden_dim=(128, 128), output_dim=128, dropout=0.0, activation="silu",
+                 norm_type="layer", bias=True, use_fp16=False):
+        super().__init__()
+        self.use_fp16 = use_fp16
+        self.activation_func = get_activation(activation)
+        self.activation_gate = get_activation("sigmoid")
+        self.gate_norm = get_normalization(name=norm_type, dim=output_dim)
+        self.core_norm = get_normalization(name=norm_type, dim=output_dim)
+        self.mlp_core = MLP(input_dim, hidden_dim, output_dim, dropout, activation, bias, use_fp16)
+        self.mlp_gate = MLP(input_dim, hidden_dim, output_dim, dropout, activation, bias, use_fp16)
+        self._pack = ops.GmlpPack()
+
+    def _fusable(self) -> bool:
+        return (isinstance(self.core_norm, nn.RMSNorm) and len(self.mlp_core.layers) == 4
+                and self.mlp_core.layers[0].bias is not None and self.mlp_core.layers[0].out_features == 128
+                and self.mlp_core.layers[3].out_features == 128)
+
+    def forward(self, x):
+        core = self.activation_func(self.core_norm(self.mlp_core(x)))
+        gate = self.activation_gate(self.gate_norm(self.mlp_gate(x)))
+        return core * gate
+
+    def fused(self, sources):
+        if not self._fusable():
+            raise NotImplementedError("fused GatedMLP needs RMSNorm, one 128-wide hidden layer and biases")
+        return ops.gated_mlp(self, self._pack, sources)
+
+
+class GraphPooling(nn.Module):
+    """functions.py:340-365 (graph sums of a [N, 1] quantity)."""
+
+    def __init__(self, average: bool = False):
+        super().__init__()
+        self.average = average
+
+    def forward(self, node_feat, segment, n_graphs: int):
+        out = node_feat.new_zeros(n_graphs, node_feat.shape[1]).index_add(0, segment, node_feat)
+        if self.average:
+            cnt = torch.bincount(segment, minlength=n_graphs).clamp_min(1)
+            out = out / cnt[:, None]
+        return out
+
+
+# ------------------------------------------------------------------------------------
+# basis functions (basis_function.py)
+# ------------------------------------------------------------------------------------
+class PolynomialEnvelope(nn.Module):
+    """basis_function.py:8-50."""
+
+    def __init__(self, cutoff: float = 6, envelope_exponent: float = 8):
+        super().__init__()
+        assert envelope_exponent > 0
+        self.cutoff = cutoff
+        self.p = float(envelope_exponent)
+        self.a = -(self.p + 1) * (self.p + 2) / 2
+        self.b = self.p * (self.p + 2)
+        self.c = -self.p * (self.p + 1) / 2
+
+    def forward(self, dist):
+        x = dist / self.cutoff
+        env = 1 + self.a * x ** self.p + self.b * x ** (self.p + 1) + self.c * x ** (self.p + 2)
+        return torch.where(x < 1, env, torch.zeros_like(x))
+
+
+class BesselExpansion(nn.Module):
+    """basis_function.py:116-186."""
+
+    def __init__(self, num_radial=9, cutoff=6, envelope_exponent=8, learnable=False):
+        super().__init__()
+        self.num_radial = num_radial
+        self.inv_cutoff = 1 / cutoff
+        self.norm_const = (2 * self.inv_cutoff) ** 0.5
+        freq = math.pi * torch.arange(1, num_radial + 1, dtype=torch.float)
+        if learnable:
+            self.frequencies = nn.Parameter(freq, requires_grad=True)
+        else:
+            self.register_buffer("frequencies", freq)
+        self.envelope_func = PolynomialEnvelope(cutoff, envelope_exponent) if envelope_exponent is not None else None
+
+    def forward(self, dist, return_smooth_factor=False):
+        dist = dist[:, None]
+        out = self.norm_const * torch.sin(self.frequencies * (dist * self.inv_cutoff)) / dist
+        if self.envelope_func is not None:
+            sf = self.envelope_func(dist)
+            out = sf * out
+            if return_smooth_factor:
+                return out, sf
+        return out
+
+
+_SBF_COEF = {
+    1: [[-1.02446483277785, -1.00834335996107, -1.00419641763893, -1.00252381898662],
+        [4.49340963363647, 7.7252516746521, 10.9041213989258, 14.0661935806274],
+        [0.22799275301076, 0.130525632358311, 0.092093290316619, 0.0712718627992818],
+        [4.49340963363647, 7.7252516746521, 10.9041213989258, 14.0661935806274]],
+    2: [[-1.04807944170731, -1.01861796359391, -1.01002272174988, -1.00628955560036],
+        [5.76345920562744, 9.09501171112061, 12.322940826416, 15.5146026611328],
+        [0.545547077361439, 0.335992298618515, 0.245888396928293, 0.194582402961821],
+        [5.76345920562744, 9.09501171112061, 12.322940826416, 15.5146026611328],
+        [0.0946561878721665, 0.0369424811413594, 0.0199537107571916, 0.0125418876146463],
+        [5.76345920562744, 9.09501171112061, 12.322940826416, 15.5146026611328]],
+    3: [[1.06942831392075, 1.0292173312802, 1.01650804843248, 1.01069656069999],
+        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477],
+        [0.918235852195231, 0.592803493701152, 0.445250264272671, 0.358326327374518],
+        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477],
+        [0.328507713452024, 0.142266673367543, 0.0812617757677838, 0.0529328657590962],
+        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477],
+        [0.0470107184508114, 0.0136570088173405, 0.0059323726279831, 0.00312775039221944],
+        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477]],
+}
+
+
+class SphericalExpansion(nn.Module):
+    """basis_function.py:222-338 (radial spherical-Bessel table x Legendre Y_l)."""
+
+    def __init__(self, max_n=4, max_l=4, cutoff=6):
+        super().__init__()
+        assert max_l <= 4 and max_n <= 4
+        self.max_n, self.max_l, self.cutoff = max_n, max_l, cutoff
+        self.register_buffer("factor", torch.sqrt(torch.tensor(2.0 / (cutoff ** 3))))
+        coef = torch.zeros(4, 9, 4)
+        coef[0, 0, :] = torch.tensor([3.14159274101257, 6.28318548202515, 9.42477798461914, 12.5663709640503])
+        coef[1, :4, :] = torch.tensor(_SBF_COEF[1])
+        coef[2, :6, :] = torch.tensor(_SBF_COEF[2])
+        coef[3, :8, :] = torch.tensor(_SBF_COEF[3])
+        self.coef = coef
+
+    def forward(self, dist, three_body):
+        c = self.coef.tolist()
+        x = dist / self.cutoff
+        rbfs = [torch.sin(c[0][0][j] * x) / x for j in range(self.max_l)]
+        if self.max_n > 1:
+            rbfs += [(c[1][0][j] * x * torch.cos(c[1][1][j] * x) + c[1][2][j] * torch.sin(c[1][3][j] * x)) / x ** 2
+                     for j in range(self.max_l)]
+        if self.max_n > 2:
+            rbfs += [(c[2][0][j] * x ** 2 * torch.sin(c[2][1][j] * x) - c[2][2][j] * x * torch.cos(c[2][3][j] * x)
+                      + c[2][4][j] * torch.sin(c[2][5][j] * x)) / x ** 3 for j in range(self.max_l)]
+        if self.max_n > 3:
+            rbfs += [(c[3][0][j] * x ** 3 * torch.cos(c[3][1][j] * x) - c[3][2][j] * x ** 2
+                      * torch.sin(c[3][3][j] * x) - c[3][4][j] * x * torch.cos(c[3][5][j] * x)
+                      + c[3][6][j] * torch.sin(c[3][7][j] * x)) / x ** 4 for j in range(self.max_l)]
+        rbfs = torch.stack(rbfs, dim=-1) * self.factor
+        ct = torch.cos(three_body)
+        ys = [torch.ones_like(ct) * 0.5 * math.sqrt(1.0 / math.pi), math.sqrt(3.0 / (4.0 * math.pi)) * ct,
+              math.sqrt(5.0 / (16.0 * math.pi)) * (3.0 * ct ** 2 - 1.0),
+              math.sqrt(7.0 / (16.0 * math.pi)) * ct * (5.0 * ct ** 2 - 3.0)][: self.max_l]
+        cbfs = torch.stack(ys, dim=-1).repeat_interleave(self.max_n, dim=1)
+        return rbfs * cbfs
+
+
+# ------------------------------------------------------------------------------------
+# embeddings (feature_embed.py)
+# ------------------------------------------------------------------------------------
+class AtomTypeEmbedding(nn.Module):
+    """feature_embed.py:16-39."""
+
+    def __init__(self, atom_feat_dim: int, max_num_elements: int = 94):
+        super().__init__()
+        self.embedding = nn.Embedding(max_num_elements, atom_feat_dim)
+        self.atom_swish_layer = SwishLayer(atom_feat_dim, atom_feat_dim, bias=False)
+
+    def forward(self, atom_type):
+        return self.atom_swish_layer(self.embedding(atom_type))
+
+
+class EdgeBasisEmbedding(nn.Module):
+    """feature_embed.py:42-148.  The reference expands W1 rbf to both directed copies,
+    applies W2 and LayerNorm, then averages the two identical copies; evaluating once
+    per undirected bond gives the same values and the same gradient (g/2 + g/2)."""
+
+    def __init__(self, pairwise_cutoff=6, three_body_cutoff=4, num_radial=7, edge_feat_dim=128,
+                 envelope_exponent=8, distance_expansion="Bessel", learnable=False):
+        super().__init__()
+        if distance_expansion.lower() != "bessel":
+            raise NotImplementedError("only the Bessel distance expansion is on the MI355X path")
+        self.distance_expansion = distance_expansion
+        self.pairwise_rbf_expansion = BesselExpansion(num_radial, pairwise_cutoff, envelope_exponent, learnable)
+        self.threebody_rbf_expansion = BesselExpansion(num_radial, three_body_cutoff, envelope_exponent, learnable)
+        self.edge_linear1 = nn.Linear(num_radial, edge_feat_dim, bias=False)
+        self.edge_linear2 = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
+        self.swish_layer = SwishLayer(edge_feat_dim, edge_feat_dim, bias=False)
+        self.edge_init_norm = get_normalization(name="layer", dim=edge_feat_dim)
+
+    def forward(self, graphs):
+        lengths = torch.index_select(graphs["edge_lengths"], 0, graphs["undirected2directed"])
+        rbf6 = self.pairwise_rbf_expansion(lengths)
+        rbf4 = self.threebody_rbf_expansion(lengths)
+        e = self.edge_init_norm(self.edge_linear2(self.edge_linear1(rbf6)))
+        e = self.swish_layer(e)
+        return e, {"atom graph": rbf6, "line graph": rbf4}
+
+
+class ThreebodyEmbedding(nn.Module):
+    """feature_embed.py:151-203 (SH expansion)."""
+
+    def __init__(self, num_angular=7, max_n=4, max_l=4, cutoff=6, three_body_feat_dim=128,
+                 three_body_expansion="sh", learnable=True):
+        super().__init__()
+        self.three_body_expansion = three_body_expansion.lower()
+        if self.three_body_expansion != "sh":
+            raise NotImplementedError("only the SH three-body expansion is on the MI355X path")
+        self.expansion = SphericalExpansion(max_n=max_n, max_l=max_l, cutoff=cutoff)
+        self.angle_embedding = nn.Linear(max_n * max_l, three_body_feat_dim, bias=False)
+        self.swish_layer = SwishLayer(three_body_feat_dim, three_body_feat_dim, bias=False)
+
+    def forward(self, graphs):
+        lg = graphs["line_graph_dict"]
+        vij = torch.index_select(graphs["unit_edge_vectors"], 0, lg["target_DE_index"])
+        vjk = torch.index_select(graphs["unit_edge_vectors"], 0, lg["source_DE_index"])
+        cos_t = torch.sum(vij * vjk, dim=1) * (1 - 1e-6)
+        angle = torch.acos(cos_t)
+        basis = self.expansion(torch.norm(vjk, dim=1), angle)
+        return self.swish_layer(self.angle_embedding(basis))
+
+
+# ------------------------------------------------------------------------------------
+# interaction block (interaction_block.py)
+# ------------------------------------------------------------------------------------
+class Graph_Attention_Layer(nn.Module):
+    """interaction_block.py:17-143 (GateMLP)."""
+
+    def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, use_bias=False, dropout=0.0,
+                 mlp_type="GateMLP", activation_type="silu", norm_type="layer", use_fp16=False):
+        super().__init__()
+        if mlp_type.lower() != "gatemlp":
+            raise NotImplementedError("the MI355X path implements graph_conv_mlp='GateMLP'")
+        self.source_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
+        self.target_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
+        self.node_nonlinear_update = GatedMLP(edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
+                                              norm_type=norm_type, dropout=dropout, activation=activation_type)
+        self.edge_nonlinear_update = GatedMLP(node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
+                                              norm_type=norm_type, dropout=dropout, activation=activation_type,
+                                              use_fp16=use_fp16)
+        self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim), requires_grad=True)
+        self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim), requires_grad=True)
+
+    def forward(self, node_feat, edge_feat, graph, d2u: ops.Grouping | None = None):
+        tgt, src = graph["grp_tgt"], graph["grp_src"]
+        if d2u is None:  # line graph: edges are the angles themselves
+            e = self.edge_nonlinear_update.fused([(edge_feat, None), (node_feat, tgt), (node_feat, src)])
+            a_s = self.source_weight_linear(edge_feat)
+            a_t = self.target_weight_linear(edge_feat)
+            y_t, y_s = ops.seg_attention(a_t, a_s, e, tgt, src)
+        else:  # atom graph: undirected bond rows expanded through d2u inside the kernels
+            e = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
+            a_s = self.source_weight_linear(edge_feat)
+            a_t = self.target_weight_linear(edge_feat)
+            y_t, y_s = ops.seg_attention(a_t, a_s, e, tgt, src, alpha_grp=d2u)
+            e = ops.seg_sum(e, d2u, 0.5)  # mean of the two directed copies (:121-122)
+        n = self.node_nonlinear_update.fused([(node_feat, None), (y_t, None), (y_s, None)])
+        return n + self.node_res_weight * node_feat, e + self.edge_res_weight * edge_feat
+
+
+class Refinement(nn.Module):
+    """interaction_block.py:146-278 (GateMLP)."""
+
+    def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, num_basis=7, dropout=0.0,
+                 mlp_type="GateMLP", activation_type="silu", norm_type="layer", use_bias=False,
+                 graph_type="atom graph", atom_feat_dim=128, use_smoothed_for_delta_edge=False, use_fp16=False):
+        super().__init__()
+        if mlp_type.lower() != "gatemlp":
+            raise NotImplementedError("the MI355X path implements graph_conv_mlp='GateMLP'")
+        self.graph_type = graph_type
+        self.use_smoothed_for_delta_edge = use_smoothed_for_delta_edge
+        input_dim = 2 * node_feat_dim + edge_feat_dim if graph_type == "atom graph" else \
+            atom_feat_dim + 2 * node_feat_dim + edge_feat_dim
+        self.edge_nonlinear_update = GatedMLP(input_dim, hidden_dim, edge_feat_dim, dropout=dropout,
+                                              norm_type=norm_type, activation=activation_type, use_fp16=use_fp16)
+        self.node_FFN = MLP(edge_feat_dim, node_feat_dim, node_feat_dim, bias=use_bias)
+        self.edge_FFN = MLP(edge_feat_dim, edge_feat_dim, edge_feat_dim, bias=use_bias, use_fp16=use_fp16)
+        self.learnable_envelope = nn.Linear(num_basis, edge_feat_dim, bias=False)
+        self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim), requires_grad=True)
+        self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim), requires_grad=True)
+
+    def forward(self, node_feat, edge_feat, smooth_weight, graph, d2u: ops.Grouping | None = None, atom_feat=None):
+        tgt, src = graph["grp_tgt"], graph["grp_src"]
+        if self.graph_type == "atom graph":
+            w = ops.gather(self.learnable_envelope(smooth_weight), d2u)
+            h = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
+        else:
+            env = self.learnable_envelope(smooth_weight)
+            w = ops.gather(env, src) * ops.gather(env, tgt)
+            h = self.edge_nonlinear_update.fused([(edge_feat, None), (atom_feat, graph["grp_atom"]),
+                                                  (node_feat, tgt), (node_feat, src)])
+        hw = h * w
+        agg = ops.seg_sum(hw, tgt)
+        to_edge = hw if (self.graph_type == "atom graph" and self.use_smoothed_for_delta_edge) else h
+        dn = self.node_FFN(agg)
+        de = self.edge_FFN(to_edge)
+        if self.graph_type == "atom graph":
+            de = ops.seg_sum(de, d2u, 0.5)
+        return dn + self.node_res_weight * node_feat, de + self.edge_res_weight * edge_feat
+
+
+class Interaction_Block(nn.Module):
+    """interaction_block.py:281-446.  The reference's activation checkpointing
+    (A > 60000, :400-413) trades memory for recompute; here the fused kernels never
+    materialise the [A, 384/512] concatenations, so it is not needed."""
+
+    def __init__(self, node_feat_dim=128, edge_feat_dim=128, three_body_feat_dim=128, num_radial=7, num_angular=7,
+                 dropout=0.0, use_bias=False, use_smoothed_for_delta_edge=False, mlp_type="GateMLP",
+                 norm_type="layer", activation_type="silu"):
+        super().__init__()
+        self.attn_block_atom_graph = Graph_Attention_Layer(node_feat_dim, edge_feat_dim, node_feat_dim, use_bias,
+                                                           mlp_type=mlp_type, norm_type=norm_type,
+                                                           activation_type=activation_type)
+        self.attn_block_line_graph = Graph_Attention_Layer(edge_feat_dim, three_body_feat_dim, edge_feat_dim,
+                                                           use_bias, mlp_type=mlp_type, norm_type=norm_type,
+                                                           activation_type=activation_type)
+        self.refine_block_atom_graph = Refinement(node_feat_dim, edge_feat_dim, node_feat_dim, num_radial, dropout,
+                                                  mlp_type, activation_type, norm_type, use_bias, "atom graph",
+                                                  use_smoothed_for_delta_edge=use_smoothed_for_delta_edge)
+        self.refine_block_line_graph = Refinement(edge_feat_dim, three_body_feat_dim, edge_feat_dim, num_angular,
+                                                  dropout, mlp_type, activation_type, norm_type, use_bias,
+                                                  "line graph", atom_feat_dim=node_feat_dim)
+
+    def forward(self, batch_graph, node_feat, edge_feat, threebody_feat, smooth_weight):
+        attn_edge, attn_tb = edge_feat, threebody_feat
+        upd_edge, upd_tb = edge_feat, threebody_feat
+        lg, ag, d2u = batch_graph["line_graph_dict"], batch_graph["atom_graph_dict"], batch_graph["grp_d2u"]
+        if threebody_feat is not None:
+            attn_edge, attn_tb = self.attn_block_line_graph(edge_feat, threebody_feat, lg)
+        attn_node, attn_edge = self.attn_block_atom_graph(node_feat, attn_edge, ag, d2u)
+        if threebody_feat is not None:
+            upd_edge, upd_tb = self.refine_block_line_graph(attn_edge, attn_tb, smooth_weight["line graph"], lg,
+                                                            atom_feat=attn_node)
+        upd_node, upd_edge = self.refine_block_atom_graph(attn_node, upd_edge, smooth_weight["atom graph"], ag,
+                                                          d2u=d2u)
+        return upd_node, upd_edge, upd_tb
+
+
+# ------------------------------------------------------------------------------------
+# readout (readout.py)
+# ------------------------------------------------------------------------------------
+class EnergyHead(nn.Module):
+    """readout.py:18-75 (mlp_type='mlp')."""
+
+    def __init__(self, feat_dim=128, hidden_dim=128, output_dim=1, mlp_type="mlp", activation_type="silu"):
+        super().__init__()
+        hd = [hidden_dim] if isinstance(hidden_dim, int) else list(hidden_dim)
+        if mlp_type.lower() != "mlp":
+            raise NotImplementedError(f"Unknown mlp_type: {mlp_type}")
+        self.energy_head = MLP(feat_dim, hd, output_dim, activation=activation_type)
+        self.pooling = GraphPooling(average=False)
+
+    def forward(self, batch_graph, node_feat):
+        e = self.energy_head(node_feat)
+        return self.pooling(e, batch_graph["atom_segment"], len(batch_graph["atoms_per_graph"])).view(-1)
+
+
+class MagmomHead(nn.Module):
+    """readout.py:77-133 (mlp_type='mlp')."""
+
+    def __init__(self, feat_dim=128, hidden_dim=128, output_dim=1, mlp_type="mlp", activation_type="silu"):
+        super().__init__()
+        hd = [hidden_dim] if isinstance(hidden_dim, int) else list(hidden_dim)
+        if mlp_type.lower() != "mlp":
+            raise NotImplementedError(f"Unknown mlp_type: {mlp_type}")
+        self.magmom_head = MLP(feat_dim, hd, output_dim, activation=activation_type)
+
+    def forward(self, batch_graph, node_feat):
+        m = torch.abs(self.magmom_head(node_feat))
+        return list(torch.split(m.view(-1), batch_graph["atoms_per_graph"]))
+
+
+class ForceStressHead(nn.Module):
+    """readout.py:136-224, conservative branch: forces and stress by autograd."""
+
+    def __init__(self, is_conservation=True, **_unused):
+        super().__init__()
+        if not is_conservation:
+            raise NotImplementedError("the MI355X path implements the conservative force/stress head")
+        self.is_conservation = is_conservation
+
+    def forward(self, batch_graph, compute_force=True, compute_stress=True, total_energy=None, is_training=False,
+                **_unused):
+        pred = {}
+        if compute_force and compute_stress:
+            gc, gs = torch.autograd.grad(total_energy.sum(),
+                                         [batch_graph["batch_cart_coords"], batch_graph["batch_strains"]],
+                                         create_graph=is_training, retain_graph=is_training)
+            pred["f"] = torch.split(-1 * gc, batch_graph["atoms_per_graph"])
+            pred["s"] = list(torch.unbind(gs * (1 / batch_graph["volumes"] * EV_A3_TO_GPA), dim=0))
+        elif compute_force:
+            (gc,) = torch.autograd.grad(total_energy.sum(), [batch_graph["batch_cart_coords"]],
+                                        create_graph=is_training, retain_graph=is_training)
+            pred["f"] = torch.split(-1 * gc, batch_graph["atoms_per_graph"])
+        return pred
+
+
+# ------------------------------------------------------------------------------------
+# MatRIS (model.py)
+# ------------------------------------------------------------------------------------
+class MatRIS(nn.Module):
+    """model.py:30-317 with the same constructor keywords and forward signature."""
+
+    def __init__(self, num_layers: int = 6, node_feat_dim: int = 128, edge_feat_dim: int = 128,
+                 three_body_feat_dim: int = 128, mlp_hidden_dims=(128, 128), dropout: float = 0.0,
+                 use_bias: bool = False, distance_expansion: str = "Bessel", three_body_expansion: str = "SH",
+                 num_radial: int = 7, num_angular: int = 7, max_l: int = 4, max_n: int = 4,
+                 envelope_exponent: int = 8, graph_conv_mlp: str = "GateMLP", activation_type: str = "silu",
+                 norm_type: str = "rms", pairwise_cutoff: float = 6, three_body_cutoff: float = 4,
+                 use_smoothed_for_delta_edge: bool = False, learnable_basis: bool = True, is_intensive: bool = True,
+                 is_conservation: bool = True, reference_energy: str | None = None, verbose: bool = False):
+        super().__init__()
+        self.config = {k: v for k, v in locals().items() if k not in ("self", "__class__", "verbose")}
+        self.is_intensive = is_intensive
+        if reference_energy is not None:
+            raise NotImplementedError("AtomRef reference energies are not on the MI355X path yet")
+        self.reference_energy = None
+        self.graph_converter = GraphConverter(atom_graph_cutoff=pairwise_cutoff, line_graph_cutoff=three_body_cutoff)
+        self.atom_embedding = AtomTypeEmbedding(atom_feat_dim=node_feat_dim)
+        self.edge_embedding = EdgeBasisEmbedding(pairwise_cutoff, three_body_cutoff, num_radial, edge_feat_dim,
+                                                 envelope_exponent, distance_expansion, learnable_basis)
+        self.three_body_embedding = ThreebodyEmbedding(num_angular, max_n, max_l, pairwise_cutoff,
+                                                       three_body_feat_dim, three_body_expansion, learnable_basis)
+        self.interaction_block = nn.ModuleList([
+            Interaction_Block(node_feat_dim, edge_feat_dim, three_body_feat_dim, num_radial, num_angular, dropout,
+                              use_bias, use_smoothed_for_delta_edge, graph_conv_mlp, norm_type, activation_type)
+            for _ in range(num_layers)])
+        self.readout_norm = get_normalization(norm_type, dim=node_feat_dim)
+        self.energy_head = EnergyHead(node_feat_dim, mlp_hidden_dims, 1, "mlp", activation_type)
+        self.magmom_head = MagmomHead(node_feat_dim, 2 * node_feat_dim, 1, "mlp", activation_type)
+        self.force_stress_head = ForceStressHead(is_conservation=is_conservation)
+        if verbose:
+            print(f"MatRIS initialized with {self.get_params()} parameters")
+
+    def forward(self, graphs, task: str = "ef", is_training: bool = False) -> dict:
+        """model.py:183-250."""
+        if is_training:
+            raise NotImplementedError("training (double backward) is outside the efsm inference path")
+        pred = {}
+        bg = process_graphs(graphs, compute_stress="s" in task)
+        node = self.atom_embedding(bg["atomic_numbers"].long() - 1)
+        edge, smooth = self.edge_embedding(graphs=bg)
+        tb = None
+        if bg["n_angles"] != 0:
+            tb = self.three_body_embedding(graphs=bg)
+        for layer in self.interaction_block:
+            node, edge, tb = layer(bg, node, edge, tb, smooth)
+        node = self.readout_norm(node)
+        total = self.energy_head(bg, node)
+        pred.update(self.force_stress_head(bg, compute_force="f" in task, compute_stress="s" in task,
+                                           total_energy=total, is_training=is_training))
+        if "m" in task:
+            pred["m"] = self.magmom_head(bg, node)
+        apg = torch.tensor(bg["atoms_per_graph"], dtype=torch.int32, device=total.device)
+        pred["e"] = total / apg if self.is_intensive else total
+        pred["atoms_per_graph"] = apg
+        pred["ref_energy"] = 0
+        return pred
+
+    def get_params(self) -> int:
+        return sum(p.numel() for p in self.parameters())
+
+    @classmethod
+    def from_dict(cls, dct: dict):
+        """model.py:256-260: {"config": kwargs, "state_dict": ...}."""
+        m = cls(**dct["config"])
+        m.load_state_dict(dct["state_dict"])
+        return m
+
+    @classmethod
+    def load(cls, model_name: str = "matris_10m_oam", device: str | None = None, path: str | None = None):
+        """model.py:262-317 without the network download: loads a local checkpoint
+        ({"config", "state_dict"}, read with weights_only=True)."""
+        import os
+        if path is None:
+            files = {"matris_10m_omat": "MatRIS_10M_OMAT.pth.tar", "matris_10m_oam": "MatRIS_10M_OAM.pth.tar",
+                     "matris_10m_mp": "MatRIS_10M_MP.pth.tar", "matris_6m_mp": "MatRIS_6M_MP.pth.tar"}
+            path = os.path.join(os.path.expanduser("~/.cache/matris"), files[model_name.lower()])
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not found (no network download on this path)")
+        ckpt = torch.load(path, map_location="cpu", weights_only=True)
+        model = cls.from_dict(ckpt)
+        return model.to(device or ("cuda" if torch.cuda.is_available() else "cpu"))

@@ -1,0 +1,299 @@
+"""torch.autograd wrappers over the C-ABI kernels of libmatris_hip.so.
+
+PyTorch supplies device memory, streams and the autograd tape; every op below runs a
+hand-written gfx950 kernel and every backward (input gradients only -- forces and
+stress never need weight gradients) runs one as well.  There is no CPU fallback: the
+ops raise on non-ROCm tensors.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+
+D = 128
+
+# Optional per-launch timing (bench.py): name -> list of (start, end, info) HIP events
+# recorded on the launch stream around each kernel call.
+_TIMING: dict | None = None
+
+
+def enable_timing(on: bool = True) -> dict | None:
+    """Start (or stop) recording HIP events around every kernel launch of this module."""
+    global _TIMING
+    _TIMING = {} if on else None
+    return _TIMING
+
+
+class _timed:
+    __slots__ = ("name", "info", "ev")
+
+    def __init__(self, name, info):
+        self.name, self.info, self.ev = name, info, None
+
+    def __enter__(self):
+        if _TIMING is not None:
+            self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            self.ev[0].record()
+
+    def __exit__(self, *exc):
+        if self.ev is not None:
+            self.ev[1].record()
+            _TIMING.setdefault(self.name, []).append((self.ev[0], self.ev[1], self.info))
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check_dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("matris_amd ops run on the ROCm device only (no CPU fallback)")
+
+
+def _f32c(t):
+    if t.dtype != torch.float32:
+        raise TypeError(f"expected float32, got {t.dtype}")
+    return t if t.is_contiguous() else t.contiguous()
+
+
+@dataclass
+class Grouping:
+    """Rows grouped by an int32 key: rows of segment s are perm[rowptr[s]:rowptr[s+1]]
+    (perm None = identity, i.e. rows already sorted by key)."""
+
+    key: torch.Tensor        # int32 [R], segment of each row
+    rowptr: torch.Tensor     # int32 [S+1]
+    perm: torch.Tensor | None  # int32 [R] or None
+    n_seg: int
+
+    @property
+    def n_rows(self) -> int:
+        return int(self.key.numel())
+
+    @staticmethod
+    def build(key: torch.Tensor, n_seg: int, sorted_rows: bool = False) -> "Grouping":
+        """Stable CSR of `key` (contiguous int32 device tensor) through matris_csr_build.
+        sorted_rows: the caller guarantees key is non-decreasing (perm is the identity)."""
+        _check_dev(key)
+        if key.dtype != torch.int32 or not key.is_contiguous():
+            raise TypeError("Grouping keys must be contiguous int32")
+        lib = _lib.load()
+        R = key.numel()
+        dev = key.device
+        rowptr = torch.empty(n_seg + 1, dtype=torch.int32, device=dev)
+        perm = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
+        ws_bytes = lib.matris_csr_workspace_bytes(R, n_seg)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.matris_csr_build(R, _p(key), 1, n_seg, _p(rowptr), _p(perm), _p(ws), ws_bytes, _stream()),
+                   "matris_csr_build")
+        return Grouping(key, rowptr, None if sorted_rows else perm[:R], n_seg)
+
+
+# ------------------------------------------------------------------------------------
+# segment sum / gather
+# ------------------------------------------------------------------------------------
+def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D, col_off: int = 0,
+                out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    lib = _lib.load()
+    if out is None:
+        out = torch.empty(grp.n_seg, D, dtype=torch.float32, device=x.device)
+    with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
+        _lib.check(lib.matris_seg_sum(_p(x), ldx, col_off, _p(grp.rowptr), _p(grp.perm), grp.n_seg, scale,
+                                      int(accumulate), _p(out), _stream()), "matris_seg_sum")
+    return out
+
+
+def gather_raw(src: torch.Tensor, idx: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    lib = _lib.load()
+    out = torch.empty(idx.numel(), D, dtype=torch.float32, device=src.device)
+    _lib.check(lib.matris_gather_rows(_p(src), _p(idx), idx.numel(), scale, 0, _p(out), _stream()),
+               "matris_gather_rows")
+    return out
+
+
+class _SegSum(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, grp: Grouping, scale: float):
+        _check_dev(x)
+        x = _f32c(x)
+        ctx.grp, ctx.scale = grp, scale
+        return seg_sum_raw(x, grp, scale)
+
+    @staticmethod
+    def backward(ctx, g):
+        g = _f32c(g)
+        return gather_raw(g, ctx.grp.key, ctx.scale), None, None
+
+
+class _Gather(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, grp: Grouping):
+        _check_dev(src)
+        src = _f32c(src)
+        ctx.grp = grp
+        return gather_raw(src, grp.key)
+
+    @staticmethod
+    def backward(ctx, g):
+        g = _f32c(g)
+        return seg_sum_raw(g, ctx.grp), None
+
+
+def seg_sum(x, grp: Grouping, scale: float = 1.0):
+    """out[s] = scale * sum of x rows with key s (aggregate(), functions.py:129-160)."""
+    return _SegSum.apply(x, grp, scale)
+
+
+def gather(src, grp: Grouping):
+    """src[grp.key] (torch.index_select), with a deterministic CSR backward."""
+    return _Gather.apply(src, grp)
+
+
+# ------------------------------------------------------------------------------------
+# segment attention
+# ------------------------------------------------------------------------------------
+class _SegAttn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp):
+        _check_dev(alpha_t, alpha_s, e)
+        alpha_t, alpha_s, e = _f32c(alpha_t), _f32c(alpha_s), _f32c(e)
+        lib = _lib.load()
+        R, S = e.shape[0], tgt.n_seg
+        dev = e.device
+        y_t = torch.empty(S, D, device=dev)
+        y_s = torch.empty(S, D, device=dev)
+        lse_t = torch.empty(S, D, device=dev)
+        lse_s = torch.empty(S, D, device=dev)
+        aidx = alpha_grp.key if alpha_grp is not None else None
+        name = "attn_fwd_atom" if aidx is not None else "attn_fwd_line"
+        with _timed(name, (R, S, src.perm is not None)):
+            _lib.check(lib.matris_attn_fwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(aidx), _p(e), _p(tgt.rowptr),
+                                           _p(tgt.perm), _p(src.rowptr), _p(src.perm), _p(y_t), _p(y_s),
+                                           _p(lse_t), _p(lse_s), _stream()), "matris_attn_fwd")
+        ctx.save_for_backward(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s)
+        ctx.tgt, ctx.src, ctx.alpha_grp = tgt, src, alpha_grp
+        return y_t, y_s
+
+    @staticmethod
+    def backward(ctx, g_yt, g_ys):
+        alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s = ctx.saved_tensors
+        g_yt = torch.zeros_like(y_t) if g_yt is None else _f32c(g_yt)
+        g_ys = torch.zeros_like(y_s) if g_ys is None else _f32c(g_ys)
+        lib = _lib.load()
+        R, S = e.shape[0], ctx.tgt.n_seg
+        g_at = torch.empty(R, D, device=e.device)
+        g_as = torch.empty(R, D, device=e.device)
+        g_e = torch.empty(R, D, device=e.device)
+        ag = ctx.alpha_grp
+        with _timed("attn_bwd_atom" if ag is not None else "attn_bwd_line", (R, S)):
+            _lib.check(lib.matris_attn_bwd(R, S, _p(alpha_t), _p(alpha_s), D,
+                                           _p(ag.key if ag is not None else None), _p(e), _p(ctx.tgt.key),
+                                           _p(ctx.src.key), _p(y_t), _p(y_s), _p(lse_t), _p(lse_s), _p(g_yt),
+                                           _p(g_ys), _p(g_at), _p(g_as), _p(g_e), _stream()), "matris_attn_bwd")
+        if ag is not None:  # alpha rows were read through alpha_grp.key: reduce back
+            g_at = seg_sum_raw(g_at, ag)
+            g_as = seg_sum_raw(g_as, ag)
+        return g_at, g_as, g_e, None, None, None
+
+
+def seg_attention(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: Grouping | None = None):
+    """(y_t, y_s): Dimwise_softmax of alpha by target / source segment times e, summed
+    per segment (interaction_block.py:113-134)."""
+    return _SegAttn.apply(alpha_t, alpha_s, e, tgt, src, alpha_grp)
+
+
+# ------------------------------------------------------------------------------------
+# fused gated MLP
+# ------------------------------------------------------------------------------------
+class GmlpPack:
+    """Packed / transposed GatedMLP weights, rebuilt when a parameter changes."""
+
+    def __init__(self):
+        self.sig = None
+
+    def get(self, mod):
+        params = (mod.mlp_core.layers[0].weight, mod.mlp_core.layers[0].bias, mod.mlp_core.layers[3].weight,
+                  mod.mlp_core.layers[3].bias, mod.mlp_gate.layers[0].weight, mod.mlp_gate.layers[0].bias,
+                  mod.mlp_gate.layers[3].weight, mod.mlp_gate.layers[3].bias, mod.core_norm.weight,
+                  mod.gate_norm.weight)
+        sig = tuple((p.data_ptr(), p._version, p.device) for p in params)
+        if sig != self.sig:
+            with torch.no_grad():
+                c1w, c1b, c2w, c2b, g1w, g1b, g2w, g2b, nc, ng = (p.detach().float() for p in params)
+                self.w1 = torch.cat([c1w, g1w], 0).contiguous()
+                self.b1 = torch.cat([c1b, g1b], 0).contiguous()
+                self.w2 = torch.cat([c2w, g2w], 0).contiguous()
+                self.b2 = torch.cat([c2b, g2b], 0).contiguous()
+                self.w1t = self.w1.t().contiguous()
+                self.w2t = self.w2.t().contiguous()
+                self.nc = nc.contiguous()
+                self.ng = ng.contiguous()
+                eps = mod.core_norm.eps
+                self.eps = float(torch.finfo(torch.float32).eps if eps is None else eps)
+            self.sig = sig
+        return self
+
+
+class _GatedMLP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pack, groupings, n_rows, *srcs):
+        _check_dev(*srcs)
+        srcs = [_f32c(s) for s in srcs]
+        lib = _lib.load()
+        nsrc = len(srcs)
+        dev = srcs[0].device
+        out = torch.empty(n_rows, D, device=dev)
+        p = torch.empty(n_rows, 256, device=dev)
+        z = torch.empty(n_rows, 256, device=dev)
+        src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
+        idx_arr = (ctypes.c_void_p * 4)(*[(g.key.data_ptr() if g is not None else None) for g in groupings])
+        with _timed("gmlp_fwd", (n_rows, nsrc * D)):
+            _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.w1), _p(pack.b1), _p(pack.w2),
+                                           _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps, _p(out), _p(p), _p(z),
+                                           _stream()), "matris_gmlp_fwd")
+        ctx.save_for_backward(p, z)
+        ctx.pack, ctx.groupings = pack, groupings
+        ctx.src_rows = [s.shape[0] for s in srcs]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        p, z = ctx.saved_tensors
+        g = _f32c(g)
+        lib = _lib.load()
+        pack = ctx.pack
+        M = p.shape[0]
+        K = D * len(ctx.groupings)
+        g_x = torch.empty(M, K, device=g.device)
+        with _timed("gmlp_bwd", (M, K)):
+            _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.w1t), _p(pack.w2t), _p(pack.nc),
+                                           _p(pack.ng), pack.eps, _p(g_x), _stream()), "matris_gmlp_bwd")
+        grads = []
+        for j, grp in enumerate(ctx.groupings):
+            if not ctx.needs_input_grad[3 + j]:
+                grads.append(None)
+            elif grp is None:
+                grads.append(g_x[:, j * D:(j + 1) * D])
+            else:
+                out = torch.empty(ctx.src_rows[j], D, device=g.device)
+                seg_sum_raw(g_x, grp, 1.0, ldx=K, col_off=j * D, out=out)
+                grads.append(out)
+        return (None, None, None, *grads)
+
+
+def gated_mlp(module, pack: GmlpPack, sources):
+    """GatedMLP(cat_j src_j[idx_j]) fused on MFMA.  sources: list of (tensor, Grouping|None);
+    a Grouping's key is the gather index, its CSR serves the backward scatter."""
+    groupings = [g for _, g in sources]
+    first = sources[0]
+    n_rows = first[1].n_rows if first[1] is not None else first[0].shape[0]
+    return _GatedMLP.apply(pack.get(module), groupings, n_rows, *[t for t, _ in sources])

@@ -58,33 +58,20 @@ static double pair_dist(const double *ci, const double *cj, const double *L, lon
     return sqrt(d2);
 }
 
-/* Number of periodic images needed along each axis: |n_k + df_k| * h_k <= r with h_k the
- * interplanar spacing; a superset is fine because the distance test decides. */
-static void image_range(long n, const double *frac, const double *L, const int *pbc, double r,
-                        long *lo, long *hi) {
-    double a[3][3];
-    memcpy(a, L, sizeof(a));
+/* r / h_k per axis, h_k the interplanar spacing of the planes spanned by the other two
+ * lattice vectors.  A displacement with fractional component x_k along axis k has length
+ * at least |x_k| h_k, so only images with |df_k + n_k| <= r / h_k can be within r. */
+static void reach(const double *L, double r, double *rk) {
     double cr[3][3];
     for (int k = 0; k < 3; ++k) {
-        const double *u = a[(k + 1) % 3], *v = a[(k + 2) % 3];
+        const double *u = L + 3 * ((k + 1) % 3), *v = L + 3 * ((k + 2) % 3);
         cr[k][0] = u[1] * v[2] - u[2] * v[1];
         cr[k][1] = u[2] * v[0] - u[0] * v[2];
         cr[k][2] = u[0] * v[1] - u[1] * v[0];
     }
-    double vol = fabs(a[0][0] * cr[0][0] + a[0][1] * cr[0][1] + a[0][2] * cr[0][2]);
-    for (int k = 0; k < 3; ++k) {
-        if (!pbc[k]) { lo[k] = hi[k] = 0; continue; }
-        double h = vol / sqrt(cr[k][0] * cr[k][0] + cr[k][1] * cr[k][1] + cr[k][2] * cr[k][2]);
-        double fmin = 0.0, fmax = 0.0;
-        for (long i = 0; i < n; ++i) {
-            double f = frac[i * 3 + k];
-            if (i == 0 || f < fmin) fmin = f;
-            if (i == 0 || f > fmax) fmax = f;
-        }
-        double span = fmax - fmin;
-        lo[k] = (long)floor(-r / h - span) - 1;
-        hi[k] = (long)ceil(r / h + span) + 1;
-    }
+    double vol = fabs(L[0] * cr[0][0] + L[1] * cr[0][1] + L[2] * cr[0][2]);
+    for (int k = 0; k < 3; ++k)
+        rk[k] = r / (vol / sqrt(cr[k][0] * cr[k][0] + cr[k][1] * cr[k][1] + cr[k][2] * cr[k][2]));
 }
 
 /* Radius graph in canonical order.  Writes at most `cap` edges; returns the total count
@@ -93,11 +80,17 @@ long og_neighbor_list(long n, const double *frac, const double *lattice, const i
                       double tol, long cap, long *center, long *neighbor, long *image, double *dist) {
     double *cart = (double *)malloc(sizeof(double) * 3 * (n > 0 ? n : 1));
     for (long i = 0; i < n; ++i) frac_to_cart(frac + 3 * i, lattice, cart + 3 * i);
-    long lo[3], hi[3];
-    image_range(n, frac, lattice, pbc, r, lo, hi);
+    double rk[3];
+    reach(lattice, r, rk);
     long count = 0;
     for (long i = 0; i < n; ++i)
-        for (long j = 0; j < n; ++j)
+        for (long j = 0; j < n; ++j) {
+            long lo[3], hi[3];
+            for (int k = 0; k < 3; ++k) {
+                double df = frac[3 * j + k] - frac[3 * i + k];
+                lo[k] = pbc[k] ? (long)ceil(-rk[k] - df - 1e-6) : 0;
+                hi[k] = pbc[k] ? (long)floor(rk[k] - df + 1e-6) : 0;
+            }
             for (long a = lo[0]; a <= hi[0]; ++a)
                 for (long b = lo[1]; b <= hi[1]; ++b)
                     for (long c = lo[2]; c <= hi[2]; ++c) {
@@ -113,6 +106,7 @@ long og_neighbor_list(long n, const double *frac, const double *lattice, const i
                         }
                         ++count;
                     }
+        }
     free(cart);
     return count;
 }

@@ -1,0 +1,83 @@
+"""Write tests/golden/fp64_oracle.npz: the CPU oracle (oracle/model_ref.py) evaluated in
+fp64 on the same graphs and seed-0 weights as the reference golden fixtures.
+
+Purpose: it measures the fp32 noise floor of the reference computation itself
+(|e_ref_fp32 - e_fp64|).  The random-init model's energies are small sums with strong
+cancellation (e.g. C1 e = -1.4e-3 eV/atom, and the three-body basis evaluates spherical
+Bessel functions at x = 1/6 where j_3 ~ x^3/105 cancels between O(1) terms), so the
+reference's own fp32 result differs from fp64 by 1e-5 .. 6e-4 relative.  The GPU parity
+tests report both distances and accept an energy within 1e-5 relative of the reference
+OR no farther from it than twice the reference's own fp32 error.
+
+    python tests/golden/make_fp64.py
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from matris_amd.config import DEFAULT_CONFIG, MATRIS_10M  # noqa: E402
+from oracle.model_ref import MatRISRef  # noqa: E402
+
+
+def graph(z, prefix):
+    dt = torch.float64
+    return dict(atomic_number=torch.tensor(z[prefix + "z"], dtype=torch.int32),
+                atom_frac_coord=torch.tensor(z[prefix + "frac"], dtype=dt),
+                lattice=torch.tensor(z[prefix + "lattice"], dtype=dt),
+                neighbor_image=torch.tensor(z[prefix + "image"], dtype=dt),
+                atom_graph=torch.tensor(z[prefix + "atom_graph"], dtype=torch.int32),
+                directed2undirected=torch.tensor(z[prefix + "d2u"], dtype=torch.int32),
+                undirected2directed=torch.tensor(z[prefix + "u2d"], dtype=torch.int32),
+                line_graph=torch.tensor(z[prefix + "line_graph"], dtype=torch.int32))
+
+
+def model64(cfg):
+    torch.manual_seed(0)
+    m = MatRISRef(**cfg).double()
+    for mod in m.modules():
+        if hasattr(mod, "coef"):
+            mod.coef = mod.coef.double()
+    return m
+
+
+def run(m, graphs):
+    o = m(graphs, task="efsm")
+    return dict(e=o["e"].detach().numpy(), f=torch.cat(o["f"]).detach().numpy(),
+                s=torch.stack(o["s"]).detach().numpy(), m=torch.cat(o["m"]).detach().numpy())
+
+
+def main():
+    torch.set_num_threads(8)
+    out = {}
+    m10 = model64(MATRIS_10M)
+    z = np.load(os.path.join(HERE, "c1_cu4.npz"))
+    for k, v in run(m10, [graph(z, "g_")]).items():
+        out[f"c1_{k}"] = v
+    for k, v in run(model64(DEFAULT_CONFIG), [graph(z, "g_")]).items():
+        out[f"c1l6_{k}"] = v
+    z = np.load(os.path.join(HERE, "cells_small.npz"))
+    for k, v in run(m10, [graph(z, f"g{i}_") for i in range(int(z["n_cells"]))]).items():
+        out[f"cells_{k}"] = v
+    if "--big" in sys.argv:
+        from matris_amd import workloads as W
+        from oracle import graph_ref
+        cr = W.c3_cu864()
+        og = graph_ref.build_graph(cr.frac, cr.lattice, cr.z)
+        g = dict(g_z=cr.z, g_frac=cr.frac, g_lattice=cr.lattice, g_image=og["image"],
+                 g_atom_graph=np.stack([og["center"], og["neighbor"]], 1), g_d2u=og["d2u"], g_u2d=og["u2d"],
+                 g_line_graph=og["line_graph"])
+        for k, v in run(m10, [graph(g, "g_")]).items():
+            out[f"c3_{k}"] = v
+    np.savez_compressed(os.path.join(HERE, "fp64_oracle.npz"), **out)
+    print({k: v.shape for k, v in out.items()})
+
+
+if __name__ == "__main__":
+    main()
