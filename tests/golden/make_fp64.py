@@ -47,7 +47,11 @@ def model64(cfg):
     return m
 
 
-def run(m, graphs):
+def run(m, graphs, energy_only=False):
+    if energy_only:  # forward only: the fp64 autograd tape of C3 does not fit in host memory
+        with torch.no_grad():
+            o = m(graphs, task="em")
+        return dict(e=o["e"].detach().numpy(), m=torch.cat(o["m"]).detach().numpy())
     o = m(graphs, task="efsm")
     return dict(e=o["e"].detach().numpy(), f=torch.cat(o["f"]).detach().numpy(),
                 s=torch.stack(o["s"]).detach().numpy(), m=torch.cat(o["m"]).detach().numpy())
@@ -73,7 +77,7 @@ def main():
         g = dict(g_z=cr.z, g_frac=cr.frac, g_lattice=cr.lattice, g_image=og["image"],
                  g_atom_graph=np.stack([og["center"], og["neighbor"]], 1), g_d2u=og["d2u"], g_u2d=og["u2d"],
                  g_line_graph=og["line_graph"])
-        for k, v in run(m10, [graph(g, "g_")]).items():
+        for k, v in run(m10, [graph(g, "g_")], energy_only=True).items():
             out[f"c3_{k}"] = v
     np.savez_compressed(os.path.join(HERE, "fp64_oracle.npz"), **out)
     print({k: v.shape for k, v in out.items()})

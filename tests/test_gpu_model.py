@@ -71,7 +71,7 @@ def _assert_close(out, ref, tag, ref64=None):
 
 def _fp64(golden, prefix):
     z = golden("fp64_oracle.npz")
-    return {k: z[f"{prefix}_{k}"] for k in "efsm"} if f"{prefix}_e" in z.files else None
+    return {k: z[f"{prefix}_{k}"] for k in "efsm" if f"{prefix}_{k}" in z.files} if f"{prefix}_e" in z.files else None
 
 
 def test_c1_vs_reference_golden(golden):

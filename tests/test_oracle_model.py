@@ -1,0 +1,163 @@
+"""Pins of the CPU model oracle (oracle/model_ref.py) and of the product module tree --
+CPU only.
+
+  * seed-0 state_dict: identical keys and bit-identical tensors to the reference's
+    MatRIS-10M (tests/golden/state_dict_seed0.json written from the reference modules),
+    for the oracle AND for matris_amd.model.MatRIS (drop-in checkpoint compatibility);
+  * e/f/s/m vs the reference's own outputs (golden fixtures);
+  * physics invariants the reference satisfies: sum of forces = 0, symmetric stress,
+    rotation equivariance, forces = -dE/dx and stress = dE/d(strain)/V by fp64 finite
+    differences.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from matris_amd.config import DEFAULT_CONFIG, MATRIS_10M, MATRIS_10M_PARAMS, MATRIS_6M_PARAMS
+from oracle.model_ref import MatRISRef
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _graph(z, p, dt=torch.float32):
+    return dict(atomic_number=torch.tensor(z[p + "z"], dtype=torch.int32),
+                atom_frac_coord=torch.tensor(z[p + "frac"], dtype=dt), lattice=torch.tensor(z[p + "lattice"], dtype=dt),
+                neighbor_image=torch.tensor(z[p + "image"], dtype=dt),
+                atom_graph=torch.tensor(z[p + "atom_graph"], dtype=torch.int32),
+                directed2undirected=torch.tensor(z[p + "d2u"], dtype=torch.int32),
+                undirected2directed=torch.tensor(z[p + "u2d"], dtype=torch.int32),
+                line_graph=torch.tensor(z[p + "line_graph"], dtype=torch.int32))
+
+
+def _fingerprint_ok(model):
+    fp = json.load(open(os.path.join(GOLDEN, "state_dict_seed0.json")))
+    sd = model.state_dict()
+    assert set(sd) == set(fp["tensors"])
+    for k, v in sd.items():
+        assert hashlib.sha256(v.detach().contiguous().numpy().tobytes()).hexdigest() == fp["tensors"][k]["sha256"], k
+    return fp["n_params"]
+
+
+def test_oracle_seed0_weights_match_reference():
+    torch.manual_seed(0)
+    m = MatRISRef(**MATRIS_10M)
+    assert _fingerprint_ok(m) == MATRIS_10M_PARAMS == sum(p.numel() for p in m.parameters())
+    torch.manual_seed(0)
+    assert sum(p.numel() for p in MatRISRef(**DEFAULT_CONFIG).parameters()) == MATRIS_6M_PARAMS
+
+
+def test_product_module_tree_matches_reference():
+    from matris_amd.model import MatRIS
+    torch.manual_seed(0)
+    m = MatRIS(**MATRIS_10M)
+    assert _fingerprint_ok(m) == m.get_params()
+
+
+def _efsm(model, graphs):
+    o = model(graphs, task="efsm")
+    return (o["e"].detach().numpy(), torch.cat([f.detach() for f in o["f"]]).numpy(),
+            torch.stack([s.detach() for s in o["s"]]).numpy(), torch.cat([m.detach() for m in o["m"]]).numpy())
+
+
+@pytest.mark.parametrize("fixture,cfg,prefixes", [
+    ("c1_cu4.npz", MATRIS_10M, ["g_"]),
+    ("cells_small.npz", MATRIS_10M, ["g0_", "g1_", "g2_"]),
+])
+def test_oracle_matches_reference_golden(golden, fixture, cfg, prefixes):
+    z = golden(fixture)
+    torch.manual_seed(0)
+    e, f, s, m = _efsm(MatRISRef(**cfg), [_graph(z, p) for p in prefixes])
+    # same fp32 CPU ops as the reference; only multithreaded reduction order differs
+    assert np.allclose(e, z["e"], rtol=1e-5, atol=0)
+    assert np.abs(f - z["f"]).max() < 1e-6
+    assert np.abs(s - z["s"]).max() < 1e-5 * np.abs(z["s"]).max()
+    assert np.abs(m - z["m"]).max() < 1e-5 * np.abs(z["m"]).max()
+
+
+def test_oracle_default_config_matches_reference_golden(golden):
+    z, zg = golden("c1_cu4_l6.npz"), golden("c1_cu4.npz")
+    torch.manual_seed(0)
+    e, f, s, m = _efsm(MatRISRef(**DEFAULT_CONFIG), [_graph(zg, "g_")])
+    assert np.allclose(e, z["e"], rtol=1e-5, atol=0) and np.abs(s - z["s"]).max() < 1e-5 * np.abs(z["s"]).max()
+
+
+def _model64():
+    torch.manual_seed(0)
+    m = MatRISRef(**MATRIS_10M).double()
+    for mod in m.modules():
+        if hasattr(mod, "coef"):
+            mod.coef = mod.coef.double()
+    return m
+
+
+def test_invariants_sum_forces_symmetric_stress(golden):
+    z = golden("cells_small.npz")
+    f, s = z["f"], z["s"]
+    off = 0
+    for i in range(int(z["n_cells"])):
+        n = len(z[f"g{i}_z"])
+        assert np.abs(f[off:off + n].sum(0)).max() < 1e-5
+        assert np.abs(s[i] - s[i].T).max() < 1e-6 * max(np.abs(s[i]).max(), 1e-12)
+        off += n
+
+
+def test_finite_difference_forces_and_stress_fp64():
+    """f = -dE/dx and s = dE/d(eps)/V (GPa) for the oracle in fp64, on a 3-atom cell.
+    The graph (edge set) is fixed while displacing, as in the reference's autograd."""
+    from matris_amd import workloads as W
+    from oracle import graph_ref
+    rng = np.random.default_rng(21)
+    cr = W.random_cell(rng, 3)
+    og = graph_ref.build_graph(cr.frac, cr.lattice, cr.z)
+    arrays = dict(g_z=cr.z, g_frac=cr.frac, g_lattice=cr.lattice, g_image=og["image"],
+                  g_atom_graph=np.stack([og["center"], og["neighbor"]], 1), g_d2u=og["d2u"], g_u2d=og["u2d"],
+                  g_line_graph=og["line_graph"])
+    m = _model64()
+    out = m([_graph(arrays, "g_", torch.float64)], task="efsm")
+    f = out["f"][0].detach().numpy()
+    s = out["s"][0].detach().numpy()
+    n = len(cr)
+    etot = lambda frac, lat: float(m([_graph(dict(arrays, g_frac=frac, g_lattice=lat), "g_", torch.float64)],
+                                       task="e")["e"].item()) * n
+    h = 1e-5
+    inv = np.linalg.inv(cr.lattice)
+    for a in range(n):
+        for k in range(3):
+            dx = np.zeros(3); dx[k] = h
+            fp, fm = cr.frac.copy(), cr.frac.copy()
+            fp[a] += dx @ inv; fm[a] -= dx @ inv
+            fd = -(etot(fp, cr.lattice) - etot(fm, cr.lattice)) / (2 * h)
+            assert abs(fd - f[a, k]) < 1e-6 + 1e-5 * abs(f[a, k]), (a, k, fd, f[a, k])
+    vol = abs(np.linalg.det(cr.lattice))
+    for i, j in ((0, 0), (1, 2), (2, 2)):
+        eps = np.zeros((3, 3)); eps[i, j] = eps[j, i] = h / (2 if i != j else 1)
+        lp = cr.lattice @ (np.eye(3) + eps); lm = cr.lattice @ (np.eye(3) - eps)
+        de = (etot(cr.frac, lp) - etot(cr.frac, lm)) / (2 * h)
+        fd = de / vol * 160.21766208  # d/d(eps_ij) with eps applied as sym(eps)
+        assert abs(fd - s[i, j]) < 1e-6 + 1e-5 * abs(s[i, j]), (i, j, fd, s[i, j])
+
+
+def test_rotation_equivariance_fp64():
+    from matris_amd import workloads as W
+    from oracle import graph_ref
+    rng = np.random.default_rng(22)
+    cr = W.random_cell(rng, 4)
+    og = graph_ref.build_graph(cr.frac, cr.lattice, cr.z)
+    arrays = dict(g_z=cr.z, g_frac=cr.frac, g_lattice=cr.lattice, g_image=og["image"],
+                  g_atom_graph=np.stack([og["center"], og["neighbor"]], 1), g_d2u=og["d2u"], g_u2d=og["u2d"],
+                  g_line_graph=og["line_graph"])
+    th = 0.7
+    R = np.array([[np.cos(th), -np.sin(th), 0], [np.sin(th), np.cos(th), 0], [0, 0, 1]]) @ \
+        np.array([[1, 0, 0], [0, np.cos(0.3), -np.sin(0.3)], [0, np.sin(0.3), np.cos(0.3)]])
+    m = _model64()
+    o1 = m([_graph(arrays, "g_", torch.float64)], task="efsm")
+    o2 = m([_graph(dict(arrays, g_lattice=cr.lattice @ R.T), "g_", torch.float64)], task="efsm")
+    assert abs(o1["e"].item() - o2["e"].item()) < 1e-10
+    f1, f2 = o1["f"][0].detach().numpy(), o2["f"][0].detach().numpy()
+    assert np.abs(f1 @ R.T - f2).max() < 1e-9
+    s1, s2 = o1["s"][0].detach().numpy(), o2["s"][0].detach().numpy()
+    assert np.abs(R @ s1 @ R.T - s2).max() < 1e-8
