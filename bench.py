@@ -33,6 +33,8 @@ def _parse():
     ap.add_argument("--workload", default="C3", choices=["C3"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-reps", type=int, default=3, help="fcc reps of the CPU baseline sample")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one plain device copy of this many MiB first (HBM counter calibration)")
     return ap.parse_args()
 
 
@@ -119,6 +121,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cr = W.c3_cu864()
     torch.manual_seed(0)
     model = MatRIS(**MATRIS_10M).to(dev).eval()

@@ -9,9 +9,10 @@
 // Work-group = 4 wave64s, BM = 64 rows.  GEMM1 streams K in 32-wide chunks through LDS
 // (X chunk gathered row by row, W1 chunk), register-prefetching the next chunk while
 // the current one feeds v_mfma_f32_32x32x2f32; each wave owns 64 output columns (a 2x2
-// grid of 32x32 tiles).  h never leaves LDS: GEMM2 reads it as the A operand, RMSNorm
-// reductions go through cross-lane shuffles plus a 64-row LDS exchange, and the
-// core * gate product is formed through LDS.  p and z are written for the backward.
+// grid of 32x32 tiles).  The [64, 256] result tile goes through LDS: p is copied out
+// with 16-byte row stores, h = SiLU(p) stays in LDS as GEMM2's A operand, z returns to
+// LDS, is copied out, and a row-per-wave epilogue applies RMSNorm, SiLU, sigmoid and
+// the product with 512-byte row stores.  p and z are written for the backward.
 //
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
@@ -86,6 +87,20 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
 // ------------------------------------------------------------------------------------
 // forward
 // ------------------------------------------------------------------------------------
+// Copy a [BM, 256] LDS tile (row stride LDH) to global rows of 256 floats with 16-byte
+// stores: consecutive threads cover consecutive 16 B of a row (1 KB per row).
+__device__ __forceinline__ void store_tile256(const float *tile, float *__restrict__ dst, int64_t m0, int64_t M,
+                                              int tid) {
+#pragma unroll
+    for (int it = 0; it < (BM * 64) / 256; ++it) {
+        const int q = it * 256 + tid;  // float4 index within the tile
+        const int row = q >> 6, c4 = (q & 63) * 4;
+        if (m0 + row < M)
+            *reinterpret_cast<float4 *>(dst + (m0 + row) * 256 + c4) =
+                *reinterpret_cast<const float4 *>(tile + row * LDH + c4);
+    }
+}
+
 __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src,
                                                           const float *__restrict__ W1, const float *__restrict__ b1,
                                                           const float *__restrict__ W2, const float *__restrict__ b2,
@@ -94,10 +109,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                           float *__restrict__ out, float *__restrict__ save_p,
                                                           float *__restrict__ save_z) {
     __shared__ __align__(16) float smem[BM * LDH];
-    __shared__ float red[4 * BM];
     float *Xs = smem;
     float *Ws = smem + BM * LDX;
-    float *Hs = smem;
+    float *Ts = smem;  // [BM, 256] tile: p, then h, then z
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
@@ -108,47 +122,54 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     const int xr = tid >> 2, xc = (tid & 3) * 8;
     const int64_t grow = m0 + xr;
     const bool xvalid = grow < M;
-    int64_t srow[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (j < nsrc && xvalid) srow[j] = src.idx[j] ? (int64_t)src.idx[j][grow] : grow;
+    int64_t sr0 = 0, sr1 = 0, sr2 = 0, sr3 = 0;
+    if (xvalid) {
+        sr0 = src.idx[0] ? (int64_t)src.idx[0][grow] : grow;
+        if (nsrc > 1) sr1 = src.idx[1] ? (int64_t)src.idx[1][grow] : grow;
+        if (nsrc > 2) sr2 = src.idx[2] ? (int64_t)src.idx[2][grow] : grow;
+        if (nsrc > 3) sr3 = src.idx[3] ? (int64_t)src.idx[3][grow] : grow;
+    }
+    const float *__restrict__ wrow = W1 + (int64_t)tid * K;  // W1 row `tid` feeds LDS row `tid`
 
-    float4 xreg[2], wreg[8];
-    auto load_chunk = [&](int kc) {
-        const int j = kc >> 7, cc = kc & 127;
-        const float *sp = src.ptr[0];
-        int64_t sr = srow[0];
-#pragma unroll
-        for (int q = 1; q < 4; ++q)
-            if (j == q) { sp = src.ptr[q]; sr = srow[q]; }
-        if (xvalid) {
-            const float4 *xp = reinterpret_cast<const float4 *>(sp + sr * MATRIS_D + cc + xc);
-            xreg[0] = xp[0];
-            xreg[1] = xp[1];
-        } else {
-            xreg[0] = xreg[1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        const float4 *wp = reinterpret_cast<const float4 *>(W1 + (int64_t)tid * K + kc);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) wreg[q] = wp[q];
-    };
+    float4 x0, x1, w0, w1, w2, w3, w4, w5, w6, w7;
+#define GMLP_LOAD(kc)                                                                                    \
+    do {                                                                                                 \
+        const int j_ = (kc) >> 7, cc_ = (kc) & 127;                                                      \
+        const float *sp_ = j_ == 0 ? src.ptr[0] + sr0 * MATRIS_D                                         \
+                         : j_ == 1 ? src.ptr[1] + sr1 * MATRIS_D                                         \
+                         : j_ == 2 ? src.ptr[2] + sr2 * MATRIS_D                                         \
+                                   : src.ptr[3] + sr3 * MATRIS_D;                                        \
+        if (xvalid) {                                                                                    \
+            const float4 *xp_ = reinterpret_cast<const float4 *>(sp_ + cc_ + xc);                        \
+            x0 = xp_[0];                                                                                 \
+            x1 = xp_[1];                                                                                 \
+        } else {                                                                                         \
+            x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);                                                   \
+        }                                                                                                \
+        const float4 *wp_ = reinterpret_cast<const float4 *>(wrow + (kc));                               \
+        w0 = wp_[0]; w1 = wp_[1]; w2 = wp_[2]; w3 = wp_[3];                                              \
+        w4 = wp_[4]; w5 = wp_[5]; w6 = wp_[6]; w7 = wp_[7];                                              \
+    } while (0)
 
     v16f acc[2][2];
     zero_acc(acc);
-    load_chunk(0);
+    GMLP_LOAD(0);
     for (int kc = 0; kc < K; kc += BK) {
         __syncthreads();
-        *reinterpret_cast<float4 *>(Xs + xr * LDX + xc) = xreg[0];
-        *reinterpret_cast<float4 *>(Xs + xr * LDX + xc + 4) = xreg[1];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) *reinterpret_cast<float4 *>(Ws + tid * LDW + 4 * q) = wreg[q];
+        float4 *xs = reinterpret_cast<float4 *>(Xs + xr * LDX + xc);
+        xs[0] = x0;
+        xs[1] = x1;
+        float4 *ws = reinterpret_cast<float4 *>(Ws + tid * LDW);
+        ws[0] = w0; ws[1] = w1; ws[2] = w2; ws[3] = w3;
+        ws[4] = w4; ws[5] = w5; ws[6] = w6; ws[7] = w7;
         __syncthreads();
-        if (kc + BK < K) load_chunk(kc + BK);
+        if (kc + BK < K) GMLP_LOAD(kc + BK);
         mfma_chunk<2, 2>(acc, Xs, LDX, Ws + (wave * 64) * LDW, LDW, lane);
     }
-    __syncthreads();  // all waves are done with Xs / Ws before Hs overwrites them
+#undef GMLP_LOAD
+    __syncthreads();  // all waves are done with Xs / Ws before the tile overwrites them
 
-    // GEMM1 epilogue: bias, save p, SiLU into LDS
+    // p = acc + b1 -> LDS; copy p out with wide stores; h = SiLU(p) in place
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int col = wave * 64 + ct * 32 + l32;
@@ -156,12 +177,17 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = rt * 32 + acc_row(i, h);
-                const float p = acc[rt][ct][i] + bias;
-                if (save_p && m0 + row < M) save_p[(m0 + row) * 256 + col] = p;
-                Hs[row * LDH + col] = silu_f(p);
-            }
+            for (int i = 0; i < 16; ++i) Ts[(rt * 32 + acc_row(i, h)) * LDH + col] = acc[rt][ct][i] + bias;
+    }
+    __syncthreads();
+    if (save_p) store_tile256(Ts, save_p, m0, M, tid);
+#pragma unroll
+    for (int it = 0; it < (BM * 64) / 256; ++it) {
+        const int q = it * 256 + tid;
+        float4 *t = reinterpret_cast<float4 *>(Ts + (q >> 6) * LDH + (q & 63) * 4);
+        float4 v = *t;
+        v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
+        *t = v;
     }
     __syncthreads();
 
@@ -170,15 +196,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     zero_acc(acc);
 #pragma unroll
     for (int kc = 0; kc < MATRIS_D; kc += BK)
-        mfma_chunk<2, 2>(acc, Hs + blk * MATRIS_D + kc, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D + kc, MATRIS_D,
+        mfma_chunk<2, 2>(acc, Ts + blk * MATRIS_D + kc, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D + kc, MATRIS_D,
                          lane);
-
-    // bias, save z, per-row sum of squares over this wave's 64 columns
-    float zsq[2][16];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) zsq[rt][i] = 0.f;
+    __syncthreads();  // every wave is done reading h
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int col = wave * 64 + ct * 32 + l32;
@@ -186,65 +206,24 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = rt * 32 + acc_row(i, h);
-                const float z = acc[rt][ct][i] + bias;
-                acc[rt][ct][i] = z;
-                if (save_z && m0 + row < M) save_z[(m0 + row) * 256 + col] = z;
-                zsq[rt][i] += z * z;
-            }
-    }
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float v = half_sum(zsq[rt][i]);
-            if (l32 == 0) red[wave * BM + rt * 32 + acc_row(i, h)] = v;
-        }
-    __syncthreads();  // red complete; every wave is past GEMM2 (Hs free)
-
-    const float *nw = blk ? norm_g : norm_c;
-    float act[2][2][16];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int row = rt * 32 + acc_row(i, h);
-            const float ss = red[wave * BM + row] + red[(wave ^ 1) * BM + row];
-            const float rinv = rsqrtf(ss * (1.0f / MATRIS_D) + eps);
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const int lc = (wave & 1) * 64 + ct * 32 + l32;  // column inside the block
-                const float a = acc[rt][ct][i] * rinv * nw[lc];
-                act[rt][ct][i] = blk ? sigm_f(a) : silu_f(a);
-            }
-        }
-    // gate -> LDS (reusing the h tile), then core * gate
-    float *Gs = smem;
-    if (blk == 1) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int row = rt * 32 + acc_row(i, h);
-                    const int lc = (wave & 1) * 64 + ct * 32 + l32;
-                    Gs[row * LDH + lc] = act[rt][ct][i];
-                }
+            for (int i = 0; i < 16; ++i) Ts[(rt * 32 + acc_row(i, h)) * LDH + col] = acc[rt][ct][i] + bias;
     }
     __syncthreads();
-    if (blk == 0) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int row = rt * 32 + acc_row(i, h);
-                    const int lc = (wave & 1) * 64 + ct * 32 + l32;
-                    if (m0 + row < M) out[(m0 + row) * MATRIS_D + lc] = act[rt][ct][i] * Gs[row * LDH + lc];
-                }
+    if (save_z) store_tile256(Ts, save_z, m0, M, tid);
+
+    // row epilogue: wave w -> rows [16w, 16w+16); lane -> columns 2l, 2l+1 of each half
+    const float2 wc = *reinterpret_cast<const float2 *>(norm_c + 2 * lane);
+    const float2 wg = *reinterpret_cast<const float2 *>(norm_g + 2 * lane);
+    for (int rr = 0; rr < BM / 4; ++rr) {
+        const int row = wave * (BM / 4) + rr;
+        const float2 zc = *reinterpret_cast<const float2 *>(Ts + row * LDH + 2 * lane);
+        const float2 zg = *reinterpret_cast<const float2 *>(Ts + row * LDH + MATRIS_D + 2 * lane);
+        const float rc = rsqrtf(wave_sum(zc.x * zc.x + zc.y * zc.y) * (1.0f / MATRIS_D) + eps);
+        const float rg = rsqrtf(wave_sum(zg.x * zg.x + zg.y * zg.y) * (1.0f / MATRIS_D) + eps);
+        float2 o;
+        o.x = silu_f(zc.x * rc * wc.x) * sigm_f(zg.x * rg * wg.x);
+        o.y = silu_f(zc.y * rc * wc.y) * sigm_f(zg.y * rg * wg.y);
+        if (m0 + row < M) *reinterpret_cast<float2 *>(out + (m0 + row) * MATRIS_D + 2 * lane) = o;
     }
 }
 
