@@ -74,6 +74,61 @@ __device__ __forceinline__ void mfma_chunk(v16f (&acc)[NRT][NCT], const float *a
     }
 }
 
+// B fragments of one 32-wide K chunk held in registers: bf[ct][q] = B row (ct*32 + l32),
+// columns 16h + 4q .. +3.  Loading the next chunk's fragments before issuing the current
+// chunk's MFMAs keeps the global (L2) latency off the MFMA stream.
+template <int NCT>
+struct BFrag {
+    float4 v[NCT][4];
+};
+
+template <int NCT>
+__device__ __forceinline__ void load_bfrag(BFrag<NCT> &bf, const float *__restrict__ b_base, int ldb, int lane) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            bf.v[ct][q] = *reinterpret_cast<const float4 *>(b_base + (int64_t)(ct * 32 + l32) * ldb + 16 * h + 4 * q);
+}
+
+template <int NRT, int NCT>
+__device__ __forceinline__ void mfma_chunk_rb(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
+                                              const BFrag<NCT> &bf, int lane) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 a[NRT];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+            a[rt] = *reinterpret_cast<const float4 *>(a_base + (rt * 32 + l32) * lda + 16 * h + 4 * q);
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                acc[rt][ct] = mfma32(a[rt].x, bf.v[ct][q].x, acc[rt][ct]);
+                acc[rt][ct] = mfma32(a[rt].y, bf.v[ct][q].y, acc[rt][ct]);
+                acc[rt][ct] = mfma32(a[rt].z, bf.v[ct][q].z, acc[rt][ct]);
+                acc[rt][ct] = mfma32(a[rt].w, bf.v[ct][q].w, acc[rt][ct]);
+            }
+    }
+}
+
+// acc += A[:, 0:KD] (LDS) * B[0:KD, :] with B read from global as rows of a [n][k]
+// array, one chunk of B fragments prefetched ahead.  KD is a multiple of BK.
+template <int NRT, int NCT, int KD>
+__device__ __forceinline__ void gemm_lds_a_global_b(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
+                                                    const float *__restrict__ b_base, int ldb, int lane) {
+    BFrag<NCT> cur, nxt;
+    load_bfrag<NCT>(cur, b_base, ldb, lane);
+#pragma unroll 1
+    for (int kc = 0; kc < KD; kc += BK) {
+        if (kc + BK < KD) load_bfrag<NCT>(nxt, b_base + kc + BK, ldb, lane);
+        mfma_chunk_rb<NRT, NCT>(acc, a_base + kc, lda, cur, lane);
+        if (kc + BK < KD) cur = nxt;
+    }
+}
+
 template <int NRT, int NCT>
 __device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
 #pragma unroll
@@ -194,10 +249,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // GEMM2: wave w -> z columns [64w, 64w+64); block = w/2 (0 core, 1 gate)
     const int blk = wave >> 1;
     zero_acc(acc);
-#pragma unroll
-    for (int kc = 0; kc < MATRIS_D; kc += BK)
-        mfma_chunk<2, 2>(acc, Ts + blk * MATRIS_D + kc, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D + kc, MATRIS_D,
-                         lane);
+    gemm_lds_a_global_b<2, 2, MATRIS_D>(acc, Ts + blk * MATRIS_D, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D,
+                                        MATRIS_D, lane);
     __syncthreads();  // every wave is done reading h
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -242,38 +295,45 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
 
-    // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g)
-    for (int rr = 0; rr < BM / 4; ++rr) {
-        const int row = wave * (BM / 4) + rr;
-        const int64_t m = m0 + row;
-        float gz[4] = {0.f, 0.f, 0.f, 0.f};  // core l, core l+64, gate l, gate l+64
+    // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g).
+    // Wave w owns rows [16w, 16w+16); lane owns columns (2l, 2l+1) of the core and gate
+    // halves.  The next row's z / g_out are loaded before the current row is processed.
+    const float2 wc = *reinterpret_cast<const float2 *>(norm_c + 2 * lane);
+    const float2 wg = *reinterpret_cast<const float2 *>(norm_g + 2 * lane);
+    const float2 zero2 = make_float2(0.f, 0.f);
+    auto ld_row = [&](int rr, float2 &zc, float2 &zg, float2 &go) {
+        const int64_t m = m0 + wave * (BM / 4) + rr;
         if (m < M) {
-            const float *zr = Z + m * 256;
-            float zc0 = zr[lane], zc1 = zr[lane + 64], zg0 = zr[128 + lane], zg1 = zr[192 + lane];
-            float go0 = g_out[m * MATRIS_D + lane], go1 = g_out[m * MATRIS_D + lane + 64];
-            float rc = rsqrtf(wave_sum(zc0 * zc0 + zc1 * zc1) * (1.0f / MATRIS_D) + eps);
-            float rg = rsqrtf(wave_sum(zg0 * zg0 + zg1 * zg1) * (1.0f / MATRIS_D) + eps);
-            float wc0 = norm_c[lane], wc1 = norm_c[lane + 64], wg0 = norm_g[lane], wg1 = norm_g[lane + 64];
-            float nc0 = zc0 * rc, nc1 = zc1 * rc, ng0 = zg0 * rg, ng1 = zg1 * rg;
-            float ac0 = nc0 * wc0, ac1 = nc1 * wc1, ag0 = ng0 * wg0, ag1 = ng1 * wg1;
-            float sc0 = sigm_f(ac0), sc1 = sigm_f(ac1);
-            float core0 = ac0 * sc0, core1 = ac1 * sc1;
-            float gate0 = sigm_f(ag0), gate1 = sigm_f(ag1);
-            float gnc0 = go0 * gate0 * (sc0 * (1.f + ac0 * (1.f - sc0))) * wc0;
-            float gnc1 = go1 * gate1 * (sc1 * (1.f + ac1 * (1.f - sc1))) * wc1;
-            float gng0 = go0 * core0 * (gate0 * (1.f - gate0)) * wg0;
-            float gng1 = go1 * core1 * (gate1 * (1.f - gate1)) * wg1;
-            float dc = wave_sum(gnc0 * nc0 + gnc1 * nc1) * (1.0f / MATRIS_D);
-            float dg = wave_sum(gng0 * ng0 + gng1 * ng1) * (1.0f / MATRIS_D);
-            gz[0] = (gnc0 - nc0 * dc) * rc;
-            gz[1] = (gnc1 - nc1 * dc) * rc;
-            gz[2] = (gng0 - ng0 * dg) * rg;
-            gz[3] = (gng1 - ng1 * dg) * rg;
+            zc = *reinterpret_cast<const float2 *>(Z + m * 256 + 2 * lane);
+            zg = *reinterpret_cast<const float2 *>(Z + m * 256 + MATRIS_D + 2 * lane);
+            go = *reinterpret_cast<const float2 *>(g_out + m * MATRIS_D + 2 * lane);
+        } else {
+            zc = zg = go = zero2;
         }
-        G[row * LDH + lane] = gz[0];
-        G[row * LDH + lane + 64] = gz[1];
-        G[row * LDH + 128 + lane] = gz[2];
-        G[row * LDH + 192 + lane] = gz[3];
+    };
+    float2 zc, zg, go, zc_n, zg_n, go_n;
+    ld_row(0, zc, zg, go);
+#pragma unroll 1
+    for (int rr = 0; rr < BM / 4; ++rr) {
+        if (rr + 1 < BM / 4) ld_row(rr + 1, zc_n, zg_n, go_n);
+        const int row = wave * (BM / 4) + rr;
+        const float rc = rsqrtf(wave_sum(zc.x * zc.x + zc.y * zc.y) * (1.0f / MATRIS_D) + eps);
+        const float rg = rsqrtf(wave_sum(zg.x * zg.x + zg.y * zg.y) * (1.0f / MATRIS_D) + eps);
+        const float nc0 = zc.x * rc, nc1 = zc.y * rc, ng0 = zg.x * rg, ng1 = zg.y * rg;
+        const float ac0 = nc0 * wc.x, ac1 = nc1 * wc.y, ag0 = ng0 * wg.x, ag1 = ng1 * wg.y;
+        const float sc0 = sigm_f(ac0), sc1 = sigm_f(ac1);
+        const float core0 = ac0 * sc0, core1 = ac1 * sc1;
+        const float gate0 = sigm_f(ag0), gate1 = sigm_f(ag1);
+        const float gnc0 = go.x * gate0 * (sc0 * (1.f + ac0 * (1.f - sc0))) * wc.x;
+        const float gnc1 = go.y * gate1 * (sc1 * (1.f + ac1 * (1.f - sc1))) * wc.y;
+        const float gng0 = go.x * core0 * (gate0 * (1.f - gate0)) * wg.x;
+        const float gng1 = go.y * core1 * (gate1 * (1.f - gate1)) * wg.y;
+        const float dc = wave_sum(gnc0 * nc0 + gnc1 * nc1) * (1.0f / MATRIS_D);
+        const float dg = wave_sum(gng0 * ng0 + gng1 * ng1) * (1.0f / MATRIS_D);
+        *reinterpret_cast<float2 *>(G + row * LDH + 2 * lane) = make_float2((gnc0 - nc0 * dc) * rc, (gnc1 - nc1 * dc) * rc);
+        *reinterpret_cast<float2 *>(G + row * LDH + MATRIS_D + 2 * lane) =
+            make_float2((gng0 - ng0 * dg) * rg, (gng1 - ng1 * dg) * rg);
+        zc = zc_n; zg = zg_n; go = go_n;
     }
     __syncthreads();
 
@@ -281,10 +341,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     const int blk = wave >> 1;
     v16f acc[2][2];
     zero_acc(acc);
-#pragma unroll
-    for (int kc = 0; kc < MATRIS_D; kc += BK)
-        mfma_chunk<2, 2>(acc, G + blk * MATRIS_D + kc, LDH,
-                         W2t + (int64_t)((wave & 1) * 64) * 256 + blk * MATRIS_D + kc, 256, lane);
+    gemm_lds_a_global_b<2, 2, MATRIS_D>(acc, G + blk * MATRIS_D, LDH,
+                                        W2t + (int64_t)((wave & 1) * 64) * 256 + blk * MATRIS_D, 256, lane);
     // g_p = g_h * SiLU'(p)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -314,9 +372,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
-#pragma unroll 2
-        for (int kc = 0; kc < 256; kc += BK)
-            mfma_chunk<2, 1>(a2, G + kc, LDH, W1t + (int64_t)col0 * 256 + kc, 256, lane);
+        gemm_lds_a_global_b<2, 1, 256>(a2, G, LDH, W1t + (int64_t)col0 * 256, 256, lane);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
