@@ -149,12 +149,22 @@ int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const f
  * fwd writes out [M,128]; save_p / save_z [M,256] (layer-1 pre-activation and layer-2
  * output, both halves) when non-NULL -- the backward needs them.
  * bwd (input gradients only) reads g_out [M,128], p, z and the transposed weights
- * w1t [K,256], w2t [128,256] (w2t[k][n] = w2[n][k]); writes g_x [M,K]. */
+ * w1t [K,256], w2t [128,256] (w2t[k][n] = w2[n][k]); writes g_x [M,K].
+ * mode selects the MFMA arithmetic (fp32 in, fp32 accumulate in every mode):
+ *   MATRIS_MMA_FP32   v_mfma_f32_32x32x2f32 on the fp32 operands;
+ *   MATRIS_MMA_BF16X6 operands split exactly into three bf16 parts, six partial
+ *                     products on v_mfma_f32_32x32x16_bf16 (fp32-grade accuracy);
+ *   MATRIS_MMA_BF16X3 two bf16 parts, three partial products (~2^-16 per product). */
+#define MATRIS_MMA_FP32 0
+#define MATRIS_MMA_BF16X3 3
+#define MATRIS_MMA_BF16X6 6
 int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
                     const float *w1, const float *b1, const float *w2, const float *b2, const float *norm_c,
-                    const float *norm_g, float eps, float *out, float *save_p, float *save_z, void *stream);
+                    const float *norm_g, float eps, float *out, float *save_p, float *save_z, int mode,
+                    void *stream);
 int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const float *w1t,
-                    const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x, void *stream);
+                    const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x, int mode,
+                    void *stream);
 
 #ifdef __cplusplus
 }

@@ -84,8 +84,8 @@ _SIGS = {
     "matris_gather_rows": (_I, [_P, _P, _I64, _F, _I, _P, _P]),
     "matris_attn_fwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P]),
-    "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P]),
+    "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _I, _P]),
+    "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -46,86 +46,127 @@ __device__ __forceinline__ float dsilu_f(float x) {
 // Row of accumulator register i of a 32x32 tile for lane half h.
 __device__ __forceinline__ int acc_row(int i, int h) { return (i >> 2) * 8 + h * 4 + (i & 3); }
 
-// acc[rt][ct] += A[rt*32.., k] * B[k, ct*32..] for a 32-wide K chunk.  A rows are read
-// from LDS at a_base + row * lda; B columns are row n of a [n][k] array at
-// b_base + n * ldb (LDS or global).  Lane half h consumes columns 16h .. 16h+15.
-template <int NRT, int NCT>
-__device__ __forceinline__ void mfma_chunk(v16f (&acc)[NRT][NCT], const float *a_base, int lda, const float *b_base,
-                                           int ldb, int lane) {
-    const int h = lane >> 5, l32 = lane & 31;
+// ------------------------------------------------------------------------------------
+// MFMA precision modes.  MODE 0: fp32 operands on v_mfma_f32_32x32x2f32.  MODE 3 / 6:
+// each fp32 operand is split exactly into bf16 parts x = hi + mid + lo (hi = bf16(x),
+// mid = bf16(x - hi), lo = bf16(x - hi - mid)) and the product is accumulated in fp32 on
+// v_mfma_f32_32x32x16_bf16 from 3 (hi*hi + hi*mid + mid*hi) or 6 (+ hi*lo + mid*mid +
+// lo*hi) partial products.  MODE 6 carries ~24 significant bits per operand, i.e. fp32
+// GEMM accuracy, at 6 x 32 cycles per 32x32x16 block instead of 8 x 64 for MODE 0.
+//
+// Operand fragments of one 32-wide K chunk: per 32-row tile the lane holds 16 values as
+// 4 float4 at columns col4(q): MODE 0 uses columns 16h + 4q (step q*4+c consumes column
+// 16h+4q+c); the bf16 modes use 16(q>>1) + 8h + 4(q&1) (sub-step s consumes the 8
+// columns 16s + 8h .. +7, the k layout of the 32x32x16 instruction).  A and B always use
+// the same permutation of K, so the sum over the chunk is unchanged.
+// ------------------------------------------------------------------------------------
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+template <int MODE>
+__device__ __forceinline__ int col4(int q, int h) {
+    return MODE == 0 ? 16 * h + 4 * q : 16 * (q >> 1) + 8 * h + 4 * (q & 1);
+}
+
+template <int MODE>
+__device__ __forceinline__ void split8(const float4 &u, const float4 &v, v8bf &hi, v8bf &mid, v8bf &lo) {
+    const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float4 a[NRT], b[NCT];
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-            a[rt] = *reinterpret_cast<const float4 *>(a_base + (rt * 32 + l32) * lda + 16 * h + 4 * q);
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-            b[ct] = *reinterpret_cast<const float4 *>(b_base + (int64_t)(ct * 32 + l32) * ldb + 16 * h + 4 * q);
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-                acc[rt][ct] = mfma32(a[rt].x, b[ct].x, acc[rt][ct]);
-                acc[rt][ct] = mfma32(a[rt].y, b[ct].y, acc[rt][ct]);
-                acc[rt][ct] = mfma32(a[rt].z, b[ct].z, acc[rt][ct]);
-                acc[rt][ct] = mfma32(a[rt].w, b[ct].w, acc[rt][ct]);
-            }
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 a = (__bf16)x[j];
+        const float r = x[j] - (float)a;
+        const __bf16 b = (__bf16)r;
+        hi[j] = a;
+        mid[j] = b;
+        if (MODE == 6) lo[j] = (__bf16)(r - (float)b);
     }
 }
 
-// B fragments of one 32-wide K chunk held in registers: bf[ct][q] = B row (ct*32 + l32),
-// columns 16h + 4q .. +3.  Loading the next chunk's fragments before issuing the current
-// chunk's MFMAs keeps the global (L2) latency off the MFMA stream.
-template <int NCT>
-struct BFrag {
-    float4 v[NCT][4];
-};
+__device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 
-template <int NCT>
-__device__ __forceinline__ void load_bfrag(BFrag<NCT> &bf, const float *__restrict__ b_base, int ldb, int lane) {
-    const int h = lane >> 5, l32 = lane & 31;
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
+// acc[rt][ct] += A-tile[rt] * B-tile[ct] for one K chunk given the fragments.
+template <int MODE, int NRT, int NCT>
+__device__ __forceinline__ void chunk_mma(v16f (&acc)[NRT][NCT], const float4 (&a)[NRT][4],
+                                          const float4 (&b)[NCT][4]) {
+    if constexpr (MODE == 0) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            bf.v[ct][q] = *reinterpret_cast<const float4 *>(b_base + (int64_t)(ct * 32 + l32) * ldb + 16 * h + 4 * q);
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) {
+                    acc[rt][ct] = mfma32(a[rt][q].x, b[ct][q].x, acc[rt][ct]);
+                    acc[rt][ct] = mfma32(a[rt][q].y, b[ct][q].y, acc[rt][ct]);
+                    acc[rt][ct] = mfma32(a[rt][q].z, b[ct][q].z, acc[rt][ct]);
+                    acc[rt][ct] = mfma32(a[rt][q].w, b[ct][q].w, acc[rt][ct]);
+                }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            v8bf ah[NRT], am[NRT], al[NRT], bh[NCT], bm[NCT], bl[NCT];
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) split8<MODE>(a[rt][2 * s], a[rt][2 * s + 1], ah[rt], am[rt], al[rt]);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) split8<MODE>(b[ct][2 * s], b[ct][2 * s + 1], bh[ct], bm[ct], bl[ct]);
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) {
+                    if constexpr (MODE == 6) {
+                        acc[rt][ct] = mfma_bf16(al[rt], bh[ct], acc[rt][ct]);
+                        acc[rt][ct] = mfma_bf16(am[rt], bm[ct], acc[rt][ct]);
+                        acc[rt][ct] = mfma_bf16(ah[rt], bl[ct], acc[rt][ct]);
+                    }
+                    acc[rt][ct] = mfma_bf16(am[rt], bh[ct], acc[rt][ct]);
+                    acc[rt][ct] = mfma_bf16(ah[rt], bm[ct], acc[rt][ct]);
+                    acc[rt][ct] = mfma_bf16(ah[rt], bh[ct], acc[rt][ct]);
+                }
+        }
+    }
 }
 
-template <int NRT, int NCT>
-__device__ __forceinline__ void mfma_chunk_rb(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
-                                              const BFrag<NCT> &bf, int lane) {
+// Fragments of NT 32-row tiles of a row-major array (rows t*32 + l32, row stride ld).
+template <int MODE, int NT>
+__device__ __forceinline__ void load_frag(float4 (&f)[NT][4], const float *base, int64_t ld, int lane) {
     const int h = lane >> 5, l32 = lane & 31;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float4 a[NRT];
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-            a[rt] = *reinterpret_cast<const float4 *>(a_base + (rt * 32 + l32) * lda + 16 * h + 4 * q);
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-                acc[rt][ct] = mfma32(a[rt].x, bf.v[ct][q].x, acc[rt][ct]);
-                acc[rt][ct] = mfma32(a[rt].y, bf.v[ct][q].y, acc[rt][ct]);
-                acc[rt][ct] = mfma32(a[rt].z, bf.v[ct][q].z, acc[rt][ct]);
-                acc[rt][ct] = mfma32(a[rt].w, bf.v[ct][q].w, acc[rt][ct]);
-            }
-    }
+        for (int q = 0; q < 4; ++q)
+            f[t][q] = *reinterpret_cast<const float4 *>(base + (int64_t)(t * 32 + l32) * ld + col4<MODE>(q, h));
+}
+
+// acc[rt][ct] += A[rt*32.., k] * B[k, ct*32..] for a 32-wide K chunk; A rows at
+// a_base + row * lda (LDS), B as rows n of a [n][k] array at b_base + n * ldb.
+template <int MODE, int NRT, int NCT>
+__device__ __forceinline__ void mfma_chunk(v16f (&acc)[NRT][NCT], const float *a_base, int lda, const float *b_base,
+                                           int ldb, int lane) {
+    float4 a[NRT][4], b[NCT][4];
+    load_frag<MODE, NRT>(a, a_base, lda, lane);
+    load_frag<MODE, NCT>(b, b_base, ldb, lane);
+    chunk_mma<MODE, NRT, NCT>(acc, a, b);
 }
 
 // acc += A[:, 0:KD] (LDS) * B[0:KD, :] with B read from global as rows of a [n][k]
-// array, one chunk of B fragments prefetched ahead.  KD is a multiple of BK.
-template <int NRT, int NCT, int KD>
+// array, the next chunk's B fragments prefetched while the current one is consumed.
+template <int MODE, int NRT, int NCT, int KD>
 __device__ __forceinline__ void gemm_lds_a_global_b(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
                                                     const float *__restrict__ b_base, int ldb, int lane) {
-    BFrag<NCT> cur, nxt;
-    load_bfrag<NCT>(cur, b_base, ldb, lane);
+    float4 cur[NCT][4], nxt[NCT][4];
+    load_frag<MODE, NCT>(cur, b_base, ldb, lane);
 #pragma unroll 1
     for (int kc = 0; kc < KD; kc += BK) {
-        if (kc + BK < KD) load_bfrag<NCT>(nxt, b_base + kc + BK, ldb, lane);
-        mfma_chunk_rb<NRT, NCT>(acc, a_base + kc, lda, cur, lane);
-        if (kc + BK < KD) cur = nxt;
+        if (kc + BK < KD) load_frag<MODE, NCT>(nxt, b_base + kc + BK, ldb, lane);
+        float4 a[NRT][4];
+        load_frag<MODE, NRT>(a, a_base + kc, lda, lane);
+        chunk_mma<MODE, NRT, NCT>(acc, a, cur);
+        if (kc + BK < KD) {
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cur[ct][q] = nxt[ct][q];
+        }
     }
 }
 
@@ -156,6 +197,7 @@ __device__ __forceinline__ void store_tile256(const float *tile, float *__restri
     }
 }
 
+template <int MODE>
 __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src,
                                                           const float *__restrict__ W1, const float *__restrict__ b1,
                                                           const float *__restrict__ W2, const float *__restrict__ b2,
@@ -219,7 +261,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         ws[4] = w4; ws[5] = w5; ws[6] = w6; ws[7] = w7;
         __syncthreads();
         if (kc + BK < K) GMLP_LOAD(kc + BK);
-        mfma_chunk<2, 2>(acc, Xs, LDX, Ws + (wave * 64) * LDW, LDW, lane);
+        mfma_chunk<MODE, 2, 2>(acc, Xs, LDX, Ws + (wave * 64) * LDW, LDW, lane);
     }
 #undef GMLP_LOAD
     __syncthreads();  // all waves are done with Xs / Ws before the tile overwrites them
@@ -249,7 +291,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // GEMM2: wave w -> z columns [64w, 64w+64); block = w/2 (0 core, 1 gate)
     const int blk = wave >> 1;
     zero_acc(acc);
-    gemm_lds_a_global_b<2, 2, MATRIS_D>(acc, Ts + blk * MATRIS_D, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D,
+    gemm_lds_a_global_b<MODE, 2, 2, MATRIS_D>(acc, Ts + blk * MATRIS_D, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D,
                                         MATRIS_D, lane);
     __syncthreads();  // every wave is done reading h
 #pragma unroll
@@ -283,6 +325,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 // ------------------------------------------------------------------------------------
 // backward
 // ------------------------------------------------------------------------------------
+template <int MODE>
 __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, const float *__restrict__ g_out,
                                                           const float *__restrict__ P, const float *__restrict__ Z,
                                                           const float *__restrict__ W1t,
@@ -341,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     const int blk = wave >> 1;
     v16f acc[2][2];
     zero_acc(acc);
-    gemm_lds_a_global_b<2, 2, MATRIS_D>(acc, G + blk * MATRIS_D, LDH,
+    gemm_lds_a_global_b<MODE, 2, 2, MATRIS_D>(acc, G + blk * MATRIS_D, LDH,
                                         W2t + (int64_t)((wave & 1) * 64) * 256 + blk * MATRIS_D, 256, lane);
     // g_p = g_h * SiLU'(p)
 #pragma unroll
@@ -372,7 +415,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
-        gemm_lds_a_global_b<2, 1, 256>(a2, G, LDH, W1t + (int64_t)col0 * 256, 256, lane);
+        gemm_lds_a_global_b<MODE, 2, 1, 256>(a2, G, LDH, W1t + (int64_t)col0 * 256, 256, lane);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -388,7 +431,8 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host,
                                const int32_t *const *src_idx_host, const float *w1, const float *b1, const float *w2,
                                const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
-                               float *save_p, float *save_z, void *stream) {
+                               float *save_p, float *save_z, int mode, void *stream) {
+    if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
     if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1 || !b1 || !w2 || !b2 || !norm_c || !norm_g || !out)
         return MATRIS_E_ARG;
     if (m == 0) return 0;
@@ -399,22 +443,35 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
         if (j < n_src && (!s.ptr[j] || !aligned16(s.ptr[j]))) return MATRIS_E_ARG;
     }
     if (!aligned16(w1) || !aligned16(w2)) return MATRIS_E_ARG;
-    gmlp_fwd_kernel<<<matris_blocks(m, BM), 256, 0, (hipStream_t)stream>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g,
-                                                                         eps, out, save_p, save_z);
+    const dim3 grid(matris_blocks(m, BM));
+    hipStream_t st = (hipStream_t)stream;
+    if (mode == 0)
+        gmlp_fwd_kernel<0><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
+    else if (mode == 3)
+        gmlp_fwd_kernel<3><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
+    else
+        gmlp_fwd_kernel<6><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
 extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const float *w1t,
                                const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x,
-                               void *stream) {
+                               int mode, void *stream) {
+    if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
     if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1t || !w2t ||
         !norm_c || !norm_g || !g_x)
         return MATRIS_E_ARG;
     if (m == 0) return 0;
     if (!aligned16(w1t) || !aligned16(w2t)) return MATRIS_E_ARG;
-    gmlp_bwd_kernel<<<matris_blocks(m, BM), 256, 0, (hipStream_t)stream>>>(m, k, g_out, p, z, w1t, w2t, norm_c,
-                                                                         norm_g, eps, g_x);
+    const dim3 grid(matris_blocks(m, BM));
+    hipStream_t st = (hipStream_t)stream;
+    if (mode == 0)
+        gmlp_bwd_kernel<0><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
+    else if (mode == 3)
+        gmlp_bwd_kernel<3><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
+    else
+        gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -16,6 +16,20 @@ from .. import _lib
 
 D = 128
 
+# MFMA arithmetic of the fused GatedMLP kernels (include/matris_hip.h MATRIS_MMA_*):
+# 0 = fp32 MFMA, 6 = three-way bf16 split (fp32-grade), 3 = two-way bf16 split.
+MMA_MODES = {"fp32": 0, "bf16x6": 6, "bf16x3": 3}
+_MMA = {"mode": 6}
+
+
+def set_mma_precision(name: str) -> None:
+    """Select the GatedMLP MFMA arithmetic: "bf16x6" (default), "fp32" or "bf16x3"."""
+    _MMA["mode"] = MMA_MODES[name]
+
+
+def get_mma_precision() -> str:
+    return {v: k for k, v in MMA_MODES.items()}[_MMA["mode"]]
+
 # Optional per-launch timing (bench.py): name -> list of (start, end, info) HIP events
 # recorded on the launch stream around each kernel call.
 _TIMING: dict | None = None
@@ -259,7 +273,8 @@ class _GatedMLP(torch.autograd.Function):
         with _timed("gmlp_fwd", (n_rows, nsrc * D)):
             _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.w1), _p(pack.b1), _p(pack.w2),
                                            _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps, _p(out), _p(p), _p(z),
-                                           _stream()), "matris_gmlp_fwd")
+                                           _MMA["mode"], _stream()), "matris_gmlp_fwd")
+        ctx.mode = _MMA["mode"]
         ctx.save_for_backward(p, z)
         ctx.pack, ctx.groupings = pack, groupings
         ctx.src_rows = [s.shape[0] for s in srcs]
@@ -276,7 +291,7 @@ class _GatedMLP(torch.autograd.Function):
         g_x = torch.empty(M, K, device=g.device)
         with _timed("gmlp_bwd", (M, K)):
             _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.w1t), _p(pack.w2t), _p(pack.nc),
-                                           _p(pack.ng), pack.eps, _p(g_x), _stream()), "matris_gmlp_bwd")
+                                           _p(pack.ng), pack.eps, _p(g_x), ctx.mode, _stream()), "matris_gmlp_bwd")
         grads = []
         for j, grp in enumerate(ctx.groupings):
             if not ctx.needs_input_grad[3 + j]:

@@ -139,9 +139,11 @@ class _ShimGated(torch.nn.Module):
         self.core_norm, self.gate_norm = t.nc, t.ng
 
 
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("bf16x3", 1e-4)])
 @pytest.mark.parametrize("nsrc,M", [(3, 1000), (4, 777), (3, 64), (4, 5)])
-def test_gated_mlp_fwd_bwd(nsrc, M):
+def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
     ops = _ops()
+    ops.set_mma_precision(mode)
     torch.manual_seed(nsrc * 100 + M)
     K = 128 * nsrc
     ref = _TorchGMLP(K)
@@ -161,8 +163,11 @@ def test_gated_mlp_fwd_bwd(nsrc, M):
     pack = ops.GmlpPack()
     sd = [s.to(DEV).requires_grad_(True) for s in srcs]
     srcs_spec = [(sd[0], None)] + [(sd[j], ops.Grouping.build(idxs[j].to(DEV), sizes[j])) for j in range(1, nsrc)]
-    out = ops.gated_mlp(mod, pack, srcs_spec)
-    assert _rel(out, out_r) < 1e-5
-    out.backward(g.to(DEV))
-    for j in range(nsrc):
-        assert _rel(sd[j].grad, s64[j].grad) < 1e-5, j
+    try:
+        out = ops.gated_mlp(mod, pack, srcs_spec)
+        assert _rel(out, out_r) < tol
+        out.backward(g.to(DEV))
+        for j in range(nsrc):
+            assert _rel(sd[j].grad, s64[j].grad) < tol, j
+    finally:
+        ops.set_mma_precision("bf16x6")

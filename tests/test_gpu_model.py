@@ -10,6 +10,7 @@ fp32 result is 1.2e-5 .. 6.3e-4 (relative) away from the same computation in fp6
 oracle).  A GPU energy inside that bar is as close to the reference as the reference's
 own fp32 rounding allows; the printed line reports both distances."""
 import hashlib
+import os
 
 import numpy as np
 import pytest
@@ -66,6 +67,8 @@ def _assert_close(out, ref, tag, ref64=None):
     s_err = np.max(np.abs(out["s"] - ref["s"])) / max(np.max(np.abs(ref["s"])), 1e-12)
     m_err = np.max(np.abs(out["m"] - ref["m"])) / max(np.max(np.abs(ref["m"])), 1e-12)
     print(f"{tag}: e_rel={e_err:.2e} f_abs={f_err:.2e} s_rel={s_err:.2e} m_rel={m_err:.2e}", flush=True)
+    with open(os.environ.get("MATRIS_PARITY_LOG", os.devnull), "a") as fh:
+        fh.write(f"{tag}: e_rel={e_err:.3e} f_abs={f_err:.3e} s_rel={s_err:.3e} m_rel={m_err:.3e}\n")
     assert e_ok and f_err <= F_ABS and s_err <= S_REL and m_err <= M_REL
 
 
@@ -105,3 +108,15 @@ def test_c3_gpu_graph_and_efsm_vs_reference_golden(golden):
         a = np.ascontiguousarray(v.cpu().numpy().astype(np.int64))
         assert hashlib.sha256(a.tobytes()).hexdigest() == str(z[f"h_{k}"]), k
     _assert_close(_efsm(model, [g]), z, "C3", _fp64(golden, "c3"))
+
+
+def test_fp32_mma_mode_vs_reference_golden(golden):
+    """The fp32-MFMA GatedMLP mode (MATRIS_MMA_FP32) on the batched triclinic cells."""
+    from matris_amd.model import ops
+    ops.set_mma_precision("fp32")
+    try:
+        z = golden("cells_small.npz")
+        graphs = [_graph_from_arrays(z, f"g{i}_") for i in range(int(z["n_cells"]))]
+        _assert_close(_efsm(_model(), graphs), z, "cells_small fp32-mma", _fp64(golden, "cells"))
+    finally:
+        ops.set_mma_precision("bf16x6")

@@ -65,7 +65,9 @@ def test_arguments_rejected_before_launch(lib):
     # gated MLP: 5 sources, or a K that is not a multiple of 128
     src = (ctypes.c_void_p * 4)()
     assert lib.matris_gmlp_fwd(10, 5, src, None, *([ctypes.c_void_p(16)] * 6), 1e-7, ctypes.c_void_p(16),
-                               None, None, None) == -1001
-    assert lib.matris_gmlp_bwd(10, 200, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), None) == -1001
+                               None, None, 6, None) == -1001
+    assert lib.matris_gmlp_bwd(10, 200, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), 6, None) == -1001
+    # unknown MFMA mode
+    assert lib.matris_gmlp_bwd(10, 256, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), 5, None) == -1001
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
