@@ -166,6 +166,26 @@ int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const 
                     const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x, int mode,
                     void *stream);
 
+/* ------------------------------------------------------------------------------------
+ * Dense layers on MFMA (same `mode` values as the gated MLP), 128-wide rows, no bias.
+ * ------------------------------------------------------------------------------------ */
+
+/* FFN out = W2 SiLU(W1 x): Refinement.node_FFN / edge_FFN, MLP(hidden=int, bias=False)
+ * (matris/model/functions.py:198-205, interaction_block.py:198-210, 269-270).
+ * w1, w2 [128,128] (Linear weights, [out, in]); save_p [M,128] = W1 x (needed by bwd).
+ * bwd: g_x = ((g W2) * SiLU'(p)) W1 with w1t = w1^T, w2t = w2^T. */
+int matris_ffn_fwd(int64_t m, const float *x, const float *w1, const float *w2, float *out, float *save_p, int mode,
+                   void *stream);
+int matris_ffn_bwd(int64_t m, const float *g, const float *p, const float *w1t, const float *w2t, float *g_x,
+                   int mode, void *stream);
+
+/* Attention projection pair (interaction_block.py:33-38, 110-111):
+ * out0 = x W[0:128]^T (source_weight_linear), out1 = x W[128:256]^T (target), w [256,128].
+ * bwd: g_x = g0 W[0:128] + g1 W[128:256] with wt = w^T [128,256]. */
+int matris_pair_fwd(int64_t m, const float *x, const float *w, float *out0, float *out1, int mode, void *stream);
+int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const float *wt, float *g_x, int mode,
+                    void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,223 @@
+// Fused dense layers on gfx950 MFMA for the 128-wide feature rows of the interaction
+// blocks (same fp32 / split-bf16 modes as the gated MLP, see mma.h):
+//
+//   FFN     out = W2 SiLU(W1 x)            node_FFN / edge_FFN of Refinement
+//           (MLP(hidden=int, bias=False), matris/model/functions.py:198-205,
+//            interaction_block.py:198-210, 269-270)
+//   PAIR    (out0, out1) = (x W0^T, x W1^T) source / target attention projections
+//           (interaction_block.py:33-38, 110-111), one [M,128]x[128,256] product
+//
+// and their input-gradient kernels.  Work-group = 4 wave64s over BM = 64 rows; the
+// [64, 128] input tile is staged once in LDS (K = 128 needs no K loop), weight rows are
+// B operands read from global with a one-chunk register prefetch, and intermediate tiles
+// (p, h, g_h) stay in LDS.  Outputs leave through LDS with 16-byte row stores.
+#include "mma.h"
+
+#define LDT 132  // LDS row stride of a [64, 128] tile
+
+// Copy rows [m0, m0+64) x 128 columns of a row-major [*, ld] array into LDS (zeros past M).
+__device__ __forceinline__ void stage_tile128(float *dst, const float *__restrict__ src, int64_t ld, int64_t m0,
+                                              int64_t M, int tid) {
+#pragma unroll
+    for (int it = 0; it < (BM * 32) / 256; ++it) {
+        const int q = it * 256 + tid;
+        const int r = q >> 5, c4 = (q & 31) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m0 + r < M) v = *reinterpret_cast<const float4 *>(src + (m0 + r) * ld + c4);
+        *reinterpret_cast<float4 *>(dst + r * LDT + c4) = v;
+    }
+}
+
+__device__ __forceinline__ void store_tile128(const float *tile, float *__restrict__ dst, int64_t ld, int64_t m0,
+                                              int64_t M, int tid) {
+#pragma unroll
+    for (int it = 0; it < (BM * 32) / 256; ++it) {
+        const int q = it * 256 + tid;
+        const int r = q >> 5, c4 = (q & 31) * 4;
+        if (m0 + r < M)
+            *reinterpret_cast<float4 *>(dst + (m0 + r) * ld + c4) = *reinterpret_cast<const float4 *>(tile + r * LDT + c4);
+    }
+}
+
+// Write a wave's accumulators (rows 0..63, columns col0 + ct*32 + l32) into an LDS tile.
+template <int NCT>
+__device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *tile, int col0, int lane) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tile[(rt * 32 + acc_row(i, h)) * LDT + col0 + ct * 32 + l32] = acc[rt][ct][i];
+}
+
+// ------------------------------------------------------------------------------------
+// FFN forward: p = x W1^T (saved), out = SiLU(p) W2^T
+// ------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float *__restrict__ x,
+                                                         const float *__restrict__ W1, const float *__restrict__ W2,
+                                                         float *__restrict__ out, float *__restrict__ save_p) {
+    __shared__ __align__(16) float T0[BM * LDT];
+    __shared__ __align__(16) float T1[BM * LDT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    stage_tile128(T0, x, MATRIS_D, m0, M, tid);
+    __syncthreads();
+    v16f acc[2][1];
+    zero_acc(acc);
+    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T0, LDT, W1 + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
+    acc_to_lds<1>(acc, T1, wave * 32, lane);
+    __syncthreads();
+    if (save_p) store_tile128(T1, save_p, MATRIS_D, m0, M, tid);
+#pragma unroll
+    for (int it = 0; it < (BM * 32) / 256; ++it) {
+        const int q = it * 256 + tid;
+        float4 *t = reinterpret_cast<float4 *>(T1 + (q >> 5) * LDT + (q & 31) * 4);
+        float4 v = *t;
+        v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
+        *t = v;
+    }
+    __syncthreads();
+    zero_acc(acc);
+    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T1, LDT, W2 + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
+    acc_to_lds<1>(acc, T0, wave * 32, lane);
+    __syncthreads();
+    store_tile128(T0, out, MATRIS_D, m0, M, tid);
+}
+
+// FFN backward: g_x = ((g W2) * SiLU'(p)) W1, with w1t = W1^T, w2t = W2^T row-major.
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
+                                                         const float *__restrict__ P, const float *__restrict__ W1t,
+                                                         const float *__restrict__ W2t, float *__restrict__ g_x) {
+    __shared__ __align__(16) float T0[BM * LDT];
+    __shared__ __align__(16) float T1[BM * LDT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    stage_tile128(T0, g, MATRIS_D, m0, M, tid);
+    __syncthreads();
+    v16f acc[2][1];
+    zero_acc(acc);
+    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T0, LDT, W2t + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
+    const int col = wave * 32 + l32;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = rt * 32 + acc_row(i, h);
+            const float p = (m0 + row < M) ? P[(m0 + row) * MATRIS_D + col] : 0.f;
+            acc[rt][0][i] *= dsilu_f(p);
+        }
+    acc_to_lds<1>(acc, T1, wave * 32, lane);
+    __syncthreads();
+    zero_acc(acc);
+    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T1, LDT, W1t + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
+    acc_to_lds<1>(acc, T0, wave * 32, lane);  // every wave finished reading T0 before the g_h sync
+    __syncthreads();
+    store_tile128(T0, g_x, MATRIS_D, m0, M, tid);
+}
+
+// ------------------------------------------------------------------------------------
+// projection pair: out0 = x W[0:128]^T, out1 = x W[128:256]^T ; backward
+// g_x = g0 W[0:128] + g1 W[128:256]
+// ------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float *__restrict__ x,
+                                                          const float *__restrict__ W, float *__restrict__ out0,
+                                                          float *__restrict__ out1) {
+    __shared__ __align__(16) float T0[BM * LDT];
+    __shared__ __align__(16) float T1[BM * LDT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    stage_tile128(T0, x, MATRIS_D, m0, M, tid);
+    __syncthreads();
+    // wave w -> output columns [64w, 64w+64) of the 256: waves 0,1 -> out0, 2,3 -> out1
+    v16f acc[2][2];
+    zero_acc(acc);
+    gemm_lds_a_global_b<MODE, 2, 2, MATRIS_D>(acc, T0, LDT, W + (int64_t)(wave * 64) * MATRIS_D, MATRIS_D, lane);
+    __syncthreads();  // T0 free
+    acc_to_lds<2>(acc, (wave < 2) ? T0 : T1, (wave & 1) * 64, lane);
+    __syncthreads();
+    store_tile128(T0, out0, MATRIS_D, m0, M, tid);
+    store_tile128(T1, out1, MATRIS_D, m0, M, tid);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
+                                                          const float *__restrict__ g1, const float *__restrict__ Wt,
+                                                          float *__restrict__ g_x) {
+    // Wt = W^T, [128, 256] row-major: g_x[m][k] = sum_n g[m][n] Wt[k][n]
+    __shared__ __align__(16) float T0[BM * LDT];
+    __shared__ __align__(16) float T1[BM * LDT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    stage_tile128(T0, g0, MATRIS_D, m0, M, tid);
+    stage_tile128(T1, g1, MATRIS_D, m0, M, tid);
+    __syncthreads();
+    v16f acc[2][1];
+    zero_acc(acc);
+    const float *wt = Wt + (int64_t)(wave * 32) * 256;
+    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T0, LDT, wt, 256, lane);
+    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T1, LDT, wt + MATRIS_D, 256, lane);
+    __syncthreads();
+    acc_to_lds<1>(acc, T0, wave * 32, lane);
+    __syncthreads();
+    store_tile128(T0, g_x, MATRIS_D, m0, M, tid);
+}
+
+// ------------------------------------------------------------------------------------
+// C ABI
+// ------------------------------------------------------------------------------------
+#define MLP_DISPATCH(KERNEL, ...)                                                         \
+    do {                                                                                  \
+        const dim3 grid_(matris_blocks(m, BM));                                           \
+        hipStream_t st_ = (hipStream_t)stream;                                            \
+        if (mode == 0) KERNEL<0><<<grid_, 256, 0, st_>>>(__VA_ARGS__);                    \
+        else if (mode == 3) KERNEL<3><<<grid_, 256, 0, st_>>>(__VA_ARGS__);               \
+        else KERNEL<6><<<grid_, 256, 0, st_>>>(__VA_ARGS__);                              \
+    } while (0)
+
+static bool mlp_args_ok(int mode, std::initializer_list<const void *> ptrs) {
+    if (mode != 0 && mode != 3 && mode != 6) return false;
+    for (const void *p : ptrs)
+        if (!p || ((uintptr_t)p & 15)) return false;
+    return true;
+}
+
+extern "C" int matris_ffn_fwd(int64_t m, const float *x, const float *w1, const float *w2, float *out,
+                              float *save_p, int mode, void *stream) {
+    if (m < 0 || !mlp_args_ok(mode, {x, w1, w2, out}) || ((uintptr_t)save_p & 15)) return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    MLP_DISPATCH(ffn_fwd_kernel, m, x, w1, w2, out, save_p);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const float *w1t, const float *w2t,
+                              float *g_x, int mode, void *stream) {
+    if (m < 0 || !mlp_args_ok(mode, {g, p, w1t, w2t, g_x})) return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    MLP_DISPATCH(ffn_bwd_kernel, m, g, p, w1t, w2t, g_x);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_pair_fwd(int64_t m, const float *x, const float *w, float *out0, float *out1, int mode,
+                               void *stream) {
+    if (m < 0 || !mlp_args_ok(mode, {x, w, out0, out1})) return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    MLP_DISPATCH(pair_fwd_kernel, m, x, w, out0, out1);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const float *wt, float *g_x, int mode,
+                               void *stream) {
+    if (m < 0 || !mlp_args_ok(mode, {g0, g1, wt, g_x})) return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, wt, g_x);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}

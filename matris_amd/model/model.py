@@ -352,18 +352,24 @@ class Graph_Attention_Layer(nn.Module):
                                               use_fp16=use_fp16)
         self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim), requires_grad=True)
         self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim), requires_grad=True)
+        self._proj = ops._WeightPack()
+
+    def _projections(self, edge_feat):
+        """(source, target) attention logits (:110-111) in one MFMA pass."""
+        lin_s, lin_t = self.source_weight_linear, self.target_weight_linear
+        if lin_s.weight.shape == (128, 128) and lin_s.bias is None and lin_t.bias is None:
+            return ops.proj_pair(self._proj.get(lin_s.weight, lin_t.weight), edge_feat)
+        return lin_s(edge_feat), lin_t(edge_feat)
 
     def forward(self, node_feat, edge_feat, graph, d2u: ops.Grouping | None = None):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
         if d2u is None:  # line graph: edges are the angles themselves
             e = self.edge_nonlinear_update.fused([(edge_feat, None), (node_feat, tgt), (node_feat, src)])
-            a_s = self.source_weight_linear(edge_feat)
-            a_t = self.target_weight_linear(edge_feat)
+            a_s, a_t = self._projections(edge_feat)
             y_t, y_s = ops.seg_attention(a_t, a_s, e, tgt, src)
         else:  # atom graph: undirected bond rows expanded through d2u inside the kernels
             e = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
-            a_s = self.source_weight_linear(edge_feat)
-            a_t = self.target_weight_linear(edge_feat)
+            a_s, a_t = self._projections(edge_feat)
             y_t, y_s = ops.seg_attention(a_t, a_s, e, tgt, src, alpha_grp=d2u)
             e = ops.seg_sum(e, d2u, 0.5)  # mean of the two directed copies (:121-122)
         n = self.node_nonlinear_update.fused([(node_feat, None), (y_t, None), (y_s, None)])
@@ -390,6 +396,17 @@ class Refinement(nn.Module):
         self.learnable_envelope = nn.Linear(num_basis, edge_feat_dim, bias=False)
         self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim), requires_grad=True)
         self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim), requires_grad=True)
+        self._node_ffn = ops._WeightPack()
+        self._edge_ffn = ops._WeightPack()
+
+    @staticmethod
+    def _ffn(mlp, pack, x):
+        """MLP(hidden=int, bias=False) as one fused MFMA kernel (functions.py:198-205)."""
+        L = mlp.layers
+        if (len(L) == 4 and L[0].bias is None and L[3].bias is None and L[0].weight.shape == (128, 128)
+                and L[3].weight.shape == (128, 128) and isinstance(L[1], FusedSiLU)):
+            return ops.ffn(pack.get(L[0].weight, L[3].weight), x)
+        return mlp(x)
 
     def forward(self, node_feat, edge_feat, smooth_weight, graph, d2u: ops.Grouping | None = None, atom_feat=None):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
@@ -404,8 +421,8 @@ class Refinement(nn.Module):
         hw = h * w
         agg = ops.seg_sum(hw, tgt)
         to_edge = hw if (self.graph_type == "atom graph" and self.use_smoothed_for_delta_edge) else h
-        dn = self.node_FFN(agg)
-        de = self.edge_FFN(to_edge)
+        dn = self._ffn(self.node_FFN, self._node_ffn, agg)
+        de = self._ffn(self.edge_FFN, self._edge_ffn, to_edge)
         if self.graph_type == "atom graph":
             de = ops.seg_sum(de, d2u, 0.5)
         return dn + self.node_res_weight * node_feat, de + self.edge_res_weight * edge_feat

@@ -312,3 +312,93 @@ def gated_mlp(module, pack: GmlpPack, sources):
     first = sources[0]
     n_rows = first[1].n_rows if first[1] is not None else first[0].shape[0]
     return _GatedMLP.apply(pack.get(module), groupings, n_rows, *[t for t, _ in sources])
+
+
+# ------------------------------------------------------------------------------------
+# dense layers on MFMA: FFN (Linear -> SiLU -> Linear, no bias) and the projection pair
+# ------------------------------------------------------------------------------------
+class _WeightPack:
+    """Contiguous fp32 weights and their transposes, rebuilt when a parameter changes."""
+
+    def __init__(self):
+        self.sig = None
+
+    def get(self, *params):
+        sig = tuple((p.data_ptr(), p._version, p.device) for p in params)
+        if sig != self.sig:
+            with torch.no_grad():
+                self.w = [p.detach().float().contiguous() for p in params]
+                self.wt = [w.t().contiguous() for w in self.w]
+                self.cat = torch.cat(self.w, 0).contiguous() if len(self.w) > 1 else self.w[0]
+                self.cat_t = self.cat.t().contiguous()
+            self.sig = sig
+        return self
+
+
+class _FFN(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, pack):
+        _check_dev(x)
+        x = _f32c(x)
+        lib = _lib.load()
+        M = x.shape[0]
+        out = torch.empty(M, D, device=x.device)
+        p = torch.empty(M, D, device=x.device)
+        with _timed("ffn_fwd", (M,)):
+            _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.w[0]), _p(pack.w[1]), _p(out), _p(p), _MMA["mode"],
+                                          _stream()), "matris_ffn_fwd")
+        ctx.save_for_backward(p)
+        ctx.pack, ctx.mode = pack, _MMA["mode"]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (p,) = ctx.saved_tensors
+        g = _f32c(g)
+        lib = _lib.load()
+        M = p.shape[0]
+        g_x = torch.empty(M, D, device=g.device)
+        with _timed("ffn_bwd", (M,)):
+            _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(ctx.pack.wt[0]), _p(ctx.pack.wt[1]), _p(g_x), ctx.mode,
+                                          _stream()), "matris_ffn_bwd")
+        return g_x, None
+
+
+def ffn(pack: _WeightPack, x):
+    """W2 SiLU(W1 x) for an MLP(hidden=int, bias=False) (functions.py:198-205)."""
+    return _FFN.apply(x, pack)
+
+
+class _Pair(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, pack):
+        _check_dev(x)
+        x = _f32c(x)
+        lib = _lib.load()
+        M = x.shape[0]
+        o0 = torch.empty(M, D, device=x.device)
+        o1 = torch.empty(M, D, device=x.device)
+        with _timed("pair_fwd", (M,)):
+            _lib.check(lib.matris_pair_fwd(M, _p(x), _p(pack.cat), _p(o0), _p(o1), _MMA["mode"], _stream()),
+                       "matris_pair_fwd")
+        ctx.pack, ctx.mode = pack, _MMA["mode"]
+        return o0, o1
+
+    @staticmethod
+    def backward(ctx, g0, g1):
+        dev = ctx.pack.cat.device
+        lib = _lib.load()
+        ref = g0 if g0 is not None else g1
+        M = ref.shape[0]
+        g0 = torch.zeros(M, D, device=dev) if g0 is None else _f32c(g0)
+        g1 = torch.zeros(M, D, device=dev) if g1 is None else _f32c(g1)
+        g_x = torch.empty(M, D, device=dev)
+        with _timed("pair_bwd", (M,)):
+            _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(ctx.pack.cat_t), _p(g_x), ctx.mode, _stream()),
+                       "matris_pair_bwd")
+        return g_x, None
+
+
+def proj_pair(pack: _WeightPack, x):
+    """(x W0^T, x W1^T) for two bias-free 128x128 Linears in one MFMA pass."""
+    return _Pair.apply(x, pack)

@@ -3,7 +3,9 @@ fp64 restatement of the reference op on identical inputs; integer kernels bit-ex
 
 Reference ops restated here: aggregate / index_add_ (functions.py:129-160),
 index_select, Dimwise_softmax + attention sums (functions.py:97-127,
-interaction_block.py:113-134), GatedMLP with RMSNorm (functions.py:245-311).
+interaction_block.py:113-134), GatedMLP with RMSNorm (functions.py:245-311), the
+bias-free FFN MLP (functions.py:198-205) and the W_s / W_t projections
+(interaction_block.py:33-38, 110-111).
 """
 import pytest
 import torch
@@ -169,5 +171,59 @@ def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
         out.backward(g.to(DEV))
         for j in range(nsrc):
             assert _rel(sd[j].grad, s64[j].grad) < tol, j
+    finally:
+        ops.set_mma_precision("bf16x6")
+
+
+_MODES = [("fp32", 1e-5), ("bf16x6", 1e-5), ("bf16x3", 1e-4)]
+
+
+@pytest.mark.parametrize("mode,tol", _MODES)
+@pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097])
+def test_ffn_fwd_bwd(M, mode, tol):
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    torch.manual_seed(M)
+    l1 = torch.nn.Linear(128, 128, bias=False)
+    l2 = torch.nn.Linear(128, 128, bias=False)
+    x = torch.randn(M, 128)
+    g = torch.randn(M, 128)
+    x64 = x.double().requires_grad_(True)
+    out_r = F.linear(F.silu(F.linear(x64, l1.weight.double())), l2.weight.double())
+    (out_r * g.double()).sum().backward()
+    w1, w2 = l1.weight.to(DEV), l2.weight.to(DEV)
+    xd = x.to(DEV).requires_grad_(True)
+    try:
+        out = ops.ffn(ops._WeightPack().get(w1, w2), xd)
+        assert _rel(out, out_r) < tol
+        out.backward(g.to(DEV))
+        assert _rel(xd.grad, x64.grad) < tol
+    finally:
+        ops.set_mma_precision("bf16x6")
+
+
+@pytest.mark.parametrize("mode,tol", _MODES)
+@pytest.mark.parametrize("M", [1, 65, 3000])
+def test_proj_pair_fwd_bwd(M, mode, tol):
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    torch.manual_seed(7 + M)
+    ws, wt = torch.randn(128, 128) / 11, torch.randn(128, 128) / 11
+    x = torch.randn(M, 128)
+    g0, g1 = torch.randn(M, 128), torch.randn(M, 128)
+    x64 = x.double().requires_grad_(True)
+    o0r, o1r = x64 @ ws.double().t(), x64 @ wt.double().t()
+    ((o0r * g0.double()).sum() + (o1r * g1.double()).sum()).backward()
+    xd = x.to(DEV).requires_grad_(True)
+    try:
+        o0, o1 = ops.proj_pair(ops._WeightPack().get(ws.to(DEV), wt.to(DEV)), xd)
+        assert _rel(o0, o0r) < tol and _rel(o1, o1r) < tol
+        torch.autograd.backward([o0, o1], [g0.to(DEV), g1.to(DEV)])
+        assert _rel(xd.grad, x64.grad) < tol
+        # one output unused: its gradient arrives as None
+        xd.grad = None
+        o0, _ = ops.proj_pair(ops._WeightPack().get(ws.to(DEV), wt.to(DEV)), xd)
+        o0.backward(g0.to(DEV))
+        assert _rel(xd.grad, (g0.double() @ ws.double())) < tol
     finally:
         ops.set_mma_precision("bf16x6")

@@ -69,5 +69,12 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_gmlp_bwd(10, 200, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), 6, None) == -1001
     # unknown MFMA mode
     assert lib.matris_gmlp_bwd(10, 256, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), 5, None) == -1001
+    # dense layers: misaligned row pointer, null operand, unknown mode
+    v16 = ctypes.c_void_p(16)
+    assert lib.matris_ffn_fwd(10, ctypes.c_void_p(8), v16, v16, v16, None, 6, None) == -1001
+    assert lib.matris_ffn_bwd(10, v16, None, v16, v16, v16, 6, None) == -1001
+    assert lib.matris_pair_fwd(10, v16, v16, v16, v16, 1, None) == -1001
+    assert lib.matris_pair_bwd(-1, v16, v16, v16, v16, 0, None) == -1001
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
+    assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, 3, None) == 0
