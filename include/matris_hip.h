@@ -136,6 +136,26 @@ int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const f
                     const float *g_ys, float *g_alpha_t, float *g_alpha_s, float *g_e, void *stream);
 
 /* ------------------------------------------------------------------------------------
+ * MFMA arithmetic and packed weights (shared by the gated MLP, FFN and projection pair).
+ * `mode` selects the arithmetic (fp32 in, fp32 accumulate in every mode):
+ *   MATRIS_MMA_FP32   v_mfma_f32_32x32x2f32 on the fp32 operands;
+ *   MATRIS_MMA_BF16X6 operands split exactly into three bf16 parts, six partial
+ *                     products on v_mfma_f32_32x32x16_bf16 (fp32-grade accuracy);
+ *   MATRIS_MMA_BF16X3 two bf16 parts, three partial products (~2^-16 per product).
+ * Every weight operand ("...p" arguments) is passed pre-packed by matris_pack_b in the
+ * SAME mode as the call that reads it: a [n, k] row-major fp32 matrix whose rows are the
+ * GEMM's output columns (an nn.Linear weight, or the transpose of one for a backward)
+ * becomes fragment-major planes of matris_pack_b_bytes(n, k, mode) bytes (n % 32 == 0,
+ * k % 16 == 0; 4 bytes per element in modes 0 and 3, 6 in mode 6).  No counterpart in
+ * the reference: it replaces the per-call weight reads of the nn.Linear layers below.
+ * ------------------------------------------------------------------------------------ */
+#define MATRIS_MMA_FP32 0
+#define MATRIS_MMA_BF16X3 3
+#define MATRIS_MMA_BF16X6 6
+size_t matris_pack_b_bytes(int64_t n, int64_t k, int mode);
+int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, void *out, void *stream);
+
+/* ------------------------------------------------------------------------------------
  * Fused gated MLP on MFMA (row M1).  Replaces GatedMLP.forward
  * (matris/model/functions.py:297-311) with its MLP / RMSNorm / FusedSiLU / FusedSigmoid
  * parts (functions.py:163-242, 10-36; op/fused_silu_op.py; op/fuse_sigmoid_op.py) and
@@ -143,47 +163,41 @@ int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const f
  *   input row m = concat_j src_j[(src_idx_j ? src_idx_j[m] : m), 0:128], j < n_src
  *   (n_src in {1..4}, K = 128 n_src); src_host / src_idx_host are host arrays of n_src
  *   device pointers (an index pointer may be NULL for the identity);
- *   w1 [256, K] = [mlp_core.layers.0.weight; mlp_gate.layers.0.weight], b1 [256];
- *   w2 [256, 128] = [mlp_core.layers.3.weight; mlp_gate.layers.3.weight], b2 [256];
+ *   w1p = pack of [mlp_core.layers.0.weight; mlp_gate.layers.0.weight] ([256, K]), b1 [256];
+ *   w2p = pack of [mlp_core.layers.3.weight; mlp_gate.layers.3.weight] ([256, 128]), b2 [256];
  *   norm_c / norm_g [128] = core_norm.weight / gate_norm.weight, RMSNorm eps.
  * fwd writes out [M,128]; save_p / save_z [M,256] (layer-1 pre-activation and layer-2
  * output, both halves) when non-NULL -- the backward needs them.
- * bwd (input gradients only) reads g_out [M,128], p, z and the transposed weights
- * w1t [K,256], w2t [128,256] (w2t[k][n] = w2[n][k]); writes g_x [M,K].
- * mode selects the MFMA arithmetic (fp32 in, fp32 accumulate in every mode):
- *   MATRIS_MMA_FP32   v_mfma_f32_32x32x2f32 on the fp32 operands;
- *   MATRIS_MMA_BF16X6 operands split exactly into three bf16 parts, six partial
- *                     products on v_mfma_f32_32x32x16_bf16 (fp32-grade accuracy);
- *   MATRIS_MMA_BF16X3 two bf16 parts, three partial products (~2^-16 per product). */
-#define MATRIS_MMA_FP32 0
-#define MATRIS_MMA_BF16X3 3
-#define MATRIS_MMA_BF16X6 6
+ * bwd (input gradients only) reads g_out [M,128], p, z and the packed transposes
+ * w1tp = pack of w1^T ([K, 256]) and w2tp = pack of [W2core^T; W2gate^T] ([256, 128]);
+ * writes g_x [M,K]. */
 int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
-                    const float *w1, const float *b1, const float *w2, const float *b2, const float *norm_c,
+                    const void *w1p, const float *b1, const void *w2p, const float *b2, const float *norm_c,
                     const float *norm_g, float eps, float *out, float *save_p, float *save_z, int mode,
                     void *stream);
-int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const float *w1t,
-                    const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x, int mode,
+int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
+                    const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x, int mode,
                     void *stream);
 
 /* ------------------------------------------------------------------------------------
- * Dense layers on MFMA (same `mode` values as the gated MLP), 128-wide rows, no bias.
+ * Dense layers on MFMA, 128-wide rows, no bias.
  * ------------------------------------------------------------------------------------ */
 
 /* FFN out = W2 SiLU(W1 x): Refinement.node_FFN / edge_FFN, MLP(hidden=int, bias=False)
  * (matris/model/functions.py:198-205, interaction_block.py:198-210, 269-270).
- * w1, w2 [128,128] (Linear weights, [out, in]); save_p [M,128] = W1 x (needed by bwd).
- * bwd: g_x = ((g W2) * SiLU'(p)) W1 with w1t = w1^T, w2t = w2^T. */
-int matris_ffn_fwd(int64_t m, const float *x, const float *w1, const float *w2, float *out, float *save_p, int mode,
+ * w1p, w2p = packs of the [128,128] Linear weights; save_p [M,128] = W1 x (for bwd).
+ * bwd: g_x = ((g W2) * SiLU'(p)) W1 with w1tp, w2tp = packs of w1^T, w2^T. */
+int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, float *out, float *save_p, int mode,
                    void *stream);
-int matris_ffn_bwd(int64_t m, const float *g, const float *p, const float *w1t, const float *w2t, float *g_x,
+int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp, float *g_x,
                    int mode, void *stream);
 
 /* Attention projection pair (interaction_block.py:33-38, 110-111):
- * out0 = x W[0:128]^T (source_weight_linear), out1 = x W[128:256]^T (target), w [256,128].
- * bwd: g_x = g0 W[0:128] + g1 W[128:256] with wt = w^T [128,256]. */
-int matris_pair_fwd(int64_t m, const float *x, const float *w, float *out0, float *out1, int mode, void *stream);
-int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const float *wt, float *g_x, int mode,
+ * out0 = x W[0:128]^T (source_weight_linear), out1 = x W[128:256]^T (target);
+ * wp = pack of W = [W_s; W_t] ([256,128]).
+ * bwd: g_x = g0 W[0:128] + g1 W[128:256] with wtp = pack of W^T ([128,256]). */
+int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, float *out1, int mode, void *stream);
+int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, int mode,
                     void *stream);
 
 #ifdef __cplusplus

@@ -6,9 +6,11 @@
 //   z    = [h_c W2c^T + b2c | h_g W2g^T + b2g]              [BM, 256]
 //   out  = SiLU(RMS(z_c) * w_c) * sigmoid(RMS(z_g) * w_g)   [BM, 128]
 //
-// Work-group = 4 wave64s, BM = 64 rows.  GEMM1 streams K in 32-wide chunks through LDS
-// (X chunk gathered row by row, W1 chunk), register-prefetching the next chunk while
-// the current one feeds v_mfma_f32_32x32x2f32; each wave owns 64 output columns (a 2x2
+// Work-group = 4 wave64s, BM = 64 rows.  GEMM1 streams K in 32-wide chunks: each thread
+// gathers 8 values of one row of the next chunk, converts them once into an operand
+// fragment (mma.h) and writes it to a double-buffered LDS chunk, so one barrier per
+// chunk suffices and no wave converts A values itself; the pre-packed W1 fragments come
+// straight from global (L2) one k-block ahead.  Each wave owns 64 output columns (2x2
 // grid of 32x32 tiles).  The [64, 256] result tile goes through LDS: p is copied out
 // with 16-byte row stores, h = SiLU(p) stays in LDS as GEMM2's A operand, z returns to
 // LDS, is copied out, and a row-per-wave epilogue applies RMSNorm, SiLU, sigmoid and
@@ -16,7 +18,7 @@
 //
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
-// tiling, with the transposed weights as B operands.
+// tiling, with packed transposed weights as B operands.
 #include "mma.h"
 
 struct GmlpSrc {
@@ -43,24 +45,27 @@ __device__ __forceinline__ void store_tile256(const float *tile, float *__restri
 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src,
-                                                          const float *__restrict__ W1, const float *__restrict__ b1,
-                                                          const float *__restrict__ W2, const float *__restrict__ b2,
+                                                          const uint4 *__restrict__ W1, const float *__restrict__ b1,
+                                                          const uint4 *__restrict__ W2, const float *__restrict__ b2,
                                                           const float *__restrict__ norm_c,
                                                           const float *__restrict__ norm_g, float eps,
                                                           float *__restrict__ out, float *__restrict__ save_p,
                                                           float *__restrict__ save_z) {
+    constexpr int NPL = Npl<MODE>::v;
+    constexpr int CHUNK = 2 * 2 * NPL * 64;  // uint4 per LDS chunk: [rt 2][kb 2][plane][lane]
     __shared__ __align__(16) float smem[BM * LDH];
-    float *Xs = smem;
-    float *Ws = smem + BM * LDX;
-    float *Ts = smem;  // [BM, 256] tile: p, then h, then z
+    uint4 *Xp = reinterpret_cast<uint4 *>(smem);  // two chunk buffers (<= 24 KB)
+    float *Ts = smem;                             // [BM, 256] tile: p, then h, then z
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
-    const int K = nsrc * MATRIS_D;
+    const int KB = nsrc * (MATRIS_D / 16);  // k-blocks of W1
+    const int nchunk = nsrc * (MATRIS_D / 32);
 
-    // gather assignment: thread -> (row xr, 8 columns at xc) of each X chunk
-    const int xr = tid >> 2, xc = (tid & 3) * 8;
+    // gather assignment: thread -> (row xr, 8 columns at 8*xq) of each 32-wide chunk,
+    // which is exactly the fragment (tile xr/32, k-block xq/2, lane xr%32 + 32*(xq&1)).
+    const int xr = tid >> 2, xq = tid & 3, xc = xq * 8;
+    const int xslot = ((xr >> 5) * 2 + (xq >> 1)) * NPL * 64 + (xr & 31) + 32 * (xq & 1);
     const int64_t grow = m0 + xr;
     const bool xvalid = grow < M;
     int64_t sr0 = 0, sr1 = 0, sr2 = 0, sr3 = 0;
@@ -70,10 +75,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         if (nsrc > 2) sr2 = src.idx[2] ? (int64_t)src.idx[2][grow] : grow;
         if (nsrc > 3) sr3 = src.idx[3] ? (int64_t)src.idx[3][grow] : grow;
     }
-    const float *__restrict__ wrow = W1 + (int64_t)tid * K;  // W1 row `tid` feeds LDS row `tid`
 
-    float4 x0, x1, w0, w1, w2, w3, w4, w5, w6, w7;
-#define GMLP_LOAD(kc)                                                                                    \
+    float4 x0, x1;
+#define GMLP_LOADX(kc)                                                                                   \
     do {                                                                                                 \
         const int j_ = (kc) >> 7, cc_ = (kc) & 127;                                                      \
         const float *sp_ = j_ == 0 ? src.ptr[0] + sr0 * MATRIS_D                                         \
@@ -87,39 +91,50 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         } else {                                                                                         \
             x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);                                                   \
         }                                                                                                \
-        const float4 *wp_ = reinterpret_cast<const float4 *>(wrow + (kc));                               \
-        w0 = wp_[0]; w1 = wp_[1]; w2 = wp_[2]; w3 = wp_[3];                                              \
-        w4 = wp_[4]; w5 = wp_[5]; w6 = wp_[6]; w7 = wp_[7];                                              \
+    } while (0)
+#define GMLP_STOREX(buf)                                                                                 \
+    do {                                                                                                 \
+        Frag<MODE> f_;                                                                                   \
+        make_frag<MODE>(f_, x0, x1);                                                                     \
+        _Pragma("unroll") for (int pl_ = 0; pl_ < NPL; ++pl_) Xp[(buf) * CHUNK + xslot + pl_ * 64] = f_.p[pl_]; \
     } while (0)
 
     v16f acc[2][2];
     zero_acc(acc);
-    GMLP_LOAD(0);
-    for (int kc = 0; kc < K; kc += BK) {
+    Frag<MODE> bcur[2], bnxt[2];
+    load_bfrags<MODE, 2>(bcur, W1, 2 * wave, KB, 0, lane);
+    GMLP_LOADX(0);
+    GMLP_STOREX(0);
+    __syncthreads();
+#pragma unroll 1
+    for (int c = 0; c < nchunk; ++c) {
+        const bool more = c + 1 < nchunk;
+        if (more) GMLP_LOADX((c + 1) * 32);
+        const uint4 *xb = Xp + (c & 1) * CHUNK;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int kb = 2 * c + sub;
+            if (kb + 1 < KB) load_bfrags<MODE, 2>(bnxt, W1, 2 * wave, KB, kb + 1, lane);
+            Frag<MODE> a[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int pl = 0; pl < NPL; ++pl) a[rt].p[pl] = xb[((rt * 2 + sub) * NPL + pl) * 64 + lane];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) mma_frag<MODE>(acc[rt][ct], a[rt], bcur[ct]);
+            bcur[0] = bnxt[0];
+            bcur[1] = bnxt[1];
+        }
+        if (more) GMLP_STOREX((c + 1) & 1);
         __syncthreads();
-        float4 *xs = reinterpret_cast<float4 *>(Xs + xr * LDX + xc);
-        xs[0] = x0;
-        xs[1] = x1;
-        float4 *ws = reinterpret_cast<float4 *>(Ws + tid * LDW);
-        ws[0] = w0; ws[1] = w1; ws[2] = w2; ws[3] = w3;
-        ws[4] = w4; ws[5] = w5; ws[6] = w6; ws[7] = w7;
-        __syncthreads();
-        if (kc + BK < K) GMLP_LOAD(kc + BK);
-        mfma_chunk<MODE, 2, 2>(acc, Xs, LDX, Ws + (wave * 64) * LDW, LDW, lane);
     }
-#undef GMLP_LOAD
-    __syncthreads();  // all waves are done with Xs / Ws before the tile overwrites them
+#undef GMLP_LOADX
+#undef GMLP_STOREX
 
     // p = acc + b1 -> LDS; copy p out with wide stores; h = SiLU(p) in place
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-        const int col = wave * 64 + ct * 32 + l32;
-        const float bias = b1[col];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) Ts[(rt * 32 + acc_row(i, h)) * LDH + col] = acc[rt][ct][i] + bias;
-    }
+    acc_to_lds<2>(acc, Ts, LDH, wave * 64, lane, b1);
     __syncthreads();
     if (save_p) store_tile256(Ts, save_p, m0, M, tid);
 #pragma unroll
@@ -135,18 +150,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // GEMM2: wave w -> z columns [64w, 64w+64); block = w/2 (0 core, 1 gate)
     const int blk = wave >> 1;
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 2, MATRIS_D>(acc, Ts + blk * MATRIS_D, LDH, W2 + (int64_t)(wave * 64) * MATRIS_D,
-                                        MATRIS_D, lane);
+    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, Ts + blk * MATRIS_D, LDH, W2, 2 * wave, MATRIS_D / 16, 0, lane);
     __syncthreads();  // every wave is done reading h
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-        const int col = wave * 64 + ct * 32 + l32;
-        const float bias = b2[col];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) Ts[(rt * 32 + acc_row(i, h)) * LDH + col] = acc[rt][ct][i] + bias;
-    }
+    acc_to_lds<2>(acc, Ts, LDH, wave * 64, lane, b2);
     __syncthreads();
     if (save_z) store_tile256(Ts, save_z, m0, M, tid);
 
@@ -172,8 +178,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, const float *__restrict__ g_out,
                                                           const float *__restrict__ P, const float *__restrict__ Z,
-                                                          const float *__restrict__ W1t,
-                                                          const float *__restrict__ W2t,
+                                                          const uint4 *__restrict__ W1t,
+                                                          const uint4 *__restrict__ W2t,
                                                           const float *__restrict__ norm_c,
                                                           const float *__restrict__ norm_g, float eps,
                                                           float *__restrict__ g_x) {
@@ -224,12 +230,12 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     }
     __syncthreads();
 
-    // phase 2: g_h = g_z W2 (block diagonal); wave w -> columns [64w, 64w+64)
+    // phase 2: g_h = g_z W2 (block diagonal); wave w -> columns [64w, 64w+64).  W2t is
+    // packed from [W2c^T ; W2g^T] ([256, 128]), so output tile nt reads block nt / 4.
     const int blk = wave >> 1;
     v16f acc[2][2];
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 2, MATRIS_D>(acc, G + blk * MATRIS_D, LDH,
-                                        W2t + (int64_t)((wave & 1) * 64) * 256 + blk * MATRIS_D, 256, lane);
+    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, G + blk * MATRIS_D, LDH, W2t, 2 * wave, MATRIS_D / 16, 0, lane);
     // g_p = g_h * SiLU'(p)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -244,22 +250,16 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             }
     }
     __syncthreads();  // every wave is done reading g_z
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-        const int col = wave * 64 + ct * 32 + l32;
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) G[(rt * 32 + acc_row(i, h)) * LDH + col] = acc[rt][ct][i];
-    }
+    acc_to_lds<2>(acc, G, LDH, wave * 64, lane);
     __syncthreads();
 
-    // phase 3: g_x = g_p W1 over 128-column blocks; wave w -> 32 columns of each block
+    // phase 3: g_x = g_p W1 over 128-column blocks; wave w -> 32 columns of each block.
+    // W1t is W1^T ([K, 256]) packed: output tile nt = column / 32, 16 k-blocks.
     for (int cb = 0; cb < K; cb += MATRIS_D) {
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
-        gemm_lds_a_global_b<MODE, 2, 1, 256>(a2, G, LDH, W1t + (int64_t)col0 * 256, 256, lane);
+        gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -273,11 +273,11 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host,
-                               const int32_t *const *src_idx_host, const float *w1, const float *b1, const float *w2,
+                               const int32_t *const *src_idx_host, const void *w1p, const float *b1, const void *w2p,
                                const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
                                float *save_p, float *save_z, int mode, void *stream) {
     if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
-    if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1 || !b1 || !w2 || !b2 || !norm_c || !norm_g || !out)
+    if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1p || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
         return MATRIS_E_ARG;
     if (m == 0) return 0;
     GmlpSrc s;
@@ -286,9 +286,10 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
         s.idx[j] = (j < n_src && src_idx_host) ? src_idx_host[j] : nullptr;
         if (j < n_src && (!s.ptr[j] || !aligned16(s.ptr[j]))) return MATRIS_E_ARG;
     }
-    if (!aligned16(w1) || !aligned16(w2)) return MATRIS_E_ARG;
+    if (!aligned16(w1p) || !aligned16(w2p)) return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
+    const uint4 *w1 = (const uint4 *)w1p, *w2 = (const uint4 *)w2p;
     if (mode == 0)
         gmlp_fwd_kernel<0><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
     else if (mode == 3)
@@ -299,23 +300,62 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
     return 0;
 }
 
-extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const float *w1t,
-                               const float *w2t, const float *norm_c, const float *norm_g, float eps, float *g_x,
+extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
+                               const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                                int mode, void *stream) {
     if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
-    if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1t || !w2t ||
+    if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1tp || !w2tp ||
         !norm_c || !norm_g || !g_x)
         return MATRIS_E_ARG;
     if (m == 0) return 0;
-    if (!aligned16(w1t) || !aligned16(w2t)) return MATRIS_E_ARG;
+    if (!aligned16(w1tp) || !aligned16(w2tp)) return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
+    const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
     if (mode == 0)
         gmlp_bwd_kernel<0><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
     else if (mode == 3)
         gmlp_bwd_kernel<3><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
     else
         gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
+// weight packing: [n, k] row-major fp32 (rows = output columns of the GEMM) -> fragment
+// planes, one thread per (tile, k-block, lane)
+// ------------------------------------------------------------------------------------
+template <int MODE>
+__global__ void pack_b_kernel(int64_t n, int64_t k, const float *__restrict__ w, uint4 *__restrict__ out) {
+    constexpr int NPL = Npl<MODE>::v;
+    const int64_t KB = k / 16;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (nt * KB + kb) * 64 + lane
+    if (t >= n / 32 * KB * 64) return;
+    const int lane = (int)(t & 63);
+    const int64_t ntkb = t >> 6, nt = ntkb / KB, kb = ntkb % KB;
+    const float *r = w + (nt * 32 + (lane & 31)) * k + kb * 16 + (lane >> 5) * 8;
+    Frag<MODE> f;
+    make_frag<MODE>(f, *reinterpret_cast<const float4 *>(r), *reinterpret_cast<const float4 *>(r + 4));
+#pragma unroll
+    for (int pl = 0; pl < NPL; ++pl) out[(ntkb * NPL + pl) * 64 + lane] = f.p[pl];
+}
+
+extern "C" size_t matris_pack_b_bytes(int64_t n, int64_t k, int mode) { return packed_b_bytes(n, k, mode); }
+
+extern "C" int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, void *out, void *stream) {
+    if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
+    if (n < 0 || k < 0 || (n % 32) || (k % 16) || !w || !out || !aligned16(w) || !aligned16(out)) return MATRIS_E_ARG;
+    const int64_t threads = n / 32 * (k / 16) * 64;
+    if (threads == 0) return 0;
+    const dim3 grid(matris_blocks(threads, 256));
+    hipStream_t st = (hipStream_t)stream;
+    if (mode == 0)
+        pack_b_kernel<0><<<grid, 256, 0, st>>>(n, k, w, (uint4 *)out);
+    else if (mode == 3)
+        pack_b_kernel<3><<<grid, 256, 0, st>>>(n, k, w, (uint4 *)out);
+    else
+        pack_b_kernel<6><<<grid, 256, 0, st>>>(n, k, w, (uint4 *)out);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -8,12 +8,12 @@
 //           (interaction_block.py:33-38, 110-111), one [M,128]x[128,256] product
 //
 // and their input-gradient kernels.  Work-group = 4 wave64s over BM = 64 rows; the
-// [64, 128] input tile is staged once in LDS (K = 128 needs no K loop), weight rows are
-// B operands read from global with a one-chunk register prefetch, and intermediate tiles
-// (p, h, g_h) stay in LDS.  Outputs leave through LDS with 16-byte row stores.
-#include "mma.h"
+// [64, 128] input tile is staged once in LDS (K = 128 needs no K loop), weights are
+// pre-packed B fragments (mma.h) read from global one k-block ahead, and intermediate
+// tiles (p, h, g_h) stay in LDS.  Outputs leave through LDS with 16-byte row stores.
+#include <initializer_list>
 
-#define LDT 132  // LDS row stride of a [64, 128] tile
+#include "mma.h"
 
 // Copy rows [m0, m0+64) x 128 columns of a row-major [*, ld] array into LDS (zeros past M).
 __device__ __forceinline__ void stage_tile128(float *dst, const float *__restrict__ src, int64_t ld, int64_t m0,
@@ -39,24 +39,12 @@ __device__ __forceinline__ void store_tile128(const float *tile, float *__restri
     }
 }
 
-// Write a wave's accumulators (rows 0..63, columns col0 + ct*32 + l32) into an LDS tile.
-template <int NCT>
-__device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *tile, int col0, int lane) {
-    const int h = lane >> 5, l32 = lane & 31;
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) tile[(rt * 32 + acc_row(i, h)) * LDT + col0 + ct * 32 + l32] = acc[rt][ct][i];
-}
-
 // ------------------------------------------------------------------------------------
 // FFN forward: p = x W1^T (saved), out = SiLU(p) W2^T
 // ------------------------------------------------------------------------------------
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float *__restrict__ x,
-                                                         const float *__restrict__ W1, const float *__restrict__ W2,
+                                                         const uint4 *__restrict__ W1, const uint4 *__restrict__ W2,
                                                          float *__restrict__ out, float *__restrict__ save_p) {
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
@@ -66,8 +54,8 @@ __global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float 
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T0, LDT, W1 + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
-    acc_to_lds<1>(acc, T1, wave * 32, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, W1, wave, MATRIS_D / 16, 0, lane);
+    acc_to_lds<1>(acc, T1, LDT, wave * 32, lane);
     __syncthreads();
     if (save_p) store_tile128(T1, save_p, MATRIS_D, m0, M, tid);
 #pragma unroll
@@ -80,8 +68,8 @@ __global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float 
     }
     __syncthreads();
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T1, LDT, W2 + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
-    acc_to_lds<1>(acc, T0, wave * 32, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, W2, wave, MATRIS_D / 16, 0, lane);
+    acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);
     __syncthreads();
     store_tile128(T0, out, MATRIS_D, m0, M, tid);
 }
@@ -89,8 +77,8 @@ __global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float 
 // FFN backward: g_x = ((g W2) * SiLU'(p)) W1, with w1t = W1^T, w2t = W2^T row-major.
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
-                                                         const float *__restrict__ P, const float *__restrict__ W1t,
-                                                         const float *__restrict__ W2t, float *__restrict__ g_x) {
+                                                         const float *__restrict__ P, const uint4 *__restrict__ W1t,
+                                                         const uint4 *__restrict__ W2t, float *__restrict__ g_x) {
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -100,7 +88,7 @@ __global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float 
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T0, LDT, W2t + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
     const int col = wave * 32 + l32;
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
@@ -110,11 +98,11 @@ __global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float 
             const float p = (m0 + row < M) ? P[(m0 + row) * MATRIS_D + col] : 0.f;
             acc[rt][0][i] *= dsilu_f(p);
         }
-    acc_to_lds<1>(acc, T1, wave * 32, lane);
+    acc_to_lds<1>(acc, T1, LDT, wave * 32, lane);
     __syncthreads();
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T1, LDT, W1t + (int64_t)(wave * 32) * MATRIS_D, MATRIS_D, lane);
-    acc_to_lds<1>(acc, T0, wave * 32, lane);  // every wave finished reading T0 before the g_h sync
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, W1t, wave, MATRIS_D / 16, 0, lane);
+    acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);  // every wave finished reading T0 before the g_h sync
     __syncthreads();
     store_tile128(T0, g_x, MATRIS_D, m0, M, tid);
 }
@@ -125,7 +113,7 @@ __global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float 
 // ------------------------------------------------------------------------------------
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float *__restrict__ x,
-                                                          const float *__restrict__ W, float *__restrict__ out0,
+                                                          const uint4 *__restrict__ W, float *__restrict__ out0,
                                                           float *__restrict__ out1) {
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
@@ -136,9 +124,9 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float
     // wave w -> output columns [64w, 64w+64) of the 256: waves 0,1 -> out0, 2,3 -> out1
     v16f acc[2][2];
     zero_acc(acc);
-    gemm_lds_a_global_b<MODE, 2, 2, MATRIS_D>(acc, T0, LDT, W + (int64_t)(wave * 64) * MATRIS_D, MATRIS_D, lane);
+    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0, lane);
     __syncthreads();  // T0 free
-    acc_to_lds<2>(acc, (wave < 2) ? T0 : T1, (wave & 1) * 64, lane);
+    acc_to_lds<2>(acc, (wave < 2) ? T0 : T1, LDT, (wave & 1) * 64, lane);
     __syncthreads();
     store_tile128(T0, out0, MATRIS_D, m0, M, tid);
     store_tile128(T1, out1, MATRIS_D, m0, M, tid);
@@ -146,9 +134,10 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float
 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
-                                                          const float *__restrict__ g1, const float *__restrict__ Wt,
+                                                          const float *__restrict__ g1, const uint4 *__restrict__ Wt,
                                                           float *__restrict__ g_x) {
-    // Wt = W^T, [128, 256] row-major: g_x[m][k] = sum_n g[m][n] Wt[k][n]
+    // Wt = W^T ([128, 256]) packed: g_x[m][k] = sum_n g[m][n] Wt[k][n], k-blocks 0..7
+    // pair with g0, 8..15 with g1
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -158,11 +147,10 @@ __global__ __launch_bounds__(256, 2) void pair_bwd_kernel(int64_t M, const float
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    const float *wt = Wt + (int64_t)(wave * 32) * 256;
-    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T0, LDT, wt, 256, lane);
-    gemm_lds_a_global_b<MODE, 2, 1, MATRIS_D>(acc, T1, LDT, wt + MATRIS_D, 256, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, Wt, wave, 256 / 16, 0, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, Wt, wave, 256 / 16, MATRIS_D / 16, lane);
     __syncthreads();
-    acc_to_lds<1>(acc, T0, wave * 32, lane);
+    acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);
     __syncthreads();
     store_tile128(T0, g_x, MATRIS_D, m0, M, tid);
 }
@@ -186,38 +174,38 @@ static bool mlp_args_ok(int mode, std::initializer_list<const void *> ptrs) {
     return true;
 }
 
-extern "C" int matris_ffn_fwd(int64_t m, const float *x, const float *w1, const float *w2, float *out,
+extern "C" int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, float *out,
                               float *save_p, int mode, void *stream) {
-    if (m < 0 || !mlp_args_ok(mode, {x, w1, w2, out}) || ((uintptr_t)save_p & 15)) return MATRIS_E_ARG;
+    if (m < 0 || !mlp_args_ok(mode, {x, w1p, w2p, out}) || ((uintptr_t)save_p & 15)) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(ffn_fwd_kernel, m, x, w1, w2, out, save_p);
+    MLP_DISPATCH(ffn_fwd_kernel, m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
-extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const float *w1t, const float *w2t,
+extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp,
                               float *g_x, int mode, void *stream) {
-    if (m < 0 || !mlp_args_ok(mode, {g, p, w1t, w2t, g_x})) return MATRIS_E_ARG;
+    if (m < 0 || !mlp_args_ok(mode, {g, p, w1tp, w2tp, g_x})) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(ffn_bwd_kernel, m, g, p, w1t, w2t, g_x);
+    MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
-extern "C" int matris_pair_fwd(int64_t m, const float *x, const float *w, float *out0, float *out1, int mode,
+extern "C" int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, float *out1, int mode,
                                void *stream) {
-    if (m < 0 || !mlp_args_ok(mode, {x, w, out0, out1})) return MATRIS_E_ARG;
+    if (m < 0 || !mlp_args_ok(mode, {x, wp, out0, out1})) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(pair_fwd_kernel, m, x, w, out0, out1);
+    MLP_DISPATCH(pair_fwd_kernel, m, x, (const uint4 *)wp, out0, out1);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
-extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const float *wt, float *g_x, int mode,
+extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, int mode,
                                void *stream) {
-    if (m < 0 || !mlp_args_ok(mode, {g0, g1, wt, g_x})) return MATRIS_E_ARG;
+    if (m < 0 || !mlp_args_ok(mode, {g0, g1, wtp, g_x})) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, wt, g_x);
+    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

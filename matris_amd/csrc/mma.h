@@ -1,18 +1,54 @@
-// MFMA building blocks shared by the fused GEMM kernels (gmlp.hip, mlp.hip): fp32
-// and split-bf16 32x32 MFMA tiles fed from LDS / global row-major operands.
+// MFMA building blocks shared by the fused GEMM kernels (gmlp.hip, mlp.hip).
+//
+// Fragments.  Every GEMM here runs on 32x32 output tiles with K consumed in 16-wide
+// blocks.  The operand fragment of one 32-row tile and one k-block is, for lane
+// l = l32 + 32h, the 8 values (row l32, k = 8h .. 8h+7).  It is held as NPL 16-byte
+// "planes":
+//   MODE 0  fp32 operands: planes = the 8 floats (2 x float4); v_mfma_f32_32x32x2f32 step
+//           s (0..7) consumes element s, i.e. k = 8h + s for lane half h.
+//   MODE 3  x = hi + mid (+ residual), hi = bf16(x), mid = bf16(x - hi): planes hi, mid;
+//           3 bf16 products (hi*hi + hi*mid + mid*hi) on v_mfma_f32_32x32x16_bf16.
+//   MODE 6  x = hi + mid + lo exactly, lo = bf16(x - hi - mid): planes hi, mid, lo;
+//           6 products (adds hi*lo + mid*mid + lo*hi): fp32-grade products.
+// A and B fragments use the same k assignment, so every mode sums over the same k.
+// The bf16 instruction's layout (A lane l: row l%32, k = 8(l/32)..+7; B lane l:
+// k = 8(l/32)..+7, column l%32) is exactly this fragment.
+//
+// Weights (B operands) are packed once per parameter version by matris_pack_b into
+// fragment-major order: 16-byte unit ((nt * KB + kb) * NPL + plane) * 64 + lane for
+// output-column tile nt, k-block kb (KB = K / 16).  A wave's fragment load is then one
+// contiguous 1 KB read per plane and no weight is converted inside a GEMM loop.
 #pragma once
 #include "common.h"
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-#define BM 64
-#define BK 32
-#define LDX 36   // LDS row stride (floats) of the X chunk
-#define LDW 36   // LDS row stride of the W1 chunk
-#define LDH 260  // LDS row stride of the [64, 256] h / gradient tiles
+#define BM 64    // rows per work-group
+#define LDH 260  // LDS row stride (floats) of a [64, 256] fp32 tile
+#define LDT 132  // LDS row stride of a [64, 128] fp32 tile
+
+template <int MODE>
+struct Npl {
+    static constexpr int v = MODE == 6 ? 3 : 2;
+};
+
+template <int MODE>
+struct Frag {
+    uint4 p[Npl<MODE>::v];
+};
+
+template <class To, class From>
+__device__ __forceinline__ To bitcast(const From &x) {
+    static_assert(sizeof(To) == sizeof(From), "size");
+    return __builtin_bit_cast(To, x);
+}
 
 __device__ __forceinline__ v16f mfma32(float a, float b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
@@ -22,129 +58,106 @@ __device__ __forceinline__ float dsilu_f(float x) {
     return s * (1.0f + x * (1.0f - s));
 }
 
-// Row of accumulator register i of a 32x32 tile for lane half h.
+// Row of accumulator register i of a 32x32 tile for lane half h (column = lane % 32).
 __device__ __forceinline__ int acc_row(int i, int h) { return (i >> 2) * 8 + h * 4 + (i & 3); }
 
-// ------------------------------------------------------------------------------------
-// MFMA precision modes.  MODE 0: fp32 operands on v_mfma_f32_32x32x2f32.  MODE 3 / 6:
-// each fp32 operand is split exactly into bf16 parts x = hi + mid + lo (hi = bf16(x),
-// mid = bf16(x - hi), lo = bf16(x - hi - mid)) and the product is accumulated in fp32 on
-// v_mfma_f32_32x32x16_bf16 from 3 (hi*hi + hi*mid + mid*hi) or 6 (+ hi*lo + mid*mid +
-// lo*hi) partial products.  MODE 6 carries ~24 significant bits per operand, i.e. fp32
-// GEMM accuracy, at 6 x 32 cycles per 32x32x16 block instead of 8 x 64 for MODE 0.
-//
-// Operand fragments of one 32-wide K chunk: per 32-row tile the lane holds 16 values as
-// 4 float4 at columns col4(q): MODE 0 uses columns 16h + 4q (step q*4+c consumes column
-// 16h+4q+c); the bf16 modes use 16(q>>1) + 8h + 4(q&1) (sub-step s consumes the 8
-// columns 16s + 8h .. +7, the k layout of the 32x32x16 instruction).  A and B always use
-// the same permutation of K, so the sum over the chunk is unchanged.
-// ------------------------------------------------------------------------------------
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-
+// 8 fp32 values (k order) -> fragment planes.
 template <int MODE>
-__device__ __forceinline__ int col4(int q, int h) {
-    return MODE == 0 ? 16 * h + 4 * q : 16 * (q >> 1) + 8 * h + 4 * (q & 1);
-}
-
-template <int MODE>
-__device__ __forceinline__ void split8(const float4 &u, const float4 &v, v8bf &hi, v8bf &mid, v8bf &lo) {
-    const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const __bf16 a = (__bf16)x[j];
-        const float r = x[j] - (float)a;
-        const __bf16 b = (__bf16)r;
-        hi[j] = a;
-        mid[j] = b;
-        if (MODE == 6) lo[j] = (__bf16)(r - (float)b);
-    }
-}
-
-__device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, v16f c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// acc[rt][ct] += A-tile[rt] * B-tile[ct] for one K chunk given the fragments.
-template <int MODE, int NRT, int NCT>
-__device__ __forceinline__ void chunk_mma(v16f (&acc)[NRT][NCT], const float4 (&a)[NRT][4],
-                                          const float4 (&b)[NCT][4]) {
+__device__ __forceinline__ void make_frag(Frag<MODE> &f, const float4 &u, const float4 &v) {
     if constexpr (MODE == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < NCT; ++ct) {
-                    acc[rt][ct] = mfma32(a[rt][q].x, b[ct][q].x, acc[rt][ct]);
-                    acc[rt][ct] = mfma32(a[rt][q].y, b[ct][q].y, acc[rt][ct]);
-                    acc[rt][ct] = mfma32(a[rt][q].z, b[ct][q].z, acc[rt][ct]);
-                    acc[rt][ct] = mfma32(a[rt][q].w, b[ct][q].w, acc[rt][ct]);
-                }
+        f.p[0] = bitcast<uint4>(u);
+        f.p[1] = bitcast<uint4>(v);
     } else {
+        const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        v8bf hi, mid, lo;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            v8bf ah[NRT], am[NRT], al[NRT], bh[NCT], bm[NCT], bl[NCT];
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) split8<MODE>(a[rt][2 * s], a[rt][2 * s + 1], ah[rt], am[rt], al[rt]);
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) split8<MODE>(b[ct][2 * s], b[ct][2 * s + 1], bh[ct], bm[ct], bl[ct]);
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < NCT; ++ct) {
-                    if constexpr (MODE == 6) {
-                        acc[rt][ct] = mfma_bf16(al[rt], bh[ct], acc[rt][ct]);
-                        acc[rt][ct] = mfma_bf16(am[rt], bm[ct], acc[rt][ct]);
-                        acc[rt][ct] = mfma_bf16(ah[rt], bl[ct], acc[rt][ct]);
-                    }
-                    acc[rt][ct] = mfma_bf16(am[rt], bh[ct], acc[rt][ct]);
-                    acc[rt][ct] = mfma_bf16(ah[rt], bm[ct], acc[rt][ct]);
-                    acc[rt][ct] = mfma_bf16(ah[rt], bh[ct], acc[rt][ct]);
-                }
+        for (int j = 0; j < 8; ++j) {
+            const __bf16 a = (__bf16)x[j];
+            const float r = x[j] - (float)a;
+            const __bf16 b = (__bf16)r;
+            hi[j] = a;
+            mid[j] = b;
+            if constexpr (MODE == 6) lo[j] = (__bf16)(r - (float)b);
         }
+        f.p[0] = bitcast<uint4>(hi);
+        f.p[1] = bitcast<uint4>(mid);
+        if constexpr (MODE == 6) f.p[2] = bitcast<uint4>(lo);
     }
 }
 
-// Fragments of NT 32-row tiles of a row-major array (rows t*32 + l32, row stride ld).
-template <int MODE, int NT>
-__device__ __forceinline__ void load_frag(float4 (&f)[NT][4], const float *base, int64_t ld, int lane) {
+// acc += A-fragment * B-fragment over one 16-wide k block.  Smallest products first.
+template <int MODE>
+__device__ __forceinline__ void mma_frag(v16f &acc, const Frag<MODE> &a, const Frag<MODE> &b) {
+    if constexpr (MODE == 0) {
+        const float4 a0 = bitcast<float4>(a.p[0]), a1 = bitcast<float4>(a.p[1]);
+        const float4 b0 = bitcast<float4>(b.p[0]), b1 = bitcast<float4>(b.p[1]);
+        acc = mfma32(a0.x, b0.x, acc);
+        acc = mfma32(a0.y, b0.y, acc);
+        acc = mfma32(a0.z, b0.z, acc);
+        acc = mfma32(a0.w, b0.w, acc);
+        acc = mfma32(a1.x, b1.x, acc);
+        acc = mfma32(a1.y, b1.y, acc);
+        acc = mfma32(a1.z, b1.z, acc);
+        acc = mfma32(a1.w, b1.w, acc);
+    } else {
+        const v8bf ah = bitcast<v8bf>(a.p[0]), am = bitcast<v8bf>(a.p[1]);
+        const v8bf bh = bitcast<v8bf>(b.p[0]), bm = bitcast<v8bf>(b.p[1]);
+        if constexpr (MODE == 6) {
+            const v8bf al = bitcast<v8bf>(a.p[2]), bl = bitcast<v8bf>(b.p[2]);
+            acc = mfma_bf16(al, bh, acc);
+            acc = mfma_bf16(am, bm, acc);
+            acc = mfma_bf16(ah, bl, acc);
+        }
+        acc = mfma_bf16(am, bh, acc);
+        acc = mfma_bf16(ah, bm, acc);
+        acc = mfma_bf16(ah, bh, acc);
+    }
+}
+
+// B fragments of output tiles nt0 .. nt0+NCT-1, k-block kb, of a packed weight with KB
+// k-blocks.
+template <int MODE, int NCT>
+__device__ __forceinline__ void load_bfrags(Frag<MODE> (&b)[NCT], const uint4 *__restrict__ W, int nt0, int KB, int kb,
+                                            int lane) {
+    constexpr int NPL = Npl<MODE>::v;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int pl = 0; pl < NPL; ++pl)
+            b[ct].p[pl] = W[((int64_t)((nt0 + ct) * KB + kb) * NPL + pl) * 64 + lane];
+}
+
+// A fragments of NRT 32-row tiles of an fp32 row-major LDS array, k-block kb.
+template <int MODE, int NRT>
+__device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *base, int ld, int kb, int lane) {
     const int h = lane >> 5, l32 = lane & 31;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            f[t][q] = *reinterpret_cast<const float4 *>(base + (int64_t)(t * 32 + l32) * ld + col4<MODE>(q, h));
+    for (int rt = 0; rt < NRT; ++rt) {
+        const float *r = base + (rt * 32 + l32) * ld + kb * 16 + h * 8;
+        make_frag<MODE>(a[rt], *reinterpret_cast<const float4 *>(r), *reinterpret_cast<const float4 *>(r + 4));
+    }
 }
 
-// acc[rt][ct] += A[rt*32.., k] * B[k, ct*32..] for a 32-wide K chunk; A rows at
-// a_base + row * lda (LDS), B as rows n of a [n][k] array at b_base + n * ldb.
-template <int MODE, int NRT, int NCT>
-__device__ __forceinline__ void mfma_chunk(v16f (&acc)[NRT][NCT], const float *a_base, int lda, const float *b_base,
-                                           int ldb, int lane) {
-    float4 a[NRT][4], b[NCT][4];
-    load_frag<MODE, NRT>(a, a_base, lda, lane);
-    load_frag<MODE, NCT>(b, b_base, ldb, lane);
-    chunk_mma<MODE, NRT, NCT>(acc, a, b);
-}
-
-// acc += A[:, 0:KD] (LDS) * B[0:KD, :] with B read from global as rows of a [n][k]
-// array, the next chunk's B fragments prefetched while the current one is consumed.
-template <int MODE, int NRT, int NCT, int KD>
-__device__ __forceinline__ void gemm_lds_a_global_b(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
-                                                    const float *__restrict__ b_base, int ldb, int lane) {
-    float4 cur[NCT][4], nxt[NCT][4];
-    load_frag<MODE, NCT>(cur, b_base, ldb, lane);
-#pragma unroll 1
-    for (int kc = 0; kc < KD; kc += BK) {
-        if (kc + BK < KD) load_frag<MODE, NCT>(nxt, b_base + kc + BK, ldb, lane);
-        float4 a[NRT][4];
-        load_frag<MODE, NRT>(a, a_base + kc, lda, lane);
-        chunk_mma<MODE, NRT, NCT>(acc, a, cur);
-        if (kc + BK < KD) {
+// acc[rt][ct] += A[rt tile, k-blocks 0..KBA) * B[k-blocks kb0.., tile nt0 + ct] with A an
+// fp32 row-major LDS array and B a packed weight (KBW k-blocks); the next k-block's B
+// fragments are loaded while the current one is consumed.
+template <int MODE, int NRT, int NCT, int KBA>
+__device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
+                                                const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
+    Frag<MODE> cur[NCT], nxt[NCT];
+    load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
+#pragma unroll 2
+    for (int kb = 0; kb < KBA; ++kb) {
+        if (kb + 1 < KBA) load_bfrags<MODE, NCT>(nxt, W, nt0, KBW, kb0 + kb + 1, lane);
+        Frag<MODE> a[NRT];
+        lds_afrags<MODE, NRT>(a, a_base, lda, kb, lane);
 #pragma unroll
-            for (int ct = 0; ct < NCT; ++ct)
+        for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) cur[ct][q] = nxt[ct][q];
+            for (int ct = 0; ct < NCT; ++ct) mma_frag<MODE>(acc[rt][ct], a[rt], cur[ct]);
+        if (kb + 1 < KBA) {
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
         }
     }
 }
@@ -159,3 +172,24 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
             for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
 }
 
+// Write a wave's accumulators (rows 0..63, columns col0 + ct*32 + lane%32), plus an
+// optional per-column bias, into an fp32 LDS tile of row stride ld.
+template <int NCT>
+__device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *tile, int ld, int col0, int lane,
+                                           const float *__restrict__ bias = nullptr) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        const int col = col0 + ct * 32 + l32;
+        const float b = bias ? bias[col] : 0.f;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tile[(rt * 32 + acc_row(i, h)) * ld + col] = acc[rt][ct][i] + b;
+    }
+}
+
+// Bytes of a packed [n, k] weight in `mode` (n % 32 == 0, k % 16 == 0).
+__host__ __device__ inline size_t packed_b_bytes(int64_t n, int64_t k, int mode) {
+    return (size_t)n * (size_t)k * (mode == 6 ? 6 : 4);
+}

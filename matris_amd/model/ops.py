@@ -228,32 +228,63 @@ def seg_attention(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: 
 # ------------------------------------------------------------------------------------
 # fused gated MLP
 # ------------------------------------------------------------------------------------
-class GmlpPack:
-    """Packed / transposed GatedMLP weights, rebuilt when a parameter changes."""
+def pack_b(w, mode: int):
+    """matris_pack_b of an fp32 [n, k] matrix whose rows are a GEMM's output columns."""
+    w = _f32c(w)
+    n, k = w.shape
+    lib = _lib.load()
+    out = torch.empty(lib.matris_pack_b_bytes(n, k, mode), dtype=torch.uint8, device=w.device)
+    _lib.check(lib.matris_pack_b(n, k, _p(w), mode, _p(out), _stream()), "matris_pack_b")
+    return out
+
+
+class _PackCache:
+    """fp32 weight matrices of one fused op, and their matris_pack_b images per MFMA mode,
+    rebuilt when any source parameter changes (data pointer or version)."""
 
     def __init__(self):
         self.sig = None
+        self.mats = {}
+        self._packed = {}
+
+    def _refresh(self, params, build):
+        sig = tuple((p.data_ptr(), p._version, p.device) for p in params)
+        if sig != self.sig:
+            with torch.no_grad():
+                build()
+            self._packed = {}
+            self.sig = sig
+
+    def b(self, name: str, mode: int):
+        key = (name, mode)
+        if key not in self._packed:
+            self._packed[key] = pack_b(self.mats[name], mode)
+        return self._packed[key]
+
+
+class GmlpPack(_PackCache):
+    """GatedMLP weights: w1 = [core; gate] layer-0 weights [256, K], w2 = layer-3 weights
+    [256, 128], their transposes for the backward, biases and norm weights."""
 
     def get(self, mod):
         params = (mod.mlp_core.layers[0].weight, mod.mlp_core.layers[0].bias, mod.mlp_core.layers[3].weight,
                   mod.mlp_core.layers[3].bias, mod.mlp_gate.layers[0].weight, mod.mlp_gate.layers[0].bias,
                   mod.mlp_gate.layers[3].weight, mod.mlp_gate.layers[3].bias, mod.core_norm.weight,
                   mod.gate_norm.weight)
-        sig = tuple((p.data_ptr(), p._version, p.device) for p in params)
-        if sig != self.sig:
-            with torch.no_grad():
-                c1w, c1b, c2w, c2b, g1w, g1b, g2w, g2b, nc, ng = (p.detach().float() for p in params)
-                self.w1 = torch.cat([c1w, g1w], 0).contiguous()
-                self.b1 = torch.cat([c1b, g1b], 0).contiguous()
-                self.w2 = torch.cat([c2w, g2w], 0).contiguous()
-                self.b2 = torch.cat([c2b, g2b], 0).contiguous()
-                self.w1t = self.w1.t().contiguous()
-                self.w2t = self.w2.t().contiguous()
-                self.nc = nc.contiguous()
-                self.ng = ng.contiguous()
-                eps = mod.core_norm.eps
-                self.eps = float(torch.finfo(torch.float32).eps if eps is None else eps)
-            self.sig = sig
+
+        def build():
+            c1w, c1b, c2w, c2b, g1w, g1b, g2w, g2b, nc, ng = (p.detach().float() for p in params)
+            w1 = torch.cat([c1w, g1w], 0).contiguous()
+            self.mats = {"w1": w1, "w2": torch.cat([c2w, g2w], 0).contiguous(), "w1t": w1.t().contiguous(),
+                         "w2bt": torch.cat([c2w.t(), g2w.t()], 0).contiguous()}
+            self.b1 = torch.cat([c1b, g1b], 0).contiguous()
+            self.b2 = torch.cat([c2b, g2b], 0).contiguous()
+            self.nc = nc.contiguous()
+            self.ng = ng.contiguous()
+            eps = mod.core_norm.eps
+            self.eps = float(torch.finfo(torch.float32).eps if eps is None else eps)
+
+        self._refresh(params, build)
         return self
 
 
@@ -271,9 +302,10 @@ class _GatedMLP(torch.autograd.Function):
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(g.key.data_ptr() if g is not None else None) for g in groupings])
         with _timed("gmlp_fwd", (n_rows, nsrc * D)):
-            _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.w1), _p(pack.b1), _p(pack.w2),
-                                           _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps, _p(out), _p(p), _p(z),
-                                           _MMA["mode"], _stream()), "matris_gmlp_fwd")
+            mode = _MMA["mode"]
+            _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
+                                           _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
+                                           _p(out), _p(p), _p(z), mode, _stream()), "matris_gmlp_fwd")
         ctx.mode = _MMA["mode"]
         ctx.save_for_backward(p, z)
         ctx.pack, ctx.groupings = pack, groupings
@@ -290,8 +322,9 @@ class _GatedMLP(torch.autograd.Function):
         K = D * len(ctx.groupings)
         g_x = torch.empty(M, K, device=g.device)
         with _timed("gmlp_bwd", (M, K)):
-            _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.w1t), _p(pack.w2t), _p(pack.nc),
-                                           _p(pack.ng), pack.eps, _p(g_x), ctx.mode, _stream()), "matris_gmlp_bwd")
+            _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", ctx.mode)),
+                                           _p(pack.b("w2bt", ctx.mode)), _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x),
+                                           ctx.mode, _stream()), "matris_gmlp_bwd")
         grads = []
         for j, grp in enumerate(ctx.groupings):
             if not ctx.needs_input_grad[3 + j]:
@@ -317,21 +350,21 @@ def gated_mlp(module, pack: GmlpPack, sources):
 # ------------------------------------------------------------------------------------
 # dense layers on MFMA: FFN (Linear -> SiLU -> Linear, no bias) and the projection pair
 # ------------------------------------------------------------------------------------
-class _WeightPack:
-    """Contiguous fp32 weights and their transposes, rebuilt when a parameter changes."""
-
-    def __init__(self):
-        self.sig = None
+class _WeightPack(_PackCache):
+    """Bias-free 128x128 Linear weights W0, W1 (FFN layers, or the W_s / W_t pair):
+    mats w0, w1, their transposes wt0, wt1, and cat = [W0; W1], cat_t = cat^T."""
 
     def get(self, *params):
-        sig = tuple((p.data_ptr(), p._version, p.device) for p in params)
-        if sig != self.sig:
-            with torch.no_grad():
-                self.w = [p.detach().float().contiguous() for p in params]
-                self.wt = [w.t().contiguous() for w in self.w]
-                self.cat = torch.cat(self.w, 0).contiguous() if len(self.w) > 1 else self.w[0]
-                self.cat_t = self.cat.t().contiguous()
-            self.sig = sig
+        def build():
+            w = [p.detach().float().contiguous() for p in params]
+            self.mats = {f"w{i}": t for i, t in enumerate(w)}
+            self.mats.update({f"wt{i}": t.t().contiguous() for i, t in enumerate(w)})
+            if len(w) > 1:
+                cat = torch.cat(w, 0).contiguous()
+                self.mats.update({"cat": cat, "cat_t": cat.t().contiguous()})
+
+        self._refresh(params, build)
+        self.device = params[0].device
         return self
 
 
@@ -345,8 +378,9 @@ class _FFN(torch.autograd.Function):
         out = torch.empty(M, D, device=x.device)
         p = torch.empty(M, D, device=x.device)
         with _timed("ffn_fwd", (M,)):
-            _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.w[0]), _p(pack.w[1]), _p(out), _p(p), _MMA["mode"],
-                                          _stream()), "matris_ffn_fwd")
+            mode = _MMA["mode"]
+            _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.b("w0", mode)), _p(pack.b("w1", mode)), _p(out), _p(p),
+                                          mode, _stream()), "matris_ffn_fwd")
         ctx.save_for_backward(p)
         ctx.pack, ctx.mode = pack, _MMA["mode"]
         return out
@@ -359,8 +393,9 @@ class _FFN(torch.autograd.Function):
         M = p.shape[0]
         g_x = torch.empty(M, D, device=g.device)
         with _timed("ffn_bwd", (M,)):
-            _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(ctx.pack.wt[0]), _p(ctx.pack.wt[1]), _p(g_x), ctx.mode,
-                                          _stream()), "matris_ffn_bwd")
+            _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(ctx.pack.b("wt0", ctx.mode)),
+                                          _p(ctx.pack.b("wt1", ctx.mode)), _p(g_x), ctx.mode, _stream()),
+                       "matris_ffn_bwd")
         return g_x, None
 
 
@@ -379,14 +414,15 @@ class _Pair(torch.autograd.Function):
         o0 = torch.empty(M, D, device=x.device)
         o1 = torch.empty(M, D, device=x.device)
         with _timed("pair_fwd", (M,)):
-            _lib.check(lib.matris_pair_fwd(M, _p(x), _p(pack.cat), _p(o0), _p(o1), _MMA["mode"], _stream()),
+            mode = _MMA["mode"]
+            _lib.check(lib.matris_pair_fwd(M, _p(x), _p(pack.b("cat", mode)), _p(o0), _p(o1), mode, _stream()),
                        "matris_pair_fwd")
         ctx.pack, ctx.mode = pack, _MMA["mode"]
         return o0, o1
 
     @staticmethod
     def backward(ctx, g0, g1):
-        dev = ctx.pack.cat.device
+        dev = ctx.pack.device
         lib = _lib.load()
         ref = g0 if g0 is not None else g1
         M = ref.shape[0]
@@ -394,8 +430,8 @@ class _Pair(torch.autograd.Function):
         g1 = torch.zeros(M, D, device=dev) if g1 is None else _f32c(g1)
         g_x = torch.empty(M, D, device=dev)
         with _timed("pair_bwd", (M,)):
-            _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(ctx.pack.cat_t), _p(g_x), ctx.mode, _stream()),
-                       "matris_pair_bwd")
+            _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(ctx.pack.b("cat_t", ctx.mode)), _p(g_x), ctx.mode,
+                                           _stream()), "matris_pair_bwd")
         return g_x, None
 
 

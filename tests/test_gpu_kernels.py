@@ -178,6 +178,29 @@ def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
 _MODES = [("fp32", 1e-5), ("bf16x6", 1e-5), ("bf16x3", 1e-4)]
 
 
+def test_pack_b_fragment_layout():
+    """Packed weight = fragment planes: unit ((nt*KB + kb)*NPL + plane)*64 + lane holds
+    row n = 32 nt + lane%32, k = 16 kb + 8 (lane//32) + j, j = 0..7."""
+    ops = _ops()
+    torch.manual_seed(3)
+    n, k = 64, 48
+    w = torch.randn(n, k) * torch.logspace(-3, 3, k)[None, :]
+    nn_, kk = torch.meshgrid(torch.arange(n), torch.arange(k), indexing="ij")
+    nt, kb, lane, j = nn_ // 32, kk // 16, nn_ % 32 + 32 * ((kk % 16) // 8), kk % 8
+    # mode 0: the fp32 values themselves, 8 per lane as two 16-byte planes
+    p0 = ops.pack_b(w.to(DEV), 0).cpu().view(torch.float32).view(n // 32, k // 16, 2, 64, 4)
+    assert torch.equal(p0[nt, kb, j // 4, lane, j % 4], w)
+    # mode 6: hi = bf16(w) (round to nearest even), and hi + mid + lo == w exactly
+    p6 = ops.pack_b(w.to(DEV), 6).cpu().view(torch.bfloat16).view(n // 32, k // 16, 3, 64, 8)
+    hi, mid, lo = (p6[nt, kb, q, lane, j].double() for q in range(3))
+    assert torch.equal(p6[nt, kb, 0, lane, j], w.to(torch.bfloat16))
+    assert torch.equal(hi + mid + lo, w.double())
+    assert (mid.abs() <= hi.abs() * 2.0 ** -8).all() and (lo.abs() <= mid.abs() * 2.0 ** -8).all()
+    # mode 3: the first two planes of mode 6
+    p3 = ops.pack_b(w.to(DEV), 3).cpu().view(torch.bfloat16).view(n // 32, k // 16, 2, 64, 8)
+    assert torch.equal(p3, p6[:, :, :2])
+
+
 @pytest.mark.parametrize("mode,tol", _MODES)
 @pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097])
 def test_ffn_fwd_bwd(M, mode, tol):

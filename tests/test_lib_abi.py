@@ -75,6 +75,12 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_ffn_bwd(10, v16, None, v16, v16, v16, 6, None) == -1001
     assert lib.matris_pair_fwd(10, v16, v16, v16, v16, 1, None) == -1001
     assert lib.matris_pair_bwd(-1, v16, v16, v16, v16, 0, None) == -1001
+    # weight packing: n not a multiple of 32, k not a multiple of 16, unknown mode
+    assert lib.matris_pack_b(48, 16, v16, 6, v16, None) == -1001
+    assert lib.matris_pack_b(32, 24, v16, 6, v16, None) == -1001
+    assert lib.matris_pack_b(32, 16, v16, 2, v16, None) == -1001
+    assert lib.matris_pack_b_bytes(256, 384, 6) == 256 * 384 * 6
+    assert lib.matris_pack_b_bytes(256, 384, 3) == lib.matris_pack_b_bytes(256, 384, 0) == 256 * 384 * 4
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
     assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, 3, None) == 0
