@@ -236,7 +236,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     v16f acc[2][2];
     zero_acc(acc);
     gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, G + blk * MATRIS_D, LDH, W2t, 2 * wave, MATRIS_D / 16, 0, lane);
-    // g_p = g_h * SiLU'(p)
+    // g_p = g_h * SiLU'(p); rows past M read row 0 of the tile (their results are unused)
+    const int nrows = (int)min((int64_t)BM, M - m0);
+    const float *__restrict__ Pt = P + m0 * 256;
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int col = wave * 64 + ct * 32 + l32;
@@ -245,17 +247,34 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = rt * 32 + acc_row(i, h);
-                const float p = (m0 + row < M) ? P[(m0 + row) * 256 + col] : 0.f;
-                acc[rt][ct][i] *= dsilu_f(p);
+                acc[rt][ct][i] *= dsilu_f(Pt[(row < nrows ? row : 0) * 256 + col]);
             }
     }
     __syncthreads();  // every wave is done reading g_z
     acc_to_lds<2>(acc, G, LDH, wave * 64, lane);
     __syncthreads();
 
-    // phase 3: g_x = g_p W1 over 128-column blocks; wave w -> 32 columns of each block.
-    // W1t is W1^T ([K, 256]) packed: output tile nt = column / 32, 16 k-blocks.
-    for (int cb = 0; cb < K; cb += MATRIS_D) {
+    // phase 3: g_x = g_p W1.  W1t is W1^T ([K, 256]) packed: output tile nt = column / 32,
+    // 16 k-blocks.  Passes of 256 columns (wave w -> 64 columns, 2 tiles, so each A
+    // fragment conversion feeds two tiles), then a 128-column pass (32 per wave) if K % 256.
+    float *__restrict__ gxt = g_x + m0 * K;
+    int cb = 0;
+    for (; cb + 256 <= K; cb += 256) {
+        v16f a2[2][2];
+        zero_acc(a2);
+        const int col0 = cb + wave * 64;
+        gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = rt * 32 + acc_row(i, h);
+                    if (row < nrows) gxt[row * K + col0 + ct * 32 + l32] = a2[rt][ct][i];
+                }
+    }
+    if (cb < K) {
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
@@ -265,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = rt * 32 + acc_row(i, h);
-                if (m0 + row < M) g_x[(m0 + row) * K + col0 + l32] = a2[rt][0][i];
+                if (row < nrows) gxt[row * K + col0 + l32] = a2[rt][0][i];
             }
     }
 }

@@ -51,8 +51,22 @@ __device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, v16f c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
-__device__ __forceinline__ float sigm_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// e^-x = 2^t, t = -x log2(e), on v_exp_f32 (1 ulp).  The rounding error of the product
+// (recovered exactly by an FMA, plus the fp32 representation error of log2 e) is applied
+// as the first-order factor 1 + err ln 2, so the result is within ~2 ulp of e^-x
+// instead of degrading with |t| ulp.  Overflow gives +inf (the product form keeps
+// inf * 1 = inf), underflow 0.
+__device__ __forceinline__ float exp_neg_f(float x) {
+    constexpr float kL2e = 1.44269502162933349609375f;  // fp32(log2 e)
+    constexpr float kL2eLo = 1.9259629911266175e-08f;   // log2 e - kL2e
+    constexpr float kLn2 = 0.693147180559945309f;
+    const float t = -x * kL2e;
+    const float err = fmaf(-x, kL2eLo, fmaf(-x, kL2e, -t));
+    return __builtin_amdgcn_exp2f(t) * (1.0f + err * kLn2);
+}
+// sigmoid = 1 / (1 + e^-x) with v_rcp_f32 (1 ulp); SiLU = x sigmoid(x).
+__device__ __forceinline__ float sigm_f(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_neg_f(x)); }
+__device__ __forceinline__ float silu_f(float x) { return x * sigm_f(x); }
 __device__ __forceinline__ float dsilu_f(float x) {
     float s = sigm_f(x);
     return s * (1.0f + x * (1.0f - s));
@@ -144,9 +158,10 @@ __device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *ba
 template <int MODE, int NRT, int NCT, int KBA>
 __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
+    constexpr int kUnroll = NCT >= 2 ? 1 : 2;  // 2-tile bodies are long enough; keeps pressure down
     Frag<MODE> cur[NCT], nxt[NCT];
     load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
-#pragma unroll 2
+#pragma unroll kUnroll
     for (int kb = 0; kb < KBA; ++kb) {
         if (kb + 1 < KBA) load_bfrags<MODE, NCT>(nxt, W, nt0, KBW, kb0 + kb + 1, lane);
         Frag<MODE> a[NRT];
