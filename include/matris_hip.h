@@ -123,9 +123,10 @@ int matris_gather_rows(const float *src, const int32_t *idx, int64_t n_rows, flo
  *   both over n_seg segments.
  * fwd writes y_t, y_s [n_seg,128] and the per-segment log-sum-exp lse_t, lse_s
  * [n_seg,128] needed by the backward.
- * bwd (input gradients only): given g_yt, g_ys, writes g_alpha_t, g_alpha_s [R,128]
- * (per row r, before any alpha_idx reduction) and g_e [R,128];
- * t_idx[R], s_idx[R] are the target / source segment of each row. */
+ * bwd (input gradients only): given g_yt, g_ys (rows of stride ldgy >= 128), writes
+ * g_alpha_t, g_alpha_s [R,128] (per row r, before any alpha_idx reduction) and
+ * g_e [R,128] (= g_e_base + the attention term when g_e_base is non-NULL; g_e_base may
+ * alias g_e); t_idx[R], s_idx[R] are the target / source segment of each row. */
 int matris_attn_fwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s, int64_t lda,
                     const int32_t *alpha_idx, const float *e, const int32_t *t_ptr, const int32_t *t_perm,
                     const int32_t *s_ptr, const int32_t *s_perm, float *y_t, float *y_s, float *lse_t,
@@ -133,7 +134,21 @@ int matris_attn_fwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const f
 int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s, int64_t lda,
                     const int32_t *alpha_idx, const float *e, const int32_t *t_idx, const int32_t *s_idx,
                     const float *y_t, const float *y_s, const float *lse_t, const float *lse_s, const float *g_yt,
-                    const float *g_ys, float *g_alpha_t, float *g_alpha_s, float *g_e, void *stream);
+                    const float *g_ys, int64_t ldgy, float *g_alpha_t, float *g_alpha_s, float *g_e,
+                    const float *g_e_base, void *stream);
+
+/* Envelope-weighted aggregation of the line-graph Refinement (interaction_block.py:243-258:
+ * smooth_weight = env[source] * env[target]; aggregate(h * smooth_weight, target)):
+ *   S[b] = sum_{a: tgt(a)=b} h[a] * env[src(a)],  agg[b] = env[b] * S[b]   (n_seg = rows of env)
+ * with the target CSR (t_ptr, t_perm|NULL) and s_idx = source of each row.
+ * bwd: g_h[a] = (accumulate ? g_h[a] : 0) + g_agg[tgt(a)] * env[tgt(a)] * env[src(a)];
+ *      g_env[b] = g_agg[b] * S[b] + sum_{a: src(a)=b} g_agg[tgt(a)] * env[tgt(a)] * h[a]
+ * (source CSR s_ptr, s_perm|NULL; t_idx = target of each row). */
+int matris_env_agg_fwd(int64_t n_seg, const float *h, const float *env, const int32_t *t_ptr, const int32_t *t_perm,
+                       const int32_t *s_idx, float *S, float *agg, void *stream);
+int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h, const float *env, const float *g_agg,
+                       const float *S, const int32_t *t_idx, const int32_t *s_idx, const int32_t *s_ptr,
+                       const int32_t *s_perm, int accumulate, float *g_h, float *g_env, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * MFMA arithmetic and packed weights (shared by the gated MLP, FFN and projection pair).
@@ -167,17 +182,22 @@ int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, void *out, voi
  *   w2p = pack of [mlp_core.layers.3.weight; mlp_gate.layers.3.weight] ([256, 128]), b2 [256];
  *   norm_c / norm_g [128] = core_norm.weight / gate_norm.weight, RMSNorm eps.
  * fwd writes out [M,128]; save_p / save_z [M,256] (layer-1 pre-activation and layer-2
- * output, both halves) when non-NULL -- the backward needs them.
+ * output, both halves) when non-NULL -- the backward needs them; with res_out non-NULL
+ * also res_out = out + res_w * res_src (the residual update `out + res_weight * feat`
+ * of interaction_block.py:140-141, res_w [128], res_src [M,128]).
  * bwd (input gradients only) reads g_out [M,128], p, z and the packed transposes
  * w1tp = pack of w1^T ([K, 256]) and w2tp = pack of [W2core^T; W2gate^T] ([256, 128]);
- * writes g_x [M,K]. */
+ * writes g_x [M,K], or, when g_x0 is non-NULL, source 0's columns to g_x0 [M,128]
+ * (added to its contents if acc0) and the rest to g_x [M,K-128] (NULL allowed if K=128).
+ * res_w non-NULL adds res_w * g_out to source 0's gradient (backward of res_out when
+ * res_src is source 0). */
 int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
                     const void *w1p, const float *b1, const void *w2p, const float *b2, const float *norm_c,
-                    const float *norm_g, float eps, float *out, float *save_p, float *save_z, int mode,
-                    void *stream);
+                    const float *norm_g, float eps, float *out, float *save_p, float *save_z,
+                    const float *res_src, const float *res_w, float *res_out, int mode, void *stream);
 int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
-                    const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x, int mode,
-                    void *stream);
+                    const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x, float *g_x0,
+                    int acc0, const float *res_w, int mode, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Dense layers on MFMA, 128-wide rows, no bias.
@@ -185,20 +205,23 @@ int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const 
 
 /* FFN out = W2 SiLU(W1 x): Refinement.node_FFN / edge_FFN, MLP(hidden=int, bias=False)
  * (matris/model/functions.py:198-205, interaction_block.py:198-210, 269-270).
- * w1p, w2p = packs of the [128,128] Linear weights; save_p [M,128] = W1 x (for bwd).
- * bwd: g_x = ((g W2) * SiLU'(p)) W1 with w1tp, w2tp = packs of w1^T, w2^T. */
-int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, float *out, float *save_p, int mode,
-                   void *stream);
+ * w1p, w2p = packs of the [128,128] Linear weights; save_p [M,128] = W1 x (for bwd);
+ * res non-NULL: out += res_w * res (the residual update, interaction_block.py:274-275).
+ * bwd: g_x = ((g W2) * SiLU'(p)) W1 with w1tp, w2tp = packs of w1^T, w2^T; g_res
+ * non-NULL receives res_w * g (gradient of the residual input). */
+int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, float *out, float *save_p,
+                   const float *res, const float *res_w, int mode, void *stream);
 int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp, float *g_x,
-                   int mode, void *stream);
+                   float *g_res, const float *res_w, int mode, void *stream);
 
 /* Attention projection pair (interaction_block.py:33-38, 110-111):
  * out0 = x W[0:128]^T (source_weight_linear), out1 = x W[128:256]^T (target);
  * wp = pack of W = [W_s; W_t] ([256,128]).
- * bwd: g_x = g0 W[0:128] + g1 W[128:256] with wtp = pack of W^T ([128,256]). */
+ * bwd: g_x = g0 W[0:128] + g1 W[128:256] (+ res_w * res when res is non-NULL) with
+ * wtp = pack of W^T ([128,256]). */
 int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, float *out1, int mode, void *stream);
-int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, int mode,
-                    void *stream);
+int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, const float *res,
+                    const float *res_w, int mode, void *stream);
 
 #ifdef __cplusplus
 }

@@ -83,15 +83,18 @@ _SIGS = {
     "matris_seg_sum": (_I, [_P, _I64, _I64, _P, _P, _I64, _F, _I, _P, _P]),
     "matris_gather_rows": (_I, [_P, _P, _I64, _F, _I, _P, _P]),
     "matris_attn_fwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _I, _P]),
-    "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P]),
+    "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
+                             _P]),
+    "matris_env_agg_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "matris_env_agg_bwd": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
+    "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I, _P]),
     "matris_pack_b_bytes": (_SZ, [_I64, _I64, _I]),
     "matris_pack_b": (_I, [_I64, _I64, _P, _I, _P, _P]),
-    "matris_ffn_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _I, _P]),
-    "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_ffn_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
-    "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
+    "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _P]),
 }
 
 EXPORTED = tuple(_SIGS)

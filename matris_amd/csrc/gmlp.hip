@@ -50,7 +50,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                           const float *__restrict__ norm_c,
                                                           const float *__restrict__ norm_g, float eps,
                                                           float *__restrict__ out, float *__restrict__ save_p,
-                                                          float *__restrict__ save_z) {
+                                                          float *__restrict__ save_z,
+                                                          const float *__restrict__ res_src,
+                                                          const float *__restrict__ res_w,
+                                                          float *__restrict__ res_out) {
     constexpr int NPL = Npl<MODE>::v;
     constexpr int CHUNK = 2 * 2 * NPL * 64;  // uint4 per LDS chunk: [rt 2][kb 2][plane][lane]
     __shared__ __align__(16) float smem[BM * LDH];
@@ -156,9 +159,11 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     __syncthreads();
     if (save_z) store_tile256(Ts, save_z, m0, M, tid);
 
-    // row epilogue: wave w -> rows [16w, 16w+16); lane -> columns 2l, 2l+1 of each half
+    // row epilogue: wave w -> rows [16w, 16w+16); lane -> columns 2l, 2l+1 of each half;
+    // optional residual output res_out = out + res_w * res_src
     const float2 wc = *reinterpret_cast<const float2 *>(norm_c + 2 * lane);
     const float2 wg = *reinterpret_cast<const float2 *>(norm_g + 2 * lane);
+    const float2 rw = res_out ? *reinterpret_cast<const float2 *>(res_w + 2 * lane) : make_float2(0.f, 0.f);
     for (int rr = 0; rr < BM / 4; ++rr) {
         const int row = wave * (BM / 4) + rr;
         const float2 zc = *reinterpret_cast<const float2 *>(Ts + row * LDH + 2 * lane);
@@ -168,13 +173,37 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         float2 o;
         o.x = silu_f(zc.x * rc * wc.x) * sigm_f(zg.x * rg * wg.x);
         o.y = silu_f(zc.y * rc * wc.y) * sigm_f(zg.y * rg * wg.y);
-        if (m0 + row < M) *reinterpret_cast<float2 *>(out + (m0 + row) * MATRIS_D + 2 * lane) = o;
+        if (m0 + row < M) {
+            *reinterpret_cast<float2 *>(out + (m0 + row) * MATRIS_D + 2 * lane) = o;
+            if (res_out) {
+                const float2 x = *reinterpret_cast<const float2 *>(res_src + (m0 + row) * MATRIS_D + 2 * lane);
+                *reinterpret_cast<float2 *>(res_out + (m0 + row) * MATRIS_D + 2 * lane) =
+                    make_float2(o.x + rw.x * x.x, o.y + rw.y * x.y);
+            }
+        }
     }
 }
 
 // ------------------------------------------------------------------------------------
 // backward
 // ------------------------------------------------------------------------------------
+// Store a wave's [64, 32*NCT] accumulators to rows of dst (row stride ld) at column
+// col + ct*32 + lane%32, rows below nrows only.
+template <int NCT>
+__device__ __forceinline__ void store_acc_rows(const v16f (&acc)[2][NCT], float *__restrict__ dst, int ld, int col,
+                                               int nrows, int lane) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = rt * 32 + acc_row(i, h);
+                if (row < nrows) dst[row * ld + col + ct * 32 + l32] = acc[rt][ct][i];
+            }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, const float *__restrict__ g_out,
                                                           const float *__restrict__ P, const float *__restrict__ Z,
@@ -182,7 +211,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                                           const uint4 *__restrict__ W2t,
                                                           const float *__restrict__ norm_c,
                                                           const float *__restrict__ norm_g, float eps,
-                                                          float *__restrict__ g_x) {
+                                                          float *__restrict__ g_x, float *__restrict__ g_x0,
+                                                          int acc0, const float *__restrict__ res_w) {
     __shared__ __align__(16) float G[BM * LDH];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
@@ -256,36 +286,63 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 
     // phase 3: g_x = g_p W1.  W1t is W1^T ([K, 256]) packed: output tile nt = column / 32,
     // 16 k-blocks.  Passes of 256 columns (wave w -> 64 columns, 2 tiles, so each A
-    // fragment conversion feeds two tiles), then a 128-column pass (32 per wave) if K % 256.
-    float *__restrict__ gxt = g_x + m0 * K;
-    int cb = 0;
-    for (; cb + 256 <= K; cb += 256) {
-        v16f a2[2][2];
-        zero_acc(a2);
-        const int col0 = cb + wave * 64;
-        gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int row = rt * 32 + acc_row(i, h);
-                    if (row < nrows) gxt[row * K + col0 + ct * 32 + l32] = a2[rt][ct][i];
-                }
-    }
-    if (cb < K) {
+    // fragment conversion feeds two tiles) and, if K % 256, one 128-column pass (32 per
+    // wave), in descending column order so that the pass holding source 0 (columns
+    // [0, 128)) ends the kernel.  Source 0's gradient goes to g_x0 when given (added to
+    // its contents if acc0) and gains res_w * g_out when res_w is given; that epilogue
+    // runs row-wise through LDS once G is no longer read.  Other columns go straight to
+    // g_x (row stride K - 128 with g_x0, K without).
+    const int coff = g_x0 ? MATRIS_D : 0;
+    const int ldr = K - coff;
+    float *__restrict__ gxr = g_x ? g_x + m0 * ldr : nullptr;
+    const bool epi0 = g_x0 != nullptr || res_w != nullptr;
+    if (K % 256) {
+        const int cb = K - MATRIS_D;
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
         gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
+        if (cb > 0 || !epi0) store_acc_rows<1>(a2, gxr, ldr, col0 - coff, nrows, lane);
+        if (cb == 0 && epi0) {  // K == 128: every wave holds source-0 columns
+            __syncthreads();
+            acc_to_lds<1>(a2, G, LDH, col0, lane);
+        }
+    }
+    for (int cb = (K / 256 - 1) * 256; cb >= 0; cb -= 256) {
+        v16f a2[2][2];
+        zero_acc(a2);
+        const int col0 = cb + wave * 64;
+        gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
+        if (col0 >= MATRIS_D || !epi0) store_acc_rows<2>(a2, gxr, ldr, col0 - coff, nrows, lane);
+        if (cb == 0 && epi0) {
+            __syncthreads();  // all waves are done reading G
+            if (col0 < MATRIS_D) acc_to_lds<2>(a2, G, LDH, col0, lane);
+        }
+    }
+    if (epi0) {
+        __syncthreads();
+        float *__restrict__ gx0 = g_x0 ? g_x0 + m0 * MATRIS_D : gxr;
+        const int ld0 = g_x0 ? MATRIS_D : ldr;
+        const float *__restrict__ got = g_out + m0 * MATRIS_D;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = rt * 32 + acc_row(i, h);
-                if (row < nrows) gxt[row * K + col0 + l32] = a2[rt][0][i];
+        for (int it = 0; it < (BM * 32) / 256; ++it) {
+            const int q = it * 256 + tid;
+            const int r = q >> 5, c4 = (q & 31) * 4;
+            if (r < nrows) {
+                float4 v = *reinterpret_cast<const float4 *>(G + r * LDH + c4);
+                if (res_w) {
+                    const float4 w = *reinterpret_cast<const float4 *>(res_w + c4);
+                    const float4 x = *reinterpret_cast<const float4 *>(got + r * MATRIS_D + c4);
+                    v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
+                }
+                float4 *o = reinterpret_cast<float4 *>(gx0 + r * ld0 + c4);
+                if (acc0) {
+                    const float4 p0 = *o;
+                    v.x += p0.x; v.y += p0.y; v.z += p0.z; v.w += p0.w;
+                }
+                *o = v;
             }
+        }
     }
 }
 
@@ -294,7 +351,8 @@ static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host,
                                const int32_t *const *src_idx_host, const void *w1p, const float *b1, const void *w2p,
                                const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
-                               float *save_p, float *save_z, int mode, void *stream) {
+                               float *save_p, float *save_z, const float *res_src, const float *res_w,
+                               float *res_out, int mode, void *stream) {
     if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
     if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1p || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
         return MATRIS_E_ARG;
@@ -306,37 +364,45 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
         if (j < n_src && (!s.ptr[j] || !aligned16(s.ptr[j]))) return MATRIS_E_ARG;
     }
     if (!aligned16(w1p) || !aligned16(w2p)) return MATRIS_E_ARG;
+    if (res_out && (!res_src || !res_w)) return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1 = (const uint4 *)w1p, *w2 = (const uint4 *)w2p;
     if (mode == 0)
-        gmlp_fwd_kernel<0><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
+        gmlp_fwd_kernel<0><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z,
+                                                 res_src, res_w, res_out);
     else if (mode == 3)
-        gmlp_fwd_kernel<3><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
+        gmlp_fwd_kernel<3><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z,
+                                                 res_src, res_w, res_out);
     else
-        gmlp_fwd_kernel<6><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z);
+        gmlp_fwd_kernel<6><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z,
+                                                 res_src, res_w, res_out);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
 extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                                const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
-                               int mode, void *stream) {
+                               float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
     if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
     if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1tp || !w2tp ||
-        !norm_c || !norm_g || !g_x)
+        !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
         return MATRIS_E_ARG;
     if (m == 0) return 0;
     if (!aligned16(w1tp) || !aligned16(w2tp)) return MATRIS_E_ARG;
+    if (acc0 && !g_x0) return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
     if (mode == 0)
-        gmlp_bwd_kernel<0><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
+        gmlp_bwd_kernel<0><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
+                                                 acc0, res_w);
     else if (mode == 3)
-        gmlp_bwd_kernel<3><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
+        gmlp_bwd_kernel<3><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
+                                                 acc0, res_w);
     else
-        gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x);
+        gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
+                                                 acc0, res_w);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

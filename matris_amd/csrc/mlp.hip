@@ -28,14 +28,39 @@ __device__ __forceinline__ void stage_tile128(float *dst, const float *__restric
     }
 }
 
+// Copy an LDS tile out to rows of dst; with res non-NULL, dst = tile + res_w * res (rows of
+// 128, per-column weight res_w).
 __device__ __forceinline__ void store_tile128(const float *tile, float *__restrict__ dst, int64_t ld, int64_t m0,
-                                              int64_t M, int tid) {
+                                              int64_t M, int tid, const float *__restrict__ res = nullptr,
+                                              const float *__restrict__ res_w = nullptr) {
 #pragma unroll
     for (int it = 0; it < (BM * 32) / 256; ++it) {
         const int q = it * 256 + tid;
         const int r = q >> 5, c4 = (q & 31) * 4;
-        if (m0 + r < M)
-            *reinterpret_cast<float4 *>(dst + (m0 + r) * ld + c4) = *reinterpret_cast<const float4 *>(tile + r * LDT + c4);
+        if (m0 + r < M) {
+            float4 v = *reinterpret_cast<const float4 *>(tile + r * LDT + c4);
+            if (res) {
+                const float4 x = *reinterpret_cast<const float4 *>(res + (m0 + r) * MATRIS_D + c4);
+                const float4 w = *reinterpret_cast<const float4 *>(res_w + c4);
+                v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
+            }
+            *reinterpret_cast<float4 *>(dst + (m0 + r) * ld + c4) = v;
+        }
+    }
+}
+
+// dst rows = w * tile (per-column weight w).
+__device__ __forceinline__ void store_tile128_scaled(const float *tile, float *__restrict__ dst,
+                                                     const float *__restrict__ w, int64_t m0, int64_t M, int tid) {
+#pragma unroll
+    for (int it = 0; it < (BM * 32) / 256; ++it) {
+        const int q = it * 256 + tid;
+        const int r = q >> 5, c4 = (q & 31) * 4;
+        if (m0 + r < M) {
+            const float4 v = *reinterpret_cast<const float4 *>(tile + r * LDT + c4);
+            const float4 s = *reinterpret_cast<const float4 *>(w + c4);
+            *reinterpret_cast<float4 *>(dst + (m0 + r) * MATRIS_D + c4) = make_float4(s.x * v.x, s.y * v.y, s.z * v.z, s.w * v.w);
+        }
     }
 }
 
@@ -45,7 +70,9 @@ __device__ __forceinline__ void store_tile128(const float *tile, float *__restri
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float *__restrict__ x,
                                                          const uint4 *__restrict__ W1, const uint4 *__restrict__ W2,
-                                                         float *__restrict__ out, float *__restrict__ save_p) {
+                                                         float *__restrict__ out, float *__restrict__ save_p,
+                                                         const float *__restrict__ res,
+                                                         const float *__restrict__ res_w) {
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -71,14 +98,15 @@ __global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float 
     gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, W2, wave, MATRIS_D / 16, 0, lane);
     acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);
     __syncthreads();
-    store_tile128(T0, out, MATRIS_D, m0, M, tid);
+    store_tile128(T0, out, MATRIS_D, m0, M, tid, res, res_w);
 }
 
 // FFN backward: g_x = ((g W2) * SiLU'(p)) W1, with w1t = W1^T, w2t = W2^T row-major.
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
                                                          const float *__restrict__ P, const uint4 *__restrict__ W1t,
-                                                         const uint4 *__restrict__ W2t, float *__restrict__ g_x) {
+                                                         const uint4 *__restrict__ W2t, float *__restrict__ g_x,
+                                                         float *__restrict__ g_res, const float *__restrict__ res_w) {
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -86,6 +114,7 @@ __global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float 
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     stage_tile128(T0, g, MATRIS_D, m0, M, tid);
     __syncthreads();
+    if (g_res) store_tile128_scaled(T0, g_res, res_w, m0, M, tid);
     v16f acc[2][1];
     zero_acc(acc);
     gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
@@ -135,7 +164,8 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
                                                           const float *__restrict__ g1, const uint4 *__restrict__ Wt,
-                                                          float *__restrict__ g_x) {
+                                                          float *__restrict__ g_x, const float *__restrict__ res,
+                                                          const float *__restrict__ res_w) {
     // Wt = W^T ([128, 256]) packed: g_x[m][k] = sum_n g[m][n] Wt[k][n], k-blocks 0..7
     // pair with g0, 8..15 with g1
     __shared__ __align__(16) float T0[BM * LDT];
@@ -152,7 +182,7 @@ __global__ __launch_bounds__(256, 2) void pair_bwd_kernel(int64_t M, const float
     __syncthreads();
     acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);
     __syncthreads();
-    store_tile128(T0, g_x, MATRIS_D, m0, M, tid);
+    store_tile128(T0, g_x, MATRIS_D, m0, M, tid, res, res_w);
 }
 
 // ------------------------------------------------------------------------------------
@@ -175,19 +205,21 @@ static bool mlp_args_ok(int mode, std::initializer_list<const void *> ptrs) {
 }
 
 extern "C" int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, float *out,
-                              float *save_p, int mode, void *stream) {
+                              float *save_p, const float *res, const float *res_w, int mode, void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {x, w1p, w2p, out}) || ((uintptr_t)save_p & 15)) return MATRIS_E_ARG;
+    if (res && (((uintptr_t)res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(ffn_fwd_kernel, m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p);
+    MLP_DISPATCH(ffn_fwd_kernel, m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p, res, res_w);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
 extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp,
-                              float *g_x, int mode, void *stream) {
+                              float *g_x, float *g_res, const float *res_w, int mode, void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {g, p, w1tp, w2tp, g_x})) return MATRIS_E_ARG;
+    if (g_res && (((uintptr_t)g_res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x);
+    MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x, g_res, res_w);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -201,11 +233,12 @@ extern "C" int matris_pair_fwd(int64_t m, const float *x, const void *wp, float 
     return 0;
 }
 
-extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, int mode,
-                               void *stream) {
+extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x,
+                               const float *res, const float *res_w, int mode, void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {g0, g1, wtp, g_x})) return MATRIS_E_ARG;
+    if (res && (((uintptr_t)res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x);
+    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x, res, res_w);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

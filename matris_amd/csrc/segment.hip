@@ -185,8 +185,8 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(
     const int32_t *__restrict__ aidx, const float *__restrict__ e, const int32_t *__restrict__ t_idx,
     const int32_t *__restrict__ s_idx, const float *__restrict__ y_t, const float *__restrict__ y_s,
     const float *__restrict__ lse_t, const float *__restrict__ lse_s, const float *__restrict__ g_yt,
-    const float *__restrict__ g_ys, float *__restrict__ g_alpha_t, float *__restrict__ g_alpha_s,
-    float *__restrict__ g_e) {
+    const float *__restrict__ g_ys, int64_t ldgy, float *__restrict__ g_alpha_t, float *__restrict__ g_alpha_s,
+    float *__restrict__ g_e, const float *__restrict__ g_e_base) {
     int64_t r = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (r >= n_rows) return;
     const int c = 2 * (threadIdx.x & 63);
@@ -195,11 +195,17 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(
     float2 at = ld2(alpha_t + a * lda + c), as = ld2(alpha_s + a * lda + c);
     float2 ev = ld2(e + r * MATRIS_D + c);
     float2 lt = ld2(lse_t + t * MATRIS_D + c), ls = ld2(lse_s + s * MATRIS_D + c);
-    float2 gt = ld2(g_yt + t * MATRIS_D + c), gs = ld2(g_ys + s * MATRIS_D + c);
+    float2 gt = ld2(g_yt + t * ldgy + c), gs = ld2(g_ys + s * ldgy + c);
     float2 yt = ld2(y_t + t * MATRIS_D + c), ys = ld2(y_s + s * MATRIS_D + c);
     float ptx = expf(at.x - lt.x), pty = expf(at.y - lt.y);
     float psx = expf(as.x - ls.x), psy = expf(as.y - ls.y);
-    st2(g_e + r * MATRIS_D + c, make_float2(ptx * gt.x + psx * gs.x, pty * gt.y + psy * gs.y));
+    float2 ge = make_float2(ptx * gt.x + psx * gs.x, pty * gt.y + psy * gs.y);
+    if (g_e_base) {
+        const float2 b0 = ld2(g_e_base + r * MATRIS_D + c);
+        ge.x += b0.x;
+        ge.y += b0.y;
+    }
+    st2(g_e + r * MATRIS_D + c, ge);
     st2(g_alpha_t + r * MATRIS_D + c, make_float2(ptx * gt.x * (ev.x - yt.x), pty * gt.y * (ev.y - yt.y)));
     st2(g_alpha_s + r * MATRIS_D + c, make_float2(psx * gs.x * (ev.x - ys.x), psy * gs.y * (ev.y - ys.y)));
 }
@@ -207,21 +213,135 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(
 extern "C" int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s,
                                int64_t lda, const int32_t *alpha_idx, const float *e, const int32_t *t_idx,
                                const int32_t *s_idx, const float *y_t, const float *y_s, const float *lse_t,
-                               const float *lse_s, const float *g_yt, const float *g_ys, float *g_alpha_t,
-                               float *g_alpha_s, float *g_e, void *stream) {
-    if (n_rows < 0 || n_seg < 0 || lda < MATRIS_D || (lda % 2) || !t_idx || !s_idx || !g_alpha_t || !g_alpha_s ||
-        !g_e)
+                               const float *lse_s, const float *g_yt, const float *g_ys, int64_t ldgy,
+                               float *g_alpha_t, float *g_alpha_s, float *g_e, const float *g_e_base, void *stream) {
+    if (n_rows < 0 || n_seg < 0 || lda < MATRIS_D || (lda % 2) || ldgy < MATRIS_D || (ldgy % 2) || !t_idx ||
+        !s_idx || !g_alpha_t || !g_alpha_s || !g_e)
         return MATRIS_E_ARG;
     if (n_rows == 0) return 0;
     if (alpha_idx)
         attn_bwd_kernel<true><<<matris_blocks(n_rows, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
-            n_rows, alpha_t, alpha_s, lda, alpha_idx, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys,
-            g_alpha_t, g_alpha_s, g_e);
+            n_rows, alpha_t, alpha_s, lda, alpha_idx, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ldgy,
+            g_alpha_t, g_alpha_s, g_e, g_e_base);
     else
         attn_bwd_kernel<false><<<matris_blocks(n_rows, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
-            n_rows, alpha_t, alpha_s, lda, nullptr, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys,
-            g_alpha_t, g_alpha_s, g_e);
+            n_rows, alpha_t, alpha_s, lda, nullptr, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ldgy,
+            g_alpha_t, g_alpha_s, g_e, g_e_base);
     MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
+// envelope-weighted aggregation of the line-graph refinement (interaction_block.py:243-258):
+//   agg[b] = sum_{a: tgt[a] = b} h[a] * env[src[a]] * env[tgt[a]] = env[b] * S[b],
+//   S[b]   = sum_{a: tgt[a] = b} h[a] * env[src[a]]
+// Backward:  g_h[a]   (+)= (g_agg * env)[tgt[a]] * env[src[a]]
+//            g_env[b]  = g_agg[b] * S[b] + sum_{a: src[a] = b} (g_agg * env)[tgt[a]] * h[a]
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void env_agg_fwd_kernel(int64_t n_seg, const float *__restrict__ h,
+                                                          const float *__restrict__ env,
+                                                          const int32_t *__restrict__ t_ptr,
+                                                          const int32_t *__restrict__ t_perm,
+                                                          const int32_t *__restrict__ s_idx, float *__restrict__ S,
+                                                          float *__restrict__ agg) {
+    const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if (seg >= n_seg) return;
+    const int c = 2 * (threadIdx.x & 63);
+    const int b = t_ptr[seg], end = t_ptr[seg + 1];
+    float2 acc = make_float2(0.f, 0.f);
+    int i = b;
+    for (; i + 2 <= end; i += 2) {
+        const int64_t r0 = t_perm ? t_perm[i] : i, r1 = t_perm ? t_perm[i + 1] : i + 1;
+        const int64_t s0 = s_idx[r0], s1 = s_idx[r1];
+        const float2 h0 = ld2(h + r0 * MATRIS_D + c), h1 = ld2(h + r1 * MATRIS_D + c);
+        const float2 w0 = ld2(env + s0 * MATRIS_D + c), w1 = ld2(env + s1 * MATRIS_D + c);
+        acc.x += h0.x * w0.x; acc.y += h0.y * w0.y;
+        acc.x += h1.x * w1.x; acc.y += h1.y * w1.y;
+    }
+    if (i < end) {
+        const int64_t r0 = t_perm ? t_perm[i] : i;
+        const float2 h0 = ld2(h + r0 * MATRIS_D + c), w0 = ld2(env + (int64_t)s_idx[r0] * MATRIS_D + c);
+        acc.x += h0.x * w0.x; acc.y += h0.y * w0.y;
+    }
+    const float2 et = ld2(env + seg * MATRIS_D + c);
+    st2(S + seg * MATRIS_D + c, acc);
+    st2(agg + seg * MATRIS_D + c, make_float2(et.x * acc.x, et.y * acc.y));
+}
+
+__global__ __launch_bounds__(256) void env_agg_bwd_rows_kernel(int64_t n_rows, const float *__restrict__ g_agg,
+                                                               const float *__restrict__ env,
+                                                               const int32_t *__restrict__ t_idx,
+                                                               const int32_t *__restrict__ s_idx, int accumulate,
+                                                               float *__restrict__ g_h) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one float4 per thread
+    const int64_t r = t >> 5;
+    if (r >= n_rows) return;
+    const int q = (int)(t & 31) * 4;
+    const int64_t tr = t_idx[r], sr = s_idx[r];
+    const float4 g = *reinterpret_cast<const float4 *>(g_agg + tr * MATRIS_D + q);
+    const float4 et = *reinterpret_cast<const float4 *>(env + tr * MATRIS_D + q);
+    const float4 es = *reinterpret_cast<const float4 *>(env + sr * MATRIS_D + q);
+    float4 v = make_float4(g.x * et.x * es.x, g.y * et.y * es.y, g.z * et.z * es.z, g.w * et.w * es.w);
+    float4 *o = reinterpret_cast<float4 *>(g_h + r * MATRIS_D + q);
+    if (accumulate) {
+        const float4 p = *o;
+        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    }
+    *o = v;
+}
+
+__global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, const float *__restrict__ h,
+                                                              const float *__restrict__ env,
+                                                              const float *__restrict__ g_agg,
+                                                              const float *__restrict__ S,
+                                                              const int32_t *__restrict__ s_ptr,
+                                                              const int32_t *__restrict__ s_perm,
+                                                              const int32_t *__restrict__ t_idx,
+                                                              float *__restrict__ g_env) {
+    const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if (seg >= n_seg) return;
+    const int c = 2 * (threadIdx.x & 63);
+    const int b = s_ptr[seg], end = s_ptr[seg + 1];
+    float2 acc = make_float2(0.f, 0.f);
+    for (int i = b; i < end; ++i) {
+        const int64_t r = s_perm ? s_perm[i] : i;
+        const int64_t tr = t_idx[r];
+        const float2 hv = ld2(h + r * MATRIS_D + c);
+        const float2 g = ld2(g_agg + tr * MATRIS_D + c), et = ld2(env + tr * MATRIS_D + c);
+        acc.x += g.x * et.x * hv.x;
+        acc.y += g.y * et.y * hv.y;
+    }
+    const float2 gs = ld2(g_agg + seg * MATRIS_D + c), sv = ld2(S + seg * MATRIS_D + c);
+    st2(g_env + seg * MATRIS_D + c, make_float2(gs.x * sv.x + acc.x, gs.y * sv.y + acc.y));
+}
+
+extern "C" int matris_env_agg_fwd(int64_t n_seg, const float *h, const float *env, const int32_t *t_ptr,
+                                  const int32_t *t_perm, const int32_t *s_idx, float *S, float *agg, void *stream) {
+    if (n_seg < 0 || !h || !env || !t_ptr || !s_idx || !S || !agg) return MATRIS_E_ARG;
+    if (n_seg == 0) return 0;
+    env_agg_fwd_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        n_seg, h, env, t_ptr, t_perm, s_idx, S, agg);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h, const float *env,
+                                  const float *g_agg, const float *S, const int32_t *t_idx, const int32_t *s_idx,
+                                  const int32_t *s_ptr, const int32_t *s_perm, int accumulate, float *g_h,
+                                  float *g_env, void *stream) {
+    if (n_rows < 0 || n_seg < 0 || !h || !env || !g_agg || !S || !t_idx || !s_idx || !s_ptr || !g_h || !g_env)
+        return MATRIS_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    if (n_rows > 0) {
+        env_agg_bwd_rows_kernel<<<matris_blocks(n_rows * 32, 256), 256, 0, st>>>(n_rows, g_agg, env, t_idx, s_idx,
+                                                                               accumulate, g_h);
+        MATRIS_CHECK_LAUNCH();
+    }
+    if (n_seg > 0) {
+        env_agg_bwd_env_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(n_seg, h, env, g_agg, S, s_ptr,
+                                                                                    s_perm, t_idx, g_env);
+        MATRIS_CHECK_LAUNCH();
+    }
     return 0;
 }
 

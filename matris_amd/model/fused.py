@@ -1,0 +1,162 @@
+"""Line-graph layers of the interaction block as single autograd nodes with an explicit
+backward.
+
+The line graph carries the A three-body rows (A >> E >> N), so every elementwise pass
+over [A, 128] tensors costs a full HBM round trip.  Here the residual updates, the
+envelope weighting and every gradient accumulation live inside the kernels
+(residual outputs of the gated-MLP / FFN epilogues, source-0 gradient accumulation in
+the gated-MLP backward, a base term in the attention backward, the fused envelope
+aggregation), so no [A, 128] tensor is touched by a separate elementwise kernel in
+either direction.  Only input gradients are produced (forces and stress need no
+parameter gradients).
+
+Reference: matris/model/interaction_block.py:17-143 (Graph_Attention_Layer, line graph
+branch) and :146-278 (Refinement, graph_type="line graph").
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .ops import D
+
+__all__ = ["line_attention", "line_refinement", "line_attention_fusable", "line_refinement_fusable"]
+
+
+def _zeros_if_none(g, like):
+    return torch.zeros_like(like) if g is None else ops._f32c(g)
+
+
+def _ffn_fusable(mlp) -> bool:
+    L = mlp.layers
+    return (len(L) == 4 and L[0].bias is None and L[3].bias is None and tuple(L[0].weight.shape) == (D, D)
+            and tuple(L[3].weight.shape) == (D, D) and type(L[1]).__name__ == "FusedSiLU")
+
+
+def _res_ok(w) -> bool:
+    return tuple(w.shape) == (1, D)
+
+
+def line_attention_fusable(layer) -> bool:
+    s, t = layer.source_weight_linear, layer.target_weight_linear
+    return (layer.edge_nonlinear_update._fusable() and layer.node_nonlinear_update._fusable()
+            and tuple(s.weight.shape) == (D, D) and s.bias is None and tuple(t.weight.shape) == (D, D)
+            and t.bias is None and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
+
+
+def line_refinement_fusable(layer) -> bool:
+    return (layer.graph_type == "line graph" and layer.edge_nonlinear_update._fusable()
+            and _ffn_fusable(layer.node_FFN) and _ffn_fusable(layer.edge_FFN)
+            and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
+
+
+class _LineAttention(torch.autograd.Function):
+    """Graph_Attention_Layer on the line graph (bonds = nodes, angles = edges):
+        e     = GatedMLP_e([tb, bond[tgt], bond[src]])                 [A]
+        y_t, y_s = attention(W_t tb, W_s tb, e; tgt, src)              [E]
+        n     = GatedMLP_n([bond, y_t, y_s])                           [E]
+        bond' = n + r_n * bond,  tb' = e + r_e * tb
+    """
+
+    @staticmethod
+    def forward(ctx, bond, tb, layer, lg):
+        ops._check_dev(bond, tb)
+        bond, tb = ops._f32c(bond), ops._f32c(tb)
+        mode = ops._MMA["mode"]
+        tgt, src = lg["grp_tgt"], lg["grp_src"]
+        A, E = tb.shape[0], bond.shape[0]
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        pe = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+        pn = layer.node_nonlinear_update._pack.get(layer.node_nonlinear_update)
+        pp = layer._proj.get(layer.source_weight_linear.weight, layer.target_weight_linear.weight)
+        e, p_e, z_e, tb_new = ops.gmlp_fwd_raw(pe, [tb, bond, bond], [None, tgt.key, src.key], A, mode, res=(tb, r_e))
+        a_s, a_t = ops.pair_fwd_raw(pp, tb, mode)
+        y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None)
+        _, p_n, z_n, bond_new = ops.gmlp_fwd_raw(pn, [bond, y_t, y_s], [None, None, None], E, mode,
+                                                 res=(bond, r_n))
+        ctx.save_for_backward(p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n)
+        ctx.mode, ctx.tgt, ctx.src = mode, tgt, src
+        ctx.packs, ctx.res = (pe, pn, pp), (r_n, r_e)
+        return bond_new, tb_new
+
+    @staticmethod
+    def backward(ctx, g_bond_new, g_tb_new):
+        p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n = ctx.saved_tensors
+        pe, pn, pp = ctx.packs
+        r_n, r_e = ctx.res
+        mode, tgt, src = ctx.mode, ctx.tgt, ctx.src
+        E, A = p_n.shape[0], p_e.shape[0]
+        g_bond_new = _zeros_if_none(g_bond_new, y_t)
+        g_tb_new = _zeros_if_none(g_tb_new, e)
+        # node update: g_bond = r_n g + dGatedMLP_n/dbond, g_y = [g_yt | g_ys]
+        g_bond = torch.empty(E, D, device=e.device)
+        g_y = ops.gmlp_bwd_raw(pn, g_bond_new, p_n, z_n, 3 * D, mode, g_x0=g_bond, acc0=False, res_w=r_n)
+        # attention: g_e = g_tb_new (residual branch) + attention term
+        g_at, g_as, g_e = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, None,
+                                           ldgy=2 * D, g_e_base=g_tb_new)
+        # projections + residual: g_tb = g_as W_s + g_at W_t + r_e g_tb_new
+        g_tb = ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_tb_new, res_w=r_e)
+        # edge update: source 0 (tb) accumulates into g_tb, bond gathers scatter into g_bond
+        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True)
+        ops.seg_sum_raw(g_x, src, ldx=2 * D, col_off=D, out=g_bond, accumulate=True)
+        return g_bond, g_tb, None, None
+
+
+class _LineRefinement(torch.autograd.Function):
+    """Refinement on the line graph:
+        h     = GatedMLP([tb, atom[atom_list], bond[tgt], bond[src]])   [A]
+        agg   = sum_tgt h * env[src] * env[tgt]                           [E]
+        bond' = node_FFN(agg) + r_n * bond,  tb' = edge_FFN(h) + r_e * tb
+    """
+
+    @staticmethod
+    def forward(ctx, tb, atom, bond, env, layer, lg):
+        ops._check_dev(tb, atom, bond, env)
+        tb, atom, bond, env = (ops._f32c(t) for t in (tb, atom, bond, env))
+        mode = ops._MMA["mode"]
+        tgt, src, grp_atom = lg["grp_tgt"], lg["grp_src"], lg["grp_atom"]
+        A = tb.shape[0]
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        ph = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+        L, M = layer.node_FFN.layers, layer.edge_FFN.layers
+        pn = layer._node_ffn.get(L[0].weight, L[3].weight)
+        pm = layer._edge_ffn.get(M[0].weight, M[3].weight)
+        h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [tb, atom, bond, bond], [None, grp_atom.key, tgt.key, src.key], A, mode)
+        agg, S = ops.env_agg_fwd_raw(h, env, tgt, src)
+        bond_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(bond, r_n))
+        tb_new, p_de = ops.ffn_fwd_raw(pm, h, mode, res=(tb, r_e))
+        ctx.save_for_backward(h, p_h, z_h, env, S, p_dn, p_de)
+        ctx.mode, ctx.tgt, ctx.src, ctx.grp_atom = mode, tgt, src, grp_atom
+        ctx.packs, ctx.res, ctx.n_atom = (ph, pn, pm), (r_n, r_e), atom.shape[0]
+        return bond_new, tb_new
+
+    @staticmethod
+    def backward(ctx, g_bond_new, g_tb_new):
+        h, p_h, z_h, env, S, p_dn, p_de = ctx.saved_tensors
+        ph, pn, pm = ctx.packs
+        r_n, r_e = ctx.res
+        mode, tgt, src = ctx.mode, ctx.tgt, ctx.src
+        E, A = env.shape[0], h.shape[0]
+        g_bond_new = _zeros_if_none(g_bond_new, env)
+        g_tb_new = _zeros_if_none(g_tb_new, h)
+        g_bond = torch.empty(E, D, device=h.device)
+        g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
+        g_tb = torch.empty(A, D, device=h.device)
+        g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, g_res=g_tb, res_w=r_e)
+        g_env = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h, accumulate=True)
+        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=True)
+        g_atom = ops.seg_sum_raw(g_x, ctx.grp_atom, ldx=3 * D, col_off=0)
+        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True)
+        ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_bond, accumulate=True)
+        return g_tb, g_atom, g_bond, g_env, None, None
+
+
+def line_attention(layer, bond, tb, lg):
+    """(bond', tb') of Graph_Attention_Layer.forward on the line graph."""
+    return _LineAttention.apply(bond, tb, layer, lg)
+
+
+def line_refinement(layer, tb, atom, bond, env, lg):
+    """(bond', tb') of Refinement.forward on the line graph; env = learnable_envelope(smooth_weight)."""
+    return _LineRefinement.apply(tb, atom, bond, env, layer, lg)

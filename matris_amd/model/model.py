@@ -4,12 +4,16 @@ weights and a reference checkpoint loads unchanged) whose forward runs the gfx95
 kernels of libmatris_hip.so:
 
   gated MLPs (every GatedMLP, with its input concatenation)  -> matris_gmlp_fwd / _bwd
+  node_FFN / edge_FFN, W_s / W_t projection pairs              -> matris_ffn_* / matris_pair_*
   Dimwise_softmax x2 + alpha * e' + both aggregations         -> matris_attn_fwd / _bwd
+  envelope-weighted line-graph aggregation                    -> matris_env_agg_fwd / _bwd
   aggregate(), index_select and their backward scatters      -> matris_seg_sum / _gather_rows
   graph construction                                          -> GraphConverter (G1-G5 kernels)
 
-Plain dense layers (edge/three-body embeddings, W_s / W_t projections, FFNs, heads) are
-library GEMMs (hipBLASLt through torch); elementwise glue is torch on the device.
+The two line-graph layers of each block (attention, refinement) run as single autograd
+nodes with an explicit backward (fused.py) so their residual updates and gradient sums
+stay inside the kernels.  The small embedding / envelope / head layers are library
+GEMMs (hipBLASLt through torch) and torch elementwise ops on the device.
 Forces and stress come from torch.autograd.grad exactly as in the reference
 (readout.py:202-217); every custom op supplies its own input-gradient kernel.
 
@@ -27,7 +31,7 @@ from torch import Tensor, nn
 
 from ..config import EV_A3_TO_GPA
 from ..graph.converter import GraphConverter
-from . import ops
+from . import fused, ops
 from .batch import process_graphs
 
 
@@ -363,6 +367,8 @@ class Graph_Attention_Layer(nn.Module):
 
     def forward(self, node_feat, edge_feat, graph, d2u: ops.Grouping | None = None):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
+        if d2u is None and fused.line_attention_fusable(self):  # one node, explicit backward
+            return fused.line_attention(self, node_feat, edge_feat, graph)
         if d2u is None:  # line graph: edges are the angles themselves
             e = self.edge_nonlinear_update.fused([(edge_feat, None), (node_feat, tgt), (node_feat, src)])
             a_s, a_t = self._projections(edge_feat)
@@ -413,6 +419,9 @@ class Refinement(nn.Module):
         if self.graph_type == "atom graph":
             w = ops.gather(self.learnable_envelope(smooth_weight), d2u)
             h = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
+        elif fused.line_refinement_fusable(self):  # one node, explicit backward
+            env = self.learnable_envelope(smooth_weight)
+            return fused.line_refinement(self, edge_feat, atom_feat, node_feat, env, graph)
         else:
             env = self.learnable_envelope(smooth_weight)
             w = ops.gather(env, src) * ops.gather(env, tgt)

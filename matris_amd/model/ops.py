@@ -175,24 +175,44 @@ def gather(src, grp: Grouping):
 # ------------------------------------------------------------------------------------
 # segment attention
 # ------------------------------------------------------------------------------------
+def attn_fwd_raw(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: Grouping | None):
+    """(y_t, y_s, lse_t, lse_s) of matris_attn_fwd."""
+    lib = _lib.load()
+    R, S = e.shape[0], tgt.n_seg
+    dev = e.device
+    y_t, y_s = torch.empty(S, D, device=dev), torch.empty(S, D, device=dev)
+    lse_t, lse_s = torch.empty(S, D, device=dev), torch.empty(S, D, device=dev)
+    aidx = alpha_grp.key if alpha_grp is not None else None
+    with _timed("attn_fwd_atom" if aidx is not None else "attn_fwd_line", (R, S, src.perm is not None)):
+        _lib.check(lib.matris_attn_fwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(aidx), _p(e), _p(tgt.rowptr),
+                                       _p(tgt.perm), _p(src.rowptr), _p(src.perm), _p(y_t), _p(y_s), _p(lse_t),
+                                       _p(lse_s), _stream()), "matris_attn_fwd")
+    return y_t, y_s, lse_t, lse_s
+
+
+def attn_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: Grouping, src: Grouping,
+                 alpha_grp: Grouping | None, ldgy: int = D, g_e_base=None):
+    """(g_alpha_t, g_alpha_s, g_e) per row of matris_attn_bwd; g_yt / g_ys may be views
+    of row stride ldgy; g_e = g_e_base + attention term when g_e_base is given."""
+    lib = _lib.load()
+    R, S = e.shape[0], tgt.n_seg
+    dev = e.device
+    g_at, g_as, g_e = (torch.empty(R, D, device=dev) for _ in range(3))
+    ag = alpha_grp
+    with _timed("attn_bwd_atom" if ag is not None else "attn_bwd_line", (R, S)):
+        _lib.check(lib.matris_attn_bwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(ag.key if ag is not None else None),
+                                       _p(e), _p(tgt.key), _p(src.key), _p(y_t), _p(y_s), _p(lse_t), _p(lse_s),
+                                       _p(g_yt), _p(g_ys), ldgy, _p(g_at), _p(g_as), _p(g_e), _p(g_e_base),
+                                       _stream()), "matris_attn_bwd")
+    return g_at, g_as, g_e
+
+
 class _SegAttn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp):
         _check_dev(alpha_t, alpha_s, e)
         alpha_t, alpha_s, e = _f32c(alpha_t), _f32c(alpha_s), _f32c(e)
-        lib = _lib.load()
-        R, S = e.shape[0], tgt.n_seg
-        dev = e.device
-        y_t = torch.empty(S, D, device=dev)
-        y_s = torch.empty(S, D, device=dev)
-        lse_t = torch.empty(S, D, device=dev)
-        lse_s = torch.empty(S, D, device=dev)
-        aidx = alpha_grp.key if alpha_grp is not None else None
-        name = "attn_fwd_atom" if aidx is not None else "attn_fwd_line"
-        with _timed(name, (R, S, src.perm is not None)):
-            _lib.check(lib.matris_attn_fwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(aidx), _p(e), _p(tgt.rowptr),
-                                           _p(tgt.perm), _p(src.rowptr), _p(src.perm), _p(y_t), _p(y_s),
-                                           _p(lse_t), _p(lse_s), _stream()), "matris_attn_fwd")
+        y_t, y_s, lse_t, lse_s = attn_fwd_raw(alpha_t, alpha_s, e, tgt, src, alpha_grp)
         ctx.save_for_backward(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s)
         ctx.tgt, ctx.src, ctx.alpha_grp = tgt, src, alpha_grp
         return y_t, y_s
@@ -202,17 +222,8 @@ class _SegAttn(torch.autograd.Function):
         alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s = ctx.saved_tensors
         g_yt = torch.zeros_like(y_t) if g_yt is None else _f32c(g_yt)
         g_ys = torch.zeros_like(y_s) if g_ys is None else _f32c(g_ys)
-        lib = _lib.load()
-        R, S = e.shape[0], ctx.tgt.n_seg
-        g_at = torch.empty(R, D, device=e.device)
-        g_as = torch.empty(R, D, device=e.device)
-        g_e = torch.empty(R, D, device=e.device)
         ag = ctx.alpha_grp
-        with _timed("attn_bwd_atom" if ag is not None else "attn_bwd_line", (R, S)):
-            _lib.check(lib.matris_attn_bwd(R, S, _p(alpha_t), _p(alpha_s), D,
-                                           _p(ag.key if ag is not None else None), _p(e), _p(ctx.tgt.key),
-                                           _p(ctx.src.key), _p(y_t), _p(y_s), _p(lse_t), _p(lse_s), _p(g_yt),
-                                           _p(g_ys), _p(g_at), _p(g_as), _p(g_e), _stream()), "matris_attn_bwd")
+        g_at, g_as, g_e = attn_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ctx.tgt, ctx.src, ag)
         if ag is not None:  # alpha rows were read through alpha_grp.key: reduce back
             g_at = seg_sum_raw(g_at, ag)
             g_as = seg_sum_raw(g_as, ag)
@@ -223,6 +234,33 @@ def seg_attention(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: 
     """(y_t, y_s): Dimwise_softmax of alpha by target / source segment times e, summed
     per segment (interaction_block.py:113-134)."""
     return _SegAttn.apply(alpha_t, alpha_s, e, tgt, src, alpha_grp)
+
+
+# ------------------------------------------------------------------------------------
+# envelope-weighted aggregation (line-graph Refinement)
+# ------------------------------------------------------------------------------------
+def env_agg_fwd_raw(h, env, tgt: Grouping, src: Grouping):
+    """(agg, S): agg[b] = env[b] * S[b], S[b] = sum over rows a with target b of
+    h[a] * env[source(a)]  (interaction_block.py:243-258)."""
+    lib = _lib.load()
+    E = env.shape[0]
+    agg, S = torch.empty(E, D, device=h.device), torch.empty(E, D, device=h.device)
+    with _timed("env_agg_fwd", (h.shape[0], E)):
+        _lib.check(lib.matris_env_agg_fwd(E, _p(h), _p(env), _p(tgt.rowptr), _p(tgt.perm), _p(src.key), _p(S),
+                                          _p(agg), _stream()), "matris_env_agg_fwd")
+    return agg, S
+
+
+def env_agg_bwd_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, g_h, accumulate: bool):
+    """g_h (+)= g_agg[tgt] * env[tgt] * env[src]; returns g_env."""
+    lib = _lib.load()
+    E = env.shape[0]
+    g_env = torch.empty(E, D, device=h.device)
+    with _timed("env_agg_bwd", (h.shape[0], E)):
+        _lib.check(lib.matris_env_agg_bwd(h.shape[0], E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key), _p(src.key),
+                                          _p(src.rowptr), _p(src.perm), int(accumulate), _p(g_h), _p(g_env),
+                                          _stream()), "matris_env_agg_bwd")
+    return g_env
 
 
 # ------------------------------------------------------------------------------------
@@ -288,25 +326,56 @@ class GmlpPack(_PackCache):
         return self
 
 
+def _vec(w):
+    """A [1, 128] residual weight as a contiguous fp32 [128] device vector."""
+    return w.detach().reshape(-1).float().contiguous()
+
+
+def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, save: bool = True):
+    """matris_gmlp_fwd; srcs are [*,128] fp32 tensors, idxs int32 gather keys or None.
+    res = (res_src, res_w) also returns res_out = out + res_w * res_src.
+    Returns (out, p, z, res_out)."""
+    lib = _lib.load()
+    dev = srcs[0].device
+    nsrc = len(srcs)
+    out = torch.empty(n_rows, D, device=dev)
+    p = torch.empty(n_rows, 256, device=dev) if save else None
+    z = torch.empty(n_rows, 256, device=dev) if save else None
+    res_out = torch.empty(n_rows, D, device=dev) if res is not None else None
+    src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
+    idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
+    rs, rw = (res if res is not None else (None, None))
+    with _timed("gmlp_fwd", (n_rows, nsrc * D)):
+        _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
+                                       _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
+                                       _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
+                   "matris_gmlp_fwd")
+    return out, p, z, res_out
+
+
+def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None, acc0: bool = False, res_w=None):
+    """matris_gmlp_bwd.  Without g_x0 returns g_x [M, K]; with g_x0 source 0's gradient
+    goes (accumulated if acc0, plus res_w * g if res_w) to g_x0 and the other columns to
+    g_x [M, K-128] (allocated when not given; None when K == 128)."""
+    lib = _lib.load()
+    M = p.shape[0]
+    if g_x is None and not (g_x0 is not None and K == D):
+        g_x = torch.empty(M, K - (D if g_x0 is not None else 0), device=g.device)
+    with _timed("gmlp_bwd", (M, K)):
+        _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)),
+                                       _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w),
+                                       mode, _stream()), "matris_gmlp_bwd")
+    return g_x
+
+
 class _GatedMLP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, pack, groupings, n_rows, *srcs):
         _check_dev(*srcs)
         srcs = [_f32c(s) for s in srcs]
-        lib = _lib.load()
-        nsrc = len(srcs)
-        dev = srcs[0].device
-        out = torch.empty(n_rows, D, device=dev)
-        p = torch.empty(n_rows, 256, device=dev)
-        z = torch.empty(n_rows, 256, device=dev)
-        src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
-        idx_arr = (ctypes.c_void_p * 4)(*[(g.key.data_ptr() if g is not None else None) for g in groupings])
-        with _timed("gmlp_fwd", (n_rows, nsrc * D)):
-            mode = _MMA["mode"]
-            _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
-                                           _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
-                                           _p(out), _p(p), _p(z), mode, _stream()), "matris_gmlp_fwd")
-        ctx.mode = _MMA["mode"]
+        mode = _MMA["mode"]
+        out, p, z, _ = gmlp_fwd_raw(pack, srcs, [g.key if g is not None else None for g in groupings], n_rows, mode)
+        ctx.mode = mode
         ctx.save_for_backward(p, z)
         ctx.pack, ctx.groupings = pack, groupings
         ctx.src_rows = [s.shape[0] for s in srcs]
@@ -316,15 +385,8 @@ class _GatedMLP(torch.autograd.Function):
     def backward(ctx, g):
         p, z = ctx.saved_tensors
         g = _f32c(g)
-        lib = _lib.load()
-        pack = ctx.pack
-        M = p.shape[0]
         K = D * len(ctx.groupings)
-        g_x = torch.empty(M, K, device=g.device)
-        with _timed("gmlp_bwd", (M, K)):
-            _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", ctx.mode)),
-                                           _p(pack.b("w2bt", ctx.mode)), _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x),
-                                           ctx.mode, _stream()), "matris_gmlp_bwd")
+        g_x = gmlp_bwd_raw(ctx.pack, g, p, z, K, ctx.mode)
         grads = []
         for j, grp in enumerate(ctx.groupings):
             if not ctx.needs_input_grad[3 + j]:
@@ -368,35 +430,66 @@ class _WeightPack(_PackCache):
         return self
 
 
+def ffn_fwd_raw(pack: _WeightPack, x, mode: int, res=None):
+    """(out, p) of matris_ffn_fwd; res = (res_src, res_w) adds res_w * res_src to out."""
+    lib = _lib.load()
+    M = x.shape[0]
+    out, p = torch.empty(M, D, device=x.device), torch.empty(M, D, device=x.device)
+    rs, rw = (res if res is not None else (None, None))
+    with _timed("ffn_fwd", (M,)):
+        _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.b("w0", mode)), _p(pack.b("w1", mode)), _p(out), _p(p),
+                                      _p(rs), _p(rw), mode, _stream()), "matris_ffn_fwd")
+    return out, p
+
+
+def ffn_bwd_raw(pack: _WeightPack, g, p, mode: int, g_res=None, res_w=None):
+    """g_x of matris_ffn_bwd; g_res (given) receives res_w * g."""
+    lib = _lib.load()
+    M = p.shape[0]
+    g_x = torch.empty(M, D, device=g.device)
+    with _timed("ffn_bwd", (M,)):
+        _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(pack.b("wt0", mode)), _p(pack.b("wt1", mode)), _p(g_x),
+                                      _p(g_res), _p(res_w), mode, _stream()), "matris_ffn_bwd")
+    return g_x
+
+
+def pair_fwd_raw(pack: _WeightPack, x, mode: int):
+    """(x W0^T, x W1^T) of matris_pair_fwd."""
+    lib = _lib.load()
+    M = x.shape[0]
+    o0, o1 = torch.empty(M, D, device=x.device), torch.empty(M, D, device=x.device)
+    with _timed("pair_fwd", (M,)):
+        _lib.check(lib.matris_pair_fwd(M, _p(x), _p(pack.b("cat", mode)), _p(o0), _p(o1), mode, _stream()),
+                   "matris_pair_fwd")
+    return o0, o1
+
+
+def pair_bwd_raw(pack: _WeightPack, g0, g1, mode: int, res=None, res_w=None):
+    """g0 W0 + g1 W1 (+ res_w * res) of matris_pair_bwd."""
+    lib = _lib.load()
+    M = g0.shape[0]
+    g_x = torch.empty(M, D, device=g0.device)
+    with _timed("pair_bwd", (M,)):
+        _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(pack.b("cat_t", mode)), _p(g_x), _p(res), _p(res_w),
+                                       mode, _stream()), "matris_pair_bwd")
+    return g_x
+
+
 class _FFN(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, pack):
         _check_dev(x)
         x = _f32c(x)
-        lib = _lib.load()
-        M = x.shape[0]
-        out = torch.empty(M, D, device=x.device)
-        p = torch.empty(M, D, device=x.device)
-        with _timed("ffn_fwd", (M,)):
-            mode = _MMA["mode"]
-            _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.b("w0", mode)), _p(pack.b("w1", mode)), _p(out), _p(p),
-                                          mode, _stream()), "matris_ffn_fwd")
+        mode = _MMA["mode"]
+        out, p = ffn_fwd_raw(pack, x, mode)
         ctx.save_for_backward(p)
-        ctx.pack, ctx.mode = pack, _MMA["mode"]
+        ctx.pack, ctx.mode = pack, mode
         return out
 
     @staticmethod
     def backward(ctx, g):
         (p,) = ctx.saved_tensors
-        g = _f32c(g)
-        lib = _lib.load()
-        M = p.shape[0]
-        g_x = torch.empty(M, D, device=g.device)
-        with _timed("ffn_bwd", (M,)):
-            _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(ctx.pack.b("wt0", ctx.mode)),
-                                          _p(ctx.pack.b("wt1", ctx.mode)), _p(g_x), ctx.mode, _stream()),
-                       "matris_ffn_bwd")
-        return g_x, None
+        return ffn_bwd_raw(ctx.pack, _f32c(g), p, ctx.mode), None
 
 
 def ffn(pack: _WeightPack, x):
@@ -409,30 +502,18 @@ class _Pair(torch.autograd.Function):
     def forward(ctx, x, pack):
         _check_dev(x)
         x = _f32c(x)
-        lib = _lib.load()
-        M = x.shape[0]
-        o0 = torch.empty(M, D, device=x.device)
-        o1 = torch.empty(M, D, device=x.device)
-        with _timed("pair_fwd", (M,)):
-            mode = _MMA["mode"]
-            _lib.check(lib.matris_pair_fwd(M, _p(x), _p(pack.b("cat", mode)), _p(o0), _p(o1), mode, _stream()),
-                       "matris_pair_fwd")
-        ctx.pack, ctx.mode = pack, _MMA["mode"]
-        return o0, o1
+        mode = _MMA["mode"]
+        ctx.pack, ctx.mode = pack, mode
+        return pair_fwd_raw(pack, x, mode)
 
     @staticmethod
     def backward(ctx, g0, g1):
         dev = ctx.pack.device
-        lib = _lib.load()
         ref = g0 if g0 is not None else g1
         M = ref.shape[0]
         g0 = torch.zeros(M, D, device=dev) if g0 is None else _f32c(g0)
         g1 = torch.zeros(M, D, device=dev) if g1 is None else _f32c(g1)
-        g_x = torch.empty(M, D, device=dev)
-        with _timed("pair_bwd", (M,)):
-            _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(ctx.pack.b("cat_t", ctx.mode)), _p(g_x), ctx.mode,
-                                           _stream()), "matris_pair_bwd")
-        return g_x, None
+        return pair_bwd_raw(ctx.pack, g0, g1, ctx.mode), None
 
 
 def proj_pair(pack: _WeightPack, x):

@@ -64,17 +64,27 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_seg_sum(None, 256, 192, ctypes.c_void_p(8), None, 1, 1.0, 0, ctypes.c_void_p(8), None) == -1001
     # gated MLP: 5 sources, or a K that is not a multiple of 128
     src = (ctypes.c_void_p * 4)()
-    assert lib.matris_gmlp_fwd(10, 5, src, None, *([ctypes.c_void_p(16)] * 6), 1e-7, ctypes.c_void_p(16),
-                               None, None, 6, None) == -1001
-    assert lib.matris_gmlp_bwd(10, 200, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), 6, None) == -1001
-    # unknown MFMA mode
-    assert lib.matris_gmlp_bwd(10, 256, *([ctypes.c_void_p(16)] * 7), 1e-7, ctypes.c_void_p(16), 5, None) == -1001
-    # dense layers: misaligned row pointer, null operand, unknown mode
     v16 = ctypes.c_void_p(16)
-    assert lib.matris_ffn_fwd(10, ctypes.c_void_p(8), v16, v16, v16, None, 6, None) == -1001
-    assert lib.matris_ffn_bwd(10, v16, None, v16, v16, v16, 6, None) == -1001
+    assert lib.matris_gmlp_fwd(10, 5, src, None, *([v16] * 6), 1e-7, v16, None, None, None, None, None, 6,
+                               None) == -1001
+    assert lib.matris_gmlp_bwd(10, 200, *([v16] * 7), 1e-7, v16, None, 0, None, 6, None) == -1001
+    # unknown MFMA mode; residual output without its source; accumulate without g_x0
+    assert lib.matris_gmlp_bwd(10, 256, *([v16] * 7), 1e-7, v16, None, 0, None, 5, None) == -1001
+    src1 = (ctypes.c_void_p * 4)(16)
+    assert lib.matris_gmlp_fwd(10, 1, src1, None, *([v16] * 6), 1e-7, v16, None, None, None, v16, v16, 6,
+                               None) == -1001
+    assert lib.matris_gmlp_bwd(10, 256, *([v16] * 7), 1e-7, v16, None, 1, None, 6, None) == -1001
+    # dense layers: misaligned row pointer, null operand, unknown mode, residual without weight
+    assert lib.matris_ffn_fwd(10, ctypes.c_void_p(8), v16, v16, v16, None, None, None, 6, None) == -1001
+    assert lib.matris_ffn_fwd(10, v16, v16, v16, v16, None, v16, None, 6, None) == -1001
+    assert lib.matris_ffn_bwd(10, v16, None, v16, v16, v16, None, None, 6, None) == -1001
     assert lib.matris_pair_fwd(10, v16, v16, v16, v16, 1, None) == -1001
-    assert lib.matris_pair_bwd(-1, v16, v16, v16, v16, 0, None) == -1001
+    assert lib.matris_pair_bwd(-1, v16, v16, v16, v16, None, None, 0, None) == -1001
+    # attention backward: gradient row stride below 128; envelope aggregation: null operand
+    assert lib.matris_attn_bwd(10, 5, v16, v16, 128, None, v16, v16, v16, v16, v16, v16, v16, v16, v16, 64, v16,
+                               v16, v16, None, None) == -1001
+    assert lib.matris_env_agg_fwd(5, v16, None, v16, None, v16, v16, v16, None) == -1001
+    assert lib.matris_env_agg_bwd(10, 5, v16, v16, v16, v16, v16, v16, v16, None, 0, None, v16, None) == -1001
     # weight packing: n not a multiple of 32, k not a multiple of 16, unknown mode
     assert lib.matris_pack_b(48, 16, v16, 6, v16, None) == -1001
     assert lib.matris_pack_b(32, 24, v16, 6, v16, None) == -1001
@@ -83,4 +93,5 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_pack_b_bytes(256, 384, 3) == lib.matris_pack_b_bytes(256, 384, 0) == 256 * 384 * 4
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
-    assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, 3, None) == 0
+    assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, None, None, 3, None) == 0
+    assert lib.matris_env_agg_fwd(0, v16, v16, v16, None, v16, v16, v16, None) == 0
