@@ -69,15 +69,15 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // which is exactly the fragment (tile xr/32, k-block xq/2, lane xr%32 + 32*(xq&1)).
     const int xr = tid >> 2, xq = tid & 3, xc = xq * 8;
     const int xslot = ((xr >> 5) * 2 + (xq >> 1)) * NPL * 64 + (xr & 31) + 32 * (xq & 1);
-    const int64_t grow = m0 + xr;
-    const bool xvalid = grow < M;
+    // Rows past M read row M-1 (their results are never stored), so every prefetch load
+    // below is unconditional and the compiler can count outstanding loads exactly
+    // instead of draining them all (a conditional load forces s_waitcnt vmcnt(0)).
+    const int64_t grow = min(m0 + xr, M - 1);
     int64_t sr0 = 0, sr1 = 0, sr2 = 0, sr3 = 0;
-    if (xvalid) {
-        sr0 = src.idx[0] ? (int64_t)src.idx[0][grow] : grow;
-        if (nsrc > 1) sr1 = src.idx[1] ? (int64_t)src.idx[1][grow] : grow;
-        if (nsrc > 2) sr2 = src.idx[2] ? (int64_t)src.idx[2][grow] : grow;
-        if (nsrc > 3) sr3 = src.idx[3] ? (int64_t)src.idx[3][grow] : grow;
-    }
+    sr0 = src.idx[0] ? (int64_t)src.idx[0][grow] : grow;
+    if (nsrc > 1) sr1 = src.idx[1] ? (int64_t)src.idx[1][grow] : grow;
+    if (nsrc > 2) sr2 = src.idx[2] ? (int64_t)src.idx[2][grow] : grow;
+    if (nsrc > 3) sr3 = src.idx[3] ? (int64_t)src.idx[3][grow] : grow;
 
     float4 x0, x1;
 #define GMLP_LOADX(kc)                                                                                   \
@@ -87,13 +87,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                          : j_ == 1 ? src.ptr[1] + sr1 * MATRIS_D                                         \
                          : j_ == 2 ? src.ptr[2] + sr2 * MATRIS_D                                         \
                                    : src.ptr[3] + sr3 * MATRIS_D;                                        \
-        if (xvalid) {                                                                                    \
-            const float4 *xp_ = reinterpret_cast<const float4 *>(sp_ + cc_ + xc);                        \
-            x0 = xp_[0];                                                                                 \
-            x1 = xp_[1];                                                                                 \
-        } else {                                                                                         \
-            x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);                                                   \
-        }                                                                                                \
+        const float4 *xp_ = reinterpret_cast<const float4 *>(sp_ + cc_ + xc);                            \
+        x0 = xp_[0];                                                                                     \
+        x1 = xp_[1];                                                                                     \
     } while (0)
 #define GMLP_STOREX(buf)                                                                                 \
     do {                                                                                                 \
@@ -111,13 +107,13 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     __syncthreads();
 #pragma unroll 1
     for (int c = 0; c < nchunk; ++c) {
-        const bool more = c + 1 < nchunk;
-        if (more) GMLP_LOADX((c + 1) * 32);
+        GMLP_LOADX(min(c + 1, nchunk - 1) * 32);  // the last iteration reloads its own chunk
         const uint4 *xb = Xp + (c & 1) * CHUNK;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const int kb = 2 * c + sub;
-            if (kb + 1 < KB) load_bfrags<MODE, 2>(bnxt, W1, 2 * wave, KB, kb + 1, lane);
+            load_bfrags<MODE, 2>(bnxt, W1, 2 * wave, KB, min(kb + 1, KB - 1), lane);
+            __builtin_amdgcn_sched_barrier(0);  // issue the prefetches before this step's MFMAs
             Frag<MODE> a[2];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
@@ -130,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             bcur[0] = bnxt[0];
             bcur[1] = bnxt[1];
         }
-        if (more) GMLP_STOREX((c + 1) & 1);
+        GMLP_STOREX((c + 1) & 1);  // unread after the last chunk
         __syncthreads();
     }
 #undef GMLP_LOADX

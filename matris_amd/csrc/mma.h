@@ -154,7 +154,9 @@ __device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *ba
 
 // acc[rt][ct] += A[rt tile, k-blocks 0..KBA) * B[k-blocks kb0.., tile nt0 + ct] with A an
 // fp32 row-major LDS array and B a packed weight (KBW k-blocks); the next k-block's B
-// fragments are loaded while the current one is consumed.
+// fragments are loaded while the current one is consumed.  The prefetch is
+// unconditional (the last step reloads its own block) so the compiler's load counting
+// stays exact.
 template <int MODE, int NRT, int NCT, int KBA>
 __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
@@ -163,17 +165,16 @@ __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const flo
     load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
 #pragma unroll kUnroll
     for (int kb = 0; kb < KBA; ++kb) {
-        if (kb + 1 < KBA) load_bfrags<MODE, NCT>(nxt, W, nt0, KBW, kb0 + kb + 1, lane);
+        load_bfrags<MODE, NCT>(nxt, W, nt0, KBW, kb0 + min(kb + 1, KBA - 1), lane);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
         Frag<MODE> a[NRT];
         lds_afrags<MODE, NRT>(a, a_base, lda, kb, lane);
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) mma_frag<MODE>(acc[rt][ct], a[rt], cur[ct]);
-        if (kb + 1 < KBA) {
 #pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
-        }
+        for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
     }
 }
 

@@ -20,7 +20,27 @@ import torch
 from . import ops
 from .ops import D
 
-__all__ = ["line_attention", "line_refinement", "line_attention_fusable", "line_refinement_fusable"]
+__all__ = ["line_attention", "line_refinement", "line_attention_fusable", "line_refinement_fusable",
+           "checkpoint_needed"]
+
+# Approximate saved-activation bytes per interaction block when nothing is recomputed:
+# per angle, line attention p_e, z_e [256] + a_s, a_t, e [128] and line refinement
+# p_h, z_h [256] + h, edge-FFN pre-activation [128], plus the block's angle output
+# [128]; per directed edge, the atom-graph layers' autograd tape (gated-MLP
+# pre-activations, attention logits, gathers, FFN) -- about 16 [E_d, 128] tensors (fp32).
+SAVED_BYTES_PER_ANGLE_BLOCK = 4 * (2 * 256 + 3 * 128 + 2 * 256 + 2 * 128 + 128)
+SAVED_BYTES_PER_EDGE_BLOCK = 4 * 16 * 128
+
+
+def checkpoint_needed(n_angles: int, n_edges: int, n_blocks: int, device=None, total_bytes: int | None = None) -> bool:
+    """Checkpoint each interaction block (keep its inputs, rerun its forward in the
+    backward) when the whole model's saved activations would exceed 45% of the device's
+    memory (total_bytes, default: the device's capacity).  The reference checkpoints its
+    two line-graph layers above 60,000 angles regardless of memory
+    (interaction_block.py:15, :400-413)."""
+    total = total_bytes if total_bytes is not None else torch.cuda.get_device_properties(device).total_memory
+    per_block = n_angles * SAVED_BYTES_PER_ANGLE_BLOCK + n_edges * SAVED_BYTES_PER_EDGE_BLOCK
+    return n_blocks * per_block > 0.45 * total
 
 
 def _zeros_if_none(g, like):
@@ -50,57 +70,98 @@ def line_refinement_fusable(layer) -> bool:
             and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 
 
+def _attn_fwd(layer, bond, tb, lg, mode, save: bool):
+    """Forward of the line attention.  Returns (bond', tb', saved tuple or None)."""
+    tgt, src = lg["grp_tgt"], lg["grp_src"]
+    A, E = tb.shape[0], bond.shape[0]
+    r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+    pe = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+    pn = layer.node_nonlinear_update._pack.get(layer.node_nonlinear_update)
+    pp = layer._proj.get(layer.source_weight_linear.weight, layer.target_weight_linear.weight)
+    e, p_e, z_e, tb_new = ops.gmlp_fwd_raw(pe, [tb, bond, bond], [None, tgt.key, src.key], A, mode, res=(tb, r_e),
+                                           save=save)
+    a_s, a_t = ops.pair_fwd_raw(pp, tb, mode)
+    y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None)
+    if not save:
+        del a_s, a_t
+    _, p_n, z_n, bond_new = ops.gmlp_fwd_raw(pn, [bond, y_t, y_s], [None, None, None], E, mode, res=(bond, r_n),
+                                             save=save)
+    saved = (p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n) if save else None
+    return bond_new, tb_new, saved
+
+
 class _LineAttention(torch.autograd.Function):
     """Graph_Attention_Layer on the line graph (bonds = nodes, angles = edges):
         e     = GatedMLP_e([tb, bond[tgt], bond[src]])                 [A]
         y_t, y_s = attention(W_t tb, W_s tb, e; tgt, src)              [E]
         n     = GatedMLP_n([bond, y_t, y_s])                           [E]
         bond' = n + r_n * bond,  tb' = e + r_e * tb
-    """
+    With recompute, only (bond, tb) are kept and the forward runs again inside the
+    backward (the reference's activation checkpointing of this layer for large A,
+    interaction_block.py:15,400-413)."""
 
     @staticmethod
-    def forward(ctx, bond, tb, layer, lg):
+    def forward(ctx, bond, tb, layer, lg, recompute):
         ops._check_dev(bond, tb)
         bond, tb = ops._f32c(bond), ops._f32c(tb)
         mode = ops._MMA["mode"]
-        tgt, src = lg["grp_tgt"], lg["grp_src"]
-        A, E = tb.shape[0], bond.shape[0]
-        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
-        pe = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
-        pn = layer.node_nonlinear_update._pack.get(layer.node_nonlinear_update)
-        pp = layer._proj.get(layer.source_weight_linear.weight, layer.target_weight_linear.weight)
-        e, p_e, z_e, tb_new = ops.gmlp_fwd_raw(pe, [tb, bond, bond], [None, tgt.key, src.key], A, mode, res=(tb, r_e))
-        a_s, a_t = ops.pair_fwd_raw(pp, tb, mode)
-        y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None)
-        _, p_n, z_n, bond_new = ops.gmlp_fwd_raw(pn, [bond, y_t, y_s], [None, None, None], E, mode,
-                                                 res=(bond, r_n))
-        ctx.save_for_backward(p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n)
-        ctx.mode, ctx.tgt, ctx.src = mode, tgt, src
-        ctx.packs, ctx.res = (pe, pn, pp), (r_n, r_e)
+        bond_new, tb_new, saved = _attn_fwd(layer, bond, tb, lg, mode, save=not recompute)
+        ctx.save_for_backward(bond, tb) if recompute else ctx.save_for_backward(*saved)
+        ctx.mode, ctx.layer, ctx.lg, ctx.recompute = mode, layer, lg, recompute
         return bond_new, tb_new
 
     @staticmethod
     def backward(ctx, g_bond_new, g_tb_new):
-        p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n = ctx.saved_tensors
-        pe, pn, pp = ctx.packs
-        r_n, r_e = ctx.res
-        mode, tgt, src = ctx.mode, ctx.tgt, ctx.src
-        E, A = p_n.shape[0], p_e.shape[0]
+        layer, lg, mode = ctx.layer, ctx.lg, ctx.mode
+        if ctx.recompute:
+            bond, tb = ctx.saved_tensors
+            _, _, saved = _attn_fwd(layer, bond, tb, lg, mode, save=True)
+        else:
+            saved = ctx.saved_tensors
+        p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n = saved
+        pe = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+        pn = layer.node_nonlinear_update._pack.get(layer.node_nonlinear_update)
+        pp = layer._proj.get(layer.source_weight_linear.weight, layer.target_weight_linear.weight)
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        tgt, src = lg["grp_tgt"], lg["grp_src"]
+        E = p_n.shape[0]
         g_bond_new = _zeros_if_none(g_bond_new, y_t)
         g_tb_new = _zeros_if_none(g_tb_new, e)
         # node update: g_bond = r_n g + dGatedMLP_n/dbond, g_y = [g_yt | g_ys]
         g_bond = torch.empty(E, D, device=e.device)
         g_y = ops.gmlp_bwd_raw(pn, g_bond_new, p_n, z_n, 3 * D, mode, g_x0=g_bond, acc0=False, res_w=r_n)
+        del p_n, z_n
         # attention: g_e = g_tb_new (residual branch) + attention term
         g_at, g_as, g_e = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, None,
                                            ldgy=2 * D, g_e_base=g_tb_new)
+        del a_t, a_s, e, saved
         # projections + residual: g_tb = g_as W_s + g_at W_t + r_e g_tb_new
         g_tb = ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_tb_new, res_w=r_e)
+        del g_as, g_at
         # edge update: source 0 (tb) accumulates into g_tb, bond gathers scatter into g_bond
         g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=True)
+        del g_e, p_e, z_e
         ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True)
         ops.seg_sum_raw(g_x, src, ldx=2 * D, col_off=D, out=g_bond, accumulate=True)
-        return g_bond, g_tb, None, None
+        return g_bond, g_tb, None, None, None
+
+
+def _refine_fwd(layer, tb, atom, bond, env, lg, mode, save: bool):
+    """Forward of the line refinement.  Returns (bond', tb', saved tuple or None)."""
+    tgt, src, grp_atom = lg["grp_tgt"], lg["grp_src"], lg["grp_atom"]
+    A = tb.shape[0]
+    r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+    ph = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+    L, M = layer.node_FFN.layers, layer.edge_FFN.layers
+    pn = layer._node_ffn.get(L[0].weight, L[3].weight)
+    pm = layer._edge_ffn.get(M[0].weight, M[3].weight)
+    h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [tb, atom, bond, bond], [None, grp_atom.key, tgt.key, src.key], A, mode,
+                                      save=save)
+    agg, S = ops.env_agg_fwd_raw(h, env, tgt, src)
+    bond_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(bond, r_n), save=save)
+    tb_new, p_de = ops.ffn_fwd_raw(pm, h, mode, res=(tb, r_e), save=save)
+    saved = (h, p_h, z_h, S, p_dn, p_de) if save else None
+    return bond_new, tb_new, saved
 
 
 class _LineRefinement(torch.autograd.Function):
@@ -108,35 +169,38 @@ class _LineRefinement(torch.autograd.Function):
         h     = GatedMLP([tb, atom[atom_list], bond[tgt], bond[src]])   [A]
         agg   = sum_tgt h * env[src] * env[tgt]                           [E]
         bond' = node_FFN(agg) + r_n * bond,  tb' = edge_FFN(h) + r_e * tb
-    """
+    With recompute, only the inputs are kept and the forward reruns in the backward."""
 
     @staticmethod
-    def forward(ctx, tb, atom, bond, env, layer, lg):
+    def forward(ctx, tb, atom, bond, env, layer, lg, recompute):
         ops._check_dev(tb, atom, bond, env)
         tb, atom, bond, env = (ops._f32c(t) for t in (tb, atom, bond, env))
         mode = ops._MMA["mode"]
-        tgt, src, grp_atom = lg["grp_tgt"], lg["grp_src"], lg["grp_atom"]
-        A = tb.shape[0]
-        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
-        ph = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
-        L, M = layer.node_FFN.layers, layer.edge_FFN.layers
-        pn = layer._node_ffn.get(L[0].weight, L[3].weight)
-        pm = layer._edge_ffn.get(M[0].weight, M[3].weight)
-        h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [tb, atom, bond, bond], [None, grp_atom.key, tgt.key, src.key], A, mode)
-        agg, S = ops.env_agg_fwd_raw(h, env, tgt, src)
-        bond_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(bond, r_n))
-        tb_new, p_de = ops.ffn_fwd_raw(pm, h, mode, res=(tb, r_e))
-        ctx.save_for_backward(h, p_h, z_h, env, S, p_dn, p_de)
-        ctx.mode, ctx.tgt, ctx.src, ctx.grp_atom = mode, tgt, src, grp_atom
-        ctx.packs, ctx.res, ctx.n_atom = (ph, pn, pm), (r_n, r_e), atom.shape[0]
+        bond_new, tb_new, saved = _refine_fwd(layer, tb, atom, bond, env, lg, mode, save=not recompute)
+        if recompute:
+            ctx.save_for_backward(tb, atom, bond, env)
+        else:
+            ctx.save_for_backward(env, *saved)
+        ctx.mode, ctx.layer, ctx.lg, ctx.recompute, ctx.n_atom = mode, layer, lg, recompute, atom.shape[0]
         return bond_new, tb_new
 
     @staticmethod
     def backward(ctx, g_bond_new, g_tb_new):
-        h, p_h, z_h, env, S, p_dn, p_de = ctx.saved_tensors
-        ph, pn, pm = ctx.packs
-        r_n, r_e = ctx.res
-        mode, tgt, src = ctx.mode, ctx.tgt, ctx.src
+        layer, lg, mode = ctx.layer, ctx.lg, ctx.mode
+        if ctx.recompute:
+            tb, atom, bond, env = ctx.saved_tensors
+            _, _, saved = _refine_fwd(layer, tb, atom, bond, env, lg, mode, save=True)
+            del tb, atom, bond
+        else:
+            env, *saved = ctx.saved_tensors
+        h, p_h, z_h, S, p_dn, p_de = saved
+        del saved
+        ph = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+        L, M = layer.node_FFN.layers, layer.edge_FFN.layers
+        pn = layer._node_ffn.get(L[0].weight, L[3].weight)
+        pm = layer._edge_ffn.get(M[0].weight, M[3].weight)
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        tgt, src = lg["grp_tgt"], lg["grp_src"]
         E, A = env.shape[0], h.shape[0]
         g_bond_new = _zeros_if_none(g_bond_new, env)
         g_tb_new = _zeros_if_none(g_tb_new, h)
@@ -144,19 +208,22 @@ class _LineRefinement(torch.autograd.Function):
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
         g_tb = torch.empty(A, D, device=h.device)
         g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, g_res=g_tb, res_w=r_e)
+        del p_de
         g_env = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h, accumulate=True)
+        del h
         g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=True)
-        g_atom = ops.seg_sum_raw(g_x, ctx.grp_atom, ldx=3 * D, col_off=0)
+        del g_h, p_h, z_h
+        g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True)
         ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_bond, accumulate=True)
-        return g_tb, g_atom, g_bond, g_env, None, None
+        return g_tb, g_atom, g_bond, g_env, None, None, None
 
 
-def line_attention(layer, bond, tb, lg):
+def line_attention(layer, bond, tb, lg, recompute: bool = False):
     """(bond', tb') of Graph_Attention_Layer.forward on the line graph."""
-    return _LineAttention.apply(bond, tb, layer, lg)
+    return _LineAttention.apply(bond, tb, layer, lg, recompute)
 
 
-def line_refinement(layer, tb, atom, bond, env, lg):
+def line_refinement(layer, tb, atom, bond, env, lg, recompute: bool = False):
     """(bond', tb') of Refinement.forward on the line graph; env = learnable_envelope(smooth_weight)."""
-    return _LineRefinement.apply(tb, atom, bond, env, layer, lg)
+    return _LineRefinement.apply(tb, atom, bond, env, layer, lg, recompute)

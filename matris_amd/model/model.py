@@ -27,6 +27,7 @@ from collections.abc import Sequence
 
 import torch
 import torch.nn.functional as F
+import torch.utils.checkpoint
 from torch import Tensor, nn
 
 from ..config import EV_A3_TO_GPA
@@ -365,10 +366,10 @@ class Graph_Attention_Layer(nn.Module):
             return ops.proj_pair(self._proj.get(lin_s.weight, lin_t.weight), edge_feat)
         return lin_s(edge_feat), lin_t(edge_feat)
 
-    def forward(self, node_feat, edge_feat, graph, d2u: ops.Grouping | None = None):
+    def forward(self, node_feat, edge_feat, graph, d2u: ops.Grouping | None = None, recompute: bool = False):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
         if d2u is None and fused.line_attention_fusable(self):  # one node, explicit backward
-            return fused.line_attention(self, node_feat, edge_feat, graph)
+            return fused.line_attention(self, node_feat, edge_feat, graph, recompute)
         if d2u is None:  # line graph: edges are the angles themselves
             e = self.edge_nonlinear_update.fused([(edge_feat, None), (node_feat, tgt), (node_feat, src)])
             a_s, a_t = self._projections(edge_feat)
@@ -414,14 +415,15 @@ class Refinement(nn.Module):
             return ops.ffn(pack.get(L[0].weight, L[3].weight), x)
         return mlp(x)
 
-    def forward(self, node_feat, edge_feat, smooth_weight, graph, d2u: ops.Grouping | None = None, atom_feat=None):
+    def forward(self, node_feat, edge_feat, smooth_weight, graph, d2u: ops.Grouping | None = None, atom_feat=None,
+                recompute: bool = False):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
         if self.graph_type == "atom graph":
             w = ops.gather(self.learnable_envelope(smooth_weight), d2u)
             h = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
         elif fused.line_refinement_fusable(self):  # one node, explicit backward
             env = self.learnable_envelope(smooth_weight)
-            return fused.line_refinement(self, edge_feat, atom_feat, node_feat, env, graph)
+            return fused.line_refinement(self, edge_feat, atom_feat, node_feat, env, graph, recompute)
         else:
             env = self.learnable_envelope(smooth_weight)
             w = ops.gather(env, src) * ops.gather(env, tgt)
@@ -438,9 +440,11 @@ class Refinement(nn.Module):
 
 
 class Interaction_Block(nn.Module):
-    """interaction_block.py:281-446.  The reference's activation checkpointing
-    (A > 60000, :400-413) trades memory for recompute; here the fused kernels never
-    materialise the [A, 384/512] concatenations, so it is not needed."""
+    """interaction_block.py:281-446.  The reference checkpoints the two line-graph layers
+    when A > 60000 (:400-413); here the fused line layers recompute their forward inside
+    their own backward when batch_graph["line_recompute"] is set (MatRIS.forward sets it
+    from the activation footprint, or from MatRIS.line_recompute), and the [A, 384/512]
+    concatenations are never materialised either way."""
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, three_body_feat_dim=128, num_radial=7, num_angular=7,
                  dropout=0.0, use_bias=False, use_smoothed_for_delta_edge=False, mlp_type="GateMLP",
@@ -463,12 +467,13 @@ class Interaction_Block(nn.Module):
         attn_edge, attn_tb = edge_feat, threebody_feat
         upd_edge, upd_tb = edge_feat, threebody_feat
         lg, ag, d2u = batch_graph["line_graph_dict"], batch_graph["atom_graph_dict"], batch_graph["grp_d2u"]
+        rc = batch_graph.get("line_recompute", False)
         if threebody_feat is not None:
-            attn_edge, attn_tb = self.attn_block_line_graph(edge_feat, threebody_feat, lg)
+            attn_edge, attn_tb = self.attn_block_line_graph(edge_feat, threebody_feat, lg, recompute=rc)
         attn_node, attn_edge = self.attn_block_atom_graph(node_feat, attn_edge, ag, d2u)
         if threebody_feat is not None:
             upd_edge, upd_tb = self.refine_block_line_graph(attn_edge, attn_tb, smooth_weight["line graph"], lg,
-                                                            atom_feat=attn_node)
+                                                            atom_feat=attn_node, recompute=rc)
         upd_node, upd_edge = self.refine_block_atom_graph(attn_node, upd_edge, smooth_weight["atom graph"], ag,
                                                           d2u=d2u)
         return upd_node, upd_edge, upd_tb
@@ -550,6 +555,12 @@ class MatRIS(nn.Module):
         super().__init__()
         self.config = {k: v for k, v in locals().items() if k not in ("self", "__class__", "verbose")}
         self.is_intensive = is_intensive
+        # Memory modes for large cells.  block_checkpoint: None = decided per call from the
+        # activation footprint (fused.checkpoint_needed), True / False = forced; each block
+        # then keeps only its inputs and reruns its forward in the backward.
+        # line_recompute: the two line-graph layers alone keep only their inputs.
+        self.block_checkpoint: bool | None = None
+        self.line_recompute: bool = False
         if reference_energy is not None:
             raise NotImplementedError("AtomRef reference energies are not on the MI355X path yet")
         self.reference_energy = None
@@ -576,13 +587,22 @@ class MatRIS(nn.Module):
             raise NotImplementedError("training (double backward) is outside the efsm inference path")
         pred = {}
         bg = process_graphs(graphs, compute_stress="s" in task)
+        bg["line_recompute"] = bool(self.line_recompute)
+        ckpt = self.block_checkpoint
+        if ckpt is None:
+            ckpt = fused.checkpoint_needed(bg["n_angles"], bg["n_directed"], len(self.interaction_block),
+                                           bg["atomic_numbers"].device)
         node = self.atom_embedding(bg["atomic_numbers"].long() - 1)
         edge, smooth = self.edge_embedding(graphs=bg)
         tb = None
         if bg["n_angles"] != 0:
             tb = self.three_body_embedding(graphs=bg)
         for layer in self.interaction_block:
-            node, edge, tb = layer(bg, node, edge, tb, smooth)
+            if ckpt:  # keep only the block inputs; the block's forward reruns in the backward
+                node, edge, tb = torch.utils.checkpoint.checkpoint(layer, bg, node, edge, tb, smooth,
+                                                                   use_reentrant=False)
+            else:
+                node, edge, tb = layer(bg, node, edge, tb, smooth)
         node = self.readout_norm(node)
         total = self.energy_head(bg, node)
         pred.update(self.force_stress_head(bg, compute_force="f" in task, compute_stress="s" in task,

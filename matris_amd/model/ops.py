@@ -430,11 +430,13 @@ class _WeightPack(_PackCache):
         return self
 
 
-def ffn_fwd_raw(pack: _WeightPack, x, mode: int, res=None):
-    """(out, p) of matris_ffn_fwd; res = (res_src, res_w) adds res_w * res_src to out."""
+def ffn_fwd_raw(pack: _WeightPack, x, mode: int, res=None, save: bool = True):
+    """(out, p) of matris_ffn_fwd; res = (res_src, res_w) adds res_w * res_src to out;
+    p (the saved pre-activation) is None when not saved."""
     lib = _lib.load()
     M = x.shape[0]
-    out, p = torch.empty(M, D, device=x.device), torch.empty(M, D, device=x.device)
+    out = torch.empty(M, D, device=x.device)
+    p = torch.empty(M, D, device=x.device) if save else None
     rs, rw = (res if res is not None else (None, None))
     with _timed("ffn_fwd", (M,)):
         _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.b("w0", mode)), _p(pack.b("w1", mode)), _p(out), _p(p),

@@ -69,8 +69,9 @@ def _randomize(mod, seed):
                 p.uniform_(0.5, 1.5)
 
 
+@pytest.mark.parametrize("recompute", [False, True])
 @pytest.mark.parametrize("A,E", [(3000, 400), (257, 64), (1, 1)])
-def test_line_attention_vs_fp64(A, E):
+def test_line_attention_vs_fp64(A, E, recompute):
     from matris_amd.model import fused
     from matris_amd.model.model import Graph_Attention_Layer
     torch.manual_seed(A)
@@ -93,15 +94,16 @@ def test_line_attention_vs_fp64(A, E):
     layer = layer.to(DEV)
     assert fused.line_attention_fusable(layer)
     bd, td = bond.to(DEV).requires_grad_(True), tb.to(DEV).requires_grad_(True)
-    bn, tn = fused.line_attention(layer, bd, td, lg)
+    bn, tn = fused.line_attention(layer, bd, td, lg, recompute)
     assert _rel(bn, bn_r) < 1e-5 and _rel(tn, tn_r) < 1e-5
     torch.autograd.backward([bn, tn], [g_b.to(DEV), g_t.to(DEV)])
     assert _rel(bd.grad, b64.grad) < 1e-5
     assert _rel(td.grad, t64.grad) < 1e-5
 
 
+@pytest.mark.parametrize("recompute", [False, True])
 @pytest.mark.parametrize("A,E,N", [(3000, 400, 60), (300, 64, 7)])
-def test_line_refinement_vs_fp64(A, E, N):
+def test_line_refinement_vs_fp64(A, E, N, recompute):
     from matris_amd.model import fused
     from matris_amd.model.model import Refinement
     torch.manual_seed(A + N)
@@ -122,7 +124,7 @@ def test_line_refinement_vs_fp64(A, E, N):
     layer = layer.to(DEV)
     assert fused.line_refinement_fusable(layer)
     dev_leaves = [x.to(DEV).requires_grad_(True) for x in (tb, atom, bond, env)]
-    bn, tn = fused.line_refinement(layer, *dev_leaves, lg)
+    bn, tn = fused.line_refinement(layer, *dev_leaves, lg, recompute)
     assert _rel(bn, bn_r) < 1e-5 and _rel(tn, tn_r) < 1e-5
     torch.autograd.backward([bn, tn], [g_b.to(DEV), g_t.to(DEV)])
     for d, r in zip(dev_leaves, leaves):

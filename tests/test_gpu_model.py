@@ -110,6 +110,26 @@ def test_c3_gpu_graph_and_efsm_vs_reference_golden(golden):
     _assert_close(_efsm(model, [g]), z, "C3", _fp64(golden, "c3"))
 
 
+def test_c3_line_recompute_vs_reference_golden(golden):
+    """C3 with the line layers recomputed in the backward (the large-A memory mode)."""
+    from matris_amd import workloads as W
+    z = golden("c3_cu864.npz")
+    model = _model()
+    model.line_recompute = True
+    g = model.graph_converter(W.c3_cu864())
+    _assert_close(_efsm(model, [g]), z, "C3 recompute", _fp64(golden, "c3"))
+
+
+def test_c3_block_checkpoint_vs_reference_golden(golden):
+    """C3 with every interaction block checkpointed (the large-cell memory mode)."""
+    from matris_amd import workloads as W
+    z = golden("c3_cu864.npz")
+    model = _model()
+    model.block_checkpoint = True
+    g = model.graph_converter(W.c3_cu864())
+    _assert_close(_efsm(model, [g]), z, "C3 checkpoint", _fp64(golden, "c3"))
+
+
 def test_fp32_mma_mode_vs_reference_golden(golden):
     """The fp32-MFMA GatedMLP mode (MATRIS_MMA_FP32) on the batched triclinic cells."""
     from matris_amd.model import ops
