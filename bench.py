@@ -1,13 +1,22 @@
 """MatRIS efsm throughput on one MI355X (atom.steps/s), with live kernel roofline numbers
 and the CPU oracle timed on the host as a baseline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C3]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--c5-steps K5] [--no-c5] [--no-c2]
 
-A step is one full efsm evaluation of MatRIS-10M (num_layers=10, random init, seed 0)
-on the workload's graph: process_graphs, forward, torch.autograd.grad for forces and
-stress, magmom head -- MatRIS.forward(graphs, task="efsm").  Inputs (the graph, built
-on the GPU once for the fixed C3 positions) are resident in HBM before the timed
-region.  Prints one JSON line.
+`value`: a step is one full efsm evaluation of MatRIS-10M (num_layers=10, random init,
+seed 0) on the C3 graph (864-atom fcc Cu): process_graphs, forward, torch.autograd.grad
+for forces and stress, magmom head -- MatRIS.forward(graphs, task="efsm").  The graph
+(built on the GPU once for the fixed C3 positions) is resident in HBM before the timed
+region.
+
+`c5_md`: the 32,000-atom a-SiO2 cell (C5) under NVT Berendsen MD (300 K, dt 1 fs,
+tau 100 fs); every step rebuilds the radius and line graphs on the GPU from the new
+positions and evaluates efs (forces for the integrator); interaction blocks are
+checkpointed (the cell's activations exceed HBM otherwise).  A bounded number of steps.
+
+`c2_line_attn`: the standalone line-attention core (forward, backward) and the
+angle->bond segment sum on the C2 graph (4096-atom random packing) with N(0,1) features,
+against HBM peak.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -22,6 +31,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+# The gated-MLP kernels compute fp32 products as 6 bf16 MFMA products (mma.h, MODE 6), so
+# their ceiling in fp32-product terms is the dense bf16 peak / 6.
+SPLIT6_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 6
 D = 128
 
 
@@ -31,6 +44,10 @@ def _parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="C3", choices=["C3"])
+    ap.add_argument("--c5-steps", type=int, default=5, help="timed C5 MD steps (after --c5-warmup)")
+    ap.add_argument("--c5-warmup", type=int, default=2)
+    ap.add_argument("--no-c5", action="store_true")
+    ap.add_argument("--no-c2", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-reps", type=int, default=3, help="fcc reps of the CPU baseline sample")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -55,8 +72,103 @@ def _attn_line_bytes(A, U, with_perm=True):
 
 
 def _gmlp_flops(M, K):
-    """One fused GatedMLP forward: [M,K]x[K,256] plus two [M,128]x[128,128]."""
+    """One fused GatedMLP forward (or backward, input gradients only):
+    [M,K]x[K,256] plus two [M,128]x[128,128]."""
     return 2.0 * M * (K * 256 + 2 * 128 * 128)
+
+
+def _events_time(fn, reps):
+    """Mean seconds per call of fn, HIP events on torch's current stream (where every
+    matris_hip launch goes)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps / 1e3
+
+
+def c2_line_attn(dev, reps: int = 20):
+    """Config C2 microbench: the line-attention core and the angle->bond segment sum on
+    the 4096-atom random packing's line graph, features N(0,1) (seed 1, order
+    alpha_s, alpha_t, e').  Algorithmic bytes count every input element read once and
+    every output written once (int32 indices included); the gathered per-segment
+    statistics of the backward are extra traffic, reported apart."""
+    import torch
+
+    from matris_amd import workloads as W
+    from matris_amd.graph.converter import GraphConverter
+    from matris_amd.model import ops
+
+    cr = W.c2_rsa4096()
+    g = GraphConverter(device=dev).from_arrays(cr.frac, cr.lattice, cr.z)
+    lg = g.line_graph
+    A, U = int(lg.shape[0]), int(g.undirected2directed.shape[0])
+    tgt = ops.Grouping.build(lg[:, 1].contiguous(), U, sorted_rows=True)
+    src = ops.Grouping.build(lg[:, 3].contiguous(), U)
+    gen = torch.Generator().manual_seed(1)
+    a_s, a_t, e = (torch.randn(A, D, generator=gen).to(dev) for _ in range(3))
+    g_yt, g_ys = (torch.randn(U, D, generator=gen).to(dev) for _ in range(2))
+    y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None)
+    t_f = _events_time(lambda: ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None), reps)
+    t_b = _events_time(lambda: ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt, src, None),
+                       reps)
+    out = torch.empty(U, D, device=dev)
+    t_s = _events_time(lambda: ops.seg_sum_raw(e, tgt, out=out), reps)
+    b_f = 4 * D * (3 * A + 2 * U) + 4 * A + 8 * (U + 1)
+    b_b = 4 * D * (6 * A + 2 * U) + 4 * A + 8 * (U + 1)
+    b_s = 4 * D * (A + U) + 4 * A + 4 * (U + 1)
+
+    def row(name, byts, t):
+        gbs = byts / t / 1e9
+        return dict(kernel=name, bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(gbs / HBM_PEAK_GBS, 4), bytes_per_launch=byts, mean_us=round(t * 1e6, 2))
+
+    return dict(workload="C2: 4096-atom random packing (rho 0.085, d_min 1.8, seed 1)", n_angles=A,
+                n_undirected=U,
+                fwd=row("attn_fwd_kernel<false>", b_f, t_f),
+                bwd=row("attn_bwd_kernel<false>", b_b, t_b) | dict(
+                    extra_stat_bytes=4 * D * 4 * U, extra_stat_note="y_t, y_s, lse_t, lse_s gathered per row"),
+                seg_sum=row("seg_sum_kernel", b_s, t_s))
+
+
+def c5_md(model, dev, steps: int, warmup: int):
+    """Config C5: NVT Berendsen MD of the 32,000-atom a-SiO2 cell, graph rebuilt on the
+    GPU every step.  Returns atom.steps/s over `steps` steps after `warmup` steps."""
+    import torch
+
+    from matris_amd import workloads as W
+    from matris_amd.applications.md import MolecularDynamics
+
+    cr = W.c5_sio2_32k()
+    torch.cuda.reset_peak_memory_stats(dev)
+    md = MolecularDynamics((cr.frac, cr.lattice, cr.z), model=model, ensemble="nvt", thermostat="Berendsen",
+                           temperature=300, starting_temperature=300, timestep=1.0, taut=100.0, task="efs",
+                           device=str(dev), seed=4)
+    md.run(warmup)
+    torch.cuda.synchronize()
+    md.timings = {"graph": 0.0, "model": 0.0}
+    t0 = time.perf_counter()
+    md.run(steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    res = md.results
+    return dict(
+        metric="atom*steps/s (NVT MD step: GPU graph rebuild + efs fwd + autograd bwd + integrator)",
+        value=round(len(cr) * steps / dt, 2), unit="atom*steps/s", steps=steps, warmup=warmup,
+        ms_per_step=round(dt / steps * 1e3, 1),
+        graph_ms_per_step=round(md.timings["graph"] / steps * 1e3, 2),
+        model_ms_per_step=round(md.timings["model"] / steps * 1e3, 1),
+        peak_mem_gib=round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 1),
+        temperature_K=round(md.kinetic_temperature(), 2),
+        e_per_atom=float(res["e"][0].detach()),
+        config={"workload": "C5: 32,000-atom a-SiO2 (2.2 g/cm3, d_min 1.5, seed 4), NVT Berendsen 300 K, "
+                            "dt 1 fs, tau 100 fs, MB velocities seed 4",
+                "n_atoms": len(cr), "block_checkpoint": "auto (on)"})
 
 
 def cpu_baseline(reps: int):
@@ -161,14 +273,24 @@ def main():
     torch.cuda.synchronize()
     e2e = n_atoms * e2e_steps / (time.perf_counter() - t1)
 
-    # rooflines: the dominant (MFMA-bound) kernel and the line attention (HBM-bound)
-    gm = stats.get("gmlp_fwd")
-    gm_line = [(m, k) for (m, k) in gm["info"] if m == A] if gm else []
-    flops = sum(_gmlp_flops(m, k) for m, k in gm["info"]) / gm["n"] if gm else 0.0
-    gm_tf = flops / gm["mean_s"] / 1e12 if gm else 0.0
-    roof = dict(kernel="gmlp_fwd_kernel", bound="mfma", achieved=round(gm_tf, 2), peak=FP32_MFMA_PEAK_TFLOPS,
-                unit="TFLOP/s", frac=round(gm_tf / FP32_MFMA_PEAK_TFLOPS, 4), traffic=None,
-                note=f"mean over {gm['n']} launches/{args.steps} steps ({len(gm_line)} with M=A={A})" if gm else "")
+    # rooflines: the dominant (MFMA-bound) kernel family and the line attention (HBM-bound)
+    def gmlp_roof(name):
+        gm = stats.get(name)
+        if not gm:
+            return None
+        flops = sum(_gmlp_flops(m, k) for m, k in gm["info"]) / gm["n"]
+        tf = flops / gm["mean_s"] / 1e12
+        n_line = sum(1 for (m, k) in gm["info"] if m == A)
+        return dict(kernel=f"{name}_kernel<6>", bound="mfma", achieved=round(tf, 2), peak=round(SPLIT6_PEAK_TFLOPS, 1),
+                    unit="TFLOP/s", frac=round(tf / SPLIT6_PEAK_TFLOPS, 4), traffic=None,
+                    flops_per_launch=round(flops), mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
+                    frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                    note=f"algorithmic fp32 FLOPs (2*M*(256K+32768)) per launch, mean over {gm['n']} launches in "
+                         f"{args.steps} steps ({n_line} with M=A={A}); peak = dense bf16 {BF16_MFMA_PEAK_TFLOPS:.0f} "
+                         f"TFLOP/s / 6 bf16 products per fp32 product")
+    r_f, r_b = gmlp_roof("gmlp_fwd"), gmlp_roof("gmlp_bwd")
+    tot = {k: v["mean_s"] * v["n"] for k, v in stats.items()}
+    roof = r_b if tot.get("gmlp_bwd", 0) >= tot.get("gmlp_fwd", 0) else r_f
     at = stats.get("attn_fwd_line")
     attn = None
     if at:
@@ -191,17 +313,22 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "fp32 (GEMMs: fp32 products as 3-way-split bf16 MFMA, fp32 accumulate)",
         "data": "synthetic (fcc Cu 6x6x6, sigma=0.05 A seed 2; random-init weights seed 0)",
         "config": {"workload": "C3: fcc Cu 6x6x6 conventional (864 atoms), efsm, MatRIS-10M (num_layers=10)",
                    "n_atoms": n_atoms, "n_directed": int(g.atom_graph.shape[0]), "n_undirected": E_u,
                    "n_angles": A, "graph": "built on GPU once (fixed positions)"},
         "e2e_with_gpu_graph_rebuild": round(e2e, 2),
         "roofline": roof,
+        "roofline_gmlp_fwd": r_f,
         "roofline_line_attn": attn,
         "kernels": kern,
         "e_per_atom": float(out["e"].item()),
     }
+    if not args.no_c2:
+        line["c2_line_attn"] = c2_line_attn(dev)
+    if not args.no_c5:
+        line["c5_md"] = c5_md(model, dev, args.c5_steps, args.c5_warmup)
     if not args.no_cpu_baseline:
         try:
             line["cpu_baseline"] = cpu_baseline(args.cpu_sample_reps)
