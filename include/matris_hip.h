@@ -103,8 +103,9 @@ int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, in
 /* out[s, :] = (accumulate ? out[s, :] : 0) + scale * sum_{i in [rowptr[s], rowptr[s+1])}
  *             x[(perm ? perm[i] : i) * ldx + col_off + :128]
  * Replaces aggregate() / GraphPooling (matris/model/functions.py:129-160, 340-365):
- * index_add_ with average=False (scale 1) or the d2u mean (scale 0.5), summed in
- * CSR order -- deterministic, no atomics. */
+ * index_add_ with average=False (scale 1) or the d2u mean (scale 0.5), summed in a
+ * fixed CSR order -- deterministic, no atomics.  ldx and col_off multiples of 4 (16-byte
+ * aligned rows). */
 int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *rowptr, const int32_t *perm,
                    int64_t n_seg, float scale, int accumulate, float *out, void *stream);
 
@@ -123,6 +124,7 @@ int matris_gather_rows(const float *src, const int32_t *idx, int64_t n_rows, flo
  *   both over n_seg segments.
  * fwd writes y_t, y_s [n_seg,128] and the per-segment log-sum-exp lse_t, lse_s
  * [n_seg,128] needed by the backward.
+ * lda (and ldgy) are multiples of 4 (16-byte aligned rows).
  * bwd (input gradients only): given g_yt, g_ys (rows of stride ldgy >= 128), writes
  * g_alpha_t, g_alpha_s [R,128] (per row r, before any alpha_idx reduction) and
  * g_e [R,128] (= g_e_base + the attention term when g_e_base is non-NULL; g_e_base may

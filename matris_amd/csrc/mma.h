@@ -51,19 +51,6 @@ __device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, v16f c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// e^-x = 2^t, t = -x log2(e), on v_exp_f32 (1 ulp).  The rounding error of the product
-// (recovered exactly by an FMA, plus the fp32 representation error of log2 e) is applied
-// as the first-order factor 1 + err ln 2, so the result is within ~2 ulp of e^-x
-// instead of degrading with |t| ulp.  Overflow gives +inf (the product form keeps
-// inf * 1 = inf), underflow 0.
-__device__ __forceinline__ float exp_neg_f(float x) {
-    constexpr float kL2e = 1.44269502162933349609375f;  // fp32(log2 e)
-    constexpr float kL2eLo = 1.9259629911266175e-08f;   // log2 e - kL2e
-    constexpr float kLn2 = 0.693147180559945309f;
-    const float t = -x * kL2e;
-    const float err = fmaf(-x, kL2eLo, fmaf(-x, kL2e, -t));
-    return __builtin_amdgcn_exp2f(t) * (1.0f + err * kLn2);
-}
 // sigmoid = 1 / (1 + e^-x) with v_rcp_f32 (1 ulp); SiLU = x sigmoid(x).
 __device__ __forceinline__ float sigm_f(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_neg_f(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x * sigm_f(x); }

@@ -1,62 +1,76 @@
 // Segmented reductions, gathers and the fused segment attention (softmax by target and
 // by source, alpha * e', both segment sums) for gfx950.
 //
-// All of these are HBM-bound.  Layout: one 64-lane wavefront per segment (or per row),
-// each lane owning two adjacent columns of a 128-wide fp32 row, so every row access is
-// one coalesced 512-byte transaction.  Reductions run in CSR order inside the wave:
-// deterministic, no float atomics.
+// All of these are HBM-bound.  Layout: one 64-lane wavefront per segment (or per pair of
+// rows); each half-wave owns a 128-wide fp32 row at a time with 16-byte lanes, so every
+// row access is one coalesced 512-byte transaction.  Reductions run in a fixed CSR
+// order inside the wave: deterministic, no float atomics.
 #include "common.h"
 
 #define WAVES_PER_BLOCK 4
 
 __device__ __forceinline__ float2 ld2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
 __device__ __forceinline__ void st2(float *p, float2 v) { *reinterpret_cast<float2 *>(p) = v; }
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+__device__ __forceinline__ float4 max4(const float4 &a, const float4 &b) {
+    return make_float4(fmaxf(a.x, b.x), fmaxf(a.y, b.y), fmaxf(a.z, b.z), fmaxf(a.w, b.w));
+}
+__device__ __forceinline__ float4 shfl_xor4(const float4 &v, int o) {
+    return make_float4(__shfl_xor(v.x, o, 64), __shfl_xor(v.y, o, 64), __shfl_xor(v.z, o, 64), __shfl_xor(v.w, o, 64));
+}
+
 
 // ------------------------------------------------------------------------------------
 // segment sum (CSR)
 // ------------------------------------------------------------------------------------
+// One wave per segment; each half-wave sums every other row with 16-byte lanes and the
+// halves combine at the end (fixed order: deterministic).
 __global__ __launch_bounds__(256) void seg_sum_kernel(const float *__restrict__ x, int64_t ldx, int64_t col_off,
                                                       const int32_t *__restrict__ rowptr,
                                                       const int32_t *__restrict__ perm, int64_t n_seg, float scale,
                                                       int accumulate, float *__restrict__ out) {
     int64_t s = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (s >= n_seg) return;
-    const int c = 2 * (threadIdx.x & 63);
+    const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
     const int b = rowptr[s], e = rowptr[s + 1];
     const float *xc = x + col_off + c;
-    float2 acc = make_float2(0.f, 0.f);
-    int i = b;
-    for (; i + 4 <= e; i += 4) {
-        int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + 1] : i + 1;
-        int64_t r2 = perm ? perm[i + 2] : i + 2, r3 = perm ? perm[i + 3] : i + 3;
-        float2 v0 = ld2(xc + r0 * ldx), v1 = ld2(xc + r1 * ldx);
-        float2 v2 = ld2(xc + r2 * ldx), v3 = ld2(xc + r3 * ldx);
-        acc.x += v0.x; acc.y += v0.y;
-        acc.x += v1.x; acc.y += v1.y;
-        acc.x += v2.x; acc.y += v2.y;
-        acc.x += v3.x; acc.y += v3.y;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = b + half;
+    for (; i + 6 < e; i += 8) {
+        const int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + 2] : i + 2;
+        const int64_t r2 = perm ? perm[i + 4] : i + 4, r3 = perm ? perm[i + 6] : i + 6;
+        const float4 v0 = ld4(xc + r0 * ldx), v1 = ld4(xc + r1 * ldx);
+        const float4 v2 = ld4(xc + r2 * ldx), v3 = ld4(xc + r3 * ldx);
+        acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;
+        acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;
+        acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;
+        acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;
     }
-    for (; i < e; ++i) {
-        int64_t r = perm ? perm[i] : i;
-        float2 v = ld2(xc + r * ldx);
-        acc.x += v.x; acc.y += v.y;
+    for (; i < e; i += 2) {
+        const int64_t r = perm ? perm[i] : i;
+        const float4 v = ld4(xc + r * ldx);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
     }
-    acc.x *= scale;
-    acc.y *= scale;
-    float *o = out + s * MATRIS_D + c;
+    // half 0 + half 1, the same order in both halves
+    const float4 o = shfl_xor4(acc, 32);
+    float4 t = half ? make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w)
+                    : make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
+    t.x *= scale; t.y *= scale; t.z *= scale; t.w *= scale;
+    if (half) return;
+    float *op = out + s * MATRIS_D + c;
     if (accumulate) {
-        float2 p = ld2(o);
-        acc.x += p.x;
-        acc.y += p.y;
+        const float4 p = ld4(op);
+        t.x += p.x; t.y += p.y; t.z += p.z; t.w += p.w;
     }
-    st2(o, acc);
+    st4(op, t);
 }
 
 extern "C" int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *rowptr,
                               const int32_t *perm, int64_t n_seg, float scale, int accumulate, float *out,
                               void *stream) {
     if (n_seg < 0 || !rowptr || !out || ldx < MATRIS_D || col_off < 0 || col_off + MATRIS_D > ldx ||
-        (ldx % 2) || (col_off % 2))
+        (ldx % 4) || (col_off % 4))
         return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
     seg_sum_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
@@ -97,19 +111,43 @@ extern "C" int matris_gather_rows(const float *src, const int32_t *idx, int64_t 
 }
 
 // ------------------------------------------------------------------------------------
-// segment attention forward: one wave per (segment, side); online softmax per column
+// segment attention forward: one wave per (segment, side).  Each half-wave owns every
+// other row of the segment with 16-byte lanes (4 columns) and runs an online softmax
+// taken four of its rows at a time: the running maximum moves once per chunk (one
+// rescale exponential), then one exponential per row, all on v_exp_f32 (exp_neg_f).
+// The two halves' (max, sum, weighted sum) states merge at the end.
 // ------------------------------------------------------------------------------------
-__device__ __forceinline__ void online_update(float2 a, float2 ev, float2 &m, float2 &s, float2 &acc) {
-    float mx = fmaxf(m.x, a.x), my = fmaxf(m.y, a.y);
-    float cx = expf(m.x - mx), cy = expf(m.y - my);  // 0 on the first row (m = -inf)
-    float wx = expf(a.x - mx), wy = expf(a.y - my);
-    s.x = s.x * cx + wx;
-    s.y = s.y * cy + wy;
-    acc.x = acc.x * cx + wx * ev.x;
-    acc.y = acc.y * cy + wy * ev.y;
-    m.x = mx;
-    m.y = my;
-}
+struct OnlineSoftmax4 {
+    float4 m, s, acc;
+    __device__ void init() {
+        m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        s = acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // raise the running maximum to mn, rescaling (s, acc) (nothing to rescale while m = -inf)
+    __device__ void raise(const float4 &mn) {
+#define OS_RAISE(k)                                                          \
+    {                                                                        \
+        const float c = m.k == -INFINITY ? 0.f : exp_neg_f(mn.k - m.k);     \
+        s.k *= c;                                                            \
+        acc.k *= c;                                                          \
+        m.k = mn.k;                                                          \
+    }
+        OS_RAISE(x) OS_RAISE(y) OS_RAISE(z) OS_RAISE(w)
+#undef OS_RAISE
+    }
+    // fold a row whose logits do not exceed m
+    __device__ void add(const float4 &x, const float4 &ev) {
+#define OS_ADD(k)                                    \
+    {                                                \
+        const float w = exp_neg_f(m.k - x.k);        \
+        s.k += w;                                    \
+        acc.k += w * ev.k;                           \
+    }
+        OS_ADD(x) OS_ADD(y) OS_ADD(z) OS_ADD(w)
+#undef OS_ADD
+    }
+};
+
 
 // HAS_AIDX distinguishes the atom-graph launch (alpha rows read through d2u) from the
 // line-graph launch, and gives them separate kernel symbols in profiles.
@@ -129,38 +167,60 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(int64_t n_seg, const floa
     const int64_t seg = src_side ? w - n_seg : w;
     const int32_t *ptr = src_side ? s_ptr : t_ptr;
     const int32_t *perm = src_side ? s_perm : t_perm;
-    const float *alpha = src_side ? alpha_s : alpha_t;
-    const int c = 2 * (threadIdx.x & 63);
+    const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
+    const float *alpha = (src_side ? alpha_s : alpha_t) + c;
+    const float *ec = e + c;
     const int b = ptr[seg], end = ptr[seg + 1];
-    float2 m = make_float2(-INFINITY, -INFINITY), s = make_float2(0.f, 0.f), acc = make_float2(0.f, 0.f);
-    int i = b;
-    for (; i + 2 <= end; i += 2) {
-        int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + 1] : i + 1;
-        int64_t a0 = HAS_AIDX ? aidx[r0] : r0, a1 = HAS_AIDX ? aidx[r1] : r1;
-        float2 x0 = ld2(alpha + a0 * lda + c), x1 = ld2(alpha + a1 * lda + c);
-        float2 e0 = ld2(e + r0 * MATRIS_D + c), e1 = ld2(e + r1 * MATRIS_D + c);
-        online_update(x0, e0, m, s, acc);
-        online_update(x1, e1, m, s, acc);
+    auto row = [&](int i) -> int64_t { return perm ? perm[i] : i; };
+    auto arow = [&](int64_t r) -> int64_t { return HAS_AIDX ? (int64_t)aidx[r] : r; };
+    OnlineSoftmax4 st;
+    st.init();
+    int i = b + half;  // this half's rows: i, i + 2, i + 4, ...
+    for (; i + 6 < end; i += 8) {
+        const int64_t r0 = row(i), r1 = row(i + 2), r2 = row(i + 4), r3 = row(i + 6);
+        const float4 x0 = ld4(alpha + arow(r0) * lda), x1 = ld4(alpha + arow(r1) * lda);
+        const float4 x2 = ld4(alpha + arow(r2) * lda), x3 = ld4(alpha + arow(r3) * lda);
+        const float4 e0 = ld4(ec + r0 * MATRIS_D), e1 = ld4(ec + r1 * MATRIS_D);
+        const float4 e2 = ld4(ec + r2 * MATRIS_D), e3 = ld4(ec + r3 * MATRIS_D);
+        st.raise(max4(st.m, max4(max4(x0, x1), max4(x2, x3))));
+        st.add(x0, e0);
+        st.add(x1, e1);
+        st.add(x2, e2);
+        st.add(x3, e3);
     }
-    if (i < end) {
-        int64_t r0 = perm ? perm[i] : i;
-        int64_t a0 = HAS_AIDX ? aidx[r0] : r0;
-        online_update(ld2(alpha + a0 * lda + c), ld2(e + r0 * MATRIS_D + c), m, s, acc);
+    for (; i < end; i += 2) {
+        const int64_t r0 = row(i);
+        const float4 x0 = ld4(alpha + arow(r0) * lda), e0 = ld4(ec + r0 * MATRIS_D);
+        st.raise(max4(st.m, x0));
+        st.add(x0, e0);
     }
-    float2 y = make_float2(0.f, 0.f), l = make_float2(0.f, 0.f);
+    // merge the other half's state (lane ^ 32 holds the same columns)
+    const float4 om = shfl_xor4(st.m, 32), os = shfl_xor4(st.s, 32), oa = shfl_xor4(st.acc, 32);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f), l = make_float4(0.f, 0.f, 0.f, 0.f);
     if (end > b) {
-        y = make_float2(acc.x / s.x, acc.y / s.y);
-        l = make_float2(m.x + logf(s.x), m.y + logf(s.y));
+#define OS_MERGE(k)                                                                       \
+    {                                                                                     \
+        const float mm = fmaxf(st.m.k, om.k);                                             \
+        const float c0 = st.m.k == -INFINITY ? 0.f : exp_neg_f(mm - st.m.k);              \
+        const float c1 = om.k == -INFINITY ? 0.f : exp_neg_f(mm - om.k);                  \
+        const float ss = st.s.k * c0 + os.k * c1;                                         \
+        y.k = (st.acc.k * c0 + oa.k * c1) / ss;                                           \
+        l.k = mm + logf(ss);                                                              \
     }
-    st2((src_side ? y_s : y_t) + seg * MATRIS_D + c, y);
-    st2((src_side ? lse_s : lse_t) + seg * MATRIS_D + c, l);
+        OS_MERGE(x) OS_MERGE(y) OS_MERGE(z) OS_MERGE(w)
+#undef OS_MERGE
+    }
+    if (half == 0) {
+        st4((src_side ? y_s : y_t) + seg * MATRIS_D + c, y);
+        st4((src_side ? lse_s : lse_t) + seg * MATRIS_D + c, l);
+    }
 }
 
 extern "C" int matris_attn_fwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s,
                                int64_t lda, const int32_t *alpha_idx, const float *e, const int32_t *t_ptr,
                                const int32_t *t_perm, const int32_t *s_ptr, const int32_t *s_perm, float *y_t,
                                float *y_s, float *lse_t, float *lse_s, void *stream) {
-    if (n_rows < 0 || n_seg < 0 || lda < MATRIS_D || (lda % 2) || !t_ptr || !s_ptr || !y_t || !y_s || !lse_t ||
+    if (n_rows < 0 || n_seg < 0 || lda < MATRIS_D || (lda % 4) || !t_ptr || !s_ptr || !y_t || !y_s || !lse_t ||
         !lse_s)
         return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
@@ -175,8 +235,8 @@ extern "C" int matris_attn_fwd(int64_t n_rows, int64_t n_seg, const float *alpha
 }
 
 // ------------------------------------------------------------------------------------
-// segment attention backward: one wave per row
-//   p = exp(alpha - lse[seg]);  g_e = p_t g_yt + p_s g_ys;
+// segment attention backward: two rows per wave (half-wave per row, 16-byte lanes)
+//   p = exp(alpha - lse[seg]) (exp_neg_f);  g_e = p_t g_yt + p_s g_ys;
 //   g_alpha = p g_y (e - y)      (column-wise softmax Jacobian)
 // ------------------------------------------------------------------------------------
 template <bool HAS_AIDX>
@@ -187,27 +247,30 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(
     const float *__restrict__ lse_t, const float *__restrict__ lse_s, const float *__restrict__ g_yt,
     const float *__restrict__ g_ys, int64_t ldgy, float *__restrict__ g_alpha_t, float *__restrict__ g_alpha_s,
     float *__restrict__ g_e, const float *__restrict__ g_e_base) {
-    int64_t r = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    const int64_t r = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1);
     if (r >= n_rows) return;
-    const int c = 2 * (threadIdx.x & 63);
+    const int c = 4 * (threadIdx.x & 31);
     const int64_t a = HAS_AIDX ? aidx[r] : r;
     const int64_t t = t_idx[r], s = s_idx[r];
-    float2 at = ld2(alpha_t + a * lda + c), as = ld2(alpha_s + a * lda + c);
-    float2 ev = ld2(e + r * MATRIS_D + c);
-    float2 lt = ld2(lse_t + t * MATRIS_D + c), ls = ld2(lse_s + s * MATRIS_D + c);
-    float2 gt = ld2(g_yt + t * ldgy + c), gs = ld2(g_ys + s * ldgy + c);
-    float2 yt = ld2(y_t + t * MATRIS_D + c), ys = ld2(y_s + s * MATRIS_D + c);
-    float ptx = expf(at.x - lt.x), pty = expf(at.y - lt.y);
-    float psx = expf(as.x - ls.x), psy = expf(as.y - ls.y);
-    float2 ge = make_float2(ptx * gt.x + psx * gs.x, pty * gt.y + psy * gs.y);
-    if (g_e_base) {
-        const float2 b0 = ld2(g_e_base + r * MATRIS_D + c);
-        ge.x += b0.x;
-        ge.y += b0.y;
+    const float4 at = ld4(alpha_t + a * lda + c), as = ld4(alpha_s + a * lda + c);
+    const float4 ev = ld4(e + r * MATRIS_D + c);
+    const float4 lt = ld4(lse_t + t * MATRIS_D + c), ls = ld4(lse_s + s * MATRIS_D + c);
+    const float4 gt = ld4(g_yt + t * ldgy + c), gs = ld4(g_ys + s * ldgy + c);
+    const float4 yt = ld4(y_t + t * MATRIS_D + c), ys = ld4(y_s + s * MATRIS_D + c);
+    float4 ge = g_e_base ? ld4(g_e_base + r * MATRIS_D + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 gat, gas;
+#define ATTN_BWD_COL(k)                                                  \
+    {                                                                    \
+        const float pt = exp_neg_f(lt.k - at.k), ps = exp_neg_f(ls.k - as.k); \
+        ge.k += pt * gt.k + ps * gs.k;                                   \
+        gat.k = pt * gt.k * (ev.k - yt.k);                               \
+        gas.k = ps * gs.k * (ev.k - ys.k);                               \
     }
-    st2(g_e + r * MATRIS_D + c, ge);
-    st2(g_alpha_t + r * MATRIS_D + c, make_float2(ptx * gt.x * (ev.x - yt.x), pty * gt.y * (ev.y - yt.y)));
-    st2(g_alpha_s + r * MATRIS_D + c, make_float2(psx * gs.x * (ev.x - ys.x), psy * gs.y * (ev.y - ys.y)));
+    ATTN_BWD_COL(x) ATTN_BWD_COL(y) ATTN_BWD_COL(z) ATTN_BWD_COL(w)
+#undef ATTN_BWD_COL
+    st4(g_e + r * MATRIS_D + c, ge);
+    st4(g_alpha_t + r * MATRIS_D + c, gat);
+    st4(g_alpha_s + r * MATRIS_D + c, gas);
 }
 
 extern "C" int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s,
@@ -215,16 +278,16 @@ extern "C" int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha
                                const int32_t *s_idx, const float *y_t, const float *y_s, const float *lse_t,
                                const float *lse_s, const float *g_yt, const float *g_ys, int64_t ldgy,
                                float *g_alpha_t, float *g_alpha_s, float *g_e, const float *g_e_base, void *stream) {
-    if (n_rows < 0 || n_seg < 0 || lda < MATRIS_D || (lda % 2) || ldgy < MATRIS_D || (ldgy % 2) || !t_idx ||
+    if (n_rows < 0 || n_seg < 0 || lda < MATRIS_D || (lda % 4) || ldgy < MATRIS_D || (ldgy % 4) || !t_idx ||
         !s_idx || !g_alpha_t || !g_alpha_s || !g_e)
         return MATRIS_E_ARG;
     if (n_rows == 0) return 0;
     if (alpha_idx)
-        attn_bwd_kernel<true><<<matris_blocks(n_rows, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        attn_bwd_kernel<true><<<matris_blocks(n_rows, 2 * WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
             n_rows, alpha_t, alpha_s, lda, alpha_idx, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ldgy,
             g_alpha_t, g_alpha_s, g_e, g_e_base);
     else
-        attn_bwd_kernel<false><<<matris_blocks(n_rows, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        attn_bwd_kernel<false><<<matris_blocks(n_rows, 2 * WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
             n_rows, alpha_t, alpha_s, lda, nullptr, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ldgy,
             g_alpha_t, g_alpha_s, g_e, g_e_base);
     MATRIS_CHECK_LAUNCH();
