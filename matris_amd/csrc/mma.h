@@ -6,9 +6,10 @@
 // "planes":
 //   MODE 0  fp32 operands: planes = the 8 floats (2 x float4); v_mfma_f32_32x32x2f32 step
 //           s (0..7) consumes element s, i.e. k = 8h + s for lane half h.
-//   MODE 3  x = hi + mid (+ residual), hi = bf16(x), mid = bf16(x - hi): planes hi, mid;
-//           3 bf16 products (hi*hi + hi*mid + mid*hi) on v_mfma_f32_32x32x16_bf16.
-//   MODE 6  x = hi + mid + lo exactly, lo = bf16(x - hi - mid): planes hi, mid, lo;
+//   MODE 3  x = hi + mid (+ residual), hi = x truncated to bf16, mid = bf16(x - hi)
+//           rounded: planes hi, mid; 3 bf16 products (hi*hi + hi*mid + mid*hi) on
+//           v_mfma_f32_32x32x16_bf16.
+//   MODE 6  x = hi + mid + lo exactly (truncated hi, mid; exact lo): planes hi, mid, lo;
 //           6 products (adds hi*lo + mid*mid + lo*hi): fp32-grade products.
 // A and B fragments use the same k assignment, so every mode sums over the same k.
 // The bf16 instruction's layout (A lane l: row l%32, k = 8(l/32)..+7; B lane l:
@@ -62,7 +63,12 @@ __device__ __forceinline__ float dsilu_f(float x) {
 // Row of accumulator register i of a 32x32 tile for lane half h (column = lane % 32).
 __device__ __forceinline__ int acc_row(int i, int h) { return (i >> 2) * 8 + h * 4 + (i & 3); }
 
-// 8 fp32 values (k order) -> fragment planes.
+// 8 fp32 values (k order) -> fragment planes.  The split truncates instead of rounding:
+// hi = x with the low 16 bits cleared (the top 8 significant bits, a bf16), r = x - hi
+// (exact), mid = r with the low 16 bits cleared, lo = r - mid (exact, at most 8
+// significant bits, so it is a bf16 as well): x = hi + mid + lo exactly, with integer
+// masks and one v_perm per packed pair instead of round-to-nearest conversions.
+// MODE 3 keeps round-to-nearest for mid (its last term).
 template <int MODE>
 __device__ __forceinline__ void make_frag(Frag<MODE> &f, const float4 &u, const float4 &v) {
     if constexpr (MODE == 0) {
@@ -70,19 +76,23 @@ __device__ __forceinline__ void make_frag(Frag<MODE> &f, const float4 &u, const 
         f.p[1] = bitcast<uint4>(v);
     } else {
         const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-        v8bf hi, mid, lo;
+        uint32_t hb[8], mb[8], lb[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const __bf16 a = (__bf16)x[j];
-            const float r = x[j] - (float)a;
-            const __bf16 b = (__bf16)r;
-            hi[j] = a;
-            mid[j] = b;
-            if constexpr (MODE == 6) lo[j] = (__bf16)(r - (float)b);
+            hb[j] = bitcast<uint32_t>(x[j]) & 0xffff0000u;
+            const float r = x[j] - bitcast<float>(hb[j]);
+            if constexpr (MODE == 6) {
+                mb[j] = bitcast<uint32_t>(r) & 0xffff0000u;
+                lb[j] = bitcast<uint32_t>(r - bitcast<float>(mb[j]));
+            } else {
+                mb[j] = (uint32_t)bitcast<uint16_t>((__bf16)r) << 16;
+            }
         }
-        f.p[0] = bitcast<uint4>(hi);
-        f.p[1] = bitcast<uint4>(mid);
-        if constexpr (MODE == 6) f.p[2] = bitcast<uint4>(lo);
+        // pack the upper halves of (even, odd) pairs: bytes 2,3 of the even word, 2,3 of the odd
+        auto pk = [](uint32_t even, uint32_t odd) { return __builtin_amdgcn_perm(odd, even, 0x07060302u); };
+        f.p[0] = make_uint4(pk(hb[0], hb[1]), pk(hb[2], hb[3]), pk(hb[4], hb[5]), pk(hb[6], hb[7]));
+        f.p[1] = make_uint4(pk(mb[0], mb[1]), pk(mb[2], mb[3]), pk(mb[4], mb[5]), pk(mb[6], mb[7]));
+        if constexpr (MODE == 6) f.p[2] = make_uint4(pk(lb[0], lb[1]), pk(lb[2], lb[3]), pk(lb[4], lb[5]), pk(lb[6], lb[7]));
     }
 }
 
@@ -165,6 +175,37 @@ __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const flo
     }
 }
 
+// One 32-row A tile against two groups of two B tiles (starting at tiles ntA and ntB):
+// acc0 += A * B[ntA, ntA+1], acc1 += A * B[ntB, ntB+1]; one A conversion per k-block
+// feeds four MFMA tiles.
+template <int MODE, int KBA>
+__device__ __forceinline__ void gemm_lds_packed2(v16f (&acc0)[1][2], v16f (&acc1)[1][2], const float *a_base,
+                                                 int lda, const uint4 *__restrict__ W, int ntA, int ntB, int KBW,
+                                                 int lane) {
+    Frag<MODE> c0[2], c1[2], n0[2], n1[2];
+    load_bfrags<MODE, 2>(c0, W, ntA, KBW, 0, lane);
+    load_bfrags<MODE, 2>(c1, W, ntB, KBW, 0, lane);
+#pragma unroll 1
+    for (int kb = 0; kb < KBA; ++kb) {
+        const int kn = min(kb + 1, KBA - 1);
+        load_bfrags<MODE, 2>(n0, W, ntA, KBW, kn, lane);
+        load_bfrags<MODE, 2>(n1, W, ntB, KBW, kn, lane);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
+        Frag<MODE> a[1];
+        lds_afrags<MODE, 1>(a, a_base, lda, kb, lane);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            mma_frag<MODE>(acc0[0][ct], a[0], c0[ct]);
+            mma_frag<MODE>(acc1[0][ct], a[0], c1[ct]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            c0[ct] = n0[ct];
+            c1[ct] = n1[ct];
+        }
+    }
+}
+
 template <int NRT, int NCT>
 __device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
 #pragma unroll
@@ -175,21 +216,28 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
             for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
 }
 
-// Write a wave's accumulators (rows 0..63, columns col0 + ct*32 + lane%32), plus an
-// optional per-column bias, into an fp32 LDS tile of row stride ld.
-template <int NCT>
-__device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *tile, int ld, int col0, int lane,
-                                           const float *__restrict__ bias = nullptr) {
+// Write a wave's accumulators (rows row0 + rt*32 + .., columns col0 + ct*32 + lane%32),
+// plus an optional per-column bias, into an fp32 LDS tile of row stride ld.
+template <int NRT, int NCT>
+__device__ __forceinline__ void acc_to_lds_rc(const v16f (&acc)[NRT][NCT], float *tile, int ld, int row0, int col0,
+                                              int lane, const float *__restrict__ bias = nullptr) {
     const int h = lane >> 5, l32 = lane & 31;
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
         const int col = col0 + ct * 32 + l32;
         const float b = bias ? bias[col] : 0.f;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) tile[(rt * 32 + acc_row(i, h)) * ld + col] = acc[rt][ct][i] + b;
+            for (int i = 0; i < 16; ++i) tile[(row0 + rt * 32 + acc_row(i, h)) * ld + col] = acc[rt][ct][i] + b;
     }
+}
+
+// The 64-row form used by the 4-waves-by-columns kernels.
+template <int NCT>
+__device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *tile, int ld, int col0, int lane,
+                                           const float *__restrict__ bias = nullptr) {
+    acc_to_lds_rc<2, NCT>(acc, tile, ld, 0, col0, lane, bias);
 }
 
 // Bytes of a packed [n, k] weight in `mode` (n % 32 == 0, k % 16 == 0).

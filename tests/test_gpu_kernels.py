@@ -190,15 +190,18 @@ def test_pack_b_fragment_layout():
     # mode 0: the fp32 values themselves, 8 per lane as two 16-byte planes
     p0 = ops.pack_b(w.to(DEV), 0).cpu().view(torch.float32).view(n // 32, k // 16, 2, 64, 4)
     assert torch.equal(p0[nt, kb, j // 4, lane, j % 4], w)
-    # mode 6: hi = bf16(w) (round to nearest even), and hi + mid + lo == w exactly
+    # mode 6: hi = w truncated to bf16 (low 16 bits cleared), mid likewise for w - hi,
+    # and hi + mid + lo == w exactly
     p6 = ops.pack_b(w.to(DEV), 6).cpu().view(torch.bfloat16).view(n // 32, k // 16, 3, 64, 8)
     hi, mid, lo = (p6[nt, kb, q, lane, j].double() for q in range(3))
-    assert torch.equal(p6[nt, kb, 0, lane, j], w.to(torch.bfloat16))
+    trunc = (w.view(torch.int32) & -65536).view(torch.float32)
+    assert torch.equal(p6[nt, kb, 0, lane, j].float(), trunc)
     assert torch.equal(hi + mid + lo, w.double())
-    assert (mid.abs() <= hi.abs() * 2.0 ** -8).all() and (lo.abs() <= mid.abs() * 2.0 ** -8).all()
-    # mode 3: the first two planes of mode 6
+    assert (mid.abs() < hi.abs() * 2.0 ** -7).all() and (lo.abs() < mid.abs() * 2.0 ** -7).all()
+    # mode 3: the same hi plane; mid = round-to-nearest bf16 of w - hi
     p3 = ops.pack_b(w.to(DEV), 3).cpu().view(torch.bfloat16).view(n // 32, k // 16, 2, 64, 8)
-    assert torch.equal(p3, p6[:, :, :2])
+    assert torch.equal(p3[:, :, 0], p6[:, :, 0])
+    assert torch.equal(p3[nt, kb, 1, lane, j], (w - trunc).to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("mode,tol", _MODES)
