@@ -153,6 +153,35 @@ int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h, const floa
                        const int32_t *s_perm, int accumulate, float *g_h, float *g_env, void *stream);
 
 /* ------------------------------------------------------------------------------------
+ * Basis functions of the embeddings (rows E2, E3), thread per row, with input gradients.
+ * ------------------------------------------------------------------------------------ */
+
+/* E2: Bessel basis times the polynomial envelope (matris/model/basis_function.py:8-50,
+ * 116-186), out [n, num_radial] with
+ *   out[i,k] = env(d_i/cutoff) * (sqrt(2/cutoff) * sin(freq[k] * d_i/cutoff) / d_i),
+ *   env(x) = 1 + a x^p + b x^(p+1) + c x^(p+2) (x < 1), 0 otherwise (p = envelope_exponent).
+ * bwd: g_dist[i] (+)= sum_k g_out[i,k] d out[i,k] / d d_i (frequency gradients are not
+ * produced). */
+int matris_bessel_fwd(int64_t n, int num_radial, const float *dist, const float *freq, double cutoff,
+                      double envelope_exponent, float *out, void *stream);
+int matris_bessel_bwd(int64_t n, int num_radial, const float *dist, const float *freq, double cutoff,
+                      double envelope_exponent, const float *g_out, int accumulate, float *g_dist, void *stream);
+
+/* E3: spherical three-body basis (feature_embed.py:183-201, basis_function.py:53-77,
+ * 222-338, max_n = max_l = 4): for angle row a with t = de_t[a] (the line graph's
+ * target_DE_index) and s = de_s[a] (source_DE_index) into unit [E_d, 3]:
+ *   c = (unit[t] . unit[s]) (1 - 1e-6), x = |unit[s]| / cutoff,
+ *   out[a, 4n+j] = sqrt(2/cutoff^3) R_{n,j}(x) Y_n(cos(acos c)),  out [A, 16].
+ * bwd: thread per directed edge d: g_unit[d] (+)= the gradient of every row that reads
+ * unit[d] as t (CSR t_ptr/t_perm of de_t over E_d) or as s (CSR s_ptr/s_perm of de_s),
+ * summed in CSR order (deterministic). */
+int matris_sbf_fwd(int64_t n_angles, const float *unit, const int32_t *de_t, const int32_t *de_s, double cutoff,
+                   float *out, void *stream);
+int matris_sbf_bwd(int64_t n_edges, const float *unit, const int32_t *de_t, const int32_t *de_s,
+                   const float *g_basis, const int32_t *t_ptr, const int32_t *t_perm, const int32_t *s_ptr,
+                   const int32_t *s_perm, double cutoff, int accumulate, float *g_unit, void *stream);
+
+/* ------------------------------------------------------------------------------------
  * MFMA arithmetic and packed weights (shared by the gated MLP, FFN and projection pair).
  * `mode` selects the arithmetic (fp32 in, fp32 accumulate in every mode):
  *   MATRIS_MMA_FP32   v_mfma_f32_32x32x2f32 on the fp32 operands;

@@ -98,7 +98,10 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
                    source_index=cols[3].long(), target_DE_index=cols[2].long(), source_DE_index=cols[4].long(),
                    grp_tgt=Grouping.build(cols[1], U, sorted_rows=True),
                    grp_src=Grouping.build(cols[3], U),
-                   grp_atom=Grouping.build(cols[0], N))
+                   grp_atom=Grouping.build(cols[0], N),
+                   # directed edges read by each angle (three-body basis and its backward)
+                   grp_de_t=Grouping.build(cols[2], E),
+                   grp_de_s=Grouping.build(cols[4], E))
     else:
         lgd = dict(line_graph=torch.zeros(0, 3, dtype=torch.int64, device=device))
     out["line_graph_dict"] = lgd

@@ -202,6 +202,8 @@ class BesselExpansion(nn.Module):
         self.envelope_func = PolynomialEnvelope(cutoff, envelope_exponent) if envelope_exponent is not None else None
 
     def forward(self, dist, return_smooth_factor=False):
+        if dist.is_cuda and self.envelope_func is not None and not return_smooth_factor:
+            return ops.bessel(dist, self.frequencies, self.envelope_func.cutoff, self.envelope_func.p)
         dist = dist[:, None]
         out = self.norm_const * torch.sin(self.frequencies * (dist * self.inv_cutoff)) / dist
         if self.envelope_func is not None:
@@ -329,6 +331,10 @@ class ThreebodyEmbedding(nn.Module):
 
     def forward(self, graphs):
         lg = graphs["line_graph_dict"]
+        exp = self.expansion
+        if graphs["unit_edge_vectors"].is_cuda and exp.max_n == 4 and exp.max_l == 4 and "grp_de_t" in lg:
+            basis = ops.spherical_basis(graphs["unit_edge_vectors"], lg["grp_de_t"], lg["grp_de_s"], exp.cutoff)
+            return self.swish_layer(self.angle_embedding(basis))
         vij = torch.index_select(graphs["unit_edge_vectors"], 0, lg["target_DE_index"])
         vjk = torch.index_select(graphs["unit_edge_vectors"], 0, lg["source_DE_index"])
         cos_t = torch.sum(vij * vjk, dim=1) * (1 - 1e-6)

@@ -521,3 +521,75 @@ class _Pair(torch.autograd.Function):
 def proj_pair(pack: _WeightPack, x):
     """(x W0^T, x W1^T) for two bias-free 128x128 Linears in one MFMA pass."""
     return _Pair.apply(x, pack)
+
+
+# ------------------------------------------------------------------------------------
+# basis functions of the embeddings (E2, E3)
+# ------------------------------------------------------------------------------------
+class _Bessel(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, dist, freq, cutoff: float, p: float):
+        _check_dev(dist, freq)
+        dist, freq = _f32c(dist), _f32c(freq.detach())
+        lib = _lib.load()
+        n, nr = dist.shape[0], freq.shape[0]
+        out = torch.empty(n, nr, device=dist.device)
+        with _timed("bessel_fwd", (n,)):
+            _lib.check(lib.matris_bessel_fwd(n, nr, _p(dist), _p(freq), cutoff, p, _p(out), _stream()),
+                       "matris_bessel_fwd")
+        ctx.save_for_backward(dist, freq)
+        ctx.cutoff, ctx.p = cutoff, p
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        dist, freq = ctx.saved_tensors
+        lib = _lib.load()
+        g = _f32c(g)
+        g_dist = torch.empty_like(dist)
+        with _timed("bessel_bwd", (dist.shape[0],)):
+            _lib.check(lib.matris_bessel_bwd(dist.shape[0], freq.shape[0], _p(dist), _p(freq), ctx.cutoff, ctx.p,
+                                             _p(g), 0, _p(g_dist), _stream()), "matris_bessel_bwd")
+        return g_dist, None, None, None
+
+
+def bessel(dist, freq, cutoff: float, envelope_exponent: float):
+    """[n, len(freq)] Bessel basis times the polynomial envelope (basis_function.py:8-50,
+    116-186); the backward returns the distance gradient only."""
+    return _Bessel.apply(dist, freq, float(cutoff), float(envelope_exponent))
+
+
+class _SBF(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, unit, grp_t: Grouping, grp_s: Grouping, cutoff: float):
+        _check_dev(unit)
+        unit = _f32c(unit)
+        lib = _lib.load()
+        A = grp_t.n_rows
+        out = torch.empty(A, 16, device=unit.device)
+        with _timed("sbf_fwd", (A,)):
+            _lib.check(lib.matris_sbf_fwd(A, _p(unit), _p(grp_t.key), _p(grp_s.key), cutoff, _p(out), _stream()),
+                       "matris_sbf_fwd")
+        ctx.save_for_backward(unit)
+        ctx.grp_t, ctx.grp_s, ctx.cutoff = grp_t, grp_s, cutoff
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (unit,) = ctx.saved_tensors
+        gt, gs = ctx.grp_t, ctx.grp_s
+        lib = _lib.load()
+        g = _f32c(g)
+        g_unit = torch.empty_like(unit)
+        with _timed("sbf_bwd", (unit.shape[0],)):
+            _lib.check(lib.matris_sbf_bwd(unit.shape[0], _p(unit), _p(gt.key), _p(gs.key), _p(g), _p(gt.rowptr),
+                                          _p(gt.perm), _p(gs.rowptr), _p(gs.perm), ctx.cutoff, 0, _p(g_unit),
+                                          _stream()), "matris_sbf_bwd")
+        return g_unit, None, None, None
+
+
+def spherical_basis(unit, grp_t: Grouping, grp_s: Grouping, cutoff: float):
+    """[A, 16] three-body basis of every angle from the unit edge vectors [E_d, 3]: grp_t /
+    grp_s group the angles by the directed edge they read as i->j (target_DE_index) and
+    j->k (source_DE_index) (feature_embed.py:183-201, basis_function.py:222-338)."""
+    return _SBF.apply(unit, grp_t, grp_s, float(cutoff))
