@@ -18,6 +18,30 @@ static inline int matris_blocks(int64_t work, int per_block) {
     return (int)(b < 1 ? 1 : b);
 }
 
+// Work-group barrier that orders LDS only: the fences are scoped to the local address
+// space, so the barrier waits for this wave's LDS operations but leaves global loads
+// (prefetches) in flight, where __syncthreads() would drain them all.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), returned in all of them:
+// quad swaps, then the half-row and row mirrors, as four VALU ops with DPP operands.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

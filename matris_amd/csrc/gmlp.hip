@@ -9,12 +9,16 @@
 // Work-group = 4 wave64s, BM = 64 rows.  GEMM1 streams K in 32-wide chunks: each thread
 // gathers 8 values of one row of the next chunk, converts them once into an operand
 // fragment (mma.h) and writes it to a double-buffered LDS chunk, so one barrier per
-// chunk suffices and no wave converts A values itself; the pre-packed W1 fragments come
+// chunk suffices and no wave converts X values itself; the pre-packed W1 fragments come
 // straight from global (L2) one k-block ahead.  Each wave owns 64 output columns (2x2
-// grid of 32x32 tiles).  The [64, 256] result tile goes through LDS: p is copied out
-// with 16-byte row stores, h = SiLU(p) stays in LDS as GEMM2's A operand, z returns to
-// LDS, is copied out, and a row-per-wave epilogue applies RMSNorm, SiLU, sigmoid and
-// the product with 512-byte row stores.  p and z are written for the backward.
+// tiles of 32x32) and both GEMMs run transposed (P^T = W1 X^T, Z^T = W2 H^T: the weight
+// fragment is the MFMA A operand), so every lane holds whole-row segments: lane
+// (row l % 32 of a row tile, half l / 32) has columns 32 ct + 8 j + 4 (l / 32) .. +3.
+// p and z go to an LDS tile with 16-byte writes.  One pass copies p out with 16-byte row
+// stores and turns it into h = SiLU(p), GEMM2's operand; a row pass with 16 lanes per
+// row saves z, applies the two RMSNorms (16-lane DPP sums), SiLU, sigmoid and their
+// product, and writes out with 512-byte row stores.  p and z are written for the
+// backward.
 //
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) mma_frag<MODE>(acc[rt][ct], a[rt], bcur[ct]);
+                for (int ct = 0; ct < 2; ++ct) mma_frag<MODE>(acc[rt][ct], bcur[ct], a[rt]);  // P^T tiles
             bcur[0] = bnxt[0];
             bcur[1] = bnxt[1];
         }
@@ -132,49 +136,85 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 #undef GMLP_LOADX
 #undef GMLP_STOREX
 
-    // p = acc + b1 -> LDS; copy p out with wide stores; h = SiLU(p) in place
-    acc_to_lds<2>(acc, Ts, LDH, wave * 64, lane, b1);
+    // p = acc + b1 -> LDS (rows in lanes: 16-byte writes); one pass copies p out with
+    // 16-byte row stores and turns it into h = SiLU(p) in place
+    acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b1);
     __syncthreads();
-    if (save_p) store_tile256(Ts, save_p, m0, M, tid);
 #pragma unroll
     for (int it = 0; it < (BM * 64) / 256; ++it) {
         const int q = it * 256 + tid;
-        float4 *t = reinterpret_cast<float4 *>(Ts + (q >> 6) * LDH + (q & 63) * 4);
+        const int row = q >> 6, c4 = (q & 63) * 4;
+        float4 *t = reinterpret_cast<float4 *>(Ts + row * LDH + c4);
         float4 v = *t;
+        if (save_p && m0 + row < M) *reinterpret_cast<float4 *>(save_p + (m0 + row) * 256 + c4) = v;
         v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
         *t = v;
     }
     __syncthreads();
 
-    // GEMM2: wave w -> z columns [64w, 64w+64); block = w/2 (0 core, 1 gate)
+    // GEMM2, transposed: wave w -> z columns [64w, 64w+64) of both row tiles, rows in lanes;
+    // block = w/2 (0 core, 1 gate)
     const int blk = wave >> 1;
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, Ts + blk * MATRIS_D, LDH, W2, 2 * wave, MATRIS_D / 16, 0, lane);
+    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Ts + blk * MATRIS_D, LDH, W2, 2 * wave, MATRIS_D / 16, 0,
+                                                     lane);
     __syncthreads();  // every wave is done reading h
-    acc_to_lds<2>(acc, Ts, LDH, wave * 64, lane, b2);
-    __syncthreads();
-    if (save_z) store_tile256(Ts, save_z, m0, M, tid);
 
-    // row epilogue: wave w -> rows [16w, 16w+16); lane -> columns 2l, 2l+1 of each half;
-    // optional residual output res_out = out + res_w * res_src
-    const float2 wc = *reinterpret_cast<const float2 *>(norm_c + 2 * lane);
-    const float2 wg = *reinterpret_cast<const float2 *>(norm_g + 2 * lane);
-    const float2 rw = res_out ? *reinterpret_cast<const float2 *>(res_w + 2 * lane) : make_float2(0.f, 0.f);
-    for (int rr = 0; rr < BM / 4; ++rr) {
-        const int row = wave * (BM / 4) + rr;
-        const float2 zc = *reinterpret_cast<const float2 *>(Ts + row * LDH + 2 * lane);
-        const float2 zg = *reinterpret_cast<const float2 *>(Ts + row * LDH + MATRIS_D + 2 * lane);
-        const float rc = rsqrtf(wave_sum(zc.x * zc.x + zc.y * zc.y) * (1.0f / MATRIS_D) + eps);
-        const float rg = rsqrtf(wave_sum(zg.x * zg.x + zg.y * zg.y) * (1.0f / MATRIS_D) + eps);
-        float2 o;
-        o.x = silu_f(zc.x * rc * wc.x) * sigm_f(zg.x * rg * wg.x);
-        o.y = silu_f(zc.y * rc * wc.y) * sigm_f(zg.y * rg * wg.y);
-        if (m0 + row < M) {
-            *reinterpret_cast<float2 *>(out + (m0 + row) * MATRIS_D + 2 * lane) = o;
+    // z = acc + b2 -> LDS (16-byte writes); then a row pass with 16 lanes per row: lane
+    // c of a row holds core columns 8c .. 8c+7 and the same gate columns, saves z and
+    // writes out with 512-byte row stores, and each RMSNorm sum is a 16-lane DPP sum
+    acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b2);
+    __syncthreads();
+    const int c8 = (lane & 15) * 8;
+    const float4 wc0 = *reinterpret_cast<const float4 *>(norm_c + c8);
+    const float4 wc1 = *reinterpret_cast<const float4 *>(norm_c + c8 + 4);
+    const float4 wg0 = *reinterpret_cast<const float4 *>(norm_g + c8);
+    const float4 wg1 = *reinterpret_cast<const float4 *>(norm_g + c8 + 4);
+#pragma unroll
+    for (int rr = 0; rr < BM / 16; ++rr) {
+        const int row = wave * (BM / 4) + rr * 4 + (lane >> 4);
+        const float *zr = Ts + row * LDH;
+        const float4 zc0 = *reinterpret_cast<const float4 *>(zr + c8);
+        const float4 zc1 = *reinterpret_cast<const float4 *>(zr + c8 + 4);
+        const float4 zg0 = *reinterpret_cast<const float4 *>(zr + MATRIS_D + c8);
+        const float4 zg1 = *reinterpret_cast<const float4 *>(zr + MATRIS_D + c8 + 4);
+        const int64_t grow = m0 + row;
+        if (save_z && grow < M) {
+            float *zo = save_z + grow * 256 + c8;
+            *reinterpret_cast<float4 *>(zo) = zc0;
+            *reinterpret_cast<float4 *>(zo + 4) = zc1;
+            *reinterpret_cast<float4 *>(zo + MATRIS_D) = zg0;
+            *reinterpret_cast<float4 *>(zo + MATRIS_D + 4) = zg1;
+        }
+        const float rc = rsqrtf(row16_sum(zc0.x * zc0.x + zc0.y * zc0.y + zc0.z * zc0.z + zc0.w * zc0.w +
+                                          zc1.x * zc1.x + zc1.y * zc1.y + zc1.z * zc1.z + zc1.w * zc1.w) *
+                                    (1.0f / MATRIS_D) + eps);
+        const float rg = rsqrtf(row16_sum(zg0.x * zg0.x + zg0.y * zg0.y + zg0.z * zg0.z + zg0.w * zg0.w +
+                                          zg1.x * zg1.x + zg1.y * zg1.y + zg1.z * zg1.z + zg1.w * zg1.w) *
+                                    (1.0f / MATRIS_D) + eps);
+        float4 o0, o1;
+        o0.x = silu_f(zc0.x * rc * wc0.x) * sigm_f(zg0.x * rg * wg0.x);
+        o0.y = silu_f(zc0.y * rc * wc0.y) * sigm_f(zg0.y * rg * wg0.y);
+        o0.z = silu_f(zc0.z * rc * wc0.z) * sigm_f(zg0.z * rg * wg0.z);
+        o0.w = silu_f(zc0.w * rc * wc0.w) * sigm_f(zg0.w * rg * wg0.w);
+        o1.x = silu_f(zc1.x * rc * wc1.x) * sigm_f(zg1.x * rg * wg1.x);
+        o1.y = silu_f(zc1.y * rc * wc1.y) * sigm_f(zg1.y * rg * wg1.y);
+        o1.z = silu_f(zc1.z * rc * wc1.z) * sigm_f(zg1.z * rg * wg1.z);
+        o1.w = silu_f(zc1.w * rc * wc1.w) * sigm_f(zg1.w * rg * wg1.w);
+        if (grow < M) {
+            float *orow = out + grow * MATRIS_D + c8;
+            *reinterpret_cast<float4 *>(orow) = o0;
+            *reinterpret_cast<float4 *>(orow + 4) = o1;
             if (res_out) {
-                const float2 x = *reinterpret_cast<const float2 *>(res_src + (m0 + row) * MATRIS_D + 2 * lane);
-                *reinterpret_cast<float2 *>(res_out + (m0 + row) * MATRIS_D + 2 * lane) =
-                    make_float2(o.x + rw.x * x.x, o.y + rw.y * x.y);
+                const float4 w0 = *reinterpret_cast<const float4 *>(res_w + c8);
+                const float4 w1 = *reinterpret_cast<const float4 *>(res_w + c8 + 4);
+                const float4 x0 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c8);
+                const float4 x1 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c8 + 4);
+                float *ro = res_out + grow * MATRIS_D + c8;
+                *reinterpret_cast<float4 *>(ro) = make_float4(o0.x + w0.x * x0.x, o0.y + w0.y * x0.y, o0.z + w0.z * x0.z,
+                                                              o0.w + w0.w * x0.w);
+                *reinterpret_cast<float4 *>(ro + 4) = make_float4(o1.x + w1.x * x1.x, o1.y + w1.y * x1.y,
+                                                                  o1.z + w1.z * x1.z, o1.w + w1.w * x1.w);
             }
         }
     }
@@ -215,44 +255,69 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     const int64_t m0 = (int64_t)blockIdx.x * BM;
 
     // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g).
-    // Wave w owns rows [16w, 16w+16); lane owns columns (2l, 2l+1) of the core and gate
-    // halves.  The next row's z / g_out are loaded before the current row is processed.
-    const float2 wc = *reinterpret_cast<const float2 *>(norm_c + 2 * lane);
-    const float2 wg = *reinterpret_cast<const float2 *>(norm_g + 2 * lane);
-    const float2 zero2 = make_float2(0.f, 0.f);
-    auto ld_row = [&](int rr, float2 &zc, float2 &zg, float2 &go) {
-        const int64_t m = m0 + wave * (BM / 4) + rr;
-        if (m < M) {
-            zc = *reinterpret_cast<const float2 *>(Z + m * 256 + 2 * lane);
-            zg = *reinterpret_cast<const float2 *>(Z + m * 256 + MATRIS_D + 2 * lane);
-            go = *reinterpret_cast<const float2 *>(g_out + m * MATRIS_D + 2 * lane);
-        } else {
-            zc = zg = go = zero2;
+    // 16 lanes per row (4 rows per wave per pass, wave w owns rows [16w, 16w+16)): lane c
+    // of a row owns core and gate columns 8c .. 8c+7, reads them with 512-byte row loads,
+    // and the four row reductions are 16-lane DPP sums.  Rows past M read zeros (g = 0).
+    {
+        const int c8 = (lane & 15) * 8;
+        float wc[8], wg[8];
+        {
+            const float4 a0 = *reinterpret_cast<const float4 *>(norm_c + c8);
+            const float4 a1 = *reinterpret_cast<const float4 *>(norm_c + c8 + 4);
+            const float4 b0 = *reinterpret_cast<const float4 *>(norm_g + c8);
+            const float4 b1 = *reinterpret_cast<const float4 *>(norm_g + c8 + 4);
+            wc[0] = a0.x; wc[1] = a0.y; wc[2] = a0.z; wc[3] = a0.w; wc[4] = a1.x; wc[5] = a1.y; wc[6] = a1.z; wc[7] = a1.w;
+            wg[0] = b0.x; wg[1] = b0.y; wg[2] = b0.z; wg[3] = b0.w; wg[4] = b1.x; wg[5] = b1.y; wg[6] = b1.z; wg[7] = b1.w;
         }
-    };
-    float2 zc, zg, go, zc_n, zg_n, go_n;
-    ld_row(0, zc, zg, go);
-#pragma unroll 1
-    for (int rr = 0; rr < BM / 4; ++rr) {
-        if (rr + 1 < BM / 4) ld_row(rr + 1, zc_n, zg_n, go_n);
-        const int row = wave * (BM / 4) + rr;
-        const float rc = rsqrtf(wave_sum(zc.x * zc.x + zc.y * zc.y) * (1.0f / MATRIS_D) + eps);
-        const float rg = rsqrtf(wave_sum(zg.x * zg.x + zg.y * zg.y) * (1.0f / MATRIS_D) + eps);
-        const float nc0 = zc.x * rc, nc1 = zc.y * rc, ng0 = zg.x * rg, ng1 = zg.y * rg;
-        const float ac0 = nc0 * wc.x, ac1 = nc1 * wc.y, ag0 = ng0 * wg.x, ag1 = ng1 * wg.y;
-        const float sc0 = sigm_f(ac0), sc1 = sigm_f(ac1);
-        const float core0 = ac0 * sc0, core1 = ac1 * sc1;
-        const float gate0 = sigm_f(ag0), gate1 = sigm_f(ag1);
-        const float gnc0 = go.x * gate0 * (sc0 * (1.f + ac0 * (1.f - sc0))) * wc.x;
-        const float gnc1 = go.y * gate1 * (sc1 * (1.f + ac1 * (1.f - sc1))) * wc.y;
-        const float gng0 = go.x * core0 * (gate0 * (1.f - gate0)) * wg.x;
-        const float gng1 = go.y * core1 * (gate1 * (1.f - gate1)) * wg.y;
-        const float dc = wave_sum(gnc0 * nc0 + gnc1 * nc1) * (1.0f / MATRIS_D);
-        const float dg = wave_sum(gng0 * ng0 + gng1 * ng1) * (1.0f / MATRIS_D);
-        *reinterpret_cast<float2 *>(G + row * LDH + 2 * lane) = make_float2((gnc0 - nc0 * dc) * rc, (gnc1 - nc1 * dc) * rc);
-        *reinterpret_cast<float2 *>(G + row * LDH + MATRIS_D + 2 * lane) =
-            make_float2((gng0 - ng0 * dg) * rg, (gng1 - ng1 * dg) * rg);
-        zc = zc_n; zg = zg_n; go = go_n;
+#pragma unroll
+        for (int rr = 0; rr < BM / 16; ++rr) {
+            const int row = wave * (BM / 4) + rr * 4 + (lane >> 4);
+            const int64_t m = m0 + row;
+            float zc[8], zg[8], go[8];
+            if (m < M) {
+                const float4 *zr = reinterpret_cast<const float4 *>(Z + m * 256 + c8);
+                const float4 *gr = reinterpret_cast<const float4 *>(g_out + m * MATRIS_D + c8);
+                const float4 z0 = zr[0], z1 = zr[1], y0 = zr[MATRIS_D / 4], y1 = zr[MATRIS_D / 4 + 1];
+                const float4 g0 = gr[0], g1 = gr[1];
+                zc[0] = z0.x; zc[1] = z0.y; zc[2] = z0.z; zc[3] = z0.w; zc[4] = z1.x; zc[5] = z1.y; zc[6] = z1.z; zc[7] = z1.w;
+                zg[0] = y0.x; zg[1] = y0.y; zg[2] = y0.z; zg[3] = y0.w; zg[4] = y1.x; zg[5] = y1.y; zg[6] = y1.z; zg[7] = y1.w;
+                go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w; go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) zc[e] = zg[e] = go[e] = 0.f;
+            }
+            float sc2 = 0.f, sg2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sc2 += zc[e] * zc[e];
+                sg2 += zg[e] * zg[e];
+            }
+            const float rc = rsqrtf(row16_sum(sc2) * (1.0f / MATRIS_D) + eps);
+            const float rg = rsqrtf(row16_sum(sg2) * (1.0f / MATRIS_D) + eps);
+            float nc[8], ng[8], gnc[8], gng[8], dcs = 0.f, dgs = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                nc[e] = zc[e] * rc;
+                ng[e] = zg[e] * rg;
+                const float ac = nc[e] * wc[e], ag = ng[e] * wg[e];
+                const float sc = sigm_f(ac), gate = sigm_f(ag);
+                gnc[e] = go[e] * gate * (sc * (1.f + ac * (1.f - sc))) * wc[e];
+                gng[e] = go[e] * (ac * sc) * (gate * (1.f - gate)) * wg[e];
+                dcs += gnc[e] * nc[e];
+                dgs += gng[e] * ng[e];
+            }
+            const float dc = row16_sum(dcs) * (1.0f / MATRIS_D), dg = row16_sum(dgs) * (1.0f / MATRIS_D);
+            float *gr = G + row * LDH + c8;
+#pragma unroll
+            for (int e4 = 0; e4 < 2; ++e4) {
+                *reinterpret_cast<float4 *>(gr + 4 * e4) =
+                    make_float4((gnc[4 * e4] - nc[4 * e4] * dc) * rc, (gnc[4 * e4 + 1] - nc[4 * e4 + 1] * dc) * rc,
+                                (gnc[4 * e4 + 2] - nc[4 * e4 + 2] * dc) * rc, (gnc[4 * e4 + 3] - nc[4 * e4 + 3] * dc) * rc);
+                *reinterpret_cast<float4 *>(gr + MATRIS_D + 4 * e4) =
+                    make_float4((gng[4 * e4] - ng[4 * e4] * dg) * rg, (gng[4 * e4 + 1] - ng[4 * e4 + 1] * dg) * rg,
+                                (gng[4 * e4 + 2] - ng[4 * e4 + 2] * dg) * rg, (gng[4 * e4 + 3] - ng[4 * e4 + 3] * dg) * rg);
+            }
+        }
     }
     __syncthreads();
 

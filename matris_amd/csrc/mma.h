@@ -154,7 +154,11 @@ __device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *ba
 // fragments are loaded while the current one is consumed.  The prefetch is
 // unconditional (the last step reloads its own block) so the compiler's load counting
 // stays exact.
-template <int MODE, int NRT, int NCT, int KBA>
+// TRANS computes the transposed product instead, acc[rt][ct] = (B^T A^T) tile: the packed
+// weight fragment is the MFMA A operand and the LDS rows the B operand, so lane l holds
+// row rt*32 + l%32 of A and its 16 registers are output columns ct*32 + acc_row(i, l/32)
+// (four runs of four consecutive columns) -- a layout with whole rows in lanes.
+template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false>
 __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
     constexpr int kUnroll = NCT >= 2 ? 1 : 2;  // 2-tile bodies are long enough; keeps pressure down
@@ -169,7 +173,12 @@ __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const flo
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) mma_frag<MODE>(acc[rt][ct], a[rt], cur[ct]);
+            for (int ct = 0; ct < NCT; ++ct) {
+                if constexpr (TRANS)
+                    mma_frag<MODE>(acc[rt][ct], cur[ct], a[rt]);
+                else
+                    mma_frag<MODE>(acc[rt][ct], a[rt], cur[ct]);
+            }
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
     }
@@ -231,6 +240,27 @@ __device__ __forceinline__ void acc_to_lds_rc(const v16f (&acc)[NRT][NCT], float
 #pragma unroll
             for (int i = 0; i < 16; ++i) tile[(row0 + rt * 32 + acc_row(i, h)) * ld + col] = acc[rt][ct][i] + b;
     }
+}
+
+// Transposed accumulators (rows in lanes, see gemm_lds_packed<..., TRANS>) plus a per-column
+// bias into a row-major fp32 LDS tile: row rt*32 + lane%32, columns col0 + ct*32 + 8j + 4h
+// .. +3 as one 16-byte write each.
+template <int NRT, int NCT>
+__device__ __forceinline__ void acc_t_to_lds(const v16f (&acc)[NRT][NCT], float *tile, int ld, int col0, int lane,
+                                             const float *__restrict__ bias) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = col0 + ct * 32 + 8 * j + 4 * h;
+            const float4 b = *reinterpret_cast<const float4 *>(bias + col);
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+                *reinterpret_cast<float4 *>(tile + (rt * 32 + l32) * ld + col) =
+                    make_float4(acc[rt][ct][4 * j] + b.x, acc[rt][ct][4 * j + 1] + b.y, acc[rt][ct][4 * j + 2] + b.z,
+                                acc[rt][ct][4 * j + 3] + b.w);
+        }
 }
 
 // The 64-row form used by the 4-waves-by-columns kernels.
