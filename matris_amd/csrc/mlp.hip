@@ -9,8 +9,10 @@
 //
 // and their input-gradient kernels.  Work-group = 4 wave64s over BM = 64 rows; the
 // [64, 128] input tile is staged once in LDS (K = 128 needs no K loop), weights are
-// pre-packed B fragments (mma.h) read from global one k-block ahead, and intermediate
-// tiles (p, h, g_h) stay in LDS.  Outputs leave through LDS with 16-byte row stores.
+// pre-packed fragments (mma.h) read from global one k-block ahead, and intermediate
+// tiles (p, h, g_h) stay in LDS.  The GEMMs run transposed (weight fragment as the MFMA A
+// operand, rows in lanes), so results reach LDS with 16-byte writes.  Outputs leave
+// through LDS with 16-byte row stores.
 #include <initializer_list>
 
 #include "mma.h"
@@ -67,73 +69,85 @@ __device__ __forceinline__ void store_tile128_scaled(const float *tile, float *_
 // ------------------------------------------------------------------------------------
 // FFN forward: p = x W1^T (saved), out = SiLU(p) W2^T
 // ------------------------------------------------------------------------------------
+// One [64, 128] LDS tile per work-group (three work-groups per CU): x, then p / h, then
+// out pass through it.  Both GEMMs run transposed (rows in lanes, mma.h), so results go
+// to the tile as 16-byte writes; one pass saves p and applies SiLU in place.
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void ffn_fwd_kernel(int64_t M, const float *__restrict__ x,
+__global__ __launch_bounds__(256, 3) void ffn_fwd_kernel(int64_t M, const float *__restrict__ x,
                                                          const uint4 *__restrict__ W1, const uint4 *__restrict__ W2,
                                                          float *__restrict__ out, float *__restrict__ save_p,
                                                          const float *__restrict__ res,
                                                          const float *__restrict__ res_w) {
-    __shared__ __align__(16) float T0[BM * LDT];
-    __shared__ __align__(16) float T1[BM * LDT];
+    __shared__ __align__(16) float T[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
-    stage_tile128(T0, x, MATRIS_D, m0, M, tid);
+    stage_tile128(T, x, MATRIS_D, m0, M, tid);
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, W1, wave, MATRIS_D / 16, 0, lane);
-    acc_to_lds<1>(acc, T1, LDT, wave * 32, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1, wave, MATRIS_D / 16, 0, lane);
+    __syncthreads();  // every wave is done reading x
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
-    if (save_p) store_tile128(T1, save_p, MATRIS_D, m0, M, tid);
 #pragma unroll
     for (int it = 0; it < (BM * 32) / 256; ++it) {
         const int q = it * 256 + tid;
-        float4 *t = reinterpret_cast<float4 *>(T1 + (q >> 5) * LDT + (q & 31) * 4);
+        const int r = q >> 5, c4 = (q & 31) * 4;
+        float4 *t = reinterpret_cast<float4 *>(T + r * LDT + c4);
         float4 v = *t;
+        if (save_p && m0 + r < M) *reinterpret_cast<float4 *>(save_p + (m0 + r) * MATRIS_D + c4) = v;
         v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
         *t = v;
     }
     __syncthreads();
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, W2, wave, MATRIS_D / 16, 0, lane);
-    acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2, wave, MATRIS_D / 16, 0, lane);
+    __syncthreads();  // every wave is done reading h
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
-    store_tile128(T0, out, MATRIS_D, m0, M, tid, res, res_w);
+    store_tile128(T, out, MATRIS_D, m0, M, tid, res, res_w);
 }
 
 // FFN backward: g_x = ((g W2) * SiLU'(p)) W1, with w1t = W1^T, w2t = W2^T row-major.
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
+__global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
                                                          const float *__restrict__ P, const uint4 *__restrict__ W1t,
                                                          const uint4 *__restrict__ W2t, float *__restrict__ g_x,
                                                          float *__restrict__ g_res, const float *__restrict__ res_w) {
-    __shared__ __align__(16) float T0[BM * LDT];
-    __shared__ __align__(16) float T1[BM * LDT];
+    __shared__ __align__(16) float T[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
-    stage_tile128(T0, g, MATRIS_D, m0, M, tid);
+    stage_tile128(T, g, MATRIS_D, m0, M, tid);
     __syncthreads();
-    if (g_res) store_tile128_scaled(T0, g_res, res_w, m0, M, tid);
+    if (g_res) store_tile128_scaled(T, g_res, res_w, m0, M, tid);
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
-    const int col = wave * 32 + l32;
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
+    // g_p = g_h * SiLU'(p): lane = row, 4 consecutive columns per register group
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < 2; ++rt) {
+        const int64_t row = m0 + rt * 32 + l32;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int row = rt * 32 + acc_row(i, h);
-            const float p = (m0 + row < M) ? P[(m0 + row) * MATRIS_D + col] : 0.f;
-            acc[rt][0][i] *= dsilu_f(p);
+        for (int j = 0; j < 4; ++j) {
+            const int col = wave * 32 + 8 * j + 4 * h;
+            const float4 p = row < M ? *reinterpret_cast<const float4 *>(P + row * MATRIS_D + col)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+            acc[rt][0][4 * j] *= dsilu_f(p.x);
+            acc[rt][0][4 * j + 1] *= dsilu_f(p.y);
+            acc[rt][0][4 * j + 2] *= dsilu_f(p.z);
+            acc[rt][0][4 * j + 3] *= dsilu_f(p.w);
         }
-    acc_to_lds<1>(acc, T1, LDT, wave * 32, lane);
+    }
+    __syncthreads();  // every wave is done reading g
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, W1t, wave, MATRIS_D / 16, 0, lane);
-    acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);  // every wave finished reading T0 before the g_h sync
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1t, wave, MATRIS_D / 16, 0, lane);
     __syncthreads();
-    store_tile128(T0, g_x, MATRIS_D, m0, M, tid);
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+    __syncthreads();
+    store_tile128(T, g_x, MATRIS_D, m0, M, tid);
 }
 
 // ------------------------------------------------------------------------------------
@@ -153,36 +167,37 @@ __global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float
     // wave w -> output columns [64w, 64w+64) of the 256: waves 0,1 -> out0, 2,3 -> out1
     v16f acc[2][2];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0, lane);
+    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0, lane);
     __syncthreads();  // T0 free
-    acc_to_lds<2>(acc, (wave < 2) ? T0 : T1, LDT, (wave & 1) * 64, lane);
+    acc_t_to_lds<2, 2>(acc, (wave < 2) ? T0 : T1, LDT, (wave & 1) * 64, lane);
     __syncthreads();
     store_tile128(T0, out0, MATRIS_D, m0, M, tid);
     store_tile128(T1, out1, MATRIS_D, m0, M, tid);
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
+__global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
                                                           const float *__restrict__ g1, const uint4 *__restrict__ Wt,
                                                           float *__restrict__ g_x, const float *__restrict__ res,
                                                           const float *__restrict__ res_w) {
     // Wt = W^T ([128, 256]) packed: g_x[m][k] = sum_n g[m][n] Wt[k][n], k-blocks 0..7
-    // pair with g0, 8..15 with g1
-    __shared__ __align__(16) float T0[BM * LDT];
-    __shared__ __align__(16) float T1[BM * LDT];
+    // pair with g0, 8..15 with g1; g0 then g1 pass through the one LDS tile
+    __shared__ __align__(16) float T[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
-    stage_tile128(T0, g0, MATRIS_D, m0, M, tid);
-    stage_tile128(T1, g1, MATRIS_D, m0, M, tid);
+    stage_tile128(T, g0, MATRIS_D, m0, M, tid);
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T0, LDT, Wt, wave, 256 / 16, 0, lane);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16>(acc, T1, LDT, Wt, wave, 256 / 16, MATRIS_D / 16, lane);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, 0, lane);
     __syncthreads();
-    acc_to_lds<1>(acc, T0, LDT, wave * 32, lane);
+    stage_tile128(T, g1, MATRIS_D, m0, M, tid);
     __syncthreads();
-    store_tile128(T0, g_x, MATRIS_D, m0, M, tid, res, res_w);
+    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, MATRIS_D / 16, lane);
+    __syncthreads();
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+    __syncthreads();
+    store_tile128(T, g_x, MATRIS_D, m0, M, tid, res, res_w);
 }
 
 // ------------------------------------------------------------------------------------

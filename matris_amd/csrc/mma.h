@@ -242,19 +242,19 @@ __device__ __forceinline__ void acc_to_lds_rc(const v16f (&acc)[NRT][NCT], float
     }
 }
 
-// Transposed accumulators (rows in lanes, see gemm_lds_packed<..., TRANS>) plus a per-column
-// bias into a row-major fp32 LDS tile: row rt*32 + lane%32, columns col0 + ct*32 + 8j + 4h
+// Transposed accumulators (rows in lanes, see gemm_lds_packed<..., TRANS>) plus an optional
+// per-column bias into a row-major fp32 LDS tile: row rt*32 + lane%32, columns col0 + ct*32 + 8j + 4h
 // .. +3 as one 16-byte write each.
 template <int NRT, int NCT>
 __device__ __forceinline__ void acc_t_to_lds(const v16f (&acc)[NRT][NCT], float *tile, int ld, int col0, int lane,
-                                             const float *__restrict__ bias) {
+                                             const float *__restrict__ bias = nullptr) {
     const int h = lane >> 5, l32 = lane & 31;
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int col = col0 + ct * 32 + 8 * j + 4 * h;
-            const float4 b = *reinterpret_cast<const float4 *>(bias + col);
+            const float4 b = bias ? *reinterpret_cast<const float4 *>(bias + col) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt)
                 *reinterpret_cast<float4 *>(tile + (rt * 32 + l32) * ld + col) =
