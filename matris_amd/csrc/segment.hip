@@ -161,10 +161,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(int64_t n_seg, const floa
                                                        const int32_t *__restrict__ s_perm, float *__restrict__ y_t,
                                                        float *__restrict__ y_s, float *__restrict__ lse_t,
                                                        float *__restrict__ lse_s) {
+    // wave w -> segment w / 2, side w % 2: the two sides of nearby segments run together,
+    // so the source side's second read of e' rows tends to find them still in cache
     int64_t w = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (w >= 2 * n_seg) return;
-    const bool src_side = w >= n_seg;
-    const int64_t seg = src_side ? w - n_seg : w;
+    const bool src_side = w & 1;
+    const int64_t seg = w >> 1;
     const int32_t *ptr = src_side ? s_ptr : t_ptr;
     const int32_t *perm = src_side ? s_perm : t_perm;
     const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
