@@ -59,6 +59,9 @@ def radius_graph_device(frac: torch.Tensor, lattice: np.ndarray, cutoff: float, 
     (center, neighbor, image int32 [E,3], dist fp64, row_ptr int64 [n+1], row_count int32)."""
     lib = _lib.load()
     dev = frac.device
+    if frac.dtype != torch.float64 or frac.dim() != 2 or frac.shape[1] != 3:
+        raise ValueError(f"frac must be fp64 [n, 3], got {frac.dtype} {tuple(frac.shape)}")
+    frac = frac.contiguous()
     n = frac.shape[0]
     lat = np.ascontiguousarray(lattice, dtype=np.float64)
     grid = (ctypes.c_int * 3)()
@@ -157,7 +160,10 @@ class GraphConverter(nn.Module):
         dev = self._device()
         n = len(z)
         lat = np.asarray(lattice, dtype=np.float64)
-        f64 = frac_device if frac_device is not None else torch.as_tensor(np.asarray(frac, np.float64), device=dev)
+        # the kernels read [n, 3] row-major: make any strided input (a transposed or
+        # Fortran-ordered array, a column slice) contiguous first
+        f64 = (frac_device if frac_device is not None else
+               torch.as_tensor(np.ascontiguousarray(frac, dtype=np.float64), device=dev)).contiguous()
         center, neighbor, image, dist, row_ptr, row_count = radius_graph_device(f64, lat, self.atom_graph_cutoff)
         # converter.py:108-113: isolated atoms stop the calculation
         n_isolated = int((row_count == 0).sum().item())

@@ -106,3 +106,22 @@ def test_c5_full_size_properties():
         d -= L * np.round(d / L)
         r = np.sqrt((d * d).sum(1))
         assert cnt[i] == int(((r <= 6.0) & (r > 1e-8)).sum()), i
+
+
+def test_strided_fractional_input_gives_the_same_graph():
+    """Regression: fractional coordinates handed over as a transposed (Fortran-ordered)
+    array or a strided device tensor build the same graph, bit for bit, as C-ordered
+    ones (the kernels read [n, 3] row-major)."""
+    import torch
+
+    from matris_amd.graph.converter import GraphConverter
+    cr = W.fcc_supercell(3.61, 2, sigma=0.05, seed=5)
+    gc = GraphConverter(6.0, 4.0)
+    ref = gc.from_arrays(cr.frac, cr.lattice, cr.z)
+    f_order = np.asfortranarray(cr.frac)
+    assert not f_order.flags.c_contiguous
+    wide = torch.zeros(len(cr.z), 6, dtype=torch.float64, device="cuda")
+    wide[:, ::2] = torch.as_tensor(cr.frac, device="cuda")
+    for g in (gc.from_arrays(f_order, cr.lattice, cr.z), gc.from_arrays(None, cr.lattice, cr.z, frac_device=wide[:, ::2])):
+        for name in ("atom_graph", "neighbor_image", "directed2undirected", "undirected2directed", "line_graph"):
+            assert torch.equal(getattr(g, name), getattr(ref, name)), name
