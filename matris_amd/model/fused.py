@@ -227,3 +227,162 @@ def line_attention(layer, bond, tb, lg, recompute: bool = False):
 def line_refinement(layer, tb, atom, bond, env, lg, recompute: bool = False):
     """(bond', tb') of Refinement.forward on the line graph; env = learnable_envelope(smooth_weight)."""
     return _LineRefinement.apply(tb, atom, bond, env, layer, lg, recompute)
+
+
+# ------------------------------------------------------------------------------------
+# atom-graph layers (directed edges E_d, undirected bonds E_u via d2u, atoms N)
+# ------------------------------------------------------------------------------------
+def atom_attention_fusable(layer) -> bool:
+    return line_attention_fusable(layer)
+
+
+def atom_refinement_fusable(layer) -> bool:
+    return (layer.graph_type == "atom graph" and layer.edge_nonlinear_update._fusable()
+            and _ffn_fusable(layer.node_FFN) and _ffn_fusable(layer.edge_FFN)
+            and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
+
+
+def _atom_packs(layer):
+    pe = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+    pn = layer.node_nonlinear_update._pack.get(layer.node_nonlinear_update)
+    pp = layer._proj.get(layer.source_weight_linear.weight, layer.target_weight_linear.weight)
+    return pe, pn, pp
+
+
+class _AtomAttention(torch.autograd.Function):
+    """Graph_Attention_Layer on the atom graph (interaction_block.py:87-143 with
+    is_atom_graph, called :416-422):
+        e      = GatedMLP_e([bond[d2u], atom[tgt], atom[src]])            [E_d]
+        y_t, y_s = attention(W_t bond[d2u], W_s bond[d2u], e; tgt, src)  [N]
+        n      = GatedMLP_n([atom, y_t, y_s])                            [N]
+        atom'  = n + r_n * atom,  bond' = mean_{d2u}(e) + r_e * bond     [E_u]
+    The attention logits are computed once per undirected bond and read through d2u."""
+
+    @staticmethod
+    def forward(ctx, atom, bond, layer, ag, d2u):
+        ops._check_dev(atom, bond)
+        atom, bond = ops._f32c(atom), ops._f32c(bond)
+        mode = ops._MMA["mode"]
+        tgt, src = ag["grp_tgt"], ag["grp_src"]
+        Ed, N = d2u.key.numel(), atom.shape[0]
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        pe, pn, pp = _atom_packs(layer)
+        e, p_e, z_e, _ = ops.gmlp_fwd_raw(pe, [bond, atom, atom], [d2u.key, tgt.key, src.key], Ed, mode)
+        a_s, a_t = ops.pair_fwd_raw(pp, bond, mode)
+        y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, d2u)
+        _, p_n, z_n, atom_new = ops.gmlp_fwd_raw(pn, [atom, y_t, y_s], [None, None, None], N, mode, res=(atom, r_n))
+        bond_new = bond * r_e
+        ops.seg_sum_raw(e, d2u, 0.5, out=bond_new, accumulate=True)  # mean of the two directed copies
+        ctx.save_for_backward(p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n)
+        ctx.mode, ctx.layer, ctx.ag, ctx.d2u = mode, layer, ag, d2u
+        return atom_new, bond_new
+
+    @staticmethod
+    def backward(ctx, g_atom_new, g_bond_new):
+        layer, ag, d2u, mode = ctx.layer, ctx.ag, ctx.d2u, ctx.mode
+        p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n = ctx.saved_tensors
+        tgt, src = ag["grp_tgt"], ag["grp_src"]
+        pe, pn, pp = _atom_packs(layer)
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        N = p_n.shape[0]
+        g_atom_new = _zeros_if_none(g_atom_new, y_t)
+        g_bond_new = _zeros_if_none(g_bond_new, a_s)
+        # node update: g_atom = r_n g + d GatedMLP_n / d atom; g_y = [g_yt | g_ys]
+        g_atom = torch.empty(N, D, device=e.device)
+        g_y = ops.gmlp_bwd_raw(pn, g_atom_new, p_n, z_n, 3 * D, mode, g_x0=g_atom, acc0=False, res_w=r_n)
+        del p_n, z_n
+        # e: half of the bond gradient of each directed copy, plus the attention term
+        g_e_base = ops.gather_raw(g_bond_new, d2u.key, 0.5)
+        g_at, g_as, g_e = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, d2u,
+                                           ldgy=2 * D, g_e_base=g_e_base)
+        del g_e_base, g_y, a_t, a_s, e
+        # logits were read through d2u: reduce to bonds, then the projections + residual
+        g_bond = ops.pair_bwd_raw(pp, ops.seg_sum_raw(g_as, d2u), ops.seg_sum_raw(g_at, d2u), mode,
+                                  res=g_bond_new, res_w=r_e)
+        del g_at, g_as
+        # edge update: sources bond[d2u], atom[tgt], atom[src]
+        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode)
+        del g_e, p_e, z_e
+        ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, out=g_bond, accumulate=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True)
+        ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_atom, accumulate=True)
+        return g_atom, g_bond, None, None, None
+
+
+class _AtomRefinement(torch.autograd.Function):
+    """Refinement on the atom graph (interaction_block.py:218-278 with is_atom_graph,
+    called :437-446):
+        w     = env[d2u]                                                  [E_d]
+        h     = GatedMLP([bond[d2u], atom[tgt], atom[src]])               [E_d]
+        atom' = node_FFN(sum_tgt h * w) + r_n * atom
+        bond' = mean_{d2u} edge_FFN(h or h * w) + r_e * bond
+    env = learnable_envelope(smooth_weight) [E_u]."""
+
+    @staticmethod
+    def forward(ctx, atom, bond, env, layer, ag, d2u):
+        ops._check_dev(atom, bond, env)
+        atom, bond, env = ops._f32c(atom), ops._f32c(bond), ops._f32c(env)
+        mode = ops._MMA["mode"]
+        tgt, src = ag["grp_tgt"], ag["grp_src"]
+        Ed = d2u.key.numel()
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        ph = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+        L, Mm = layer.node_FFN.layers, layer.edge_FFN.layers
+        pn = layer._node_ffn.get(L[0].weight, L[3].weight)
+        pm = layer._edge_ffn.get(Mm[0].weight, Mm[3].weight)
+        w = ops.gather_raw(env, d2u.key)
+        h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [bond, atom, atom], [d2u.key, tgt.key, src.key], Ed, mode)
+        hw = h * w
+        agg = ops.seg_sum_raw(hw, tgt)
+        atom_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(atom, r_n))
+        smoothed = bool(layer.use_smoothed_for_delta_edge)
+        de, p_de = ops.ffn_fwd_raw(pm, hw if smoothed else h, mode)
+        del hw, agg
+        bond_new = bond * r_e
+        ops.seg_sum_raw(de, d2u, 0.5, out=bond_new, accumulate=True)
+        ctx.save_for_backward(w, h, p_h, z_h, p_dn, p_de)
+        ctx.mode, ctx.layer, ctx.ag, ctx.d2u, ctx.smoothed = mode, layer, ag, d2u, smoothed
+        return atom_new, bond_new
+
+    @staticmethod
+    def backward(ctx, g_atom_new, g_bond_new):
+        layer, ag, d2u, mode = ctx.layer, ctx.ag, ctx.d2u, ctx.mode
+        w, h, p_h, z_h, p_dn, p_de = ctx.saved_tensors
+        tgt, src = ag["grp_tgt"], ag["grp_src"]
+        ph = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
+        L, Mm = layer.node_FFN.layers, layer.edge_FFN.layers
+        pn = layer._node_ffn.get(L[0].weight, L[3].weight)
+        pm = layer._edge_ffn.get(Mm[0].weight, Mm[3].weight)
+        r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
+        N = p_dn.shape[0]
+        g_atom_new = _zeros_if_none(g_atom_new, p_dn)
+        g_bond_new = _zeros_if_none(g_bond_new, torch.empty(d2u.n_seg, D, device=h.device))
+        g_atom = torch.empty(N, D, device=h.device)
+        g_agg = ops.ffn_bwd_raw(pn, g_atom_new, p_dn, mode, g_res=g_atom, res_w=r_n)
+        g_te = ops.ffn_bwd_raw(pm, ops.gather_raw(g_bond_new, d2u.key, 0.5), p_de, mode)
+        del p_dn, p_de
+        g_hw = ops.gather_raw(g_agg, tgt.key)
+        if ctx.smoothed:
+            g_hw += g_te
+            g_h = g_hw * w
+        else:
+            g_h = torch.addcmul(g_te, g_hw, w)
+        g_env = ops.seg_sum_raw(g_hw * h, d2u)
+        del g_hw, g_te, h, w
+        g_bond = g_bond_new * r_e
+        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode)
+        del g_h, p_h, z_h
+        ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, out=g_bond, accumulate=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True)
+        ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_atom, accumulate=True)
+        return g_atom, g_bond, g_env, None, None, None
+
+
+def atom_attention(layer, atom, bond, ag, d2u):
+    """(atom', bond') of Graph_Attention_Layer.forward on the atom graph."""
+    return _AtomAttention.apply(atom, bond, layer, ag, d2u)
+
+
+def atom_refinement(layer, atom, bond, env, ag, d2u):
+    """(atom', bond') of Refinement.forward on the atom graph; env = learnable_envelope(smooth_weight)."""
+    return _AtomRefinement.apply(atom, bond, env, layer, ag, d2u)

@@ -376,6 +376,8 @@ class Graph_Attention_Layer(nn.Module):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
         if d2u is None and fused.line_attention_fusable(self):  # one node, explicit backward
             return fused.line_attention(self, node_feat, edge_feat, graph, recompute)
+        if d2u is not None and fused.atom_attention_fusable(self):
+            return fused.atom_attention(self, node_feat, edge_feat, graph, d2u)
         if d2u is None:  # line graph: edges are the angles themselves
             e = self.edge_nonlinear_update.fused([(edge_feat, None), (node_feat, tgt), (node_feat, src)])
             a_s, a_t = self._projections(edge_feat)
@@ -424,6 +426,9 @@ class Refinement(nn.Module):
     def forward(self, node_feat, edge_feat, smooth_weight, graph, d2u: ops.Grouping | None = None, atom_feat=None,
                 recompute: bool = False):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
+        if self.graph_type == "atom graph" and fused.atom_refinement_fusable(self):  # one node, explicit backward
+            return fused.atom_refinement(self, node_feat, edge_feat, self.learnable_envelope(smooth_weight), graph,
+                                         d2u)
         if self.graph_type == "atom graph":
             w = ops.gather(self.learnable_envelope(smooth_weight), d2u)
             h = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])

@@ -143,3 +143,80 @@ def test_line_layers_unused_output_gradient():
     bn, _ = fused.line_refinement(layer, *xs, env, lg)
     bn.sum().backward()
     assert all(torch.isfinite(x.grad).all() for x in xs) and torch.isfinite(env.grad).all()
+
+
+def _atom_graph(N, E_u, seed):
+    """A random directed atom graph: every bond u appears twice (d2u), with sorted targets."""
+    from matris_amd.model import ops
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randint(0, N, (E_u,), generator=g)
+    b = (a + torch.randint(1, N, (E_u,), generator=g)) % N
+    tgt = torch.cat([a, b])
+    src = torch.cat([b, a])
+    d2u = torch.cat([torch.arange(E_u), torch.arange(E_u)])
+    order = torch.sort(tgt, stable=True)[1]
+    tgt, src, d2u = tgt[order], src[order], d2u[order]
+    ag = {"grp_tgt": ops.Grouping.build(tgt.to(torch.int32).to(DEV), N, sorted_rows=True),
+          "grp_src": ops.Grouping.build(src.to(torch.int32).to(DEV), N)}
+    gd2u = ops.Grouping.build(d2u.to(torch.int32).to(DEV), E_u)
+    return ag, gd2u, tgt, src, d2u
+
+
+@pytest.mark.parametrize("N,E_u", [(60, 700), (7, 9)])
+def test_atom_attention_vs_fp64(N, E_u):
+    from matris_amd.model import fused
+    from matris_amd.model.model import Graph_Attention_Layer
+    torch.manual_seed(N)
+    layer = Graph_Attention_Layer(128, 128, 128, norm_type="rms")
+    _randomize(layer, N + 5)
+    ag, gd2u, tgt, src, d2u = _atom_graph(N, E_u, N + 6)
+    atom, bond = torch.randn(N, 128), torch.randn(E_u, 128)
+    g_a, g_b = torch.randn(N, 128), torch.randn(E_u, 128)
+    a64, b64 = atom.double().requires_grad_(True), bond.double().requires_grad_(True)
+    e = _gmlp64(layer.edge_nonlinear_update, torch.cat([b64[d2u], a64[tgt], a64[src]], 1))
+    a_s = b64 @ layer.source_weight_linear.weight.double().t()
+    a_t = b64 @ layer.target_weight_linear.weight.double().t()
+    y_t, y_s = _softmax_sum(a_t[d2u], e, tgt, N), _softmax_sum(a_s[d2u], e, src, N)
+    n = _gmlp64(layer.node_nonlinear_update, torch.cat([a64, y_t, y_s], 1))
+    an_r = n + layer.node_res_weight.double() * a64
+    bn_r = 0.5 * torch.zeros(E_u, 128, dtype=torch.float64).index_add(0, d2u, e) + layer.edge_res_weight.double() * b64
+    ((an_r * g_a.double()).sum() + (bn_r * g_b.double()).sum()).backward()
+    layer = layer.to(DEV)
+    assert fused.atom_attention_fusable(layer)
+    ad, bd = atom.to(DEV).requires_grad_(True), bond.to(DEV).requires_grad_(True)
+    an, bn = fused.atom_attention(layer, ad, bd, ag, gd2u)
+    assert _rel(an, an_r) < 1e-5 and _rel(bn, bn_r) < 1e-5
+    torch.autograd.backward([an, bn], [g_a.to(DEV), g_b.to(DEV)])
+    assert _rel(ad.grad, a64.grad) < 1e-5
+    assert _rel(bd.grad, b64.grad) < 1e-5
+
+
+@pytest.mark.parametrize("smoothed", [False, True])
+def test_atom_refinement_vs_fp64(smoothed):
+    from matris_amd.model import fused
+    from matris_amd.model.model import Refinement
+    N, E_u = 50, 600
+    torch.manual_seed(E_u)
+    layer = Refinement(128, 128, 128, 7, norm_type="rms", graph_type="atom graph",
+                       use_smoothed_for_delta_edge=smoothed)
+    _randomize(layer, 3)
+    ag, gd2u, tgt, src, d2u = _atom_graph(N, E_u, 4)
+    atom, bond, env = torch.randn(N, 128), torch.randn(E_u, 128), torch.rand(E_u, 128) + 0.1
+    g_a, g_b = torch.randn(N, 128), torch.randn(E_u, 128)
+    leaves = [x.double().requires_grad_(True) for x in (atom, bond, env)]
+    a64, b64, env64 = leaves
+    h = _gmlp64(layer.edge_nonlinear_update, torch.cat([b64[d2u], a64[tgt], a64[src]], 1))
+    hw = h * env64[d2u]
+    agg = torch.zeros(N, 128, dtype=torch.float64).index_add(0, tgt, hw)
+    an_r = _ffn64(layer.node_FFN, agg) + layer.node_res_weight.double() * a64
+    de = _ffn64(layer.edge_FFN, hw if smoothed else h)
+    bn_r = 0.5 * torch.zeros(E_u, 128, dtype=torch.float64).index_add(0, d2u, de) + layer.edge_res_weight.double() * b64
+    ((an_r * g_a.double()).sum() + (bn_r * g_b.double()).sum()).backward()
+    layer = layer.to(DEV)
+    assert fused.atom_refinement_fusable(layer)
+    dev_leaves = [x.to(DEV).requires_grad_(True) for x in (atom, bond, env)]
+    an, bn = fused.atom_refinement(layer, *dev_leaves, ag, gd2u)
+    assert _rel(an, an_r) < 1e-5 and _rel(bn, bn_r) < 1e-5
+    torch.autograd.backward([an, bn], [g_a.to(DEV), g_b.to(DEV)])
+    for d, r in zip(dev_leaves, leaves):
+        assert _rel(d.grad, r.grad) < 1e-5
