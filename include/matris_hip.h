@@ -115,6 +115,14 @@ int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *
 int matris_gather_rows(const float *src, const int32_t *idx, int64_t n_rows, float scale, int accumulate,
                        float *out, void *stream);
 
+/* Backward of the edge vectors vec[e] = cart[tgt[e]] - (cart[src[e]] + shift[e])
+ * (row P1, matris/model/processgraph.py:192-199): g_cart [n_atoms, 3] fp32 =
+ * sum over the atom's target rows of g_vec [E, 3] minus the sum over its source rows,
+ * through the CSR groupings of tgt and src (perm NULL = identity).  Deterministic;
+ * replaces the sort-based backward of the two index_select gathers. */
+int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const int32_t *t_ptr, const int32_t *t_perm,
+                        const int32_t *s_ptr, const int32_t *s_perm, float *g_cart, void *stream);
+
 /* ------------------------------------------------------------------------------------
  * Segment attention (rows M2 + M4 / M5): Dimwise_softmax by target and by source,
  * alpha * e' and both segment sums, fused.  Replaces interaction_block.py:113-134 with

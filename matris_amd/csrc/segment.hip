@@ -111,6 +111,54 @@ extern "C" int matris_gather_rows(const float *src, const int32_t *idx, int64_t 
 }
 
 // ------------------------------------------------------------------------------------
+// edge-vector backward: vec[e] = cart[tgt[e]] - cart[src[e]] - shift[e]  =>
+//   g_cart[i] = sum_{tgt[e]=i} g_vec[e] - sum_{src[e]=i} g_vec[e]
+// One wave per atom walks its target and source CSR rows (lanes stride the rows) and
+// reduces the three components across the wave: a fixed summation order.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void edge_vec_bwd_kernel(int64_t n, const float *__restrict__ g,
+                                                           const int32_t *__restrict__ t_ptr,
+                                                           const int32_t *__restrict__ t_perm,
+                                                           const int32_t *__restrict__ s_ptr,
+                                                           const int32_t *__restrict__ s_perm,
+                                                           float *__restrict__ g_cart) {
+    const int64_t a = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if (a >= n) return;
+    const int lane = threadIdx.x & 63;
+    float x = 0.f, y = 0.f, z = 0.f;
+    for (int i = t_ptr[a] + lane; i < t_ptr[a + 1]; i += 64) {
+        const int64_t r = t_perm ? t_perm[i] : i;
+        x += g[3 * r];
+        y += g[3 * r + 1];
+        z += g[3 * r + 2];
+    }
+    for (int i = s_ptr[a] + lane; i < s_ptr[a + 1]; i += 64) {
+        const int64_t r = s_perm ? s_perm[i] : i;
+        x -= g[3 * r];
+        y -= g[3 * r + 1];
+        z -= g[3 * r + 2];
+    }
+    x = wave_sum(x);
+    y = wave_sum(y);
+    z = wave_sum(z);
+    if (lane == 0) {
+        g_cart[3 * a] = x;
+        g_cart[3 * a + 1] = y;
+        g_cart[3 * a + 2] = z;
+    }
+}
+
+extern "C" int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const int32_t *t_ptr, const int32_t *t_perm,
+                                   const int32_t *s_ptr, const int32_t *s_perm, float *g_cart, void *stream) {
+    if (n_atoms < 0 || !t_ptr || !s_ptr || !g_cart) return MATRIS_E_ARG;
+    if (n_atoms == 0) return 0;
+    edge_vec_bwd_kernel<<<matris_blocks(n_atoms, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        n_atoms, g_vec, t_ptr, t_perm, s_ptr, s_perm, g_cart);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
 // segment attention forward: one wave per (segment, side).  Each half-wave owns every
 // other row of the segment with 16-byte lanes (4 columns) and runs an online softmax
 // taken four of its rows at a time: the running maximum moves once per chunk (one

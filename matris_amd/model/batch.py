@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import torch
 
+from . import ops
 from .ops import Grouping
 
 
@@ -66,7 +67,10 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     if compute_stress:
         strains = torch.zeros((G, 3, 3), dtype=dtype, device=device, requires_grad=True)
         sym = 0.5 * (strains + strains.transpose(-1, -2))
-        cart = cart + torch.bmm(cart.unsqueeze(1), sym[atom_segment]).squeeze(1)
+        if G == 1:  # one graph: the per-atom strain is a broadcast, not a gather
+            cart = cart + cart @ sym[0]
+        else:
+            cart = cart + torch.bmm(cart.unsqueeze(1), sym[atom_segment]).squeeze(1)
         lat3 = lat3 + torch.matmul(lat3, sym)
         lattice = lat3.reshape(-1, 3)
 
@@ -76,7 +80,9 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     else:
         edge_graph = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_dir, device=device))
         shift = torch.bmm(image.unsqueeze(1), lat3[edge_graph]).squeeze(1)
-    vec = cart[tgt] - (cart[src] + shift)
+    grp_tgt = Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32))
+    grp_src = Grouping.build(src32, N)
+    vec = ops.edge_vectors(cart, shift, grp_tgt, grp_src)
     length = torch.norm(vec, dim=1)
     unit = vec / length[:, None]
 
@@ -88,8 +94,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     out["grp_d2u"] = Grouping.build(d2u32, U, sorted_rows=False)
     out["atom_graph_dict"] = dict(
         atom_graph=atom_graph, target_index=tgt, source_index=src,
-        grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32)),
-        grp_src=Grouping.build(src32, N))
+        grp_tgt=grp_tgt, grp_src=grp_src)
     lgd: dict = {}
     if A:
         lg = torch.cat(lgs, 0)

@@ -134,6 +134,33 @@ def gather_raw(src: torch.Tensor, idx: torch.Tensor, scale: float = 1.0) -> torc
     return out
 
 
+class _EdgeVec(torch.autograd.Function):
+    """vec = cart[tgt] - (cart[src] + shift) with a deterministic CSR backward for cart."""
+
+    @staticmethod
+    def forward(ctx, cart, shift, tgt: "Grouping", src: "Grouping"):
+        _check_dev(cart, shift)
+        ctx.tgt, ctx.src, ctx.n = tgt, src, cart.shape[0]
+        return cart.index_select(0, tgt.key) - (cart.index_select(0, src.key) + shift)
+
+    @staticmethod
+    def backward(ctx, g):
+        g = g.float().contiguous()
+        lib = _lib.load()
+        g_cart = torch.empty(ctx.n, 3, dtype=torch.float32, device=g.device)
+        t, s = ctx.tgt, ctx.src
+        with _timed("edge_vec_bwd", (ctx.n,)):
+            _lib.check(lib.matris_edge_vec_bwd(ctx.n, _p(g), _p(t.rowptr), _p(t.perm), _p(s.rowptr), _p(s.perm),
+                                               _p(g_cart), _stream()), "matris_edge_vec_bwd")
+        return g_cart, -g, None, None
+
+
+def edge_vectors(cart, shift, tgt: "Grouping", src: "Grouping"):
+    """cart[tgt] - (cart[src] + shift) (processgraph.py:192-199) for fp32 cart [N,3] and
+    shift [E,3]; tgt / src are the atom graph's CSR groupings."""
+    return _EdgeVec.apply(cart, shift, tgt, src)
+
+
 class _SegSum(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, grp: Grouping, scale: float):

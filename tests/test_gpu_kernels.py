@@ -253,3 +253,25 @@ def test_proj_pair_fwd_bwd(M, mode, tol):
         assert _rel(xd.grad, (g0.double() @ ws.double())) < tol
     finally:
         ops.set_mma_precision("bf16x6")
+
+
+@pytest.mark.parametrize("N,E", [(864, 67396), (5, 7), (1, 0)])
+def test_edge_vectors_backward_vs_fp64(N, E):
+    """matris_edge_vec_bwd: g_cart = sum over target rows - sum over source rows (the
+    backward of cart[tgt] - (cart[src] + shift)), against fp64 autograd."""
+    from matris_amd.model import ops
+    g = torch.Generator().manual_seed(N + E)
+    tgt = torch.sort(torch.randint(0, N, (E,), generator=g))[0]
+    src = torch.randint(0, N, (E,), generator=g)
+    cart, shift, gv = torch.randn(N, 3, generator=g), torch.randn(E, 3, generator=g), torch.randn(E, 3, generator=g)
+    c64, s64 = cart.double().requires_grad_(True), shift.double().requires_grad_(True)
+    ref = c64[tgt] - (c64[src] + s64)
+    (ref * gv.double()).sum().backward()
+    gt = ops.Grouping.build(tgt.to(torch.int32).to("cuda"), N, sorted_rows=True)
+    gs = ops.Grouping.build(src.to(torch.int32).to("cuda"), N)
+    cd, sd = cart.to("cuda").requires_grad_(True), shift.to("cuda").requires_grad_(True)
+    out = ops.edge_vectors(cd, sd, gt, gs)
+    assert torch.allclose(out.double().cpu(), ref.detach(), atol=1e-6)
+    out.backward(gv.to("cuda"))
+    assert torch.allclose(cd.grad.double().cpu(), c64.grad, atol=1e-4, rtol=1e-5)
+    assert torch.equal(sd.grad.cpu(), -gv)
