@@ -32,9 +32,20 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
-# The gated-MLP kernels compute fp32 products as 6 bf16 MFMA products (mma.h, MODE 6), so
-# their ceiling in fp32-product terms is the dense bf16 peak / 6.
-SPLIT6_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 6
+F16_MFMA_PEAK_TFLOPS = 2500.0
+# The GEMM kernels compute each fp32 product as several 16-bit MFMA products (mma.h), so
+# their ceiling in fp32-product terms is the dense 16-bit peak divided by that count.
+# mode name -> (kernel template index, peak TFLOP/s in fp32 products, peak note, dtype)
+MMA_ROOF = {
+    "f16x3": (2, F16_MFMA_PEAK_TFLOPS / 3, "dense fp16 2500 TFLOP/s / 3 fp16 products per fp32 product",
+              "fp32 (GEMMs: fp32 products as 3 fp16 MFMA products of an fp16 hi/lo split with a power-of-two "
+              "weight scale, fp32 accumulate)"),
+    "bf16x6": (6, BF16_MFMA_PEAK_TFLOPS / 6, "dense bf16 2500 TFLOP/s / 6 bf16 products per fp32 product",
+               "fp32 (GEMMs: fp32 products as 6 bf16 MFMA products of an exact 3-way bf16 split, fp32 accumulate)"),
+    "fp32": (0, FP32_MFMA_PEAK_TFLOPS, "dense fp32 MFMA 157.3 TFLOP/s", "fp32 (GEMMs: fp32 MFMA)"),
+    "bf16x3": (3, BF16_MFMA_PEAK_TFLOPS / 3, "dense bf16 2500 TFLOP/s / 3 bf16 products per fp32 product",
+               "fp32 in, ~2^-16 products (GEMMs: 2-way bf16 split, 3 MFMA products)"),
+}
 D = 128
 
 
@@ -278,6 +289,8 @@ def main():
     e2e = n_atoms * e2e_steps / (time.perf_counter() - t1)
 
     # rooflines: the dominant (MFMA-bound) kernel family and the line attention (HBM-bound)
+    mode_idx, mma_peak, peak_note, dtype = MMA_ROOF[ops.get_mma_precision()]
+
     def gmlp_roof(name):
         gm = stats.get(name)
         if not gm:
@@ -285,13 +298,12 @@ def main():
         flops = sum(_gmlp_flops(m, k) for m, k in gm["info"]) / gm["n"]
         tf = flops / gm["mean_s"] / 1e12
         n_line = sum(1 for (m, k) in gm["info"] if m == A)
-        return dict(kernel=f"{name}_kernel<6>", bound="mfma", achieved=round(tf, 2), peak=round(SPLIT6_PEAK_TFLOPS, 1),
-                    unit="TFLOP/s", frac=round(tf / SPLIT6_PEAK_TFLOPS, 4), traffic=None,
+        return dict(kernel=f"{name}_kernel<{mode_idx}>", bound="mfma", achieved=round(tf, 2), peak=round(mma_peak, 1),
+                    unit="TFLOP/s", frac=round(tf / mma_peak, 4), traffic=None,
                     flops_per_launch=round(flops), mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
                     frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
                     note=f"algorithmic fp32 FLOPs (2*M*(256K+32768)) per launch, mean over {gm['n']} launches in "
-                         f"{args.steps} steps ({n_line} with M=A={A}); peak = dense bf16 {BF16_MFMA_PEAK_TFLOPS:.0f} "
-                         f"TFLOP/s / 6 bf16 products per fp32 product")
+                         f"{args.steps} steps ({n_line} with M=A={A}); peak = {peak_note}")
     r_f, r_b = gmlp_roof("gmlp_fwd"), gmlp_roof("gmlp_bwd")
     tot = {k: v["mean_s"] * v["n"] for k, v in stats.items()}
     roof = r_b if tot.get("gmlp_bwd", 0) >= tot.get("gmlp_fwd", 0) else r_f
@@ -317,7 +329,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 (GEMMs: fp32 products as 6 bf16 MFMA products of an exact 3-way bf16 split, fp32 accumulate)",
+        "dtype": dtype,
         "data": "synthetic (fcc Cu 6x6x6, sigma=0.05 A seed 2; random-init weights seed 0)",
         "config": {"workload": "C3: fcc Cu 6x6x6 conventional (864 atoms), efsm, MatRIS-10M (num_layers=10)",
                    "n_atoms": n_atoms, "n_directed": int(g.atom_graph.shape[0]), "n_undirected": E_u,

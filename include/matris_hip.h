@@ -195,19 +195,31 @@ int matris_sbf_bwd(int64_t n_edges, const float *unit, const int32_t *de_t, cons
  *   MATRIS_MMA_FP32   v_mfma_f32_32x32x2f32 on the fp32 operands;
  *   MATRIS_MMA_BF16X6 operands split exactly into three bf16 parts, six partial
  *                     products on v_mfma_f32_32x32x16_bf16 (fp32-grade accuracy);
- *   MATRIS_MMA_BF16X3 two bf16 parts, three partial products (~2^-16 per product).
+ *   MATRIS_MMA_BF16X3 two bf16 parts, three partial products (~2^-16 per product);
+ *   MATRIS_MMA_F16X3  activations split into fp16 hi + 2^-11 lo, weights scaled by a
+ *                     power of two and split into two fp16 parts, three partial products
+ *                     on v_mfma_f32_32x32x16_f16 (~2^-22 per product, fp32-grade).  fp16
+ *                     bounds the activations: a kernel that meets |x| >= 65504 in an
+ *                     operand it splits sets the device's range flag (its results are
+ *                     then unusable); matris_f16_range_take reads and clears the flag.
  * Every weight operand ("...p" arguments) is passed pre-packed by matris_pack_b in the
  * SAME mode as the call that reads it: a [n, k] row-major fp32 matrix whose rows are the
  * GEMM's output columns (an nn.Linear weight, or the transpose of one for a backward)
  * becomes fragment-major planes of matris_pack_b_bytes(n, k, mode) bytes (n % 32 == 0,
- * k % 16 == 0; 4 bytes per element in modes 0 and 3, 6 in mode 6).  No counterpart in
- * the reference: it replaces the per-call weight reads of the nn.Linear layers below.
+ * k % 16 == 0; 4 bytes per element in modes 0, 2 and 3, 6 in mode 6, plus a 16-byte
+ * scale header in mode 2).  No counterpart in the reference: it replaces the per-call
+ * weight reads of the nn.Linear layers below.
  * ------------------------------------------------------------------------------------ */
 #define MATRIS_MMA_FP32 0
+#define MATRIS_MMA_F16X3 2
 #define MATRIS_MMA_BF16X3 3
 #define MATRIS_MMA_BF16X6 6
 size_t matris_pack_b_bytes(int64_t n, int64_t k, int mode);
 int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, void *out, void *stream);
+/* *flagged = 1 if a MATRIS_MMA_F16X3 kernel on the current device met an activation
+ * outside the fp16 range since the last call, else 0; clears the flag.  Synchronizes
+ * `stream` (the kernels to check must have been launched on it or before it). */
+int matris_f16_range_take(int *flagged, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Fused gated MLP on MFMA (row M1).  Replaces GatedMLP.forward

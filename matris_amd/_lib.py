@@ -96,6 +96,7 @@ _SIGS = {
     "matris_sbf_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _I, _P, _P]),
     "matris_pack_b_bytes": (_SZ, [_I64, _I64, _I]),
     "matris_pack_b": (_I, [_I64, _I64, _P, _I, _P, _P]),
+    "matris_f16_range_take": (_I, [_P, _P]),
     "matris_ffn_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),

@@ -23,7 +23,31 @@
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
 // tiling, with packed transposed weights as B operands.
+//
+// This file also owns the device word that MODE 2 (fp16 split) kernels of every GEMM
+// file flag when an activation exceeds the fp16 range (matris_f16_range_take).
 #include "mma.h"
+
+// Set (to 1) by a MODE 2 kernel that met |x| >= 65504 in an operand it split; one copy
+// per device.
+static __device__ unsigned matris_f16_range_word;
+
+unsigned *matris_range_flag() {
+    static unsigned *ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(matris_f16_range_word)) != hipSuccess) return nullptr;
+        ptr[dev] = (unsigned *)p;
+    }
+    return ptr[dev];
+}
+
+__global__ void range_take_kernel(unsigned *flag, unsigned *out) {
+    out[0] = flag[0];
+    flag[0] = 0u;
+}
 
 struct GmlpSrc {
     const float *ptr[4];
@@ -57,7 +81,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                           float *__restrict__ save_z,
                                                           const float *__restrict__ res_src,
                                                           const float *__restrict__ res_w,
-                                                          float *__restrict__ res_out) {
+                                                          float *__restrict__ res_out, unsigned *range_flag) {
     constexpr int NPL = Npl<MODE>::v;
     constexpr int CHUNK = 2 * 2 * NPL * 64;  // uint4 per LDS chunk: [rt 2][kb 2][plane][lane]
     __shared__ __align__(16) float smem[BM * LDH];
@@ -67,6 +91,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const int KB = nsrc * (MATRIS_D / 16);  // k-blocks of W1
+    const float w1s = take_wscale<MODE>(W1), w2s = take_wscale<MODE>(W2);
+    float amax = 0.f;
     const int nchunk = nsrc * (MATRIS_D / 32);
 
     // gather assignment: thread -> (row xr, 8 columns at 8*xq) of each 32-wide chunk,
@@ -98,6 +124,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 #define GMLP_STOREX(buf)                                                                                 \
     do {                                                                                                 \
         Frag<MODE> f_;                                                                                   \
+        amax = frag_amax<MODE>(amax, x0, x1);                                                            \
         make_frag<MODE>(f_, x0, x1);                                                                     \
         _Pragma("unroll") for (int pl_ = 0; pl_ < NPL; ++pl_) Xp[(buf) * CHUNK + xslot + pl_ * 64] = f_.p[pl_]; \
     } while (0)
@@ -123,10 +150,12 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
                 for (int pl = 0; pl < NPL; ++pl) a[rt].p[pl] = xb[((rt * 2 + sub) * NPL + pl) * 64 + lane];
+            prep_w<MODE>(bcur[0]);
+            prep_w<MODE>(bcur[1]);
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) mma_frag<MODE>(acc[rt][ct], bcur[ct], a[rt]);  // P^T tiles
+                for (int ct = 0; ct < 2; ++ct) mma_wx<MODE>(acc[rt][ct], bcur[ct], a[rt]);  // P^T tiles
             bcur[0] = bnxt[0];
             bcur[1] = bnxt[1];
         }
@@ -138,6 +167,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 
     // p = acc + b1 -> LDS (rows in lanes: 16-byte writes); one pass copies p out with
     // 16-byte row stores and turns it into h = SiLU(p) in place
+    scale_acc<MODE>(acc, w1s);
     acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b1);
     __syncthreads();
 #pragma unroll
@@ -156,8 +186,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // block = w/2 (0 core, 1 gate)
     const int blk = wave >> 1;
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Ts + blk * MATRIS_D, LDH, W2, 2 * wave, MATRIS_D / 16, 0,
-                                                     lane);
+    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Ts + blk * MATRIS_D, LDH, W2, 2 * wave,
+                                                                        MATRIS_D / 16, 0, lane));
+    scale_acc<MODE>(acc, w2s);
     __syncthreads();  // every wave is done reading h
 
     // z = acc + b2 -> LDS (16-byte writes); then a row pass with 16 lanes per row: lane
@@ -218,6 +249,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             }
         }
     }
+    report_range<MODE>(amax, range_flag);
 }
 
 // ------------------------------------------------------------------------------------
@@ -248,11 +280,14 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                                           const float *__restrict__ norm_c,
                                                           const float *__restrict__ norm_g, float eps,
                                                           float *__restrict__ g_x, float *__restrict__ g_x0,
-                                                          int acc0, const float *__restrict__ res_w) {
+                                                          int acc0, const float *__restrict__ res_w,
+                                                          unsigned *range_flag) {
     __shared__ __align__(16) float G[BM * LDH];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
+    float amax = 0.f;
 
     // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g).
     // 16 lanes per row (4 rows per wave per pass, wave w owns rows [16w, 16w+16)): lane c
@@ -326,7 +361,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     const int blk = wave >> 1;
     v16f acc[2][2];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, G + blk * MATRIS_D, LDH, W2t, 2 * wave, MATRIS_D / 16, 0, lane);
+    amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, G + blk * MATRIS_D, LDH, W2t, 2 * wave, MATRIS_D / 16, 0,
+                                                      lane);
+    scale_acc<MODE>(acc, w2s);
     // g_p = g_h * SiLU'(p); rows past M read row 0 of the tile (their results are unused)
     const int nrows = (int)min((int64_t)BM, M - m0);
     const float *__restrict__ Pt = P + m0 * 256;
@@ -362,7 +399,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
-        gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
+        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
+        scale_acc<MODE>(a2, w1s);
         if (cb > 0 || !epi0) store_acc_rows<1>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {  // K == 128: every wave holds source-0 columns
             __syncthreads();
@@ -373,7 +411,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         v16f a2[2][2];
         zero_acc(a2);
         const int col0 = cb + wave * 64;
-        gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane);
+        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
+        scale_acc<MODE>(a2, w1s);
         if (col0 >= MATRIS_D || !epi0) store_acc_rows<2>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {
             __syncthreads();  // all waves are done reading G
@@ -405,6 +444,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             }
         }
     }
+    report_range<MODE>(amax, range_flag);
 }
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -414,7 +454,7 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
                                const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
                                float *save_p, float *save_z, const float *res_src, const float *res_w,
                                float *res_out, int mode, void *stream) {
-    if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
+    if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1p || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
         return MATRIS_E_ARG;
     if (m == 0) return 0;
@@ -429,15 +469,10 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1 = (const uint4 *)w1p, *w2 = (const uint4 *)w2p;
-    if (mode == 0)
-        gmlp_fwd_kernel<0><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z,
-                                                 res_src, res_w, res_out);
-    else if (mode == 3)
-        gmlp_fwd_kernel<3><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z,
-                                                 res_src, res_w, res_out);
-    else
-        gmlp_fwd_kernel<6><<<grid, 256, 0, st>>>(m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p, save_z,
-                                                 res_src, res_w, res_out);
+    unsigned *flag = nullptr;
+    if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+    MATRIS_MODE_DISPATCH(gmlp_fwd_kernel, grid, st, m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p,
+                         save_z, res_src, res_w, res_out, flag);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -445,7 +480,7 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
 extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                                const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                                float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
-    if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
+    if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1tp || !w2tp ||
         !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
         return MATRIS_E_ARG;
@@ -455,15 +490,10 @@ extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
-    if (mode == 0)
-        gmlp_bwd_kernel<0><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
-                                                 acc0, res_w);
-    else if (mode == 3)
-        gmlp_bwd_kernel<3><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
-                                                 acc0, res_w);
-    else
-        gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
-                                                 acc0, res_w);
+    unsigned *flag = nullptr;
+    if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+    MATRIS_MODE_DISPATCH(gmlp_bwd_kernel, grid, st, m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
+                         res_w, flag);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -472,6 +502,29 @@ extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float
 // weight packing: [n, k] row-major fp32 (rows = output columns of the GEMM) -> fragment
 // planes, one thread per (tile, k-block, lane)
 // ------------------------------------------------------------------------------------
+// MODE 2 header {1/s, s, 0, 0}: s = 2^(14 - e) with 2^e <= max |w| < 2^(e+1), so the
+// scaled weights reach [2^14, 2^15) at most (s = 1 for an all-zero or non-finite matrix).
+// One work-group.
+__global__ void wscale_kernel(int64_t count, const float *__restrict__ w, float *__restrict__ hdr) {
+    __shared__ float part[4];
+    float m = 0.f;
+    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) m = fmaxf(m, fabsf(w[i]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+        int e = 0;
+        if (m > 0.f && m <= 3.0e38f) e = ilogbf(m) - 14;  // s = 2^-e
+        e = max(-120, min(120, e));
+        hdr[0] = ldexpf(1.0f, e);
+        hdr[1] = ldexpf(1.0f, -e);
+        hdr[2] = 0.f;
+        hdr[3] = 0.f;
+    }
+}
+
 template <int MODE>
 __global__ void pack_b_kernel(int64_t n, int64_t k, const float *__restrict__ w, uint4 *__restrict__ out) {
     constexpr int NPL = Npl<MODE>::v;
@@ -481,27 +534,64 @@ __global__ void pack_b_kernel(int64_t n, int64_t k, const float *__restrict__ w,
     const int lane = (int)(t & 63);
     const int64_t ntkb = t >> 6, nt = ntkb / KB, kb = ntkb % KB;
     const float *r = w + (nt * 32 + (lane & 31)) * k + kb * 16 + (lane >> 5) * 8;
-    Frag<MODE> f;
-    make_frag<MODE>(f, *reinterpret_cast<const float4 *>(r), *reinterpret_cast<const float4 *>(r + 4));
+    const float4 u = *reinterpret_cast<const float4 *>(r), v = *reinterpret_cast<const float4 *>(r + 4);
+    if constexpr (MODE == 2) {
+        // u0 = fp16(s w), u1 = fp16(s w - u0) after the header written by wscale_kernel
+        const float sc = reinterpret_cast<const float *>(out)[1];
+        const float x[8] = {u.x * sc, u.y * sc, u.z * sc, u.w * sc, v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+        uint32_t p0[4], p1[4];
 #pragma unroll
-    for (int pl = 0; pl < NPL; ++pl) out[(ntkb * NPL + pl) * 64 + lane] = f.p[pl];
+        for (int j = 0; j < 4; ++j) {
+            const f2v xv = {x[2 * j], x[2 * j + 1]};
+            const h2v hv = __builtin_convertvector(xv, h2v);
+            p0[j] = bitcast<uint32_t>(hv);
+            p1[j] = bitcast<uint32_t>(__builtin_convertvector(xv - __builtin_convertvector(hv, f2v), h2v));
+        }
+        out += 1;
+        out[(ntkb * NPL + 0) * 64 + lane] = make_uint4(p0[0], p0[1], p0[2], p0[3]);
+        out[(ntkb * NPL + 1) * 64 + lane] = make_uint4(p1[0], p1[1], p1[2], p1[3]);
+    } else {
+        Frag<MODE> f;
+        make_frag<MODE>(f, u, v);
+#pragma unroll
+        for (int pl = 0; pl < NPL; ++pl) out[(ntkb * NPL + pl) * 64 + lane] = f.p[pl];
+    }
 }
 
 extern "C" size_t matris_pack_b_bytes(int64_t n, int64_t k, int mode) { return packed_b_bytes(n, k, mode); }
 
 extern "C" int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, void *out, void *stream) {
-    if (mode != 0 && mode != 3 && mode != 6) return MATRIS_E_ARG;
+    if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (n < 0 || k < 0 || (n % 32) || (k % 16) || !w || !out || !aligned16(w) || !aligned16(out)) return MATRIS_E_ARG;
     const int64_t threads = n / 32 * (k / 16) * 64;
+    hipStream_t st = (hipStream_t)stream;
+    if (mode == 2) {  // the header comes first, also for an empty matrix
+        wscale_kernel<<<1, 256, 0, st>>>(n * k, w, (float *)out);
+        MATRIS_CHECK_LAUNCH();
+    }
     if (threads == 0) return 0;
     const dim3 grid(matris_blocks(threads, 256));
-    hipStream_t st = (hipStream_t)stream;
-    if (mode == 0)
-        pack_b_kernel<0><<<grid, 256, 0, st>>>(n, k, w, (uint4 *)out);
-    else if (mode == 3)
-        pack_b_kernel<3><<<grid, 256, 0, st>>>(n, k, w, (uint4 *)out);
-    else
-        pack_b_kernel<6><<<grid, 256, 0, st>>>(n, k, w, (uint4 *)out);
+    MATRIS_MODE_DISPATCH(pack_b_kernel, grid, st, n, k, w, (uint4 *)out);
     MATRIS_CHECK_LAUNCH();
     return 0;
+}
+
+extern "C" int matris_f16_range_take(int *flagged, void *stream) {
+    if (!flagged) return MATRIS_E_ARG;
+    unsigned *flag = matris_range_flag();
+    if (!flag) return MATRIS_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    // one pinned host word per device, written by the kernel: the read and the reset stay
+    // ordered on the caller's stream
+    static unsigned *host_word[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MATRIS_E_ARG;
+    if (!host_word[dev] && hipHostMalloc((void **)&host_word[dev], sizeof(unsigned), hipHostMallocDefault) != hipSuccess)
+        return MATRIS_E_ARG;
+    unsigned *out = host_word[dev];
+    range_take_kernel<<<1, 1, 0, st>>>(flag, out);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    *flagged = e == hipSuccess ? (int)(out[0] != 0u) : 0;
+    return (int)e;
 }

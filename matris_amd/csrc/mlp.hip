@@ -1,5 +1,5 @@
 // Fused dense layers on gfx950 MFMA for the 128-wide feature rows of the interaction
-// blocks (same fp32 / split-bf16 modes as the gated MLP, see mma.h):
+// blocks (same fp32 / split-bf16 / split-fp16 modes as the gated MLP, see mma.h):
 //
 //   FFN     out = W2 SiLU(W1 x)            node_FFN / edge_FFN of Refinement
 //           (MLP(hidden=int, bias=False), matris/model/functions.py:198-205,
@@ -77,15 +77,17 @@ __global__ __launch_bounds__(256, 3) void ffn_fwd_kernel(int64_t M, const float 
                                                          const uint4 *__restrict__ W1, const uint4 *__restrict__ W2,
                                                          float *__restrict__ out, float *__restrict__ save_p,
                                                          const float *__restrict__ res,
-                                                         const float *__restrict__ res_w) {
+                                                         const float *__restrict__ res_w, unsigned *range_flag) {
     __shared__ __align__(16) float T[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float w1s = take_wscale<MODE>(W1), w2s = take_wscale<MODE>(W2);
     stage_tile128(T, x, MATRIS_D, m0, M, tid);
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1, wave, MATRIS_D / 16, 0, lane);
+    float amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1, wave, MATRIS_D / 16, 0, lane);
+    scale_acc<MODE>(acc, w1s);
     __syncthreads();  // every wave is done reading x
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
@@ -101,11 +103,13 @@ __global__ __launch_bounds__(256, 3) void ffn_fwd_kernel(int64_t M, const float 
     }
     __syncthreads();
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2, wave, MATRIS_D / 16, 0, lane);
+    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2, wave, MATRIS_D / 16, 0, lane));
+    scale_acc<MODE>(acc, w2s);
     __syncthreads();  // every wave is done reading h
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
     store_tile128(T, out, MATRIS_D, m0, M, tid, res, res_w);
+    report_range<MODE>(amax, range_flag);
 }
 
 // FFN backward: g_x = ((g W2) * SiLU'(p)) W1, with w1t = W1^T, w2t = W2^T row-major.
@@ -113,17 +117,20 @@ template <int MODE>
 __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
                                                          const float *__restrict__ P, const uint4 *__restrict__ W1t,
                                                          const uint4 *__restrict__ W2t, float *__restrict__ g_x,
-                                                         float *__restrict__ g_res, const float *__restrict__ res_w) {
+                                                         float *__restrict__ g_res, const float *__restrict__ res_w,
+                                                         unsigned *range_flag) {
     __shared__ __align__(16) float T[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
     stage_tile128(T, g, MATRIS_D, m0, M, tid);
     __syncthreads();
     if (g_res) store_tile128_scaled(T, g_res, res_w, m0, M, tid);
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
+    float amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
+    scale_acc<MODE>(acc, w2s);
     // g_p = g_h * SiLU'(p): lane = row, 4 consecutive columns per register group
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
@@ -143,11 +150,13 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1t, wave, MATRIS_D / 16, 0, lane);
+    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1t, wave, MATRIS_D / 16, 0, lane));
+    scale_acc<MODE>(acc, w1s);
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
     store_tile128(T, g_x, MATRIS_D, m0, M, tid);
+    report_range<MODE>(amax, range_flag);
 }
 
 // ------------------------------------------------------------------------------------
@@ -157,47 +166,55 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float *__restrict__ x,
                                                           const uint4 *__restrict__ W, float *__restrict__ out0,
-                                                          float *__restrict__ out1) {
+                                                          float *__restrict__ out1, unsigned *range_flag) {
     __shared__ __align__(16) float T0[BM * LDT];
     __shared__ __align__(16) float T1[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float ws = take_wscale<MODE>(W);
     stage_tile128(T0, x, MATRIS_D, m0, M, tid);
     __syncthreads();
     // wave w -> output columns [64w, 64w+64) of the 256: waves 0,1 -> out0, 2,3 -> out1
     v16f acc[2][2];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0, lane);
+    const float amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0,
+                                                                        lane);
+    scale_acc<MODE>(acc, ws);
     __syncthreads();  // T0 free
     acc_t_to_lds<2, 2>(acc, (wave < 2) ? T0 : T1, LDT, (wave & 1) * 64, lane);
     __syncthreads();
     store_tile128(T0, out0, MATRIS_D, m0, M, tid);
     store_tile128(T1, out1, MATRIS_D, m0, M, tid);
+    report_range<MODE>(amax, range_flag);
 }
 
 template <int MODE>
 __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
                                                           const float *__restrict__ g1, const uint4 *__restrict__ Wt,
                                                           float *__restrict__ g_x, const float *__restrict__ res,
-                                                          const float *__restrict__ res_w) {
+                                                          const float *__restrict__ res_w, unsigned *range_flag) {
     // Wt = W^T ([128, 256]) packed: g_x[m][k] = sum_n g[m][n] Wt[k][n], k-blocks 0..7
     // pair with g0, 8..15 with g1; g0 then g1 pass through the one LDS tile
     __shared__ __align__(16) float T[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float ws = take_wscale<MODE>(Wt);
     stage_tile128(T, g0, MATRIS_D, m0, M, tid);
     __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, 0, lane);
+    float amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, 0, lane);
     __syncthreads();
     stage_tile128(T, g1, MATRIS_D, m0, M, tid);
     __syncthreads();
-    gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, MATRIS_D / 16, lane);
+    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, MATRIS_D / 16,
+                                                                        lane));
+    scale_acc<MODE>(acc, ws);  // both halves share the one weight scale
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
     store_tile128(T, g_x, MATRIS_D, m0, M, tid, res, res_w);
+    report_range<MODE>(amax, range_flag);
 }
 
 // ------------------------------------------------------------------------------------
@@ -205,15 +222,15 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
 // ------------------------------------------------------------------------------------
 #define MLP_DISPATCH(KERNEL, ...)                                                         \
     do {                                                                                  \
+        unsigned *flag_ = nullptr;                                                        \
+        if (mode == 2 && !(flag_ = matris_range_flag())) return MATRIS_E_ARG;             \
         const dim3 grid_(matris_blocks(m, BM));                                           \
         hipStream_t st_ = (hipStream_t)stream;                                            \
-        if (mode == 0) KERNEL<0><<<grid_, 256, 0, st_>>>(__VA_ARGS__);                    \
-        else if (mode == 3) KERNEL<3><<<grid_, 256, 0, st_>>>(__VA_ARGS__);               \
-        else KERNEL<6><<<grid_, 256, 0, st_>>>(__VA_ARGS__);                              \
+        MATRIS_MODE_DISPATCH(KERNEL, grid_, st_, __VA_ARGS__, flag_);                     \
     } while (0)
 
 static bool mlp_args_ok(int mode, std::initializer_list<const void *> ptrs) {
-    if (mode != 0 && mode != 3 && mode != 6) return false;
+    if (!matris_mode_ok(mode)) return false;
     for (const void *p : ptrs)
         if (!p || ((uintptr_t)p & 15)) return false;
     return true;

@@ -11,19 +11,33 @@
 //           v_mfma_f32_32x32x16_bf16.
 //   MODE 6  x = hi + mid + lo exactly (truncated hi, mid; exact lo): planes hi, mid, lo;
 //           6 products (adds hi*lo + mid*mid + lo*hi): fp32-grade products.
+//   MODE 2  fp16 split on v_mfma_f32_32x32x16_f16.  Activations: hi = fp16(x), lo =
+//           fp16((x - hi) 2^11) (both round-to-nearest), so x = hi + 2^-11 lo to ~2^-22 |x|
+//           (subnormal fp16 keeps the absolute error of tiny x near 2^-36).  Weights are
+//           scaled by a power of two s per matrix (max |s w| in [2^14, 2^15)) and stored
+//           as u0 = fp16(s w), u1 = fp16(s w - u0); a third register plane u0 2^-11 is made
+//           at use (one v_pk_mul_f16 per register).  3 products into one accumulator:
+//           u1 hi + (2^-11 u0) lo + u0 hi = s w x to ~2^-22 relative, and the result is
+//           scaled back by 1/s (exact).  fp16 has a finite range: activations with
+//           |x| >= 65504 are flagged (report_range) so the caller can redo the work in
+//           MODE 6.
 // A and B fragments use the same k assignment, so every mode sums over the same k.
-// The bf16 instruction's layout (A lane l: row l%32, k = 8(l/32)..+7; B lane l:
+// The bf16 / f16 instructions' layout (A lane l: row l%32, k = 8(l/32)..+7; B lane l:
 // k = 8(l/32)..+7, column l%32) is exactly this fragment.
 //
 // Weights (B operands) are packed once per parameter version by matris_pack_b into
 // fragment-major order: 16-byte unit ((nt * KB + kb) * NPL + plane) * 64 + lane for
 // output-column tile nt, k-block kb (KB = K / 16).  A wave's fragment load is then one
-// contiguous 1 KB read per plane and no weight is converted inside a GEMM loop.
+// contiguous 1 KB read per plane and no weight is converted inside a GEMM loop.  A
+// MODE 2 image starts with a 16-byte header {1/s, s, 0, 0} (take_wscale).
 #pragma once
 #include "common.h"
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f2v __attribute__((ext_vector_type(2)));
 
 #define BM 64    // rows per work-group
 #define LDH 260  // LDS row stride (floats) of a [64, 256] fp32 tile
@@ -34,10 +48,15 @@ struct Npl {
     static constexpr int v = MODE == 6 ? 3 : 2;
 };
 
+// Register planes: MODE 2 weight fragments carry the derived plane u0 2^-11 (prep_w) as
+// p[2]; activation fragments leave it unused.
 template <int MODE>
 struct Frag {
-    uint4 p[Npl<MODE>::v];
+    uint4 p[MODE == 2 ? 3 : Npl<MODE>::v];
 };
+
+// fp16 overflow threshold of the MODE 2 activation split.
+#define MATRIS_F16_MAX 65504.0f
 
 template <class To, class From>
 __device__ __forceinline__ To bitcast(const From &x) {
@@ -50,6 +69,9 @@ __device__ __forceinline__ v16f mfma32(float a, float b, v16f c) {
 }
 __device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v16f mfma_f16(const v8h &a, const v8h &b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // sigmoid = 1 / (1 + e^-x) with v_rcp_f32 (1 ulp); SiLU = x sigmoid(x).
@@ -74,6 +96,17 @@ __device__ __forceinline__ void make_frag(Frag<MODE> &f, const float4 &u, const 
     if constexpr (MODE == 0) {
         f.p[0] = bitcast<uint4>(u);
         f.p[1] = bitcast<uint4>(v);
+    } else if constexpr (MODE == 2) {
+        // hi = fp16(x) and lo = fp16((x - hi) 2^11), two values per v_cvt_pk_f16_f32
+        const f2v x0 = {u.x, u.y}, x1 = {u.z, u.w}, x2 = {v.x, v.y}, x3 = {v.z, v.w};
+        const h2v h0 = __builtin_convertvector(x0, h2v), h1 = __builtin_convertvector(x1, h2v);
+        const h2v h2 = __builtin_convertvector(x2, h2v), h3 = __builtin_convertvector(x3, h2v);
+        const h2v l0 = __builtin_convertvector((x0 - __builtin_convertvector(h0, f2v)) * 2048.0f, h2v);
+        const h2v l1 = __builtin_convertvector((x1 - __builtin_convertvector(h1, f2v)) * 2048.0f, h2v);
+        const h2v l2 = __builtin_convertvector((x2 - __builtin_convertvector(h2, f2v)) * 2048.0f, h2v);
+        const h2v l3 = __builtin_convertvector((x3 - __builtin_convertvector(h3, f2v)) * 2048.0f, h2v);
+        f.p[0] = make_uint4(bitcast<uint32_t>(h0), bitcast<uint32_t>(h1), bitcast<uint32_t>(h2), bitcast<uint32_t>(h3));
+        f.p[1] = make_uint4(bitcast<uint32_t>(l0), bitcast<uint32_t>(l1), bitcast<uint32_t>(l2), bitcast<uint32_t>(l3));
     } else {
         const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
         uint32_t hb[8], mb[8], lb[8];
@@ -96,7 +129,57 @@ __device__ __forceinline__ void make_frag(Frag<MODE> &f, const float4 &u, const 
     }
 }
 
+// Running max |x| of the values a MODE 2 conversion sees (0 in the other modes, which have
+// no range limit).  NaN inputs are not counted: they give NaN in every mode.
+template <int MODE>
+__device__ __forceinline__ float frag_amax(float m, const float4 &u, const float4 &v) {
+    if constexpr (MODE == 2) {
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+        return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    } else {
+        return m;
+    }
+}
+
+// The derived plane of a MODE 2 weight fragment, made once its load has landed.
+template <int MODE>
+__device__ __forceinline__ void prep_w(Frag<MODE> &w) {
+    if constexpr (MODE == 2) w.p[2] = bitcast<uint4>(bitcast<v8h>(w.p[0]) * (_Float16)0.00048828125f);
+}
+
+// MODE 2: the weight's 1/s from the header of its packed image, which the pointer then
+// skips; 1 in the other modes.
+template <int MODE>
+__device__ __forceinline__ float take_wscale(const uint4 *__restrict__ &W) {
+    if constexpr (MODE == 2) {
+        const float s = reinterpret_cast<const float *>(W)[0];
+        W += 1;
+        return s;
+    } else {
+        return 1.0f;
+    }
+}
+
+template <int MODE, int NRT, int NCT>
+__device__ __forceinline__ void scale_acc(v16f (&acc)[NRT][NCT], float s) {
+    if constexpr (MODE == 2) {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] *= s;
+    }
+}
+
+// MODE 2: flag the device's range word if any lane converted a value fp16 cannot hold.
+template <int MODE>
+__device__ __forceinline__ void report_range(float amax, unsigned *flag) {
+    if constexpr (MODE == 2) {
+        if (__ballot(amax >= MATRIS_F16_MAX) != 0 && (threadIdx.x & 63) == 0 && flag) atomicOr(flag, 1u);
+    }
+}
+
 // acc += A-fragment * B-fragment over one 16-wide k block.  Smallest products first.
+// (Modes 0, 3, 6; MODE 2 goes through mma_wx / mma_xw, which know the weight side.)
 template <int MODE>
 __device__ __forceinline__ void mma_frag(v16f &acc, const Frag<MODE> &a, const Frag<MODE> &b) {
     if constexpr (MODE == 0) {
@@ -125,6 +208,32 @@ __device__ __forceinline__ void mma_frag(v16f &acc, const Frag<MODE> &a, const F
     }
 }
 
+// acc += W-fragment (MFMA A operand) * X-fragment (B operand): the transposed products.
+template <int MODE>
+__device__ __forceinline__ void mma_wx(v16f &acc, const Frag<MODE> &w, const Frag<MODE> &x) {
+    if constexpr (MODE == 2) {
+        const v8h xh = bitcast<v8h>(x.p[0]), xl = bitcast<v8h>(x.p[1]);
+        acc = mfma_f16(bitcast<v8h>(w.p[1]), xh, acc);
+        acc = mfma_f16(bitcast<v8h>(w.p[2]), xl, acc);
+        acc = mfma_f16(bitcast<v8h>(w.p[0]), xh, acc);
+    } else {
+        mma_frag<MODE>(acc, w, x);
+    }
+}
+
+// acc += X-fragment (MFMA A operand) * W-fragment (B operand).
+template <int MODE>
+__device__ __forceinline__ void mma_xw(v16f &acc, const Frag<MODE> &x, const Frag<MODE> &w) {
+    if constexpr (MODE == 2) {
+        const v8h xh = bitcast<v8h>(x.p[0]), xl = bitcast<v8h>(x.p[1]);
+        acc = mfma_f16(xh, bitcast<v8h>(w.p[1]), acc);
+        acc = mfma_f16(xl, bitcast<v8h>(w.p[2]), acc);
+        acc = mfma_f16(xh, bitcast<v8h>(w.p[0]), acc);
+    } else {
+        mma_frag<MODE>(acc, x, w);
+    }
+}
+
 // B fragments of output tiles nt0 .. nt0+NCT-1, k-block kb, of a packed weight with KB
 // k-blocks.
 template <int MODE, int NCT>
@@ -140,12 +249,15 @@ __device__ __forceinline__ void load_bfrags(Frag<MODE> (&b)[NCT], const uint4 *_
 
 // A fragments of NRT 32-row tiles of an fp32 row-major LDS array, k-block kb.
 template <int MODE, int NRT>
-__device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *base, int ld, int kb, int lane) {
+__device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *base, int ld, int kb, int lane,
+                                           float &amax) {
     const int h = lane >> 5, l32 = lane & 31;
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
         const float *r = base + (rt * 32 + l32) * ld + kb * 16 + h * 8;
-        make_frag<MODE>(a[rt], *reinterpret_cast<const float4 *>(r), *reinterpret_cast<const float4 *>(r + 4));
+        const float4 u = *reinterpret_cast<const float4 *>(r), v = *reinterpret_cast<const float4 *>(r + 4);
+        amax = frag_amax<MODE>(amax, u, v);
+        make_frag<MODE>(a[rt], u, v);
     }
 }
 
@@ -158,10 +270,13 @@ __device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *ba
 // weight fragment is the MFMA A operand and the LDS rows the B operand, so lane l holds
 // row rt*32 + l%32 of A and its 16 registers are output columns ct*32 + acc_row(i, l/32)
 // (four runs of four consecutive columns) -- a layout with whole rows in lanes.
+// Returns the running max |A| of a MODE 2 conversion (0 otherwise).  MODE 2 sums carry the
+// weight's scale s: the caller applies scale_acc once its last product is in.
 template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false>
-__device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
-                                                const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
+__device__ __forceinline__ float gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
+                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
     constexpr int kUnroll = NCT >= 2 ? 1 : 2;  // 2-tile bodies are long enough; keeps pressure down
+    float amax = 0.f;
     Frag<MODE> cur[NCT], nxt[NCT];
     load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
 #pragma unroll kUnroll
@@ -169,50 +284,22 @@ __device__ __forceinline__ void gemm_lds_packed(v16f (&acc)[NRT][NCT], const flo
         load_bfrags<MODE, NCT>(nxt, W, nt0, KBW, kb0 + min(kb + 1, KBA - 1), lane);
         __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
         Frag<MODE> a[NRT];
-        lds_afrags<MODE, NRT>(a, a_base, lda, kb, lane);
+        lds_afrags<MODE, NRT>(a, a_base, lda, kb, lane, amax);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) prep_w<MODE>(cur[ct]);
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) {
                 if constexpr (TRANS)
-                    mma_frag<MODE>(acc[rt][ct], cur[ct], a[rt]);
+                    mma_wx<MODE>(acc[rt][ct], cur[ct], a[rt]);
                 else
-                    mma_frag<MODE>(acc[rt][ct], a[rt], cur[ct]);
+                    mma_xw<MODE>(acc[rt][ct], a[rt], cur[ct]);
             }
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
     }
-}
-
-// One 32-row A tile against two groups of two B tiles (starting at tiles ntA and ntB):
-// acc0 += A * B[ntA, ntA+1], acc1 += A * B[ntB, ntB+1]; one A conversion per k-block
-// feeds four MFMA tiles.
-template <int MODE, int KBA>
-__device__ __forceinline__ void gemm_lds_packed2(v16f (&acc0)[1][2], v16f (&acc1)[1][2], const float *a_base,
-                                                 int lda, const uint4 *__restrict__ W, int ntA, int ntB, int KBW,
-                                                 int lane) {
-    Frag<MODE> c0[2], c1[2], n0[2], n1[2];
-    load_bfrags<MODE, 2>(c0, W, ntA, KBW, 0, lane);
-    load_bfrags<MODE, 2>(c1, W, ntB, KBW, 0, lane);
-#pragma unroll 1
-    for (int kb = 0; kb < KBA; ++kb) {
-        const int kn = min(kb + 1, KBA - 1);
-        load_bfrags<MODE, 2>(n0, W, ntA, KBW, kn, lane);
-        load_bfrags<MODE, 2>(n1, W, ntB, KBW, kn, lane);
-        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
-        Frag<MODE> a[1];
-        lds_afrags<MODE, 1>(a, a_base, lda, kb, lane);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            mma_frag<MODE>(acc0[0][ct], a[0], c0[ct]);
-            mma_frag<MODE>(acc1[0][ct], a[0], c1[ct]);
-        }
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            c0[ct] = n0[ct];
-            c1[ct] = n1[ct];
-        }
-    }
+    return amax;
 }
 
 template <int NRT, int NCT>
@@ -270,7 +357,22 @@ __device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *til
     acc_to_lds_rc<2, NCT>(acc, tile, ld, 0, col0, lane, bias);
 }
 
+// MFMA arithmetic modes the GEMM kernels are built for.
+static inline bool matris_mode_ok(int mode) { return mode == 0 || mode == 2 || mode == 3 || mode == 6; }
+
+// Launch KERNEL<mode> (mode already checked by matris_mode_ok).
+#define MATRIS_MODE_DISPATCH(KERNEL, GRID, STREAM, ...)                                     \
+    do {                                                                                    \
+        if (mode == 0) KERNEL<0><<<(GRID), 256, 0, (STREAM)>>>(__VA_ARGS__);                \
+        else if (mode == 2) KERNEL<2><<<(GRID), 256, 0, (STREAM)>>>(__VA_ARGS__);           \
+        else if (mode == 3) KERNEL<3><<<(GRID), 256, 0, (STREAM)>>>(__VA_ARGS__);           \
+        else KERNEL<6><<<(GRID), 256, 0, (STREAM)>>>(__VA_ARGS__);                          \
+    } while (0)
+
+// The current device's MODE 2 range word (defined in gmlp.hip), nullptr on failure.
+unsigned *matris_range_flag();
+
 // Bytes of a packed [n, k] weight in `mode` (n % 32 == 0, k % 16 == 0).
 __host__ __device__ inline size_t packed_b_bytes(int64_t n, int64_t k, int mode) {
-    return (size_t)n * (size_t)k * (mode == 6 ? 6 : 4);
+    return (size_t)n * (size_t)k * (mode == 6 ? 6 : 4) + (mode == 2 ? 16 : 0);
 }

@@ -593,9 +593,28 @@ class MatRIS(nn.Module):
             print(f"MatRIS initialized with {self.get_params()} parameters")
 
     def forward(self, graphs, task: str = "ef", is_training: bool = False) -> dict:
-        """model.py:183-250."""
+        """model.py:183-250.
+
+        In the "f16x3" MFMA arithmetic the evaluation ends by reading the device's fp16
+        range flag; if any GEMM operand exceeded the fp16 range the whole evaluation is
+        redone in "bf16x6" (a warning says so), so results never carry an overflow."""
         if is_training:
             raise NotImplementedError("training (double backward) is outside the efsm inference path")
+        if ops.get_mma_precision() != "f16x3":
+            return self._evaluate(graphs, task)
+        dev = next(self.parameters()).device
+        ops.f16_range_take(dev)  # start clean: a failed earlier call may have left it set
+        pred = self._evaluate(graphs, task)
+        if ops.f16_range_take(dev):
+            import warnings
+            warnings.warn("MatRIS: an activation exceeded the fp16 range of the f16x3 GEMMs; "
+                          "the evaluation was redone in bf16x6", RuntimeWarning, stacklevel=2)
+            with ops.mma_precision("bf16x6"):
+                pred = self._evaluate(graphs, task)
+        return pred
+
+    def _evaluate(self, graphs, task: str) -> dict:
+        is_training = False
         pred = {}
         bg = process_graphs(graphs, compute_stress="s" in task)
         bg["line_recompute"] = bool(self.line_recompute)

@@ -16,19 +16,49 @@ from .. import _lib
 
 D = 128
 
-# MFMA arithmetic of the fused GatedMLP kernels (include/matris_hip.h MATRIS_MMA_*):
-# 0 = fp32 MFMA, 6 = three-way bf16 split (fp32-grade), 3 = two-way bf16 split.
-MMA_MODES = {"fp32": 0, "bf16x6": 6, "bf16x3": 3}
-_MMA = {"mode": 6}
+# MFMA arithmetic of the fused GEMM kernels (include/matris_hip.h MATRIS_MMA_*):
+# 0 = fp32 MFMA, 6 = three-way bf16 split (fp32-grade), 2 = fp16 hi/lo split with a
+# scaled weight (fp32-grade, half the MFMA work of 6; activations must stay below the
+# fp16 range, which the kernels flag), 3 = two-way bf16 split (~2^-16).
+MMA_MODES = {"fp32": 0, "f16x3": 2, "bf16x6": 6, "bf16x3": 3}
+DEFAULT_MMA = "f16x3"
+_MMA = {"mode": MMA_MODES[DEFAULT_MMA]}
 
 
 def set_mma_precision(name: str) -> None:
-    """Select the GatedMLP MFMA arithmetic: "bf16x6" (default), "fp32" or "bf16x3"."""
+    """Select the MFMA arithmetic of the GEMM kernels: one of MMA_MODES (DEFAULT_MMA
+    unless set)."""
     _MMA["mode"] = MMA_MODES[name]
 
 
 def get_mma_precision() -> str:
     return {v: k for k, v in MMA_MODES.items()}[_MMA["mode"]]
+
+
+class mma_precision:
+    """Context manager: run the enclosed ops in another MFMA arithmetic."""
+
+    def __init__(self, name: str):
+        self.name, self.prev = name, None
+
+    def __enter__(self):
+        self.prev = get_mma_precision()
+        set_mma_precision(self.name)
+        return self
+
+    def __exit__(self, *exc):
+        set_mma_precision(self.prev)
+
+
+def f16_range_take(device=None) -> bool:
+    """True if an "f16x3" kernel met an activation outside the fp16 range on `device` since
+    the last call (its results are unusable); clears the flag.  Synchronizes the current
+    stream."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    flag = ctypes.c_int(0)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().matris_f16_range_take(ctypes.byref(flag), _stream()), "matris_f16_range_take")
+    return bool(flag.value)
 
 # Optional per-launch timing (bench.py): name -> list of (start, end, info) HIP events
 # recorded on the launch stream around each kernel call.

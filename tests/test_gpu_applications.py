@@ -41,7 +41,7 @@ def test_calculator_matches_model(model):
     f, s, m = atoms.get_forces(), atoms.get_stress(), atoms.get_magnetic_moments()
     out = model([model.graph_converter(cr)], task="efsm")
     n = len(cr.z)
-    assert e == pytest.approx(float(out["e"][0]) * n, rel=1e-6, abs=1e-6)
+    assert e == pytest.approx(float(out["e"][0].detach()) * n, rel=1e-6, abs=1e-6)
     np.testing.assert_allclose(f, out["f"][0].detach().cpu().numpy(), atol=1e-6)
     np.testing.assert_allclose(s, out["s"][0].detach().cpu().numpy() * GPA, atol=1e-9)
     np.testing.assert_allclose(m, out["m"][0].detach().cpu().numpy(), atol=1e-6)

@@ -141,7 +141,7 @@ class _ShimGated(torch.nn.Module):
         self.core_norm, self.gate_norm = t.nc, t.ng
 
 
-@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
 @pytest.mark.parametrize("nsrc,M", [(3, 1000), (4, 777), (3, 64), (4, 5)])
 def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
     ops = _ops()
@@ -172,10 +172,10 @@ def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
         for j in range(nsrc):
             assert _rel(sd[j].grad, s64[j].grad) < tol, j
     finally:
-        ops.set_mma_precision("bf16x6")
+        ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
-_MODES = [("fp32", 1e-5), ("bf16x6", 1e-5), ("bf16x3", 1e-4)]
+_MODES = [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)]
 
 
 def test_pack_b_fragment_layout():
@@ -202,6 +202,55 @@ def test_pack_b_fragment_layout():
     p3 = ops.pack_b(w.to(DEV), 3).cpu().view(torch.bfloat16).view(n // 32, k // 16, 2, 64, 8)
     assert torch.equal(p3[:, :, 0], p6[:, :, 0])
     assert torch.equal(p3[nt, kb, 1, lane, j], (w - trunc).to(torch.bfloat16))
+    # mode 2: header {1/s, s, 0, 0} with s = 2^(14 - floor(log2 max|w|)); then u0 =
+    # round-to-nearest fp16 of s w and u1 = fp16 of s w - u0
+    raw = ops.pack_b(w.to(DEV), 2).cpu()
+    hdr = raw[:16].view(torch.float32)
+    e = int(torch.floor(torch.log2(w.abs().max())).item())
+    assert hdr.tolist() == [2.0 ** (e - 14), 2.0 ** (14 - e), 0.0, 0.0]
+    p2 = raw[16:].view(torch.float16).view(n // 32, k // 16, 2, 64, 8)
+    sw = w * 2.0 ** (14 - e)
+    assert sw.abs().max().item() < 2.0 ** 15
+    u0 = sw.to(torch.float16)
+    assert torch.equal(p2[nt, kb, 0, lane, j], u0)
+    assert torch.equal(p2[nt, kb, 1, lane, j], (sw - u0.float()).to(torch.float16))
+    big = sw.abs() >= 2.0 ** -3  # where the residual plane is a normal fp16
+    err = (u0.double() + p2[nt, kb, 1, lane, j].double() - sw.double()).abs()
+    assert (err[big] <= sw.double().abs()[big] * 2.0 ** -21).all()
+
+
+@pytest.mark.parametrize("kind", ["gmlp", "ffn", "pair"])
+def test_f16x3_range_flag(kind):
+    """An activation beyond the fp16 range sets the device's range flag in every f16x3
+    kernel family (forward and backward); values inside the range leave it clear."""
+    ops = _ops()
+    torch.manual_seed(11)
+    M = 200
+    ops.set_mma_precision("f16x3")
+    try:
+        assert not ops.f16_range_take()
+        for big in (False, True):
+            x = torch.randn(M, 128, device=DEV)
+            if big:
+                x[77, 5] = 1.0e5
+            xd = x.requires_grad_(True)
+            if kind == "gmlp":
+                ref = _TorchGMLP(128)
+                out = ops.gated_mlp(_ShimGated(ref).to(DEV), ops.GmlpPack(), [(xd, None)])
+            elif kind == "ffn":
+                w1, w2 = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
+                out = ops.ffn(ops._WeightPack().get(w1, w2), xd)
+            else:
+                ws, wt = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
+                out = ops.proj_pair(ops._WeightPack().get(ws, wt), xd)[0]
+            assert ops.f16_range_take() == big, ("forward", big)
+            g = torch.randn(M, 128, device=DEV)
+            if big:  # a gradient beyond the range, through the backward kernels alone
+                g[3, 9] = -2.0e5
+            out.backward(g)
+            assert ops.f16_range_take() == big, ("backward", big)
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
 @pytest.mark.parametrize("mode,tol", _MODES)
@@ -225,7 +274,7 @@ def test_ffn_fwd_bwd(M, mode, tol):
         out.backward(g.to(DEV))
         assert _rel(xd.grad, x64.grad) < tol
     finally:
-        ops.set_mma_precision("bf16x6")
+        ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
 @pytest.mark.parametrize("mode,tol", _MODES)
@@ -252,7 +301,7 @@ def test_proj_pair_fwd_bwd(M, mode, tol):
         o0.backward(g0.to(DEV))
         assert _rel(xd.grad, (g0.double() @ ws.double())) < tol
     finally:
-        ops.set_mma_precision("bf16x6")
+        ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
 @pytest.mark.parametrize("N,E", [(864, 67396), (5, 7), (1, 0)])

@@ -139,4 +139,40 @@ def test_fp32_mma_mode_vs_reference_golden(golden):
         graphs = [_graph_from_arrays(z, f"g{i}_") for i in range(int(z["n_cells"]))]
         _assert_close(_efsm(_model(), graphs), z, "cells_small fp32-mma", _fp64(golden, "cells"))
     finally:
-        ops.set_mma_precision("bf16x6")
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
+@pytest.mark.parametrize("mode", ["bf16x6", "f16x3"])
+def test_fp32_grade_mma_modes_vs_reference_golden(golden, mode):
+    """Both fp32-grade split arithmetics (three-way bf16 and fp16 hi/lo) on C1, the batched
+    triclinic cells and C3, whichever of them is the default."""
+    from matris_amd import workloads as W
+    from matris_amd.model import ops
+    with ops.mma_precision(mode):
+        z = golden("c1_cu4.npz")
+        _assert_close(_efsm(_model(), [_graph_from_arrays(z, "g_")]), z, f"C1 {mode}", _fp64(golden, "c1"))
+        z = golden("cells_small.npz")
+        graphs = [_graph_from_arrays(z, f"g{i}_") for i in range(int(z["n_cells"]))]
+        _assert_close(_efsm(_model(), graphs), z, f"cells_small {mode}", _fp64(golden, "cells"))
+        z = golden("c3_cu864.npz")
+        model = _model()
+        _assert_close(_efsm(model, [model.graph_converter(W.c3_cu864())]), z, f"C3 {mode}", _fp64(golden, "c3"))
+
+
+def test_f16x3_overflow_falls_back_to_bf16x6(golden):
+    """Atom embeddings scaled by 1e6 push the first GEMM operands past the fp16 range: the
+    f16x3 evaluation must notice, warn, and return exactly the bf16x6 results."""
+    from matris_amd.model import ops
+    z = golden("c1_cu4.npz")
+    model = _model()
+    with torch.no_grad():
+        model.atom_embedding.embedding.weight.mul_(1.0e6)
+    g = [_graph_from_arrays(z, "g_")]
+    with ops.mma_precision("bf16x6"):
+        ref = _efsm(model, g)
+    with ops.mma_precision("f16x3"):
+        with pytest.warns(RuntimeWarning, match="fp16 range"):
+            out = _efsm(model, g)
+        assert not ops.f16_range_take()
+    for k in "efsm":
+        assert np.all(np.isfinite(out[k])) and np.array_equal(out[k], ref[k]), k

@@ -88,9 +88,12 @@ def test_arguments_rejected_before_launch(lib):
     # weight packing: n not a multiple of 32, k not a multiple of 16, unknown mode
     assert lib.matris_pack_b(48, 16, v16, 6, v16, None) == -1001
     assert lib.matris_pack_b(32, 24, v16, 6, v16, None) == -1001
-    assert lib.matris_pack_b(32, 16, v16, 2, v16, None) == -1001
+    assert lib.matris_pack_b(32, 16, v16, 5, v16, None) == -1001
+    assert lib.matris_ffn_fwd(10, v16, v16, v16, v16, None, None, None, 1, None) == -1001
     assert lib.matris_pack_b_bytes(256, 384, 6) == 256 * 384 * 6
     assert lib.matris_pack_b_bytes(256, 384, 3) == lib.matris_pack_b_bytes(256, 384, 0) == 256 * 384 * 4
+    assert lib.matris_pack_b_bytes(256, 384, 2) == 256 * 384 * 4 + 16
+    assert lib.matris_f16_range_take(None, None) == -1001
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
     assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, None, None, 3, None) == 0
