@@ -44,6 +44,15 @@ AMU_A2_FS2_EV = 103.642691        # 1 amu * (Angstrom/fs)^2 in eV
 FORCE_TO_ACC = 1.0 / AMU_A2_FS2_EV  # (eV/Angstrom)/amu -> Angstrom/fs^2
 
 
+def _detached(v):
+    """Results without the autograd graph of the forward (tensors or lists of tensors)."""
+    if isinstance(v, torch.Tensor):
+        return v.detach()
+    if isinstance(v, (list, tuple)):
+        return type(v)(t.detach() if isinstance(t, torch.Tensor) else t for t in v)
+    return v
+
+
 class MolecularDynamics:
     """GPU molecular dynamics with the reference's constructor keywords (md.py:34-54).
 
@@ -135,7 +144,7 @@ class MolecularDynamics:
         torch.cuda.synchronize()
         self.timings["graph"] += t1 - t0
         self.timings["model"] += time.perf_counter() - t1
-        self.results = pred
+        self.results = {k: _detached(v) for k, v in pred.items()}
         return forces
 
     def step(self) -> None:

@@ -44,10 +44,7 @@ unsigned *matris_range_flag() {
     return ptr[dev];
 }
 
-__global__ void range_take_kernel(unsigned *flag, unsigned *out) {
-    out[0] = flag[0];
-    flag[0] = 0u;
-}
+__global__ void range_reset_kernel(unsigned *flag) { flag[0] = 0u; }
 
 struct GmlpSrc {
     const float *ptr[4];
@@ -504,17 +501,23 @@ extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float
 // ------------------------------------------------------------------------------------
 // MODE 2 header {1/s, s, 0, 0}: s = 2^(14 - e) with 2^e <= max |w| < 2^(e+1), so the
 // scaled weights reach [2^14, 2^15) at most (s = 1 for an all-zero or non-finite matrix).
-// One work-group.
-__global__ void wscale_kernel(int64_t count, const float *__restrict__ w, float *__restrict__ hdr) {
-    __shared__ float part[4];
+// One work-group of 1024 threads (count is a multiple of 512, w 16-byte aligned).
+__global__ __launch_bounds__(1024) void wscale_kernel(int64_t count, const float *__restrict__ w,
+                                                      float *__restrict__ hdr) {
+    __shared__ float part[16];
     float m = 0.f;
-    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) m = fmaxf(m, fabsf(w[i]));
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    for (int64_t i = threadIdx.x; i < count / 4; i += blockDim.x) {
+        const float4 v = w4[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
-        m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+        m = 0.f;
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, part[i]);
         int e = 0;
         if (m > 0.f && m <= 3.0e38f) e = ilogbf(m) - 14;  // s = 2^-e
         e = max(-120, min(120, e));
@@ -566,7 +569,7 @@ extern "C" int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, voi
     const int64_t threads = n / 32 * (k / 16) * 64;
     hipStream_t st = (hipStream_t)stream;
     if (mode == 2) {  // the header comes first, also for an empty matrix
-        wscale_kernel<<<1, 256, 0, st>>>(n * k, w, (float *)out);
+        wscale_kernel<<<1, 1024, 0, st>>>(n * k, w, (float *)out);
         MATRIS_CHECK_LAUNCH();
     }
     if (threads == 0) return 0;
@@ -581,17 +584,14 @@ extern "C" int matris_f16_range_take(int *flagged, void *stream) {
     unsigned *flag = matris_range_flag();
     if (!flag) return MATRIS_E_ARG;
     hipStream_t st = (hipStream_t)stream;
-    // one pinned host word per device, written by the kernel: the read and the reset stay
-    // ordered on the caller's stream
-    static unsigned *host_word[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MATRIS_E_ARG;
-    if (!host_word[dev] && hipHostMalloc((void **)&host_word[dev], sizeof(unsigned), hipHostMallocDefault) != hipSuccess)
-        return MATRIS_E_ARG;
-    unsigned *out = host_word[dev];
-    range_take_kernel<<<1, 1, 0, st>>>(flag, out);
-    hipError_t e = hipGetLastError();
+    // read, then clear with a kernel (no memset node), both ordered on the caller's stream
+    unsigned v = 0u;
+    hipError_t e = hipMemcpyAsync(&v, flag, sizeof(v), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) {
+        range_reset_kernel<<<1, 1, 0, st>>>(flag);
+        e = hipGetLastError();
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
-    *flagged = e == hipSuccess ? (int)(out[0] != 0u) : 0;
+    *flagged = e == hipSuccess ? (int)(v != 0u) : 0;
     return (int)e;
 }
