@@ -210,52 +210,6 @@ __global__ void rg_scatter_kernel(int64_t n, RGWork w) {
     w.cell_atoms[pos] = (int)i;
 }
 
-// Visit every candidate (j, n) of atom i once; f(j, n0, n1, n2, dist) on accepted edges.
-template <typename F>
-__device__ __forceinline__ void rg_visit(int64_t i, const RGPlan &plan, const RGWork &w, double cutoff, double tol,
-                                         F &&f) {
-    const double *ci = w.cart + 3 * i;
-    int cid = w.cell[i];
-    int c2 = cid % plan.g[2];
-    int c1 = (cid / plan.g[2]) % plan.g[1];
-    int c0 = cid / (plan.g[2] * plan.g[1]);
-    int wi0 = w.wrap[3 * i], wi1 = w.wrap[3 * i + 1], wi2 = w.wrap[3 * i + 2];
-    for (int d0 = -plan.r[0]; d0 <= plan.r[0]; ++d0) {
-        int a0 = c0 + d0;
-        int s0 = (int)floor((double)a0 / plan.g[0]);
-        int q0 = a0 - s0 * plan.g[0];
-        for (int d1 = -plan.r[1]; d1 <= plan.r[1]; ++d1) {
-            int a1 = c1 + d1;
-            int s1 = (int)floor((double)a1 / plan.g[1]);
-            int q1 = a1 - s1 * plan.g[1];
-            for (int d2 = -plan.r[2]; d2 <= plan.r[2]; ++d2) {
-                int a2 = c2 + d2;
-                int s2 = (int)floor((double)a2 / plan.g[2]);
-                int q2 = a2 - s2 * plan.g[2];
-                int q = (q0 * plan.g[1] + q1) * plan.g[2] + q2;
-                for (int p = w.cell_start[q]; p < w.cell_start[q + 1]; ++p) {
-                    int j = w.cell_atoms[p];
-                    // wrapped-frame image s -> original-frame image
-                    int n0 = s0 - w.wrap[3 * j] + wi0;
-                    int n1 = s1 - w.wrap[3 * j + 1] + wi1;
-                    int n2 = s2 - w.wrap[3 * j + 2] + wi2;
-                    double d = pair_dist_d(ci, w.cart + 3 * j, plan.L, n0, n1, n2);
-                    if (d <= cutoff && d > tol) f(j, n0, n1, n2, d);
-                }
-            }
-        }
-    }
-}
-
-__global__ void rg_count_kernel(int64_t n, RGPlan plan, RGWork w, double cutoff, double tol,
-                                int32_t *__restrict__ row_count) {
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    int cnt = 0;
-    rg_visit(i, plan, w, cutoff, tol, [&](int, int, int, int, double) { ++cnt; });
-    row_count[i] = cnt;
-}
-
 __device__ __forceinline__ bool key_less(int ja, const int *na, int jb, const int *nb) {
     if (ja != jb) return ja < jb;
     if (na[0] != nb[0]) return na[0] < nb[0];
@@ -263,45 +217,184 @@ __device__ __forceinline__ bool key_less(int ja, const int *na, int jb, const in
     return na[2] < nb[2];
 }
 
-__global__ void rg_fill_kernel(int64_t n, RGPlan plan, RGWork w, double cutoff, double tol,
-                               const int64_t *__restrict__ row_ptr, int32_t *__restrict__ center,
-                               int32_t *__restrict__ neighbor, int32_t *__restrict__ image,
-                               double *__restrict__ dist) {
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    int64_t b = row_ptr[i];
-    int64_t m = 0;
-    rg_visit(i, plan, w, cutoff, tol, [&](int j, int n0, int n1, int n2, double d) {
-        int64_t o = b + m++;
-        neighbor[o] = j;
-        image[3 * o] = n0;
-        image[3 * o + 1] = n1;
-        image[3 * o + 2] = n2;
-        dist[o] = d;
-    });
-    // insertion sort of this row by (neighbor, image) -- rows hold ~10^2 edges
-    for (int64_t a = 1; a < m; ++a) {
-        int ja = neighbor[b + a];
-        int na[3] = {image[3 * (b + a)], image[3 * (b + a) + 1], image[3 * (b + a) + 2]};
-        double da = dist[b + a];
-        int64_t p = a - 1;
-        while (p >= 0) {
-            int nb[3] = {image[3 * (b + p)], image[3 * (b + p) + 1], image[3 * (b + p) + 2]};
-            if (!key_less(ja, na, neighbor[b + p], nb)) break;
-            neighbor[b + p + 1] = neighbor[b + p];
-            image[3 * (b + p + 1)] = nb[0];
-            image[3 * (b + p + 1) + 1] = nb[1];
-            image[3 * (b + p + 1) + 2] = nb[2];
-            dist[b + p + 1] = dist[b + p];
-            --p;
-        }
-        neighbor[b + p + 1] = ja;
-        image[3 * (b + p + 1)] = na[0];
-        image[3 * (b + p + 1) + 1] = na[1];
-        image[3 * (b + p + 1) + 2] = na[2];
-        dist[b + p + 1] = da;
+// Count and fill passes, one wave per atom: the 64 lanes of a wave share the atom's
+// candidates.  The (2r+1)^3 candidate cells are taken 64 at a time (one per lane:
+// its cell id, image shift and atom range), a wave scan of the cell sizes gives each
+// chunk's candidate offsets, and every lane takes candidates k = lane, lane + 64, ...
+// (the cell found by binary search over the offsets); the candidate's image is the cell's
+// periodic shift in the wrapped frame taken back to the original frame.  An edge is
+// accepted when tol < |r_j + n L - r_i| <= cutoff (pair_dist_d, the oracle's expression).
+// Edges emitted by a fill are ordered by (neighbor, image): the key is unique within a
+// row, so every emission order gives the same row.
+#define RG_ROW_CAP 1024  // edges a wave sorts in LDS; longer rows sort in place in global
+
+struct RGChunk {
+    int off[65];  // candidate offset of each cell of the chunk (exclusive), off[64] = total
+    int start[64], q[64], s0[64], s1[64], s2[64];
+};
+
+// Load chunk `c0 .. c0+63` of the candidate cells of an atom in cell (c0_, c1_, c2_).
+__device__ __forceinline__ void rg_chunk(RGChunk &ch, const RGPlan &plan, const RGWork &w, int cell0, int ncells,
+                                         int a_c0, int a_c1, int a_c2, int lane) {
+    const int c = cell0 + lane;
+    int size = 0, st = 0, q = 0, s0 = 0, s1 = 0, s2 = 0;
+    if (c < ncells) {
+        const int n1 = 2 * plan.r[1] + 1, n2 = 2 * plan.r[2] + 1;
+        const int d0 = c / (n1 * n2) - plan.r[0], d1 = (c / n2) % n1 - plan.r[1], d2 = c % n2 - plan.r[2];
+        const int a0 = a_c0 + d0, a1 = a_c1 + d1, a2 = a_c2 + d2;
+        s0 = (int)floor((double)a0 / plan.g[0]);
+        s1 = (int)floor((double)a1 / plan.g[1]);
+        s2 = (int)floor((double)a2 / plan.g[2]);
+        const int q0 = a0 - s0 * plan.g[0], q1 = a1 - s1 * plan.g[1], q2 = a2 - s2 * plan.g[2];
+        q = (q0 * plan.g[1] + q1) * plan.g[2] + q2;
+        st = w.cell_start[q];
+        size = w.cell_start[q + 1] - st;
     }
-    for (int64_t a = 0; a < m; ++a) center[b + a] = (int32_t)i;
+    // inclusive wave scan of the sizes
+    int incl = size;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    ch.off[lane] = incl - size;
+    if (lane == 63) ch.off[64] = incl;
+    ch.start[lane] = st;
+    ch.q[lane] = q;
+    ch.s0[lane] = s0;
+    ch.s1[lane] = s1;
+    ch.s2[lane] = s2;
+}
+
+// Candidate k of the chunk: the cell cc with off[cc] <= k < off[cc + 1].
+__device__ __forceinline__ int rg_cell_of(const RGChunk &ch, int k) {
+    int lo = 0, hi = 63;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (ch.off[mid] <= k) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Visit every candidate of atom i with the wave; f(accept, j, n0, n1, n2, d) is called by
+// every lane on every round (accept false on idle lanes) so that it can use ballots.
+template <typename F>
+__device__ __forceinline__ void rg_visit_wave(int64_t i, const RGPlan &plan, const RGWork &w, double cutoff,
+                                              double tol, RGChunk &ch, int lane, F &&f) {
+    const double ci[3] = {w.cart[3 * i], w.cart[3 * i + 1], w.cart[3 * i + 2]};
+    const int cid = w.cell[i];
+    const int c2 = cid % plan.g[2], c1 = (cid / plan.g[2]) % plan.g[1], c0 = cid / (plan.g[2] * plan.g[1]);
+    const int wi0 = w.wrap[3 * i], wi1 = w.wrap[3 * i + 1], wi2 = w.wrap[3 * i + 2];
+    const int ncells = (2 * plan.r[0] + 1) * (2 * plan.r[1] + 1) * (2 * plan.r[2] + 1);
+    for (int cell0 = 0; cell0 < ncells; cell0 += 64) {
+        rg_chunk(ch, plan, w, cell0, ncells, c0, c1, c2, lane);
+        __syncthreads();  // one wave per work-group: orders the chunk's LDS writes and reads
+        const int total = ch.off[64];
+        for (int k0 = 0; k0 < total; k0 += 64) {
+            const int k = k0 + lane;
+            bool acc = false;
+            int j = 0, n0 = 0, n1 = 0, n2 = 0;
+            double d = 0.0;
+            if (k < total) {
+                const int cc = rg_cell_of(ch, k);
+                j = w.cell_atoms[ch.start[cc] + (k - ch.off[cc])];
+                n0 = ch.s0[cc] - w.wrap[3 * j] + wi0;
+                n1 = ch.s1[cc] - w.wrap[3 * j + 1] + wi1;
+                n2 = ch.s2[cc] - w.wrap[3 * j + 2] + wi2;
+                d = pair_dist_d(ci, w.cart + 3 * j, plan.L, n0, n1, n2);
+                acc = d <= cutoff && d > tol;
+            }
+            f(acc, j, n0, n1, n2, d);
+        }
+        __syncthreads();  // the chunk is read before the next one overwrites it
+    }
+}
+
+__global__ __launch_bounds__(64) void rg_count_wave_kernel(int64_t n, RGPlan plan, RGWork w, double cutoff,
+                                                           double tol, int32_t *__restrict__ row_count) {
+    __shared__ RGChunk ch;
+    const int64_t i = blockIdx.x;
+    const int lane = threadIdx.x;
+    int cnt = 0;
+    rg_visit_wave(i, plan, w, cutoff, tol, ch, lane, [&](bool acc, int, int, int, int, double) {
+        cnt += __popcll(__ballot(acc));
+    });
+    if (lane == 0) row_count[i] = cnt;
+}
+
+__global__ __launch_bounds__(64) void rg_fill_wave_kernel(int64_t n, RGPlan plan, RGWork w, double cutoff,
+                                                          double tol, const int64_t *__restrict__ row_ptr,
+                                                          int32_t *__restrict__ center, int32_t *__restrict__ neighbor,
+                                                          int32_t *__restrict__ image, double *__restrict__ dist) {
+    __shared__ RGChunk ch;
+    __shared__ int sj[RG_ROW_CAP], sn[RG_ROW_CAP][3];
+    __shared__ double sd[RG_ROW_CAP];
+    const int64_t i = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int64_t b = row_ptr[i];
+    const int64_t m = row_ptr[i + 1] - b;
+    const bool in_lds = m <= RG_ROW_CAP;
+    int64_t e = 0;  // edges emitted so far (wave-uniform)
+    rg_visit_wave(i, plan, w, cutoff, tol, ch, lane, [&](bool acc, int j, int n0, int n1, int n2, double d) {
+        const uint64_t bal = __ballot(acc);
+        const int64_t o = e + lanes_below(bal);
+        if (acc && o < m) {  // o < m always holds (count and fill accept the same edges)
+            if (in_lds) {
+                sj[o] = j;
+                sn[o][0] = n0;
+                sn[o][1] = n1;
+                sn[o][2] = n2;
+                sd[o] = d;
+            } else {
+                neighbor[b + o] = j;
+                image[3 * (b + o)] = n0;
+                image[3 * (b + o) + 1] = n1;
+                image[3 * (b + o) + 2] = n2;
+                dist[b + o] = d;
+            }
+        }
+        e += __popcll(bal);
+    });
+    if (in_lds) {
+        __syncthreads();
+        // rank sort: the unique key's rank is its position in the row
+        for (int a = lane; a < (int)m; a += 64) {
+            const int ja = sj[a];
+            const int na[3] = {sn[a][0], sn[a][1], sn[a][2]};
+            int rank = 0;
+            for (int c = 0; c < (int)m; ++c) rank += key_less(sj[c], sn[c], ja, na) ? 1 : 0;
+            neighbor[b + rank] = ja;
+            image[3 * (b + rank)] = na[0];
+            image[3 * (b + rank) + 1] = na[1];
+            image[3 * (b + rank) + 2] = na[2];
+            dist[b + rank] = sd[a];
+            center[b + rank] = (int32_t)i;
+        }
+    } else if (lane == 0) {
+        // a row longer than the LDS buffer: insertion sort in place (rows this long are rare)
+        for (int64_t a = 1; a < m; ++a) {
+            const int ja = neighbor[b + a];
+            const int na[3] = {image[3 * (b + a)], image[3 * (b + a) + 1], image[3 * (b + a) + 2]};
+            const double da = dist[b + a];
+            int64_t p = a - 1;
+            while (p >= 0) {
+                const int nb[3] = {image[3 * (b + p)], image[3 * (b + p) + 1], image[3 * (b + p) + 2]};
+                if (!key_less(ja, na, neighbor[b + p], nb)) break;
+                neighbor[b + p + 1] = neighbor[b + p];
+                image[3 * (b + p + 1)] = nb[0];
+                image[3 * (b + p + 1) + 1] = nb[1];
+                image[3 * (b + p + 1) + 2] = nb[2];
+                dist[b + p + 1] = dist[b + p];
+                --p;
+            }
+            neighbor[b + p + 1] = ja;
+            image[3 * (b + p + 1)] = na[0];
+            image[3 * (b + p + 1) + 1] = na[1];
+            image[3 * (b + p + 1) + 2] = na[2];
+            dist[b + p + 1] = da;
+        }
+        for (int64_t a = 0; a < m; ++a) center[b + a] = (int32_t)i;
+    }
 }
 
 static void rg_make_plan(const double *lattice_host, const int *grid_host, const int *search_host, RGPlan *plan) {
@@ -360,7 +453,7 @@ extern "C" int matris_radius_graph_count(int64_t n, const double *frac, const do
     if (rc) return rc;
     fill<int>(w.cursor, ncell, 0, st);
     rg_scatter_kernel<<<matris_blocks(n, 256), 256, 0, st>>>(n, w);
-    rg_count_kernel<<<matris_blocks(n, 64), 64, 0, st>>>(n, plan, w, cutoff, tol, row_count);
+    rg_count_wave_kernel<<<(unsigned)n, 64, 0, st>>>(n, plan, w, cutoff, tol, row_count);
     MATRIS_CHECK_LAUNCH();
     return scan_exclusive<int32_t, int64_t>(row_count, n, row_ptr, w.scan_ws, st);
 }
@@ -375,8 +468,8 @@ extern "C" int matris_radius_graph_fill(int64_t n, const double *lattice_host, d
     rg_make_plan(lattice_host, grid_host, search_host, &plan);
     int64_t ncell = (int64_t)plan.g[0] * plan.g[1] * plan.g[2];
     RGWork w = rg_carve(workspace, n, ncell);
-    rg_fill_kernel<<<matris_blocks(n, 64), 64, 0, (hipStream_t)stream>>>(n, plan, w, cutoff, tol, row_ptr, center,
-                                                                          neighbor, image, dist);
+    rg_fill_wave_kernel<<<(unsigned)n, 64, 0, (hipStream_t)stream>>>(n, plan, w, cutoff, tol, row_ptr, center,
+                                                                       neighbor, image, dist);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

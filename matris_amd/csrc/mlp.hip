@@ -13,6 +13,7 @@
 // tiles (p, h, g_h) stay in LDS.  The GEMMs run transposed (weight fragment as the MFMA A
 // operand, rows in lanes), so results reach LDS with 16-byte writes.  Outputs leave
 // through LDS with 16-byte row stores.
+#include <algorithm>
 #include <initializer_list>
 
 #include "mma.h"
@@ -109,6 +110,184 @@ __global__ __launch_bounds__(256, 3) void ffn_fwd_kernel(int64_t M, const float 
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
     store_tile128(T, out, MATRIS_D, m0, M, tid, res, res_w);
+    report_range<MODE>(amax, range_flag);
+}
+
+// ------------------------------------------------------------------------------------
+// Weight-stationary persistent forms (modes with two fragment planes: 0, 2, 3)
+// ------------------------------------------------------------------------------------
+// The weights are small (128 x 128 per layer), so each wave keeps its 32 output columns
+// of both layers in registers for the whole launch (8 k-blocks x 2 planes x 2 layers =
+// 128 VGPRs) and the work-groups loop over 64-row tiles.  The next tile's rows are
+// loaded into registers while the current tile computes; a tile is staged into LDS
+// already split into fragment planes, once; outputs leave straight from the transposed
+// accumulators (lane = row, 16-byte column runs).  With no weight loads inside the loop,
+// no load waits behind the previous tile's stores (vmcnt counts both).
+
+// Fragment planes of 4 consecutive k values (half of a fragment unit): p0, p1 as 8 bytes
+// each (MODE 2: fp16 hi / lo; MODE 3: bf16 hi / mid).  MODE 0 keeps fp32 (see hfrag_put).
+template <int MODE>
+__device__ __forceinline__ void frag4(const float4 &v, uint2 &p0, uint2 &p1) {
+    if constexpr (MODE == 2) {
+        const f2v x0 = {v.x, v.y}, x1 = {v.z, v.w};
+        const h2v h0 = __builtin_convertvector(x0, h2v), h1 = __builtin_convertvector(x1, h2v);
+        const h2v l0 = __builtin_convertvector((x0 - __builtin_convertvector(h0, f2v)) * 2048.0f, h2v);
+        const h2v l1 = __builtin_convertvector((x1 - __builtin_convertvector(h1, f2v)) * 2048.0f, h2v);
+        p0 = make_uint2(bitcast<uint32_t>(h0), bitcast<uint32_t>(h1));
+        p1 = make_uint2(bitcast<uint32_t>(l0), bitcast<uint32_t>(l1));
+    } else {
+        Frag<MODE> f;
+        make_frag<MODE>(f, v, v);
+        p0 = make_uint2(f.p[0].x, f.p[0].y);
+        p1 = make_uint2(f.p[1].x, f.p[1].y);
+    }
+}
+
+// Store 4 values (k = 4h .. 4h+3 of fragment unit `unit`, lane `fl`) of a two-plane
+// fragment buffer laid out [unit][plane][64 lanes] x 16 bytes.
+template <int MODE>
+__device__ __forceinline__ void hfrag_put(uint4 *buf, int unit, int fl, int h, const float4 &v) {
+    if constexpr (MODE == 0) {
+        buf[(unit * 2 + h) * 64 + fl] = bitcast<uint4>(v);
+    } else {
+        uint2 p0, p1;
+        frag4<MODE>(v, p0, p1);
+        reinterpret_cast<uint2 *>(buf + (unit * 2 + 0) * 64 + fl)[h] = p0;
+        reinterpret_cast<uint2 *>(buf + (unit * 2 + 1) * 64 + fl)[h] = p1;
+    }
+}
+
+// Resident weight fragments of output tile nt (8 k-blocks, two planes) of a packed
+// [*, 128] weight.
+__device__ __forceinline__ void load_wres(uint4 (&w)[8][2], const uint4 *__restrict__ W, int nt, int lane) {
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) w[kb][pl] = W[((nt * 8 + kb) * 2 + pl) * 64 + lane];
+}
+
+// acc += (W tile) * (row tile rt of a fragment buffer)^T over one k-block, W resident.
+template <int MODE, int KB>
+__device__ __forceinline__ void gemm_res_kb(v16f &acc, const uint4 (&w)[8][2], const uint4 *buf, int rt, int lane) {
+    Frag<MODE> wf, a;
+    wf.p[0] = w[KB][0];
+    wf.p[1] = w[KB][1];
+    // MODE 2's derived plane is loop-invariant; made opaque here, it is recomputed at use
+    // instead of being hoisted out of the tile loop (64 more live VGPRs)
+    if constexpr (MODE == 2) asm volatile("" : "+v"(wf.p[0].x), "+v"(wf.p[0].y), "+v"(wf.p[0].z), "+v"(wf.p[0].w));
+    prep_w<MODE>(wf);
+    a.p[0] = buf[((rt * 8 + KB) * 2 + 0) * 64 + lane];
+    a.p[1] = buf[((rt * 8 + KB) * 2 + 1) * 64 + lane];
+    mma_wx<MODE>(acc, wf, a);
+}
+
+// The 8 k-blocks, unrolled by hand (constant register indices for the resident weights).
+template <int MODE>
+__device__ __forceinline__ void gemm_res(v16f &acc, const uint4 (&w)[8][2], const uint4 *buf, int rt, int lane) {
+    gemm_res_kb<MODE, 0>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 1>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 2>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 3>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 4>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 5>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 6>(acc, w, buf, rt, lane);
+    gemm_res_kb<MODE, 7>(acc, w, buf, rt, lane);
+}
+
+// Rows of a [*, 128] array for tile rows m0 .. m0+63, 512 threads: thread (row tid/8,
+// 8-column groups q and q+8 for q = tid%8); rows past M read row M-1.
+__device__ __forceinline__ void load_rows4(float4 (&xr)[4], const float *__restrict__ x, int64_t m0, int64_t M,
+                                           int tid) {
+    const int64_t row = min(m0 + (tid >> 3), M - 1);
+    const float4 *p = reinterpret_cast<const float4 *>(x + row * MATRIS_D) + (tid & 7) * 2;
+    xr[0] = p[0];
+    xr[1] = p[1];
+    xr[2] = p[16];
+    xr[3] = p[17];
+}
+
+// Stage those rows as fragment planes: group g of row r is fragment unit (r/32) * 8 + g/2,
+// lane r%32 + 32 (g%2).
+template <int MODE>
+__device__ __forceinline__ float stage_rows4(uint4 *buf, const float4 (&xr)[4], int tid, float amax) {
+    const int r = tid >> 3, q = tid & 7;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int g = q + 8 * i;
+        const int unit = (r >> 5) * 8 + (g >> 1), fl = (r & 31) + 32 * (g & 1);
+        amax = frag_amax<MODE>(amax, xr[2 * i], xr[2 * i + 1]);
+        Frag<MODE> f;
+        make_frag<MODE>(f, xr[2 * i], xr[2 * i + 1]);
+        buf[(unit * 2 + 0) * 64 + fl] = f.p[0];
+        buf[(unit * 2 + 1) * 64 + fl] = f.p[1];
+    }
+    return amax;
+}
+
+// FFN forward, weight-stationary: 512 threads = 8 waves; wave w owns output columns
+// [32 (w%4), +32) of both layers and rows [32 (w/4), +32) of each 64-row tile.
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void ffn_fwd_ws_kernel(int64_t M, const float *__restrict__ x,
+                                                            const uint4 *__restrict__ W1,
+                                                            const uint4 *__restrict__ W2, float *__restrict__ out,
+                                                            float *__restrict__ save_p, const float *__restrict__ res,
+                                                            const float *__restrict__ res_w, unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes only");
+    __shared__ uint4 Xf[2 * 8 * 2 * 64];  // x tile as fragment planes (32 KB)
+    __shared__ uint4 Hf[2 * 8 * 2 * 64];  // h = SiLU(p) tile, the same layout
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int ct = wave & 3, rt = wave >> 2;
+    const float w1s = take_wscale<MODE>(W1), w2s = take_wscale<MODE>(W2);
+    uint4 w1[8][2], w2[8][2];
+    load_wres(w1, W1, ct, lane);
+    load_wres(w2, W2, ct, lane);
+    const int64_t ntiles = (M + BM - 1) / BM;
+    float amax = 0.f;
+    float4 xr[4];
+    int64_t tile = blockIdx.x;
+    load_rows4(xr, x, tile * BM, M, tid);
+#pragma unroll 1
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t m0 = tile * BM;
+        amax = stage_rows4<MODE>(Xf, xr, tid, amax);
+        __syncthreads();  // x staged; every wave is past the previous tile's GEMM2
+        load_rows4(xr, x, min(tile + (int64_t)gridDim.x, ntiles - 1) * BM, M, tid);  // next tile
+        v16f acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, w1, Xf, rt, lane);
+        // p (saved) and h = SiLU(p) into the second fragment buffer: lane (row l32, half h)
+        // holds columns 32 ct + 8 j + 4 h .. +3, i.e. half h of fragment unit
+        // (rt, k-block 2 ct + j/2), lane l32 + 32 (j%2)
+        const int64_t row = m0 + rt * 32 + l32;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float4 v = make_float4(acc[4 * j] * w1s, acc[4 * j + 1] * w1s, acc[4 * j + 2] * w1s, acc[4 * j + 3] * w1s);
+            if (save_p && row < M)
+                *reinterpret_cast<float4 *>(save_p + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) = v;
+            v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
+            amax = frag_amax<MODE>(amax, v, v);
+            hfrag_put<MODE>(Hf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, v);
+        }
+        __syncthreads();  // h complete; every wave is past GEMM1 (Xf free)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, w2, Hf, rt, lane);
+        if (row < M) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = ct * 32 + 8 * j + 4 * h;
+                float4 v = make_float4(acc[4 * j] * w2s, acc[4 * j + 1] * w2s, acc[4 * j + 2] * w2s,
+                                       acc[4 * j + 3] * w2s);
+                if (res) {
+                    const float4 r = *reinterpret_cast<const float4 *>(res + row * MATRIS_D + col);
+                    const float4 rw = *reinterpret_cast<const float4 *>(res_w + col);
+                    v.x += rw.x * r.x; v.y += rw.y * r.y; v.z += rw.z * r.z; v.w += rw.w * r.w;
+                }
+                *reinterpret_cast<float4 *>(out + row * MATRIS_D + col) = v;
+            }
+        }
+    }
     report_range<MODE>(amax, range_flag);
 }
 
@@ -236,12 +415,40 @@ static bool mlp_args_ok(int mode, std::initializer_list<const void *> ptrs) {
     return true;
 }
 
+// Work-groups of a persistent launch: one 512-thread work-group per CU (the register
+// budget of the weight-stationary kernels), never more than the tiles.
+static dim3 persistent_grid(int64_t m) {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus[dev] = 256;
+    const int64_t tiles = matris_blocks(m, BM);
+    return dim3((unsigned)std::min<int64_t>(tiles, (int64_t)cus[dev]));
+}
+
 extern "C" int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, float *out,
                               float *save_p, const float *res, const float *res_w, int mode, void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {x, w1p, w2p, out}) || ((uintptr_t)save_p & 15)) return MATRIS_E_ARG;
     if (res && (((uintptr_t)res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(ffn_fwd_kernel, m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p, res, res_w);
+    if (mode == 6) {
+        MLP_DISPATCH(ffn_fwd_kernel, m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p, res, res_w);
+    } else {
+        unsigned *flag = nullptr;
+        if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+        const dim3 grid = persistent_grid(m);
+        hipStream_t st = (hipStream_t)stream;
+        if (mode == 0)
+            ffn_fwd_ws_kernel<0><<<grid, 512, 0, st>>>(m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p, res,
+                                                       res_w, flag);
+        else if (mode == 2)
+            ffn_fwd_ws_kernel<2><<<grid, 512, 0, st>>>(m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p, res,
+                                                       res_w, flag);
+        else
+            ffn_fwd_ws_kernel<3><<<grid, 512, 0, st>>>(m, x, (const uint4 *)w1p, (const uint4 *)w2p, out, save_p, res,
+                                                       res_w, flag);
+    }
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

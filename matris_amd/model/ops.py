@@ -63,12 +63,15 @@ def f16_range_take(device=None) -> bool:
 # Optional per-launch timing (bench.py): name -> list of (start, end, info) HIP events
 # recorded on the launch stream around each kernel call.
 _TIMING: dict | None = None
+_TIMING_ONLY: frozenset | None = None
 
 
-def enable_timing(on: bool = True) -> dict | None:
-    """Start (or stop) recording HIP events around every kernel launch of this module."""
-    global _TIMING
+def enable_timing(on: bool = True, only=None) -> dict | None:
+    """Start (or stop) recording HIP events around the kernel launches of this module: all
+    of them, or only the launch names in `only` (fewer events, less host overhead)."""
+    global _TIMING, _TIMING_ONLY
     _TIMING = {} if on else None
+    _TIMING_ONLY = frozenset(only) if (on and only is not None) else None
     return _TIMING
 
 
@@ -79,7 +82,7 @@ class _timed:
         self.name, self.info, self.ev = name, info, None
 
     def __enter__(self):
-        if _TIMING is not None:
+        if _TIMING is not None and (_TIMING_ONLY is None or self.name in _TIMING_ONLY):
             self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             self.ev[0].record()
 
