@@ -106,8 +106,12 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     if (nsrc > 2) sr2 = src.idx[2] ? (int64_t)src.idx[2][grow] : grow;
     if (nsrc > 3) sr3 = src.idx[3] ? (int64_t)src.idx[3][grow] : grow;
 
-    float4 x0, x1;
-#define GMLP_LOADX(kc)                                                                                   \
+    // Prefetch depth: two register sets of gathered X (A, B) -- chunk c+1 is converted
+    // from one set while chunk c+3 loads into it -- and the weight fragments in a ring of
+    // four, three k-blocks ahead; the loop body covers two chunks so that every ring slot
+    // is a fixed register set.
+    float4 xa0, xa1, xb0, xb1;
+#define GMLP_LOADX(kc, r0, r1)                                                                           \
     do {                                                                                                 \
         const int j_ = (kc) >> 7, cc_ = (kc) & 127;                                                      \
         const float *sp_ = j_ == 0 ? src.ptr[0] + sr0 * MATRIS_D                                         \
@@ -115,50 +119,58 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                          : j_ == 2 ? src.ptr[2] + sr2 * MATRIS_D                                         \
                                    : src.ptr[3] + sr3 * MATRIS_D;                                        \
         const float4 *xp_ = reinterpret_cast<const float4 *>(sp_ + cc_ + xc);                            \
-        x0 = xp_[0];                                                                                     \
-        x1 = xp_[1];                                                                                     \
+        r0 = xp_[0];                                                                                     \
+        r1 = xp_[1];                                                                                     \
     } while (0)
-#define GMLP_STOREX(buf)                                                                                 \
+#define GMLP_STOREX(buf, r0, r1)                                                                         \
     do {                                                                                                 \
         Frag<MODE> f_;                                                                                   \
-        amax = frag_amax<MODE>(amax, x0, x1);                                                            \
-        make_frag<MODE>(f_, x0, x1);                                                                     \
+        amax = frag_amax<MODE>(amax, r0, r1);                                                            \
+        make_frag<MODE>(f_, r0, r1);                                                                     \
         _Pragma("unroll") for (int pl_ = 0; pl_ < NPL; ++pl_) Xp[(buf) * CHUNK + xslot + pl_ * 64] = f_.p[pl_]; \
+    } while (0)
+#define GMLP_SUB(kb, sub, xb, BCUR, BPF)                                                                 \
+    do {                                                                                                 \
+        load_bfrags<MODE, 2>(BPF, W1, 2 * wave, KB, min((kb) + BDIST, KB - 1), lane);                    \
+        __builtin_amdgcn_sched_barrier(0);                                                               \
+        Frag<MODE> a[2];                                                                                 \
+        _Pragma("unroll") for (int rt = 0; rt < 2; ++rt)                                                 \
+            _Pragma("unroll") for (int pl = 0; pl < NPL; ++pl)                                           \
+                a[rt].p[pl] = xb[((rt * 2 + (sub)) * NPL + pl) * 64 + lane];                             \
+        prep_w<MODE>(BCUR[0]);                                                                           \
+        prep_w<MODE>(BCUR[1]);                                                                           \
+        _Pragma("unroll") for (int rt = 0; rt < 2; ++rt)                                                 \
+            _Pragma("unroll") for (int ct = 0; ct < 2; ++ct) mma_wx<MODE>(acc[rt][ct], BCUR[ct], a[rt]); \
+    } while (0)
+#define GMLP_CHUNK(c, r0, r1, BS0, BS1, BP0, BP1)                                                        \
+    do {                                                                                                 \
+        const uint4 *xb = Xp + ((c) & 1) * CHUNK;                                                        \
+        GMLP_SUB(2 * (c), 0, xb, BS0, BP0);                                                              \
+        GMLP_SUB(2 * (c) + 1, 1, xb, BS1, BP1);                                                          \
+        GMLP_STOREX(((c) + 1) & 1, r0, r1); /* chunk c+1; unread after the last chunk */                 \
+        GMLP_LOADX(min((c) + 3, nchunk - 1) * 32, r0, r1);                                               \
+        __syncthreads();                                                                                 \
     } while (0)
 
     v16f acc[2][2];
     zero_acc(acc);
-    Frag<MODE> bcur[2], bnxt[2];
-    load_bfrags<MODE, 2>(bcur, W1, 2 * wave, KB, 0, lane);
-    GMLP_LOADX(0);
-    GMLP_STOREX(0);
+    constexpr int BDIST = 3;
+    Frag<MODE> bq0[2], bq1[2], bq2[2], bq3[2];
+    load_bfrags<MODE, 2>(bq0, W1, 2 * wave, KB, 0, lane);
+    load_bfrags<MODE, 2>(bq1, W1, 2 * wave, KB, min(1, KB - 1), lane);
+    load_bfrags<MODE, 2>(bq2, W1, 2 * wave, KB, min(2, KB - 1), lane);
+    GMLP_LOADX(0, xa0, xa1);
+    GMLP_STOREX(0, xa0, xa1);
+    GMLP_LOADX(min(1, nchunk - 1) * 32, xa0, xa1);
+    GMLP_LOADX(min(2, nchunk - 1) * 32, xb0, xb1);
     __syncthreads();
 #pragma unroll 1
-    for (int c = 0; c < nchunk; ++c) {
-        GMLP_LOADX(min(c + 1, nchunk - 1) * 32);  // the last iteration reloads its own chunk
-        const uint4 *xb = Xp + (c & 1) * CHUNK;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            const int kb = 2 * c + sub;
-            load_bfrags<MODE, 2>(bnxt, W1, 2 * wave, KB, min(kb + 1, KB - 1), lane);
-            __builtin_amdgcn_sched_barrier(0);  // issue the prefetches before this step's MFMAs
-            Frag<MODE> a[2];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                for (int pl = 0; pl < NPL; ++pl) a[rt].p[pl] = xb[((rt * 2 + sub) * NPL + pl) * 64 + lane];
-            prep_w<MODE>(bcur[0]);
-            prep_w<MODE>(bcur[1]);
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) mma_wx<MODE>(acc[rt][ct], bcur[ct], a[rt]);  // P^T tiles
-            bcur[0] = bnxt[0];
-            bcur[1] = bnxt[1];
-        }
-        GMLP_STOREX((c + 1) & 1);  // unread after the last chunk
-        __syncthreads();
+    for (int c = 0; c < nchunk; c += 2) {  // nchunk = 4 nsrc is even
+        GMLP_CHUNK(c, xa0, xa1, bq0, bq1, bq3, bq0);
+        GMLP_CHUNK(c + 1, xb0, xb1, bq2, bq3, bq1, bq2);
     }
+#undef GMLP_CHUNK
+#undef GMLP_SUB
 #undef GMLP_LOADX
 #undef GMLP_STOREX
 

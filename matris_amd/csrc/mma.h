@@ -272,32 +272,74 @@ __device__ __forceinline__ void lds_afrags(Frag<MODE> (&a)[NRT], const float *ba
 // (four runs of four consecutive columns) -- a layout with whole rows in lanes.
 // Returns the running max |A| of a MODE 2 conversion (0 otherwise).  MODE 2 sums carry the
 // weight's scale s: the caller applies scale_acc once its last product is in.
+// One k-block of gemm_lds_packed: prefetch k-block `kpf` into BPF, then accumulate
+// k-block `kb` (A from LDS, B = BCUR).
+template <int MODE, int NRT, int NCT, bool TRANS>
+__device__ __forceinline__ void gemm_lds_step(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
+                                              const uint4 *__restrict__ W, int nt0, int KBW, int kb, int kpf,
+                                              Frag<MODE> (&BCUR)[NCT], Frag<MODE> (&BPF)[NCT], int lane,
+                                              float &amax) {
+    load_bfrags<MODE, NCT>(BPF, W, nt0, KBW, kpf, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
+    Frag<MODE> a[NRT];
+    lds_afrags<MODE, NRT>(a, a_base, lda, kb, lane, amax);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) prep_w<MODE>(BCUR[ct]);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+            if constexpr (TRANS)
+                mma_wx<MODE>(acc[rt][ct], BCUR[ct], a[rt]);
+            else
+                mma_xw<MODE>(acc[rt][ct], a[rt], BCUR[ct]);
+        }
+}
+
+// acc[rt][ct] += A[rt tile, k-blocks 0..KBA) * B[k-blocks kb0.., tile nt0 + ct] with A an
+// fp32 row-major LDS array and B a packed weight (KBW k-blocks).  With two output tiles
+// per wave in a two-plane mode the B fragments are prefetched three k-blocks ahead in a
+// ring of four register sets; otherwise one ahead (MODE 6's three planes, or one-tile
+// kernels, whose occupancy the deeper ring would lower).  Prefetches past the end reload
+// the last k-block, so the compiler's load counting stays exact.
+// TRANS computes the transposed product instead, acc[rt][ct] = (B^T A^T) tile: the packed
+// weight fragment is the MFMA A operand and the LDS rows the B operand, so lane l holds
+// row rt*32 + l%32 of A and its 16 registers are output columns ct*32 + acc_row(i, l/32)
+// (four runs of four consecutive columns) -- a layout with whole rows in lanes.
+// Returns the running max |A| of a MODE 2 conversion (0 otherwise).  MODE 2 sums carry the
+// weight's scale s: the caller applies scale_acc once its last product is in.
 template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false>
 __device__ __forceinline__ float gemm_lds_packed(v16f (&acc)[NRT][NCT], const float *a_base, int lda,
                                                  const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
-    constexpr int kUnroll = NCT >= 2 ? 1 : 2;  // 2-tile bodies are long enough; keeps pressure down
     float amax = 0.f;
-    Frag<MODE> cur[NCT], nxt[NCT];
-    load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
+    if constexpr (Npl<MODE>::v == 2 && NCT == 2) {
+        static_assert(KBA % 4 == 0, "ring of four");
+        Frag<MODE> b0[NCT], b1[NCT], b2[NCT], b3[NCT];
+        load_bfrags<MODE, NCT>(b0, W, nt0, KBW, kb0, lane);
+        load_bfrags<MODE, NCT>(b1, W, nt0, KBW, kb0 + 1, lane);
+        load_bfrags<MODE, NCT>(b2, W, nt0, KBW, kb0 + 2, lane);
+#pragma unroll 1
+        for (int kb = 0; kb < KBA; kb += 4) {
+            gemm_lds_step<MODE, NRT, NCT, TRANS>(acc, a_base, lda, W, nt0, KBW, kb, kb0 + min(kb + 3, KBA - 1), b0,
+                                                 b3, lane, amax);
+            gemm_lds_step<MODE, NRT, NCT, TRANS>(acc, a_base, lda, W, nt0, KBW, kb + 1, kb0 + min(kb + 4, KBA - 1),
+                                                 b1, b0, lane, amax);
+            gemm_lds_step<MODE, NRT, NCT, TRANS>(acc, a_base, lda, W, nt0, KBW, kb + 2, kb0 + min(kb + 5, KBA - 1),
+                                                 b2, b1, lane, amax);
+            gemm_lds_step<MODE, NRT, NCT, TRANS>(acc, a_base, lda, W, nt0, KBW, kb + 3, kb0 + min(kb + 6, KBA - 1),
+                                                 b3, b2, lane, amax);
+        }
+    } else {
+        constexpr int kUnroll = NCT >= 2 ? 1 : 2;  // 2-tile bodies are long enough; keeps pressure down
+        Frag<MODE> cur[NCT], nxt[NCT];
+        load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
 #pragma unroll kUnroll
-    for (int kb = 0; kb < KBA; ++kb) {
-        load_bfrags<MODE, NCT>(nxt, W, nt0, KBW, kb0 + min(kb + 1, KBA - 1), lane);
-        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
-        Frag<MODE> a[NRT];
-        lds_afrags<MODE, NRT>(a, a_base, lda, kb, lane, amax);
+        for (int kb = 0; kb < KBA; ++kb) {
+            gemm_lds_step<MODE, NRT, NCT, TRANS>(acc, a_base, lda, W, nt0, KBW, kb, kb0 + min(kb + 1, KBA - 1), cur,
+                                                 nxt, lane, amax);
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) prep_w<MODE>(cur[ct]);
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-                if constexpr (TRANS)
-                    mma_wx<MODE>(acc[rt][ct], cur[ct], a[rt]);
-                else
-                    mma_xw<MODE>(acc[rt][ct], a[rt], cur[ct]);
-            }
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
+            for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
+        }
     }
     return amax;
 }
