@@ -22,7 +22,9 @@
 //
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
-// tiling, with packed transposed weights as B operands.
+// tiling, with packed transposed weights.  In the two-plane modes g_z and g_p are stored
+// in LDS already split into fragment units by the pass that produces them, so neither
+// GEMM converts anything (g_p is otherwise re-split by every wave of every column pass).
 //
 // This file also owns the device word that MODE 2 (fp16 split) kernels of every GEMM
 // file flag when an activation exceeds the fp16 range (matris_f16_range_take).
@@ -175,7 +177,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 #undef GMLP_STOREX
 
     // p = acc + b1 -> LDS (rows in lanes: 16-byte writes); one pass copies p out with
-    // 16-byte row stores and turns it into h = SiLU(p) in place
+    // 16-byte row stores and turns it into h = SiLU(p) in place.  (Pre-splitting h into
+    // fragment units here, as the backward does for g_z / g_p, measured slower: it costs
+    // a barrier and 24 more VGPRs for a conversion that two waves share.)
     scale_acc<MODE>(acc, w1s);
     acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b1);
     __syncthreads();
@@ -292,6 +296,11 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                                           int acc0, const float *__restrict__ res_w,
                                                           unsigned *range_flag) {
     __shared__ __align__(16) float G[BM * LDH];
+    // Two-plane modes keep g_z, then g_p, in G pre-split into fragment units
+    // [rt 2][kb 16][plane 2][64 lanes] (64 KB, converted once by their writer); MODE 6
+    // keeps fp32 rows and converts at each fragment read.
+    constexpr bool PS = Npl<MODE>::v == 2;
+    uint4 *Gf = reinterpret_cast<uint4 *>(G);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
@@ -351,15 +360,30 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                 dgs += gng[e] * ng[e];
             }
             const float dc = row16_sum(dcs) * (1.0f / MATRIS_D), dg = row16_sum(dgs) * (1.0f / MATRIS_D);
-            float *gr = G + row * LDH + c8;
+            float4 vc[2], vg[2];
 #pragma unroll
             for (int e4 = 0; e4 < 2; ++e4) {
-                *reinterpret_cast<float4 *>(gr + 4 * e4) =
-                    make_float4((gnc[4 * e4] - nc[4 * e4] * dc) * rc, (gnc[4 * e4 + 1] - nc[4 * e4 + 1] * dc) * rc,
-                                (gnc[4 * e4 + 2] - nc[4 * e4 + 2] * dc) * rc, (gnc[4 * e4 + 3] - nc[4 * e4 + 3] * dc) * rc);
-                *reinterpret_cast<float4 *>(gr + MATRIS_D + 4 * e4) =
-                    make_float4((gng[4 * e4] - ng[4 * e4] * dg) * rg, (gng[4 * e4 + 1] - ng[4 * e4 + 1] * dg) * rg,
-                                (gng[4 * e4 + 2] - ng[4 * e4 + 2] * dg) * rg, (gng[4 * e4 + 3] - ng[4 * e4 + 3] * dg) * rg);
+                vc[e4] = make_float4((gnc[4 * e4] - nc[4 * e4] * dc) * rc, (gnc[4 * e4 + 1] - nc[4 * e4 + 1] * dc) * rc,
+                                     (gnc[4 * e4 + 2] - nc[4 * e4 + 2] * dc) * rc,
+                                     (gnc[4 * e4 + 3] - nc[4 * e4 + 3] * dc) * rc);
+                vg[e4] = make_float4((gng[4 * e4] - ng[4 * e4] * dg) * rg, (gng[4 * e4 + 1] - ng[4 * e4 + 1] * dg) * rg,
+                                     (gng[4 * e4 + 2] - ng[4 * e4 + 2] * dg) * rg,
+                                     (gng[4 * e4 + 3] - ng[4 * e4 + 3] * dg) * rg);
+            }
+            if constexpr (PS) {
+                // g_z columns c8 .. c8+7 (core) and 128 + c8 .. (gate) of this row: one
+                // fragment unit each, (rt = row/32, kb = c8/16 (+8), lane row%32 + 32 (c8/8 % 2))
+                const int unit = (row >> 5) * 16 + (c8 >> 4), fl = (row & 31) + 32 * ((c8 >> 3) & 1);
+                amax = frag_amax<MODE>(frag_amax<MODE>(amax, vc[0], vc[1]), vg[0], vg[1]);
+                frag_put8<MODE>(Gf, unit, fl, vc[0], vc[1]);
+                frag_put8<MODE>(Gf, unit + 8, fl, vg[0], vg[1]);
+            } else {
+                float *gr = G + row * LDH + c8;
+#pragma unroll
+                for (int e4 = 0; e4 < 2; ++e4) {
+                    *reinterpret_cast<float4 *>(gr + 4 * e4) = vc[e4];
+                    *reinterpret_cast<float4 *>(gr + MATRIS_D + 4 * e4) = vg[e4];
+                }
             }
         }
     }
@@ -367,28 +391,64 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 
     // phase 2: g_h = g_z W2 (block diagonal); wave w -> columns [64w, 64w+64).  W2t is
     // packed from [W2c^T ; W2g^T] ([256, 128]), so output tile nt reads block nt / 4.
+    // g_p = g_h * SiLU'(p); rows past M read row 0 of the tile (their results are unused).
     const int blk = wave >> 1;
-    v16f acc[2][2];
-    zero_acc(acc);
-    amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, G + blk * MATRIS_D, LDH, W2t, 2 * wave, MATRIS_D / 16, 0,
-                                                      lane);
-    scale_acc<MODE>(acc, w2s);
-    // g_p = g_h * SiLU'(p); rows past M read row 0 of the tile (their results are unused)
     const int nrows = (int)min((int64_t)BM, M - m0);
     const float *__restrict__ Pt = P + m0 * 256;
+    v16f acc[2][2];
+    zero_acc(acc);
+    if constexpr (PS) {
+        // transposed (rows in lanes): lane (row rt*32 + l32, half h) holds columns
+        // 64 wave + 32 ct + 8 j + 4 h .. +3, read from P as 16-byte runs and written back
+        // as half fragment units of g_p
+        gemm_frag_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Gf, 16, blk * 8, W2t, 2 * wave, MATRIS_D / 16, 0,
+                                                          lane);
+        scale_acc<MODE>(acc, w2s);
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-        const int col = wave * 64 + ct * 32 + l32;
+        for (int rt = 0; rt < 2; ++rt) {
+            const int row = rt * 32 + l32;
+            const float *pr = Pt + (row < nrows ? row : 0) * 256 + wave * 64 + 4 * h;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 pv = *reinterpret_cast<const float4 *>(pr + ct * 32 + 8 * j);
+                    acc[rt][ct][4 * j] *= dsilu_f(pv.x);
+                    acc[rt][ct][4 * j + 1] *= dsilu_f(pv.y);
+                    acc[rt][ct][4 * j + 2] *= dsilu_f(pv.z);
+                    acc[rt][ct][4 * j + 3] *= dsilu_f(pv.w);
+                }
+        }
+        __syncthreads();  // every wave is done reading g_z
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = rt * 32 + acc_row(i, h);
-                acc[rt][ct][i] *= dsilu_f(Pt[(row < nrows ? row : 0) * 256 + col]);
-            }
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 v = make_float4(acc[rt][ct][4 * j], acc[rt][ct][4 * j + 1], acc[rt][ct][4 * j + 2],
+                                                 acc[rt][ct][4 * j + 3]);
+                    amax = frag_amax<MODE>(amax, v, v);
+                    frag_put4<MODE>(Gf, rt * 16 + 4 * wave + 2 * ct + (j >> 1), l32 + 32 * (j & 1), h, v);
+                }
+    } else {
+        amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16>(acc, G + blk * MATRIS_D, LDH, W2t, 2 * wave, MATRIS_D / 16,
+                                                          0, lane);
+        scale_acc<MODE>(acc, w2s);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int col = wave * 64 + ct * 32 + l32;
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = rt * 32 + acc_row(i, h);
+                    acc[rt][ct][i] *= dsilu_f(Pt[(row < nrows ? row : 0) * 256 + col]);
+                }
+        }
+        __syncthreads();  // every wave is done reading g_z
+        acc_to_lds<2>(acc, G, LDH, wave * 64, lane);
     }
-    __syncthreads();  // every wave is done reading g_z
-    acc_to_lds<2>(acc, G, LDH, wave * 64, lane);
     __syncthreads();
 
     // phase 3: g_x = g_p W1.  W1t is W1^T ([K, 256]) packed: output tile nt = column / 32,
@@ -408,7 +468,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         v16f a2[2][1];
         zero_acc(a2);
         const int col0 = cb + wave * 32;
-        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
+        if constexpr (PS)
+            gemm_frag_packed<MODE, 2, 1, 256 / 16>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
+        else
+            amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
         scale_acc<MODE>(a2, w1s);
         if (cb > 0 || !epi0) store_acc_rows<1>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {  // K == 128: every wave holds source-0 columns
@@ -420,7 +483,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         v16f a2[2][2];
         zero_acc(a2);
         const int col0 = cb + wave * 64;
-        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
+        if constexpr (PS)
+            gemm_frag_packed<MODE, 2, 2, 256 / 16>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
+        else
+            amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
         scale_acc<MODE>(a2, w1s);
         if (col0 >= MATRIS_D || !epi0) store_acc_rows<2>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {

@@ -124,39 +124,6 @@ __global__ __launch_bounds__(256, 3) void ffn_fwd_kernel(int64_t M, const float 
 // accumulators (lane = row, 16-byte column runs).  With no weight loads inside the loop,
 // no load waits behind the previous tile's stores (vmcnt counts both).
 
-// Fragment planes of 4 consecutive k values (half of a fragment unit): p0, p1 as 8 bytes
-// each (MODE 2: fp16 hi / lo; MODE 3: bf16 hi / mid).  MODE 0 keeps fp32 (see hfrag_put).
-template <int MODE>
-__device__ __forceinline__ void frag4(const float4 &v, uint2 &p0, uint2 &p1) {
-    if constexpr (MODE == 2) {
-        const f2v x0 = {v.x, v.y}, x1 = {v.z, v.w};
-        const h2v h0 = __builtin_convertvector(x0, h2v), h1 = __builtin_convertvector(x1, h2v);
-        const h2v l0 = __builtin_convertvector((x0 - __builtin_convertvector(h0, f2v)) * 2048.0f, h2v);
-        const h2v l1 = __builtin_convertvector((x1 - __builtin_convertvector(h1, f2v)) * 2048.0f, h2v);
-        p0 = make_uint2(bitcast<uint32_t>(h0), bitcast<uint32_t>(h1));
-        p1 = make_uint2(bitcast<uint32_t>(l0), bitcast<uint32_t>(l1));
-    } else {
-        Frag<MODE> f;
-        make_frag<MODE>(f, v, v);
-        p0 = make_uint2(f.p[0].x, f.p[0].y);
-        p1 = make_uint2(f.p[1].x, f.p[1].y);
-    }
-}
-
-// Store 4 values (k = 4h .. 4h+3 of fragment unit `unit`, lane `fl`) of a two-plane
-// fragment buffer laid out [unit][plane][64 lanes] x 16 bytes.
-template <int MODE>
-__device__ __forceinline__ void hfrag_put(uint4 *buf, int unit, int fl, int h, const float4 &v) {
-    if constexpr (MODE == 0) {
-        buf[(unit * 2 + h) * 64 + fl] = bitcast<uint4>(v);
-    } else {
-        uint2 p0, p1;
-        frag4<MODE>(v, p0, p1);
-        reinterpret_cast<uint2 *>(buf + (unit * 2 + 0) * 64 + fl)[h] = p0;
-        reinterpret_cast<uint2 *>(buf + (unit * 2 + 1) * 64 + fl)[h] = p1;
-    }
-}
-
 // Resident weight fragments of output tile nt (8 k-blocks, two planes) of a packed
 // [*, 128] weight.
 __device__ __forceinline__ void load_wres(uint4 (&w)[8][2], const uint4 *__restrict__ W, int nt, int lane) {
@@ -267,7 +234,7 @@ __global__ __launch_bounds__(512, 1) void ffn_fwd_ws_kernel(int64_t M, const flo
                 *reinterpret_cast<float4 *>(save_p + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) = v;
             v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
             amax = frag_amax<MODE>(amax, v, v);
-            hfrag_put<MODE>(Hf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, v);
+            frag_put4<MODE>(Hf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, v);
         }
         __syncthreads();  // h complete; every wave is past GEMM1 (Xf free)
 #pragma unroll

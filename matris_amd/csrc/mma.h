@@ -344,6 +344,119 @@ __device__ __forceinline__ float gemm_lds_packed(v16f (&acc)[NRT][NCT], const fl
     return amax;
 }
 
+// ------------------------------------------------------------------------------------
+// Pre-split operand tiles in LDS (two-plane modes): a tile of rows x K stored as fragment
+// units [rt][kb][plane][64 lanes] x 16 bytes, so a GEMM reads its A / B fragments with
+// one 16-byte LDS read per plane and converts nothing.  The writer converts each value
+// once.
+// ------------------------------------------------------------------------------------
+
+// Fragment planes of 4 consecutive k values (half of a unit): 8 bytes per plane (MODE 2:
+// fp16 hi / lo; MODE 3: bf16 hi / mid).  MODE 0 keeps fp32 (frag_put4 writes plane h).
+template <int MODE>
+__device__ __forceinline__ void frag4(const float4 &v, uint2 &p0, uint2 &p1) {
+    if constexpr (MODE == 2) {
+        const f2v x0 = {v.x, v.y}, x1 = {v.z, v.w};
+        const h2v h0 = __builtin_convertvector(x0, h2v), h1 = __builtin_convertvector(x1, h2v);
+        const h2v l0 = __builtin_convertvector((x0 - __builtin_convertvector(h0, f2v)) * 2048.0f, h2v);
+        const h2v l1 = __builtin_convertvector((x1 - __builtin_convertvector(h1, f2v)) * 2048.0f, h2v);
+        p0 = make_uint2(bitcast<uint32_t>(h0), bitcast<uint32_t>(h1));
+        p1 = make_uint2(bitcast<uint32_t>(l0), bitcast<uint32_t>(l1));
+    } else {
+        Frag<MODE> f;
+        make_frag<MODE>(f, v, v);
+        p0 = make_uint2(f.p[0].x, f.p[0].y);
+        p1 = make_uint2(f.p[1].x, f.p[1].y);
+    }
+}
+
+// Store 4 values (k = 4 hh .. 4 hh + 3 of unit `unit`, fragment lane `fl`) of a two-plane
+// fragment buffer.
+template <int MODE>
+__device__ __forceinline__ void frag_put4(uint4 *buf, int unit, int fl, int hh, const float4 &v) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes");
+    if constexpr (MODE == 0) {
+        buf[(unit * 2 + hh) * 64 + fl] = bitcast<uint4>(v);
+    } else {
+        uint2 p0, p1;
+        frag4<MODE>(v, p0, p1);
+        reinterpret_cast<uint2 *>(buf + (unit * 2 + 0) * 64 + fl)[hh] = p0;
+        reinterpret_cast<uint2 *>(buf + (unit * 2 + 1) * 64 + fl)[hh] = p1;
+    }
+}
+
+// Store 8 values (a whole unit) of a two-plane fragment buffer.
+template <int MODE>
+__device__ __forceinline__ void frag_put8(uint4 *buf, int unit, int fl, const float4 &u, const float4 &v) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes");
+    Frag<MODE> f;
+    make_frag<MODE>(f, u, v);
+    buf[(unit * 2 + 0) * 64 + fl] = f.p[0];
+    buf[(unit * 2 + 1) * 64 + fl] = f.p[1];
+}
+
+// One k-block of gemm_frag_packed: prefetch k-block `kpf` of B into BPF, then accumulate
+// k-block `kb` (A fragments from the pre-split buffer, B = BCUR).
+template <int MODE, int NRT, int NCT, bool TRANS>
+__device__ __forceinline__ void gemm_frag_step(v16f (&acc)[NRT][NCT], const uint4 *abuf, int aKB, int akb,
+                                               const uint4 *__restrict__ W, int nt0, int KBW, int kpf,
+                                               Frag<MODE> (&BCUR)[NCT], Frag<MODE> (&BPF)[NCT], int lane) {
+    load_bfrags<MODE, NCT>(BPF, W, nt0, KBW, kpf, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
+    Frag<MODE> a[NRT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) a[rt].p[pl] = abuf[((rt * aKB + akb) * 2 + pl) * 64 + lane];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) prep_w<MODE>(BCUR[ct]);
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+            if constexpr (TRANS)
+                mma_wx<MODE>(acc[rt][ct], BCUR[ct], a[rt]);
+            else
+                mma_xw<MODE>(acc[rt][ct], a[rt], BCUR[ct]);
+        }
+}
+
+// gemm_lds_packed with a pre-split A (two-plane modes): k-blocks akb0 .. akb0+KBA-1 of a
+// fragment buffer holding aKB k-blocks per row tile; same B prefetch rings.
+template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false>
+__device__ __forceinline__ void gemm_frag_packed(v16f (&acc)[NRT][NCT], const uint4 *abuf, int aKB, int akb0,
+                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes");
+    if constexpr (NCT == 2) {
+        static_assert(KBA % 4 == 0, "ring of four");
+        Frag<MODE> b0[NCT], b1[NCT], b2[NCT], b3[NCT];
+        load_bfrags<MODE, NCT>(b0, W, nt0, KBW, kb0, lane);
+        load_bfrags<MODE, NCT>(b1, W, nt0, KBW, kb0 + 1, lane);
+        load_bfrags<MODE, NCT>(b2, W, nt0, KBW, kb0 + 2, lane);
+#pragma unroll 1
+        for (int kb = 0; kb < KBA; kb += 4) {
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb, W, nt0, KBW, kb0 + min(kb + 3, KBA - 1),
+                                                  b0, b3, lane);
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb + 1, W, nt0, KBW,
+                                                  kb0 + min(kb + 4, KBA - 1), b1, b0, lane);
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb + 2, W, nt0, KBW,
+                                                  kb0 + min(kb + 5, KBA - 1), b2, b1, lane);
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb + 3, W, nt0, KBW,
+                                                  kb0 + min(kb + 6, KBA - 1), b3, b2, lane);
+        }
+    } else {
+        Frag<MODE> cur[NCT], nxt[NCT];
+        load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
+#pragma unroll 2
+        for (int kb = 0; kb < KBA; ++kb) {
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb, W, nt0, KBW, kb0 + min(kb + 1, KBA - 1),
+                                                  cur, nxt, lane);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
+        }
+    }
+}
+
 template <int NRT, int NCT>
 __device__ __forceinline__ void zero_acc(v16f (&acc)[NRT][NCT]) {
 #pragma unroll
