@@ -9,8 +9,6 @@
 
 #define WAVES_PER_BLOCK 4
 
-__device__ __forceinline__ float2 ld2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
-__device__ __forceinline__ void st2(float *p, float2 v) { *reinterpret_cast<float2 *>(p) = v; }
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 __device__ __forceinline__ float4 max4(const float4 &a, const float4 &b) {
@@ -351,6 +349,8 @@ extern "C" int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha
 // Backward:  g_h[a]   (+)= (g_agg * env)[tgt[a]] * env[src[a]]
 //            g_env[b]  = g_agg[b] * S[b] + sum_{a: src[a] = b} (g_agg * env)[tgt[a]] * h[a]
 // ------------------------------------------------------------------------------------
+// One wave per segment; the two half-waves take alternating rows (16-byte lanes, four
+// rows each in flight) and combine in the same order in both halves.
 __global__ __launch_bounds__(256) void env_agg_fwd_kernel(int64_t n_seg, const float *__restrict__ h,
                                                           const float *__restrict__ env,
                                                           const int32_t *__restrict__ t_ptr,
@@ -359,26 +359,35 @@ __global__ __launch_bounds__(256) void env_agg_fwd_kernel(int64_t n_seg, const f
                                                           float *__restrict__ agg) {
     const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (seg >= n_seg) return;
-    const int c = 2 * (threadIdx.x & 63);
+    const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
     const int b = t_ptr[seg], end = t_ptr[seg + 1];
-    float2 acc = make_float2(0.f, 0.f);
-    int i = b;
-    for (; i + 2 <= end; i += 2) {
-        const int64_t r0 = t_perm ? t_perm[i] : i, r1 = t_perm ? t_perm[i + 1] : i + 1;
-        const int64_t s0 = s_idx[r0], s1 = s_idx[r1];
-        const float2 h0 = ld2(h + r0 * MATRIS_D + c), h1 = ld2(h + r1 * MATRIS_D + c);
-        const float2 w0 = ld2(env + s0 * MATRIS_D + c), w1 = ld2(env + s1 * MATRIS_D + c);
-        acc.x += h0.x * w0.x; acc.y += h0.y * w0.y;
-        acc.x += h1.x * w1.x; acc.y += h1.y * w1.y;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = b + half;
+    for (; i + 6 < end; i += 8) {
+        const int64_t r0 = t_perm ? t_perm[i] : i, r1 = t_perm ? t_perm[i + 2] : i + 2;
+        const int64_t r2 = t_perm ? t_perm[i + 4] : i + 4, r3 = t_perm ? t_perm[i + 6] : i + 6;
+        const int64_t s0 = s_idx[r0], s1 = s_idx[r1], s2 = s_idx[r2], s3 = s_idx[r3];
+        const float4 h0 = ld4(h + r0 * MATRIS_D + c), h1 = ld4(h + r1 * MATRIS_D + c);
+        const float4 h2 = ld4(h + r2 * MATRIS_D + c), h3 = ld4(h + r3 * MATRIS_D + c);
+        const float4 w0 = ld4(env + s0 * MATRIS_D + c), w1 = ld4(env + s1 * MATRIS_D + c);
+        const float4 w2 = ld4(env + s2 * MATRIS_D + c), w3 = ld4(env + s3 * MATRIS_D + c);
+        acc.x += h0.x * w0.x; acc.y += h0.y * w0.y; acc.z += h0.z * w0.z; acc.w += h0.w * w0.w;
+        acc.x += h1.x * w1.x; acc.y += h1.y * w1.y; acc.z += h1.z * w1.z; acc.w += h1.w * w1.w;
+        acc.x += h2.x * w2.x; acc.y += h2.y * w2.y; acc.z += h2.z * w2.z; acc.w += h2.w * w2.w;
+        acc.x += h3.x * w3.x; acc.y += h3.y * w3.y; acc.z += h3.z * w3.z; acc.w += h3.w * w3.w;
     }
-    if (i < end) {
+    for (; i < end; i += 2) {
         const int64_t r0 = t_perm ? t_perm[i] : i;
-        const float2 h0 = ld2(h + r0 * MATRIS_D + c), w0 = ld2(env + (int64_t)s_idx[r0] * MATRIS_D + c);
-        acc.x += h0.x * w0.x; acc.y += h0.y * w0.y;
+        const float4 h0 = ld4(h + r0 * MATRIS_D + c), w0 = ld4(env + (int64_t)s_idx[r0] * MATRIS_D + c);
+        acc.x += h0.x * w0.x; acc.y += h0.y * w0.y; acc.z += h0.z * w0.z; acc.w += h0.w * w0.w;
     }
-    const float2 et = ld2(env + seg * MATRIS_D + c);
-    st2(S + seg * MATRIS_D + c, acc);
-    st2(agg + seg * MATRIS_D + c, make_float2(et.x * acc.x, et.y * acc.y));
+    const float4 o = shfl_xor4(acc, 32);
+    const float4 t = half ? make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w)
+                          : make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
+    if (half) return;
+    const float4 et = ld4(env + seg * MATRIS_D + c);
+    st4(S + seg * MATRIS_D + c, t);
+    st4(agg + seg * MATRIS_D + c, make_float4(et.x * t.x, et.y * t.y, et.z * t.z, et.w * t.w));
 }
 
 __global__ __launch_bounds__(256) void env_agg_bwd_rows_kernel(int64_t n_rows, const float *__restrict__ g_agg,
@@ -403,6 +412,7 @@ __global__ __launch_bounds__(256) void env_agg_bwd_rows_kernel(int64_t n_rows, c
     *o = v;
 }
 
+// g_env: one wave per source segment, half-waves on alternating rows as in the forward.
 __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, const float *__restrict__ h,
                                                               const float *__restrict__ env,
                                                               const float *__restrict__ g_agg,
@@ -413,19 +423,39 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
                                                               float *__restrict__ g_env) {
     const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (seg >= n_seg) return;
-    const int c = 2 * (threadIdx.x & 63);
+    const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
     const int b = s_ptr[seg], end = s_ptr[seg + 1];
-    float2 acc = make_float2(0.f, 0.f);
-    for (int i = b; i < end; ++i) {
-        const int64_t r = s_perm ? s_perm[i] : i;
-        const int64_t tr = t_idx[r];
-        const float2 hv = ld2(h + r * MATRIS_D + c);
-        const float2 g = ld2(g_agg + tr * MATRIS_D + c), et = ld2(env + tr * MATRIS_D + c);
-        acc.x += g.x * et.x * hv.x;
-        acc.y += g.y * et.y * hv.y;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = b + half;
+    for (; i + 6 < end; i += 8) {
+        const int64_t r0 = s_perm ? s_perm[i] : i, r1 = s_perm ? s_perm[i + 2] : i + 2;
+        const int64_t r2 = s_perm ? s_perm[i + 4] : i + 4, r3 = s_perm ? s_perm[i + 6] : i + 6;
+        const int64_t t0 = t_idx[r0], t1 = t_idx[r1], t2 = t_idx[r2], t3 = t_idx[r3];
+        const float4 h0 = ld4(h + r0 * MATRIS_D + c), h1 = ld4(h + r1 * MATRIS_D + c);
+        const float4 h2 = ld4(h + r2 * MATRIS_D + c), h3 = ld4(h + r3 * MATRIS_D + c);
+        const float4 g0 = ld4(g_agg + t0 * MATRIS_D + c), g1 = ld4(g_agg + t1 * MATRIS_D + c);
+        const float4 g2 = ld4(g_agg + t2 * MATRIS_D + c), g3 = ld4(g_agg + t3 * MATRIS_D + c);
+        const float4 e0 = ld4(env + t0 * MATRIS_D + c), e1 = ld4(env + t1 * MATRIS_D + c);
+        const float4 e2 = ld4(env + t2 * MATRIS_D + c), e3 = ld4(env + t3 * MATRIS_D + c);
+        acc.x += g0.x * e0.x * h0.x; acc.y += g0.y * e0.y * h0.y; acc.z += g0.z * e0.z * h0.z; acc.w += g0.w * e0.w * h0.w;
+        acc.x += g1.x * e1.x * h1.x; acc.y += g1.y * e1.y * h1.y; acc.z += g1.z * e1.z * h1.z; acc.w += g1.w * e1.w * h1.w;
+        acc.x += g2.x * e2.x * h2.x; acc.y += g2.y * e2.y * h2.y; acc.z += g2.z * e2.z * h2.z; acc.w += g2.w * e2.w * h2.w;
+        acc.x += g3.x * e3.x * h3.x; acc.y += g3.y * e3.y * h3.y; acc.z += g3.z * e3.z * h3.z; acc.w += g3.w * e3.w * h3.w;
     }
-    const float2 gs = ld2(g_agg + seg * MATRIS_D + c), sv = ld2(S + seg * MATRIS_D + c);
-    st2(g_env + seg * MATRIS_D + c, make_float2(gs.x * sv.x + acc.x, gs.y * sv.y + acc.y));
+    for (; i < end; i += 2) {
+        const int64_t r0 = s_perm ? s_perm[i] : i;
+        const int64_t t0 = t_idx[r0];
+        const float4 h0 = ld4(h + r0 * MATRIS_D + c), g0 = ld4(g_agg + t0 * MATRIS_D + c);
+        const float4 e0 = ld4(env + t0 * MATRIS_D + c);
+        acc.x += g0.x * e0.x * h0.x; acc.y += g0.y * e0.y * h0.y; acc.z += g0.z * e0.z * h0.z; acc.w += g0.w * e0.w * h0.w;
+    }
+    const float4 o = shfl_xor4(acc, 32);
+    const float4 t = half ? make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w)
+                          : make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
+    if (half) return;
+    const float4 gs = ld4(g_agg + seg * MATRIS_D + c), sv = ld4(S + seg * MATRIS_D + c);
+    st4(g_env + seg * MATRIS_D + c,
+        make_float4(gs.x * sv.x + t.x, gs.y * sv.y + t.y, gs.z * sv.z + t.z, gs.w * sv.w + t.w));
 }
 
 extern "C" int matris_env_agg_fwd(int64_t n_seg, const float *h, const float *env, const int32_t *t_ptr,
