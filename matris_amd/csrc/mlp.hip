@@ -8,11 +8,13 @@
 //           (interaction_block.py:33-38, 110-111), one [M,128]x[128,256] product
 //
 // and their input-gradient kernels.  Work-group = 4 wave64s over BM = 64 rows; the
-// [64, 128] input tile is staged once in LDS (K = 128 needs no K loop), weights are
-// pre-packed fragments (mma.h) read from global one k-block ahead, and intermediate
-// tiles (p, h, g_h) stay in LDS.  The GEMMs run transposed (weight fragment as the MFMA A
-// operand, rows in lanes), so results reach LDS with 16-byte writes.  Outputs leave
-// through LDS with 16-byte row stores.
+// [64, 128] input tile is staged once in one LDS tile (K = 128 needs no K loop) -- in the
+// two-plane modes already split into fragment units, so no wave converts an operand --
+// weights are pre-packed fragments (mma.h) read from global ahead of use, and
+// intermediate tiles (g_p) stay in LDS.  The GEMMs run transposed (weight fragment as
+// the MFMA A operand, rows in lanes), so results reach LDS with 16-byte writes.  Outputs
+// leave through LDS with 16-byte row stores.  The FFN forward of the two-plane modes is
+// weight-stationary and persistent instead (ffn_fwd_ws_kernel).
 #include <algorithm>
 #include <initializer_list>
 
@@ -65,6 +67,38 @@ __device__ __forceinline__ void store_tile128_scaled(const float *tile, float *_
             *reinterpret_cast<float4 *>(dst + (m0 + r) * MATRIS_D + c4) = make_float4(s.x * v.x, s.y * v.y, s.z * v.z, s.w * v.w);
         }
     }
+}
+
+// Stage rows m0 .. m0+63 of a [*, 128] array into LDS pre-split into fragment units
+// [rt 2][kb 8][plane 2][64 lanes] (two-plane modes; zeros past M): thread (row tid/4,
+// 8-column groups q, q+4, q+8, q+12 for q = tid%4), each value converted once.  With
+// g_res, also writes g_res = res_w * rows (the FFN backward's residual gradient).
+template <int MODE>
+__device__ __forceinline__ float stage_frag128(uint4 *buf, const float *__restrict__ src, int64_t m0, int64_t M,
+                                               int tid, float amax, float *__restrict__ g_res = nullptr,
+                                               const float *__restrict__ res_w = nullptr) {
+    const int r = tid >> 2, q = tid & 3;
+    const bool in = m0 + r < M;
+    const float4 *p = reinterpret_cast<const float4 *>(src + (m0 + r) * MATRIS_D);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = q + 4 * i;
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
+        if (in) {
+            u = p[2 * g];
+            v = p[2 * g + 1];
+            if (g_res) {
+                const float4 wu = *reinterpret_cast<const float4 *>(res_w + 8 * g);
+                const float4 wv = *reinterpret_cast<const float4 *>(res_w + 8 * g + 4);
+                float4 *o = reinterpret_cast<float4 *>(g_res + (m0 + r) * MATRIS_D + 8 * g);
+                o[0] = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
+                o[1] = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
+            }
+        }
+        amax = frag_amax<MODE>(amax, u, v);
+        frag_put8<MODE>(buf, (r >> 5) * 8 + (g >> 1), (r & 31) + 32 * (g & 1), u, v);
+    }
+    return amax;
 }
 
 // ------------------------------------------------------------------------------------
@@ -270,12 +304,23 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
-    stage_tile128(T, g, MATRIS_D, m0, M, tid);
-    __syncthreads();
-    if (g_res) store_tile128_scaled(T, g_res, res_w, m0, M, tid);
+    // two-plane modes: g, then g_p, pass through T pre-split into fragment units
+    constexpr bool PS = Npl<MODE>::v == 2;
+    uint4 *Tf = reinterpret_cast<uint4 *>(T);
     v16f acc[2][1];
     zero_acc(acc);
-    float amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
+    float amax = 0.f;
+    if constexpr (PS) {
+        amax = stage_frag128<MODE>(Tf, g, m0, M, tid, amax, g_res, res_w);
+        __syncthreads();
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W2t, wave, MATRIS_D / 16, 0,
+                                                          lane);
+    } else {
+        stage_tile128(T, g, MATRIS_D, m0, M, tid);
+        __syncthreads();
+        if (g_res) store_tile128_scaled(T, g_res, res_w, m0, M, tid);
+        amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2t, wave, MATRIS_D / 16, 0, lane);
+    }
     scale_acc<MODE>(acc, w2s);
     // g_p = g_h * SiLU'(p): lane = row, 4 consecutive columns per register group
 #pragma unroll
@@ -293,10 +338,29 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
         }
     }
     __syncthreads();  // every wave is done reading g
-    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
-    __syncthreads();
-    zero_acc(acc);
-    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1t, wave, MATRIS_D / 16, 0, lane));
+    if constexpr (PS) {
+        // lane (row rt*32 + l32, half h) holds g_p columns 32 wave + 8 j + 4 h .. +3: half h
+        // of unit (rt, k-block 2 wave + j/2), lane l32 + 32 (j%2)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = make_float4(acc[rt][0][4 * j], acc[rt][0][4 * j + 1], acc[rt][0][4 * j + 2],
+                                             acc[rt][0][4 * j + 3]);
+                amax = frag_amax<MODE>(amax, v, v);
+                frag_put4<MODE>(Tf, rt * 8 + 2 * wave + (j >> 1), l32 + 32 * (j & 1), h, v);
+            }
+        __syncthreads();
+        zero_acc(acc);
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W1t, wave, MATRIS_D / 16, 0,
+                                                          lane);
+    } else {
+        acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+        __syncthreads();
+        zero_acc(acc);
+        amax = fmaxf(amax,
+                     gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1t, wave, MATRIS_D / 16, 0, lane));
+    }
     scale_acc<MODE>(acc, w1s);
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
@@ -310,27 +374,38 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
 // g_x = g0 W[0:128] + g1 W[128:256]
 // ------------------------------------------------------------------------------------
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void pair_fwd_kernel(int64_t M, const float *__restrict__ x,
+__global__ __launch_bounds__(256, MODE == 6 ? 2 : 3) void pair_fwd_kernel(int64_t M, const float *__restrict__ x,
                                                           const uint4 *__restrict__ W, float *__restrict__ out0,
                                                           float *__restrict__ out1, unsigned *range_flag) {
     __shared__ __align__(16) float T0[BM * LDT];
-    __shared__ __align__(16) float T1[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const float ws = take_wscale<MODE>(W);
-    stage_tile128(T0, x, MATRIS_D, m0, M, tid);
-    __syncthreads();
     // wave w -> output columns [64w, 64w+64) of the 256: waves 0,1 -> out0, 2,3 -> out1
     v16f acc[2][2];
     zero_acc(acc);
-    const float amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0,
-                                                                        lane);
+    float amax = 0.f;
+    if constexpr (Npl<MODE>::v == 2) {  // x pre-split into fragment units in T0
+        uint4 *Tf = reinterpret_cast<uint4 *>(T0);
+        amax = stage_frag128<MODE>(Tf, x, m0, M, tid, amax);
+        __syncthreads();
+        gemm_frag_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W, 2 * wave, MATRIS_D / 16, 0,
+                                                          lane);
+    } else {
+        stage_tile128(T0, x, MATRIS_D, m0, M, tid);
+        __syncthreads();
+        amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0, lane);
+    }
     scale_acc<MODE>(acc, ws);
+    // out0 (waves 0, 1), then out1 (waves 2, 3), pass through the one tile
     __syncthreads();  // T0 free
-    acc_t_to_lds<2, 2>(acc, (wave < 2) ? T0 : T1, LDT, (wave & 1) * 64, lane);
+    if (wave < 2) acc_t_to_lds<2, 2>(acc, T0, LDT, (wave & 1) * 64, lane);
     __syncthreads();
     store_tile128(T0, out0, MATRIS_D, m0, M, tid);
-    store_tile128(T1, out1, MATRIS_D, m0, M, tid);
+    __syncthreads();
+    if (wave >= 2) acc_t_to_lds<2, 2>(acc, T0, LDT, (wave & 1) * 64, lane);
+    __syncthreads();
+    store_tile128(T0, out1, MATRIS_D, m0, M, tid);
     report_range<MODE>(amax, range_flag);
 }
 
@@ -345,16 +420,29 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const float ws = take_wscale<MODE>(Wt);
-    stage_tile128(T, g0, MATRIS_D, m0, M, tid);
-    __syncthreads();
     v16f acc[2][1];
     zero_acc(acc);
-    float amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, 0, lane);
-    __syncthreads();
-    stage_tile128(T, g1, MATRIS_D, m0, M, tid);
-    __syncthreads();
-    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, MATRIS_D / 16,
-                                                                        lane));
+    float amax = 0.f;
+    if constexpr (Npl<MODE>::v == 2) {  // g0, then g1, pre-split into fragment units in T
+        uint4 *Tf = reinterpret_cast<uint4 *>(T);
+        amax = stage_frag128<MODE>(Tf, g0, m0, M, tid, amax);
+        __syncthreads();
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, Wt, wave, 256 / 16, 0, lane);
+        __syncthreads();
+        amax = stage_frag128<MODE>(Tf, g1, m0, M, tid, amax);
+        __syncthreads();
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, Wt, wave, 256 / 16,
+                                                          MATRIS_D / 16, lane);
+    } else {
+        stage_tile128(T, g0, MATRIS_D, m0, M, tid);
+        __syncthreads();
+        amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16, 0, lane);
+        __syncthreads();
+        stage_tile128(T, g1, MATRIS_D, m0, M, tid);
+        __syncthreads();
+        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Wt, wave, 256 / 16,
+                                                                            MATRIS_D / 16, lane));
+    }
     scale_acc<MODE>(acc, ws);  // both halves share the one weight scale
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
