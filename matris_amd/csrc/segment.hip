@@ -24,20 +24,15 @@ __device__ __forceinline__ float4 shfl_xor4(const float4 &v, int o) {
 // ------------------------------------------------------------------------------------
 // One wave per segment; each half-wave sums every other row with 16-byte lanes and the
 // halves combine at the end (fixed order: deterministic).
-__global__ __launch_bounds__(256) void seg_sum_kernel(const float *__restrict__ x, int64_t ldx, int64_t col_off,
-                                                      const int32_t *__restrict__ rowptr,
-                                                      const int32_t *__restrict__ perm, int64_t n_seg, float scale,
-                                                      int accumulate, float *__restrict__ out) {
-    int64_t s = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
-    if (s >= n_seg) return;
-    const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
-    const int b = rowptr[s], e = rowptr[s + 1];
-    const float *xc = x + col_off + c;
+// Partial sum of the rows i = start, start + stride, ... < end of one CSR segment, four
+// rows in flight (16-byte lanes, xc = row base + column offset of the lane).
+__device__ __forceinline__ float4 seg_rows(const float *__restrict__ xc, int64_t ldx,
+                                           const int32_t *__restrict__ perm, int i, int end, int stride) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int i = b + half;
-    for (; i + 6 < e; i += 8) {
-        const int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + 2] : i + 2;
-        const int64_t r2 = perm ? perm[i + 4] : i + 4, r3 = perm ? perm[i + 6] : i + 6;
+    for (; i + 3 * stride < end; i += 4 * stride) {
+        const int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + stride] : i + stride;
+        const int64_t r2 = perm ? perm[i + 2 * stride] : i + 2 * stride;
+        const int64_t r3 = perm ? perm[i + 3 * stride] : i + 3 * stride;
         const float4 v0 = ld4(xc + r0 * ldx), v1 = ld4(xc + r1 * ldx);
         const float4 v2 = ld4(xc + r2 * ldx), v3 = ld4(xc + r3 * ldx);
         acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;
@@ -45,36 +40,101 @@ __global__ __launch_bounds__(256) void seg_sum_kernel(const float *__restrict__ 
         acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;
         acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;
     }
-    for (; i < e; i += 2) {
+    for (; i < end; i += stride) {
         const int64_t r = perm ? perm[i] : i;
         const float4 v = ld4(xc + r * ldx);
         acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
     }
-    // half 0 + half 1, the same order in both halves
-    const float4 o = shfl_xor4(acc, 32);
-    float4 t = half ? make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w)
-                    : make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
-    t.x *= scale; t.y *= scale; t.z *= scale; t.w *= scale;
-    if (half) return;
-    float *op = out + s * MATRIS_D + c;
-    if (accumulate) {
-        const float4 p = ld4(op);
-        t.x += p.x; t.y += p.y; t.z += p.z; t.w += p.w;
+    return acc;
+}
+
+struct SegSrc {
+    const float *x;  // nullptr: no second source
+    int64_t ldx, col_off;
+    const int32_t *rowptr, *perm;
+    float scale;
+};
+
+__device__ __forceinline__ float4 add4(const float4 &a, const float4 &b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// out[s] (+)= a.scale * sum_{rows of a's segment s} a.x[row] + b.scale * (the same for b).
+// WPS waves per segment: 1 (four segments per work-group), or 4 for long segments (the
+// waves take interleaved row slices and combine through LDS).  In a wave the half-waves
+// take alternating rows.  Every combination runs in a fixed order: deterministic.
+template <int WPS>
+__global__ __launch_bounds__(256) void seg_sum_kernel(SegSrc a, SegSrc b, int64_t n_seg, int accumulate,
+                                                      float *__restrict__ out) {
+    const int w = threadIdx.x >> 6, half = (threadIdx.x >> 5) & 1, l = threadIdx.x & 31, c = 4 * l;
+    const int64_t s = (int64_t)blockIdx.x * (WAVES_PER_BLOCK / WPS) + w / WPS;
+    const int slice = w % WPS;
+    const bool live = s < n_seg;
+    float4 ta = make_float4(0.f, 0.f, 0.f, 0.f), tb = ta;
+    if (live) {
+        const int off = 2 * slice + half, stride = 2 * WPS;
+        ta = seg_rows(a.x + a.col_off + c, a.ldx, a.perm, a.rowptr[s] + off, a.rowptr[s + 1], stride);
+        if (b.x) tb = seg_rows(b.x + b.col_off + c, b.ldx, b.perm, b.rowptr[s] + off, b.rowptr[s + 1], stride);
+        // half 0 + half 1, the same order in both halves
+        const float4 oa = shfl_xor4(ta, 32), ob = shfl_xor4(tb, 32);
+        ta = half ? add4(oa, ta) : add4(ta, oa);
+        tb = half ? add4(ob, tb) : add4(tb, ob);
     }
+    if constexpr (WPS > 1) {
+        __shared__ float4 part[WAVES_PER_BLOCK][2][32];
+        if (half == 0) {
+            part[w][0][l] = ta;
+            part[w][1][l] = tb;
+        }
+        __syncthreads();
+        if (!live || slice != 0 || half) return;
+#pragma unroll
+        for (int k = 1; k < WPS; ++k) {
+            ta = add4(ta, part[w + k][0][l]);
+            tb = add4(tb, part[w + k][1][l]);
+        }
+    } else {
+        if (!live || half) return;
+    }
+    float4 t = make_float4(ta.x * a.scale, ta.y * a.scale, ta.z * a.scale, ta.w * a.scale);
+    if (b.x) t = add4(t, make_float4(tb.x * b.scale, tb.y * b.scale, tb.z * b.scale, tb.w * b.scale));
+    float *op = out + s * MATRIS_D + c;
+    if (accumulate) t = add4(t, ld4(op));
     st4(op, t);
+}
+
+static bool seg_src_ok(const SegSrc &v) {
+    return v.rowptr && v.ldx >= MATRIS_D && v.col_off >= 0 && v.col_off + MATRIS_D <= v.ldx && !(v.ldx % 4) &&
+           !(v.col_off % 4);
+}
+
+static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64_t rows_hint, int accumulate,
+                          float *out, void *stream) {
+    if (n_seg < 0 || !out || !seg_src_ok(a) || (b.x && !seg_src_ok(b))) return MATRIS_E_ARG;
+    if (n_seg == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (rows_hint >= 32 * n_seg)  // long segments: a work-group each
+        seg_sum_kernel<4><<<(unsigned)n_seg, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+    else
+        seg_sum_kernel<1><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(a, b, n_seg, accumulate, out);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
 }
 
 extern "C" int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *rowptr,
                               const int32_t *perm, int64_t n_seg, float scale, int accumulate, float *out,
                               void *stream) {
-    if (n_seg < 0 || !rowptr || !out || ldx < MATRIS_D || col_off < 0 || col_off + MATRIS_D > ldx ||
-        (ldx % 4) || (col_off % 4))
-        return MATRIS_E_ARG;
-    if (n_seg == 0) return 0;
-    seg_sum_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
-        x, ldx, col_off, rowptr, perm, n_seg, scale, accumulate, out);
-    MATRIS_CHECK_LAUNCH();
-    return 0;
+    const SegSrc a{x, ldx, col_off, rowptr, perm, scale}, none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f};
+    return seg_sum_launch(a, none, n_seg, 0, accumulate, out, stream);
+}
+
+extern "C" int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t lda, int64_t offa,
+                               const int32_t *rowptr_a, const int32_t *perm_a, float scale_a, const float *xb,
+                               int64_t ldb, int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b,
+                               float scale_b, int accumulate, float *out, void *stream) {
+    const SegSrc a{xa, lda, offa, rowptr_a, perm_a, scale_a};
+    const SegSrc b{xb, ldb, offb, rowptr_b, perm_b, scale_b};
+    return seg_sum_launch(a, b, n_seg, rows_hint, accumulate, out, stream);
 }
 
 // ------------------------------------------------------------------------------------

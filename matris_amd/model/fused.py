@@ -141,8 +141,8 @@ class _LineAttention(torch.autograd.Function):
         # edge update: source 0 (tb) accumulates into g_tb, bond gathers scatter into g_bond
         g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=True)
         del g_e, p_e, z_e
-        ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True)
-        ops.seg_sum_raw(g_x, src, ldx=2 * D, col_off=D, out=g_bond, accumulate=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True,
+                        second=(g_x, src, 1.0, 2 * D, D))
         return g_bond, g_tb, None, None, None
 
 
@@ -214,8 +214,8 @@ class _LineRefinement(torch.autograd.Function):
         g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=True)
         del g_h, p_h, z_h
         g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
-        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True)
-        ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_bond, accumulate=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True,
+                        second=(g_x, src, 1.0, 3 * D, 2 * D))
         return g_tb, g_atom, g_bond, g_env, None, None, None
 
 
@@ -304,8 +304,8 @@ class _AtomAttention(torch.autograd.Function):
         g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode)
         del g_e, p_e, z_e
         ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, out=g_bond, accumulate=True)
-        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True)
-        ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_atom, accumulate=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
+                        second=(g_x, src, 1.0, 3 * D, 2 * D))
         return g_atom, g_bond, None, None, None
 
 
@@ -373,8 +373,8 @@ class _AtomRefinement(torch.autograd.Function):
         g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode)
         del g_h, p_h, z_h
         ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, out=g_bond, accumulate=True)
-        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True)
-        ops.seg_sum_raw(g_x, src, ldx=3 * D, col_off=2 * D, out=g_atom, accumulate=True)
+        ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
+                        second=(g_x, src, 1.0, 3 * D, 2 * D))
         return g_atom, g_bond, g_env, None, None, None
 
 

@@ -60,6 +60,29 @@ def test_seg_sum_matches_index_add(R, S, scale, acc):
     assert _rel(out, ref) < 2e-6
 
 
+@pytest.mark.parametrize("R,S", [(37, 5), (5000, 800), (20000, 3), (3000, 100), (0, 4)])
+@pytest.mark.parametrize("acc", [False, True])
+def test_seg_sum_two_groupings_one_pass(R, S, acc):
+    """matris_seg_sum2: two groupings of different row sets into one output (the target-
+    and source-side scatters), short segments (a wave each) and long ones (a work-group
+    each, R/S >= 32), against two fp64 index_add_ calls."""
+    ops = _ops()
+    torch.manual_seed(R + S)
+    ka, kb = _keys(R, S, 2).to(DEV), _keys(R + 7, S, 3).to(DEV)
+    ga, gb = ops.Grouping.build(ka, S), ops.Grouping.build(kb, S)
+    x = torch.randn(max(R, 1), 384, device=DEV)[:R]
+    xb = torch.randn(R + 7, 256, device=DEV)
+    base = torch.randn(S, 128, device=DEV)
+    out = base.clone()
+    ops.seg_sum_raw(x, ga, 0.5, ldx=384, col_off=256, out=out, accumulate=acc, second=(xb, gb, 1.0, 256, 128))
+    ref = torch.zeros(S, 128, dtype=torch.float64).index_add_(0, ka.cpu().long(), x[:, 256:].double().cpu()) * 0.5
+    ref = ref.index_add_(0, kb.cpu().long(), xb[:, 128:].double().cpu())
+    ref = ref + (base.double().cpu() if acc else 0)
+    assert _rel(out, ref) < 2e-6
+    with pytest.raises(ValueError):
+        ops.seg_sum_raw(x, ga, second=(xb, ops.Grouping.build(kb, S + 1), 1.0, 256, 128))
+
+
 def test_gather_exact():
     ops = _ops()
     src = torch.randn(100, 128, device=DEV)
