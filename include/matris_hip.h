@@ -95,6 +95,12 @@ int matris_line_graph_fill(int64_t n_atoms, int64_t n_edges, int64_t n_undirecte
 size_t matris_csr_workspace_bytes(int64_t n_rows, int64_t n_segments);
 int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t n_segments,
                      int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes, void *stream);
+/* matris_csr_build without its host read: a key outside [0, nseg) is left out and sets
+ * MATRIS_STATUS_CSR_KEY in the device status word (matris_status_take) instead of
+ * returning MATRIS_E_ARG, so a model evaluation's groupings cost no stream syncs. */
+int matris_csr_build_deferred(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
+                              int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes,
+                              void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Segmented reductions and gathers (row M3)
@@ -212,8 +218,8 @@ int matris_sbf_bwd(int64_t n_edges, const float *unit, const int32_t *de_t, cons
  *                     power of two and split into two fp16 parts, three partial products
  *                     on v_mfma_f32_32x32x16_f16 (~2^-22 per product, fp32-grade).  fp16
  *                     bounds the activations: a kernel that meets |x| >= 65504 in an
- *                     operand it splits sets the device's range flag (its results are
- *                     then unusable); matris_f16_range_take reads and clears the flag.
+ *                     operand it splits sets MATRIS_STATUS_F16_RANGE in the device's
+ *                     status word (its results are then unusable; matris_status_take).
  * Every weight operand ("...p" arguments) is passed pre-packed by matris_pack_b in the
  * SAME mode as the call that reads it: a [n, k] row-major fp32 matrix whose rows are the
  * GEMM's output columns (an nn.Linear weight, or the transpose of one for a backward)
@@ -228,10 +234,16 @@ int matris_sbf_bwd(int64_t n_edges, const float *unit, const int32_t *de_t, cons
 #define MATRIS_MMA_BF16X6 6
 size_t matris_pack_b_bytes(int64_t n, int64_t k, int mode);
 int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, void *out, void *stream);
-/* *flagged = 1 if a MATRIS_MMA_F16X3 kernel on the current device met an activation
- * outside the fp16 range since the last call, else 0; clears the flag.  Synchronizes
- * `stream` (the kernels to check must have been launched on it or before it). */
-int matris_f16_range_take(int *flagged, void *stream);
+/* The device status word: bits set by kernels of this library since the last take.
+ *   MATRIS_STATUS_F16_RANGE  a MATRIS_MMA_F16X3 kernel met an activation outside the fp16
+ *                            range (its outputs are unusable: redo in MATRIS_MMA_BF16X6);
+ *   MATRIS_STATUS_CSR_KEY    matris_csr_build_deferred met a key outside [0, nseg).
+ * *bits = the word of the current device, which is then cleared.  Synchronizes `stream`
+ * (the kernels to check must have been launched on it or before it).  No counterpart in
+ * the reference: it lets one host read per model evaluation replace a read per check. */
+#define MATRIS_STATUS_F16_RANGE 1u
+#define MATRIS_STATUS_CSR_KEY 2u
+int matris_status_take(unsigned *bits, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Fused gated MLP on MFMA (row M1).  Replaces GatedMLP.forward

@@ -80,6 +80,7 @@ _SIGS = {
     "matris_line_graph_fill": (_I, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _D, _P, _P, _P]),
     "matris_csr_workspace_bytes": (_SZ, [_I64, _I64]),
     "matris_csr_build": (_I, [_I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "matris_csr_build_deferred": (_I, [_I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "matris_seg_sum": (_I, [_P, _I64, _I64, _P, _P, _I64, _F, _I, _P, _P]),
     "matris_seg_sum2": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P]),
     "matris_gather_rows": (_I, [_P, _P, _I64, _F, _I, _P, _P]),
@@ -97,7 +98,7 @@ _SIGS = {
     "matris_sbf_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _I, _P, _P]),
     "matris_pack_b_bytes": (_SZ, [_I64, _I64, _I]),
     "matris_pack_b": (_I, [_I64, _I64, _P, _I, _P, _P]),
-    "matris_f16_range_take": (_I, [_P, _P]),
+    "matris_status_take": (_I, [_P, _P]),
     "matris_ffn_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),

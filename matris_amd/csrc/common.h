@@ -13,6 +13,10 @@
         if (_e != hipSuccess) return (int)_e;          \
     } while (0)
 
+// The current device's status word (defined in gmlp.hip; MATRIS_STATUS_* bits), nullptr
+// on failure.
+unsigned *matris_range_flag();
+
 static inline int matris_blocks(int64_t work, int per_block) {
     int64_t b = (work + per_block - 1) / per_block;
     return (int)(b < 1 ? 1 : b);

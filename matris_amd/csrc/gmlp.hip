@@ -26,13 +26,13 @@
 // in LDS already split into fragment units by the pass that produces them, so neither
 // GEMM converts anything (g_p is otherwise re-split by every wave of every column pass).
 //
-// This file also owns the device word that MODE 2 (fp16 split) kernels of every GEMM
-// file flag when an activation exceeds the fp16 range (matris_f16_range_take).
+// This file also owns the device status word: MODE 2 (fp16 split) kernels of every GEMM
+// file set bit 0 when an activation exceeds the fp16 range, deferred CSR builds set bit 1
+// on a key outside its segment range; matris_status_take reads and clears it.
 #include "mma.h"
 
-// Set (to 1) by a MODE 2 kernel that met |x| >= 65504 in an operand it split; one copy
-// per device.
-static __device__ unsigned matris_f16_range_word;
+// Bits set by kernels of this library (MATRIS_STATUS_*); one copy per device.
+static __device__ unsigned matris_status_word;
 
 unsigned *matris_range_flag() {
     static unsigned *ptr[64] = {};
@@ -40,7 +40,7 @@ unsigned *matris_range_flag() {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     if (!ptr[dev]) {
         void *p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(matris_f16_range_word)) != hipSuccess) return nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(matris_status_word)) != hipSuccess) return nullptr;
         ptr[dev] = (unsigned *)p;
     }
     return ptr[dev];
@@ -657,8 +657,8 @@ extern "C" int matris_pack_b(int64_t n, int64_t k, const float *w, int mode, voi
     return 0;
 }
 
-extern "C" int matris_f16_range_take(int *flagged, void *stream) {
-    if (!flagged) return MATRIS_E_ARG;
+extern "C" int matris_status_take(unsigned *bits, void *stream) {
+    if (!bits) return MATRIS_E_ARG;
     unsigned *flag = matris_range_flag();
     if (!flag) return MATRIS_E_ARG;
     hipStream_t st = (hipStream_t)stream;
@@ -670,6 +670,6 @@ extern "C" int matris_f16_range_take(int *flagged, void *stream) {
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
-    *flagged = e == hipSuccess ? (int)(v != 0u) : 0;
+    *bits = e == hipSuccess ? v : 0u;
     return (int)e;
 }

@@ -684,12 +684,12 @@ extern "C" int matris_line_graph_fill(int64_t n_atoms, int64_t E, int64_t n_u, c
 // stable CSR builder
 // ------------------------------------------------------------------------------------
 __global__ void csr_hist_kernel(int64_t n, const int32_t *__restrict__ keys, int64_t ks, int64_t nseg,
-                                int *__restrict__ cnt, int *__restrict__ err) {
+                                int *__restrict__ cnt, unsigned *__restrict__ err, unsigned err_bit) {
     int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n) return;
     int k = keys[r * ks];
     if (k < 0 || k >= nseg) {
-        atomicOr(err, 1);
+        atomicOr(err, err_bit);
         return;
     }
     atomicAdd(&cnt[k], 1);
@@ -725,21 +725,21 @@ extern "C" size_t matris_csr_workspace_bytes(int64_t n_rows, int64_t nseg) {
            scan_workspace_bytes(nseg) + 256;
 }
 
-extern "C" int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
-                                int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes,
-                                void *stream) {
+// Histogram, scan, scatter and per-segment sort on `stream`; out-of-range keys are not
+// placed and set err_bit in *err.
+static int csr_build_launch(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg, int32_t *rowptr,
+                            int32_t *perm, void *workspace, size_t workspace_bytes, unsigned *err, unsigned err_bit,
+                            hipStream_t st) {
     if (n_rows < 0 || nseg <= 0 || !rowptr || !perm || !workspace || (n_rows > 0 && !keys)) return MATRIS_E_ARG;
     if (workspace_bytes < matris_csr_workspace_bytes(n_rows, nseg) || n_rows >= INT32_MAX) return MATRIS_E_ARG;
-    hipStream_t st = (hipStream_t)stream;
     char *p = (char *)workspace;
     int *cnt = (int *)p; p += align256(sizeof(int) * (nseg + 1));
     int32_t *tmp = (int32_t *)p; p += align256(sizeof(int32_t) * (n_rows + 1));
-    int *err = (int *)p; p += 256;
+    p += 256;  // (the synchronous form's error word)
     void *scan_ws = p;
     fill<int>(cnt, nseg, 0, st);
-    fill<int>(err, 1, 0, st);
     if (n_rows > 0)
-        csr_hist_kernel<<<matris_blocks(n_rows, 256), 256, 0, st>>>(n_rows, keys, key_stride, nseg, cnt, err);
+        csr_hist_kernel<<<matris_blocks(n_rows, 256), 256, 0, st>>>(n_rows, keys, key_stride, nseg, cnt, err, err_bit);
     int rc = scan_exclusive<int, int32_t>(cnt, nseg, rowptr, scan_ws, st);
     if (rc) return rc;
     if (n_rows > 0) {
@@ -749,9 +749,33 @@ extern "C" int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key
         csr_sort_kernel<<<matris_blocks(nseg, 4), 256, 0, st>>>(nseg, rowptr, tmp, perm);
     }
     MATRIS_CHECK_LAUNCH();
-    int h_err = 0;
-    hipError_t e = hipMemcpyAsync(&h_err, err, sizeof(int), hipMemcpyDeviceToHost, st);
+    return 0;
+}
+
+extern "C" int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
+                                int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes,
+                                void *stream) {
+    if (n_rows < 0 || nseg <= 0 || !workspace || workspace_bytes < matris_csr_workspace_bytes(n_rows, nseg))
+        return MATRIS_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    char *p = (char *)workspace;
+    p += align256(sizeof(int) * (nseg + 1)) + align256(sizeof(int32_t) * (n_rows + 1));
+    unsigned *err = (unsigned *)p;
+    fill<unsigned>(err, 1, 0u, st);
+    int rc = csr_build_launch(n_rows, keys, key_stride, nseg, rowptr, perm, workspace, workspace_bytes, err, 1u, st);
+    if (rc) return rc;
+    unsigned h_err = 0;
+    hipError_t e = hipMemcpyAsync(&h_err, err, sizeof(h_err), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) return (int)e;
     return h_err ? MATRIS_E_ARG : 0;
+}
+
+extern "C" int matris_csr_build_deferred(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
+                                         int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes,
+                                         void *stream) {
+    unsigned *status = matris_range_flag();
+    if (!status) return MATRIS_E_ARG;
+    return csr_build_launch(n_rows, keys, key_stride, nseg, rowptr, perm, workspace, workspace_bytes, status,
+                            (unsigned)MATRIS_STATUS_CSR_KEY, (hipStream_t)stream);
 }

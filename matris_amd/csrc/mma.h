@@ -174,7 +174,8 @@ __device__ __forceinline__ void scale_acc(v16f (&acc)[NRT][NCT], float s) {
 template <int MODE>
 __device__ __forceinline__ void report_range(float amax, unsigned *flag) {
     if constexpr (MODE == 2) {
-        if (__ballot(amax >= MATRIS_F16_MAX) != 0 && (threadIdx.x & 63) == 0 && flag) atomicOr(flag, 1u);
+        if (__ballot(amax >= MATRIS_F16_MAX) != 0 && (threadIdx.x & 63) == 0 && flag)
+            atomicOr(flag, (unsigned)MATRIS_STATUS_F16_RANGE);
     }
 }
 
@@ -524,8 +525,6 @@ static inline bool matris_mode_ok(int mode) { return mode == 0 || mode == 2 || m
         else KERNEL<6><<<(GRID), 256, 0, (STREAM)>>>(__VA_ARGS__);                          \
     } while (0)
 
-// The current device's MODE 2 range word (defined in gmlp.hip), nullptr on failure.
-unsigned *matris_range_flag();
 
 // Bytes of a packed [n, k] weight in `mode` (n % 32 == 0, k % 16 == 0).
 __host__ __device__ inline size_t packed_b_bytes(int64_t n, int64_t k, int mode) {

@@ -18,7 +18,35 @@ def _sorted(x: torch.Tensor) -> bool:
     return x.numel() < 2 or bool((x[1:] >= x[:-1]).all().item())
 
 
+def validate_graph_indices(g) -> None:
+    """Raise ValueError unless every index array of graph g is inside its range: atom_graph
+    [E, 2] in [0, N), directed2undirected [E] in [0, U), undirected2directed [U] in [0, E)
+    and the line graph's columns (center atom, bond, directed edge, bond, directed edge).
+    The gather and segment kernels read rows through these indices, so they are checked
+    before any of them runs: one host read per graph, remembered in g.meta (graphs built
+    by GraphConverter are valid by construction and carry the mark already).  A graph's
+    index tensors must not be changed in place after its first evaluation."""
+    if g.meta.get("indices_checked", False):
+        return
+    N = int(g.atomic_number.shape[0])
+    E = int(g.atom_graph.shape[0])
+    U = int(g.undirected2directed.shape[0])
+    lg = g.line_graph
+    if g.atom_graph.dim() != 2 or g.atom_graph.shape[1] != 2 or g.directed2undirected.shape[0] != E or \
+            (len(lg) and (lg.dim() != 2 or lg.shape[1] != 5)):
+        raise ValueError("graph index arrays have the wrong shape")
+    checks = [(g.atom_graph, N), (g.directed2undirected, U), (g.undirected2directed, E)]
+    if len(lg):
+        checks += [(lg[:, 0], N), (lg[:, 1], U), (lg[:, 2], E), (lg[:, 3], U), (lg[:, 4], E)]
+    flags = [((x < 0) | (x >= n)).any() for x, n in checks if x.numel()]
+    if flags and bool(torch.stack(flags).any()):
+        raise ValueError("graph index outside its range (atom, bond, directed-edge or angle index)")
+    g.meta["indices_checked"] = True
+
+
 def process_graphs(graphs, compute_stress: bool = True) -> dict:
+    for g in graphs:
+        validate_graph_indices(g)
     device = graphs[0].lattice.device
     dtype = graphs[0].lattice.dtype
     G = len(graphs)
@@ -36,8 +64,11 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         d2u.append(g.directed2undirected.to(torch.int32) + u_off)
         u2d.append(g.undirected2directed.to(torch.int32) + d_off)
         if nl:
-            off = torch.tensor([a_off, u_off, d_off, u_off, d_off], dtype=torch.int32, device=device)
-            lgs.append(g.line_graph.to(torch.int32) + off)
+            if a_off or u_off or d_off:
+                off = torch.tensor([a_off, u_off, d_off, u_off, d_off], dtype=torch.int32, device=device)
+                lgs.append(g.line_graph.to(torch.int32) + off)
+            else:  # the first graph: no offsets, and no host-to-device copy
+                lgs.append(g.line_graph.to(torch.int32))
         frac = g.atom_frac_coord.detach()
         lat = g.lattice.detach()
         carts.append(frac @ lat)  # processgraph.py:87
@@ -56,8 +87,11 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     lattice = torch.cat(lats, 0)  # [3G, 3]
     cart = torch.cat(carts, 0)
     image = torch.cat(imgs, 0)
-    counts = torch.tensor(n_atoms, device=device)
-    atom_segment = torch.repeat_interleave(torch.arange(G, device=device), counts)
+    if G == 1:
+        atom_segment = torch.zeros(N, dtype=torch.long, device=device)
+    else:
+        atom_segment = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_atoms, device=device),
+                                               output_size=N)
     lat3 = lattice.reshape(G, 3, 3)
     volumes = torch.einsum("ni,ni->n", lat3[:, 0], torch.linalg.cross(lat3[:, 1], lat3[:, 2]))[:, None, None]
 
@@ -78,10 +112,13 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     if G == 1:
         shift = image @ lattice
     else:
-        edge_graph = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_dir, device=device))
+        edge_graph = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_dir, device=device),
+                                             output_size=E)
         shift = torch.bmm(image.unsqueeze(1), lat3[edge_graph]).squeeze(1)
-    grp_tgt = Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32))
-    grp_src = Grouping.build(src32, N)
+    # deferred builds: key-range errors surface in the status word that MatRIS.forward
+    # reads once per evaluation (no stream sync per grouping)
+    grp_tgt = Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True)
+    grp_src = Grouping.build(src32, N, deferred=True)
     vec = ops.edge_vectors(cart, shift, grp_tgt, grp_src)
     length = torch.norm(vec, dim=1)
     unit = vec / length[:, None]
@@ -91,7 +128,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
                directed2undirected=d2u32.long(), undirected2directed=u2d32.long(), volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
                n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
-    out["grp_d2u"] = Grouping.build(d2u32, U, sorted_rows=False)
+    out["grp_d2u"] = Grouping.build(d2u32, U, sorted_rows=False, deferred=True)
     out["atom_graph_dict"] = dict(
         atom_graph=atom_graph, target_index=tgt, source_index=src,
         grp_tgt=grp_tgt, grp_src=grp_src)
@@ -101,12 +138,12 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         cols = [lg[:, k].contiguous() for k in range(5)]
         lgd = dict(line_graph=lg[:, [0, 1, 3]], atom_list=cols[0].long(), target_index=cols[1].long(),
                    source_index=cols[3].long(), target_DE_index=cols[2].long(), source_DE_index=cols[4].long(),
-                   grp_tgt=Grouping.build(cols[1], U, sorted_rows=True),
-                   grp_src=Grouping.build(cols[3], U),
-                   grp_atom=Grouping.build(cols[0], N),
+                   grp_tgt=Grouping.build(cols[1], U, sorted_rows=True, deferred=True),
+                   grp_src=Grouping.build(cols[3], U, deferred=True),
+                   grp_atom=Grouping.build(cols[0], N, deferred=True),
                    # directed edges read by each angle (three-body basis and its backward)
-                   grp_de_t=Grouping.build(cols[2], E),
-                   grp_de_s=Grouping.build(cols[4], E))
+                   grp_de_t=Grouping.build(cols[2], E, deferred=True),
+                   grp_de_s=Grouping.build(cols[4], E, deferred=True))
     else:
         lgd = dict(line_graph=torch.zeros(0, 3, dtype=torch.int64, device=device))
     out["line_graph_dict"] = lgd

@@ -595,22 +595,29 @@ class MatRIS(nn.Module):
     def forward(self, graphs, task: str = "ef", is_training: bool = False) -> dict:
         """model.py:183-250.
 
-        In the "f16x3" MFMA arithmetic the evaluation ends by reading the device's fp16
-        range flag; if any GEMM operand exceeded the fp16 range the whole evaluation is
-        redone in "bf16x6" (a warning says so), so results never carry an overflow."""
+        The evaluation ends with one read of the device status word (the only stream
+        sync of an evaluation): a graph index outside its range (found by the groupings'
+        deferred checks) raises; in the "f16x3" MFMA arithmetic, a GEMM operand beyond the
+        fp16 range makes the whole evaluation run again in "bf16x6" (a warning says so),
+        so results never carry an overflow."""
         if is_training:
             raise NotImplementedError("training (double backward) is outside the efsm inference path")
-        if ops.get_mma_precision() != "f16x3":
-            return self._evaluate(graphs, task)
         dev = next(self.parameters()).device
-        ops.f16_range_take(dev)  # start clean: a failed earlier call may have left it set
-        pred = self._evaluate(graphs, task)
-        if ops.f16_range_take(dev):
+        try:
+            pred = self._evaluate(graphs, task)
+        except BaseException:
+            ops.status_take(dev)  # leave no bits of a failed evaluation behind
+            raise
+        bits = ops.status_take(dev)
+        if bits & ops.STATUS_CSR_KEY:
+            raise RuntimeError("MatRIS: a graph index is outside its range (atom, bond or angle index)")
+        if bits & ops.STATUS_F16_RANGE and ops.get_mma_precision() == "f16x3":
             import warnings
             warnings.warn("MatRIS: an activation exceeded the fp16 range of the f16x3 GEMMs; "
                           "the evaluation was redone in bf16x6", RuntimeWarning, stacklevel=2)
             with ops.mma_precision("bf16x6"):
                 pred = self._evaluate(graphs, task)
+            ops.status_take(dev)
         return pred
 
     def _evaluate(self, graphs, task: str) -> dict:
@@ -639,7 +646,10 @@ class MatRIS(nn.Module):
                                            total_energy=total, is_training=is_training))
         if "m" in task:
             pred["m"] = self.magmom_head(bg, node)
-        apg = torch.tensor(bg["atoms_per_graph"], dtype=torch.int32, device=total.device)
+        if len(bg["atoms_per_graph"]) == 1:  # no host-to-device copy (a stream sync) for one graph
+            apg = torch.full((1,), bg["atoms_per_graph"][0], dtype=torch.int32, device=total.device)
+        else:
+            apg = torch.tensor(bg["atoms_per_graph"], dtype=torch.int32, device=total.device)
         pred["e"] = total / apg if self.is_intensive else total
         pred["atoms_per_graph"] = apg
         pred["ref_energy"] = 0

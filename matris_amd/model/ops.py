@@ -50,15 +50,25 @@ class mma_precision:
         set_mma_precision(self.prev)
 
 
+# Bits of the device status word (include/matris_hip.h MATRIS_STATUS_*).
+STATUS_F16_RANGE = 1  # an "f16x3" kernel met an activation outside the fp16 range
+STATUS_CSR_KEY = 2    # a deferred CSR build met a key outside its segment range
+
+
+def status_take(device=None) -> int:
+    """The device status word (STATUS_* bits) set since the last take; clears it.
+    Synchronizes the current stream: one host read per model evaluation."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    bits = ctypes.c_uint(0)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().matris_status_take(ctypes.byref(bits), _stream()), "matris_status_take")
+    return int(bits.value)
+
+
 def f16_range_take(device=None) -> bool:
     """True if an "f16x3" kernel met an activation outside the fp16 range on `device` since
-    the last call (its results are unusable); clears the flag.  Synchronizes the current
-    stream."""
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    flag = ctypes.c_int(0)
-    with torch.cuda.device(dev):
-        _lib.check(_lib.load().matris_f16_range_take(ctypes.byref(flag), _stream()), "matris_f16_range_take")
-    return bool(flag.value)
+    the last take (its results are unusable).  Clears the whole status word."""
+    return bool(status_take(device) & STATUS_F16_RANGE)
 
 # Optional per-launch timing (bench.py): name -> list of (start, end, info) HIP events
 # recorded on the launch stream around each kernel call.
@@ -127,9 +137,11 @@ class Grouping:
         return int(self.key.numel())
 
     @staticmethod
-    def build(key: torch.Tensor, n_seg: int, sorted_rows: bool = False) -> "Grouping":
+    def build(key: torch.Tensor, n_seg: int, sorted_rows: bool = False, deferred: bool = False) -> "Grouping":
         """Stable CSR of `key` (contiguous int32 device tensor) through matris_csr_build.
-        sorted_rows: the caller guarantees key is non-decreasing (perm is the identity)."""
+        sorted_rows: the caller guarantees key is non-decreasing (perm is the identity).
+        deferred: no host read; a key outside [0, n_seg) sets STATUS_CSR_KEY in the
+        device status word (status_take) instead of raising here."""
         _check_dev(key)
         if key.dtype != torch.int32 or not key.is_contiguous():
             raise TypeError("Grouping keys must be contiguous int32")
@@ -140,8 +152,8 @@ class Grouping:
         perm = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
         ws_bytes = lib.matris_csr_workspace_bytes(R, n_seg)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        _lib.check(lib.matris_csr_build(R, _p(key), 1, n_seg, _p(rowptr), _p(perm), _p(ws), ws_bytes, _stream()),
-                   "matris_csr_build")
+        fn = lib.matris_csr_build_deferred if deferred else lib.matris_csr_build
+        _lib.check(fn(R, _p(key), 1, n_seg, _p(rowptr), _p(perm), _p(ws), ws_bytes, _stream()), "matris_csr_build")
         return Grouping(key, rowptr, None if sorted_rows else perm[:R], n_seg)
 
 

@@ -83,6 +83,26 @@ def test_seg_sum_two_groupings_one_pass(R, S, acc):
         ops.seg_sum_raw(x, ga, second=(xb, ops.Grouping.build(kb, S + 1), 1.0, 256, 128))
 
 
+def test_deferred_csr_build_flags_bad_keys():
+    """matris_csr_build_deferred: valid keys give the same grouping as the synchronous
+    build; a key outside [0, n_seg) is left out and sets STATUS_CSR_KEY (the synchronous
+    build raises instead)."""
+    ops = _ops()
+    ops.status_take()
+    key = _keys(5000, 300, 9).to(DEV)
+    a, b = ops.Grouping.build(key, 300), ops.Grouping.build(key, 300, deferred=True)
+    assert torch.equal(a.rowptr, b.rowptr) and torch.equal(a.perm, b.perm)
+    assert ops.status_take() == 0
+    bad = key.clone()
+    bad[17] = 300
+    g = ops.Grouping.build(bad, 300, deferred=True)
+    assert ops.status_take() == ops.STATUS_CSR_KEY
+    assert int(g.rowptr[-1]) == 4999  # the bad row is not placed
+    with pytest.raises(RuntimeError):
+        ops.Grouping.build(bad, 300)
+    assert ops.status_take() == 0
+
+
 def test_gather_exact():
     ops = _ops()
     src = torch.randn(100, 128, device=DEV)

@@ -176,3 +176,15 @@ def test_f16x3_overflow_falls_back_to_bf16x6(golden):
         assert not ops.f16_range_take()
     for k in "efsm":
         assert np.all(np.isfinite(out[k])) and np.array_equal(out[k], ref[k]), k
+
+
+def test_out_of_range_graph_index_raises(golden):
+    """A graph index outside its range (here an angle's bond index) is refused by the
+    per-graph range check before any kernel reads through it."""
+    z = golden("c1_cu4.npz")
+    g = _graph_from_arrays(z, "g_")
+    g.line_graph[3, 1] = int(g.undirected2directed.shape[0]) + 5
+    model = _model()
+    with pytest.raises(ValueError, match="outside its range"):
+        model([g], task="ef")
+    _efsm(model, [_graph_from_arrays(z, "g_")])  # the next evaluation is clean

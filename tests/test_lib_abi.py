@@ -93,7 +93,8 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_pack_b_bytes(256, 384, 6) == 256 * 384 * 6
     assert lib.matris_pack_b_bytes(256, 384, 3) == lib.matris_pack_b_bytes(256, 384, 0) == 256 * 384 * 4
     assert lib.matris_pack_b_bytes(256, 384, 2) == 256 * 384 * 4 + 16
-    assert lib.matris_f16_range_take(None, None) == -1001
+    assert lib.matris_status_take(None, None) == -1001
+    assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
     assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, None, None, 3, None) == 0
