@@ -14,6 +14,24 @@ from . import ops
 from .ops import Grouping
 
 
+class _ImageShift(torch.autograd.Function):
+    """shift = image @ lattice ([E, 3] x [3, 3]) whose lattice gradient, image^T g ([3, E]
+    x [E, 3]), is a 9-value reduction over the edges: summed as one elementwise product
+    and a reduction instead of a matrix product with K = E (which the library GEMM runs
+    far below bandwidth)."""
+
+    @staticmethod
+    def forward(ctx, image, lattice):
+        ctx.save_for_backward(image)
+        return image @ lattice
+
+    @staticmethod
+    def backward(ctx, g):
+        (image,) = ctx.saved_tensors
+        g_lat = (image[:, :, None] * g[:, None, :]).sum(0) if ctx.needs_input_grad[1] else None
+        return None, g_lat
+
+
 def _sorted(x: torch.Tensor) -> bool:
     return x.numel() < 2 or bool((x[1:] >= x[:-1]).all().item())
 
@@ -110,7 +128,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
 
     # edge geometry (processgraph.py:192-199); image . lattice of the edge's own graph
     if G == 1:
-        shift = image @ lattice
+        shift = _ImageShift.apply(image, lattice)
     else:
         edge_graph = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_dir, device=device),
                                              output_size=E)
