@@ -298,6 +298,17 @@ int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, floa
 int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, const float *res,
                     const float *res_w, int mode, void *stream);
 
+/* Three-body embedding (row E3's consumer): tb = SiLU(Ws (Wa b)) for b [m, 16] the angle
+ * basis, wa = Wa [128, 16] row-major fp32 (angle_embedding, no bias), wsp = Ws [128, 128]
+ * packed by matris_pack_b (SwishLayer linear, no bias) -- ThreebodyEmbedding.forward's
+ * angle_embedding + swish_layer (feature_embed.py:151-203, functions.py:70-95).  Backward:
+ * g_b = Wa^T (Ws^T (g_tb * SiLU'(z))), z = Ws Wa b recomputed from b; wstp = Ws^T packed.
+ * Modes 0, 2, 3 (two fragment planes). */
+int matris_tb_embed_fwd(int64_t m, const float *basis, const float *wa, const void *wsp, float *out, int mode,
+                        void *stream);
+int matris_tb_embed_bwd(int64_t m, const float *basis, const float *g_tb, const float *wa, const void *wsp,
+                        const void *wstp, float *g_basis, int mode, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,6 +103,8 @@ _SIGS = {
     "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
     "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_tb_embed_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
+    "matris_tb_embed_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _P]),
 }
 
 EXPORTED = tuple(_SIGS)

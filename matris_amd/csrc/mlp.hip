@@ -292,6 +292,187 @@ __global__ __launch_bounds__(512, 1) void ffn_fwd_ws_kernel(int64_t M, const flo
     report_range<MODE>(amax, range_flag);
 }
 
+// ------------------------------------------------------------------------------------
+// Three-body embedding (feature_embed.py:151-203 with functions.py:70-95):
+//   tb = SiLU(Ws u),  u = Wa b        b = [M, 16] angle basis, Wa [128, 16], Ws [128, 128]
+// and its input gradient g_b = Wa^T (Ws^T (g_tb * SiLU'(z))), z = Ws u.  Weight-stationary
+// and persistent like ffn_fwd_ws_kernel: u is computed in fp32 while a tile is staged
+// (16 FMAs per value, Wa in LDS) and written as fragment units; the backward recomputes u
+// and z instead of reading saved activations (the basis is 64 B per row).
+// ------------------------------------------------------------------------------------
+#define TB_K 16  // basis width: max_n * max_l
+// Wa in LDS: row r at r * 16 + (r / 16) * 8 floats, so the 8 lanes that read rows 16 q + c
+// (q = 0..7) at one time hit 8 different banks
+#define TB_WA_LDS (128 * TB_K + 8 * 8)
+__device__ __forceinline__ int tb_wa_row(int r) { return r * TB_K + (r >> 4) * 8; }
+
+__device__ __forceinline__ void stage_wa(float *Wa, const float *__restrict__ wa, int tid) {
+    for (int i = tid; i < 128 * TB_K; i += 512) Wa[tb_wa_row(i / TB_K) + i % TB_K] = wa[i];
+}
+
+// Basis rows of tile m0 (rows past M read row M-1): thread (row tid/8, all 16 values).
+__device__ __forceinline__ void load_basis(float4 (&br)[4], const float *__restrict__ b, int64_t m0, int64_t M,
+                                           int tid) {
+    const int64_t row = min(m0 + (tid >> 3), M - 1);
+    const float4 *p = reinterpret_cast<const float4 *>(b + row * TB_K);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) br[i] = p[i];
+}
+
+// u columns 16 q .. 16 q + 15 (q = tid % 8) of the thread's row, as fragment unit k-block q
+// (both halves) of the tile buffer.
+template <int MODE>
+__device__ __forceinline__ float stage_u(uint4 *buf, const float4 (&br)[4], const float *Wa, int tid, float amax) {
+    const int r = tid >> 3, q = tid & 7;
+    const float bv[TB_K] = {br[0].x, br[0].y, br[0].z, br[0].w, br[1].x, br[1].y, br[1].z, br[1].w,
+                            br[2].x, br[2].y, br[2].z, br[2].w, br[3].x, br[3].y, br[3].z, br[3].w};
+    float u[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const float *w = Wa + tb_wa_row(16 * q + c);
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < TB_K; ++j) t = fmaf(w[j], bv[j], t);
+        u[c] = t;
+    }
+    const int unit = (r >> 5) * 8 + q;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const float4 a = make_float4(u[8 * hh], u[8 * hh + 1], u[8 * hh + 2], u[8 * hh + 3]);
+        const float4 c = make_float4(u[8 * hh + 4], u[8 * hh + 5], u[8 * hh + 6], u[8 * hh + 7]);
+        amax = frag_amax<MODE>(amax, a, c);
+        frag_put8<MODE>(buf, unit, (r & 31) + 32 * hh, a, c);
+    }
+    return amax;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void tb_embed_fwd_kernel(int64_t M, const float *__restrict__ basis,
+                                                              const float *__restrict__ wa,
+                                                              const uint4 *__restrict__ Ws, float *__restrict__ out,
+                                                              unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes only");
+    __shared__ uint4 Uf[2 * 8 * 2 * 64];  // u tile as fragment units (32 KB)
+    __shared__ __align__(16) float Wa[TB_WA_LDS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int ct = wave & 3, rt = wave >> 2;
+    const float ss = take_wscale<MODE>(Ws);
+    stage_wa(Wa, wa, tid);
+    uint4 w[8][2];
+    load_wres(w, Ws, ct, lane);
+    const int64_t ntiles = (M + BM - 1) / BM;
+    float amax = 0.f;
+    float4 br[4];
+    int64_t tile = blockIdx.x;
+    load_basis(br, basis, tile * BM, M, tid);
+    __syncthreads();  // Wa staged
+#pragma unroll 1
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t m0 = tile * BM;
+        amax = stage_u<MODE>(Uf, br, Wa, tid, amax);
+        __syncthreads();  // u staged; every wave is past the previous tile's GEMM
+        load_basis(br, basis, min(tile + (int64_t)gridDim.x, ntiles - 1) * BM, M, tid);  // next tile
+        v16f acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, w, Uf, rt, lane);
+        const int64_t row = m0 + rt * 32 + l32;
+        if (row < M) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = make_float4(silu_f(acc[4 * j] * ss), silu_f(acc[4 * j + 1] * ss),
+                                             silu_f(acc[4 * j + 2] * ss), silu_f(acc[4 * j + 3] * ss));
+                *reinterpret_cast<float4 *>(out + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) = v;
+            }
+        }
+        __syncthreads();  // every wave is done reading Uf
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void tb_embed_bwd_kernel(int64_t M, const float *__restrict__ basis,
+                                                              const float *__restrict__ g_tb,
+                                                              const float *__restrict__ wa,
+                                                              const uint4 *__restrict__ Ws,
+                                                              const uint4 *__restrict__ Wst,
+                                                              float *__restrict__ g_basis, unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes only");
+    __shared__ uint4 Uf[2 * 8 * 2 * 64];    // u, then g_z, as fragment units (32 KB)
+    __shared__ __align__(16) float Wa[TB_WA_LDS];
+    __shared__ float part[4][BM][TB_K + 1];  // g_b partial sums per column block (17 KB)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int ct = wave & 3, rt = wave >> 2;
+    const float ss = take_wscale<MODE>(Ws), sst = take_wscale<MODE>(Wst);
+    stage_wa(Wa, wa, tid);
+    uint4 w[8][2], wt[8][2];
+    load_wres(w, Ws, ct, lane);
+    load_wres(wt, Wst, ct, lane);
+    const int64_t ntiles = (M + BM - 1) / BM;
+    float amax = 0.f;
+    float4 br[4];
+    int64_t tile = blockIdx.x;
+    load_basis(br, basis, tile * BM, M, tid);
+    __syncthreads();  // Wa staged
+#pragma unroll 1
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t m0 = tile * BM;
+        amax = stage_u<MODE>(Uf, br, Wa, tid, amax);
+        __syncthreads();  // u staged
+        load_basis(br, basis, min(tile + (int64_t)gridDim.x, ntiles - 1) * BM, M, tid);  // next tile
+        v16f acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, w, Uf, rt, lane);  // z (recomputed)
+        // g_z = g_tb * SiLU'(z): lane (row rt*32 + l32, half h), columns 32 ct + 8 j + 4 h .. +3
+        const int64_t row = m0 + rt * 32 + l32;
+        float4 gz[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 g = row < M ? *reinterpret_cast<const float4 *>(g_tb + row * MATRIS_D + ct * 32 + 8 * j + 4 * h)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+            gz[j] = make_float4(g.x * dsilu_f(acc[4 * j] * ss), g.y * dsilu_f(acc[4 * j + 1] * ss),
+                                g.z * dsilu_f(acc[4 * j + 2] * ss), g.w * dsilu_f(acc[4 * j + 3] * ss));
+            amax = frag_amax<MODE>(amax, gz[j], gz[j]);
+        }
+        __syncthreads();  // every wave is done reading u
+#pragma unroll
+        for (int j = 0; j < 4; ++j) frag_put4<MODE>(Uf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, gz[j]);
+        __syncthreads();  // g_z complete
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, wt, Uf, rt, lane);  // g_u columns 32 ct + 8 j + 4 h .. +3 of the row
+        // g_b partial over this lane's 16 u columns, then over the lane halves
+        float gb[TB_K];
+#pragma unroll
+        for (int k = 0; k < TB_K; ++k) gb[k] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float gu = acc[i] * sst;
+            const float *wr = Wa + tb_wa_row(ct * 32 + 8 * (i >> 2) + 4 * h + (i & 3));
+#pragma unroll
+            for (int k = 0; k < TB_K; ++k) gb[k] = fmaf(wr[k], gu, gb[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < TB_K; ++k) {
+            const float o = __shfl_xor(gb[k], 32, 64);
+            gb[k] = h ? o + gb[k] : gb[k] + o;
+        }
+        if (h == 0) {
+#pragma unroll
+            for (int k = 0; k < TB_K; ++k) part[ct][rt * 32 + l32][k] = gb[k];
+        }
+        __syncthreads();  // partials complete; every wave is done reading g_z
+        for (int e = tid; e < BM * TB_K; e += 512) {
+            const int r = e >> 4, k = e & 15;
+            if (m0 + r < M)
+                g_basis[(m0 + r) * TB_K + k] = ((part[0][r][k] + part[1][r][k]) + part[2][r][k]) + part[3][r][k];
+        }
+        __syncthreads();  // part is read before the next tile overwrites it
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
 // FFN backward: g_x = ((g W2) * SiLU'(p)) W1, with w1t = W1^T, w2t = W2^T row-major.
 template <int MODE>
 __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float *__restrict__ g,
@@ -533,6 +714,46 @@ extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, cons
     if (res && (((uintptr_t)res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
     MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x, res, res_w);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_tb_embed_fwd(int64_t m, const float *basis, const float *wa, const void *wsp, float *out,
+                                   int mode, void *stream) {
+    if (m < 0 || (mode != 0 && mode != 2 && mode != 3) || !mlp_args_ok(mode, {basis, wa, wsp, out}))
+        return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    unsigned *flag = nullptr;
+    if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+    const dim3 grid = persistent_grid(m);
+    hipStream_t st = (hipStream_t)stream;
+    const uint4 *ws = (const uint4 *)wsp;
+    if (mode == 0)
+        tb_embed_fwd_kernel<0><<<grid, 512, 0, st>>>(m, basis, wa, ws, out, flag);
+    else if (mode == 2)
+        tb_embed_fwd_kernel<2><<<grid, 512, 0, st>>>(m, basis, wa, ws, out, flag);
+    else
+        tb_embed_fwd_kernel<3><<<grid, 512, 0, st>>>(m, basis, wa, ws, out, flag);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_tb_embed_bwd(int64_t m, const float *basis, const float *g_tb, const float *wa,
+                                   const void *wsp, const void *wstp, float *g_basis, int mode, void *stream) {
+    if (m < 0 || (mode != 0 && mode != 2 && mode != 3) || !mlp_args_ok(mode, {basis, g_tb, wa, wsp, wstp, g_basis}))
+        return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    unsigned *flag = nullptr;
+    if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+    const dim3 grid = persistent_grid(m);
+    hipStream_t st = (hipStream_t)stream;
+    const uint4 *ws = (const uint4 *)wsp, *wst = (const uint4 *)wstp;
+    if (mode == 0)
+        tb_embed_bwd_kernel<0><<<grid, 512, 0, st>>>(m, basis, g_tb, wa, ws, wst, g_basis, flag);
+    else if (mode == 2)
+        tb_embed_bwd_kernel<2><<<grid, 512, 0, st>>>(m, basis, g_tb, wa, ws, wst, g_basis, flag);
+    else
+        tb_embed_bwd_kernel<3><<<grid, 512, 0, st>>>(m, basis, g_tb, wa, ws, wst, g_basis, flag);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -328,12 +328,18 @@ class ThreebodyEmbedding(nn.Module):
         self.expansion = SphericalExpansion(max_n=max_n, max_l=max_l, cutoff=cutoff)
         self.angle_embedding = nn.Linear(max_n * max_l, three_body_feat_dim, bias=False)
         self.swish_layer = SwishLayer(three_body_feat_dim, three_body_feat_dim, bias=False)
+        self._pack = ops._WeightPack()
 
     def forward(self, graphs):
         lg = graphs["line_graph_dict"]
         exp = self.expansion
         if graphs["unit_edge_vectors"].is_cuda and exp.max_n == 4 and exp.max_l == 4 and "grp_de_t" in lg:
             basis = ops.spherical_basis(graphs["unit_edge_vectors"], lg["grp_de_t"], lg["grp_de_s"], exp.cutoff)
+            lin = self.swish_layer.linear
+            if (ops.tb_embed_supported() and self.angle_embedding.bias is None and lin.bias is None
+                    and tuple(self.angle_embedding.weight.shape) == (128, 16)
+                    and tuple(lin.weight.shape) == (128, 128)):
+                return ops.tb_embed(basis, self.angle_embedding.weight, lin.weight, self._pack)
             return self.swish_layer(self.angle_embedding(basis))
         vij = torch.index_select(graphs["unit_edge_vectors"], 0, lg["target_DE_index"])
         vjk = torch.index_select(graphs["unit_edge_vectors"], 0, lg["source_DE_index"])

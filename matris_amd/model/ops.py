@@ -672,6 +672,50 @@ class _SBF(torch.autograd.Function):
         return g_unit, None, None, None
 
 
+class _TbEmbed(torch.autograd.Function):
+    """tb = SiLU(Ws (Wa b)) over the [A, 16] angle basis (matris_tb_embed_fwd / _bwd);
+    input gradient only."""
+
+    @staticmethod
+    def forward(ctx, basis, wa, pack, mode):
+        _check_dev(basis)
+        lib = _lib.load()
+        basis = _f32c(basis)
+        M = basis.shape[0]
+        out = torch.empty(M, D, dtype=torch.float32, device=basis.device)
+        with _timed("tb_embed_fwd", (M,)):
+            _lib.check(lib.matris_tb_embed_fwd(M, _p(basis), _p(wa), _p(pack.b("w0", mode)), _p(out), mode,
+                                               _stream()), "matris_tb_embed_fwd")
+        ctx.save_for_backward(basis)
+        ctx.wa, ctx.pack, ctx.mode = wa, pack, mode
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (basis,) = ctx.saved_tensors
+        lib = _lib.load()
+        g = _f32c(g)
+        M = basis.shape[0]
+        g_b = torch.empty_like(basis)
+        with _timed("tb_embed_bwd", (M,)):
+            _lib.check(lib.matris_tb_embed_bwd(M, _p(basis), _p(g), _p(ctx.wa), _p(ctx.pack.b("w0", ctx.mode)),
+                                               _p(ctx.pack.b("wt0", ctx.mode)), _p(g_b), ctx.mode, _stream()),
+                       "matris_tb_embed_bwd")
+        return g_b, None, None, None
+
+
+def tb_embed_supported() -> bool:
+    """The fused three-body embedding runs in the two-plane MFMA modes (fp32, f16x3, bf16x3)."""
+    return _MMA["mode"] in (0, 2, 3)
+
+
+def tb_embed(basis, wa_param, ws_param, pack: "_WeightPack"):
+    """SiLU(ws (wa basis)) for bias-free Linear weights wa [128, 16], ws [128, 128]."""
+    pack.get(ws_param)
+    wa = wa_param.detach().float().contiguous()
+    return _TbEmbed.apply(basis, wa, pack, _MMA["mode"])
+
+
 def spherical_basis(unit, grp_t: Grouping, grp_s: Grouping, cutoff: float):
     """[A, 16] three-body basis of every angle from the unit edge vectors [E_d, 3]: grp_t /
     grp_s group the angles by the directed edge they read as i->j (target_DE_index) and

@@ -221,6 +221,31 @@ def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
 _MODES = [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)]
 
 
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("M", [1, 63, 64, 1000, 40961])
+def test_three_body_embedding_fwd_bwd(M, mode, tol):
+    """matris_tb_embed_fwd / _bwd: SiLU(Ws (Wa b)) over the [M, 16] angle basis and its input
+    gradient (ThreebodyEmbedding's angle_embedding + swish_layer, no biases) against fp64."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    torch.manual_seed(M)
+    wa = torch.nn.Linear(16, 128, bias=False).weight.detach()
+    ws = torch.nn.Linear(128, 128, bias=False).weight.detach()
+    b = torch.randn(M, 16)
+    g = torch.randn(M, 128)
+    b64 = b.double().requires_grad_(True)
+    ref = F.silu(F.linear(F.linear(b64, wa.double()), ws.double()))
+    (ref * g.double()).sum().backward()
+    bd = b.to(DEV).requires_grad_(True)
+    try:
+        out = ops.tb_embed(bd, wa.to(DEV), ws.to(DEV), ops._WeightPack())
+        assert _rel(out, ref) < tol
+        out.backward(g.to(DEV))
+        assert _rel(bd.grad, b64.grad) < tol
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 def test_pack_b_fragment_layout():
     """Packed weight = fragment planes: unit ((nt*KB + kb)*NPL + plane)*64 + lane holds
     row n = 32 nt + lane%32, k = 16 kb + 8 (lane//32) + j, j = 0..7."""
