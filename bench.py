@@ -315,8 +315,9 @@ def main():
                     unit="TFLOP/s", frac=round(tf / mma_peak, 4), traffic=None,
                     flops_per_launch=round(flops), mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
                     frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-                    note=f"algorithmic fp32 FLOPs (2*M*(256K+32768)) per launch, mean over {gm['n']} launches in "
-                         f"{args.steps} steps ({n_line} with M=A={A}); peak = {peak_note}")
+                    note=f"algorithmic fp32 FLOPs (2*M*(256K+32768)) per launch, K = the layer-1 width the kernel "
+                         f"multiplies (sources projected before their gather by gmlp_proj excluded), mean over "
+                         f"{gm['n']} launches in {args.steps} steps ({n_line} with M=A={A}); peak = {peak_note}")
     r_f, r_b = gmlp_roof("gmlp_fwd"), gmlp_roof("gmlp_bwd")
     tot = {k: v["mean_s"] * v["n"] for k, v in stats.items()}
     roof = r_b if tot.get("gmlp_bwd", 0) >= tot.get("gmlp_fwd", 0) else r_f

@@ -274,6 +274,29 @@ int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const 
                     const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x, float *g_x0,
                     int acc0, const float *res_w, int mode, void *stream);
 
+/* GatedMLP forward with the layer-1 product of gathered sources taken before the gather
+ * (same layer as matris_gmlp_fwd, GatedMLP.forward in functions.py:297-311, for inputs
+ * such as [angle, bond[tgt], bond[src]] whose gathered rows repeat): a source j read
+ * through an index costs one product per table row instead of one per output row.
+ *   matris_gmlp_project: out [m, 256 n_blk] = x W^T for x [m,128] and W [256 n_blk, 128]
+ *     packed by matris_pack_b -- block b of W is W1's column block of one source
+ *     ([256, 128]: the core rows, then the gate rows), written to columns 256b .. 256b+255.
+ *   matris_gmlp_fwd_proj: matris_gmlp_fwd over the n_src (0..4) sources still multiplied
+ *     in place (w1p = pack of W1's columns of those sources, unused when n_src = 0) plus
+ *     n_proj (0..3) projected sources: row r of the layer-1 output gains
+ *     proj_host[j][proj_idx_host[j][r] * proj_ld_host[j] + c], c < 256 (an index may be
+ *     NULL for the identity; row strides >= 256 and multiples of 4; pointers 16-byte
+ *     aligned; the three arrays are host arrays of n_proj entries).
+ * Outputs and saved p / z are those of matris_gmlp_fwd, so matris_gmlp_bwd with the full
+ * W1^T is its backward. */
+int matris_gmlp_project(int64_t m, const float *x, const void *wp, int n_blk, float *out, int mode, void *stream);
+int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
+                         int n_proj, const float *const *proj_host, const int32_t *const *proj_idx_host,
+                         const int64_t *proj_ld_host, const void *w1p, const float *b1, const void *w2p, const float *b2,
+                         const float *norm_c, const float *norm_g, float eps, float *out, float *save_p,
+                         float *save_z, const float *res_src, const float *res_w, float *res_out, int mode,
+                         void *stream);
+
 /* ------------------------------------------------------------------------------------
  * Dense layers on MFMA, 128-wide rows, no bias.
  * ------------------------------------------------------------------------------------ */

@@ -91,6 +91,9 @@ _SIGS = {
     "matris_env_agg_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_env_agg_bwd": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
     "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_gmlp_project": (_I, [_I64, _P, _P, _I, _P, _I, _P]),
+    "matris_gmlp_fwd_proj": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
+                                  _P, _I, _P]),
     "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I, _P]),
     "matris_bessel_fwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _P]),
     "matris_bessel_bwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _I, _P, _P]),

@@ -53,6 +53,15 @@ struct GmlpSrc {
     const int32_t *idx[4];
 };
 
+// Projected sources (gather after GEMM): row r of the GEMM1 output gains
+// ptr[j][idx[j][r] * ld[j] + c] for c < 256, rows already multiplied by their block of W1.
+struct GmlpProj {
+    const float *ptr[3];
+    const int32_t *idx[3];
+    int64_t ld[3];
+    int n;
+};
+
 // ------------------------------------------------------------------------------------
 // forward
 // ------------------------------------------------------------------------------------
@@ -71,7 +80,7 @@ __device__ __forceinline__ void store_tile256(const float *tile, float *__restri
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src,
+__global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src, GmlpProj proj,
                                                           const uint4 *__restrict__ W1, const float *__restrict__ b1,
                                                           const uint4 *__restrict__ W2, const float *__restrict__ b2,
                                                           const float *__restrict__ norm_c,
@@ -89,8 +98,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
-    const int KB = nsrc * (MATRIS_D / 16);  // k-blocks of W1
-    const float w1s = take_wscale<MODE>(W1), w2s = take_wscale<MODE>(W2);
+    const int KB = nsrc * (MATRIS_D / 16);  // k-blocks of W1 (none without gathered sources)
+    // MODE 2: the accumulator holds s * (W1 x) until scale_acc multiplies by 1/s
+    const float w1up = (MODE == 2 && nsrc > 0) ? reinterpret_cast<const float *>(W1)[1] : 1.0f;
+    const float w1s = nsrc > 0 ? take_wscale<MODE>(W1) : 1.0f, w2s = take_wscale<MODE>(W2);
     float amax = 0.f;
     const int nchunk = nsrc * (MATRIS_D / 32);
 
@@ -156,20 +167,48 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 
     v16f acc[2][2];
     zero_acc(acc);
-    constexpr int BDIST = 3;
-    Frag<MODE> bq0[2], bq1[2], bq2[2], bq3[2];
-    load_bfrags<MODE, 2>(bq0, W1, 2 * wave, KB, 0, lane);
-    load_bfrags<MODE, 2>(bq1, W1, 2 * wave, KB, min(1, KB - 1), lane);
-    load_bfrags<MODE, 2>(bq2, W1, 2 * wave, KB, min(2, KB - 1), lane);
-    GMLP_LOADX(0, xa0, xa1);
-    GMLP_STOREX(0, xa0, xa1);
-    GMLP_LOADX(min(1, nchunk - 1) * 32, xa0, xa1);
-    GMLP_LOADX(min(2, nchunk - 1) * 32, xb0, xb1);
-    __syncthreads();
+    // Projected rows go straight into the accumulator (layout of acc_t_to_lds: row
+    // rt*32 + lane%32, columns 64 wave + 32 ct + 8 j + 4 (lane/32) .. +3).  Issued before
+    // GEMM1's first loads, they arrive while the pipeline fills.
+    if (proj.n > 0) {
+        const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int64_t r = min(m0 + rt * 32 + l32, M - 1);
 #pragma unroll 1
-    for (int c = 0; c < nchunk; c += 2) {  // nchunk = 4 nsrc is even
-        GMLP_CHUNK(c, xa0, xa1, bq0, bq1, bq3, bq0);
-        GMLP_CHUNK(c + 1, xb0, xb1, bq2, bq3, bq1, bq2);
+            for (int j = 0; j < proj.n; ++j) {
+                const int64_t pr = proj.idx[j] ? (int64_t)proj.idx[j][r] : r;
+                const float *pp = proj.ptr[j] + pr * proj.ld[j] + wave * 64 + 4 * h;
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const float4 v = *reinterpret_cast<const float4 *>(pp + ct * 32 + 8 * jj);
+                        acc[rt][ct][4 * jj] += v.x;
+                        acc[rt][ct][4 * jj + 1] += v.y;
+                        acc[rt][ct][4 * jj + 2] += v.z;
+                        acc[rt][ct][4 * jj + 3] += v.w;
+                    }
+            }
+        }
+        if (MODE == 2 && nsrc > 0) scale_acc<MODE>(acc, w1up);  // power of two: exact
+    }
+    if (nsrc > 0) {
+        constexpr int BDIST = 3;
+        Frag<MODE> bq0[2], bq1[2], bq2[2], bq3[2];
+        load_bfrags<MODE, 2>(bq0, W1, 2 * wave, KB, 0, lane);
+        load_bfrags<MODE, 2>(bq1, W1, 2 * wave, KB, min(1, KB - 1), lane);
+        load_bfrags<MODE, 2>(bq2, W1, 2 * wave, KB, min(2, KB - 1), lane);
+        GMLP_LOADX(0, xa0, xa1);
+        GMLP_STOREX(0, xa0, xa1);
+        GMLP_LOADX(min(1, nchunk - 1) * 32, xa0, xa1);
+        GMLP_LOADX(min(2, nchunk - 1) * 32, xb0, xb1);
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < nchunk; c += 2) {  // nchunk = 4 nsrc is even
+            GMLP_CHUNK(c, xa0, xa1, bq0, bq1, bq3, bq0);
+            GMLP_CHUNK(c + 1, xb0, xb1, bq2, bq3, bq1, bq2);
+        }
     }
 #undef GMLP_CHUNK
 #undef GMLP_SUB
@@ -524,14 +563,17 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host,
-                               const int32_t *const *src_idx_host, const void *w1p, const float *b1, const void *w2p,
-                               const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
-                               float *save_p, float *save_z, const float *res_src, const float *res_w,
-                               float *res_out, int mode, void *stream) {
+static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
+                           int n_proj, const float *const *proj_host, const int32_t *const *proj_idx_host,
+                           const int64_t *proj_ld_host, const void *w1p, const float *b1, const void *w2p, const float *b2,
+                           const float *norm_c, const float *norm_g, float eps, float *out, float *save_p,
+                           float *save_z, const float *res_src, const float *res_w, float *res_out, int mode,
+                           void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
-    if (m < 0 || n_src < 1 || n_src > 4 || !src_host || !w1p || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
+    if (m < 0 || n_src < 0 || n_src > 4 || n_proj < 0 || n_proj > 3 || n_src + n_proj < 1 ||
+        (n_src && (!src_host || !w1p)) || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
         return MATRIS_E_ARG;
+    if (n_proj && (!proj_host || !proj_ld_host)) return MATRIS_E_ARG;
     if (m == 0) return 0;
     GmlpSrc s;
     for (int j = 0; j < 4; ++j) {
@@ -539,17 +581,48 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
         s.idx[j] = (j < n_src && src_idx_host) ? src_idx_host[j] : nullptr;
         if (j < n_src && (!s.ptr[j] || !aligned16(s.ptr[j]))) return MATRIS_E_ARG;
     }
-    if (!aligned16(w1p) || !aligned16(w2p)) return MATRIS_E_ARG;
+    GmlpProj pj;
+    pj.n = n_proj;
+    for (int j = 0; j < 3; ++j) {
+        pj.ptr[j] = j < n_proj ? proj_host[j] : nullptr;
+        pj.idx[j] = (j < n_proj && proj_idx_host) ? proj_idx_host[j] : nullptr;
+        pj.ld[j] = j < n_proj ? proj_ld_host[j] : 0;
+        if (j < n_proj && (!pj.ptr[j] || !aligned16(pj.ptr[j]) || pj.ld[j] < 256 || (pj.ld[j] & 3)))
+            return MATRIS_E_ARG;
+    }
+    if ((n_src && !aligned16(w1p)) || !aligned16(w2p)) return MATRIS_E_ARG;
     if (res_out && (!res_src || !res_w)) return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
-    const uint4 *w1 = (const uint4 *)w1p, *w2 = (const uint4 *)w2p;
+    const uint4 *w1 = n_src ? (const uint4 *)w1p : nullptr, *w2 = (const uint4 *)w2p;
     unsigned *flag = nullptr;
     if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
-    MATRIS_MODE_DISPATCH(gmlp_fwd_kernel, grid, st, m, n_src, s, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p,
+    MATRIS_MODE_DISPATCH(gmlp_fwd_kernel, grid, st, m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p,
                          save_z, res_src, res_w, res_out, flag);
     MATRIS_CHECK_LAUNCH();
     return 0;
+}
+
+extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host,
+                               const int32_t *const *src_idx_host, const void *w1p, const float *b1, const void *w2p,
+                               const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
+                               float *save_p, float *save_z, const float *res_src, const float *res_w,
+                               float *res_out, int mode, void *stream) {
+    if (n_src < 1) return MATRIS_E_ARG;
+    return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, 0, nullptr, nullptr, nullptr, w1p, b1, w2p, b2, norm_c, norm_g,
+                           eps, out, save_p, save_z, res_src, res_w, res_out, mode, stream);
+}
+
+extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *src_host,
+                                    const int32_t *const *src_idx_host, int n_proj, const float *const *proj_host,
+                                    const int32_t *const *proj_idx_host, const int64_t *proj_ld_host,
+                                    const void *w1p,
+                                    const float *b1, const void *w2p, const float *b2, const float *norm_c,
+                                    const float *norm_g, float eps, float *out, float *save_p, float *save_z,
+                                    const float *res_src, const float *res_w, float *res_out, int mode,
+                                    void *stream) {
+    return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, n_proj, proj_host, proj_idx_host, proj_ld_host, w1p, b1, w2p,
+                           b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, mode, stream);
 }
 
 extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,

@@ -292,6 +292,50 @@ __global__ __launch_bounds__(512, 1) void ffn_fwd_ws_kernel(int64_t M, const flo
     report_range<MODE>(amax, range_flag);
 }
 
+// Projection of a table by column blocks of W (matris_gmlp_project), weight-stationary:
+// work-group (x, y) keeps W rows 256y .. 256y+255 resident (wave w: the 32 columns
+// 32 w .. +31, 64 VGPRs) and loops over 64-row tiles; out columns 256y + 32w + ...
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void proj_ws_kernel(int64_t M, const float *__restrict__ x,
+                                                         const uint4 *__restrict__ W, float *__restrict__ out,
+                                                         int64_t ldo, unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes only");
+    __shared__ uint4 Xf[2 * 8 * 2 * 64];  // x tile as fragment planes (32 KB)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const float ws = take_wscale<MODE>(W);
+    uint4 w[8][2];
+    load_wres(w, W, 8 * blockIdx.y + wave, lane);
+    out += 256 * blockIdx.y + 32 * wave + 4 * h;
+    const int64_t ntiles = (M + BM - 1) / BM;
+    float amax = 0.f;
+    float4 xr[4];
+    int64_t tile = blockIdx.x;
+    load_rows4(xr, x, tile * BM, M, tid);
+#pragma unroll 1
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t m0 = tile * BM;
+        amax = stage_rows4<MODE>(Xf, xr, tid, amax);
+        __syncthreads();  // x staged
+        load_rows4(xr, x, min(tile + (int64_t)gridDim.x, ntiles - 1) * BM, M, tid);  // next tile
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            v16f acc;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+            gemm_res<MODE>(acc, w, Xf, rt, lane);
+            const int64_t row = m0 + rt * 32 + l32;
+            if (row < M) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    *reinterpret_cast<float4 *>(out + row * ldo + 8 * j) =
+                        make_float4(acc[4 * j] * ws, acc[4 * j + 1] * ws, acc[4 * j + 2] * ws, acc[4 * j + 3] * ws);
+            }
+        }
+        __syncthreads();  // every wave is done reading Xf
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
 // ------------------------------------------------------------------------------------
 // Three-body embedding (feature_embed.py:151-203 with functions.py:70-95):
 //   tb = SiLU(Ws u),  u = Wa b        b = [M, 16] angle basis, Wa [128, 16], Ws [128, 128]
@@ -553,15 +597,21 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
 // ------------------------------------------------------------------------------------
 // projection pair: out0 = x W[0:128]^T, out1 = x W[128:256]^T ; backward
 // g_x = g0 W[0:128] + g1 W[128:256]
+// The forward also serves W of 256 * gridDim.y rows: block y writes x W[256y : 256y+256]^T
+// to columns 256y .. 256y+255 of out0 / out1 (row stride ldo).
 // ------------------------------------------------------------------------------------
 template <int MODE>
 __global__ __launch_bounds__(256, MODE == 6 ? 2 : 3) void pair_fwd_kernel(int64_t M, const float *__restrict__ x,
                                                           const uint4 *__restrict__ W, float *__restrict__ out0,
-                                                          float *__restrict__ out1, unsigned *range_flag) {
+                                                          float *__restrict__ out1, int64_t ldo,
+                                                          unsigned *range_flag) {
     __shared__ __align__(16) float T0[BM * LDT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const float ws = take_wscale<MODE>(W);
+    const int nt0 = 8 * blockIdx.y + 2 * wave;  // first 32-column tile of this wave
+    out0 += 256 * blockIdx.y;
+    out1 += 256 * blockIdx.y;
     // wave w -> output columns [64w, 64w+64) of the 256: waves 0,1 -> out0, 2,3 -> out1
     v16f acc[2][2];
     zero_acc(acc);
@@ -570,23 +620,22 @@ __global__ __launch_bounds__(256, MODE == 6 ? 2 : 3) void pair_fwd_kernel(int64_
         uint4 *Tf = reinterpret_cast<uint4 *>(T0);
         amax = stage_frag128<MODE>(Tf, x, m0, M, tid, amax);
         __syncthreads();
-        gemm_frag_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W, 2 * wave, MATRIS_D / 16, 0,
-                                                          lane);
+        gemm_frag_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W, nt0, MATRIS_D / 16, 0, lane);
     } else {
         stage_tile128(T0, x, MATRIS_D, m0, M, tid);
         __syncthreads();
-        amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, 2 * wave, MATRIS_D / 16, 0, lane);
+        amax = gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, T0, LDT, W, nt0, MATRIS_D / 16, 0, lane);
     }
     scale_acc<MODE>(acc, ws);
     // out0 (waves 0, 1), then out1 (waves 2, 3), pass through the one tile
     __syncthreads();  // T0 free
     if (wave < 2) acc_t_to_lds<2, 2>(acc, T0, LDT, (wave & 1) * 64, lane);
     __syncthreads();
-    store_tile128(T0, out0, MATRIS_D, m0, M, tid);
+    store_tile128(T0, out0, ldo, m0, M, tid);
     __syncthreads();
     if (wave >= 2) acc_t_to_lds<2, 2>(acc, T0, LDT, (wave & 1) * 64, lane);
     __syncthreads();
-    store_tile128(T0, out1, MATRIS_D, m0, M, tid);
+    store_tile128(T0, out1, ldo, m0, M, tid);
     report_range<MODE>(amax, range_flag);
 }
 
@@ -703,7 +752,34 @@ extern "C" int matris_pair_fwd(int64_t m, const float *x, const void *wp, float 
                                void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {x, wp, out0, out1})) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(pair_fwd_kernel, m, x, (const uint4 *)wp, out0, out1);
+    MLP_DISPATCH(pair_fwd_kernel, m, x, (const uint4 *)wp, out0, out1, (int64_t)MATRIS_D);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_gmlp_project(int64_t m, const float *x, const void *wp, int n_blk, float *out, int mode,
+                                   void *stream) {
+    if (m < 0 || n_blk < 1 || n_blk > 4 || !mlp_args_ok(mode, {x, wp, out})) return MATRIS_E_ARG;
+    if (m == 0) return 0;
+    unsigned *flag = nullptr;
+    if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t ldo = 256 * (int64_t)n_blk;
+    if (mode == 6) {
+        const dim3 grid(matris_blocks(m, BM), n_blk);
+        MATRIS_MODE_DISPATCH(pair_fwd_kernel, grid, st, m, x, (const uint4 *)wp, out, out + MATRIS_D, ldo, flag);
+    } else {
+        // one 512-thread work-group per CU in total, split over the column blocks
+        const dim3 pg = persistent_grid(m);
+        const dim3 grid(std::max(1u, pg.x / (unsigned)n_blk), n_blk);
+        const uint4 *w = (const uint4 *)wp;
+        if (mode == 0)
+            proj_ws_kernel<0><<<grid, 512, 0, st>>>(m, x, w, out, ldo, flag);
+        else if (mode == 2)
+            proj_ws_kernel<2><<<grid, 512, 0, st>>>(m, x, w, out, ldo, flag);
+        else
+            proj_ws_kernel<3><<<grid, 512, 0, st>>>(m, x, w, out, ldo, flag);
+    }
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

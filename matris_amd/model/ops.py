@@ -409,16 +409,70 @@ class GmlpPack(_PackCache):
         self._refresh(params, build)
         return self
 
+    def b_blocks(self, blocks: tuple, mode: int):
+        """Pack of W1's column blocks `blocks` side by side ([256, 128 len(blocks)]): the
+        layer-1 weight of the sources multiplied in place."""
+        key = ("w1_cols", blocks, mode)
+        if key not in self._packed:
+            w1 = self.mats["w1"]
+            self._packed[key] = pack_b(torch.cat([w1[:, D * j:D * (j + 1)] for j in blocks], 1).contiguous(), mode)
+        return self._packed[key]
+
+    def b_stack(self, blocks: tuple, mode: int):
+        """Pack of W1's column blocks `blocks` stacked ([256 len(blocks), 128]): the weight
+        of matris_gmlp_project for sources multiplied before their gather."""
+        key = ("w1_stack", blocks, mode)
+        if key not in self._packed:
+            w1 = self.mats["w1"]
+            self._packed[key] = pack_b(torch.cat([w1[:, D * j:D * (j + 1)] for j in blocks], 0).contiguous(), mode)
+        return self._packed[key]
+
 
 def _vec(w):
     """A [1, 128] residual weight as a contiguous fp32 [128] device vector."""
     return w.detach().reshape(-1).float().contiguous()
 
 
+# Gather after GEMM: in a GatedMLP of at least 2^17 rows, a gathered source whose table
+# has at most a quarter as many rows is multiplied by its block of W1 once per table row
+# (matris_gmlp_project) and its products are gathered instead of its features.  Smaller
+# layers lose: the saved layer-1 work is below the cost of the extra launch.
+_GTG = {"on": True, "min_rows": 1 << 17, "ratio": 4}
+
+
+class gather_after_gemm:
+    """Context manager: switch the gather-after-GEMM forward of the GatedMLPs on or off,
+    optionally with another threshold (layers of at least min_rows rows; tables of at
+    most n_rows / ratio rows)."""
+
+    def __init__(self, on: bool, min_rows: int | None = None, ratio: int | None = None):
+        self.new = {"on": bool(on)}
+        if min_rows is not None:
+            self.new["min_rows"] = int(min_rows)
+        if ratio is not None:
+            self.new["ratio"] = int(ratio)
+
+    def __enter__(self):
+        self.old = dict(_GTG)
+        _GTG.update(self.new)
+
+    def __exit__(self, *exc):
+        _GTG.update(self.old)
+
+
+def _projected_sources(srcs, idxs, n_rows: int):
+    """Indices of the sources to multiply before their gather (at most three)."""
+    if not _GTG["on"] or n_rows < _GTG["min_rows"]:
+        return []
+    r = _GTG["ratio"]
+    return [j for j, (s, i) in enumerate(zip(srcs, idxs)) if i is not None and r * s.shape[0] <= n_rows][:3]
+
+
 def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, save: bool = True):
     """matris_gmlp_fwd; srcs are [*,128] fp32 tensors, idxs int32 gather keys or None.
     res = (res_src, res_w) also returns res_out = out + res_w * res_src.
-    Returns (out, p, z, res_out)."""
+    Returns (out, p, z, res_out); the same whether or not sources are projected first
+    (matris_gmlp_fwd_proj), up to the order of the fp32 sums of layer 1."""
     lib = _lib.load()
     dev = srcs[0].device
     nsrc = len(srcs)
@@ -426,14 +480,48 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     p = torch.empty(n_rows, 256, device=dev) if save else None
     z = torch.empty(n_rows, 256, device=dev) if save else None
     res_out = torch.empty(n_rows, D, device=dev) if res is not None else None
-    src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
-    idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
     rs, rw = (res if res is not None else (None, None))
-    with _timed("gmlp_fwd", (n_rows, nsrc * D)):
-        _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
-                                       _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
-                                       _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
-                   "matris_gmlp_fwd")
+    proj = _projected_sources(srcs, idxs, n_rows)
+    if not proj:
+        src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
+        idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
+        with _timed("gmlp_fwd", (n_rows, nsrc * D)):
+            _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
+                                           _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
+                                           _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
+                       "matris_gmlp_fwd")
+        return out, p, z, res_out
+    # one projection launch per distinct table, all of its blocks side by side
+    tables: dict = {}
+    for j in proj:
+        tables.setdefault((srcs[j].data_ptr(), srcs[j].shape[0]), []).append(j)
+    p_ptr, p_idx, p_ld, keep = [], [], [], []
+    for blocks in tables.values():
+        x = srcs[blocks[0]]
+        nb = len(blocks)
+        P = torch.empty(x.shape[0], 256 * nb, device=dev)
+        keep.append(P)
+        with _timed("gmlp_proj", (x.shape[0], nb)):
+            _lib.check(lib.matris_gmlp_project(x.shape[0], _p(x), _p(pack.b_stack(tuple(blocks), mode)), nb, _p(P),
+                                               mode, _stream()), "matris_gmlp_project")
+        for b, j in enumerate(blocks):
+            p_ptr.append(P.data_ptr() + 4 * 256 * b)
+            p_idx.append(idxs[j].data_ptr())
+            p_ld.append(256 * nb)
+    rest = [j for j in range(nsrc) if j not in proj]
+    src_arr = (ctypes.c_void_p * 4)(*[srcs[j].data_ptr() for j in rest])
+    idx_arr = (ctypes.c_void_p * 4)(*[(idxs[j].data_ptr() if idxs[j] is not None else None) for j in rest])
+    n_pj = len(p_ptr)
+    pj_arr = (ctypes.c_void_p * 3)(*p_ptr)
+    pji_arr = (ctypes.c_void_p * 3)(*p_idx)
+    pld_arr = (ctypes.c_int64 * 3)(*p_ld)
+    w1 = _p(pack.b_blocks(tuple(rest), mode)) if rest else None
+    with _timed("gmlp_fwd", (n_rows, len(rest) * D)):  # the layer-1 width this kernel multiplies
+        _lib.check(lib.matris_gmlp_fwd_proj(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr, w1,
+                                            _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
+                                            _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),
+                                            _p(res_out), mode, _stream()), "matris_gmlp_fwd_proj")
+    del keep  # the stream orders any later reuse of these blocks after the launch
     return out, p, z, res_out
 
 

@@ -184,10 +184,62 @@ class _ShimGated(torch.nn.Module):
         self.core_norm, self.gate_norm = t.nc, t.ng
 
 
+@pytest.mark.parametrize("gtg", [True, False])
 @pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
 @pytest.mark.parametrize("nsrc,M", [(3, 1000), (4, 777), (3, 64), (4, 5)])
-def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol):
+def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol, gtg):
+    """GatedMLP over [x0, x1[i1], ...] against fp64; with gtg the gathered tables of at
+    most M/2 rows (M = 1000, 777 here) are multiplied before their gather."""
     ops = _ops()
+    with ops.gather_after_gemm(gtg, min_rows=0, ratio=2):
+        _gated_mlp_case(ops, nsrc, M, mode, tol)
+
+
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("layout", ["atom_graph", "one_table", "big"])
+def test_gated_mlp_all_sources_projected(layout, mode, tol):
+    """matris_gmlp_project + matris_gmlp_fwd_proj with no source multiplied in place
+    (layer 1 is only gathered products): the atom-graph layout [bond[d2u], atom[tgt],
+    atom[src]] (two tables), three gathers of one table (one projection of three blocks),
+    and a 40,000-row table (several row tiles per projection work-group). Values and
+    input gradients against fp64, and against the plain forward."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    torch.manual_seed({"atom_graph": 5, "one_table": 6, "big": 7}[layout])
+    M = 90001 if layout == "big" else 4099
+    sizes = {"atom_graph": [2011, 300, 300], "one_table": [1500] * 3, "big": [40000, 300, 300]}[layout]
+    two = layout != "one_table"
+    base = [torch.randn(sizes[0], 128), torch.randn(sizes[1], 128)][:2 if two else 1]
+    idxs = [torch.randint(0, n, (M,), dtype=torch.int32) for n in sizes]
+    ref = _TorchGMLP(384)
+    b64 = [b.double().requires_grad_(True) for b in base]
+    t64 = [b64[0], b64[1], b64[1]] if two else [b64[0]] * 3
+    x = torch.cat([t64[j][idxs[j].long()] for j in range(3)], 1)
+    ref64 = _TorchGMLP(384).double()
+    ref64.load_state_dict({k: v.double() for k, v in ref.state_dict().items()})
+    out_r = ref64(x)
+    g = torch.randn(M, 128)
+    (out_r * g.double()).sum().backward()
+    mod = _ShimGated(ref).to(DEV)
+    pack = ops.GmlpPack()
+    bd = [b.to(DEV).requires_grad_(True) for b in base]
+    td = [bd[0], bd[1], bd[1]] if two else [bd[0]] * 3
+    try:
+        spec = [(td[j], ops.Grouping.build(idxs[j].to(DEV), sizes[j])) for j in range(3)]
+        with ops.gather_after_gemm(True, min_rows=0, ratio=2):
+            out = ops.gated_mlp(mod, pack, spec)
+        assert _rel(out, out_r) < tol
+        out.backward(g.to(DEV))
+        for j in range(len(base)):
+            assert _rel(bd[j].grad, b64[j].grad) < tol, j
+        with torch.no_grad(), ops.gather_after_gemm(False):
+            plain = ops.gated_mlp(mod, pack, spec)
+        assert _rel(out.detach(), plain.double()) < tol
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
+def _gated_mlp_case(ops, nsrc, M, mode, tol):
     ops.set_mma_precision(mode)
     torch.manual_seed(nsrc * 100 + M)
     K = 128 * nsrc

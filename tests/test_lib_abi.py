@@ -74,6 +74,22 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_gmlp_fwd(10, 1, src1, None, *([v16] * 6), 1e-7, v16, None, None, None, v16, v16, 6,
                                None) == -1001
     assert lib.matris_gmlp_bwd(10, 256, *([v16] * 7), 1e-7, v16, None, 1, None, 6, None) == -1001
+    # gather after GEMM: 0 or 5 projected blocks; no source at all; 4 projected sources;
+    # a projected row stride below 256 or not a multiple of 4; a misaligned projected table
+    assert lib.matris_gmlp_project(10, v16, v16, 0, v16, 6, None) == -1001
+    assert lib.matris_gmlp_project(10, v16, v16, 5, v16, 6, None) == -1001
+    pj = (ctypes.c_void_p * 3)(16, 16, 16)
+    ld = (ctypes.c_int64 * 3)(256, 512, 512)
+    tail = (v16, v16, v16, v16, v16, 1e-7, v16, None, None, None, None, None, 6, None)
+    assert lib.matris_gmlp_fwd_proj(10, 0, None, None, 0, pj, None, ld, None, *tail) == -1001
+    assert lib.matris_gmlp_fwd_proj(10, 0, None, None, 4, pj, None, ld, None, *tail) == -1001
+    assert lib.matris_gmlp_fwd_proj(10, 0, None, None, 1, pj, None, (ctypes.c_int64 * 3)(128, 0, 0), None,
+                                    *tail) == -1001
+    assert lib.matris_gmlp_fwd_proj(10, 0, None, None, 1, pj, None, (ctypes.c_int64 * 3)(258, 0, 0), None,
+                                    *tail) == -1001
+    assert lib.matris_gmlp_fwd_proj(10, 0, None, None, 1, (ctypes.c_void_p * 3)(8), None, ld, None,
+                                    *tail) == -1001
+    assert lib.matris_gmlp_fwd_proj(10, 1, None, None, 1, pj, None, ld, v16, *tail) == -1001
     # dense layers: misaligned row pointer, null operand, unknown mode, residual without weight
     assert lib.matris_ffn_fwd(10, ctypes.c_void_p(8), v16, v16, v16, None, None, None, 6, None) == -1001
     assert lib.matris_ffn_fwd(10, v16, v16, v16, v16, None, v16, None, 6, None) == -1001
