@@ -133,6 +133,22 @@ int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t l
 int matris_gather_rows(const float *src, const int32_t *idx, int64_t n_rows, float scale, int accumulate,
                        float *out, void *stream);
 
+/* Envelope weighting of the atom-graph Refinement (interaction_block.py:243-258 with
+ * is_atom_graph: w = env[d2u]; aggregate(h * w, target)) without materialising h * w:
+ *   matris_seg_sum_mul: out[s, :] = (accumulate ? out[s, :] : 0) + scale *
+ *     sum_{rows r of segment s} x[r, col_off:col_off+128] * mul[mul_idx[r], :]
+ *     (the product first, then the order-fixed segment sum of matris_seg_sum2; mul
+ *     [*, 128] rows; mul_idx NULL: row r's own index; rows_hint as in matris_seg_sum2);
+ *   matris_gather_mul: out[r, :] = (accumulate ? out[r, :] : 0) + a[ia[r], :] * b[ib[r], :]
+ *     (an index may be NULL for the identity).
+ * The refinement's backward is g_h = g_edge_ffn + g_agg[tgt] * env[d2u] (gather_mul) and
+ * g_env = segment sums over d2u of h * g_agg[tgt] (seg_sum_mul). */
+int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx, int64_t col_off,
+                       const int32_t *rowptr, const int32_t *perm, const float *mul, const int32_t *mul_idx,
+                       float scale, int accumulate, float *out, void *stream);
+int matris_gather_mul(int64_t n_rows, const float *a, const int32_t *ia, const float *b, const int32_t *ib,
+                      int accumulate, float *out, void *stream);
+
 /* Backward of the edge vectors vec[e] = cart[tgt[e]] - (cart[src[e]] + shift[e])
  * (row P1, matris/model/processgraph.py:192-199): g_cart [n_atoms, 3] fp32 =
  * sum over the atom's target rows of g_vec [E, 3] minus the sum over its source rows,

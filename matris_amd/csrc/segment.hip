@@ -24,17 +24,32 @@ __device__ __forceinline__ float4 shfl_xor4(const float4 &v, int o) {
 // ------------------------------------------------------------------------------------
 // One wave per segment; each half-wave sums every other row with 16-byte lanes and the
 // halves combine at the end (fixed order: deterministic).
+__device__ __forceinline__ float4 mul4(const float4 &a, const float4 &b) {
+    return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+
 // Partial sum of the rows i = start, start + stride, ... < end of one CSR segment, four
-// rows in flight (16-byte lanes, xc = row base + column offset of the lane).
+// rows in flight (16-byte lanes, xc = row base + column offset of the lane).  MUL: row r
+// contributes x[r] * mc[midx ? midx[r] : r] (mc = a [*, 128] table + the lane's column;
+// the product first, as the reference's h * w before its index_add_).
+template <bool MUL>
 __device__ __forceinline__ float4 seg_rows(const float *__restrict__ xc, int64_t ldx,
-                                           const int32_t *__restrict__ perm, int i, int end, int stride) {
+                                           const int32_t *__restrict__ perm, int i, int end, int stride,
+                                           const float *__restrict__ mc = nullptr,
+                                           const int32_t *__restrict__ midx = nullptr) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (; i + 3 * stride < end; i += 4 * stride) {
         const int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + stride] : i + stride;
         const int64_t r2 = perm ? perm[i + 2 * stride] : i + 2 * stride;
         const int64_t r3 = perm ? perm[i + 3 * stride] : i + 3 * stride;
-        const float4 v0 = ld4(xc + r0 * ldx), v1 = ld4(xc + r1 * ldx);
-        const float4 v2 = ld4(xc + r2 * ldx), v3 = ld4(xc + r3 * ldx);
+        float4 v0 = ld4(xc + r0 * ldx), v1 = ld4(xc + r1 * ldx);
+        float4 v2 = ld4(xc + r2 * ldx), v3 = ld4(xc + r3 * ldx);
+        if constexpr (MUL) {
+            v0 = mul4(v0, ld4(mc + (midx ? (int64_t)midx[r0] : r0) * MATRIS_D));
+            v1 = mul4(v1, ld4(mc + (midx ? (int64_t)midx[r1] : r1) * MATRIS_D));
+            v2 = mul4(v2, ld4(mc + (midx ? (int64_t)midx[r2] : r2) * MATRIS_D));
+            v3 = mul4(v3, ld4(mc + (midx ? (int64_t)midx[r3] : r3) * MATRIS_D));
+        }
         acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;
         acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;
         acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;
@@ -42,7 +57,8 @@ __device__ __forceinline__ float4 seg_rows(const float *__restrict__ xc, int64_t
     }
     for (; i < end; i += stride) {
         const int64_t r = perm ? perm[i] : i;
-        const float4 v = ld4(xc + r * ldx);
+        float4 v = ld4(xc + r * ldx);
+        if constexpr (MUL) v = mul4(v, ld4(mc + (midx ? (int64_t)midx[r] : r) * MATRIS_D));
         acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
     }
     return acc;
@@ -53,17 +69,27 @@ struct SegSrc {
     int64_t ldx, col_off;
     const int32_t *rowptr, *perm;
     float scale;
+    const float *mul;        // optional per-row multiplier rows mul[mul_idx[r]] ([*, 128])
+    const int32_t *mul_idx;
 };
 
 __device__ __forceinline__ float4 add4(const float4 &a, const float4 &b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
+template <bool MUL>
+__device__ __forceinline__ float4 seg_src_rows(const SegSrc &v, int64_t s, int c, int off, int stride) {
+    if (MUL && v.mul)
+        return seg_rows<true>(v.x + v.col_off + c, v.ldx, v.perm, v.rowptr[s] + off, v.rowptr[s + 1], stride,
+                              v.mul + c, v.mul_idx);
+    return seg_rows<false>(v.x + v.col_off + c, v.ldx, v.perm, v.rowptr[s] + off, v.rowptr[s + 1], stride);
+}
+
 // out[s] (+)= a.scale * sum_{rows of a's segment s} a.x[row] + b.scale * (the same for b).
 // WPS waves per segment: 1 (four segments per work-group), or 4 for long segments (the
 // waves take interleaved row slices and combine through LDS).  In a wave the half-waves
 // take alternating rows.  Every combination runs in a fixed order: deterministic.
-template <int WPS>
+template <int WPS, bool MUL>
 __global__ __launch_bounds__(256) void seg_sum_kernel(SegSrc a, SegSrc b, int64_t n_seg, int accumulate,
                                                       float *__restrict__ out) {
     const int w = threadIdx.x >> 6, half = (threadIdx.x >> 5) & 1, l = threadIdx.x & 31, c = 4 * l;
@@ -73,8 +99,8 @@ __global__ __launch_bounds__(256) void seg_sum_kernel(SegSrc a, SegSrc b, int64_
     float4 ta = make_float4(0.f, 0.f, 0.f, 0.f), tb = ta;
     if (live) {
         const int off = 2 * slice + half, stride = 2 * WPS;
-        ta = seg_rows(a.x + a.col_off + c, a.ldx, a.perm, a.rowptr[s] + off, a.rowptr[s + 1], stride);
-        if (b.x) tb = seg_rows(b.x + b.col_off + c, b.ldx, b.perm, b.rowptr[s] + off, b.rowptr[s + 1], stride);
+        ta = seg_src_rows<MUL>(a, s, c, off, stride);
+        if (b.x) tb = seg_src_rows<MUL>(b, s, c, off, stride);
         // half 0 + half 1, the same order in both halves
         const float4 oa = shfl_xor4(ta, 32), ob = shfl_xor4(tb, 32);
         ta = half ? add4(oa, ta) : add4(ta, oa);
@@ -113,10 +139,17 @@ static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64
     if (n_seg < 0 || !out || !seg_src_ok(a) || (b.x && !seg_src_ok(b))) return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    if (rows_hint >= 32 * n_seg)  // long segments: a work-group each
-        seg_sum_kernel<4><<<(unsigned)n_seg, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+    const bool mul = a.mul || (b.x && b.mul);
+    const bool wide = rows_hint >= 32 * n_seg;  // long segments: a work-group each
+    const unsigned grid = wide ? (unsigned)n_seg : (unsigned)matris_blocks(n_seg, WAVES_PER_BLOCK);
+    if (wide && mul)
+        seg_sum_kernel<4, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+    else if (wide)
+        seg_sum_kernel<4, false><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+    else if (mul)
+        seg_sum_kernel<1, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
     else
-        seg_sum_kernel<1><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(a, b, n_seg, accumulate, out);
+        seg_sum_kernel<1, false><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -124,7 +157,8 @@ static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64
 extern "C" int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *rowptr,
                               const int32_t *perm, int64_t n_seg, float scale, int accumulate, float *out,
                               void *stream) {
-    const SegSrc a{x, ldx, col_off, rowptr, perm, scale}, none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f};
+    const SegSrc a{x, ldx, col_off, rowptr, perm, scale, nullptr, nullptr};
+    const SegSrc none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f, nullptr, nullptr};
     return seg_sum_launch(a, none, n_seg, 0, accumulate, out, stream);
 }
 
@@ -132,9 +166,18 @@ extern "C" int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa
                                const int32_t *rowptr_a, const int32_t *perm_a, float scale_a, const float *xb,
                                int64_t ldb, int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b,
                                float scale_b, int accumulate, float *out, void *stream) {
-    const SegSrc a{xa, lda, offa, rowptr_a, perm_a, scale_a};
-    const SegSrc b{xb, ldb, offb, rowptr_b, perm_b, scale_b};
+    const SegSrc a{xa, lda, offa, rowptr_a, perm_a, scale_a, nullptr, nullptr};
+    const SegSrc b{xb, ldb, offb, rowptr_b, perm_b, scale_b, nullptr, nullptr};
     return seg_sum_launch(a, b, n_seg, rows_hint, accumulate, out, stream);
+}
+
+extern "C" int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx, int64_t col_off,
+                                  const int32_t *rowptr, const int32_t *perm, const float *mul,
+                                  const int32_t *mul_idx, float scale, int accumulate, float *out, void *stream) {
+    if (!mul) return MATRIS_E_ARG;
+    const SegSrc a{x, ldx, col_off, rowptr, perm, scale, mul, mul_idx};
+    const SegSrc none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f, nullptr, nullptr};
+    return seg_sum_launch(a, none, n_seg, rows_hint, accumulate, out, stream);
 }
 
 // ------------------------------------------------------------------------------------
@@ -156,6 +199,33 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float *__restric
         v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
     }
     *o = v;
+}
+
+// out[r] (+)= a[ia[r]] * b[ib[r]] (index NULL: the identity), one float4 per thread.
+__global__ __launch_bounds__(256) void gather_mul_kernel(int64_t n_rows, const float *__restrict__ a,
+                                                         const int32_t *__restrict__ ia,
+                                                         const float *__restrict__ b,
+                                                         const int32_t *__restrict__ ib, int accumulate,
+                                                         float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r = t >> 5;
+    if (r >= n_rows) return;
+    const int q = (int)(t & 31) * 4;
+    const int64_t ra = ia ? ia[r] : r, rb = ib ? ib[r] : r;
+    float4 v = mul4(ld4(a + ra * MATRIS_D + q), ld4(b + rb * MATRIS_D + q));
+    float *o = out + r * MATRIS_D + q;
+    if (accumulate) v = add4(ld4(o), v);
+    st4(o, v);
+}
+
+extern "C" int matris_gather_mul(int64_t n_rows, const float *a, const int32_t *ia, const float *b,
+                                 const int32_t *ib, int accumulate, float *out, void *stream) {
+    if (n_rows < 0 || !a || !b || !out) return MATRIS_E_ARG;
+    if (n_rows == 0) return 0;
+    gather_mul_kernel<<<matris_blocks(n_rows * 32, 256), 256, 0, (hipStream_t)stream>>>(n_rows, a, ia, b, ib,
+                                                                                     accumulate, out);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
 }
 
 extern "C" int matris_gather_rows(const float *src, const int32_t *idx, int64_t n_rows, float scale,

@@ -330,17 +330,21 @@ class _AtomRefinement(torch.autograd.Function):
         L, Mm = layer.node_FFN.layers, layer.edge_FFN.layers
         pn = layer._node_ffn.get(L[0].weight, L[3].weight)
         pm = layer._edge_ffn.get(Mm[0].weight, Mm[3].weight)
-        w = ops.gather_raw(env, d2u.key)
         h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [bond, atom, atom], [d2u.key, tgt.key, src.key], Ed, mode)
-        hw = h * w
-        agg = ops.seg_sum_raw(hw, tgt)
-        atom_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(atom, r_n))
         smoothed = bool(layer.use_smoothed_for_delta_edge)
+        if smoothed:  # h * w also feeds the edge FFN: materialised
+            w = ops.gather_raw(env, d2u.key)
+            hw = h * w
+            agg = ops.seg_sum_raw(hw, tgt)
+        else:  # sum_tgt h * env[d2u] in one pass, w never materialised
+            w, hw = env, None
+            agg = ops.seg_sum_mul_raw(h, tgt, env, d2u.key)
+        atom_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(atom, r_n))
         de, p_de = ops.ffn_fwd_raw(pm, hw if smoothed else h, mode)
         del hw, agg
         bond_new = bond * r_e
         ops.seg_sum_raw(de, d2u, 0.5, out=bond_new, accumulate=True)
-        ctx.save_for_backward(w, h, p_h, z_h, p_dn, p_de)
+        ctx.save_for_backward(w, h, p_h, z_h, p_dn, p_de)  # w = env[d2u] if smoothed, else env
         ctx.mode, ctx.layer, ctx.ag, ctx.d2u, ctx.smoothed = mode, layer, ag, d2u, smoothed
         return atom_new, bond_new
 
@@ -361,14 +365,16 @@ class _AtomRefinement(torch.autograd.Function):
         g_agg = ops.ffn_bwd_raw(pn, g_atom_new, p_dn, mode, g_res=g_atom, res_w=r_n)
         g_te = ops.ffn_bwd_raw(pm, ops.gather_raw(g_bond_new, d2u.key, 0.5), p_de, mode)
         del p_dn, p_de
-        g_hw = ops.gather_raw(g_agg, tgt.key)
         if ctx.smoothed:
+            g_hw = ops.gather_raw(g_agg, tgt.key)
             g_hw += g_te
             g_h = g_hw * w
-        else:
-            g_h = torch.addcmul(g_te, g_hw, w)
-        g_env = ops.seg_sum_raw(g_hw * h, d2u)
-        del g_hw, g_te, h, w
+            g_env = ops.seg_sum_raw(g_hw * h, d2u)
+            del g_hw
+        else:  # g_h = g_te + g_agg[tgt] * env[d2u];  g_env = sum_d2u h * g_agg[tgt]
+            g_h = ops.gather_mul_raw(g_agg, tgt.key, w, d2u.key, out=g_te, accumulate=True)
+            g_env = ops.seg_sum_mul_raw(h, d2u, g_agg, tgt.key)
+        del g_te, h, w
         g_bond = g_bond_new * r_e
         g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode)
         del g_h, p_h, z_h

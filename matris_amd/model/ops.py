@@ -191,6 +191,30 @@ def gather_raw(src: torch.Tensor, idx: torch.Tensor, scale: float = 1.0) -> torc
     return out
 
 
+def seg_sum_mul_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: torch.Tensor,
+                    out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """out (+)= segment sums over grp of x[r] * mul[mul_idx[r]] (matris_seg_sum_mul)."""
+    lib = _lib.load()
+    if out is None:
+        out = torch.empty(grp.n_seg, D, dtype=torch.float32, device=x.device)
+    with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
+        _lib.check(lib.matris_seg_sum_mul(grp.n_seg, grp.n_rows, _p(x), D, 0, _p(grp.rowptr), _p(grp.perm), _p(mul),
+                                          _p(mul_idx), 1.0, int(accumulate), _p(out), _stream()),
+                   "matris_seg_sum_mul")
+    return out
+
+
+def gather_mul_raw(a: torch.Tensor, ia, b: torch.Tensor, ib, out: torch.Tensor, accumulate: bool = False):
+    """out[r] (+)= a[ia[r]] * b[ib[r]] (matris_gather_mul; an index None is the identity)."""
+    if out.shape[0] == 0:
+        return out
+    lib = _lib.load()
+    with _timed("gather", (out.shape[0],)):
+        _lib.check(lib.matris_gather_mul(out.shape[0], _p(a), _p(ia), _p(b), _p(ib), int(accumulate), _p(out),
+                                         _stream()), "matris_gather_mul")
+    return out
+
+
 class _EdgeVec(torch.autograd.Function):
     """vec = cart[tgt] - (cart[src] + shift) with a deterministic CSR backward for cart."""
 

@@ -83,6 +83,38 @@ def test_seg_sum_two_groupings_one_pass(R, S, acc):
         ops.seg_sum_raw(x, ga, second=(xb, ops.Grouping.build(kb, S + 1), 1.0, 256, 128))
 
 
+@pytest.mark.parametrize("R,S,T", [(67396, 864, 33698), (5000, 800, 300), (37, 5, 11), (0, 4, 3)])
+@pytest.mark.parametrize("acc", [False, True])
+def test_seg_sum_mul_and_gather_mul(R, S, T, acc):
+    """matris_seg_sum_mul: segment sums of x[r] * mul[mul_idx[r]] (the atom-graph envelope
+    weighting h * env[d2u] summed by target; 78 rows per segment in the first case, one
+    work-group per segment) and matris_gather_mul: out (+)= a[ia] * b[ib], against fp64
+    products followed by index_add_."""
+    ops = _ops()
+    torch.manual_seed(R + S)
+    key = _keys(R, S, 4).to(DEV)
+    grp = ops.Grouping.build(key, S)
+    x = torch.randn(max(R, 1), 128, device=DEV)[:R]
+    mul = torch.randn(T, 128, device=DEV)
+    midx = torch.randint(0, T, (R,), dtype=torch.int32, device=DEV)
+    base = torch.randn(S, 128, device=DEV)
+    out = base.clone()
+    ops.seg_sum_mul_raw(x, grp, mul, midx, out=out, accumulate=acc)
+    prod = x.double().cpu() * mul.double().cpu()[midx.cpu().long()]
+    ref = torch.zeros(S, 128, dtype=torch.float64).index_add_(0, key.cpu().long(), prod)
+    ref = ref + (base.double().cpu() if acc else 0)
+    assert _rel(out, ref) < 2e-6
+    a = torch.randn(S, 128, device=DEV)
+    o2 = torch.randn(R, 128, device=DEV)
+    ref2 = a.double().cpu()[key.cpu().long()] * mul.double().cpu()[midx.cpu().long()]
+    ref2 = ref2 + (o2.double().cpu() if acc else 0)
+    ops.gather_mul_raw(a, key, mul, midx, out=o2, accumulate=acc)
+    if R:
+        assert _rel(o2, ref2) < 1e-6
+    ident = ops.gather_mul_raw(x, None, x, None, out=torch.empty_like(x))
+    assert torch.equal(ident, x * x)
+
+
 def test_deferred_csr_build_flags_bad_keys():
     """matris_csr_build_deferred: valid keys give the same grouping as the synchronous
     build; a key outside [0, n_seg) is left out and sets STATUS_CSR_KEY (the synchronous

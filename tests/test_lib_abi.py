@@ -110,6 +110,10 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_pack_b_bytes(256, 384, 3) == lib.matris_pack_b_bytes(256, 384, 0) == 256 * 384 * 4
     assert lib.matris_pack_b_bytes(256, 384, 2) == 256 * 384 * 4 + 16
     assert lib.matris_status_take(None, None) == -1001
+    # envelope weighting: no multiplier table; a row stride below 128; no output
+    assert lib.matris_seg_sum_mul(4, 10, v16, 128, 0, v16, None, None, v16, 1.0, 0, v16, None) == -1001
+    assert lib.matris_seg_sum_mul(4, 10, v16, 64, 0, v16, None, v16, v16, 1.0, 0, v16, None) == -1001
+    assert lib.matris_gather_mul(10, v16, None, v16, None, 0, None, None) == -1001
     assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
