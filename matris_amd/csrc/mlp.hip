@@ -292,20 +292,21 @@ __global__ __launch_bounds__(512, 1) void ffn_fwd_ws_kernel(int64_t M, const flo
     report_range<MODE>(amax, range_flag);
 }
 
-// Projection of a table by column blocks of W (matris_gmlp_project), weight-stationary:
-// work-group (x, y) keeps W rows 256y .. 256y+255 resident (wave w: the 32 columns
-// 32 w .. +31, 64 VGPRs) and loops over 64-row tiles; out columns 256y + 32w + ...
+// x W^T for W of 256 gridDim.y rows, weight-stationary (the projection pair, and
+// matris_gmlp_project's column blocks): work-group (x, y) keeps W rows 256y .. 256y+255
+// resident (wave w: the 32 columns 32 w .. +31, 64 VGPRs) and loops over 64-row tiles.
+// Columns 256y + c go to out0 + 256y + c (c < 128) or out1 + 256y + c - 128, row stride ldo.
 template <int MODE>
 __global__ __launch_bounds__(512, 1) void proj_ws_kernel(int64_t M, const float *__restrict__ x,
-                                                         const uint4 *__restrict__ W, float *__restrict__ out,
-                                                         int64_t ldo, unsigned *range_flag) {
+                                                         const uint4 *__restrict__ W, float *__restrict__ out0,
+                                                         float *__restrict__ out1, int64_t ldo, unsigned *range_flag) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes only");
     __shared__ uint4 Xf[2 * 8 * 2 * 64];  // x tile as fragment planes (32 KB)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
     const float ws = take_wscale<MODE>(W);
     uint4 w[8][2];
     load_wres(w, W, 8 * blockIdx.y + wave, lane);
-    out += 256 * blockIdx.y + 32 * wave + 4 * h;
+    float *out = (wave < 4 ? out0 + 32 * wave : out1 + 32 * (wave - 4)) + 256 * blockIdx.y + 4 * h;
     const int64_t ntiles = (M + BM - 1) / BM;
     float amax = 0.f;
     float4 xr[4];
@@ -332,6 +333,78 @@ __global__ __launch_bounds__(512, 1) void proj_ws_kernel(int64_t M, const float 
             }
         }
         __syncthreads();  // every wave is done reading Xf
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
+// FFN backward, weight-stationary like ffn_fwd_ws_kernel: g_x = ((g W2) * SiLU'(p)) W1 with
+// w1t, w2t = packs of W1^T, W2^T resident (wave w: columns 32 (w%4) .. +31 of both, rows
+// 32 (w/4) .. +31 of each tile); g_res (optional) = res_w * g, written while g is staged.
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void ffn_bwd_ws_kernel(int64_t M, const float *__restrict__ g,
+                                                            const float *__restrict__ P,
+                                                            const uint4 *__restrict__ W1t,
+                                                            const uint4 *__restrict__ W2t, float *__restrict__ g_x,
+                                                            float *__restrict__ g_res,
+                                                            const float *__restrict__ res_w, unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes only");
+    __shared__ uint4 Xf[2 * 8 * 2 * 64];  // g tile as fragment planes (32 KB)
+    __shared__ uint4 Hf[2 * 8 * 2 * 64];  // g_p tile, the same layout
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int ct = wave & 3, rt = wave >> 2;
+    const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
+    uint4 w1[8][2], w2[8][2];
+    load_wres(w1, W1t, ct, lane);
+    load_wres(w2, W2t, ct, lane);
+    const int64_t ntiles = (M + BM - 1) / BM;
+    float amax = 0.f;
+    float4 xr[4];
+    int64_t tile = blockIdx.x;
+    load_rows4(xr, g, tile * BM, M, tid);
+#pragma unroll 1
+    for (; tile < ntiles; tile += gridDim.x) {
+        const int64_t m0 = tile * BM;
+        if (g_res && m0 + (tid >> 3) < M) {  // the thread's row: columns 8 q .. +7 and 64 + 8 q .. +7
+            const int q = (tid & 7) * 8;
+            float *o = g_res + (m0 + (tid >> 3)) * MATRIS_D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int col = q + 4 * (i & 1) + 64 * (i >> 1);
+                const float4 rw = *reinterpret_cast<const float4 *>(res_w + col);
+                *reinterpret_cast<float4 *>(o + col) =
+                    make_float4(rw.x * xr[i].x, rw.y * xr[i].y, rw.z * xr[i].z, rw.w * xr[i].w);
+            }
+        }
+        amax = stage_rows4<MODE>(Xf, xr, tid, amax);
+        __syncthreads();  // g staged; every wave is past the previous tile's second GEMM
+        load_rows4(xr, g, min(tile + (int64_t)gridDim.x, ntiles - 1) * BM, M, tid);  // next tile
+        v16f acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, w2, Xf, rt, lane);
+        // g_p = (g W2) * SiLU'(p) into Hf: lane (row l32, half h) holds columns
+        // 32 ct + 8 j + 4 h .. +3, half h of unit (rt, k-block 2 ct + j/2), lane l32 + 32 (j%2)
+        const int64_t row = m0 + rt * 32 + l32;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = ct * 32 + 8 * j + 4 * h;
+            const float4 p = row < M ? *reinterpret_cast<const float4 *>(P + row * MATRIS_D + col)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 v = make_float4(acc[4 * j] * w2s * dsilu_f(p.x), acc[4 * j + 1] * w2s * dsilu_f(p.y),
+                                         acc[4 * j + 2] * w2s * dsilu_f(p.z), acc[4 * j + 3] * w2s * dsilu_f(p.w));
+            amax = frag_amax<MODE>(amax, v, v);
+            frag_put4<MODE>(Hf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, v);
+        }
+        __syncthreads();  // g_p complete; every wave is past the first GEMM (Xf free)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        gemm_res<MODE>(acc, w1, Hf, rt, lane);
+        if (row < M) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<float4 *>(g_x + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) =
+                    make_float4(acc[4 * j] * w1s, acc[4 * j + 1] * w1s, acc[4 * j + 2] * w1s, acc[4 * j + 3] * w1s);
+        }
     }
     report_range<MODE>(amax, range_flag);
 }
@@ -700,6 +773,12 @@ static bool mlp_args_ok(int mode, std::initializer_list<const void *> ptrs) {
     return true;
 }
 
+// The weight-stationary FFN backward and projection pair pay their per-work-group weight
+// load back only over many row tiles: below this many rows the tiled kernels are as fast
+// or faster (C3's bond and edge layers, 34k-67k rows, measured on MI355X); the FFN
+// forward is weight-stationary at every size.
+static bool weight_stationary(int64_t m) { return m >= (int64_t(1) << 17); }
+
 // Work-groups of a persistent launch: one 512-thread work-group per CU (the register
 // budget of the weight-stationary kernels), never more than the tiles.
 static dim3 persistent_grid(int64_t m) {
@@ -743,7 +822,21 @@ extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const v
     if (m < 0 || !mlp_args_ok(mode, {g, p, w1tp, w2tp, g_x})) return MATRIS_E_ARG;
     if (g_res && (((uintptr_t)g_res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x, g_res, res_w);
+    if (mode == 6 || !weight_stationary(m)) {
+        MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x, g_res, res_w);
+    } else {
+        unsigned *flag = nullptr;
+        if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+        const dim3 grid = persistent_grid(m);
+        hipStream_t st = (hipStream_t)stream;
+        const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
+        if (mode == 0)
+            ffn_bwd_ws_kernel<0><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, flag);
+        else if (mode == 2)
+            ffn_bwd_ws_kernel<2><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, flag);
+        else
+            ffn_bwd_ws_kernel<3><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, flag);
+    }
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -752,7 +845,22 @@ extern "C" int matris_pair_fwd(int64_t m, const float *x, const void *wp, float 
                                void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {x, wp, out0, out1})) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(pair_fwd_kernel, m, x, (const uint4 *)wp, out0, out1, (int64_t)MATRIS_D);
+    if (mode == 6 || !weight_stationary(m)) {
+        MLP_DISPATCH(pair_fwd_kernel, m, x, (const uint4 *)wp, out0, out1, (int64_t)MATRIS_D);
+    } else {
+        unsigned *flag = nullptr;
+        if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+        const dim3 grid = persistent_grid(m);
+        hipStream_t st = (hipStream_t)stream;
+        const uint4 *w = (const uint4 *)wp;
+        const int64_t ld = MATRIS_D;
+        if (mode == 0)
+            proj_ws_kernel<0><<<grid, 512, 0, st>>>(m, x, w, out0, out1, ld, flag);
+        else if (mode == 2)
+            proj_ws_kernel<2><<<grid, 512, 0, st>>>(m, x, w, out0, out1, ld, flag);
+        else
+            proj_ws_kernel<3><<<grid, 512, 0, st>>>(m, x, w, out0, out1, ld, flag);
+    }
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -774,11 +882,11 @@ extern "C" int matris_gmlp_project(int64_t m, const float *x, const void *wp, in
         const dim3 grid(std::max(1u, pg.x / (unsigned)n_blk), n_blk);
         const uint4 *w = (const uint4 *)wp;
         if (mode == 0)
-            proj_ws_kernel<0><<<grid, 512, 0, st>>>(m, x, w, out, ldo, flag);
+            proj_ws_kernel<0><<<grid, 512, 0, st>>>(m, x, w, out, out + MATRIS_D, ldo, flag);
         else if (mode == 2)
-            proj_ws_kernel<2><<<grid, 512, 0, st>>>(m, x, w, out, ldo, flag);
+            proj_ws_kernel<2><<<grid, 512, 0, st>>>(m, x, w, out, out + MATRIS_D, ldo, flag);
         else
-            proj_ws_kernel<3><<<grid, 512, 0, st>>>(m, x, w, out, ldo, flag);
+            proj_ws_kernel<3><<<grid, 512, 0, st>>>(m, x, w, out, out + MATRIS_D, ldo, flag);
     }
     MATRIS_CHECK_LAUNCH();
     return 0;

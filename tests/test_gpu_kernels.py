@@ -406,8 +406,10 @@ def test_f16x3_range_flag(kind):
 
 
 @pytest.mark.parametrize("mode,tol", _MODES)
-@pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097])
+@pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097, 140001])
 def test_ffn_fwd_bwd(M, mode, tol):
+    """FFN (Linear -> SiLU -> Linear, no bias) against fp64; 140,001 rows take the
+    weight-stationary kernels (modes 0, 2, 3), the others the tiled ones."""
     ops = _ops()
     ops.set_mma_precision(mode)
     torch.manual_seed(M)
@@ -430,8 +432,10 @@ def test_ffn_fwd_bwd(M, mode, tol):
 
 
 @pytest.mark.parametrize("mode,tol", _MODES)
-@pytest.mark.parametrize("M", [1, 65, 3000])
+@pytest.mark.parametrize("M", [1, 65, 3000, 140001])
 def test_proj_pair_fwd_bwd(M, mode, tol):
+    """W_s x, W_t x and the input gradient against fp64 (140,001 rows: the weight-stationary
+    forward in modes 0, 2, 3)."""
     ops = _ops()
     ops.set_mma_precision(mode)
     torch.manual_seed(7 + M)
