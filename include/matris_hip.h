@@ -116,16 +116,19 @@ int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, const int32_t *
                    int64_t n_seg, float scale, int accumulate, float *out, void *stream);
 
 /* out[s, :] = (accumulate ? out[s, :] : 0) + scale_a * (segment sum of source a)
- *             + scale_b * (segment sum of source b), source b optional (xb NULL):
- * two index_add_ calls into one output (the target- and source-side scatters of a
- * gathered GatedMLP input, interaction_block.py:96-100 / functions.py:129-160) in one
- * pass.  Both groupings have n_seg segments.  rows_hint (the rows of the larger grouping)
- * selects one work-group per segment for long segments (>= 32 rows on average) instead
- * of one wave.  Same order-fixed, atomic-free sums as matris_seg_sum. */
+ *             + scale_b * (segment sum of source b) [+ base_w * base[s, :]],
+ * source b optional (xb NULL): two index_add_ calls into one output (the target- and
+ * source-side scatters of a gathered GatedMLP input, interaction_block.py:96-100 /
+ * functions.py:129-160) in one pass.  Both groupings have n_seg segments.  rows_hint (the
+ * rows of the larger grouping) selects one work-group per segment for long segments
+ * (>= 32 rows on average) instead of one wave.  base (optional, [n_seg, 128], with
+ * base_w [128]) adds a residual term, the `de + res_weight * edge_feat` of
+ * interaction_block.py:274-275 (order: the sums, then + base_w * base, then + out).
+ * Same order-fixed, atomic-free sums as matris_seg_sum. */
 int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t lda, int64_t offa,
                     const int32_t *rowptr_a, const int32_t *perm_a, float scale_a, const float *xb, int64_t ldb,
                     int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b, float scale_b, int accumulate,
-                    float *out, void *stream);
+                    const float *base, const float *base_w, float *out, void *stream);
 
 /* out[r, :] = (accumulate ? out[r, :] : 0) + scale * src[idx ? idx[r] : r, :]
  * torch.index_select(x, 0, idx) (interaction_block.py:96-100) and the backward of a

@@ -82,7 +82,8 @@ _SIGS = {
     "matris_csr_build": (_I, [_I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "matris_csr_build_deferred": (_I, [_I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "matris_seg_sum": (_I, [_P, _I64, _I64, _P, _P, _I64, _F, _I, _P, _P]),
-    "matris_seg_sum2": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P]),
+    "matris_seg_sum2": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P, _P,
+                             _P]),
     "matris_gather_rows": (_I, [_P, _P, _I64, _F, _I, _P, _P]),
     "matris_seg_sum_mul": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _F, _I, _P, _P]),
     "matris_gather_mul": (_I, [_I64, _P, _P, _P, _P, _I, _P, _P]),

@@ -85,13 +85,15 @@ __device__ __forceinline__ float4 seg_src_rows(const SegSrc &v, int64_t s, int c
     return seg_rows<false>(v.x + v.col_off + c, v.ldx, v.perm, v.rowptr[s] + off, v.rowptr[s + 1], stride);
 }
 
-// out[s] (+)= a.scale * sum_{rows of a's segment s} a.x[row] + b.scale * (the same for b).
+// out[s] (+)= a.scale * sum_{rows of a's segment s} a.x[row] + b.scale * (the same for b)
+// [+ base_w * base[s]: a residual term, as the reference's `de + res_weight * feat`].
 // WPS waves per segment: 1 (four segments per work-group), or 4 for long segments (the
 // waves take interleaved row slices and combine through LDS).  In a wave the half-waves
 // take alternating rows.  Every combination runs in a fixed order: deterministic.
 template <int WPS, bool MUL>
 __global__ __launch_bounds__(256) void seg_sum_kernel(SegSrc a, SegSrc b, int64_t n_seg, int accumulate,
-                                                      float *__restrict__ out) {
+                                                      const float *__restrict__ base,
+                                                      const float *__restrict__ base_w, float *__restrict__ out) {
     const int w = threadIdx.x >> 6, half = (threadIdx.x >> 5) & 1, l = threadIdx.x & 31, c = 4 * l;
     const int64_t s = (int64_t)blockIdx.x * (WAVES_PER_BLOCK / WPS) + w / WPS;
     const int slice = w % WPS;
@@ -125,6 +127,7 @@ __global__ __launch_bounds__(256) void seg_sum_kernel(SegSrc a, SegSrc b, int64_
     float4 t = make_float4(ta.x * a.scale, ta.y * a.scale, ta.z * a.scale, ta.w * a.scale);
     if (b.x) t = add4(t, make_float4(tb.x * b.scale, tb.y * b.scale, tb.z * b.scale, tb.w * b.scale));
     float *op = out + s * MATRIS_D + c;
+    if (base) t = add4(t, mul4(ld4(base_w + c), ld4(base + s * MATRIS_D + c)));
     if (accumulate) t = add4(t, ld4(op));
     st4(op, t);
 }
@@ -135,21 +138,21 @@ static bool seg_src_ok(const SegSrc &v) {
 }
 
 static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64_t rows_hint, int accumulate,
-                          float *out, void *stream) {
-    if (n_seg < 0 || !out || !seg_src_ok(a) || (b.x && !seg_src_ok(b))) return MATRIS_E_ARG;
+                          float *out, void *stream, const float *base = nullptr, const float *base_w = nullptr) {
+    if (n_seg < 0 || !out || !seg_src_ok(a) || (b.x && !seg_src_ok(b)) || (base && !base_w)) return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     const bool mul = a.mul || (b.x && b.mul);
     const bool wide = rows_hint >= 32 * n_seg;  // long segments: a work-group each
     const unsigned grid = wide ? (unsigned)n_seg : (unsigned)matris_blocks(n_seg, WAVES_PER_BLOCK);
     if (wide && mul)
-        seg_sum_kernel<4, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+        seg_sum_kernel<4, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
     else if (wide)
-        seg_sum_kernel<4, false><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+        seg_sum_kernel<4, false><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
     else if (mul)
-        seg_sum_kernel<1, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+        seg_sum_kernel<1, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
     else
-        seg_sum_kernel<1, false><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, out);
+        seg_sum_kernel<1, false><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -165,10 +168,11 @@ extern "C" int matris_seg_sum(const float *x, int64_t ldx, int64_t col_off, cons
 extern "C" int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t lda, int64_t offa,
                                const int32_t *rowptr_a, const int32_t *perm_a, float scale_a, const float *xb,
                                int64_t ldb, int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b,
-                               float scale_b, int accumulate, float *out, void *stream) {
+                               float scale_b, int accumulate, const float *base, const float *base_w, float *out,
+                               void *stream) {
     const SegSrc a{xa, lda, offa, rowptr_a, perm_a, scale_a, nullptr, nullptr};
     const SegSrc b{xb, ldb, offb, rowptr_b, perm_b, scale_b, nullptr, nullptr};
-    return seg_sum_launch(a, b, n_seg, rows_hint, accumulate, out, stream);
+    return seg_sum_launch(a, b, n_seg, rows_hint, accumulate, out, stream, base, base_w);
 }
 
 extern "C" int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx, int64_t col_off,

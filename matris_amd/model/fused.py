@@ -271,8 +271,7 @@ class _AtomAttention(torch.autograd.Function):
         a_s, a_t = ops.pair_fwd_raw(pp, bond, mode)
         y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, d2u)
         _, p_n, z_n, atom_new = ops.gmlp_fwd_raw(pn, [atom, y_t, y_s], [None, None, None], N, mode, res=(atom, r_n))
-        bond_new = bond * r_e
-        ops.seg_sum_raw(e, d2u, 0.5, out=bond_new, accumulate=True)  # mean of the two directed copies
+        bond_new = ops.seg_sum_raw(e, d2u, 0.5, base=(bond, r_e))  # mean of the two directed copies + r_e bond
         ctx.save_for_backward(p_e, z_e, a_s, a_t, e, y_t, y_s, lse_t, lse_s, p_n, z_n)
         ctx.mode, ctx.layer, ctx.ag, ctx.d2u = mode, layer, ag, d2u
         return atom_new, bond_new
@@ -342,8 +341,7 @@ class _AtomRefinement(torch.autograd.Function):
         atom_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(atom, r_n))
         de, p_de = ops.ffn_fwd_raw(pm, hw if smoothed else h, mode)
         del hw, agg
-        bond_new = bond * r_e
-        ops.seg_sum_raw(de, d2u, 0.5, out=bond_new, accumulate=True)
+        bond_new = ops.seg_sum_raw(de, d2u, 0.5, base=(bond, r_e))
         ctx.save_for_backward(w, h, p_h, z_h, p_dn, p_de)  # w = env[d2u] if smoothed, else env
         ctx.mode, ctx.layer, ctx.ag, ctx.d2u, ctx.smoothed = mode, layer, ag, d2u, smoothed
         return atom_new, bond_new
@@ -375,10 +373,9 @@ class _AtomRefinement(torch.autograd.Function):
             g_h = ops.gather_mul_raw(g_agg, tgt.key, w, d2u.key, out=g_te, accumulate=True)
             g_env = ops.seg_sum_mul_raw(h, d2u, g_agg, tgt.key)
         del g_te, h, w
-        g_bond = g_bond_new * r_e
         g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode)
         del g_h, p_h, z_h
-        ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, out=g_bond, accumulate=True)
+        g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
                         second=(g_x, src, 1.0, 3 * D, 2 * D))
         return g_atom, g_bond, g_env, None, None, None

@@ -161,10 +161,11 @@ class Grouping:
 # segment sum / gather
 # ------------------------------------------------------------------------------------
 def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D, col_off: int = 0,
-                out: torch.Tensor | None = None, accumulate: bool = False, second=None) -> torch.Tensor:
+                out: torch.Tensor | None = None, accumulate: bool = False, second=None, base=None) -> torch.Tensor:
     """out (+)= scale * segment sums of x[:, col_off:col_off+128] over grp; with
     second = (x2, grp2, scale2, ldx2, col_off2) also + scale2 * those of x2 over grp2 (same
-    segment count), in the same pass (matris_seg_sum2)."""
+    segment count), in the same pass (matris_seg_sum2); with base = (feat [n_seg, 128],
+    w [128]) also + w * feat (a residual term)."""
     lib = _lib.load()
     if out is None:
         out = torch.empty(grp.n_seg, D, dtype=torch.float32, device=x.device)
@@ -177,9 +178,11 @@ def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D
         args2 = (_p(x2), ld2, off2, _p(g2.rowptr), _p(g2.perm), s2)
     else:
         args2 = (None, D, 0, None, None, 0.0)
+    bx, bw = base if base is not None else (None, None)
     with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
         _lib.check(lib.matris_seg_sum2(grp.n_seg, rows, _p(x), ldx, col_off, _p(grp.rowptr), _p(grp.perm), scale,
-                                       *args2, int(accumulate), _p(out), _stream()), "matris_seg_sum2")
+                                       *args2, int(accumulate), _p(bx), _p(bw), _p(out), _stream()),
+                   "matris_seg_sum2")
     return out
 
 

@@ -115,6 +115,25 @@ def test_seg_sum_mul_and_gather_mul(R, S, T, acc):
     assert torch.equal(ident, x * x)
 
 
+@pytest.mark.parametrize("R,S", [(67396, 33698), (5000, 80)])
+@pytest.mark.parametrize("acc", [False, True])
+def test_seg_sum_residual_base(R, S, acc):
+    """matris_seg_sum2 with base: out = 0.5 * (segment sums) + w * feat (the atom-graph
+    layers' mean of the two directed copies plus the residual), against fp64."""
+    ops = _ops()
+    torch.manual_seed(R)
+    key = _keys(R, S, 5).to(DEV)
+    grp = ops.Grouping.build(key, S)
+    x = torch.randn(R, 384, device=DEV)
+    feat = torch.randn(S, 128, device=DEV)
+    w = torch.rand(128, device=DEV)
+    prior = torch.randn(S, 128, device=DEV)
+    out = ops.seg_sum_raw(x, grp, 0.5, ldx=384, col_off=128, base=(feat, w), out=prior.clone(), accumulate=acc)
+    ref = torch.zeros(S, 128, dtype=torch.float64).index_add_(0, key.cpu().long(), x[:, 128:256].double().cpu())
+    ref = 0.5 * ref + w.double().cpu() * feat.double().cpu() + (prior.double().cpu() if acc else 0)
+    assert _rel(out, ref) < 2e-6
+
+
 def test_deferred_csr_build_flags_bad_keys():
     """matris_csr_build_deferred: valid keys give the same grouping as the synchronous
     build; a key outside [0, n_seg) is left out and sets STATUS_CSR_KEY (the synchronous
