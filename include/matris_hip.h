@@ -91,7 +91,9 @@ int matris_line_graph_fill(int64_t n_atoms, int64_t n_edges, int64_t n_undirecte
  * Used for every gather's backward (the deterministic replacement of index_add_,
  * matris/model/functions.py:156-157) and for the source side of the segment softmax
  * (functions.py:110-123).  keys may be strided (key of row r = keys[r * key_stride]).
- * workspace: matris_csr_workspace_bytes(n_rows, n_segments). */
+ * workspace: matris_csr_workspace_bytes(n_rows, n_segments).  perm NULL: the caller
+ * guarantees ascending keys, and only rowptr is built (one pass over the keys); a descent
+ * is reported like an out-of-range key. */
 size_t matris_csr_workspace_bytes(int64_t n_rows, int64_t n_segments);
 int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t n_segments,
                      int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes, void *stream);

@@ -720,18 +720,41 @@ __global__ void csr_sort_kernel(int64_t nseg, const int32_t *__restrict__ rowptr
     }
 }
 
+// Row pointers of keys already in ascending order (no permutation): thread i in [0, n]
+// writes rowptr[s] = i for the segments s in (key[i-1], key[i]] (key[-1] = -1, key[n] =
+// nseg).  A key outside [0, nseg) or a descent sets err_bit; every value written is a row
+// position in [0, n] and rowptr is zero-filled first, so even then no reader goes out of
+// bounds.
+__global__ void csr_sorted_kernel(int64_t n, const int32_t *__restrict__ keys, int64_t ks, int64_t nseg,
+                                  int32_t *__restrict__ rowptr, unsigned *__restrict__ err, unsigned err_bit) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > n) return;
+    const int64_t kp = i > 0 ? (int64_t)keys[(i - 1) * ks] : -1;
+    const int64_t k = i < n ? (int64_t)keys[i * ks] : nseg;
+    if ((i < n && (k < 0 || k >= nseg)) || kp > k) atomicOr(err, err_bit);
+    const int64_t s1 = min(k, nseg);
+    for (int64_t s = max(kp + 1, (int64_t)0); s <= s1; ++s) rowptr[s] = (int32_t)i;
+}
+
 extern "C" size_t matris_csr_workspace_bytes(int64_t n_rows, int64_t nseg) {
     return align256(sizeof(int) * (nseg + 1)) + align256(sizeof(int32_t) * (n_rows + 1)) + 256 +
            scan_workspace_bytes(nseg) + 256;
 }
 
 // Histogram, scan, scatter and per-segment sort on `stream`; out-of-range keys are not
-// placed and set err_bit in *err.
+// placed and set err_bit in *err.  perm NULL: the keys are ascending, rowptr only.
 static int csr_build_launch(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg, int32_t *rowptr,
                             int32_t *perm, void *workspace, size_t workspace_bytes, unsigned *err, unsigned err_bit,
                             hipStream_t st) {
-    if (n_rows < 0 || nseg <= 0 || !rowptr || !perm || !workspace || (n_rows > 0 && !keys)) return MATRIS_E_ARG;
+    if (n_rows < 0 || nseg <= 0 || !rowptr || !workspace || (n_rows > 0 && !keys)) return MATRIS_E_ARG;
     if (workspace_bytes < matris_csr_workspace_bytes(n_rows, nseg) || n_rows >= INT32_MAX) return MATRIS_E_ARG;
+    if (!perm) {
+        fill<int32_t>(rowptr, nseg + 1, 0, st);
+        csr_sorted_kernel<<<matris_blocks(n_rows + 1, 256), 256, 0, st>>>(n_rows, keys, key_stride, nseg, rowptr,
+                                                                          err, err_bit);
+        MATRIS_CHECK_LAUNCH();
+        return 0;
+    }
     char *p = (char *)workspace;
     int *cnt = (int *)p; p += align256(sizeof(int) * (nseg + 1));
     int32_t *tmp = (int32_t *)p; p += align256(sizeof(int32_t) * (n_rows + 1));

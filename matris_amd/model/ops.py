@@ -149,7 +149,8 @@ class Grouping:
         R = key.numel()
         dev = key.device
         rowptr = torch.empty(n_seg + 1, dtype=torch.int32, device=dev)
-        perm = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
+        # sorted keys: row pointers only (a descent is reported like an out-of-range key)
+        perm = None if sorted_rows else torch.empty(max(R, 1), dtype=torch.int32, device=dev)
         ws_bytes = lib.matris_csr_workspace_bytes(R, n_seg)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         fn = lib.matris_csr_build_deferred if deferred else lib.matris_csr_build

@@ -45,6 +45,29 @@ def test_csr_build_is_stable_argsort(R, S):
     assert torch.equal(grp.rowptr.cpu().long(), ref_ptr)
 
 
+@pytest.mark.parametrize("R,S", [(0, 5), (1, 1), (264384, 33698), (5000, 800), (7, 40)])
+def test_csr_sorted_keys_rowptr_only(R, S):
+    """Sorted keys (perm NULL): the one-pass row pointers equal the full build's, with
+    empty leading, trailing and interior segments; a descent is flagged like an
+    out-of-range key (status bit when deferred, an error when synchronous)."""
+    ops = _ops()
+    ops.status_take()
+    key = torch.sort(_keys(R, S, R + 3))[0].to(DEV) if R else torch.zeros(0, dtype=torch.int32, device=DEV)
+    a = ops.Grouping.build(key, S, sorted_rows=True, deferred=True)
+    b = ops.Grouping.build(key, S)
+    assert a.perm is None and torch.equal(a.rowptr, b.rowptr)
+    assert ops.status_take() == 0
+    if R > 1:
+        bad = key.clone()
+        bad[0] = S - 1  # a descent after the first row (keys stay in range)
+        if bool((bad[1:] < bad[:-1]).any()):
+            ops.Grouping.build(bad, S, sorted_rows=True, deferred=True)
+            assert ops.status_take() == ops.STATUS_CSR_KEY
+            with pytest.raises(RuntimeError):
+                ops.Grouping.build(bad, S, sorted_rows=True)
+    assert ops.status_take() == 0
+
+
 @pytest.mark.parametrize("R,S,scale,acc", [(3000, 500, 1.0, False), (3000, 500, 0.5, True), (10, 40, 1.0, False)])
 def test_seg_sum_matches_index_add(R, S, scale, acc):
     ops = _ops()
