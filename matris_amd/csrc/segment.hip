@@ -132,6 +132,82 @@ __global__ __launch_bounds__(256) void seg_sum_kernel(SegSrc a, SegSrc b, int64_
     st4(op, t);
 }
 
+// Short segments (at most 4 rows on average, e.g. the two directed copies of a bond): a
+// wave takes 4 consecutive segments, and each half-wave loads the first row of its parity
+// in all four before summing (4 rows in flight where one wave per segment had 1), then
+// any further rows.  Rows are added in the order seg_rows adds them and the halves
+// combine as in seg_sum_kernel: the results are identical.
+template <bool MUL>
+__device__ __forceinline__ void seg_rows4(const SegSrc &v, int64_t s0, int64_t n_seg, int half, int c,
+                                          float4 (&acc)[4]) {
+    const float *xc = v.x + v.col_off + c;
+    int b[4], e[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool in = s0 + j < n_seg;
+        b[j] = in ? v.rowptr[s0 + j] : 0;
+        e[j] = in ? v.rowptr[s0 + j + 1] : 0;
+    }
+    int64_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = b[j] + half;
+        r[j] = i < e[j] ? (v.perm ? (int64_t)v.perm[i] : (int64_t)i) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r[j] >= 0) {
+            x = ld4(xc + r[j] * v.ldx);
+            if constexpr (MUL) x = mul4(x, ld4(v.mul + c + (v.mul_idx ? (int64_t)v.mul_idx[r[j]] : r[j]) * MATRIS_D));
+        }
+        acc[j] = x;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        for (int i = b[j] + half + 2; i < e[j]; i += 2) {
+            const int64_t rr = v.perm ? (int64_t)v.perm[i] : (int64_t)i;
+            float4 x = ld4(xc + rr * v.ldx);
+            if constexpr (MUL) x = mul4(x, ld4(v.mul + c + (v.mul_idx ? (int64_t)v.mul_idx[rr] : rr) * MATRIS_D));
+            acc[j] = add4(acc[j], x);
+        }
+    }
+}
+
+template <bool MUL>
+__global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, int64_t n_seg, int accumulate,
+                                                            const float *__restrict__ base,
+                                                            const float *__restrict__ base_w,
+                                                            float *__restrict__ out) {
+    const int w = threadIdx.x >> 6, half = (threadIdx.x >> 5) & 1, l = threadIdx.x & 31, c = 4 * l;
+    const int64_t s0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + w) * 4;
+    if (s0 >= n_seg) return;  // whole wave
+    float4 ta[4], tb[4];
+    seg_rows4<MUL>(a, s0, n_seg, half, c, ta);
+    if (b.x) seg_rows4<MUL>(b, s0, n_seg, half, c, tb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 oa = shfl_xor4(ta[j], 32);
+        ta[j] = half ? add4(oa, ta[j]) : add4(ta[j], oa);
+        if (b.x) {
+            const float4 ob = shfl_xor4(tb[j], 32);
+            tb[j] = half ? add4(ob, tb[j]) : add4(tb[j], ob);
+        }
+    }
+    if (half) return;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t s = s0 + j;
+        if (s >= n_seg) break;
+        float4 t = make_float4(ta[j].x * a.scale, ta[j].y * a.scale, ta[j].z * a.scale, ta[j].w * a.scale);
+        if (b.x) t = add4(t, make_float4(tb[j].x * b.scale, tb[j].y * b.scale, tb[j].z * b.scale, tb[j].w * b.scale));
+        float *op = out + s * MATRIS_D + c;
+        if (base) t = add4(t, mul4(ld4(base_w + c), ld4(base + s * MATRIS_D + c)));
+        if (accumulate) t = add4(t, ld4(op));
+        st4(op, t);
+    }
+}
+
 static bool seg_src_ok(const SegSrc &v) {
     return v.rowptr && v.ldx >= MATRIS_D && v.col_off >= 0 && v.col_off + MATRIS_D <= v.ldx && !(v.ldx % 4) &&
            !(v.col_off % 4);
@@ -144,6 +220,15 @@ static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64
     hipStream_t st = (hipStream_t)stream;
     const bool mul = a.mul || (b.x && b.mul);
     const bool wide = rows_hint >= 32 * n_seg;  // long segments: a work-group each
+    if (rows_hint > 0 && rows_hint <= 4 * n_seg) {  // short segments: four per wave
+        const unsigned g4 = (unsigned)matris_blocks(n_seg, 4 * WAVES_PER_BLOCK);
+        if (mul)
+            seg_sum_short_kernel<true><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
+        else
+            seg_sum_short_kernel<false><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
+        MATRIS_CHECK_LAUNCH();
+        return 0;
+    }
     const unsigned grid = wide ? (unsigned)n_seg : (unsigned)matris_blocks(n_seg, WAVES_PER_BLOCK);
     if (wide && mul)
         seg_sum_kernel<4, true><<<grid, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);

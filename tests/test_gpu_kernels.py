@@ -83,11 +83,12 @@ def test_seg_sum_matches_index_add(R, S, scale, acc):
     assert _rel(out, ref) < 2e-6
 
 
-@pytest.mark.parametrize("R,S", [(37, 5), (5000, 800), (20000, 3), (3000, 100), (0, 4)])
+@pytest.mark.parametrize("R,S", [(37, 5), (5000, 800), (20000, 3), (3000, 100), (0, 4), (67396, 33698), (61, 59)])
 @pytest.mark.parametrize("acc", [False, True])
 def test_seg_sum_two_groupings_one_pass(R, S, acc):
     """matris_seg_sum2: two groupings of different row sets into one output (the target-
-    and source-side scatters), short segments (a wave each) and long ones (a work-group
+    and source-side scatters): segments of at most 4 rows on average (four per wave, as
+    the two directed copies of a bond), of more (a wave each) and long ones (a work-group
     each, R/S >= 32), against two fp64 index_add_ calls."""
     ops = _ops()
     torch.manual_seed(R + S)
@@ -106,7 +107,8 @@ def test_seg_sum_two_groupings_one_pass(R, S, acc):
         ops.seg_sum_raw(x, ga, second=(xb, ops.Grouping.build(kb, S + 1), 1.0, 256, 128))
 
 
-@pytest.mark.parametrize("R,S,T", [(67396, 864, 33698), (5000, 800, 300), (37, 5, 11), (0, 4, 3)])
+@pytest.mark.parametrize("R,S,T", [(67396, 864, 33698), (5000, 800, 300), (37, 5, 11), (0, 4, 3), (67396, 33698, 864),
+                                   (9, 7, 5)])
 @pytest.mark.parametrize("acc", [False, True])
 def test_seg_sum_mul_and_gather_mul(R, S, T, acc):
     """matris_seg_sum_mul: segment sums of x[r] * mul[mul_idx[r]] (the atom-graph envelope
