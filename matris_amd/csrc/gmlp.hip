@@ -244,30 +244,31 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     __syncthreads();  // every wave is done reading h
 
     // z = acc + b2 -> LDS (16-byte writes); then a row pass with 16 lanes per row: lane
-    // c of a row holds core columns 8c .. 8c+7 and the same gate columns, saves z and
-    // writes out with 512-byte row stores, and each RMSNorm sum is a 16-lane DPP sum
+    // c of a row holds core columns 4c .. 4c+3 and 64 + 4c .. +3 and the same gate
+    // columns, so each store instruction writes 256 contiguous bytes of a row; each
+    // RMSNorm sum is a 16-lane DPP sum
     acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b2);
     __syncthreads();
-    const int c8 = (lane & 15) * 8;
-    const float4 wc0 = *reinterpret_cast<const float4 *>(norm_c + c8);
-    const float4 wc1 = *reinterpret_cast<const float4 *>(norm_c + c8 + 4);
-    const float4 wg0 = *reinterpret_cast<const float4 *>(norm_g + c8);
-    const float4 wg1 = *reinterpret_cast<const float4 *>(norm_g + c8 + 4);
+    const int c4 = (lane & 15) * 4;
+    const float4 wc0 = *reinterpret_cast<const float4 *>(norm_c + c4);
+    const float4 wc1 = *reinterpret_cast<const float4 *>(norm_c + 64 + c4);
+    const float4 wg0 = *reinterpret_cast<const float4 *>(norm_g + c4);
+    const float4 wg1 = *reinterpret_cast<const float4 *>(norm_g + 64 + c4);
 #pragma unroll
     for (int rr = 0; rr < BM / 16; ++rr) {
         const int row = wave * (BM / 4) + rr * 4 + (lane >> 4);
         const float *zr = Ts + row * LDH;
-        const float4 zc0 = *reinterpret_cast<const float4 *>(zr + c8);
-        const float4 zc1 = *reinterpret_cast<const float4 *>(zr + c8 + 4);
-        const float4 zg0 = *reinterpret_cast<const float4 *>(zr + MATRIS_D + c8);
-        const float4 zg1 = *reinterpret_cast<const float4 *>(zr + MATRIS_D + c8 + 4);
+        const float4 zc0 = *reinterpret_cast<const float4 *>(zr + c4);
+        const float4 zc1 = *reinterpret_cast<const float4 *>(zr + 64 + c4);
+        const float4 zg0 = *reinterpret_cast<const float4 *>(zr + MATRIS_D + c4);
+        const float4 zg1 = *reinterpret_cast<const float4 *>(zr + MATRIS_D + 64 + c4);
         const int64_t grow = m0 + row;
         if (save_z && grow < M) {
-            float *zo = save_z + grow * 256 + c8;
+            float *zo = save_z + grow * 256 + c4;
             *reinterpret_cast<float4 *>(zo) = zc0;
-            *reinterpret_cast<float4 *>(zo + 4) = zc1;
+            *reinterpret_cast<float4 *>(zo + 64) = zc1;
             *reinterpret_cast<float4 *>(zo + MATRIS_D) = zg0;
-            *reinterpret_cast<float4 *>(zo + MATRIS_D + 4) = zg1;
+            *reinterpret_cast<float4 *>(zo + MATRIS_D + 64) = zg1;
         }
         const float rc = rsqrtf(row16_sum(zc0.x * zc0.x + zc0.y * zc0.y + zc0.z * zc0.z + zc0.w * zc0.w +
                                           zc1.x * zc1.x + zc1.y * zc1.y + zc1.z * zc1.z + zc1.w * zc1.w) *
@@ -285,19 +286,19 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         o1.z = silu_f(zc1.z * rc * wc1.z) * sigm_f(zg1.z * rg * wg1.z);
         o1.w = silu_f(zc1.w * rc * wc1.w) * sigm_f(zg1.w * rg * wg1.w);
         if (grow < M) {
-            float *orow = out + grow * MATRIS_D + c8;
+            float *orow = out + grow * MATRIS_D + c4;
             *reinterpret_cast<float4 *>(orow) = o0;
-            *reinterpret_cast<float4 *>(orow + 4) = o1;
+            *reinterpret_cast<float4 *>(orow + 64) = o1;
             if (res_out) {
-                const float4 w0 = *reinterpret_cast<const float4 *>(res_w + c8);
-                const float4 w1 = *reinterpret_cast<const float4 *>(res_w + c8 + 4);
-                const float4 x0 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c8);
-                const float4 x1 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c8 + 4);
-                float *ro = res_out + grow * MATRIS_D + c8;
+                const float4 w0 = *reinterpret_cast<const float4 *>(res_w + c4);
+                const float4 w1 = *reinterpret_cast<const float4 *>(res_w + 64 + c4);
+                const float4 x0 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c4);
+                const float4 x1 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + 64 + c4);
+                float *ro = res_out + grow * MATRIS_D + c4;
                 *reinterpret_cast<float4 *>(ro) = make_float4(o0.x + w0.x * x0.x, o0.y + w0.y * x0.y, o0.z + w0.z * x0.z,
                                                               o0.w + w0.w * x0.w);
-                *reinterpret_cast<float4 *>(ro + 4) = make_float4(o1.x + w1.x * x1.x, o1.y + w1.y * x1.y,
-                                                                  o1.z + w1.z * x1.z, o1.w + w1.w * x1.w);
+                *reinterpret_cast<float4 *>(ro + 64) = make_float4(o1.x + w1.x * x1.x, o1.y + w1.y * x1.y,
+                                                                   o1.z + w1.z * x1.z, o1.w + w1.w * x1.w);
             }
         }
     }
@@ -348,16 +349,17 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 
     // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g).
     // 16 lanes per row (4 rows per wave per pass, wave w owns rows [16w, 16w+16)): lane c
-    // of a row owns core and gate columns 8c .. 8c+7, reads them with 512-byte row loads,
-    // and the four row reductions are 16-lane DPP sums.  Rows past M read zeros (g = 0).
+    // of a row owns core and gate columns 4c .. 4c+3 and 64 + 4c .. +3, so each load
+    // instruction reads 256 contiguous bytes of a row; the four row reductions are
+    // 16-lane DPP sums.  Rows past M read zeros (g = 0).
     {
-        const int c8 = (lane & 15) * 8;
+        const int c4 = (lane & 15) * 4;
         float wc[8], wg[8];
         {
-            const float4 a0 = *reinterpret_cast<const float4 *>(norm_c + c8);
-            const float4 a1 = *reinterpret_cast<const float4 *>(norm_c + c8 + 4);
-            const float4 b0 = *reinterpret_cast<const float4 *>(norm_g + c8);
-            const float4 b1 = *reinterpret_cast<const float4 *>(norm_g + c8 + 4);
+            const float4 a0 = *reinterpret_cast<const float4 *>(norm_c + c4);
+            const float4 a1 = *reinterpret_cast<const float4 *>(norm_c + 64 + c4);
+            const float4 b0 = *reinterpret_cast<const float4 *>(norm_g + c4);
+            const float4 b1 = *reinterpret_cast<const float4 *>(norm_g + 64 + c4);
             wc[0] = a0.x; wc[1] = a0.y; wc[2] = a0.z; wc[3] = a0.w; wc[4] = a1.x; wc[5] = a1.y; wc[6] = a1.z; wc[7] = a1.w;
             wg[0] = b0.x; wg[1] = b0.y; wg[2] = b0.z; wg[3] = b0.w; wg[4] = b1.x; wg[5] = b1.y; wg[6] = b1.z; wg[7] = b1.w;
         }
@@ -367,10 +369,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             const int64_t m = m0 + row;
             float zc[8], zg[8], go[8];
             if (m < M) {
-                const float4 *zr = reinterpret_cast<const float4 *>(Z + m * 256 + c8);
-                const float4 *gr = reinterpret_cast<const float4 *>(g_out + m * MATRIS_D + c8);
-                const float4 z0 = zr[0], z1 = zr[1], y0 = zr[MATRIS_D / 4], y1 = zr[MATRIS_D / 4 + 1];
-                const float4 g0 = gr[0], g1 = gr[1];
+                const float4 *zr = reinterpret_cast<const float4 *>(Z + m * 256 + c4);
+                const float4 *gr = reinterpret_cast<const float4 *>(g_out + m * MATRIS_D + c4);
+                const float4 z0 = zr[0], z1 = zr[16], y0 = zr[MATRIS_D / 4], y1 = zr[MATRIS_D / 4 + 16];
+                const float4 g0 = gr[0], g1 = gr[16];
                 zc[0] = z0.x; zc[1] = z0.y; zc[2] = z0.z; zc[3] = z0.w; zc[4] = z1.x; zc[5] = z1.y; zc[6] = z1.z; zc[7] = z1.w;
                 zg[0] = y0.x; zg[1] = y0.y; zg[2] = y0.z; zg[3] = y0.w; zg[4] = y1.x; zg[5] = y1.y; zg[6] = y1.z; zg[7] = y1.w;
                 go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w; go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
@@ -410,18 +412,23 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                      (gng[4 * e4 + 3] - ng[4 * e4 + 3] * dg) * rg);
             }
             if constexpr (PS) {
-                // g_z columns c8 .. c8+7 (core) and 128 + c8 .. (gate) of this row: one
-                // fragment unit each, (rt = row/32, kb = c8/16 (+8), lane row%32 + 32 (c8/8 % 2))
-                const int unit = (row >> 5) * 16 + (c8 >> 4), fl = (row & 31) + 32 * ((c8 >> 3) & 1);
+                // g_z columns c (= 4c' and 64 + 4c', core; + 128, gate) of this row: half
+                // (c/4 % 2) of fragment unit (rt = row/32, kb = c/16), lane row%32 + 32 (c/8 % 2)
                 amax = frag_amax<MODE>(frag_amax<MODE>(amax, vc[0], vc[1]), vg[0], vg[1]);
-                frag_put8<MODE>(Gf, unit, fl, vc[0], vc[1]);
-                frag_put8<MODE>(Gf, unit + 8, fl, vg[0], vg[1]);
-            } else {
-                float *gr = G + row * LDH + c8;
+                const int rb = (row >> 5) * 16, fr = row & 31;
 #pragma unroll
                 for (int e4 = 0; e4 < 2; ++e4) {
-                    *reinterpret_cast<float4 *>(gr + 4 * e4) = vc[e4];
-                    *reinterpret_cast<float4 *>(gr + MATRIS_D + 4 * e4) = vg[e4];
+                    const int c = c4 + 64 * e4;
+                    const int fl = fr + 32 * ((c >> 3) & 1), hh = (c >> 2) & 1;
+                    frag_put4<MODE>(Gf, rb + (c >> 4), fl, hh, vc[e4]);
+                    frag_put4<MODE>(Gf, rb + 8 + (c >> 4), fl, hh, vg[e4]);
+                }
+            } else {
+                float *gr = G + row * LDH + c4;
+#pragma unroll
+                for (int e4 = 0; e4 < 2; ++e4) {
+                    *reinterpret_cast<float4 *>(gr + 64 * e4) = vc[e4];
+                    *reinterpret_cast<float4 *>(gr + MATRIS_D + 64 * e4) = vg[e4];
                 }
             }
         }
