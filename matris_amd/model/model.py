@@ -22,6 +22,7 @@ readout.py, basis_function.py.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from collections.abc import Sequence
 
@@ -456,6 +457,12 @@ class Refinement(nn.Module):
         return dn + self.node_res_weight * node_feat, de + self.edge_res_weight * edge_feat
 
 
+def _ckpt_contexts():
+    """torch.utils.checkpoint context_fn: the original pass of a checkpointed block writes no
+    saved-for-backward activations (ops.discard_saves); the recomputation writes them."""
+    return ops.discard_saves(), contextlib.nullcontext()
+
+
 class Interaction_Block(nn.Module):
     """interaction_block.py:281-446.  The reference checkpoints the two line-graph layers
     when A > 60000 (:400-413); here the fused line layers recompute their forward inside
@@ -643,7 +650,7 @@ class MatRIS(nn.Module):
         for layer in self.interaction_block:
             if ckpt:  # keep only the block inputs; the block's forward reruns in the backward
                 node, edge, tb = torch.utils.checkpoint.checkpoint(layer, bg, node, edge, tb, smooth,
-                                                                   use_reentrant=False)
+                                                                   use_reentrant=False, context_fn=_ckpt_contexts)
             else:
                 node, edge, tb = layer(bg, node, edge, tb, smooth)
         node = self.readout_norm(node)

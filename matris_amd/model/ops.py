@@ -461,6 +461,27 @@ def _vec(w):
     return w.detach().reshape(-1).float().contiguous()
 
 
+# Discarded saves: inside the original pass of a non-reentrant activation checkpoint the
+# tensors a layer saves for its backward are dropped (the backward recomputes them), so
+# the GatedMLP and FFN forwards there leave their saved pre-activations unwritten: p and z
+# come back as uninitialised tensors of the right shape (the checkpoint still checks the
+# shapes of what the recomputation saves against them) and the kernels skip those stores.
+_DISCARD = {"on": False}
+
+
+class discard_saves:
+    """Context manager for the original pass of a checkpointed region (torch.utils.checkpoint
+    context_fn): saved-for-backward activations are not written.  Everything a layer returns
+    is computed as usual."""
+
+    def __enter__(self):
+        self.old = _DISCARD["on"]
+        _DISCARD["on"] = True
+
+    def __exit__(self, *exc):
+        _DISCARD["on"] = self.old
+
+
 # Gather after GEMM: in a GatedMLP of at least 2^17 rows, a gathered source whose table
 # has at most a quarter as many rows is multiplied by its block of W1 once per table row
 # (matris_gmlp_project) and its products are gathered instead of its features.  Smaller
@@ -510,6 +531,9 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     res_out = torch.empty(n_rows, D, device=dev) if res is not None else None
     rs, rw = (res if res is not None else (None, None))
     proj = _projected_sources(srcs, idxs, n_rows)
+    ret_p, ret_z = p, z
+    if _DISCARD["on"]:  # placeholders: the kernel writes neither
+        p = z = None
     if not proj:
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
@@ -518,7 +542,7 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
                                            _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
                                            _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
                        "matris_gmlp_fwd")
-        return out, p, z, res_out
+        return out, ret_p, ret_z, res_out
     # one projection launch per distinct table, all of its blocks side by side
     tables: dict = {}
     for j in proj:
@@ -550,7 +574,7 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
                                             _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),
                                             _p(res_out), mode, _stream()), "matris_gmlp_fwd_proj")
     del keep  # the stream orders any later reuse of these blocks after the launch
-    return out, p, z, res_out
+    return out, ret_p, ret_z, res_out
 
 
 def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None, acc0: bool = False, res_w=None):
@@ -638,8 +662,9 @@ def ffn_fwd_raw(pack: _WeightPack, x, mode: int, res=None, save: bool = True):
     out = torch.empty(M, D, device=x.device)
     p = torch.empty(M, D, device=x.device) if save else None
     rs, rw = (res if res is not None else (None, None))
+    kp = None if _DISCARD["on"] else p  # discarded saves: a placeholder, not written
     with _timed("ffn_fwd", (M,)):
-        _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.b("w0", mode)), _p(pack.b("w1", mode)), _p(out), _p(p),
+        _lib.check(lib.matris_ffn_fwd(M, _p(x), _p(pack.b("w0", mode)), _p(pack.b("w1", mode)), _p(out), _p(kp),
                                       _p(rs), _p(rw), mode, _stream()), "matris_ffn_fwd")
     return out, p
 

@@ -449,6 +449,32 @@ def test_f16x3_range_flag(kind):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+def test_discarded_saves_leave_outputs_unchanged():
+    """ops.discard_saves (the original pass of a checkpointed block): the GatedMLP and FFN
+    forwards return the same outputs bit for bit, and placeholders of the saved tensors'
+    shapes instead of written p / z."""
+    ops = _ops()
+    torch.manual_seed(3)
+    ref = _TorchGMLP(384)
+    mod = _ShimGated(ref).to(DEV)
+    pack = ops.GmlpPack()
+    M = 140001
+    tb, bond = torch.randn(M, 128, device=DEV), torch.randn(5000, 128, device=DEV)
+    it = torch.randint(0, 5000, (M,), device=DEV, dtype=torch.int32)
+    isrc = torch.randint(0, 5000, (M,), device=DEV, dtype=torch.int32)
+    args = (pack.get(mod), [tb, bond, bond], [None, it, isrc], M, ops._MMA["mode"])
+    out, p, z, _ = ops.gmlp_fwd_raw(*args)
+    with ops.discard_saves():
+        out2, p2, z2, _ = ops.gmlp_fwd_raw(*args)
+    assert torch.equal(out, out2) and p2.shape == p.shape and z2.shape == z.shape
+    l1, l2 = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
+    wp = ops._WeightPack().get(l1, l2)
+    o, q = ops.ffn_fwd_raw(wp, tb, ops._MMA["mode"])
+    with ops.discard_saves():
+        o2, q2 = ops.ffn_fwd_raw(wp, tb, ops._MMA["mode"])
+    assert torch.equal(o, o2) and q2.shape == q.shape
+
+
 @pytest.mark.parametrize("mode,tol", _MODES)
 @pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097, 140001])
 def test_ffn_fwd_bwd(M, mode, tol):
