@@ -32,15 +32,27 @@ SAVED_BYTES_PER_ANGLE_BLOCK = 4 * (2 * 256 + 3 * 128 + 2 * 256 + 2 * 128 + 128)
 SAVED_BYTES_PER_EDGE_BLOCK = 4 * 16 * 128
 
 
-def checkpoint_needed(n_angles: int, n_edges: int, n_blocks: int, device=None, total_bytes: int | None = None) -> bool:
-    """Checkpoint each interaction block (keep its inputs, rerun its forward in the
-    backward) when the whole model's saved activations would exceed 45% of the device's
-    memory (total_bytes, default: the device's capacity).  The reference checkpoints its
-    two line-graph layers above 60,000 angles regardless of memory
+def blocks_to_checkpoint(n_angles: int, n_edges: int, n_blocks: int, device=None,
+                         total_bytes: int | None = None) -> int:
+    """How many leading interaction blocks to checkpoint (keep their inputs, rerun their
+    forward in the backward): none when the whole model's saved activations fit in 45% of
+    the device's memory (total_bytes, default: the device's capacity), otherwise all but
+    as many trailing blocks as fit there.  The trailing blocks' backward runs first and
+    frees their activations before any checkpointed block is recomputed, so keeping k of
+    them raises the peak over full checkpointing only when k exceeds one.  The reference
+    checkpoints its two line-graph layers above 60,000 angles regardless of memory
     (interaction_block.py:15, :400-413)."""
     total = total_bytes if total_bytes is not None else torch.cuda.get_device_properties(device).total_memory
     per_block = n_angles * SAVED_BYTES_PER_ANGLE_BLOCK + n_edges * SAVED_BYTES_PER_EDGE_BLOCK
-    return n_blocks * per_block > 0.45 * total
+    budget = 0.45 * total
+    if n_blocks * per_block <= budget:
+        return 0
+    return n_blocks - min(n_blocks, int(budget // per_block))
+
+
+def checkpoint_needed(n_angles: int, n_edges: int, n_blocks: int, device=None, total_bytes: int | None = None) -> bool:
+    """Whether any interaction block is checkpointed (blocks_to_checkpoint > 0)."""
+    return blocks_to_checkpoint(n_angles, n_edges, n_blocks, device, total_bytes) > 0
 
 
 def _zeros_if_none(g, like):

@@ -580,8 +580,9 @@ class MatRIS(nn.Module):
         self.config = {k: v for k, v in locals().items() if k not in ("self", "__class__", "verbose")}
         self.is_intensive = is_intensive
         # Memory modes for large cells.  block_checkpoint: None = decided per call from the
-        # activation footprint (fused.checkpoint_needed), True / False = forced; each block
-        # then keeps only its inputs and reruns its forward in the backward.
+        # activation footprint (fused.blocks_to_checkpoint: the leading blocks that do not
+        # fit), True / False = all / none; a checkpointed block keeps only its inputs and
+        # reruns its forward in the backward.
         # line_recompute: the two line-graph layers alone keep only their inputs.
         self.block_checkpoint: bool | None = None
         self.line_recompute: bool = False
@@ -638,17 +639,19 @@ class MatRIS(nn.Module):
         pred = {}
         bg = process_graphs(graphs, compute_stress="s" in task)
         bg["line_recompute"] = bool(self.line_recompute)
-        ckpt = self.block_checkpoint
-        if ckpt is None:
-            ckpt = fused.checkpoint_needed(bg["n_angles"], bg["n_directed"], len(self.interaction_block),
-                                           bg["atomic_numbers"].device)
+        n_blocks = len(self.interaction_block)
+        if self.block_checkpoint is None:
+            n_ckpt = fused.blocks_to_checkpoint(bg["n_angles"], bg["n_directed"], n_blocks,
+                                                bg["atomic_numbers"].device)
+        else:
+            n_ckpt = n_blocks if self.block_checkpoint else 0
         node = self.atom_embedding(bg["atomic_numbers"].long() - 1)
         edge, smooth = self.edge_embedding(graphs=bg)
         tb = None
         if bg["n_angles"] != 0:
             tb = self.three_body_embedding(graphs=bg)
-        for layer in self.interaction_block:
-            if ckpt:  # keep only the block inputs; the block's forward reruns in the backward
+        for i, layer in enumerate(self.interaction_block):
+            if i < n_ckpt:  # keep only the block inputs; the block's forward reruns in the backward
                 node, edge, tb = torch.utils.checkpoint.checkpoint(layer, bg, node, edge, tb, smooth,
                                                                    use_reentrant=False, context_fn=_ckpt_contexts)
             else:
