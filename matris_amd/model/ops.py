@@ -482,11 +482,13 @@ class discard_saves:
         _DISCARD["on"] = self.old
 
 
-# Gather after GEMM: in a GatedMLP of at least 2^17 rows, a gathered source whose table
+# Gather after GEMM: in a GatedMLP of at least 2^16 rows, a gathered source whose table
 # has at most a quarter as many rows is multiplied by its block of W1 once per table row
-# (matris_gmlp_project) and its products are gathered instead of its features.  Smaller
-# layers lose: the saved layer-1 work is below the cost of the extra launch.
-_GTG = {"on": True, "min_rows": 1 << 17, "ratio": 4}
+# (matris_gmlp_project) and its products are gathered instead of its features.  Measured
+# at C3 (one box, whole step): the angle rows' bond and atom tables gain 0.8 ms, the
+# edge rows' atom tables ~0.05 ms; projecting the edge rows' bond table (half as many
+# rows as the layer) loses 0.15 ms, and smaller layers lose to the extra launch.
+_GTG = {"on": True, "min_rows": 1 << 16, "ratio": 4}
 
 
 class gather_after_gemm:
