@@ -83,7 +83,8 @@ def test_seg_sum_matches_index_add(R, S, scale, acc):
     assert _rel(out, ref) < 2e-6
 
 
-@pytest.mark.parametrize("R,S", [(37, 5), (5000, 800), (20000, 3), (3000, 100), (0, 4), (67396, 33698), (61, 59)])
+@pytest.mark.parametrize("R,S", [(37, 5), (5000, 800), (20000, 3), (3000, 100), (0, 4), (67396, 33698), (61, 59),
+                                 (6400, 90)])
 @pytest.mark.parametrize("acc", [False, True])
 def test_seg_sum_two_groupings_one_pass(R, S, acc):
     """matris_seg_sum2: two groupings of different row sets into one output (the target-
