@@ -34,6 +34,7 @@ from torch import Tensor, nn
 from ..config import EV_A3_TO_GPA
 from ..graph.converter import GraphConverter
 from . import fused, ops
+from .atomref import AtomRef
 from .batch import process_graphs
 
 
@@ -586,9 +587,10 @@ class MatRIS(nn.Module):
         # line_recompute: the two line-graph layers alone keep only their inputs.
         self.block_checkpoint: bool | None = None
         self.line_recompute: bool = False
-        if reference_energy is not None:
-            raise NotImplementedError("AtomRef reference energies are not on the MI355X path yet")
-        self.reference_energy = None
+        # created before the other modules, as in the reference (model.py:104-109): its Linear
+        # consumes random numbers, so the seed-0 weights of the rest match with it too
+        self.reference_energy = (AtomRef(reference_energy=reference_energy, is_intensive=is_intensive)
+                                 if reference_energy is not None else None)
         self.graph_converter = GraphConverter(atom_graph_cutoff=pairwise_cutoff, line_graph_cutoff=three_body_cutoff)
         self.atom_embedding = AtomTypeEmbedding(atom_feat_dim=node_feat_dim)
         self.edge_embedding = EdgeBasisEmbedding(pairwise_cutoff, three_body_cutoff, num_radial, edge_feat_dim,
@@ -668,7 +670,10 @@ class MatRIS(nn.Module):
             apg = torch.tensor(bg["atoms_per_graph"], dtype=torch.int32, device=total.device)
         pred["e"] = total / apg if self.is_intensive else total
         pred["atoms_per_graph"] = apg
-        pred["ref_energy"] = 0
+        # model.py:245-249: the composition energy of AtomRef (no position dependence)
+        ref = 0 if self.reference_energy is None else self.reference_energy(graphs)
+        pred["e"] = pred["e"] + ref
+        pred["ref_energy"] = ref
         return pred
 
     def get_params(self) -> int:
