@@ -58,6 +58,28 @@ int matris_radius_graph_fill(int64_t n, const double *lattice_host, double cutof
                              const int *search_host, const int64_t *row_ptr, int32_t *center, int32_t *neighbor,
                              int32_t *image, double *dist, void *workspace, size_t workspace_bytes, void *stream);
 
+/* G1 by Verlet-skin reuse (no counterpart in the reference, whose MD driver rebuilds the
+ * graph every step, matris/applications/base.py:96-97; it replaces that per-step
+ * get_neighbor_list call when the atoms moved less than skin / 2).  The candidates are a
+ * matris_radius_graph_count/fill result at cutoff + skin (cand_* [n_cand], rows by center,
+ * cand_row_ptr [n+1]); dk [n,3] int32 is each atom's integer frame jump since that build
+ * (floor of its fractional coordinates now minus then, i.e. the wrap).  Edges are
+ * re-decided with the builder's fp64 expression on the current frac and compacted stably,
+ * so the output equals matris_radius_graph_count/fill at cutoff on the same frac, edge for
+ * edge, whenever every atom moved less than skin / 2 (the caller checks that).  Two phases,
+ * as the builder: count (row_count, row_ptr; row_ptr[n] = E) then fill, with the same
+ * workspace of matris_skin_filter_workspace_bytes(n_cand). */
+size_t matris_skin_filter_workspace_bytes(int64_t n_cand);
+int matris_skin_filter_count(int64_t n, int64_t n_cand, const double *frac, const double *lattice_host, double cutoff,
+                             double tol, const int32_t *cand_center, const int32_t *cand_neighbor,
+                             const int32_t *cand_image, const int64_t *cand_row_ptr, const int32_t *dk,
+                             int32_t *row_count, int64_t *row_ptr, void *workspace, size_t workspace_bytes,
+                             void *stream);
+int matris_skin_filter_fill(int64_t n, int64_t n_cand, const double *frac, const double *lattice_host, double cutoff,
+                            double tol, const int32_t *cand_center, const int32_t *cand_neighbor,
+                            const int32_t *cand_image, const int32_t *dk, int32_t *center, int32_t *neighbor,
+                            int32_t *image, double *dist, void *workspace, size_t workspace_bytes, void *stream);
+
 /* G3/G4: directed -> undirected pairing.  Replaces create_graph()
  * (matris/graph/fast_converter_libraries/create_graph.c:100-219) and the Python
  * Graph.add_edge / adjacency_list / undirected2directed (matris/graph/radiusgraph.py:

@@ -73,6 +73,9 @@ _SIGS = {
     "matris_radius_graph_workspace_bytes": (_SZ, [_I64, _P]),
     "matris_radius_graph_count": (_I, [_I64, _P, _P, _D, _D, _P, _P, _P, _P, _P, _SZ, _P]),
     "matris_radius_graph_fill": (_I, [_I64, _P, _D, _D, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "matris_skin_filter_workspace_bytes": (_SZ, [_I64]),
+    "matris_skin_filter_count": (_I, [_I64, _I64, _P, _P, _D, _D, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "matris_skin_filter_fill": (_I, [_I64, _I64, _P, _P, _D, _D, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "matris_pair_edges_workspace_bytes": (_SZ, [_I64]),
     "matris_pair_edges": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "matris_line_graph_workspace_bytes": (_SZ, [_I64, _I64]),

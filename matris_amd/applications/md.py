@@ -70,7 +70,7 @@ class MolecularDynamics:
                  taut: float | None = None, taup: float | None = None, bulk_modulus: float | None = None,
                  trajectory=None, logfile: str | None = None, loginterval: int = 1,
                  crystal_feas_logfile: str | None = None, append_trajectory: bool = False, task: str = "efs",
-                 device: str | None = None, seed: int | None = None):
+                 device: str | None = None, seed: int | None = None, skin: float = 0.0):
         from ..graph.converter import _structure_arrays
         from ..model.model import MatRIS
         self.ensemble, self.thermostat = ensemble.lower(), thermostat
@@ -109,6 +109,13 @@ class MolecularDynamics:
         self.timings = {"graph": 0.0, "model": 0.0}
         self.results = None
         self._forces = None
+        # skin > 0: Verlet-skin reuse of the neighbour list (graphs identical to a rebuild
+        # every step, which is what the reference does and what skin = 0 keeps)
+        self.skin = float(skin)
+        self._neighbors = None
+        if self.skin > 0:
+            from ..graph.converter import SkinNeighborList
+            self._neighbors = SkinNeighborList(self.lattice, self.model.graph_converter.atom_graph_cutoff, self.skin)
 
     # --------------------------------------------------------------------------------
     def maxwell_boltzmann(self, temperature: float, seed: int | None = None) -> None:
@@ -135,8 +142,10 @@ class MolecularDynamics:
     def _evaluate(self):
         """Rebuild the graph on the GPU from the current positions and evaluate the model."""
         t0 = time.perf_counter()
-        frac = (self.pos @ self._inv_lat_t).remainder(1.0)  # wrap: the graph is periodic
-        graph = self.model.graph_converter.from_arrays(None, self.lattice, self.z, frac_device=frac.contiguous())
+        x = self.pos @ self._inv_lat_t
+        frac = x.remainder(1.0).contiguous()  # wrap: the graph is periodic
+        nbrs = self._neighbors.update(frac, x, self.pos) if self._neighbors is not None else None
+        graph = self.model.graph_converter.from_arrays(None, self.lattice, self.z, frac_device=frac, neighbors=nbrs)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         pred = self.model([graph], task=self.task)

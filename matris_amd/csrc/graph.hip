@@ -475,6 +475,135 @@ extern "C" int matris_radius_graph_fill(int64_t n, const double *lattice_host, d
 }
 
 // ------------------------------------------------------------------------------------
+// G1 from a Verlet-skin candidate list.  The candidates are a radius graph built at
+// cutoff + skin (canonical order, rows by center); dk[n,3] is each atom's integer frame
+// jump since then (the wrap of its fractional coordinates).  The candidate (i, j, n) is
+// the pair (i, j, n + dk_j - dk_i) in the current frame: the shift is one vector per
+// (i, j) group, so the group's image order is kept.  The decision is the builder's own
+// (frac_to_cart_d, pair_dist_d, tol < d <= cutoff), and a stable compaction keeps the
+// canonical order: when every atom moved less than skin / 2 the result is the radius
+// graph a fresh build at cutoff returns, edge for edge.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ bool skin_accept(int64_t e, const double *__restrict__ frac, const double *L,
+                                            const int32_t *__restrict__ cc, const int32_t *__restrict__ cn,
+                                            const int32_t *__restrict__ ci, const int32_t *__restrict__ dk,
+                                            double cutoff, double tol, int *img, double *dist) {
+    const int i = cc[e], j = cn[e];
+    double fi[3] = {frac[3 * i], frac[3 * i + 1], frac[3 * i + 2]};
+    double fj[3] = {frac[3 * j], frac[3 * j + 1], frac[3 * j + 2]};
+    double ri[3], rj[3];
+    frac_to_cart_d(fi, L, ri);
+    frac_to_cart_d(fj, L, rj);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) img[k] = ci[3 * e + k] + dk[3 * j + k] - dk[3 * i + k];
+    const double d = pair_dist_d(ri, rj, L, img[0], img[1], img[2]);
+    *dist = d;
+    return d <= cutoff && d > tol;
+}
+
+__global__ void skin_flag_kernel(int64_t n_cand, const double *__restrict__ frac, RGPlan plan,
+                                 const int32_t *__restrict__ cc, const int32_t *__restrict__ cn,
+                                 const int32_t *__restrict__ ci, const int32_t *__restrict__ dk, double cutoff,
+                                 double tol, int32_t *__restrict__ flag) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_cand) return;
+    int img[3];
+    double d;
+    flag[e] = skin_accept(e, frac, plan.L, cc, cn, ci, dk, cutoff, tol, img, &d) ? 1 : 0;
+}
+
+// row_ptr[i] = pos[cand_row_ptr[i]] (i = 0..n); row_count[i] = its difference
+__global__ void skin_rows_kernel(int64_t n, const int64_t *__restrict__ cand_row_ptr,
+                                 const int64_t *__restrict__ pos, int64_t *__restrict__ row_ptr,
+                                 int32_t *__restrict__ row_count) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > n) return;
+    row_ptr[i] = pos[cand_row_ptr[i]];
+    if (i < n) row_count[i] = (int32_t)(pos[cand_row_ptr[i + 1]] - pos[cand_row_ptr[i]]);
+}
+
+__global__ void skin_fill_kernel(int64_t n_cand, const double *__restrict__ frac, RGPlan plan,
+                                 const int32_t *__restrict__ cc, const int32_t *__restrict__ cn,
+                                 const int32_t *__restrict__ ci, const int32_t *__restrict__ dk, double cutoff,
+                                 double tol, const int64_t *__restrict__ pos, int32_t *__restrict__ center,
+                                 int32_t *__restrict__ neighbor, int32_t *__restrict__ image,
+                                 double *__restrict__ dist) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_cand) return;
+    const int64_t o = pos[e];
+    if (pos[e + 1] == o) return;  // rejected by the count pass (same decision)
+    int img[3];
+    double d;
+    skin_accept(e, frac, plan.L, cc, cn, ci, dk, cutoff, tol, img, &d);
+    center[o] = cc[e];
+    neighbor[o] = cn[e];
+    image[3 * o] = img[0];
+    image[3 * o + 1] = img[1];
+    image[3 * o + 2] = img[2];
+    dist[o] = d;
+}
+
+extern "C" size_t matris_skin_filter_workspace_bytes(int64_t n_cand) {
+    if (n_cand < 0) return 0;
+    return align256(sizeof(int32_t) * (size_t)(n_cand + 1)) + align256(sizeof(int64_t) * (size_t)(n_cand + 1)) +
+           scan_workspace_bytes(n_cand) + 256;
+}
+
+static bool skin_args_ok(int64_t n, int64_t n_cand, const double *frac, const double *lattice_host,
+                         const int32_t *cc, const int32_t *cn, const int32_t *ci, const int32_t *dk, void *ws,
+                         size_t ws_bytes) {
+    return n > 0 && n_cand >= 0 && frac && lattice_host && dk && ws &&
+           (n_cand == 0 || (cc && cn && ci)) && ws_bytes >= matris_skin_filter_workspace_bytes(n_cand);
+}
+
+extern "C" int matris_skin_filter_count(int64_t n, int64_t n_cand, const double *frac, const double *lattice_host,
+                                        double cutoff, double tol, const int32_t *cand_center,
+                                        const int32_t *cand_neighbor, const int32_t *cand_image,
+                                        const int64_t *cand_row_ptr, const int32_t *dk, int32_t *row_count,
+                                        int64_t *row_ptr, void *workspace, size_t workspace_bytes, void *stream) {
+    if (!skin_args_ok(n, n_cand, frac, lattice_host, cand_center, cand_neighbor, cand_image, dk, workspace,
+                      workspace_bytes) ||
+        !cand_row_ptr || !row_count || !row_ptr || !(cutoff > 0))
+        return MATRIS_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    RGPlan plan;
+    memcpy(plan.L, lattice_host, sizeof(plan.L));
+    char *p = (char *)workspace;
+    int32_t *flag = (int32_t *)p;
+    p += align256(sizeof(int32_t) * (size_t)(n_cand + 1));
+    int64_t *pos = (int64_t *)p;
+    p += align256(sizeof(int64_t) * (size_t)(n_cand + 1));
+    if (n_cand > 0)
+        skin_flag_kernel<<<matris_blocks(n_cand, 256), 256, 0, st>>>(n_cand, frac, plan, cand_center, cand_neighbor,
+                                                                      cand_image, dk, cutoff, tol, flag);
+    int rc = scan_exclusive<int32_t, int64_t>(flag, n_cand, pos, p, st);
+    if (rc) return rc;
+    skin_rows_kernel<<<matris_blocks(n + 1, 256), 256, 0, st>>>(n, cand_row_ptr, pos, row_ptr, row_count);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_skin_filter_fill(int64_t n, int64_t n_cand, const double *frac, const double *lattice_host,
+                                       double cutoff, double tol, const int32_t *cand_center,
+                                       const int32_t *cand_neighbor, const int32_t *cand_image, const int32_t *dk,
+                                       int32_t *center, int32_t *neighbor, int32_t *image, double *dist,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+    if (!skin_args_ok(n, n_cand, frac, lattice_host, cand_center, cand_neighbor, cand_image, dk, workspace,
+                      workspace_bytes) ||
+        !center || !neighbor || !image || !dist || !(cutoff > 0))
+        return MATRIS_E_ARG;
+    if (n_cand == 0) return 0;
+    RGPlan plan;
+    memcpy(plan.L, lattice_host, sizeof(plan.L));
+    const int64_t *pos = (const int64_t *)((char *)workspace + align256(sizeof(int32_t) * (size_t)(n_cand + 1)));
+    skin_fill_kernel<<<matris_blocks(n_cand, 256), 256, 0, (hipStream_t)stream>>>(
+        n_cand, frac, plan, cand_center, cand_neighbor, cand_image, dk, cutoff, tol, pos, center, neighbor, image,
+        dist);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
 // G3/G4: pairing (canonical order makes the reverse edge a binary search in its row)
 // ------------------------------------------------------------------------------------
 __device__ __forceinline__ int cmp_key(int ja, const int32_t *ia, int jb, int n0, int n1, int n2) {

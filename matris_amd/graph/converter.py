@@ -87,6 +87,69 @@ def radius_graph_device(frac: torch.Tensor, lattice: np.ndarray, cutoff: float, 
     return center[:E], neighbor[:E], image[:E], dist[:E], row_ptr, row_count
 
 
+class SkinNeighborList:
+    """G1 with Verlet-skin reuse for MD (no counterpart in the reference, which rebuilds the
+    neighbour list every step, base.py:96-97).  Candidates come from one radius graph at
+    cutoff + skin; each later call re-decides them on the current coordinates on the GPU
+    (matris_skin_filter_count/fill) until some atom has moved skin / 2 or more since the
+    candidate build, which triggers a fresh candidate build.  Every call returns exactly
+    what radius_graph_device(frac, lattice, cutoff) returns for the same frac.
+
+    update(frac, x, pos): frac = the wrapped fractional coordinates the graph is built
+    from (fp64 [n,3] device), x = the same coordinates unwrapped (frac = x - integer),
+    pos = unwrapped Cartesian positions (fp64 [n,3]), used for the displacement test.
+    The lattice is fixed for the list's lifetime."""
+
+    def __init__(self, lattice: np.ndarray, cutoff: float, skin: float, tol: float = 1e-8):
+        if not skin > 0:
+            raise ValueError(f"skin must be positive, got {skin}")
+        self.lattice = np.ascontiguousarray(lattice, dtype=np.float64)
+        self.cutoff, self.skin, self.tol = float(cutoff), float(skin), float(tol)
+        self.n_builds = 0
+        self._cand = None
+
+    def _rebuild(self, frac, x, pos):
+        c, nb, im, _, rp, _ = radius_graph_device(frac, self.lattice, self.cutoff + self.skin, self.tol)
+        self._cand = (c.contiguous(), nb.contiguous(), im.contiguous(), rp)
+        self._frame0 = (x - frac).clone()  # the integer wrap of every atom at the candidate build
+        self._pos0 = pos.clone()
+        self.n_builds += 1
+
+    def update(self, frac: torch.Tensor, x: torch.Tensor, pos: torch.Tensor):
+        """(center, neighbor, image int32 [E,3], dist fp64, row_ptr int64 [n+1], row_count int32)."""
+        frac = frac.contiguous()
+        n = frac.shape[0]
+        if self._cand is None or self._cand[3].shape[0] != n + 1:
+            self._rebuild(frac, x, pos)
+        else:
+            # strict margin below skin / 2: the rounding of the candidate decisions cannot matter
+            moved = float(torch.linalg.vector_norm(pos - self._pos0, dim=1).max().item())
+            if moved >= 0.5 * self.skin * (1.0 - 1e-9):
+                self._rebuild(frac, x, pos)
+        cc, cn, ci, crp = self._cand
+        dk = torch.round((x - frac) - self._frame0).to(torch.int32).contiguous()
+        lib = _lib.load()
+        dev = frac.device
+        n_cand = cc.shape[0]
+        ws_bytes = lib.matris_skin_filter_workspace_bytes(n_cand)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        row_count = torch.empty(n, dtype=torch.int32, device=dev)
+        row_ptr = torch.empty(n + 1, dtype=torch.int64, device=dev)
+        latp = self.lattice.ctypes.data_as(ctypes.c_void_p)
+        _lib.check(lib.matris_skin_filter_count(n, n_cand, _p(frac), latp, self.cutoff, self.tol, _p(cc), _p(cn),
+                                                _p(ci), _p(crp), _p(dk), _p(row_count), _p(row_ptr), _p(ws),
+                                                ws_bytes, _stream()), "matris_skin_filter_count")
+        E = int(row_ptr[n].item())
+        center = torch.empty(max(E, 1), dtype=torch.int32, device=dev)
+        neighbor = torch.empty(max(E, 1), dtype=torch.int32, device=dev)
+        image = torch.empty(max(E, 1), 3, dtype=torch.int32, device=dev)
+        dist = torch.empty(max(E, 1), dtype=torch.float64, device=dev)
+        _lib.check(lib.matris_skin_filter_fill(n, n_cand, _p(frac), latp, self.cutoff, self.tol, _p(cc), _p(cn),
+                                               _p(ci), _p(dk), _p(center), _p(neighbor), _p(image), _p(dist),
+                                               _p(ws), ws_bytes, _stream()), "matris_skin_filter_fill")
+        return center[:E], neighbor[:E], image[:E], dist[:E], row_ptr, row_count
+
+
 def pair_edges_device(n: int, center, neighbor, image, row_ptr):
     """G3/G4 on the device: (rev, d2u, u2d, u_second)."""
     lib = _lib.load()
@@ -154,9 +217,11 @@ class GraphConverter(nn.Module):
         return self.from_arrays(frac, lat, z, graph_id=graph_id, mp_id=mp_id, composition=formula)
 
     def from_arrays(self, frac, lattice, z, graph_id=None, mp_id=None, composition=None,
-                    frac_device: torch.Tensor | None = None) -> RadiusGraph:
+                    frac_device: torch.Tensor | None = None, neighbors=None) -> RadiusGraph:
         """Build from fractional coordinates (fp64), lattice rows (fp64) and atomic numbers.
-        frac_device: an fp64 device copy of frac, when the caller already holds one."""
+        frac_device: an fp64 device copy of frac, when the caller already holds one.
+        neighbors: the atom-graph edges when the caller already holds them for this frac and
+        the atom-graph cutoff (SkinNeighborList.update's result)."""
         dev = self._device()
         n = len(z)
         lat = np.asarray(lattice, dtype=np.float64)
@@ -164,7 +229,8 @@ class GraphConverter(nn.Module):
         # Fortran-ordered array, a column slice) contiguous first
         f64 = (frac_device if frac_device is not None else
                torch.as_tensor(np.ascontiguousarray(frac, dtype=np.float64), device=dev)).contiguous()
-        center, neighbor, image, dist, row_ptr, row_count = radius_graph_device(f64, lat, self.atom_graph_cutoff)
+        center, neighbor, image, dist, row_ptr, row_count = (
+            neighbors if neighbors is not None else radius_graph_device(f64, lat, self.atom_graph_cutoff))
         # converter.py:108-113: isolated atoms stop the calculation
         n_isolated = int((row_count == 0).sum().item())
         if n_isolated:

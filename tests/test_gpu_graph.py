@@ -125,3 +125,63 @@ def test_strided_fractional_input_gives_the_same_graph():
     for g in (gc.from_arrays(f_order, cr.lattice, cr.z), gc.from_arrays(None, cr.lattice, cr.z, frac_device=wide[:, ::2])):
         for name in ("atom_graph", "neighbor_image", "directed2undirected", "undirected2directed", "line_graph"):
             assert torch.equal(getattr(g, name), getattr(ref, name)), name
+
+
+@pytest.mark.parametrize("case", ["fcc108", "triclinic40"])
+def test_skin_neighbor_list_equals_fresh_build(case):
+    """Verlet-skin reuse (SkinNeighborList): along a drifting, jittered trajectory whose atoms
+    cross the cell faces (their wrapped fractional coordinates jump by 1), every update returns
+    the fresh cutoff build's arrays bit for bit; the candidate list is rebuilt only once an
+    atom has moved skin / 2, and reused (with wrap jumps) in between."""
+    from matris_amd.graph.converter import SkinNeighborList, radius_graph_device
+    rng = np.random.default_rng(7)
+    cr = (W.fcc_supercell(3.61, 3, sigma=0.05, seed=3) if case == "fcc108"
+          else W.random_cell(np.random.default_rng(2), 40))
+    lat = torch.tensor(cr.lattice, device="cuda")
+    inv = torch.linalg.inv(lat)
+    pos = torch.tensor(cr.frac @ cr.lattice, device="cuda")
+    n = pos.shape[0]
+    nl = SkinNeighborList(cr.lattice, 6.0, skin=1.0)
+    drift = np.array([0.07, 0.05, 0.03])
+    k_build = None
+    reused_wraps = 0
+    for step in range(14):
+        x = pos @ inv
+        frac = x.remainder(1.0).contiguous()
+        before = nl.n_builds
+        got = nl.update(frac, x, pos)
+        ref = radius_graph_device(frac, cr.lattice, 6.0)
+        for name, a, b in zip(("center", "neighbor", "image", "dist", "row_ptr", "row_count"), got, ref):
+            assert a.dtype == b.dtype and torch.equal(a, b), (step, name)
+        k = torch.round(x - frac)
+        if nl.n_builds != before:
+            k_build = k
+        else:
+            reused_wraps += int((k != k_build).any().item())
+        jitter = rng.normal(size=(n, 3))
+        jitter *= (0.1 * rng.random((n, 1))) / np.linalg.norm(jitter, axis=1, keepdims=True)
+        pos = pos + torch.tensor(drift + jitter, device="cuda")
+    assert 2 <= nl.n_builds <= 10, nl.n_builds
+    assert reused_wraps >= 1
+
+
+def test_md_with_skin_matches_rebuild_every_step():
+    """MolecularDynamics(skin=1.0) runs the same trajectory as the per-step rebuild of the
+    reference (skin=0): positions and energies agree bit for bit over 12 NVE steps."""
+    from matris_amd.applications import MolecularDynamics
+    from matris_amd.config import MATRIS_10M
+    from matris_amd.model import MatRIS
+    torch.manual_seed(0)
+    model = MatRIS(**{**MATRIS_10M, "num_layers": 2}).to("cuda").eval()
+    cr = W.fcc_supercell(3.61, 2, sigma=0.05, seed=5)
+    runs = []
+    for skin in (0.0, 1.0):
+        md = MolecularDynamics((cr.frac, cr.lattice, cr.z), model=model, ensemble="nve", starting_temperature=2000,
+                               timestep=2.0, task="ef", device="cuda", seed=3, skin=skin)
+        es = []
+        for _ in range(12):
+            md.run(1)
+            es.append(float(md.results["e"][0]))
+        runs.append((md.get_positions(), es, md))
+    assert np.array_equal(runs[0][0], runs[1][0]) and runs[0][1] == runs[1][1]
+    assert runs[1][2]._neighbors.n_builds < 13

@@ -115,6 +115,15 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_seg_sum_mul(4, 10, v16, 64, 0, v16, None, v16, v16, 1.0, 0, v16, None) == -1001
     assert lib.matris_gather_mul(10, v16, None, v16, None, 0, None, None) == -1001
     assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
+    # neighbour-list reuse: no atoms; a workspace below its size; a non-positive cutoff
+    big = 1 << 20
+    assert lib.matris_skin_filter_count(0, 0, v16, v16, 6.0, 1e-8, None, None, None, v16, v16, v16, v16, v16, big,
+                                        None) == -1001
+    assert lib.matris_skin_filter_count(4, 10, v16, v16, 6.0, 1e-8, v16, v16, v16, v16, v16, v16, v16, v16, 8,
+                                        None) == -1001
+    assert lib.matris_skin_filter_fill(4, 10, v16, v16, 0.0, 1e-8, v16, v16, v16, v16, v16, v16, v16, v16, v16, big,
+                                       None) == -1001
+    assert lib.matris_skin_filter_workspace_bytes(1000) > lib.matris_skin_filter_workspace_bytes(10) > 0
     # empty work is a no-op success
     assert lib.matris_seg_sum(None, 128, 0, ctypes.c_void_p(8), None, 0, 1.0, 0, ctypes.c_void_p(8), None) == 0
     assert lib.matris_ffn_fwd(0, v16, v16, v16, v16, None, None, None, 3, None) == 0
