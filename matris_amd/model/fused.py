@@ -35,7 +35,7 @@ SAVED_BYTES_PER_EDGE_BLOCK = 4 * 16 * 128
 def blocks_to_checkpoint(n_angles: int, n_edges: int, n_blocks: int, device=None,
                          total_bytes: int | None = None) -> int:
     """How many leading interaction blocks to checkpoint (keep their inputs, rerun their
-    forward in the backward): none when the whole model's saved activations fit in 45% of
+    forward in the backward): none when the whole model's saved activations fit in 55% of
     the device's memory (total_bytes, default: the device's capacity), otherwise all but
     as many trailing blocks as fit there.  The trailing blocks' backward runs first and
     frees their activations before any checkpointed block is recomputed, so keeping k of
@@ -44,7 +44,7 @@ def blocks_to_checkpoint(n_angles: int, n_edges: int, n_blocks: int, device=None
     (interaction_block.py:15, :400-413)."""
     total = total_bytes if total_bytes is not None else torch.cuda.get_device_properties(device).total_memory
     per_block = n_angles * SAVED_BYTES_PER_ANGLE_BLOCK + n_edges * SAVED_BYTES_PER_EDGE_BLOCK
-    budget = 0.45 * total
+    budget = 0.55 * total
     if n_blocks * per_block <= budget:
         return 0
     return n_blocks - min(n_blocks, int(budget // per_block))

@@ -25,8 +25,8 @@ def test_block_checkpoint_policy():
     assert not fused.checkpoint_needed(264_384, 67_396, 10, total_bytes=hbm)
     assert fused.checkpoint_needed(9_027_734, 1_892_918, 10, total_bytes=hbm)
     assert not fused.checkpoint_needed(0, 100, 10, total_bytes=hbm)
-    # C5: one block's saved activations (~80 GB by the upper-bound estimate) fit the 45%
-    # budget, so the last block keeps them and the first nine are checkpointed
-    assert fused.blocks_to_checkpoint(9_027_734, 1_892_918, 10, total_bytes=hbm) == 9
+    # C5: two blocks' saved activations (~80 GB each by the upper-bound estimate) fit the
+    # 55% budget, so the last two blocks keep them and the first eight are checkpointed
+    assert fused.blocks_to_checkpoint(9_027_734, 1_892_918, 10, total_bytes=hbm) == 8
     assert fused.blocks_to_checkpoint(264_384, 67_396, 10, total_bytes=hbm) == 0
     assert fused.blocks_to_checkpoint(10 ** 9, 0, 10, total_bytes=hbm) == 10
