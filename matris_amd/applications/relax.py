@@ -7,8 +7,9 @@ relax_cell, with MatRISCalculator attached and the trajectory observer called ev
 loginterval steps.  ASE is not part of this image; without it, relax() runs the FIRE
 optimizer natively on the atomic positions (relax_cell=False) -- the published method
 (Bitzek, Koskinen, Gaehler, Moseler & Gumbsch, Phys. Rev. Lett. 97, 170201 (2006)) with
-ASE's default FIRE parameters and its cap on the step length -- and raises for cell
-relaxation or another optimizer.
+ASE's default FIRE parameters and its cap on the step length -- over the atomic
+positions, or with relax_cell over positions and cell together (CellFilterDOF, the
+deformation-gradient filter), and raises for another optimizer.
 """
 from __future__ import annotations
 
@@ -98,6 +99,48 @@ def fire_relax(atoms, fmax: float = 0.05, steps: int = 500, observer=None, login
     return False
 
 
+def _stress33(s) -> np.ndarray:
+    s = np.asarray(s, dtype=np.float64)
+    if s.shape == (6,):  # Voigt order xx, yy, zz, yz, xz, xy
+        xx, yy, zz, yz, xz, xy = s
+        return np.array([[xx, xy, xz], [xy, yy, yz], [xz, yz, zz]])
+    return s.reshape(3, 3)
+
+
+class CellFilterDOF:
+    """Positions and cell as one set of generalised coordinates, restated from the
+    deformation-gradient cell filter that ASE's UnitCellFilter implements (Tadmor, Smith,
+    Bernstein & Kaxiras, Phys. Rev. B 59, 235 (1999)): with F the deformation gradient of
+    the current cell against the starting one (cell = cell0 F^T, r = r0 F^T), the
+    coordinates are (r0 [n,3], c F [3,3]) with c = n_atoms, and their forces are
+    (f F, W F^-T / c) with the virial W = -V (stress + p I).  A converged state has zero
+    atomic forces and zero stress (or the hydrostatic pressure p, eV/A^3)."""
+
+    def __init__(self, atoms, scalar_pressure: float = 0.0):
+        self.atoms = atoms
+        self.cell0 = np.asarray(atoms.get_cell(), dtype=np.float64).reshape(3, 3).copy()
+        self.c = float(len(atoms))
+        self.p = float(scalar_pressure)
+        self.F = np.eye(3)
+
+    def get_positions(self) -> np.ndarray:
+        r0 = np.linalg.solve(self.F, np.asarray(self.atoms.get_positions(), np.float64).T).T
+        return np.vstack([r0, self.c * self.F])
+
+    def set_positions(self, x) -> None:
+        x = np.asarray(x, dtype=np.float64)
+        n = len(self.atoms)
+        self.F = x[n:] / self.c
+        self.atoms.set_cell(self.cell0 @ self.F.T, scale_atoms=False)
+        self.atoms.set_positions(x[:n] @ self.F.T)
+
+    def get_forces(self) -> np.ndarray:
+        f = np.asarray(self.atoms.get_forces(), dtype=np.float64) @ self.F
+        vol = abs(np.linalg.det(np.asarray(self.atoms.get_cell(), np.float64).reshape(3, 3)))
+        virial = -vol * (_stress33(self.atoms.get_stress()) + self.p * np.eye(3))
+        return np.vstack([f, np.linalg.solve(self.F, virial.T).T / self.c])
+
+
 class StructOptimizer:
     """Structure optimiser with the reference's constructor (relax.py:23-52)."""
 
@@ -142,11 +185,11 @@ class StructOptimizer:
                 opt.run(fmax=fmax, steps=steps)
                 obs()
         else:
-            if relax_cell or self.optimizer != "FIRE":
-                raise NotImplementedError("without ASE this build relaxes positions with FIRE only "
-                                          "(relax_cell=False, optimizer='FIRE')")
+            if self.optimizer != "FIRE":
+                raise NotImplementedError("without ASE this build relaxes with FIRE only (optimizer='FIRE')")
             with contextlib.redirect_stdout(stream):
-                fire_relax(atoms, fmax=fmax, steps=steps, observer=obs, loginterval=loginterval, **kwargs)
+                target = CellFilterDOF(atoms, kwargs.pop("scalar_pressure", 0.0)) if relax_cell else atoms
+                fire_relax(target, fmax=fmax, steps=steps, observer=obs, loginterval=loginterval, **kwargs)
                 obs()
         if save_path is not None:
             obs.save(save_path)

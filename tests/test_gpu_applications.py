@@ -86,7 +86,25 @@ def test_fire_relaxation_lowers_energy(model):
     assert traj.energies[-1] < traj.energies[0]
     assert res["final_structure"] is atoms
     with pytest.raises(NotImplementedError):
-        opt.relax(atoms, steps=1, relax_cell=True, verbose=False)
+        StructOptimizer(model=model, task="efs", optimizer="BFGS").relax(atoms, steps=1, verbose=False)
+
+
+def test_cell_relaxation_without_ase(model):
+    """relax_cell=True (the reference's default) runs FIRE over positions and cell: the
+    energy falls, the cell changes, and both the atomic forces and the stress shrink."""
+    from matris_amd.applications import StructOptimizer
+    cr, atoms = _cu32(sigma=0.05, seed=9)
+    atoms.set_cell(atoms.get_cell() * 1.04, scale_atoms=True)
+    opt = StructOptimizer(model=model, task="efs")
+    atoms.calc = opt.calculator
+    s0 = np.abs(np.asarray(atoms.get_stress())).max()
+    cell0 = atoms.get_cell()
+    res = opt.relax(atoms, fmax=0.02, steps=150, relax_cell=True, verbose=False)
+    traj = res["trajectory"]
+    assert traj.energies[-1] < traj.energies[0]
+    assert not np.allclose(atoms.get_cell(), cell0)
+    s1 = np.abs(np.asarray(atoms.get_stress())).max()
+    assert s1 < 0.5 * s0, (s0, s1)
 
 
 def test_md_nve_conserves_energy_and_nvt_thermostat(model):
