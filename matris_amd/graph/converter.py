@@ -246,8 +246,8 @@ class GraphConverter(nn.Module):
         atom_graph = torch.stack([center, neighbor], dim=1)
         # the indices come from this builder's own kernels: valid by construction
         meta = dict(canonical=True, dist=dist, rev=rev, u_second=u_second, row_ptr=row_ptr, angle_ptr=angle_ptr,
-                    frac64=f64, indices_checked=True)
-        return RadiusGraph(
+                    frac64=f64)
+        g = RadiusGraph(
             graph_id=graph_id, mp_id=mp_id, composition=composition,
             atomic_number=torch.as_tensor(np.asarray(z), dtype=torch.int32, device=dev),
             atom_frac_coord=f64.to(datatype),
@@ -260,6 +260,8 @@ class GraphConverter(nn.Module):
             directed2undirected=d2u,
             undirected2directed=u2d,
             meta=meta)
+        g.meta["indices_checked"] = g.index_signature()
+        return g
 
     def as_dict(self) -> dict:
         return {"atom_graph_cutoff": self.atom_graph_cutoff, "line_graph_cutoff": self.line_graph_cutoff,

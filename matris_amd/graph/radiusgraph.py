@@ -42,6 +42,14 @@ class RadiusGraph:
 
     _FIELDS = ("atomic_number", "atom_frac_coord", "lattice", "neighbor_image", "atom_graph", "line_graph",
                "directed2undirected", "undirected2directed")
+    _INDEX_FIELDS = ("atomic_number", "atom_graph", "line_graph", "directed2undirected", "undirected2directed")
+
+    def index_signature(self) -> tuple:
+        """Identity and version of every index tensor (and the atom count).  Any in-place
+        edit bumps a tensor's version counter and assigning a new tensor changes its
+        identity, so a range check remembered under this signature is redone after either."""
+        return tuple((f, id(t), t.data_ptr(), t._version, tuple(t.shape))
+                     for f in self._INDEX_FIELDS for t in (getattr(self, f),))
 
     def to(self, device: str = "cpu") -> "RadiusGraph":
         """radiusgraph.py:97-113."""

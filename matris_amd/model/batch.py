@@ -32,6 +32,22 @@ class _ImageShift(torch.autograd.Function):
         return None, g_lat
 
 
+class _GraphBroadcast(torch.autograd.Function):
+    """x [G, ...] repeated lengths[g] times per graph (rows contiguous per graph), with the
+    backward summed per graph in a fixed order (a segmented reduction instead of the
+    atomic index_add_ of an indexing backward), so batched stresses are reproducible."""
+
+    @staticmethod
+    def forward(ctx, x, lengths, total):
+        ctx.save_for_backward(lengths)
+        return torch.repeat_interleave(x, lengths, dim=0, output_size=total)
+
+    @staticmethod
+    def backward(ctx, g):
+        (lengths,) = ctx.saved_tensors
+        return torch.segment_reduce(g, "sum", lengths=lengths, axis=0), None, None
+
+
 def _sorted(x: torch.Tensor) -> bool:
     return x.numel() < 2 or bool((x[1:] >= x[:-1]).all().item())
 
@@ -41,11 +57,14 @@ def validate_graph_indices(g) -> None:
     [E, 2] in [0, N), directed2undirected [E] in [0, U), undirected2directed [U] in [0, E)
     and the line graph's columns (center atom, bond, directed edge, bond, directed edge).
     The gather and segment kernels read rows through these indices, so they are checked
-    before any of them runs: one host read per graph, remembered in g.meta (graphs built
-    by GraphConverter are valid by construction and carry the mark already).  A graph's
-    index tensors must not be changed in place after its first evaluation."""
-    if g.meta.get("indices_checked", False):
+    before any of them runs: one host read per graph.  The result is remembered in g.meta
+    under the index tensors' identities and version counters (RadiusGraph.index_signature),
+    so an index tensor edited in place or replaced after a check is checked again.  Graphs
+    built by GraphConverter are valid by construction and carry the mark already."""
+    sig = g.index_signature()
+    if g.meta.get("indices_checked") == sig:
         return
+    g.meta.pop("indices_checked", None)
     N = int(g.atomic_number.shape[0])
     E = int(g.atom_graph.shape[0])
     U = int(g.undirected2directed.shape[0])
@@ -59,7 +78,7 @@ def validate_graph_indices(g) -> None:
     flags = [((x < 0) | (x >= n)).any() for x, n in checks if x.numel()]
     if flags and bool(torch.stack(flags).any()):
         raise ValueError("graph index outside its range (atom, bond, directed-edge or angle index)")
-    g.meta["indices_checked"] = True
+    g.meta["indices_checked"] = sig
 
 
 def process_graphs(graphs, compute_stress: bool = True) -> dict:
@@ -108,8 +127,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     if G == 1:
         atom_segment = torch.zeros(N, dtype=torch.long, device=device)
     else:
-        atom_segment = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_atoms, device=device),
-                                               output_size=N)
+        atoms_len = torch.tensor(n_atoms, device=device)
+        atom_segment = torch.repeat_interleave(torch.arange(G, device=device), atoms_len, output_size=N)
     lat3 = lattice.reshape(G, 3, 3)
     volumes = torch.einsum("ni,ni->n", lat3[:, 0], torch.linalg.cross(lat3[:, 1], lat3[:, 2]))[:, None, None]
 
@@ -122,7 +141,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         if G == 1:  # one graph: the per-atom strain is a broadcast, not a gather
             cart = cart + cart @ sym[0]
         else:
-            cart = cart + torch.bmm(cart.unsqueeze(1), sym[atom_segment]).squeeze(1)
+            cart = cart + torch.bmm(cart.unsqueeze(1), _GraphBroadcast.apply(sym, atoms_len, N)).squeeze(1)
         lat3 = lat3 + torch.matmul(lat3, sym)
         lattice = lat3.reshape(-1, 3)
 
@@ -130,9 +149,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     if G == 1:
         shift = _ImageShift.apply(image, lattice)
     else:
-        edge_graph = torch.repeat_interleave(torch.arange(G, device=device), torch.tensor(n_dir, device=device),
-                                             output_size=E)
-        shift = torch.bmm(image.unsqueeze(1), lat3[edge_graph]).squeeze(1)
+        lat_e = _GraphBroadcast.apply(lat3, torch.tensor(n_dir, device=device), E)
+        shift = torch.bmm(image.unsqueeze(1), lat_e).squeeze(1)
     # deferred builds: key-range errors surface in the status word that MatRIS.forward
     # reads once per evaluation (no stream sync per grouping)
     grp_tgt = Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True)

@@ -160,10 +160,16 @@ class GraphPooling(nn.Module):
         self.average = average
 
     def forward(self, node_feat, segment, n_graphs: int):
-        out = node_feat.new_zeros(n_graphs, node_feat.shape[1]).index_add(0, segment, node_feat)
+        """Per-graph sums in a fixed order (no float atomics, so the energies are bitwise
+        reproducible): one reduction for one graph, a segmented reduction over the atoms,
+        which are contiguous per graph, otherwise."""
+        if n_graphs == 1:
+            out = node_feat.sum(0, keepdim=True)
+        else:
+            cnt = torch.bincount(segment, minlength=n_graphs)
+            out = torch.segment_reduce(node_feat, "sum", lengths=cnt, axis=0)
         if self.average:
-            cnt = torch.bincount(segment, minlength=n_graphs).clamp_min(1)
-            out = out / cnt[:, None]
+            out = out / torch.bincount(segment, minlength=n_graphs).clamp_min(1)[:, None]
         return out
 
 
@@ -204,76 +210,25 @@ class BesselExpansion(nn.Module):
         self.envelope_func = PolynomialEnvelope(cutoff, envelope_exponent) if envelope_exponent is not None else None
 
     def forward(self, dist, return_smooth_factor=False):
-        if dist.is_cuda and self.envelope_func is not None and not return_smooth_factor:
-            return ops.bessel(dist, self.frequencies, self.envelope_func.cutoff, self.envelope_func.p)
-        dist = dist[:, None]
-        out = self.norm_const * torch.sin(self.frequencies * (dist * self.inv_cutoff)) / dist
-        if self.envelope_func is not None:
-            sf = self.envelope_func(dist)
-            out = sf * out
-            if return_smooth_factor:
-                return out, sf
-        return out
-
-
-_SBF_COEF = {
-    1: [[-1.02446483277785, -1.00834335996107, -1.00419641763893, -1.00252381898662],
-        [4.49340963363647, 7.7252516746521, 10.9041213989258, 14.0661935806274],
-        [0.22799275301076, 0.130525632358311, 0.092093290316619, 0.0712718627992818],
-        [4.49340963363647, 7.7252516746521, 10.9041213989258, 14.0661935806274]],
-    2: [[-1.04807944170731, -1.01861796359391, -1.01002272174988, -1.00628955560036],
-        [5.76345920562744, 9.09501171112061, 12.322940826416, 15.5146026611328],
-        [0.545547077361439, 0.335992298618515, 0.245888396928293, 0.194582402961821],
-        [5.76345920562744, 9.09501171112061, 12.322940826416, 15.5146026611328],
-        [0.0946561878721665, 0.0369424811413594, 0.0199537107571916, 0.0125418876146463],
-        [5.76345920562744, 9.09501171112061, 12.322940826416, 15.5146026611328]],
-    3: [[1.06942831392075, 1.0292173312802, 1.01650804843248, 1.01069656069999],
-        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477],
-        [0.918235852195231, 0.592803493701152, 0.445250264272671, 0.358326327374518],
-        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477],
-        [0.328507713452024, 0.142266673367543, 0.0812617757677838, 0.0529328657590962],
-        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477],
-        [0.0470107184508114, 0.0136570088173405, 0.0059323726279831, 0.00312775039221944],
-        [6.9879322052002, 10.4171180725098, 13.6980228424072, 16.9236221313477]],
-}
+        """B_n(r) env(r) on the device (matris_bessel_fwd / _bwd); there is no host path."""
+        if self.envelope_func is None or return_smooth_factor:
+            raise NotImplementedError("the MI355X path evaluates the enveloped Bessel basis only")
+        if not dist.is_cuda:
+            raise RuntimeError("matris_amd ops run on the ROCm device only (no CPU fallback)")
+        return ops.bessel(dist, self.frequencies, self.envelope_func.cutoff, self.envelope_func.p)
 
 
 class SphericalExpansion(nn.Module):
-    """basis_function.py:222-338 (radial spherical-Bessel table x Legendre Y_l)."""
+    """basis_function.py:222-338: the spherical-Bessel radial table times Legendre Y_l.
+    The basis itself is computed on the device (matris_sbf_fwd / _bwd, which hold the
+    root table); this module carries the reference's buffer so state_dict keys match."""
 
     def __init__(self, max_n=4, max_l=4, cutoff=6):
         super().__init__()
-        assert max_l <= 4 and max_n <= 4
+        if max_n != 4 or max_l != 4:
+            raise NotImplementedError("the MI355X path implements the 4 x 4 spherical basis (max_n = max_l = 4)")
         self.max_n, self.max_l, self.cutoff = max_n, max_l, cutoff
         self.register_buffer("factor", torch.sqrt(torch.tensor(2.0 / (cutoff ** 3))))
-        coef = torch.zeros(4, 9, 4)
-        coef[0, 0, :] = torch.tensor([3.14159274101257, 6.28318548202515, 9.42477798461914, 12.5663709640503])
-        coef[1, :4, :] = torch.tensor(_SBF_COEF[1])
-        coef[2, :6, :] = torch.tensor(_SBF_COEF[2])
-        coef[3, :8, :] = torch.tensor(_SBF_COEF[3])
-        self.coef = coef
-
-    def forward(self, dist, three_body):
-        c = self.coef.tolist()
-        x = dist / self.cutoff
-        rbfs = [torch.sin(c[0][0][j] * x) / x for j in range(self.max_l)]
-        if self.max_n > 1:
-            rbfs += [(c[1][0][j] * x * torch.cos(c[1][1][j] * x) + c[1][2][j] * torch.sin(c[1][3][j] * x)) / x ** 2
-                     for j in range(self.max_l)]
-        if self.max_n > 2:
-            rbfs += [(c[2][0][j] * x ** 2 * torch.sin(c[2][1][j] * x) - c[2][2][j] * x * torch.cos(c[2][3][j] * x)
-                      + c[2][4][j] * torch.sin(c[2][5][j] * x)) / x ** 3 for j in range(self.max_l)]
-        if self.max_n > 3:
-            rbfs += [(c[3][0][j] * x ** 3 * torch.cos(c[3][1][j] * x) - c[3][2][j] * x ** 2
-                      * torch.sin(c[3][3][j] * x) - c[3][4][j] * x * torch.cos(c[3][5][j] * x)
-                      + c[3][6][j] * torch.sin(c[3][7][j] * x)) / x ** 4 for j in range(self.max_l)]
-        rbfs = torch.stack(rbfs, dim=-1) * self.factor
-        ct = torch.cos(three_body)
-        ys = [torch.ones_like(ct) * 0.5 * math.sqrt(1.0 / math.pi), math.sqrt(3.0 / (4.0 * math.pi)) * ct,
-              math.sqrt(5.0 / (16.0 * math.pi)) * (3.0 * ct ** 2 - 1.0),
-              math.sqrt(7.0 / (16.0 * math.pi)) * ct * (5.0 * ct ** 2 - 3.0)][: self.max_l]
-        cbfs = torch.stack(ys, dim=-1).repeat_interleave(self.max_n, dim=1)
-        return rbfs * cbfs
 
 
 # ------------------------------------------------------------------------------------
@@ -334,21 +289,14 @@ class ThreebodyEmbedding(nn.Module):
 
     def forward(self, graphs):
         lg = graphs["line_graph_dict"]
-        exp = self.expansion
-        if graphs["unit_edge_vectors"].is_cuda and exp.max_n == 4 and exp.max_l == 4 and "grp_de_t" in lg:
-            basis = ops.spherical_basis(graphs["unit_edge_vectors"], lg["grp_de_t"], lg["grp_de_s"], exp.cutoff)
-            lin = self.swish_layer.linear
-            if (ops.tb_embed_supported() and self.angle_embedding.bias is None and lin.bias is None
-                    and tuple(self.angle_embedding.weight.shape) == (128, 16)
-                    and tuple(lin.weight.shape) == (128, 128)):
-                return ops.tb_embed(basis, self.angle_embedding.weight, lin.weight, self._pack)
-            return self.swish_layer(self.angle_embedding(basis))
-        vij = torch.index_select(graphs["unit_edge_vectors"], 0, lg["target_DE_index"])
-        vjk = torch.index_select(graphs["unit_edge_vectors"], 0, lg["source_DE_index"])
-        cos_t = torch.sum(vij * vjk, dim=1) * (1 - 1e-6)
-        angle = torch.acos(cos_t)
-        basis = self.expansion(torch.norm(vjk, dim=1), angle)
-        return self.swish_layer(self.angle_embedding(basis))
+        if not graphs["unit_edge_vectors"].is_cuda:
+            raise RuntimeError("matris_amd ops run on the ROCm device only (no CPU fallback)")
+        basis = ops.spherical_basis(graphs["unit_edge_vectors"], lg["grp_de_t"], lg["grp_de_s"], self.expansion.cutoff)
+        lin = self.swish_layer.linear
+        if (ops.tb_embed_supported() and self.angle_embedding.bias is None and lin.bias is None
+                and tuple(self.angle_embedding.weight.shape) == (128, 16) and tuple(lin.weight.shape) == (128, 128)):
+            return ops.tb_embed(basis, self.angle_embedding.weight, lin.weight, self._pack)
+        return self.swish_layer(self.angle_embedding(basis))  # bf16x6 mode: library GEMMs on the device
 
 
 # ------------------------------------------------------------------------------------
@@ -582,10 +530,10 @@ class MatRIS(nn.Module):
         self.is_intensive = is_intensive
         # Memory modes for large cells.  block_checkpoint: None = decided per call from the
         # activation footprint (fused.blocks_to_checkpoint: the leading blocks that do not
-        # fit), True / False = all / none; a checkpointed block keeps only its inputs and
-        # reruns its forward in the backward.
+        # fit), True / False = all / none, an int k = the first k blocks; a checkpointed block
+        # keeps only its inputs and reruns its forward in the backward.
         # line_recompute: the two line-graph layers alone keep only their inputs.
-        self.block_checkpoint: bool | None = None
+        self.block_checkpoint: bool | int | None = None
         self.line_recompute: bool = False
         # created before the other modules, as in the reference (model.py:104-109): its Linear
         # consumes random numbers, so the seed-0 weights of the rest match with it too
@@ -645,8 +593,10 @@ class MatRIS(nn.Module):
         if self.block_checkpoint is None:
             n_ckpt = fused.blocks_to_checkpoint(bg["n_angles"], bg["n_directed"], n_blocks,
                                                 bg["atomic_numbers"].device)
-        else:
+        elif isinstance(self.block_checkpoint, bool):
             n_ckpt = n_blocks if self.block_checkpoint else 0
+        else:
+            n_ckpt = max(0, min(int(self.block_checkpoint), n_blocks))
         node = self.atom_embedding(bg["atomic_numbers"].long() - 1)
         edge, smooth = self.edge_embedding(graphs=bg)
         tb = None

@@ -25,7 +25,7 @@ def _graph():
 def test_valid_graph_passes_and_is_marked():
     g = _graph()
     validate_graph_indices(g)
-    assert g.meta["indices_checked"] is True
+    assert g.meta["indices_checked"] == g.index_signature()
 
 
 @pytest.mark.parametrize("field,row,col,delta", [
@@ -44,3 +44,32 @@ def test_out_of_range_index_refused_before_device_work(field, row, col, delta):
     with pytest.raises(ValueError, match="outside its range"):
         process_graphs([g])  # raises before any op that needs a GPU
     assert "indices_checked" not in g.meta
+
+
+@pytest.mark.parametrize("how", ["in_place", "replaced"])
+def test_edit_after_a_passed_check_is_checked_again(how):
+    """A graph whose indices passed the check and were then edited (in place, which bumps
+    the tensor's version counter, or by assigning a new tensor) is checked again: the
+    out-of-range index is refused before any device work."""
+    g = _graph()
+    validate_graph_indices(g)
+    U = len(g.undirected2directed)
+    if how == "in_place":
+        g.line_graph[3, 1] = U + 7
+    else:
+        lg = g.line_graph.clone()
+        lg[3, 1] = U + 7
+        g.line_graph = lg
+    with pytest.raises(ValueError, match="outside its range"):
+        process_graphs([g])
+    assert "indices_checked" not in g.meta
+
+
+def test_unchanged_graph_is_not_checked_twice(monkeypatch):
+    """The remembered check holds while no index tensor changes (one host read per graph)."""
+    g = _graph()
+    validate_graph_indices(g)
+    calls = []
+    monkeypatch.setattr(torch, "stack", lambda *a, **k: calls.append(1) or torch.cat([x[None] for x in a[0]]))
+    validate_graph_indices(g)
+    assert not calls
