@@ -57,29 +57,46 @@ def run(m, graphs, energy_only=False):
                 s=torch.stack(o["s"]).detach().numpy(), m=torch.cat(o["m"]).detach().numpy())
 
 
+def _oracle_graph(cr):
+    from oracle import graph_ref
+    og = graph_ref.build_graph(cr.frac, cr.lattice, cr.z)
+    return graph(dict(g_z=cr.z, g_frac=cr.frac, g_lattice=cr.lattice, g_image=og["image"],
+                      g_atom_graph=np.stack([og["center"], og["neighbor"]], 1), g_d2u=og["d2u"], g_u2d=og["u2d"],
+                      g_line_graph=og["line_graph"]), "g_")
+
+
 def main():
+    """python tests/golden/make_fp64.py [--big] [--only degenerate c4]: --only adds or
+    replaces just those entries of the existing fp64_oracle.npz."""
     torch.set_num_threads(8)
-    out = {}
+    path = os.path.join(HERE, "fp64_oracle.npz")
+    only = sys.argv[sys.argv.index("--only") + 1:] if "--only" in sys.argv else None
+    out = dict(np.load(path)) if only else {}
     m10 = model64(MATRIS_10M)
-    z = np.load(os.path.join(HERE, "c1_cu4.npz"))
-    for k, v in run(m10, [graph(z, "g_")]).items():
-        out[f"c1_{k}"] = v
-    for k, v in run(model64(DEFAULT_CONFIG), [graph(z, "g_")]).items():
-        out[f"c1l6_{k}"] = v
-    z = np.load(os.path.join(HERE, "cells_small.npz"))
-    for k, v in run(m10, [graph(z, f"g{i}_") for i in range(int(z["n_cells"]))]).items():
-        out[f"cells_{k}"] = v
-    if "--big" in sys.argv:
+    if only is None:
+        z = np.load(os.path.join(HERE, "c1_cu4.npz"))
+        for k, v in run(m10, [graph(z, "g_")]).items():
+            out[f"c1_{k}"] = v
+        for k, v in run(model64(DEFAULT_CONFIG), [graph(z, "g_")]).items():
+            out[f"c1l6_{k}"] = v
+        z = np.load(os.path.join(HERE, "cells_small.npz"))
+        for k, v in run(m10, [graph(z, f"g{i}_") for i in range(int(z["n_cells"]))]).items():
+            out[f"cells_{k}"] = v
+    if only is None and "--big" in sys.argv:
         from matris_amd import workloads as W
-        from oracle import graph_ref
-        cr = W.c3_cu864()
-        og = graph_ref.build_graph(cr.frac, cr.lattice, cr.z)
-        g = dict(g_z=cr.z, g_frac=cr.frac, g_lattice=cr.lattice, g_image=og["image"],
-                 g_atom_graph=np.stack([og["center"], og["neighbor"]], 1), g_d2u=og["d2u"], g_u2d=og["u2d"],
-                 g_line_graph=og["line_graph"])
-        for k, v in run(m10, [graph(g, "g_")], energy_only=True).items():
+        for k, v in run(m10, [_oracle_graph(W.c3_cu864())], energy_only=True).items():
             out[f"c3_{k}"] = v
-    np.savez_compressed(os.path.join(HERE, "fp64_oracle.npz"), **out)
+    if only and "degenerate" in only:
+        z = np.load(os.path.join(HERE, "degenerate.npz"))
+        for k, v in run(m10, [graph(z, "dil_")]).items():
+            out[f"dil_{k}"] = v
+        for k, v in run(m10, [graph(z, p) for p in ("cu_", "dil_", "tri_")]).items():
+            out[f"mixed_{k}"] = v
+    if only and "c4" in only:
+        from matris_amd import workloads as W
+        for k, v in run(m10, [_oracle_graph(cr) for cr in W.c4_batch64()], energy_only=True).items():
+            out[f"c4_{k}"] = v
+    np.savez_compressed(path, **out)
     print({k: v.shape for k, v in out.items()})
 
 

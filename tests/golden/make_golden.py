@@ -22,6 +22,17 @@ Outputs (small .npz / .json files; torch version recorded in meta):
   lg_cases.npz        reference line graphs for edge-case cells (cutoff boundary, self images)
   state_dict_seed0.json  per-tensor sha256 / sum of the seed-0 MatRIS-10M state_dict
   c3_cu864.npz        (--big) C3 graph hashes + efsm outputs
+  c4_batch64.npz      (--only c4) C4: per-graph hashes of the 64 reference graphs + efsm of
+                      the one disjoint batch
+  degenerate.npz      (--only degenerate) a cell with no bond under the line-graph cutoff
+                      (empty line graph: the line layers are skipped, model.py:201-203,
+                      interaction_block.py:406,425) alone, and batched between two cells
+                      that have angles; graph arrays + efsm
+
+  c1_graph_ref.pt     (--only graphfile) the C1 graph written by the reference's own
+                      RadiusGraph.save (radiusgraph.py:132-146): a torch.save of to_dict()
+
+    python tests/golden/make_golden.py --only c4 degenerate graphfile   (those fixtures only)
 """
 from __future__ import annotations
 
@@ -201,20 +212,71 @@ def sc_self_images():
     return W.Crystal(np.zeros((1, 3)), np.eye(3) * 3.0, np.array([29]))
 
 
+def dilute_cell():
+    """Two atoms in a 5.0 A cubic cell at (0,0,0) and (1/2,1/2,1/2): every bond (4.33 A to
+    the other atom, 5.0 A to the own images) is inside the 6 A atom-graph cutoff and outside
+    the 4 A line-graph cutoff, so the line graph is empty."""
+    return W.Crystal(np.array([[0.0, 0.0, 0.0], [0.5, 0.5, 0.5]]), np.eye(3) * 5.0, np.array([11, 17]))
+
+
+def hashes_of(a, keys=("center", "neighbor", "image", "atom_graph", "d2u", "u2d", "line_graph")):
+    return {k: hashlib.sha256(np.ascontiguousarray(a[k]).tobytes()).hexdigest() for k in keys}
+
+
 def small_cells():
     rng = np.random.default_rng(11)
     return [W.random_cell(rng, n) for n in (5, 8, 11)]
 
 
+def write_c4(model10):
+    """C4: 64 random triclinic cells (workloads.c4_batch64, seed 3) as one disjoint batch."""
+    cells = W.c4_batch64()
+    graphs, payload = [], {}
+    for i, cr in enumerate(cells):
+        a, g = reference_graph(cr)
+        for k, h in hashes_of(a).items():
+            payload[f"g{i}_h_{k}"] = np.array(h)
+        payload[f"g{i}_n"] = np.array([len(cr), len(a["center"]), len(a["u2d"]), len(a["line_graph"])])
+        graphs.append(g)
+    save("c4_batch64.npz", n_cells=np.array(len(cells)), **payload, **run_efsm(model10, graphs))
+
+
+def write_degenerate(model10):
+    """A cell whose line graph is empty, alone and inside a batch of cells with angles."""
+    payload = {}
+    a_d, g_d = reference_graph(dilute_cell())
+    assert len(a_d["line_graph"]) == 0 and len(a_d["center"]) > 0
+    payload.update(graph_payload("dil_", a_d))
+    payload.update({f"alone_{k}": v for k, v in run_efsm(model10, [g_d]).items()})
+    a_1, g_1 = reference_graph(W.c1_cu4())
+    a_c, g_c = reference_graph(small_cells()[0])
+    payload.update(graph_payload("cu_", a_1))
+    payload.update(graph_payload("tri_", a_c))
+    payload.update({f"mixed_{k}": v for k, v in run_efsm(model10, [g_1, g_d, g_c]).items()})
+    save("degenerate.npz", **payload)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--big", action="store_true", help="also write the C3 (864-atom) fixture")
+    ap.add_argument("--only", nargs="+", choices=["c4", "degenerate", "graphfile"],
+                    help="write only these fixtures (the base set and C3 are left as they are)")
     args = ap.parse_args()
     torch.set_num_threads(8)
     torch.set_default_dtype(torch.float32)
 
     cfg10 = dict(MATRIS_10M)
     model10 = make_model(cfg10)
+    if args.only:
+        if "degenerate" in args.only:
+            write_degenerate(model10)
+        if "graphfile" in args.only:
+            _, g = reference_graph(W.c1_cu4())
+            g.graph_id = "c1_cu4"
+            print("wrote", g.save(fname="c1_graph_ref.pt", save_dir=HERE))
+        if "c4" in args.only:
+            write_c4(model10)
+        return
     with open(os.path.join(HERE, "state_dict_seed0.json"), "w") as fh:
         json.dump(dict(n_params=sum(p.numel() for p in model10.parameters()), tensors=sd_fingerprint(model10)), fh,
                   indent=0, sort_keys=True)

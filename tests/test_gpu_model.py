@@ -210,3 +210,112 @@ def test_reference_energy_adds_composition_energy(golden):
     assert abs(out1["e"][0] - (out0["e"][0] + TABLES["mptrj"][28])) <= 1e-5 * abs(out1["e"][0])
     for k in "fsm":
         assert np.array_equal(out0[k], out1[k]), k
+
+
+def test_c3_mixed_checkpoint_split_is_bitwise_unchanged(golden):
+    """The first 3 of 10 blocks checkpointed (their original pass writes no saved
+    activations and reruns in the backward), the other 7 keeping theirs: the mixed split
+    the default picks for large cells.  e/f/s/m are bitwise those without checkpointing,
+    and within the bars of the C3 reference golden."""
+    from matris_amd import workloads as W
+    z = golden("c3_cu864.npz")
+    model = _model()
+    g = model.graph_converter(W.c3_cu864())
+    model.block_checkpoint = False
+    plain = _efsm(model, [g])
+    model.block_checkpoint = 3
+    mixed = _efsm(model, [g])
+    for k in "efsm":
+        assert np.array_equal(plain[k], mixed[k]), k
+    _assert_close(mixed, z, "C3 mixed checkpoint", _fp64(golden, "c3"))
+
+
+def _degenerate_graph(z, prefix):
+    return _graph_from_arrays({f"{prefix}{k}": z[f"{prefix}{k}"] for k in
+                               ("z", "frac", "lattice", "image", "atom_graph", "line_graph", "d2u", "u2d")}, prefix)
+
+
+def test_empty_line_graph_cell_vs_reference_golden(golden):
+    """A cell with no bond under the 4 A line-graph cutoff: the converter gives an empty
+    line graph (bit-exact atom graph, pairing and line graph against the reference Graph's)
+    and the model skips both line-graph layers of every block (model.py:201-203,
+    interaction_block.py:406,425); e/f/s/m against the reference modules' output."""
+    from matris_amd import workloads as W
+    z = golden("degenerate.npz")
+    model = _model()
+    cr = W.Crystal(np.asarray(z["dil_frac"]), np.asarray(z["dil_lattice"]), np.asarray(z["dil_z"]))
+    g = model.graph_converter(cr)
+    assert tuple(g.line_graph.shape) == (0, 5)
+    assert np.array_equal(g.atom_graph.cpu().numpy(), z["dil_atom_graph"])
+    assert np.array_equal(g.directed2undirected.cpu().numpy(), z["dil_d2u"])
+    assert np.array_equal(g.undirected2directed.cpu().numpy(), z["dil_u2d"])
+    ref = {k: z[f"alone_{k}"] for k in "efsm"}
+    _assert_close(_efsm(model, [g]), ref, "empty line graph (converter)", _fp64(golden, "dil"))
+    _assert_close(_efsm(model, [_degenerate_graph(z, "dil_")]), ref, "empty line graph (reference arrays)",
+                  _fp64(golden, "dil"))
+
+
+def test_mixed_batch_with_an_angle_free_cell_vs_reference_golden(golden):
+    """[Cu4, the angle-free cell, a triclinic cell] as one batch: the line layers run on the
+    batch's angles, and the angle-free cell's bonds still pass through the line attention's
+    node update with empty attention sums (the reference's index_add over no rows), so its
+    results differ from the cell evaluated alone; e/f/s/m against the reference."""
+    z = golden("degenerate.npz")
+    graphs = [_degenerate_graph(z, p) for p in ("cu_", "dil_", "tri_")]
+    ref = {k: z[f"mixed_{k}"] for k in "efsm"}
+    out = _efsm(_model(), graphs)
+    _assert_close(out, ref, "mixed batch with an angle-free cell", _fp64(golden, "mixed"))
+    assert not np.allclose(out["e"][1], z["alone_e"][0], rtol=1e-3)
+
+
+def test_isolated_atom_raises():
+    """converter.py:108-113: a structure with an atom that has no neighbour inside the
+    atom-graph cutoff stops with ValueError."""
+    from matris_amd import workloads as W
+    from matris_amd.graph import GraphConverter
+    cr = W.Crystal(np.array([[0.0, 0.0, 0.0], [0.5, 0.5, 0.5]]), np.eye(3) * 13.0, np.array([3, 3]))
+    with pytest.raises(ValueError, match="isolated atom"):
+        GraphConverter()(cr)
+
+
+def test_checkpoint_and_reference_graph_file_vs_reference_golden(golden, tmp_path):
+    """MatRIS.load of a {"config", "state_dict"} checkpoint (seed-0 weights, pinned to the
+    reference's by tests/test_files.py) and the C1 graph file written by the reference's
+    own RadiusGraph.save, evaluated on the device: e/f/s/m against the C1 golden."""
+    from matris_amd.graph import RadiusGraph
+    from matris_amd.model import MatRIS
+    torch.manual_seed(0)
+    m = MatRIS(**MATRIS_10M)
+    path = tmp_path / "ckpt.pth.tar"
+    torch.save({"config": dict(MATRIS_10M), "state_dict": m.state_dict()}, path)
+    model = MatRIS.load(path=str(path), device="cuda").eval()
+    g = RadiusGraph.from_file(os.path.join(os.path.dirname(__file__), "golden", "c1_graph_ref.pt")).to("cuda")
+    _assert_close(_efsm(model, [g]), golden("c1_cu4.npz"), "C1 checkpoint + reference graph file",
+                  _fp64(golden, "c1"))
+
+
+def test_c4_batch64_graphs_and_efsm_vs_reference_golden(golden):
+    """Config C4: 64 random triclinic cells of 8-64 atoms (Z 1..94, seed 3), each graph built
+    on the GPU and hash-equal to the reference Graph's arrays, then evaluated as ONE
+    disjoint batch (processgraph.py:58-120 offsets, per-graph strain and image shifts)."""
+    from matris_amd import workloads as W
+    z = golden("c4_batch64.npz")
+    model = _model()
+    cells = W.c4_batch64()
+    assert len(cells) == int(z["n_cells"]) == 64
+    graphs = []
+    for i, cr in enumerate(cells):
+        g = model.graph_converter(cr)
+        arrays = dict(center=g.atom_graph[:, 0], neighbor=g.atom_graph[:, 1], image=g.neighbor_image,
+                      atom_graph=g.atom_graph, d2u=g.directed2undirected, u2d=g.undirected2directed,
+                      line_graph=g.line_graph)
+        for k, v in arrays.items():
+            a = np.ascontiguousarray(v.cpu().numpy().astype(np.int64))
+            assert hashlib.sha256(a.tobytes()).hexdigest() == str(z[f"g{i}_h_{k}"]), (i, k)
+        graphs.append(g)
+    out = _efsm(model, graphs)
+    assert out["e"].shape == (64,) and out["f"].shape[0] == sum(len(c) for c in cells)
+    _assert_close(out, z, "C4 batch of 64", _fp64(golden, "c4"))
+    again = _efsm(model, graphs)  # no float atomics on the path: bitwise reproducible
+    for k in "efsm":
+        assert np.array_equal(out[k], again[k]), k
