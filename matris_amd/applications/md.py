@@ -1,26 +1,59 @@
 """Molecular dynamics on the GPU with MatRIS forces.
 
-Reference: matris/applications/md.py:31-330 (MolecularDynamics), which wraps ASE's
-VelocityVerlet (NVE) and NVTBerendsen (NVT, thermostat "Berendsen*") integrators around
-MatRISCalculator.  ASE is not part of this build, so the two integrators are restated
-from their published methods and run with every per-atom array resident on the device:
+Reference: matris/applications/md.py:31-330 (MolecularDynamics), which builds one of
+ASE's integrators around MatRISCalculator (md.py:120-289):
+
+  ensemble "nve"                               VelocityVerlet
+  "nvt", thermostat "Berendsen*"               NVTBerendsen
+  "nvt", thermostat "Nose-Hoover"              NPT with pfactor=None (Nose-Hoover thermostat)
+  "npt", thermostat "Nose-Hoover"              NPT (Nose-Hoover + Parrinello-Rahman barostat)
+  "npt", thermostat "Berendsen_inhomogeneous"  Inhomogeneous_NPTBerendsen
+  "npt", thermostat "NPT_Berendsen"            NPTBerendsen
+
+ASE is not part of this build, so the integrators are restated from their published
+methods and run with every per-atom array resident on the device (fp64):
 
   velocity Verlet (Swope, Andersen, Berendsen & Wilson, J. Chem. Phys. 76, 637 (1982)):
       v += dt/2 a(x);  x += dt v;  a = F(x)/m;  v += dt/2 a
-  Berendsen weak coupling (Berendsen et al., J. Chem. Phys. 81, 3684 (1984)), applied to
-  the velocities before each Verlet step:
-      lambda = sqrt(1 + dt/tau (T0/T - 1)), clamped to [0.9, 1.1]
-  with the kinetic temperature T = 2 KE / (3 N k_B).
+  Berendsen weak coupling (Berendsen et al., J. Chem. Phys. 81, 3684 (1984)), applied
+  before each Verlet step:
+      thermostat  v *= sqrt(1 + dt/tau_T (T0/T - 1)), the factor clamped to [0.9, 1.1]
+      barostat    cell, x *= 1 - dt beta / (3 tau_P) (P0 - P)        (isotropic, P = -tr(sigma)/3)
+                  lattice vector k *= 1 - dt beta / (3 tau_P) (P0 + sigma_kk)   (inhomogeneous)
+      with beta = 1 / bulk modulus and sigma the stress including the ideal-gas term
+      -sum m v v^T / V;
+  Nose-Hoover thermostat with a Parrinello-Rahman barostat in Melchionna's form
+  (Melchionna, Ciccotti & Holian, Mol. Phys. 78, 533 (1993)):
+      dr/dt = v + eta (r - R_cm)          dv/dt = F/m - (eta + zeta) v
+      dzeta/dt = (2 KE - g k T0) / Q      Q = g k T0 tau_T^2,  g = 3 (N - 1)
+      deta/dt = V (P - P0 I) / W          W = V0 tau_P^2 B  (B the bulk modulus)
+      dh/dt = eta h                       (h: lattice vectors as columns)
+  with eta kept lower-triangular in that column convention, so the cell, transformed to
+  upper-triangular rows first as the reference does (md.py:323-349), stays so.  The
+  pressure tensor is P = -sigma (ideal-gas term included).  The integrator is a
+  symmetric splitting (thermostat/barostat half steps around a velocity-Verlet step with
+  exp(-(eta + zeta) dt/2) velocity scalings and exp(eta dt/2) position/cell maps); it
+  conserves
+      H = E_pot + KE + P0 V + W tr(eta^T eta)/2 + Q zeta^2/2 + g k T0 xi,  dxi/dt = zeta
+  (conserved_energy()) to O(dt^2).  Without a barostat (ensemble "nvt") eta stays 0.
+
+ASE's own NPT integrator is not restated step for step, so trajectories are checked by
+the invariants above, not against ASE (ASE is absent here).  The reference's fallback
+when bulk_modulus is None (an equation-of-state fit whose class is never imported in
+md.py, so it always ends in its `except`: bulk modulus 2 GPa with a warning,
+md.py:193-212) is kept as that warning and 2 GPa.
 
 Each step rebuilds the radius graph and line graph on the GPU (GraphConverter) from the
-current positions and evaluates MatRIS (task "ef" plus whatever `task` asks for).
+current positions and cell and evaluates MatRIS (task "ef", plus "s" for the barostats).
 Units: positions in Angstrom, time in fs, velocities in Angstrom/fs, masses in amu,
-energies in eV.
+energies in eV, stress in eV/A^3 (pressure and bulk_modulus arguments in GPa, as in the
+reference).
 """
 from __future__ import annotations
 
 import math
 import time
+import warnings
 
 import numpy as np
 import torch
@@ -42,6 +75,8 @@ ATOMIC_MASSES = np.array([
 KB_EV = 8.617333262e-5            # Boltzmann constant, eV/K
 AMU_A2_FS2_EV = 103.642691        # 1 amu * (Angstrom/fs)^2 in eV
 FORCE_TO_ACC = 1.0 / AMU_A2_FS2_EV  # (eV/Angstrom)/amu -> Angstrom/fs^2
+GPA_EV_A3 = 1.0 / 160.21766208    # 1 GPa in eV/A^3
+DEFAULT_BULK_MODULUS_GPA = 2.0    # md.py:207-209
 
 
 def _detached(v):
@@ -53,15 +88,216 @@ def _detached(v):
     return v
 
 
+def upper_triangular_basis(cell: np.ndarray) -> np.ndarray:
+    """The lattice with the same lengths and angles as `cell` (rows a, b, c) in the
+    upper-triangular orientation the reference switches to before its Nose-Hoover
+    integrators (md.py:323-349): a = (a sin(beta) sin(phi), a sin(beta) cos(phi),
+    a cos(beta)), b = (0, b sin(alpha), b cos(alpha)), c = (0, 0, c), with cos(phi) =
+    (cos(gamma) - cos(alpha) cos(beta)) / (sin(alpha) sin(beta))."""
+    cell = np.asarray(cell, np.float64)
+    a, b, c = np.linalg.norm(cell, axis=1)
+    cos_a = cell[1] @ cell[2] / (b * c)
+    cos_b = cell[0] @ cell[2] / (a * c)
+    cos_g = cell[0] @ cell[1] / (a * b)
+    sin_a, sin_b = math.sqrt(max(0.0, 1 - cos_a ** 2)), math.sqrt(max(0.0, 1 - cos_b ** 2))
+    cos_p = float(np.clip((cos_g - cos_a * cos_b) / (sin_a * sin_b), -1.0, 1.0))
+    sin_p = math.sqrt(1 - cos_p ** 2)
+    return np.array([[a * sin_b * sin_p, a * sin_b * cos_p, a * cos_b], [0.0, b * sin_a, b * cos_a], [0.0, 0.0, c]])
+
+
+def _is_upper_triangular(cell) -> bool:
+    c = np.asarray(cell)
+    return bool(c[1, 0] == 0 and c[2, 0] == 0 and c[2, 1] == 0)
+
+
+class Dynamics:
+    """The integrators on device-resident fp64 state, independent of the force model.
+
+    evaluate(pos [n,3], cell [3,3] rows, need_stress) -> (forces [n,3] eV/A, stress
+    [3,3] eV/A^3 or None, potential energy eV (a float) or None).  The caller owns
+    pos / vel / cell (torch fp64, one device).
+    """
+
+    def __init__(self, pos, vel, masses, cell, evaluate, kind: str, timestep: float, temperature: float,
+                 taut: float, pressure_gpa: float = 0.0, taup: float | None = None,
+                 bulk_modulus_gpa: float | None = None, mask=(1, 1, 1)):
+        self.pos, self.vel, self.masses, self.cell = pos, vel, masses, cell
+        self.evaluate = evaluate
+        self.kind = kind  # nve | nvt_berendsen | nvt_nose_hoover | npt_berendsen | npt_berendsen_inhom | npt_nose_hoover
+        self.dt = float(timestep)
+        self.temperature = float(temperature)
+        self.taut = float(taut)
+        self.pressure = float(pressure_gpa) * GPA_EV_A3
+        self.taup = float(taup) if taup is not None else 1000.0 * self.dt
+        self.bulk = (bulk_modulus_gpa if bulk_modulus_gpa is not None else DEFAULT_BULK_MODULUS_GPA) * GPA_EV_A3
+        self.mask = torch.as_tensor(mask, dtype=pos.dtype, device=pos.device)
+        n = pos.shape[0]
+        self.n = n
+        self.g = 3 * (n - 1) if n > 1 else 3
+        kt0 = KB_EV * self.temperature
+        self.Q = self.g * kt0 * self.taut ** 2
+        self.zeta = 0.0
+        self.xi = 0.0
+        self.eta = torch.zeros(3, 3, dtype=pos.dtype, device=pos.device)
+        self.V0 = self.volume()
+        self.W = self.V0 * self.taup ** 2 * self.bulk
+        self.forces = None
+        self.stress = None
+        self.epot = None
+        self.nsteps = 0
+
+    # -- state --------------------------------------------------------------------
+    def volume(self) -> float:
+        return float(abs(torch.linalg.det(self.cell)))
+
+    def kinetic_energy(self) -> float:
+        return float(0.5 * (self.masses[:, None] * self.vel * self.vel).sum() * AMU_A2_FS2_EV)
+
+    def temperature_now(self) -> float:
+        return 2.0 * self.kinetic_energy() / (3.0 * self.n * KB_EV)
+
+    def ideal_gas_stress(self):
+        """-sum m v v^T / V in eV/A^3 (the kinetic part of the stress)."""
+        mv = self.masses[:, None] * self.vel
+        return -(mv.t() @ self.vel) * AMU_A2_FS2_EV / self.volume()
+
+    def pressure_tensor(self):
+        return -(self.stress + self.ideal_gas_stress())
+
+    def conserved_energy(self) -> float:
+        """E_pot + KE (+ the thermostat and barostat terms for the Nose-Hoover kinds)."""
+        h = self.epot + self.kinetic_energy()
+        if self.kind in ("nvt_nose_hoover", "npt_nose_hoover"):
+            h += 0.5 * self.Q * self.zeta ** 2 + self.g * KB_EV * self.temperature * self.xi
+        if self.kind == "npt_nose_hoover":
+            h += self.pressure * self.volume() + 0.5 * self.W * float((self.eta * self.eta).sum())
+        return h
+
+    def _need_stress(self) -> bool:
+        return self.kind.startswith("npt")
+
+    def _refresh(self):
+        self.forces, self.stress, self.epot = self.evaluate(self.pos, self.cell, self._need_stress())
+
+    def _set_cell(self, new_cell):
+        """New cell with the atoms carried along in fractional coordinates (ASE's
+        set_cell(..., scale_atoms=True))."""
+        self.pos = self.pos @ torch.linalg.solve(self.cell, new_cell)
+        self.cell = new_cell
+
+    # -- steps --------------------------------------------------------------------
+    def _verlet(self):
+        inv_m = (FORCE_TO_ACC / self.masses)[:, None]
+        self.vel += 0.5 * self.dt * self.forces * inv_m
+        self.pos += self.dt * self.vel
+        self._refresh()
+        self.vel += 0.5 * self.dt * self.forces * inv_m
+
+    def _berendsen_thermostat(self):
+        t = self.temperature_now()
+        lam = math.sqrt(1.0 + self.dt / self.taut * (self.temperature / t - 1.0)) if t > 0 else 1.0
+        self.vel *= min(max(lam, 0.9), 1.1)
+
+    def _berendsen_barostat(self, inhomogeneous: bool):
+        sigma = self.stress + self.ideal_gas_stress()
+        k = self.dt / (3.0 * self.taup * self.bulk)
+        if inhomogeneous:  # each lattice vector scaled by its own diagonal component
+            f = 1.0 - k * (self.pressure + torch.diagonal(sigma)) * self.mask
+            new = self.cell * f[:, None]
+        else:
+            p = -float(torch.trace(sigma)) / 3.0
+            new = self.cell * (1.0 - k * (self.pressure - p))
+        self._set_cell(new)
+
+    def _nh_half(self, with_barostat: bool):
+        """Half step of the thermostat (and barostat) variables from the current KE and
+        pressure tensor."""
+        h = 0.5 * self.dt
+        ke = self.kinetic_energy()
+        kt0 = KB_EV * self.temperature
+        self.zeta += h * (2.0 * ke - self.g * kt0) / self.Q
+        if with_barostat:
+            d = (self.pressure_tensor() - self.pressure * torch.eye(3, dtype=self.pos.dtype, device=self.pos.device))
+            self.eta = self.eta + h * self.volume() / self.W * torch.tril(d)
+
+    def _nh_step(self, with_barostat: bool):
+        h = 0.5 * self.dt
+        eye = torch.eye(3, dtype=self.pos.dtype, device=self.pos.device)
+        self._nh_half(with_barostat)
+        self.xi += self.dt * self.zeta  # the thermostat integral over the two drag half steps
+        drag = torch.linalg.matrix_exp(-(self.eta + self.zeta * eye) * h)  # v <- drag v
+        self.vel = self.vel @ drag.t()
+        inv_m = (FORCE_TO_ACC / self.masses)[:, None]
+        self.vel += h * self.forces * inv_m
+        if with_barostat:
+            grow = torch.linalg.matrix_exp(self.eta * h)  # r - R_cm <- grow (r - R_cm), twice
+            com = (self.masses[:, None] * self.pos).sum(0) / self.masses.sum()
+            self.pos = com + (self.pos - com) @ grow.t()
+            self.pos += self.dt * self.vel
+            com = (self.masses[:, None] * self.pos).sum(0) / self.masses.sum()
+            self.pos = com + (self.pos - com) @ grow.t()
+            self.cell = self.cell @ (grow @ grow).t()  # rows: h_rows <- h_rows exp(eta dt)^T
+        else:
+            self.pos += self.dt * self.vel
+        self._refresh()
+        self.vel += h * self.forces * inv_m
+        self.vel = self.vel @ drag.t()
+        self._nh_half(with_barostat)
+
+    def step(self) -> None:
+        if self.forces is None:
+            self._refresh()
+        k = self.kind
+        if k == "nve":
+            self._verlet()
+        elif k == "nvt_berendsen":
+            self._berendsen_thermostat()
+            self._verlet()
+        elif k in ("npt_berendsen", "npt_berendsen_inhom"):
+            self._berendsen_thermostat()
+            self._berendsen_barostat(inhomogeneous=k.endswith("inhom"))
+            self._verlet()
+        elif k == "nvt_nose_hoover":
+            self._nh_step(with_barostat=False)
+        elif k == "npt_nose_hoover":
+            self._nh_step(with_barostat=True)
+        else:  # pragma: no cover - rejected in the constructor
+            raise ValueError(k)
+        self.nsteps += 1
+
+
+def _kind(ensemble: str, thermostat: str) -> str:
+    """The reference's ensemble / thermostat choice (md.py:120-289), as an integrator kind."""
+    ens, th = ensemble.lower(), thermostat.lower()
+    if ens == "nve":
+        return "nve"
+    if ens == "nvt":
+        if th == "nose-hoover":
+            return "nvt_nose_hoover"
+        if th.startswith("berendsen"):
+            return "nvt_berendsen"
+        raise ValueError("Thermostat not supported, choose in 'Nose-Hoover', 'Berendsen', "
+                         "'Berendsen_inhomogeneous'")
+    if ens == "npt":
+        if th == "nose-hoover":
+            return "npt_nose_hoover"
+        if th == "berendsen_inhomogeneous":
+            return "npt_berendsen_inhom"
+        if th == "npt_berendsen":
+            return "npt_berendsen"
+        raise ValueError("Thermostat not supported, choose in 'Nose-Hoover', 'Berendsen', "
+                         "'Berendsen_inhomogeneous'")
+    raise ValueError(f"ensemble {ensemble!r} not supported: 'nve', 'nvt' or 'npt'")
+
+
 class MolecularDynamics:
     """GPU molecular dynamics with the reference's constructor keywords (md.py:34-54).
 
     atoms: (frac [n,3], lattice [3,3] rows, Z [n]) arrays, an object with frac / lattice /
     z attributes (matris_amd.workloads.Crystal), or an ASE Atoms when ASE is installed.
     model: a MatRIS instance (reference names such as "matris_10m_oam" need a local
-    checkpoint, see MatRIS.load).  Supported: ensemble "nve", or "nvt" with a
-    "Berendsen*" thermostat; the other reference choices (Nose-Hoover, NPT) rely on ASE
-    and raise NotImplementedError.
+    checkpoint, see MatRIS.load).  seed: the Maxwell-Boltzmann draw of starting_temperature.
+    skin > 0 reuses the neighbour list across steps (constant-volume ensembles only).
     """
 
     def __init__(self, atoms, model="matris_10m_oam", ensemble: str = "nvt",
@@ -74,10 +310,7 @@ class MolecularDynamics:
         from ..graph.converter import _structure_arrays
         from ..model.model import MatRIS
         self.ensemble, self.thermostat = ensemble.lower(), thermostat
-        if self.ensemble not in ("nve", "nvt") or (self.ensemble == "nvt"
-                                                    and not thermostat.lower().startswith("berendsen")):
-            raise NotImplementedError(f"ensemble={ensemble!r} thermostat={thermostat!r} needs ASE; "
-                                      "this build runs 'nve' and 'nvt' with a Berendsen thermostat")
+        kind = _kind(ensemble, thermostat)
         if isinstance(model, str):
             model = MatRIS.load(model, device=device)
         self.model = model
@@ -87,28 +320,45 @@ class MolecularDynamics:
         frac, lat, z, _ = _structure_arrays(atoms)
         self.z = np.asarray(z, np.int64)
         self.n = len(self.z)
-        self.lattice = np.asarray(lat, np.float64)
-        self._lat_t = torch.as_tensor(self.lattice, device=self.device)
-        self._inv_lat_t = torch.linalg.inv(self._lat_t)
-        self.pos = torch.as_tensor(np.asarray(frac, np.float64) @ self.lattice, device=self.device)
-        self.masses = torch.as_tensor(ATOMIC_MASSES[self.z - 1], device=self.device)
-        self.vel = torch.zeros_like(self.pos)
+        lattice = np.asarray(lat, np.float64)
+        pos = np.asarray(frac, np.float64) @ lattice
+        if kind.endswith("nose_hoover") and not _is_upper_triangular(lattice):  # md.py:136,229
+            new = upper_triangular_basis(lattice)
+            pos = pos @ np.linalg.solve(lattice, new)
+            lattice = new
+        dev = self.device
+        masses = torch.as_tensor(ATOMIC_MASSES[self.z - 1], device=dev)
+        vel = torch.zeros(self.n, 3, dtype=torch.float64, device=dev)
         momenta = getattr(atoms, "get_momenta", None)
         if momenta is not None:  # ASE Atoms: momenta in sqrt(amu eV) -> v in Angstrom/fs
-            p = torch.as_tensor(np.asarray(momenta(), np.float64), device=self.device)
-            self.vel = p / self.masses[:, None] * math.sqrt(1.0 / AMU_A2_FS2_EV)
+            p = torch.as_tensor(np.asarray(momenta(), np.float64), device=dev)
+            vel = p / masses[:, None] * math.sqrt(1.0 / AMU_A2_FS2_EV)
+        if taut is None:
+            taut = 100 * timestep
+        if taup is None:
+            taup = 1000 * timestep
+        if kind.startswith("npt") and bulk_modulus is None:
+            warnings.warn("bulk_modulus not given: using 2 GPa (the reference's fallback when its equation-of-state "
+                          "fit fails); the pressure relaxation time is then only nominal", RuntimeWarning,
+                          stacklevel=2)
+        self.bulk_modulus = bulk_modulus if bulk_modulus is not None else (
+            DEFAULT_BULK_MODULUS_GPA if kind.startswith("npt") else None)
+        if skin > 0 and kind.startswith("npt"):
+            raise ValueError("skin > 0 reuses one cell's neighbour list: not with a barostat")
+        self.task = task if "f" in task else task + "f"
+        if kind.startswith("npt") and "s" not in self.task:
+            self.task += "s"
+        self.dyn = Dynamics(torch.as_tensor(pos, device=dev), vel, masses, torch.as_tensor(lattice, device=dev),
+                            self._evaluate, kind, timestep, temperature, taut, pressure, taup, self.bulk_modulus)
         if starting_temperature is not None:
             self.maxwell_boltzmann(starting_temperature, seed)
         self.temperature = float(temperature)
         self.timestep = float(timestep)
-        self.taut = float(taut) if taut is not None else 100.0 * timestep
-        self.task = task if "f" in task else task + "f"
+        self.taut, self.taup = float(taut), float(taup)
         self.logfile, self.loginterval = logfile, loginterval
         self.trajectory = trajectory
-        self.nsteps = 0
         self.timings = {"graph": 0.0, "model": 0.0}
         self.results = None
-        self._forces = None
         # skin > 0: Verlet-skin reuse of the neighbour list (graphs identical to a rebuild
         # every step, which is what the reference does and what skin = 0 keeps)
         self.skin = float(skin)
@@ -118,63 +368,79 @@ class MolecularDynamics:
             self._neighbors = SkinNeighborList(self.lattice, self.model.graph_converter.atom_graph_cutoff, self.skin)
 
     # --------------------------------------------------------------------------------
+    @property
+    def pos(self):
+        return self.dyn.pos
+
+    @property
+    def vel(self):
+        return self.dyn.vel
+
+    @property
+    def masses(self):
+        return self.dyn.masses
+
+    @property
+    def lattice(self) -> np.ndarray:
+        return self.dyn.cell.cpu().numpy()
+
+    @property
+    def nsteps(self) -> int:
+        return self.dyn.nsteps
+
     def maxwell_boltzmann(self, temperature: float, seed: int | None = None) -> None:
-        """Velocities from the Maxwell-Boltzmann distribution at `temperature`, zero total
-        momentum, then rescaled to exactly `temperature` (ASE's MaxwellBoltzmannDistribution
-        with force_temp=True followed by Stationary, restated)."""
+        """Velocities from the Maxwell-Boltzmann distribution at `temperature`, rescaled to
+        exactly `temperature`, then the centre-of-mass motion removed (so the start sits
+        O(1/N) below it): ASE's MaxwellBoltzmannDistribution(force_temp=True) followed by
+        Stationary, the reference's order (md.py:105-109), restated."""
         rng = np.random.default_rng(seed)
-        m = self.masses.cpu().numpy()
+        m = self.dyn.masses.cpu().numpy()
         sigma = np.sqrt(KB_EV * temperature / (m * AMU_A2_FS2_EV))
         v = rng.standard_normal((self.n, 3)) * sigma[:, None]
-        v -= (m[:, None] * v).sum(0) / m.sum()  # zero total momentum
-        self.vel = torch.as_tensor(v, device=self.device)
-        t = self.kinetic_temperature()
+        t = float((m[:, None] * v * v).sum() * AMU_A2_FS2_EV / (3.0 * self.n * KB_EV))
         if t > 0:
-            self.vel *= math.sqrt(temperature / t)
+            v *= math.sqrt(temperature / t)
+        v -= (m[:, None] * v).sum(0) / m.sum()
+        self.dyn.vel = torch.as_tensor(v, device=self.device)
 
     def kinetic_energy(self) -> float:
-        return float(0.5 * (self.masses[:, None] * self.vel * self.vel).sum() * AMU_A2_FS2_EV)
+        return self.dyn.kinetic_energy()
 
     def kinetic_temperature(self) -> float:
-        return 2.0 * self.kinetic_energy() / (3.0 * self.n * KB_EV)
+        return self.dyn.temperature_now()
+
+    def conserved_energy(self) -> float:
+        return self.dyn.conserved_energy()
 
     # --------------------------------------------------------------------------------
-    def _evaluate(self):
-        """Rebuild the graph on the GPU from the current positions and evaluate the model."""
+    def _evaluate(self, pos, cell, need_stress):
+        """Rebuild the graph on the GPU from the current positions and cell and evaluate
+        the model: forces (eV/A), stress (eV/A^3, ASE's sign) and the potential energy."""
         t0 = time.perf_counter()
-        x = self.pos @ self._inv_lat_t
+        inv = torch.linalg.inv(cell)
+        x = pos @ inv
         frac = x.remainder(1.0).contiguous()  # wrap: the graph is periodic
-        nbrs = self._neighbors.update(frac, x, self.pos) if self._neighbors is not None else None
-        graph = self.model.graph_converter.from_arrays(None, self.lattice, self.z, frac_device=frac, neighbors=nbrs)
+        nbrs = self._neighbors.update(frac, x, pos) if self._neighbors is not None else None
+        graph = self.model.graph_converter.from_arrays(None, cell.cpu().numpy(), self.z, frac_device=frac,
+                                                       neighbors=nbrs)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         pred = self.model([graph], task=self.task)
-        forces = pred["f"][0].to(torch.float64)
+        forces = pred["f"][0].detach().to(torch.float64)
+        stress = pred["s"][0].detach().to(torch.float64) * GPA_EV_A3 if need_stress else None
         torch.cuda.synchronize()
         self.timings["graph"] += t1 - t0
         self.timings["model"] += time.perf_counter() - t1
         self.results = {k: _detached(v) for k, v in pred.items()}
-        return forces
+        e = self.results["e"][0] * self.n if self.model.is_intensive else self.results["e"][0]
+        return forces, stress, float(e)
 
     def step(self) -> None:
-        dt = self.timestep
-        if self._forces is None:
-            self._forces = self._evaluate()
-        if self.ensemble == "nvt":
-            t = self.kinetic_temperature()
-            lam = math.sqrt(1.0 + dt / self.taut * (self.temperature / t - 1.0)) if t > 0 else 1.0
-            self.vel *= min(max(lam, 0.9), 1.1)
-        inv_m = (FORCE_TO_ACC / self.masses)[:, None]
-        self.vel += 0.5 * dt * self._forces * inv_m
-        self.pos += dt * self.vel
-        self._forces = self._evaluate()
-        self.vel += 0.5 * dt * self._forces * inv_m
-        self.nsteps += 1
+        self.dyn.step()
         if self.logfile and self.nsteps % self.loginterval == 0:
             with open(self.logfile, "a") as fh:
-                e = float(self.results["e"][0]) * self.n
-                fh.write(f"{self.nsteps * dt:10.3f} fs  Epot {e:14.6f} eV  Ekin {self.kinetic_energy():12.6f} eV  "
-                         f"T {self.kinetic_temperature():9.2f} K\n")
+                fh.write(f"{self.nsteps * self.timestep:10.3f} fs  Epot {self.dyn.epot:14.6f} eV  "
+                         f"Ekin {self.kinetic_energy():12.6f} eV  T {self.kinetic_temperature():9.2f} K\n")
 
     def run(self, steps: int) -> None:
         """Advance `steps` MD steps (md.py:297-310)."""
@@ -182,4 +448,4 @@ class MolecularDynamics:
             self.step()
 
     def get_positions(self) -> np.ndarray:
-        return self.pos.cpu().numpy()
+        return self.dyn.pos.cpu().numpy()

@@ -131,3 +131,45 @@ def test_md_nve_conserves_energy_and_nvt_thermostat(model):
     t0 = nvt.kinetic_temperature()
     nvt.run(15)
     assert nvt.kinetic_temperature() > t0 + 100
+
+
+@pytest.mark.parametrize("ensemble", ["nvt", "npt"])
+def test_md_nose_hoover_conserves_extended_energy(model, ensemble):
+    """The Nose-Hoover thermostat (ensemble "nvt") and Nose-Hoover + Parrinello-Rahman
+    (ensemble "npt") of md.py:129-150,224-243 with MatRIS forces and stress: the extended
+    energy (conserved_energy) drifts far less than the kinetic energy swings; the NPT cell
+    is upper-triangular (md.py:323-349) and moves."""
+    from matris_amd.applications import MolecularDynamics
+    cr, _ = _cu32(sigma=0.02)
+    kw = dict(bulk_modulus=100.0, taup=200.0) if ensemble == "npt" else {}
+    md = MolecularDynamics((cr.frac, cr.lattice, cr.z), model=model, ensemble=ensemble, thermostat="Nose-Hoover",
+                           temperature=300, starting_temperature=300, timestep=1.0, taut=20.0, task="efs",
+                           device="cuda", seed=13, **kw)
+    md.run(1)
+    h0, ek, lat0 = md.conserved_energy(), [], md.lattice.copy()
+    for _ in range(20):
+        md.run(1)
+        ek.append(md.kinetic_energy())
+    drift = abs(md.conserved_energy() - h0)
+    assert drift < 0.05 * (max(ek) - min(ek)) + 1e-4, (drift, max(ek) - min(ek))
+    if ensemble == "npt":
+        lat = md.lattice
+        assert lat[1, 0] == 0 and lat[2, 0] == 0 and lat[2, 1] == 0
+        assert not np.array_equal(lat, lat0)
+
+
+@pytest.mark.parametrize("thermostat", ["Berendsen_inhomogeneous", "NPT_Berendsen"])
+def test_md_npt_berendsen_moves_the_cell(model, thermostat):
+    """The two Berendsen barostats of md.py:245-283 run with MatRIS stress: the cell
+    changes and stays finite; without bulk_modulus the reference's 2 GPa fallback warns."""
+    from matris_amd.applications import MolecularDynamics
+    cr, _ = _cu32(sigma=0.02)
+    with pytest.warns(RuntimeWarning, match="bulk_modulus"):
+        md = MolecularDynamics((cr.frac, cr.lattice, cr.z), model=model, ensemble="npt", thermostat=thermostat,
+                               temperature=300, starting_temperature=300, timestep=1.0, taup=50.0, task="ef",
+                               device="cuda", seed=14)
+    assert "s" in md.task
+    lat0 = md.lattice.copy()
+    md.run(5)
+    assert np.all(np.isfinite(md.lattice)) and not np.array_equal(md.lattice, lat0)
+    assert np.all(np.isfinite(md.get_positions()))

@@ -1,0 +1,205 @@
+"""The MD integrators (matris_amd.applications.md.Dynamics) on the CPU, driven by an
+analytic periodic pair potential whose forces and stress come from autograd of the same
+energy (stress = (1/V) dE/d(strain), ASE's sign).  ASE is absent, so the ensembles are
+pinned by what their published equations guarantee:
+
+  * NVE velocity Verlet: E_pot + KE conserved;
+  * Nose-Hoover NVT and NPT (Melchionna): the extended energy conserved, its drift
+    shrinking ~dt^2; the centre of mass fixed; the NPT cell kept upper-triangular;
+  * Berendsen NVT / NPT: the temperature and the pressure relax toward their targets, the
+    inhomogeneous barostat scaling each lattice vector on its own (angles unchanged);
+  * the reference's ensemble / thermostat names (md.py:120-289) and its error messages;
+  * the reference's upper-triangular cell transform (md.py:323-349): same lengths and
+    angles, fractional coordinates unchanged.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from matris_amd.applications.md import (AMU_A2_FS2_EV, KB_EV, Dynamics, _kind, upper_triangular_basis)
+
+RC = 3.2
+IMAGES = torch.tensor([(i, j, k) for i in (-1, 0, 1) for j in (-1, 0, 1) for k in (-1, 0, 1)], dtype=torch.float64)
+
+
+def pair_energy(pos, cell):
+    """sum over ordered pairs (all images within RC) of ((RC - r)^4 - 0.8 (RC - r)^3) / 2."""
+    shifts = IMAGES @ cell  # [27, 3]
+    d = pos[None, :, None, :] + shifts[None, None] - pos[:, None, None, :]  # [i, j, img, 3]
+    r2 = (d * d).sum(-1)
+    n = pos.shape[0]
+    self_mask = torch.eye(n, dtype=torch.bool)[:, :, None] & (IMAGES.abs().sum(1) == 0)[None, None, :]
+    r2 = torch.where(self_mask, torch.full_like(r2, 100.0), r2)
+    r = torch.sqrt(r2)
+    x = torch.clamp(RC - r, min=0.0)
+    return 0.5 * (x ** 4 - 0.8 * x ** 3).sum()
+
+
+def evaluate(pos, cell, need_stress):
+    p = pos.detach().clone().requires_grad_(True)
+    eps = torch.zeros(3, 3, dtype=torch.float64, requires_grad=True)
+    sym = 0.5 * (eps + eps.t())
+    eye = torch.eye(3, dtype=torch.float64)
+    e = pair_energy(p @ (eye + sym), cell @ (eye + sym))
+    gp, ge = torch.autograd.grad(e, [p, eps])
+    vol = float(abs(torch.linalg.det(cell)))
+    return -gp, (ge / vol if need_stress else None), float(e.detach())
+
+
+def fcc(a=3.68, reps=2, jitter=0.02, seed=0):
+    base = np.array([[0, 0, 0], [0, .5, .5], [.5, 0, .5], [.5, .5, 0]])
+    cells = np.array([(i, j, k) for i in range(reps) for j in range(reps) for k in range(reps)], float)
+    frac = ((cells[:, None] + base[None]) / reps).reshape(-1, 3)
+    cell = np.eye(3) * a * reps
+    rng = np.random.default_rng(seed)
+    pos = frac @ cell + jitter * rng.normal(size=frac.shape)
+    return torch.tensor(pos), torch.tensor(cell)
+
+
+def make(kind, dt=1.0, T=300.0, pos_cell=None, seed=1, **kw):
+    pos, cell = pos_cell if pos_cell is not None else fcc()
+    n = pos.shape[0]
+    masses = torch.full((n,), 63.546, dtype=torch.float64)
+    rng = np.random.default_rng(seed)
+    v = rng.standard_normal((n, 3)) * np.sqrt(KB_EV * T / (63.546 * AMU_A2_FS2_EV))
+    v -= v.mean(0)
+    dyn = Dynamics(pos.clone(), torch.tensor(v), masses, cell.clone(), evaluate, kind, dt, T,
+                   kw.pop("taut", 20.0), **kw)
+    dyn._refresh()
+    return dyn
+
+
+def test_potential_forces_and_stress_by_finite_differences():
+    pos, cell = fcc(jitter=0.05)
+    f, s, e = evaluate(pos, cell, True)
+    h = 1e-5
+    for i, k in ((0, 0), (5, 2), (17, 1)):
+        pp, pm = pos.clone(), pos.clone()
+        pp[i, k] += h
+        pm[i, k] -= h
+        fd = -(pair_energy(pp, cell) - pair_energy(pm, cell)) / (2 * h)
+        assert abs(float(fd) - float(f[i, k])) < 1e-7
+    eye = torch.eye(3, dtype=torch.float64)
+    for a, b in ((0, 0), (1, 2)):
+        d = torch.zeros(3, 3, dtype=torch.float64)
+        d[a, b] = d[b, a] = h / 2 if a != b else h
+        ep = pair_energy(pos @ (eye + d), cell @ (eye + d))
+        em = pair_energy(pos @ (eye - d), cell @ (eye - d))
+        fd = (ep - em) / (2 * h) / float(torch.linalg.det(cell))
+        assert abs(float(fd) - float(s[a, b])) < 1e-8
+
+
+def _drift(dyn, steps):
+    h0 = dyn.conserved_energy()
+    hs = []
+    for _ in range(steps):
+        dyn.step()
+        hs.append(dyn.conserved_energy())
+    return max(abs(x - h0) for x in hs)
+
+
+def test_nve_conserves_energy():
+    dyn = make("nve", dt=1.0)
+    ke = []
+    h0 = dyn.conserved_energy()
+    for _ in range(200):
+        dyn.step()
+        ke.append(dyn.kinetic_energy())
+    assert abs(dyn.conserved_energy() - h0) < 0.02 * (max(ke) - min(ke))
+
+
+@pytest.mark.parametrize("kind", ["nvt_nose_hoover", "npt_nose_hoover"])
+def test_nose_hoover_conserves_extended_energy_to_dt2(kind):
+    kw = dict(taup=200.0, bulk_modulus_gpa=100.0, pressure_gpa=0.5) if kind.startswith("npt") else {}
+    d1 = _drift(make(kind, dt=1.0, T=600.0, **kw), 200)
+    d2 = _drift(make(kind, dt=0.5, T=600.0, **kw), 400)
+    dyn = make(kind, dt=1.0, T=600.0, **kw)
+    ke = []
+    for _ in range(200):
+        dyn.step()
+        ke.append(dyn.kinetic_energy())
+    assert d1 < 0.01 * (max(ke) - min(ke))
+    assert d2 < 0.5 * d1  # second order: ~4x smaller at half the step
+
+
+def test_nose_hoover_npt_keeps_com_and_upper_triangular_cell():
+    dyn = make("npt_nose_hoover", dt=1.0, T=300.0, taup=100.0, bulk_modulus_gpa=100.0, pressure_gpa=2.0)
+    com0 = (dyn.masses[:, None] * dyn.pos).sum(0) / dyn.masses.sum()
+    v0 = dyn.volume()
+    for _ in range(100):
+        dyn.step()
+    com = (dyn.masses[:, None] * dyn.pos).sum(0) / dyn.masses.sum()
+    assert torch.allclose(com, com0, atol=1e-9)
+    c = dyn.cell
+    assert float(c[1, 0]) == 0.0 and float(c[2, 0]) == 0.0 and float(c[2, 1]) == 0.0
+    assert dyn.volume() != v0  # the barostat acts
+
+
+def test_nose_hoover_nvt_thermalises():
+    dyn = make("nvt_nose_hoover", dt=2.0, T=500.0, taut=10.0)
+    dyn.vel *= 0.1  # start cold
+    temps = []
+    for _ in range(300):
+        dyn.step()
+        temps.append(dyn.temperature_now())
+    assert np.mean(temps[150:]) > 250.0
+
+
+def test_berendsen_nvt_heats_toward_target():
+    dyn = make("nvt_berendsen", dt=1.0, T=800.0, taut=10.0)
+    dyn.vel *= 0.3  # start cold
+    t0 = dyn.temperature_now()
+    for _ in range(60):
+        dyn.step()
+    assert dyn.temperature_now() > t0 + 150
+
+
+@pytest.mark.parametrize("kind", ["npt_berendsen", "npt_berendsen_inhom"])
+def test_berendsen_barostat_relaxes_pressure(kind):
+    """A compressed cell (positive pressure) expands toward P0 = 0; the isotropic barostat
+    keeps the cell shape, the inhomogeneous one scales each lattice vector by its own
+    factor (the angles stay)."""
+    pos, cell = fcc(a=3.55, jitter=0.0)
+    cell = cell @ torch.tensor([[1.0, 0.0, 0.0], [0.0, 1.03, 0.0], [0.0, 0.0, 0.98]], dtype=torch.float64)
+    pos = pos @ torch.tensor([[1.0, 0.0, 0.0], [0.0, 1.03, 0.0], [0.0, 0.0, 0.98]], dtype=torch.float64)
+    dyn = make(kind, dt=1.0, T=100.0, pos_cell=(pos, cell), taup=50.0, bulk_modulus_gpa=50.0, pressure_gpa=0.0)
+    p0 = -float(torch.trace(dyn.stress + dyn.ideal_gas_stress())) / 3
+    v0, cell0 = dyn.volume(), dyn.cell.clone()
+    for _ in range(80):
+        dyn.step()
+    p1 = -float(torch.trace(dyn.stress + dyn.ideal_gas_stress())) / 3
+    assert p0 > 0 and dyn.volume() > v0 and abs(p1) < 0.5 * abs(p0)
+    ratio = torch.linalg.norm(dyn.cell, dim=1) / torch.linalg.norm(cell0, dim=1)
+    if kind == "npt_berendsen":
+        assert torch.allclose(ratio, ratio[0].expand(3), rtol=1e-12)
+    else:
+        assert float(ratio.max() - ratio.min()) > 1e-4
+    cos = lambda c, i, j: float(c[i] @ c[j] / (torch.linalg.norm(c[i]) * torch.linalg.norm(c[j])))
+    for i, j in ((0, 1), (0, 2), (1, 2)):
+        assert abs(cos(dyn.cell, i, j) - cos(cell0, i, j)) < 1e-12
+
+
+def test_reference_ensemble_names():
+    assert _kind("NVE", "anything") == "nve"
+    assert _kind("nvt", "Berendsen_inhomogeneous") == "nvt_berendsen"
+    assert _kind("nvt", "Nose-Hoover") == "nvt_nose_hoover"
+    assert _kind("npt", "Nose-Hoover") == "npt_nose_hoover"
+    assert _kind("npt", "Berendsen_inhomogeneous") == "npt_berendsen_inhom"
+    assert _kind("npt", "NPT_Berendsen") == "npt_berendsen"
+    for ens, th in (("nvt", "langevin"), ("npt", "berendsen")):
+        with pytest.raises(ValueError, match="Thermostat not supported"):
+            _kind(ens, th)
+
+
+def test_upper_triangular_basis_keeps_cell_parameters():
+    rng = np.random.default_rng(5)
+    for _ in range(5):
+        cell = rng.normal(size=(3, 3)) + 4 * np.eye(3)
+        new = upper_triangular_basis(cell)
+        assert new[1, 0] == 0 and new[2, 0] == 0 and new[2, 1] == 0
+        assert np.allclose(np.linalg.norm(new, axis=1), np.linalg.norm(cell, axis=1))
+        gram = lambda c: (c @ c.T) / np.outer(np.linalg.norm(c, axis=1), np.linalg.norm(c, axis=1))
+        assert np.allclose(gram(new), gram(cell))
+        assert math.isclose(abs(np.linalg.det(new)), abs(np.linalg.det(cell)), rel_tol=1e-12)
