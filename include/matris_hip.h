@@ -31,6 +31,7 @@ extern "C" {
 #define MATRIS_E_IMAGES (-1003)    /* periodic image range beyond +-511           */
 #define MATRIS_E_UNPAIRED (-1004)  /* a directed edge has no reverse partner      */
 #define MATRIS_E_ORDER (-1005)     /* edges not in canonical (center, neighbor, image) order */
+#define MATRIS_E_SCRATCH (-1006)   /* the call needs more than the library's static scratch */
 
 /* Library version / build identification (for tests: "is the HIP path loaded"). */
 const char *matris_version(void);
@@ -125,6 +126,20 @@ int matris_csr_build(int64_t n_rows, const int32_t *keys, int64_t key_stride, in
 int matris_csr_build_deferred(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
                               int32_t *rowptr, int32_t *perm, void *workspace, size_t workspace_bytes,
                               void *stream);
+/* matris_csr_build_deferred that allocates nothing and takes no workspace: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.  Its
+ * workspace is a static device array of MATRIS_CSR_SCRATCH_BYTES per device, held from
+ * the library's first use on that device until the process ends; a call whose
+ * matris_csr_workspace_bytes(n_rows, nseg) exceeds it returns MATRIS_E_SCRATCH before any
+ * launch (48 MiB covers n_rows + n_segments up to about 12.5 M, e.g. the 9.0 M angles
+ * and 0.95 M bonds of a 32,000-atom cell).  Every call on one device shares that device's
+ * array: calls that overlap on one device (two streams, or two host threads) race, so
+ * callers order them on one stream.  Results, errors (MATRIS_STATUS_CSR_KEY) and launches
+ * are those of matris_csr_build_deferred. */
+#define MATRIS_CSR_SCRATCH_BYTES (48u << 20)
+int matris_csr_build_noalloc(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
+                             int32_t *rowptr, int32_t *perm, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Segmented reductions and gathers (row M3)

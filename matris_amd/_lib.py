@@ -27,6 +27,7 @@ ERRORS = {
     -1003: "MATRIS_E_IMAGES (periodic image range too large)",
     -1004: "MATRIS_E_UNPAIRED (directed edge without reverse partner)",
     -1005: "MATRIS_E_ORDER (edges not in canonical order)",
+    -1006: "MATRIS_E_SCRATCH (the call needs more than the static scratch array)",
 }
 
 _lock = threading.Lock()
@@ -84,6 +85,7 @@ _SIGS = {
     "matris_csr_workspace_bytes": (_SZ, [_I64, _I64]),
     "matris_csr_build": (_I, [_I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "matris_csr_build_deferred": (_I, [_I64, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "matris_csr_build_noalloc": (_I, [_I64, _P, _I64, _I64, _P, _P, _P]),
     "matris_seg_sum": (_I, [_P, _I64, _I64, _P, _P, _I64, _F, _I, _P, _P]),
     "matris_seg_sum2": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P, _P,
                              _P]),

@@ -9,6 +9,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.h"
 
 // ------------------------------------------------------------------------------------
@@ -929,5 +931,43 @@ extern "C" int matris_csr_build_deferred(int64_t n_rows, const int32_t *keys, in
     unsigned *status = matris_range_flag();
     if (!status) return MATRIS_E_ARG;
     return csr_build_launch(n_rows, keys, key_stride, nseg, rowptr, perm, workspace, workspace_bytes, status,
+                            (unsigned)MATRIS_STATUS_CSR_KEY, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------------
+// matris_csr_build_noalloc: matris_csr_build_deferred with its workspace carved from a
+// file-scope device array instead of a caller allocation.  Each device holds its own copy
+// of the array (MATRIS_CSR_SCRATCH_BYTES) from the library's first use on it until the
+// process ends; its address on a device is taken once, with that device current, and kept
+// per device.  Host code never passes the array's name to a kernel or a copy: on the host
+// it is a stand-in symbol, not a device address.
+// ------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[MATRIS_CSR_SCRATCH_BYTES];
+
+static void *csr_scratch_ptr() {
+    static std::mutex mu;
+    static void *ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
+
+extern "C" int matris_csr_build_noalloc(int64_t n_rows, const int32_t *keys, int64_t key_stride, int64_t nseg,
+                                        int32_t *rowptr, int32_t *perm, void *stream) {
+    if (n_rows < 0 || nseg <= 0) return MATRIS_E_ARG;
+    const size_t need = matris_csr_workspace_bytes(n_rows, nseg);
+    if (need > (size_t)MATRIS_CSR_SCRATCH_BYTES) return MATRIS_E_SCRATCH;
+    unsigned *status = matris_range_flag();
+    void *ws = csr_scratch_ptr();
+    if (!status || !ws) return MATRIS_E_ARG;
+    // csr_build_launch zero-fills what must start at zero (the counts) with a kernel on
+    // `stream`, so the previous call's contents never leak into this one.
+    return csr_build_launch(n_rows, keys, key_stride, nseg, rowptr, perm, ws, need, status,
                             (unsigned)MATRIS_STATUS_CSR_KEY, (hipStream_t)stream);
 }
