@@ -1,7 +1,7 @@
 """MatRIS efsm throughput on one MI355X (atom.steps/s), with live kernel roofline numbers
 and the CPU oracle timed on the host as a baseline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--c5-steps K5] [--no-c5] [--no-c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--c5-steps K5] [--no-c5] [--no-c2] [--no-c4]
 
 `value`: a step is one full efsm evaluation of MatRIS-10M (num_layers=10, random init,
 seed 0) on the C3 graph (864-atom fcc Cu): process_graphs, forward, torch.autograd.grad
@@ -13,6 +13,9 @@ region.
 tau 100 fs); every step rebuilds the radius and line graphs on the GPU from the new
 positions and evaluates efs (forces for the integrator); interaction blocks are
 checkpointed (the cell's activations exceed HBM otherwise).  A bounded number of steps.
+
+`c4_batch`: the 64 random triclinic cells of C4 (8-64 atoms each) as one disjoint batch,
+efsm, graphs built on the GPU once.
 
 `c2_line_attn`: the standalone line-attention core (forward, backward) and the
 angle->bond segment sum on the C2 graph (4096-atom random packing) with N(0,1) features,
@@ -61,9 +64,12 @@ def _parse():
     ap.add_argument("--c5-warmup", type=int, default=2)
     ap.add_argument("--no-c5", action="store_true")
     ap.add_argument("--no-c2", action="store_true")
+    ap.add_argument("--no-c4", action="store_true")
     ap.add_argument("--c5-only", action="store_true", help="run only the C5 MD line (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-reps", type=int, default=3, help="fcc reps of the CPU baseline sample")
+    ap.add_argument("--cpu-sample-reps", type=int, default=6,
+                    help="fcc reps of the CPU baseline sample (6: the C3 cell itself)")
+    ap.add_argument("--cpu-steps", type=int, default=2, help="timed CPU baseline steps (after one warm-up)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (HBM counter calibration)")
     return ap.parse_args()
@@ -89,6 +95,39 @@ def _gmlp_flops(M, K):
     """One fused GatedMLP forward (or backward, input gradients only):
     [M,K]x[K,256] plus two [M,128]x[128,128]."""
     return 2.0 * M * (K * 256 + 2 * 128 * 128)
+
+
+# HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the
+# 512 MiB copy calibration: x2.0 and x1.0) for the kernels the roofline fields describe,
+# at C3 and at C2 (profiles/c3_efsm_hbm_traffic.md, profiles/c2_line_attn_hbm_traffic.md).
+# Keys: (launch name, config); a mean over that family's launches in one step where the
+# shapes differ.
+TRAFFIC_BYTES = {}
+
+
+def c4_batch(model, dev, steps: int, warmup: int):
+    """Config C4: 64 random triclinic cells of 8-64 atoms (Z 1..94, seed 3) evaluated as one
+    disjoint batch (efsm); graphs built on the GPU once, resident before the timed region."""
+    import torch
+
+    from matris_amd import workloads as W
+
+    cells = W.c4_batch64()
+    graphs = [model.graph_converter(c) for c in cells]
+    n = sum(len(c) for c in cells)
+    for _ in range(warmup):
+        model(graphs, task="efsm")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model(graphs, task="efsm")
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return dict(metric="atom*steps/s (efsm of one disjoint batch of 64 cells)", value=round(n * steps / dt, 2),
+                unit="atom*steps/s", steps=steps, warmup=warmup, ms_per_step=round(dt / steps * 1e3, 3),
+                config={"workload": "C4: 64 random triclinic cells, 8-64 atoms, Z 1..94 (seed 3), one batch",
+                        "n_atoms": n, "n_directed": sum(int(g.atom_graph.shape[0]) for g in graphs),
+                        "n_angles": sum(int(g.line_graph.shape[0]) for g in graphs)})
 
 
 def _events_time(fn, reps):
@@ -191,12 +230,12 @@ def c5_md(model, dev, steps: int, warmup: int):
                 "block_checkpoint": f"auto ({n_ck} of {len(model.interaction_block)} blocks)"})
 
 
-def cpu_baseline(reps: int):
+def cpu_baseline(reps: int, steps: int):
     """The CPU oracle (oracle/model_ref.py, a plain fp32 torch restatement of the
-    reference forward + autograd) on the host cores, on a bounded sample of the C3
-    workload: an fcc Cu reps^3 conventional supercell with the same lattice constant and
-    thermal displacements (same per-atom environment as C3), one warm-up step then timed
-    steps.  Returns atom.steps/s and the thread count used."""
+    reference forward + autograd) on the host cores: the C3 cell itself at reps = 6 (a
+    smaller fcc Cu reps^3 supercell with the same lattice constant and displacements
+    otherwise), one warm-up step then `steps` timed steps.  Returns atom.steps/s and the
+    thread count used (16: the GPU box's host share)."""
     import torch
 
     from matris_amd import workloads as W
@@ -220,12 +259,9 @@ def cpu_baseline(reps: int):
     model = MatRISRef(**MATRIS_10M).eval()
     model([g], task="efsm")
     t0 = time.perf_counter()
-    n = 0
-    while True:
+    for n in range(1, steps + 1):
         model([g], task="efsm")
-        n += 1
-        if time.perf_counter() - t0 > 10.0 or n >= 5:
-            break
+        print(f"cpu baseline: step {n} of {steps} done", file=sys.stderr, flush=True)
     dt = time.perf_counter() - t0
     return dict(value=round(len(cr) * n / dt, 3), unit="atom*steps/s", cores=threads, kind="port",
                 sample=f"oracle/model_ref.py efsm (fp32 torch CPU) on fcc Cu {reps}x{reps}x{reps} "
@@ -311,19 +347,34 @@ def main():
     mode_idx, mma_peak, peak_note, dtype = MMA_ROOF[ops.get_mma_precision()]
 
     def gmlp_roof(name):
+        """The GatedMLP family against the roofline that binds it: its algorithmic FLOPs per
+        algorithmic byte lie below the machine balance (split-MFMA peak / HBM peak), so
+        the bound is HBM and `achieved` is bytes per second; the MFMA figures ride along."""
         gm = stats.get(name)
         if not gm:
             return None
-        flops = sum(_gmlp_flops(m, k) for m, k in gm["info"]) / gm["n"]
+        flops = sum(_gmlp_flops(m, k) for m, k, _ in gm["info"]) / gm["n"]
+        byts = sum(b for _, _, b in gm["info"]) / gm["n"]
         tf = flops / gm["mean_s"] / 1e12
-        n_line = sum(1 for (m, k) in gm["info"] if m == A)
-        return dict(kernel=f"{name}_kernel<{mode_idx}>", bound="mfma", achieved=round(tf, 2), peak=round(mma_peak, 1),
-                    unit="TFLOP/s", frac=round(tf / mma_peak, 4), traffic=None,
-                    flops_per_launch=round(flops), mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
-                    frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-                    note=f"algorithmic fp32 FLOPs (2*M*(256K+32768)) per launch, K = the layer-1 width the kernel "
-                         f"multiplies (sources projected before their gather by gmlp_proj excluded), mean over "
-                         f"{gm['n']} launches in {args.steps} steps ({n_line} with M=A={A}); peak = {peak_note}")
+        gbs = byts / gm["mean_s"] / 1e9
+        n_line = sum(1 for (m, _, _) in gm["info"] if m == A)
+        intensity, balance = flops / byts, mma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
+        traffic = TRAFFIC_BYTES.get((name, "C3"))
+        common = dict(kernel=f"{name}_kernel<{mode_idx}>", mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
+                      flops_per_launch=round(flops), bytes_per_launch=round(byts),
+                      flop_per_byte=round(intensity, 1), machine_balance_flop_per_byte=round(balance, 1),
+                      mfma_achieved_tflops=round(tf, 2), mfma_peak_tflops=round(mma_peak, 1),
+                      mfma_frac=round(tf / mma_peak, 4), frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                      note=f"means over {gm['n']} launches in {args.steps} steps ({n_line} with M=A={A}); "
+                           f"bytes: every input table read once (gathered sources as whole tables, projected "
+                           f"sources as their product tables), outputs, saved p/z and gradients written once; "
+                           f"FLOPs 2*M*(256K+32768) with K the layer-1 width the kernel multiplies; MFMA peak = "
+                           f"{peak_note}")
+        if intensity < balance:
+            return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=round(gbs / HBM_PEAK_GBS, 4), traffic=traffic, **common)
+        return dict(bound="mfma", achieved=round(tf, 2), peak=round(mma_peak, 1), unit="TFLOP/s",
+                    frac=round(tf / mma_peak, 4), traffic=traffic, **common)
     r_f, r_b = gmlp_roof("gmlp_fwd"), gmlp_roof("gmlp_bwd")
     tot = {k: v["mean_s"] * v["n"] for k, v in stats.items()}
     roof = r_b if tot.get("gmlp_bwd", 0) >= tot.get("gmlp_fwd", 0) else r_f
@@ -333,7 +384,8 @@ def main():
         byts = _attn_line_bytes(A, E_u)
         gbs = byts / at["mean_s"] / 1e9
         attn = dict(kernel="attn_fwd_kernel<false>", bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS,
-                    unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None, bytes_per_launch=byts,
+                    unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4), traffic=TRAFFIC_BYTES.get(("attn_fwd_line", "C3")),
+                    bytes_per_launch=byts,
                     mean_us=round(at["mean_s"] * 1e6, 2), launches=at["n"])
     kern = {k: dict(launches=v["n"], mean_us=round(v["mean_s"] * 1e6, 2),
                     total_ms_per_step=round(v["mean_s"] * v["n"] * 1e3 / n_brk, 3)) for k, v in stats_all.items()}
@@ -364,13 +416,15 @@ def main():
                         f"events",
         "e_per_atom": float(out["e"].item()),
     }
+    if not args.no_c4:
+        line["c4_batch"] = c4_batch(model, dev, max(3, args.steps // 2), 2)
     if not args.no_c2:
         line["c2_line_attn"] = c2_line_attn(dev)
     if not args.no_c5:
         line["c5_md"] = c5_md(model, dev, args.c5_steps, args.c5_warmup)
     if not args.no_cpu_baseline:
         try:
-            line["cpu_baseline"] = cpu_baseline(args.cpu_sample_reps)
+            line["cpu_baseline"] = cpu_baseline(args.cpu_sample_reps, args.cpu_steps)
         except Exception as exc:  # report, never fake
             line["cpu_baseline"] = dict(error=repr(exc))
     print(json.dumps(line), flush=True)

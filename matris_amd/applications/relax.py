@@ -16,6 +16,7 @@ from __future__ import annotations
 import contextlib
 import io
 import sys
+import warnings
 
 import numpy as np
 
@@ -141,6 +142,23 @@ class CellFilterDOF:
         return np.vstack([f, np.linalg.solve(self.F, virial.T).T / self.c])
 
 
+# Cell filters whose stationary point (zero forces, stress equal to -scalar_pressure) the
+# native deformation-gradient coordinates reach; ASE's StrainFilter keeps the atoms fixed.
+NATIVE_CELL_FILTERS = ("UnitCellFilter", "FrechetCellFilter", "ExpCellFilter")
+
+
+def _ase_filter_class(ase_filter, filter_classes):
+    """relax.py:88-98: a Filter subclass of ase.filters by name (ValueError for other
+    names), or a class passed as is."""
+    if not isinstance(ase_filter, str):
+        return ase_filter
+    import inspect
+    valid = [n for n, c in inspect.getmembers(filter_classes, inspect.isclass) if issubclass(c, filter_classes.Filter)]
+    if ase_filter not in valid:
+        raise ValueError(f"Invalid ase_filter={ase_filter!r}, must be one of {valid}. ")
+    return getattr(filter_classes, ase_filter)
+
+
 class StructOptimizer:
     """Structure optimiser with the reference's constructor (relax.py:23-52)."""
 
@@ -163,9 +181,7 @@ class StructOptimizer:
             have_ase = True
         except ImportError:
             have_ase = False
-        structure_in = None
         if hasattr(atoms, "frac_coords") and hasattr(atoms, "lattice"):  # pymatgen Structure
-            structure_in = atoms
             if have_ase:
                 from pymatgen.io.ase import AseAtomsAdaptor
                 atoms = AseAtomsAdaptor().get_atoms(atoms)
@@ -177,9 +193,10 @@ class StructOptimizer:
         stream = sys.stdout if verbose else io.StringIO()
         if have_ase and not isinstance(atoms, SimpleAtoms):
             import ase.filters as filter_classes
+            filter_cls = _ase_filter_class(ase_filter, filter_classes)
             opt_cls = getattr(ase_optimize, self.optimizer) if isinstance(self.optimizer, str) else self.optimizer
             with contextlib.redirect_stdout(stream):
-                target = getattr(filter_classes, ase_filter)(atoms) if relax_cell else atoms
+                target = filter_cls(atoms) if relax_cell else atoms
                 opt = opt_cls(target, **kwargs)
                 opt.attach(obs, interval=loginterval)
                 opt.run(fmax=fmax, steps=steps)
@@ -187,16 +204,30 @@ class StructOptimizer:
         else:
             if self.optimizer != "FIRE":
                 raise NotImplementedError("without ASE this build relaxes with FIRE only (optimizer='FIRE')")
+            name = ase_filter if isinstance(ase_filter, str) else getattr(ase_filter, "__name__", str(ase_filter))
+            if relax_cell and name not in NATIVE_CELL_FILTERS:
+                raise ValueError(f"Invalid ase_filter={name!r}, must be one of {list(NATIVE_CELL_FILTERS)} "
+                                 "(without ASE the cell relaxes through the native deformation-gradient filter)")
+            if relax_cell and name != "UnitCellFilter":
+                warnings.warn(f"without ASE, ase_filter={name!r} relaxes the cell through UnitCellFilter's "
+                              "deformation-gradient coordinates (same stationary point, different path)",
+                              RuntimeWarning, stacklevel=2)
             with contextlib.redirect_stdout(stream):
                 target = CellFilterDOF(atoms, kwargs.pop("scalar_pressure", 0.0)) if relax_cell else atoms
                 fire_relax(target, fmax=fmax, steps=steps, observer=obs, loginterval=loginterval, **kwargs)
                 obs()
         if save_path is not None:
             obs.save(save_path)
-        final = atoms
-        if structure_in is not None and have_ase:
-            from pymatgen.io.ase import AseAtomsAdaptor
-            final = AseAtomsAdaptor.get_structure(atoms)
-            if assign_magmoms and atoms.get_magnetic_moments() is not None:
-                final.add_site_property("magmom", [float(m) for m in atoms.get_magnetic_moments()])
+        final = atoms  # without pymatgen and ASE: the relaxed atoms object itself
+        if have_ase and not isinstance(atoms, SimpleAtoms):
+            try:  # relax.py:137-146: always a pymatgen Structure when pymatgen is there
+                from pymatgen.io.ase import AseAtomsAdaptor
+            except ImportError:
+                AseAtomsAdaptor = None
+            if AseAtomsAdaptor is not None:
+                final = AseAtomsAdaptor.get_structure(atoms)
+                if assign_magmoms and atoms.get_magnetic_moments() is not None:
+                    for key in list(final.site_properties):
+                        final.remove_site_property(property_name=key)
+                    final.add_site_property("magmom", [float(m) for m in atoms.get_magnetic_moments()])
         return {"final_structure": final, "trajectory": obs}

@@ -519,6 +519,19 @@ def _projected_sources(srcs, idxs, n_rows: int):
     return [j for j, (s, i) in enumerate(zip(srcs, idxs)) if i is not None and r * s.shape[0] <= n_rows][:3]
 
 
+def _gmlp_fwd_bytes(srcs, idxs, n_rows: int, saved: bool, res: bool, proj_tables=()) -> int:
+    """Algorithmic HBM bytes of one GatedMLP forward launch: every input table read once
+    (a gathered source's whole table, not its gathered rows; a projected source's product
+    table), one int32 index per row and gathered source, out written once, p and z when
+    saved, the residual source read and the residual output written."""
+    b = 0
+    for s, i in zip(srcs, idxs):
+        b += 4 * D * (s.shape[0] if i is not None else n_rows) + (4 * n_rows if i is not None else 0)
+    for rows, cols, n_idx in proj_tables:
+        b += 4 * rows * cols + 4 * n_rows * n_idx
+    return b + 4 * D * n_rows + (2 * 4 * 256 * n_rows if saved else 0) + (2 * 4 * D * n_rows if res else 0)
+
+
 def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, save: bool = True):
     """matris_gmlp_fwd; srcs are [*,128] fp32 tensors, idxs int32 gather keys or None.
     res = (res_src, res_w) also returns res_out = out + res_w * res_src.
@@ -539,7 +552,8 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     if not proj:
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
-        with _timed("gmlp_fwd", (n_rows, nsrc * D)):
+        with _timed("gmlp_fwd", (n_rows, nsrc * D, _gmlp_fwd_bytes(srcs, idxs, n_rows, p is not None,
+                                                                    res is not None))):
             _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
                                            _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
                                            _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
@@ -570,7 +584,10 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     pji_arr = (ctypes.c_void_p * 3)(*p_idx)
     pld_arr = (ctypes.c_int64 * 3)(*p_ld)
     w1 = _p(pack.b_blocks(tuple(rest), mode)) if rest else None
-    with _timed("gmlp_fwd", (n_rows, len(rest) * D)):  # the layer-1 width this kernel multiplies
+    ptab = [(keep[k].shape[0], keep[k].shape[1], len(b)) for k, b in enumerate(tables.values())]
+    nbytes = _gmlp_fwd_bytes([srcs[j] for j in rest], [idxs[j] for j in rest], n_rows, p is not None,
+                             res is not None, ptab)
+    with _timed("gmlp_fwd", (n_rows, len(rest) * D, nbytes)):  # K: the layer-1 width this kernel multiplies
         _lib.check(lib.matris_gmlp_fwd_proj(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr, w1,
                                             _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
                                             _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),
@@ -587,7 +604,9 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
     M = p.shape[0]
     if g_x is None and not (g_x0 is not None and K == D):
         g_x = torch.empty(M, K - (D if g_x0 is not None else 0), device=g.device)
-    with _timed("gmlp_bwd", (M, K)):
+    # algorithmic bytes: g_out, p, z (and the accumulated source-0 block) read once, g_x written once
+    nbytes = 4 * M * (D + 2 * 256 + (D if (g_x0 is not None and acc0) else 0) + K)
+    with _timed("gmlp_bwd", (M, K, nbytes)):
         _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)),
                                        _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w),
                                        mode, _stream()), "matris_gmlp_bwd")

@@ -74,3 +74,22 @@ def test_fire_reports_failure_within_budget():
     at.calc = _Harmonic(np.array([[50.0, 0.0, 0.0]]), np.array([1.0, 1.0, 1.0]))
     assert not fire_relax(at, fmax=1e-6, steps=3)
     assert at.calc.calls == 4  # initial evaluation + one per step
+
+
+def test_native_relax_validates_the_cell_filter_name():
+    """relax.py:88-98 refuses unknown filter names; without ASE the native cell DOF runs
+    for the UnitCellFilter-type names and warns for the other two (same stationary point)."""
+    import pytest
+
+    from matris_amd.applications import relax as R
+
+    class _Calc:
+        pass
+
+    opt = R.StructOptimizer.__new__(R.StructOptimizer)
+    opt.optimizer, opt.calculator = "FIRE", _Calc()
+    a = SimpleAtoms.from_fractional([[0, 0, 0]], [[3.0, 0, 0], [0, 3.0, 0], [0, 0, 3.0]], [29])
+    with pytest.raises(ValueError, match="Invalid ase_filter"):
+        opt.relax(a, ase_filter="StrainFilter", verbose=False)
+    with pytest.raises(ValueError, match="Invalid ase_filter"):
+        opt.relax(a, ase_filter="NoSuchFilter", verbose=False)

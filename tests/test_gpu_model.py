@@ -319,3 +319,76 @@ def test_c4_batch64_graphs_and_efsm_vs_reference_golden(golden):
     again = _efsm(model, graphs)  # no float atomics on the path: bitwise reproducible
     for k in "efsm":
         assert np.array_equal(out[k], again[k]), k
+
+
+def test_stress_is_the_strain_derivative_of_the_energy_with_the_graph_fixed():
+    """V tr(s) against central differences of E under isotropic and shear strain of a
+    jittered 32-atom Cu cell, on the device in fp32, with the graph (edge and angle sets)
+    held fixed as in the autograd derivative.  Rebuilding the graph at each strained cell
+    instead can add or drop an edge at the 6 A cutoff: the envelope takes its basis to zero
+    there, but the attention softmax over a centre's edges has no such weight, so the
+    energy jumps, and such a difference can be far from the stress."""
+    from matris_amd import workloads as W
+    from matris_amd.graph import RadiusGraph
+    model = _model()
+    cr = W.fcc_supercell(3.61, 2, sigma=0.08, seed=3)
+    g = model.graph_converter(cr)
+    out = model([g], task="efs")
+    s = out["s"][0].detach().double().cpu().numpy() / 160.21766208  # eV/A^3
+    lat = np.asarray(cr.lattice)
+    vol, n = abs(np.linalg.det(lat)), len(cr)
+
+    def energy(eps, rebuild=False):
+        new = lat @ (np.eye(3) + eps)
+        if rebuild:
+            gg = model.graph_converter(W.Crystal(cr.frac, new, cr.z))
+        else:
+            gg = RadiusGraph(**{**g.to_dict(), "lattice": torch.as_tensor(new, dtype=torch.float32, device="cuda")})
+        return float(model([gg], task="e")["e"][0]) * n, (len(gg.atom_graph), len(gg.line_graph))
+
+    h = 1e-3
+    for eps, pred in ((np.eye(3) * h, vol * np.trace(s) * h),
+                      (np.array([[0, h, 0], [h, 0, 0], [0, 0, 0.0]]), vol * 2 * s[0, 1] * h)):
+        (ep, _), (em, _) = energy(eps), energy(-eps)
+        fd = (ep - em) / 2
+        print(f"fixed-graph strain difference {fd:.6e} eV, stress prediction {pred:.6e} eV", flush=True)
+        assert abs(fd - pred) <= 2e-3 * abs(pred) + 2e-6
+    (_, a_plus), (_, a_minus) = energy(np.eye(3) * h, True), energy(-np.eye(3) * h, True)
+    print(f"(edges, angles) at +/-0.1% isotropic strain with the graph rebuilt: {a_plus} / {a_minus} "
+          f"(fixed: {(len(g.atom_graph), len(g.line_graph))})", flush=True)
+
+
+@pytest.mark.parametrize("scale", [1e-4, pytest.param(10.0, marks=pytest.mark.xfail(strict=True, reason=(
+    "f16x3 gradient operands below the fp16 normal range lose bits (per-row scaling pending)"))),
+    pytest.param(100.0, marks=pytest.mark.xfail(strict=True, reason="as for 10")),
+    pytest.param(1e3, marks=pytest.mark.xfail(strict=True, reason="as for 10"))])
+def test_f16x3_matches_fp32_mfma_across_activation_scales(golden, scale):
+    """The initial atom, bond and angle features scaled by 1e-4 (small values, where the
+    fp16 hi part of the activation split loses bits) and by 1e3 (large values, near or
+    past the fp16 range, where the evaluation falls back to bf16x6): the default f16x3
+    arithmetic against plain fp32 MFMA products on the batched triclinic cells."""
+    import warnings
+    from matris_amd.model import ops
+    z = golden("cells_small.npz")
+    model = _model()
+    with torch.no_grad():
+        model.atom_embedding.embedding.weight.mul_(scale)
+        model.edge_embedding.swish_layer.linear.weight.mul_(scale)
+        model.three_body_embedding.swish_layer.linear.weight.mul_(scale)
+    graphs = [_graph_from_arrays(z, f"g{i}_") for i in range(int(z["n_cells"]))]
+    with ops.mma_precision("fp32"):
+        ref = _efsm(model, graphs)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        with ops.mma_precision("f16x3"):
+            out = _efsm(model, graphs)
+    fell_back = any("fp16 range" in str(w.message) for w in caught)
+    e_rel = np.max(np.abs(out["e"] - ref["e"]) / np.abs(ref["e"]))
+    f_rel = np.max(np.abs(out["f"] - ref["f"])) / np.max(np.abs(ref["f"]))
+    s_rel = np.max(np.abs(out["s"] - ref["s"])) / np.max(np.abs(ref["s"]))
+    m_rel = np.max(np.abs(out["m"] - ref["m"])) / np.max(np.abs(ref["m"]))
+    print(f"scale {scale:g}: bf16x6 fallback={fell_back} e_rel={e_rel:.2e} f_rel={f_rel:.2e} s_rel={s_rel:.2e} "
+          f"m_rel={m_rel:.2e}", flush=True)
+    for k in "efsm":
+        assert np.all(np.isfinite(out[k])), k
+    assert e_rel <= 1e-5 and f_rel <= 1e-4 and s_rel <= 1e-4 and m_rel <= 1e-4
