@@ -325,6 +325,27 @@ __device__ __forceinline__ void store_acc_rows(const v16f (&acc)[2][NCT], float 
             }
 }
 
+// MODE 2: multiply accumulator rows (layout of store_acc_rows: element i of lane half h is
+// row rt*32 + 8 (i/4) + 4h + i%4) by their rows' factors, four rows per 16-byte LDS read.
+template <int MODE, int NCT>
+__device__ __forceinline__ void unscale_acc_rows(v16f (&a)[2][NCT], const float *rinv, int h) {
+    if constexpr (MODE == 2) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 r = *reinterpret_cast<const float4 *>(rinv + rt * 32 + 8 * q + 4 * h);
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) {
+                    a[rt][ct][4 * q] *= r.x;
+                    a[rt][ct][4 * q + 1] *= r.y;
+                    a[rt][ct][4 * q + 2] *= r.z;
+                    a[rt][ct][4 * q + 3] *= r.w;
+                }
+            }
+    }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, const float *__restrict__ g_out,
                                                           const float *__restrict__ P, const float *__restrict__ Z,
@@ -336,6 +357,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                                           int acc0, const float *__restrict__ res_w,
                                                           unsigned *range_flag) {
     __shared__ __align__(16) float G[BM * LDH];
+    __shared__ __align__(16) float rinv[BM];  // MODE 2: 2^-k w1s for each row (g_z / g_p scaled by 2^k)
     // Two-plane modes keep g_z, then g_p, in G pre-split into fragment units
     // [rt 2][kb 16][plane 2][64 lanes] (64 KB, converted once by their writer); MODE 6
     // keeps fp32 rows and converts at each fragment read.
@@ -410,6 +432,16 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                 vg[e4] = make_float4((gng[4 * e4] - ng[4 * e4] * dg) * rg, (gng[4 * e4 + 1] - ng[4 * e4 + 1] * dg) * rg,
                                      (gng[4 * e4 + 2] - ng[4 * e4 + 2] * dg) * rg,
                                      (gng[4 * e4 + 3] - ng[4 * e4 + 3] * dg) * rg);
+            }
+            if constexpr (MODE == 2) {  // the row's g_z (and later g_p) scaled by 2^k
+                const float m = abs_max4(abs_max4(abs_max4(abs_max4(0.f, vc[0]), vc[1]), vg[0]), vg[1]);
+                const RowScale rs = row_scale(row16_max(m));
+#pragma unroll
+                for (int e4 = 0; e4 < 2; ++e4) {
+                    vc[e4] = mul4(vc[e4], rs.s);
+                    vg[e4] = mul4(vg[e4], rs.s);
+                }
+                if ((lane & 15) == 0) rinv[row] = rs.inv * w1s;  // phase 3's weight scale folded in
             }
             if constexpr (PS) {
                 // g_z columns c (= 4c' and 64 + 4c', core; + 128, gate) of this row: half
@@ -518,7 +550,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             gemm_frag_packed<MODE, 2, 1, 256 / 16>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
         else
             amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
-        scale_acc<MODE>(a2, w1s);
+        if constexpr (MODE == 2)
+            unscale_acc_rows<MODE, 1>(a2, rinv, h);  // 2^-k w1s per row
+        else
+            scale_acc<MODE>(a2, w1s);
         if (cb > 0 || !epi0) store_acc_rows<1>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {  // K == 128: every wave holds source-0 columns
             __syncthreads();
@@ -533,7 +568,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             gemm_frag_packed<MODE, 2, 2, 256 / 16>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
         else
             amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 2, 256 / 16>(a2, G, LDH, W1t, col0 / 32, 256 / 16, 0, lane));
-        scale_acc<MODE>(a2, w1s);
+        if constexpr (MODE == 2)
+            unscale_acc_rows<MODE, 2>(a2, rinv, h);  // 2^-k w1s per row
+        else
+            scale_acc<MODE>(a2, w1s);
         if (col0 >= MATRIS_D || !epi0) store_acc_rows<2>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {
             __syncthreads();  // all waves are done reading G

@@ -69,36 +69,96 @@ __device__ __forceinline__ void store_tile128_scaled(const float *tile, float *_
     }
 }
 
-// Stage rows m0 .. m0+63 of a [*, 128] array into LDS pre-split into fragment units
-// [rt 2][kb 8][plane 2][64 lanes] (two-plane modes; zeros past M): thread (row tid/4,
-// 8-column groups q, q+4, q+8, q+12 for q = tid%4), each value converted once.  With
-// g_res, also writes g_res = res_w * rows (the FFN backward's residual gradient).
-template <int MODE>
-__device__ __forceinline__ float stage_frag128(uint4 *buf, const float *__restrict__ src, int64_t m0, int64_t M,
-                                               int tid, float amax, float *__restrict__ g_res = nullptr,
-                                               const float *__restrict__ res_w = nullptr) {
+// A thread's share of rows m0 .. m0+63 of a [*, 128] array: row tid/4, 8-column groups
+// q, q+4, q+8, q+12 for q = tid%4 (zeros past M).
+struct Rows128 {
+    float4 u[4], v[4];
+};
+__device__ __forceinline__ void load_rows128(Rows128 &x, const float *__restrict__ src, int64_t m0, int64_t M,
+                                             int tid) {
     const int r = tid >> 2, q = tid & 3;
     const bool in = m0 + r < M;
     const float4 *p = reinterpret_cast<const float4 *>(src + (m0 + r) * MATRIS_D);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int g = q + 4 * i;
-        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
-        if (in) {
-            u = p[2 * g];
-            v = p[2 * g + 1];
-            if (g_res) {
-                const float4 wu = *reinterpret_cast<const float4 *>(res_w + 8 * g);
-                const float4 wv = *reinterpret_cast<const float4 *>(res_w + 8 * g + 4);
-                float4 *o = reinterpret_cast<float4 *>(g_res + (m0 + r) * MATRIS_D + 8 * g);
-                o[0] = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
-                o[1] = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
-            }
-        }
+        x.u[i] = in ? p[2 * g] : make_float4(0.f, 0.f, 0.f, 0.f);
+        x.v[i] = in ? p[2 * g + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// max |x| over the row (the 4 threads that hold it)
+__device__ __forceinline__ float rows128_absmax(const Rows128 &x) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = abs_max4(abs_max4(m, x.u[i]), x.v[i]);
+    return group4_max(m);
+}
+
+// g_res = res_w * rows (the FFN backward's residual gradient), rows below M
+__device__ __forceinline__ void store_res128(const Rows128 &x, float *__restrict__ g_res,
+                                             const float *__restrict__ res_w, int64_t m0, int64_t M, int tid) {
+    const int r = tid >> 2, q = tid & 3;
+    if (m0 + r >= M) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = q + 4 * i;
+        const float4 wu = *reinterpret_cast<const float4 *>(res_w + 8 * g);
+        const float4 wv = *reinterpret_cast<const float4 *>(res_w + 8 * g + 4);
+        float4 *o = reinterpret_cast<float4 *>(g_res + (m0 + r) * MATRIS_D + 8 * g);
+        o[0] = make_float4(wu.x * x.u[i].x, wu.y * x.u[i].y, wu.z * x.u[i].z, wu.w * x.u[i].w);
+        o[1] = make_float4(wv.x * x.v[i].x, wv.y * x.v[i].y, wv.z * x.v[i].z, wv.w * x.v[i].w);
+    }
+}
+
+// Stage the rows, times s, into LDS pre-split into fragment units [rt 2][kb 8][plane 2][64
+// lanes] (two-plane modes), each value converted once.
+template <int MODE>
+__device__ __forceinline__ float stage_rows128(uint4 *buf, const Rows128 &x, int tid, float amax, float s = 1.f) {
+    const int r = tid >> 2, q = tid & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = q + 4 * i;
+        const float4 u = s == 1.f ? x.u[i] : mul4(x.u[i], s), v = s == 1.f ? x.v[i] : mul4(x.v[i], s);
         amax = frag_amax<MODE>(amax, u, v);
         frag_put8<MODE>(buf, (r >> 5) * 8 + (g >> 1), (r & 31) + 32 * (g & 1), u, v);
     }
     return amax;
+}
+
+template <int MODE>
+__device__ __forceinline__ float stage_frag128(uint4 *buf, const float *__restrict__ src, int64_t m0, int64_t M,
+                                               int tid, float amax) {
+    Rows128 x;
+    load_rows128(x, src, m0, M, tid);
+    return stage_rows128<MODE>(buf, x, tid, amax);
+}
+
+// MODE 2: the row scale of a gradient tile (2^k, recorded as 2^-k in rinv by one of the
+// row's threads); 1 in the other modes.
+// MODE 2: multiply transposed accumulators (rows in lanes: row rt*32 + l32) by their rows'
+// 2^-k.
+template <int MODE, int NCT>
+__device__ __forceinline__ void unscale_rows_t(v16f (&acc)[2][NCT], const float *rinv, int l32) {
+    if constexpr (MODE == 2) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const float r = rinv[rt * 32 + l32];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) acc[rt][ct] *= r;
+        }
+    }
+}
+
+template <int MODE>
+__device__ __forceinline__ float tile_row_scale(float row_absmax, float *rinv, int tid) {
+    if constexpr (MODE == 2) {
+        const RowScale rs = row_scale(row_absmax);
+        if ((tid & 3) == 0) rinv[tid >> 2] = rs.inv;
+        return rs.s;
+    } else {
+        return 1.f;
+    }
 }
 
 // ------------------------------------------------------------------------------------
@@ -223,6 +283,19 @@ __device__ __forceinline__ float stage_rows4(uint4 *buf, const float4 (&xr)[4], 
         buf[(unit * 2 + 1) * 64 + fl] = f.p[1];
     }
     return amax;
+}
+
+// MODE 2: scale the thread's share of its row (load_rows4 layout: 8 threads per row) by the
+// row's 2^k (row_scale) and record 2^-k in rinv[row].
+template <int MODE>
+__device__ __forceinline__ void scale_rows4(float4 (&xr)[4], float *rinv, int tid) {
+    if constexpr (MODE == 2) {
+        const float m = abs_max4(abs_max4(abs_max4(abs_max4(0.f, xr[0]), xr[1]), xr[2]), xr[3]);
+        const RowScale rs = row_scale(group8_max(m));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[i] = mul4(xr[i], rs.s);
+        if ((tid & 7) == 0) rinv[tid >> 3] = rs.inv;
+    }
 }
 
 // FFN forward, weight-stationary: 512 threads = 8 waves; wave w owns output columns
@@ -350,6 +423,7 @@ __global__ __launch_bounds__(512, 1) void ffn_bwd_ws_kernel(int64_t M, const flo
     static_assert(Npl<MODE>::v == 2, "two-plane modes only");
     __shared__ uint4 Xf[2 * 8 * 2 * 64];  // g tile as fragment planes (32 KB)
     __shared__ uint4 Hf[2 * 8 * 2 * 64];  // g_p tile, the same layout
+    __shared__ float rinv[BM];            // MODE 2: 2^-k of each row's g / g_p scaling
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
     const int ct = wave & 3, rt = wave >> 2;
     const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
@@ -375,8 +449,10 @@ __global__ __launch_bounds__(512, 1) void ffn_bwd_ws_kernel(int64_t M, const flo
                     make_float4(rw.x * xr[i].x, rw.y * xr[i].y, rw.z * xr[i].z, rw.w * xr[i].w);
             }
         }
+        scale_rows4<MODE>(xr, rinv, tid);
         amax = stage_rows4<MODE>(Xf, xr, tid, amax);
         __syncthreads();  // g staged; every wave is past the previous tile's second GEMM
+        const float ri = MODE == 2 ? rinv[rt * 32 + l32] : 1.f;  // read before the next tile's staging
         load_rows4(xr, g, min(tile + (int64_t)gridDim.x, ntiles - 1) * BM, M, tid);  // next tile
         v16f acc;
 #pragma unroll
@@ -400,10 +476,11 @@ __global__ __launch_bounds__(512, 1) void ffn_bwd_ws_kernel(int64_t M, const flo
         for (int i = 0; i < 16; ++i) acc[i] = 0.f;
         gemm_res<MODE>(acc, w1, Hf, rt, lane);
         if (row < M) {
+            const float sc = w1s * ri;  // both powers of two
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 *reinterpret_cast<float4 *>(g_x + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) =
-                    make_float4(acc[4 * j] * w1s, acc[4 * j + 1] * w1s, acc[4 * j + 2] * w1s, acc[4 * j + 3] * w1s);
+                    make_float4(acc[4 * j] * sc, acc[4 * j + 1] * sc, acc[4 * j + 2] * sc, acc[4 * j + 3] * sc);
         }
     }
     report_range<MODE>(amax, range_flag);
@@ -518,6 +595,7 @@ __global__ __launch_bounds__(512, 1) void tb_embed_bwd_kernel(int64_t M, const f
     __shared__ uint4 Uf[2 * 8 * 2 * 64];    // u, then g_z, as fragment units (32 KB)
     __shared__ __align__(16) float Wa[TB_WA_LDS];
     __shared__ float part[4][BM][TB_K + 1];  // g_b partial sums per column block (17 KB)
+    __shared__ float pmax[4][BM];            // MODE 2: per column block, max |g_z| of each row
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
     const int ct = wave & 3, rt = wave >> 2;
     const float ss = take_wscale<MODE>(Ws), sst = take_wscale<MODE>(Wst);
@@ -550,11 +628,24 @@ __global__ __launch_bounds__(512, 1) void tb_embed_bwd_kernel(int64_t M, const f
                                      : make_float4(0.f, 0.f, 0.f, 0.f);
             gz[j] = make_float4(g.x * dsilu_f(acc[4 * j] * ss), g.y * dsilu_f(acc[4 * j + 1] * ss),
                                 g.z * dsilu_f(acc[4 * j + 2] * ss), g.w * dsilu_f(acc[4 * j + 3] * ss));
-            amax = frag_amax<MODE>(amax, gz[j], gz[j]);
         }
-        __syncthreads();  // every wave is done reading u
+        if constexpr (MODE == 2) {  // the row's maximum over its four column blocks, through LDS
+            float m = abs_max4(abs_max4(abs_max4(abs_max4(0.f, gz[0]), gz[1]), gz[2]), gz[3]);
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            if (h == 0) pmax[ct][rt * 32 + l32] = m;
+        }
+        __syncthreads();  // every wave is done reading u (and the row maxima are complete)
+        RowScale rs = {1.f, 1.f};
+        if constexpr (MODE == 2) {
+            const int r = rt * 32 + l32;
+            rs = row_scale(fmaxf(fmaxf(pmax[0][r], pmax[1][r]), fmaxf(pmax[2][r], pmax[3][r])));
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) frag_put4<MODE>(Uf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, gz[j]);
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (MODE == 2) gz[j] = mul4(gz[j], rs.s);
+            amax = frag_amax<MODE>(amax, gz[j], gz[j]);
+            frag_put4<MODE>(Uf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, gz[j]);
+        }
         __syncthreads();  // g_z complete
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[i] = 0.f;
@@ -565,7 +656,7 @@ __global__ __launch_bounds__(512, 1) void tb_embed_bwd_kernel(int64_t M, const f
         for (int k = 0; k < TB_K; ++k) gb[k] = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float gu = acc[i] * sst;
+            const float gu = acc[i] * (sst * rs.inv);
             const float *wr = Wa + tb_wa_row(ct * 32 + 8 * (i >> 2) + 4 * h + (i & 3));
 #pragma unroll
             for (int k = 0; k < TB_K; ++k) gb[k] = fmaf(wr[k], gu, gb[k]);
@@ -598,6 +689,7 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
                                                          float *__restrict__ g_res, const float *__restrict__ res_w,
                                                          unsigned *range_flag) {
     __shared__ __align__(16) float T[BM * LDT];
+    __shared__ float rinv[BM];  // MODE 2: 2^-k of each row's g / g_p scaling
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
@@ -609,7 +701,11 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
     zero_acc(acc);
     float amax = 0.f;
     if constexpr (PS) {
-        amax = stage_frag128<MODE>(Tf, g, m0, M, tid, amax, g_res, res_w);
+        Rows128 gx;
+        load_rows128(gx, g, m0, M, tid);
+        if (g_res) store_res128(gx, g_res, res_w, m0, M, tid);
+        const float sr = tile_row_scale<MODE>(MODE == 2 ? rows128_absmax(gx) : 0.f, rinv, tid);
+        amax = stage_rows128<MODE>(Tf, gx, tid, amax, sr);
         __syncthreads();
         gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W2t, wave, MATRIS_D / 16, 0,
                                                           lane);
@@ -660,6 +756,7 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
                      gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W1t, wave, MATRIS_D / 16, 0, lane));
     }
     scale_acc<MODE>(acc, w1s);
+    unscale_rows_t<MODE, 1>(acc, rinv, l32);
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
@@ -720,6 +817,7 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
     // Wt = W^T ([128, 256]) packed: g_x[m][k] = sum_n g[m][n] Wt[k][n], k-blocks 0..7
     // pair with g0, 8..15 with g1; g0 then g1 pass through the one LDS tile
     __shared__ __align__(16) float T[BM * LDT];
+    __shared__ float rinv[BM];  // MODE 2: 2^-k of each row's common g0 / g1 scaling
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const float ws = take_wscale<MODE>(Wt);
@@ -728,11 +826,17 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
     float amax = 0.f;
     if constexpr (Npl<MODE>::v == 2) {  // g0, then g1, pre-split into fragment units in T
         uint4 *Tf = reinterpret_cast<uint4 *>(T);
-        amax = stage_frag128<MODE>(Tf, g0, m0, M, tid, amax);
+        Rows128 x0, x1;
+        load_rows128(x0, g0, m0, M, tid);
+        load_rows128(x1, g1, m0, M, tid);
+        // one scale per row for both halves: they accumulate into the same sums
+        const float sr = tile_row_scale<MODE>(MODE == 2 ? fmaxf(rows128_absmax(x0), rows128_absmax(x1)) : 0.f,
+                                              rinv, tid);
+        amax = stage_rows128<MODE>(Tf, x0, tid, amax, sr);
         __syncthreads();
         gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, Wt, wave, 256 / 16, 0, lane);
         __syncthreads();
-        amax = stage_frag128<MODE>(Tf, g1, m0, M, tid, amax);
+        amax = stage_rows128<MODE>(Tf, x1, tid, amax, sr);
         __syncthreads();
         gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, Wt, wave, 256 / 16,
                                                           MATRIS_D / 16, lane);
@@ -747,6 +851,7 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
                                                                             MATRIS_D / 16, lane));
     }
     scale_acc<MODE>(acc, ws);  // both halves share the one weight scale
+    unscale_rows_t<MODE, 1>(acc, rinv, lane & 31);
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();

@@ -58,6 +58,38 @@ struct Frag {
 // fp16 overflow threshold of the MODE 2 activation split.
 #define MATRIS_F16_MAX 65504.0f
 
+// Per-row power-of-two scaling of MODE 2 gradient operands.  fp16's exponent range keeps
+// ~22 bits of an activation only inside [2^-14, 2^16); the backward GEMMs' operands are
+// gradients whose rows can sit far below it (the RMSNorm Jacobian divides by the row's
+// norm, so large features mean small gradients).  Their producers therefore scale each
+// row by 2^k with max |row| 2^k in [2^10, 2^11) -- five bits of headroom for what the row
+// becomes downstream -- and the consumers multiply that row's accumulators by 2^-k.  Both
+// factors are powers of two, so a row already inside the range gives the same products.
+// k is clamped to [-100, 100]; a zero or non-finite maximum leaves the row unscaled.
+struct RowScale {
+    float s, inv;
+};
+__device__ __forceinline__ RowScale row_scale(float m) {
+    if (!(m > 0.f) || m == INFINITY) return {1.f, 1.f};
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xffu) - 127;  // floor(log2 m); -127 if subnormal
+    const int k = max(-100, min(100, 10 - e));
+    return {__uint_as_float((uint32_t)(127 + k) << 23), __uint_as_float((uint32_t)(127 - k) << 23)};
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+    return fmaxf(x, dpp_f<CTRL>(x));
+}
+// max over lanes 4q .. 4q+3, over lanes 8q .. 8q+7, over a DPP row of 16 lanes
+__device__ __forceinline__ float group4_max(float v) { return dpp_max<0x4E>(dpp_max<0xB1>(v)); }
+__device__ __forceinline__ float group8_max(float v) { return dpp_max<0x141>(group4_max(v)); }
+__device__ __forceinline__ float row16_max(float v) { return dpp_max<0x140>(group8_max(v)); }
+
+__device__ __forceinline__ float abs_max4(float m, const float4 &v) {
+    return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+}
+__device__ __forceinline__ float4 mul4(const float4 &v, float s) { return make_float4(v.x * s, v.y * s, v.z * s, v.w * s); }
+
 template <class To, class From>
 __device__ __forceinline__ To bitcast(const From &x) {
     static_assert(sizeof(To) == sizeof(From), "size");

@@ -418,11 +418,30 @@ def test_pack_b_fragment_layout():
 
 @pytest.mark.parametrize("kind", ["gmlp", "ffn", "pair"])
 def test_f16x3_range_flag(kind):
-    """An activation beyond the fp16 range sets the device's range flag in every f16x3
-    kernel family (forward and backward); values inside the range leave it clear."""
+    """A forward activation beyond the fp16 range sets the device's range flag in every
+    f16x3 kernel family; values inside the range leave it clear.  The backward kernels scale
+    each gradient row by a power of two first (mma.h row_scale), so a gradient row with an
+    element of 2e5 or one of 1e-9 is carried at full precision without the flag: its input
+    gradient matches the plain fp32 MFMA mode's."""
     ops = _ops()
     torch.manual_seed(11)
     M = 200
+    w1, w2 = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
+    ref = _TorchGMLP(128)
+    shim = _ShimGated(ref).to(DEV)
+
+    def run(x, g=None):
+        xd = x.clone().requires_grad_(True)
+        if kind == "gmlp":
+            out = ops.gated_mlp(shim, ops.GmlpPack(), [(xd, None)])
+        elif kind == "ffn":
+            out = ops.ffn(ops._WeightPack().get(w1, w2), xd)
+        else:
+            out = ops.proj_pair(ops._WeightPack().get(w1, w2), xd)[0]
+        if g is not None:
+            out.backward(g)
+        return out, xd.grad
+
     ops.set_mma_precision("f16x3")
     try:
         assert not ops.f16_range_take()
@@ -430,22 +449,19 @@ def test_f16x3_range_flag(kind):
             x = torch.randn(M, 128, device=DEV)
             if big:
                 x[77, 5] = 1.0e5
-            xd = x.requires_grad_(True)
-            if kind == "gmlp":
-                ref = _TorchGMLP(128)
-                out = ops.gated_mlp(_ShimGated(ref).to(DEV), ops.GmlpPack(), [(xd, None)])
-            elif kind == "ffn":
-                w1, w2 = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
-                out = ops.ffn(ops._WeightPack().get(w1, w2), xd)
-            else:
-                ws, wt = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
-                out = ops.proj_pair(ops._WeightPack().get(ws, wt), xd)[0]
+            run(x)
             assert ops.f16_range_take() == big, ("forward", big)
-            g = torch.randn(M, 128, device=DEV)
-            if big:  # a gradient beyond the range, through the backward kernels alone
-                g[3, 9] = -2.0e5
-            out.backward(g)
-            assert ops.f16_range_take() == big, ("backward", big)
+        x = torch.randn(M, 128, device=DEV)
+        g = torch.randn(M, 128, device=DEV)
+        g[3, 9] = -2.0e5   # a row far above the fp16 range
+        g[40] *= 1e-9      # a row far below its normal range
+        _, gx = run(x, g)
+        assert not ops.f16_range_take(), "backward"
+        with ops.mma_precision("fp32"):
+            _, gx32 = run(x, g)
+        for r in (3, 40, 100):
+            err = ((gx[r] - gx32[r]).abs().max() / gx32[r].abs().max()).item()
+            assert err < 1e-5, (r, err)
     finally:
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
