@@ -206,8 +206,9 @@ int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const int32_t *t_pt
  *   alpha_t / alpha_s: logits, row r at (alpha_idx ? alpha_idx[r] : r) * lda;
  *   e [R,128]; target CSR (t_ptr, t_perm|NULL), source CSR (s_ptr, s_perm|NULL),
  *   both over n_seg segments.
- * fwd writes y_t, y_s [n_seg,128] and the per-segment log-sum-exp lse_t, lse_s
- * [n_seg,128] needed by the backward.
+ * fwd writes y_t, y_s [n_seg,128] (zero rows for empty segments) and the per-segment
+ * log-sum-exp lse_t, lse_s [n_seg,128] needed by the backward (rows of empty segments,
+ * which no row of the backward reads, are left unwritten).
  * lda (and ldgy) are multiples of 4 (16-byte aligned rows).
  * bwd (input gradients only): given g_yt, g_ys (rows of stride ldgy >= 128), writes
  * g_alpha_t, g_alpha_s [R,128] (per row r, before any alpha_idx reduction) and

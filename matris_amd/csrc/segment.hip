@@ -28,8 +28,9 @@ __device__ __forceinline__ float4 mul4(const float4 &a, const float4 &b) {
     return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
 }
 
-// Partial sum of the rows i = start, start + stride, ... < end of one CSR segment, four
-// rows in flight (16-byte lanes, xc = row base + column offset of the lane).  MUL: row r
+// Partial sum of the rows i = start, start + stride, ... < end of one CSR segment, eight
+// (then four, then one) rows in flight (16-byte lanes, xc = row base + column offset of
+// the lane); the adds run in row order whatever the chunking.  MUL: row r
 // contributes x[r] * mc[midx ? midx[r] : r] (mc = a [*, 128] table + the lane's column;
 // the product first, as the reference's h * w before its index_add_).
 template <bool MUL>
@@ -38,6 +39,22 @@ __device__ __forceinline__ float4 seg_rows(const float *__restrict__ xc, int64_t
                                            const float *__restrict__ mc = nullptr,
                                            const int32_t *__restrict__ midx = nullptr) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (; i + 7 * stride < end; i += 8 * stride) {  // eight rows in flight
+        int64_t r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = perm ? perm[i + k * stride] : i + k * stride;
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = ld4(xc + r[k] * ldx);
+        if constexpr (MUL) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = mul4(v[k], ld4(mc + (midx ? (int64_t)midx[r[k]] : r[k]) * MATRIS_D));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            acc.x += v[k].x; acc.y += v[k].y; acc.z += v[k].z; acc.w += v[k].w;
+        }
+    }
     for (; i + 3 * stride < end; i += 4 * stride) {
         const int64_t r0 = perm ? perm[i] : i, r1 = perm ? perm[i + stride] : i + stride;
         const int64_t r2 = perm ? perm[i + 2 * stride] : i + 2 * stride;
@@ -378,9 +395,11 @@ extern "C" int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const in
 // ------------------------------------------------------------------------------------
 // segment attention forward: one wave per (segment, side).  Each half-wave owns every
 // other row of the segment with 16-byte lanes (4 columns) and runs an online softmax
-// taken four of its rows at a time: the running maximum moves once per chunk (one
-// rescale exponential), then one exponential per row, all on v_exp_f32 (exp_neg_f).
-// The two halves' (max, sum, weighted sum) states merge at the end.
+// taken eight of its rows at a time (sixteen rows of loads in flight per wave), then four,
+// then one: the running maximum moves once per chunk (one rescale exponential), then
+// one exponential per row, all on v_exp_f32 (exp_neg_f).  The two halves' (max, sum,
+// weighted sum) states merge at the end.  An empty segment writes y = 0 and no log-sum-exp
+// (the backward reads the statistics of non-empty segments only).
 // ------------------------------------------------------------------------------------
 struct OnlineSoftmax4 {
     float4 m, s, acc;
@@ -438,11 +457,30 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(int64_t n_seg, const floa
     const float *alpha = (src_side ? alpha_s : alpha_t) + c;
     const float *ec = e + c;
     const int b = ptr[seg], end = ptr[seg + 1];
+    float *yo = (src_side ? y_s : y_t) + seg * MATRIS_D + c;
+    if (end <= b) {
+        if (half == 0) st4(yo, make_float4(0.f, 0.f, 0.f, 0.f));
+        return;
+    }
     auto row = [&](int i) -> int64_t { return perm ? perm[i] : i; };
     auto arow = [&](int64_t r) -> int64_t { return HAS_AIDX ? (int64_t)aidx[r] : r; };
     OnlineSoftmax4 st;
     st.init();
     int i = b + half;  // this half's rows: i, i + 2, i + 4, ...
+    for (; i + 14 < end; i += 16) {
+        int64_t r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = row(i + 2 * k);
+        float4 x[8], ev[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            x[k] = ld4(alpha + arow(r[k]) * lda);
+            ev[k] = ld4(ec + r[k] * MATRIS_D);
+        }
+        st.raise(max4(st.m, max4(max4(max4(x[0], x[1]), max4(x[2], x[3])), max4(max4(x[4], x[5]), max4(x[6], x[7])))));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) st.add(x[k], ev[k]);
+    }
     for (; i + 6 < end; i += 8) {
         const int64_t r0 = row(i), r1 = row(i + 2), r2 = row(i + 4), r3 = row(i + 6);
         const float4 x0 = ld4(alpha + arow(r0) * lda), x1 = ld4(alpha + arow(r1) * lda);
@@ -461,10 +499,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(int64_t n_seg, const floa
         st.raise(max4(st.m, x0));
         st.add(x0, e0);
     }
-    // merge the other half's state (lane ^ 32 holds the same columns)
+    // merge the other half's state (lane ^ 32 holds the same columns); a half with no rows
+    // (a one-row segment) has m = -inf and contributes nothing
     const float4 om = shfl_xor4(st.m, 32), os = shfl_xor4(st.s, 32), oa = shfl_xor4(st.acc, 32);
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f), l = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (end > b) {
+    float4 y, l;
 #define OS_MERGE(k)                                                                       \
     {                                                                                     \
         const float mm = fmaxf(st.m.k, om.k);                                             \
@@ -474,11 +512,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(int64_t n_seg, const floa
         y.k = (st.acc.k * c0 + oa.k * c1) / ss;                                           \
         l.k = mm + logf(ss);                                                              \
     }
-        OS_MERGE(x) OS_MERGE(y) OS_MERGE(z) OS_MERGE(w)
+    OS_MERGE(x) OS_MERGE(y) OS_MERGE(z) OS_MERGE(w)
 #undef OS_MERGE
-    }
     if (half == 0) {
-        st4((src_side ? y_s : y_t) + seg * MATRIS_D + c, y);
+        st4(yo, y);
         st4((src_side ? lse_s : lse_t) + seg * MATRIS_D + c, l);
     }
 }
