@@ -99,10 +99,17 @@ def _gmlp_flops(M, K):
 
 # HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the
 # 512 MiB copy calibration: x2.0 and x1.0) for the kernels the roofline fields describe,
-# at C3 and at C2 (profiles/c3_efsm_hbm_traffic.md, profiles/c2_line_attn_hbm_traffic.md).
+# at C3 and at C2 (profiles/c3_efsm_hbm_traffic.md, which lists both).
 # Keys: (launch name, config); a mean over that family's launches in one step where the
 # shapes differ.
-TRAFFIC_BYTES = {}
+TRAFFIC_BYTES = {
+    ("gmlp_bwd", "C3"): 569.2e6,       # all four launch shapes, 420 launches; 1334.3 MB at M = A
+    ("gmlp_fwd", "C3"): 476.8e6,       # all four launch shapes, 420 launches; 1106.0 MB at M = A
+    ("attn_fwd_line", "C3"): 580.4e6,  # 538.0 read + 42.5 written
+    ("attn_fwd", "C2"): 4062.1e6,
+    ("attn_bwd", "C2"): 8431.5e6,
+    ("seg_sum", "C2"): 1048.1e6,
+}
 
 
 def c4_batch(model, dev, steps: int, warmup: int):
@@ -176,17 +183,18 @@ def c2_line_attn(dev, reps: int = 20):
     b_b = 4 * D * (6 * A + 2 * U) + 4 * A + 8 * (U + 1)
     b_s = 4 * D * (A + U) + 4 * A + 4 * (U + 1)
 
-    def row(name, byts, t):
+    def row(name, byts, t, key):
         gbs = byts / t / 1e9
         return dict(kernel=name, bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(gbs / HBM_PEAK_GBS, 4), bytes_per_launch=byts, mean_us=round(t * 1e6, 2))
+                    frac=round(gbs / HBM_PEAK_GBS, 4), traffic=TRAFFIC_BYTES.get((key, "C2")),
+                    bytes_per_launch=byts, mean_us=round(t * 1e6, 2))
 
     return dict(workload="C2: 4096-atom random packing (rho 0.085, d_min 1.8, seed 1)", n_angles=A,
                 n_undirected=U,
-                fwd=row("attn_fwd_kernel<false>", b_f, t_f),
-                bwd=row("attn_bwd_kernel<false>", b_b, t_b) | dict(
+                fwd=row("attn_fwd_kernel<false>", b_f, t_f, "attn_fwd"),
+                bwd=row("attn_bwd_kernel<false>", b_b, t_b, "attn_bwd") | dict(
                     extra_stat_bytes=4 * D * 4 * U, extra_stat_note="y_t, y_s, lse_t, lse_s gathered per row"),
-                seg_sum=row("seg_sum_kernel", b_s, t_s))
+                seg_sum=row("seg_sum_kernel", b_s, t_s, "seg_sum"))
 
 
 def c5_md(model, dev, steps: int, warmup: int):
