@@ -214,7 +214,12 @@ def c5_md(model, dev, steps: int, warmup: int):
     torch.cuda.synchronize()
     md.timings = {"graph": 0.0, "model": 0.0}
     t0 = time.perf_counter()
-    md.run(steps)
+    done = 0
+    while done < steps:  # progress lines for long runs (each MD step ends in a stream sync anyway)
+        k = min(20, steps - done)
+        md.run(k)
+        done += k
+        print(f"c5 md: {done} of {steps} steps", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     res = md.results

@@ -56,7 +56,7 @@ def checkpoint_needed(n_angles: int, n_edges: int, n_blocks: int, device=None, t
 
 
 def _zeros_if_none(g, like):
-    return torch.zeros_like(like) if g is None else ops._f32c(g)
+    return ops._rows(like.shape[0], like.shape[1], like.device).zero_() if g is None else ops._f32c(g)
 
 
 def _ffn_fusable(mlp) -> bool:
@@ -140,7 +140,7 @@ class _LineAttention(torch.autograd.Function):
         g_bond_new = _zeros_if_none(g_bond_new, y_t)
         g_tb_new = _zeros_if_none(g_tb_new, e)
         # node update: g_bond = r_n g + dGatedMLP_n/dbond, g_y = [g_yt | g_ys]
-        g_bond = torch.empty(E, D, device=e.device)
+        g_bond = ops._rows(E, D, e.device)
         g_y = ops.gmlp_bwd_raw(pn, g_bond_new, p_n, z_n, 3 * D, mode, g_x0=g_bond, acc0=False, res_w=r_n)
         del p_n, z_n
         # attention: g_e = g_tb_new (residual branch) + attention term
@@ -216,9 +216,9 @@ class _LineRefinement(torch.autograd.Function):
         E, A = env.shape[0], h.shape[0]
         g_bond_new = _zeros_if_none(g_bond_new, env)
         g_tb_new = _zeros_if_none(g_tb_new, h)
-        g_bond = torch.empty(E, D, device=h.device)
+        g_bond = ops._rows(E, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
-        g_tb = torch.empty(A, D, device=h.device)
+        g_tb = ops._rows(A, D, h.device)
         g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, g_res=g_tb, res_w=r_e)
         del p_de
         g_env = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h, accumulate=True)
@@ -299,7 +299,7 @@ class _AtomAttention(torch.autograd.Function):
         g_atom_new = _zeros_if_none(g_atom_new, y_t)
         g_bond_new = _zeros_if_none(g_bond_new, a_s)
         # node update: g_atom = r_n g + d GatedMLP_n / d atom; g_y = [g_yt | g_ys]
-        g_atom = torch.empty(N, D, device=e.device)
+        g_atom = ops._rows(N, D, e.device)
         g_y = ops.gmlp_bwd_raw(pn, g_atom_new, p_n, z_n, 3 * D, mode, g_x0=g_atom, acc0=False, res_w=r_n)
         del p_n, z_n
         # e: half of the bond gradient of each directed copy, plus the attention term
@@ -370,8 +370,8 @@ class _AtomRefinement(torch.autograd.Function):
         r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
         N = p_dn.shape[0]
         g_atom_new = _zeros_if_none(g_atom_new, p_dn)
-        g_bond_new = _zeros_if_none(g_bond_new, torch.empty(d2u.n_seg, D, device=h.device))
-        g_atom = torch.empty(N, D, device=h.device)
+        g_bond_new = _zeros_if_none(g_bond_new, ops._rows(d2u.n_seg, D, h.device))
+        g_atom = ops._rows(N, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_atom_new, p_dn, mode, g_res=g_atom, res_w=r_n)
         g_te = ops.ffn_bwd_raw(pm, ops.gather_raw(g_bond_new, d2u.key, 0.5), p_de, mode)
         del p_dn, p_de

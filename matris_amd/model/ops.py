@@ -102,6 +102,21 @@ class _timed:
             _TIMING.setdefault(self.name, []).append((self.ev[0], self.ev[1], self.info))
 
 
+def _rows(n: int, cols: int, device, dtype=torch.float32) -> torch.Tensor:
+    """An uninitialised [n, cols] tensor whose storage is rounded up to a coarse row count:
+    the first n rows of a [cap(n), cols] allocation, cap(n) = n below 2^16 rows, else n
+    rounded up to a multiple of 2^(floor(log2 n) - 5) (at most 3% more).  A molecular-
+    dynamics run rebuilds its graph every step with slightly different counts; with exact
+    sizes the caching allocator's blocks end up a little too small for the next step's
+    tensors and, for a large cell, the pool fills with unusable pieces.  Quantised sizes
+    let each step reuse the previous step's blocks."""
+    if n >= (1 << 16):
+        g = 1 << (n.bit_length() - 6)
+        cap = (n + g - 1) // g * g
+        return torch.empty(cap, cols, dtype=dtype, device=device)[:n]
+    return torch.empty(n, cols, dtype=dtype, device=device)
+
+
 def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
@@ -150,9 +165,9 @@ class Grouping:
         dev = key.device
         rowptr = torch.empty(n_seg + 1, dtype=torch.int32, device=dev)
         # sorted keys: row pointers only (a descent is reported like an out-of-range key)
-        perm = None if sorted_rows else torch.empty(max(R, 1), dtype=torch.int32, device=dev)
+        perm = None if sorted_rows else _rows(max(R, 1), 1, dev, torch.int32).view(-1)
         ws_bytes = lib.matris_csr_workspace_bytes(R, n_seg)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ws = _rows(ws_bytes, 1, dev, torch.uint8).view(-1)
         fn = lib.matris_csr_build_deferred if deferred else lib.matris_csr_build
         _lib.check(fn(R, _p(key), 1, n_seg, _p(rowptr), _p(perm), _p(ws), ws_bytes, _stream()), "matris_csr_build")
         return Grouping(key, rowptr, None if sorted_rows else perm[:R], n_seg)
@@ -169,7 +184,7 @@ def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D
     w [128]) also + w * feat (a residual term)."""
     lib = _lib.load()
     if out is None:
-        out = torch.empty(grp.n_seg, D, dtype=torch.float32, device=x.device)
+        out = _rows(grp.n_seg, D, x.device)
     rows = grp.n_rows
     if second is not None:
         x2, g2, s2, ld2, off2 = second
@@ -189,7 +204,7 @@ def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D
 
 def gather_raw(src: torch.Tensor, idx: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
     lib = _lib.load()
-    out = torch.empty(idx.numel(), D, dtype=torch.float32, device=src.device)
+    out = _rows(idx.numel(), D, src.device)
     _lib.check(lib.matris_gather_rows(_p(src), _p(idx), idx.numel(), scale, 0, _p(out), _stream()),
                "matris_gather_rows")
     return out
@@ -200,7 +215,7 @@ def seg_sum_mul_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: 
     """out (+)= segment sums over grp of x[r] * mul[mul_idx[r]] (matris_seg_sum_mul)."""
     lib = _lib.load()
     if out is None:
-        out = torch.empty(grp.n_seg, D, dtype=torch.float32, device=x.device)
+        out = _rows(grp.n_seg, D, x.device)
     with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
         _lib.check(lib.matris_seg_sum_mul(grp.n_seg, grp.n_rows, _p(x), D, 0, _p(grp.rowptr), _p(grp.perm), _p(mul),
                                           _p(mul_idx), 1.0, int(accumulate), _p(out), _stream()),
@@ -292,8 +307,8 @@ def attn_fwd_raw(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: G
     lib = _lib.load()
     R, S = e.shape[0], tgt.n_seg
     dev = e.device
-    y_t, y_s = torch.empty(S, D, device=dev), torch.empty(S, D, device=dev)
-    lse_t, lse_s = torch.empty(S, D, device=dev), torch.empty(S, D, device=dev)
+    y_t, y_s = _rows(S, D, dev), _rows(S, D, dev)
+    lse_t, lse_s = _rows(S, D, dev), _rows(S, D, dev)
     aidx = alpha_grp.key if alpha_grp is not None else None
     with _timed("attn_fwd_atom" if aidx is not None else "attn_fwd_line", (R, S, src.perm is not None)):
         _lib.check(lib.matris_attn_fwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(aidx), _p(e), _p(tgt.rowptr),
@@ -309,7 +324,7 @@ def attn_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: G
     lib = _lib.load()
     R, S = e.shape[0], tgt.n_seg
     dev = e.device
-    g_at, g_as, g_e = (torch.empty(R, D, device=dev) for _ in range(3))
+    g_at, g_as, g_e = (_rows(R, D, dev) for _ in range(3))
     ag = alpha_grp
     with _timed("attn_bwd_atom" if ag is not None else "attn_bwd_line", (R, S)):
         _lib.check(lib.matris_attn_bwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(ag.key if ag is not None else None),
@@ -356,7 +371,7 @@ def env_agg_fwd_raw(h, env, tgt: Grouping, src: Grouping):
     h[a] * env[source(a)]  (interaction_block.py:243-258)."""
     lib = _lib.load()
     E = env.shape[0]
-    agg, S = torch.empty(E, D, device=h.device), torch.empty(E, D, device=h.device)
+    agg, S = _rows(E, D, h.device), _rows(E, D, h.device)
     with _timed("env_agg_fwd", (h.shape[0], E)):
         _lib.check(lib.matris_env_agg_fwd(E, _p(h), _p(env), _p(tgt.rowptr), _p(tgt.perm), _p(src.key), _p(S),
                                           _p(agg), _stream()), "matris_env_agg_fwd")
@@ -367,7 +382,7 @@ def env_agg_bwd_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, g_h, accumul
     """g_h (+)= g_agg[tgt] * env[tgt] * env[src]; returns g_env."""
     lib = _lib.load()
     E = env.shape[0]
-    g_env = torch.empty(E, D, device=h.device)
+    g_env = _rows(E, D, h.device)
     with _timed("env_agg_bwd", (h.shape[0], E)):
         _lib.check(lib.matris_env_agg_bwd(h.shape[0], E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key), _p(src.key),
                                           _p(src.rowptr), _p(src.perm), int(accumulate), _p(g_h), _p(g_env),
@@ -540,10 +555,10 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     lib = _lib.load()
     dev = srcs[0].device
     nsrc = len(srcs)
-    out = torch.empty(n_rows, D, device=dev)
-    p = torch.empty(n_rows, 256, device=dev) if save else None
-    z = torch.empty(n_rows, 256, device=dev) if save else None
-    res_out = torch.empty(n_rows, D, device=dev) if res is not None else None
+    out = _rows(n_rows, D, dev)
+    p = _rows(n_rows, 256, dev) if save else None
+    z = _rows(n_rows, 256, dev) if save else None
+    res_out = _rows(n_rows, D, dev) if res is not None else None
     rs, rw = (res if res is not None else (None, None))
     proj = _projected_sources(srcs, idxs, n_rows)
     ret_p, ret_z = p, z
@@ -567,7 +582,7 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     for blocks in tables.values():
         x = srcs[blocks[0]]
         nb = len(blocks)
-        P = torch.empty(x.shape[0], 256 * nb, device=dev)
+        P = _rows(x.shape[0], 256 * nb, dev)
         keep.append(P)
         with _timed("gmlp_proj", (x.shape[0], nb)):
             _lib.check(lib.matris_gmlp_project(x.shape[0], _p(x), _p(pack.b_stack(tuple(blocks), mode)), nb, _p(P),
@@ -603,7 +618,7 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
     lib = _lib.load()
     M = p.shape[0]
     if g_x is None and not (g_x0 is not None and K == D):
-        g_x = torch.empty(M, K - (D if g_x0 is not None else 0), device=g.device)
+        g_x = _rows(M, K - (D if g_x0 is not None else 0), g.device)
     # algorithmic bytes: g_out, p, z (and the accumulated source-0 block) read once, g_x written once
     nbytes = 4 * M * (D + 2 * 256 + (D if (g_x0 is not None and acc0) else 0) + K)
     with _timed("gmlp_bwd", (M, K, nbytes)):
@@ -639,7 +654,7 @@ class _GatedMLP(torch.autograd.Function):
             elif grp is None:
                 grads.append(g_x[:, j * D:(j + 1) * D])
             else:
-                out = torch.empty(ctx.src_rows[j], D, device=g.device)
+                out = _rows(ctx.src_rows[j], D, g.device)
                 seg_sum_raw(g_x, grp, 1.0, ldx=K, col_off=j * D, out=out)
                 grads.append(out)
         return (None, None, None, *grads)
@@ -680,8 +695,8 @@ def ffn_fwd_raw(pack: _WeightPack, x, mode: int, res=None, save: bool = True):
     p (the saved pre-activation) is None when not saved."""
     lib = _lib.load()
     M = x.shape[0]
-    out = torch.empty(M, D, device=x.device)
-    p = torch.empty(M, D, device=x.device) if save else None
+    out = _rows(M, D, x.device)
+    p = _rows(M, D, x.device) if save else None
     rs, rw = (res if res is not None else (None, None))
     kp = None if _DISCARD["on"] else p  # discarded saves: a placeholder, not written
     with _timed("ffn_fwd", (M,)):
@@ -694,7 +709,7 @@ def ffn_bwd_raw(pack: _WeightPack, g, p, mode: int, g_res=None, res_w=None):
     """g_x of matris_ffn_bwd; g_res (given) receives res_w * g."""
     lib = _lib.load()
     M = p.shape[0]
-    g_x = torch.empty(M, D, device=g.device)
+    g_x = _rows(M, D, g.device)
     with _timed("ffn_bwd", (M,)):
         _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(pack.b("wt0", mode)), _p(pack.b("wt1", mode)), _p(g_x),
                                       _p(g_res), _p(res_w), mode, _stream()), "matris_ffn_bwd")
@@ -705,7 +720,7 @@ def pair_fwd_raw(pack: _WeightPack, x, mode: int):
     """(x W0^T, x W1^T) of matris_pair_fwd."""
     lib = _lib.load()
     M = x.shape[0]
-    o0, o1 = torch.empty(M, D, device=x.device), torch.empty(M, D, device=x.device)
+    o0, o1 = _rows(M, D, x.device), _rows(M, D, x.device)
     with _timed("pair_fwd", (M,)):
         _lib.check(lib.matris_pair_fwd(M, _p(x), _p(pack.b("cat", mode)), _p(o0), _p(o1), mode, _stream()),
                    "matris_pair_fwd")
@@ -716,7 +731,7 @@ def pair_bwd_raw(pack: _WeightPack, g0, g1, mode: int, res=None, res_w=None):
     """g0 W0 + g1 W1 (+ res_w * res) of matris_pair_bwd."""
     lib = _lib.load()
     M = g0.shape[0]
-    g_x = torch.empty(M, D, device=g0.device)
+    g_x = _rows(M, D, g0.device)
     with _timed("pair_bwd", (M,)):
         _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(pack.b("cat_t", mode)), _p(g_x), _p(res), _p(res_w),
                                        mode, _stream()), "matris_pair_bwd")
@@ -759,8 +774,8 @@ class _Pair(torch.autograd.Function):
         dev = ctx.pack.device
         ref = g0 if g0 is not None else g1
         M = ref.shape[0]
-        g0 = torch.zeros(M, D, device=dev) if g0 is None else _f32c(g0)
-        g1 = torch.zeros(M, D, device=dev) if g1 is None else _f32c(g1)
+        g0 = _rows(M, D, dev).zero_() if g0 is None else _f32c(g0)
+        g1 = _rows(M, D, dev).zero_() if g1 is None else _f32c(g1)
         return pair_bwd_raw(ctx.pack, g0, g1, ctx.mode), None
 
 
@@ -812,7 +827,7 @@ class _SBF(torch.autograd.Function):
         unit = _f32c(unit)
         lib = _lib.load()
         A = grp_t.n_rows
-        out = torch.empty(A, 16, device=unit.device)
+        out = _rows(A, 16, unit.device)
         with _timed("sbf_fwd", (A,)):
             _lib.check(lib.matris_sbf_fwd(A, _p(unit), _p(grp_t.key), _p(grp_s.key), cutoff, _p(out), _stream()),
                        "matris_sbf_fwd")
@@ -844,7 +859,7 @@ class _TbEmbed(torch.autograd.Function):
         lib = _lib.load()
         basis = _f32c(basis)
         M = basis.shape[0]
-        out = torch.empty(M, D, dtype=torch.float32, device=basis.device)
+        out = _rows(M, D, basis.device)
         with _timed("tb_embed_fwd", (M,)):
             _lib.check(lib.matris_tb_embed_fwd(M, _p(basis), _p(wa), _p(pack.b("w0", mode)), _p(out), mode,
                                                _stream()), "matris_tb_embed_fwd")
