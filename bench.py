@@ -70,6 +70,8 @@ def _parse():
     ap.add_argument("--cpu-sample-reps", type=int, default=6,
                     help="fcc reps of the CPU baseline sample (6: the C3 cell itself)")
     ap.add_argument("--cpu-steps", type=int, default=2, help="timed CPU baseline steps (after one warm-up)")
+    ap.add_argument("--cpu-c5-proxy", action="store_true",
+                    help="only time the CPU oracle on the reduced 4,000-atom a-SiO2 cell (no GPU)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (HBM counter calibration)")
     return ap.parse_args()
@@ -243,6 +245,44 @@ def c5_md(model, dev, steps: int, warmup: int):
                 "block_checkpoint": f"auto ({n_ck} of {len(model.interaction_block)} blocks)"})
 
 
+def cpu_c5_proxy(steps: int, n_atoms: int = 4000):
+    """The CPU oracle on a reduced a-SiO2 cell (BASELINE's C5 CPU plan: the 32,000-atom cell
+    does not fit a CPU timing run, so the same generator at the same density with n_atoms
+    atoms, seed 4), efs (forces and stress), one warm-up step then `steps` timed steps;
+    atom-steps/s, labelled reduced."""
+    import torch
+
+    from matris_amd import workloads as W
+    from matris_amd.config import MATRIS_10M
+    from oracle import graph_ref
+    from oracle.model_ref import MatRISRef
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    cr = W.sio2(n_atoms, seed=4)
+    og = graph_ref.build_graph(cr.frac, cr.lattice, cr.z)
+    g = dict(atomic_number=torch.tensor(cr.z, dtype=torch.int32),
+             atom_frac_coord=torch.tensor(cr.frac, dtype=torch.float32),
+             lattice=torch.tensor(cr.lattice, dtype=torch.float32),
+             neighbor_image=torch.tensor(og["image"], dtype=torch.float32),
+             atom_graph=torch.tensor(np_stack(og["center"], og["neighbor"]), dtype=torch.int32),
+             directed2undirected=torch.tensor(og["d2u"], dtype=torch.int32),
+             undirected2directed=torch.tensor(og["u2d"], dtype=torch.int32),
+             line_graph=torch.tensor(og["line_graph"], dtype=torch.int32))
+    torch.manual_seed(0)
+    model = MatRISRef(**MATRIS_10M).eval()
+    model([g], task="efs")
+    t0 = time.perf_counter()
+    for n in range(1, steps + 1):
+        model([g], task="efs")
+        print(f"cpu c5 proxy: step {n} of {steps} done", file=sys.stderr, flush=True)
+    dt = time.perf_counter() - t0
+    return dict(value=round(len(cr) * steps / dt, 3), unit="atom*steps/s", cores=threads, kind="port",
+                sample=f"reduced: oracle/model_ref.py efs (fp32 torch CPU) on a {len(cr)}-atom a-SiO2 cell (2.2 g/cm3, "
+                       f"d_min 1.5, seed 4; {len(og['center'])} edges, {len(og['line_graph'])} angles), {steps} timed "
+                       f"steps after 1 warm-up, graph prebuilt")
+
+
 def cpu_baseline(reps: int, steps: int):
     """The CPU oracle (oracle/model_ref.py, a plain fp32 torch restatement of the
     reference forward + autograd) on the host cores: the C3 cell itself at reps = 6 (a
@@ -289,6 +329,9 @@ def np_stack(a, b):
 
 def main():
     args = _parse()
+    if args.cpu_c5_proxy:
+        print(json.dumps({"cpu_c5_proxy": cpu_c5_proxy(args.cpu_steps)}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested); multi-GPU scaling is a design "
               f"note, not built in this tree", file=sys.stderr)

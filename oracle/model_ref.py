@@ -25,6 +25,7 @@ from collections.abc import Sequence
 
 import torch
 import torch.nn.functional as F
+import torch.utils.checkpoint
 from torch import Tensor, nn
 
 
@@ -421,13 +422,22 @@ class InteractionBlock(nn.Module):
     def forward(self, g, node_feat, edge_feat, tb_feat, smooth_weight):
         attn_edge, attn_tb = edge_feat, tb_feat
         upd_edge, upd_tb = edge_feat, tb_feat
+        # interaction_block.py:15,400-413: the two line-graph layers are checkpointed above
+        # 60,000 angles (same values, less memory, their forward rerun in the backward)
+        ckpt = tb_feat is not None and tb_feat.shape[0] > 60000 and torch.is_grad_enabled()
+
+        def run(layer, *args, **kw):
+            if ckpt:
+                return torch.utils.checkpoint.checkpoint(layer, *args, use_reentrant=False, **kw)
+            return layer(*args, **kw)
+
         if tb_feat is not None:
-            attn_edge, attn_tb = self.attn_block_line_graph(edge_feat, tb_feat, g["line_graph_dict"])
+            attn_edge, attn_tb = run(self.attn_block_line_graph, edge_feat, tb_feat, g["line_graph_dict"])
         attn_node, attn_edge = self.attn_block_atom_graph(node_feat, attn_edge, g["atom_graph_dict"],
                                                           g["directed2undirected"])
         if tb_feat is not None:
-            upd_edge, upd_tb = self.refine_block_line_graph(attn_edge, attn_tb, smooth_weight["line graph"],
-                                                            g["line_graph_dict"], atom_feat=attn_node)
+            upd_edge, upd_tb = run(self.refine_block_line_graph, attn_edge, attn_tb, smooth_weight["line graph"],
+                                   g["line_graph_dict"], atom_feat=attn_node)
         upd_node, upd_edge = self.refine_block_atom_graph(attn_node, upd_edge, smooth_weight["atom graph"],
                                                           g["atom_graph_dict"], d2u=g["directed2undirected"])
         return upd_node, upd_edge, upd_tb
