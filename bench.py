@@ -271,6 +271,20 @@ def cpu_c5_proxy(steps: int, n_atoms: int = 4000):
              line_graph=torch.tensor(og["line_graph"], dtype=torch.int32))
     torch.manual_seed(0)
     model = MatRISRef(**MATRIS_10M).eval()
+    print(f"cpu c5 proxy: {len(cr)} atoms, {len(og['line_graph'])} angles, {threads} threads", file=sys.stderr,
+          flush=True)
+    # a CPU evaluation of this cell runs for minutes: each interaction block reports when its
+    # forward and its backward finish
+    def report(i):
+        def hook(_mod, _args, out):
+            print(f"cpu c5 proxy: block {i} forward", file=sys.stderr, flush=True)
+            if out[0].requires_grad:
+                out[0].register_hook(lambda _g: print(f"cpu c5 proxy: block {i} backward", file=sys.stderr,
+                                                      flush=True))
+        return hook
+
+    for i, blk in enumerate(model.interaction_block):
+        blk.register_forward_hook(report(i))
     model([g], task="efs")
     t0 = time.perf_counter()
     for n in range(1, steps + 1):

@@ -131,9 +131,15 @@ def test_strided_fractional_input_gives_the_same_graph():
 def test_skin_neighbor_list_equals_fresh_build(case):
     """Verlet-skin reuse (SkinNeighborList): along a drifting, jittered trajectory whose atoms
     cross the cell faces (their wrapped fractional coordinates jump by 1), every update returns
-    the fresh cutoff build's arrays bit for bit; the candidate list is rebuilt only once an
-    atom has moved skin / 2, and reused (with wrap jumps) in between."""
+    the fresh cutoff build's arrays bit for bit, and the CPU oracle's neighbour list
+    (oracle.graph_ref.neighbor_list: center, neighbor, image, fp64 distance) on the same
+    wrapped coordinates, including the frames just after a wrap jump on a reused candidate
+    list; the whole graph built from the skin list (GraphConverter.from_arrays(neighbors=...))
+    equals the oracle's build_graph (pairing and line graph) on those frames.  The candidate
+    list is rebuilt only once an atom has moved skin / 2, and reused in between."""
+    from matris_amd.graph import GraphConverter
     from matris_amd.graph.converter import SkinNeighborList, radius_graph_device
+    from oracle import graph_ref
     rng = np.random.default_rng(7)
     cr = (W.fcc_supercell(3.61, 3, sigma=0.05, seed=3) if case == "fcc108"
           else W.random_cell(np.random.default_rng(2), 40))
@@ -153,11 +159,26 @@ def test_skin_neighbor_list_equals_fresh_build(case):
         ref = radius_graph_device(frac, cr.lattice, 6.0)
         for name, a, b in zip(("center", "neighbor", "image", "dist", "row_ptr", "row_count"), got, ref):
             assert a.dtype == b.dtype and torch.equal(a, b), (step, name)
+        fr_np = frac.cpu().numpy()
+        oc, onb, oim, od = graph_ref.neighbor_list(fr_np, cr.lattice, 6.0)
+        assert np.array_equal(got[0].cpu().numpy(), oc) and np.array_equal(got[1].cpu().numpy(), onb), step
+        assert np.array_equal(got[2].cpu().numpy().astype(np.int64), oim), step
+        assert np.array_equal(got[3].cpu().numpy(), od), step  # fp64, bit-exact
         k = torch.round(x - frac)
+        wrapped = False
         if nl.n_builds != before:
             k_build = k
         else:
-            reused_wraps += int((k != k_build).any().item())
+            wrapped = bool((k != k_build).any().item())
+            reused_wraps += int(wrapped)
+        if wrapped or step in (0, 13):
+            g = GraphConverter(6.0, 4.0, device="cuda").from_arrays(fr_np, cr.lattice, cr.z, frac_device=frac,
+                                                                    neighbors=got)
+            og = graph_ref.build_graph(fr_np, cr.lattice, cr.z, 6.0, 4.0)
+            assert np.array_equal(g.atom_graph.cpu().numpy()[:, 1], og["neighbor"]), step
+            assert np.array_equal(g.directed2undirected.cpu().numpy(), og["d2u"]), step
+            assert np.array_equal(g.undirected2directed.cpu().numpy(), og["u2d"]), step
+            assert np.array_equal(g.line_graph.cpu().numpy().reshape(-1, 5), og["line_graph"]), step
         jitter = rng.normal(size=(n, 3))
         jitter *= (0.1 * rng.random((n, 1))) / np.linalg.norm(jitter, axis=1, keepdims=True)
         pos = pos + torch.tensor(drift + jitter, device="cuda")
