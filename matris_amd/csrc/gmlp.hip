@@ -18,7 +18,7 @@
 // stores and turns it into h = SiLU(p), GEMM2's operand; a row pass with 16 lanes per
 // row saves z, applies the two RMSNorms (16-lane DPP sums), SiLU, sigmoid and their
 // product, and writes out with 512-byte row stores.  p and z are written for the
-// backward.
+// backward, with streaming stores.
 //
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
@@ -172,23 +172,36 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // GEMM1's first loads, they arrive while the pipeline fills.
     if (proj.n > 0) {
         const int h = lane >> 5, l32 = lane & 31;
+        // every table's row of a 32-row tile is loaded before any is added: one round
+        // trip per row tile instead of one per table
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             const int64_t r = min(m0 + rt * 32 + l32, M - 1);
-#pragma unroll 1
-            for (int j = 0; j < proj.n; ++j) {
-                const int64_t pr = proj.idx[j] ? (int64_t)proj.idx[j][r] : r;
-                const float *pp = proj.ptr[j] + pr * proj.ld[j] + wave * 64 + 4 * h;
+            float4 v[3][2][4];
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
+            for (int j = 0; j < 3; ++j) {
+                if (j < proj.n) {
+                    const int64_t pr = proj.idx[j] ? (int64_t)proj.idx[j][r] : r;
+                    const float *pp = proj.ptr[j] + pr * proj.ld[j] + wave * 64 + 4 * h;
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const float4 v = *reinterpret_cast<const float4 *>(pp + ct * 32 + 8 * jj);
-                        acc[rt][ct][4 * jj] += v.x;
-                        acc[rt][ct][4 * jj + 1] += v.y;
-                        acc[rt][ct][4 * jj + 2] += v.z;
-                        acc[rt][ct][4 * jj + 3] += v.w;
-                    }
+                    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) v[j][ct][jj] = *reinterpret_cast<const float4 *>(pp + ct * 32 + 8 * jj);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                if (j < proj.n) {
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) {
+                            acc[rt][ct][4 * jj] += v[j][ct][jj].x;
+                            acc[rt][ct][4 * jj + 1] += v[j][ct][jj].y;
+                            acc[rt][ct][4 * jj + 2] += v[j][ct][jj].z;
+                            acc[rt][ct][4 * jj + 3] += v[j][ct][jj].w;
+                        }
+                }
             }
         }
         if (MODE == 2 && nsrc > 0) scale_acc<MODE>(acc, w1up);  // power of two: exact
@@ -228,7 +241,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         const int row = q >> 6, c4 = (q & 63) * 4;
         float4 *t = reinterpret_cast<float4 *>(Ts + row * LDH + c4);
         float4 v = *t;
-        if (save_p && m0 + row < M) *reinterpret_cast<float4 *>(save_p + (m0 + row) * 256 + c4) = v;
+        // p and z are read again only by the backward: streaming (non-temporal) stores
+        if (save_p && m0 + row < M) st_nt4(save_p + (m0 + row) * 256 + c4, v);
         v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
         *t = v;
     }
@@ -241,6 +255,18 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 2, MATRIS_D / 16, true>(acc, Ts + blk * MATRIS_D, LDH, W2, 2 * wave,
                                                                         MATRIS_D / 16, 0, lane));
     scale_acc<MODE>(acc, w2s);
+    // the residual rows of the row pass below, loaded before its z and out stores so
+    // that waiting for them does not wait for those stores too
+    const int c4 = (lane & 15) * 4;
+    float4 rx0[BM / 16], rx1[BM / 16];
+    if (res_out) {
+#pragma unroll
+        for (int rr = 0; rr < BM / 16; ++rr) {
+            const int64_t grow = min(m0 + wave * (BM / 4) + rr * 4 + (lane >> 4), M - 1);
+            rx0[rr] = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c4);
+            rx1[rr] = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + 64 + c4);
+        }
+    }
     __syncthreads();  // every wave is done reading h
 
     // z = acc + b2 -> LDS (16-byte writes); then a row pass with 16 lanes per row: lane
@@ -249,7 +275,6 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // RMSNorm sum is a 16-lane DPP sum
     acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b2);
     __syncthreads();
-    const int c4 = (lane & 15) * 4;
     const float4 wc0 = *reinterpret_cast<const float4 *>(norm_c + c4);
     const float4 wc1 = *reinterpret_cast<const float4 *>(norm_c + 64 + c4);
     const float4 wg0 = *reinterpret_cast<const float4 *>(norm_g + c4);
@@ -265,10 +290,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         const int64_t grow = m0 + row;
         if (save_z && grow < M) {
             float *zo = save_z + grow * 256 + c4;
-            *reinterpret_cast<float4 *>(zo) = zc0;
-            *reinterpret_cast<float4 *>(zo + 64) = zc1;
-            *reinterpret_cast<float4 *>(zo + MATRIS_D) = zg0;
-            *reinterpret_cast<float4 *>(zo + MATRIS_D + 64) = zg1;
+            st_nt4(zo, zc0);
+            st_nt4(zo + 64, zc1);
+            st_nt4(zo + MATRIS_D, zg0);
+            st_nt4(zo + MATRIS_D + 64, zg1);
         }
         const float rc = rsqrtf(row16_sum(zc0.x * zc0.x + zc0.y * zc0.y + zc0.z * zc0.z + zc0.w * zc0.w +
                                           zc1.x * zc1.x + zc1.y * zc1.y + zc1.z * zc1.z + zc1.w * zc1.w) *
@@ -292,8 +317,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             if (res_out) {
                 const float4 w0 = *reinterpret_cast<const float4 *>(res_w + c4);
                 const float4 w1 = *reinterpret_cast<const float4 *>(res_w + 64 + c4);
-                const float4 x0 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + c4);
-                const float4 x1 = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + 64 + c4);
+                const float4 x0 = rx0[rr], x1 = rx1[rr];
                 float *ro = res_out + grow * MATRIS_D + c4;
                 *reinterpret_cast<float4 *>(ro) = make_float4(o0.x + w0.x * x0.x, o0.y + w0.y * x0.y, o0.z + w0.z * x0.z,
                                                               o0.w + w0.w * x0.w);
@@ -309,7 +333,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 // backward
 // ------------------------------------------------------------------------------------
 // Store a wave's [64, 32*NCT] accumulators to rows of dst (row stride ld) at column
-// col + ct*32 + lane%32, rows below nrows only.
+// col + ct*32 + lane%32, rows below nrows only, with streaming stores (the gradient rows
+// are read once, by the segment sums that follow).
 template <int NCT>
 __device__ __forceinline__ void store_acc_rows(const v16f (&acc)[2][NCT], float *__restrict__ dst, int ld, int col,
                                                int nrows, int lane) {
@@ -321,7 +346,7 @@ __device__ __forceinline__ void store_acc_rows(const v16f (&acc)[2][NCT], float 
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = rt * 32 + acc_row(i, h);
-                if (row < nrows) dst[row * ld + col + ct * 32 + l32] = acc[rt][ct][i];
+                if (row < nrows) st_nt(dst + row * ld + col + ct * 32 + l32, acc[rt][ct][i]);
             }
 }
 

@@ -58,6 +58,15 @@ struct Frag {
 // fp16 overflow threshold of the MODE 2 activation split.
 #define MATRIS_F16_MAX 65504.0f
 
+// Streaming (non-temporal) stores for rows that no kernel reads back soon: they do not
+// displace the gathered tables and weights that later loads of the same kernel hit in L2.
+typedef float matris_f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_nt4(float *p, float4 v) {
+    const matris_f4v w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<matris_f4v *>(p));
+}
+__device__ __forceinline__ void st_nt(float *p, float v) { __builtin_nontemporal_store(v, p); }
+
 // Per-row power-of-two scaling of MODE 2 gradient operands.  fp16's exponent range keeps
 // ~22 bits of an activation only inside [2^-14, 2^16); the backward GEMMs' operands are
 // gradients whose rows can sit far below it (the RMSNorm Jacobian divides by the row's
