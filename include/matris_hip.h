@@ -169,6 +169,18 @@ int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t l
                     int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b, float scale_b, int accumulate,
                     const float *base, const float *base_w, float *out, void *stream);
 
+/* matris_seg_sum2 whose first source holds tile-run partial sums (the output of
+ * matris_gmlp_bwd_runs): its rows ascend by segment (rowptr_a, no permutation) and
+ * segment s = rows [rs, re) adds only row rs and each later multiple of tile_a below re
+ * -- one partial per tile of tile_a rows that the segment spans -- instead of every row.
+ * The second source (xb may be NULL) is summed as in matris_seg_sum2.  Completes the
+ * reference's aggregate / index_add_ of a gathered source's gradient (functions.py:
+ * 131-160) when its rows were pre-summed inside the GatedMLP backward's tiles. */
+int matris_seg_sum2_runs(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t lda, int64_t offa,
+                         const int32_t *rowptr_a, int tile_a, float scale_a, const float *xb, int64_t ldb,
+                         int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b, float scale_b, int accumulate,
+                         float *out, void *stream);
+
 /* out[r, :] = (accumulate ? out[r, :] : 0) + scale * src[idx ? idx[r] : r, :]
  * torch.index_select(x, 0, idx) (interaction_block.py:96-100) and the backward of a
  * segment sum. */
@@ -332,6 +344,21 @@ int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_host, const in
 int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                     const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x, float *g_x0,
                     int acc0, const float *res_w, int mode, void *stream);
+
+/* matris_gmlp_bwd for a gathered source whose index run_key [m] (int32) ascends with the
+ * row (the target bond of angle rows, the centre atom of edge rows): source block run_blk
+ * (its columns 128 run_blk .. +127 of the K; not source 0 when g_x0 is given) leaves as
+ * tile-run partial sums -- within each tile of matris_gmlp_tile_rows() rows, the sum of
+ * every run of equal keys, at the run's first row of g_x; the block's other rows are not
+ * written.  matris_seg_sum2_runs with the same tile size completes the segment sums
+ * (functions.py:131-160) from those partials, reading one row per run instead of every
+ * gathered row.  Other sources and outputs are those of matris_gmlp_bwd. */
+int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
+                         const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
+                         float *g_x0, int acc0, const float *res_w, const int32_t *run_key, int run_blk, int mode,
+                         void *stream);
+/* Rows per GatedMLP work-group tile (the tile of matris_gmlp_bwd_runs's partial sums). */
+int matris_gmlp_tile_rows(void);
 
 /* GatedMLP forward with the layer-1 product of gathered sources taken before the gather
  * (same layer as matris_gmlp_fwd, GatedMLP.forward in functions.py:297-311, for inputs

@@ -89,6 +89,7 @@ _SIGS = {
     "matris_seg_sum": (_I, [_P, _I64, _I64, _P, _P, _I64, _F, _I, _P, _P]),
     "matris_seg_sum2": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P, _P,
                              _P]),
+    "matris_seg_sum2_runs": (_I, [_I64, _I64, _P, _I64, _I64, _P, _I, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P]),
     "matris_gather_rows": (_I, [_P, _P, _I64, _F, _I, _P, _P]),
     "matris_seg_sum_mul": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _F, _I, _P, _P]),
     "matris_gather_mul": (_I, [_I64, _P, _P, _P, _P, _I, _P, _P]),
@@ -103,6 +104,8 @@ _SIGS = {
     "matris_gmlp_fwd_proj": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
                                   _P, _I, _P]),
     "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I, _P]),
+    "matris_gmlp_bwd_runs": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _P, _I, _I, _P]),
+    "matris_gmlp_tile_rows": (_I, []),
     "matris_bessel_fwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _P]),
     "matris_bessel_bwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _I, _P, _P]),
     "matris_sbf_fwd": (_I, [_I64, _P, _P, _P, _D, _P, _P]),

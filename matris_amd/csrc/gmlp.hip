@@ -350,6 +350,38 @@ __device__ __forceinline__ void store_acc_rows(const v16f (&acc)[2][NCT], float 
             }
 }
 
+// Tile-run sums instead of rows (rows ascending by key): for each run of equal keys among
+// the tile's rows [s, e) -- `starts` has bit s set for every run start -- store the sum
+// of the run's rows at row s (columns col + ct*32 + lane%32); other rows are not written.
+// Each lane adds its rows in row order, then lane half 0 + half 1: deterministic.
+template <int NCT>
+__device__ __forceinline__ void store_acc_runs(const v16f (&acc)[2][NCT], float *__restrict__ dst, int ld, int col,
+                                               uint64_t starts, int nrows, int lane) {
+    const int h = lane >> 5, l32 = lane & 31;
+    while (starts) {  // wave-uniform
+        const int s = __builtin_ctzll(starts);
+        starts &= starts - 1;
+        const int e = starts ? __builtin_ctzll(starts) : nrows;
+        // row of element (rt, i) = rt*32 + acc_row(i, 0) + 4h: compare the constant part
+        // against the run's bounds shifted by 4h
+        const int s4 = s - 4 * h, e4 = e - 4 * h;
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+            float t = 0.f;
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int r0 = rt * 32 + acc_row(i, 0);
+                    t += (r0 >= s4 && r0 < e4) ? acc[rt][ct][i] : 0.f;
+                }
+            const float o = __shfl_xor(t, 32, 64);
+            t = h ? o + t : t + o;
+            if (h == 0) dst[(int64_t)s * ld + col + ct * 32 + l32] = t;
+        }
+    }
+}
+
 // MODE 2: multiply accumulator rows (layout of store_acc_rows: element i of lane half h is
 // row rt*32 + 8 (i/4) + 4h + i%4) by their rows' factors, four rows per 16-byte LDS read.
 template <int MODE, int NCT>
@@ -380,6 +412,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                                           const float *__restrict__ norm_g, float eps,
                                                           float *__restrict__ g_x, float *__restrict__ g_x0,
                                                           int acc0, const float *__restrict__ res_w,
+                                                          const int32_t *__restrict__ run_key, int run_blk,
                                                           unsigned *range_flag) {
     __shared__ __align__(16) float G[BM * LDH];
     __shared__ __align__(16) float rinv[BM];  // MODE 2: 2^-k w1s for each row (g_z / g_p scaled by 2^k)
@@ -393,6 +426,9 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
     float amax = 0.f;
+    // run_key: source block run_blk leaves as tile-run sums (store_acc_runs); each wave
+    // reads the tile's 64 keys now, lane r holding row r's
+    const int run_k = run_key ? run_key[min(m0 + lane, M - 1)] : 0;
 
     // phase 1: row-wise Jacobian of out = SiLU(RMS(z_c) w_c) * sigmoid(RMS(z_g) w_g).
     // 16 lanes per row (4 rows per wave per pass, wave w owns rows [16w, 16w+16)): lane c
@@ -564,6 +600,12 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     // g_x (row stride K - 128 with g_x0, K without).
     const int coff = g_x0 ? MATRIS_D : 0;
     const int ldr = K - coff;
+    // bit r: row r (< nrows) starts a run of equal keys within the tile (the shuffle runs
+    // on every lane: a lane reading from one that skipped it would see no value)
+    const int run_prev = __shfl(run_k, (lane + 63) & 63, 64);
+    const uint64_t run_starts =
+        run_key ? (uint64_t)__ballot(lane < nrows && (lane == 0 || run_k != run_prev)) : 0;
+    const int run_c0 = run_blk * MATRIS_D;  // the reduced block's columns [run_c0, run_c0 + 128)
     float *__restrict__ gxr = g_x ? g_x + m0 * ldr : nullptr;
     const bool epi0 = g_x0 != nullptr || res_w != nullptr;
     if (K % 256) {
@@ -579,7 +621,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             unscale_acc_rows<MODE, 1>(a2, rinv, h);  // 2^-k w1s per row
         else
             scale_acc<MODE>(a2, w1s);
-        if (cb > 0 || !epi0) store_acc_rows<1>(a2, gxr, ldr, col0 - coff, nrows, lane);
+        if (run_key && col0 >= run_c0 && col0 < run_c0 + MATRIS_D)
+            store_acc_runs<1>(a2, gxr, ldr, col0 - coff, run_starts, nrows, lane);
+        else if (cb > 0 || !epi0)
+            store_acc_rows<1>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {  // K == 128: every wave holds source-0 columns
             __syncthreads();
             acc_to_lds<1>(a2, G, LDH, col0, lane);
@@ -597,7 +642,10 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             unscale_acc_rows<MODE, 2>(a2, rinv, h);  // 2^-k w1s per row
         else
             scale_acc<MODE>(a2, w1s);
-        if (col0 >= MATRIS_D || !epi0) store_acc_rows<2>(a2, gxr, ldr, col0 - coff, nrows, lane);
+        if (run_key && col0 >= run_c0 && col0 < run_c0 + MATRIS_D)
+            store_acc_runs<2>(a2, gxr, ldr, col0 - coff, run_starts, nrows, lane);
+        else if (col0 >= MATRIS_D || !epi0)
+            store_acc_rows<2>(a2, gxr, ldr, col0 - coff, nrows, lane);
         if (cb == 0 && epi0) {
             __syncthreads();  // all waves are done reading G
             if (col0 < MATRIS_D) acc_to_lds<2>(a2, G, LDH, col0, lane);
@@ -695,13 +743,16 @@ extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *sr
                            b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, mode, stream);
 }
 
-extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
-                               const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
-                               float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
+static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
+                           const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
+                           float *g_x0, int acc0, const float *res_w, const int32_t *run_key, int run_blk, int mode,
+                           void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1tp || !w2tp ||
         !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
         return MATRIS_E_ARG;
+    // the reduced block goes to g_x: not source 0 when source 0 has its own output
+    if (run_key && (!g_x || run_blk < (g_x0 ? 1 : 0) || run_blk >= k / MATRIS_D)) return MATRIS_E_ARG;
     if (m == 0) return 0;
     if (!aligned16(w1tp) || !aligned16(w2tp)) return MATRIS_E_ARG;
     if (acc0 && !g_x0) return MATRIS_E_ARG;
@@ -711,10 +762,28 @@ extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float
     unsigned *flag = nullptr;
     if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
     MATRIS_MODE_DISPATCH(gmlp_bwd_kernel, grid, st, m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                         res_w, flag);
+                         res_w, run_key, run_blk, flag);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
+
+extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
+                               const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
+                               float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
+    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, nullptr, -1,
+                           mode, stream);
+}
+
+extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, const float *z,
+                                    const void *w1tp, const void *w2tp, const float *norm_c, const float *norm_g,
+                                    float eps, float *g_x, float *g_x0, int acc0, const float *res_w,
+                                    const int32_t *run_key, int run_blk, int mode, void *stream) {
+    if (!run_key) return MATRIS_E_ARG;
+    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, run_key,
+                           run_blk, mode, stream);
+}
+
+extern "C" int matris_gmlp_tile_rows(void) { return BM; }
 
 // ------------------------------------------------------------------------------------
 // weight packing: [n, k] row-major fp32 (rows = output columns of the GEMM) -> fragment

@@ -88,7 +88,29 @@ struct SegSrc {
     float scale;
     const float *mul;        // optional per-row multiplier rows mul[mul_idx[r]] ([*, 128])
     const int32_t *mul_idx;
+    // tile > 0: rows ascend by segment (no perm) and x holds tile-run partial sums (the
+    // GatedMLP backward's matris_gmlp_bwd_runs): a segment [rs, re) adds only its row rs
+    // and each later multiple of `tile` below re -- one partial per tile it spans.
+    int tile;
 };
+
+// The k-th summed row of a tile-run segment starting at row rs (see SegSrc::tile).
+__device__ __forceinline__ int64_t tile_run_row(int64_t rs, int k, int tile) {
+    return k == 0 ? rs : (rs / tile + k) * (int64_t)tile;
+}
+
+// Partial sum of the tile-run rows k = off, off + stride, ... of the segment [rs, re).
+__device__ __forceinline__ float4 seg_tile_rows(const float *__restrict__ xc, int64_t ldx, int64_t rs, int64_t re,
+                                                int tile, int off, int stride) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = off;; k += stride) {
+        const int64_t r = tile_run_row(rs, k, tile);
+        if (r >= re) break;
+        const float4 v = ld4(xc + r * ldx);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    return acc;
+}
 
 __device__ __forceinline__ float4 add4(const float4 &a, const float4 &b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
@@ -96,6 +118,7 @@ __device__ __forceinline__ float4 add4(const float4 &a, const float4 &b) {
 
 template <bool MUL>
 __device__ __forceinline__ float4 seg_src_rows(const SegSrc &v, int64_t s, int c, int off, int stride) {
+    if (v.tile > 0) return seg_tile_rows(v.x + v.col_off + c, v.ldx, v.rowptr[s], v.rowptr[s + 1], v.tile, off, stride);
     if (MUL && v.mul)
         return seg_rows<true>(v.x + v.col_off + c, v.ldx, v.perm, v.rowptr[s] + off, v.rowptr[s + 1], stride,
                               v.mul + c, v.mul_idx);
@@ -165,6 +188,11 @@ __device__ __forceinline__ void seg_rows4(const SegSrc &v, int64_t s0, int64_t n
         b[j] = in ? v.rowptr[s0 + j] : 0;
         e[j] = in ? v.rowptr[s0 + j + 1] : 0;
     }
+    if (v.tile > 0) {  // tile-run partials: the same rows and order as seg_sum_kernel's
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = seg_tile_rows(xc, v.ldx, b[j], e[j], v.tile, half, 2);
+        return;
+    }
     int64_t r[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -227,7 +255,7 @@ __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, 
 
 static bool seg_src_ok(const SegSrc &v) {
     return v.rowptr && v.ldx >= MATRIS_D && v.col_off >= 0 && v.col_off + MATRIS_D <= v.ldx && !(v.ldx % 4) &&
-           !(v.col_off % 4);
+           !(v.col_off % 4) && v.tile >= 0 && !(v.tile > 0 && (v.perm || v.mul));
 }
 
 static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64_t rows_hint, int accumulate,
@@ -275,6 +303,16 @@ extern "C" int matris_seg_sum2(int64_t n_seg, int64_t rows_hint, const float *xa
     const SegSrc a{xa, lda, offa, rowptr_a, perm_a, scale_a, nullptr, nullptr};
     const SegSrc b{xb, ldb, offb, rowptr_b, perm_b, scale_b, nullptr, nullptr};
     return seg_sum_launch(a, b, n_seg, rows_hint, accumulate, out, stream, base, base_w);
+}
+
+extern "C" int matris_seg_sum2_runs(int64_t n_seg, int64_t rows_hint, const float *xa, int64_t lda, int64_t offa,
+                                    const int32_t *rowptr_a, int tile_a, float scale_a, const float *xb, int64_t ldb,
+                                    int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b, float scale_b,
+                                    int accumulate, float *out, void *stream) {
+    if (tile_a <= 0) return MATRIS_E_ARG;
+    const SegSrc a{xa, lda, offa, rowptr_a, nullptr, scale_a, nullptr, nullptr, tile_a};
+    const SegSrc b{xb, ldb, offb, rowptr_b, perm_b, scale_b, nullptr, nullptr};
+    return seg_sum_launch(a, b, n_seg, rows_hint, accumulate, out, stream);
 }
 
 extern "C" int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx, int64_t col_off,

@@ -69,6 +69,16 @@ def _res_ok(w) -> bool:
     return tuple(w.shape) == (1, D)
 
 
+def _runs(grp: ops.Grouping, blk: int):
+    """(key, blk) for gmlp_bwd_raw's tile-run sums when grp's rows ascend by key (no
+    permutation), else None (the block leaves as rows)."""
+    return (grp.key, blk) if grp.perm is None else None
+
+
+def _tile_rows(grp: ops.Grouping) -> int:
+    return ops.gmlp_tile_rows() if grp.perm is None else 0
+
+
 def line_attention_fusable(layer) -> bool:
     s, t = layer.source_weight_linear, layer.target_weight_linear
     return (layer.edge_nonlinear_update._fusable() and layer.node_nonlinear_update._fusable()
@@ -151,10 +161,11 @@ class _LineAttention(torch.autograd.Function):
         g_tb = ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_tb_new, res_w=r_e)
         del g_as, g_at
         # edge update: source 0 (tb) accumulates into g_tb, bond gathers scatter into g_bond
-        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=True)
+        # the target-bond block (rows ascend by target) leaves as tile-run partial sums
+        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=True, runs=_runs(tgt, 1))
         del g_e, p_e, z_e
         ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True,
-                        second=(g_x, src, 1.0, 2 * D, D))
+                        second=(g_x, src, 1.0, 2 * D, D), tile_rows=_tile_rows(tgt))
         return g_bond, g_tb, None, None, None
 
 
@@ -223,11 +234,11 @@ class _LineRefinement(torch.autograd.Function):
         del p_de
         g_env = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h, accumulate=True)
         del h
-        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=True)
+        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=True, runs=_runs(tgt, 2))
         del g_h, p_h, z_h
         g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True,
-                        second=(g_x, src, 1.0, 3 * D, 2 * D))
+                        second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
         return g_tb, g_atom, g_bond, g_env, None, None, None
 
 
@@ -312,11 +323,12 @@ class _AtomAttention(torch.autograd.Function):
                                   res=g_bond_new, res_w=r_e)
         del g_at, g_as
         # edge update: sources bond[d2u], atom[tgt], atom[src]
-        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode)
+        # the centre-atom block (rows ascend by centre) leaves as tile-run partial sums
+        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, runs=_runs(tgt, 1))
         del g_e, p_e, z_e
         ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, out=g_bond, accumulate=True)
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
-                        second=(g_x, src, 1.0, 3 * D, 2 * D))
+                        second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
         return g_atom, g_bond, None, None, None
 
 
@@ -385,11 +397,11 @@ class _AtomRefinement(torch.autograd.Function):
             g_h = ops.gather_mul_raw(g_agg, tgt.key, w, d2u.key, out=g_te, accumulate=True)
             g_env = ops.seg_sum_mul_raw(h, d2u, g_agg, tgt.key)
         del g_te, h, w
-        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode)
+        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode, runs=_runs(tgt, 1))
         del g_h, p_h, z_h
         g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
-                        second=(g_x, src, 1.0, 3 * D, 2 * D))
+                        second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
         return g_atom, g_bond, g_env, None, None, None
 
 

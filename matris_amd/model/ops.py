@@ -177,11 +177,14 @@ class Grouping:
 # segment sum / gather
 # ------------------------------------------------------------------------------------
 def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D, col_off: int = 0,
-                out: torch.Tensor | None = None, accumulate: bool = False, second=None, base=None) -> torch.Tensor:
+                out: torch.Tensor | None = None, accumulate: bool = False, second=None, base=None,
+                tile_rows: int = 0) -> torch.Tensor:
     """out (+)= scale * segment sums of x[:, col_off:col_off+128] over grp; with
     second = (x2, grp2, scale2, ldx2, col_off2) also + scale2 * those of x2 over grp2 (same
     segment count), in the same pass (matris_seg_sum2); with base = (feat [n_seg, 128],
-    w [128]) also + w * feat (a residual term)."""
+    w [128]) also + w * feat (a residual term).  tile_rows > 0: x holds tile-run partial
+    sums of rows ascending by grp's key (gmlp_bwd_raw's runs) and each segment adds one
+    partial per tile it spans (matris_seg_sum2_runs; no base)."""
     lib = _lib.load()
     if out is None:
         out = _rows(grp.n_seg, D, x.device)
@@ -194,6 +197,14 @@ def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D
         args2 = (_p(x2), ld2, off2, _p(g2.rowptr), _p(g2.perm), s2)
     else:
         args2 = (None, D, 0, None, None, 0.0)
+    if tile_rows:
+        if grp.perm is not None or base is not None:
+            raise ValueError("seg_sum_raw: tile-run partials need rows ascending by segment and no base term")
+        with _timed("seg_sum", (grp.n_rows, grp.n_seg, "runs")):
+            _lib.check(lib.matris_seg_sum2_runs(grp.n_seg, rows, _p(x), ldx, col_off, _p(grp.rowptr), int(tile_rows),
+                                                scale, *args2, int(accumulate), _p(out), _stream()),
+                       "matris_seg_sum2_runs")
+        return out
     bx, bw = base if base is not None else (None, None)
     with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
         _lib.check(lib.matris_seg_sum2(grp.n_seg, rows, _p(x), ldx, col_off, _p(grp.rowptr), _p(grp.perm), scale,
@@ -611,20 +622,38 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     return out, ret_p, ret_z, res_out
 
 
-def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None, acc0: bool = False, res_w=None):
+def gmlp_tile_rows() -> int:
+    """Rows per GatedMLP work-group tile (the tile of matris_gmlp_bwd_runs's partials)."""
+    return int(_lib.load().matris_gmlp_tile_rows())
+
+
+def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None, acc0: bool = False, res_w=None,
+                 runs=None):
     """matris_gmlp_bwd.  Without g_x0 returns g_x [M, K]; with g_x0 source 0's gradient
     goes (accumulated if acc0, plus res_w * g if res_w) to g_x0 and the other columns to
-    g_x [M, K-128] (allocated when not given; None when K == 128)."""
+    g_x [M, K-128] (allocated when not given; None when K == 128).
+    runs = (key, blk): source block blk, gathered through `key` (int32 [M], ascending),
+    leaves as tile-run partial sums (matris_gmlp_bwd_runs), to be completed by
+    seg_sum_raw(..., tile_rows=gmlp_tile_rows())."""
     lib = _lib.load()
     M = p.shape[0]
     if g_x is None and not (g_x0 is not None and K == D):
         g_x = _rows(M, K - (D if g_x0 is not None else 0), g.device)
-    # algorithmic bytes: g_out, p, z (and the accumulated source-0 block) read once, g_x written once
+    # algorithmic bytes: g_out, p, z (and the accumulated source-0 block) read once, g_x
+    # written once; a run-summed block: its key read, at least one partial row per tile
     nbytes = 4 * M * (D + 2 * 256 + (D if (g_x0 is not None and acc0) else 0) + K)
+    if runs is not None:
+        nbytes += 4 * M - 4 * D * M + 4 * D * -(-M // gmlp_tile_rows())
     with _timed("gmlp_bwd", (M, K, nbytes)):
-        _lib.check(lib.matris_gmlp_bwd(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)),
-                                       _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w),
-                                       mode, _stream()), "matris_gmlp_bwd")
+        args = (M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)), _p(pack.nc),
+                _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w))
+        if runs is None:
+            _lib.check(lib.matris_gmlp_bwd(*args, mode, _stream()), "matris_gmlp_bwd")
+        else:
+            key, blk = runs
+            if key.dtype != torch.int32 or key.numel() != M or not key.is_contiguous():
+                raise ValueError("gmlp_bwd_raw: runs key must be a contiguous int32 tensor of one entry per row")
+            _lib.check(lib.matris_gmlp_bwd_runs(*args, _p(key), int(blk), mode, _stream()), "matris_gmlp_bwd_runs")
     return g_x
 
 

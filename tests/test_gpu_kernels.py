@@ -492,6 +492,65 @@ def test_discarded_saves_leave_outputs_unchanged():
     assert torch.equal(o, o2) and q2.shape == q.shape
 
 
+def _sorted_keys(M, S, seed):
+    """Ascending int32 keys in [0, S): random segment lengths with empty segments, one-row
+    segments and one segment of 200 rows (spanning four 64-row tiles when M allows)."""
+    g = torch.Generator().manual_seed(seed)
+    k = torch.sort(torch.randint(0, S, (M,), generator=g)).values
+    if M > 400 and S > 10:
+        k[100:300] = k[100]
+        k = torch.sort(k).values
+    return k.to(torch.int32)
+
+
+@pytest.mark.parametrize("mode", ["f16x3", "fp32", "bf16x6"])
+@pytest.mark.parametrize("K,blk,with_x0", [(384, 1, True), (512, 2, True), (384, 1, False), (384, 0, False)])
+@pytest.mark.parametrize("M,S", [(5000, 300), (4097, 20), (64, 3), (1, 1), (70001, 9000)])
+def test_gmlp_bwd_tile_run_sums(M, S, K, blk, with_x0, mode):
+    """matris_gmlp_bwd_runs + matris_seg_sum2_runs: the segment sums of the run-summed
+    block (rows ascending by key) equal the fp64 sums of the plain backward's rows
+    (matris_gmlp_bwd) to fp32 rounding (1e-5 of the largest), also paired with a second,
+    permuted source in one pass; every other output is bit-identical."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + K)
+        mod = _ShimGated(_TorchGMLP(K)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        srcs = [torch.randn(M, 128, device=DEV) for _ in range(K // 128)]
+        _, p, z, _ = ops.gmlp_fwd_raw(pack, srcs, [None] * (K // 128), M, mm)
+        g = torch.randn(M, 128, device=DEV)
+        key = _sorted_keys(M, S, M).to(DEV)
+        base = torch.randn(M, 128, device=DEV)
+        x0a, x0b = (base.clone(), base.clone()) if with_x0 else (None, None)
+        gxa = ops.gmlp_bwd_raw(pack, g, p, z, K, mm, g_x0=x0a, acc0=with_x0)
+        gxb = ops.gmlp_bwd_raw(pack, g, p, z, K, mm, g_x0=x0b, acc0=with_x0, runs=(key, blk))
+        c = (blk - (1 if with_x0 else 0)) * 128
+        ld = gxa.shape[1]
+        keep = torch.ones(ld, dtype=torch.bool)
+        keep[c:c + 128] = False
+        assert torch.equal(gxa[:, keep.to(DEV)], gxb[:, keep.to(DEV)])
+        if with_x0:
+            assert torch.equal(x0a, x0b)
+        grp = ops.Grouping.build(key, S, sorted_rows=True)
+        T = ops.gmlp_tile_rows()
+        got = ops.seg_sum_raw(gxb, grp, ldx=ld, col_off=c, tile_rows=T)
+        ref = torch.zeros(S, 128, dtype=torch.float64).index_add_(0, key.long().cpu(), gxa[:, c:c + 128].double().cpu())
+        assert _rel(got, ref) < 1e-5
+        # paired with a second, permuted source (the source-bond block of the line graph)
+        other = 0 if c else 128
+        skey = _keys(M, S, M + 1).to(DEV)
+        sgrp = ops.Grouping.build(skey, S)
+        acc = torch.randn(S, 128, device=DEV)
+        got2 = ops.seg_sum_raw(gxb, grp, ldx=ld, col_off=c, tile_rows=T, out=acc.clone(), accumulate=True,
+                               second=(gxa, sgrp, 1.0, ld, other))
+        ref2 = (acc.double().cpu() + ref).index_add_(0, skey.long().cpu(), gxa[:, other:other + 128].double().cpu())
+        assert _rel(got2, ref2) < 1e-5
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode,tol", _MODES)
 @pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097, 140001])
 def test_ffn_fwd_bwd(M, mode, tol):
