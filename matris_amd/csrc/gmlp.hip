@@ -95,8 +95,18 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     __shared__ __align__(16) float smem[BM * LDH];
     uint4 *Xp = reinterpret_cast<uint4 *>(smem);  // two chunk buffers (<= 24 KB)
     float *Ts = smem;                             // [BM, 256] tile: p, then h, then z
+    // Per-column vectors b1 [256], b2 [256], norm_c [128], norm_g [128], res_w [128] in LDS:
+    // read there, they never wait behind this work-group's global stores (a load from
+    // global memory waits for every earlier store of its wave).  Loaded into registers at
+    // kernel start, written to LDS once the projected-row gather is in flight.
+    __shared__ __align__(16) float cvec[896];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    float cv[4];  // cvec entries tid, tid + 256, tid + 512 and (tid < 128) tid + 768
+    cv[0] = b1 ? b1[tid] : 0.f;
+    cv[1] = b2 ? b2[tid] : 0.f;
+    cv[2] = tid < 128 ? norm_c[tid] : norm_g[tid - 128];
+    cv[3] = (tid < 128 && res_w) ? res_w[tid] : 0.f;
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const int KB = nsrc * (MATRIS_D / 16);  // k-blocks of W1 (none without gathered sources)
     // MODE 2: the accumulator holds s * (W1 x) until scale_acc multiplies by 1/s
@@ -165,6 +175,14 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         __syncthreads();                                                                                 \
     } while (0)
 
+    // GEMM1's first three chunks are requested before the projected-row gather below, so
+    // their latency overlaps it
+    float4 x00, x01;
+    if (nsrc > 0) {
+        GMLP_LOADX(0, x00, x01);
+        GMLP_LOADX(min(1, nchunk - 1) * 32, xa0, xa1);
+        GMLP_LOADX(min(2, nchunk - 1) * 32, xb0, xb1);
+    }
     v16f acc[2][2];
     zero_acc(acc);
     // Projected rows go straight into the accumulator (layout of acc_t_to_lds: row
@@ -206,16 +224,17 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         }
         if (MODE == 2 && nsrc > 0) scale_acc<MODE>(acc, w1up);  // power of two: exact
     }
+    cvec[tid] = cv[0];
+    cvec[256 + tid] = cv[1];
+    cvec[512 + tid] = cv[2];
+    if (tid < 128) cvec[768 + tid] = cv[3];
     if (nsrc > 0) {
         constexpr int BDIST = 3;
         Frag<MODE> bq0[2], bq1[2], bq2[2], bq3[2];
         load_bfrags<MODE, 2>(bq0, W1, 2 * wave, KB, 0, lane);
         load_bfrags<MODE, 2>(bq1, W1, 2 * wave, KB, min(1, KB - 1), lane);
         load_bfrags<MODE, 2>(bq2, W1, 2 * wave, KB, min(2, KB - 1), lane);
-        GMLP_LOADX(0, xa0, xa1);
-        GMLP_STOREX(0, xa0, xa1);
-        GMLP_LOADX(min(1, nchunk - 1) * 32, xa0, xa1);
-        GMLP_LOADX(min(2, nchunk - 1) * 32, xb0, xb1);
+        GMLP_STOREX(0, x00, x01);
         __syncthreads();
 #pragma unroll 1
         for (int c = 0; c < nchunk; c += 2) {  // nchunk = 4 nsrc is even
@@ -233,7 +252,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // fragment units here, as the backward does for g_z / g_p, measured slower: it costs
     // a barrier and 24 more VGPRs for a conversion that two waves share.)
     scale_acc<MODE>(acc, w1s);
-    acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b1);
+    if (nsrc == 0) __syncthreads();  // cvec written (GEMM1's barriers cover it otherwise)
+    acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, cvec);
     __syncthreads();
 #pragma unroll
     for (int it = 0; it < (BM * 64) / 256; ++it) {
@@ -273,12 +293,12 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     // c of a row holds core columns 4c .. 4c+3 and 64 + 4c .. +3 and the same gate
     // columns, so each store instruction writes 256 contiguous bytes of a row; each
     // RMSNorm sum is a 16-lane DPP sum
-    acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, b2);
+    acc_t_to_lds<2, 2>(acc, Ts, LDH, wave * 64, lane, cvec + 256);
     __syncthreads();
-    const float4 wc0 = *reinterpret_cast<const float4 *>(norm_c + c4);
-    const float4 wc1 = *reinterpret_cast<const float4 *>(norm_c + 64 + c4);
-    const float4 wg0 = *reinterpret_cast<const float4 *>(norm_g + c4);
-    const float4 wg1 = *reinterpret_cast<const float4 *>(norm_g + 64 + c4);
+    const float4 wc0 = *reinterpret_cast<const float4 *>(cvec + 512 + c4);
+    const float4 wc1 = *reinterpret_cast<const float4 *>(cvec + 512 + 64 + c4);
+    const float4 wg0 = *reinterpret_cast<const float4 *>(cvec + 640 + c4);
+    const float4 wg1 = *reinterpret_cast<const float4 *>(cvec + 640 + 64 + c4);
 #pragma unroll
     for (int rr = 0; rr < BM / 16; ++rr) {
         const int row = wave * (BM / 4) + rr * 4 + (lane >> 4);
@@ -315,8 +335,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             *reinterpret_cast<float4 *>(orow) = o0;
             *reinterpret_cast<float4 *>(orow + 64) = o1;
             if (res_out) {
-                const float4 w0 = *reinterpret_cast<const float4 *>(res_w + c4);
-                const float4 w1 = *reinterpret_cast<const float4 *>(res_w + 64 + c4);
+                const float4 w0 = *reinterpret_cast<const float4 *>(cvec + 768 + c4);
+                const float4 w1 = *reinterpret_cast<const float4 *>(cvec + 768 + 64 + c4);
                 const float4 x0 = rx0[rr], x1 = rx1[rr];
                 float *ro = res_out + grow * MATRIS_D + c4;
                 *reinterpret_cast<float4 *>(ro) = make_float4(o0.x + w0.x * x0.x, o0.y + w0.y * x0.y, o0.z + w0.z * x0.z,
