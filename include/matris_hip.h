@@ -401,11 +401,12 @@ int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, 
 /* Attention projection pair (interaction_block.py:33-38, 110-111):
  * out0 = x W[0:128]^T (source_weight_linear), out1 = x W[128:256]^T (target);
  * wp = pack of W = [W_s; W_t] ([256,128]).
- * bwd: g_x = g0 W[0:128] + g1 W[128:256] (+ res_w * res when res is non-NULL) with
- * wtp = pack of W^T ([128,256]). */
+ * bwd: g_x = g0 W[0:128] + g1 W[128:256] (+ res_w * res when res is non-NULL), plus
+ * g_x's previous contents (added last) when accumulate, with wtp = pack of W^T
+ * ([128,256]). */
 int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, float *out1, int mode, void *stream);
 int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, const float *res,
-                    const float *res_w, int mode, void *stream);
+                    const float *res_w, int accumulate, int mode, void *stream);
 
 /* Three-body embedding (row E3's consumer): tb = SiLU(Ws (Wa b)) for b [m, 16] the angle
  * basis, wa = Wa [128, 16] row-major fp32 (angle_embedding, no bias), wsp = Ws [128, 128]

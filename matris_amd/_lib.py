@@ -116,7 +116,7 @@ _SIGS = {
     "matris_ffn_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
-    "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "matris_tb_embed_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
     "matris_tb_embed_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _P]),
 }

@@ -466,20 +466,34 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
             wc[0] = a0.x; wc[1] = a0.y; wc[2] = a0.z; wc[3] = a0.w; wc[4] = a1.x; wc[5] = a1.y; wc[6] = a1.z; wc[7] = a1.w;
             wg[0] = b0.x; wg[1] = b0.y; wg[2] = b0.z; wg[3] = b0.w; wg[4] = b1.x; wg[5] = b1.y; wg[6] = b1.z; wg[7] = b1.w;
         }
+        // every row group's z / g_out loads are requested before any is used: unconditional
+        // (rows past M read row M-1, then count as zeros) so that they all stay in flight
+        float4 ld_z[BM / 16][4], ld_g[BM / 16][2];
+#pragma unroll
+        for (int rr = 0; rr < BM / 16; ++rr) {
+            const int64_t m = min(m0 + wave * (BM / 4) + rr * 4 + (lane >> 4), M - 1);
+            const float4 *zr = reinterpret_cast<const float4 *>(Z + m * 256 + c4);
+            const float4 *gr = reinterpret_cast<const float4 *>(g_out + m * MATRIS_D + c4);
+            ld_z[rr][0] = zr[0];
+            ld_z[rr][1] = zr[16];
+            ld_z[rr][2] = zr[MATRIS_D / 4];
+            ld_z[rr][3] = zr[MATRIS_D / 4 + 16];
+            ld_g[rr][0] = gr[0];
+            ld_g[rr][1] = gr[16];
+        }
 #pragma unroll
         for (int rr = 0; rr < BM / 16; ++rr) {
             const int row = wave * (BM / 4) + rr * 4 + (lane >> 4);
             const int64_t m = m0 + row;
             float zc[8], zg[8], go[8];
-            if (m < M) {
-                const float4 *zr = reinterpret_cast<const float4 *>(Z + m * 256 + c4);
-                const float4 *gr = reinterpret_cast<const float4 *>(g_out + m * MATRIS_D + c4);
-                const float4 z0 = zr[0], z1 = zr[16], y0 = zr[MATRIS_D / 4], y1 = zr[MATRIS_D / 4 + 16];
-                const float4 g0 = gr[0], g1 = gr[16];
+            {
+                const float4 z0 = ld_z[rr][0], z1 = ld_z[rr][1], y0 = ld_z[rr][2], y1 = ld_z[rr][3];
+                const float4 g0 = ld_g[rr][0], g1 = ld_g[rr][1];
                 zc[0] = z0.x; zc[1] = z0.y; zc[2] = z0.z; zc[3] = z0.w; zc[4] = z1.x; zc[5] = z1.y; zc[6] = z1.z; zc[7] = z1.w;
                 zg[0] = y0.x; zg[1] = y0.y; zg[2] = y0.z; zg[3] = y0.w; zg[4] = y1.x; zg[5] = y1.y; zg[6] = y1.z; zg[7] = y1.w;
                 go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w; go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
-            } else {
+            }
+            if (m >= M) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) zc[e] = zg[e] = go[e] = 0.f;
             }

@@ -34,10 +34,10 @@ __device__ __forceinline__ void stage_tile128(float *dst, const float *__restric
 }
 
 // Copy an LDS tile out to rows of dst; with res non-NULL, dst = tile + res_w * res (rows of
-// 128, per-column weight res_w).
+// 128, per-column weight res_w); with accumulate, dst's previous contents are added last.
 __device__ __forceinline__ void store_tile128(const float *tile, float *__restrict__ dst, int64_t ld, int64_t m0,
                                               int64_t M, int tid, const float *__restrict__ res = nullptr,
-                                              const float *__restrict__ res_w = nullptr) {
+                                              const float *__restrict__ res_w = nullptr, int accumulate = 0) {
 #pragma unroll
     for (int it = 0; it < (BM * 32) / 256; ++it) {
         const int q = it * 256 + tid;
@@ -49,7 +49,12 @@ __device__ __forceinline__ void store_tile128(const float *tile, float *__restri
                 const float4 w = *reinterpret_cast<const float4 *>(res_w + c4);
                 v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
             }
-            *reinterpret_cast<float4 *>(dst + (m0 + r) * ld + c4) = v;
+            float4 *o = reinterpret_cast<float4 *>(dst + (m0 + r) * ld + c4);
+            if (accumulate) {
+                const float4 a = *o;
+                v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+            }
+            *o = v;
         }
     }
 }
@@ -813,7 +818,8 @@ template <int MODE>
 __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float *__restrict__ g0,
                                                           const float *__restrict__ g1, const uint4 *__restrict__ Wt,
                                                           float *__restrict__ g_x, const float *__restrict__ res,
-                                                          const float *__restrict__ res_w, unsigned *range_flag) {
+                                                          const float *__restrict__ res_w, int accumulate,
+                                                          unsigned *range_flag) {
     // Wt = W^T ([128, 256]) packed: g_x[m][k] = sum_n g[m][n] Wt[k][n], k-blocks 0..7
     // pair with g0, 8..15 with g1; g0 then g1 pass through the one LDS tile
     __shared__ __align__(16) float T[BM * LDT];
@@ -855,7 +861,7 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
-    store_tile128(T, g_x, MATRIS_D, m0, M, tid, res, res_w);
+    store_tile128(T, g_x, MATRIS_D, m0, M, tid, res, res_w, accumulate);
     report_range<MODE>(amax, range_flag);
 }
 
@@ -998,11 +1004,11 @@ extern "C" int matris_gmlp_project(int64_t m, const float *x, const void *wp, in
 }
 
 extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x,
-                               const float *res, const float *res_w, int mode, void *stream) {
+                               const float *res, const float *res_w, int accumulate, int mode, void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {g0, g1, wtp, g_x})) return MATRIS_E_ARG;
     if (res && (((uintptr_t)res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
-    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x, res, res_w);
+    MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x, res, res_w, accumulate);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -756,14 +756,17 @@ def pair_fwd_raw(pack: _WeightPack, x, mode: int):
     return o0, o1
 
 
-def pair_bwd_raw(pack: _WeightPack, g0, g1, mode: int, res=None, res_w=None):
-    """g0 W0 + g1 W1 (+ res_w * res) of matris_pair_bwd."""
+def pair_bwd_raw(pack: _WeightPack, g0, g1, mode: int, res=None, res_w=None, out=None, accumulate: bool = False):
+    """g0 W0 + g1 W1 (+ res_w * res) of matris_pair_bwd, into `out` (allocated when None;
+    its previous contents added last when accumulate)."""
     lib = _lib.load()
     M = g0.shape[0]
-    g_x = _rows(M, D, g0.device)
+    if accumulate and out is None:
+        raise ValueError("pair_bwd_raw: accumulate needs out")
+    g_x = _rows(M, D, g0.device) if out is None else out
     with _timed("pair_bwd", (M,)):
         _lib.check(lib.matris_pair_bwd(M, _p(g0), _p(g1), _p(pack.b("cat_t", mode)), _p(g_x), _p(res), _p(res_w),
-                                       mode, _stream()), "matris_pair_bwd")
+                                       int(accumulate), mode, _stream()), "matris_pair_bwd")
     return g_x
 
 

@@ -95,7 +95,7 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_ffn_fwd(10, v16, v16, v16, v16, None, v16, None, 6, None) == -1001
     assert lib.matris_ffn_bwd(10, v16, None, v16, v16, v16, None, None, 6, None) == -1001
     assert lib.matris_pair_fwd(10, v16, v16, v16, v16, 1, None) == -1001
-    assert lib.matris_pair_bwd(-1, v16, v16, v16, v16, None, None, 0, None) == -1001
+    assert lib.matris_pair_bwd(-1, v16, v16, v16, v16, None, None, 0, 0, None) == -1001
     # attention backward: gradient row stride below 128; envelope aggregation: null operand
     assert lib.matris_attn_bwd(10, 5, v16, v16, 128, None, v16, v16, v16, v16, v16, v16, v16, v16, v16, 64, v16,
                                v16, v16, None, None) == -1001
