@@ -419,6 +419,18 @@ int matris_tb_embed_fwd(int64_t m, const float *basis, const float *wa, const vo
 int matris_tb_embed_bwd(int64_t m, const float *basis, const float *g_tb, const float *wa, const void *wsp,
                         const void *wstp, float *g_basis, int mode, void *stream);
 
+/* ------------------------------------------------------------------------------------
+ * SiLU derivatives: the reference's torch op library matris_op (op/src/RegisterOp.cpp:
+ * 9-13, Opdefine.h:7-10; arithmetic of op/fused_silu_op.py:5-28), element-wise over n
+ * floats (any layout, 16-byte vectors when every pointer is aligned):
+ *   matris_silu_bwd:      out = dgrad * s'(x)                (fuse_silu_bwd)
+ *   matris_silu_grad_bwd: ggo = ggi * s'(x), gx = ggi * go * s''(x)  (fuse_silu_grad_bwd)
+ * with s(x) = x sigmoid(x).  torch.ops.matris_op.fuse_silu_bwd / fuse_silu_grad_bwd
+ * (matris_amd.torch_ops) wrap them with the reference's schemas. */
+int matris_silu_bwd(int64_t n, const float *dgrad, const float *x, float *out, void *stream);
+int matris_silu_grad_bwd(int64_t n, const float *ggi, const float *go, const float *x, float *ggo, float *gx,
+                         void *stream);
+
 #ifdef __cplusplus
 }
 #endif

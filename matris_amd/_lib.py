@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(_HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(_HERE), "include")
 LIB_PATH = os.path.join(CSRC, "libmatris_hip.so")
-SOURCES = ["graph.hip", "segment.hip", "gmlp.hip", "mlp.hip", "basis.hip"]
+SOURCES = ["graph.hip", "segment.hip", "gmlp.hip", "mlp.hip", "basis.hip", "silu.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
              "-packed-fp32-ops"]
@@ -106,6 +106,8 @@ _SIGS = {
     "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_bwd_runs": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _P, _I, _I, _P]),
     "matris_gmlp_tile_rows": (_I, []),
+    "matris_silu_bwd": (_I, [_I64, _P, _P, _P, _P]),
+    "matris_silu_grad_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P]),
     "matris_bessel_fwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _P]),
     "matris_bessel_bwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _I, _P, _P]),
     "matris_sbf_fwd": (_I, [_I64, _P, _P, _P, _D, _P, _P]),

@@ -102,6 +102,22 @@ class _timed:
             _TIMING.setdefault(self.name, []).append((self.ev[0], self.ev[1], self.info))
 
 
+_EXACT_ROWS = [False]
+
+
+class exact_rows:
+    """Context manager: _rows allocates exactly n rows (no view of a larger block) -- for
+    outputs handed to torch's dispatcher as custom-op results."""
+
+    def __enter__(self):
+        self.prev = _EXACT_ROWS[0]
+        _EXACT_ROWS[0] = True
+        return self
+
+    def __exit__(self, *exc):
+        _EXACT_ROWS[0] = self.prev
+
+
 def _rows(n: int, cols: int, device, dtype=torch.float32) -> torch.Tensor:
     """An uninitialised [n, cols] tensor whose storage is rounded up to a coarse row count:
     the first n rows of a [cap(n), cols] allocation, cap(n) = n below 2^16 rows, else n
@@ -110,7 +126,7 @@ def _rows(n: int, cols: int, device, dtype=torch.float32) -> torch.Tensor:
     sizes the caching allocator's blocks end up a little too small for the next step's
     tensors and, for a large cell, the pool fills with unusable pieces.  Quantised sizes
     let each step reuse the previous step's blocks."""
-    if n >= (1 << 16):
+    if n >= (1 << 16) and not _EXACT_ROWS[0]:
         g = 1 << (n.bit_length() - 6)
         cap = (n + g - 1) // g * g
         return torch.empty(cap, cols, dtype=dtype, device=device)[:n]
@@ -461,6 +477,25 @@ class GmlpPack(_PackCache):
             self.eps = float(torch.finfo(torch.float32).eps if eps is None else eps)
 
         self._refresh(params, build)
+        return self
+
+    def get_tensors(self, w1, b1, w2, b2, norm_c, norm_g, eps: float):
+        """The same pack from plain tensors: w1 [256, K] (core rows, then gate rows), b1
+        [256] or None, w2 [256, 128] (core, then gate), b2 [256] or None, norm weights [128]."""
+        params = tuple(t for t in (w1, b1, w2, b2, norm_c, norm_g) if t is not None)
+
+        def build():
+            W1, W2 = w1.detach().float().contiguous(), w2.detach().float().contiguous()
+            self.mats = {"w1": W1, "w2": W2, "w1t": W1.t().contiguous(),
+                         "w2bt": torch.cat([W2[:D].t(), W2[D:].t()], 0).contiguous()}
+            z = torch.zeros(256, dtype=torch.float32, device=w1.device)
+            self.b1 = (b1.detach().float() if b1 is not None else z).contiguous()
+            self.b2 = (b2.detach().float() if b2 is not None else z).contiguous()
+            self.nc = norm_c.detach().float().contiguous()
+            self.ng = norm_g.detach().float().contiguous()
+
+        self._refresh(params, build)
+        self.eps = float(eps)
         return self
 
     def b_blocks(self, blocks: tuple, mode: int):
