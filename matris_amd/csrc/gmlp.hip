@@ -22,7 +22,9 @@
 //
 // Backward (input gradients only) recomputes the norm/activation Jacobians row-wise
 // from z, then runs g_h = g_z W2 and g_x = (g_h * SiLU'(p)) W1 through the same MFMA
-// tiling, with packed transposed weights.  In the two-plane modes g_z and g_p are stored
+// tiling, with packed transposed weights.  In the two-plane modes it runs with eight
+// waves per 64-row tile (gmlp_bwd8_kernel: 32 columns per wave, 128 registers, so a CU
+// holds 16 waves); MODE 6 keeps four (gmlp_bwd_kernel).  In the two-plane modes g_z and g_p are stored
 // in LDS already split into fragment units by the pass that produces them, so neither
 // GEMM converts anything (g_p is otherwise re-split by every wave of every column pass).
 //
@@ -713,6 +715,222 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
     report_range<MODE>(amax, range_flag);
 }
 
+
+// The backward with eight waves per 64-row tile (two-plane modes): the same three phases
+// as gmlp_bwd_kernel with each wave owning 8 rows in phase 1 and one 32-column tile in
+// phases 2 and 3 -- half the registers per wave, so a CU holds 16 waves instead of 8 at
+// the same LDS per work-group.  Phase 3 runs 256-column passes from the top of K, source
+// 0's block last (for K = 384 / 128 only waves 0-3 have columns in the last pass).
+template <int MODE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void gmlp_bwd8_kernel(int64_t M, int K, const float *__restrict__ g_out,
+                                                           const float *__restrict__ P, const float *__restrict__ Z,
+                                                           const uint4 *__restrict__ W1t,
+                                                           const uint4 *__restrict__ W2t,
+                                                           const float *__restrict__ norm_c,
+                                                           const float *__restrict__ norm_g, float eps,
+                                                           float *__restrict__ g_x, float *__restrict__ g_x0,
+                                                           int acc0, const float *__restrict__ res_w,
+                                                           const int32_t *__restrict__ run_key, int run_blk,
+                                                           unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes");
+    __shared__ __align__(16) float G[BM * LDH];
+    __shared__ __align__(16) float rinv[BM];
+    uint4 *Gf = reinterpret_cast<uint4 *>(G);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float w1s = take_wscale<MODE>(W1t), w2s = take_wscale<MODE>(W2t);
+    float amax = 0.f;
+    const int run_k = run_key ? run_key[min(m0 + lane, M - 1)] : 0;
+
+    // phase 1: wave w owns rows [8w, 8w + 8), 16 lanes per row
+    {
+        const int c4 = (lane & 15) * 4;
+        float wc[8], wg[8];
+        {
+            const float4 a0 = *reinterpret_cast<const float4 *>(norm_c + c4);
+            const float4 a1 = *reinterpret_cast<const float4 *>(norm_c + 64 + c4);
+            const float4 b0 = *reinterpret_cast<const float4 *>(norm_g + c4);
+            const float4 b1 = *reinterpret_cast<const float4 *>(norm_g + 64 + c4);
+            wc[0] = a0.x; wc[1] = a0.y; wc[2] = a0.z; wc[3] = a0.w; wc[4] = a1.x; wc[5] = a1.y; wc[6] = a1.z; wc[7] = a1.w;
+            wg[0] = b0.x; wg[1] = b0.y; wg[2] = b0.z; wg[3] = b0.w; wg[4] = b1.x; wg[5] = b1.y; wg[6] = b1.z; wg[7] = b1.w;
+        }
+#pragma unroll 1
+        for (int rr = 0; rr < BM / 32; ++rr) {
+            const int row = wave * (BM / 8) + rr * 4 + (lane >> 4);
+            const int64_t m = m0 + row;
+            float zc[8], zg[8], go[8];
+            {
+                const int64_t ml = min(m, M - 1);  // rows past M read row M-1, then count as zeros
+                const float4 *zr = reinterpret_cast<const float4 *>(Z + ml * 256 + c4);
+                const float4 *gr = reinterpret_cast<const float4 *>(g_out + ml * MATRIS_D + c4);
+                const float4 z0 = zr[0], z1 = zr[16], y0 = zr[MATRIS_D / 4], y1 = zr[MATRIS_D / 4 + 16];
+                const float4 g0 = gr[0], g1 = gr[16];
+                zc[0] = z0.x; zc[1] = z0.y; zc[2] = z0.z; zc[3] = z0.w; zc[4] = z1.x; zc[5] = z1.y; zc[6] = z1.z; zc[7] = z1.w;
+                zg[0] = y0.x; zg[1] = y0.y; zg[2] = y0.z; zg[3] = y0.w; zg[4] = y1.x; zg[5] = y1.y; zg[6] = y1.z; zg[7] = y1.w;
+                go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w; go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
+            }
+            if (m >= M) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) zc[e] = zg[e] = go[e] = 0.f;
+            }
+            float sc2 = 0.f, sg2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sc2 += zc[e] * zc[e];
+                sg2 += zg[e] * zg[e];
+            }
+            const float rc = rsqrtf(row16_sum(sc2) * (1.0f / MATRIS_D) + eps);
+            const float rg = rsqrtf(row16_sum(sg2) * (1.0f / MATRIS_D) + eps);
+            float nc[8], ng[8], gnc[8], gng[8], dcs = 0.f, dgs = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                nc[e] = zc[e] * rc;
+                ng[e] = zg[e] * rg;
+                const float ac = nc[e] * wc[e], ag = ng[e] * wg[e];
+                const float sc = sigm_f(ac), gate = sigm_f(ag);
+                gnc[e] = go[e] * gate * (sc * (1.f + ac * (1.f - sc))) * wc[e];
+                gng[e] = go[e] * (ac * sc) * (gate * (1.f - gate)) * wg[e];
+                dcs += gnc[e] * nc[e];
+                dgs += gng[e] * ng[e];
+            }
+            const float dc = row16_sum(dcs) * (1.0f / MATRIS_D), dg = row16_sum(dgs) * (1.0f / MATRIS_D);
+            float4 vc[2], vg[2];
+#pragma unroll
+            for (int e4 = 0; e4 < 2; ++e4) {
+                vc[e4] = make_float4((gnc[4 * e4] - nc[4 * e4] * dc) * rc, (gnc[4 * e4 + 1] - nc[4 * e4 + 1] * dc) * rc,
+                                     (gnc[4 * e4 + 2] - nc[4 * e4 + 2] * dc) * rc,
+                                     (gnc[4 * e4 + 3] - nc[4 * e4 + 3] * dc) * rc);
+                vg[e4] = make_float4((gng[4 * e4] - ng[4 * e4] * dg) * rg, (gng[4 * e4 + 1] - ng[4 * e4 + 1] * dg) * rg,
+                                     (gng[4 * e4 + 2] - ng[4 * e4 + 2] * dg) * rg,
+                                     (gng[4 * e4 + 3] - ng[4 * e4 + 3] * dg) * rg);
+            }
+            if constexpr (MODE == 2) {
+                const float mx = abs_max4(abs_max4(abs_max4(abs_max4(0.f, vc[0]), vc[1]), vg[0]), vg[1]);
+                const RowScale rs = row_scale(row16_max(mx));
+#pragma unroll
+                for (int e4 = 0; e4 < 2; ++e4) {
+                    vc[e4] = mul4(vc[e4], rs.s);
+                    vg[e4] = mul4(vg[e4], rs.s);
+                }
+                if ((lane & 15) == 0) rinv[row] = rs.inv * w1s;
+            }
+            amax = frag_amax<MODE>(frag_amax<MODE>(amax, vc[0], vc[1]), vg[0], vg[1]);
+            const int rb = (row >> 5) * 16, fr = row & 31;
+#pragma unroll
+            for (int e4 = 0; e4 < 2; ++e4) {
+                const int c = c4 + 64 * e4;
+                const int fl = fr + 32 * ((c >> 3) & 1), hh = (c >> 2) & 1;
+                frag_put4<MODE>(Gf, rb + (c >> 4), fl, hh, vc[e4]);
+                frag_put4<MODE>(Gf, rb + 8 + (c >> 4), fl, hh, vg[e4]);
+            }
+        }
+    }
+    __syncthreads();
+
+    // phase 2: g_h = g_z W2, wave w -> columns [32w, 32w + 32) (block w / 4), then
+    // g_p = g_h * SiLU'(p) written back pre-split
+    const int blk = wave >> 2;
+    const int nrows = (int)min((int64_t)BM, M - m0);
+    const float *__restrict__ Pt = P + m0 * 256;
+    {
+        v16f acc[2][1];
+        zero_acc(acc);
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Gf, 16, blk * 8, W2t, wave, MATRIS_D / 16, 0, lane);
+        scale_acc<MODE>(acc, w2s);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int row = rt * 32 + l32;
+            const float *pr = Pt + (row < nrows ? row : 0) * 256 + wave * 32 + 4 * h;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 pv = *reinterpret_cast<const float4 *>(pr + 8 * j);
+                acc[rt][0][4 * j] *= dsilu_f(pv.x);
+                acc[rt][0][4 * j + 1] *= dsilu_f(pv.y);
+                acc[rt][0][4 * j + 2] *= dsilu_f(pv.z);
+                acc[rt][0][4 * j + 3] *= dsilu_f(pv.w);
+            }
+        }
+        __syncthreads();  // every wave is done reading g_z
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = make_float4(acc[rt][0][4 * j], acc[rt][0][4 * j + 1], acc[rt][0][4 * j + 2],
+                                             acc[rt][0][4 * j + 3]);
+                amax = frag_amax<MODE>(amax, v, v);
+                frag_put4<MODE>(Gf, rt * 16 + 2 * wave + (j >> 1), l32 + 32 * (j & 1), h, v);
+            }
+    }
+    __syncthreads();
+
+    // phase 3: g_x = g_p W1 in 256-column passes from the top of K; the last pass holds
+    // source 0 ([0, 128)), whose gradient goes through LDS when g_x0 or res_w is given
+    const int coff = g_x0 ? MATRIS_D : 0;
+    const int ldr = K - coff;
+    float *__restrict__ gxr = g_x ? g_x + m0 * ldr : nullptr;
+    const bool epi0 = g_x0 != nullptr || res_w != nullptr;
+    const int run_prev = __shfl(run_k, (lane + 63) & 63, 64);
+    const uint64_t run_starts =
+        run_key ? (uint64_t)__ballot(lane < nrows && (lane == 0 || run_k != run_prev)) : 0;
+    const int run_c0 = run_blk * MATRIS_D;
+    int top = K;
+    while (top > 0) {
+        const bool last = top <= 256;
+        const int base = last ? 0 : top - 256;
+        const int col0 = base + 32 * wave;
+        const bool active = col0 < top;
+        // an opaque copy of the row stride: the store addresses below are computed in this
+        // pass instead of being hoisted out of the loop (32 live 64-bit offsets would spill)
+        int ldp = ldr;
+        asm volatile("" : "+s"(ldp));
+        v16f a2[2][1];
+        zero_acc(a2);
+        if (active) gemm_frag_packed<MODE, 2, 1, 256 / 16>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
+        if constexpr (MODE == 2)
+            unscale_acc_rows<MODE, 1>(a2, rinv, h);  // 2^-k w1s per row
+        else
+            scale_acc<MODE>(a2, w1s);
+        if (active) {
+            if (run_key && col0 >= run_c0 && col0 < run_c0 + MATRIS_D)
+                store_acc_runs<1>(a2, gxr, ldp, col0 - coff, run_starts, nrows, lane);
+            else if (col0 >= MATRIS_D || !epi0)
+                store_acc_rows<1>(a2, gxr, ldp, col0 - coff, nrows, lane);
+        }
+        if (last && epi0) {
+            __syncthreads();  // all waves are done reading G
+            if (active && col0 < MATRIS_D) acc_to_lds<1>(a2, G, LDH, col0, lane);
+        }
+        top = base;
+    }
+    if (epi0) {
+        __syncthreads();
+        float *__restrict__ gx0 = g_x0 ? g_x0 + m0 * MATRIS_D : gxr;
+        const int ld0 = g_x0 ? MATRIS_D : ldr;
+        const float *__restrict__ got = g_out + m0 * MATRIS_D;
+#pragma unroll
+        for (int it = 0; it < (BM * 32) / 512; ++it) {
+            const int q = it * 512 + tid;
+            const int r = q >> 5, c4 = (q & 31) * 4;
+            if (r < nrows) {
+                float4 v = *reinterpret_cast<const float4 *>(G + r * LDH + c4);
+                if (res_w) {
+                    const float4 w = *reinterpret_cast<const float4 *>(res_w + c4);
+                    const float4 x = *reinterpret_cast<const float4 *>(got + r * MATRIS_D + c4);
+                    v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
+                }
+                float4 *o = reinterpret_cast<float4 *>(gx0 + r * ld0 + c4);
+                if (acc0) {
+                    const float4 p0 = *o;
+                    v.x += p0.x; v.y += p0.y; v.z += p0.z; v.w += p0.w;
+                }
+                *o = v;
+            }
+        }
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
@@ -795,8 +1013,19 @@ static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p,
     const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
     unsigned *flag = nullptr;
     if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
-    MATRIS_MODE_DISPATCH(gmlp_bwd_kernel, grid, st, m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                         res_w, run_key, run_blk, flag);
+    if (mode == 6) {
+        gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
+                                                 res_w, run_key, run_blk, flag);
+    } else if (mode == 0) {
+        gmlp_bwd8_kernel<0><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
+                                                  res_w, run_key, run_blk, flag);
+    } else if (mode == 2) {
+        gmlp_bwd8_kernel<2><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
+                                                  res_w, run_key, run_blk, flag);
+    } else {
+        gmlp_bwd8_kernel<3><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
+                                                  res_w, run_key, run_blk, flag);
+    }
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
