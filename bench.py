@@ -105,11 +105,11 @@ def _gmlp_flops(M, K):
 # Keys: (launch name, config); a mean over that family's launches in one step where the
 # shapes differ.
 TRAFFIC_BYTES = {
-    ("gmlp_bwd", "C3"): 569.2e6,       # all four launch shapes, 420 launches; 1334.3 MB at M = A
-    ("gmlp_fwd", "C3"): 476.8e6,       # all four launch shapes, 420 launches; 1106.0 MB at M = A
+    ("gmlp_bwd", "C3"): 488.9e6,       # all four launch shapes, 420 launches; 1128.9 MB at M = A
+    ("gmlp_fwd", "C3"): 465.7e6,       # all four launch shapes, 420 launches; 1078.4 MB at M = A
     ("attn_fwd_line", "C3"): 580.4e6,  # 538.0 read + 42.5 written
-    ("attn_fwd", "C2"): 4062.1e6,
-    ("attn_bwd", "C2"): 8431.5e6,
+    ("attn_fwd", "C2"): 4061.9e6,
+    ("attn_bwd", "C2"): 8451.6e6,
     ("seg_sum", "C2"): 1048.1e6,
 }
 
