@@ -345,18 +345,23 @@ int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const 
                     const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x, float *g_x0,
                     int acc0, const float *res_w, int mode, void *stream);
 
-/* matris_gmlp_bwd for a gathered source whose index run_key [m] (int32) ascends with the
- * row (the target bond of angle rows, the centre atom of edge rows): source block run_blk
- * (its columns 128 run_blk .. +127 of the K; not source 0 when g_x0 is given) leaves as
- * tile-run partial sums -- within each tile of matris_gmlp_tile_rows() rows, the sum of
- * every run of equal keys, at the run's first row of g_x; the block's other rows are not
- * written.  matris_seg_sum2_runs with the same tile size completes the segment sums
- * (functions.py:131-160) from those partials, reading one row per run instead of every
- * gathered row.  Other sources and outputs are those of matris_gmlp_bwd. */
+/* matris_gmlp_bwd with two options:
+ * - run_key (may be NULL): for a gathered source whose index run_key [m] (int32) ascends
+ *   with the row (the target bond of angle rows, the centre atom of edge rows), source
+ *   block run_blk (its columns 128 run_blk .. +127 of the K; not source 0 when g_x0 is
+ *   given) leaves as tile-run partial sums -- within each tile of matris_gmlp_tile_rows()
+ *   rows, the sum of every run of equal keys, at the run's first row of g_x; the block's
+ *   other rows are not written.  matris_seg_sum2_runs with the same tile size completes the
+ *   segment sums (functions.py:131-160) from those partials, reading one row per run
+ *   instead of every gathered row.
+ * - res_src (may be NULL): the residual term source 0's gradient gains is res_w * res_src
+ *   [m,128] instead of res_w * g_out (the residual branch of the layer's output when it
+ *   does not pass through this GatedMLP, e.g. tb' = FFN(h) + r tb).
+ * Other sources and outputs are those of matris_gmlp_bwd. */
 int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                          const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
-                         float *g_x0, int acc0, const float *res_w, const int32_t *run_key, int run_blk, int mode,
-                         void *stream);
+                         float *g_x0, int acc0, const float *res_w, const float *res_src, const int32_t *run_key,
+                         int run_blk, int mode, void *stream);
 /* Rows per GatedMLP work-group tile (the tile of matris_gmlp_bwd_runs's partial sums). */
 int matris_gmlp_tile_rows(void);
 

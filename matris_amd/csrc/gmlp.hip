@@ -434,6 +434,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
                                                           const float *__restrict__ norm_g, float eps,
                                                           float *__restrict__ g_x, float *__restrict__ g_x0,
                                                           int acc0, const float *__restrict__ res_w,
+                                                          const float *__restrict__ res_src,
                                                           const int32_t *__restrict__ run_key, int run_blk,
                                                           unsigned *range_flag) {
     __shared__ __align__(16) float G[BM * LDH];
@@ -691,7 +692,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
         __syncthreads();
         float *__restrict__ gx0 = g_x0 ? g_x0 + m0 * MATRIS_D : gxr;
         const int ld0 = g_x0 ? MATRIS_D : ldr;
-        const float *__restrict__ got = g_out + m0 * MATRIS_D;
+        const float *__restrict__ got = (res_src ? res_src : g_out) + m0 * MATRIS_D;
 #pragma unroll
         for (int it = 0; it < (BM * 32) / 256; ++it) {
             const int q = it * 256 + tid;
@@ -730,6 +731,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                                                            const float *__restrict__ norm_g, float eps,
                                                            float *__restrict__ g_x, float *__restrict__ g_x0,
                                                            int acc0, const float *__restrict__ res_w,
+                                                           const float *__restrict__ res_src,
                                                            const int32_t *__restrict__ run_key, int run_blk,
                                                            unsigned *range_flag) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes");
@@ -907,7 +909,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         __syncthreads();
         float *__restrict__ gx0 = g_x0 ? g_x0 + m0 * MATRIS_D : gxr;
         const int ld0 = g_x0 ? MATRIS_D : ldr;
-        const float *__restrict__ got = g_out + m0 * MATRIS_D;
+        const float *__restrict__ got = (res_src ? res_src : g_out) + m0 * MATRIS_D;
 #pragma unroll
         for (int it = 0; it < (BM * 32) / 512; ++it) {
             const int q = it * 512 + tid;
@@ -997,8 +999,8 @@ extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *sr
 
 static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                            const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
-                           float *g_x0, int acc0, const float *res_w, const int32_t *run_key, int run_blk, int mode,
-                           void *stream) {
+                           float *g_x0, int acc0, const float *res_w, const float *res_src, const int32_t *run_key,
+                           int run_blk, int mode, void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1tp || !w2tp ||
         !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
@@ -1008,6 +1010,7 @@ static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p,
     if (m == 0) return 0;
     if (!aligned16(w1tp) || !aligned16(w2tp)) return MATRIS_E_ARG;
     if (acc0 && !g_x0) return MATRIS_E_ARG;
+    if (res_src && !res_w) return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
@@ -1015,16 +1018,16 @@ static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p,
     if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
     if (mode == 6) {
         gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                 res_w, run_key, run_blk, flag);
+                                                 res_w, res_src, run_key, run_blk, flag);
     } else if (mode == 0) {
         gmlp_bwd8_kernel<0><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, run_key, run_blk, flag);
+                                                  res_w, res_src, run_key, run_blk, flag);
     } else if (mode == 2) {
         gmlp_bwd8_kernel<2><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, run_key, run_blk, flag);
+                                                  res_w, res_src, run_key, run_blk, flag);
     } else {
         gmlp_bwd8_kernel<3><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, run_key, run_blk, flag);
+                                                  res_w, res_src, run_key, run_blk, flag);
     }
     MATRIS_CHECK_LAUNCH();
     return 0;
@@ -1033,17 +1036,17 @@ static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p,
 extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                                const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                                float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
-    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, nullptr, -1,
-                           mode, stream);
+    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, nullptr,
+                           nullptr, -1, mode, stream);
 }
 
 extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, const float *z,
                                     const void *w1tp, const void *w2tp, const float *norm_c, const float *norm_g,
                                     float eps, float *g_x, float *g_x0, int acc0, const float *res_w,
-                                    const int32_t *run_key, int run_blk, int mode, void *stream) {
-    if (!run_key) return MATRIS_E_ARG;
-    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, run_key,
-                           run_blk, mode, stream);
+                                    const float *res_src, const int32_t *run_key, int run_blk, int mode,
+                                    void *stream) {
+    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, res_src,
+                           run_key, run_key ? run_blk : -1, mode, stream);
 }
 
 extern "C" int matris_gmlp_tile_rows(void) { return BM; }

@@ -232,12 +232,15 @@ class _LineRefinement(torch.autograd.Function):
         g_tb_new = _zeros_if_none(g_tb_new, h)
         g_bond = ops._rows(E, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
-        g_tb = ops._rows(A, D, h.device)
-        g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, g_res=g_tb, res_w=r_e)
+        g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode)
         del p_de
         g_env = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h, accumulate=True)
         del h
-        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=True, runs=_runs(tgt, 2))
+        # g_tb = (source 0's GatedMLP gradient) + r_e g_tb_new, the residual term added in
+        # the GatedMLP backward's epilogue (nothing writes r_e g_tb_new on its own)
+        g_tb = ops._rows(A, D, g_h.device)
+        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=False, res_w=r_e, res_src=g_tb_new,
+                               runs=_runs(tgt, 2))
         del g_h, p_h, z_h
         g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True,

@@ -663,13 +663,14 @@ def gmlp_tile_rows() -> int:
 
 
 def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None, acc0: bool = False, res_w=None,
-                 runs=None):
+                 runs=None, res_src=None):
     """matris_gmlp_bwd.  Without g_x0 returns g_x [M, K]; with g_x0 source 0's gradient
     goes (accumulated if acc0, plus res_w * g if res_w) to g_x0 and the other columns to
     g_x [M, K-128] (allocated when not given; None when K == 128).
     runs = (key, blk): source block blk, gathered through `key` (int32 [M], ascending),
     leaves as tile-run partial sums (matris_gmlp_bwd_runs), to be completed by
-    seg_sum_raw(..., tile_rows=gmlp_tile_rows())."""
+    seg_sum_raw(..., tile_rows=gmlp_tile_rows()).  res_src: the residual term is
+    res_w * res_src instead of res_w * g."""
     lib = _lib.load()
     M = p.shape[0]
     if g_x is None and not (g_x0 is not None and K == D):
@@ -682,13 +683,16 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
     with _timed("gmlp_bwd", (M, K, nbytes)):
         args = (M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)), _p(pack.nc),
                 _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w))
-        if runs is None:
+        if runs is None and res_src is None:
             _lib.check(lib.matris_gmlp_bwd(*args, mode, _stream()), "matris_gmlp_bwd")
         else:
-            key, blk = runs
-            if key.dtype != torch.int32 or key.numel() != M or not key.is_contiguous():
+            key, blk = runs if runs is not None else (None, -1)
+            if key is not None and (key.dtype != torch.int32 or key.numel() != M or not key.is_contiguous()):
                 raise ValueError("gmlp_bwd_raw: runs key must be a contiguous int32 tensor of one entry per row")
-            _lib.check(lib.matris_gmlp_bwd_runs(*args, _p(key), int(blk), mode, _stream()), "matris_gmlp_bwd_runs")
+            if res_src is not None and (res_w is None or tuple(res_src.shape) != (M, D) or not res_src.is_contiguous()):
+                raise ValueError("gmlp_bwd_raw: res_src must be a contiguous [M, 128] tensor, with res_w")
+            _lib.check(lib.matris_gmlp_bwd_runs(*args, _p(res_src), _p(key), int(blk), mode, _stream()),
+                       "matris_gmlp_bwd_runs")
     return g_x
 
 

@@ -551,6 +551,39 @@ def test_gmlp_bwd_tile_run_sums(M, S, K, blk, with_x0, mode):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("mode", ["f16x3", "fp32", "bf16x6"])
+@pytest.mark.parametrize("M", [1, 64, 4097, 70001])
+def test_gmlp_bwd_res_src(M, mode):
+    """matris_gmlp_bwd_runs with res_src: source 0's gradient gains res_w * res_src in the
+    epilogue, equal (to one fp32 rounding) to the plain backward accumulating onto
+    res_w * res_src written beforehand; the other sources' gradients are bit-identical."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + 11)
+        mod = _ShimGated(_TorchGMLP(512)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        srcs = [torch.randn(M, 128, device=DEV) for _ in range(4)]
+        _, p, z, _ = ops.gmlp_fwd_raw(pack, srcs, [None] * 4, M, mm)
+        g, r_src = torch.randn(M, 128, device=DEV), torch.randn(M, 128, device=DEV)
+        r_w = torch.rand(128, device=DEV)
+        x0a = r_w * r_src
+        gxa = ops.gmlp_bwd_raw(pack, g, p, z, 512, mm, g_x0=x0a, acc0=True)
+        x0b = torch.full((M, 128), float("nan"), device=DEV)
+        gxb = ops.gmlp_bwd_raw(pack, g, p, z, 512, mm, g_x0=x0b, acc0=False, res_w=r_w, res_src=r_src)
+        assert torch.equal(gxa, gxb)
+        assert (x0b - x0a).abs().max().item() <= 2e-6 * x0a.abs().max().item()
+        key = _sorted_keys(M, max(1, M // 7), M).to(DEV)
+        x0c = torch.full((M, 128), float("nan"), device=DEV)
+        ops.gmlp_bwd_raw(pack, g, p, z, 512, mm, g_x0=x0c, acc0=False, res_w=r_w, res_src=r_src, runs=(key, 2))
+        assert torch.equal(x0b, x0c)
+        with pytest.raises(ValueError):
+            ops.gmlp_bwd_raw(pack, g, p, z, 512, mm, g_x0=x0c, res_src=r_src)
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode,tol", _MODES)
 @pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097, 140001])
 def test_ffn_fwd_bwd(M, mode, tol):
