@@ -248,6 +248,13 @@ int matris_env_agg_fwd(int64_t n_seg, const float *h, const float *env, const in
 int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h, const float *env, const float *g_agg,
                        const float *S, const int32_t *t_idx, const int32_t *s_idx, const int32_t *s_ptr,
                        const int32_t *s_perm, int accumulate, float *g_h, float *g_env, void *stream);
+/* g_env of matris_env_agg_bwd alone, plus (g_agg_env non-NULL) the per-bond factor of the
+ * g_h term, g_agg_env[b] = g_agg[b] * env[b] (n_seg rows); matris_ffn_bwd_env then adds
+ * g_agg_env[tgt(a)] * env[src(a)] to the FFN input gradient it writes, so g_h makes one
+ * trip through memory. */
+int matris_env_agg_bwd_env(int64_t n_seg, const float *h, const float *env, const float *g_agg, const float *S,
+                           const int32_t *t_idx, const int32_t *s_ptr, const int32_t *s_perm, float *g_env,
+                           float *g_agg_env, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Basis functions of the embeddings (rows E2, E3), thread per row, with input gradients.
@@ -402,6 +409,14 @@ int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const void *w2p, 
                    const float *res, const float *res_w, int mode, void *stream);
 int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp, float *g_x,
                    float *g_res, const float *res_w, int mode, void *stream);
+/* matris_ffn_bwd plus the envelope term of the line Refinement's hidden-row gradient
+ * (interaction_block.py:243-258, 269-270: h feeds both edge_FFN and the envelope-weighted
+ * aggregate): g_x[a] = FFN input gradient + g_agg_env[t_idx[a]] * env[s_idx[a]], with
+ * g_agg_env from matris_env_agg_bwd_env (the g_h of matris_env_agg_bwd with accumulate,
+ * in one kernel and one write). */
+int matris_ffn_bwd_env(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp, float *g_x,
+                       const float *g_agg_env, const float *env, const int32_t *t_idx, const int32_t *s_idx, int mode,
+                       void *stream);
 
 /* Attention projection pair (interaction_block.py:33-38, 110-111):
  * out0 = x W[0:128]^T (source_weight_linear), out1 = x W[128:256]^T (target);

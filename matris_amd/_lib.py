@@ -99,6 +99,7 @@ _SIGS = {
                              _P]),
     "matris_env_agg_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_env_agg_bwd": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
+    "matris_env_agg_bwd_env": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_gmlp_project": (_I, [_I64, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_fwd_proj": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
@@ -117,6 +118,7 @@ _SIGS = {
     "matris_status_take": (_I, [_P, _P]),
     "matris_ffn_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_ffn_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "matris_ffn_bwd_env": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
     "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "matris_tb_embed_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),

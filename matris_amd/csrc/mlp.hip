@@ -116,6 +116,39 @@ __device__ __forceinline__ void store_res128(const Rows128 &x, float *__restrict
     }
 }
 
+// The envelope term of the line refinement's hidden-row gradient, the backward of
+// agg[b] = sum_{a: t[a] = b} h[a] * env[s[a]] * env[t[a]] (interaction_block.py:243-258):
+//   add[a] = ge[t[a]] * env[s[a]],  ge = g_agg * env (per bond, written beforehand by
+//   matris_env_agg_bwd_env)                    (ge == nullptr: no term)
+struct EnvTerm {
+    const float *ge, *env;
+    const int32_t *t, *s;
+};
+
+__device__ __forceinline__ float4 env_term4(const EnvTerm &e, int64_t tr, int64_t sr, int col) {
+    const float4 g = *reinterpret_cast<const float4 *>(e.ge + tr * MATRIS_D + col);
+    const float4 b = *reinterpret_cast<const float4 *>(e.env + sr * MATRIS_D + col);
+    return make_float4(g.x * b.x, g.y * b.y, g.z * b.z, g.w * b.w);
+}
+
+// store_tile128 of a [*, 128] output plus the envelope term of each row.
+__device__ __forceinline__ void store_tile128_env(const float *tile, float *__restrict__ dst, int64_t m0, int64_t M,
+                                                  int tid, const EnvTerm &et) {
+#pragma unroll
+    for (int it = 0; it < (BM * 32) / 256; ++it) {
+        const int q = it * 256 + tid;
+        const int r = q >> 5, c4 = (q & 31) * 4;
+        if (m0 + r < M) {
+            float4 v = *reinterpret_cast<const float4 *>(tile + r * LDT + c4);
+            if (et.ge) {
+                const float4 a = env_term4(et, et.t[m0 + r], et.s[m0 + r], c4);
+                v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+            }
+            *reinterpret_cast<float4 *>(dst + (m0 + r) * MATRIS_D + c4) = v;
+        }
+    }
+}
+
 // Stage the rows, times s, into LDS pre-split into fragment units [rt 2][kb 8][plane 2][64
 // lanes] (two-plane modes), each value converted once.
 template <int MODE>
@@ -417,14 +450,16 @@ __global__ __launch_bounds__(512, 1) void proj_ws_kernel(int64_t M, const float 
 
 // FFN backward, weight-stationary like ffn_fwd_ws_kernel: g_x = ((g W2) * SiLU'(p)) W1 with
 // w1t, w2t = packs of W1^T, W2^T resident (wave w: columns 32 (w%4) .. +31 of both, rows
-// 32 (w/4) .. +31 of each tile); g_res (optional) = res_w * g, written while g is staged.
+// 32 (w/4) .. +31 of each tile); g_res (optional) = res_w * g, written while g is staged;
+// the envelope term (optional) is added to g_x, its rows loaded before the second GEMM.
 template <int MODE>
 __global__ __launch_bounds__(512, 1) void ffn_bwd_ws_kernel(int64_t M, const float *__restrict__ g,
                                                             const float *__restrict__ P,
                                                             const uint4 *__restrict__ W1t,
                                                             const uint4 *__restrict__ W2t, float *__restrict__ g_x,
                                                             float *__restrict__ g_res,
-                                                            const float *__restrict__ res_w, unsigned *range_flag) {
+                                                            const float *__restrict__ res_w, EnvTerm et,
+                                                            unsigned *range_flag) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes only");
     __shared__ uint4 Xf[2 * 8 * 2 * 64];  // g tile as fragment planes (32 KB)
     __shared__ uint4 Hf[2 * 8 * 2 * 64];  // g_p tile, the same layout
@@ -477,15 +512,26 @@ __global__ __launch_bounds__(512, 1) void ffn_bwd_ws_kernel(int64_t M, const flo
             frag_put4<MODE>(Hf, rt * 8 + ct * 2 + (j >> 1), l32 + 32 * (j & 1), h, v);
         }
         __syncthreads();  // g_p complete; every wave is past the first GEMM (Xf free)
+        float4 ev[4];
+        if (et.ge) {
+            const int64_t rr = min(row, M - 1);
+            const int64_t tr = et.t[rr], sr = et.s[rr];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ev[j] = env_term4(et, tr, sr, ct * 32 + 8 * j + 4 * h);
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[i] = 0.f;
         gemm_res<MODE>(acc, w1, Hf, rt, lane);
         if (row < M) {
             const float sc = w1s * ri;  // both powers of two
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<float4 *>(g_x + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) =
-                    make_float4(acc[4 * j] * sc, acc[4 * j + 1] * sc, acc[4 * j + 2] * sc, acc[4 * j + 3] * sc);
+            for (int j = 0; j < 4; ++j) {
+                float4 v = make_float4(acc[4 * j] * sc, acc[4 * j + 1] * sc, acc[4 * j + 2] * sc, acc[4 * j + 3] * sc);
+                if (et.ge) {
+                    v.x += ev[j].x; v.y += ev[j].y; v.z += ev[j].z; v.w += ev[j].w;
+                }
+                *reinterpret_cast<float4 *>(g_x + row * MATRIS_D + ct * 32 + 8 * j + 4 * h) = v;
+            }
         }
     }
     report_range<MODE>(amax, range_flag);
@@ -692,7 +738,7 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
                                                          const float *__restrict__ P, const uint4 *__restrict__ W1t,
                                                          const uint4 *__restrict__ W2t, float *__restrict__ g_x,
                                                          float *__restrict__ g_res, const float *__restrict__ res_w,
-                                                         unsigned *range_flag) {
+                                                         EnvTerm et, unsigned *range_flag) {
     __shared__ __align__(16) float T[BM * LDT];
     __shared__ float rinv[BM];  // MODE 2: 2^-k of each row's g / g_p scaling
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -765,7 +811,7 @@ __global__ __launch_bounds__(256, 3) void ffn_bwd_kernel(int64_t M, const float 
     __syncthreads();
     acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
     __syncthreads();
-    store_tile128(T, g_x, MATRIS_D, m0, M, tid);
+    store_tile128_env(T, g_x, m0, M, tid, et);
     report_range<MODE>(amax, range_flag);
 }
 
@@ -928,13 +974,13 @@ extern "C" int matris_ffn_fwd(int64_t m, const float *x, const void *w1p, const 
     return 0;
 }
 
-extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp,
-                              float *g_x, float *g_res, const float *res_w, int mode, void *stream) {
+static int ffn_bwd_launch(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp, float *g_x,
+                          float *g_res, const float *res_w, const EnvTerm &et, int mode, void *stream) {
     if (m < 0 || !mlp_args_ok(mode, {g, p, w1tp, w2tp, g_x})) return MATRIS_E_ARG;
     if (g_res && (((uintptr_t)g_res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
     if (mode == 6 || !weight_stationary(m)) {
-        MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x, g_res, res_w);
+        MLP_DISPATCH(ffn_bwd_kernel, m, g, p, (const uint4 *)w1tp, (const uint4 *)w2tp, g_x, g_res, res_w, et);
     } else {
         unsigned *flag = nullptr;
         if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
@@ -942,14 +988,29 @@ extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const v
         hipStream_t st = (hipStream_t)stream;
         const uint4 *w1t = (const uint4 *)w1tp, *w2t = (const uint4 *)w2tp;
         if (mode == 0)
-            ffn_bwd_ws_kernel<0><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, flag);
+            ffn_bwd_ws_kernel<0><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, et, flag);
         else if (mode == 2)
-            ffn_bwd_ws_kernel<2><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, flag);
+            ffn_bwd_ws_kernel<2><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, et, flag);
         else
-            ffn_bwd_ws_kernel<3><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, flag);
+            ffn_bwd_ws_kernel<3><<<grid, 512, 0, st>>>(m, g, p, w1t, w2t, g_x, g_res, res_w, et, flag);
     }
     MATRIS_CHECK_LAUNCH();
     return 0;
+}
+
+extern "C" int matris_ffn_bwd(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp,
+                              float *g_x, float *g_res, const float *res_w, int mode, void *stream) {
+    return ffn_bwd_launch(m, g, p, w1tp, w2tp, g_x, g_res, res_w, EnvTerm{nullptr, nullptr, nullptr, nullptr}, mode,
+                          stream);
+}
+
+extern "C" int matris_ffn_bwd_env(int64_t m, const float *g, const float *p, const void *w1tp, const void *w2tp,
+                                  float *g_x, const float *g_agg_env, const float *env, const int32_t *t_idx,
+                                  const int32_t *s_idx, int mode, void *stream) {
+    if (!g_agg_env || !env || !t_idx || !s_idx || ((uintptr_t)g_agg_env & 15) || ((uintptr_t)env & 15))
+        return MATRIS_E_ARG;
+    return ffn_bwd_launch(m, g, p, w1tp, w2tp, g_x, nullptr, nullptr, EnvTerm{g_agg_env, env, t_idx, s_idx}, mode,
+                          stream);
 }
 
 extern "C" int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, float *out1, int mode,

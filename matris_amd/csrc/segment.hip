@@ -706,7 +706,8 @@ __global__ __launch_bounds__(256) void env_agg_bwd_rows_kernel(int64_t n_rows, c
     *o = v;
 }
 
-// g_env: one wave per source segment, half-waves on alternating rows as in the forward.
+// g_env: one wave per source segment, half-waves on alternating rows as in the forward;
+// with ge given, also ge[b] = g_agg[b] * env[b] (the per-bond factor of g_h's term).
 __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, const float *__restrict__ h,
                                                               const float *__restrict__ env,
                                                               const float *__restrict__ g_agg,
@@ -714,7 +715,7 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
                                                               const int32_t *__restrict__ s_ptr,
                                                               const int32_t *__restrict__ s_perm,
                                                               const int32_t *__restrict__ t_idx,
-                                                              float *__restrict__ g_env) {
+                                                              float *__restrict__ g_env, float *__restrict__ ge) {
     const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (seg >= n_seg) return;
     const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
@@ -748,6 +749,10 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
                           : make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
     if (half) return;
     const float4 gs = ld4(g_agg + seg * MATRIS_D + c), sv = ld4(S + seg * MATRIS_D + c);
+    if (ge) {
+        const float4 es = ld4(env + seg * MATRIS_D + c);
+        st4(ge + seg * MATRIS_D + c, make_float4(gs.x * es.x, gs.y * es.y, gs.z * es.z, gs.w * es.w));
+    }
     st4(g_env + seg * MATRIS_D + c,
         make_float4(gs.x * sv.x + t.x, gs.y * sv.y + t.y, gs.z * sv.z + t.z, gs.w * sv.w + t.w));
 }
@@ -768,6 +773,9 @@ extern "C" int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h,
                                   float *g_env, void *stream) {
     if (n_rows < 0 || n_seg < 0 || !h || !env || !g_agg || !S || !t_idx || !s_idx || !s_ptr || !g_h || !g_env)
         return MATRIS_E_ARG;
+    // h, env, g_agg, S and g_h are read as float4 rows
+    if (((uintptr_t)h | (uintptr_t)env | (uintptr_t)g_agg | (uintptr_t)S | (uintptr_t)g_h | (uintptr_t)g_env) & 15)
+        return MATRIS_E_ARG;
     hipStream_t st = (hipStream_t)stream;
     if (n_rows > 0) {
         env_agg_bwd_rows_kernel<<<matris_blocks(n_rows * 32, 256), 256, 0, st>>>(n_rows, g_agg, env, t_idx, s_idx,
@@ -776,9 +784,23 @@ extern "C" int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h,
     }
     if (n_seg > 0) {
         env_agg_bwd_env_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(n_seg, h, env, g_agg, S, s_ptr,
-                                                                                    s_perm, t_idx, g_env);
+                                                                                    s_perm, t_idx, g_env, nullptr);
         MATRIS_CHECK_LAUNCH();
     }
+    return 0;
+}
+
+extern "C" int matris_env_agg_bwd_env(int64_t n_seg, const float *h, const float *env, const float *g_agg,
+                                      const float *S, const int32_t *t_idx, const int32_t *s_ptr,
+                                      const int32_t *s_perm, float *g_env, float *g_agg_env, void *stream) {
+    if (n_seg < 0 || !h || !env || !g_agg || !S || !t_idx || !s_ptr || !g_env) return MATRIS_E_ARG;
+    if (((uintptr_t)h | (uintptr_t)env | (uintptr_t)g_agg | (uintptr_t)S | (uintptr_t)g_env | (uintptr_t)g_agg_env) &
+        15)
+        return MATRIS_E_ARG;
+    if (n_seg == 0) return 0;
+    env_agg_bwd_env_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, g_agg_env);
+    MATRIS_CHECK_LAUNCH();
     return 0;
 }
 

@@ -232,10 +232,11 @@ class _LineRefinement(torch.autograd.Function):
         g_tb_new = _zeros_if_none(g_tb_new, h)
         g_bond = ops._rows(E, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
-        g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode)
-        del p_de
-        g_env = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h, accumulate=True)
+        g_env, g_agg_env = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src)
         del h
+        # g_h = edge_FFN's input gradient + the aggregate's term, written once
+        g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, env_term=(g_agg_env, env, tgt, src))
+        del p_de, g_agg_env
         # g_tb = (source 0's GatedMLP gradient) + r_e g_tb_new, the residual term added in
         # the GatedMLP backward's epilogue (nothing writes r_e g_tb_new on its own)
         g_tb = ops._rows(A, D, g_h.device)

@@ -405,6 +405,18 @@ def env_agg_fwd_raw(h, env, tgt: Grouping, src: Grouping):
     return agg, S
 
 
+def env_agg_bwd_env_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping):
+    """(g_env, g_agg_env) of matris_env_agg_bwd_env: g_env as env_agg_bwd_raw returns it and
+    g_agg_env = g_agg * env, the per-bond factor ffn_bwd_raw(..., env_term=...) takes."""
+    lib = _lib.load()
+    E = env.shape[0]
+    g_env, ge = _rows(E, D, h.device), _rows(E, D, h.device)
+    with _timed("env_agg_bwd", (h.shape[0], E)):
+        _lib.check(lib.matris_env_agg_bwd_env(E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key), _p(src.rowptr),
+                                              _p(src.perm), _p(g_env), _p(ge), _stream()), "matris_env_agg_bwd_env")
+    return g_env, ge
+
+
 def env_agg_bwd_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, g_h, accumulate: bool):
     """g_h (+)= g_agg[tgt] * env[tgt] * env[src]; returns g_env."""
     lib = _lib.load()
@@ -773,14 +785,25 @@ def ffn_fwd_raw(pack: _WeightPack, x, mode: int, res=None, save: bool = True):
     return out, p
 
 
-def ffn_bwd_raw(pack: _WeightPack, g, p, mode: int, g_res=None, res_w=None):
-    """g_x of matris_ffn_bwd; g_res (given) receives res_w * g."""
+def ffn_bwd_raw(pack: _WeightPack, g, p, mode: int, g_res=None, res_w=None, env_term=None):
+    """g_x of matris_ffn_bwd; g_res (given) receives res_w * g.  env_term = (g_agg_env, env,
+    tgt, src): g_x also gains g_agg_env[tgt.key] * env[src.key] (matris_ffn_bwd_env)."""
     lib = _lib.load()
     M = p.shape[0]
     g_x = _rows(M, D, g.device)
     with _timed("ffn_bwd", (M,)):
-        _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(pack.b("wt0", mode)), _p(pack.b("wt1", mode)), _p(g_x),
-                                      _p(g_res), _p(res_w), mode, _stream()), "matris_ffn_bwd")
+        if env_term is None:
+            _lib.check(lib.matris_ffn_bwd(M, _p(g), _p(p), _p(pack.b("wt0", mode)), _p(pack.b("wt1", mode)),
+                                          _p(g_x), _p(g_res), _p(res_w), mode, _stream()), "matris_ffn_bwd")
+        else:
+            if g_res is not None:
+                raise ValueError("ffn_bwd_raw: env_term and g_res do not combine")
+            ge, env, tgt, src = env_term
+            if tgt.key.numel() != M or src.key.numel() != M or ge.shape != env.shape:
+                raise ValueError("ffn_bwd_raw: env_term needs one target / source per row and ge shaped as env")
+            _lib.check(lib.matris_ffn_bwd_env(M, _p(g), _p(p), _p(pack.b("wt0", mode)), _p(pack.b("wt1", mode)),
+                                              _p(g_x), _p(ge), _p(env), _p(tgt.key), _p(src.key), mode, _stream()),
+                       "matris_ffn_bwd_env")
     return g_x
 
 

@@ -584,6 +584,43 @@ def test_gmlp_bwd_res_src(M, mode):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("mode", ["f16x3", "fp32", "bf16x6", "bf16x3"])
+@pytest.mark.parametrize("M,E", [(1, 1), (1000, 130), (140001, 18000), (264384, 33698)])
+def test_ffn_bwd_env_term(M, E, mode):
+    """matris_env_agg_bwd_env + matris_ffn_bwd_env (the refinement's hidden-row gradient in
+    one write) against matris_ffn_bwd followed by matris_env_agg_bwd with accumulate:
+    g_env bit-identical, g_agg_env = g_agg * env exactly, g_h equal to one fp32 rounding
+    (the term's product and sum may fuse into one FMA), and the added term equal to its
+    fp64 value to fp32 rounding."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M)
+        mm = ops._MMA["mode"]
+        wp = ops._WeightPack().get(torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11)
+        tkey = _sorted_keys(M, E, M).to(DEV)
+        skey = _keys(M, E, M + 5).to(DEV)
+        tgt = ops.Grouping.build(tkey, E, sorted_rows=True)
+        src = ops.Grouping.build(skey, E)
+        h, g, p = (torch.randn(M, 128, device=DEV) for _ in range(3))
+        env, g_agg, S = torch.rand(E, 128, device=DEV), torch.randn(E, 128, device=DEV), torch.randn(E, 128, device=DEV)
+        g_h_ref = ops.ffn_bwd_raw(wp, g, p, mm)
+        g_ffn = g_h_ref.clone()
+        g_env_ref = ops.env_agg_bwd_raw(h, env, g_agg, S, tgt, src, g_h_ref, accumulate=True)
+        g_env, ge = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src)
+        assert torch.equal(ge, g_agg * env)
+        assert torch.equal(g_env, g_env_ref)
+        g_h = ops.ffn_bwd_raw(wp, g, p, mm, env_term=(ge, env, tgt, src))
+        ulp = 2.0 ** -23 * (g_ffn.abs() + (ge[tkey.long()] * env[skey.long()]).abs())
+        assert bool(((g_h - g_h_ref).abs() <= ulp).all())
+        term = (g_agg.double() * env.double())[tkey.long()] * env.double()[skey.long()]
+        assert _rel(g_h.double() - g_ffn.double(), term) < 1e-6
+        with pytest.raises(ValueError):
+            ops.ffn_bwd_raw(wp, g, p, mm, g_res=torch.empty_like(g), res_w=env[0], env_term=(ge, env, tgt, src))
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode,tol", _MODES)
 @pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097, 140001])
 def test_ffn_fwd_bwd(M, mode, tol):
