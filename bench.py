@@ -93,10 +93,10 @@ def _attn_line_bytes(A, U, with_perm=True):
     return 4 * D * (3 * A + 2 * U) + (4 * A if with_perm else 0) + 8 * (U + 1)
 
 
-def _gmlp_flops(M, K):
+def _gmlp_flops(M, K, tail_rows=0):
     """One fused GatedMLP forward (or backward, input gradients only):
-    [M,K]x[K,256] plus two [M,128]x[128,128]."""
-    return 2.0 * M * (K * 256 + 2 * 128 * 128)
+    [M,K]x[K,256] plus two [M,128]x[128,128]; an FFN tail adds two more [M,128]x[128,128]."""
+    return 2.0 * M * (K * 256 + 2 * 128 * 128) + 2.0 * tail_rows * 2 * 128 * 128
 
 
 # HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the
@@ -423,11 +423,11 @@ def main():
         gm = stats.get(name)
         if not gm:
             return None
-        flops = sum(_gmlp_flops(m, k) for m, k, _ in gm["info"]) / gm["n"]
-        byts = sum(b for _, _, b in gm["info"]) / gm["n"]
+        flops = sum(_gmlp_flops(i[0], i[1], i[3] if len(i) > 3 else 0) for i in gm["info"]) / gm["n"]
+        byts = sum(i[2] for i in gm["info"]) / gm["n"]
         tf = flops / gm["mean_s"] / 1e12
         gbs = byts / gm["mean_s"] / 1e9
-        n_line = sum(1 for (m, _, _) in gm["info"] if m == A)
+        n_line = sum(1 for i in gm["info"] if i[0] == A)
         intensity, balance = flops / byts, mma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
         traffic = TRAFFIC_BYTES.get((name, "C3"))
         common = dict(kernel=f"{name}_kernel<{mode_idx}>", mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
@@ -438,7 +438,8 @@ def main():
                       note=f"means over {gm['n']} launches in {args.steps} steps ({n_line} with M=A={A}); "
                            f"bytes: every input table read once (gathered sources as whole tables, projected "
                            f"sources as their product tables), outputs, saved p/z and gradients written once; "
-                           f"FLOPs 2*M*(256K+32768) with K the layer-1 width the kernel multiplies; MFMA peak = "
+                           f"FLOPs 2*M*(256K+32768) with K the layer-1 width the kernel multiplies (+2*M*32768 "
+                           f"for the launches that carry the line refinement's FFN); MFMA peak = "
                            f"{peak_note}")
         if intensity < balance:
             return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",

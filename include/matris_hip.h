@@ -394,6 +394,20 @@ int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *src_host, con
                          const float *norm_c, const float *norm_g, float eps, float *out, float *save_p,
                          float *save_z, const float *res_src, const float *res_w, float *res_out, int mode,
                          void *stream);
+/* matris_gmlp_fwd_proj (n_src may be 0 when every source is projected, n_proj 0 when none
+ * is) with the line Refinement's edge_FFN on the output rows, in the same kernel
+ * (interaction_block.py:263-275: tb' = edge_FFN(h) + r_e tb with h this GatedMLP's out):
+ *   t = h W1^T (saved to ffn_save_p [m,128] when non-NULL),
+ *   ffn_out [m,128] = SiLU(t) W2^T + ffn_res_w * ffn_res
+ * with ffn_w1p, ffn_w2p the packs matris_ffn_fwd takes.  out (h) is still written; the
+ * GatedMLP residual (res_src / res_w / res_out) is not available here.  Equal to
+ * matris_gmlp_fwd_proj followed by matris_ffn_fwd up to the FFN's fp32 sum order. */
+int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
+                        int n_proj, const float *const *proj_host, const int32_t *const *proj_idx_host,
+                        const int64_t *proj_ld_host, const void *w1p, const float *b1, const void *w2p,
+                        const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
+                        float *save_p, float *save_z, const void *ffn_w1p, const void *ffn_w2p, float *ffn_save_p,
+                        const float *ffn_res, const float *ffn_res_w, float *ffn_out, int mode, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Dense layers on MFMA, 128-wide rows, no bias.

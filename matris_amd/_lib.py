@@ -104,6 +104,8 @@ _SIGS = {
     "matris_gmlp_project": (_I, [_I64, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_fwd_proj": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
                                   _P, _I, _P]),
+    "matris_gmlp_fwd_ffn": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
+                                 _P, _P, _P, _P, _I, _P]),
     "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_bwd_runs": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
     "matris_gmlp_tile_rows": (_I, []),

@@ -64,6 +64,15 @@ struct GmlpProj {
     int n;
 };
 
+// A tail on the output rows (the line refinement's edge_FFN, interaction_block.py:269-275):
+//   t = W1 out (saved to save_p when given),  ffn_out = W2 SiLU(t) + res_w * res
+// with W1, W2 packs of the FFN's [128, 128] Linear weights.
+struct FfnTail {
+    const uint4 *W1, *W2;
+    float *save_p, *out;
+    const float *res, *res_w;
+};
+
 // ------------------------------------------------------------------------------------
 // forward
 // ------------------------------------------------------------------------------------
@@ -81,7 +90,7 @@ __device__ __forceinline__ void store_tile256(const float *tile, float *__restri
     }
 }
 
-template <int MODE>
+template <int MODE, bool TAIL = false>
 __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src, GmlpProj proj,
                                                           const uint4 *__restrict__ W1, const float *__restrict__ b1,
                                                           const uint4 *__restrict__ W2, const float *__restrict__ b2,
@@ -91,7 +100,8 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                           float *__restrict__ save_z,
                                                           const float *__restrict__ res_src,
                                                           const float *__restrict__ res_w,
-                                                          float *__restrict__ res_out, unsigned *range_flag) {
+                                                          float *__restrict__ res_out, FfnTail tail,
+                                                          unsigned *range_flag) {
     constexpr int NPL = Npl<MODE>::v;
     constexpr int CHUNK = 2 * 2 * NPL * 64;  // uint4 per LDS chunk: [rt 2][kb 2][plane][lane]
     __shared__ __align__(16) float smem[BM * LDH];
@@ -289,6 +299,16 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             rx1[rr] = *reinterpret_cast<const float4 *>(res_src + grow * MATRIS_D + 64 + c4);
         }
     }
+    // the tail's residual rows (layout of its final row stores), loaded here for the same reason
+    float4 tres[(BM * 32) / 256];
+    if constexpr (TAIL) {
+#pragma unroll
+        for (int it = 0; it < (BM * 32) / 256; ++it) {
+            const int q = it * 256 + tid;
+            const int64_t grow = min(m0 + (q >> 5), M - 1);
+            tres[it] = *reinterpret_cast<const float4 *>(tail.res + grow * MATRIS_D + (q & 31) * 4);
+        }
+    }
     __syncthreads();  // every wave is done reading h
 
     // z = acc + b2 -> LDS (16-byte writes); then a row pass with 16 lanes per row: lane
@@ -345,6 +365,53 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                               o0.w + w0.w * x0.w);
                 *reinterpret_cast<float4 *>(ro + 64) = make_float4(o1.x + w1.x * x1.x, o1.y + w1.y * x1.y,
                                                                    o1.z + w1.z * x1.z, o1.w + w1.w * x1.w);
+            }
+        }
+        if constexpr (TAIL) {  // the out rows, the tail's GEMM operand, over this row's z (already read)
+            *reinterpret_cast<float4 *>(Ts + row * LDH + c4) = o0;
+            *reinterpret_cast<float4 *>(Ts + row * LDH + 64 + c4) = o1;
+        }
+    }
+    if constexpr (TAIL) {
+        // t = W1 out -> columns 128..255 of the tile (GEMM A reads columns 0..127); one pass
+        // saves t and applies SiLU; W2 SiLU(t) -> columns 0..127; rows leave with the residual
+        const uint4 *tw1 = tail.W1, *tw2 = tail.W2;
+        const float t1s = take_wscale<MODE>(tw1), t2s = take_wscale<MODE>(tw2);
+        v16f ta[2][1];
+        zero_acc(ta);
+        __syncthreads();  // out rows complete
+        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(ta, Ts, LDH, tw1, wave, MATRIS_D / 16, 0,
+                                                                            lane));
+        scale_acc<MODE>(ta, t1s);
+        acc_t_to_lds<2, 1>(ta, Ts + MATRIS_D, LDH, wave * 32, lane);
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < (BM * 32) / 256; ++it) {
+            const int q = it * 256 + tid;
+            const int row = q >> 5, cc = (q & 31) * 4;
+            float4 *t = reinterpret_cast<float4 *>(Ts + row * LDH + MATRIS_D + cc);
+            float4 v = *t;
+            if (tail.save_p && m0 + row < M) st_nt4(tail.save_p + (m0 + row) * MATRIS_D + cc, v);
+            v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
+            *t = v;
+        }
+        __syncthreads();
+        zero_acc(ta);
+        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(ta, Ts + MATRIS_D, LDH, tw2, wave,
+                                                                            MATRIS_D / 16, 0, lane));
+        scale_acc<MODE>(ta, t2s);
+        acc_t_to_lds<2, 1>(ta, Ts, LDH, wave * 32, lane);  // every wave is past GEMM A (barrier above)
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < (BM * 32) / 256; ++it) {
+            const int q = it * 256 + tid;
+            const int row = q >> 5, cc = (q & 31) * 4;
+            if (m0 + row < M) {
+                float4 v = *reinterpret_cast<const float4 *>(Ts + row * LDH + cc);
+                const float4 w = *reinterpret_cast<const float4 *>(tail.res_w + cc);
+                const float4 x = tres[it];
+                v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
+                *reinterpret_cast<float4 *>(tail.out + (m0 + row) * MATRIS_D + cc) = v;
             }
         }
     }
@@ -939,8 +1006,8 @@ static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, c
                            int n_proj, const float *const *proj_host, const int32_t *const *proj_idx_host,
                            const int64_t *proj_ld_host, const void *w1p, const float *b1, const void *w2p, const float *b2,
                            const float *norm_c, const float *norm_g, float eps, float *out, float *save_p,
-                           float *save_z, const float *res_src, const float *res_w, float *res_out, int mode,
-                           void *stream) {
+                           float *save_z, const float *res_src, const float *res_w, float *res_out,
+                           const FfnTail &tail, int mode, void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (m < 0 || n_src < 0 || n_src > 4 || n_proj < 0 || n_proj > 3 || n_src + n_proj < 1 ||
         (n_src && (!src_host || !w1p)) || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
@@ -964,13 +1031,32 @@ static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, c
     }
     if ((n_src && !aligned16(w1p)) || !aligned16(w2p)) return MATRIS_E_ARG;
     if (res_out && (!res_src || !res_w)) return MATRIS_E_ARG;
+    const bool has_tail = tail.W1 != nullptr;
+    if (has_tail && (res_out || !aligned16(tail.W1) || !tail.W2 || !aligned16(tail.W2) || !tail.out ||
+                     !aligned16(tail.out) || !tail.res || !aligned16(tail.res) || !tail.res_w ||
+                     !aligned16(tail.res_w) || !aligned16(tail.save_p)))
+        return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1 = n_src ? (const uint4 *)w1p : nullptr, *w2 = (const uint4 *)w2p;
     unsigned *flag = nullptr;
     if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
-    MATRIS_MODE_DISPATCH(gmlp_fwd_kernel, grid, st, m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out, save_p,
-                         save_z, res_src, res_w, res_out, flag);
+    if (!has_tail) {
+        MATRIS_MODE_DISPATCH(gmlp_fwd_kernel, grid, st, m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
+                             save_p, save_z, res_src, res_w, res_out, tail, flag);
+    } else if (mode == 0) {
+        gmlp_fwd_kernel<0, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
+                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
+    } else if (mode == 2) {
+        gmlp_fwd_kernel<2, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
+                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
+    } else if (mode == 3) {
+        gmlp_fwd_kernel<3, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
+                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
+    } else {
+        gmlp_fwd_kernel<6, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
+                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
+    }
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -982,7 +1068,7 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
                                float *res_out, int mode, void *stream) {
     if (n_src < 1) return MATRIS_E_ARG;
     return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, 0, nullptr, nullptr, nullptr, w1p, b1, w2p, b2, norm_c, norm_g,
-                           eps, out, save_p, save_z, res_src, res_w, res_out, mode, stream);
+                           eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{}, mode, stream);
 }
 
 extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *src_host,
@@ -994,7 +1080,22 @@ extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *sr
                                     const float *res_src, const float *res_w, float *res_out, int mode,
                                     void *stream) {
     return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, n_proj, proj_host, proj_idx_host, proj_ld_host, w1p, b1, w2p,
-                           b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, mode, stream);
+                           b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{}, mode,
+                           stream);
+}
+
+extern "C" int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src_host,
+                                   const int32_t *const *src_idx_host, int n_proj, const float *const *proj_host,
+                                   const int32_t *const *proj_idx_host, const int64_t *proj_ld_host, const void *w1p,
+                                   const float *b1, const void *w2p, const float *b2, const float *norm_c,
+                                   const float *norm_g, float eps, float *out, float *save_p, float *save_z,
+                                   const void *ffn_w1p, const void *ffn_w2p, float *ffn_save_p, const float *ffn_res,
+                                   const float *ffn_res_w, float *ffn_out, int mode, void *stream) {
+    if (!ffn_w1p) return MATRIS_E_ARG;
+    const FfnTail tail{(const uint4 *)ffn_w1p, (const uint4 *)ffn_w2p, ffn_save_p, ffn_out, ffn_res, ffn_res_w};
+    return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, n_proj, proj_host, proj_idx_host, proj_ld_host, w1p, b1, w2p,
+                           b2, norm_c, norm_g, eps, out, save_p, save_z, nullptr, nullptr, nullptr, tail, mode,
+                           stream);
 }
 
 static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,

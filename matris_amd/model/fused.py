@@ -181,11 +181,12 @@ def _refine_fwd(layer, tb, atom, bond, env, lg, mode, save: bool):
     L, M = layer.node_FFN.layers, layer.edge_FFN.layers
     pn = layer._node_ffn.get(L[0].weight, L[3].weight)
     pm = layer._edge_ffn.get(M[0].weight, M[3].weight)
-    h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [tb, atom, bond, bond], [None, grp_atom.key, tgt.key, src.key], A, mode,
-                                      save=save)
+    # h = GatedMLP(...) and tb' = edge_FFN(h) + r_e tb in one launch
+    h, p_h, z_h, tb_new, p_de = ops.gmlp_fwd_ffn_raw(ph, [tb, atom, bond, bond],
+                                                     [None, grp_atom.key, tgt.key, src.key], A, mode, pm, tb, r_e,
+                                                     save=save)
     agg, S = ops.env_agg_fwd_raw(h, env, tgt, src)
     bond_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(bond, r_n), save=save)
-    tb_new, p_de = ops.ffn_fwd_raw(pm, h, mode, res=(tb, r_e), save=save)
     saved = (h, p_h, z_h, S, p_dn, p_de) if save else None
     return bond_new, tb_new, saved
 

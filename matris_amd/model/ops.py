@@ -610,6 +610,19 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     res = (res_src, res_w) also returns res_out = out + res_w * res_src.
     Returns (out, p, z, res_out); the same whether or not sources are projected first
     (matris_gmlp_fwd_proj), up to the order of the fp32 sums of layer 1."""
+    return _gmlp_fwd(pack, srcs, idxs, n_rows, mode, res, save, None)[:4]
+
+
+def gmlp_fwd_ffn_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, ffn: "_WeightPack", ffn_res, ffn_res_w,
+                     save: bool = True):
+    """matris_gmlp_fwd_ffn: the GatedMLP forward with the FFN tail on its output rows,
+    ffn_out = W2 SiLU(W1 out) + ffn_res_w * ffn_res (ffn = the FFN's pack, as for
+    ffn_fwd_raw).  Returns (out, p, z, ffn_out, ffn_p); p, z, ffn_p None when not saved."""
+    out, p, z, _, t_out, t_p = _gmlp_fwd(pack, srcs, idxs, n_rows, mode, None, save, (ffn, ffn_res, ffn_res_w))
+    return out, p, z, t_out, t_p
+
+
+def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: bool, tail):
     lib = _lib.load()
     dev = srcs[0].device
     nsrc = len(srcs)
@@ -620,19 +633,32 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     rs, rw = (res if res is not None else (None, None))
     proj = _projected_sources(srcs, idxs, n_rows)
     ret_p, ret_z = p, z
+    t_out = t_p = ret_tp = None
+    if tail is not None:
+        t_pack, t_res, t_rw = tail
+        if res is not None or tuple(t_res.shape) != (n_rows, D) or not t_res.is_contiguous():
+            raise ValueError("gmlp_fwd_ffn_raw: the residual source must be a contiguous [n_rows, 128] tensor")
+        t_out = _rows(n_rows, D, dev)
+        t_p = ret_tp = _rows(n_rows, D, dev) if save else None
     if _DISCARD["on"]:  # placeholders: the kernel writes neither
-        p = z = None
-    if not proj:
+        p = z = t_p = None
+    t_bytes = 0 if tail is None else 4 * D * n_rows * (2 + (t_p is not None))
+    if tail is not None:
+        # the tail rides the gather-after-GEMM entry point (with or without projected sources)
+        t_args = (_p(t_pack.b("w0", mode)), _p(t_pack.b("w1", mode)), _p(t_p), _p(t_res), _p(_f32c(t_rw)),
+                  _p(t_out))
+    if not proj and tail is None:
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
         with _timed("gmlp_fwd", (n_rows, nsrc * D, _gmlp_fwd_bytes(srcs, idxs, n_rows, p is not None,
-                                                                    res is not None))):
+                                                                    res is not None), 0)):
             _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
                                            _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
                                            _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
                        "matris_gmlp_fwd")
-        return out, ret_p, ret_z, res_out
-    # one projection launch per distinct table, all of its blocks side by side
+        return out, ret_p, ret_z, res_out, None, None
+    # one projection launch per distinct table, all of its blocks side by side (none when
+    # nothing is projected: the FFN-tail launch with every source gathered)
     tables: dict = {}
     for j in proj:
         tables.setdefault((srcs[j].data_ptr(), srcs[j].shape[0]), []).append(j)
@@ -659,14 +685,21 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     w1 = _p(pack.b_blocks(tuple(rest), mode)) if rest else None
     ptab = [(keep[k].shape[0], keep[k].shape[1], len(b)) for k, b in enumerate(tables.values())]
     nbytes = _gmlp_fwd_bytes([srcs[j] for j in rest], [idxs[j] for j in rest], n_rows, p is not None,
-                             res is not None, ptab)
-    with _timed("gmlp_fwd", (n_rows, len(rest) * D, nbytes)):  # K: the layer-1 width this kernel multiplies
-        _lib.check(lib.matris_gmlp_fwd_proj(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr, w1,
-                                            _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
-                                            _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),
-                                            _p(res_out), mode, _stream()), "matris_gmlp_fwd_proj")
+                             res is not None, ptab) + t_bytes
+    # K: the layer-1 width this kernel multiplies; the last field: rows of the FFN tail
+    with _timed("gmlp_fwd", (n_rows, len(rest) * D, nbytes, n_rows if tail is not None else 0)):
+        if tail is None:
+            _lib.check(lib.matris_gmlp_fwd_proj(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr,
+                                                w1, _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
+                                                _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),
+                                                _p(res_out), mode, _stream()), "matris_gmlp_fwd_proj")
+        else:
+            _lib.check(lib.matris_gmlp_fwd_ffn(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr,
+                                               w1, _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
+                                               _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), *t_args, mode,
+                                               _stream()), "matris_gmlp_fwd_ffn")
     del keep  # the stream orders any later reuse of these blocks after the launch
-    return out, ret_p, ret_z, res_out
+    return out, ret_p, ret_z, res_out, t_out, ret_tp
 
 
 def gmlp_tile_rows() -> int:

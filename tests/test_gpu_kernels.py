@@ -272,6 +272,50 @@ def test_gated_mlp_fwd_bwd(nsrc, M, mode, tol, gtg):
         _gated_mlp_case(ops, nsrc, M, mode, tol)
 
 
+@pytest.mark.parametrize("gtg", [True, False])
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("M", [1, 64, 4097, 70001])
+def test_gated_mlp_fwd_ffn_tail(M, mode, tol, gtg):
+    """matris_gmlp_fwd_ffn (the line refinement's [tb, atom[i], bond[t], bond[s]] GatedMLP
+    with edge_FFN(h) + r tb on its output rows): out, p and z bit-identical to the plain
+    forward; the tail's t and output against fp64 of the kernel's own h (and against
+    matris_ffn_fwd on it to the same bar); nothing saved when saves are discarded."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + 3)
+        mod = _ShimGated(_TorchGMLP(512)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        n_atom, n_bond = max(1, M // 300), max(1, M // 8)
+        tb = torch.randn(M, 128, device=DEV)
+        atom, bond = torch.randn(n_atom, 128, device=DEV), torch.randn(n_bond, 128, device=DEV)
+        idx = [None, torch.randint(0, n_atom, (M,), dtype=torch.int32, device=DEV),
+               torch.randint(0, n_bond, (M,), dtype=torch.int32, device=DEV),
+               torch.randint(0, n_bond, (M,), dtype=torch.int32, device=DEV)]
+        srcs = [tb, atom, bond, bond]
+        w1, w2 = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
+        fp = ops._WeightPack().get(w1, w2)
+        r = torch.rand(128, device=DEV)
+        with ops.gather_after_gemm(gtg, min_rows=1 << 12, ratio=4):
+            h0, p0, z0, _ = ops.gmlp_fwd_raw(pack, srcs, idx, M, mm)
+            h, p, z, t_out, t_p = ops.gmlp_fwd_ffn_raw(pack, srcs, idx, M, mm, fp, tb, r)
+            assert torch.equal(h, h0) and torch.equal(p, p0) and torch.equal(z, z0)
+            h64 = h.double()
+            t64 = h64 @ w1.double().t()
+            o64 = F.silu(t64) @ w2.double().t() + r.double() * tb.double()
+            assert _rel(t_p, t64) < tol and _rel(t_out, o64) < tol
+            o_sep, p_sep = ops.ffn_fwd_raw(fp, h, mm, res=(tb, r))
+            assert _rel(t_out, o_sep.double()) < tol and _rel(t_p, p_sep.double()) < tol
+            with ops.discard_saves():
+                _, _, _, t_out2, _ = ops.gmlp_fwd_ffn_raw(pack, srcs, idx, M, mm, fp, tb, r)
+            assert torch.equal(t_out2, t_out)
+            _, p3, z3, t_out3, t_p3 = ops.gmlp_fwd_ffn_raw(pack, srcs, idx, M, mm, fp, tb, r, save=False)
+            assert p3 is None and z3 is None and t_p3 is None and torch.equal(t_out3, t_out)
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
 @pytest.mark.parametrize("layout", ["atom_graph", "one_table", "big"])
 def test_gated_mlp_all_sources_projected(layout, mode, tol):
