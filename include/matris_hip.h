@@ -369,6 +369,19 @@ int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, c
                          const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                          float *g_x0, int acc0, const float *res_w, const float *res_src, const int32_t *run_key,
                          int run_blk, int mode, void *stream);
+/* The GatedMLP backward of the line Refinement with the edge_FFN backward in front of it,
+ * in one kernel (two-plane modes 0, 2, 3; interaction_block.py:243-275): the output
+ * gradient g_out of matris_gmlp_bwd is not read but computed per tile as
+ *   g_out = ((ffn_g W2) * SiLU'(ffn_p)) W1 + g_agg_env[t_idx] * env[s_idx]
+ * (matris_ffn_bwd_env's g_x; g_agg_env may be NULL for no envelope term), with ffn_g the
+ * gradient of tb' = edge_FFN(h) + r tb, ffn_p the FFN's saved W1 h and ffn_w1tp / ffn_w2tp
+ * the packs matris_ffn_bwd takes.  Source 0's gradient gains res_w * ffn_g (res_w may be
+ * NULL).  run_key / run_blk as in matris_gmlp_bwd_runs (run_key may be NULL). */
+int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float *z, const void *w1tp, const void *w2tp,
+                        const float *norm_c, const float *norm_g, float eps, float *g_x, float *g_x0,
+                        const float *res_w, const int32_t *run_key, int run_blk, const float *ffn_g,
+                        const float *ffn_p, const void *ffn_w1tp, const void *ffn_w2tp, const float *g_agg_env,
+                        const float *env, const int32_t *t_idx, const int32_t *s_idx, int mode, void *stream);
 /* Rows per GatedMLP work-group tile (the tile of matris_gmlp_bwd_runs's partial sums). */
 int matris_gmlp_tile_rows(void);
 

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                 const float4 w = *reinterpret_cast<const float4 *>(tail.res_w + cc);
                 const float4 x = tres[it];
                 v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
-                *reinterpret_cast<float4 *>(tail.out + (m0 + row) * MATRIS_D + cc) = v;
+                st_nt4(tail.out + (m0 + row) * MATRIS_D + cc, v);  // read again only by the next block
             }
         }
     }
@@ -421,6 +421,18 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 // ------------------------------------------------------------------------------------
 // backward
 // ------------------------------------------------------------------------------------
+// A head in front of the backward (the line refinement's edge_FFN backward, with the
+// envelope term of the aggregate, interaction_block.py:243-275): the GatedMLP's output
+// gradient is not read but computed per tile,
+//   g_out = ((g W2) * SiLU'(p)) W1 + ge[t] * env[s]      (ge == NULL: no envelope term)
+// with g, p [M,128] the FFN's output gradient and saved W1 x, W1t / W2t packs of W1^T /
+// W2^T (as matris_ffn_bwd takes them), ge [*,128] = g_agg * env per bond.
+struct FfnHead {
+    const float *g, *p;
+    const uint4 *W1t, *W2t;
+    const float *ge, *env;
+    const int32_t *t, *s;
+};
 // Store a wave's [64, 32*NCT] accumulators to rows of dst (row stride ld) at column
 // col + ct*32 + lane%32, rows below nrows only, with streaming stores (the gradient rows
 // are read once, by the segment sums that follow).
@@ -789,7 +801,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 // phases 2 and 3 -- half the registers per wave, so a CU holds 16 waves instead of 8 at
 // the same LDS per work-group.  Phase 3 runs 256-column passes from the top of K, source
 // 0's block last (for K = 384 / 128 only waves 0-3 have columns in the last pass).
-template <int MODE>
+template <int MODE, bool HEAD = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void gmlp_bwd8_kernel(int64_t M, int K, const float *__restrict__ g_out,
                                                            const float *__restrict__ P, const float *__restrict__ Z,
                                                            const uint4 *__restrict__ W1t,
@@ -800,7 +812,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                                                            int acc0, const float *__restrict__ res_w,
                                                            const float *__restrict__ res_src,
                                                            const int32_t *__restrict__ run_key, int run_blk,
-                                                           unsigned *range_flag) {
+                                                           FfnHead head, unsigned *range_flag) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes");
     __shared__ __align__(16) float G[BM * LDH];
     __shared__ __align__(16) float rinv[BM];
@@ -812,9 +824,79 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     float amax = 0.f;
     const int run_k = run_key ? run_key[min(m0 + lane, M - 1)] : 0;
 
+    // phase 0 (head): the tile's g_out into G's first 32 KB as fp32 [64, 128].  g is staged
+    // pre-split in G's first half, (g W2) * SiLU'(p) pre-split in its second half; wave w
+    // computes the 32 x 32 tile (rows 32 (w / 4), columns 32 (w % 4)) of both products.
+    float *gh = G;
+    if constexpr (HEAD) {
+        __shared__ float hinv[BM];  // MODE 2: 2^-k of each row's scaling of g
+        const uint4 *hw1 = head.W1t, *hw2 = head.W2t;
+        const float h1s = take_wscale<MODE>(hw1), h2s = take_wscale<MODE>(hw2);
+        const int hrt = wave >> 2, hct = wave & 3;
+        const int64_t hrow = min(m0 + hrt * 32 + l32, M - 1);
+        float4 xr[4], pv[4];
+        load_rows4(xr, head.g, m0, M, tid);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            pv[j] = *reinterpret_cast<const float4 *>(head.p + hrow * MATRIS_D + hct * 32 + 8 * j + 4 * h);
+        scale_rows4<MODE>(xr, hinv, tid);
+        amax = stage_rows4<MODE>(Gf, xr, tid, amax);
+        __syncthreads();
+        v16f ha[1][1];
+        zero_acc(ha);
+        gemm_frag_packed<MODE, 1, 1, MATRIS_D / 16, true>(ha, Gf + hrt * (8 * 2 * 64), 8, 0, hw2, hct, 8, 0, lane);
+        uint4 *Hf = Gf + 2 * 8 * 2 * 64;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = make_float4(ha[0][0][4 * j] * h2s * dsilu_f(pv[j].x), ha[0][0][4 * j + 1] * h2s * dsilu_f(pv[j].y),
+                                         ha[0][0][4 * j + 2] * h2s * dsilu_f(pv[j].z),
+                                         ha[0][0][4 * j + 3] * h2s * dsilu_f(pv[j].w));
+            amax = frag_amax<MODE>(amax, v, v);
+            frag_put4<MODE>(Hf, hrt * 8 + hct * 2 + (j >> 1), l32 + 32 * (j & 1), h, v);
+        }
+        __syncthreads();  // the second product's operand complete; every wave is past the first
+        float4 ev[4];
+        if (head.ge) {
+            const int64_t tr = head.t[hrow], sr = head.s[hrow];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = hct * 32 + 8 * j + 4 * h;
+                const float4 a = *reinterpret_cast<const float4 *>(head.ge + tr * MATRIS_D + col);
+                const float4 b = *reinterpret_cast<const float4 *>(head.env + sr * MATRIS_D + col);
+                ev[j] = make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+            }
+        }
+        zero_acc(ha);
+        gemm_frag_packed<MODE, 1, 1, MATRIS_D / 16, true>(ha, Hf + hrt * (8 * 2 * 64), 8, 0, hw1, hct, 8, 0, lane);
+        const float sc = MODE == 2 ? h1s * hinv[hrt * 32 + l32] : h1s;  // both powers of two
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float4 v = make_float4(ha[0][0][4 * j] * sc, ha[0][0][4 * j + 1] * sc, ha[0][0][4 * j + 2] * sc,
+                                   ha[0][0][4 * j + 3] * sc);
+            if (head.ge) {
+                v.x += ev[j].x; v.y += ev[j].y; v.z += ev[j].z; v.w += ev[j].w;
+            }
+            *reinterpret_cast<float4 *>(gh + (hrt * 32 + l32) * MATRIS_D + hct * 32 + 8 * j + 4 * h) = v;
+        }
+        __syncthreads();
+    }
+
     // phase 1: wave w owns rows [8w, 8w + 8), 16 lanes per row
     {
         const int c4 = (lane & 15) * 4;
+        // HEAD: the wave's g_out rows, all read before any wave writes g_z over them
+        float hg[2][8];
+        if constexpr (HEAD) {
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+                const float *gr = gh + (wave * (BM / 8) + rr * 4 + (lane >> 4)) * MATRIS_D + c4;
+                const float4 g0 = *reinterpret_cast<const float4 *>(gr);
+                const float4 g1 = *reinterpret_cast<const float4 *>(gr + 64);
+                hg[rr][0] = g0.x; hg[rr][1] = g0.y; hg[rr][2] = g0.z; hg[rr][3] = g0.w;
+                hg[rr][4] = g1.x; hg[rr][5] = g1.y; hg[rr][6] = g1.z; hg[rr][7] = g1.w;
+            }
+            __syncthreads();
+        }
         float wc[8], wg[8];
         {
             const float4 a0 = *reinterpret_cast<const float4 *>(norm_c + c4);
@@ -832,12 +914,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             {
                 const int64_t ml = min(m, M - 1);  // rows past M read row M-1, then count as zeros
                 const float4 *zr = reinterpret_cast<const float4 *>(Z + ml * 256 + c4);
-                const float4 *gr = reinterpret_cast<const float4 *>(g_out + ml * MATRIS_D + c4);
                 const float4 z0 = zr[0], z1 = zr[16], y0 = zr[MATRIS_D / 4], y1 = zr[MATRIS_D / 4 + 16];
-                const float4 g0 = gr[0], g1 = gr[16];
                 zc[0] = z0.x; zc[1] = z0.y; zc[2] = z0.z; zc[3] = z0.w; zc[4] = z1.x; zc[5] = z1.y; zc[6] = z1.z; zc[7] = z1.w;
                 zg[0] = y0.x; zg[1] = y0.y; zg[2] = y0.z; zg[3] = y0.w; zg[4] = y1.x; zg[5] = y1.y; zg[6] = y1.z; zg[7] = y1.w;
-                go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w; go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
+                if constexpr (HEAD) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) go[e] = rr ? hg[1][e] : hg[0][e];
+                } else {
+                    const float4 *gr = reinterpret_cast<const float4 *>(g_out + ml * MATRIS_D + c4);
+                    const float4 g0 = gr[0], g1 = gr[16];
+                    go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w; go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
+                }
             }
             if (m >= M) {
 #pragma unroll
@@ -1101,10 +1188,15 @@ extern "C" int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src
 static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                            const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                            float *g_x0, int acc0, const float *res_w, const float *res_src, const int32_t *run_key,
-                           int run_blk, int mode, void *stream) {
+                           int run_blk, const FfnHead &head, int mode, void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
-    if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || !g_out || !p || !z || !w1tp || !w2tp ||
-        !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
+    const bool has_head = head.W1t != nullptr;
+    if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || (!g_out && !has_head) || !p || !z || !w1tp ||
+        !w2tp || !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
+        return MATRIS_E_ARG;
+    if (has_head && (mode == 6 || !aligned16(head.W1t) || !head.W2t || !aligned16(head.W2t) || !head.g ||
+                     !aligned16(head.g) || !head.p || !aligned16(head.p) || !aligned16(head.ge) ||
+                     (head.ge && (!head.env || !aligned16(head.env) || !head.t || !head.s))))
         return MATRIS_E_ARG;
     // the reduced block goes to g_x: not source 0 when source 0 has its own output
     if (run_key && (!g_x || run_blk < (g_x0 ? 1 : 0) || run_blk >= k / MATRIS_D)) return MATRIS_E_ARG;
@@ -1120,15 +1212,25 @@ static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p,
     if (mode == 6) {
         gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
                                                  res_w, res_src, run_key, run_blk, flag);
+    } else if (has_head) {
+        if (mode == 0)
+            gmlp_bwd8_kernel<0, true><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
+                                                            acc0, res_w, res_src, run_key, run_blk, head, flag);
+        else if (mode == 2)
+            gmlp_bwd8_kernel<2, true><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
+                                                            acc0, res_w, res_src, run_key, run_blk, head, flag);
+        else
+            gmlp_bwd8_kernel<3, true><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
+                                                            acc0, res_w, res_src, run_key, run_blk, head, flag);
     } else if (mode == 0) {
         gmlp_bwd8_kernel<0><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, res_src, run_key, run_blk, flag);
+                                                  res_w, res_src, run_key, run_blk, head, flag);
     } else if (mode == 2) {
         gmlp_bwd8_kernel<2><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, res_src, run_key, run_blk, flag);
+                                                  res_w, res_src, run_key, run_blk, head, flag);
     } else {
         gmlp_bwd8_kernel<3><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, res_src, run_key, run_blk, flag);
+                                                  res_w, res_src, run_key, run_blk, head, flag);
     }
     MATRIS_CHECK_LAUNCH();
     return 0;
@@ -1138,7 +1240,7 @@ extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float
                                const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                                float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
     return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, nullptr,
-                           nullptr, -1, mode, stream);
+                           nullptr, -1, FfnHead{}, mode, stream);
 }
 
 extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, const float *z,
@@ -1147,7 +1249,20 @@ extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const 
                                     const float *res_src, const int32_t *run_key, int run_blk, int mode,
                                     void *stream) {
     return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, res_src,
-                           run_key, run_key ? run_blk : -1, mode, stream);
+                           run_key, run_key ? run_blk : -1, FfnHead{}, mode, stream);
+}
+
+extern "C" int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float *z, const void *w1tp,
+                                   const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
+                                   float *g_x0, const float *res_w, const int32_t *run_key, int run_blk,
+                                   const float *ffn_g, const float *ffn_p, const void *ffn_w1tp, const void *ffn_w2tp,
+                                   const float *g_agg_env, const float *env, const int32_t *t_idx,
+                                   const int32_t *s_idx, int mode, void *stream) {
+    if (!ffn_w1tp) return MATRIS_E_ARG;
+    const FfnHead head{ffn_g, ffn_p, (const uint4 *)ffn_w1tp, (const uint4 *)ffn_w2tp, g_agg_env, env, t_idx, s_idx};
+    // the residual term of source 0's gradient is res_w * (the FFN's output gradient)
+    return gmlp_bwd_launch(m, k, nullptr, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, 0, res_w,
+                           res_w ? ffn_g : nullptr, run_key, run_key ? run_blk : -1, head, mode, stream);
 }
 
 extern "C" int matris_gmlp_tile_rows(void) { return BM; }

@@ -557,6 +557,52 @@ __device__ __forceinline__ void acc_to_lds(const v16f (&acc)[2][NCT], float *til
 // MFMA arithmetic modes the GEMM kernels are built for.
 static inline bool matris_mode_ok(int mode) { return mode == 0 || mode == 2 || mode == 3 || mode == 6; }
 
+// ------------------------------------------------------------------------------------
+// 64-row tiles of [*, 128] rows staged by 512 threads (two-plane modes)
+// ------------------------------------------------------------------------------------
+// Rows of a [*, 128] array for tile rows m0 .. m0+63, 512 threads: thread (row tid/8,
+// 8-column groups q and q+8 for q = tid%8); rows past M read row M-1.
+__device__ __forceinline__ void load_rows4(float4 (&xr)[4], const float *__restrict__ x, int64_t m0, int64_t M,
+                                           int tid) {
+    const int64_t row = min(m0 + (tid >> 3), M - 1);
+    const float4 *p = reinterpret_cast<const float4 *>(x + row * MATRIS_D) + (tid & 7) * 2;
+    xr[0] = p[0];
+    xr[1] = p[1];
+    xr[2] = p[16];
+    xr[3] = p[17];
+}
+
+// Stage those rows as fragment planes: group g of row r is fragment unit (r/32) * 8 + g/2,
+// lane r%32 + 32 (g%2).
+template <int MODE>
+__device__ __forceinline__ float stage_rows4(uint4 *buf, const float4 (&xr)[4], int tid, float amax) {
+    const int r = tid >> 3, q = tid & 7;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int g = q + 8 * i;
+        const int unit = (r >> 5) * 8 + (g >> 1), fl = (r & 31) + 32 * (g & 1);
+        amax = frag_amax<MODE>(amax, xr[2 * i], xr[2 * i + 1]);
+        Frag<MODE> f;
+        make_frag<MODE>(f, xr[2 * i], xr[2 * i + 1]);
+        buf[(unit * 2 + 0) * 64 + fl] = f.p[0];
+        buf[(unit * 2 + 1) * 64 + fl] = f.p[1];
+    }
+    return amax;
+}
+
+// MODE 2: scale the thread's share of its row (load_rows4 layout: 8 threads per row) by the
+// row's 2^k (row_scale) and record 2^-k in rinv[row].
+template <int MODE>
+__device__ __forceinline__ void scale_rows4(float4 (&xr)[4], float *rinv, int tid) {
+    if constexpr (MODE == 2) {
+        const float m = abs_max4(abs_max4(abs_max4(abs_max4(0.f, xr[0]), xr[1]), xr[2]), xr[3]);
+        const RowScale rs = row_scale(group8_max(m));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[i] = mul4(xr[i], rs.s);
+        if ((tid & 7) == 0) rinv[tid >> 3] = rs.inv;
+    }
+}
+
 // Launch KERNEL<mode> (mode already checked by matris_mode_ok).
 #define MATRIS_MODE_DISPATCH(KERNEL, GRID, STREAM, ...)                                     \
     do {                                                                                    \

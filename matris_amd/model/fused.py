@@ -235,15 +235,19 @@ class _LineRefinement(torch.autograd.Function):
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
         g_env, g_agg_env = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src)
         del h
-        # g_h = edge_FFN's input gradient + the aggregate's term, written once
-        g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, env_term=(g_agg_env, env, tgt, src))
-        del p_de, g_agg_env
-        # g_tb = (source 0's GatedMLP gradient) + r_e g_tb_new, the residual term added in
-        # the GatedMLP backward's epilogue (nothing writes r_e g_tb_new on its own)
-        g_tb = ops._rows(A, D, g_h.device)
-        g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=False, res_w=r_e, res_src=g_tb_new,
-                               runs=_runs(tgt, 2))
-        del g_h, p_h, z_h
+        # g_h = edge_FFN's input gradient + the aggregate's term; g_tb = source 0's
+        # GatedMLP gradient + r_e g_tb_new.  In the two-plane modes g_h never leaves the
+        # GatedMLP backward (its head computes it per tile).
+        g_tb = ops._rows(A, D, g_tb_new.device)
+        if mode != 6:
+            g_x = ops.gmlp_bwd_ffn_raw(ph, p_h, z_h, 4 * D, mode, pm, g_tb_new, p_de, env_term=(g_agg_env, env, tgt, src),
+                                       g_x0=g_tb, res_w=r_e, runs=_runs(tgt, 2))
+        else:
+            g_h = ops.ffn_bwd_raw(pm, g_tb_new, p_de, mode, env_term=(g_agg_env, env, tgt, src))
+            g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=False, res_w=r_e,
+                                   res_src=g_tb_new, runs=_runs(tgt, 2))
+            del g_h
+        del p_de, g_agg_env, p_h, z_h
         g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True,
                         second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))

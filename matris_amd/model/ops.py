@@ -722,7 +722,7 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
         g_x = _rows(M, K - (D if g_x0 is not None else 0), g.device)
     # algorithmic bytes: g_out, p, z (and the accumulated source-0 block) read once, g_x
     # written once; a run-summed block: its key read, at least one partial row per tile
-    nbytes = 4 * M * (D + 2 * 256 + (D if (g_x0 is not None and acc0) else 0) + K)
+    nbytes = 4 * M * (D + 2 * 256 + (D if (g_x0 is not None and acc0) else 0) + K + (D if res_src is not None else 0))
     if runs is not None:
         nbytes += 4 * M - 4 * D * M + 4 * D * -(-M // gmlp_tile_rows())
     with _timed("gmlp_bwd", (M, K, nbytes)):
@@ -738,6 +738,41 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
                 raise ValueError("gmlp_bwd_raw: res_src must be a contiguous [M, 128] tensor, with res_w")
             _lib.check(lib.matris_gmlp_bwd_runs(*args, _p(res_src), _p(key), int(blk), mode, _stream()),
                        "matris_gmlp_bwd_runs")
+    return g_x
+
+
+def gmlp_bwd_ffn_raw(pack: GmlpPack, p, z, K: int, mode: int, ffn: "_WeightPack", ffn_g, ffn_p, env_term=None,
+                     g_x0=None, res_w=None, runs=None):
+    """matris_gmlp_bwd_ffn: gmlp_bwd_raw(pack, g, p, z, K, mode, g_x0=g_x0, res_w=res_w,
+    res_src=ffn_g, runs=runs) with g = ffn_bwd_raw(ffn, ffn_g, ffn_p, mode, env_term=...)
+    computed inside the kernel (two-plane modes).  Returns g_x as gmlp_bwd_raw does."""
+    lib = _lib.load()
+    M = p.shape[0]
+    if mode == 6:
+        raise ValueError("gmlp_bwd_ffn_raw: two-plane modes only (0, 2, 3)")
+    for t in (ffn_g, ffn_p):
+        if tuple(t.shape) != (M, D) or not t.is_contiguous():
+            raise ValueError("gmlp_bwd_ffn_raw: ffn_g and ffn_p must be contiguous [M, 128] tensors")
+    g_x = None if (g_x0 is not None and K == D) else _rows(M, K - (D if g_x0 is not None else 0), p.device)
+    ge = env = tk = sk = None
+    nbytes = 4 * M * (2 * D + 2 * 256 + K)
+    if env_term is not None:
+        ge, env, tgt, src = env_term
+        tk, sk = tgt.key, src.key
+        if tk.numel() != M or sk.numel() != M or ge.shape != env.shape:
+            raise ValueError("gmlp_bwd_ffn_raw: env_term needs one target / source per row and ge shaped as env")
+        nbytes += 8 * M + 2 * 4 * D * env.shape[0]
+    key, blk = runs if runs is not None else (None, -1)
+    if key is not None:
+        if key.dtype != torch.int32 or key.numel() != M or not key.is_contiguous():
+            raise ValueError("gmlp_bwd_ffn_raw: runs key must be a contiguous int32 tensor of one entry per row")
+        nbytes += 4 * M - 4 * D * M + 4 * D * -(-M // gmlp_tile_rows())
+    with _timed("gmlp_bwd", (M, K, nbytes, M)):  # the last field: rows of the FFN head
+        _lib.check(lib.matris_gmlp_bwd_ffn(M, K, _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)),
+                                           _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), _p(res_w),
+                                           _p(key), int(blk), _p(ffn_g), _p(ffn_p), _p(ffn.b("wt0", mode)),
+                                           _p(ffn.b("wt1", mode)), _p(ge), _p(env), _p(tk), _p(sk), mode, _stream()),
+                   "matris_gmlp_bwd_ffn")
     return g_x
 
 

@@ -595,6 +595,50 @@ def test_gmlp_bwd_tile_run_sums(M, S, K, blk, with_x0, mode):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("mode,tol", [("f16x3", 1e-5), ("fp32", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("M,E", [(1, 1), (64, 9), (4097, 600), (140001, 18000)])
+@pytest.mark.parametrize("env,runs", [(True, True), (False, False)])
+def test_gmlp_bwd_ffn_head(M, E, env, runs, mode, tol):
+    """matris_gmlp_bwd_ffn (the edge_FFN backward computed per tile in front of the
+    GatedMLP backward) against matris_ffn_bwd(_env) followed by matris_gmlp_bwd_runs with
+    the same residual source: every gradient equal to fp32 rounding of the largest."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + 17)
+        mod = _ShimGated(_TorchGMLP(512)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        srcs = [torch.randn(M, 128, device=DEV) for _ in range(4)]
+        _, p, z, _ = ops.gmlp_fwd_raw(pack, srcs, [None] * 4, M, mm)
+        fp = ops._WeightPack().get(torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11)
+        g_new, p_de = torch.randn(M, 128, device=DEV), torch.randn(M, 128, device=DEV)
+        r = torch.rand(128, device=DEV)
+        tkey = _sorted_keys(M, E, M).to(DEV)
+        tgt = ops.Grouping.build(tkey, E, sorted_rows=True)
+        src = ops.Grouping.build(_keys(M, E, M + 9).to(DEV), E)
+        et = (torch.randn(E, 128, device=DEV), torch.rand(E, 128, device=DEV), tgt, src) if env else None
+        rn = (tkey, 2) if runs else None
+        g_h = ops.ffn_bwd_raw(fp, g_new, p_de, mm, env_term=et)
+        x0a, x0b = torch.empty(M, 128, device=DEV), torch.empty(M, 128, device=DEV)
+        gxa = ops.gmlp_bwd_raw(pack, g_h, p, z, 512, mm, g_x0=x0a, res_w=r, res_src=g_new, runs=rn)
+        gxb = ops.gmlp_bwd_ffn_raw(pack, p, z, 512, mm, fp, g_new, p_de, env_term=et, g_x0=x0b, res_w=r, runs=rn)
+        assert _rel(x0b, x0a) < tol
+        if runs:  # the run-summed block holds partials at run starts only: compare the rest
+            assert _rel(torch.cat([gxb[:, :128], gxb[:, 256:]], 1), torch.cat([gxa[:, :128], gxa[:, 256:]], 1)) < tol
+            grp = ops.Grouping.build(tkey, E, sorted_rows=True)
+            T = ops.gmlp_tile_rows()
+            sa = ops.seg_sum_raw(gxa, grp, ldx=384, col_off=128, tile_rows=T)
+            sb = ops.seg_sum_raw(gxb, grp, ldx=384, col_off=128, tile_rows=T)
+            assert _rel(sb, sa) < tol
+        else:
+            assert _rel(gxb, gxa) < tol
+        with pytest.raises(ValueError):
+            ops.gmlp_bwd_ffn_raw(pack, p, z, 512, 6, fp, g_new, p_de)
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode", ["f16x3", "fp32", "bf16x6"])
 @pytest.mark.parametrize("M", [1, 64, 4097, 70001])
 def test_gmlp_bwd_res_src(M, mode):
