@@ -105,11 +105,13 @@ def _gmlp_flops(M, K, tail_rows=0):
 # Keys: (launch name, config); a mean over that family's launches in one step where the
 # shapes differ.
 TRAFFIC_BYTES = {
-    ("gmlp_bwd", "C3"): 488.9e6,       # all four launch shapes, 420 launches; 1128.9 MB at M = A
-    ("gmlp_fwd", "C3"): 465.7e6,       # all four launch shapes, 420 launches; 1078.4 MB at M = A
+    ("gmlp_bwd", "C3"): 530.7e6,       # every launch shape, 420 launches; at M = A 989.2 MB (line attention)
+                                       # and 1520.2 MB (line refinement, with the FFN head)
+    ("gmlp_fwd", "C3"): 530.0e6,       # every launch shape, 420 launches; at M = A 1203.4 MB (line attention)
+                                       # and 1339.6 MB (line refinement, with the FFN tail)
     ("attn_fwd_line", "C3"): 580.4e6,  # 538.0 read + 42.5 written
-    ("attn_fwd", "C2"): 4061.9e6,
-    ("attn_bwd", "C2"): 8451.6e6,
+    ("attn_fwd", "C2"): 4062.0e6,
+    ("attn_bwd", "C2"): 8446.4e6,
     ("seg_sum", "C2"): 1048.1e6,
 }
 
@@ -430,7 +432,14 @@ def main():
         n_line = sum(1 for i in gm["info"] if i[0] == A)
         intensity, balance = flops / byts, mma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
         traffic = TRAFFIC_BYTES.get((name, "C3"))
-        common = dict(kernel=f"{name}_kernel<{mode_idx}>", mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
+        # the line refinement's launches are the <.., true> instances (FFN head / tail); MODE 6
+        # runs the four-wave backward without a head
+        if name == "gmlp_fwd":
+            kname = f"gmlp_fwd_kernel<{mode_idx}, false> + <{mode_idx}, true>"
+        else:
+            kname = f"gmlp_bwd_kernel<{mode_idx}>" if mode_idx == 6 else \
+                f"gmlp_bwd8_kernel<{mode_idx}, false> + <{mode_idx}, true>"
+        common = dict(kernel=kname, mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
                       flops_per_launch=round(flops), bytes_per_launch=round(byts),
                       flop_per_byte=round(intensity, 1), machine_balance_flop_per_byte=round(balance, 1),
                       mfma_achieved_tflops=round(tf, 2), mfma_peak_tflops=round(mma_peak, 1),
