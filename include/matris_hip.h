@@ -235,6 +235,18 @@ int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const f
                     const float *y_t, const float *y_s, const float *lse_t, const float *lse_s, const float *g_yt,
                     const float *g_ys, int64_t ldgy, float *g_alpha_t, float *g_alpha_s, float *g_e,
                     const float *g_e_base, void *stream);
+/* The atom-graph matris_attn_bwd by undirected bond (interaction_block.py:104-134 with
+ * is_atom_graph: the logits W bond are per bond, read by both directed copies through
+ * d2u): alpha_t / alpha_s [n_bond, lda] per bond, the directed rows of bond u are the d2u
+ * CSR segment u (u_ptr [n_bond+1], u_perm or NULL); t_idx / s_idx, e and g_e per directed
+ * row.  g_alpha_t / g_alpha_s [n_bond,128] are the sums over each bond's rows (the d2u
+ * reduction of matris_attn_bwd's per-row outputs) and g_e = base_scale * g_base[bond] +
+ * the attention term (g_base [n_bond,128] or NULL). */
+int matris_attn_bwd_bond(int64_t n_bond, const float *alpha_t, const float *alpha_s, int64_t lda, const float *e,
+                         const int32_t *u_ptr, const int32_t *u_perm, const int32_t *t_idx, const int32_t *s_idx,
+                         const float *y_t, const float *y_s, const float *lse_t, const float *lse_s,
+                         const float *g_yt, const float *g_ys, int64_t ldgy, const float *g_base, float base_scale,
+                         float *g_alpha_t, float *g_alpha_s, float *g_e, void *stream);
 
 /* Envelope-weighted aggregation of the line-graph Refinement (interaction_block.py:243-258:
  * smooth_weight = env[source] * env[target]; aggregate(h * smooth_weight, target)):

@@ -97,6 +97,8 @@ _SIGS = {
     "matris_attn_fwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
                              _P]),
+    "matris_attn_bwd_bond": (_I, [_I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _F, _P, _P,
+                                  _P, _P]),
     "matris_env_agg_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_env_agg_bwd": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
     "matris_env_agg_bwd_env": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),

@@ -615,6 +615,74 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(
     st4(g_alpha_s + r * MATRIS_D + c, gas);
 }
 
+// The atom-graph backward by undirected bond: the logits are per bond (read by both
+// directed copies through d2u), so one wave takes a bond's directed rows (its d2u segment,
+// half-waves on alternate rows), reads the bond's logit rows and base gradient once, writes
+// g_e per directed row and the bond's g_alpha_t / g_alpha_s (the sums over its rows, the
+// halves combined) -- the d2u reductions of per-row logit gradients and the gather of the
+// base gradient happen here instead of in three more launches.
+__global__ __launch_bounds__(256) void attn_bwd_bond_kernel(
+    int64_t n_bond, const float *__restrict__ alpha_t, const float *__restrict__ alpha_s, int64_t lda,
+    const float *__restrict__ e, const int32_t *__restrict__ u_ptr, const int32_t *__restrict__ u_perm,
+    const int32_t *__restrict__ t_idx, const int32_t *__restrict__ s_idx, const float *__restrict__ y_t,
+    const float *__restrict__ y_s, const float *__restrict__ lse_t, const float *__restrict__ lse_s,
+    const float *__restrict__ g_yt, const float *__restrict__ g_ys, int64_t ldgy, const float *__restrict__ g_base,
+    float base_scale, float *__restrict__ g_alpha_t, float *__restrict__ g_alpha_s, float *__restrict__ g_e) {
+    const int64_t u = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    if (u >= n_bond) return;
+    const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
+    const float4 at = ld4(alpha_t + u * lda + c), as = ld4(alpha_s + u * lda + c);
+    float4 gb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g_base) {
+        const float4 v = ld4(g_base + u * MATRIS_D + c);
+        gb = make_float4(base_scale * v.x, base_scale * v.y, base_scale * v.z, base_scale * v.w);
+    }
+    float4 sat = make_float4(0.f, 0.f, 0.f, 0.f), sas = sat;
+    const int b = u_ptr[u], end = u_ptr[u + 1];
+    for (int i = b + half; i < end; i += 2) {
+        const int64_t r = u_perm ? u_perm[i] : i;
+        const int64_t t = t_idx[r], s = s_idx[r];
+        const float4 ev = ld4(e + r * MATRIS_D + c);
+        const float4 lt = ld4(lse_t + t * MATRIS_D + c), ls = ld4(lse_s + s * MATRIS_D + c);
+        const float4 gt = ld4(g_yt + t * ldgy + c), gs = ld4(g_ys + s * ldgy + c);
+        const float4 yt = ld4(y_t + t * MATRIS_D + c), ys = ld4(y_s + s * MATRIS_D + c);
+        float4 ge = gb;
+#define ATTN_BWD_COL(k)                                                       \
+    {                                                                         \
+        const float pt = exp_neg_f(lt.k - at.k), ps = exp_neg_f(ls.k - as.k); \
+        ge.k += pt * gt.k + ps * gs.k;                                        \
+        sat.k += pt * gt.k * (ev.k - yt.k);                                   \
+        sas.k += ps * gs.k * (ev.k - ys.k);                                   \
+    }
+        ATTN_BWD_COL(x) ATTN_BWD_COL(y) ATTN_BWD_COL(z) ATTN_BWD_COL(w)
+#undef ATTN_BWD_COL
+        st4(g_e + r * MATRIS_D + c, ge);
+    }
+    const float4 ot = shfl_xor4(sat, 32), os = shfl_xor4(sas, 32);
+    if (half == 0) {
+        st4(g_alpha_t + u * MATRIS_D + c, make_float4(sat.x + ot.x, sat.y + ot.y, sat.z + ot.z, sat.w + ot.w));
+        st4(g_alpha_s + u * MATRIS_D + c, make_float4(sas.x + os.x, sas.y + os.y, sas.z + os.z, sas.w + os.w));
+    }
+}
+
+extern "C" int matris_attn_bwd_bond(int64_t n_bond, const float *alpha_t, const float *alpha_s, int64_t lda,
+                                    const float *e, const int32_t *u_ptr, const int32_t *u_perm,
+                                    const int32_t *t_idx, const int32_t *s_idx, const float *y_t, const float *y_s,
+                                    const float *lse_t, const float *lse_s, const float *g_yt, const float *g_ys,
+                                    int64_t ldgy, const float *g_base, float base_scale, float *g_alpha_t,
+                                    float *g_alpha_s, float *g_e, void *stream) {
+    if (n_bond < 0 || lda < MATRIS_D || (lda % 4) || ldgy < MATRIS_D || (ldgy % 4) || !alpha_t || !alpha_s || !e ||
+        !u_ptr || !t_idx || !s_idx || !y_t || !y_s || !lse_t || !lse_s || !g_yt || !g_ys || !g_alpha_t ||
+        !g_alpha_s || !g_e)
+        return MATRIS_E_ARG;
+    if (n_bond == 0) return 0;
+    attn_bwd_bond_kernel<<<matris_blocks(n_bond, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        n_bond, alpha_t, alpha_s, lda, e, u_ptr, u_perm, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ldgy,
+        g_base, base_scale, g_alpha_t, g_alpha_s, g_e);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
 extern "C" int matris_attn_bwd(int64_t n_rows, int64_t n_seg, const float *alpha_t, const float *alpha_s,
                                int64_t lda, const int32_t *alpha_idx, const float *e, const int32_t *t_idx,
                                const int32_t *s_idx, const float *y_t, const float *y_s, const float *lse_t,

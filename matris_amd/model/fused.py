@@ -325,14 +325,13 @@ class _AtomAttention(torch.autograd.Function):
         g_atom = ops._rows(N, D, e.device)
         g_y = ops.gmlp_bwd_raw(pn, g_atom_new, p_n, z_n, 3 * D, mode, g_x0=g_atom, acc0=False, res_w=r_n)
         del p_n, z_n
-        # e: half of the bond gradient of each directed copy, plus the attention term
-        g_e_base = ops.gather_raw(g_bond_new, d2u.key, 0.5)
-        g_at, g_as, g_e = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, d2u,
-                                           ldgy=2 * D, g_e_base=g_e_base)
-        del g_e_base, g_y, a_t, a_s, e
-        # logits were read through d2u: reduce to bonds, then the projections + residual
-        g_bond = ops.pair_bwd_raw(pp, ops.seg_sum_raw(g_as, d2u), ops.seg_sum_raw(g_at, d2u), mode,
-                                  res=g_bond_new, res_w=r_e)
+        # by bond: g_e = half of the bond gradient of each directed copy + the attention
+        # term; the logits were read through d2u, so their gradients are the bond's sums
+        g_at, g_as, g_e = ops.attn_bwd_bond_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, d2u,
+                                                ldgy=2 * D, g_base=g_bond_new, base_scale=0.5)
+        del g_y, a_t, a_s, e
+        # the projections + residual
+        g_bond = ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_bond_new, res_w=r_e)
         del g_at, g_as
         # edge update: sources bond[d2u], atom[tgt], atom[src]
         # the centre-atom block (rows ascend by centre) leaves as tile-run partial sums

@@ -361,6 +361,24 @@ def attn_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: G
     return g_at, g_as, g_e
 
 
+def attn_bwd_bond_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: Grouping, src: Grouping,
+                      d2u: Grouping, ldgy: int = D, g_base=None, base_scale: float = 1.0):
+    """(g_alpha_t, g_alpha_s) per bond and g_e per directed row of matris_attn_bwd_bond: the
+    atom-graph backward with the logits per bond (rows of d2u's segments)."""
+    lib = _lib.load()
+    R, U = e.shape[0], d2u.n_seg
+    dev = e.device
+    if alpha_t.shape[0] != U or tgt.key.numel() != R or src.key.numel() != R:
+        raise ValueError("attn_bwd_bond_raw: logits per bond, one target / source per directed row")
+    g_at, g_as, g_e = _rows(U, D, dev), _rows(U, D, dev), _rows(R, D, dev)
+    with _timed("attn_bwd_atom", (R, tgt.n_seg)):
+        _lib.check(lib.matris_attn_bwd_bond(U, _p(alpha_t), _p(alpha_s), D, _p(e), _p(d2u.rowptr), _p(d2u.perm),
+                                            _p(tgt.key), _p(src.key), _p(y_t), _p(y_s), _p(lse_t), _p(lse_s),
+                                            _p(g_yt), _p(g_ys), ldgy, _p(g_base), float(base_scale), _p(g_at),
+                                            _p(g_as), _p(g_e), _stream()), "matris_attn_bwd_bond")
+    return g_at, g_as, g_e
+
+
 class _SegAttn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp):

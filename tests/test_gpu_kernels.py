@@ -709,6 +709,55 @@ def test_ffn_bwd_env_term(M, E, mode):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("case", ["c3", "small", "uneven"])
+def test_attn_bwd_by_bond(case):
+    """matris_attn_bwd_bond (the atom-graph attention backward by undirected bond) against
+    matris_attn_bwd through d2u followed by the d2u segment sums of its logit gradients
+    and the gathered base gradient: bit-identical when every bond has its two directed
+    copies (C3 atom graph, a small random graph), to fp32 rounding when segments are
+    uneven (d2u segments of 0-5 rows)."""
+    ops = _ops()
+    torch.manual_seed(3)
+    if case == "c3":
+        from matris_amd import workloads as W
+        from matris_amd.model.batch import process_graphs
+        from matris_amd.model.model import MatRIS
+        g = MatRIS().to(DEV).graph_converter(W.c3_cu864())
+        bg = process_graphs([g])
+        tgt, src = bg["atom_graph_dict"]["grp_tgt"], bg["atom_graph_dict"]["grp_src"]
+        d2u_key = bg["directed2undirected"].to(torch.int32).contiguous()
+        N, U = tgt.n_seg, bg["n_undirected"]
+    else:
+        N, U = 50, 400
+        if case == "small":
+            d2u_key = torch.arange(U, dtype=torch.int32).repeat_interleave(2)[torch.randperm(2 * U)]
+        else:
+            d2u_key = torch.randint(0, U, (2 * U,), dtype=torch.int32)
+        d2u_key = d2u_key.to(DEV)
+        R = d2u_key.numel()
+        tgt = ops.Grouping.build(torch.sort(torch.randint(0, N, (R,), device=DEV)).values.to(torch.int32), N,
+                                 sorted_rows=True)
+        src = ops.Grouping.build(torch.randint(0, N, (R,), dtype=torch.int32, device=DEV), N)
+    R = d2u_key.numel()
+    d2u = ops.Grouping.build(d2u_key, U)
+    a_t, a_s = torch.randn(U, 128, device=DEV), torch.randn(U, 128, device=DEV)
+    e = torch.randn(R, 128, device=DEV)
+    y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, d2u)
+    g_y = torch.randn(N, 256, device=DEV)
+    g_b = torch.randn(U, 128, device=DEV)
+    base = ops.gather_raw(g_b, d2u.key, 0.5)
+    at_r, as_r, ge_r = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, 128:], tgt, src, d2u,
+                                        ldgy=256, g_e_base=base)
+    at_r, as_r = ops.seg_sum_raw(at_r, d2u), ops.seg_sum_raw(as_r, d2u)
+    at_b, as_b, ge_b = ops.attn_bwd_bond_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, 128:], tgt, src, d2u,
+                                             ldgy=256, g_base=g_b, base_scale=0.5)
+    assert torch.equal(ge_b, ge_r)
+    if case == "uneven":
+        assert _rel(at_b, at_r) < 1e-6 and _rel(as_b, as_r) < 1e-6
+    else:
+        assert torch.equal(at_b, at_r) and torch.equal(as_b, as_r)
+
+
 @pytest.mark.parametrize("mode,tol", _MODES)
 @pytest.mark.parametrize("M", [1, 63, 64, 1000, 4097, 140001])
 def test_ffn_fwd_bwd(M, mode, tol):
