@@ -381,19 +381,22 @@ int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, c
                          const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                          float *g_x0, int acc0, const float *res_w, const float *res_src, const int32_t *run_key,
                          int run_blk, int mode, void *stream);
-/* The GatedMLP backward of the line Refinement with the edge_FFN backward in front of it,
- * in one kernel (two-plane modes 0, 2, 3; interaction_block.py:243-275): the output
- * gradient g_out of matris_gmlp_bwd is not read but computed per tile as
- *   g_out = ((ffn_g W2) * SiLU'(ffn_p)) W1 + g_agg_env[t_idx] * env[s_idx]
- * (matris_ffn_bwd_env's g_x; g_agg_env may be NULL for no envelope term), with ffn_g the
- * gradient of tb' = edge_FFN(h) + r tb, ffn_p the FFN's saved W1 h and ffn_w1tp / ffn_w2tp
- * the packs matris_ffn_bwd takes.  Source 0's gradient gains res_w * ffn_g (res_w may be
- * NULL).  run_key / run_blk as in matris_gmlp_bwd_runs (run_key may be NULL). */
+/* The GatedMLP backward of a Refinement with the edge_FFN backward in front of it, in
+ * one kernel (two-plane modes 0, 2, 3; interaction_block.py:218-278): the output gradient
+ * g_out of matris_gmlp_bwd is not read but computed per tile as
+ *   g_out = ((G W2) * SiLU'(ffn_p)) W1 + g_agg_env[t_idx] * env[s_idx]
+ * (matris_ffn_bwd_env's g_x; g_agg_env may be NULL for no envelope term), with G the
+ * gradient of the FFN's output -- ffn_g [m,128], or with ffn_g_idx (may be NULL) row r of
+ * G is ffn_g_scale * ffn_g[ffn_g_idx[r]] (the atom graph: half the bond gradient of each
+ * directed copy) -- ffn_p the FFN's saved W1 h and ffn_w1tp / ffn_w2tp the packs
+ * matris_ffn_bwd takes.  Source 0's gradient gains res_w * ffn_g (res_w may be NULL; not
+ * with ffn_g_idx).  run_key / run_blk as in matris_gmlp_bwd_runs (run_key may be NULL). */
 int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float *z, const void *w1tp, const void *w2tp,
                         const float *norm_c, const float *norm_g, float eps, float *g_x, float *g_x0,
                         const float *res_w, const int32_t *run_key, int run_blk, const float *ffn_g,
-                        const float *ffn_p, const void *ffn_w1tp, const void *ffn_w2tp, const float *g_agg_env,
-                        const float *env, const int32_t *t_idx, const int32_t *s_idx, int mode, void *stream);
+                        const int32_t *ffn_g_idx, float ffn_g_scale, const float *ffn_p, const void *ffn_w1tp,
+                        const void *ffn_w2tp, const float *g_agg_env, const float *env, const int32_t *t_idx,
+                        const int32_t *s_idx, int mode, void *stream);
 /* Rows per GatedMLP work-group tile (the tile of matris_gmlp_bwd_runs's partial sums). */
 int matris_gmlp_tile_rows(void);
 
@@ -423,7 +426,8 @@ int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *src_host, con
  * is) with the line Refinement's edge_FFN on the output rows, in the same kernel
  * (interaction_block.py:263-275: tb' = edge_FFN(h) + r_e tb with h this GatedMLP's out):
  *   t = h W1^T (saved to ffn_save_p [m,128] when non-NULL),
- *   ffn_out [m,128] = SiLU(t) W2^T + ffn_res_w * ffn_res
+ *   ffn_out [m,128] = SiLU(t) W2^T + ffn_res_w * ffn_res   (ffn_res may be NULL: no residual,
+ *   as in the atom-graph Refinement, whose residual comes after the d2u mean)
  * with ffn_w1p, ffn_w2p the packs matris_ffn_fwd takes.  out (h) is still written; the
  * GatedMLP residual (res_src / res_w / res_out) is not available here.  Equal to
  * matris_gmlp_fwd_proj followed by matris_ffn_fwd up to the FFN's fp32 sum order. */

@@ -64,8 +64,8 @@ struct GmlpProj {
     int n;
 };
 
-// A tail on the output rows (the line refinement's edge_FFN, interaction_block.py:269-275):
-//   t = W1 out (saved to save_p when given),  ffn_out = W2 SiLU(t) + res_w * res
+// A tail on the output rows (a Refinement's edge_FFN, interaction_block.py:269-275):
+//   t = W1 out (saved to save_p when given),  ffn_out = W2 SiLU(t) (+ res_w * res if res)
 // with W1, W2 packs of the FFN's [128, 128] Linear weights.
 struct FfnTail {
     const uint4 *W1, *W2;
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
     }
     // the tail's residual rows (layout of its final row stores), loaded here for the same reason
     float4 tres[(BM * 32) / 256];
-    if constexpr (TAIL) {
+    if (TAIL && tail.res) {
 #pragma unroll
         for (int it = 0; it < (BM * 32) / 256; ++it) {
             const int q = it * 256 + tid;
@@ -408,9 +408,11 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
             const int row = q >> 5, cc = (q & 31) * 4;
             if (m0 + row < M) {
                 float4 v = *reinterpret_cast<const float4 *>(Ts + row * LDH + cc);
-                const float4 w = *reinterpret_cast<const float4 *>(tail.res_w + cc);
-                const float4 x = tres[it];
-                v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
+                if (tail.res) {
+                    const float4 w = *reinterpret_cast<const float4 *>(tail.res_w + cc);
+                    const float4 x = tres[it];
+                    v.x += w.x * x.x; v.y += w.y * x.y; v.z += w.z * x.z; v.w += w.w * x.w;
+                }
                 st_nt4(tail.out + (m0 + row) * MATRIS_D + cc, v);  // read again only by the next block
             }
         }
@@ -426,12 +428,16 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
 // gradient is not read but computed per tile,
 //   g_out = ((g W2) * SiLU'(p)) W1 + ge[t] * env[s]      (ge == NULL: no envelope term)
 // with g, p [M,128] the FFN's output gradient and saved W1 x, W1t / W2t packs of W1^T /
-// W2^T (as matris_ffn_bwd takes them), ge [*,128] = g_agg * env per bond.
+// W2^T (as matris_ffn_bwd takes them), ge [*,128] = g_agg * env per bond.  With gidx, g is
+// read through it and scaled: row r of the FFN's output gradient is gscale * g[gidx[r]]
+// (the atom-graph Refinement: half the bond gradient of each directed copy).
 struct FfnHead {
     const float *g, *p;
     const uint4 *W1t, *W2t;
     const float *ge, *env;
     const int32_t *t, *s;
+    const int32_t *gidx;
+    float gscale;
 };
 // Store a wave's [64, 32*NCT] accumulators to rows of dst (row stride ld) at column
 // col + ct*32 + lane%32, rows below nrows only, with streaming stores (the gradient rows
@@ -835,7 +841,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         const int hrt = wave >> 2, hct = wave & 3;
         const int64_t hrow = min(m0 + hrt * 32 + l32, M - 1);
         float4 xr[4], pv[4];
-        load_rows4(xr, head.g, m0, M, tid);
+        if (head.gidx) {  // load_rows4's layout, rows read through gidx and scaled
+            const int64_t gr = head.gidx[min(m0 + (tid >> 3), M - 1)];
+            const float4 *gp = reinterpret_cast<const float4 *>(head.g + gr * MATRIS_D) + (tid & 7) * 2;
+            xr[0] = gp[0]; xr[1] = gp[1]; xr[2] = gp[16]; xr[3] = gp[17];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xr[q] = mul4(xr[q], head.gscale);
+        } else {
+            load_rows4(xr, head.g, m0, M, tid);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             pv[j] = *reinterpret_cast<const float4 *>(head.p + hrow * MATRIS_D + hct * 32 + 8 * j + 4 * h);
@@ -1120,7 +1134,7 @@ static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, c
     if (res_out && (!res_src || !res_w)) return MATRIS_E_ARG;
     const bool has_tail = tail.W1 != nullptr;
     if (has_tail && (res_out || !aligned16(tail.W1) || !tail.W2 || !aligned16(tail.W2) || !tail.out ||
-                     !aligned16(tail.out) || !tail.res || !aligned16(tail.res) || !tail.res_w ||
+                     !aligned16(tail.out) || !aligned16(tail.res) || (tail.res && !tail.res_w) ||
                      !aligned16(tail.res_w) || !aligned16(tail.save_p)))
         return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
@@ -1255,11 +1269,13 @@ extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const 
 extern "C" int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float *z, const void *w1tp,
                                    const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                                    float *g_x0, const float *res_w, const int32_t *run_key, int run_blk,
-                                   const float *ffn_g, const float *ffn_p, const void *ffn_w1tp, const void *ffn_w2tp,
+                                   const float *ffn_g, const int32_t *ffn_g_idx, float ffn_g_scale,
+                                   const float *ffn_p, const void *ffn_w1tp, const void *ffn_w2tp,
                                    const float *g_agg_env, const float *env, const int32_t *t_idx,
                                    const int32_t *s_idx, int mode, void *stream) {
-    if (!ffn_w1tp) return MATRIS_E_ARG;
-    const FfnHead head{ffn_g, ffn_p, (const uint4 *)ffn_w1tp, (const uint4 *)ffn_w2tp, g_agg_env, env, t_idx, s_idx};
+    if (!ffn_w1tp || (ffn_g_idx && res_w)) return MATRIS_E_ARG;
+    const FfnHead head{ffn_g,  ffn_p, (const uint4 *)ffn_w1tp, (const uint4 *)ffn_w2tp, g_agg_env, env, t_idx, s_idx,
+                       ffn_g_idx, ffn_g_idx ? ffn_g_scale : 1.0f};
     // the residual term of source 0's gradient is res_w * (the FFN's output gradient)
     return gmlp_bwd_launch(m, k, nullptr, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, 0, res_w,
                            res_w ? ffn_g : nullptr, run_key, run_key ? run_blk : -1, head, mode, stream);

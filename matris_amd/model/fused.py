@@ -364,17 +364,19 @@ class _AtomRefinement(torch.autograd.Function):
         L, Mm = layer.node_FFN.layers, layer.edge_FFN.layers
         pn = layer._node_ffn.get(L[0].weight, L[3].weight)
         pm = layer._edge_ffn.get(Mm[0].weight, Mm[3].weight)
-        h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [bond, atom, atom], [d2u.key, tgt.key, src.key], Ed, mode)
         smoothed = bool(layer.use_smoothed_for_delta_edge)
         if smoothed:  # h * w also feeds the edge FFN: materialised
+            h, p_h, z_h, _ = ops.gmlp_fwd_raw(ph, [bond, atom, atom], [d2u.key, tgt.key, src.key], Ed, mode)
             w = ops.gather_raw(env, d2u.key)
             hw = h * w
             agg = ops.seg_sum_raw(hw, tgt)
-        else:  # sum_tgt h * env[d2u] in one pass, w never materialised
+            de, p_de = ops.ffn_fwd_raw(pm, hw, mode)
+        else:  # de = edge_FFN(h) in the GatedMLP's launch; sum_tgt h * env[d2u] in one pass
+            h, p_h, z_h, de, p_de = ops.gmlp_fwd_ffn_raw(ph, [bond, atom, atom], [d2u.key, tgt.key, src.key], Ed,
+                                                         mode, pm)
             w, hw = env, None
             agg = ops.seg_sum_mul_raw(h, tgt, env, d2u.key)
         atom_new, p_dn = ops.ffn_fwd_raw(pn, agg, mode, res=(atom, r_n))
-        de, p_de = ops.ffn_fwd_raw(pm, hw if smoothed else h, mode)
         del hw, agg
         bond_new = ops.seg_sum_raw(de, d2u, 0.5, base=(bond, r_e))
         ctx.save_for_backward(w, h, p_h, z_h, p_dn, p_de)  # w = env[d2u] if smoothed, else env
@@ -396,8 +398,21 @@ class _AtomRefinement(torch.autograd.Function):
         g_bond_new = _zeros_if_none(g_bond_new, ops._rows(d2u.n_seg, D, h.device))
         g_atom = ops._rows(N, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_atom_new, p_dn, mode, g_res=g_atom, res_w=r_n)
+        del p_dn
+        if not ctx.smoothed and mode != 6:
+            # g_h = edge_FFN's input gradient (from half the bond gradient of each directed
+            # copy) + g_agg[tgt] * env[d2u], computed per tile inside the GatedMLP backward
+            g_env = ops.seg_sum_mul_raw(h, d2u, g_agg, tgt.key)
+            del h
+            g_x = ops.gmlp_bwd_ffn_raw(ph, p_h, z_h, 3 * D, mode, pm, g_bond_new, p_de, env_term=(g_agg, w, tgt, d2u),
+                                       runs=_runs(tgt, 1), ffn_g_idx=d2u.key, ffn_g_scale=0.5)
+            del p_h, z_h, p_de, w
+            g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
+            ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
+                            second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
+            return g_atom, g_bond, g_env, None, None, None
         g_te = ops.ffn_bwd_raw(pm, ops.gather_raw(g_bond_new, d2u.key, 0.5), p_de, mode)
-        del p_dn, p_de
+        del p_de
         if ctx.smoothed:
             g_hw = ops.gather_raw(g_agg, tgt.key)
             g_hw += g_te

@@ -631,11 +631,12 @@ def gmlp_fwd_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res=None, s
     return _gmlp_fwd(pack, srcs, idxs, n_rows, mode, res, save, None)[:4]
 
 
-def gmlp_fwd_ffn_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, ffn: "_WeightPack", ffn_res, ffn_res_w,
-                     save: bool = True):
+def gmlp_fwd_ffn_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, ffn: "_WeightPack", ffn_res=None,
+                     ffn_res_w=None, save: bool = True):
     """matris_gmlp_fwd_ffn: the GatedMLP forward with the FFN tail on its output rows,
-    ffn_out = W2 SiLU(W1 out) + ffn_res_w * ffn_res (ffn = the FFN's pack, as for
-    ffn_fwd_raw).  Returns (out, p, z, ffn_out, ffn_p); p, z, ffn_p None when not saved."""
+    ffn_out = W2 SiLU(W1 out) (+ ffn_res_w * ffn_res when given; ffn = the FFN's pack, as
+    for ffn_fwd_raw).  Returns (out, p, z, ffn_out, ffn_p); p, z, ffn_p None when not
+    saved."""
     out, p, z, _, t_out, t_p = _gmlp_fwd(pack, srcs, idxs, n_rows, mode, None, save, (ffn, ffn_res, ffn_res_w))
     return out, p, z, t_out, t_p
 
@@ -654,17 +655,19 @@ def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: boo
     t_out = t_p = ret_tp = None
     if tail is not None:
         t_pack, t_res, t_rw = tail
-        if res is not None or tuple(t_res.shape) != (n_rows, D) or not t_res.is_contiguous():
-            raise ValueError("gmlp_fwd_ffn_raw: the residual source must be a contiguous [n_rows, 128] tensor")
+        if res is not None or (t_res is not None and (tuple(t_res.shape) != (n_rows, D) or not t_res.is_contiguous()
+                                                      or t_rw is None)):
+            raise ValueError("gmlp_fwd_ffn_raw: the residual source must be a contiguous [n_rows, 128] tensor, "
+                             "with its weights")
         t_out = _rows(n_rows, D, dev)
         t_p = ret_tp = _rows(n_rows, D, dev) if save else None
     if _DISCARD["on"]:  # placeholders: the kernel writes neither
         p = z = t_p = None
-    t_bytes = 0 if tail is None else 4 * D * n_rows * (2 + (t_p is not None))
+    t_bytes = 0 if tail is None else 4 * D * n_rows * (1 + (t_res is not None) + (t_p is not None))
     if tail is not None:
         # the tail rides the gather-after-GEMM entry point (with or without projected sources)
-        t_args = (_p(t_pack.b("w0", mode)), _p(t_pack.b("w1", mode)), _p(t_p), _p(t_res), _p(_f32c(t_rw)),
-                  _p(t_out))
+        t_args = (_p(t_pack.b("w0", mode)), _p(t_pack.b("w1", mode)), _p(t_p), _p(t_res),
+                  _p(_f32c(t_rw) if t_rw is not None else None), _p(t_out))
     if not proj and tail is None:
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
@@ -760,26 +763,35 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
 
 
 def gmlp_bwd_ffn_raw(pack: GmlpPack, p, z, K: int, mode: int, ffn: "_WeightPack", ffn_g, ffn_p, env_term=None,
-                     g_x0=None, res_w=None, runs=None):
+                     g_x0=None, res_w=None, runs=None, ffn_g_idx=None, ffn_g_scale: float = 1.0):
     """matris_gmlp_bwd_ffn: gmlp_bwd_raw(pack, g, p, z, K, mode, g_x0=g_x0, res_w=res_w,
-    res_src=ffn_g, runs=runs) with g = ffn_bwd_raw(ffn, ffn_g, ffn_p, mode, env_term=...)
-    computed inside the kernel (two-plane modes).  Returns g_x as gmlp_bwd_raw does."""
+    res_src=ffn_g, runs=runs) with g = ffn_bwd_raw(ffn, G, ffn_p, mode, env_term=...)
+    computed inside the kernel (two-plane modes), G = ffn_g, or ffn_g_scale *
+    ffn_g[ffn_g_idx] with an index (int32, one per row; not with res_w).  env_term =
+    (ge, env, a, b): the term ge[a.key] * env[b.key] (a, b groupings with one key per row).
+    Returns g_x as gmlp_bwd_raw does."""
     lib = _lib.load()
     M = p.shape[0]
     if mode == 6:
         raise ValueError("gmlp_bwd_ffn_raw: two-plane modes only (0, 2, 3)")
-    for t in (ffn_g, ffn_p):
-        if tuple(t.shape) != (M, D) or not t.is_contiguous():
-            raise ValueError("gmlp_bwd_ffn_raw: ffn_g and ffn_p must be contiguous [M, 128] tensors")
+    if ffn_g_idx is None:
+        if tuple(ffn_g.shape) != (M, D) or not ffn_g.is_contiguous():
+            raise ValueError("gmlp_bwd_ffn_raw: ffn_g must be a contiguous [M, 128] tensor")
+    elif (ffn_g_idx.dtype != torch.int32 or ffn_g_idx.numel() != M or not ffn_g_idx.is_contiguous()
+          or ffn_g.shape[1] != D or not ffn_g.is_contiguous() or res_w is not None):
+        raise ValueError("gmlp_bwd_ffn_raw: ffn_g_idx is one int32 row of ffn_g per row, without res_w")
+    if tuple(ffn_p.shape) != (M, D) or not ffn_p.is_contiguous():
+        raise ValueError("gmlp_bwd_ffn_raw: ffn_p must be a contiguous [M, 128] tensor")
     g_x = None if (g_x0 is not None and K == D) else _rows(M, K - (D if g_x0 is not None else 0), p.device)
     ge = env = tk = sk = None
-    nbytes = 4 * M * (2 * D + 2 * 256 + K)
+    nbytes = 4 * M * (2 * D + 2 * 256 + K) if ffn_g_idx is None else \
+        4 * M * (D + 2 * 256 + K + 1) + 4 * D * ffn_g.shape[0]
     if env_term is not None:
         ge, env, tgt, src = env_term
         tk, sk = tgt.key, src.key
-        if tk.numel() != M or sk.numel() != M or ge.shape != env.shape:
-            raise ValueError("gmlp_bwd_ffn_raw: env_term needs one target / source per row and ge shaped as env")
-        nbytes += 8 * M + 2 * 4 * D * env.shape[0]
+        if tk.numel() != M or sk.numel() != M or ge.shape[1] != D or env.shape[1] != D:
+            raise ValueError("gmlp_bwd_ffn_raw: env_term needs one key per row in both groupings, 128-wide tables")
+        nbytes += 8 * M + 4 * D * (ge.shape[0] + env.shape[0])
     key, blk = runs if runs is not None else (None, -1)
     if key is not None:
         if key.dtype != torch.int32 or key.numel() != M or not key.is_contiguous():
@@ -788,7 +800,8 @@ def gmlp_bwd_ffn_raw(pack: GmlpPack, p, z, K: int, mode: int, ffn: "_WeightPack"
     with _timed("gmlp_bwd", (M, K, nbytes, M)):  # the last field: rows of the FFN head
         _lib.check(lib.matris_gmlp_bwd_ffn(M, K, _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)),
                                            _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), _p(res_w),
-                                           _p(key), int(blk), _p(ffn_g), _p(ffn_p), _p(ffn.b("wt0", mode)),
+                                           _p(key), int(blk), _p(ffn_g), _p(ffn_g_idx), float(ffn_g_scale),
+                                           _p(ffn_p), _p(ffn.b("wt0", mode)),
                                            _p(ffn.b("wt1", mode)), _p(ge), _p(env), _p(tk), _p(sk), mode, _stream()),
                    "matris_gmlp_bwd_ffn")
     return g_x

@@ -310,6 +310,10 @@ def test_gated_mlp_fwd_ffn_tail(M, mode, tol, gtg):
             with ops.discard_saves():
                 _, _, _, t_out2, _ = ops.gmlp_fwd_ffn_raw(pack, srcs, idx, M, mm, fp, tb, r)
             assert torch.equal(t_out2, t_out)
+            # no residual (the atom-graph Refinement's edge FFN)
+            _, _, _, t_out4, t_p4 = ops.gmlp_fwd_ffn_raw(pack, srcs, idx, M, mm, fp)
+            assert torch.equal(t_p4, t_p)
+            assert _rel(t_out4, F.silu(t64) @ w2.double().t()) < tol
             _, p3, z3, t_out3, t_p3 = ops.gmlp_fwd_ffn_raw(pack, srcs, idx, M, mm, fp, tb, r, save=False)
             assert p3 is None and z3 is None and t_p3 is None and torch.equal(t_out3, t_out)
     finally:
@@ -635,6 +639,45 @@ def test_gmlp_bwd_ffn_head(M, E, env, runs, mode, tol):
             assert _rel(gxb, gxa) < tol
         with pytest.raises(ValueError):
             ops.gmlp_bwd_ffn_raw(pack, p, z, 512, 6, fp, g_new, p_de)
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
+@pytest.mark.parametrize("mode,tol", [("f16x3", 1e-5), ("fp32", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("M,U,N", [(1, 1, 1), (300, 150, 20), (67396, 33698, 864)])
+def test_gmlp_bwd_ffn_head_gathered(M, U, N, mode, tol):
+    """matris_gmlp_bwd_ffn as the atom-graph Refinement uses it: the FFN's output gradient
+    read through the directed-to-undirected index at half scale, the term g_agg[tgt] *
+    env[d2u], no residual, the centre-atom block run-summed -- against matris_gather,
+    matris_ffn_bwd, matris_gather_mul and matris_gmlp_bwd_runs, to fp32 rounding."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + 23)
+        mod = _ShimGated(_TorchGMLP(384)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        srcs = [torch.randn(M, 128, device=DEV) for _ in range(3)]
+        _, p, z, _ = ops.gmlp_fwd_raw(pack, srcs, [None] * 3, M, mm)
+        fp = ops._WeightPack().get(torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11)
+        g_b, p_de = torch.randn(U, 128, device=DEV), torch.randn(M, 128, device=DEV)
+        env, g_agg = torch.rand(U, 128, device=DEV), torch.randn(N, 128, device=DEV)
+        d2u = ops.Grouping.build(_keys(M, U, M + 2, empty_every=10 ** 9).to(DEV), U)
+        tkey = _sorted_keys(M, N, M + 4).to(DEV)
+        tgt = ops.Grouping.build(tkey, N, sorted_rows=True)
+        g_te = ops.ffn_bwd_raw(fp, ops.gather_raw(g_b, d2u.key, 0.5), p_de, mm)
+        g_h = ops.gather_mul_raw(g_agg, tkey, env, d2u.key, out=g_te, accumulate=True)
+        gxa = ops.gmlp_bwd_raw(pack, g_h, p, z, 384, mm, runs=(tkey, 1))
+        gxb = ops.gmlp_bwd_ffn_raw(pack, p, z, 384, mm, fp, g_b, p_de, env_term=(g_agg, env, tgt, d2u),
+                                   runs=(tkey, 1), ffn_g_idx=d2u.key, ffn_g_scale=0.5)
+        assert _rel(torch.cat([gxb[:, :128], gxb[:, 256:]], 1), torch.cat([gxa[:, :128], gxa[:, 256:]], 1)) < tol
+        T = ops.gmlp_tile_rows()
+        sa = ops.seg_sum_raw(gxa, tgt, ldx=384, col_off=128, tile_rows=T)
+        sb = ops.seg_sum_raw(gxb, tgt, ldx=384, col_off=128, tile_rows=T)
+        assert _rel(sb, sa) < tol
+        with pytest.raises(ValueError):  # a gathered G has no residual term
+            ops.gmlp_bwd_ffn_raw(pack, p, z, 384, mm, fp, g_b, p_de, g_x0=torch.empty(M, 128, device=DEV),
+                                 res_w=env[0], ffn_g_idx=d2u.key, ffn_g_scale=0.5)
     finally:
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
