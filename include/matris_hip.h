@@ -397,6 +397,17 @@ int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float *z, const 
                         const int32_t *ffn_g_idx, float ffn_g_scale, const float *ffn_p, const void *ffn_w1tp,
                         const void *ffn_w2tp, const float *g_agg_env, const float *env, const int32_t *t_idx,
                         const int32_t *s_idx, int mode, void *stream);
+/* matris_gmlp_bwd_runs (two-plane modes 0, 2, 3; g_x0 required, K >= 256) with a
+ * projection added to source 0's gradient before it is stored: g_x0 = source 0's
+ * gradient + pair_g0 W[0:128] + pair_g1 W[128:256] (+ res_w * res_src), pair_wtp the pack
+ * of W^T that matris_pair_bwd takes.  The line graph attention (interaction_block.py:104-
+ * 134): its logits are W_s tb and W_t tb of the same angle rows as the edge update's
+ * source 0, so their backward lands in the same gradient rows (matris_pair_bwd with
+ * accumulate, without the separate read-modify-write of g_x0). */
+int matris_gmlp_bwd_pair(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
+                         const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
+                         float *g_x0, const float *res_w, const float *res_src, const int32_t *run_key, int run_blk,
+                         const float *pair_g0, const float *pair_g1, const void *pair_wtp, int mode, void *stream);
 /* Rows per GatedMLP work-group tile (the tile of matris_gmlp_bwd_runs's partial sums). */
 int matris_gmlp_tile_rows(void);
 

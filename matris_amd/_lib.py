@@ -112,6 +112,8 @@ _SIGS = {
     "matris_gmlp_bwd_runs": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
     "matris_gmlp_bwd_ffn": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _P, _P, _F, _P, _P, _P, _P,
                                  _P, _P, _P, _I, _P]),
+    "matris_gmlp_bwd_pair": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I,
+                                  _P]),
     "matris_gmlp_tile_rows": (_I, []),
     "matris_silu_bwd": (_I, [_I64, _P, _P, _P, _P]),
     "matris_silu_grad_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P]),

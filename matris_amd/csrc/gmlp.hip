@@ -439,6 +439,16 @@ struct FfnHead {
     const int32_t *gidx;
     float gscale;
 };
+
+// A projection added to source 0's gradient before it leaves (the line graph attention's
+// W_s / W_t backward, interaction_block.py:104-112: the attention logits are projections
+// of the same angle rows as the edge update's source 0):
+//   g_x0 += g0 W[0:128] + g1 W[128:256]
+// with g0, g1 [M,128] and Wt the pack of W^T ([128, 256]) that matris_pair_bwd takes.
+struct PairTail {
+    const float *g0, *g1;
+    const uint4 *Wt;
+};
 // Store a wave's [64, 32*NCT] accumulators to rows of dst (row stride ld) at column
 // col + ct*32 + lane%32, rows below nrows only, with streaming stores (the gradient rows
 // are read once, by the segment sums that follow).
@@ -807,7 +817,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_bwd_kernel(int64_t M, int K, cons
 // phases 2 and 3 -- half the registers per wave, so a CU holds 16 waves instead of 8 at
 // the same LDS per work-group.  Phase 3 runs 256-column passes from the top of K, source
 // 0's block last (for K = 384 / 128 only waves 0-3 have columns in the last pass).
-template <int MODE, bool HEAD = false>
+template <int MODE, bool HEAD = false, bool PAIR = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void gmlp_bwd8_kernel(int64_t M, int K, const float *__restrict__ g_out,
                                                            const float *__restrict__ P, const float *__restrict__ Z,
                                                            const uint4 *__restrict__ W1t,
@@ -818,7 +828,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                                                            int acc0, const float *__restrict__ res_w,
                                                            const float *__restrict__ res_src,
                                                            const int32_t *__restrict__ run_key, int run_blk,
-                                                           FfnHead head, unsigned *range_flag) {
+                                                           FfnHead head, PairTail pair, unsigned *range_flag) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes");
     __shared__ __align__(16) float G[BM * LDH];
     __shared__ __align__(16) float rinv[BM];
@@ -1069,7 +1079,55 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         }
         if (last && epi0) {
             __syncthreads();  // all waves are done reading G
-            if (active && col0 < MATRIS_D) acc_to_lds<1>(a2, G, LDH, col0, lane);
+            // with the pair tail, source 0's block goes to G's first 32 KB (row stride 128)
+            // and the other 32 KB stage g0, then g1
+            constexpr int LD0 = PAIR ? MATRIS_D : LDH;
+            if (active && col0 < MATRIS_D) acc_to_lds<1>(a2, G, LD0, col0, lane);
+            if constexpr (PAIR) {
+                // wave w adds the 32 x 32 tile (rows 32 (w / 4), columns 32 (w % 4)) of
+                // g0 W[0:128] + g1 W[128:256] to source 0's block (one power-of-two scale
+                // per row for g0 and g1 in MODE 2)
+                __shared__ float pinv[BM];
+                uint4 *Pf = Gf + 2 * 8 * 2 * 64;
+                const uint4 *pw = pair.Wt;
+                const float pws = take_wscale<MODE>(pw);
+                const int prt = wave >> 2, pct = wave & 3;
+                float4 xa[4], xb[4];
+                load_rows4(xa, pair.g0, m0, M, tid);
+                load_rows4(xb, pair.g1, m0, M, tid);
+                if constexpr (MODE == 2) {
+                    float mx = 0.f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) mx = abs_max4(abs_max4(mx, xa[q]), xb[q]);
+                    const RowScale rs = row_scale(group8_max(mx));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        xa[q] = mul4(xa[q], rs.s);
+                        xb[q] = mul4(xb[q], rs.s);
+                    }
+                    if ((tid & 7) == 0) pinv[tid >> 3] = rs.inv * pws;
+                }
+                amax = stage_rows4<MODE>(Pf, xa, tid, amax);
+                __syncthreads();
+                v16f pa[1][1];
+                zero_acc(pa);
+                gemm_frag_packed<MODE, 1, 1, MATRIS_D / 16, true>(pa, Pf + prt * (8 * 2 * 64), 8, 0, pw, pct, 256 / 16,
+                                                                  0, lane);
+                __syncthreads();  // every wave is done reading g0
+                amax = stage_rows4<MODE>(Pf, xb, tid, amax);
+                __syncthreads();
+                gemm_frag_packed<MODE, 1, 1, MATRIS_D / 16, true>(pa, Pf + prt * (8 * 2 * 64), 8, 0, pw, pct, 256 / 16,
+                                                                  MATRIS_D / 16, lane);
+                const float sc = MODE == 2 ? pinv[prt * 32 + l32] : pws;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float4 *t = reinterpret_cast<float4 *>(G + (prt * 32 + l32) * MATRIS_D + pct * 32 + 8 * j + 4 * h);
+                    float4 v = *t;
+                    v.x += pa[0][0][4 * j] * sc; v.y += pa[0][0][4 * j + 1] * sc;
+                    v.z += pa[0][0][4 * j + 2] * sc; v.w += pa[0][0][4 * j + 3] * sc;
+                    *t = v;
+                }
+            }
         }
         top = base;
     }
@@ -1083,7 +1141,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             const int q = it * 512 + tid;
             const int r = q >> 5, c4 = (q & 31) * 4;
             if (r < nrows) {
-                float4 v = *reinterpret_cast<const float4 *>(G + r * LDH + c4);
+                float4 v = *reinterpret_cast<const float4 *>(G + r * (PAIR ? MATRIS_D : LDH) + c4);
                 if (res_w) {
                     const float4 w = *reinterpret_cast<const float4 *>(res_w + c4);
                     const float4 x = *reinterpret_cast<const float4 *>(got + r * MATRIS_D + c4);
@@ -1202,9 +1260,12 @@ extern "C" int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src
 static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,
                            const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                            float *g_x0, int acc0, const float *res_w, const float *res_src, const int32_t *run_key,
-                           int run_blk, const FfnHead &head, int mode, void *stream) {
+                           int run_blk, const FfnHead &head, const PairTail &pair, int mode, void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
-    const bool has_head = head.W1t != nullptr;
+    const bool has_head = head.W1t != nullptr, has_pair = pair.Wt != nullptr;
+    if (has_pair && (has_head || mode == 6 || !g_x0 || k < 2 * MATRIS_D || !pair.g0 || !aligned16(pair.g0) ||
+                     !pair.g1 || !aligned16(pair.g1) || !aligned16(pair.Wt)))
+        return MATRIS_E_ARG;
     if (m < 0 || k < MATRIS_D || k > 4 * MATRIS_D || (k % MATRIS_D) || (!g_out && !has_head) || !p || !z || !w1tp ||
         !w2tp || !norm_c || !norm_g || (!g_x && !(g_x0 && k == MATRIS_D)))
         return MATRIS_E_ARG;
@@ -1226,25 +1287,24 @@ static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p,
     if (mode == 6) {
         gmlp_bwd_kernel<6><<<grid, 256, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
                                                  res_w, res_src, run_key, run_blk, flag);
-    } else if (has_head) {
-        if (mode == 0)
-            gmlp_bwd8_kernel<0, true><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
-                                                            acc0, res_w, res_src, run_key, run_blk, head, flag);
-        else if (mode == 2)
-            gmlp_bwd8_kernel<2, true><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
-                                                            acc0, res_w, res_src, run_key, run_blk, head, flag);
-        else
-            gmlp_bwd8_kernel<3, true><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0,
-                                                            acc0, res_w, res_src, run_key, run_blk, head, flag);
-    } else if (mode == 0) {
-        gmlp_bwd8_kernel<0><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, res_src, run_key, run_blk, head, flag);
-    } else if (mode == 2) {
-        gmlp_bwd8_kernel<2><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, res_src, run_key, run_blk, head, flag);
     } else {
-        gmlp_bwd8_kernel<3><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, acc0,
-                                                  res_w, res_src, run_key, run_blk, head, flag);
+#define GMLP_BWD8(M_, H_, P_)                                                                                      \
+    gmlp_bwd8_kernel<M_, H_, P_><<<grid, 512, 0, st>>>(m, k, g_out, p, z, w1t, w2t, norm_c, norm_g, eps, g_x, g_x0, \
+                                                       acc0, res_w, res_src, run_key, run_blk, head, pair, flag)
+        if (has_head) {
+            if (mode == 0) GMLP_BWD8(0, true, false);
+            else if (mode == 2) GMLP_BWD8(2, true, false);
+            else GMLP_BWD8(3, true, false);
+        } else if (has_pair) {
+            if (mode == 0) GMLP_BWD8(0, false, true);
+            else if (mode == 2) GMLP_BWD8(2, false, true);
+            else GMLP_BWD8(3, false, true);
+        } else {
+            if (mode == 0) GMLP_BWD8(0, false, false);
+            else if (mode == 2) GMLP_BWD8(2, false, false);
+            else GMLP_BWD8(3, false, false);
+        }
+#undef GMLP_BWD8
     }
     MATRIS_CHECK_LAUNCH();
     return 0;
@@ -1254,7 +1314,7 @@ extern "C" int matris_gmlp_bwd(int64_t m, int k, const float *g_out, const float
                                const void *w2tp, const float *norm_c, const float *norm_g, float eps, float *g_x,
                                float *g_x0, int acc0, const float *res_w, int mode, void *stream) {
     return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, nullptr,
-                           nullptr, -1, FfnHead{}, mode, stream);
+                           nullptr, -1, FfnHead{}, PairTail{}, mode, stream);
 }
 
 extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const float *p, const float *z,
@@ -1263,7 +1323,7 @@ extern "C" int matris_gmlp_bwd_runs(int64_t m, int k, const float *g_out, const 
                                     const float *res_src, const int32_t *run_key, int run_blk, int mode,
                                     void *stream) {
     return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, acc0, res_w, res_src,
-                           run_key, run_key ? run_blk : -1, FfnHead{}, mode, stream);
+                           run_key, run_key ? run_blk : -1, FfnHead{}, PairTail{}, mode, stream);
 }
 
 extern "C" int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float *z, const void *w1tp,
@@ -1278,7 +1338,18 @@ extern "C" int matris_gmlp_bwd_ffn(int64_t m, int k, const float *p, const float
                        ffn_g_idx, ffn_g_idx ? ffn_g_scale : 1.0f};
     // the residual term of source 0's gradient is res_w * (the FFN's output gradient)
     return gmlp_bwd_launch(m, k, nullptr, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, 0, res_w,
-                           res_w ? ffn_g : nullptr, run_key, run_key ? run_blk : -1, head, mode, stream);
+                           res_w ? ffn_g : nullptr, run_key, run_key ? run_blk : -1, head, PairTail{}, mode, stream);
+}
+
+extern "C" int matris_gmlp_bwd_pair(int64_t m, int k, const float *g_out, const float *p, const float *z,
+                                    const void *w1tp, const void *w2tp, const float *norm_c, const float *norm_g,
+                                    float eps, float *g_x, float *g_x0, const float *res_w, const float *res_src,
+                                    const int32_t *run_key, int run_blk, const float *pair_g0, const float *pair_g1,
+                                    const void *pair_wtp, int mode, void *stream) {
+    if (!pair_wtp) return MATRIS_E_ARG;
+    const PairTail pair{pair_g0, pair_g1, (const uint4 *)pair_wtp};
+    return gmlp_bwd_launch(m, k, g_out, p, z, w1tp, w2tp, norm_c, norm_g, eps, g_x, g_x0, 0, res_w, res_src, run_key,
+                           run_key ? run_blk : -1, FfnHead{}, pair, mode, stream);
 }
 
 extern "C" int matris_gmlp_tile_rows(void) { return BM; }

@@ -160,12 +160,18 @@ class _LineAttention(torch.autograd.Function):
         # edge update: source 0's (tb) gradient to g_tb, the bond gathers' to g_x (the
         # target-bond block, rows ascending by target, as tile-run partial sums)
         g_tb = ops._rows(p_e.shape[0], D, p_e.device)
-        g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=False, runs=_runs(tgt, 1))
-        del g_e, p_e, z_e
-        # projections + residual, added to g_tb: g_tb = (g_as W_s + g_at W_t + r_e g_tb_new) + g_tb
-        # (the read-modify-write of g_tb happens in the pair kernel, which stores nothing
-        # before it, instead of behind the GatedMLP backward's stores)
-        ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_tb_new, res_w=r_e, out=g_tb, accumulate=True)
+        if mode != 6:
+            # the projections' backward and the residual join source 0's gradient inside the
+            # GatedMLP backward: g_tb = tb's GatedMLP gradient + g_as W_s + g_at W_t + r_e g_tb_new
+            g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, res_w=r_e, res_src=g_tb_new,
+                                   runs=_runs(tgt, 1), pair=(pp, g_as, g_at))
+            del g_e, p_e, z_e
+        else:
+            g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=False, runs=_runs(tgt, 1))
+            del g_e, p_e, z_e
+            # projections + residual, added to g_tb by the pair kernel (which stores nothing
+            # before its read-modify-write of g_tb)
+            ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_tb_new, res_w=r_e, out=g_tb, accumulate=True)
         del g_as, g_at
         ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True,
                         second=(g_x, src, 1.0, 2 * D, D), tile_rows=_tile_rows(tgt))

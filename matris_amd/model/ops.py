@@ -729,14 +729,15 @@ def gmlp_tile_rows() -> int:
 
 
 def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None, acc0: bool = False, res_w=None,
-                 runs=None, res_src=None):
+                 runs=None, res_src=None, pair=None):
     """matris_gmlp_bwd.  Without g_x0 returns g_x [M, K]; with g_x0 source 0's gradient
     goes (accumulated if acc0, plus res_w * g if res_w) to g_x0 and the other columns to
     g_x [M, K-128] (allocated when not given; None when K == 128).
     runs = (key, blk): source block blk, gathered through `key` (int32 [M], ascending),
     leaves as tile-run partial sums (matris_gmlp_bwd_runs), to be completed by
     seg_sum_raw(..., tile_rows=gmlp_tile_rows()).  res_src: the residual term is
-    res_w * res_src instead of res_w * g."""
+    res_w * res_src instead of res_w * g.  pair = (pack, g0, g1): g_x0 also gains
+    pair_bwd_raw(pack, g0, g1) (matris_gmlp_bwd_pair; two-plane modes, with g_x0)."""
     lib = _lib.load()
     M = p.shape[0]
     if g_x is None and not (g_x0 is not None and K == D):
@@ -746,6 +747,21 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
     nbytes = 4 * M * (D + 2 * 256 + (D if (g_x0 is not None and acc0) else 0) + K + (D if res_src is not None else 0))
     if runs is not None:
         nbytes += 4 * M - 4 * D * M + 4 * D * -(-M // gmlp_tile_rows())
+    if pair is not None:
+        if mode == 6 or g_x0 is None or acc0:
+            raise ValueError("gmlp_bwd_raw: pair needs a two-plane mode and a separate g_x0 (not accumulated)")
+        pp, g0, g1 = pair
+        for t in (g0, g1):
+            if tuple(t.shape) != (M, D) or not t.is_contiguous():
+                raise ValueError("gmlp_bwd_raw: pair gradients must be contiguous [M, 128] tensors")
+        nbytes += 2 * 4 * D * M
+        key, blk = runs if runs is not None else (None, -1)
+        with _timed("gmlp_bwd", (M, K, nbytes)):
+            _lib.check(lib.matris_gmlp_bwd_pair(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)),
+                                                _p(pack.b("w2bt", mode)), _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x),
+                                                _p(g_x0), _p(res_w), _p(res_src), _p(key), int(blk), _p(g0), _p(g1),
+                                                _p(pp.b("cat_t", mode)), mode, _stream()), "matris_gmlp_bwd_pair")
+        return g_x
     with _timed("gmlp_bwd", (M, K, nbytes)):
         args = (M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)), _p(pack.nc),
                 _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w))

@@ -682,6 +682,42 @@ def test_gmlp_bwd_ffn_head_gathered(M, U, N, mode, tol):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("mode,tol", [("f16x3", 1e-6), ("fp32", 1e-6), ("bf16x3", 1e-5)])
+@pytest.mark.parametrize("M", [1, 64, 4097, 70001])
+@pytest.mark.parametrize("runs", [True, False])
+def test_gmlp_bwd_pair_tail(M, runs, mode, tol):
+    """matris_gmlp_bwd_pair (the line attention's projection backward added to source 0's
+    gradient inside the GatedMLP backward) against matris_gmlp_bwd_runs followed by
+    matris_pair_bwd with accumulate: source 0's gradient equal to a few fp32 roundings of
+    its largest value (the sum order differs), every other output bit-identical."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + 31)
+        mod = _ShimGated(_TorchGMLP(384)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        srcs = [torch.randn(M, 128, device=DEV) for _ in range(3)]
+        _, p, z, _ = ops.gmlp_fwd_raw(pack, srcs, [None] * 3, M, mm)
+        pp = ops._WeightPack().get(torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11)
+        g, g_as, g_at, g_new = (torch.randn(M, 128, device=DEV) for _ in range(4))
+        r = torch.rand(128, device=DEV)
+        rn = (_sorted_keys(M, max(1, M // 8), M).to(DEV), 1) if runs else None
+        x0a, x0b = torch.empty(M, 128, device=DEV), torch.empty(M, 128, device=DEV)
+        gxa = ops.gmlp_bwd_raw(pack, g, p, z, 384, mm, g_x0=x0a, runs=rn)
+        ops.pair_bwd_raw(pp, g_as, g_at, mm, res=g_new, res_w=r, out=x0a, accumulate=True)
+        gxb = ops.gmlp_bwd_raw(pack, g, p, z, 384, mm, g_x0=x0b, res_w=r, res_src=g_new, runs=rn, pair=(pp, g_as, g_at))
+        assert _rel(x0b, x0a) < tol
+        if runs:
+            assert torch.equal(gxb[:, 128:], gxa[:, 128:])
+        else:
+            assert torch.equal(gxb, gxa)
+        with pytest.raises(ValueError):
+            ops.gmlp_bwd_raw(pack, g, p, z, 384, mm, pair=(pp, g_as, g_at))
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode", ["f16x3", "fp32", "bf16x6"])
 @pytest.mark.parametrize("M", [1, 64, 4097, 70001])
 def test_gmlp_bwd_res_src(M, mode):
