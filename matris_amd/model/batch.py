@@ -8,6 +8,8 @@ CSR structures built by matris_csr_build.
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import ops
@@ -81,6 +83,62 @@ def validate_graph_indices(g) -> None:
     g.meta["indices_checked"] = sig
 
 
+def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
+    """Everything of a batch that depends on its graphs' index arrays only: the int32 index
+    columns (offset per graph) and their CSR groupings.  Deferred builds: a key outside
+    its range surfaces in the status word that MatRIS.forward reads once per evaluation."""
+    device = graphs[0].lattice.device
+    N, E, U, A = sum(n_atoms), sum(n_dir), sum(n_und), sum(n_ang)
+    canonical = all(g.meta.get("canonical", False) for g in graphs)
+    a_off = u_off = d_off = 0
+    ag, d2u, u2d, lgs = [], [], [], []
+    for g, na, nd, nu, nl in zip(graphs, n_atoms, n_dir, n_und, n_ang):
+        ag.append(g.atom_graph.to(torch.int32) + a_off)
+        d2u.append(g.directed2undirected.to(torch.int32) + u_off)
+        u2d.append(g.undirected2directed.to(torch.int32) + d_off)
+        if nl:
+            if a_off or u_off or d_off:
+                off = torch.tensor([a_off, u_off, d_off, u_off, d_off], dtype=torch.int32, device=device)
+                lgs.append(g.line_graph.to(torch.int32) + off)
+            else:  # the first graph: no offsets, and no host-to-device copy
+                lgs.append(g.line_graph.to(torch.int32))
+        a_off += na
+        u_off += nu
+        d_off += nd
+    atom_graph = torch.cat(ag, 0)
+    tgt32 = atom_graph[:, 0].contiguous()
+    src32 = atom_graph[:, 1].contiguous()
+    d2u32 = torch.cat(d2u, 0).contiguous()
+    u2d32 = torch.cat(u2d, 0).contiguous()
+    t = dict(atom_graph=atom_graph, tgt=tgt32.long(), src=src32.long(), d2u32=d2u32, u2d32=u2d32,
+             grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True),
+             grp_src=Grouping.build(src32, N, deferred=True),
+             grp_d2u=Grouping.build(d2u32, U, sorted_rows=False, deferred=True))
+    if A:
+        lg = torch.cat(lgs, 0)
+        cols = [lg[:, k].contiguous() for k in range(5)]
+        t["line_graph_dict"] = dict(
+            line_graph=torch.stack((cols[0], cols[1], cols[3]), 1), atom_list=cols[0].long(),
+            target_index=cols[1].long(), source_index=cols[3].long(), target_DE_index=cols[2].long(),
+            source_DE_index=cols[4].long(),
+            grp_tgt=Grouping.build(cols[1], U, sorted_rows=True, deferred=True),
+            grp_src=Grouping.build(cols[3], U, deferred=True),
+            grp_atom=Grouping.build(cols[0], N, deferred=True),
+            # directed edges read by each angle (three-body basis and its backward)
+            grp_de_t=Grouping.build(cols[2], E, deferred=True),
+            grp_de_s=Grouping.build(cols[4], E, deferred=True))
+    else:
+        t["line_graph_dict"] = dict(line_graph=torch.zeros(0, 3, dtype=torch.int64, device=device))
+    return t
+
+
+# Topology of single graphs, remembered per graph object under its index signature (the
+# identity, data pointer, version and shape of every index tensor): an edited, replaced or
+# moved index tensor misses.  Positions, lattice and everything derived from them are
+# recomputed on every call.
+_TOPOLOGY: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
 def process_graphs(graphs, compute_stress: bool = True) -> dict:
     for g in graphs:
         validate_graph_indices(g)
@@ -92,35 +150,27 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     n_und = [int(g.undirected2directed.shape[0]) for g in graphs]
     n_ang = [int(g.line_graph.shape[0]) if len(g.line_graph) else 0 for g in graphs]
     N, E, U, A = sum(n_atoms), sum(n_dir), sum(n_und), sum(n_ang)
-    canonical = all(g.meta.get("canonical", False) for g in graphs)
+    if G == 1:
+        sig = graphs[0].index_signature()
+        hit = _TOPOLOGY.get(graphs[0])
+        if hit is None or hit[0] != sig:
+            hit = (sig, _topology(graphs, n_atoms, n_dir, n_und, n_ang))
+            _TOPOLOGY[graphs[0]] = hit
+        topo = hit[1]
+    else:
+        topo = _topology(graphs, n_atoms, n_dir, n_und, n_ang)
 
-    a_off = u_off = d_off = 0
-    ag, d2u, u2d, lgs, carts, lats, imgs = [], [], [], [], [], [], []
-    for g, na, nd, nu, nl in zip(graphs, n_atoms, n_dir, n_und, n_ang):
-        ag.append(g.atom_graph.to(torch.int32) + a_off)
-        d2u.append(g.directed2undirected.to(torch.int32) + u_off)
-        u2d.append(g.undirected2directed.to(torch.int32) + d_off)
-        if nl:
-            if a_off or u_off or d_off:
-                off = torch.tensor([a_off, u_off, d_off, u_off, d_off], dtype=torch.int32, device=device)
-                lgs.append(g.line_graph.to(torch.int32) + off)
-            else:  # the first graph: no offsets, and no host-to-device copy
-                lgs.append(g.line_graph.to(torch.int32))
+    carts, lats, imgs = [], [], []
+    for g in graphs:
         frac = g.atom_frac_coord.detach()
         lat = g.lattice.detach()
         carts.append(frac @ lat)  # processgraph.py:87
         lats.append(lat)
         imgs.append(g.neighbor_image)
-        a_off += na
-        u_off += nu
-        d_off += nd
 
-    atom_graph = torch.cat(ag, 0)
-    tgt32 = atom_graph[:, 0].contiguous()
-    src32 = atom_graph[:, 1].contiguous()
-    tgt, src = tgt32.long(), src32.long()
-    d2u32 = torch.cat(d2u, 0).contiguous()
-    u2d32 = torch.cat(u2d, 0).contiguous()
+    atom_graph, tgt, src = topo["atom_graph"], topo["tgt"], topo["src"]
+    d2u32, u2d32 = topo["d2u32"], topo["u2d32"]
+    grp_tgt, grp_src = topo["grp_tgt"], topo["grp_src"]
     lattice = torch.cat(lats, 0)  # [3G, 3]
     cart = torch.cat(carts, 0)
     image = torch.cat(imgs, 0)
@@ -151,10 +201,6 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     else:
         lat_e = _GraphBroadcast.apply(lat3, torch.tensor(n_dir, device=device), E)
         shift = torch.bmm(image.unsqueeze(1), lat_e).squeeze(1)
-    # deferred builds: key-range errors surface in the status word that MatRIS.forward
-    # reads once per evaluation (no stream sync per grouping)
-    grp_tgt = Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True)
-    grp_src = Grouping.build(src32, N, deferred=True)
     vec = ops.edge_vectors(cart, shift, grp_tgt, grp_src)
     length = torch.norm(vec, dim=1)
     unit = vec / length[:, None]
@@ -164,23 +210,9 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
                directed2undirected=d2u32.long(), undirected2directed=u2d32.long(), volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
                n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
-    out["grp_d2u"] = Grouping.build(d2u32, U, sorted_rows=False, deferred=True)
+    out["grp_d2u"] = topo["grp_d2u"]
     out["atom_graph_dict"] = dict(
         atom_graph=atom_graph, target_index=tgt, source_index=src,
         grp_tgt=grp_tgt, grp_src=grp_src)
-    lgd: dict = {}
-    if A:
-        lg = torch.cat(lgs, 0)
-        cols = [lg[:, k].contiguous() for k in range(5)]
-        lgd = dict(line_graph=lg[:, [0, 1, 3]], atom_list=cols[0].long(), target_index=cols[1].long(),
-                   source_index=cols[3].long(), target_DE_index=cols[2].long(), source_DE_index=cols[4].long(),
-                   grp_tgt=Grouping.build(cols[1], U, sorted_rows=True, deferred=True),
-                   grp_src=Grouping.build(cols[3], U, deferred=True),
-                   grp_atom=Grouping.build(cols[0], N, deferred=True),
-                   # directed edges read by each angle (three-body basis and its backward)
-                   grp_de_t=Grouping.build(cols[2], E, deferred=True),
-                   grp_de_s=Grouping.build(cols[4], E, deferred=True))
-    else:
-        lgd = dict(line_graph=torch.zeros(0, 3, dtype=torch.int64, device=device))
-    out["line_graph_dict"] = lgd
+    out["line_graph_dict"] = dict(topo["line_graph_dict"])
     return out

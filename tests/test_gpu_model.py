@@ -230,6 +230,28 @@ def test_c3_mixed_checkpoint_split_is_bitwise_unchanged(golden):
     _assert_close(mixed, z, "C3 mixed checkpoint", _fp64(golden, "c3"))
 
 
+def test_topology_cache_hits_and_misses(golden):
+    """process_graphs keeps one graph's index columns and CSR groupings between calls: a
+    second evaluation reuses them (bitwise the same results), an in-place edit of an index
+    tensor (its version changes) builds them again, and the results stay those of a fresh
+    graph."""
+    from matris_amd import workloads as W
+    from matris_amd.model import batch
+    model = _model()
+    g = model.graph_converter(W.c4_batch64()[5])
+    first = _efsm(model, [g])
+    topo = batch._TOPOLOGY[g][1]
+    second = _efsm(model, [g])
+    assert batch._TOPOLOGY[g][1] is topo
+    for k in "efsm":
+        assert np.array_equal(first[k], second[k]), k
+    g.line_graph.add_(0)  # same values, new version: the remembered topology is stale
+    third = _efsm(model, [g])
+    assert batch._TOPOLOGY[g][1] is not topo
+    for k in "efsm":
+        assert np.array_equal(first[k], third[k]), k
+
+
 def _degenerate_graph(z, prefix):
     return _graph_from_arrays({f"{prefix}{k}": z[f"{prefix}{k}"] for k in
                                ("z", "frac", "lattice", "image", "atom_graph", "line_graph", "d2u", "u2d")}, prefix)
