@@ -1009,14 +1009,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     __syncthreads();
 
     // phase 2: g_h = g_z W2, wave w -> columns [32w, 32w + 32) (block w / 4), then
-    // g_p = g_h * SiLU'(p) written back pre-split
+    // g_p = g_h * SiLU'(p) written back pre-split.  (With the FFN head, phases 2 and 3
+    // prefetch their weight fragments three k-blocks ahead instead of one: -4% for that
+    // instance; the others lose or spill with the deeper ring.)
     const int blk = wave >> 2;
     const int nrows = (int)min((int64_t)BM, M - m0);
     const float *__restrict__ Pt = P + m0 * 256;
     {
         v16f acc[2][1];
         zero_acc(acc);
-        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Gf, 16, blk * 8, W2t, wave, MATRIS_D / 16, 0, lane);
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true, HEAD>(acc, Gf, 16, blk * 8, W2t, wave, MATRIS_D / 16, 0, lane);
         scale_acc<MODE>(acc, w2s);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
@@ -1066,7 +1068,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         asm volatile("" : "+s"(ldp));
         v16f a2[2][1];
         zero_acc(a2);
-        if (active) gemm_frag_packed<MODE, 2, 1, 256 / 16>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
+        if (active) gemm_frag_packed<MODE, 2, 1, 256 / 16, false, HEAD>(a2, Gf, 16, 0, W1t, col0 / 32, 256 / 16, 0, lane);
         if constexpr (MODE == 2)
             unscale_acc_rows<MODE, 1>(a2, rinv, h);  // 2^-k w1s per row
         else

@@ -464,12 +464,13 @@ __device__ __forceinline__ void gemm_frag_step(v16f (&acc)[NRT][NCT], const uint
 }
 
 // gemm_lds_packed with a pre-split A (two-plane modes): k-blocks akb0 .. akb0+KBA-1 of a
-// fragment buffer holding aKB k-blocks per row tile; same B prefetch rings.
-template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false>
+// fragment buffer holding aKB k-blocks per row tile; same B prefetch rings (RING: the ring
+// of four for one output tile as well, where the caller has the registers for it).
+template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false, bool RING = (NCT == 2)>
 __device__ __forceinline__ void gemm_frag_packed(v16f (&acc)[NRT][NCT], const uint4 *abuf, int aKB, int akb0,
                                                  const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes");
-    if constexpr (NCT == 2) {
+    if constexpr (RING) {
         static_assert(KBA % 4 == 0, "ring of four");
         Frag<MODE> b0[NCT], b1[NCT], b2[NCT], b3[NCT];
         load_bfrags<MODE, NCT>(b0, W, nt0, KBW, kb0, lane);
