@@ -95,7 +95,8 @@ def _attn_line_bytes(A, U, with_perm=True):
 
 def _gmlp_flops(M, K, tail_rows=0):
     """One fused GatedMLP forward (or backward, input gradients only):
-    [M,K]x[K,256] plus two [M,128]x[128,128]; an FFN tail adds two more [M,128]x[128,128]."""
+    [M,K]x[K,256] plus two [M,128]x[128,128]; an FFN tail (forward) or head (backward) adds two
+    more [M,128]x[128,128], the backward's pair projection one [M,256]x[256,128] (the same count)."""
     return 2.0 * M * (K * 256 + 2 * 128 * 128) + 2.0 * tail_rows * 2 * 128 * 128
 
 
@@ -105,13 +106,13 @@ def _gmlp_flops(M, K, tail_rows=0):
 # Keys: (launch name, config); a mean over that family's launches in one step where the
 # shapes differ.
 TRAFFIC_BYTES = {
-    ("gmlp_bwd", "C3"): 530.7e6,       # every launch shape, 420 launches; at M = A 989.2 MB (line attention)
-                                       # and 1520.2 MB (line refinement, with the FFN head)
-    ("gmlp_fwd", "C3"): 530.0e6,       # every launch shape, 420 launches; at M = A 1203.4 MB (line attention)
-                                       # and 1339.6 MB (line refinement, with the FFN tail)
-    ("attn_fwd_line", "C3"): 580.4e6,  # 538.0 read + 42.5 written
-    ("attn_fwd", "C2"): 4062.0e6,
-    ("attn_bwd", "C2"): 8446.4e6,
+    ("gmlp_bwd", "C3"): 617.7e6,       # every launch shape, 420 launches; at M = A 1429.5 MB (line attention,
+                                       # with the pair projection) and 1525.8 MB (line refinement, with the FFN head)
+    ("gmlp_fwd", "C3"): 541.0e6,       # every launch shape, 420 launches; at M = A 1199.8 MB (line attention)
+                                       # and 1338.2 MB (line refinement, with the FFN tail)
+    ("attn_fwd_line", "C3"): 580.4e6,  # 537.9 read + 42.5 written
+    ("attn_fwd", "C2"): 4061.9e6,
+    ("attn_bwd", "C2"): 8457.3e6,
     ("seg_sum", "C2"): 1048.1e6,
 }
 
@@ -432,13 +433,14 @@ def main():
         n_line = sum(1 for i in gm["info"] if i[0] == A)
         intensity, balance = flops / byts, mma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
         traffic = TRAFFIC_BYTES.get((name, "C3"))
-        # the line refinement's launches are the <.., true> instances (FFN head / tail); MODE 6
-        # runs the four-wave backward without a head
+        # every instance of the family: the Refinements' launches carry the FFN (forward tail /
+        # backward head), the line attention's backward the pair projection; MODE 6 runs the
+        # four-wave backward without either
         if name == "gmlp_fwd":
-            kname = f"gmlp_fwd_kernel<{mode_idx}, false> + <{mode_idx}, true>"
+            kname = f"gmlp_fwd_kernel<{mode_idx}, *>"
         else:
             kname = f"gmlp_bwd_kernel<{mode_idx}>" if mode_idx == 6 else \
-                f"gmlp_bwd8_kernel<{mode_idx}, false> + <{mode_idx}, true>"
+                f"gmlp_bwd8_kernel<{mode_idx}, *, *>"
         common = dict(kernel=kname, mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
                       flops_per_launch=round(flops), bytes_per_launch=round(byts),
                       flop_per_byte=round(intensity, 1), machine_balance_flop_per_byte=round(balance, 1),
@@ -448,7 +450,7 @@ def main():
                            f"bytes: every input table read once (gathered sources as whole tables, projected "
                            f"sources as their product tables), outputs, saved p/z and gradients written once; "
                            f"FLOPs 2*M*(256K+32768) with K the layer-1 width the kernel multiplies (+2*M*32768 "
-                           f"for the launches that carry the line refinement's FFN); MFMA peak = "
+                           f"for the launches that carry a Refinement's FFN or the line attention's pair projection); MFMA peak = "
                            f"{peak_note}")
         if intensity < balance:
             return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",

@@ -756,7 +756,7 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
                 raise ValueError("gmlp_bwd_raw: pair gradients must be contiguous [M, 128] tensors")
         nbytes += 2 * 4 * D * M
         key, blk = runs if runs is not None else (None, -1)
-        with _timed("gmlp_bwd", (M, K, nbytes)):
+        with _timed("gmlp_bwd", (M, K, nbytes, M)):  # the last field: rows of the pair projection
             _lib.check(lib.matris_gmlp_bwd_pair(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)),
                                                 _p(pack.b("w2bt", mode)), _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x),
                                                 _p(g_x0), _p(res_w), _p(res_src), _p(key), int(blk), _p(g0), _p(g1),
