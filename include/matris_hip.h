@@ -211,6 +211,35 @@ int matris_gather_mul(int64_t n_rows, const float *a, const int32_t *ia, const f
 int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const int32_t *t_ptr, const int32_t *t_perm,
                         const int32_t *s_ptr, const int32_t *s_perm, float *g_cart, void *stream);
 
+/* Edge geometry of one graph with the strain trick (row P1, matris/model/processgraph.py:
+ * 169-199: symmetric_strains, the strained positions and lattice, neighbor_pos + image @
+ * lattice, edge_vectors, edge_lengths, unit_edge_vectors), forward in one launch.  With
+ * sym = (strain + strain^T) / 2 (strain [3,3] fp32, NULL = no strain: sym = 0),
+ * x' = cart + cart sym, L' = lattice + lattice sym:
+ *   vec[e] = x'[tgt[e]] - (x'[src[e]] + image[e] L')   (cart [N,3], image [E,3] fp32;
+ *   tgt, src int32 [E] atom indices), length [E] = |vec|, unit [E,3] = vec / length,
+ *   lattice_out [3,3] = L', volume [1] = det(lattice) (unstrained, for the stress). */
+int matris_edge_geom_fwd(int64_t n_edges, const float *cart, const float *lattice, const float *strain,
+                         const float *image, const int32_t *tgt, const int32_t *src, float *length, float *unit,
+                         float *lattice_out, float *volume, void *stream);
+
+/* Blocks of the backward's per-edge pass: its partial array holds 9 * MATRIS_GEOM_PARTS
+ * floats at most. */
+#define MATRIS_GEOM_PARTS 512
+
+/* Backward of matris_edge_geom_fwd, the autograd chain of processgraph.py:169-199 for the
+ * positions and the strain: g_length [E] and g_unit [E,3] (either NULL = zero) give
+ * g_vec [E,3] (written out); g_cart [n_atoms,3] = g' + g' sym with g' the sum of g_vec
+ * over the atom's target rows minus its source rows (the CSR groupings of tgt and src,
+ * perm NULL = identity); g_strain [3,3] (NULL = not needed; needs strain) =
+ * sym-part of (cart^T g' - lattice^T sum_e image[e]^T g_vec[e]).  partial: workspace of
+ * 9 * MATRIS_GEOM_PARTS floats.  Every sum runs in a fixed order (reproducible). */
+int matris_edge_geom_bwd(int64_t n_atoms, int64_t n_edges, const float *g_length, const float *g_unit,
+                         const float *length, const float *unit, const float *cart, const float *lattice,
+                         const float *strain, const float *image, const int32_t *t_ptr, const int32_t *t_perm,
+                         const int32_t *s_ptr, const int32_t *s_perm, float *g_vec, float *partial, float *g_cart,
+                         float *g_strain, void *stream);
+
 /* ------------------------------------------------------------------------------------
  * Segment attention (rows M2 + M4 / M5): Dimwise_softmax by target and by source,
  * alpha * e' and both segment sums, fused.  Replaces interaction_block.py:113-134 with

@@ -94,6 +94,8 @@ _SIGS = {
     "matris_seg_sum_mul": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _F, _I, _P, _P]),
     "matris_gather_mul": (_I, [_I64, _P, _P, _P, _P, _I, _P, _P]),
     "matris_edge_vec_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P]),
+    "matris_edge_geom_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "matris_edge_geom_bwd": (_I, [_I64, _I64] + [_P] * 17),
     "matris_attn_fwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
                              _P]),

@@ -431,6 +431,237 @@ extern "C" int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const in
 }
 
 // ------------------------------------------------------------------------------------
+// Edge geometry of one graph with the strain trick, forward and backward in a few
+// launches instead of a chain of small tensor operations:
+//   sym = (S + S^T) / 2,  x' = x + x sym (atoms),  L' = L + L sym,
+//   vec[e] = x'[tgt[e]] - (x'[src[e]] + image[e] L'),  len = |vec|,  unit = vec / len.
+// Without a strain sym is zero and x' = x, L' = L exactly.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ void geom_sym(const float *__restrict__ S, float sym[9]) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) sym[3 * i + j] = S ? 0.5f * (S[3 * i + j] + S[3 * j + i]) : 0.f;
+}
+
+// y = x + x sym for a row vector x
+__device__ __forceinline__ void geom_strain_row(const float x[3], const float sym[9], float y[3]) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        float t = x[0] * sym[j];
+        t = fmaf(x[1], sym[3 + j], t);
+        t = fmaf(x[2], sym[6 + j], t);
+        y[j] = x[j] + t;
+    }
+}
+
+__global__ __launch_bounds__(256) void edge_geom_fwd_kernel(int64_t n, const float *__restrict__ cart,
+                                                            const float *__restrict__ lat,
+                                                            const float *__restrict__ S,
+                                                            const float *__restrict__ image,
+                                                            const int32_t *__restrict__ tgt,
+                                                            const int32_t *__restrict__ src,
+                                                            float *__restrict__ len_out,
+                                                            float *__restrict__ unit_out,
+                                                            float *__restrict__ lat_out,
+                                                            float *__restrict__ vol_out) {
+    float sym[9], Ls[9];
+    geom_sym(S, sym);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float row[3] = {lat[3 * i], lat[3 * i + 1], lat[3 * i + 2]};
+        geom_strain_row(row, sym, Ls + 3 * i);
+    }
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e == 0) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) lat_out[k] = Ls[k];
+        // det of the unstrained lattice: L0 . (L1 x L2)
+        const float c0 = lat[4] * lat[8] - lat[5] * lat[7];
+        const float c1 = lat[5] * lat[6] - lat[3] * lat[8];
+        const float c2 = lat[3] * lat[7] - lat[4] * lat[6];
+        vol_out[0] = lat[0] * c0 + lat[1] * c1 + lat[2] * c2;
+    }
+    if (e >= n) return;
+    const int64_t t = tgt[e], s = src[e];
+    const float xt[3] = {cart[3 * t], cart[3 * t + 1], cart[3 * t + 2]};
+    const float xs[3] = {cart[3 * s], cart[3 * s + 1], cart[3 * s + 2]};
+    const float im[3] = {image[3 * e], image[3 * e + 1], image[3 * e + 2]};
+    float yt[3], ys[3], v[3];
+    geom_strain_row(xt, sym, yt);
+    geom_strain_row(xs, sym, ys);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        float sh = im[0] * Ls[j];
+        sh = fmaf(im[1], Ls[3 + j], sh);
+        sh = fmaf(im[2], Ls[6 + j], sh);
+        v[j] = yt[j] - (ys[j] + sh);
+    }
+    const float l = sqrtf(fmaf(v[2], v[2], fmaf(v[1], v[1], v[0] * v[0])));
+    len_out[e] = l;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) unit_out[3 * e + j] = v[j] / l;
+}
+
+// Per edge: g_vec = g_len unit + (g_unit - (g_unit . unit) unit) / len, written out, and
+// this block's share of P = sum_e image[e]^T g_vec[e] (3 x 3), reduced in a fixed order.
+__global__ __launch_bounds__(256) void edge_geom_bwd_edge_kernel(int64_t n, const float *__restrict__ g_len,
+                                                                 const float *__restrict__ g_unit,
+                                                                 const float *__restrict__ len,
+                                                                 const float *__restrict__ unit,
+                                                                 const float *__restrict__ image,
+                                                                 float *__restrict__ g_vec,
+                                                                 float *__restrict__ partial) {
+    float P[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) P[k] = 0.f;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+        const float u[3] = {unit[3 * e], unit[3 * e + 1], unit[3 * e + 2]};
+        float gv[3] = {0.f, 0.f, 0.f};
+        if (g_len) {
+            const float gl = g_len[e];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) gv[j] = gl * u[j];
+        }
+        if (g_unit) {
+            const float gu[3] = {g_unit[3 * e], g_unit[3 * e + 1], g_unit[3 * e + 2]};
+            const float d = fmaf(gu[2], u[2], fmaf(gu[1], u[1], gu[0] * u[0]));
+            const float l = len[e];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) gv[j] += (gu[j] - d * u[j]) / l;
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) g_vec[3 * e + j] = gv[j];
+        const float im[3] = {image[3 * e], image[3 * e + 1], image[3 * e + 2]};
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) P[3 * i + j] = fmaf(im[i], gv[j], P[3 * i + j]);
+    }
+    __shared__ float part[4][9];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const float v = wave_sum(P[k]);
+        if (lane == 0) part[w][k] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 9)
+        partial[9 * blockIdx.x + threadIdx.x] =
+            ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) + part[3][threadIdx.x];
+}
+
+// One work-group: P from the partials, C = sum_a x_a^T g'_a over the atoms (g' = the
+// gradient of the strained positions, in g_cart), then
+//   g_cart = g' + g' sym^T,  g_sym = C + L^T (-P),  g_S = (g_sym + g_sym^T) / 2.
+__global__ __launch_bounds__(1024) void edge_geom_bwd_final_kernel(int64_t n_atoms, int n_part,
+                                                                   const float *__restrict__ partial,
+                                                                   const float *__restrict__ cart,
+                                                                   const float *__restrict__ lat,
+                                                                   const float *__restrict__ S,
+                                                                   float *__restrict__ g_cart,
+                                                                   float *__restrict__ g_strain) {
+    float sym[9], acc[18];
+    geom_sym(S, sym);
+#pragma unroll
+    for (int k = 0; k < 18; ++k) acc[k] = 0.f;
+    for (int b = threadIdx.x; b < n_part; b += 1024)
+#pragma unroll
+        for (int k = 0; k < 9; ++k) acc[k] += partial[9 * b + k];
+    for (int64_t a = threadIdx.x; a < n_atoms; a += 1024) {
+        const float g[3] = {g_cart[3 * a], g_cart[3 * a + 1], g_cart[3 * a + 2]};
+        const float x[3] = {cart[3 * a], cart[3 * a + 1], cart[3 * a + 2]};
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc[9 + 3 * i + j] = fmaf(x[i], g[j], acc[9 + 3 * i + j]);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {  // sym is symmetric: g sym^T = g sym
+            float t = g[0] * sym[j];
+            t = fmaf(g[1], sym[3 + j], t);
+            t = fmaf(g[2], sym[6 + j], t);
+            g_cart[3 * a + j] = g[j] + t;
+        }
+    }
+    __shared__ float part[16][18];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < 18; ++k) {
+        const float v = wave_sum(acc[k]);
+        if (lane == 0) part[w][k] = v;
+    }
+    __syncthreads();
+    __shared__ float tot[18];
+    if (threadIdx.x < 18) {
+        float s = 0.f;
+        for (int q = 0; q < 16; ++q) s += part[q][threadIdx.x];
+        tot[threadIdx.x] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && g_strain) {
+        float gs[9];
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {  // (L^T (-P))[i][j] = -sum_k L[k][i] P[k][j]
+                float t = lat[i] * tot[j];
+                t = fmaf(lat[3 + i], tot[3 + j], t);
+                t = fmaf(lat[6 + i], tot[6 + j], t);
+                gs[3 * i + j] = tot[9 + 3 * i + j] - t;
+            }
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) g_strain[3 * i + j] = 0.5f * (gs[3 * i + j] + gs[3 * j + i]);
+    }
+}
+
+static inline int geom_parts(int64_t n_edges) {
+    const int b = matris_blocks(n_edges, 256);
+    return b < MATRIS_GEOM_PARTS ? b : MATRIS_GEOM_PARTS;
+}
+
+extern "C" int matris_edge_geom_fwd(int64_t n_edges, const float *cart, const float *lattice, const float *strain,
+                                    const float *image, const int32_t *tgt, const int32_t *src, float *length,
+                                    float *unit, float *lattice_out, float *volume, void *stream) {
+    if (n_edges < 0 || !lattice || !lattice_out || !volume) return MATRIS_E_ARG;
+    if (n_edges > 0 && (!cart || !image || !tgt || !src || !length || !unit)) return MATRIS_E_ARG;
+    edge_geom_fwd_kernel<<<matris_blocks(n_edges, 256), 256, 0, (hipStream_t)stream>>>(
+        n_edges, cart, lattice, strain, image, tgt, src, length, unit, lattice_out, volume);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_edge_geom_bwd(int64_t n_atoms, int64_t n_edges, const float *g_length, const float *g_unit,
+                                    const float *length, const float *unit, const float *cart, const float *lattice,
+                                    const float *strain, const float *image, const int32_t *t_ptr,
+                                    const int32_t *t_perm, const int32_t *s_ptr, const int32_t *s_perm,
+                                    float *g_vec, float *partial, float *g_cart, float *g_strain, void *stream) {
+    if (n_atoms < 0 || n_edges < 0 || !cart || !lattice || !t_ptr || !s_ptr || !partial || !g_cart)
+        return MATRIS_E_ARG;
+    if (n_edges > 0 && (!length || !unit || !image || !g_vec)) return MATRIS_E_ARG;
+    if (g_strain && !strain) return MATRIS_E_ARG;
+    const int parts = geom_parts(n_edges);
+    hipStream_t st = (hipStream_t)stream;
+    if (n_edges > 0) {
+        edge_geom_bwd_edge_kernel<<<parts, 256, 0, st>>>(n_edges, g_length, g_unit, length, unit, image, g_vec,
+                                                         partial);
+        MATRIS_CHECK_LAUNCH();
+    }
+    if (n_atoms > 0) {
+        edge_vec_bwd_kernel<<<matris_blocks(n_atoms, WAVES_PER_BLOCK), 256, 0, st>>>(n_atoms, g_vec, t_ptr, t_perm,
+                                                                                     s_ptr, s_perm, g_cart);
+        MATRIS_CHECK_LAUNCH();
+    }
+    if (strain) {  // g' -> g_cart through the strained positions, and the strain's gradient
+        edge_geom_bwd_final_kernel<<<1, 1024, 0, st>>>(n_atoms, n_edges > 0 ? parts : 0, partial, cart, lattice,
+                                                       strain, g_cart, g_strain);
+        MATRIS_CHECK_LAUNCH();
+    }
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
 // segment attention forward: one wave per (segment, side).  Each half-wave owns every
 // other row of the segment with 16-byte lanes (4 columns) and runs an online softmax
 // taken eight of its rows at a time (sixteen rows of loads in flight per wave), then four,

@@ -54,7 +54,7 @@ def _sorted(x: torch.Tensor) -> bool:
     return x.numel() < 2 or bool((x[1:] >= x[:-1]).all().item())
 
 
-def validate_graph_indices(g) -> None:
+def validate_graph_indices(g) -> tuple:
     """Raise ValueError unless every index array of graph g is inside its range: atom_graph
     [E, 2] in [0, N), directed2undirected [E] in [0, U), undirected2directed [U] in [0, E)
     and the line graph's columns (center atom, bond, directed edge, bond, directed edge).
@@ -62,10 +62,11 @@ def validate_graph_indices(g) -> None:
     before any of them runs: one host read per graph.  The result is remembered in g.meta
     under the index tensors' identities and version counters (RadiusGraph.index_signature),
     so an index tensor edited in place or replaced after a check is checked again.  Graphs
-    built by GraphConverter are valid by construction and carry the mark already."""
+    built by GraphConverter are valid by construction and carry the mark already.
+    Returns the signature."""
     sig = g.index_signature()
     if g.meta.get("indices_checked") == sig:
-        return
+        return sig
     g.meta.pop("indices_checked", None)
     N = int(g.atomic_number.shape[0])
     E = int(g.atom_graph.shape[0])
@@ -81,6 +82,7 @@ def validate_graph_indices(g) -> None:
     if flags and bool(torch.stack(flags).any()):
         raise ValueError("graph index outside its range (atom, bond, directed-edge or angle index)")
     g.meta["indices_checked"] = sig
+    return sig
 
 
 def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
@@ -110,7 +112,13 @@ def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
     src32 = atom_graph[:, 1].contiguous()
     d2u32 = torch.cat(d2u, 0).contiguous()
     u2d32 = torch.cat(u2d, 0).contiguous()
+    if len(graphs) == 1:
+        atom_segment = torch.zeros(N, dtype=torch.long, device=device)
+    else:
+        atom_segment = torch.repeat_interleave(torch.arange(len(graphs), device=device),
+                                               torch.tensor(n_atoms, device=device), output_size=N)
     t = dict(atom_graph=atom_graph, tgt=tgt32.long(), src=src32.long(), d2u32=d2u32, u2d32=u2d32,
+             d2u64=d2u32.long(), u2d64=u2d32.long(), atom_segment=atom_segment,
              grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True),
              grp_src=Grouping.build(src32, N, deferred=True),
              grp_d2u=Grouping.build(d2u32, U, sorted_rows=False, deferred=True))
@@ -140,8 +148,7 @@ _TOPOLOGY: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 
 
 def process_graphs(graphs, compute_stress: bool = True) -> dict:
-    for g in graphs:
-        validate_graph_indices(g)
+    sigs = [validate_graph_indices(g) for g in graphs]
     device = graphs[0].lattice.device
     dtype = graphs[0].lattice.dtype
     G = len(graphs)
@@ -151,7 +158,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     n_ang = [int(g.line_graph.shape[0]) if len(g.line_graph) else 0 for g in graphs]
     N, E, U, A = sum(n_atoms), sum(n_dir), sum(n_und), sum(n_ang)
     if G == 1:
-        sig = graphs[0].index_signature()
+        sig = sigs[0]
         hit = _TOPOLOGY.get(graphs[0])
         if hit is None or hit[0] != sig:
             hit = (sig, _topology(graphs, n_atoms, n_dir, n_und, n_ang))
@@ -159,6 +166,10 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         topo = hit[1]
     else:
         topo = _topology(graphs, n_atoms, n_dir, n_und, n_ang)
+
+    if G == 1 and dtype == torch.float32 and graphs[0].atom_frac_coord.dtype == torch.float32 and \
+            graphs[0].neighbor_image.dtype == torch.float32:
+        return _one_graph(graphs[0], topo, compute_stress, n_atoms, N, E, U, A)
 
     carts, lats, imgs = [], [], []
     for g in graphs:
@@ -174,11 +185,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     lattice = torch.cat(lats, 0)  # [3G, 3]
     cart = torch.cat(carts, 0)
     image = torch.cat(imgs, 0)
-    if G == 1:
-        atom_segment = torch.zeros(N, dtype=torch.long, device=device)
-    else:
-        atoms_len = torch.tensor(n_atoms, device=device)
-        atom_segment = torch.repeat_interleave(torch.arange(G, device=device), atoms_len, output_size=N)
+    atom_segment = topo["atom_segment"]
+    atoms_len = torch.tensor(n_atoms, device=device)
     lat3 = lattice.reshape(G, 3, 3)
     volumes = torch.einsum("ni,ni->n", lat3[:, 0], torch.linalg.cross(lat3[:, 1], lat3[:, 2]))[:, None, None]
 
@@ -207,12 +215,38 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
 
     out = dict(atomic_numbers=torch.cat([g.atomic_number for g in graphs], 0), edge_lengths=length,
                unit_edge_vectors=unit, atom_segment=atom_segment, atoms_per_graph=n_atoms,
-               directed2undirected=d2u32.long(), undirected2directed=u2d32.long(), volumes=volumes,
+               directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
                n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
     out["grp_d2u"] = topo["grp_d2u"]
     out["atom_graph_dict"] = dict(
         atom_graph=atom_graph, target_index=tgt, source_index=src,
         grp_tgt=grp_tgt, grp_src=grp_src)
+    out["line_graph_dict"] = dict(topo["line_graph_dict"])
+    return out
+
+
+def _one_graph(g, topo, compute_stress, n_atoms, N, E, U, A) -> dict:
+    """process_graphs for one fp32 graph: the same fields, with the strain trick and the
+    edge geometry (processgraph.py:169-199) in one launch (ops.edge_geometry) and the
+    topology's columns used as they are (no per-call concatenations or casts).  Only the
+    position leaf (frac @ lattice, processgraph.py:87) and the zero strain are made
+    besides it, so the host issues few operations before the first layer."""
+    lat = g.lattice.detach()
+    cart = g.atom_frac_coord.detach() @ lat
+    cart.requires_grad_(True)
+    strains = None
+    if compute_stress:
+        strains = torch.zeros((1, 3, 3), dtype=torch.float32, device=lat.device, requires_grad=True)
+    grp_tgt, grp_src = topo["grp_tgt"], topo["grp_src"]
+    length, unit, lattice, volumes = ops.edge_geometry(cart, strains, lat, g.neighbor_image, grp_tgt, grp_src)
+    out = dict(atomic_numbers=g.atomic_number, edge_lengths=length, unit_edge_vectors=unit,
+               atom_segment=topo["atom_segment"], atoms_per_graph=n_atoms,
+               directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], volumes=volumes,
+               lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
+               n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
+    out["grp_d2u"] = topo["grp_d2u"]
+    out["atom_graph_dict"] = dict(atom_graph=topo["atom_graph"], target_index=topo["tgt"],
+                                  source_index=topo["src"], grp_tgt=grp_tgt, grp_src=grp_src)
     out["line_graph_dict"] = dict(topo["line_graph_dict"])
     return out

@@ -288,6 +288,68 @@ def edge_vectors(cart, shift, tgt: "Grouping", src: "Grouping"):
     return _EdgeVec.apply(cart, shift, tgt, src)
 
 
+GEOM_PARTS = 512  # MATRIS_GEOM_PARTS: blocks of matris_edge_geom_bwd's per-edge pass
+
+
+class _EdgeGeometry(torch.autograd.Function):
+    """One graph's edge geometry with the strain trick (processgraph.py:169-199) through
+    matris_edge_geom_fwd / matris_edge_geom_bwd.  Differentiable in cart and strain; the
+    strained lattice and the volume are returned as plain values."""
+
+    @staticmethod
+    def forward(ctx, cart, strain, lattice, image, tgt: "Grouping", src: "Grouping"):
+        _check_dev(cart, strain, lattice, image)
+        cart, lattice, image = _f32c(cart), _f32c(lattice), _f32c(image)
+        strain = None if strain is None else _f32c(strain)
+        if cart.dim() != 2 or cart.shape[1] != 3 or lattice.numel() != 9 or image.dim() != 2 or \
+                image.shape[1] != 3 or (strain is not None and strain.numel() != 9) or \
+                tgt.n_rows != image.shape[0] or src.n_rows != image.shape[0] or tgt.n_seg != cart.shape[0] or \
+                src.n_seg != cart.shape[0]:
+            raise ValueError("edge_geometry: expected cart [N,3], lattice [3,3], strain [1,3,3], image [E,3] and "
+                             "groupings of E rows over N atoms")
+        E, dev = image.shape[0], cart.device
+        length = _rows(E, 1, dev).view(-1)
+        unit = _rows(E, 3, dev)
+        lat_out = torch.empty(3, 3, device=dev)
+        vol = torch.empty(1, 1, 1, device=dev)
+        with _timed("edge_geom_fwd", (E,)):
+            _lib.check(_lib.load().matris_edge_geom_fwd(E, _p(cart), _p(lattice), _p(strain), _p(image), _p(tgt.key),
+                                                        _p(src.key), _p(length), _p(unit), _p(lat_out), _p(vol),
+                                                        _stream()), "matris_edge_geom_fwd")
+        ctx.save_for_backward(length, unit, cart, strain, lattice, image)
+        ctx.tgt, ctx.src = tgt, src
+        ctx.mark_non_differentiable(lat_out, vol)
+        ctx.set_materialize_grads(False)
+        return length, unit, lat_out, vol
+
+    @staticmethod
+    def backward(ctx, g_len, g_unit, _g_lat, _g_vol):
+        length, unit, cart, strain, lattice, image = ctx.saved_tensors
+        N, E, dev = cart.shape[0], image.shape[0], cart.device
+        g_len = None if g_len is None else _f32c(g_len)
+        g_unit = None if g_unit is None else _f32c(g_unit)
+        g_vec = _rows(E, 3, dev)
+        partial = torch.empty(9 * GEOM_PARTS, device=dev)
+        g_cart = torch.empty(N, 3, device=dev)
+        g_strain = torch.empty_like(strain) if (strain is not None and ctx.needs_input_grad[1]) else None
+        t, s = ctx.tgt, ctx.src
+        with _timed("edge_geom_bwd", (E,)):
+            _lib.check(_lib.load().matris_edge_geom_bwd(N, E, _p(g_len), _p(g_unit), _p(length), _p(unit), _p(cart),
+                                                        _p(lattice), _p(strain), _p(image), _p(t.rowptr),
+                                                        _p(t.perm), _p(s.rowptr), _p(s.perm), _p(g_vec),
+                                                        _p(partial), _p(g_cart), _p(g_strain), _stream()),
+                       "matris_edge_geom_bwd")
+        return g_cart, g_strain, None, None, None, None
+
+
+def edge_geometry(cart, strain, lattice, image, tgt: "Grouping", src: "Grouping"):
+    """(length [E], unit [E,3], strained lattice [3,3], volume [1,1,1]) of one graph:
+    processgraph.py:169-199 with sym = (strain + strain^T)/2 applied to the positions and
+    the lattice (strain [1,3,3] or None), vec = x'[tgt] - (x'[src] + image L').  cart [N,3],
+    lattice [3,3] and image [E,3] contiguous fp32; tgt / src the atom graph's groupings."""
+    return _EdgeGeometry.apply(cart, strain, lattice, image, tgt, src)
+
+
 class _SegSum(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, grp: Grouping, scale: float):

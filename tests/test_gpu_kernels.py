@@ -912,3 +912,63 @@ def test_edge_vectors_backward_vs_fp64(N, E):
     out.backward(gv.to("cuda"))
     assert torch.allclose(cd.grad.double().cpu(), c64.grad, atol=1e-4, rtol=1e-5)
     assert torch.equal(sd.grad.cpu(), -gv)
+
+
+@pytest.mark.parametrize("N,E,strain,use", [(864, 67396, True, "both"), (5, 7, True, "both"), (64, 900, False, "both"),
+                                            (40, 500, True, "length"), (1, 0, True, "both")])
+def test_edge_geometry_vs_fp64(N, E, strain, use):
+    """matris_edge_geom_fwd / _bwd against an fp64 autograd restatement of
+    processgraph.py:169-199 with a non-zero, non-symmetric strain: sym = (S + S^T)/2,
+    x' = x + x sym, L' = L + L sym, vec = x'[tgt] - (x'[src] + image L'), length, unit;
+    the gradients of the positions and of the strain."""
+    from matris_amd.model import ops
+    g = torch.Generator().manual_seed(N + E + int(strain))
+    tgt = torch.sort(torch.randint(0, N, (E,), generator=g))[0]
+    src = torch.randint(0, N, (E,), generator=g)
+    cart = 10 * torch.rand(N, 3, generator=g)
+    lat = 8 * torch.eye(3) + torch.randn(3, 3, generator=g)
+    img = torch.randint(-2, 3, (E, 3), generator=g).float()
+    img[(tgt == src) & (img.abs().sum(1) == 0), 0] = 1.0  # no zero-length edge
+    S = 0.01 * torch.randn(1, 3, 3, generator=g)
+    # no edge shorter than 1 Angstrom (as in a real graph): fp32 rounding of vec would dominate
+    pre = cart.double()[tgt] - (cart.double()[src] + img.double() @ lat.double())
+    keep = pre.norm(dim=1) >= 1.0
+    tgt, src, img = tgt[keep], src[keep], img[keep]
+    E = int(keep.sum())
+    gl, gu = torch.randn(E, generator=g), torch.randn(E, 3, generator=g)
+
+    x64 = cart.double().requires_grad_(True)
+    S64 = S.double().requires_grad_(True)
+    sym = 0.5 * (S64 + S64.transpose(-1, -2))[0] if strain else torch.zeros(3, 3, dtype=torch.float64)
+    xs = x64 + x64 @ sym
+    Ls = lat.double() + lat.double() @ sym
+    vec = xs[tgt] - (xs[src] + img.double() @ Ls)
+    l64 = torch.norm(vec, dim=1)
+    u64 = vec / l64[:, None]
+    loss = (l64 * gl.double()).sum() + ((u64 * gu.double()).sum() if use == "both" else 0)
+    ref_g = torch.autograd.grad(loss, [x64, S64] if strain else [x64], allow_unused=True) if E else None
+
+    gt = ops.Grouping.build(tgt.to(torch.int32).to(DEV), N, sorted_rows=True)
+    gs = ops.Grouping.build(src.to(torch.int32).to(DEV), N)
+    cd = cart.to(DEV).requires_grad_(True)
+    Sd = S.to(DEV).requires_grad_(True) if strain else None
+    length, unit, lat_out, vol = ops.edge_geometry(cd, Sd, lat.to(DEV), img.to(DEV), gt, gs)
+    assert _rel(lat_out, Ls.detach()) < 1e-6
+    assert abs(vol.item() - torch.linalg.det(lat.double()).item()) < 1e-5 * abs(torch.linalg.det(lat.double()).item())
+    if E == 0:
+        return
+    assert _rel(length, l64.detach()) < 1e-6
+    # fp32 rounding of the operands of vec (|x'| and |image L'|, tens of Angstrom) over the
+    # edge length bounds each unit vector's error
+    mag = xs.detach()[tgt].norm(dim=1) + xs.detach()[src].norm(dim=1) + (img.double() @ Ls.detach()).norm(dim=1)
+    bound = 4 * 2.0 ** -24 * mag / l64.detach() + 2.0 ** -23
+    assert ((unit.double().cpu() - u64.detach()).abs().max(dim=1).values <= bound).all()
+    loss_d = (length * gl.to(DEV)).sum() + ((unit * gu.to(DEV)).sum() if use == "both" else 0)
+    got = torch.autograd.grad(loss_d, [cd, Sd] if strain else [cd])
+    assert _rel(got[0], ref_g[0]) < 1e-5
+    if strain:
+        # the strain gradient sums over every edge and atom: bound by the sums of magnitudes
+        err = (got[1].double().cpu() - ref_g[1]).abs().max().item()
+        scale = (x64.detach().abs().T @ ref_g[0].abs()).max().item() + \
+            (lat.double().abs().T @ (img.double().abs().T @ (gl.double().abs()[:, None] + gu.double().abs()))).max().item()
+        assert err < 1e-5 * scale, (err, scale)
