@@ -435,10 +435,10 @@ def main():
         intensity, balance = flops / byts, mma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
         traffic = TRAFFIC_BYTES.get((name, "C3"))
         # every instance of the family: the Refinements' launches carry the FFN (forward tail /
-        # backward head), the line attention's backward the pair projection; MODE 6 runs the
-        # four-wave backward without either
+        # backward head), the line attention's the logit projection pair (forward tail /
+        # backward epilogue); MODE 6 runs the four-wave backward without a head or epilogue
         if name == "gmlp_fwd":
-            kname = f"gmlp_fwd_kernel<{mode_idx}, *>"
+            kname = f"gmlp_fwd_kernel<{mode_idx}, *, *>"
         else:
             kname = f"gmlp_bwd_kernel<{mode_idx}>" if mode_idx == 6 else \
                 f"gmlp_bwd8_kernel<{mode_idx}, *, *>"

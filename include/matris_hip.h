@@ -477,6 +477,20 @@ int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src_host, cons
                         const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
                         float *save_p, float *save_z, const void *ffn_w1p, const void *ffn_w2p, float *ffn_save_p,
                         const float *ffn_res, const float *ffn_res_w, float *ffn_out, int mode, void *stream);
+/* matris_gmlp_fwd_proj with the line graph attention's logit projections of the residual
+ * source's rows in the same kernel (interaction_block.py:104-112: source_weight_linear and
+ * target_weight_linear applied to the angle rows tb, which are also the edge update's
+ * residual, tb' = e + r_e tb):
+ *   pair_out0 [m,128] = res_src W[0:128]^T,  pair_out1 [m,128] = res_src W[128:256]^T
+ * with pair_wp the pack matris_pair_fwd takes (W = [W_s; W_t]).  Needs the residual
+ * (res_src, res_w, res_out).  Equal to matris_gmlp_fwd_proj followed by matris_pair_fwd on
+ * res_src. */
+int matris_gmlp_fwd_pair(int64_t m, int n_src, const float *const *src_host, const int32_t *const *src_idx_host,
+                         int n_proj, const float *const *proj_host, const int32_t *const *proj_idx_host,
+                         const int64_t *proj_ld_host, const void *w1p, const float *b1, const void *w2p,
+                         const float *b2, const float *norm_c, const float *norm_g, float eps, float *out,
+                         float *save_p, float *save_z, const float *res_src, const float *res_w, float *res_out,
+                         const void *pair_wp, float *pair_out0, float *pair_out1, int mode, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Dense layers on MFMA, 128-wide rows, no bias.

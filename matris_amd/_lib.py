@@ -110,6 +110,8 @@ _SIGS = {
                                   _P, _I, _P]),
     "matris_gmlp_fwd_ffn": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
                                  _P, _P, _P, _P, _I, _P]),
+    "matris_gmlp_fwd_pair": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,
+                                  _P, _P, _P, _P, _I, _P]),
     "matris_gmlp_bwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_bwd_runs": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _P, _P, _I, _I, _P]),
     "matris_gmlp_bwd_ffn": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _P, _P, _F, _P, _P, _P, _P,

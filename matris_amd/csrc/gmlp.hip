@@ -73,6 +73,15 @@ struct FfnTail {
     const float *res, *res_w;
 };
 
+// A projection pair on the residual source's rows (the line graph attention's logits,
+// interaction_block.py:104-112: W_s and W_t applied to the same angle rows as the edge
+// update's residual): o0 = res W[0:128]^T, o1 = res W[128:256]^T, W the pack that
+// matris_pair_fwd takes.  The residual rows are already in registers for res_out.
+struct PairOut {
+    const uint4 *W;
+    float *o0, *o1;
+};
+
 // ------------------------------------------------------------------------------------
 // forward
 // ------------------------------------------------------------------------------------
@@ -90,7 +99,7 @@ __device__ __forceinline__ void store_tile256(const float *tile, float *__restri
     }
 }
 
-template <int MODE, bool TAIL = false>
+template <int MODE, bool TAIL = false, bool PTAIL = false>
 __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, GmlpSrc src, GmlpProj proj,
                                                           const uint4 *__restrict__ W1, const float *__restrict__ b1,
                                                           const uint4 *__restrict__ W2, const float *__restrict__ b2,
@@ -101,7 +110,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                           const float *__restrict__ res_src,
                                                           const float *__restrict__ res_w,
                                                           float *__restrict__ res_out, FfnTail tail,
-                                                          unsigned *range_flag) {
+                                                          PairOut pout, unsigned *range_flag) {
     constexpr int NPL = Npl<MODE>::v;
     constexpr int CHUNK = 2 * 2 * NPL * 64;  // uint4 per LDS chunk: [rt 2][kb 2][plane][lane]
     __shared__ __align__(16) float smem[BM * LDH];
@@ -370,6 +379,35 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
         if constexpr (TAIL) {  // the out rows, the tail's GEMM operand, over this row's z (already read)
             *reinterpret_cast<float4 *>(Ts + row * LDH + c4) = o0;
             *reinterpret_cast<float4 *>(Ts + row * LDH + 64 + c4) = o1;
+        }
+        if constexpr (PTAIL) {  // the residual rows, the pair's GEMM operand, likewise
+            *reinterpret_cast<float4 *>(Ts + row * LDH + c4) = rx0[rr];
+            *reinterpret_cast<float4 *>(Ts + row * LDH + 64 + c4) = rx1[rr];
+        }
+    }
+    if constexpr (PTAIL) {
+        // o0 = res W[0:128]^T, then o1 = res W[128:256]^T: each wave one 32-column tile of
+        // the pass, through columns 128..255 of the tile (the GEMM reads columns 0..127)
+        const float ps = take_wscale<MODE>(pout.W);
+#pragma unroll 1
+        for (int half = 0; half < 2; ++half) {
+            v16f pa[2][1];
+            zero_acc(pa);
+            __syncthreads();  // residual rows complete; the previous pass's rows stored
+            amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(pa, Ts, LDH, pout.W, 4 * half + wave,
+                                                                                MATRIS_D / 16, 0, lane));
+            scale_acc<MODE>(pa, ps);
+            acc_t_to_lds<2, 1>(pa, Ts + MATRIS_D, LDH, wave * 32, lane);
+            __syncthreads();
+            float *dst = half ? pout.o1 : pout.o0;
+#pragma unroll
+            for (int it = 0; it < (BM * 32) / 256; ++it) {
+                const int q = it * 256 + tid;
+                const int row = q >> 5, cc = (q & 31) * 4;
+                if (m0 + row < M)
+                    st_nt4(dst + (m0 + row) * MATRIS_D + cc,
+                           *reinterpret_cast<const float4 *>(Ts + row * LDH + MATRIS_D + cc));
+            }
         }
     }
     if constexpr (TAIL) {
@@ -1168,7 +1206,7 @@ static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, c
                            const int64_t *proj_ld_host, const void *w1p, const float *b1, const void *w2p, const float *b2,
                            const float *norm_c, const float *norm_g, float eps, float *out, float *save_p,
                            float *save_z, const float *res_src, const float *res_w, float *res_out,
-                           const FfnTail &tail, int mode, void *stream) {
+                           const FfnTail &tail, const PairOut &pout, int mode, void *stream) {
     if (!matris_mode_ok(mode)) return MATRIS_E_ARG;
     if (m < 0 || n_src < 0 || n_src > 4 || n_proj < 0 || n_proj > 3 || n_src + n_proj < 1 ||
         (n_src && (!src_host || !w1p)) || !b1 || !w2p || !b2 || !norm_c || !norm_g || !out)
@@ -1197,27 +1235,33 @@ static int gmlp_fwd_launch(int64_t m, int n_src, const float *const *src_host, c
                      !aligned16(tail.out) || !aligned16(tail.res) || (tail.res && !tail.res_w) ||
                      !aligned16(tail.res_w) || !aligned16(tail.save_p)))
         return MATRIS_E_ARG;
+    const bool has_pair = pout.W != nullptr;
+    if (has_pair && (has_tail || !res_out || !aligned16(pout.W) || !pout.o0 || !aligned16(pout.o0) || !pout.o1 ||
+                     !aligned16(pout.o1)))
+        return MATRIS_E_ARG;
     const dim3 grid(matris_blocks(m, BM));
     hipStream_t st = (hipStream_t)stream;
     const uint4 *w1 = n_src ? (const uint4 *)w1p : nullptr, *w2 = (const uint4 *)w2p;
     unsigned *flag = nullptr;
     if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
-    if (!has_tail) {
+#define GMLP_FWD(M_, T_, P_)                                                                                       \
+    gmlp_fwd_kernel<M_, T_, P_><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,   \
+                                                      save_p, save_z, res_src, res_w, res_out, tail, pout, flag)
+    if (!has_tail && !has_pair) {
         MATRIS_MODE_DISPATCH(gmlp_fwd_kernel, grid, st, m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
-                             save_p, save_z, res_src, res_w, res_out, tail, flag);
-    } else if (mode == 0) {
-        gmlp_fwd_kernel<0, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
-                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
-    } else if (mode == 2) {
-        gmlp_fwd_kernel<2, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
-                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
-    } else if (mode == 3) {
-        gmlp_fwd_kernel<3, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
-                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
+                             save_p, save_z, res_src, res_w, res_out, tail, pout, flag);
+    } else if (has_tail) {
+        if (mode == 0) GMLP_FWD(0, true, false);
+        else if (mode == 2) GMLP_FWD(2, true, false);
+        else if (mode == 3) GMLP_FWD(3, true, false);
+        else GMLP_FWD(6, true, false);
     } else {
-        gmlp_fwd_kernel<6, true><<<grid, 256, 0, st>>>(m, n_src, s, pj, w1, b1, w2, b2, norm_c, norm_g, eps, out,
-                                                       save_p, save_z, res_src, res_w, res_out, tail, flag);
+        if (mode == 0) GMLP_FWD(0, false, true);
+        else if (mode == 2) GMLP_FWD(2, false, true);
+        else if (mode == 3) GMLP_FWD(3, false, true);
+        else GMLP_FWD(6, false, true);
     }
+#undef GMLP_FWD
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
@@ -1229,7 +1273,7 @@ extern "C" int matris_gmlp_fwd(int64_t m, int n_src, const float *const *src_hos
                                float *res_out, int mode, void *stream) {
     if (n_src < 1) return MATRIS_E_ARG;
     return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, 0, nullptr, nullptr, nullptr, w1p, b1, w2p, b2, norm_c, norm_g,
-                           eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{}, mode, stream);
+                           eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{}, PairOut{}, mode, stream);
 }
 
 extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *src_host,
@@ -1241,8 +1285,23 @@ extern "C" int matris_gmlp_fwd_proj(int64_t m, int n_src, const float *const *sr
                                     const float *res_src, const float *res_w, float *res_out, int mode,
                                     void *stream) {
     return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, n_proj, proj_host, proj_idx_host, proj_ld_host, w1p, b1, w2p,
-                           b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{}, mode,
-                           stream);
+                           b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{},
+                           PairOut{}, mode, stream);
+}
+
+extern "C" int matris_gmlp_fwd_pair(int64_t m, int n_src, const float *const *src_host,
+                                    const int32_t *const *src_idx_host, int n_proj, const float *const *proj_host,
+                                    const int32_t *const *proj_idx_host, const int64_t *proj_ld_host,
+                                    const void *w1p, const float *b1, const void *w2p, const float *b2,
+                                    const float *norm_c, const float *norm_g, float eps, float *out, float *save_p,
+                                    float *save_z, const float *res_src, const float *res_w, float *res_out,
+                                    const void *pair_wp, float *pair_out0, float *pair_out1, int mode,
+                                    void *stream) {
+    if (!pair_wp) return MATRIS_E_ARG;
+    const PairOut pout{(const uint4 *)pair_wp, pair_out0, pair_out1};
+    return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, n_proj, proj_host, proj_idx_host, proj_ld_host, w1p, b1, w2p,
+                           b2, norm_c, norm_g, eps, out, save_p, save_z, res_src, res_w, res_out, FfnTail{}, pout,
+                           mode, stream);
 }
 
 extern "C" int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src_host,
@@ -1255,8 +1314,8 @@ extern "C" int matris_gmlp_fwd_ffn(int64_t m, int n_src, const float *const *src
     if (!ffn_w1p) return MATRIS_E_ARG;
     const FfnTail tail{(const uint4 *)ffn_w1p, (const uint4 *)ffn_w2p, ffn_save_p, ffn_out, ffn_res, ffn_res_w};
     return gmlp_fwd_launch(m, n_src, src_host, src_idx_host, n_proj, proj_host, proj_idx_host, proj_ld_host, w1p, b1, w2p,
-                           b2, norm_c, norm_g, eps, out, save_p, save_z, nullptr, nullptr, nullptr, tail, mode,
-                           stream);
+                           b2, norm_c, norm_g, eps, out, save_p, save_z, nullptr, nullptr, nullptr, tail,
+                           PairOut{}, mode, stream);
 }
 
 static int gmlp_bwd_launch(int64_t m, int k, const float *g_out, const float *p, const float *z, const void *w1tp,

@@ -100,9 +100,9 @@ def _attn_fwd(layer, bond, tb, lg, mode, save: bool):
     pe = layer.edge_nonlinear_update._pack.get(layer.edge_nonlinear_update)
     pn = layer.node_nonlinear_update._pack.get(layer.node_nonlinear_update)
     pp = layer._proj.get(layer.source_weight_linear.weight, layer.target_weight_linear.weight)
-    e, p_e, z_e, tb_new = ops.gmlp_fwd_raw(pe, [tb, bond, bond], [None, tgt.key, src.key], A, mode, res=(tb, r_e),
-                                           save=save)
-    a_s, a_t = ops.pair_fwd_raw(pp, tb, mode)
+    # the logit projections W_s tb, W_t tb ride the edge update's launch, which reads tb anyway
+    e, p_e, z_e, tb_new, a_s, a_t = ops.gmlp_fwd_pair_raw(pe, [tb, bond, bond], [None, tgt.key, src.key], A, mode,
+                                                          (tb, r_e), pp, save=save)
     y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None)
     if not save:
         del a_s, a_t

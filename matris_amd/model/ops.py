@@ -703,7 +703,17 @@ def gmlp_fwd_ffn_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, ffn: "_
     return out, p, z, t_out, t_p
 
 
-def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: bool, tail):
+def gmlp_fwd_pair_raw(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, pair: "_WeightPack",
+                      save: bool = True):
+    """matris_gmlp_fwd_pair: gmlp_fwd_raw with res = (res_src, res_w) and the projection
+    pair on res_src's rows in the same launch.  Returns (out, p, z, res_out, o0, o1) with
+    (o0, o1) = pair_fwd_raw(pair, res_src)."""
+    if res is None:
+        raise ValueError("gmlp_fwd_pair_raw: the pair projects the residual source; res is required")
+    return _gmlp_fwd(pack, srcs, idxs, n_rows, mode, res, save, None, pair)
+
+
+def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: bool, tail, pair=None):
     lib = _lib.load()
     dev = srcs[0].device
     nsrc = len(srcs)
@@ -726,11 +736,17 @@ def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: boo
     if _DISCARD["on"]:  # placeholders: the kernel writes neither
         p = z = t_p = None
     t_bytes = 0 if tail is None else 4 * D * n_rows * (1 + (t_res is not None) + (t_p is not None))
+    if pair is not None:
+        rs = _f32c(rs)
+        if tuple(rs.shape) != (n_rows, D):
+            raise ValueError("gmlp_fwd_pair_raw: the residual source must be [n_rows, 128]")
+        t_out, ret_tp = _rows(n_rows, D, dev), _rows(n_rows, D, dev)
+        t_bytes = 2 * 4 * D * n_rows  # the two projections written (res_src is read for res_out already)
     if tail is not None:
         # the tail rides the gather-after-GEMM entry point (with or without projected sources)
         t_args = (_p(t_pack.b("w0", mode)), _p(t_pack.b("w1", mode)), _p(t_p), _p(t_res),
                   _p(_f32c(t_rw) if t_rw is not None else None), _p(t_out))
-    if not proj and tail is None:
+    if not proj and tail is None and pair is None:
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
         with _timed("gmlp_fwd", (n_rows, nsrc * D, _gmlp_fwd_bytes(srcs, idxs, n_rows, p is not None,
@@ -769,9 +785,16 @@ def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: boo
     ptab = [(keep[k].shape[0], keep[k].shape[1], len(b)) for k, b in enumerate(tables.values())]
     nbytes = _gmlp_fwd_bytes([srcs[j] for j in rest], [idxs[j] for j in rest], n_rows, p is not None,
                              res is not None, ptab) + t_bytes
-    # K: the layer-1 width this kernel multiplies; the last field: rows of the FFN tail
-    with _timed("gmlp_fwd", (n_rows, len(rest) * D, nbytes, n_rows if tail is not None else 0)):
-        if tail is None:
+    # K: the layer-1 width this kernel multiplies; the last field: rows of the FFN tail or the
+    # projection pair (both add 2 * 128 * 256 FLOPs per row)
+    with _timed("gmlp_fwd", (n_rows, len(rest) * D, nbytes, n_rows if (tail is not None or pair is not None) else 0)):
+        if pair is not None:
+            _lib.check(lib.matris_gmlp_fwd_pair(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr,
+                                                w1, _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
+                                                _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),
+                                                _p(res_out), _p(pair.b("cat", mode)), _p(t_out), _p(ret_tp), mode,
+                                                _stream()), "matris_gmlp_fwd_pair")
+        elif tail is None:
             _lib.check(lib.matris_gmlp_fwd_proj(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr,
                                                 w1, _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
                                                 _p(pack.ng), pack.eps, _p(out), _p(p), _p(z), _p(rs), _p(rw),

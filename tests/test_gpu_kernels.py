@@ -320,6 +320,47 @@ def test_gated_mlp_fwd_ffn_tail(M, mode, tol, gtg):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("gtg", [True, False])
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("M", [1, 64, 4097, 70001])
+def test_gated_mlp_fwd_pair_tail(M, mode, tol, gtg):
+    """matris_gmlp_fwd_pair (the line attention's [tb, bond[t], bond[s]] GatedMLP with the
+    logit projections W_s tb, W_t tb in the same launch): out, p, z and res_out
+    bit-identical to the plain forward with the residual; the projections against fp64
+    and against matris_pair_fwd on tb to the same bar; unchanged when saves are skipped
+    or discarded."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + 5)
+        mod = _ShimGated(_TorchGMLP(384)).to(DEV)
+        pack = ops.GmlpPack().get(mod)
+        mm = ops._MMA["mode"]
+        n_bond = max(1, M // 8)
+        tb, bond = torch.randn(M, 128, device=DEV), torch.randn(n_bond, 128, device=DEV)
+        idx = [None, torch.randint(0, n_bond, (M,), dtype=torch.int32, device=DEV),
+               torch.randint(0, n_bond, (M,), dtype=torch.int32, device=DEV)]
+        srcs = [tb, bond, bond]
+        ws, wt = torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11
+        pp = ops._WeightPack().get(ws, wt)
+        r = torch.rand(128, device=DEV)
+        with ops.gather_after_gemm(gtg, min_rows=1 << 12, ratio=4):
+            e0, p0, z0, tbn0 = ops.gmlp_fwd_raw(pack, srcs, idx, M, mm, res=(tb, r))
+            e, p, z, tbn, a_s, a_t = ops.gmlp_fwd_pair_raw(pack, srcs, idx, M, mm, (tb, r), pp)
+            assert torch.equal(e, e0) and torch.equal(p, p0) and torch.equal(z, z0) and torch.equal(tbn, tbn0)
+            t64 = tb.double()
+            assert _rel(a_s, t64 @ ws.double().t()) < tol and _rel(a_t, t64 @ wt.double().t()) < tol
+            s_sep, t_sep = ops.pair_fwd_raw(pp, tb, mm)
+            assert _rel(a_s, s_sep.double()) < tol and _rel(a_t, t_sep.double()) < tol
+            with ops.discard_saves():
+                _, _, _, tbn2, a_s2, a_t2 = ops.gmlp_fwd_pair_raw(pack, srcs, idx, M, mm, (tb, r), pp)
+            assert torch.equal(tbn2, tbn) and torch.equal(a_s2, a_s) and torch.equal(a_t2, a_t)
+            _, p3, z3, _, a_s3, a_t3 = ops.gmlp_fwd_pair_raw(pack, srcs, idx, M, mm, (tb, r), pp, save=False)
+            assert p3 is None and z3 is None and torch.equal(a_s3, a_s) and torch.equal(a_t3, a_t)
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
 @pytest.mark.parametrize("layout", ["atom_graph", "one_table", "big"])
 def test_gated_mlp_all_sources_projected(layout, mode, tol):
