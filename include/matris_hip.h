@@ -312,6 +312,35 @@ int matris_bessel_fwd(int64_t n, int num_radial, const float *dist, const float 
 int matris_bessel_bwd(int64_t n, int num_radial, const float *dist, const float *freq, double cutoff,
                       double envelope_exponent, const float *g_out, int accumulate, float *g_dist, void *stream);
 
+/* E2 with the edge embedding after it, one row per undirected bond (EdgeBasisEmbedding,
+ * matris/model/feature_embed.py:42-148, which evaluates both directed copies and averages
+ * them; the copies are equal, so once per bond gives the same values and gradient).
+ * Bond u, d = edge_len[u2d[u]] (edge_len [E], u2d int32 [n_bonds]):
+ *   rbf6 [n_bonds, 7] = the enveloped Bessel basis at cutoff6 (frequencies freq6),
+ *   rbf4 [n_bonds, 7] = the same at cutoff4 (freq4), both written out (they also weight
+ *     the atom- and line-graph aggregations),
+ *   e = SiLU(LayerNorm(rbf6 W1^T W2^T; ln_g, ln_b, ln_eps) Ws^T)   [n_bonds, 128]
+ * with W1 [128, 7] fp32 (edge_linear1), w2p / wsp the packs of edge_linear2 and the swish
+ * layer's linear (as matris_ffn_fwd takes them).  num_radial must be 7.  Saves h3 (the
+ * pre-activation), xhat (the normalised rows) [n_bonds, 128] and 1/sigma [n_bonds] for
+ * the backward. */
+int matris_edge_embed_fwd(int64_t n_bonds, const float *edge_len, const int32_t *u2d, const float *freq6,
+                          double cutoff6, const float *freq4, double cutoff4, int num_radial,
+                          double envelope_exponent, const float *w1, const void *w2p, const float *ln_g,
+                          const float *ln_b, double ln_eps, const void *wsp, float *e, float *rbf6, float *rbf4,
+                          float *save_h3, float *save_xhat, float *save_rstd, int mode, void *stream);
+/* Backward of matris_edge_embed_fwd in the bond lengths: from g_e [n_bonds, 128] and the
+ * other readers' g_rbf6, g_rbf4 [n_bonds, 7] (either NULL = zero), writes
+ * g_len[u2d[u]] = dL/dd of bond u (the other rows of g_len are left as they are: the
+ * caller zeroes them).  w2tp / wstp: the packs of W2^T and Ws^T (as matris_ffn_bwd takes
+ * them). */
+int matris_edge_embed_bwd(int64_t n_bonds, const float *edge_len, const int32_t *u2d, const float *freq6,
+                          double cutoff6, const float *freq4, double cutoff4, int num_radial,
+                          double envelope_exponent, const float *w1, const void *w2tp, const float *ln_g,
+                          const void *wstp, const float *g_e, const float *g_rbf6, const float *g_rbf4,
+                          const float *save_h3, const float *save_xhat, const float *save_rstd, float *g_len,
+                          int mode, void *stream);
+
 /* E3: spherical three-body basis (feature_embed.py:183-201, basis_function.py:53-77,
  * 222-338, max_n = max_l = 4): for angle row a with t = de_t[a] (the line graph's
  * target_DE_index) and s = de_s[a] (source_DE_index) into unit [E_d, 3]:

@@ -123,6 +123,10 @@ _SIGS = {
     "matris_silu_grad_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P]),
     "matris_bessel_fwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _P]),
     "matris_bessel_bwd": (_I, [_I64, _I, _P, _P, _D, _D, _P, _I, _P, _P]),
+    "matris_edge_embed_fwd": (_I, [_I64, _P, _P, _P, _D, _P, _D, _I, _D, _P, _P, _P, _P, _D, _P, _P, _P, _P, _P, _P,
+                                   _P, _I, _P]),
+    "matris_edge_embed_bwd": (_I, [_I64, _P, _P, _P, _D, _P, _D, _I, _D, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _I, _P]),
     "matris_sbf_fwd": (_I, [_I64, _P, _P, _P, _D, _P, _P]),
     "matris_sbf_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _I, _P, _P]),
     "matris_pack_b_bytes": (_SZ, [_I64, _I64, _I]),

@@ -15,6 +15,7 @@
 //       with R the spherical-Bessel root expansions of the coefficient table below and
 //       Y_l the m = 0 real spherical harmonics.
 #include "common.h"
+#include "bessel.h"
 
 // No FMA contraction in this file: products and sums round separately, as the
 // reference's elementwise torch ops do.
@@ -218,21 +219,12 @@ __global__ __launch_bounds__(256) void sbf_bwd_kernel(int64_t n_edges, const flo
 // ------------------------------------------------------------------------------------
 // E2: Bessel basis with the polynomial envelope
 // ------------------------------------------------------------------------------------
-struct BesselParams {
-    float inv_rc, norm, a, b, c, p;
-};
-
 __global__ __launch_bounds__(256) void bessel_fwd_kernel(int64_t n, int nr, const float *__restrict__ dist,
                                                          const float *__restrict__ freq, BesselParams P,
                                                          float rc, float *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float d = dist[i];
-    const float x = d / rc;
-    float sf = 0.f;
-    if (x < 1.0f) sf = 1.0f + P.a * powf(x, P.p) + P.b * powf(x, P.p + 1.0f) + P.c * powf(x, P.p + 2.0f);
-    const float dic = d * P.inv_rc;
-    for (int k = 0; k < nr; ++k) out[i * nr + k] = sf * (P.norm * sinf(freq[k] * dic) / d);
+    bessel_row(dist[i], nr, freq, P, rc, out + i * nr);
 }
 
 __global__ __launch_bounds__(256) void bessel_bwd_kernel(int64_t n, int nr, const float *__restrict__ dist,
@@ -241,35 +233,8 @@ __global__ __launch_bounds__(256) void bessel_bwd_kernel(int64_t n, int nr, cons
                                                          float *__restrict__ g_dist) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float d = dist[i];
-    const float x = d / rc;
-    float sf = 0.f, dsf = 0.f;
-    if (x < 1.0f) {
-        sf = 1.0f + P.a * powf(x, P.p) + P.b * powf(x, P.p + 1.0f) + P.c * powf(x, P.p + 2.0f);
-        dsf = (P.a * P.p * powf(x, P.p - 1.0f) + P.b * (P.p + 1.0f) * powf(x, P.p) +
-               P.c * (P.p + 2.0f) * powf(x, P.p + 1.0f)) / rc;
-    }
-    const float dic = d * P.inv_rc;
-    float acc = 0.f;
-    for (int k = 0; k < nr; ++k) {
-        const float f = freq[k];
-        const float s = sinf(f * dic), c = cosf(f * dic);
-        const float base = P.norm * s / d;
-        const float dbase = P.norm * (f * P.inv_rc * c / d - s / (d * d));
-        acc += g_out[i * nr + k] * (dsf * base + sf * dbase);
-    }
+    const float acc = bessel_row_grad(dist[i], nr, freq, P, rc, g_out + i * nr);
     g_dist[i] = accumulate ? g_dist[i] + acc : acc;
-}
-
-static BesselParams bessel_params(double cutoff, double p) {
-    BesselParams P;
-    P.inv_rc = (float)(1.0 / cutoff);
-    P.norm = (float)std::sqrt(2.0 / cutoff);
-    P.a = (float)(-(p + 1) * (p + 2) / 2);
-    P.b = (float)(p * (p + 2));
-    P.c = (float)(-p * (p + 1) / 2);
-    P.p = (float)p;
-    return P;
 }
 
 extern "C" int matris_bessel_fwd(int64_t n, int num_radial, const float *dist, const float *freq, double cutoff,

@@ -19,6 +19,7 @@
 #include <initializer_list>
 
 #include "mma.h"
+#include "bessel.h"
 
 // Copy rows [m0, m0+64) x 128 columns of a row-major [*, ld] array into LDS (zeros past M).
 __device__ __forceinline__ void stage_tile128(float *dst, const float *__restrict__ src, int64_t ld, int64_t m0,
@@ -871,6 +872,308 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
 // ------------------------------------------------------------------------------------
 // C ABI
 // ------------------------------------------------------------------------------------
+// ------------------------------------------------------------------------------------
+// Edge embedding (feature_embed.py:42-148, evaluated once per undirected bond as the
+// reference's mean of two identical directed copies is): bond u, d = len[u2d[u]],
+//   rbf6 = B_6(d), rbf4 = B_4(d)   (the enveloped Bessel bases of the two cutoffs, out)
+//   h1 = rbf6 W1^T [7 -> 128],  h2 = h1 W2^T,  y = LayerNorm(h2) (gamma, beta, eps),
+//   e = SiLU(y Ws^T)
+// The forward saves h3 = y Ws^T, xhat = (h2 - mu) / sigma and 1 / sigma per bond; the
+// backward returns the length gradient through every path (e, rbf6 and rbf4 are each
+// read by later layers), written at row u2d[u] of g_len.
+// ------------------------------------------------------------------------------------
+#define EE_NR 7  // radial functions per cutoff (num_radial)
+
+struct EdgeEmbedArgs {
+    const float *len;
+    const int32_t *u2d;
+    const float *f6, *f4;  // frequencies of the two bases [EE_NR]
+    BesselParams P6, P4;
+    float rc6, rc4;
+    const float *w1;  // [128, EE_NR] fp32 (Linear(7, 128).weight)
+    const float *ln_g, *ln_b;
+    float eps;
+};
+
+__device__ __forceinline__ float group4_sum(float v) {
+    v += dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
+    return v;
+}
+
+// W1 into LDS: W1s[j * EE_NR + k] = W1[j][k]
+__device__ __forceinline__ void ee_stage_w1(float *W1s, const float *__restrict__ w1, int tid) {
+    for (int i = tid; i < MATRIS_D * EE_NR; i += 256) W1s[i] = w1[i];
+}
+
+// A thread's 32 columns of row tid/4 in the Rows128 layout, from / to an LDS tile.
+__device__ __forceinline__ void ee_tile_get(Rows128 &x, const float *T, int tid) {
+    const int r = tid >> 2, q = tid & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float *p = T + r * LDT + 8 * (q + 4 * i);
+        x.u[i] = *reinterpret_cast<const float4 *>(p);
+        x.v[i] = *reinterpret_cast<const float4 *>(p + 4);
+    }
+}
+__device__ __forceinline__ void ee_tile_put(float *T, const Rows128 &x, int tid) {
+    const int r = tid >> 2, q = tid & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float *p = T + r * LDT + 8 * (q + 4 * i);
+        *reinterpret_cast<float4 *>(p) = x.u[i];
+        *reinterpret_cast<float4 *>(p + 4) = x.v[i];
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 3) void edge_embed_fwd_kernel(int64_t M, EdgeEmbedArgs a,
+                                                                const uint4 *__restrict__ W2,
+                                                                const uint4 *__restrict__ Ws, float *__restrict__ e,
+                                                                float *__restrict__ rbf6, float *__restrict__ rbf4,
+                                                                float *__restrict__ save_h3,
+                                                                float *__restrict__ save_xhat,
+                                                                float *__restrict__ save_rstd, unsigned *range_flag) {
+    __shared__ __align__(16) float T[BM * LDT];
+    __shared__ float R[BM][EE_NR];
+    __shared__ float W1s[MATRIS_D * EE_NR];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r = tid >> 2, q = tid & 3;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float w2s = take_wscale<MODE>(W2), wss = take_wscale<MODE>(Ws);
+    ee_stage_w1(W1s, a.w1, tid);
+    if (tid < BM) {
+        const int64_t u = m0 + tid;
+        float b6[EE_NR], b4[EE_NR];
+        if (u < M) {
+            const float d = a.len[a.u2d[u]];
+            bessel_row(d, EE_NR, a.f6, a.P6, a.rc6, b6);
+            bessel_row(d, EE_NR, a.f4, a.P4, a.rc4, b4);
+#pragma unroll
+            for (int k = 0; k < EE_NR; ++k) {
+                rbf6[u * EE_NR + k] = b6[k];
+                rbf4[u * EE_NR + k] = b4[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < EE_NR; ++k) b6[k] = 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < EE_NR; ++k) R[tid][k] = b6[k];
+    }
+    __syncthreads();
+    {  // h1 = rbf6 W1^T
+        float b[EE_NR];
+#pragma unroll
+        for (int k = 0; k < EE_NR; ++k) b[k] = R[r][k];
+        Rows128 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c0 = 8 * (q + 4 * i);
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float t = 0.f;
+#pragma unroll
+                for (int k = 0; k < EE_NR; ++k) t = fmaf(b[k], W1s[(c0 + j) * EE_NR + k], t);
+                v[j] = t;
+            }
+            h.u[i] = make_float4(v[0], v[1], v[2], v[3]);
+            h.v[i] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        ee_tile_put(T, h, tid);
+    }
+    __syncthreads();
+    v16f acc[2][1];
+    zero_acc(acc);
+    float amax = gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W2, wave, MATRIS_D / 16, 0, lane);
+    scale_acc<MODE>(acc, w2s);
+    __syncthreads();  // every wave is done reading h1
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+    __syncthreads();
+    {  // LayerNorm over the row (4 threads per row), y back to the tile
+        Rows128 x;
+        ee_tile_get(x, T, tid);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            s += (x.u[i].x + x.u[i].y + x.u[i].z + x.u[i].w) + (x.v[i].x + x.v[i].y + x.v[i].z + x.v[i].w);
+        const float mu = group4_sum(s) * (1.0f / MATRIS_D);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 du = make_float4(x.u[i].x - mu, x.u[i].y - mu, x.u[i].z - mu, x.u[i].w - mu);
+            const float4 dv = make_float4(x.v[i].x - mu, x.v[i].y - mu, x.v[i].z - mu, x.v[i].w - mu);
+            ss += (du.x * du.x + du.y * du.y + du.z * du.z + du.w * du.w) +
+                  (dv.x * dv.x + dv.y * dv.y + dv.z * dv.z + dv.w * dv.w);
+            x.u[i] = du;
+            x.v[i] = dv;
+        }
+        const float rstd = rsqrtf(group4_sum(ss) * (1.0f / MATRIS_D) + a.eps);
+        const bool in = m0 + r < M;
+        if (in && q == 0) save_rstd[m0 + r] = rstd;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c0 = 8 * (q + 4 * i);
+            const float4 xu = mul4(x.u[i], rstd), xv = mul4(x.v[i], rstd);
+            if (in) {
+                st_nt4(save_xhat + (m0 + r) * MATRIS_D + c0, xu);
+                st_nt4(save_xhat + (m0 + r) * MATRIS_D + c0 + 4, xv);
+            }
+            const float4 gu = *reinterpret_cast<const float4 *>(a.ln_g + c0);
+            const float4 gv = *reinterpret_cast<const float4 *>(a.ln_g + c0 + 4);
+            const float4 bu = *reinterpret_cast<const float4 *>(a.ln_b + c0);
+            const float4 bv = *reinterpret_cast<const float4 *>(a.ln_b + c0 + 4);
+            x.u[i] = make_float4(xu.x * gu.x + bu.x, xu.y * gu.y + bu.y, xu.z * gu.z + bu.z, xu.w * gu.w + bu.w);
+            x.v[i] = make_float4(xv.x * gv.x + bv.x, xv.y * gv.y + bv.y, xv.z * gv.z + bv.z, xv.w * gv.w + bv.w);
+        }
+        ee_tile_put(T, x, tid);  // the thread's own columns: no other thread reads them here
+    }
+    __syncthreads();
+    zero_acc(acc);
+    amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, Ws, wave, MATRIS_D / 16, 0, lane));
+    scale_acc<MODE>(acc, wss);
+    __syncthreads();  // every wave is done reading y
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < (BM * 32) / 256; ++it) {
+        const int qq = it * 256 + tid;
+        const int rr = qq >> 5, c4 = (qq & 31) * 4;
+        if (m0 + rr < M) {
+            const float4 v = *reinterpret_cast<const float4 *>(T + rr * LDT + c4);
+            st_nt4(save_h3 + (m0 + rr) * MATRIS_D + c4, v);
+            *reinterpret_cast<float4 *>(e + (m0 + rr) * MATRIS_D + c4) =
+                make_float4(silu_f(v.x), silu_f(v.y), silu_f(v.z), silu_f(v.w));
+        }
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
+// One backward GEMM of the edge embedding: acc = rows W (W the pack of a transposed
+// weight), the rows scaled per row in MODE 2 (rinv receives 2^-k), staged pre-split in
+// the two-plane modes.  Leaves the result unscaled in the tile T (fp32, [64, 128]).
+template <int MODE>
+__device__ __forceinline__ float ee_bwd_gemm(float *T, float *rinv, const Rows128 &x, const uint4 *__restrict__ W,
+                                             int tid, int wave, int lane, float amax) {
+    constexpr bool PS = Npl<MODE>::v == 2;
+    uint4 *Tf = reinterpret_cast<uint4 *>(T);
+    const float ws = take_wscale<MODE>(W);
+    const float sr = tile_row_scale<MODE>(MODE == 2 ? rows128_absmax(x) : 0.f, rinv, tid);
+    v16f acc[2][1];
+    zero_acc(acc);
+    if constexpr (PS) {
+        amax = stage_rows128<MODE>(Tf, x, tid, amax, sr);
+        __syncthreads();
+        gemm_frag_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, Tf, MATRIS_D / 16, 0, W, wave, MATRIS_D / 16, 0, lane);
+    } else {
+        ee_tile_put(T, x, tid);
+        __syncthreads();
+        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(acc, T, LDT, W, wave, MATRIS_D / 16, 0,
+                                                                            lane));
+    }
+    scale_acc<MODE>(acc, ws);
+    unscale_rows_t<MODE, 1>(acc, rinv, lane & 31);
+    __syncthreads();  // every wave is done reading the operand (and rinv)
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+    __syncthreads();
+    return amax;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 3) void edge_embed_bwd_kernel(int64_t M, EdgeEmbedArgs a,
+                                                                const uint4 *__restrict__ Wst,
+                                                                const uint4 *__restrict__ W2t,
+                                                                const float *__restrict__ g_e,
+                                                                const float *__restrict__ g_rbf6,
+                                                                const float *__restrict__ g_rbf4,
+                                                                const float *__restrict__ save_h3,
+                                                                const float *__restrict__ save_xhat,
+                                                                const float *__restrict__ save_rstd,
+                                                                float *__restrict__ g_len, unsigned *range_flag) {
+    __shared__ __align__(16) float T[BM * LDT];
+    __shared__ float rinv[BM];
+    __shared__ float W1s[MATRIS_D * EE_NR];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r = tid >> 2, q = tid & 3;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const bool in = m0 + r < M;
+    ee_stage_w1(W1s, a.w1, tid);
+    // g_h3 = g_e * SiLU'(h3)
+    Rows128 g, h;
+    load_rows128(g, g_e, m0, M, tid);
+    load_rows128(h, save_h3, m0, M, tid);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        g.u[i] = make_float4(g.u[i].x * dsilu_f(h.u[i].x), g.u[i].y * dsilu_f(h.u[i].y), g.u[i].z * dsilu_f(h.u[i].z),
+                             g.u[i].w * dsilu_f(h.u[i].w));
+        g.v[i] = make_float4(g.v[i].x * dsilu_f(h.v[i].x), g.v[i].y * dsilu_f(h.v[i].y), g.v[i].z * dsilu_f(h.v[i].z),
+                             g.v[i].w * dsilu_f(h.v[i].w));
+    }
+    load_rows128(h, save_xhat, m0, M, tid);  // xhat, for the LayerNorm backward
+    const float rstd = in ? save_rstd[m0 + r] : 0.f;
+    float amax = ee_bwd_gemm<MODE>(T, rinv, g, Wst, tid, wave, lane, 0.f);  // g_y = g_h3 Ws
+    {  // LayerNorm backward: g_xhat = g_y gamma, g_h2 = rstd (g_xhat - mean(g_xhat) - xhat mean(g_xhat xhat))
+        ee_tile_get(g, T, tid);
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c0 = 8 * (q + 4 * i);
+            const float4 gu = *reinterpret_cast<const float4 *>(a.ln_g + c0);
+            const float4 gv = *reinterpret_cast<const float4 *>(a.ln_g + c0 + 4);
+            g.u[i] = make_float4(g.u[i].x * gu.x, g.u[i].y * gu.y, g.u[i].z * gu.z, g.u[i].w * gu.w);
+            g.v[i] = make_float4(g.v[i].x * gv.x, g.v[i].y * gv.y, g.v[i].z * gv.z, g.v[i].w * gv.w);
+            s1 += (g.u[i].x + g.u[i].y + g.u[i].z + g.u[i].w) + (g.v[i].x + g.v[i].y + g.v[i].z + g.v[i].w);
+            s2 += (g.u[i].x * h.u[i].x + g.u[i].y * h.u[i].y + g.u[i].z * h.u[i].z + g.u[i].w * h.u[i].w) +
+                  (g.v[i].x * h.v[i].x + g.v[i].y * h.v[i].y + g.v[i].z * h.v[i].z + g.v[i].w * h.v[i].w);
+        }
+        const float m1 = group4_sum(s1) * (1.0f / MATRIS_D), m2 = group4_sum(s2) * (1.0f / MATRIS_D);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g.u[i] = make_float4(rstd * (g.u[i].x - m1 - h.u[i].x * m2), rstd * (g.u[i].y - m1 - h.u[i].y * m2),
+                                 rstd * (g.u[i].z - m1 - h.u[i].z * m2), rstd * (g.u[i].w - m1 - h.u[i].w * m2));
+            g.v[i] = make_float4(rstd * (g.v[i].x - m1 - h.v[i].x * m2), rstd * (g.v[i].y - m1 - h.v[i].y * m2),
+                                 rstd * (g.v[i].z - m1 - h.v[i].z * m2), rstd * (g.v[i].w - m1 - h.v[i].w * m2));
+        }
+        __syncthreads();  // every thread has read g_y from the tile the next operand overwrites
+    }
+    amax = ee_bwd_gemm<MODE>(T, rinv, g, W2t, tid, wave, lane, amax);  // g_h1 = g_h2 W2
+    // g_rbf6 = g_h1 W1 (+ its other readers' gradient); the length through both bases
+    float p[EE_NR];
+#pragma unroll
+    for (int k = 0; k < EE_NR; ++k) p[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c0 = 8 * (q + 4 * i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float gv = T[r * LDT + c0 + j];
+#pragma unroll
+            for (int k = 0; k < EE_NR; ++k) p[k] = fmaf(gv, W1s[(c0 + j) * EE_NR + k], p[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < EE_NR; ++k) p[k] = group4_sum(p[k]);
+    if (in && q == 0) {
+        const int64_t u = m0 + r;
+        const int64_t ei = a.u2d[u];
+        const float d = a.len[ei];
+        if (g_rbf6) {
+#pragma unroll
+            for (int k = 0; k < EE_NR; ++k) p[k] += g_rbf6[u * EE_NR + k];
+        }
+        float gd = bessel_row_grad(d, EE_NR, a.f6, a.P6, a.rc6, p);
+        if (g_rbf4) {
+            float g4[EE_NR];
+#pragma unroll
+            for (int k = 0; k < EE_NR; ++k) g4[k] = g_rbf4[u * EE_NR + k];
+            gd += bessel_row_grad(d, EE_NR, a.f4, a.P4, a.rc4, g4);
+        }
+        g_len[ei] = gd;
+    }
+    report_range<MODE>(amax, range_flag);
+}
+
 #define MLP_DISPATCH(KERNEL, ...)                                                         \
     do {                                                                                  \
         unsigned *flag_ = nullptr;                                                        \
@@ -1067,6 +1370,58 @@ extern "C" int matris_tb_embed_bwd(int64_t m, const float *basis, const float *g
         tb_embed_bwd_kernel<2><<<grid, 512, 0, st>>>(m, basis, g_tb, wa, ws, wst, g_basis, flag);
     else
         tb_embed_bwd_kernel<3><<<grid, 512, 0, st>>>(m, basis, g_tb, wa, ws, wst, g_basis, flag);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+static bool edge_embed_args(EdgeEmbedArgs &a, int64_t n_bonds, const float *edge_len, const int32_t *u2d,
+                            const float *freq6, double cutoff6, const float *freq4, double cutoff4, int num_radial,
+                            double envelope_exponent, const float *w1, const float *ln_g, const float *ln_b,
+                            double ln_eps) {
+    if (n_bonds < 0 || num_radial != EE_NR || !(cutoff6 > 0) || !(cutoff4 > 0) || !(envelope_exponent > 0) ||
+        !edge_len || !u2d || !freq6 || !freq4 || !w1 || !ln_g || ((uintptr_t)ln_g & 15) ||
+        (ln_b && ((uintptr_t)ln_b & 15)))
+        return false;
+    a = EdgeEmbedArgs{edge_len, u2d, freq6, freq4, bessel_params(cutoff6, envelope_exponent),
+                      bessel_params(cutoff4, envelope_exponent), (float)cutoff6, (float)cutoff4, w1, ln_g, ln_b,
+                      (float)ln_eps};
+    return true;
+}
+
+extern "C" int matris_edge_embed_fwd(int64_t n_bonds, const float *edge_len, const int32_t *u2d, const float *freq6,
+                                     double cutoff6, const float *freq4, double cutoff4, int num_radial,
+                                     double envelope_exponent, const float *w1, const void *w2p, const float *ln_g,
+                                     const float *ln_b, double ln_eps, const void *wsp, float *e, float *rbf6,
+                                     float *rbf4, float *save_h3, float *save_xhat, float *save_rstd, int mode,
+                                     void *stream) {
+    EdgeEmbedArgs a;
+    if (!edge_embed_args(a, n_bonds, edge_len, u2d, freq6, cutoff6, freq4, cutoff4, num_radial, envelope_exponent,
+                         w1, ln_g, ln_b, ln_eps) ||
+        !ln_b || !mlp_args_ok(mode, {w2p, wsp, e, save_h3, save_xhat}) || !rbf6 || !rbf4 || !save_rstd)
+        return MATRIS_E_ARG;
+    const int64_t m = n_bonds;
+    if (m == 0) return 0;
+    MLP_DISPATCH(edge_embed_fwd_kernel, m, a, (const uint4 *)w2p, (const uint4 *)wsp, e, rbf6, rbf4, save_h3, save_xhat,
+                 save_rstd);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_edge_embed_bwd(int64_t n_bonds, const float *edge_len, const int32_t *u2d, const float *freq6,
+                                     double cutoff6, const float *freq4, double cutoff4, int num_radial,
+                                     double envelope_exponent, const float *w1, const void *w2tp, const float *ln_g,
+                                     const void *wstp, const float *g_e, const float *g_rbf6, const float *g_rbf4,
+                                     const float *save_h3, const float *save_xhat, const float *save_rstd,
+                                     float *g_len, int mode, void *stream) {
+    EdgeEmbedArgs a;
+    if (!edge_embed_args(a, n_bonds, edge_len, u2d, freq6, cutoff6, freq4, cutoff4, num_radial, envelope_exponent,
+                         w1, ln_g, nullptr, 0.0) ||
+        !mlp_args_ok(mode, {w2tp, wstp, g_e, save_h3, save_xhat}) || !save_rstd || !g_len)
+        return MATRIS_E_ARG;
+    const int64_t m = n_bonds;
+    if (m == 0) return 0;
+    MLP_DISPATCH(edge_embed_bwd_kernel, m, a, (const uint4 *)wstp, (const uint4 *)w2tp, g_e, g_rbf6, g_rbf4, save_h3,
+                 save_xhat, save_rstd, g_len);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

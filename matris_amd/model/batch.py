@@ -215,7 +215,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
 
     out = dict(atomic_numbers=torch.cat([g.atomic_number for g in graphs], 0), edge_lengths=length,
                unit_edge_vectors=unit, atom_segment=atom_segment, atoms_per_graph=n_atoms,
-               directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], volumes=volumes,
+               directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], u2d32=topo["u2d32"],
+               volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
                n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
     out["grp_d2u"] = topo["grp_d2u"]
@@ -242,7 +243,8 @@ def _one_graph(g, topo, compute_stress, n_atoms, N, E, U, A) -> dict:
     length, unit, lattice, volumes = ops.edge_geometry(cart, strains, lat, g.neighbor_image, grp_tgt, grp_src)
     out = dict(atomic_numbers=g.atomic_number, edge_lengths=length, unit_edge_vectors=unit,
                atom_segment=topo["atom_segment"], atoms_per_graph=n_atoms,
-               directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], volumes=volumes,
+               directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], u2d32=topo["u2d32"],
+               volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
                n_atoms=N, n_directed=E, n_undirected=U, n_angles=A)
     out["grp_d2u"] = topo["grp_d2u"]

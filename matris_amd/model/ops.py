@@ -1114,6 +1114,65 @@ def bessel(dist, freq, cutoff: float, envelope_exponent: float):
     return _Bessel.apply(dist, freq, float(cutoff), float(envelope_exponent))
 
 
+class _EdgeEmbed(torch.autograd.Function):
+    """matris_edge_embed_fwd / _bwd: EdgeBasisEmbedding (feature_embed.py:42-148) per bond,
+    differentiable in the edge lengths only (the efsm path takes no weight gradients)."""
+
+    @staticmethod
+    def forward(ctx, length, u2d32, mod):
+        _check_dev(length, u2d32)
+        length = _f32c(length)
+        lib = _lib.load()
+        mode = _MMA["mode"]
+        b6, b4 = mod.pairwise_rbf_expansion, mod.threebody_rbf_expansion
+        f6, f4 = _f32c(b6.frequencies.detach()), _f32c(b4.frequencies.detach())
+        w1 = _f32c(mod.edge_linear1.weight.detach())
+        ln = mod.edge_init_norm
+        lg, lb = _f32c(ln.weight.detach()), _f32c(ln.bias.detach())
+        pack = mod._pack.get(mod.edge_linear2.weight, mod.swish_layer.linear.weight)
+        U, nr, dev = u2d32.shape[0], f6.shape[0], length.device
+        e, h3, xhat = _rows(U, D, dev), _rows(U, D, dev), _rows(U, D, dev)
+        rbf6, rbf4 = torch.empty(U, nr, device=dev), torch.empty(U, nr, device=dev)
+        rstd = torch.empty(U, device=dev)
+        args = (U, _p(length), _p(u2d32), _p(f6), float(b6.envelope_func.cutoff), _p(f4),
+                float(b4.envelope_func.cutoff), nr, float(b6.envelope_func.p), _p(w1))
+        with _timed("edge_embed_fwd", (U,)):
+            _lib.check(lib.matris_edge_embed_fwd(*args, _p(pack.b("w0", mode)), _p(lg), _p(lb), float(ln.eps),
+                                                 _p(pack.b("w1", mode)), _p(e), _p(rbf6), _p(rbf4), _p(h3), _p(xhat),
+                                                 _p(rstd), mode, _stream()), "matris_edge_embed_fwd")
+        ctx.save_for_backward(length, u2d32, f6, f4, w1, lg, h3, xhat, rstd)
+        ctx.mod, ctx.mode, ctx.pack = mod, mode, pack
+        ctx.set_materialize_grads(False)
+        return e, rbf6, rbf4
+
+    @staticmethod
+    def backward(ctx, g_e, g6, g4):
+        length, u2d32, f6, f4, w1, lg, h3, xhat, rstd = ctx.saved_tensors
+        mod, mode, pack = ctx.mod, ctx.mode, ctx.pack
+        U, dev = u2d32.shape[0], length.device
+        g_len = torch.zeros_like(length)
+        g_e = _zeros_if_none(g_e, h3)
+        b6, b4 = mod.pairwise_rbf_expansion, mod.threebody_rbf_expansion
+        with _timed("edge_embed_bwd", (U,)):
+            _lib.check(_lib.load().matris_edge_embed_bwd(
+                U, _p(length), _p(u2d32), _p(f6), float(b6.envelope_func.cutoff), _p(f4),
+                float(b4.envelope_func.cutoff), f6.shape[0], float(b6.envelope_func.p), _p(w1),
+                _p(pack.b("wt0", mode)), _p(lg), _p(pack.b("wt1", mode)), _p(g_e),
+                _p(None if g6 is None else _f32c(g6)), _p(None if g4 is None else _f32c(g4)), _p(h3), _p(xhat),
+                _p(rstd), _p(g_len), mode, _stream()), "matris_edge_embed_bwd")
+        return g_len, None, None
+
+
+def _zeros_if_none(g, like):
+    return torch.zeros_like(like) if g is None else _f32c(g)
+
+
+def edge_embed(length, u2d32, mod):
+    """(e [U,128], rbf6 [U,7], rbf4 [U,7]) of EdgeBasisEmbedding `mod` for the bonds whose
+    first directed edge is u2d32 (int32 [U]), from the directed edges' lengths [E]."""
+    return _EdgeEmbed.apply(length, u2d32, mod)
+
+
 class _SBF(torch.autograd.Function):
     @staticmethod
     def forward(ctx, unit, grp_t: Grouping, grp_s: Grouping, cutoff: float):

@@ -1013,3 +1013,72 @@ def test_edge_geometry_vs_fp64(N, E, strain, use):
         scale = (x64.detach().abs().T @ ref_g[0].abs()).max().item() + \
             (lat.double().abs().T @ (img.double().abs().T @ (gl.double().abs()[:, None] + gu.double().abs()))).max().item()
         assert err < 1e-5 * scale, (err, scale)
+
+
+def _edge_basis64(d, mod):
+    """fp64 enveloped Bessel bases of both cutoffs (basis_function.py:8-50, 116-186)."""
+    def basis(b):
+        rc, p = b.envelope_func.cutoff, b.envelope_func.p
+        a_, b_, c_ = -(p + 1) * (p + 2) / 2, p * (p + 2), -p * (p + 1) / 2
+        x = d / rc
+        env = torch.where(x < 1, 1 + a_ * x ** p + b_ * x ** (p + 1) + c_ * x ** (p + 2), torch.zeros_like(x))
+        f = b.frequencies.detach().double().cpu()
+        return env[:, None] * ((2 / rc) ** 0.5 * torch.sin(f[None, :] * d[:, None] / rc) / d[:, None])
+    return basis(mod.pairwise_rbf_expansion), basis(mod.threebody_rbf_expansion)
+
+
+def _edge_mlp64(r6, mod):
+    """fp64 rest of EdgeBasisEmbedding (feature_embed.py:42-148) on the radial basis r6:
+    two bias-free linears, LayerNorm, the swish layer."""
+    w = lambda lin: lin.weight.detach().double().cpu()
+    ln = mod.edge_init_norm
+    h2 = r6 @ w(mod.edge_linear1).t() @ w(mod.edge_linear2).t()
+    y = F.layer_norm(h2, (128,), ln.weight.detach().double().cpu(), ln.bias.detach().double().cpu(), ln.eps)
+    return F.silu(y @ w(mod.swish_layer.linear).t())
+
+
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-5), ("bf16x6", 1e-5), ("f16x3", 1e-5), ("bf16x3", 1e-4)])
+@pytest.mark.parametrize("U", [1, 64, 65, 5000])
+def test_edge_embedding_vs_fp64(U, mode, tol):
+    """matris_edge_embed_fwd / _bwd (EdgeBasisEmbedding once per bond) against an fp64
+    restatement: both bases (also bitwise against matris_bessel_fwd, the reference's fp32
+    evaluation), e from the kernel's own fp32 basis (the basis's fp32 rounding, ~1e-6
+    absolute, is amplified by the LayerNorm's 1/sigma like any fp32 evaluation's), and the
+    edge-length gradient through e and both bases (fp64 derivatives of the bases), written
+    at the bonds' first directed edges only."""
+    from matris_amd.model.model import EdgeBasisEmbedding
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(U + 11)
+        mod = EdgeBasisEmbedding(6, 4, 7, 128, 8, "Bessel", learnable=True).to(DEV)
+        with torch.no_grad():  # trained-looking parameters: off the initial values
+            for prm in (mod.pairwise_rbf_expansion.frequencies, mod.threebody_rbf_expansion.frequencies):
+                prm.mul_(1 + 0.05 * torch.randn_like(prm))
+            mod.edge_init_norm.weight.copy_(1 + 0.1 * torch.randn(128))
+            mod.edge_init_norm.bias.copy_(0.1 * torch.randn(128))
+        assert mod._fusable()
+        E = 2 * U
+        length = 0.8 + 5.6 * torch.rand(E, device=DEV)  # across both cutoffs
+        u2d = torch.randperm(E, device=DEV)[:U].to(torch.int32)
+        ld = length.clone().requires_grad_(True)
+        e, r6, r4 = ops.edge_embed(ld, u2d, mod)
+        d64 = length.double().cpu()[u2d.long().cpu()].requires_grad_(True)
+        r664, r464 = _edge_basis64(d64, mod)
+        assert _rel(r6, r664.detach()) < 1e-5 and _rel(r4, r464.detach()) < 1e-5
+        r6_own = r6.detach().double().cpu().requires_grad_(True)
+        e64 = _edge_mlp64(r6_own, mod)
+        assert _rel(e, e64.detach()) < tol
+        b = mod.pairwise_rbf_expansion
+        assert torch.equal(r6, ops.bessel(length[u2d.long()], b.frequencies, b.envelope_func.cutoff, b.envelope_func.p))
+        ge, g6, g4 = torch.randn(U, 128, device=DEV), torch.randn(U, 7, device=DEV), torch.randn(U, 7, device=DEV)
+        (g_len,) = torch.autograd.grad((e * ge).sum() + (r6 * g6).sum() + (r4 * g4).sum(), [ld])
+        (g_r6,) = torch.autograd.grad((e64 * ge.double().cpu()).sum(), [r6_own])
+        (g64,) = torch.autograd.grad((r664 * (g_r6 + g6.double().cpu())).sum() + (r464 * g4.double().cpu()).sum(),
+                                     [d64])
+        mask = torch.zeros(E, dtype=torch.bool)
+        mask[u2d.long().cpu()] = True
+        assert torch.all(g_len.cpu()[~mask] == 0)
+        assert _rel(g_len[u2d.long()], g64) < 10 * tol
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
