@@ -32,6 +32,19 @@ SAVED_BYTES_PER_ANGLE_BLOCK = 4 * (2 * 256 + 3 * 128 + 2 * 256 + 2 * 128 + 128)
 SAVED_BYTES_PER_EDGE_BLOCK = 4 * 16 * 128
 
 
+_DEVICE_BYTES: dict = {}
+
+
+def _device_bytes(device) -> int:
+    """The device's memory capacity (queried once per device)."""
+    idx = torch.device(device).index if device is not None else None
+    if idx is None:
+        idx = torch.cuda.current_device()
+    if idx not in _DEVICE_BYTES:
+        _DEVICE_BYTES[idx] = torch.cuda.get_device_properties(idx).total_memory
+    return _DEVICE_BYTES[idx]
+
+
 def blocks_to_checkpoint(n_angles: int, n_edges: int, n_blocks: int, device=None,
                          total_bytes: int | None = None) -> int:
     """How many leading interaction blocks to checkpoint (keep their inputs, rerun their
@@ -42,7 +55,7 @@ def blocks_to_checkpoint(n_angles: int, n_edges: int, n_blocks: int, device=None
     them raises the peak over full checkpointing only when k exceeds one.  The reference
     checkpoints its two line-graph layers above 60,000 angles regardless of memory
     (interaction_block.py:15, :400-413)."""
-    total = total_bytes if total_bytes is not None else torch.cuda.get_device_properties(device).total_memory
+    total = total_bytes if total_bytes is not None else _device_bytes(device)
     per_block = n_angles * SAVED_BYTES_PER_ANGLE_BLOCK + n_edges * SAVED_BYTES_PER_EDGE_BLOCK
     budget = 0.55 * total
     if n_blocks * per_block <= budget:

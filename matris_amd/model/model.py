@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import contextlib
 import math
+import weakref
 from collections.abc import Sequence
 
 import torch
@@ -241,9 +242,27 @@ class AtomTypeEmbedding(nn.Module):
         super().__init__()
         self.embedding = nn.Embedding(max_num_elements, atom_feat_dim)
         self.atom_swish_layer = SwishLayer(atom_feat_dim, atom_feat_dim, bias=False)
+        self._memo = None  # (weakref to the atomic numbers, key, features)
 
     def forward(self, atom_type):
         return self.atom_swish_layer(self.embedding(atom_type))
+
+    def embed(self, atomic_numbers: Tensor) -> Tensor:
+        """forward(atomic_numbers - 1) without a gradient (the efsm path differentiates in
+        positions and strain only), remembered while the same atomic-number tensor (held
+        by a weak reference, so a freed tensor never matches) and the weights keep their
+        storage and version counters: repeated evaluations of one structure (MD,
+        relaxation) issue no operations for it."""
+        prm = [p for p in self.parameters()]
+        key = (atomic_numbers.data_ptr(), atomic_numbers._version, tuple(atomic_numbers.shape),
+               tuple((p.data_ptr(), p._version) for p in prm))
+        m = self._memo
+        if m is not None and m[0]() is atomic_numbers and m[1] == key:
+            return m[2]
+        with torch.no_grad():
+            out = self.forward(atomic_numbers.long() - 1)
+        self._memo = (weakref.ref(atomic_numbers), key, out)
+        return out
 
 
 class EdgeBasisEmbedding(nn.Module):
@@ -614,7 +633,7 @@ class MatRIS(nn.Module):
             n_ckpt = n_blocks if self.block_checkpoint else 0
         else:
             n_ckpt = max(0, min(int(self.block_checkpoint), n_blocks))
-        node = self.atom_embedding(bg["atomic_numbers"].long() - 1)
+        node = self.atom_embedding.embed(bg["atomic_numbers"])
         edge, smooth = self.edge_embedding(graphs=bg)
         tb = None
         if bg["n_angles"] != 0:
