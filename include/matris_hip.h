@@ -346,14 +346,16 @@ int matris_edge_embed_bwd(int64_t n_bonds, const float *edge_len, const int32_t 
  * target_DE_index) and s = de_s[a] (source_DE_index) into unit [E_d, 3]:
  *   c = (unit[t] . unit[s]) (1 - 1e-6), x = |unit[s]| / cutoff,
  *   out[a, 4n+j] = sqrt(2/cutoff^3) R_{n,j}(x) Y_n(cos(acos c)),  out [A, 16].
- * bwd: thread per directed edge d: g_unit[d] (+)= the gradient of every row that reads
- * unit[d] as t (CSR t_ptr/t_perm of de_t over E_d) or as s (CSR s_ptr/s_perm of de_s),
- * summed in CSR order (deterministic). */
+ * bwd: g_unit[d] (+)= the gradient of every row that reads unit[d] as t (CSR t_ptr/t_perm
+ * of de_t over E_d) or as s (CSR s_ptr/s_perm of de_s), summed in CSR order
+ * (deterministic): each row's two contributions are computed once into work
+ * [n_angles, 6] (thread per row), then summed per directed edge (thread per edge). */
 int matris_sbf_fwd(int64_t n_angles, const float *unit, const int32_t *de_t, const int32_t *de_s, double cutoff,
                    float *out, void *stream);
-int matris_sbf_bwd(int64_t n_edges, const float *unit, const int32_t *de_t, const int32_t *de_s,
+int matris_sbf_bwd(int64_t n_edges, int64_t n_angles, const float *unit, const int32_t *de_t, const int32_t *de_s,
                    const float *g_basis, const int32_t *t_ptr, const int32_t *t_perm, const int32_t *s_ptr,
-                   const int32_t *s_perm, double cutoff, int accumulate, float *g_unit, void *stream);
+                   const int32_t *s_perm, double cutoff, int accumulate, float *work, float *g_unit,
+                   void *stream);
 
 /* ------------------------------------------------------------------------------------
  * MFMA arithmetic and packed weights (shared by the gated MLP, FFN and projection pair).

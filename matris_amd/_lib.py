@@ -128,7 +128,7 @@ _SIGS = {
     "matris_edge_embed_bwd": (_I, [_I64, _P, _P, _P, _D, _P, _D, _I, _D, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _I, _P]),
     "matris_sbf_fwd": (_I, [_I64, _P, _P, _P, _D, _P, _P]),
-    "matris_sbf_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _I, _P, _P]),
+    "matris_sbf_bwd": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _I, _P, _P, _P]),
     "matris_pack_b_bytes": (_SZ, [_I64, _I64, _I]),
     "matris_pack_b": (_I, [_I64, _I64, _P, _I, _P, _P]),
     "matris_status_take": (_I, [_P, _P]),

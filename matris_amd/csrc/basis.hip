@@ -166,44 +166,55 @@ __device__ __forceinline__ void sbf_row_grad(const SbfGeom &g, const float *__re
 
 // Thread per directed edge d: the gradient of its unit vector collects every angle row
 // that reads it as u_t (target CSR) or as u_s (source CSR), in CSR order.
-__global__ __launch_bounds__(256) void sbf_bwd_kernel(int64_t n_edges, const float *__restrict__ unit,
-                                                      const int32_t *__restrict__ de_t,
-                                                      const int32_t *__restrict__ de_s,
-                                                      const float *__restrict__ g_basis, const int32_t *__restrict__ t_ptr,
-                                                      const int32_t *__restrict__ t_perm,
-                                                      const int32_t *__restrict__ s_ptr,
-                                                      const int32_t *__restrict__ s_perm, float rc, float factor,
-                                                      int accumulate, float *__restrict__ g_unit) {
+// Backward, first pass: thread per angle row, the row's gradient into unit[t] and into
+// unit[s] (work [n, 6]); every row's geometry and derivatives are evaluated once.
+__global__ __launch_bounds__(256) void sbf_bwd_row_kernel(int64_t n, const float *__restrict__ unit,
+                                                          const int32_t *__restrict__ de_t,
+                                                          const int32_t *__restrict__ de_s,
+                                                          const float *__restrict__ g_basis, float rc, float factor,
+                                                          float *__restrict__ work) {
+    const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    const float *ut = unit + 3 * (int64_t)de_t[a], *us = unit + 3 * (int64_t)de_s[a];
+    const SbfGeom g = sbf_geom(ut, us, rc);
+    float gb[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gb[k] = g_basis[16 * a + k] * factor;
+    float g_c, g_x;
+    sbf_row_grad(g, gb, g_c, g_x);
+    const float w = g_c * 0.999999f, v = g_x / (rc * g.len);
+    float *o = work + 6 * a;
+    // unit[t]: dc/du_t = u_s (1 - 1e-6); unit[s]: dc/du_s = u_t (1 - 1e-6), dx/du_s = u_s / (rc |u_s|)
+    o[0] = w * us[0];
+    o[1] = w * us[1];
+    o[2] = w * us[2];
+    o[3] = w * ut[0] + v * us[0];
+    o[4] = w * ut[1] + v * us[1];
+    o[5] = w * ut[2] + v * us[2];
+}
+
+// Second pass: thread per directed edge d, the rows that read unit[d] as t, then as s, in
+// CSR order (deterministic).
+__global__ __launch_bounds__(256) void sbf_bwd_edge_kernel(int64_t n_edges, const int32_t *__restrict__ t_ptr,
+                                                           const int32_t *__restrict__ t_perm,
+                                                           const int32_t *__restrict__ s_ptr,
+                                                           const int32_t *__restrict__ s_perm,
+                                                           const float *__restrict__ work, int accumulate,
+                                                           float *__restrict__ g_unit) {
     const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= n_edges) return;
-    const float *ud = unit + 3 * d;
     float gx = 0.f, gy = 0.f, gz = 0.f;
-    float gb[16];
-    for (int i = t_ptr[d]; i < t_ptr[d + 1]; ++i) {  // d = i->j of the row: dc/du_t = u_s (1 - 1e-6)
-        const int64_t a = t_perm ? t_perm[i] : i;
-        const float *us = unit + 3 * (int64_t)de_s[a];
-        const SbfGeom g = sbf_geom(ud, us, rc);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) gb[k] = g_basis[16 * a + k] * factor;
-        float g_c, g_x;
-        sbf_row_grad(g, gb, g_c, g_x);
-        const float w = g_c * 0.999999f;
-        gx += w * us[0];
-        gy += w * us[1];
-        gz += w * us[2];
+    for (int i = t_ptr[d]; i < t_ptr[d + 1]; ++i) {
+        const float *o = work + 6 * (int64_t)(t_perm ? t_perm[i] : i);
+        gx += o[0];
+        gy += o[1];
+        gz += o[2];
     }
-    for (int i = s_ptr[d]; i < s_ptr[d + 1]; ++i) {  // d = j->k: dc/du_s = u_t (1 - 1e-6), dx/du_s = u_s / (rc |u_s|)
-        const int64_t a = s_perm ? s_perm[i] : i;
-        const float *ut = unit + 3 * (int64_t)de_t[a];
-        const SbfGeom g = sbf_geom(ut, ud, rc);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) gb[k] = g_basis[16 * a + k] * factor;
-        float g_c, g_x;
-        sbf_row_grad(g, gb, g_c, g_x);
-        const float w = g_c * 0.999999f, v = g_x / (rc * g.len);
-        gx += w * ut[0] + v * ud[0];
-        gy += w * ut[1] + v * ud[1];
-        gz += w * ut[2] + v * ud[2];
+    for (int i = s_ptr[d]; i < s_ptr[d + 1]; ++i) {
+        const float *o = work + 6 * (int64_t)(s_perm ? s_perm[i] : i);
+        gx += o[3];
+        gy += o[4];
+        gz += o[5];
     }
     float *o = g_unit + 3 * d;
     if (accumulate) {
@@ -216,9 +227,6 @@ __global__ __launch_bounds__(256) void sbf_bwd_kernel(int64_t n_edges, const flo
     o[2] = gz;
 }
 
-// ------------------------------------------------------------------------------------
-// E2: Bessel basis with the polynomial envelope
-// ------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void bessel_fwd_kernel(int64_t n, int nr, const float *__restrict__ dist,
                                                          const float *__restrict__ freq, BesselParams P,
                                                          float rc, float *__restrict__ out) {
@@ -273,16 +281,22 @@ extern "C" int matris_sbf_fwd(int64_t n_angles, const float *unit, const int32_t
     return 0;
 }
 
-extern "C" int matris_sbf_bwd(int64_t n_edges, const float *unit, const int32_t *de_t, const int32_t *de_s,
-                              const float *g_basis, const int32_t *t_ptr, const int32_t *t_perm,
+extern "C" int matris_sbf_bwd(int64_t n_edges, int64_t n_angles, const float *unit, const int32_t *de_t,
+                              const int32_t *de_s, const float *g_basis, const int32_t *t_ptr, const int32_t *t_perm,
                               const int32_t *s_ptr, const int32_t *s_perm, double cutoff, int accumulate,
-                              float *g_unit, void *stream) {
-    if (n_edges < 0 || !(cutoff > 0) || !unit || !de_t || !de_s || !g_basis || !t_ptr || !s_ptr || !g_unit)
+                              float *work, float *g_unit, void *stream) {
+    if (n_edges < 0 || n_angles < 0 || !(cutoff > 0) || !unit || !t_ptr || !s_ptr || !g_unit ||
+        (n_angles > 0 && (!de_t || !de_s || !g_basis || !work)))
         return MATRIS_E_ARG;
     if (n_edges == 0) return 0;
-    sbf_bwd_kernel<<<matris_blocks(n_edges, 256), 256, 0, (hipStream_t)stream>>>(
-        n_edges, unit, de_t, de_s, g_basis, t_ptr, t_perm, s_ptr, s_perm, (float)cutoff, sbf_factor(cutoff),
-        accumulate, g_unit);
+    hipStream_t st = (hipStream_t)stream;
+    if (n_angles > 0) {
+        sbf_bwd_row_kernel<<<matris_blocks(n_angles, 256), 256, 0, st>>>(n_angles, unit, de_t, de_s, g_basis,
+                                                                         (float)cutoff, sbf_factor(cutoff), work);
+        MATRIS_CHECK_LAUNCH();
+    }
+    sbf_bwd_edge_kernel<<<matris_blocks(n_edges, 256), 256, 0, st>>>(n_edges, t_ptr, t_perm, s_ptr, s_perm, work,
+                                                                     accumulate, g_unit);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -1195,10 +1195,12 @@ class _SBF(torch.autograd.Function):
         lib = _lib.load()
         g = _f32c(g)
         g_unit = torch.empty_like(unit)
+        A = gt.n_rows
+        work = _rows(max(A, 1), 6, unit.device)
         with _timed("sbf_bwd", (unit.shape[0],)):
-            _lib.check(lib.matris_sbf_bwd(unit.shape[0], _p(unit), _p(gt.key), _p(gs.key), _p(g), _p(gt.rowptr),
-                                          _p(gt.perm), _p(gs.rowptr), _p(gs.perm), ctx.cutoff, 0, _p(g_unit),
-                                          _stream()), "matris_sbf_bwd")
+            _lib.check(lib.matris_sbf_bwd(unit.shape[0], A, _p(unit), _p(gt.key), _p(gs.key), _p(g), _p(gt.rowptr),
+                                          _p(gt.perm), _p(gs.rowptr), _p(gs.perm), ctx.cutoff, 0, _p(work),
+                                          _p(g_unit), _stream()), "matris_sbf_bwd")
         return g_unit, None, None, None
 
 
