@@ -206,3 +206,32 @@ def test_md_with_skin_matches_rebuild_every_step():
         runs.append((md.get_positions(), es, md))
     assert np.array_equal(runs[0][0], runs[1][0]) and runs[0][1] == runs[1][1]
     assert runs[1][2]._neighbors.n_builds < 13
+
+
+@pytest.mark.parametrize("seed", [5, 6])
+def test_one_graph_geometry_equals_batched_path(seed):
+    """process_graphs for one graph (the strain trick and edge geometry in one launch,
+    matris_edge_geom_fwd / _bwd) against the batched torch form of processgraph.py:169-199
+    on the same cell (the first graph of [g, g]): lengths, unit vectors, volume, and the
+    gradients of one loss in the positions and the strain."""
+    from matris_amd.model.batch import process_graphs
+    g = _gpu_graph(W.random_cell(np.random.default_rng(seed), 24))
+    one = process_graphs([g], compute_stress=True)
+    two = process_graphs([g, g], compute_stress=True)
+    E = int(g.atom_graph.shape[0])
+    assert torch.allclose(one["edge_lengths"], two["edge_lengths"][:E], rtol=1e-6, atol=1e-6)
+    assert torch.allclose(one["unit_edge_vectors"], two["unit_edge_vectors"][:E], rtol=0, atol=2e-6)
+    assert torch.allclose(one["volumes"].reshape(-1), two["volumes"].reshape(-1)[:1], rtol=1e-6)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    gl = torch.randn(E, device="cuda", generator=gen)
+    gu = torch.randn(E, 3, device="cuda", generator=gen)
+
+    def grads(bg, n):
+        loss = (bg["edge_lengths"][:n] * gl).sum() + (bg["unit_edge_vectors"][:n] * gu).sum()
+        return torch.autograd.grad(loss, [bg["batch_cart_coords"], bg["batch_strains"]])
+    gc1, gs1 = grads(one, E)
+    gc2, gs2 = grads(two, E)
+    N = int(g.atomic_number.shape[0])
+    assert torch.allclose(gc1, gc2[:N], rtol=1e-5, atol=1e-5)
+    assert torch.allclose(gs1[0], gs2[0], rtol=1e-5, atol=1e-4 * float(gs2[0].abs().max()))
+    assert float(gc2[N:].abs().max()) == 0.0 and float(gs2[1].abs().max()) == 0.0
