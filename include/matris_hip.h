@@ -202,6 +202,16 @@ int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float *x, int64_t
                        float scale, int accumulate, float *out, void *stream);
 int matris_gather_mul(int64_t n_rows, const float *a, const int32_t *ia, const float *b, const int32_t *ib,
                       int accumulate, float *out, void *stream);
+/* matris_seg_sum_mul for short segments (rows_hint <= 4 n_seg, e.g. the two directed
+ * copies of each bond) with each segment's sum projected onto the learnable envelope's
+ * basis instead of written: proj_out[s, k] = sum_c sum_s[c] proj_wt[k, c] ([n_seg, proj_k],
+ * proj_k <= 8, proj_wt the Linear(proj_k, 128) weight transposed, [proj_k, 128] row-major,
+ * 16-byte aligned).  The atom-graph Refinement's g_env =
+ * sum_{d2u} h * g_agg[tgt] goes straight to the input gradient of learnable_envelope
+ * (interaction_block.py:240-241). */
+int matris_seg_sum_mul_proj(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx, int64_t col_off,
+                            const int32_t *rowptr, const int32_t *perm, const float *mul, const int32_t *mul_idx,
+                            float scale, const float *proj_wt, int proj_k, float *proj_out, void *stream);
 
 /* Backward of the edge vectors vec[e] = cart[tgt[e]] - (cart[src[e]] + shift[e])
  * (row P1, matris/model/processgraph.py:192-199): g_cart [n_atoms, 3] fp32 =
@@ -296,6 +306,18 @@ int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h, const floa
 int matris_env_agg_bwd_env(int64_t n_seg, const float *h, const float *env, const float *g_agg, const float *S,
                            const int32_t *t_idx, const int32_t *s_ptr, const int32_t *s_perm, float *g_env,
                            float *g_agg_env, void *stream);
+/* matris_env_agg_bwd_env with g_env projected onto the learnable envelope's basis in the
+ * same pass: g_basis[b, k] = sum_c g_env[b, c] wt[k, c] ([n_seg, proj_k], proj_k <= 8; wt
+ * the Linear(proj_k, 128) weight transposed, row-major [proj_k, 128], 16-byte aligned) --
+ * the input gradient of learnable_envelope (interaction_block.py:244), so g_env never
+ * reaches memory. */
+int matris_env_agg_bwd_env_proj(int64_t n_seg, const float *h, const float *env, const float *g_agg,
+                                const float *S, const int32_t *t_idx, const int32_t *s_ptr, const int32_t *s_perm,
+                                const float *proj_wt, int proj_k, float *g_basis, float *g_agg_env, void *stream);
+/* The learnable envelope itself (interaction_block.py:240-246, nn.Linear(num_basis, 128,
+ * bias=False)): env[r, c] = sum_k basis[r, k] wt[k, c], basis [n, k] (k <= 8), wt the
+ * weight transposed [k, 128] row-major, env [n, 128] (wt and env 16-byte aligned). */
+int matris_env_linear(int64_t n, int k, const float *basis, const float *wt, float *env, void *stream);
 
 /* ------------------------------------------------------------------------------------
  * Basis functions of the embeddings (rows E2, E3), thread per row, with input gradients.

@@ -116,6 +116,38 @@ __device__ __forceinline__ float4 add4(const float4 &a, const float4 &b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
+// Projection of a 128-wide row onto K (<= 8) basis columns, out[k] = sum_c row[c] wt[k][c]
+// with wt [K, 128] row-major (a Linear(K, 128) weight, transposed), the row held as one
+// float4 per lane of a 32-lane half-wave (lane l: columns 4l .. 4l+3).  Every lane of the
+// half-wave must be active; lane 16 of it stores the K values.  This is the input gradient
+// of a Linear(K, 128) without bias (the learnable envelope, interaction_block.py:240-246)
+// formed in the epilogue of the kernel that produces the 128-wide gradient row, so that
+// row never reaches memory.  Each term: one coalesced float4 of wt, a 16-lane DPP sum and
+// one DPP broadcast between the half-wave's two rows.
+#define MATRIS_PROJ_KMAX 8
+// The two 16-lane DPP rows of a half-wave combined: lanes 16 .. 31 (and 48 .. 63) gain the
+// value of lane 15 (47) of the row before them (DPP row_bcast:15 on rows 1 and 3).
+__device__ __forceinline__ float rows_combine(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
+}
+// wt: global or LDS (a block's staged copy); the half-wave's lane 16 stores.
+__device__ __forceinline__ void proj_row_store(const float4 &t, int l, const float *wt, int K,
+                                               float *__restrict__ dst) {
+    float p[MATRIS_PROJ_KMAX];
+#pragma unroll
+    for (int k = 0; k < MATRIS_PROJ_KMAX; ++k) {
+        p[k] = 0.f;
+        if (k < K) {
+            const float4 w = *reinterpret_cast<const float4 *>(wt + k * MATRIS_D + 4 * l);
+            p[k] = rows_combine(row16_sum(t.x * w.x + t.y * w.y + t.z * w.z + t.w * w.w));
+        }
+    }
+    if (l == 16)
+#pragma unroll
+        for (int k = 0; k < MATRIS_PROJ_KMAX; ++k)
+            if (k < K) dst[k] = p[k];
+}
+
 template <bool MUL>
 __device__ __forceinline__ float4 seg_src_rows(const SegSrc &v, int64_t s, int c, int off, int stride) {
     if (v.tile > 0) return seg_tile_rows(v.x + v.col_off + c, v.ldx, v.rowptr[s], v.rowptr[s + 1], v.tile, off, stride);
@@ -219,11 +251,15 @@ __device__ __forceinline__ void seg_rows4(const SegSrc &v, int64_t s0, int64_t n
     }
 }
 
-template <bool MUL>
+// With proj_w (a [K, 128] transposed Linear weight), each segment's row is projected
+// (proj_row_store) into proj_out [n_seg, K] instead of being written to out.
+template <bool MUL, bool PROJ = false>
 __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, int64_t n_seg, int accumulate,
                                                             const float *__restrict__ base,
                                                             const float *__restrict__ base_w,
-                                                            float *__restrict__ out) {
+                                                            float *__restrict__ out,
+                                                            const float *__restrict__ proj_w, int proj_k,
+                                                            float *__restrict__ proj_out) {
     const int w = threadIdx.x >> 6, half = (threadIdx.x >> 5) & 1, l = threadIdx.x & 31, c = 4 * l;
     const int64_t s0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + w) * 4;
     if (s0 >= n_seg) return;  // whole wave
@@ -246,6 +282,10 @@ __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, 
         if (s >= n_seg) break;
         float4 t = make_float4(ta[j].x * a.scale, ta[j].y * a.scale, ta[j].z * a.scale, ta[j].w * a.scale);
         if (b.x) t = add4(t, make_float4(tb[j].x * b.scale, tb[j].y * b.scale, tb[j].z * b.scale, tb[j].w * b.scale));
+        if constexpr (PROJ) {  // uniform over the wave: s < n_seg is the same for all its lanes
+            proj_row_store(t, l, proj_w, proj_k, proj_out + s * proj_k);
+            continue;
+        }
         float *op = out + s * MATRIS_D + c;
         if (base) t = add4(t, mul4(ld4(base_w + c), ld4(base + s * MATRIS_D + c)));
         if (accumulate) t = add4(t, ld4(op));
@@ -258,19 +298,40 @@ static bool seg_src_ok(const SegSrc &v) {
            !(v.col_off % 4) && v.tile >= 0 && !(v.tile > 0 && (v.perm || v.mul));
 }
 
+// proj_w / proj_k / proj_out: project each segment's row onto the K rows of proj_w
+// ([K, 128], K <= 8) into proj_out [n_seg, K] instead of writing out (short segments only:
+// rows_hint <= 4 n_seg; no accumulate or base).
 static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64_t rows_hint, int accumulate,
-                          float *out, void *stream, const float *base = nullptr, const float *base_w = nullptr) {
-    if (n_seg < 0 || !out || !seg_src_ok(a) || (b.x && !seg_src_ok(b)) || (base && !base_w)) return MATRIS_E_ARG;
+                          float *out, void *stream, const float *base = nullptr, const float *base_w = nullptr,
+                          const float *proj_w = nullptr, int proj_k = 0, float *proj_out = nullptr) {
+    if (n_seg < 0 || !seg_src_ok(a) || (b.x && !seg_src_ok(b)) || (base && !base_w)) return MATRIS_E_ARG;
+    // rows_hint 0 means "not given", except for a projection, which passes the row count
+    // itself (0: every segment is empty and projects to zeros)
+    const bool short_segs = (rows_hint > 0 || proj_w) && rows_hint >= 0 && rows_hint <= 4 * n_seg;
+    if (proj_w) {
+        if (!proj_out || proj_k < 1 || proj_k > MATRIS_PROJ_KMAX || !short_segs || accumulate || base)
+            return MATRIS_E_ARG;
+    } else if (!out) {
+        return MATRIS_E_ARG;
+    }
     if (n_seg == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     const bool mul = a.mul || (b.x && b.mul);
     const bool wide = rows_hint >= 32 * n_seg;  // long segments: a work-group each
-    if (rows_hint > 0 && rows_hint <= 4 * n_seg) {  // short segments: four per wave
+    if (short_segs) {  // short segments: four per wave
         const unsigned g4 = (unsigned)matris_blocks(n_seg, 4 * WAVES_PER_BLOCK);
-        if (mul)
-            seg_sum_short_kernel<true><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
+        if (mul && proj_w)
+            seg_sum_short_kernel<true, true><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out, proj_w,
+                                                                 proj_k, proj_out);
+        else if (mul)
+            seg_sum_short_kernel<true><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out, nullptr, 0,
+                                                           nullptr);
+        else if (proj_w)
+            seg_sum_short_kernel<false, true><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out, proj_w,
+                                                                  proj_k, proj_out);
         else
-            seg_sum_short_kernel<false><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out);
+            seg_sum_short_kernel<false><<<g4, 256, 0, st>>>(a, b, n_seg, accumulate, base, base_w, out, nullptr, 0,
+                                                            nullptr);
         MATRIS_CHECK_LAUNCH();
         return 0;
     }
@@ -322,6 +383,16 @@ extern "C" int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float 
     const SegSrc a{x, ldx, col_off, rowptr, perm, scale, mul, mul_idx};
     const SegSrc none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f, nullptr, nullptr};
     return seg_sum_launch(a, none, n_seg, rows_hint, accumulate, out, stream);
+}
+
+extern "C" int matris_seg_sum_mul_proj(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx,
+                                       int64_t col_off, const int32_t *rowptr, const int32_t *perm, const float *mul,
+                                       const int32_t *mul_idx, float scale, const float *proj_w, int proj_k,
+                                       float *proj_out, void *stream) {
+    if (!mul || !proj_w || ((uintptr_t)proj_w & 15)) return MATRIS_E_ARG;
+    const SegSrc a{x, ldx, col_off, rowptr, perm, scale, mul, mul_idx};
+    const SegSrc none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f, nullptr, nullptr};
+    return seg_sum_launch(a, none, n_seg, rows_hint, 0, nullptr, stream, nullptr, nullptr, proj_w, proj_k, proj_out);
 }
 
 // ------------------------------------------------------------------------------------
@@ -1007,6 +1078,7 @@ __global__ __launch_bounds__(256) void env_agg_bwd_rows_kernel(int64_t n_rows, c
 
 // g_env: one wave per source segment, half-waves on alternating rows as in the forward;
 // with ge given, also ge[b] = g_agg[b] * env[b] (the per-bond factor of g_h's term).
+template <bool PROJ>
 __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, const float *__restrict__ h,
                                                               const float *__restrict__ env,
                                                               const float *__restrict__ g_agg,
@@ -1014,7 +1086,14 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
                                                               const int32_t *__restrict__ s_ptr,
                                                               const int32_t *__restrict__ s_perm,
                                                               const int32_t *__restrict__ t_idx,
-                                                              float *__restrict__ g_env, float *__restrict__ ge) {
+                                                              float *__restrict__ g_env, float *__restrict__ ge,
+                                                              const float *__restrict__ proj_w, int proj_k) {
+    __shared__ __align__(16) float wts[PROJ ? MATRIS_PROJ_KMAX * MATRIS_D : 4];
+    if constexpr (PROJ) {  // the block's copy of wt (before any wave leaves)
+        for (int q = threadIdx.x; q < proj_k * MATRIS_D / 4; q += blockDim.x)
+            reinterpret_cast<float4 *>(wts)[q] = ld4(proj_w + 4 * q);
+        lds_barrier();
+    }
     const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (seg >= n_seg) return;
     const int half = (threadIdx.x >> 5) & 1, c = 4 * (threadIdx.x & 31);
@@ -1052,8 +1131,11 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
         const float4 es = ld4(env + seg * MATRIS_D + c);
         st4(ge + seg * MATRIS_D + c, make_float4(gs.x * es.x, gs.y * es.y, gs.z * es.z, gs.w * es.w));
     }
-    st4(g_env + seg * MATRIS_D + c,
-        make_float4(gs.x * sv.x + t.x, gs.y * sv.y + t.y, gs.z * sv.z + t.z, gs.w * sv.w + t.w));
+    const float4 gv = make_float4(gs.x * sv.x + t.x, gs.y * sv.y + t.y, gs.z * sv.z + t.z, gs.w * sv.w + t.w);
+    if constexpr (PROJ)  // g_env projected onto the envelope's basis: [n_seg, K]
+        proj_row_store(gv, threadIdx.x & 31, wts, proj_k, g_env + seg * proj_k);
+    else
+        st4(g_env + seg * MATRIS_D + c, gv);
 }
 
 extern "C" int matris_env_agg_fwd(int64_t n_seg, const float *h, const float *env, const int32_t *t_ptr,
@@ -1082,8 +1164,8 @@ extern "C" int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h,
         MATRIS_CHECK_LAUNCH();
     }
     if (n_seg > 0) {
-        env_agg_bwd_env_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(n_seg, h, env, g_agg, S, s_ptr,
-                                                                                    s_perm, t_idx, g_env, nullptr);
+        env_agg_bwd_env_kernel<false><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(
+            n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, nullptr, nullptr, 0);
         MATRIS_CHECK_LAUNCH();
     }
     return 0;
@@ -1097,8 +1179,76 @@ extern "C" int matris_env_agg_bwd_env(int64_t n_seg, const float *h, const float
         15)
         return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
-    env_agg_bwd_env_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
-        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, g_agg_env);
+    env_agg_bwd_env_kernel<false><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, g_agg_env, nullptr, 0);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_env_agg_bwd_env_proj(int64_t n_seg, const float *h, const float *env, const float *g_agg,
+                                           const float *S, const int32_t *t_idx, const int32_t *s_ptr,
+                                           const int32_t *s_perm, const float *proj_w, int proj_k, float *g_basis,
+                                           float *g_agg_env, void *stream) {
+    if (n_seg < 0 || !h || !env || !g_agg || !S || !t_idx || !s_ptr || !g_basis || !proj_w || proj_k < 1 ||
+        proj_k > MATRIS_PROJ_KMAX)
+        return MATRIS_E_ARG;
+    if (((uintptr_t)h | (uintptr_t)env | (uintptr_t)g_agg | (uintptr_t)S | (uintptr_t)g_agg_env | (uintptr_t)proj_w) &
+        15)
+        return MATRIS_E_ARG;
+    if (n_seg == 0) return 0;
+    env_agg_bwd_env_kernel<true><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
+        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_basis, g_agg_env, proj_w, proj_k);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
+// the learnable envelope (interaction_block.py:240-246): env = basis W^T, a Linear(K, 128)
+// without bias on each bond's K basis values (K <= 8).  A half-wave per row (lane l:
+// columns 4l .. 4l+3) with the lane's K float4 of W^T held in registers over a
+// grid-stride loop of 32-row passes.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void env_linear_kernel(int64_t n, int K, const float *__restrict__ basis,
+                                                         const float *__restrict__ wt, float *__restrict__ env) {
+    // per block pass: 32 rows, their K basis values staged in LDS by one coalesced load;
+    // half-wave j takes rows j, j + 8, j + 16, j + 24 of the pass
+    __shared__ float bs[32 * MATRIS_PROJ_KMAX];
+    const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;
+    float4 w[MATRIS_PROJ_KMAX];
+#pragma unroll
+    for (int k = 0; k < MATRIS_PROJ_KMAX; ++k) w[k] = k < K ? ld4(wt + k * MATRIS_D + 4 * l) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t r0 = (int64_t)blockIdx.x * 32; r0 < n; r0 += (int64_t)gridDim.x * 32) {  // uniform over the block
+        const int64_t nr = n - r0 < 32 ? n - r0 : 32;
+        const float bv = threadIdx.x < nr * K ? basis[r0 * K + threadIdx.x] : 0.f;
+        lds_barrier();  // the previous pass is done reading bs (W's loads stay in flight)
+        if (threadIdx.x < nr * K) bs[threadIdx.x] = bv;
+        lds_barrier();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int rr = hw + 8 * q;
+            if (rr >= nr) break;
+            const float *b = bs + rr * K;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < MATRIS_PROJ_KMAX; ++k)
+                if (k < K) {
+                    const float x = b[k];
+                    o.x = fmaf(x, w[k].x, o.x);
+                    o.y = fmaf(x, w[k].y, o.y);
+                    o.z = fmaf(x, w[k].z, o.z);
+                    o.w = fmaf(x, w[k].w, o.w);
+                }
+            st4(env + (r0 + rr) * MATRIS_D + 4 * l, o);
+        }
+    }
+}
+
+extern "C" int matris_env_linear(int64_t n, int k, const float *basis, const float *wt, float *env, void *stream) {
+    if (n < 0 || k < 1 || k > MATRIS_PROJ_KMAX) return MATRIS_E_ARG;
+    if (n == 0) return 0;
+    if (!basis || !wt || !env || (((uintptr_t)env | (uintptr_t)wt) & 15)) return MATRIS_E_ARG;
+    const int64_t nb = matris_blocks(n, 32), blocks = nb < 2048 ? nb : 2048;
+    env_linear_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(n, k, basis, wt, env);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -82,6 +82,11 @@ def _res_ok(w) -> bool:
     return tuple(w.shape) == (1, D)
 
 
+def _env_wt(layer):
+    """The learnable envelope's weight transposed, [K, 128] (kept per weight version)."""
+    return layer._env.get(layer.learnable_envelope.weight).mats["wt0"]
+
+
 def _runs(grp: ops.Grouping, blk: int):
     """(key, blk) for gmlp_bwd_raw's tile-run sums when grp's rows ascend by key (no
     permutation), else None (the block leaves as rows)."""
@@ -218,10 +223,11 @@ class _LineRefinement(torch.autograd.Function):
     With recompute, only the inputs are kept and the forward reruns in the backward."""
 
     @staticmethod
-    def forward(ctx, tb, atom, bond, env, layer, lg, recompute):
-        ops._check_dev(tb, atom, bond, env)
-        tb, atom, bond, env = (ops._f32c(t) for t in (tb, atom, bond, env))
+    def forward(ctx, tb, atom, bond, basis, layer, lg, recompute):
+        ops._check_dev(tb, atom, bond, basis)
+        tb, atom, bond, basis = (ops._f32c(t) for t in (tb, atom, bond, basis))
         mode = ops._MMA["mode"]
+        env = ops.env_linear_raw(basis, _env_wt(layer))
         bond_new, tb_new, saved = _refine_fwd(layer, tb, atom, bond, env, lg, mode, save=not recompute)
         if recompute:
             ctx.save_for_backward(tb, atom, bond, env)
@@ -252,7 +258,9 @@ class _LineRefinement(torch.autograd.Function):
         g_tb_new = _zeros_if_none(g_tb_new, h)
         g_bond = ops._rows(E, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
-        g_env, g_agg_env = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src)
+        # the envelope's gradient leaves projected onto its basis (the learnable envelope's
+        # input gradient), so the [E, 128] g_env is never stored
+        g_basis, g_agg_env = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src, proj_wt=_env_wt(layer))
         del h
         # g_h = edge_FFN's input gradient + the aggregate's term; g_tb = source 0's
         # GatedMLP gradient + r_e g_tb_new.  In the two-plane modes g_h never leaves the
@@ -270,7 +278,7 @@ class _LineRefinement(torch.autograd.Function):
         g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True,
                         second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
-        return g_tb, g_atom, g_bond, g_env, None, None, None
+        return g_tb, g_atom, g_bond, g_basis, None, None, None
 
 
 def line_attention(layer, bond, tb, lg, recompute: bool = False):
@@ -278,9 +286,10 @@ def line_attention(layer, bond, tb, lg, recompute: bool = False):
     return _LineAttention.apply(bond, tb, layer, lg, recompute)
 
 
-def line_refinement(layer, tb, atom, bond, env, lg, recompute: bool = False):
-    """(bond', tb') of Refinement.forward on the line graph; env = learnable_envelope(smooth_weight)."""
-    return _LineRefinement.apply(tb, atom, bond, env, layer, lg, recompute)
+def line_refinement(layer, tb, atom, bond, basis, lg, recompute: bool = False):
+    """(bond', tb') of Refinement.forward on the line graph; basis = the smooth weights the
+    learnable envelope maps to env (formed inside, matris_env_linear)."""
+    return _LineRefinement.apply(tb, atom, bond, basis, layer, lg, recompute)
 
 
 # ------------------------------------------------------------------------------------
@@ -369,12 +378,14 @@ class _AtomRefinement(torch.autograd.Function):
         h     = GatedMLP([bond[d2u], atom[tgt], atom[src]])               [E_d]
         atom' = node_FFN(sum_tgt h * w) + r_n * atom
         bond' = mean_{d2u} edge_FFN(h or h * w) + r_e * bond
-    env = learnable_envelope(smooth_weight) [E_u]."""
+    env = learnable_envelope(basis) [E_u], formed here (matris_env_linear); the backward
+    returns the basis gradient."""
 
     @staticmethod
-    def forward(ctx, atom, bond, env, layer, ag, d2u):
-        ops._check_dev(atom, bond, env)
-        atom, bond, env = ops._f32c(atom), ops._f32c(bond), ops._f32c(env)
+    def forward(ctx, atom, bond, basis, layer, ag, d2u):
+        ops._check_dev(atom, bond, basis)
+        atom, bond = ops._f32c(atom), ops._f32c(bond)
+        env = ops.env_linear_raw(basis, _env_wt(layer))
         mode = ops._MMA["mode"]
         tgt, src = ag["grp_tgt"], ag["grp_src"]
         Ed = d2u.key.numel()
@@ -420,8 +431,9 @@ class _AtomRefinement(torch.autograd.Function):
         del p_dn
         if not ctx.smoothed and mode != 6:
             # g_h = edge_FFN's input gradient (from half the bond gradient of each directed
-            # copy) + g_agg[tgt] * env[d2u], computed per tile inside the GatedMLP backward
-            g_env = ops.seg_sum_mul_raw(h, d2u, g_agg, tgt.key)
+            # copy) + g_agg[tgt] * env[d2u], computed per tile inside the GatedMLP backward;
+            # g_env = sum_{d2u} h * g_agg[tgt] leaves projected onto the envelope's basis
+            g_basis = ops.seg_sum_mul_proj_raw(h, d2u, g_agg, tgt.key, _env_wt(layer))
             del h
             g_x = ops.gmlp_bwd_ffn_raw(ph, p_h, z_h, 3 * D, mode, pm, g_bond_new, p_de, env_term=(g_agg, w, tgt, d2u),
                                        runs=_runs(tgt, 1), ffn_g_idx=d2u.key, ffn_g_scale=0.5)
@@ -429,7 +441,7 @@ class _AtomRefinement(torch.autograd.Function):
             g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
             ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
                             second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
-            return g_atom, g_bond, g_env, None, None, None
+            return g_atom, g_bond, g_basis, None, None, None
         g_te = ops.ffn_bwd_raw(pm, ops.gather_raw(g_bond_new, d2u.key, 0.5), p_de, mode)
         del p_de
         if ctx.smoothed:
@@ -447,7 +459,7 @@ class _AtomRefinement(torch.autograd.Function):
         g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
                         second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
-        return g_atom, g_bond, g_env, None, None, None
+        return g_atom, g_bond, g_env @ _env_wt(layer).t(), None, None, None
 
 
 def atom_attention(layer, atom, bond, ag, d2u):
@@ -455,6 +467,7 @@ def atom_attention(layer, atom, bond, ag, d2u):
     return _AtomAttention.apply(atom, bond, layer, ag, d2u)
 
 
-def atom_refinement(layer, atom, bond, env, ag, d2u):
-    """(atom', bond') of Refinement.forward on the atom graph; env = learnable_envelope(smooth_weight)."""
-    return _AtomRefinement.apply(atom, bond, env, layer, ag, d2u)
+def atom_refinement(layer, atom, bond, basis, ag, d2u):
+    """(atom', bond') of Refinement.forward on the atom graph; basis = the smooth weights the
+    learnable envelope maps to env (formed inside, matris_env_linear)."""
+    return _AtomRefinement.apply(atom, bond, basis, layer, ag, d2u)

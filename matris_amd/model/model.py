@@ -405,6 +405,7 @@ class Refinement(nn.Module):
         self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim), requires_grad=True)
         self._node_ffn = ops._WeightPack()
         self._edge_ffn = ops._WeightPack()
+        self._env = ops._WeightPack()  # learnable_envelope.weight^T for the fused kernels
 
     @staticmethod
     def _ffn(mlp, pack, x):
@@ -419,14 +420,12 @@ class Refinement(nn.Module):
                 recompute: bool = False):
         tgt, src = graph["grp_tgt"], graph["grp_src"]
         if self.graph_type == "atom graph" and fused.atom_refinement_fusable(self):  # one node, explicit backward
-            return fused.atom_refinement(self, node_feat, edge_feat, self.learnable_envelope(smooth_weight), graph,
-                                         d2u)
+            return fused.atom_refinement(self, node_feat, edge_feat, smooth_weight, graph, d2u)
         if self.graph_type == "atom graph":
             w = ops.gather(self.learnable_envelope(smooth_weight), d2u)
             h = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
         elif fused.line_refinement_fusable(self):  # one node, explicit backward
-            env = self.learnable_envelope(smooth_weight)
-            return fused.line_refinement(self, edge_feat, atom_feat, node_feat, env, graph, recompute)
+            return fused.line_refinement(self, edge_feat, atom_feat, node_feat, smooth_weight, graph, recompute)
         else:
             env = self.learnable_envelope(smooth_weight)
             w = ops.gather(env, src) * ops.gather(env, tgt)

@@ -250,6 +250,21 @@ def seg_sum_mul_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: 
     return out
 
 
+def seg_sum_mul_proj_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: torch.Tensor,
+                         proj_wt: torch.Tensor) -> torch.Tensor:
+    """[n_seg, K]: the segment sums of seg_sum_mul_raw(x, grp, mul, mul_idx) times W, with
+    proj_wt = W^T [K, 128] (matris_seg_sum_mul_proj; short segments: at most 4 rows per
+    segment on average, e.g. the two directed copies of each bond)."""
+    lib = _lib.load()
+    wt = _f32c(proj_wt)
+    out = torch.empty(grp.n_seg, wt.shape[0], dtype=torch.float32, device=x.device)
+    with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
+        _lib.check(lib.matris_seg_sum_mul_proj(grp.n_seg, grp.n_rows, _p(x), D, 0, _p(grp.rowptr), _p(grp.perm),
+                                               _p(mul), _p(mul_idx), 1.0, _p(wt), wt.shape[0], _p(out), _stream()),
+                   "matris_seg_sum_mul_proj")
+    return out
+
+
 def gather_mul_raw(a: torch.Tensor, ia, b: torch.Tensor, ib, out: torch.Tensor, accumulate: bool = False):
     """out[r] (+)= a[ia[r]] * b[ib[r]] (matris_gather_mul; an index None is the identity)."""
     if out.shape[0] == 0:
@@ -485,16 +500,41 @@ def env_agg_fwd_raw(h, env, tgt: Grouping, src: Grouping):
     return agg, S
 
 
-def env_agg_bwd_env_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping):
+def env_agg_bwd_env_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, proj_wt=None):
     """(g_env, g_agg_env) of matris_env_agg_bwd_env: g_env as env_agg_bwd_raw returns it and
-    g_agg_env = g_agg * env, the per-bond factor ffn_bwd_raw(..., env_term=...) takes."""
+    g_agg_env = g_agg * env, the per-bond factor ffn_bwd_raw(..., env_term=...) takes.  With
+    proj_wt (the envelope's Linear(K, 128) weight transposed, [K, 128]) the first result is
+    g_env W [E, K], the gradient of the envelope's basis (matris_env_agg_bwd_env_proj)."""
     lib = _lib.load()
     E = env.shape[0]
-    g_env, ge = _rows(E, D, h.device), _rows(E, D, h.device)
+    ge = _rows(E, D, h.device)
+    if proj_wt is not None:
+        wt = _f32c(proj_wt)
+        g_basis = torch.empty(E, wt.shape[0], dtype=torch.float32, device=h.device)
+        with _timed("env_agg_bwd", (h.shape[0], E)):
+            _lib.check(lib.matris_env_agg_bwd_env_proj(E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key),
+                                                       _p(src.rowptr), _p(src.perm), _p(wt), wt.shape[0],
+                                                       _p(g_basis), _p(ge), _stream()), "matris_env_agg_bwd_env_proj")
+        return g_basis, ge
+    g_env = _rows(E, D, h.device)
     with _timed("env_agg_bwd", (h.shape[0], E)):
         _lib.check(lib.matris_env_agg_bwd_env(E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key), _p(src.rowptr),
                                               _p(src.perm), _p(g_env), _p(ge), _stream()), "matris_env_agg_bwd_env")
     return g_env, ge
+
+
+def env_linear_raw(basis, wt):
+    """The learnable envelope env = basis W^T (matris_env_linear; interaction_block.py:240-246,
+    nn.Linear(K, 128, bias=False)): basis [E, K], wt = W^T [K, 128] -> env [E, 128]."""
+    lib = _lib.load()
+    basis, wt = _f32c(basis), _f32c(wt)
+    E, K = basis.shape
+    if tuple(wt.shape) != (K, D):
+        raise ValueError(f"env_linear_raw: the transposed weight must be [{K}, {D}], got {tuple(wt.shape)}")
+    env = _rows(E, D, basis.device)
+    with _timed("env_linear", (E,)):
+        _lib.check(lib.matris_env_linear(E, K, _p(basis), _p(wt), _p(env), _stream()), "matris_env_linear")
+    return env
 
 
 def env_agg_bwd_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, g_h, accumulate: bool):

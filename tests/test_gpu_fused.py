@@ -111,10 +111,11 @@ def test_line_refinement_vs_fp64(A, E, N, recompute):
     _randomize(layer, A + 3)
     lg, tgt, src, atom_l = _graph(A, E, N, A + 4)
     tb, atom, bond = torch.randn(A, 128), torch.randn(N, 128), torch.randn(E, 128)
-    env = torch.rand(E, 128) + 0.1
+    basis = torch.rand(E, 7) + 0.1  # the smooth weights the learnable envelope maps to env
     g_b, g_t = torch.randn(E, 128), torch.randn(A, 128)
-    leaves = [x.double().requires_grad_(True) for x in (tb, atom, bond, env)]
-    t64, a64, b64, env64 = leaves
+    leaves = [x.double().requires_grad_(True) for x in (tb, atom, bond, basis)]
+    t64, a64, b64, basis64 = leaves
+    env64 = basis64 @ layer.learnable_envelope.weight.double().t()
     h = _gmlp64(layer.edge_nonlinear_update, torch.cat([t64, a64[atom_l], b64[tgt], b64[src]], 1))
     hw = h * (env64[src] * env64[tgt])
     agg = torch.zeros(E, 128, dtype=torch.float64).index_add(0, tgt, hw)
@@ -123,7 +124,7 @@ def test_line_refinement_vs_fp64(A, E, N, recompute):
     ((bn_r * g_b.double()).sum() + (tn_r * g_t.double()).sum()).backward()
     layer = layer.to(DEV)
     assert fused.line_refinement_fusable(layer)
-    dev_leaves = [x.to(DEV).requires_grad_(True) for x in (tb, atom, bond, env)]
+    dev_leaves = [x.to(DEV).requires_grad_(True) for x in (tb, atom, bond, basis)]
     bn, tn = fused.line_refinement(layer, *dev_leaves, lg, recompute)
     assert _rel(bn, bn_r) < 1e-5 and _rel(tn, tn_r) < 1e-5
     torch.autograd.backward([bn, tn], [g_b.to(DEV), g_t.to(DEV)])
@@ -139,10 +140,10 @@ def test_line_layers_unused_output_gradient():
     layer = Refinement(128, 128, 128, 7, norm_type="rms", graph_type="line graph").to(DEV)
     lg, _, _, _ = _graph(500, 80, 9, 9)
     xs = [torch.randn(n, 128, device=DEV).requires_grad_(True) for n in (500, 9, 80)]
-    env = (torch.rand(80, 128, device=DEV) + 0.1).requires_grad_(True)
-    bn, _ = fused.line_refinement(layer, *xs, env, lg)
+    basis = (torch.rand(80, 7, device=DEV) + 0.1).requires_grad_(True)
+    bn, _ = fused.line_refinement(layer, *xs, basis, lg)
     bn.sum().backward()
-    assert all(torch.isfinite(x.grad).all() for x in xs) and torch.isfinite(env.grad).all()
+    assert all(torch.isfinite(x.grad).all() for x in xs) and torch.isfinite(basis.grad).all()
 
 
 def _atom_graph(N, E_u, seed):
@@ -201,10 +202,11 @@ def test_atom_refinement_vs_fp64(smoothed):
                        use_smoothed_for_delta_edge=smoothed)
     _randomize(layer, 3)
     ag, gd2u, tgt, src, d2u = _atom_graph(N, E_u, 4)
-    atom, bond, env = torch.randn(N, 128), torch.randn(E_u, 128), torch.rand(E_u, 128) + 0.1
+    atom, bond, basis = torch.randn(N, 128), torch.randn(E_u, 128), torch.rand(E_u, 7) + 0.1
     g_a, g_b = torch.randn(N, 128), torch.randn(E_u, 128)
-    leaves = [x.double().requires_grad_(True) for x in (atom, bond, env)]
-    a64, b64, env64 = leaves
+    leaves = [x.double().requires_grad_(True) for x in (atom, bond, basis)]
+    a64, b64, basis64 = leaves
+    env64 = basis64 @ layer.learnable_envelope.weight.double().t()
     h = _gmlp64(layer.edge_nonlinear_update, torch.cat([b64[d2u], a64[tgt], a64[src]], 1))
     hw = h * env64[d2u]
     agg = torch.zeros(N, 128, dtype=torch.float64).index_add(0, tgt, hw)
@@ -214,7 +216,7 @@ def test_atom_refinement_vs_fp64(smoothed):
     ((an_r * g_a.double()).sum() + (bn_r * g_b.double()).sum()).backward()
     layer = layer.to(DEV)
     assert fused.atom_refinement_fusable(layer)
-    dev_leaves = [x.to(DEV).requires_grad_(True) for x in (atom, bond, env)]
+    dev_leaves = [x.to(DEV).requires_grad_(True) for x in (atom, bond, basis)]
     an, bn = fused.atom_refinement(layer, *dev_leaves, ag, gd2u)
     assert _rel(an, an_r) < 1e-5 and _rel(bn, bn_r) < 1e-5
     torch.autograd.backward([an, bn], [g_a.to(DEV), g_b.to(DEV)])

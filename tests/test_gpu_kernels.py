@@ -108,6 +108,71 @@ def test_seg_sum_two_groupings_one_pass(R, S, acc):
         ops.seg_sum_raw(x, ga, second=(xb, ops.Grouping.build(kb, S + 1), 1.0, 256, 128))
 
 
+@pytest.mark.parametrize("E,K", [(33698, 7), (1, 7), (0, 7), (513, 1), (777, 8), (100, 3)])
+def test_env_linear(E, K):
+    """matris_env_linear: the learnable envelope env = basis W^T (interaction_block.py:
+    240-246, Linear(K, 128) without bias) against the fp64 product."""
+    ops = _ops()
+    torch.manual_seed(E + K)
+    basis = torch.randn(E, K, device=DEV)
+    w = torch.randn(128, K, device=DEV) / 3
+    env = ops.env_linear_raw(basis, w.t().contiguous())
+    assert tuple(env.shape) == (E, 128)
+    if E:
+        ref = basis.double().cpu() @ w.double().cpu().t()
+        assert _rel(env, ref) < 1e-6
+    with pytest.raises(ValueError):
+        ops.env_linear_raw(basis, torch.randn(K, 64, device=DEV))
+
+
+@pytest.mark.parametrize("R,E_u,K", [(67396, 33698, 7), (2, 1, 7), (0, 5, 7), (1000, 500, 8), (10, 5, 1)])
+def test_seg_sum_mul_proj(R, E_u, K):
+    """matris_seg_sum_mul_proj: the atom-graph envelope gradient sum_{d2u} h * g_agg[tgt]
+    (two directed copies per bond) projected onto the envelope's basis, g_env W ([E_u, K]),
+    against fp64 index_add_ followed by the fp64 product; the unprojected sums as a second
+    check of the same rows."""
+    ops = _ops()
+    torch.manual_seed(R + K)
+    d2u = torch.arange(R, dtype=torch.int32) // 2 if R else torch.zeros(0, dtype=torch.int32)
+    d2u = torch.minimum(d2u, torch.tensor(E_u - 1, dtype=torch.int32))
+    grp = ops.Grouping.build(d2u.to(DEV), E_u)
+    h = torch.randn(max(R, 1), 128, device=DEV)[:R]
+    T = 400
+    g_agg = torch.randn(T, 128, device=DEV)
+    tk = torch.randint(0, T, (R,), dtype=torch.int32, device=DEV)
+    w = torch.randn(128, K, device=DEV) / 5
+    g_basis = ops.seg_sum_mul_proj_raw(h, grp, g_agg, tk, w.t().contiguous())
+    g_env = torch.zeros(E_u, 128, dtype=torch.float64).index_add_(
+        0, d2u.long(), h.double().cpu() * g_agg.double().cpu()[tk.cpu().long()])
+    ref = g_env @ w.double().cpu()
+    assert tuple(g_basis.shape) == (E_u, K)
+    assert _rel(g_basis, ref) < 2e-6
+    plain = ops.seg_sum_mul_raw(h, grp, g_agg, tk)
+    assert _rel(plain.double().cpu() @ w.double().cpu(), ref) < 2e-6
+
+
+@pytest.mark.parametrize("A,E,K", [(264384, 33698, 7), (3000, 400, 7), (50, 9, 8)])
+def test_env_agg_bwd_env_proj(A, E, K):
+    """matris_env_agg_bwd_env_proj: the line Refinement's g_env (interaction_block.py:243-258)
+    projected onto the envelope's basis in the same pass.  g_agg_env is bit-identical to the
+    unprojected entry point's; g_basis equals its g_env times W to fp32 rounding (fp64
+    product of the fp32 g_env)."""
+    ops = _ops()
+    torch.manual_seed(A + K)
+    tkey = torch.sort(_keys(A, E, A + 1))[0].to(DEV)
+    skey = _keys(A, E, A + 2).to(DEV)
+    tgt = ops.Grouping.build(tkey, E, sorted_rows=True)
+    src = ops.Grouping.build(skey, E)
+    h = torch.randn(A, 128, device=DEV)
+    env, g_agg, S = torch.rand(E, 128, device=DEV), torch.randn(E, 128, device=DEV), torch.randn(E, 128, device=DEV)
+    w = torch.randn(128, K, device=DEV) / 5
+    g_env, ge = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src)
+    g_basis, ge2 = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src, proj_wt=w.t().contiguous())
+    assert torch.equal(ge, ge2)
+    assert tuple(g_basis.shape) == (E, K)
+    assert _rel(g_basis, g_env.double().cpu() @ w.double().cpu()) < 2e-6
+
+
 @pytest.mark.parametrize("R,S,T", [(67396, 864, 33698), (5000, 800, 300), (37, 5, 11), (0, 4, 3), (67396, 33698, 864),
                                    (9, 7, 5)])
 @pytest.mark.parametrize("acc", [False, True])

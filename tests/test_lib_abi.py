@@ -114,6 +114,17 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_seg_sum_mul(4, 10, v16, 128, 0, v16, None, None, v16, 1.0, 0, v16, None) == -1001
     assert lib.matris_seg_sum_mul(4, 10, v16, 64, 0, v16, None, v16, v16, 1.0, 0, v16, None) == -1001
     assert lib.matris_gather_mul(10, v16, None, v16, None, 0, None, None) == -1001
+    # learnable envelope: K outside 1..8, a misaligned env; projected sums: K = 0, long
+    # segments (rows_hint above 4 per segment), no projection output
+    assert lib.matris_env_linear(10, 9, v16, v16, v16, None) == -1001
+    assert lib.matris_env_linear(10, 0, v16, v16, v16, None) == -1001
+    assert lib.matris_env_linear(10, 7, v16, v16, ctypes.c_void_p(8), None) == -1001
+    assert lib.matris_env_linear(0, 7, v16, v16, v16, None) == 0
+    assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 0, v16, None) == -1001
+    assert lib.matris_seg_sum_mul_proj(4, 40, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, v16, None) == -1001
+    assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, None, None) == -1001
+    assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, v16, 9, v16, v16, None) == -1001
+    assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, None, 7, v16, v16, None) == -1001
     assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
     # neighbour-list reuse: no atoms; a workspace below its size; a non-positive cutoff
     big = 1 << 20
