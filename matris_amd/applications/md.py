@@ -21,11 +21,14 @@ methods and run with every per-atom array resident on the device (fp64):
       barostat    cell, x *= 1 - dt beta / (3 tau_P) (P0 - P)        (isotropic, P = -tr(sigma)/3)
                   lattice vector k *= 1 - dt beta / (3 tau_P) (P0 + sigma_kk)   (inhomogeneous)
       with beta = 1 / bulk modulus and sigma the stress including the ideal-gas term
-      -sum m v v^T / V;
+      -sum m v v^T / V (velocities after the thermostat scaling).  The Verlet step that
+      follows a barostat rescaling starts from forces evaluated on the rescaled cell and
+      positions, as ASE's NPTBerendsen.step does (its get_forces after set_cell(...,
+      scale_atoms=True)): two force evaluations per step for these two ensembles;
   Nose-Hoover thermostat with a Parrinello-Rahman barostat in Melchionna's form
   (Melchionna, Ciccotti & Holian, Mol. Phys. 78, 533 (1993)):
       dr/dt = v + eta (r - R_cm)          dv/dt = F/m - (eta + zeta) v
-      dzeta/dt = (2 KE - g k T0) / Q      Q = g k T0 tau_T^2,  g = 3 (N - 1)
+      dzeta/dt = (2 KE - g k T0) / Q      Q = 3 N k T0 tau_T^2,  g = 3 (N - 1)
       deta/dt = V (P - P0 I) / W          W = V0 tau_P^2 B  (B the bulk modulus)
       dh/dt = eta h                       (h: lattice vectors as columns)
   with eta kept lower-triangular in that column convention, so the cell, transformed to
@@ -36,12 +39,17 @@ methods and run with every per-atom array resident on the device (fp64):
   conserves
       H = E_pot + KE + P0 V + W tr(eta^T eta)/2 + Q zeta^2/2 + g k T0 xi,  dxi/dt = zeta
   (conserved_energy()) to O(dt^2).  Without a barostat (ensemble "nvt") eta stays 0.
+  The thermostat mass follows ASE's NPT (its tfact = 2 / (3 N k T0 tau_T^2) with the target
+  kinetic energy 3 (N - 1) k T0 / 2): Q carries 3 N, the target g = 3 (N - 1).
 
 ASE's own NPT integrator is not restated step for step, so trajectories are checked by
 the invariants above, not against ASE (ASE is absent here).  The reference's fallback
 when bulk_modulus is None (an equation-of-state fit whose class is never imported in
 md.py, so it always ends in its `except`: bulk modulus 2 GPa with a warning,
-md.py:193-212) is kept as that warning and 2 GPa.
+md.py:193-212) is kept as that warning and 2 GPa for the two Berendsen barostats.  Its
+Nose-Hoover NPT branch has no such fallback: it multiplies the still-None bulk modulus
+(pfactor = bulk_modulus * GPa, md.py:231-246), a TypeError; here the same case raises a
+ValueError that asks for bulk_modulus.
 
 Each step rebuilds the radius graph and line graph on the GPU (GraphConverter) from the
 current positions and cell and evaluates MatRIS (task "ef", plus "s" for the barostats).
@@ -135,7 +143,7 @@ class Dynamics:
         self.n = n
         self.g = 3 * (n - 1) if n > 1 else 3
         kt0 = KB_EV * self.temperature
-        self.Q = self.g * kt0 * self.taut ** 2
+        self.Q = 3 * n * kt0 * self.taut ** 2  # ASE NPT's tfact = 2 / (3 N k T0 tau_T^2)
         self.zeta = 0.0
         self.xi = 0.0
         self.eta = torch.zeros(3, 3, dtype=pos.dtype, device=pos.device)
@@ -256,6 +264,7 @@ class Dynamics:
         elif k in ("npt_berendsen", "npt_berendsen_inhom"):
             self._berendsen_thermostat()
             self._berendsen_barostat(inhomogeneous=k.endswith("inhom"))
+            self._refresh()  # forces of the rescaled cell and positions (ASE NPTBerendsen.step)
             self._verlet()
         elif k == "nvt_nose_hoover":
             self._nh_step(with_barostat=False)
@@ -337,6 +346,11 @@ class MolecularDynamics:
             taut = 100 * timestep
         if taup is None:
             taup = 1000 * timestep
+        if kind == "npt_nose_hoover" and bulk_modulus is None:
+            # the reference computes pfactor = bulk_modulus * GPa with bulk_modulus None here
+            # (md.py:231-246), a TypeError: its Nose-Hoover NPT needs a bulk modulus
+            raise ValueError("npt with the Nose-Hoover thermostat needs bulk_modulus (GPa): the reference has no "
+                             "fallback for it in this ensemble")
         if kind.startswith("npt") and bulk_modulus is None:
             warnings.warn("bulk_modulus not given: using 2 GPa (the reference's fallback when its equation-of-state "
                           "fit fails); the pressure relaxation time is then only nominal", RuntimeWarning,

@@ -47,8 +47,14 @@ class RadiusGraph:
     def index_signature(self) -> tuple:
         """Identity and version of every index tensor (and the atom count).  Any in-place
         edit bumps a tensor's version counter and assigning a new tensor changes its
-        identity, so a range check remembered under this signature is redone after either."""
-        return tuple((f, id(t), t.data_ptr(), t._version, tuple(t.shape))
+        identity, so a range check remembered under this signature -- and the topology
+        (CSR groupings) that process_graphs keeps per graph under it -- is redone after
+        either.  A storage swapped in through `.data = ...` or `set_()` bumps no version
+        counter; the signature also holds the address of the storage object, which such a
+        swap changes, but an allocator that hands the old addresses back cannot be told
+        apart.  Edit index tensors in place or assign new tensors; do not swap their storage
+        through `.data` or `set_()`."""
+        return tuple((f, id(t), t.data_ptr(), t.untyped_storage()._cdata, t._version, tuple(t.shape))
                      for f in self._INDEX_FIELDS for t in (getattr(self, f),))
 
     def to(self, device: str = "cpu") -> "RadiusGraph":

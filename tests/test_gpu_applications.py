@@ -173,3 +173,13 @@ def test_md_npt_berendsen_moves_the_cell(model, thermostat):
     md.run(5)
     assert np.all(np.isfinite(md.lattice)) and not np.array_equal(md.lattice, lat0)
     assert np.all(np.isfinite(md.get_positions()))
+
+
+def test_md_npt_nose_hoover_needs_a_bulk_modulus(model):
+    """The reference's Nose-Hoover NPT multiplies a None bulk modulus (md.py:231-246); here
+    the same call is a ValueError that names the missing argument."""
+    from matris_amd.applications import MolecularDynamics
+    cr, _ = _cu32(sigma=0.02)
+    with pytest.raises(ValueError, match="bulk_modulus"):
+        MolecularDynamics((cr.frac, cr.lattice, cr.z), model=model, ensemble="npt", thermostat="Nose-Hoover",
+                          temperature=300, timestep=1.0, device="cuda")

@@ -3,12 +3,16 @@ written from the reference modules by tests/golden/make_golden.py).
 
 Tolerances (north star): forces 1e-4 eV/A absolute, stress 1e-4 relative to the largest
 component (GPa), magmoms 1e-4 relative to the largest magnitude, energy 1e-5 relative.
-For the energy the bar is max(1e-5 |e_ref|, 2 |e_ref - e_fp64|): the random-init
-model's energies are small sums with heavy fp32 cancellation, and the reference's own
-fp32 result is 1.2e-5 .. 6.3e-4 (relative) away from the same computation in fp64
-(tests/golden/fp64_oracle.npz, written by tests/golden/make_fp64.py from the CPU
-oracle).  A GPU energy inside that bar is as close to the reference as the reference's
-own fp32 rounding allows; the printed line reports both distances."""
+Every default-arithmetic case asserts the energy at 1e-5 relative to the reference's
+output.  Only the cases listed in FP32_FLOOR_CASES use max(1e-5 |e_ref|,
+2 |e_ref - e_fp64|) instead: the random-init model's energies are small sums with heavy
+fp32 cancellation, the reference's own fp32 result is 1.2e-5 .. 6.3e-4 (relative) away
+from the same computation in fp64 (tests/golden/fp64_oracle.npz, written by
+tests/golden/make_fp64.py from the CPU oracle), and in those cases -- the angle-free
+cell (e = -6.4e-4 eV/atom, measured 6.4e-5 against a floor of 5.9e-4), a batch that
+contains it (1.4e-5), and the bf16x6 fallback arithmetic at C1 (3.7e-5 against a floor
+of 6.3e-4) -- the GPU energy is inside that floor but not inside 1e-5.  The printed line
+reports both distances."""
 import hashlib
 import os
 
@@ -21,6 +25,9 @@ from matris_amd.config import DEFAULT_CONFIG, MATRIS_10M
 pytestmark = pytest.mark.gpu
 
 E_REL, F_ABS, S_REL, M_REL = 1e-5, 1e-4, 1e-4, 1e-4
+# the only cases whose energy is held to the reference's fp32-vs-fp64 floor (docstring)
+FP32_FLOOR_CASES = ("C1 bf16x6", "empty line graph (converter)", "empty line graph (reference arrays)",
+                    "mixed batch with an angle-free cell")
 
 
 def _model(cfg=MATRIS_10M, seed=0):
@@ -56,8 +63,9 @@ def _efsm(model, graphs):
 def _assert_close(out, ref, tag, ref64=None):
     e_ref = np.asarray(ref["e"], np.float64)
     e_bar = E_REL * np.abs(e_ref)
-    if ref64 is not None:
+    if ref64 is not None and tag in FP32_FLOOR_CASES:
         e_bar = np.maximum(e_bar, 2.0 * np.abs(e_ref - ref64["e"]))
+    if ref64 is not None:
         e64_err = np.max(np.abs(out["e"] - ref64["e"]) / np.abs(ref64["e"]))
         print(f"{tag}: e_rel_vs_fp64={e64_err:.2e} ref_fp32_vs_fp64="
               f"{np.max(np.abs(e_ref - ref64['e']) / np.abs(ref64['e'])):.2e}", flush=True)

@@ -65,6 +65,21 @@ def test_edit_after_a_passed_check_is_checked_again(how):
     assert "indices_checked" not in g.meta
 
 
+def test_storage_swap_changes_the_signature():
+    """A storage swapped in through set_() bumps no version counter; the signature still
+    changes (it holds the storage object's address), so the range check and the kept
+    topology are redone."""
+    g = _graph()
+    validate_graph_indices(g)
+    sig = g.index_signature()
+    lg = g.line_graph.clone()
+    lg[3, 1] = len(g.undirected2directed) + 7
+    g.line_graph.set_(lg)
+    assert g.index_signature() != sig
+    with pytest.raises(ValueError, match="outside its range"):
+        process_graphs([g])
+
+
 def test_unchanged_graph_is_not_checked_twice(monkeypatch):
     """The remembered check holds while no index tensor changes (one host read per graph)."""
     g = _graph()

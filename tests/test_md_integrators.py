@@ -203,3 +203,69 @@ def test_upper_triangular_basis_keeps_cell_parameters():
         gram = lambda c: (c @ c.T) / np.outer(np.linalg.norm(c, axis=1), np.linalg.norm(c, axis=1))
         assert np.allclose(gram(new), gram(cell))
         assert math.isclose(abs(np.linalg.det(new)), abs(np.linalg.det(cell)), rel_tol=1e-12)
+
+
+def _berendsen_npt_step_restated(pos, vel, m, cell, dt, T0, taut, taup, bulk, P0, inhom, mask=(1.0, 1.0, 1.0)):
+    """One ASE NPTBerendsen / Inhomogeneous_NPTBerendsen step written out in order:
+    thermostat scaling, barostat rescaling of the cell with the atoms carried in fractional
+    coordinates (stress with the ideal-gas term of the scaled velocities), forces of the
+    rescaled geometry, then velocity Verlet."""
+    n = pos.shape[0]
+    ke = 0.5 * float((m[:, None] * vel * vel).sum()) * AMU_A2_FS2_EV
+    t_now = 2.0 * ke / (3.0 * n * KB_EV)
+    lam = min(max(math.sqrt(1.0 + dt / taut * (T0 / t_now - 1.0)), 0.9), 1.1)
+    vel = vel * lam
+    _, stress, _ = evaluate(pos, cell, True)
+    vol = abs(float(torch.linalg.det(cell)))
+    sigma = stress - (m[:, None] * vel).t() @ vel * AMU_A2_FS2_EV / vol
+    k = dt / (3.0 * taup * bulk)
+    frac = pos @ torch.linalg.inv(cell)
+    if inhom:
+        f = 1.0 - k * (P0 + torch.diagonal(sigma)) * torch.tensor(mask, dtype=torch.float64)
+        cell = cell * f[:, None]
+    else:
+        cell = cell * (1.0 - k * (P0 + float(torch.trace(sigma)) / 3.0))
+    pos = frac @ cell
+    forces, _, _ = evaluate(pos, cell, True)
+    acc = forces / m[:, None] / AMU_A2_FS2_EV
+    vel = vel + 0.5 * dt * acc
+    pos = pos + dt * vel
+    forces, _, _ = evaluate(pos, cell, True)
+    vel = vel + 0.5 * dt * forces / m[:, None] / AMU_A2_FS2_EV
+    return pos, vel, cell
+
+
+@pytest.mark.parametrize("kind", ["npt_berendsen", "npt_berendsen_inhom"])
+def test_berendsen_npt_one_step_matches_the_restated_update(kind):
+    """One Berendsen NPT step of Dynamics equals the ASE step order restated above: the
+    Verlet half-kick uses forces of the rescaled cell (not those of the previous step), and
+    the barostat's stress carries the ideal-gas term of the thermostat-scaled velocities."""
+    pos, cell = fcc(a=3.55, jitter=0.03)
+    cell = cell @ torch.tensor([[1.0, 0.0, 0.0], [0.0, 1.03, 0.0], [0.0, 0.0, 0.98]], dtype=torch.float64)
+    pos = pos @ torch.tensor([[1.0, 0.0, 0.0], [0.0, 1.03, 0.0], [0.0, 0.0, 0.98]], dtype=torch.float64)
+    dyn = make(kind, dt=2.0, T=350.0, pos_cell=(pos, cell), taut=15.0, taup=40.0, bulk_modulus_gpa=30.0,
+               pressure_gpa=0.3)
+    gpa = 1.0 / 160.21766208
+    p0, v0, c0 = dyn.pos.clone(), dyn.vel.clone(), dyn.cell.clone()
+    ref_pos, ref_vel, ref_cell = _berendsen_npt_step_restated(p0, v0, dyn.masses, c0, 2.0, 350.0, 15.0, 40.0,
+                                                              30.0 * gpa, 0.3 * gpa, kind.endswith("inhom"))
+    dyn.step()
+    assert torch.allclose(dyn.cell, ref_cell, rtol=0, atol=1e-12)
+    assert torch.allclose(dyn.pos, ref_pos, rtol=0, atol=1e-11)
+    assert torch.allclose(dyn.vel, ref_vel, rtol=0, atol=1e-13)
+    # the old order (the previous step's forces for the first half-kick) differs measurably
+    assert float((dyn.cell - c0).abs().max()) > 1e-5
+
+
+def test_nose_hoover_thermostat_rate_follows_ase_npt():
+    """The friction's rate dzeta/dt = (2 KE - 3 (N - 1) k T0) / (3 N k T0 tau^2), written
+    the way ASE's NPT integrator states it: tfact (KE - 1.5 (N - 1) k T0) with tfact =
+    2 / (3 N k T0 tau^2)."""
+    dyn = make("nvt_nose_hoover", dt=1.0, T=300.0, taut=25.0)
+    n = dyn.n
+    kt0 = KB_EV * 300.0
+    tfact = 2.0 / (3 * n * kt0 * 25.0 ** 2)
+    ke = dyn.kinetic_energy()
+    z0 = dyn.zeta
+    dyn._nh_half(with_barostat=False)
+    assert math.isclose(dyn.zeta - z0, 0.5 * tfact * (ke - 1.5 * (n - 1) * kt0), rel_tol=1e-12, abs_tol=1e-18)
