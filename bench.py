@@ -12,14 +12,23 @@ region.
 `c5_md`: the 32,000-atom a-SiO2 cell (C5) under NVT Berendsen MD (300 K, dt 1 fs,
 tau 100 fs); every step rebuilds the radius and line graphs on the GPU from the new
 positions and evaluates efs (forces for the integrator); interaction blocks are
-checkpointed (the cell's activations exceed HBM otherwise).  A bounded number of steps.
+checkpointed as far as the cell's activations exceed HBM.  40 of the config's 200 steps
+by default (--c5-steps), after 2 warm-up steps.
 
 `c4_batch`: the 64 random triclinic cells of C4 (8-64 atoms each) as one disjoint batch,
 efsm, graphs built on the GPU once.
 
 `c2_line_attn`: the standalone line-attention core (forward, backward) and the
 angle->bond segment sum on the C2 graph (4096-atom random packing) with N(0,1) features,
-against HBM peak.  Prints one JSON line.
+against HBM peak.
+
+`roofline`: the dominant GatedMLP family (the most kernel time per step) against the MFMA
+roofline of the arithmetic in use, its HBM figure alongside (`hbm`: the layer's inputs
+and outputs, the saved pre-activations apart); `roofline_<other>`: the other direction;
+`roofline_line_attn`: the line-attention forward against HBM; `hbm_in_model`: the HBM
+fractions of the segment-sum, envelope-aggregation and line-attention families inside
+the C3 step; `fp32_mfma`: the same C3 step with every GEMM in plain fp32 MFMA products.
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -58,13 +67,14 @@ def _parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="C3", choices=["C3"])
-    ap.add_argument("--c5-steps", type=int, default=5, help="timed C5 MD steps (after --c5-warmup)")
+    ap.add_argument("--c5-steps", type=int, default=40, help="timed C5 MD steps (after --c5-warmup)")
     ap.add_argument("--c5-warmup", type=int, default=2)
     ap.add_argument("--no-c5", action="store_true")
     ap.add_argument("--no-c2", action="store_true")
     ap.add_argument("--no-c4", action="store_true")
     ap.add_argument("--c5-only", action="store_true", help="run only the C5 MD line (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fp32-mfma", action="store_true", help="skip the plain fp32 MFMA (MODE 0) C3 step time")
     ap.add_argument("--cpu-sample-reps", type=int, default=6,
                     help="fcc reps of the CPU baseline sample (6: the C3 cell itself)")
     ap.add_argument("--cpu-steps", type=int, default=2, help="timed CPU baseline steps (after one warm-up)")
@@ -76,11 +86,12 @@ def _parse():
 
 
 def _kernel_stats(timing):
-    """Per kernel name: launches, mean duration (s) and the info tuples."""
+    """Per kernel name: launches, mean duration (s), each launch's duration (ms) and the
+    info records."""
     out = {}
     for name, evs in timing.items():
         ms = [a.elapsed_time(b) for a, b, _ in evs]
-        out[name] = dict(n=len(ms), mean_s=sum(ms) / len(ms) / 1e3, info=[i for _, _, i in evs])
+        out[name] = dict(n=len(ms), mean_s=sum(ms) / len(ms) / 1e3, ms=ms, info=[i for _, _, i in evs])
     return out
 
 
@@ -421,19 +432,23 @@ def main():
     mode_idx, mma_peak, peak_note, dtype = MMA_ROOF[ops.get_mma_precision()]
 
     def gmlp_roof(name, st, n_steps, where):
-        """The GatedMLP family against the roofline that binds it: its algorithmic FLOPs per
-        algorithmic byte lie below the machine balance (split-MFMA peak / HBM peak), so
-        the bound is HBM and `achieved` is bytes per second; the MFMA figures ride along."""
+        """The GatedMLP family against the MFMA roofline, the bound SURVEY's measurement
+        plan gives the GEMMs (kept fixed): achieved = algorithmic fp32-product FLOPs per
+        launch / mean launch time, against the split-product peak of the arithmetic in use.
+        The HBM figure rides along under `hbm`, its bytes the layer's inputs and outputs
+        only (the pre-activations the build saves for its backward, p / z and the FFN's,
+        are counted apart)."""
         gm = st.get(name)
         if not gm:
             return None
-        flops = sum(_gmlp_flops(i[0], i[1], i[3] if len(i) > 3 else 0) for i in gm["info"]) / gm["n"]
-        byts = sum(i[2] for i in gm["info"]) / gm["n"]
+        info = gm["info"]
+        flops = sum(_gmlp_flops(i["rows"], i["k"], i["extra_rows"]) for i in info) / gm["n"]
+        byts_all = sum(i["bytes"] for i in info) / gm["n"]
+        saved = sum(i["saved_bytes"] for i in info) / gm["n"]
+        byts = byts_all - saved
         tf = flops / gm["mean_s"] / 1e12
         gbs = byts / gm["mean_s"] / 1e9
-        n_line = sum(1 for i in gm["info"] if i[0] == A)
-        intensity, balance = flops / byts, mma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
-        traffic = TRAFFIC_BYTES.get((name, "C3"))
+        n_line = sum(1 for i in info if i["rows"] == A)
         # every instance of the family: the Refinements' launches carry the FFN (forward tail /
         # backward head), the line attention's the logit projection pair (forward tail /
         # backward epilogue); MODE 6 runs the four-wave backward without a head or epilogue
@@ -442,28 +457,59 @@ def main():
         else:
             kname = f"gmlp_bwd_kernel<{mode_idx}>" if mode_idx == 6 else \
                 f"gmlp_bwd8_kernel<{mode_idx}, *, *>"
-        common = dict(kernel=kname, mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"],
-                      flops_per_launch=round(flops), bytes_per_launch=round(byts),
-                      flop_per_byte=round(intensity, 1), machine_balance_flop_per_byte=round(balance, 1),
-                      mfma_achieved_tflops=round(tf, 2), mfma_peak_tflops=round(mma_peak, 1),
-                      mfma_frac=round(tf / mma_peak, 4), frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-                      note=f"means over {gm['n']} launches in {n_steps} steps of the {where} ({n_line} with "
-                           f"M=A={A}); "
-                           f"bytes: every input table read once (gathered sources as whole tables, projected "
-                           f"sources as their product tables), outputs, saved p/z and gradients written once; "
-                           f"FLOPs 2*M*(256K+32768) with K the layer-1 width the kernel multiplies (+2*M*32768 "
-                           f"for the launches that carry a Refinement's FFN or the line attention's pair projection); MFMA peak = "
-                           f"{peak_note}")
-        if intensity < balance:
-            return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=round(gbs / HBM_PEAK_GBS, 4), traffic=traffic, **common)
+        hbm = dict(achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                   bytes_per_launch=round(byts), saved_bytes_per_launch=round(saved),
+                   achieved_with_saved=round(byts_all / gm["mean_s"] / 1e9, 1),
+                   note="bytes: the layer's inputs (gathered sources as whole tables, projected sources as their "
+                        "product tables, int32 indices, residual and gradient rows) read once and its outputs "
+                        "written once; the saved pre-activations (p, z, the FFN's) apart, in "
+                        "saved_bytes_per_launch and achieved_with_saved")
         return dict(bound="mfma", achieved=round(tf, 2), peak=round(mma_peak, 1), unit="TFLOP/s",
-                    frac=round(tf / mma_peak, 4), traffic=traffic, **common)
+                    frac=round(tf / mma_peak, 4), traffic=TRAFFIC_BYTES.get((name, "C3")), kernel=kname,
+                    mean_us=round(gm["mean_s"] * 1e6, 2), launches=gm["n"], flops_per_launch=round(flops),
+                    frac_of_fp32_mfma_peak=round(tf / FP32_MFMA_PEAK_TFLOPS, 4), hbm=hbm,
+                    note=f"means over {gm['n']} launches in {n_steps} steps of the {where} ({n_line} with "
+                         f"M=A={A}); FLOPs 2*M*(256K+32768) with K the layer-1 width the kernel multiplies "
+                         f"(+2*M*32768 for the launches that carry a Refinement's FFN or the line attention's "
+                         f"pair projection), fp32 products; peak = {peak_note}")
+
+    def inmodel_hbm(st, n_steps):
+        """In-model HBM fractions of the reduction and attention families from the breakdown
+        pass: algorithmic bytes (the byte formulas of the measurement plan: every input
+        element read once, every output written once, int32 indices; saved statistics apart)
+        summed over the family's launches / their summed duration; the angle-row (M = A)
+        launches also on their own."""
+        out = {}
+        for fam in ("seg_sum", "env_agg_fwd", "env_agg_bwd", "attn_fwd_line", "attn_bwd_line"):
+            v = st.get(fam)
+            if not v:
+                continue
+            ms = v["ms"]
+            info = v["info"]
+            rows = [(i, t) for i, t in zip(info, ms) if isinstance(i, dict) and "bytes" in i]
+            if not rows:
+                continue
+
+            def frac(sel):
+                b = sum(i["bytes"] - i.get("saved_bytes", 0) for i, _ in sel)
+                t = sum(t for _, t in sel) / 1e3
+                gbs = b / t / 1e9
+                return dict(achieved=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4), launches=len(sel),
+                            bytes_per_step=round(b / n_steps), ms_per_step=round(t * 1e3 / n_steps, 3))
+            out[fam] = dict(all=frac(rows))
+            line = [(i, t) for i, t in rows if i.get("rows") == A]
+            if line and len(line) != len(rows):
+                out[fam]["angle_rows"] = frac(line)
+        return dict(unit="GB/s", peak=HBM_PEAK_GBS, families=out,
+                    note=f"HIP events around every launch of a {n_brk}-step breakdown pass (the event pair adds "
+                         f"~1-2 us to each launch, so short launches read low)")
+
     other = "gmlp_fwd" if dom == "gmlp_bwd" else "gmlp_bwd"
     roof = gmlp_roof(dom, stats, args.steps, "timed region")
     r_other = gmlp_roof(other, stats_all, n_brk, "breakdown pass")
     at = stats_all.get("attn_fwd_line")
     attn = None
+    hbm_inmodel = inmodel_hbm(stats_all, n_brk)
     if at:
         byts = _attn_line_bytes(A, E_u)
         gbs = byts / at["mean_s"] / 1e9
@@ -474,6 +520,24 @@ def main():
                     note=f"means over {at['n']} launches in {n_brk} steps of the breakdown pass")
     kern = {k: dict(launches=v["n"], mean_us=round(v["mean_s"] * 1e6, 2),
                     total_ms_per_step=round(v["mean_s"] * v["n"] * 1e3 / n_brk, 3)) for k, v in stats_all.items()}
+
+    # the same step in plain fp32 MFMA products (MODE 0, v_mfma_f32_32x32x2f32) beside `value`
+    fp32_mfma = None
+    if not args.no_fp32_mfma:
+        with ops.mma_precision("fp32"):
+            for _ in range(2):
+                model([g], task="efsm")
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            n32 = max(3, args.steps // 2)
+            for _ in range(n32):
+                model([g], task="efsm")
+            torch.cuda.synchronize()
+            dt32 = time.perf_counter() - t2
+        fp32_mfma = dict(value=round(n_atoms * n32 / dt32, 2), unit="atom*steps/s",
+                         ms_per_step=round(dt32 / n32 * 1e3, 3), steps=n32, warmup=2,
+                         note="C3 efsm with every GEMM in plain fp32 MFMA products (mma_precision('fp32'), "
+                              "v_mfma_f32_32x32x2f32) instead of the default f16x3 split")
 
     line = {
         "metric": "atom*steps/s (efsm fwd+autograd bwd), MatRIS-10M, 864-atom fcc Cu (C3)",
@@ -499,6 +563,8 @@ def main():
         "roofline": roof,
         f"roofline_{other}": r_other,
         "roofline_line_attn": attn,
+        "hbm_in_model": hbm_inmodel,
+        "fp32_mfma": fp32_mfma,
         "kernels": kern,
         "kernels_note": f"per-launch HIP event timing of every kernel family over {n_brk} steps of a breakdown "
                         f"pass before the timed region (ms per step); inside the timed region only {dom} carries "

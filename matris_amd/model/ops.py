@@ -192,6 +192,13 @@ class Grouping:
 # ------------------------------------------------------------------------------------
 # segment sum / gather
 # ------------------------------------------------------------------------------------
+def _seg_src_bytes(grp: "Grouping", rows_read: int | None = None) -> int:
+    """Algorithmic bytes of one summed source: its 128-wide rows read once (rows_read of
+    them; all of the grouping's rows by default), its int32 permutation and row pointers."""
+    r = grp.n_rows if rows_read is None else rows_read
+    return 4 * D * r + (4 * grp.n_rows if grp.perm is not None else 0) + 4 * (grp.n_seg + 1)
+
+
 def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D, col_off: int = 0,
                 out: torch.Tensor | None = None, accumulate: bool = False, second=None, base=None,
                 tile_rows: int = 0) -> torch.Tensor:
@@ -213,16 +220,24 @@ def seg_sum_raw(x: torch.Tensor, grp: Grouping, scale: float = 1.0, ldx: int = D
         args2 = (_p(x2), ld2, off2, _p(g2.rowptr), _p(g2.perm), s2)
     else:
         args2 = (None, D, 0, None, None, 0.0)
+    # algorithmic bytes: each source's rows (a tile-run source: one partial row per tile and
+    # segment start), indices and row pointers; out written (and read when accumulated);
+    # the base term's rows and weights
+    out_b = 4 * D * grp.n_seg * (2 if accumulate else 1)
+    b2 = _seg_src_bytes(second[1]) if second is not None else 0
     if tile_rows:
         if grp.perm is not None or base is not None:
             raise ValueError("seg_sum_raw: tile-run partials need rows ascending by segment and no base term")
-        with _timed("seg_sum", (grp.n_rows, grp.n_seg, "runs")):
+        nb = _seg_src_bytes(grp, min(grp.n_rows, grp.n_seg + -(-grp.n_rows // int(tile_rows)))) + b2 + out_b
+        with _timed("seg_sum", dict(rows=grp.n_rows, segs=grp.n_seg, kind="runs", bytes=nb)):
             _lib.check(lib.matris_seg_sum2_runs(grp.n_seg, rows, _p(x), ldx, col_off, _p(grp.rowptr), int(tile_rows),
                                                 scale, *args2, int(accumulate), _p(out), _stream()),
                        "matris_seg_sum2_runs")
         return out
     bx, bw = base if base is not None else (None, None)
-    with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
+    nb = _seg_src_bytes(grp) + b2 + out_b + (4 * D * (grp.n_seg + 1) if base is not None else 0)
+    with _timed("seg_sum", dict(rows=grp.n_rows, segs=grp.n_seg, kind="perm" if grp.perm is not None else "sorted",
+                                bytes=nb)):
         _lib.check(lib.matris_seg_sum2(grp.n_seg, rows, _p(x), ldx, col_off, _p(grp.rowptr), _p(grp.perm), scale,
                                        *args2, int(accumulate), _p(bx), _p(bw), _p(out), _stream()),
                    "matris_seg_sum2")
@@ -243,7 +258,8 @@ def seg_sum_mul_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: 
     lib = _lib.load()
     if out is None:
         out = _rows(grp.n_seg, D, x.device)
-    with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
+    nb = _seg_src_bytes(grp) + 4 * D * mul.shape[0] + 4 * grp.n_rows + 4 * D * grp.n_seg * (2 if accumulate else 1)
+    with _timed("seg_sum", dict(rows=grp.n_rows, segs=grp.n_seg, kind="mul", bytes=nb)):
         _lib.check(lib.matris_seg_sum_mul(grp.n_seg, grp.n_rows, _p(x), D, 0, _p(grp.rowptr), _p(grp.perm), _p(mul),
                                           _p(mul_idx), 1.0, int(accumulate), _p(out), _stream()),
                    "matris_seg_sum_mul")
@@ -258,7 +274,8 @@ def seg_sum_mul_proj_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_
     lib = _lib.load()
     wt = _f32c(proj_wt)
     out = torch.empty(grp.n_seg, wt.shape[0], dtype=torch.float32, device=x.device)
-    with _timed("seg_sum", (grp.n_rows, grp.n_seg, grp.perm is not None)):
+    nb = _seg_src_bytes(grp) + 4 * D * mul.shape[0] + 4 * grp.n_rows + 4 * wt.shape[0] * grp.n_seg
+    with _timed("seg_sum", dict(rows=grp.n_rows, segs=grp.n_seg, kind="mul_proj", bytes=nb)):
         _lib.check(lib.matris_seg_sum_mul_proj(grp.n_seg, grp.n_rows, _p(x), D, 0, _p(grp.rowptr), _p(grp.perm),
                                                _p(mul), _p(mul_idx), 1.0, _p(wt), wt.shape[0], _p(out), _stream()),
                    "matris_seg_sum_mul_proj")
@@ -414,7 +431,14 @@ def attn_fwd_raw(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: G
     y_t, y_s = _rows(S, D, dev), _rows(S, D, dev)
     lse_t, lse_s = _rows(S, D, dev), _rows(S, D, dev)
     aidx = alpha_grp.key if alpha_grp is not None else None
-    with _timed("attn_fwd_atom" if aidx is not None else "attn_fwd_line", (R, S, src.perm is not None)):
+    # algorithmic bytes (in: alpha_t, alpha_s (whole tables when gathered), e; out: y_t, y_s;
+    # int32 permutation / alpha index and two row-pointer arrays); lse_t / lse_s are saved
+    # statistics, counted apart
+    n_alpha = alpha_t.shape[0]
+    nb = 4 * D * (2 * n_alpha + R + 2 * S) + (4 * R if src.perm is not None else 0) + \
+        (4 * R if aidx is not None else 0) + 8 * (S + 1)
+    with _timed("attn_fwd_atom" if aidx is not None else "attn_fwd_line",
+                dict(rows=R, segs=S, bytes=nb, saved_bytes=2 * 4 * D * S)):
         _lib.check(lib.matris_attn_fwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(aidx), _p(e), _p(tgt.rowptr),
                                        _p(tgt.perm), _p(src.rowptr), _p(src.perm), _p(y_t), _p(y_s), _p(lse_t),
                                        _p(lse_s), _stream()), "matris_attn_fwd")
@@ -430,7 +454,13 @@ def attn_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: G
     dev = e.device
     g_at, g_as, g_e = (_rows(R, D, dev) for _ in range(3))
     ag = alpha_grp
-    with _timed("attn_bwd_atom" if ag is not None else "attn_bwd_line", (R, S)):
+    # algorithmic bytes (in: alpha_t, alpha_s, e [R], g_yt, g_ys [S], the fused base term
+    # [R]; out: g_alpha_t, g_alpha_s, g_e [R]; target and source keys); y_t, y_s, lse_t,
+    # lse_s are saved statistics, counted apart
+    nb = 4 * D * (6 * R + 2 * S) + (4 * D * R if g_e_base is not None else 0) + 8 * R + \
+        (4 * R if ag is not None else 0)
+    with _timed("attn_bwd_atom" if ag is not None else "attn_bwd_line",
+                dict(rows=R, segs=S, bytes=nb, saved_bytes=4 * 4 * D * S)):
         _lib.check(lib.matris_attn_bwd(R, S, _p(alpha_t), _p(alpha_s), D, _p(ag.key if ag is not None else None),
                                        _p(e), _p(tgt.key), _p(src.key), _p(y_t), _p(y_s), _p(lse_t), _p(lse_s),
                                        _p(g_yt), _p(g_ys), ldgy, _p(g_at), _p(g_as), _p(g_e), _p(g_e_base),
@@ -448,7 +478,7 @@ def attn_bwd_bond_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, t
     if alpha_t.shape[0] != U or tgt.key.numel() != R or src.key.numel() != R:
         raise ValueError("attn_bwd_bond_raw: logits per bond, one target / source per directed row")
     g_at, g_as, g_e = _rows(U, D, dev), _rows(U, D, dev), _rows(R, D, dev)
-    with _timed("attn_bwd_atom", (R, tgt.n_seg)):
+    with _timed("attn_bwd_atom", dict(rows=R, segs=tgt.n_seg)):
         _lib.check(lib.matris_attn_bwd_bond(U, _p(alpha_t), _p(alpha_s), D, _p(e), _p(d2u.rowptr), _p(d2u.perm),
                                             _p(tgt.key), _p(src.key), _p(y_t), _p(y_s), _p(lse_t), _p(lse_s),
                                             _p(g_yt), _p(g_ys), ldgy, _p(g_base), float(base_scale), _p(g_at),
@@ -494,7 +524,9 @@ def env_agg_fwd_raw(h, env, tgt: Grouping, src: Grouping):
     lib = _lib.load()
     E = env.shape[0]
     agg, S = _rows(E, D, h.device), _rows(E, D, h.device)
-    with _timed("env_agg_fwd", (h.shape[0], E)):
+    A = h.shape[0]
+    with _timed("env_agg_fwd", dict(rows=A, segs=E, bytes=4 * D * (A + 2 * E) + 4 * A + 4 * (E + 1),
+                                    saved_bytes=4 * D * E)):
         _lib.check(lib.matris_env_agg_fwd(E, _p(h), _p(env), _p(tgt.rowptr), _p(tgt.perm), _p(src.key), _p(S),
                                           _p(agg), _stream()), "matris_env_agg_fwd")
     return agg, S
@@ -511,13 +543,19 @@ def env_agg_bwd_env_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, proj_wt=
     if proj_wt is not None:
         wt = _f32c(proj_wt)
         g_basis = torch.empty(E, wt.shape[0], dtype=torch.float32, device=h.device)
-        with _timed("env_agg_bwd", (h.shape[0], E)):
+        A = h.shape[0]
+        # in: h [A], env, g_agg, S [E] (S saved), target keys, source permutation and pointers;
+        # out: g_basis [E, K], g_agg * env [E]
+        nb = 4 * D * (A + 3 * E) + 4 * D * E + 4 * wt.shape[0] * E + 8 * A + 4 * (E + 1)
+        with _timed("env_agg_bwd", dict(rows=A, segs=E, bytes=nb, saved_bytes=4 * D * E)):
             _lib.check(lib.matris_env_agg_bwd_env_proj(E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key),
                                                        _p(src.rowptr), _p(src.perm), _p(wt), wt.shape[0],
                                                        _p(g_basis), _p(ge), _stream()), "matris_env_agg_bwd_env_proj")
         return g_basis, ge
     g_env = _rows(E, D, h.device)
-    with _timed("env_agg_bwd", (h.shape[0], E)):
+    A = h.shape[0]
+    nb = 4 * D * (A + 3 * E) + 2 * 4 * D * E + 8 * A + 4 * (E + 1)
+    with _timed("env_agg_bwd", dict(rows=A, segs=E, bytes=nb, saved_bytes=4 * D * E)):
         _lib.check(lib.matris_env_agg_bwd_env(E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key), _p(src.rowptr),
                                               _p(src.perm), _p(g_env), _p(ge), _stream()), "matris_env_agg_bwd_env")
     return g_env, ge
@@ -542,7 +580,9 @@ def env_agg_bwd_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, g_h, accumul
     lib = _lib.load()
     E = env.shape[0]
     g_env = _rows(E, D, h.device)
-    with _timed("env_agg_bwd", (h.shape[0], E)):
+    A = h.shape[0]
+    nb = 4 * D * (A + 3 * E) + 4 * D * E + 4 * D * A * (2 if accumulate else 1) + 12 * A + 4 * (E + 1)
+    with _timed("env_agg_bwd", dict(rows=A, segs=E, bytes=nb, saved_bytes=4 * D * E)):
         _lib.check(lib.matris_env_agg_bwd(h.shape[0], E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key), _p(src.key),
                                           _p(src.rowptr), _p(src.perm), int(accumulate), _p(g_h), _p(g_env),
                                           _stream()), "matris_env_agg_bwd")
@@ -789,8 +829,9 @@ def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: boo
     if not proj and tail is None and pair is None:
         src_arr = (ctypes.c_void_p * 4)(*[s.data_ptr() for s in srcs])
         idx_arr = (ctypes.c_void_p * 4)(*[(i.data_ptr() if i is not None else None) for i in idxs])
-        with _timed("gmlp_fwd", (n_rows, nsrc * D, _gmlp_fwd_bytes(srcs, idxs, n_rows, p is not None,
-                                                                    res is not None), 0)):
+        with _timed("gmlp_fwd", dict(rows=n_rows, k=nsrc * D, extra_rows=0,
+                                     bytes=_gmlp_fwd_bytes(srcs, idxs, n_rows, p is not None, res is not None),
+                                     saved_bytes=2 * 4 * 256 * n_rows if p is not None else 0)):
             _lib.check(lib.matris_gmlp_fwd(n_rows, nsrc, src_arr, idx_arr, _p(pack.b("w1", mode)), _p(pack.b1),
                                            _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc), _p(pack.ng), pack.eps,
                                            _p(out), _p(p), _p(z), _p(rs), _p(rw), _p(res_out), mode, _stream()),
@@ -825,9 +866,13 @@ def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: boo
     ptab = [(keep[k].shape[0], keep[k].shape[1], len(b)) for k, b in enumerate(tables.values())]
     nbytes = _gmlp_fwd_bytes([srcs[j] for j in rest], [idxs[j] for j in rest], n_rows, p is not None,
                              res is not None, ptab) + t_bytes
-    # K: the layer-1 width this kernel multiplies; the last field: rows of the FFN tail or the
-    # projection pair (both add 2 * 128 * 256 FLOPs per row)
-    with _timed("gmlp_fwd", (n_rows, len(rest) * D, nbytes, n_rows if (tail is not None or pair is not None) else 0)):
+    # k: the layer-1 width this kernel multiplies; extra_rows: rows of the FFN tail or the
+    # projection pair (both add 2 * 128 * 256 FLOPs per row); saved_bytes: the pre-activations
+    # written only for the backward (p, z and the tail's t), inside bytes
+    saved = (2 * 4 * 256 * n_rows if p is not None else 0) + (4 * D * n_rows if t_p is not None and tail is not None
+                                                                else 0)
+    with _timed("gmlp_fwd", dict(rows=n_rows, k=len(rest) * D, bytes=nbytes, saved_bytes=saved,
+                                 extra_rows=n_rows if (tail is not None or pair is not None) else 0)):
         if pair is not None:
             _lib.check(lib.matris_gmlp_fwd_pair(n_rows, len(rest), src_arr, idx_arr, n_pj, pj_arr, pji_arr, pld_arr,
                                                 w1, _p(pack.b1), _p(pack.b("w2", mode)), _p(pack.b2), _p(pack.nc),
@@ -881,13 +926,13 @@ def gmlp_bwd_raw(pack: GmlpPack, g, p, z, K: int, mode: int, g_x=None, g_x0=None
                 raise ValueError("gmlp_bwd_raw: pair gradients must be contiguous [M, 128] tensors")
         nbytes += 2 * 4 * D * M
         key, blk = runs if runs is not None else (None, -1)
-        with _timed("gmlp_bwd", (M, K, nbytes, M)):  # the last field: rows of the pair projection
+        with _timed("gmlp_bwd", dict(rows=M, k=K, bytes=nbytes, saved_bytes=2 * 4 * 256 * M, extra_rows=M)):
             _lib.check(lib.matris_gmlp_bwd_pair(M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)),
                                                 _p(pack.b("w2bt", mode)), _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x),
                                                 _p(g_x0), _p(res_w), _p(res_src), _p(key), int(blk), _p(g0), _p(g1),
                                                 _p(pp.b("cat_t", mode)), mode, _stream()), "matris_gmlp_bwd_pair")
         return g_x
-    with _timed("gmlp_bwd", (M, K, nbytes)):
+    with _timed("gmlp_bwd", dict(rows=M, k=K, bytes=nbytes, saved_bytes=2 * 4 * 256 * M, extra_rows=0)):
         args = (M, K, _p(g), _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)), _p(pack.nc),
                 _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), int(acc0), _p(res_w))
         if runs is None and res_src is None:
@@ -938,7 +983,8 @@ def gmlp_bwd_ffn_raw(pack: GmlpPack, p, z, K: int, mode: int, ffn: "_WeightPack"
         if key.dtype != torch.int32 or key.numel() != M or not key.is_contiguous():
             raise ValueError("gmlp_bwd_ffn_raw: runs key must be a contiguous int32 tensor of one entry per row")
         nbytes += 4 * M - 4 * D * M + 4 * D * -(-M // gmlp_tile_rows())
-    with _timed("gmlp_bwd", (M, K, nbytes, M)):  # the last field: rows of the FFN head
+    # extra_rows: rows of the FFN head; saved_bytes: p, z and the FFN's pre-activation read
+    with _timed("gmlp_bwd", dict(rows=M, k=K, bytes=nbytes, saved_bytes=4 * M * (2 * 256 + D), extra_rows=M)):
         _lib.check(lib.matris_gmlp_bwd_ffn(M, K, _p(p), _p(z), _p(pack.b("w1t", mode)), _p(pack.b("w2bt", mode)),
                                            _p(pack.nc), _p(pack.ng), pack.eps, _p(g_x), _p(g_x0), _p(res_w),
                                            _p(key), int(blk), _p(ffn_g), _p(ffn_g_idx), float(ffn_g_scale),
