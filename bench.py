@@ -18,6 +18,10 @@ by default (--c5-steps), after 2 warm-up steps.
 `c4_batch`: the 64 random triclinic cells of C4 (8-64 atoms each) as one disjoint batch,
 efsm, graphs built on the GPU once.
 
+`captured` (C3, and inside `c4_batch`): the same evaluation replayed from a captured HIP
+graph (MatRIS.capture, opt-in for graphs whose index arrays stay fixed), one status read
+per replay.  `value` stays the eager rate.
+
 `c2_line_attn`: the standalone line-attention core (forward, backward) and the
 angle->bond segment sum on the C2 graph (4096-atom random packing) with N(0,1) features,
 against HBM peak.
@@ -85,6 +89,26 @@ def _parse():
     return ap.parse_args()
 
 
+def _captured_rate(model, graphs, n_atoms, steps, warmup):
+    """atom*steps/s of MatRIS.capture(graphs) replays (each with its status read), over
+    `steps` replays after `warmup`; the eager `value` stays the headline figure."""
+    import torch
+    cap = model.capture(graphs, task="efsm")
+    for _ in range(warmup):
+        cap.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        cap.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    del cap
+    return dict(value=round(n_atoms * steps / dt, 2), unit="atom*steps/s", ms_per_step=round(dt / steps * 1e3, 3),
+                steps=steps, warmup=warmup,
+                note="opt-in HIP graph of the whole evaluation (MatRIS.capture): one replay and one status "
+                     "read per step, for graphs whose index arrays stay fixed")
+
+
 def _kernel_stats(timing):
     """Per kernel name: launches, mean duration (s), each launch's duration (ms) and the
     info records."""
@@ -144,8 +168,10 @@ def c4_batch(model, dev, steps: int, warmup: int):
         model(graphs, task="efsm")
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    captured = _captured_rate(model, graphs, n, steps, warmup)
     return dict(metric="atom*steps/s (efsm of one disjoint batch of 64 cells)", value=round(n * steps / dt, 2),
                 unit="atom*steps/s", steps=steps, warmup=warmup, ms_per_step=round(dt / steps * 1e3, 3),
+                captured=captured,
                 config={"workload": "C4: 64 random triclinic cells, 8-64 atoms, Z 1..94 (seed 3), one batch",
                         "n_atoms": n, "n_directed": sum(int(g.atom_graph.shape[0]) for g in graphs),
                         "n_angles": sum(int(g.line_graph.shape[0]) for g in graphs)})
@@ -428,6 +454,9 @@ def main():
     torch.cuda.synchronize()
     e2e = n_atoms * e2e_steps / (time.perf_counter() - t1)
 
+    # the same step replayed from a captured HIP graph (opt-in; beside `value`)
+    captured = _captured_rate(model, [g], n_atoms, args.steps, args.warmup)
+
     # rooflines: the dominant (MFMA-bound) kernel family and the line attention (HBM-bound)
     mode_idx, mma_peak, peak_note, dtype = MMA_ROOF[ops.get_mma_precision()]
 
@@ -560,6 +589,7 @@ def main():
                             "geometry, strain and every layer run each step (e2e_with_gpu_graph_rebuild: the "
                             "radius graph, line graph and groupings rebuilt every step)"},
         "e2e_with_gpu_graph_rebuild": round(e2e, 2),
+        "captured": captured,
         "roofline": roof,
         f"roofline_{other}": r_other,
         "roofline_line_attn": attn,

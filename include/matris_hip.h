@@ -181,6 +181,14 @@ int matris_seg_sum2_runs(int64_t n_seg, int64_t rows_hint, const float *xa, int6
                          int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b, float scale_b, int accumulate,
                          float *out, void *stream);
 
+/* out[s, :] = sum over rows r in [rowptr[s], rowptr[s+1]) of x[r, :] for narrow rows
+ * (x, out row-major with `width` floats per row, 1 <= width <= 32), summed in a fixed order
+ * (no atomics): the per-graph pooling of a batch's atom energies (functions.py:340-365,
+ * GraphPooling, readout.py:70-75) and the per-graph sums of its strain and lattice
+ * gradients (processgraph.py:169-199, the backward of the per-graph broadcasts). */
+int matris_seg_sum_narrow(int64_t n_seg, const int32_t *rowptr, const float *x, int width, float *out,
+                          void *stream);
+
 /* out[r, :] = (accumulate ? out[r, :] : 0) + scale * src[idx ? idx[r] : r, :]
  * torch.index_select(x, 0, idx) (interaction_block.py:96-100) and the backward of a
  * segment sum. */

@@ -107,6 +107,7 @@ _SIGS = {
     "matris_env_agg_bwd_env": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_env_agg_bwd_env_proj": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
     "matris_env_linear": (_I, [_I64, _I, _P, _P, _P, _P]),
+    "matris_seg_sum_narrow": (_I, [_I64, _P, _P, _I, _P, _P]),
     "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_gmlp_project": (_I, [_I64, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_fwd_proj": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,

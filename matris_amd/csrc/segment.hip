@@ -396,6 +396,46 @@ extern "C" int matris_seg_sum_mul_proj(int64_t n_seg, int64_t rows_hint, const f
 }
 
 // ------------------------------------------------------------------------------------
+// segment sums of narrow rows (width <= 32 floats: per-graph energies, per-graph strain
+// and lattice gradients of a batch), in a fixed order: one wave per segment; lane l takes
+// column l % width of rows b + l / width, b + l / width + slots, ... (slots = 64 / width),
+// then lanes 0 .. width-1 add the slots' partial sums in slot order from LDS.  No atomics:
+// the per-graph sums of a batch are bitwise reproducible.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void seg_sum_narrow_kernel(int64_t n_seg, const int32_t *__restrict__ rowptr,
+                                                             const float *__restrict__ x, int width,
+                                                             float *__restrict__ out) {
+    __shared__ float part[WAVES_PER_BLOCK][64];
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int64_t seg = (int64_t)blockIdx.x * WAVES_PER_BLOCK + w;
+    const int slots = 64 / width;
+    float acc = 0.f;
+    if (seg < n_seg && l < slots * width) {
+        const int64_t b = rowptr[seg], e = rowptr[seg + 1];
+        const int col = l % width;
+        for (int64_t r = b + l / width; r < e; r += slots) acc += x[r * width + col];
+    }
+    part[w][l] = acc;
+    __syncthreads();
+    if (seg < n_seg && l < width) {
+        float t = 0.f;
+        for (int k = 0; k < slots; ++k) t += part[w][k * width + l];
+        out[seg * width + l] = t;
+    }
+}
+
+extern "C" int matris_seg_sum_narrow(int64_t n_seg, const int32_t *rowptr, const float *x, int width, float *out,
+                                     void *stream) {
+    if (n_seg < 0 || width < 1 || width > 32) return MATRIS_E_ARG;
+    if (n_seg == 0) return 0;
+    if (!rowptr || !out) return MATRIS_E_ARG;
+    seg_sum_narrow_kernel<<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(n_seg, rowptr, x,
+                                                                                               width, out);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
 // row gather
 // ------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gather_rows_kernel(const float *__restrict__ src,

@@ -8,6 +8,7 @@ CSR structures built by matris_csr_build.
 """
 from __future__ import annotations
 
+import collections
 import weakref
 
 import torch
@@ -35,19 +36,21 @@ class _ImageShift(torch.autograd.Function):
 
 
 class _GraphBroadcast(torch.autograd.Function):
-    """x [G, ...] repeated lengths[g] times per graph (rows contiguous per graph), with the
-    backward summed per graph in a fixed order (a segmented reduction instead of the
-    atomic index_add_ of an indexing backward), so batched stresses are reproducible."""
+    """x [G, ...] repeated lengths[g] times per graph (rows contiguous per graph, int32 row
+    pointers rowptr), with the backward summed per graph in a fixed order
+    (ops.seg_sum_narrow_raw instead of the atomic index_add_ of an indexing backward), so
+    batched stresses are reproducible."""
 
     @staticmethod
-    def forward(ctx, x, lengths, total):
-        ctx.save_for_backward(lengths)
+    def forward(ctx, x, lengths, total, rowptr):
+        ctx.save_for_backward(rowptr)
+        ctx.n = x.shape[0]
         return torch.repeat_interleave(x, lengths, dim=0, output_size=total)
 
     @staticmethod
     def backward(ctx, g):
-        (lengths,) = ctx.saved_tensors
-        return torch.segment_reduce(g, "sum", lengths=lengths, axis=0), None, None
+        (rowptr,) = ctx.saved_tensors
+        return ops.seg_sum_narrow_raw(g, rowptr, ctx.n), None, None, None
 
 
 def _sorted(x: torch.Tensor) -> bool:
@@ -112,13 +115,21 @@ def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
     src32 = atom_graph[:, 1].contiguous()
     d2u32 = torch.cat(d2u, 0).contiguous()
     u2d32 = torch.cat(u2d, 0).contiguous()
+    # per-graph counts on the device, made once here: the evaluation itself then copies
+    # nothing from the host (which also keeps it capturable in a HIP graph)
+    atoms_len = torch.tensor(n_atoms, device=device)
+    dir_len = torch.tensor(n_dir, device=device)
+    zero = torch.zeros(1, dtype=torch.int32, device=device)
+    atom_rowptr = torch.cat([zero, torch.cumsum(atoms_len, 0).to(torch.int32)])
+    dir_rowptr = torch.cat([zero, torch.cumsum(dir_len, 0).to(torch.int32)])
     if len(graphs) == 1:
         atom_segment = torch.zeros(N, dtype=torch.long, device=device)
     else:
-        atom_segment = torch.repeat_interleave(torch.arange(len(graphs), device=device),
-                                               torch.tensor(n_atoms, device=device), output_size=N)
+        atom_segment = torch.repeat_interleave(torch.arange(len(graphs), device=device), atoms_len, output_size=N)
     t = dict(atom_graph=atom_graph, tgt=tgt32.long(), src=src32.long(), d2u32=d2u32, u2d32=u2d32,
-             d2u64=d2u32.long(), u2d64=u2d32.long(), atom_segment=atom_segment,
+             d2u64=d2u32.long(), u2d64=u2d32.long(), atom_segment=atom_segment, atoms_len=atoms_len,
+             dir_len=dir_len, atoms_per_graph32=atoms_len.to(torch.int32), atom_rowptr=atom_rowptr,
+             dir_rowptr=dir_rowptr,
              grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True),
              grp_src=Grouping.build(src32, N, deferred=True),
              grp_d2u=Grouping.build(d2u32, U, sorted_rows=False, deferred=True))
@@ -141,10 +152,28 @@ def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
 
 
 # Topology of single graphs, remembered per graph object under its index signature (the
-# identity, data pointer, version and shape of every index tensor): an edited, replaced or
-# moved index tensor misses.  Positions, lattice and everything derived from them are
-# recomputed on every call.
+# identity, data pointer, storage, version and shape of every index tensor): an edited,
+# replaced or moved index tensor misses.  Batches are remembered the same way, the last
+# few of them, under their graphs' identities and signatures.  Positions, lattice and
+# everything derived from them are recomputed on every call.
 _TOPOLOGY: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+_BATCH_TOPOLOGY: "collections.OrderedDict" = collections.OrderedDict()
+_BATCH_TOPOLOGY_MAX = 4
+
+
+def _batch_topology(graphs, sigs, n_atoms, n_dir, n_und, n_ang) -> dict:
+    key = tuple(id(g) for g in graphs)
+    hit = _BATCH_TOPOLOGY.get(key)
+    if hit is not None:
+        refs, hsigs, topo = hit
+        if all(r() is g for r, g in zip(refs, graphs)) and hsigs == tuple(sigs):
+            _BATCH_TOPOLOGY.move_to_end(key)
+            return topo
+    topo = _topology(graphs, n_atoms, n_dir, n_und, n_ang)
+    _BATCH_TOPOLOGY[key] = ([weakref.ref(g) for g in graphs], tuple(sigs), topo)
+    while len(_BATCH_TOPOLOGY) > _BATCH_TOPOLOGY_MAX:
+        _BATCH_TOPOLOGY.popitem(last=False)
+    return topo
 
 
 def process_graphs(graphs, compute_stress: bool = True) -> dict:
@@ -165,7 +194,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
             _TOPOLOGY[graphs[0]] = hit
         topo = hit[1]
     else:
-        topo = _topology(graphs, n_atoms, n_dir, n_und, n_ang)
+        topo = _batch_topology(graphs, sigs, n_atoms, n_dir, n_und, n_ang)
 
     if G == 1 and dtype == torch.float32 and graphs[0].atom_frac_coord.dtype == torch.float32 and \
             graphs[0].neighbor_image.dtype == torch.float32:
@@ -186,7 +215,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     cart = torch.cat(carts, 0)
     image = torch.cat(imgs, 0)
     atom_segment = topo["atom_segment"]
-    atoms_len = torch.tensor(n_atoms, device=device)
+    atoms_len = topo["atoms_len"]
     lat3 = lattice.reshape(G, 3, 3)
     volumes = torch.einsum("ni,ni->n", lat3[:, 0], torch.linalg.cross(lat3[:, 1], lat3[:, 2]))[:, None, None]
 
@@ -199,7 +228,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         if G == 1:  # one graph: the per-atom strain is a broadcast, not a gather
             cart = cart + cart @ sym[0]
         else:
-            cart = cart + torch.bmm(cart.unsqueeze(1), _GraphBroadcast.apply(sym, atoms_len, N)).squeeze(1)
+            cart = cart + torch.bmm(cart.unsqueeze(1), _GraphBroadcast.apply(sym, atoms_len, N,
+                                                                             topo["atom_rowptr"])).squeeze(1)
         lat3 = lat3 + torch.matmul(lat3, sym)
         lattice = lat3.reshape(-1, 3)
 
@@ -207,7 +237,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     if G == 1:
         shift = _ImageShift.apply(image, lattice)
     else:
-        lat_e = _GraphBroadcast.apply(lat3, torch.tensor(n_dir, device=device), E)
+        lat_e = _GraphBroadcast.apply(lat3, topo["dir_len"], E, topo["dir_rowptr"])
         shift = torch.bmm(image.unsqueeze(1), lat_e).squeeze(1)
     vec = ops.edge_vectors(cart, shift, grp_tgt, grp_src)
     length = torch.norm(vec, dim=1)
@@ -215,6 +245,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
 
     out = dict(atomic_numbers=torch.cat([g.atomic_number for g in graphs], 0), edge_lengths=length,
                unit_edge_vectors=unit, atom_segment=atom_segment, atoms_per_graph=n_atoms,
+               atoms_len=topo["atoms_len"], atoms_per_graph32=topo["atoms_per_graph32"],
+               atom_rowptr=topo["atom_rowptr"],
                directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], u2d32=topo["u2d32"],
                volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,
@@ -242,7 +274,8 @@ def _one_graph(g, topo, compute_stress, n_atoms, N, E, U, A) -> dict:
     grp_tgt, grp_src = topo["grp_tgt"], topo["grp_src"]
     length, unit, lattice, volumes = ops.edge_geometry(cart, strains, lat, g.neighbor_image, grp_tgt, grp_src)
     out = dict(atomic_numbers=g.atomic_number, edge_lengths=length, unit_edge_vectors=unit,
-               atom_segment=topo["atom_segment"], atoms_per_graph=n_atoms,
+               atom_segment=topo["atom_segment"], atoms_per_graph=n_atoms, atoms_len=topo["atoms_len"],
+               atoms_per_graph32=topo["atoms_per_graph32"],
                directed2undirected=topo["d2u64"], undirected2directed=topo["u2d64"], u2d32=topo["u2d32"],
                volumes=volumes,
                lattice=lattice, batch_cart_coords=cart, batch_strains=strains,

@@ -160,15 +160,18 @@ class GraphPooling(nn.Module):
         super().__init__()
         self.average = average
 
-    def forward(self, node_feat, segment, n_graphs: int):
+    def forward(self, node_feat, segment, n_graphs: int, rowptr=None):
         """Per-graph sums in a fixed order (no float atomics, so the energies are bitwise
-        reproducible): one reduction for one graph, a segmented reduction over the atoms,
-        which are contiguous per graph, otherwise."""
+        reproducible): one reduction for one graph, otherwise a segmented reduction over
+        the atoms, which are contiguous per graph (ops.SegSumNarrow with the graphs' int32
+        row pointers; made from segment when not given)."""
         if n_graphs == 1:
             out = node_feat.sum(0, keepdim=True)
         else:
-            cnt = torch.bincount(segment, minlength=n_graphs)
-            out = torch.segment_reduce(node_feat, "sum", lengths=cnt, axis=0)
+            if rowptr is None:
+                cnt = torch.bincount(segment, minlength=n_graphs)
+                rowptr = torch.cat([cnt.new_zeros(1), torch.cumsum(cnt, 0)]).to(torch.int32)
+            out = ops.SegSumNarrow.apply(node_feat, rowptr, segment, n_graphs)
         if self.average:
             out = out / torch.bincount(segment, minlength=n_graphs).clamp_min(1)[:, None]
         return out
@@ -503,7 +506,8 @@ class EnergyHead(nn.Module):
 
     def forward(self, batch_graph, node_feat):
         e = self.energy_head(node_feat)
-        return self.pooling(e, batch_graph["atom_segment"], len(batch_graph["atoms_per_graph"])).view(-1)
+        return self.pooling(e, batch_graph["atom_segment"], len(batch_graph["atoms_per_graph"]),
+                            batch_graph.get("atom_rowptr")).view(-1)
 
 
 class MagmomHead(nn.Module):
@@ -619,6 +623,14 @@ class MatRIS(nn.Module):
             ops.status_take(dev)
         return pred
 
+    def capture(self, graphs, task: str = "efsm", warmup: int = 2):
+        """Opt-in: this evaluation of `graphs` recorded as a HIP graph (capture.py).  The
+        returned object's replay() gives forward(graphs, task)'s outputs for the graphs'
+        current positions and lattices, with their index arrays held fixed, the weights and
+        MFMA arithmetic of capture time, and the same one status read per evaluation."""
+        from .capture import CapturedEvaluation
+        return CapturedEvaluation(self, graphs, task, warmup)
+
     def _evaluate(self, graphs, task: str) -> dict:
         is_training = False
         pred = {}
@@ -649,12 +661,9 @@ class MatRIS(nn.Module):
                                            total_energy=total, is_training=is_training))
         if "m" in task:
             pred["m"] = self.magmom_head(bg, node)
-        if len(bg["atoms_per_graph"]) == 1:  # no host-to-device copy (a stream sync) for one graph
-            apg = torch.full((1,), bg["atoms_per_graph"][0], dtype=torch.int32, device=total.device)
-        else:
-            apg = torch.tensor(bg["atoms_per_graph"], dtype=torch.int32, device=total.device)
+        apg = bg["atoms_per_graph32"]  # made with the graph's topology: no host-to-device copy here
         pred["e"] = total / apg if self.is_intensive else total
-        pred["atoms_per_graph"] = apg
+        pred["atoms_per_graph"] = apg.clone()  # the caller's own copy, not the kept topology's
         # model.py:245-249: the composition energy of AtomRef (no position dependence)
         ref = 0 if self.reference_energy is None else self.reference_energy(graphs)
         pred["e"] = pred["e"] + ref

@@ -192,6 +192,38 @@ class Grouping:
 # ------------------------------------------------------------------------------------
 # segment sum / gather
 # ------------------------------------------------------------------------------------
+def seg_sum_narrow_raw(x: torch.Tensor, rowptr: torch.Tensor, n_seg: int) -> torch.Tensor:
+    """[n_seg, *x.shape[1:]]: sums of the contiguous row ranges [rowptr[s], rowptr[s+1]) of
+    x (at most 32 floats per row) in a fixed order (matris_seg_sum_narrow)."""
+    lib = _lib.load()
+    x = _f32c(x)
+    w = 1
+    for d in x.shape[1:]:
+        w *= int(d)
+    out = torch.empty((n_seg,) + tuple(x.shape[1:]), dtype=torch.float32, device=x.device)
+    if rowptr.dtype != torch.int32 or rowptr.numel() != n_seg + 1:
+        raise ValueError("seg_sum_narrow_raw: rowptr must be int32 with n_seg + 1 entries")
+    with _timed("seg_sum_narrow", dict(rows=x.shape[0], segs=n_seg)):
+        _lib.check(lib.matris_seg_sum_narrow(n_seg, _p(rowptr), _p(x), w, _p(out), _stream()),
+                   "matris_seg_sum_narrow")
+    return out
+
+
+class SegSumNarrow(torch.autograd.Function):
+    """Per-segment sums of narrow rows (seg_sum_narrow_raw) whose backward broadcasts each
+    segment's gradient to its rows (segment ids `seg`, int64 [R])."""
+
+    @staticmethod
+    def forward(ctx, x, rowptr, seg, n_seg: int):
+        ctx.save_for_backward(seg)
+        return seg_sum_narrow_raw(x, rowptr, n_seg)
+
+    @staticmethod
+    def backward(ctx, g):
+        (seg,) = ctx.saved_tensors
+        return g.index_select(0, seg), None, None, None
+
+
 def _seg_src_bytes(grp: "Grouping", rows_read: int | None = None) -> int:
     """Algorithmic bytes of one summed source: its 128-wide rows read once (rows_read of
     them; all of the grouping's rows by default), its int32 permutation and row pointers."""

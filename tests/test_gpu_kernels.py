@@ -108,6 +108,25 @@ def test_seg_sum_two_groupings_one_pass(R, S, acc):
         ops.seg_sum_raw(x, ga, second=(xb, ops.Grouping.build(kb, S + 1), 1.0, 256, 128))
 
 
+@pytest.mark.parametrize("lengths,width", [([54, 0, 18, 1, 63, 200], 1), ([3000, 1, 0, 64, 65], 9),
+                                           ([7, 129], 32), ([0, 0], 4), ([5000], 1)])
+def test_seg_sum_narrow(lengths, width):
+    """matris_seg_sum_narrow: per-segment sums of narrow rows (batched energies, per-graph
+    strain / lattice gradients) against fp64 sums, empty segments included; two calls are
+    bitwise equal (fixed order, no atomics)."""
+    ops = _ops()
+    torch.manual_seed(sum(lengths) + width)
+    R = sum(lengths)
+    x = torch.randn(max(R, 1), width, device=DEV)[:R]
+    ptr = torch.tensor([0] + list(torch.cumsum(torch.tensor(lengths), 0)), dtype=torch.int32, device=DEV)
+    out = ops.seg_sum_narrow_raw(x, ptr, len(lengths))
+    x64 = x.double().cpu()
+    ref = torch.stack([x64[int(a):int(b)].sum(0) for a, b in zip(ptr[:-1].cpu(), ptr[1:].cpu())])
+    assert tuple(out.shape) == (len(lengths), width)
+    assert (out.double().cpu() - ref).abs().max().item() <= 1e-5 * max(1.0, ref.abs().max().item())
+    assert torch.equal(out, ops.seg_sum_narrow_raw(x, ptr, len(lengths)))
+
+
 @pytest.mark.parametrize("E,K", [(33698, 7), (1, 7), (0, 7), (513, 1), (777, 8), (100, 3)])
 def test_env_linear(E, K):
     """matris_env_linear: the learnable envelope env = basis W^T (interaction_block.py:

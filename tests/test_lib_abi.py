@@ -120,6 +120,10 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_env_linear(10, 0, v16, v16, v16, None) == -1001
     assert lib.matris_env_linear(10, 7, v16, v16, ctypes.c_void_p(8), None) == -1001
     assert lib.matris_env_linear(0, 7, v16, v16, v16, None) == 0
+    # narrow segment sums: width outside 1..32
+    assert lib.matris_seg_sum_narrow(4, v16, v16, 0, v16, None) == -1001
+    assert lib.matris_seg_sum_narrow(4, v16, v16, 33, v16, None) == -1001
+    assert lib.matris_seg_sum_narrow(0, None, None, 9, None, None) == 0
     assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 0, v16, None) == -1001
     assert lib.matris_seg_sum_mul_proj(4, 40, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, v16, None) == -1001
     assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, None, None) == -1001
