@@ -261,6 +261,12 @@ __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, 
                                                             const float *__restrict__ proj_w, int proj_k,
                                                             float *__restrict__ proj_out) {
     const int w = threadIdx.x >> 6, half = (threadIdx.x >> 5) & 1, l = threadIdx.x & 31, c = 4 * l;
+    __shared__ __align__(16) float wts[PROJ ? MATRIS_PROJ_KMAX * MATRIS_D : 4];
+    if constexpr (PROJ) {  // the block's copy of the projection weights (before any wave leaves)
+        for (int q = threadIdx.x; q < proj_k * MATRIS_D / 4; q += blockDim.x)
+            reinterpret_cast<float4 *>(wts)[q] = ld4(proj_w + 4 * q);
+        lds_barrier();
+    }
     const int64_t s0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + w) * 4;
     if (s0 >= n_seg) return;  // whole wave
     float4 ta[4], tb[4];
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, 
         float4 t = make_float4(ta[j].x * a.scale, ta[j].y * a.scale, ta[j].z * a.scale, ta[j].w * a.scale);
         if (b.x) t = add4(t, make_float4(tb[j].x * b.scale, tb[j].y * b.scale, tb[j].z * b.scale, tb[j].w * b.scale));
         if constexpr (PROJ) {  // uniform over the wave: s < n_seg is the same for all its lanes
-            proj_row_store(t, l, proj_w, proj_k, proj_out + s * proj_k);
+            proj_row_store(t, l, wts, proj_k, proj_out + s * proj_k);
             continue;
         }
         float *op = out + s * MATRIS_D + c;
