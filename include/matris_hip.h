@@ -181,6 +181,25 @@ int matris_seg_sum2_runs(int64_t n_seg, int64_t rows_hint, const float *xa, int6
                          int64_t offb, const int32_t *rowptr_b, const int32_t *perm_b, float scale_b, int accumulate,
                          float *out, void *stream);
 
+/* The readout (model.py:238-244 readout_norm; readout.py:18-75 EnergyHead with
+ * mlp_hidden_dims (128, 128); readout.py:77-133 MagmomHead with hidden 256) on n node rows
+ * x [n, 128] (16-byte aligned), fused per row:
+ *   nrm = x rsqrt(mean(x^2) + eps) wn          (nn.RMSNorm(128); eps its own or fp32 epsilon)
+ *   e   = w3 . SiLU(W2 SiLU(W1 nrm + b1) + b2) + b3          -> e [n]
+ *   m   = | w5 . SiLU(W4 nrm + b4) + b5 |                     -> m [n]
+ * with w1t = W1^T, w2t = W2^T ([128][128] row-major), w4t = W4^T ([128][256]), w3 [128],
+ * w5 [256], b1, b2 [128], b4 [256], b3 and b5 device scalars.
+ * matris_readout_bwd: g_x [n, 128] (+)= d(sum_r g_e[r] e[r]) / dx, the energy branch's
+ * backward (the magmom head is not differentiated), recomputing the forward of its rows;
+ * w1, w2 the untransposed [128][128] weights.  fp32 sums in a fixed order. */
+int matris_readout_fwd(int64_t n, const float *x, const float *wn, const float *w1t, const float *b1,
+                       const float *w2t, const float *b2, const float *w3, const float *b3, const float *w4t,
+                       const float *b4, const float *w5, const float *b5, float eps, float *e, float *m,
+                       void *stream);
+int matris_readout_bwd(int64_t n, const float *x, const float *wn, const float *w1t, const float *b1,
+                       const float *w1, const float *w2t, const float *b2, const float *w2, const float *w3,
+                       float eps, const float *g_e, int accumulate, float *g_x, void *stream);
+
 /* out[s, :] = sum over rows r in [rowptr[s], rowptr[s+1]) of x[r, :] for narrow rows
  * (x, out row-major with `width` floats per row, 1 <= width <= 32), summed in a fixed order
  * (no atomics): the per-graph pooling of a batch's atom energies (functions.py:340-365,

@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(_HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(_HERE), "include")
 LIB_PATH = os.path.join(CSRC, "libmatris_hip.so")
-SOURCES = ["graph.hip", "segment.hip", "gmlp.hip", "mlp.hip", "basis.hip", "silu.hip"]
+SOURCES = ["graph.hip", "segment.hip", "gmlp.hip", "mlp.hip", "basis.hip", "silu.hip", "readout.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
              "-packed-fp32-ops"]
@@ -108,6 +108,8 @@ _SIGS = {
     "matris_env_agg_bwd_env_proj": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
     "matris_env_linear": (_I, [_I64, _I, _P, _P, _P, _P]),
     "matris_seg_sum_narrow": (_I, [_I64, _P, _P, _I, _P, _P]),
+    "matris_readout_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P]),
+    "matris_readout_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _P, _P]),
     "matris_gmlp_fwd": (_I, [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_gmlp_project": (_I, [_I64, _P, _P, _I, _P, _I, _P]),
     "matris_gmlp_fwd_proj": (_I, [_I64, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P,

@@ -1371,3 +1371,84 @@ def spherical_basis(unit, grp_t: Grouping, grp_s: Grouping, cutoff: float):
     grp_s group the angles by the directed edge they read as i->j (target_DE_index) and
     j->k (source_DE_index) (feature_embed.py:183-201, basis_function.py:222-338)."""
     return _SBF.apply(unit, grp_t, grp_s, float(cutoff))
+
+
+# ------------------------------------------------------------------------------------
+# readout
+# ------------------------------------------------------------------------------------
+class ReadoutPack(_PackCache):
+    """The readout's weights (RMSNorm weight, energy MLP 128-128-128-1, magmom MLP 128-256-1)
+    in the layouts matris_readout_fwd / _bwd read, rebuilt when a parameter changes."""
+
+    def get(self, norm, energy_mlp, magmom_mlp):
+        L, M = energy_mlp.layers, magmom_mlp.layers
+        lin_e = [l for l in L if isinstance(l, torch.nn.Linear)]
+        lin_m = [l for l in M if isinstance(l, torch.nn.Linear)]
+        params = (norm.weight, *[p for l in lin_e + lin_m for p in (l.weight, l.bias)])
+
+        def build():
+            w1, w2, w3 = (l.weight.detach().float() for l in lin_e)
+            w4, w5 = (l.weight.detach().float() for l in lin_m)
+            self.mats = dict(wn=norm.weight.detach().float().contiguous(), w1=w1.contiguous(),
+                             w1t=w1.t().contiguous(), w2=w2.contiguous(), w2t=w2.t().contiguous(),
+                             w3=w3.reshape(-1).contiguous(), w4t=w4.t().contiguous(),
+                             w5=w5.reshape(-1).contiguous())
+            for k, l in zip(("b1", "b2", "b3"), lin_e):
+                self.mats[k] = l.bias.detach().float().reshape(-1).contiguous()
+            for k, l in zip(("b4", "b5"), lin_m):
+                self.mats[k] = l.bias.detach().float().reshape(-1).contiguous()
+            eps = norm.eps
+            self.eps = float(torch.finfo(torch.float32).eps if eps is None else eps)
+
+        self._refresh(params, build)
+        return self
+
+
+def readout_fwd_raw(pack: ReadoutPack, x):
+    """(e [N], m [N]) of matris_readout_fwd: per-row energy and |magmom| of the readout."""
+    lib = _lib.load()
+    x = _f32c(x)
+    N = x.shape[0]
+    e = torch.empty(N, dtype=torch.float32, device=x.device)
+    m = torch.empty(N, dtype=torch.float32, device=x.device)
+    w = pack.mats
+    with _timed("readout_fwd", dict(rows=N)):
+        _lib.check(lib.matris_readout_fwd(N, _p(x), _p(w["wn"]), _p(w["w1t"]), _p(w["b1"]), _p(w["w2t"]),
+                                          _p(w["b2"]), _p(w["w3"]), _p(w["b3"]), _p(w["w4t"]), _p(w["b4"]),
+                                          _p(w["w5"]), _p(w["b5"]), pack.eps, _p(e), _p(m), _stream()),
+                   "matris_readout_fwd")
+    return e, m
+
+
+def readout_bwd_raw(pack: ReadoutPack, x, g_e):
+    """g_x [N, 128] of matris_readout_bwd: the energy branch's input gradient."""
+    lib = _lib.load()
+    x, g_e = _f32c(x), _f32c(g_e)
+    g_x = _rows(x.shape[0], D, x.device)
+    w = pack.mats
+    with _timed("readout_bwd", dict(rows=x.shape[0])):
+        _lib.check(lib.matris_readout_bwd(x.shape[0], _p(x), _p(w["wn"]), _p(w["w1t"]), _p(w["b1"]), _p(w["w1"]),
+                                          _p(w["w2t"]), _p(w["b2"]), _p(w["w2"]), _p(w["w3"]), pack.eps, _p(g_e),
+                                          0, _p(g_x), _stream()), "matris_readout_bwd")
+    return g_x
+
+
+class Readout(torch.autograd.Function):
+    """(e [N], m [N]) of the fused readout; e is differentiable (its backward is
+    readout_bwd_raw), m is not (the magmom head is evaluated, never differentiated)."""
+
+    @staticmethod
+    def forward(ctx, x, pack):
+        _check_dev(x)
+        e, m = readout_fwd_raw(pack, x)
+        ctx.save_for_backward(x)
+        ctx.pack = pack
+        ctx.mark_non_differentiable(m)
+        return e, m
+
+    @staticmethod
+    def backward(ctx, g_e, g_m):
+        (x,) = ctx.saved_tensors
+        if g_e is None:
+            return None, None
+        return readout_bwd_raw(ctx.pack, x, g_e), None

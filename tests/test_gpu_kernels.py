@@ -1166,3 +1166,34 @@ def test_edge_embedding_vs_fp64(U, mode, tol):
         assert _rel(g_len[u2d.long()], g64) < 10 * tol
     finally:
         ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
+@pytest.mark.parametrize("N", [864, 1, 17, 5000])
+def test_readout_fused_vs_fp64(N):
+    """matris_readout_fwd / _bwd: readout_norm (RMSNorm), the energy MLP 128-128-128-1 and the
+    magmom MLP 128-256-1 (model.py readout, readout.py:18-133) against the same torch modules
+    evaluated in fp64: per-row energies, |magmom| and the energy branch's input gradient."""
+    from matris_amd.model.model import EnergyHead, MagmomHead, get_normalization
+    ops = _ops()
+    torch.manual_seed(N)
+    norm = get_normalization("rms", 128)
+    eh, mh = EnergyHead(128, (128, 128), 1, "mlp", "silu"), MagmomHead(128, 256, 1, "mlp", "silu")
+    with torch.no_grad():
+        norm.weight.uniform_(0.5, 1.5)
+        for p in list(eh.parameters()) + list(mh.parameters()):
+            p.add_(0.05 * torch.randn_like(p))
+    x = torch.randn(N, 128) * 2
+    g_e = torch.randn(N)
+    x64 = x.double().requires_grad_(True)
+    n64 = norm.double()(x64)
+    e64 = eh.energy_head.double()(n64).view(-1)
+    m64 = torch.abs(mh.magmom_head.double()(n64)).view(-1)
+    (e64 * g_e.double()).sum().backward()
+    pack = ops.ReadoutPack().get(norm.float().to(DEV), eh.energy_head.float().to(DEV), mh.magmom_head.float().to(DEV))
+    xd = x.to(DEV)
+    e, m = ops.readout_fwd_raw(pack, xd)
+    g_x = ops.readout_bwd_raw(pack, xd, g_e.to(DEV))
+    assert _rel(e, e64.detach()) < 1e-5 and _rel(m, m64.detach()) < 1e-5
+    assert _rel(g_x, x64.grad) < 1e-5
+    e2, _ = ops.readout_fwd_raw(pack, xd)
+    assert torch.equal(e, e2)  # fixed summation order
