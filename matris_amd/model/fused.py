@@ -234,6 +234,9 @@ class _LineRefinement(torch.autograd.Function):
         else:
             ctx.save_for_backward(env, *saved)
         ctx.mode, ctx.layer, ctx.lg, ctx.recompute, ctx.n_atom = mode, layer, lg, recompute, atom.shape[0]
+        # an unused output (the last block's three-body features) arrives as None, not as a
+        # materialised [A, 128] zero tensor
+        ctx.set_materialize_grads(False)
         return bond_new, tb_new
 
     @staticmethod
@@ -255,7 +258,6 @@ class _LineRefinement(torch.autograd.Function):
         tgt, src = lg["grp_tgt"], lg["grp_src"]
         E, A = env.shape[0], h.shape[0]
         g_bond_new = _zeros_if_none(g_bond_new, env)
-        g_tb_new = _zeros_if_none(g_tb_new, h)
         g_bond = ops._rows(E, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
         # the envelope's gradient leaves projected onto its basis (the learnable envelope's
@@ -265,8 +267,13 @@ class _LineRefinement(torch.autograd.Function):
         # g_h = edge_FFN's input gradient + the aggregate's term; g_tb = source 0's
         # GatedMLP gradient + r_e g_tb_new.  In the two-plane modes g_h never leaves the
         # GatedMLP backward (its head computes it per tile).
-        g_tb = ops._rows(A, D, g_tb_new.device)
-        if mode != 6:
+        g_tb = ops._rows(A, D, env.device)
+        if g_tb_new is None:
+            # tb' unused: no edge_FFN or residual term, g_h is the aggregate's term alone
+            g_h = ops.gather_mul_raw(g_agg_env, tgt.key, env, src.key, out=ops._rows(A, D, env.device))
+            g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 4 * D, mode, g_x0=g_tb, acc0=False, runs=_runs(tgt, 2))
+            del g_h
+        elif mode != 6:
             g_x = ops.gmlp_bwd_ffn_raw(ph, p_h, z_h, 4 * D, mode, pm, g_tb_new, p_de, env_term=(g_agg_env, env, tgt, src),
                                        g_x0=g_tb, res_w=r_e, runs=_runs(tgt, 2))
         else:
