@@ -233,12 +233,13 @@ int matris_gather_mul(int64_t n_rows, const float *a, const int32_t *ia, const f
  * copies of each bond) with each segment's sum projected onto the learnable envelope's
  * basis instead of written: proj_out[s, k] = sum_c sum_s[c] proj_wt[k, c] ([n_seg, proj_k],
  * proj_k <= 8, proj_wt the Linear(proj_k, 128) weight transposed, [proj_k, 128] row-major,
- * 16-byte aligned).  The atom-graph Refinement's g_env =
+ * 16-byte aligned; accumulate: added to proj_out).  The atom-graph Refinement's g_env =
  * sum_{d2u} h * g_agg[tgt] goes straight to the input gradient of learnable_envelope
- * (interaction_block.py:240-241). */
+ * (interaction_block.py:240-241), accumulated over the blocks that share the basis. */
 int matris_seg_sum_mul_proj(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx, int64_t col_off,
                             const int32_t *rowptr, const int32_t *perm, const float *mul, const int32_t *mul_idx,
-                            float scale, const float *proj_wt, int proj_k, float *proj_out, void *stream);
+                            float scale, const float *proj_wt, int proj_k, int accumulate, float *proj_out,
+                            void *stream);
 
 /* Backward of the edge vectors vec[e] = cart[tgt[e]] - (cart[src[e]] + shift[e])
  * (row P1, matris/model/processgraph.py:192-199): g_cart [n_atoms, 3] fp32 =
@@ -247,6 +248,13 @@ int matris_seg_sum_mul_proj(int64_t n_seg, int64_t rows_hint, const float *x, in
  * replaces the sort-based backward of the two index_select gathers. */
 int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const int32_t *t_ptr, const int32_t *t_perm,
                         const int32_t *s_ptr, const int32_t *s_perm, float *g_cart, void *stream);
+
+/* Cartesian positions of one graph (row P1, matris/model/processgraph.py:87,
+ * atom_frac_coord @ lattice): cart[i, j] = sum_k frac[i, k] lattice[k, j] (frac, cart
+ * [n, 3], lattice [3, 3], fp32), and, with strain_zero non-NULL, strain_zero[0 .. 8] = 0
+ * (the zero strain of processgraph.py:173-177, which the stress differentiates against). */
+int matris_frac_to_cart(int64_t n, const float *frac, const float *lattice, float *cart, float *strain_zero,
+                        void *stream);
 
 /* Edge geometry of one graph with the strain trick (row P1, matris/model/processgraph.py:
  * 169-199: symmetric_strains, the strained positions and lattice, neighbor_pos + image @
@@ -337,10 +345,11 @@ int matris_env_agg_bwd_env(int64_t n_seg, const float *h, const float *env, cons
  * same pass: g_basis[b, k] = sum_c g_env[b, c] wt[k, c] ([n_seg, proj_k], proj_k <= 8; wt
  * the Linear(proj_k, 128) weight transposed, row-major [proj_k, 128], 16-byte aligned) --
  * the input gradient of learnable_envelope (interaction_block.py:244), so g_env never
- * reaches memory. */
+ * reaches memory; accumulate adds it to g_basis (the blocks sharing one basis). */
 int matris_env_agg_bwd_env_proj(int64_t n_seg, const float *h, const float *env, const float *g_agg,
                                 const float *S, const int32_t *t_idx, const int32_t *s_ptr, const int32_t *s_perm,
-                                const float *proj_wt, int proj_k, float *g_basis, float *g_agg_env, void *stream);
+                                const float *proj_wt, int proj_k, int accumulate, float *g_basis, float *g_agg_env,
+                                void *stream);
 /* The learnable envelope itself (interaction_block.py:240-246, nn.Linear(num_basis, 128,
  * bias=False)): env[r, c] = sum_k basis[r, k] wt[k, c], basis [n, k] (k <= 8), wt the
  * weight transposed [k, 128] row-major, env [n, 128] (wt and env 16-byte aligned). */

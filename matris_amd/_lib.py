@@ -92,10 +92,11 @@ _SIGS = {
     "matris_seg_sum2_runs": (_I, [_I64, _I64, _P, _I64, _I64, _P, _I, _F, _P, _I64, _I64, _P, _P, _F, _I, _P, _P]),
     "matris_gather_rows": (_I, [_P, _P, _I64, _F, _I, _P, _P]),
     "matris_seg_sum_mul": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _F, _I, _P, _P]),
-    "matris_seg_sum_mul_proj": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _F, _P, _I, _P, _P]),
+    "matris_seg_sum_mul_proj": (_I, [_I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _F, _P, _I, _I, _P, _P]),
     "matris_gather_mul": (_I, [_I64, _P, _P, _P, _P, _I, _P, _P]),
     "matris_edge_vec_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P]),
     "matris_edge_geom_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "matris_frac_to_cart": (_I, [_I64, _P, _P, _P, _P, _P]),
     "matris_edge_geom_bwd": (_I, [_I64, _I64] + [_P] * 17),
     "matris_attn_fwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
@@ -105,7 +106,7 @@ _SIGS = {
     "matris_env_agg_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_env_agg_bwd": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
     "matris_env_agg_bwd_env": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "matris_env_agg_bwd_env_proj": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P]),
+    "matris_env_agg_bwd_env_proj": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P]),
     "matris_env_linear": (_I, [_I64, _I, _P, _P, _P, _P]),
     "matris_seg_sum_narrow": (_I, [_I64, _P, _P, _I, _P, _P]),
     "matris_readout_fwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P]),

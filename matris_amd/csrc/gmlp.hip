@@ -113,6 +113,7 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                           PairOut pout, unsigned *range_flag) {
     constexpr int NPL = Npl<MODE>::v;
     constexpr int CHUNK = 2 * 2 * NPL * 64;  // uint4 per LDS chunk: [rt 2][kb 2][plane][lane]
+    constexpr bool PRE = NPL == 2;           // the tails' GEMM operands as pre-split rows
     __shared__ __align__(16) float smem[BM * LDH];
     uint4 *Xp = reinterpret_cast<uint4 *>(smem);  // two chunk buffers (<= 24 KB)
     float *Ts = smem;                             // [BM, 256] tile: p, then h, then z
@@ -376,28 +377,42 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                                                                    o1.z + w1.z * x1.z, o1.w + w1.w * x1.w);
             }
         }
-        if constexpr (TAIL) {  // the out rows, the tail's GEMM operand, over this row's z (already read)
-            *reinterpret_cast<float4 *>(Ts + row * LDH + c4) = o0;
-            *reinterpret_cast<float4 *>(Ts + row * LDH + 64 + c4) = o1;
-        }
-        if constexpr (PTAIL) {  // the residual rows, the pair's GEMM operand, likewise
-            *reinterpret_cast<float4 *>(Ts + row * LDH + c4) = rx0[rr];
-            *reinterpret_cast<float4 *>(Ts + row * LDH + 64 + c4) = rx1[rr];
+        // The tail's GEMM operand (the out rows) or the pair's (the residual rows), written
+        // over this row's z (already read).  Two-plane modes convert it once here, into the
+        // row's gate half as pre-split units (rowfrag_put4): the tail GEMMs give each wave
+        // one 32-column tile, so every wave would convert all 64 rows again.
+        if constexpr (TAIL || PTAIL) {
+            const float4 a0 = TAIL ? o0 : rx0[rr], a1 = TAIL ? o1 : rx1[rr];
+            if constexpr (PRE) {
+                amax = frag_amax<MODE>(amax, a0, a1);
+                rowfrag_put4<MODE>(Ts + row * LDH + MATRIS_D, c4, a0);
+                rowfrag_put4<MODE>(Ts + row * LDH + MATRIS_D, 64 + c4, a1);
+            } else {
+                *reinterpret_cast<float4 *>(Ts + row * LDH + c4) = a0;
+                *reinterpret_cast<float4 *>(Ts + row * LDH + 64 + c4) = a1;
+            }
         }
     }
     if constexpr (PTAIL) {
         // o0 = res W[0:128]^T, then o1 = res W[128:256]^T: each wave one 32-column tile of
-        // the pass, through columns 128..255 of the tile (the GEMM reads columns 0..127)
+        // the pass, through the half of the tile the GEMM does not read (it reads the
+        // pre-split rows in columns 128..255, or fp32 rows in columns 0..127)
         const float ps = take_wscale<MODE>(pout.W);
+        constexpr int OUTC = PRE ? 0 : MATRIS_D;
 #pragma unroll 1
         for (int half = 0; half < 2; ++half) {
             v16f pa[2][1];
             zero_acc(pa);
             __syncthreads();  // residual rows complete; the previous pass's rows stored
-            amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(pa, Ts, LDH, pout.W, 4 * half + wave,
-                                                                                MATRIS_D / 16, 0, lane));
+            if constexpr (PRE)
+                gemm_frag_src<MODE, 2, 1, MATRIS_D / 16, true>(pa, AFragRows{Ts + MATRIS_D, LDH}, 0, pout.W,
+                                                               4 * half + wave, MATRIS_D / 16, 0, lane);
+            else
+                amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(pa, Ts, LDH, pout.W,
+                                                                                    4 * half + wave, MATRIS_D / 16, 0,
+                                                                                    lane));
             scale_acc<MODE>(pa, ps);
-            acc_t_to_lds<2, 1>(pa, Ts + MATRIS_D, LDH, wave * 32, lane);
+            acc_t_to_lds<2, 1>(pa, Ts + OUTC, LDH, wave * 32, lane);
             __syncthreads();
             float *dst = half ? pout.o1 : pout.o0;
 #pragma unroll
@@ -406,39 +421,57 @@ __global__ __launch_bounds__(256, 2) void gmlp_fwd_kernel(int64_t M, int nsrc, G
                 const int row = q >> 5, cc = (q & 31) * 4;
                 if (m0 + row < M)
                     st_nt4(dst + (m0 + row) * MATRIS_D + cc,
-                           *reinterpret_cast<const float4 *>(Ts + row * LDH + MATRIS_D + cc));
+                           *reinterpret_cast<const float4 *>(Ts + row * LDH + OUTC + cc));
             }
         }
     }
     if constexpr (TAIL) {
-        // t = W1 out -> columns 128..255 of the tile (GEMM A reads columns 0..127); one pass
-        // saves t and applies SiLU; W2 SiLU(t) -> columns 0..127; rows leave with the residual
+        // t = W1 out -> the half of the tile GEMM A does not read; one pass saves t and
+        // applies SiLU (two-plane modes: writing SiLU(t) pre-split into columns 128..255,
+        // which GEMM A has finished reading); W2 SiLU(t) -> columns 0..127; rows leave with
+        // the residual.  Without pre-split rows: out in columns 0..127, t in 128..255.
         const uint4 *tw1 = tail.W1, *tw2 = tail.W2;
         const float t1s = take_wscale<MODE>(tw1), t2s = take_wscale<MODE>(tw2);
+        constexpr int TC = PRE ? 0 : MATRIS_D;  // t's columns
         v16f ta[2][1];
         zero_acc(ta);
         __syncthreads();  // out rows complete
-        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(ta, Ts, LDH, tw1, wave, MATRIS_D / 16, 0,
-                                                                            lane));
+        if constexpr (PRE)
+            gemm_frag_src<MODE, 2, 1, MATRIS_D / 16, true>(ta, AFragRows{Ts + MATRIS_D, LDH}, 0, tw1, wave,
+                                                           MATRIS_D / 16, 0, lane);
+        else
+            amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(ta, Ts, LDH, tw1, wave, MATRIS_D / 16,
+                                                                                0, lane));
         scale_acc<MODE>(ta, t1s);
-        acc_t_to_lds<2, 1>(ta, Ts + MATRIS_D, LDH, wave * 32, lane);
+        acc_t_to_lds<2, 1>(ta, Ts + TC, LDH, wave * 32, lane);
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < (BM * 32) / 256; ++it) {
             const int q = it * 256 + tid;
             const int row = q >> 5, cc = (q & 31) * 4;
-            float4 *t = reinterpret_cast<float4 *>(Ts + row * LDH + MATRIS_D + cc);
+            float4 *t = reinterpret_cast<float4 *>(Ts + row * LDH + TC + cc);
             float4 v = *t;
             if (tail.save_p && m0 + row < M) st_nt4(tail.save_p + (m0 + row) * MATRIS_D + cc, v);
             v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
-            *t = v;
+            if constexpr (PRE) {
+                amax = frag_amax<MODE>(amax, v, v);
+                rowfrag_put4<MODE>(Ts + row * LDH + MATRIS_D, cc, v);
+            } else {
+                *t = v;
+            }
         }
         __syncthreads();
         zero_acc(ta);
-        amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(ta, Ts + MATRIS_D, LDH, tw2, wave,
-                                                                            MATRIS_D / 16, 0, lane));
+        if constexpr (PRE)
+            gemm_frag_src<MODE, 2, 1, MATRIS_D / 16, true>(ta, AFragRows{Ts + MATRIS_D, LDH}, 0, tw2, wave,
+                                                           MATRIS_D / 16, 0, lane);
+        else
+            amax = fmaxf(amax, gemm_lds_packed<MODE, 2, 1, MATRIS_D / 16, true>(ta, Ts + MATRIS_D, LDH, tw2, wave,
+                                                                                MATRIS_D / 16, 0, lane));
         scale_acc<MODE>(ta, t2s);
-        acc_t_to_lds<2, 1>(ta, Ts, LDH, wave * 32, lane);  // every wave is past GEMM A (barrier above)
+        // columns 0..127: GEMM B reads 128..255, and every wave is past the SiLU pass's
+        // reads of t (barrier above)
+        acc_t_to_lds<2, 1>(ta, Ts, LDH, wave * 32, lane);
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < (BM * 32) / 256; ++it) {

@@ -437,19 +437,64 @@ __device__ __forceinline__ void frag_put8(uint4 *buf, int unit, int fl, const fl
     buf[(unit * 2 + 1) * 64 + fl] = f.p[1];
 }
 
+// Pre-split rows (two-plane modes): the 32 fragment units of a 128-column row kept inside
+// 128 floats of the row itself, unit (k-block kb, plane pl, half h) at float offset
+// ((kb * 2 + pl) * 2 + h) * 4 (h: which 8 columns of the 16-column k-block), so a pass
+// that owns a row can convert its values into a free half of that row with no barrier.
+// Store 4 values, columns col .. col+3 (col % 4 == 0), of such a row.
+template <int MODE>
+__device__ __forceinline__ void rowfrag_put4(float *row, int col, const float4 &v) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes");
+    const int kb = col >> 4, h = (col >> 3) & 1, hh = (col >> 2) & 1;
+    if constexpr (MODE == 0) {  // the planes are the unit's two fp32 halves
+        *reinterpret_cast<float4 *>(row + ((kb * 2 + hh) * 2 + h) * 4) = v;
+    } else {
+        uint2 p0, p1;
+        frag4<MODE>(v, p0, p1);
+        reinterpret_cast<uint2 *>(row + ((kb * 2 + 0) * 2 + h) * 4)[hh] = p0;
+        reinterpret_cast<uint2 *>(row + ((kb * 2 + 1) * 2 + h) * 4)[hh] = p1;
+    }
+}
+
+// Where a GEMM reads its pre-split A fragments from: a fragment buffer
+// [rt][kb][plane][64 lanes] x 16 bytes with aKB k-blocks per row tile ...
+struct AFragBuf {
+    const uint4 *buf;
+    int aKB;
+    template <int MODE, int NRT>
+    __device__ __forceinline__ void get(Frag<MODE> (&a)[NRT], int kb, int lane) const {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) a[rt].p[pl] = buf[((rt * aKB + kb) * 2 + pl) * 64 + lane];
+    }
+};
+// ... or pre-split rows (rowfrag_put4) of row stride ld: lane l reads row rt*32 + l%32.
+struct AFragRows {
+    const float *base;
+    int ld;
+    template <int MODE, int NRT>
+    __device__ __forceinline__ void get(Frag<MODE> (&a)[NRT], int kb, int lane) const {
+        const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            const float *r = base + (rt * 32 + l32) * ld;
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) a[rt].p[pl] = *reinterpret_cast<const uint4 *>(r + ((kb * 2 + pl) * 2 + h) * 4);
+        }
+    }
+};
+
 // One k-block of gemm_frag_packed: prefetch k-block `kpf` of B into BPF, then accumulate
 // k-block `kb` (A fragments from the pre-split buffer, B = BCUR).
-template <int MODE, int NRT, int NCT, bool TRANS>
-__device__ __forceinline__ void gemm_frag_step(v16f (&acc)[NRT][NCT], const uint4 *abuf, int aKB, int akb,
+template <int MODE, int NRT, int NCT, bool TRANS, class ASRC>
+__device__ __forceinline__ void gemm_frag_step(v16f (&acc)[NRT][NCT], const ASRC &asrc, int akb,
                                                const uint4 *__restrict__ W, int nt0, int KBW, int kpf,
                                                Frag<MODE> (&BCUR)[NCT], Frag<MODE> (&BPF)[NCT], int lane) {
     load_bfrags<MODE, NCT>(BPF, W, nt0, KBW, kpf, lane);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
     Frag<MODE> a[NRT];
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int pl = 0; pl < 2; ++pl) a[rt].p[pl] = abuf[((rt * aKB + akb) * 2 + pl) * 64 + lane];
+    asrc.template get<MODE, NRT>(a, akb, lane);
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) prep_w<MODE>(BCUR[ct]);
 #pragma unroll
@@ -463,12 +508,12 @@ __device__ __forceinline__ void gemm_frag_step(v16f (&acc)[NRT][NCT], const uint
         }
 }
 
-// gemm_lds_packed with a pre-split A (two-plane modes): k-blocks akb0 .. akb0+KBA-1 of a
-// fragment buffer holding aKB k-blocks per row tile; same B prefetch rings (RING: the ring
-// of four for one output tile as well, where the caller has the registers for it).
-template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false, bool RING = (NCT == 2)>
-__device__ __forceinline__ void gemm_frag_packed(v16f (&acc)[NRT][NCT], const uint4 *abuf, int aKB, int akb0,
-                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
+// gemm_lds_packed with a pre-split A (two-plane modes): k-blocks akb0 .. akb0+KBA-1 of the
+// fragments asrc holds (AFragBuf, AFragRows); same B prefetch rings (RING: the ring of four
+// for one output tile as well, where the caller has the registers for it).
+template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false, bool RING = (NCT == 2), class ASRC>
+__device__ __forceinline__ void gemm_frag_src(v16f (&acc)[NRT][NCT], const ASRC &asrc, int akb0,
+                                              const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
     static_assert(Npl<MODE>::v == 2, "two-plane modes");
     if constexpr (RING) {
         static_assert(KBA % 4 == 0, "ring of four");
@@ -478,13 +523,13 @@ __device__ __forceinline__ void gemm_frag_packed(v16f (&acc)[NRT][NCT], const ui
         load_bfrags<MODE, NCT>(b2, W, nt0, KBW, kb0 + 2, lane);
 #pragma unroll 1
         for (int kb = 0; kb < KBA; kb += 4) {
-            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb, W, nt0, KBW, kb0 + min(kb + 3, KBA - 1),
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, asrc, akb0 + kb, W, nt0, KBW, kb0 + min(kb + 3, KBA - 1),
                                                   b0, b3, lane);
-            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb + 1, W, nt0, KBW,
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, asrc, akb0 + kb + 1, W, nt0, KBW,
                                                   kb0 + min(kb + 4, KBA - 1), b1, b0, lane);
-            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb + 2, W, nt0, KBW,
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, asrc, akb0 + kb + 2, W, nt0, KBW,
                                                   kb0 + min(kb + 5, KBA - 1), b2, b1, lane);
-            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb + 3, W, nt0, KBW,
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, asrc, akb0 + kb + 3, W, nt0, KBW,
                                                   kb0 + min(kb + 6, KBA - 1), b3, b2, lane);
         }
     } else {
@@ -492,12 +537,19 @@ __device__ __forceinline__ void gemm_frag_packed(v16f (&acc)[NRT][NCT], const ui
         load_bfrags<MODE, NCT>(cur, W, nt0, KBW, kb0, lane);
 #pragma unroll 2
         for (int kb = 0; kb < KBA; ++kb) {
-            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, abuf, aKB, akb0 + kb, W, nt0, KBW, kb0 + min(kb + 1, KBA - 1),
+            gemm_frag_step<MODE, NRT, NCT, TRANS>(acc, asrc, akb0 + kb, W, nt0, KBW, kb0 + min(kb + 1, KBA - 1),
                                                   cur, nxt, lane);
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) cur[ct] = nxt[ct];
         }
     }
+}
+
+// gemm_frag_src from a fragment buffer holding aKB k-blocks per row tile.
+template <int MODE, int NRT, int NCT, int KBA, bool TRANS = false, bool RING = (NCT == 2)>
+__device__ __forceinline__ void gemm_frag_packed(v16f (&acc)[NRT][NCT], const uint4 *abuf, int aKB, int akb0,
+                                                 const uint4 *__restrict__ W, int nt0, int KBW, int kb0, int lane) {
+    gemm_frag_src<MODE, NRT, NCT, KBA, TRANS, RING>(acc, AFragBuf{abuf, aKB}, akb0, W, nt0, KBW, kb0, lane);
 }
 
 template <int NRT, int NCT>

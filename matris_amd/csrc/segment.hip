@@ -130,22 +130,24 @@ __device__ __forceinline__ float4 add4(const float4 &a, const float4 &b) {
 __device__ __forceinline__ float rows_combine(float v) {
     return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
 }
-// wt: global or LDS (a block's staged copy); the half-wave's lane 16 stores.
-__device__ __forceinline__ void proj_row_store(const float4 &t, int l, const float *wt, int K,
+// wt: global or LDS (a block's staged copy).  Lanes 16 .. 31 all end with the K sums;
+// lane 16 + k stores sum k (added to dst[k] with accumulate, whose load is issued first so
+// that the dot products cover its latency).
+__device__ __forceinline__ void proj_row_store(const float4 &t, int l, const float *wt, int K, int accumulate,
                                                float *__restrict__ dst) {
-    float p[MATRIS_PROJ_KMAX];
+    const int k_own = l - 16;
+    const bool owner = k_own >= 0 && k_own < K;
+    const float prev = (accumulate && owner) ? dst[k_own] : 0.f;
+    float mine = 0.f;
 #pragma unroll
     for (int k = 0; k < MATRIS_PROJ_KMAX; ++k) {
-        p[k] = 0.f;
         if (k < K) {
             const float4 w = *reinterpret_cast<const float4 *>(wt + k * MATRIS_D + 4 * l);
-            p[k] = rows_combine(row16_sum(t.x * w.x + t.y * w.y + t.z * w.z + t.w * w.w));
+            const float pk = rows_combine(row16_sum(t.x * w.x + t.y * w.y + t.z * w.z + t.w * w.w));
+            if (k == k_own) mine = pk;
         }
     }
-    if (l == 16)
-#pragma unroll
-        for (int k = 0; k < MATRIS_PROJ_KMAX; ++k)
-            if (k < K) dst[k] = p[k];
+    if (owner) dst[k_own] = accumulate ? prev + mine : mine;
 }
 
 template <bool MUL>
@@ -252,7 +254,8 @@ __device__ __forceinline__ void seg_rows4(const SegSrc &v, int64_t s0, int64_t n
 }
 
 // With proj_w (a [K, 128] transposed Linear weight), each segment's row is projected
-// (proj_row_store) into proj_out [n_seg, K] instead of being written to out.
+// (proj_row_store) into proj_out [n_seg, K] (added to it with accumulate) instead of being
+// written to out.
 template <bool MUL, bool PROJ = false>
 __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, int64_t n_seg, int accumulate,
                                                             const float *__restrict__ base,
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(256) void seg_sum_short_kernel(SegSrc a, SegSrc b, 
         float4 t = make_float4(ta[j].x * a.scale, ta[j].y * a.scale, ta[j].z * a.scale, ta[j].w * a.scale);
         if (b.x) t = add4(t, make_float4(tb[j].x * b.scale, tb[j].y * b.scale, tb[j].z * b.scale, tb[j].w * b.scale));
         if constexpr (PROJ) {  // uniform over the wave: s < n_seg is the same for all its lanes
-            proj_row_store(t, l, wts, proj_k, proj_out + s * proj_k);
+            proj_row_store(t, l, wts, proj_k, accumulate, proj_out + s * proj_k);
             continue;
         }
         float *op = out + s * MATRIS_D + c;
@@ -306,7 +309,7 @@ static bool seg_src_ok(const SegSrc &v) {
 
 // proj_w / proj_k / proj_out: project each segment's row onto the K rows of proj_w
 // ([K, 128], K <= 8) into proj_out [n_seg, K] instead of writing out (short segments only:
-// rows_hint <= 4 n_seg; no accumulate or base).
+// rows_hint <= 4 n_seg; no base; accumulate adds to proj_out).
 static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64_t rows_hint, int accumulate,
                           float *out, void *stream, const float *base = nullptr, const float *base_w = nullptr,
                           const float *proj_w = nullptr, int proj_k = 0, float *proj_out = nullptr) {
@@ -315,7 +318,7 @@ static int seg_sum_launch(const SegSrc &a, const SegSrc &b, int64_t n_seg, int64
     // itself (0: every segment is empty and projects to zeros)
     const bool short_segs = (rows_hint > 0 || proj_w) && rows_hint >= 0 && rows_hint <= 4 * n_seg;
     if (proj_w) {
-        if (!proj_out || proj_k < 1 || proj_k > MATRIS_PROJ_KMAX || !short_segs || accumulate || base)
+        if (!proj_out || proj_k < 1 || proj_k > MATRIS_PROJ_KMAX || !short_segs || base)
             return MATRIS_E_ARG;
     } else if (!out) {
         return MATRIS_E_ARG;
@@ -394,11 +397,12 @@ extern "C" int matris_seg_sum_mul(int64_t n_seg, int64_t rows_hint, const float 
 extern "C" int matris_seg_sum_mul_proj(int64_t n_seg, int64_t rows_hint, const float *x, int64_t ldx,
                                        int64_t col_off, const int32_t *rowptr, const int32_t *perm, const float *mul,
                                        const int32_t *mul_idx, float scale, const float *proj_w, int proj_k,
-                                       float *proj_out, void *stream) {
+                                       int accumulate, float *proj_out, void *stream) {
     if (!mul || !proj_w || ((uintptr_t)proj_w & 15)) return MATRIS_E_ARG;
     const SegSrc a{x, ldx, col_off, rowptr, perm, scale, mul, mul_idx};
     const SegSrc none{nullptr, MATRIS_D, 0, nullptr, nullptr, 0.f, nullptr, nullptr};
-    return seg_sum_launch(a, none, n_seg, rows_hint, 0, nullptr, stream, nullptr, nullptr, proj_w, proj_k, proj_out);
+    return seg_sum_launch(a, none, n_seg, rows_hint, accumulate, nullptr, stream, nullptr, nullptr, proj_w, proj_k,
+                          proj_out);
 }
 
 // ------------------------------------------------------------------------------------
@@ -731,6 +735,30 @@ __global__ __launch_bounds__(1024) void edge_geom_bwd_final_kernel(int64_t n_ato
 #pragma unroll
             for (int j = 0; j < 3; ++j) g_strain[3 * i + j] = 0.5f * (gs[3 * i + j] + gs[3 * j + i]);
     }
+}
+
+// Cartesian positions of one graph, cart[i] = frac[i] L (a row vector times the lattice,
+// each column summed in index order with FMA), and the zero strain [3, 3] the stress is
+// taken against (zero9, optional), in one launch.
+__global__ __launch_bounds__(256) void frac_cart_kernel(int64_t n, const float *__restrict__ frac,
+                                                        const float *__restrict__ lat, float *__restrict__ cart,
+                                                        float *__restrict__ zero9) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (zero9 && i < 9) zero9[i] = 0.f;
+    if (i >= n) return;
+    const float f0 = frac[3 * i], f1 = frac[3 * i + 1], f2 = frac[3 * i + 2];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) cart[3 * i + j] = fmaf(f2, lat[6 + j], fmaf(f1, lat[3 + j], f0 * lat[j]));
+}
+
+extern "C" int matris_frac_to_cart(int64_t n, const float *frac, const float *lattice, float *cart,
+                                   float *strain_zero, void *stream) {
+    if (n < 0 || (n > 0 && (!frac || !lattice || !cart))) return MATRIS_E_ARG;
+    if (n == 0 && !strain_zero) return 0;
+    frac_cart_kernel<<<matris_blocks(n > 9 ? n : 9, 256), 256, 0, (hipStream_t)stream>>>(n, frac, lattice, cart,
+                                                                                         strain_zero);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
 }
 
 static inline int geom_parts(int64_t n_edges) {
@@ -1133,7 +1161,8 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
                                                               const int32_t *__restrict__ s_perm,
                                                               const int32_t *__restrict__ t_idx,
                                                               float *__restrict__ g_env, float *__restrict__ ge,
-                                                              const float *__restrict__ proj_w, int proj_k) {
+                                                              const float *__restrict__ proj_w, int proj_k,
+                                                              int accumulate) {
     __shared__ __align__(16) float wts[PROJ ? MATRIS_PROJ_KMAX * MATRIS_D : 4];
     if constexpr (PROJ) {  // the block's copy of wt (before any wave leaves)
         for (int q = threadIdx.x; q < proj_k * MATRIS_D / 4; q += blockDim.x)
@@ -1179,7 +1208,7 @@ __global__ __launch_bounds__(256) void env_agg_bwd_env_kernel(int64_t n_seg, con
     }
     const float4 gv = make_float4(gs.x * sv.x + t.x, gs.y * sv.y + t.y, gs.z * sv.z + t.z, gs.w * sv.w + t.w);
     if constexpr (PROJ)  // g_env projected onto the envelope's basis: [n_seg, K]
-        proj_row_store(gv, threadIdx.x & 31, wts, proj_k, g_env + seg * proj_k);
+        proj_row_store(gv, threadIdx.x & 31, wts, proj_k, accumulate, g_env + seg * proj_k);
     else
         st4(g_env + seg * MATRIS_D + c, gv);
 }
@@ -1211,7 +1240,7 @@ extern "C" int matris_env_agg_bwd(int64_t n_rows, int64_t n_seg, const float *h,
     }
     if (n_seg > 0) {
         env_agg_bwd_env_kernel<false><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, st>>>(
-            n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, nullptr, nullptr, 0);
+            n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, nullptr, nullptr, 0, 0);
         MATRIS_CHECK_LAUNCH();
     }
     return 0;
@@ -1226,15 +1255,15 @@ extern "C" int matris_env_agg_bwd_env(int64_t n_seg, const float *h, const float
         return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
     env_agg_bwd_env_kernel<false><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
-        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, g_agg_env, nullptr, 0);
+        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_env, g_agg_env, nullptr, 0, 0);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }
 
 extern "C" int matris_env_agg_bwd_env_proj(int64_t n_seg, const float *h, const float *env, const float *g_agg,
                                            const float *S, const int32_t *t_idx, const int32_t *s_ptr,
-                                           const int32_t *s_perm, const float *proj_w, int proj_k, float *g_basis,
-                                           float *g_agg_env, void *stream) {
+                                           const int32_t *s_perm, const float *proj_w, int proj_k, int accumulate,
+                                           float *g_basis, float *g_agg_env, void *stream) {
     if (n_seg < 0 || !h || !env || !g_agg || !S || !t_idx || !s_ptr || !g_basis || !proj_w || proj_k < 1 ||
         proj_k > MATRIS_PROJ_KMAX)
         return MATRIS_E_ARG;
@@ -1243,7 +1272,7 @@ extern "C" int matris_env_agg_bwd_env_proj(int64_t n_seg, const float *h, const 
         return MATRIS_E_ARG;
     if (n_seg == 0) return 0;
     env_agg_bwd_env_kernel<true><<<matris_blocks(n_seg, WAVES_PER_BLOCK), 256, 0, (hipStream_t)stream>>>(
-        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_basis, g_agg_env, proj_w, proj_k);
+        n_seg, h, env, g_agg, S, s_ptr, s_perm, t_idx, g_basis, g_agg_env, proj_w, proj_k, accumulate);
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

@@ -264,13 +264,13 @@ def _one_graph(g, topo, compute_stress, n_atoms, N, E, U, A) -> dict:
     edge geometry (processgraph.py:169-199) in one launch (ops.edge_geometry) and the
     topology's columns used as they are (no per-call concatenations or casts).  Only the
     position leaf (frac @ lattice, processgraph.py:87) and the zero strain are made
-    besides it, so the host issues few operations before the first layer."""
+    besides it, both in one more launch (ops.frac_to_cart), so the host issues few
+    operations before the first layer."""
     lat = g.lattice.detach()
-    cart = g.atom_frac_coord.detach() @ lat
+    cart, strains = ops.frac_to_cart(g.atom_frac_coord.detach(), lat, compute_stress)
     cart.requires_grad_(True)
-    strains = None
-    if compute_stress:
-        strains = torch.zeros((1, 3, 3), dtype=torch.float32, device=lat.device, requires_grad=True)
+    if strains is not None:
+        strains.requires_grad_(True)
     grp_tgt, grp_src = topo["grp_tgt"], topo["grp_src"]
     length, unit, lattice, volumes = ops.edge_geometry(cart, strains, lat, g.neighbor_image, grp_tgt, grp_src)
     out = dict(atomic_numbers=g.atomic_number, edge_lengths=length, unit_edge_vectors=unit,

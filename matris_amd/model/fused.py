@@ -21,7 +21,7 @@ from . import ops
 from .ops import D
 
 __all__ = ["line_attention", "line_refinement", "line_attention_fusable", "line_refinement_fusable",
-           "checkpoint_needed"]
+           "checkpoint_needed", "shared_grad"]
 
 # Approximate saved-activation bytes per interaction block when nothing is recomputed:
 # per angle, line attention p_e, z_e [256] + a_s, a_t, e [128] and line refinement
@@ -66,6 +66,82 @@ def blocks_to_checkpoint(n_angles: int, n_edges: int, n_blocks: int, device=None
 def checkpoint_needed(n_angles: int, n_edges: int, n_blocks: int, device=None, total_bytes: int | None = None) -> bool:
     """Whether any interaction block is checkpointed (blocks_to_checkpoint > 0)."""
     return blocks_to_checkpoint(n_angles, n_edges, n_blocks, device, total_bytes) > 0
+
+
+# ------------------------------------------------------------------------------------
+# one gradient buffer for a tensor read by several fused layers
+# ------------------------------------------------------------------------------------
+class GradAccumulator:
+    """The gradient of a tensor that several fused layers read (the smooth basis of every
+    block's Refinement, a block's attended atom features), built in one buffer: the first
+    layer's backward writes it, later ones add to it inside their kernels, so autograd
+    issues no separate add per extra reader."""
+    __slots__ = ("buf",)
+
+    def __init__(self):
+        self.buf = None
+
+
+class _GradSink(torch.autograd.Function):
+    """y = x, with y's fused readers leaving their x-gradients in a GradAccumulator; the
+    backward returns that buffer plus whatever reached y through autograd itself."""
+
+    @staticmethod
+    def forward(ctx, x, acc):
+        ctx.acc = acc
+        ctx.set_materialize_grads(False)
+        return x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        buf, ctx.acc.buf = ctx.acc.buf, None
+        if g is not None:
+            buf = g if buf is None else buf + g
+        return buf, None
+
+
+def shared_grad(x: torch.Tensor) -> torch.Tensor:
+    """x itself, marked so that the fused layers reading it accumulate their x-gradients in
+    one buffer (the Refinements' basis and atom inputs).  Readers that are not fused
+    layers return their gradients through autograd as usual; the two are added."""
+    if not (torch.is_grad_enabled() and x.requires_grad):
+        return x
+    acc = GradAccumulator()
+    y = _GradSink.apply(x, acc)
+    y._matris_grad_acc = acc
+    return y
+
+
+def _acc_of(t):
+    return getattr(t, "_matris_grad_acc", None)
+
+
+def _acc_out(acc):
+    """(out, accumulate) for a kernel writing this reader's gradient: the accumulator's
+    buffer to add to, or a new output when it is empty or there is none."""
+    if acc is None or acc.buf is None:
+        return None, False
+    return acc.buf, True
+
+
+def _acc_keep(acc, g):
+    """Leave g (the reader's gradient, already added to acc.buf when that existed) in the
+    accumulator; returns what the reader hands autograd (None when acc took it)."""
+    if acc is None:
+        return g
+    acc.buf = g
+    return None
+
+
+def _acc_add(acc, g):
+    """g computed on its own: added to the accumulator (or kept as its first term)."""
+    if acc is None:
+        return g
+    if acc.buf is None:
+        acc.buf = g
+    else:
+        acc.buf.add_(g)
+    return None
 
 
 def _zeros_if_none(g, like):
@@ -225,6 +301,7 @@ class _LineRefinement(torch.autograd.Function):
     @staticmethod
     def forward(ctx, tb, atom, bond, basis, layer, lg, recompute):
         ops._check_dev(tb, atom, bond, basis)
+        ctx.acc_atom, ctx.acc_basis = _acc_of(atom), _acc_of(basis)
         tb, atom, bond, basis = (ops._f32c(t) for t in (tb, atom, bond, basis))
         mode = ops._MMA["mode"]
         env = ops.env_linear_raw(basis, _env_wt(layer))
@@ -262,7 +339,9 @@ class _LineRefinement(torch.autograd.Function):
         g_agg = ops.ffn_bwd_raw(pn, g_bond_new, p_dn, mode, g_res=g_bond, res_w=r_n)
         # the envelope's gradient leaves projected onto its basis (the learnable envelope's
         # input gradient), so the [E, 128] g_env is never stored
-        g_basis, g_agg_env = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src, proj_wt=_env_wt(layer))
+        g_basis, g_agg_env = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src, proj_wt=_env_wt(layer),
+                                                     g_basis=_acc_out(ctx.acc_basis)[0])
+        g_basis = _acc_keep(ctx.acc_basis, g_basis)
         del h
         # g_h = edge_FFN's input gradient + the aggregate's term; g_tb = source 0's
         # GatedMLP gradient + r_e g_tb_new.  In the two-plane modes g_h never leaves the
@@ -282,7 +361,9 @@ class _LineRefinement(torch.autograd.Function):
                                    res_src=g_tb_new, runs=_runs(tgt, 2))
             del g_h
         del p_de, g_agg_env, p_h, z_h
-        g_atom = ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0)
+        out, acc = _acc_out(ctx.acc_atom)
+        g_atom = _acc_keep(ctx.acc_atom, ops.seg_sum_raw(g_x, lg["grp_atom"], ldx=3 * D, col_off=0, out=out,
+                                                         accumulate=acc))
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_bond, accumulate=True,
                         second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
         return g_tb, g_atom, g_bond, g_basis, None, None, None
@@ -391,6 +472,7 @@ class _AtomRefinement(torch.autograd.Function):
     @staticmethod
     def forward(ctx, atom, bond, basis, layer, ag, d2u):
         ops._check_dev(atom, bond, basis)
+        ctx.acc_atom, ctx.acc_basis = _acc_of(atom), _acc_of(basis)
         atom, bond = ops._f32c(atom), ops._f32c(bond)
         env = ops.env_linear_raw(basis, _env_wt(layer))
         mode = ops._MMA["mode"]
@@ -418,6 +500,7 @@ class _AtomRefinement(torch.autograd.Function):
         bond_new = ops.seg_sum_raw(de, d2u, 0.5, base=(bond, r_e))
         ctx.save_for_backward(w, h, p_h, z_h, p_dn, p_de)  # w = env[d2u] if smoothed, else env
         ctx.mode, ctx.layer, ctx.ag, ctx.d2u, ctx.smoothed = mode, layer, ag, d2u, smoothed
+        ctx.set_materialize_grads(False)  # the last block's bond' is unused: its gradient is None
         return atom_new, bond_new
 
     @staticmethod
@@ -432,7 +515,6 @@ class _AtomRefinement(torch.autograd.Function):
         r_n, r_e = ops._vec(layer.node_res_weight), ops._vec(layer.edge_res_weight)
         N = p_dn.shape[0]
         g_atom_new = _zeros_if_none(g_atom_new, p_dn)
-        g_bond_new = _zeros_if_none(g_bond_new, ops._rows(d2u.n_seg, D, h.device))
         g_atom = ops._rows(N, D, h.device)
         g_agg = ops.ffn_bwd_raw(pn, g_atom_new, p_dn, mode, g_res=g_atom, res_w=r_n)
         del p_dn
@@ -440,15 +522,26 @@ class _AtomRefinement(torch.autograd.Function):
             # g_h = edge_FFN's input gradient (from half the bond gradient of each directed
             # copy) + g_agg[tgt] * env[d2u], computed per tile inside the GatedMLP backward;
             # g_env = sum_{d2u} h * g_agg[tgt] leaves projected onto the envelope's basis
-            g_basis = ops.seg_sum_mul_proj_raw(h, d2u, g_agg, tgt.key, _env_wt(layer))
+            g_basis = ops.seg_sum_mul_proj_raw(h, d2u, g_agg, tgt.key, _env_wt(layer),
+                                               out=_acc_out(ctx.acc_basis)[0])
+            g_basis = _acc_keep(ctx.acc_basis, g_basis)
             del h
-            g_x = ops.gmlp_bwd_ffn_raw(ph, p_h, z_h, 3 * D, mode, pm, g_bond_new, p_de, env_term=(g_agg, w, tgt, d2u),
-                                       runs=_runs(tgt, 1), ffn_g_idx=d2u.key, ffn_g_scale=0.5)
-            del p_h, z_h, p_de, w
-            g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
+            if g_bond_new is None:
+                # bond' unused: no edge_FFN or residual term, g_h is the aggregate's term alone
+                g_h = ops.gather_mul_raw(g_agg, tgt.key, w, d2u.key, out=ops._rows(d2u.key.numel(), D, w.device))
+                g_x = ops.gmlp_bwd_raw(ph, g_h, p_h, z_h, 3 * D, mode, runs=_runs(tgt, 1))
+                del g_h, p_h, z_h, p_de, w
+                g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0)
+            else:
+                g_x = ops.gmlp_bwd_ffn_raw(ph, p_h, z_h, 3 * D, mode, pm, g_bond_new, p_de,
+                                           env_term=(g_agg, w, tgt, d2u), runs=_runs(tgt, 1), ffn_g_idx=d2u.key,
+                                           ffn_g_scale=0.5)
+                del p_h, z_h, p_de, w
+                g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
             ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
                             second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
-            return g_atom, g_bond, g_basis, None, None, None
+            return _acc_add(ctx.acc_atom, g_atom), g_bond, g_basis, None, None, None
+        g_bond_new = _zeros_if_none(g_bond_new, ops._rows(d2u.n_seg, D, h.device))
         g_te = ops.ffn_bwd_raw(pm, ops.gather_raw(g_bond_new, d2u.key, 0.5), p_de, mode)
         del p_de
         if ctx.smoothed:
@@ -466,7 +559,8 @@ class _AtomRefinement(torch.autograd.Function):
         g_bond = ops.seg_sum_raw(g_x, d2u, ldx=3 * D, col_off=0, base=(g_bond_new, r_e))
         ops.seg_sum_raw(g_x, tgt, ldx=3 * D, col_off=D, out=g_atom, accumulate=True,
                         second=(g_x, src, 1.0, 3 * D, 2 * D), tile_rows=_tile_rows(tgt))
-        return g_atom, g_bond, g_env @ _env_wt(layer).t(), None, None, None
+        return (_acc_add(ctx.acc_atom, g_atom), g_bond, _acc_add(ctx.acc_basis, g_env @ _env_wt(layer).t()), None,
+                None, None)
 
 
 def atom_attention(layer, atom, bond, ag, d2u):

@@ -482,6 +482,8 @@ class Interaction_Block(nn.Module):
         if threebody_feat is not None:
             attn_edge, attn_tb = self.attn_block_line_graph(edge_feat, threebody_feat, lg, recompute=rc)
         attn_node, attn_edge = self.attn_block_atom_graph(node_feat, attn_edge, ag, d2u)
+        # read by both Refinements: their fused backwards build its gradient in one buffer
+        attn_node = fused.shared_grad(attn_node)
         if threebody_feat is not None:
             upd_edge, upd_tb = self.refine_block_line_graph(attn_edge, attn_tb, smooth_weight["line graph"], lg,
                                                             atom_feat=attn_node, recompute=rc)
@@ -668,6 +670,8 @@ class MatRIS(nn.Module):
             n_ckpt = max(0, min(int(self.block_checkpoint), n_blocks))
         node = self.atom_embedding.embed(bg["atomic_numbers"])
         edge, smooth = self.edge_embedding(graphs=bg)
+        # each basis is read by the Refinement of every block: one gradient buffer each
+        smooth = {k: fused.shared_grad(v) for k, v in smooth.items()}
         tb = None
         if bg["n_angles"] != 0:
             tb = self.three_body_embedding(graphs=bg)

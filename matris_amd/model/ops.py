@@ -153,6 +153,12 @@ def _f32c(t):
     return t if t.is_contiguous() else t.contiguous()
 
 
+def _check_out(t, shape):
+    """An output buffer a kernel adds to: fp32, contiguous, on the device, of this shape."""
+    if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda or tuple(t.shape) != tuple(shape):
+        raise ValueError(f"output buffer must be a contiguous fp32 device tensor of shape {tuple(shape)}")
+
+
 @dataclass
 class Grouping:
     """Rows grouped by an int32 key: rows of segment s are perm[rowptr[s]:rowptr[s+1]]
@@ -299,17 +305,24 @@ def seg_sum_mul_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: 
 
 
 def seg_sum_mul_proj_raw(x: torch.Tensor, grp: Grouping, mul: torch.Tensor, mul_idx: torch.Tensor,
-                         proj_wt: torch.Tensor) -> torch.Tensor:
+                         proj_wt: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """[n_seg, K]: the segment sums of seg_sum_mul_raw(x, grp, mul, mul_idx) times W, with
     proj_wt = W^T [K, 128] (matris_seg_sum_mul_proj; short segments: at most 4 rows per
-    segment on average, e.g. the two directed copies of each bond)."""
+    segment on average, e.g. the two directed copies of each bond).  Added to `out` when
+    it is given (fp32 contiguous [n_seg, K])."""
     lib = _lib.load()
     wt = _f32c(proj_wt)
-    out = torch.empty(grp.n_seg, wt.shape[0], dtype=torch.float32, device=x.device)
-    nb = _seg_src_bytes(grp) + 4 * D * mul.shape[0] + 4 * grp.n_rows + 4 * wt.shape[0] * grp.n_seg
+    acc = out is not None
+    if acc:
+        _check_out(out, (grp.n_seg, wt.shape[0]))
+    else:
+        out = torch.empty(grp.n_seg, wt.shape[0], dtype=torch.float32, device=x.device)
+    nb = (_seg_src_bytes(grp) + 4 * D * mul.shape[0] + 4 * grp.n_rows
+          + (2 if acc else 1) * 4 * wt.shape[0] * grp.n_seg)
     with _timed("seg_sum", dict(rows=grp.n_rows, segs=grp.n_seg, kind="mul_proj", bytes=nb)):
         _lib.check(lib.matris_seg_sum_mul_proj(grp.n_seg, grp.n_rows, _p(x), D, 0, _p(grp.rowptr), _p(grp.perm),
-                                               _p(mul), _p(mul_idx), 1.0, _p(wt), wt.shape[0], _p(out), _stream()),
+                                               _p(mul), _p(mul_idx), 1.0, _p(wt), wt.shape[0], int(acc), _p(out),
+                                               _stream()),
                    "matris_seg_sum_mul_proj")
     return out
 
@@ -404,6 +417,22 @@ class _EdgeGeometry(torch.autograd.Function):
                                                         _p(partial), _p(g_cart), _p(g_strain), _stream()),
                        "matris_edge_geom_bwd")
         return g_cart, g_strain, None, None, None, None
+
+
+def frac_to_cart(frac: torch.Tensor, lattice: torch.Tensor, with_strain: bool):
+    """(cart [N, 3] = frac @ lattice, zero strain [1, 3, 3] or None) of one graph in one
+    launch (matris_frac_to_cart; processgraph.py:87 and :173-177), both new tensors without
+    autograd history: the caller makes them the leaves forces and stress differentiate."""
+    _check_dev(frac, lattice)
+    frac, lattice = _f32c(frac), _f32c(lattice)
+    if frac.dim() != 2 or frac.shape[1] != 3 or tuple(lattice.shape) != (3, 3):
+        raise ValueError("frac_to_cart: frac must be [N, 3] and lattice [3, 3]")
+    lib = _lib.load()
+    cart = torch.empty_like(frac)
+    strain = torch.empty((1, 3, 3), dtype=torch.float32, device=frac.device) if with_strain else None
+    _lib.check(lib.matris_frac_to_cart(frac.shape[0], _p(frac), _p(lattice), _p(cart), _p(strain), _stream()),
+               "matris_frac_to_cart")
+    return cart, strain
 
 
 def edge_geometry(cart, strain, lattice, image, tgt: "Grouping", src: "Grouping"):
@@ -564,24 +593,29 @@ def env_agg_fwd_raw(h, env, tgt: Grouping, src: Grouping):
     return agg, S
 
 
-def env_agg_bwd_env_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, proj_wt=None):
+def env_agg_bwd_env_raw(h, env, g_agg, S, tgt: Grouping, src: Grouping, proj_wt=None, g_basis=None):
     """(g_env, g_agg_env) of matris_env_agg_bwd_env: g_env as env_agg_bwd_raw returns it and
     g_agg_env = g_agg * env, the per-bond factor ffn_bwd_raw(..., env_term=...) takes.  With
     proj_wt (the envelope's Linear(K, 128) weight transposed, [K, 128]) the first result is
-    g_env W [E, K], the gradient of the envelope's basis (matris_env_agg_bwd_env_proj)."""
+    g_env W [E, K], the gradient of the envelope's basis (matris_env_agg_bwd_env_proj),
+    added to g_basis when that is given."""
     lib = _lib.load()
     E = env.shape[0]
     ge = _rows(E, D, h.device)
     if proj_wt is not None:
         wt = _f32c(proj_wt)
-        g_basis = torch.empty(E, wt.shape[0], dtype=torch.float32, device=h.device)
+        acc = g_basis is not None
+        if acc:
+            _check_out(g_basis, (E, wt.shape[0]))
+        else:
+            g_basis = torch.empty(E, wt.shape[0], dtype=torch.float32, device=h.device)
         A = h.shape[0]
         # in: h [A], env, g_agg, S [E] (S saved), target keys, source permutation and pointers;
-        # out: g_basis [E, K], g_agg * env [E]
-        nb = 4 * D * (A + 3 * E) + 4 * D * E + 4 * wt.shape[0] * E + 8 * A + 4 * (E + 1)
+        # out: g_basis [E, K] (read too when accumulating), g_agg * env [E]
+        nb = 4 * D * (A + 3 * E) + 4 * D * E + (2 if acc else 1) * 4 * wt.shape[0] * E + 8 * A + 4 * (E + 1)
         with _timed("env_agg_bwd", dict(rows=A, segs=E, bytes=nb, saved_bytes=4 * D * E)):
             _lib.check(lib.matris_env_agg_bwd_env_proj(E, _p(h), _p(env), _p(g_agg), _p(S), _p(tgt.key),
-                                                       _p(src.rowptr), _p(src.perm), _p(wt), wt.shape[0],
+                                                       _p(src.rowptr), _p(src.perm), _p(wt), wt.shape[0], int(acc),
                                                        _p(g_basis), _p(ge), _stream()), "matris_env_agg_bwd_env_proj")
         return g_basis, ge
     g_env = _rows(E, D, h.device)

@@ -127,6 +127,26 @@ def test_seg_sum_narrow(lengths, width):
     assert torch.equal(out, ops.seg_sum_narrow_raw(x, ptr, len(lengths)))
 
 
+@pytest.mark.parametrize("N", [864, 1, 0, 300])
+def test_frac_to_cart(N):
+    """matris_frac_to_cart: positions frac @ lattice (processgraph.py:87) against the fp64
+    product, and the zero strain written in the same launch."""
+    ops = _ops()
+    torch.manual_seed(N + 3)
+    frac = torch.rand(N, 3, device=DEV)
+    lat = (torch.eye(3) * 9.0 + torch.randn(3, 3)).to(DEV)
+    cart, strain = ops.frac_to_cart(frac, lat, True)
+    ref = frac.double().cpu() @ lat.double().cpu()
+    assert tuple(cart.shape) == (N, 3) and tuple(strain.shape) == (1, 3, 3)
+    if N:
+        assert float((cart.double().cpu() - ref).abs().max()) < 4e-6
+    assert torch.equal(strain.cpu(), torch.zeros(1, 3, 3))
+    cart2, none = ops.frac_to_cart(frac, lat, False)
+    assert none is None and torch.equal(cart2, cart)
+    with pytest.raises(ValueError):
+        ops.frac_to_cart(frac, lat[:2], True)
+
+
 @pytest.mark.parametrize("E,K", [(33698, 7), (1, 7), (0, 7), (513, 1), (777, 8), (100, 3)])
 def test_env_linear(E, K):
     """matris_env_linear: the learnable envelope env = basis W^T (interaction_block.py:
@@ -168,6 +188,11 @@ def test_seg_sum_mul_proj(R, E_u, K):
     assert _rel(g_basis, ref) < 2e-6
     plain = ops.seg_sum_mul_raw(h, grp, g_agg, tk)
     assert _rel(plain.double().cpu() @ w.double().cpu(), ref) < 2e-6
+    # accumulate: added to an existing buffer (the blocks sharing one basis)
+    base = torch.randn(E_u, K, device=DEV)
+    acc = base.clone()
+    assert ops.seg_sum_mul_proj_raw(h, grp, g_agg, tk, w.t().contiguous(), out=acc) is acc
+    assert _rel(acc, base.double().cpu() + ref) < 2e-6
 
 
 @pytest.mark.parametrize("A,E,K", [(264384, 33698, 7), (3000, 400, 7), (50, 9, 8)])
@@ -190,6 +215,12 @@ def test_env_agg_bwd_env_proj(A, E, K):
     assert torch.equal(ge, ge2)
     assert tuple(g_basis.shape) == (E, K)
     assert _rel(g_basis, g_env.double().cpu() @ w.double().cpu()) < 2e-6
+    # accumulate into an existing g_basis: that buffer plus the same projection, bitwise
+    base = torch.randn(E, K, device=DEV)
+    acc = base.clone()
+    out, ge3 = ops.env_agg_bwd_env_raw(h, env, g_agg, S, tgt, src, proj_wt=w.t().contiguous(), g_basis=acc)
+    assert out is acc and torch.equal(ge, ge3)
+    assert torch.equal(acc, base + g_basis)
 
 
 @pytest.mark.parametrize("R,S,T", [(67396, 864, 33698), (5000, 800, 300), (37, 5, 11), (0, 4, 3), (67396, 33698, 864),

@@ -124,11 +124,15 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_seg_sum_narrow(4, v16, v16, 0, v16, None) == -1001
     assert lib.matris_seg_sum_narrow(4, v16, v16, 33, v16, None) == -1001
     assert lib.matris_seg_sum_narrow(0, None, None, 9, None, None) == 0
-    assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 0, v16, None) == -1001
-    assert lib.matris_seg_sum_mul_proj(4, 40, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, v16, None) == -1001
-    assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, None, None) == -1001
-    assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, v16, 9, v16, v16, None) == -1001
-    assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, None, 7, v16, v16, None) == -1001
+    assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 0, 0, v16, None) == -1001
+    assert lib.matris_seg_sum_mul_proj(4, 40, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, 1, v16, None) == -1001
+    assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, 0, None, None) == -1001
+    assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, v16, 9, 0, v16, v16, None) == -1001
+    assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, None, 7, 1, v16, v16, None) == -1001
+    # positions: a negative count, atoms without a lattice; nothing to do without atoms or strain
+    assert lib.matris_frac_to_cart(-1, v16, v16, v16, None, None) == -1001
+    assert lib.matris_frac_to_cart(3, v16, None, v16, v16, None) == -1001
+    assert lib.matris_frac_to_cart(0, None, None, None, None, None) == 0
     assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
     # neighbour-list reuse: no atoms; a workspace below its size; a non-positive cutoff
     big = 1 << 20
