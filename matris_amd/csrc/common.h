@@ -22,6 +22,16 @@ static inline int matris_blocks(int64_t work, int per_block) {
     return (int)(b < 1 ? 1 : b);
 }
 
+// The work-group's place in the grid with each XCD given one contiguous range: the
+// hardware deals work-groups to the 8 XCDs round-robin (group b to XCD b % 8), so
+// neighbouring groups -- which read neighbouring segments' rows and the rows those share
+// -- would otherwise sit behind eight different L2s.  A bijection of [0, gridDim.x).
+__device__ __forceinline__ int64_t xcd_block() {
+    const int64_t nb = gridDim.x, b = blockIdx.x;
+    const int64_t q = nb >> 3, r = nb & 7, x = b & 7;
+    return x * q + (x < r ? x : r) + (b >> 3);
+}
+
 // Work-group barrier that orders LDS only: the fences are scoped to the local address
 // space, so the barrier waits for this wave's LDS operations but leaves global loads
 // (prefetches) in flight, where __syncthreads() would drain them all.

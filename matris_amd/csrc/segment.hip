@@ -861,7 +861,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(int64_t n_seg, const floa
                                                        float *__restrict__ lse_s) {
     // wave w -> segment w / 2, side w % 2: the two sides of nearby segments run together,
     // so the source side's second read of e' rows tends to find them still in cache
-    int64_t w = (int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    // the atom-graph launch (N segments, rows gathered from the bonds' logits) reads less
+    // from HBM with each XCD on one range of atoms; the line-graph launch is faster with
+    // the hardware's round-robin spread
+    int64_t w = (HAS_AIDX ? xcd_block() : (int64_t)blockIdx.x) * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     if (w >= 2 * n_seg) return;
     const bool src_side = w & 1;
     const int64_t seg = w >> 1;
