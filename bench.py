@@ -77,6 +77,8 @@ def _parse():
     ap.add_argument("--no-c2", action="store_true")
     ap.add_argument("--no-c4", action="store_true")
     ap.add_argument("--c5-only", action="store_true", help="run only the C5 MD line (for profiling)")
+    ap.add_argument("--c4-only", action="store_true",
+                    help="run only the C4 batch line, --steps timed evaluations after --warmup (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp32-mfma", action="store_true", help="skip the plain fp32 MFMA (MODE 0) C3 step time")
     ap.add_argument("--cpu-sample-reps", type=int, default=6,
@@ -409,6 +411,9 @@ def main():
     model = MatRIS(**MATRIS_10M).to(dev).eval()
     if args.c5_only:
         print(json.dumps({"c5_md": c5_md(model, dev, args.c5_steps, args.c5_warmup)}), flush=True)
+        return
+    if args.c4_only:
+        print(json.dumps({"c4_batch": c4_batch(model, dev, args.steps, args.warmup)}), flush=True)
         return
     cr = W.c3_cu864()
     g = model.graph_converter(cr)

@@ -217,7 +217,10 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     atom_segment = topo["atom_segment"]
     atoms_len = topo["atoms_len"]
     lat3 = lattice.reshape(G, 3, 3)
-    volumes = torch.einsum("ni,ni->n", lat3[:, 0], torch.linalg.cross(lat3[:, 1], lat3[:, 2]))[:, None, None]
+    # The small products below are written as broadcast products and sums over the
+    # 3-wide axis: as batched GEMMs of 3x3 blocks (one per atom, per edge) the library
+    # runs them far below bandwidth.
+    volumes = (lat3[:, 0] * torch.linalg.cross(lat3[:, 1], lat3[:, 2])).sum(1)[:, None, None]
 
     # strain trick (processgraph.py:169-189)
     cart.requires_grad_(True)
@@ -227,10 +230,10 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         sym = 0.5 * (strains + strains.transpose(-1, -2))
         if G == 1:  # one graph: the per-atom strain is a broadcast, not a gather
             cart = cart + cart @ sym[0]
-        else:
-            cart = cart + torch.bmm(cart.unsqueeze(1), _GraphBroadcast.apply(sym, atoms_len, N,
-                                                                             topo["atom_rowptr"])).squeeze(1)
-        lat3 = lat3 + torch.matmul(lat3, sym)
+        else:  # cart[n] sym[graph(n)]
+            sym_n = _GraphBroadcast.apply(sym, atoms_len, N, topo["atom_rowptr"])
+            cart = cart + (cart.unsqueeze(2) * sym_n).sum(1)
+        lat3 = lat3 + (lat3.unsqueeze(3) * sym.unsqueeze(1)).sum(2)  # lat3[g] sym[g]
         lattice = lat3.reshape(-1, 3)
 
     # edge geometry (processgraph.py:192-199); image . lattice of the edge's own graph
@@ -238,7 +241,7 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
         shift = _ImageShift.apply(image, lattice)
     else:
         lat_e = _GraphBroadcast.apply(lat3, topo["dir_len"], E, topo["dir_rowptr"])
-        shift = torch.bmm(image.unsqueeze(1), lat_e).squeeze(1)
+        shift = (image.unsqueeze(2) * lat_e).sum(1)  # image[e] lattice[graph(e)]
     vec = ops.edge_vectors(cart, shift, grp_tgt, grp_src)
     length = torch.norm(vec, dim=1)
     unit = vec / length[:, None]
