@@ -613,6 +613,23 @@ int matris_ffn_bwd_env(int64_t m, const float *g, const float *p, const void *w1
 int matris_pair_fwd(int64_t m, const float *x, const void *wp, float *out0, float *out1, int mode, void *stream);
 int matris_pair_bwd(int64_t m, const float *g0, const float *g1, const void *wtp, float *g_x, const float *res,
                     const float *res_w, int accumulate, int mode, void *stream);
+/* The line graph attention's backward with its logit projections' backward in one launch
+ * (interaction_block.py:104-134: Dimwise_softmax of W_s tb and W_t tb over the angle rows'
+ * source and target bonds, then source_weight_linear / target_weight_linear), replacing
+ * matris_attn_bwd + matris_pair_bwd on the line graph: per angle row r (t_idx, s_idx its
+ * target / source bond, int32),
+ *   p_t = exp(alpha_t[r] - lse_t[t]), p_s = exp(alpha_s[r] - lse_s[s]),
+ *   g_e[r] = base[r] + p_t g_yt[t] + p_s g_ys[s]                 (as matris_attn_bwd)
+ *   g_tb[r] = g_as W[0:128] + g_at W[128:256] + res_w * base[r]  (as matris_pair_bwd)
+ * with g_at = p_t g_yt[t] (e[r] - y_t[t]), g_as likewise, which are never written; wtp the
+ * pack of W^T ([128,256]) matris_pair_bwd takes.  alpha rows of stride lda, g_y rows of
+ * stride ldgy (both >= 128, multiples of 4), other rows 128 floats; base and res_w optional
+ * (res_w needs base).  Modes 0, 2, 3 (two fragment planes). */
+int matris_attn_pair_bwd(int64_t n_rows, const float *alpha_t, const float *alpha_s, int64_t lda, const float *e,
+                         const int32_t *t_idx, const int32_t *s_idx, const float *y_t, const float *y_s,
+                         const float *lse_t, const float *lse_s, const float *g_yt, const float *g_ys, int64_t ldgy,
+                         const float *base, const void *wtp, const float *res_w, int mode, float *g_e, float *g_tb,
+                         void *stream);
 
 /* Three-body embedding (row E3's consumer): tb = SiLU(Ws (Wa b)) for b [m, 16] the angle
  * basis, wa = Wa [128, 16] row-major fp32 (angle_embedding, no bias), wsp = Ws [128, 128]

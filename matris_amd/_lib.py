@@ -144,6 +144,8 @@ _SIGS = {
     "matris_ffn_bwd_env": (_I, [_I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "matris_pair_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
     "matris_pair_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    "matris_attn_pair_bwd": (_I, [_I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I, _P, _P,
+                                  _P]),
     "matris_tb_embed_fwd": (_I, [_I64, _P, _P, _P, _P, _I, _P]),
     "matris_tb_embed_bwd": (_I, [_I64, _P, _P, _P, _P, _P, _P, _I, _P]),
 }

@@ -870,6 +870,105 @@ __global__ __launch_bounds__(256, 3) void pair_bwd_kernel(int64_t M, const float
 }
 
 // ------------------------------------------------------------------------------------
+// Line-graph attention backward with the logit projections' input gradient
+// (interaction_block.py:104-134: the two softmaxes' backward, then that of
+// source_weight_linear / target_weight_linear, which read the same angle rows): per row r,
+// t = t_idx[r], s = s_idx[r],
+//   p_t = exp(alpha_t[r] - lse_t[t]),  p_s = exp(alpha_s[r] - lse_s[s])
+//   g_e[r]  = base[r] + p_t g_yt[t] + p_s g_ys[s]
+//   g_at    = p_t g_yt[t] (e[r] - y_t[t]),  g_as = p_s g_ys[s] (e[r] - y_s[s])
+//   g_tb[r] = g_as W_s + g_at W_t + res_w * base[r]
+// with Wt the pack matris_pair_bwd takes (k-blocks 0..7 pair with g_as, 8..15 with g_at).
+// The logit gradients never reach memory: a 64-row tile converts g_at into pre-split rows
+// in LDS (rowfrag_put4) and holds g_as in registers until g_at's product is in, then
+// converts g_as into the same rows -- one power-of-two scale per row for both in MODE 2.
+// Rows: a half-wave per row, 4 columns per lane, the arithmetic of matris_attn_bwd (g_e is
+// the same bits).  Two-plane modes.
+// ------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(256, 3) void attn_pair_bwd_kernel(
+    int64_t M, const float *__restrict__ alpha_t, const float *__restrict__ alpha_s, int64_t lda,
+    const float *__restrict__ e, const int32_t *__restrict__ t_idx, const int32_t *__restrict__ s_idx,
+    const float *__restrict__ y_t, const float *__restrict__ y_s, const float *__restrict__ lse_t,
+    const float *__restrict__ lse_s, const float *__restrict__ g_yt, const float *__restrict__ g_ys, int64_t ldgy,
+    const float *__restrict__ base, const uint4 *__restrict__ Wt, const float *__restrict__ res_w,
+    float *__restrict__ g_e, float *__restrict__ g_tb, unsigned *range_flag) {
+    static_assert(Npl<MODE>::v == 2, "two-plane modes");
+    __shared__ __align__(16) float T[BM * LDT];  // pre-split rows (128 floats of each), then the g_tb tile
+    __shared__ float rinv[BM];                   // MODE 2: 2^-k of each row's g_at / g_as scaling
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+    const int c = 4 * l32;
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const float ws = take_wscale<MODE>(Wt);
+    float amax = 0.f;
+    float4 gs_keep[BM / 8];
+#pragma unroll
+    for (int i = 0; i < BM / 8; ++i) {
+        const int row = wave * (BM / 4) + 2 * i + half;
+        const int64_t r = m0 + row;
+        const bool in = r < M;
+        const int64_t rr = in ? r : M - 1;  // rows past M read row M-1 and count as zeros
+        const int64_t t = t_idx[rr], s = s_idx[rr];
+        const float4 at = *reinterpret_cast<const float4 *>(alpha_t + rr * lda + c);
+        const float4 as = *reinterpret_cast<const float4 *>(alpha_s + rr * lda + c);
+        const float4 ev = *reinterpret_cast<const float4 *>(e + rr * MATRIS_D + c);
+        const float4 lt = *reinterpret_cast<const float4 *>(lse_t + t * MATRIS_D + c);
+        const float4 ls = *reinterpret_cast<const float4 *>(lse_s + s * MATRIS_D + c);
+        const float4 gt = *reinterpret_cast<const float4 *>(g_yt + t * ldgy + c);
+        const float4 gs = *reinterpret_cast<const float4 *>(g_ys + s * ldgy + c);
+        const float4 yt = *reinterpret_cast<const float4 *>(y_t + t * MATRIS_D + c);
+        const float4 ys = *reinterpret_cast<const float4 *>(y_s + s * MATRIS_D + c);
+        float4 ge = base ? *reinterpret_cast<const float4 *>(base + rr * MATRIS_D + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 gat, gas;
+#define ATTN_PAIR_COL(k)                                                       \
+    {                                                                          \
+        const float pt = exp_neg_f(lt.k - at.k), ps = exp_neg_f(ls.k - as.k); \
+        ge.k += pt * gt.k + ps * gs.k;                                         \
+        gat.k = pt * gt.k * (ev.k - yt.k);                                     \
+        gas.k = ps * gs.k * (ev.k - ys.k);                                     \
+    }
+        ATTN_PAIR_COL(x) ATTN_PAIR_COL(y) ATTN_PAIR_COL(z) ATTN_PAIR_COL(w)
+#undef ATTN_PAIR_COL
+        if (in) {
+            *reinterpret_cast<float4 *>(g_e + r * MATRIS_D + c) = ge;
+        } else {
+            gat = gas = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if constexpr (MODE == 2) {  // one scale for the row's 256 values (both sums meet in g_tb)
+            float mx = row16_max(abs_max4(abs_max4(0.f, gat), gas));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            const RowScale rs = row_scale(mx);
+            gat = mul4(gat, rs.s);
+            gas = mul4(gas, rs.s);
+            if (l32 == 0) rinv[row] = rs.inv;
+        }
+        amax = frag_amax<MODE>(amax, gat, gas);
+        rowfrag_put4<MODE>(T + row * LDT, c, gat);
+        gs_keep[i] = gas;
+        // at most two row pairs of loads in flight: the registers of 16 would spill
+        if (i & 1) __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    // wave w: g_tb columns [32w, 32w + 32), rows in lanes
+    v16f acc[2][1];
+    zero_acc(acc);
+    gemm_frag_src<MODE, 2, 1, MATRIS_D / 16, true>(acc, AFragRows{T, LDT}, 0, Wt, wave, 256 / 16, MATRIS_D / 16,
+                                                   lane);
+    __syncthreads();  // every wave is done reading g_at
+#pragma unroll
+    for (int i = 0; i < BM / 8; ++i) rowfrag_put4<MODE>(T + (wave * (BM / 4) + 2 * i + half) * LDT, c, gs_keep[i]);
+    __syncthreads();
+    gemm_frag_src<MODE, 2, 1, MATRIS_D / 16, true>(acc, AFragRows{T, LDT}, 0, Wt, wave, 256 / 16, 0, lane);
+    scale_acc<MODE>(acc, ws);
+    unscale_rows_t<MODE, 1>(acc, rinv, l32);
+    __syncthreads();  // every wave is done reading g_as
+    acc_t_to_lds<2, 1>(acc, T, LDT, wave * 32, lane);
+    __syncthreads();
+    store_tile128(T, g_tb, MATRIS_D, m0, M, tid, base, res_w);
+    report_range<MODE>(amax, range_flag);
+}
+
+// ------------------------------------------------------------------------------------
 // C ABI
 // ------------------------------------------------------------------------------------
 // ------------------------------------------------------------------------------------
@@ -1330,6 +1429,36 @@ extern "C" int matris_pair_bwd(int64_t m, const float *g0, const float *g1, cons
     if (res && (((uintptr_t)res & 15) || !res_w || ((uintptr_t)res_w & 15))) return MATRIS_E_ARG;
     if (m == 0) return 0;
     MLP_DISPATCH(pair_bwd_kernel, m, g0, g1, (const uint4 *)wtp, g_x, res, res_w, accumulate);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_attn_pair_bwd(int64_t n_rows, const float *alpha_t, const float *alpha_s, int64_t lda,
+                                    const float *e, const int32_t *t_idx, const int32_t *s_idx, const float *y_t,
+                                    const float *y_s, const float *lse_t, const float *lse_s, const float *g_yt,
+                                    const float *g_ys, int64_t ldgy, const float *base, const void *wtp,
+                                    const float *res_w, int mode, float *g_e, float *g_tb, void *stream) {
+    if (n_rows < 0 || (mode != 0 && mode != 2 && mode != 3)) return MATRIS_E_ARG;
+    if (lda < MATRIS_D || (lda % 4) || ldgy < MATRIS_D || (ldgy % 4)) return MATRIS_E_ARG;
+    if (!mlp_args_ok(mode, {alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, wtp, g_e, g_tb}) || !t_idx ||
+        !s_idx)
+        return MATRIS_E_ARG;
+    if ((base && ((uintptr_t)base & 15)) || (res_w && (!base || ((uintptr_t)res_w & 15)))) return MATRIS_E_ARG;
+    if (n_rows == 0) return 0;
+    unsigned *flag = nullptr;
+    if (mode == 2 && !(flag = matris_range_flag())) return MATRIS_E_ARG;
+    const dim3 grid(matris_blocks(n_rows, BM));
+    hipStream_t st = (hipStream_t)stream;
+    const uint4 *w = (const uint4 *)wtp;
+#define ATTN_PAIR_ARGS n_rows, alpha_t, alpha_s, lda, e, t_idx, s_idx, y_t, y_s, lse_t, lse_s, g_yt, g_ys, ldgy, base, w, \
+                       res_w, g_e, g_tb, flag
+    if (mode == 0)
+        attn_pair_bwd_kernel<0><<<grid, 256, 0, st>>>(ATTN_PAIR_ARGS);
+    else if (mode == 2)
+        attn_pair_bwd_kernel<2><<<grid, 256, 0, st>>>(ATTN_PAIR_ARGS);
+    else
+        attn_pair_bwd_kernel<3><<<grid, 256, 0, st>>>(ATTN_PAIR_ARGS);
+#undef ATTN_PAIR_ARGS
     MATRIS_CHECK_LAUNCH();
     return 0;
 }

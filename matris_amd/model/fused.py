@@ -247,26 +247,29 @@ class _LineAttention(torch.autograd.Function):
         g_bond = ops._rows(E, D, e.device)
         g_y = ops.gmlp_bwd_raw(pn, g_bond_new, p_n, z_n, 3 * D, mode, g_x0=g_bond, acc0=False, res_w=r_n)
         del p_n, z_n
-        # attention: g_e = g_tb_new (residual branch) + attention term
-        g_at, g_as, g_e = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, None,
-                                           ldgy=2 * D, g_e_base=g_tb_new)
-        del a_t, a_s, e, saved
-        # edge update: source 0's (tb) gradient to g_tb, the bond gathers' to g_x (the
-        # target-bond block, rows ascending by target, as tile-run partial sums)
-        g_tb = ops._rows(p_e.shape[0], D, p_e.device)
+        # attention: g_e = g_tb_new (residual branch) + attention term.  Edge update: source
+        # 0's (tb) gradient to g_tb, the bond gathers' to g_x (the target-bond block, rows
+        # ascending by target, as tile-run partial sums).
         if mode != 6:
-            # the projections' backward and the residual join source 0's gradient inside the
-            # GatedMLP backward: g_tb = tb's GatedMLP gradient + g_as W_s + g_at W_t + r_e g_tb_new
-            g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, res_w=r_e, res_src=g_tb_new,
-                                   runs=_runs(tgt, 1), pair=(pp, g_as, g_at))
+            # the attention's backward and the logit projections' in one launch: g_e, and
+            # g_tb = g_as W_s + g_at W_t + r_e g_tb_new (the logit gradients stay on chip),
+            # to which the GatedMLP backward adds tb's gradient
+            g_e, g_tb = ops.attn_pair_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, tgt, src, g_tb_new, pp, r_e,
+                                              mode)
+            del a_t, a_s, e, saved
+            g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=True, runs=_runs(tgt, 1))
             del g_e, p_e, z_e
         else:
+            g_at, g_as, g_e = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, D:], tgt, src, None,
+                                               ldgy=2 * D, g_e_base=g_tb_new)
+            del a_t, a_s, e, saved
+            g_tb = ops._rows(p_e.shape[0], D, p_e.device)
             g_x = ops.gmlp_bwd_raw(pe, g_e, p_e, z_e, 3 * D, mode, g_x0=g_tb, acc0=False, runs=_runs(tgt, 1))
             del g_e, p_e, z_e
             # projections + residual, added to g_tb by the pair kernel (which stores nothing
             # before its read-modify-write of g_tb)
             ops.pair_bwd_raw(pp, g_as, g_at, mode, res=g_tb_new, res_w=r_e, out=g_tb, accumulate=True)
-        del g_as, g_at
+            del g_as, g_at
         ops.seg_sum_raw(g_x, tgt, ldx=2 * D, col_off=0, out=g_bond, accumulate=True,
                         second=(g_x, src, 1.0, 2 * D, D), tile_rows=_tile_rows(tgt))
         return g_bond, g_tb, None, None, None

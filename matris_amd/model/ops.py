@@ -529,6 +529,29 @@ def attn_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: G
     return g_at, g_as, g_e
 
 
+def attn_pair_bwd_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_y, tgt: Grouping, src: Grouping, base,
+                      pair: "_WeightPack", res_w, mode: int):
+    """(g_e, g_tb) of matris_attn_pair_bwd on the line graph: g_e = base + attention term (as
+    attn_bwd_raw), g_tb = g_as W_s + g_at W_t + res_w * base (as pair_bwd_raw of attn_bwd_raw's
+    logit gradients, which are not materialised).  g_y = [g_yt | g_ys] rows of 256; modes
+    0, 2, 3."""
+    lib = _lib.load()
+    R, S = e.shape[0], tgt.n_seg
+    dev = e.device
+    g_e, g_tb = _rows(R, D, dev), _rows(R, D, dev)
+    if g_y.shape[1] != 2 * D or g_y.stride(0) != 2 * D:
+        raise ValueError("attn_pair_bwd_raw: g_y must be [S, 256] rows")
+    # in: alpha_t, alpha_s, e, base [R], g_y [S, 256]; out: g_e, g_tb [R]; keys; the saved
+    # statistics y_t, y_s, lse_t, lse_s counted apart
+    nb = 4 * D * (4 * R + 2 * S) + 4 * D * 2 * R + 8 * R
+    with _timed("attn_bwd_line", dict(rows=R, segs=S, bytes=nb, saved_bytes=4 * 4 * D * S, kind="pair")):
+        _lib.check(lib.matris_attn_pair_bwd(R, _p(alpha_t), _p(alpha_s), D, _p(e), _p(tgt.key), _p(src.key), _p(y_t),
+                                            _p(y_s), _p(lse_t), _p(lse_s), _p(g_y), _p(g_y[:, D:]), 2 * D, _p(base),
+                                            _p(pair.b("cat_t", mode)), _p(res_w), mode, _p(g_e), _p(g_tb),
+                                            _stream()), "matris_attn_pair_bwd")
+    return g_e, g_tb
+
+
 def attn_bwd_bond_raw(alpha_t, alpha_s, e, y_t, y_s, lse_t, lse_s, g_yt, g_ys, tgt: Grouping, src: Grouping,
                       d2u: Grouping, ldgy: int = D, g_base=None, base_scale: float = 1.0):
     """(g_alpha_t, g_alpha_s) per bond and g_e per directed row of matris_attn_bwd_bond: the

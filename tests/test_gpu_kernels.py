@@ -874,6 +874,42 @@ def test_gmlp_bwd_pair_tail(M, runs, mode, tol):
         ops.set_mma_precision(ops.DEFAULT_MMA)
 
 
+@pytest.mark.parametrize("mode,tol", [("f16x3", 1e-6), ("fp32", 1e-6), ("bf16x3", 1e-5)])
+@pytest.mark.parametrize("M,S", [(1, 1), (63, 9), (4097, 700), (70001, 9000)])
+def test_attn_pair_bwd(M, S, mode, tol):
+    """matris_attn_pair_bwd (the line attention's backward and its logit projections' in
+    one launch) against matris_attn_bwd followed by matris_pair_bwd of its logit gradients
+    with the residual term: g_e bit-identical, g_tb equal to a few fp32 roundings of its
+    largest value (the two k-halves are summed in the other order).  Statistics from
+    matris_attn_fwd on the same rows; targets ascending with empty segments, sources
+    random.  Rows past the last full tile and one-row segments included."""
+    ops = _ops()
+    ops.set_mma_precision(mode)
+    try:
+        torch.manual_seed(M + S)
+        mm = ops._MMA["mode"]
+        tkey = _sorted_keys(M, S, M + 5).to(DEV)
+        skey = _keys(M, S, M + 6).to(DEV)
+        tgt = ops.Grouping.build(tkey, S, sorted_rows=True)
+        src = ops.Grouping.build(skey, S)
+        a_t, a_s = 2 * torch.randn(M, 128, device=DEV), 2 * torch.randn(M, 128, device=DEV)
+        e = torch.randn(M, 128, device=DEV)
+        y_t, y_s, lse_t, lse_s = ops.attn_fwd_raw(a_t, a_s, e, tgt, src, None)
+        g_y = torch.randn(S, 256, device=DEV) * 1e-2
+        base = torch.randn(M, 128, device=DEV) * 1e-2
+        r = torch.rand(128, device=DEV)
+        pp = ops._WeightPack().get(torch.randn(128, 128, device=DEV) / 11, torch.randn(128, 128, device=DEV) / 11)
+        g_at, g_as, ge_ref = ops.attn_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, g_y[:, 128:], tgt, src, None,
+                                              ldgy=256, g_e_base=base)
+        gtb_ref = ops.pair_bwd_raw(pp, g_as, g_at, mm, res=base, res_w=r)
+        g_e, g_tb = ops.attn_pair_bwd_raw(a_t, a_s, e, y_t, y_s, lse_t, lse_s, g_y, tgt, src, base, pp, r, mm)
+        assert torch.equal(g_e, ge_ref)
+        assert _rel(g_tb, gtb_ref) < tol
+        assert ops.status_take() == 0
+    finally:
+        ops.set_mma_precision(ops.DEFAULT_MMA)
+
+
 @pytest.mark.parametrize("mode", ["f16x3", "fp32", "bf16x6"])
 @pytest.mark.parametrize("M", [1, 64, 4097, 70001])
 def test_gmlp_bwd_res_src(M, mode):

@@ -129,6 +129,12 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_seg_sum_mul_proj(4, 8, v16, 128, 0, v16, None, v16, v16, 1.0, v16, 7, 0, None, None) == -1001
     assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, v16, 9, 0, v16, v16, None) == -1001
     assert lib.matris_env_agg_bwd_env_proj(5, v16, v16, v16, v16, v16, v16, None, None, 7, 1, v16, v16, None) == -1001
+    # attention + pair backward: MODE 6 (three planes), a short row stride, res_w without base
+    pa = [v16, v16, 128, v16, v16, v16, v16, v16, v16, v16, v16, v16, 256, v16, v16, v16]
+    assert lib.matris_attn_pair_bwd(8, *pa, 6, v16, v16, None) == -1001
+    assert lib.matris_attn_pair_bwd(8, *pa[:2], 64, *pa[3:], 2, v16, v16, None) == -1001
+    assert lib.matris_attn_pair_bwd(8, *pa[:13], None, v16, v16, 2, v16, v16, None) == -1001
+    assert lib.matris_attn_pair_bwd(0, *pa, 2, v16, v16, None) == 0
     # positions: a negative count, atoms without a lattice; nothing to do without atoms or strain
     assert lib.matris_frac_to_cart(-1, v16, v16, v16, None, None) == -1001
     assert lib.matris_frac_to_cart(3, v16, None, v16, v16, None) == -1001
