@@ -141,13 +141,13 @@ def _gmlp_flops(M, K, tail_rows=0):
 # Keys: (launch name, config); a mean over that family's launches in one step where the
 # shapes differ.
 TRAFFIC_BYTES = {
-    ("gmlp_bwd", "C3"): 617.5e6,       # every launch shape, 420 launches; at M = A 1428.5 MB (line attention,
-                                       # with the pair projection) and 1525.8 MB (line refinement, with the FFN head)
-    ("gmlp_fwd", "C3"): 587.2e6,       # every launch shape, 420 launches; at M = A 1476.6 MB (line attention,
-                                       # with the pair projection) and 1337.9 MB (line refinement, with the FFN tail)
+    ("gmlp_bwd", "C3"): 559.8e6,       # every launch shape, 660 launches; at M = A 1129.8 MB (line attention,
+                                       # plain instance) and 1525.8 MB (line refinement, with the FFN head)
+    ("gmlp_fwd", "C3"): 588.6e6,       # every launch shape, 660 launches; at M = A 1483.7 MB (line attention,
+                                       # with the logit projections) and 1339.6 MB (line refinement, with the FFN tail)
     ("attn_fwd_line", "C3"): 580.4e6,  # 537.9 read + 42.5 written
     ("attn_fwd", "C2"): 4061.9e6,
-    ("attn_bwd", "C2"): 8450.3e6,
+    ("attn_bwd", "C2"): 8461.9e6,
     ("seg_sum", "C2"): 1048.1e6,
 }
 
