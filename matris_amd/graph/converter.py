@@ -3,7 +3,7 @@
 Mirrors the reference GraphConverter (matris/graph/converter.py:22-129): the same
 constructor arguments, `forward(structure, graph_id, mp_id) -> RadiusGraph`, the same
 RadiusGraph field dtypes and the same error behaviour (isolated atom -> ValueError;
-line-graph failure -> empty line graph).  The host work of the reference (pymatgen
+line-graph failure -> the structure written to error_graph.cif and an empty line graph).  The host work of the reference (pymatgen
 neighbour search, C/Cython pairing, the Python line-graph loop) is replaced by the
 gfx950 kernels of libmatris_hip.so, driven through the C ABI:
 
@@ -23,6 +23,7 @@ import torch
 from torch import nn
 
 from .. import _lib
+from .cif import write_cif
 from .radiusgraph import RadiusGraph, datatype
 
 
@@ -239,8 +240,12 @@ class GraphConverter(nn.Module):
         try:
             lg, angle_ptr = line_graph_device(n, center, neighbor, dist, row_ptr, d2u, u2d, u_second,
                                               self.line_graph_cutoff)
-        except RuntimeError as exc:  # converter.py:99-106 keeps an empty line graph
-            warnings.warn(f"line graph construction failed ({exc}); using an empty line graph")
+        except RuntimeError as exc:
+            # converter.py:99-106: the structure is dumped to error_graph.cif in the working
+            # directory and the graph keeps an empty line graph
+            write_cif("error_graph.cif", frac if frac is not None else f64.cpu().numpy(), lat, z)
+            warnings.warn(f"line graph construction failed ({exc}); the structure was written to "
+                          "error_graph.cif and the line graph is empty")
             lg = torch.zeros(0, 5, dtype=torch.int32, device=dev)
             angle_ptr = None
         atom_graph = torch.stack([center, neighbor], dim=1)
