@@ -256,6 +256,17 @@ int matris_edge_vec_bwd(int64_t n_atoms, const float *g_vec, const int32_t *t_pt
 int matris_frac_to_cart(int64_t n, const float *frac, const float *lattice, float *cart, float *strain_zero,
                         void *stream);
 
+/* The same for a disjoint batch of graphs (row P1, matris/model/processgraph.py:87 per
+ * graph, then the batch concatenation of :120-130): atom i of the batch uses the lattice of
+ * its graph, cart[i] = frac[i] lattice[graph_of_atom[i]] (frac, cart [n, 3], lattice
+ * [n_graphs, 3, 3], graph_of_atom [n] int32), in the same arithmetic as
+ * matris_frac_to_cart; with strain_zero non-NULL, strain_zero[0 .. 9 n_graphs - 1] = 0.
+ * An index outside [0, n_graphs) sets MATRIS_STATUS_CSR_KEY in the status word
+ * (matris_status_take) and leaves that atom's row unwritten.  One launch in place of one
+ * [n_g, 3] x [3, 3] product per graph. */
+int matris_frac_to_cart_batch(int64_t n, int64_t n_graphs, const float *frac, const float *lattice,
+                              const int32_t *graph_of_atom, float *cart, float *strain_zero, void *stream);
+
 /* Edge geometry of one graph with the strain trick (row P1, matris/model/processgraph.py:
  * 169-199: symmetric_strains, the strained positions and lattice, neighbor_pos + image @
  * lattice, edge_vectors, edge_lengths, unit_edge_vectors), forward in one launch.  With

@@ -751,6 +751,43 @@ __global__ __launch_bounds__(256) void frac_cart_kernel(int64_t n, const float *
     for (int j = 0; j < 3; ++j) cart[3 * i + j] = fmaf(f2, lat[6 + j], fmaf(f1, lat[3 + j], f0 * lat[j]));
 }
 
+// The same for a batch of graphs: atom i uses the lattice of its graph gidx[i]; an index
+// outside [0, n_graphs) sets MATRIS_STATUS_CSR_KEY in the status word and leaves the
+// atom's row unwritten.  zero: nz floats set to zero (the batch's zero strains).
+__global__ __launch_bounds__(256) void frac_cart_batch_kernel(int64_t n, int64_t n_graphs,
+                                                              const float *__restrict__ frac,
+                                                              const float *__restrict__ lat,
+                                                              const int32_t *__restrict__ gidx,
+                                                              float *__restrict__ cart, int64_t nz,
+                                                              float *__restrict__ zero, unsigned *status) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (zero && i < nz) zero[i] = 0.f;
+    if (i >= n) return;
+    const int g = gidx[i];
+    if (g < 0 || g >= n_graphs) {
+        atomicOr(status, (unsigned)MATRIS_STATUS_CSR_KEY);
+        return;
+    }
+    const float *L = lat + 9 * (int64_t)g;
+    const float f0 = frac[3 * i], f1 = frac[3 * i + 1], f2 = frac[3 * i + 2];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) cart[3 * i + j] = fmaf(f2, L[6 + j], fmaf(f1, L[3 + j], f0 * L[j]));
+}
+
+extern "C" int matris_frac_to_cart_batch(int64_t n, int64_t n_graphs, const float *frac, const float *lattice,
+                                         const int32_t *graph_of_atom, float *cart, float *strain_zero,
+                                         void *stream) {
+    if (n < 0 || n_graphs < 1 || (n > 0 && (!frac || !lattice || !graph_of_atom || !cart))) return MATRIS_E_ARG;
+    const int64_t nz = strain_zero ? 9 * n_graphs : 0;
+    if (n == 0 && nz == 0) return 0;
+    unsigned *status = matris_range_flag();
+    if (!status) return MATRIS_E_ARG;
+    frac_cart_batch_kernel<<<matris_blocks(n > nz ? n : nz, 256), 256, 0, (hipStream_t)stream>>>(
+        n, n_graphs, frac, lattice, graph_of_atom, cart, nz, strain_zero, status);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
 extern "C" int matris_frac_to_cart(int64_t n, const float *frac, const float *lattice, float *cart,
                                    float *strain_zero, void *stream) {
     if (n < 0 || (n > 0 && (!frac || !lattice || !cart))) return MATRIS_E_ARG;

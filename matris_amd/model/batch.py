@@ -129,7 +129,7 @@ def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
     t = dict(atom_graph=atom_graph, tgt=tgt32.long(), src=src32.long(), d2u32=d2u32, u2d32=u2d32,
              d2u64=d2u32.long(), u2d64=u2d32.long(), atom_segment=atom_segment, atoms_len=atoms_len,
              dir_len=dir_len, atoms_per_graph32=atoms_len.to(torch.int32), atom_rowptr=atom_rowptr,
-             dir_rowptr=dir_rowptr,
+             dir_rowptr=dir_rowptr, atom_graph32=atom_segment.to(torch.int32),
              grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True),
              grp_src=Grouping.build(src32, N, deferred=True),
              grp_d2u=Grouping.build(d2u32, U, sorted_rows=False, deferred=True))
@@ -200,23 +200,18 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
             graphs[0].neighbor_image.dtype == torch.float32:
         return _one_graph(graphs[0], topo, compute_stress, n_atoms, N, E, U, A)
 
-    carts, lats, imgs = [], [], []
-    for g in graphs:
-        frac = g.atom_frac_coord.detach()
-        lat = g.lattice.detach()
-        carts.append(frac @ lat)  # processgraph.py:87
-        lats.append(lat)
-        imgs.append(g.neighbor_image)
-
     atom_graph, tgt, src = topo["atom_graph"], topo["tgt"], topo["src"]
     d2u32, u2d32 = topo["d2u32"], topo["u2d32"]
     grp_tgt, grp_src = topo["grp_tgt"], topo["grp_src"]
-    lattice = torch.cat(lats, 0)  # [3G, 3]
-    cart = torch.cat(carts, 0)
-    image = torch.cat(imgs, 0)
+    lattice = torch.cat([g.lattice.detach() for g in graphs], 0)  # [3G, 3]
+    image = torch.cat([g.neighbor_image for g in graphs], 0)
     atom_segment = topo["atom_segment"]
     atoms_len = topo["atoms_len"]
     lat3 = lattice.reshape(G, 3, 3)
+    # processgraph.py:87 for every graph and the zero strains in one launch (each atom reads
+    # its own graph's lattice) instead of one small product per graph
+    frac = torch.cat([g.atom_frac_coord.detach() for g in graphs], 0)
+    cart, strains = ops.frac_to_cart_batch(frac.to(dtype), lat3, topo["atom_graph32"], compute_stress)
     # The small products below are written as broadcast products and sums over the
     # 3-wide axis: as batched GEMMs of 3x3 blocks (one per atom, per edge) the library
     # runs them far below bandwidth.
@@ -224,9 +219,8 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
 
     # strain trick (processgraph.py:169-189)
     cart.requires_grad_(True)
-    strains = None
     if compute_stress:
-        strains = torch.zeros((G, 3, 3), dtype=dtype, device=device, requires_grad=True)
+        strains.requires_grad_(True)
         sym = 0.5 * (strains + strains.transpose(-1, -2))
         if G == 1:  # one graph: the per-atom strain is a broadcast, not a gather
             cart = cart + cart @ sym[0]

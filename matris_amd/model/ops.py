@@ -435,6 +435,28 @@ def frac_to_cart(frac: torch.Tensor, lattice: torch.Tensor, with_strain: bool):
     return cart, strain
 
 
+def frac_to_cart_batch(frac: torch.Tensor, lattice: torch.Tensor, graph_of_atom: torch.Tensor, with_strain: bool):
+    """(cart [N, 3], zero strains [G, 3, 3] or None) of a disjoint batch in one launch
+    (matris_frac_to_cart_batch): cart[i] = frac[i] @ lattice[graph_of_atom[i]] with frac
+    [N, 3], lattice [G, 3, 3] and graph_of_atom [N] int32, the arithmetic of frac_to_cart
+    (processgraph.py:87 per graph).  New tensors without autograd history.  A graph index
+    outside [0, G) surfaces in the status word (STATUS_CSR_KEY)."""
+    _check_dev(frac, lattice, graph_of_atom)
+    frac, lattice = _f32c(frac), _f32c(lattice)
+    G = lattice.shape[0]
+    if frac.dim() != 2 or frac.shape[1] != 3 or lattice.dim() != 3 or tuple(lattice.shape[1:]) != (3, 3) or G < 1:
+        raise ValueError("frac_to_cart_batch: frac must be [N, 3] and lattice [G, 3, 3] with G >= 1")
+    if graph_of_atom.dtype != torch.int32 or tuple(graph_of_atom.shape) != (frac.shape[0],):
+        raise ValueError("frac_to_cart_batch: graph_of_atom must be int32 [N]")
+    graph_of_atom = graph_of_atom.contiguous()
+    lib = _lib.load()
+    cart = torch.empty_like(frac)
+    strain = torch.empty((G, 3, 3), dtype=torch.float32, device=frac.device) if with_strain else None
+    _lib.check(lib.matris_frac_to_cart_batch(frac.shape[0], G, _p(frac), _p(lattice), _p(graph_of_atom), _p(cart),
+                                             _p(strain), _stream()), "matris_frac_to_cart_batch")
+    return cart, strain
+
+
 def edge_geometry(cart, strain, lattice, image, tgt: "Grouping", src: "Grouping"):
     """(length [E], unit [E,3], strained lattice [3,3], volume [1,1,1]) of one graph:
     processgraph.py:169-199 with sym = (strain + strain^T)/2 applied to the positions and

@@ -147,6 +147,45 @@ def test_frac_to_cart(N):
         ops.frac_to_cart(frac, lat[:2], True)
 
 
+@pytest.mark.parametrize("sizes", [[24, 1, 64, 0, 8], [2162], [0, 0], [5] * 64])
+def test_frac_to_cart_batch(sizes):
+    """matris_frac_to_cart_batch: every atom's frac @ its own graph's lattice against the
+    fp64 products, bitwise equal to matris_frac_to_cart graph by graph (the one-graph path),
+    the zero strains of all graphs, and a graph index outside [0, G) reported in the status
+    word with the atom's row left as it was."""
+    ops = _ops()
+    G, N = len(sizes), sum(sizes)
+    torch.manual_seed(G * 7 + N)
+    frac = torch.rand(N, 3, device=DEV)
+    lat = (torch.eye(3) * 9.0 + torch.randn(G, 3, 3)).to(DEV)
+    gidx = torch.repeat_interleave(torch.arange(G), torch.tensor(sizes)).to(torch.int32).to(DEV)
+    ops.status_take()
+    cart, strain = ops.frac_to_cart_batch(frac, lat, gidx, True)
+    assert ops.status_take() == 0
+    assert tuple(cart.shape) == (N, 3) and tuple(strain.shape) == (G, 3, 3)
+    assert torch.equal(strain.cpu(), torch.zeros(G, 3, 3))
+    ref = torch.bmm(frac.double().cpu().unsqueeze(1), lat.double().cpu()[gidx.long().cpu()]).squeeze(1)
+    if N:
+        assert float((cart.double().cpu() - ref).abs().max()) < 4e-6
+    o = 0
+    for g, n in enumerate(sizes):
+        one, _ = ops.frac_to_cart(frac[o:o + n], lat[g], False)
+        assert torch.equal(one, cart[o:o + n])
+        o += n
+    cart2, none = ops.frac_to_cart_batch(frac, lat, gidx, False)
+    assert none is None and torch.equal(cart2, cart)
+    if N:
+        bad = gidx.clone()
+        bad[N - 1] = G  # one past the last graph: no read, a status bit
+        out = ops.frac_to_cart_batch(frac, lat, bad, False)[0]
+        assert ops.status_take() == ops.STATUS_CSR_KEY
+        assert torch.equal(out[:N - 1], cart[:N - 1])
+    with pytest.raises(ValueError):
+        ops.frac_to_cart_batch(frac, lat, gidx.long(), True)
+    with pytest.raises(ValueError):
+        ops.frac_to_cart_batch(frac, lat[:, :2], gidx, True)
+
+
 @pytest.mark.parametrize("E,K", [(33698, 7), (1, 7), (0, 7), (513, 1), (777, 8), (100, 3)])
 def test_env_linear(E, K):
     """matris_env_linear: the learnable envelope env = basis W^T (interaction_block.py:

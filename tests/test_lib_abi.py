@@ -139,6 +139,11 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_frac_to_cart(-1, v16, v16, v16, None, None) == -1001
     assert lib.matris_frac_to_cart(3, v16, None, v16, v16, None) == -1001
     assert lib.matris_frac_to_cart(0, None, None, None, None, None) == 0
+    # the batch form: no graphs; atoms without a graph index; nothing to do without atoms or strain
+    assert lib.matris_frac_to_cart_batch(3, 0, v16, v16, v16, v16, None, None) == -1001
+    assert lib.matris_frac_to_cart_batch(3, 2, v16, v16, None, v16, None, None) == -1001
+    assert lib.matris_frac_to_cart_batch(-1, 2, v16, v16, v16, v16, None, None) == -1001
+    assert lib.matris_frac_to_cart_batch(0, 2, None, None, None, None, None, None) == 0
     assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
     # neighbour-list reuse: no atoms; a workspace below its size; a non-positive cutoff
     big = 1 << 20
