@@ -296,6 +296,31 @@ int matris_edge_geom_bwd(int64_t n_atoms, int64_t n_edges, const float *g_length
                          const int32_t *s_ptr, const int32_t *s_perm, float *g_vec, float *partial, float *g_cart,
                          float *g_strain, void *stream);
 
+/* Edge geometry of a disjoint batch of graphs (row P1, processgraph.py:169-199 per graph,
+ * as the reference's batched tensors do it), forward in one launch: matris_edge_geom_fwd
+ * with edge e using the lattice and strain of its graph graph_of_edge[e] (int32 [E]);
+ * lattice [G,3,3], strain [G,3,3] or NULL, lattice_out [G,3,3] (the strained lattices),
+ * volume [G] (det of each unstrained lattice); cart [N,3] and tgt / src are the batch's
+ * (offset) atom rows.  A graph index outside [0, n_graphs) sets MATRIS_STATUS_CSR_KEY in the
+ * status word and leaves that edge's outputs unwritten. */
+int matris_edge_geom_fwd_batch(int64_t n_graphs, int64_t n_edges, const float *cart, const float *lattice,
+                               const float *strain, const float *image, const int32_t *tgt, const int32_t *src,
+                               const int32_t *graph_of_edge, float *length, float *unit, float *lattice_out,
+                               float *volume, void *stream);
+
+/* Backward of matris_edge_geom_fwd_batch (three launches): g_vec per edge, g_cart through
+ * the CSR groupings of tgt / src as in matris_edge_geom_bwd, then, with a strain, one
+ * work-group per graph over its atoms [atom_ptr[g], atom_ptr[g+1]) and edges
+ * [edge_ptr[g], edge_ptr[g+1]) (int32 [G+1] each: the batch's graphs are contiguous row
+ * ranges) for g_cart's strain term and g_strain [G,3,3] (when non-NULL).  Every sum runs in
+ * a fixed order (reproducible). */
+int matris_edge_geom_bwd_batch(int64_t n_graphs, int64_t n_atoms, int64_t n_edges, const float *g_length,
+                               const float *g_unit, const float *length, const float *unit, const float *cart,
+                               const float *lattice, const float *strain, const float *image, const int32_t *t_ptr,
+                               const int32_t *t_perm, const int32_t *s_ptr, const int32_t *s_perm,
+                               const int32_t *atom_ptr, const int32_t *edge_ptr, float *g_vec, float *g_cart,
+                               float *g_strain, void *stream);
+
 /* ------------------------------------------------------------------------------------
  * Segment attention (rows M2 + M4 / M5): Dimwise_softmax by target and by source,
  * alpha * e' and both segment sums, fused.  Replaces interaction_block.py:113-134 with

@@ -99,6 +99,8 @@ _SIGS = {
     "matris_frac_to_cart": (_I, [_I64, _P, _P, _P, _P, _P]),
     "matris_frac_to_cart_batch": (_I, [_I64, _I64, _P, _P, _P, _P, _P, _P]),
     "matris_edge_geom_bwd": (_I, [_I64, _I64] + [_P] * 17),
+    "matris_edge_geom_fwd_batch": (_I, [_I64, _I64] + [_P] * 11 + [_P]),
+    "matris_edge_geom_bwd_batch": (_I, [_I64, _I64, _I64] + [_P] * 17 + [_P]),
     "matris_attn_fwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "matris_attn_bwd": (_I, [_I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
                              _P]),

@@ -844,6 +844,217 @@ extern "C" int matris_edge_geom_bwd(int64_t n_atoms, int64_t n_edges, const floa
 }
 
 // ------------------------------------------------------------------------------------
+// Edge geometry of a disjoint batch of graphs: the kernels above with each edge (and, in
+// the backward, each graph's atoms and edges) using its own graph's lattice and strain.
+// ------------------------------------------------------------------------------------
+// Per edge e of graph gidx[e]: vec = x'[tgt] - (x'[src] + image L'_g) with the graph's
+// strain; threads g < n_graphs also write that graph's L'_g and det(L_g).  A graph index
+// outside [0, n_graphs) sets MATRIS_STATUS_CSR_KEY and leaves the edge's outputs unwritten.
+__global__ __launch_bounds__(256) void edge_geom_fwd_batch_kernel(int64_t n, int64_t n_graphs,
+                                                                  const float *__restrict__ cart,
+                                                                  const float *__restrict__ lat,
+                                                                  const float *__restrict__ S,
+                                                                  const float *__restrict__ image,
+                                                                  const int32_t *__restrict__ tgt,
+                                                                  const int32_t *__restrict__ src,
+                                                                  const int32_t *__restrict__ gidx,
+                                                                  float *__restrict__ len_out,
+                                                                  float *__restrict__ unit_out,
+                                                                  float *__restrict__ lat_out,
+                                                                  float *__restrict__ vol_out, unsigned *status) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    float sym[9], Ls[9];
+    if (e < n_graphs) {  // graph e's strained lattice and volume
+        const float *L = lat + 9 * e;
+        geom_sym(S ? S + 9 * e : nullptr, sym);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const float row[3] = {L[3 * i], L[3 * i + 1], L[3 * i + 2]};
+            geom_strain_row(row, sym, Ls + 3 * i);
+        }
+#pragma unroll
+        for (int k = 0; k < 9; ++k) lat_out[9 * e + k] = Ls[k];
+        const float c0 = L[4] * L[8] - L[5] * L[7];
+        const float c1 = L[5] * L[6] - L[3] * L[8];
+        const float c2 = L[3] * L[7] - L[4] * L[6];
+        vol_out[e] = L[0] * c0 + L[1] * c1 + L[2] * c2;
+    }
+    if (e >= n) return;
+    const int g = gidx[e];
+    if (g < 0 || g >= n_graphs) {
+        atomicOr(status, (unsigned)MATRIS_STATUS_CSR_KEY);
+        return;
+    }
+    const float *L = lat + 9 * (int64_t)g;
+    geom_sym(S ? S + 9 * (int64_t)g : nullptr, sym);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float row[3] = {L[3 * i], L[3 * i + 1], L[3 * i + 2]};
+        geom_strain_row(row, sym, Ls + 3 * i);
+    }
+    const int64_t t = tgt[e], s = src[e];
+    const float xt[3] = {cart[3 * t], cart[3 * t + 1], cart[3 * t + 2]};
+    const float xs[3] = {cart[3 * s], cart[3 * s + 1], cart[3 * s + 2]};
+    const float im[3] = {image[3 * e], image[3 * e + 1], image[3 * e + 2]};
+    float yt[3], ys[3], v[3];
+    geom_strain_row(xt, sym, yt);
+    geom_strain_row(xs, sym, ys);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        float sh = im[0] * Ls[j];
+        sh = fmaf(im[1], Ls[3 + j], sh);
+        sh = fmaf(im[2], Ls[6 + j], sh);
+        v[j] = yt[j] - (ys[j] + sh);
+    }
+    const float l = sqrtf(fmaf(v[2], v[2], fmaf(v[1], v[1], v[0] * v[0])));
+    len_out[e] = l;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) unit_out[3 * e + j] = v[j] / l;
+}
+
+// Per edge: g_vec = g_len unit + (g_unit - (g_unit . unit) unit) / len.
+__global__ __launch_bounds__(256) void edge_gvec_kernel(int64_t n, const float *__restrict__ g_len,
+                                                        const float *__restrict__ g_unit,
+                                                        const float *__restrict__ len,
+                                                        const float *__restrict__ unit, float *__restrict__ g_vec) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const float u[3] = {unit[3 * e], unit[3 * e + 1], unit[3 * e + 2]};
+    float gv[3] = {0.f, 0.f, 0.f};
+    if (g_len) {
+        const float gl = g_len[e];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) gv[j] = gl * u[j];
+    }
+    if (g_unit) {
+        const float gu[3] = {g_unit[3 * e], g_unit[3 * e + 1], g_unit[3 * e + 2]};
+        const float d = fmaf(gu[2], u[2], fmaf(gu[1], u[1], gu[0] * u[0]));
+        const float l = len[e];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) gv[j] += (gu[j] - d * u[j]) / l;
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) g_vec[3 * e + j] = gv[j];
+}
+
+// One work-group per graph g (its atoms [atom_ptr[g], atom_ptr[g+1]), its edges
+// [edge_ptr[g], edge_ptr[g+1])): P = sum_e image[e]^T g_vec[e], C = sum_a x_a^T g'_a, then
+//   g_cart = g' + g' sym^T,  g_sym = C + L^T (-P),  g_S = (g_sym + g_sym^T) / 2,
+// every sum in a fixed order (thread-strided, then the waves in order).
+__global__ __launch_bounds__(256) void edge_geom_bwd_graph_kernel(const int32_t *__restrict__ atom_ptr,
+                                                                  const int32_t *__restrict__ edge_ptr,
+                                                                  const float *__restrict__ g_vec,
+                                                                  const float *__restrict__ image,
+                                                                  const float *__restrict__ cart,
+                                                                  const float *__restrict__ lat,
+                                                                  const float *__restrict__ S,
+                                                                  float *__restrict__ g_cart,
+                                                                  float *__restrict__ g_strain) {
+    const int64_t g = blockIdx.x;
+    float sym[9], acc[18];
+    geom_sym(S + 9 * g, sym);
+#pragma unroll
+    for (int k = 0; k < 18; ++k) acc[k] = 0.f;
+    for (int64_t e = edge_ptr[g] + threadIdx.x; e < edge_ptr[g + 1]; e += 256) {
+        const float im[3] = {image[3 * e], image[3 * e + 1], image[3 * e + 2]};
+        const float gv[3] = {g_vec[3 * e], g_vec[3 * e + 1], g_vec[3 * e + 2]};
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc[3 * i + j] = fmaf(im[i], gv[j], acc[3 * i + j]);
+    }
+    for (int64_t a = atom_ptr[g] + threadIdx.x; a < atom_ptr[g + 1]; a += 256) {
+        const float gp[3] = {g_cart[3 * a], g_cart[3 * a + 1], g_cart[3 * a + 2]};
+        const float x[3] = {cart[3 * a], cart[3 * a + 1], cart[3 * a + 2]};
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc[9 + 3 * i + j] = fmaf(x[i], gp[j], acc[9 + 3 * i + j]);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {  // sym is symmetric: g sym^T = g sym
+            float t = gp[0] * sym[j];
+            t = fmaf(gp[1], sym[3 + j], t);
+            t = fmaf(gp[2], sym[6 + j], t);
+            g_cart[3 * a + j] = gp[j] + t;
+        }
+    }
+    __shared__ float part[4][18];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < 18; ++k) {
+        const float v = wave_sum(acc[k]);
+        if (lane == 0) part[w][k] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && g_strain) {
+        float tot[18], gs[9];
+#pragma unroll
+        for (int k = 0; k < 18; ++k) tot[k] = ((part[0][k] + part[1][k]) + part[2][k]) + part[3][k];
+        const float *L = lat + 9 * g;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {  // (L^T (-P))[i][j] = -sum_k L[k][i] P[k][j]
+                float t = L[i] * tot[j];
+                t = fmaf(L[3 + i], tot[3 + j], t);
+                t = fmaf(L[6 + i], tot[6 + j], t);
+                gs[3 * i + j] = tot[9 + 3 * i + j] - t;
+            }
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) g_strain[9 * g + 3 * i + j] = 0.5f * (gs[3 * i + j] + gs[3 * j + i]);
+    }
+}
+
+extern "C" int matris_edge_geom_fwd_batch(int64_t n_graphs, int64_t n_edges, const float *cart, const float *lattice,
+                                          const float *strain, const float *image, const int32_t *tgt,
+                                          const int32_t *src, const int32_t *graph_of_edge, float *length,
+                                          float *unit, float *lattice_out, float *volume, void *stream) {
+    if (n_graphs < 1 || n_edges < 0 || !lattice || !lattice_out || !volume) return MATRIS_E_ARG;
+    if (n_edges > 0 && (!cart || !image || !tgt || !src || !graph_of_edge || !length || !unit)) return MATRIS_E_ARG;
+    unsigned *status = matris_range_flag();
+    if (!status) return MATRIS_E_ARG;
+    const int64_t nt = n_edges > n_graphs ? n_edges : n_graphs;
+    edge_geom_fwd_batch_kernel<<<matris_blocks(nt, 256), 256, 0, (hipStream_t)stream>>>(
+        n_edges, n_graphs, cart, lattice, strain, image, tgt, src, graph_of_edge, length, unit, lattice_out, volume,
+        status);
+    MATRIS_CHECK_LAUNCH();
+    return 0;
+}
+
+extern "C" int matris_edge_geom_bwd_batch(int64_t n_graphs, int64_t n_atoms, int64_t n_edges, const float *g_length,
+                                          const float *g_unit, const float *length, const float *unit,
+                                          const float *cart, const float *lattice, const float *strain,
+                                          const float *image, const int32_t *t_ptr, const int32_t *t_perm,
+                                          const int32_t *s_ptr, const int32_t *s_perm, const int32_t *atom_ptr,
+                                          const int32_t *edge_ptr, float *g_vec, float *g_cart, float *g_strain,
+                                          void *stream) {
+    if (n_graphs < 1 || n_atoms < 0 || n_edges < 0 || !cart || !lattice || !t_ptr || !s_ptr || !g_cart)
+        return MATRIS_E_ARG;
+    if (n_edges > 0 && (!length || !unit || !image || !g_vec)) return MATRIS_E_ARG;
+    if (g_strain && !strain) return MATRIS_E_ARG;
+    if (strain && (!atom_ptr || !edge_ptr)) return MATRIS_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    if (n_edges > 0) {
+        edge_gvec_kernel<<<matris_blocks(n_edges, 256), 256, 0, st>>>(n_edges, g_length, g_unit, length, unit,
+                                                                      g_vec);
+        MATRIS_CHECK_LAUNCH();
+    }
+    if (n_atoms > 0) {
+        edge_vec_bwd_kernel<<<matris_blocks(n_atoms, WAVES_PER_BLOCK), 256, 0, st>>>(n_atoms, g_vec, t_ptr, t_perm,
+                                                                                     s_ptr, s_perm, g_cart);
+        MATRIS_CHECK_LAUNCH();
+    }
+    if (strain) {  // per graph: g' -> g_cart through the strained positions, and the strain's gradient
+        edge_geom_bwd_graph_kernel<<<(unsigned)n_graphs, 256, 0, st>>>(atom_ptr, edge_ptr, g_vec, image, cart,
+                                                                       lattice, strain, g_cart, g_strain);
+        MATRIS_CHECK_LAUNCH();
+    }
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------
 // segment attention forward: one wave per (segment, side).  Each half-wave owns every
 // other row of the segment with 16-byte lanes (4 columns) and runs an online softmax
 // taken eight of its rows at a time (sixteen rows of loads in flight per wave), then four,

@@ -17,42 +17,6 @@ from . import ops
 from .ops import Grouping
 
 
-class _ImageShift(torch.autograd.Function):
-    """shift = image @ lattice ([E, 3] x [3, 3]) whose lattice gradient, image^T g ([3, E]
-    x [E, 3]), is a 9-value reduction over the edges: summed as one elementwise product
-    and a reduction instead of a matrix product with K = E (which the library GEMM runs
-    far below bandwidth)."""
-
-    @staticmethod
-    def forward(ctx, image, lattice):
-        ctx.save_for_backward(image)
-        return image @ lattice
-
-    @staticmethod
-    def backward(ctx, g):
-        (image,) = ctx.saved_tensors
-        g_lat = (image[:, :, None] * g[:, None, :]).sum(0) if ctx.needs_input_grad[1] else None
-        return None, g_lat
-
-
-class _GraphBroadcast(torch.autograd.Function):
-    """x [G, ...] repeated lengths[g] times per graph (rows contiguous per graph, int32 row
-    pointers rowptr), with the backward summed per graph in a fixed order
-    (ops.seg_sum_narrow_raw instead of the atomic index_add_ of an indexing backward), so
-    batched stresses are reproducible."""
-
-    @staticmethod
-    def forward(ctx, x, lengths, total, rowptr):
-        ctx.save_for_backward(rowptr)
-        ctx.n = x.shape[0]
-        return torch.repeat_interleave(x, lengths, dim=0, output_size=total)
-
-    @staticmethod
-    def backward(ctx, g):
-        (rowptr,) = ctx.saved_tensors
-        return ops.seg_sum_narrow_raw(g, rowptr, ctx.n), None, None, None
-
-
 def _sorted(x: torch.Tensor) -> bool:
     return x.numel() < 2 or bool((x[1:] >= x[:-1]).all().item())
 
@@ -130,6 +94,9 @@ def _topology(graphs, n_atoms, n_dir, n_und, n_ang) -> dict:
              d2u64=d2u32.long(), u2d64=u2d32.long(), atom_segment=atom_segment, atoms_len=atoms_len,
              dir_len=dir_len, atoms_per_graph32=atoms_len.to(torch.int32), atom_rowptr=atom_rowptr,
              dir_rowptr=dir_rowptr, atom_graph32=atom_segment.to(torch.int32),
+             dir_graph32=(torch.zeros(E, dtype=torch.int32, device=device) if len(graphs) == 1 else
+                          torch.repeat_interleave(torch.arange(len(graphs), device=device, dtype=torch.int32),
+                                                  dir_len, output_size=E)),
              grp_tgt=Grouping.build(tgt32, N, sorted_rows=canonical or _sorted(tgt32), deferred=True),
              grp_src=Grouping.build(src32, N, deferred=True),
              grp_d2u=Grouping.build(d2u32, U, sorted_rows=False, deferred=True))
@@ -206,39 +173,20 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     lattice = torch.cat([g.lattice.detach() for g in graphs], 0)  # [3G, 3]
     image = torch.cat([g.neighbor_image for g in graphs], 0)
     atom_segment = topo["atom_segment"]
-    atoms_len = topo["atoms_len"]
     lat3 = lattice.reshape(G, 3, 3)
     # processgraph.py:87 for every graph and the zero strains in one launch (each atom reads
     # its own graph's lattice) instead of one small product per graph
     frac = torch.cat([g.atom_frac_coord.detach() for g in graphs], 0)
     cart, strains = ops.frac_to_cart_batch(frac.to(dtype), lat3, topo["atom_graph32"], compute_stress)
-    # The small products below are written as broadcast products and sums over the
-    # 3-wide axis: as batched GEMMs of 3x3 blocks (one per atom, per edge) the library
-    # runs them far below bandwidth.
-    volumes = (lat3[:, 0] * torch.linalg.cross(lat3[:, 1], lat3[:, 2])).sum(1)[:, None, None]
-
-    # strain trick (processgraph.py:169-189)
     cart.requires_grad_(True)
-    if compute_stress:
+    if strains is not None:
         strains.requires_grad_(True)
-        sym = 0.5 * (strains + strains.transpose(-1, -2))
-        if G == 1:  # one graph: the per-atom strain is a broadcast, not a gather
-            cart = cart + cart @ sym[0]
-        else:  # cart[n] sym[graph(n)]
-            sym_n = _GraphBroadcast.apply(sym, atoms_len, N, topo["atom_rowptr"])
-            cart = cart + (cart.unsqueeze(2) * sym_n).sum(1)
-        lat3 = lat3 + (lat3.unsqueeze(3) * sym.unsqueeze(1)).sum(2)  # lat3[g] sym[g]
-        lattice = lat3.reshape(-1, 3)
-
-    # edge geometry (processgraph.py:192-199); image . lattice of the edge's own graph
-    if G == 1:
-        shift = _ImageShift.apply(image, lattice)
-    else:
-        lat_e = _GraphBroadcast.apply(lat3, topo["dir_len"], E, topo["dir_rowptr"])
-        shift = (image.unsqueeze(2) * lat_e).sum(1)  # image[e] lattice[graph(e)]
-    vec = ops.edge_vectors(cart, shift, grp_tgt, grp_src)
-    length = torch.norm(vec, dim=1)
-    unit = vec / length[:, None]
+    # the strain trick and the edge geometry (processgraph.py:169-199) of every graph in one
+    # launch each way, each edge with its own graph's lattice and strain
+    length, unit, lat_s, volumes = ops.edge_geometry_batch(cart, strains, lat3, image, grp_tgt, grp_src,
+                                                           topo["dir_graph32"], topo["atom_rowptr"],
+                                                           topo["dir_rowptr"])
+    lattice = lat_s.reshape(-1, 3)
 
     out = dict(atomic_numbers=torch.cat([g.atomic_number for g in graphs], 0), edge_lengths=length,
                unit_edge_vectors=unit, atom_segment=atom_segment, atoms_per_graph=n_atoms,

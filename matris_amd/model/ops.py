@@ -419,6 +419,71 @@ class _EdgeGeometry(torch.autograd.Function):
         return g_cart, g_strain, None, None, None, None
 
 
+class _EdgeGeometryBatch(torch.autograd.Function):
+    """A disjoint batch's edge geometry with the strain trick (processgraph.py:169-199,
+    each edge with its own graph's lattice and strain) through matris_edge_geom_fwd_batch /
+    matris_edge_geom_bwd_batch.  Differentiable in cart and strain; the strained lattices
+    and the volumes are returned as plain values."""
+
+    @staticmethod
+    def forward(ctx, cart, strain, lattice, image, tgt: "Grouping", src: "Grouping", graph_of_edge, atom_ptr,
+                edge_ptr):
+        _check_dev(cart, strain, lattice, image, graph_of_edge, atom_ptr, edge_ptr)
+        cart, lattice, image = _f32c(cart), _f32c(lattice), _f32c(image)
+        strain = None if strain is None else _f32c(strain)
+        G = lattice.shape[0]
+        E = image.shape[0]
+        if cart.dim() != 2 or cart.shape[1] != 3 or lattice.dim() != 3 or tuple(lattice.shape[1:]) != (3, 3) or \
+                image.dim() != 2 or image.shape[1] != 3 or (strain is not None and tuple(strain.shape) != (G, 3, 3)) \
+                or tgt.n_rows != E or src.n_rows != E or tgt.n_seg != cart.shape[0] or src.n_seg != cart.shape[0] \
+                or graph_of_edge.dtype != torch.int32 or tuple(graph_of_edge.shape) != (E,) or \
+                tuple(atom_ptr.shape) != (G + 1,) or tuple(edge_ptr.shape) != (G + 1,) or G < 1:
+            raise ValueError("edge_geometry_batch: expected cart [N,3], lattice and strain [G,3,3], image [E,3], "
+                             "groupings of E rows over N atoms, int32 graph_of_edge [E] and row pointers [G+1]")
+        dev = cart.device
+        length = _rows(E, 1, dev).view(-1)
+        unit = _rows(E, 3, dev)
+        lat_out = torch.empty(G, 3, 3, device=dev)
+        vol = torch.empty(G, 1, 1, device=dev)
+        with _timed("edge_geom_fwd", (E,)):
+            _lib.check(_lib.load().matris_edge_geom_fwd_batch(G, E, _p(cart), _p(lattice), _p(strain), _p(image),
+                                                              _p(tgt.key), _p(src.key), _p(graph_of_edge),
+                                                              _p(length), _p(unit), _p(lat_out), _p(vol), _stream()),
+                       "matris_edge_geom_fwd_batch")
+        ctx.save_for_backward(length, unit, cart, strain, lattice, image, atom_ptr, edge_ptr)
+        ctx.tgt, ctx.src = tgt, src
+        ctx.mark_non_differentiable(lat_out, vol)
+        ctx.set_materialize_grads(False)
+        return length, unit, lat_out, vol
+
+    @staticmethod
+    def backward(ctx, g_len, g_unit, _g_lat, _g_vol):
+        length, unit, cart, strain, lattice, image, atom_ptr, edge_ptr = ctx.saved_tensors
+        G, N, E, dev = lattice.shape[0], cart.shape[0], image.shape[0], cart.device
+        g_len = None if g_len is None else _f32c(g_len)
+        g_unit = None if g_unit is None else _f32c(g_unit)
+        g_vec = _rows(E, 3, dev)
+        g_cart = torch.empty(N, 3, device=dev)
+        g_strain = torch.empty_like(strain) if (strain is not None and ctx.needs_input_grad[1]) else None
+        t, s = ctx.tgt, ctx.src
+        with _timed("edge_geom_bwd", (E,)):
+            _lib.check(_lib.load().matris_edge_geom_bwd_batch(G, N, E, _p(g_len), _p(g_unit), _p(length), _p(unit),
+                                                              _p(cart), _p(lattice), _p(strain), _p(image),
+                                                              _p(t.rowptr), _p(t.perm), _p(s.rowptr), _p(s.perm),
+                                                              _p(atom_ptr), _p(edge_ptr), _p(g_vec), _p(g_cart),
+                                                              _p(g_strain), _stream()), "matris_edge_geom_bwd_batch")
+        return g_cart, g_strain, None, None, None, None, None, None, None
+
+
+def edge_geometry_batch(cart, strain, lattice, image, tgt: "Grouping", src: "Grouping", graph_of_edge, atom_ptr,
+                        edge_ptr):
+    """(length [E], unit [E,3], strained lattices [G,3,3], volumes [G,1,1]) of a disjoint
+    batch (processgraph.py:169-199 per graph): cart [N,3], strain [G,3,3] or None, lattice
+    [G,3,3], image [E,3] fp32; tgt / src the batch's atom-graph groupings; graph_of_edge int32
+    [E]; atom_ptr / edge_ptr int32 [G+1], each graph's contiguous atom and edge rows."""
+    return _EdgeGeometryBatch.apply(cart, strain, lattice, image, tgt, src, graph_of_edge, atom_ptr, edge_ptr)
+
+
 def frac_to_cart(frac: torch.Tensor, lattice: torch.Tensor, with_strain: bool):
     """(cart [N, 3] = frac @ lattice, zero strain [1, 3, 3] or None) of one graph in one
     launch (matris_frac_to_cart; processgraph.py:87 and :173-177), both new tensors without

@@ -208,6 +208,52 @@ def test_md_with_skin_matches_rebuild_every_step():
     assert runs[1][2]._neighbors.n_builds < 13
 
 
+@pytest.mark.parametrize("sizes", [(24, 8, 40, 12), (16,) * 9])
+def test_batched_geometry_vs_fp64_oracle(sizes):
+    """process_graphs of a mixed batch (matris_frac_to_cart_batch, matris_edge_geom_fwd_batch /
+    _bwd_batch: each atom and edge with its own graph's lattice and strain) against the fp64
+    oracle restatement of processgraph.py:6-245 on the same graphs: edge lengths, unit
+    vectors, volumes, strained lattices, and the gradients of one random loss in the
+    positions and in every graph's strain (at zero strain the oracle's strained positions
+    and the leaf positions have the same gradient)."""
+    from matris_amd.model.batch import process_graphs
+    from oracle import model_ref
+    rng = np.random.default_rng(sum(sizes))
+    gs = [_gpu_graph(W.random_cell(rng, n)) for n in sizes]
+    bg = process_graphs(gs, compute_stress=True)
+    cpu = [{k: getattr(g, k).detach().cpu() for k in ("atomic_number", "atom_frac_coord", "lattice",
+                                                      "neighbor_image", "atom_graph", "directed2undirected",
+                                                      "undirected2directed", "line_graph")} for g in gs]
+    for d in cpu:
+        for k in ("atom_frac_coord", "lattice", "neighbor_image"):
+            d[k] = d[k].double()
+    ref = model_ref.process_graphs(cpu, compute_stress=True)
+    E, G = ref["edge_lengths"].shape[0], len(sizes)
+    assert torch.allclose(bg["edge_lengths"].double().cpu(), ref["edge_lengths"], rtol=2e-6, atol=2e-6)
+    assert torch.allclose(bg["unit_edge_vectors"].double().cpu(), ref["unit_edge_vectors"], rtol=0, atol=4e-6)
+    assert torch.allclose(bg["volumes"].double().cpu().reshape(-1), ref["volumes"].reshape(-1), rtol=2e-6)
+    assert torch.allclose(bg["lattice"].double().cpu(), ref["lattice"].detach(), rtol=0, atol=1e-5)
+    gen = torch.Generator().manual_seed(len(sizes))
+    gl = torch.randn(E, generator=gen, dtype=torch.float64)
+    gu = torch.randn(E, 3, generator=gen, dtype=torch.float64)
+    loss = (bg["edge_lengths"] * gl.float().cuda()).sum() + (bg["unit_edge_vectors"] * gu.float().cuda()).sum()
+    gc, gsn = torch.autograd.grad(loss, [bg["batch_cart_coords"], bg["batch_strains"]])
+    rloss = (ref["edge_lengths"] * gl).sum() + (ref["unit_edge_vectors"] * gu).sum()
+    rc, rs = torch.autograd.grad(rloss, [ref["batch_cart_coords"], ref["batch_strains"]])
+    assert tuple(gsn.shape) == (G, 3, 3)
+    assert (gc.double().cpu() - rc).abs().max().item() <= 2e-4 * max(1.0, rc.abs().max().item())
+    assert (gsn.double().cpu() - rs).abs().max().item() <= 2e-4 * max(1.0, rs.abs().max().item())
+    # a graph index outside the batch: reported in the status word, no access
+    from matris_amd.model import ops
+    ops.status_take()
+    bad = torch.full((E,), G, dtype=torch.int32, device="cuda")
+    cart = bg["batch_cart_coords"].detach()
+    ops.edge_geometry_batch(cart, None, bg["lattice"].detach().reshape(G, 3, 3), torch.cat(
+        [g.neighbor_image for g in gs]), bg["atom_graph_dict"]["grp_tgt"], bg["atom_graph_dict"]["grp_src"], bad,
+        bg["atom_rowptr"], bg["atom_rowptr"])
+    assert ops.status_take() == ops.STATUS_CSR_KEY
+
+
 @pytest.mark.parametrize("seed", [5, 6])
 def test_one_graph_geometry_equals_batched_path(seed):
     """process_graphs for one graph (the strain trick and edge geometry in one launch,

@@ -144,6 +144,15 @@ def test_arguments_rejected_before_launch(lib):
     assert lib.matris_frac_to_cart_batch(3, 2, v16, v16, None, v16, None, None) == -1001
     assert lib.matris_frac_to_cart_batch(-1, 2, v16, v16, v16, v16, None, None) == -1001
     assert lib.matris_frac_to_cart_batch(0, 2, None, None, None, None, None, None) == 0
+    # batched edge geometry: no graphs; edges without a graph index; a strain gradient
+    # without a strain; a strain without the graphs' row ranges
+    assert lib.matris_edge_geom_fwd_batch(0, 4, *([v16] * 11), None) == -1001
+    assert lib.matris_edge_geom_fwd_batch(2, 4, *([v16] * 6), None, *([v16] * 4), None) == -1001
+    assert lib.matris_edge_geom_fwd_batch(2, 4, v16, None, *([v16] * 9), None) == -1001
+    bw = [v16] * 17
+    assert lib.matris_edge_geom_bwd_batch(0, 3, 4, *bw, None) == -1001
+    assert lib.matris_edge_geom_bwd_batch(2, 3, 4, *bw[:6], None, *bw[7:], None) == -1001
+    assert lib.matris_edge_geom_bwd_batch(2, 3, 4, *bw[:12], None, None, *bw[14:], None) == -1001
     assert lib.matris_csr_build_deferred(10, None, 1, 4, v16, v16, v16, 1, None) == -1001
     # neighbour-list reuse: no atoms; a workspace below its size; a non-positive cutoff
     big = 1 << 20
