@@ -243,6 +243,13 @@ def test_batched_geometry_vs_fp64_oracle(sizes):
     assert tuple(gsn.shape) == (G, 3, 3)
     assert (gc.double().cpu() - rc).abs().max().item() <= 2e-4 * max(1.0, rc.abs().max().item())
     assert (gsn.double().cpu() - rs).abs().max().item() <= 2e-4 * max(1.0, rs.abs().max().item())
+    # without a strain (task "ef"): no strain leaf, the same lengths and position gradient
+    bg0 = process_graphs(gs, compute_stress=False)
+    assert bg0["batch_strains"] is None
+    assert torch.equal(bg0["edge_lengths"], bg["edge_lengths"])
+    loss0 = (bg0["edge_lengths"] * gl.float().cuda()).sum() + (bg0["unit_edge_vectors"] * gu.float().cuda()).sum()
+    (gc0,) = torch.autograd.grad(loss0, [bg0["batch_cart_coords"]])
+    assert torch.equal(gc0, gc)
     # a graph index outside the batch: reported in the status word, no access
     from matris_amd.model import ops
     ops.status_take()
