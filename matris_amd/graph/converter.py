@@ -243,9 +243,12 @@ class GraphConverter(nn.Module):
         except RuntimeError as exc:
             # converter.py:99-106: the structure is dumped to error_graph.cif in the working
             # directory and the graph keeps an empty line graph
-            write_cif("error_graph.cif", frac if frac is not None else f64.cpu().numpy(), lat, z)
-            warnings.warn(f"line graph construction failed ({exc}); the structure was written to "
-                          "error_graph.cif and the line graph is empty")
+            try:
+                write_cif("error_graph.cif", frac if frac is not None else f64.cpu().numpy(), lat, z)
+                where = "the structure was written to error_graph.cif"
+            except OSError as err:  # an unwritable working directory must not hide the failure
+                where = f"error_graph.cif could not be written ({err})"
+            warnings.warn(f"line graph construction failed ({exc}); {where} and the line graph is empty")
             lg = torch.zeros(0, 5, dtype=torch.int32, device=dev)
             angle_ptr = None
         atom_graph = torch.stack([center, neighbor], dim=1)

@@ -110,3 +110,29 @@ def test_failed_line_graph_writes_error_cif(tmp_path, monkeypatch):
     assert keys["_cell_length_a"] == pytest.approx(2.9) and keys["_cell_angle_gamma"] == pytest.approx(90.0)
     assert [s[0] for s in sites] == ["Fe", "Fe"]
     np.testing.assert_allclose([s[2:] for s in sites], frac, atol=1e-8)
+
+
+def test_failed_line_graph_in_an_unwritable_directory_still_builds(tmp_path, monkeypatch):
+    """The dump failing (here: error_graph.cif is a directory) is reported in the warning;
+    the graph is still built with an empty line graph."""
+    monkeypatch.chdir(tmp_path)
+    (tmp_path / "error_graph.cif").mkdir()
+    center = torch.tensor([0, 1], dtype=torch.int32)
+    neighbor = torch.tensor([1, 0], dtype=torch.int32)
+    nb = (center, neighbor, torch.zeros(2, 3, dtype=torch.int32), torch.full((2,), 2.5, dtype=torch.float64),
+          torch.tensor([0, 1, 2], dtype=torch.int32), torch.tensor([1, 1], dtype=torch.int32))
+    monkeypatch.setattr(conv, "pair_edges_device", lambda *a: (torch.tensor([1, 0], dtype=torch.int32),
+                                                               torch.tensor([0, 0], dtype=torch.int32),
+                                                               torch.tensor([0], dtype=torch.int32),
+                                                               torch.tensor([1], dtype=torch.int32)))
+
+    def line_graph(*args):
+        raise RuntimeError("line graph failed")
+
+    monkeypatch.setattr(conv, "line_graph_device", line_graph)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        g = conv.GraphConverter(device="cpu").from_arrays(np.array([[0.0, 0, 0], [0.5, 0.5, 0.5]]), 2.9 * np.eye(3),
+                                                          np.array([26, 26]), neighbors=nb)
+    assert any("could not be written" in str(x.message) for x in w)
+    assert g.line_graph.shape == (0, 5)
