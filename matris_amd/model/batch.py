@@ -170,14 +170,17 @@ def process_graphs(graphs, compute_stress: bool = True) -> dict:
     atom_graph, tgt, src = topo["atom_graph"], topo["tgt"], topo["src"]
     d2u32, u2d32 = topo["d2u32"], topo["u2d32"]
     grp_tgt, grp_src = topo["grp_tgt"], topo["grp_src"]
-    lattice = torch.cat([g.lattice.detach() for g in graphs], 0)  # [3G, 3]
-    image = torch.cat([g.neighbor_image for g in graphs], 0)
+    # fp32 throughout, the dtype of the reference's graphs (radiusgraph.py, `datatype`): a
+    # graph built with integer images or fp64 coordinates is converted here
+    f32 = torch.float32
+    lattice = torch.cat([g.lattice.detach().to(f32) for g in graphs], 0)  # [3G, 3]
+    image = torch.cat([g.neighbor_image.to(f32) for g in graphs], 0)
     atom_segment = topo["atom_segment"]
     lat3 = lattice.reshape(G, 3, 3)
     # processgraph.py:87 for every graph and the zero strains in one launch (each atom reads
     # its own graph's lattice) instead of one small product per graph
-    frac = torch.cat([g.atom_frac_coord.detach() for g in graphs], 0)
-    cart, strains = ops.frac_to_cart_batch(frac.to(dtype), lat3, topo["atom_graph32"], compute_stress)
+    frac = torch.cat([g.atom_frac_coord.detach().to(f32) for g in graphs], 0)
+    cart, strains = ops.frac_to_cart_batch(frac, lat3, topo["atom_graph32"], compute_stress)
     cart.requires_grad_(True)
     if strains is not None:
         strains.requires_grad_(True)

@@ -261,6 +261,29 @@ def test_batched_geometry_vs_fp64_oracle(sizes):
     assert ops.status_take() == ops.STATUS_CSR_KEY
 
 
+def test_batched_path_converts_integer_images_and_fp64_coordinates():
+    """A graph carrying int32 images and fp64 coordinates goes through the batched path,
+    which works in fp32 (the reference graphs' dtype): the same lengths, unit vectors,
+    volume and gradients as the fp32 graph through the one-graph path."""
+    from matris_amd.graph.radiusgraph import RadiusGraph
+    from matris_amd.model.batch import process_graphs
+    g = _gpu_graph(W.random_cell(np.random.default_rng(11), 16))
+    kw = {f: getattr(g, f) for f in RadiusGraph._FIELDS}
+    kw.update(neighbor_image=g.neighbor_image.to(torch.int32), atom_frac_coord=g.atom_frac_coord.double(),
+              lattice=g.lattice.double())
+    g2 = RadiusGraph(graph_id=None, mp_id=None, composition=None, atom_graph_cutoff=g.atom_graph_cutoff,
+                     line_graph_cutoff=g.line_graph_cutoff, **kw)
+    one = process_graphs([g], compute_stress=True)
+    two = process_graphs([g2], compute_stress=True)
+    for k in ("edge_lengths", "unit_edge_vectors", "volumes"):
+        assert torch.equal(one[k].reshape(-1), two[k].reshape(-1)), k
+    loss = lambda bg: (bg["edge_lengths"] ** 2).sum() + bg["unit_edge_vectors"][:, 0].sum()
+    ga = torch.autograd.grad(loss(one), [one["batch_cart_coords"], one["batch_strains"]])
+    gb = torch.autograd.grad(loss(two), [two["batch_cart_coords"], two["batch_strains"]])
+    assert torch.allclose(ga[0], gb[0], rtol=1e-5, atol=1e-5)
+    assert torch.allclose(ga[1], gb[1], rtol=1e-5, atol=1e-4)
+
+
 @pytest.mark.parametrize("seed", [5, 6])
 def test_one_graph_geometry_equals_batched_path(seed):
     """process_graphs for one graph (the strain trick and edge geometry in one launch,
