@@ -151,7 +151,15 @@ def _zeros_if_none(g, like):
 def _ffn_fusable(mlp) -> bool:
     L = mlp.layers
     return (len(L) == 4 and L[0].bias is None and L[3].bias is None and tuple(L[0].weight.shape) == (D, D)
-            and tuple(L[3].weight.shape) == (D, D) and type(L[1]).__name__ == "FusedSiLU")
+            and tuple(L[3].weight.shape) == (D, D) and type(L[1]).__name__ == "FusedSiLU"
+            and not getattr(mlp, "use_fp16", False))
+
+
+def _gmlp_fusable(m) -> bool:
+    """A GatedMLP in the form the fused kernels implement (an MLP-and-norm update of
+    graph_conv_mlp="MLP" is not one)."""
+    f = getattr(m, "_fusable", None)
+    return f is not None and f()
 
 
 def _res_ok(w) -> bool:
@@ -175,13 +183,13 @@ def _tile_rows(grp: ops.Grouping) -> int:
 
 def line_attention_fusable(layer) -> bool:
     s, t = layer.source_weight_linear, layer.target_weight_linear
-    return (layer.edge_nonlinear_update._fusable() and layer.node_nonlinear_update._fusable()
+    return (_gmlp_fusable(layer.edge_nonlinear_update) and _gmlp_fusable(layer.node_nonlinear_update)
             and tuple(s.weight.shape) == (D, D) and s.bias is None and tuple(t.weight.shape) == (D, D)
             and t.bias is None and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 
 
 def line_refinement_fusable(layer) -> bool:
-    return (layer.graph_type == "line graph" and layer.edge_nonlinear_update._fusable()
+    return (layer.graph_type == "line graph" and _gmlp_fusable(layer.edge_nonlinear_update)
             and _ffn_fusable(layer.node_FFN) and _ffn_fusable(layer.edge_FFN)
             and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 
@@ -391,7 +399,7 @@ def atom_attention_fusable(layer) -> bool:
 
 
 def atom_refinement_fusable(layer) -> bool:
-    return (layer.graph_type == "atom graph" and layer.edge_nonlinear_update._fusable()
+    return (layer.graph_type == "atom graph" and _gmlp_fusable(layer.edge_nonlinear_update)
             and _ffn_fusable(layer.node_FFN) and _ffn_fusable(layer.edge_FFN)
             and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 

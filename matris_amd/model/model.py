@@ -118,6 +118,10 @@ class MLP(nn.Module):
         self.layers = nn.Sequential(*layers)
 
     def forward(self, x):
+        if self.use_fp16 and x.is_cuda:  # functions.py:231-236: fp16 autocast, fp32 result
+            with torch.autocast(device_type="cuda", dtype=torch.float16):
+                out = self.layers(x)
+            return out.to(torch.float32)
         return self.layers(x)
 
 
@@ -140,7 +144,8 @@ class GatedMLP(nn.Module):
     def _fusable(self) -> bool:
         return (isinstance(self.core_norm, nn.RMSNorm) and len(self.mlp_core.layers) == 4
                 and self.mlp_core.layers[0].bias is not None and self.mlp_core.layers[0].out_features == 128
-                and self.mlp_core.layers[3].out_features == 128)
+                and self.mlp_core.layers[3].out_features == 128 and not self.use_fp16
+                and not self.mlp_core.use_fp16 and not self.mlp_gate.use_fp16)
 
     def forward(self, x):
         core = self.activation_func(self.core_norm(self.mlp_core(x)))
@@ -148,9 +153,36 @@ class GatedMLP(nn.Module):
         return core * gate
 
     def fused(self, sources):
-        if not self._fusable():
-            raise NotImplementedError("fused GatedMLP needs RMSNorm, one 128-wide hidden layer and biases")
-        return ops.gated_mlp(self, self._pack, sources)
+        """The block on the concatenation of `sources` ((rows, grouping or None) pairs, the
+        grouping's keys selecting rows): matris_gmlp_fwd for the MatRIS-10M form (RMSNorm,
+        one 128-wide hidden layer, biases); any other form (LayerNorm or BatchNorm, other
+        widths, the fp16 autocast MLPs) runs this module's own forward on the gathered
+        concatenation, on the device."""
+        if self._fusable():
+            return ops.gated_mlp(self, self._pack, sources)
+        return self(gathered_concat(sources))
+
+
+def gathered_concat(sources):
+    """torch.cat of the sources' rows ((tensor, grouping or None) pairs; a grouping's keys
+    select the rows, ops.gather) along the feature axis: the reference's index_select +
+    cat (interaction_block.py:96-106, 230-237)."""
+    return torch.cat([t if g is None else ops.gather(t, g) for t, g in sources], dim=1)
+
+
+def nonlinear_update(module, sources):
+    """A layer's edge or node update on its concatenated sources: GatedMLP.fused, or, for
+    graph_conv_mlp="MLP" (an MLP followed by a norm, interaction_block.py:39-62, 172-184),
+    the module on the gathered concatenation."""
+    if isinstance(module, GatedMLP):
+        return module.fused(sources)
+    return module(gathered_concat(sources))
+
+
+def _mlp_update(in_dim, hidden_dim, out_dim, dropout, use_bias, activation, norm_type, use_fp16=False):
+    """interaction_block.py:39-62 / 172-184 (mlp_type "MLP"): MLP then a norm."""
+    return nn.Sequential(MLP(in_dim, hidden_dim, out_dim, dropout, activation, use_bias, use_fp16),
+                         get_normalization(name=norm_type, dim=out_dim))
 
 
 class GraphPooling(nn.Module):
@@ -342,20 +374,29 @@ class ThreebodyEmbedding(nn.Module):
 # interaction block (interaction_block.py)
 # ------------------------------------------------------------------------------------
 class Graph_Attention_Layer(nn.Module):
-    """interaction_block.py:17-143 (GateMLP)."""
+    """interaction_block.py:17-143.  The fused kernels take the MatRIS-10M form (RMSNorm
+    GatedMLPs, 128-wide); LayerNorm / BatchNorm GatedMLPs and graph_conv_mlp "MLP" run the
+    generic path below (device gathers, segment attention and sums; the update module
+    itself as torch layers on the device)."""
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, use_bias=False, dropout=0.0,
                  mlp_type="GateMLP", activation_type="silu", norm_type="layer", use_fp16=False):
         super().__init__()
-        if mlp_type.lower() != "gatemlp":
-            raise NotImplementedError("the MI355X path implements graph_conv_mlp='GateMLP'")
         self.source_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
         self.target_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
-        self.node_nonlinear_update = GatedMLP(edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
-                                              norm_type=norm_type, dropout=dropout, activation=activation_type)
-        self.edge_nonlinear_update = GatedMLP(node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
-                                              norm_type=norm_type, dropout=dropout, activation=activation_type,
-                                              use_fp16=use_fp16)
+        if mlp_type.lower() == "mlp":
+            self.node_nonlinear_update = _mlp_update(edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
+                                                     dropout, use_bias, activation_type, norm_type)
+            self.edge_nonlinear_update = _mlp_update(node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
+                                                     dropout, use_bias, activation_type, norm_type, use_fp16)
+        elif mlp_type.lower() == "gatemlp":
+            self.node_nonlinear_update = GatedMLP(edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
+                                                  norm_type=norm_type, dropout=dropout, activation=activation_type)
+            self.edge_nonlinear_update = GatedMLP(node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
+                                                  norm_type=norm_type, dropout=dropout, activation=activation_type,
+                                                  use_fp16=use_fp16)
+        else:
+            raise NotImplementedError(f"Unknown mlp_type: {mlp_type}")
         self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim), requires_grad=True)
         self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim), requires_grad=True)
         self._proj = ops._WeightPack()
@@ -374,33 +415,37 @@ class Graph_Attention_Layer(nn.Module):
         if d2u is not None and fused.atom_attention_fusable(self):
             return fused.atom_attention(self, node_feat, edge_feat, graph, d2u)
         if d2u is None:  # line graph: edges are the angles themselves
-            e = self.edge_nonlinear_update.fused([(edge_feat, None), (node_feat, tgt), (node_feat, src)])
+            e = nonlinear_update(self.edge_nonlinear_update, [(edge_feat, None), (node_feat, tgt), (node_feat, src)])
             a_s, a_t = self._projections(edge_feat)
             y_t, y_s = ops.seg_attention(a_t, a_s, e, tgt, src)
         else:  # atom graph: undirected bond rows expanded through d2u inside the kernels
-            e = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
+            e = nonlinear_update(self.edge_nonlinear_update, [(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
             a_s, a_t = self._projections(edge_feat)
             y_t, y_s = ops.seg_attention(a_t, a_s, e, tgt, src, alpha_grp=d2u)
             e = ops.seg_sum(e, d2u, 0.5)  # mean of the two directed copies (:121-122)
-        n = self.node_nonlinear_update.fused([(node_feat, None), (y_t, None), (y_s, None)])
+        n = nonlinear_update(self.node_nonlinear_update, [(node_feat, None), (y_t, None), (y_s, None)])
         return n + self.node_res_weight * node_feat, e + self.edge_res_weight * edge_feat
 
 
 class Refinement(nn.Module):
-    """interaction_block.py:146-278 (GateMLP)."""
+    """interaction_block.py:146-278; update forms as in Graph_Attention_Layer."""
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, num_basis=7, dropout=0.0,
                  mlp_type="GateMLP", activation_type="silu", norm_type="layer", use_bias=False,
                  graph_type="atom graph", atom_feat_dim=128, use_smoothed_for_delta_edge=False, use_fp16=False):
         super().__init__()
-        if mlp_type.lower() != "gatemlp":
-            raise NotImplementedError("the MI355X path implements graph_conv_mlp='GateMLP'")
         self.graph_type = graph_type
         self.use_smoothed_for_delta_edge = use_smoothed_for_delta_edge
         input_dim = 2 * node_feat_dim + edge_feat_dim if graph_type == "atom graph" else \
             atom_feat_dim + 2 * node_feat_dim + edge_feat_dim
-        self.edge_nonlinear_update = GatedMLP(input_dim, hidden_dim, edge_feat_dim, dropout=dropout,
-                                              norm_type=norm_type, activation=activation_type, use_fp16=use_fp16)
+        if mlp_type.lower() == "mlp":
+            self.edge_nonlinear_update = _mlp_update(input_dim, hidden_dim, edge_feat_dim, dropout, use_bias,
+                                                     activation_type, norm_type, use_fp16)
+        elif mlp_type.lower() == "gatemlp":
+            self.edge_nonlinear_update = GatedMLP(input_dim, hidden_dim, edge_feat_dim, dropout=dropout,
+                                                  norm_type=norm_type, activation=activation_type, use_fp16=use_fp16)
+        else:
+            raise NotImplementedError(f"Unknown mlp_type: {mlp_type}")
         self.node_FFN = MLP(edge_feat_dim, node_feat_dim, node_feat_dim, bias=use_bias)
         self.edge_FFN = MLP(edge_feat_dim, edge_feat_dim, edge_feat_dim, bias=use_bias, use_fp16=use_fp16)
         self.learnable_envelope = nn.Linear(num_basis, edge_feat_dim, bias=False)
@@ -415,7 +460,7 @@ class Refinement(nn.Module):
         """MLP(hidden=int, bias=False) as one fused MFMA kernel (functions.py:198-205)."""
         L = mlp.layers
         if (len(L) == 4 and L[0].bias is None and L[3].bias is None and L[0].weight.shape == (128, 128)
-                and L[3].weight.shape == (128, 128) and isinstance(L[1], FusedSiLU)):
+                and L[3].weight.shape == (128, 128) and isinstance(L[1], FusedSiLU) and not mlp.use_fp16):
             return ops.ffn(pack.get(L[0].weight, L[3].weight), x)
         return mlp(x)
 
@@ -426,14 +471,14 @@ class Refinement(nn.Module):
             return fused.atom_refinement(self, node_feat, edge_feat, smooth_weight, graph, d2u)
         if self.graph_type == "atom graph":
             w = ops.gather(self.learnable_envelope(smooth_weight), d2u)
-            h = self.edge_nonlinear_update.fused([(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
+            h = nonlinear_update(self.edge_nonlinear_update, [(edge_feat, d2u), (node_feat, tgt), (node_feat, src)])
         elif fused.line_refinement_fusable(self):  # one node, explicit backward
             return fused.line_refinement(self, edge_feat, atom_feat, node_feat, smooth_weight, graph, recompute)
         else:
             env = self.learnable_envelope(smooth_weight)
             w = ops.gather(env, src) * ops.gather(env, tgt)
-            h = self.edge_nonlinear_update.fused([(edge_feat, None), (atom_feat, graph["grp_atom"]),
-                                                  (node_feat, tgt), (node_feat, src)])
+            h = nonlinear_update(self.edge_nonlinear_update, [(edge_feat, None), (atom_feat, graph["grp_atom"]),
+                                                              (node_feat, tgt), (node_feat, src)])
         hw = h * w
         agg = ops.seg_sum(hw, tgt)
         to_edge = hw if (self.graph_type == "atom graph" and self.use_smoothed_for_delta_edge) else h

@@ -973,6 +973,14 @@ def _gmlp_fwd(pack: GmlpPack, srcs, idxs, n_rows: int, mode: int, res, save: boo
     lib = _lib.load()
     dev = srcs[0].device
     nsrc = len(srcs)
+    # the kernel reads each source as [rows, 128] rows and W1 as 128-column blocks, one per
+    # source: widths it cannot see through the pointers
+    K = int(pack.mats["w1"].shape[1])
+    if K != D * nsrc or any(s.dim() != 2 or s.shape[1] != D for s in srcs):
+        raise ValueError(f"matris_gmlp_fwd: {nsrc} source(s) of shapes {[tuple(s.shape) for s in srcs]} for a "
+                         f"layer-1 weight with K = {K}; each source must be [rows, 128] and K = 128 x sources")
+    if any(i is None and s.shape[0] != n_rows for s, i in zip(srcs, idxs)):
+        raise ValueError(f"matris_gmlp_fwd: an ungathered source must have the output's {n_rows} rows")
     out = _rows(n_rows, D, dev)
     p = _rows(n_rows, 256, dev) if save else None
     z = _rows(n_rows, 256, dev) if save else None

@@ -12,6 +12,9 @@ order so that `torch.manual_seed(s)` yields the same weights (and the same
 Pins (see tests/test_oracle_model.py):
   * seed-0 state_dict fingerprint and C1 e/f/s/m golden vectors written by
     tests/golden/make_golden.py from the reference's own modules;
+  * the non-default update forms (LayerNorm / BatchNorm GatedMLPs, graph_conv_mlp "MLP"
+    with RMSNorm and with LayerNorm): per-tensor state_dict sums and the e/f/s/m of C1 and
+    of three batched triclinic cells, from the reference modules (tests/golden/configs.npz);
   * parameter counts 6,286,736 (defaults) / 10,379,664 (num_layers=10);
   * sum of forces = 0, stress symmetry, rotation equivariance, finite-difference
     forces and stress in fp64.
@@ -330,17 +333,29 @@ class ThreebodyEmbedding(nn.Module):
 # --------------------------------------------------------------------------------------
 # interaction block (matris/model/interaction_block.py)
 # --------------------------------------------------------------------------------------
-class GraphAttentionLayer(nn.Module):
-    """interaction_block.py:17-143 (GateMLP branch)."""
+def _update(mlp_type, input_dim, hidden_dim, output_dim, norm_type, bias):
+    """The nonlinear update of an attention / refinement layer: a GatedMLP (its MLPs keep
+    their biases), or, for mlp_type "MLP", MLP(bias=use_bias) followed by the norm
+    (interaction_block.py:39-74, 172-197)."""
+    if mlp_type.lower() == "gatemlp":
+        return GatedMLP(input_dim, hidden_dim, output_dim, norm_type=norm_type)
+    if mlp_type.lower() == "mlp":
+        return nn.Sequential(MLP(input_dim, hidden_dim, output_dim, bias=bias), _norm(norm_type, output_dim))
+    raise NotImplementedError(mlp_type)
 
-    def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, norm_type="layer"):
+
+class GraphAttentionLayer(nn.Module):
+    """interaction_block.py:17-143."""
+
+    def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, norm_type="layer",
+                 mlp_type="GateMLP", use_bias=False):
         super().__init__()
         self.source_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
         self.target_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
-        self.node_nonlinear_update = GatedMLP(edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
-                                              norm_type=norm_type)
-        self.edge_nonlinear_update = GatedMLP(node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
-                                              norm_type=norm_type)
+        self.node_nonlinear_update = _update(mlp_type, edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
+                                             norm_type, use_bias)
+        self.edge_nonlinear_update = _update(mlp_type, node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
+                                             norm_type, use_bias)
         self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim))
         self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim))
 
@@ -362,11 +377,11 @@ class GraphAttentionLayer(nn.Module):
 
 
 class Refinement(nn.Module):
-    """interaction_block.py:146-278 (GateMLP branch)."""
+    """interaction_block.py:146-278."""
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, num_basis=7,
                  norm_type="layer", graph_type="atom graph", atom_feat_dim=128,
-                 use_smoothed_for_delta_edge=False, use_bias=False):
+                 use_smoothed_for_delta_edge=False, use_bias=False, mlp_type="GateMLP"):
         super().__init__()
         self.graph_type = graph_type
         self.use_smoothed_for_delta_edge = use_smoothed_for_delta_edge
@@ -374,7 +389,7 @@ class Refinement(nn.Module):
             input_dim = 2 * node_feat_dim + edge_feat_dim
         else:
             input_dim = atom_feat_dim + 2 * node_feat_dim + edge_feat_dim
-        self.edge_nonlinear_update = GatedMLP(input_dim, hidden_dim, edge_feat_dim, norm_type=norm_type)
+        self.edge_nonlinear_update = _update(mlp_type, input_dim, hidden_dim, edge_feat_dim, norm_type, use_bias)
         self.node_FFN = MLP(edge_feat_dim, node_feat_dim, node_feat_dim, bias=use_bias)
         self.edge_FFN = MLP(edge_feat_dim, edge_feat_dim, edge_feat_dim, bias=use_bias)
         self.learnable_envelope = nn.Linear(num_basis, edge_feat_dim, bias=False)
@@ -408,16 +423,19 @@ class InteractionBlock(nn.Module):
     """interaction_block.py:281-446 (checkpointing changes memory, not values)."""
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, three_body_feat_dim=128, num_radial=7,
-                 num_angular=7, use_bias=False, use_smoothed_for_delta_edge=False, norm_type="layer"):
+                 num_angular=7, use_bias=False, use_smoothed_for_delta_edge=False, norm_type="layer",
+                 mlp_type="GateMLP"):
         super().__init__()
-        self.attn_block_atom_graph = GraphAttentionLayer(node_feat_dim, edge_feat_dim, node_feat_dim, norm_type)
-        self.attn_block_line_graph = GraphAttentionLayer(edge_feat_dim, three_body_feat_dim, edge_feat_dim, norm_type)
+        self.attn_block_atom_graph = GraphAttentionLayer(node_feat_dim, edge_feat_dim, node_feat_dim, norm_type,
+                                                         mlp_type, use_bias)
+        self.attn_block_line_graph = GraphAttentionLayer(edge_feat_dim, three_body_feat_dim, edge_feat_dim, norm_type,
+                                                         mlp_type, use_bias)
         self.refine_block_atom_graph = Refinement(node_feat_dim, edge_feat_dim, node_feat_dim, num_radial, norm_type,
                                                   "atom graph", use_smoothed_for_delta_edge=use_smoothed_for_delta_edge,
-                                                  use_bias=use_bias)
+                                                  use_bias=use_bias, mlp_type=mlp_type)
         self.refine_block_line_graph = Refinement(edge_feat_dim, three_body_feat_dim, edge_feat_dim, num_angular,
                                                   norm_type, "line graph", atom_feat_dim=node_feat_dim,
-                                                  use_bias=use_bias)
+                                                  use_bias=use_bias, mlp_type=mlp_type)
 
     def forward(self, g, node_feat, edge_feat, tb_feat, smooth_weight):
         attn_edge, attn_tb = edge_feat, tb_feat
@@ -533,7 +551,7 @@ class MatRISRef(nn.Module):
                  pairwise_cutoff=6, three_body_cutoff=4, use_smoothed_for_delta_edge=False,
                  learnable_basis=True, is_intensive=True, is_conservation=True, reference_energy=None):
         super().__init__()
-        assert graph_conv_mlp.lower() == "gatemlp" and is_conservation and reference_energy is None
+        assert is_conservation and reference_energy is None
         self.is_intensive = is_intensive
         self.atom_embedding = AtomTypeEmbedding(node_feat_dim)
         self.edge_embedding = EdgeBasisEmbedding(pairwise_cutoff, three_body_cutoff, num_radial, edge_feat_dim,
@@ -542,7 +560,7 @@ class MatRISRef(nn.Module):
                                                        three_body_feat_dim, three_body_expansion, learnable_basis)
         self.interaction_block = nn.ModuleList([
             InteractionBlock(node_feat_dim, edge_feat_dim, three_body_feat_dim, num_radial, num_angular,
-                             use_bias, use_smoothed_for_delta_edge, norm_type)
+                             use_bias, use_smoothed_for_delta_edge, norm_type, graph_conv_mlp)
             for _ in range(num_layers)])
         self.readout_norm = _norm(norm_type, node_feat_dim)
         hd = [mlp_hidden_dims] if isinstance(mlp_hidden_dims, int) else list(mlp_hidden_dims)

@@ -4,12 +4,15 @@ fp64 on the same graphs and seed-0 weights as the reference golden fixtures.
 Purpose: it measures the fp32 noise floor of the reference computation itself
 (|e_ref_fp32 - e_fp64|).  The random-init model's energies are small sums with strong
 cancellation (e.g. C1 e = -1.4e-3 eV/atom, and the three-body basis evaluates spherical
-Bessel functions at x = 1/6 where j_3 ~ x^3/105 cancels between O(1) terms), so the
-reference's own fp32 result differs from fp64 by 1e-5 .. 6e-4 relative.  The GPU parity
-tests report both distances and accept an energy within 1e-5 relative of the reference
-OR no farther from it than twice the reference's own fp32 error.
+Bessel functions at x = 1/6 where j_3 ~ x^3/105 cancels between O(1) terms).
 
-    python tests/golden/make_fp64.py
+The fp64 model computes the same function as the fp32 one: nn.RMSNorm(eps=None) takes
+eps = finfo(input dtype).eps, 1.19e-7 for the fp32 reference but 2.2e-16 in float64, and
+rows whose mean square is small (the symmetric C1 cell, bias-free MLP-then-norm updates)
+feel the difference (6e-4 of the C1 energy), so every RMSNorm here gets the fp32 constant.
+
+    python tests/golden/make_fp64.py [--big]
+    python tests/golden/make_fp64.py --only variants    (the non-default update forms)
 """
 from __future__ import annotations
 
@@ -38,12 +41,21 @@ def graph(z, prefix):
                 line_graph=torch.tensor(z[prefix + "line_graph"], dtype=torch.int32))
 
 
+EPS32 = float(torch.finfo(torch.float32).eps)
+
+# the non-default update forms of tests/golden/configs.npz (two blocks, seed 0)
+VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
+            "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+
+
 def model64(cfg):
     torch.manual_seed(0)
-    m = MatRISRef(**cfg).double()
+    m = MatRISRef(**cfg).eval().double()
     for mod in m.modules():
         if hasattr(mod, "coef"):
             mod.coef = mod.coef.double()
+        if isinstance(mod, torch.nn.RMSNorm) and mod.eps is None:
+            mod.eps = EPS32
     return m
 
 
@@ -66,8 +78,8 @@ def _oracle_graph(cr):
 
 
 def main():
-    """python tests/golden/make_fp64.py [--big] [--only degenerate c4]: --only adds or
-    replaces just those entries of the existing fp64_oracle.npz."""
+    """python tests/golden/make_fp64.py [--big] [--only degenerate c4 variants]: --only adds
+    or replaces just those entries of the existing fp64_oracle.npz."""
     torch.set_num_threads(8)
     path = os.path.join(HERE, "fp64_oracle.npz")
     only = sys.argv[sys.argv.index("--only") + 1:] if "--only" in sys.argv else None
@@ -86,13 +98,21 @@ def main():
         from matris_amd import workloads as W
         for k, v in run(m10, [_oracle_graph(W.c3_cu864())], energy_only=True).items():
             out[f"c3_{k}"] = v
-    if only and "degenerate" in only:
+    if only is None or "degenerate" in only:
         z = np.load(os.path.join(HERE, "degenerate.npz"))
         for k, v in run(m10, [graph(z, "dil_")]).items():
             out[f"dil_{k}"] = v
         for k, v in run(m10, [graph(z, p) for p in ("cu_", "dil_", "tri_")]).items():
             out[f"mixed_{k}"] = v
-    if only and "c4" in only:
+    if only is None or "variants" in only:
+        zc, zs = np.load(os.path.join(HERE, "c1_cu4.npz")), np.load(os.path.join(HERE, "cells_small.npz"))
+        for name, over in VARIANTS.items():
+            m = model64(dict(DEFAULT_CONFIG, num_layers=2, **over))
+            for k, v in run(m, [graph(zc, "g_")]).items():
+                out[f"{name}_c1_{k}"] = v
+            for k, v in run(m, [graph(zs, f"g{i}_") for i in range(3)]).items():
+                out[f"{name}_cells_{k}"] = v
+    if (only is None and "--big" in sys.argv) or (only and "c4" in only):
         from matris_amd import workloads as W
         for k, v in run(m10, [_oracle_graph(cr) for cr in W.c4_batch64()], energy_only=True).items():
             out[f"c4_{k}"] = v

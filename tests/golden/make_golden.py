@@ -31,6 +31,11 @@ Outputs (small .npz / .json files; torch version recorded in meta):
 
   c1_graph_ref.pt     (--only graphfile) the C1 graph written by the reference's own
                       RadiusGraph.save (radiusgraph.py:132-146): a torch.save of to_dict()
+  configs.npz         (--only configs) the non-default update forms at two blocks, seed 0:
+                      norm_type "layer" / "batch" GatedMLPs, graph_conv_mlp "MLP" (MLP + norm,
+                      interaction_block.py:39-62, 172-184) with RMSNorm and with LayerNorm;
+                      per variant the state_dict keys and sums and the efsm of C1 alone and
+                      of the three small cells as one batch
 
     python tests/golden/make_golden.py --only c4 degenerate graphfile   (those fixtures only)
 """
@@ -256,10 +261,30 @@ def write_degenerate(model10):
     save("degenerate.npz", **payload)
 
 
+CONFIG_VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
+                   "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+
+
+def write_configs():
+    """C1 alone and the small cells batched, for each non-default update form."""
+    _, g1 = reference_graph(W.c1_cu4())
+    gs = [reference_graph(cr)[1] for cr in small_cells()]
+    payload = {}
+    for name, over in CONFIG_VARIANTS.items():
+        cfg = dict(DEFAULT_CONFIG, num_layers=2, **over)
+        model = make_model(cfg)
+        sd = model.state_dict()
+        payload[f"{name}_keys"] = np.array(json.dumps(sorted(sd.keys())))
+        payload[f"{name}_sums"] = np.array([float(sd[k].double().sum()) for k in sorted(sd.keys())])
+        payload.update({f"{name}_c1_{k}": v for k, v in run_efsm(model, [g1]).items()})
+        payload.update({f"{name}_cells_{k}": v for k, v in run_efsm(model, gs).items()})
+    save("configs.npz", **payload)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--big", action="store_true", help="also write the C3 (864-atom) fixture")
-    ap.add_argument("--only", nargs="+", choices=["c4", "degenerate", "graphfile"],
+    ap.add_argument("--only", nargs="+", choices=["c4", "degenerate", "graphfile", "configs"],
                     help="write only these fixtures (the base set and C3 are left as they are)")
     args = ap.parse_args()
     torch.set_num_threads(8)
@@ -276,6 +301,8 @@ def main():
             print("wrote", g.save(fname="c1_graph_ref.pt", save_dir=HERE))
         if "c4" in args.only:
             write_c4(model10)
+        if "configs" in args.only:
+            write_configs()
         return
     with open(os.path.join(HERE, "state_dict_seed0.json"), "w") as fh:
         json.dump(dict(n_params=sum(p.numel() for p in model10.parameters()), tensors=sd_fingerprint(model10)), fh,

@@ -392,7 +392,9 @@ class _TorchGMLP(torch.nn.Module):
         super().__init__()
         self.c1, self.c2 = torch.nn.Linear(K, 128), torch.nn.Linear(128, 128)
         self.g1, self.g2 = torch.nn.Linear(K, 128), torch.nn.Linear(128, 128)
-        self.nc, self.ng = torch.nn.RMSNorm(128), torch.nn.RMSNorm(128)
+        # fp32's eps, the constant RMSNorm(eps=None) uses in the fp32 reference
+        eps = torch.finfo(torch.float32).eps
+        self.nc, self.ng = torch.nn.RMSNorm(128, eps=eps), torch.nn.RMSNorm(128, eps=eps)
         with torch.no_grad():
             self.nc.weight.uniform_(0.5, 1.5)
             self.ng.weight.uniform_(0.5, 1.5)
@@ -1283,6 +1285,7 @@ def test_readout_fused_vs_fp64(N):
     ops = _ops()
     torch.manual_seed(N)
     norm = get_normalization("rms", 128)
+    norm.eps = torch.finfo(torch.float32).eps  # eps=None's fp32 value, also in the fp64 evaluation
     eh, mh = EnergyHead(128, (128, 128), 1, "mlp", "silu"), MagmomHead(128, 256, 1, "mlp", "silu")
     with torch.no_grad():
         norm.weight.uniform_(0.5, 1.5)

@@ -3,16 +3,24 @@ written from the reference modules by tests/golden/make_golden.py).
 
 Tolerances (north star): forces 1e-4 eV/A absolute, stress 1e-4 relative to the largest
 component (GPa), magmoms 1e-4 relative to the largest magnitude, energy 1e-5 relative.
-Every default-arithmetic case asserts the energy at 1e-5 relative to the reference's
-output.  Only the cases listed in FP32_FLOOR_CASES use max(1e-5 |e_ref|,
-2 |e_ref - e_fp64|) instead: the random-init model's energies are small sums with heavy
-fp32 cancellation, the reference's own fp32 result is 1.2e-5 .. 6.3e-4 (relative) away
-from the same computation in fp64 (tests/golden/fp64_oracle.npz, written by
-tests/golden/make_fp64.py from the CPU oracle), and in those cases -- the angle-free
-cell (e = -6.4e-4 eV/atom, measured 6.4e-5 against a floor of 5.9e-4), a batch that
-contains it (1.4e-5), and the bf16x6 fallback arithmetic at C1 (3.7e-5 against a floor
-of 6.3e-4) -- the GPU energy is inside that floor but not inside 1e-5.  The printed line
-reports both distances."""
+
+Two widenings, one rule for every case (_assert_close):
+  * energies below 0.01 eV/atom get the bar of a 0.01 eV/atom energy, E_ABS = 1e-7
+    eV/atom.  The random-init model's energies there are cancelled sums of O(0.1) terms
+    that fp32 resolves to a few 1e-8 eV/atom: measured against the fp64 evaluation, the
+    reference's own fp32 result is 5e-9 .. 1.7e-8 eV/atom away on C1 (-1.4e-3 eV/atom)
+    and the angle-free cell (-6.4e-4), and this build's plain fp32 MFMA products,
+    f16x3 and bf16x6 are 1.6e-8 .. 5.1e-8 away (so 2e-5 .. 8e-5 relative);
+  * where the reference's own fp32 result is farther than half a bar from the same
+    computation in fp64 (tests/golden/fp64_oracle.npz, the CPU oracle in float64 with
+    RMSNorm's fp32 eps; tests/golden/make_fp64.py), that bar becomes twice the reference's
+    distance (energies: twice its largest relative distance over the case's graphs, times
+    each graph's energy, one sample per graph being a noisy estimate).  This binds only for graph_conv_mlp "MLP" on the triclinic cells, where a
+    bias-free MLP feeds a norm and rows of small mean square amplify rounding: the
+    reference's fp32 forces there are 1.2e-4 eV/A from fp64 and its stress 6e-4.
+With an fp64 evaluation present, the GPU result must also lie within the same bars of
+it, so a widened bar cannot hide a result farther from exact arithmetic than the
+reference's own.  The printed lines report both distances."""
 import hashlib
 import os
 
@@ -25,9 +33,7 @@ from matris_amd.config import DEFAULT_CONFIG, MATRIS_10M
 pytestmark = pytest.mark.gpu
 
 E_REL, F_ABS, S_REL, M_REL = 1e-5, 1e-4, 1e-4, 1e-4
-# the only cases whose energy is held to the reference's fp32-vs-fp64 floor (docstring)
-FP32_FLOOR_CASES = ("C1 bf16x6", "empty line graph (converter)", "empty line graph (reference arrays)",
-                    "mixed batch with an angle-free cell")
+E_ABS = 1e-7  # eV/atom: the energy bar of a 0.01 eV/atom energy (docstring)
 
 
 def _model(cfg=MATRIS_10M, seed=0):
@@ -60,24 +66,40 @@ def _efsm(model, graphs):
                 m=torch.cat([m.detach() for m in out["m"]]).cpu().numpy())
 
 
+def _dists(a, b):
+    """Per-quantity distances of a from b: energy per graph (elementwise |de|), forces max
+    |df| (eV/A), stress and magmoms max |d| (as bars, scaled by the reference's largest
+    magnitude)."""
+    return {k: (np.abs(np.asarray(a[k], np.float64) - b[k]) if k == "e" else np.max(np.abs(a[k] - b[k])))
+            for k in "efsm" if k in a and k in b}
+
+
 def _assert_close(out, ref, tag, ref64=None):
     e_ref = np.asarray(ref["e"], np.float64)
-    e_bar = E_REL * np.abs(e_ref)
-    if ref64 is not None and tag in FP32_FLOOR_CASES:
-        e_bar = np.maximum(e_bar, 2.0 * np.abs(e_ref - ref64["e"]))
+    bar = {"e": np.maximum(E_REL * np.abs(e_ref), E_ABS), "f": F_ABS,
+           "s": S_REL * max(np.max(np.abs(ref["s"])), 1e-12), "m": M_REL * max(np.max(np.abs(ref["m"])), 1e-12)}
+    d_ref = _dists(out, ref)
     if ref64 is not None:
-        e64_err = np.max(np.abs(out["e"] - ref64["e"]) / np.abs(ref64["e"]))
-        print(f"{tag}: e_rel_vs_fp64={e64_err:.2e} ref_fp32_vs_fp64="
-              f"{np.max(np.abs(e_ref - ref64['e']) / np.abs(ref64['e'])):.2e}", flush=True)
-    e_ok = bool(np.all(np.abs(out["e"] - e_ref) <= e_bar))
+        d_own = _dists(ref, ref64)  # the reference's own fp32 distance from fp64
+        # energies: its largest relative distance over the case's graphs, per graph energy
+        own_e = np.max(d_own["e"] / np.abs(ref64["e"])) * np.abs(e_ref)
+        bar = {k: np.maximum(bar[k], 2.0 * (own_e if k == "e" else d_own[k])) if k in d_own else bar[k] for k in bar}
+        d64 = _dists(out, ref64)
+        print(f"{tag}: vs fp64 " + " ".join(f"{k}={np.max(d64[k] / bar[k]):.2f}bar" for k in d64)
+              + " | reference fp32 vs fp64 " + " ".join(f"{k}={np.max(d_own[k] / bar[k]):.2f}bar" for k in d_own),
+              flush=True)
     e_err = np.max(np.abs(out["e"] - e_ref) / np.maximum(np.abs(e_ref), 1e-12))
-    f_err = np.max(np.abs(out["f"] - ref["f"]))
-    s_err = np.max(np.abs(out["s"] - ref["s"])) / max(np.max(np.abs(ref["s"])), 1e-12)
-    m_err = np.max(np.abs(out["m"] - ref["m"])) / max(np.max(np.abs(ref["m"])), 1e-12)
+    f_err = d_ref["f"]
+    s_err = d_ref["s"] / max(np.max(np.abs(ref["s"])), 1e-12)
+    m_err = d_ref["m"] / max(np.max(np.abs(ref["m"])), 1e-12)
     print(f"{tag}: e_rel={e_err:.2e} f_abs={f_err:.2e} s_rel={s_err:.2e} m_rel={m_err:.2e}", flush=True)
     with open(os.environ.get("MATRIS_PARITY_LOG", os.devnull), "a") as fh:
         fh.write(f"{tag}: e_rel={e_err:.3e} f_abs={f_err:.3e} s_rel={s_err:.3e} m_rel={m_err:.3e}\n")
-    assert e_ok and f_err <= F_ABS and s_err <= S_REL and m_err <= M_REL
+    for k in d_ref:
+        assert np.all(d_ref[k] <= bar[k]), (tag, k, "vs reference", d_ref[k], bar[k])
+    if ref64 is not None:
+        for k in d64:
+            assert np.all(d64[k] <= bar[k]), (tag, k, "vs fp64", d64[k], bar[k])
 
 
 def _fp64(golden, prefix):
@@ -421,3 +443,40 @@ def test_f16x3_matches_fp32_mfma_across_activation_scales(golden, scale):
     for k in "efsm":
         assert np.all(np.isfinite(out[k])), k
     assert e_rel <= 1e-5 and f_rel <= 1e-4 and s_rel <= 1e-4 and m_rel <= 1e-4
+
+
+CONFIG_VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
+                   "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+
+
+@pytest.mark.parametrize("name", list(CONFIG_VARIANTS))
+def test_non_default_update_forms_vs_reference_golden(golden, name):
+    """LayerNorm / BatchNorm GatedMLPs and graph_conv_mlp "MLP" (MLP then the norm) at two
+    blocks, seed 0, against the reference modules' outputs (tests/golden/configs.npz): C1
+    alone and the three triclinic cells as one batch.  These forms run the generic layer
+    path (device gathers, segment attention / sums, the update as torch layers)."""
+    z, zc, zs = golden("configs.npz"), golden("c1_cu4.npz"), golden("cells_small.npz")
+    model = _model(dict(DEFAULT_CONFIG, num_layers=2, **CONFIG_VARIANTS[name]))
+    for tag, graphs in (("c1", [_graph_from_arrays(zc, "g_")]),
+                        ("cells", [_graph_from_arrays(zs, f"g{i}_") for i in range(3)])):
+        _assert_close(_efsm(model, graphs), {k: z[f"{name}_{tag}_{k}"] for k in "efsm"}, f"{name} {tag}",
+                      _fp64(golden, f"{name}_{tag}"))
+
+
+def test_fp16_update_runs_under_autocast():
+    """use_fp16 (functions.py:231-242): the MLPs run under fp16 autocast and return fp32; the
+    GatedMLP is then not the fused form and its device forward is the module's own."""
+    from matris_amd.model.model import GatedMLP
+    torch.manual_seed(0)
+    g16 = GatedMLP(384, 128, 128, norm_type="rms", use_fp16=True).cuda()
+    g32 = GatedMLP(384, 128, 128, norm_type="rms").cuda()
+    g32.load_state_dict(g16.state_dict())
+    xs = [(torch.randn(1000, 128, device="cuda"), None) for _ in range(3)]
+    out16 = g16.fused(xs)
+    out32 = g32.fused(xs)  # matris_gmlp_fwd
+    assert out16.dtype == torch.float32 and out16.shape == (1000, 128)
+    err = (out16 - out32).abs().max().item() / out32.abs().max().item()
+    print(f"fp16 autocast GatedMLP vs fused fp32: rel {err:.2e}", flush=True)
+    assert 0 < err < 1e-2  # fp16 products (11-bit mantissa), not the fp32-grade fused kernel
+    with pytest.raises(ValueError, match="each source must be"):
+        g32.fused([(torch.randn(1000, 384, device="cuda"), None)])  # one 384-wide source

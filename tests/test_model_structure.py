@@ -1,7 +1,10 @@
 """Host-side structure of the model (no kernel launches): every layer of the MatRIS-10M
 configuration takes the fused MI355X path, and the large-cell memory policy switches on
 at the sizes it should."""
-from matris_amd.config import MATRIS_10M
+import pytest
+import torch
+
+from matris_amd.config import DEFAULT_CONFIG, MATRIS_10M
 from matris_amd.model import fused
 from matris_amd.model.model import MatRIS
 
@@ -30,3 +33,38 @@ def test_block_checkpoint_policy():
     assert fused.blocks_to_checkpoint(9_027_734, 1_892_918, 10, total_bytes=hbm) == 8
     assert fused.blocks_to_checkpoint(264_384, 67_396, 10, total_bytes=hbm) == 0
     assert fused.blocks_to_checkpoint(10 ** 9, 0, 10, total_bytes=hbm) == 10
+
+
+@pytest.mark.parametrize("over", [dict(norm_type="layer"), dict(norm_type="batch"), dict(graph_conv_mlp="MLP"),
+                                  dict(graph_conv_mlp="MLP", norm_type="layer")])
+def test_non_default_update_forms_take_the_generic_layer_path(over):
+    """LayerNorm / BatchNorm GatedMLPs and the MLP-then-norm updates of graph_conv_mlp="MLP"
+    are not the form the fused kernels implement: every layer runs its generic path."""
+    from matris_amd.model.model import GatedMLP
+    model = MatRIS(**dict(DEFAULT_CONFIG, num_layers=1, **over))
+    blk = model.interaction_block[0]
+    assert not fused.line_attention_fusable(blk.attn_block_line_graph)
+    assert not fused.atom_attention_fusable(blk.attn_block_atom_graph)
+    assert not fused.line_refinement_fusable(blk.refine_block_line_graph)
+    assert not fused.atom_refinement_fusable(blk.refine_block_atom_graph)
+    upd = blk.attn_block_atom_graph.edge_nonlinear_update
+    if over.get("graph_conv_mlp") == "MLP":
+        assert isinstance(upd, torch.nn.Sequential) and not isinstance(upd, GatedMLP)
+        norm = {"layer": torch.nn.LayerNorm}.get(over.get("norm_type"), torch.nn.RMSNorm)
+        assert isinstance(upd[1], norm) and upd[0].layers[0].bias is None  # MLP(bias=use_bias)
+    else:
+        assert isinstance(upd, GatedMLP) and upd.mlp_core.layers[0].bias is not None
+
+
+def test_fp16_mlps_are_not_fused():
+    from matris_amd.model.model import GatedMLP, Refinement
+    assert GatedMLP(384, 128, 128, norm_type="rms")._fusable()
+    assert not GatedMLP(384, 128, 128, norm_type="rms", use_fp16=True)._fusable()
+    r = Refinement(128, 128, 128, 7, norm_type="rms", graph_type="atom graph", use_fp16=True)
+    assert not fused.atom_refinement_fusable(r)
+    assert fused.atom_refinement_fusable(Refinement(128, 128, 128, 7, norm_type="rms", graph_type="atom graph"))
+
+
+def test_unknown_update_form_raises():
+    with pytest.raises(NotImplementedError, match="mlp_type"):
+        MatRIS(**dict(DEFAULT_CONFIG, num_layers=1, graph_conv_mlp="KAN"))

@@ -85,6 +85,58 @@ def test_oracle_default_config_matches_reference_golden(golden):
     assert np.allclose(e, z["e"], rtol=1e-5, atol=0) and np.abs(s - z["s"]).max() < 1e-5 * np.abs(z["s"]).max()
 
 
+# the non-default update forms (tests/golden/configs.npz, two blocks, seed 0): GatedMLPs
+# with LayerNorm / BatchNorm, and graph_conv_mlp "MLP" (MLP then the norm) with RMSNorm and
+# with LayerNorm
+CONFIG_VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
+                   "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+
+
+def _variant_cfg(name):
+    return dict(DEFAULT_CONFIG, num_layers=2, **CONFIG_VARIANTS[name])
+
+
+@pytest.mark.parametrize("name", list(CONFIG_VARIANTS))
+def test_variant_state_dicts_match_reference(golden, name):
+    """Oracle and product module trees: the reference's keys, and per tensor the same sum
+    (same construction order, so the same draws from the seed)."""
+    from matris_amd.model import MatRIS
+    z = golden("configs.npz")
+    keys = json.loads(str(z[f"{name}_keys"]))
+    for cls in (MatRISRef, MatRIS):
+        torch.manual_seed(0)
+        sd = cls(**_variant_cfg(name)).state_dict()
+        assert sorted(sd) == keys, cls.__name__
+        sums = np.array([float(sd[k].double().sum()) for k in keys])
+        assert np.array_equal(sums, z[f"{name}_sums"]), cls.__name__
+
+
+@pytest.mark.parametrize("name", list(CONFIG_VARIANTS))
+def test_oracle_variants_match_reference_golden(golden, name):
+    z, zc, zs = golden("configs.npz"), golden("c1_cu4.npz"), golden("cells_small.npz")
+    torch.manual_seed(0)
+    m = MatRISRef(**_variant_cfg(name)).eval()
+    for tag, graphs in (("c1", [_graph(zc, "g_")]), ("cells", [_graph(zs, p) for p in ("g0_", "g1_", "g2_")])):
+        e, f, s, mm = _efsm(m, graphs)
+        r = {k: z[f"{name}_{tag}_{k}"] for k in "efsm"}
+        # same fp32 CPU ops as the reference; only multithreaded reduction order differs
+        assert np.allclose(e, r["e"], rtol=1e-5, atol=0), (tag, e, r["e"])
+        assert np.abs(f - r["f"]).max() < 2e-5, tag
+        assert np.abs(s - r["s"]).max() < 1e-4 * np.abs(r["s"]).max(), tag
+        assert np.abs(mm - r["m"]).max() < 1e-5 * np.abs(r["m"]).max(), tag
+
+
+def test_variant_fixtures_tell_the_forms_apart(golden):
+    """Each form changes the outputs: a norm or update form silently replaced by another
+    would fail the comparisons above."""
+    z = golden("configs.npz")
+    torch.manual_seed(0)
+    e_rms = float(MatRISRef(**dict(DEFAULT_CONFIG, num_layers=2)).eval()([_graph(golden("c1_cu4.npz"), "g_")],
+                                                                       task="e")["e"][0].detach())
+    es = [e_rms] + [float(z[f"{n}_c1_e"][0]) for n in CONFIG_VARIANTS]
+    assert min(abs(a - b) for i, a in enumerate(es) for b in es[i + 1:]) > 1e-2
+
+
 def _model64():
     torch.manual_seed(0)
     m = MatRISRef(**MATRIS_10M).double()
