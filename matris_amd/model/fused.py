@@ -188,8 +188,18 @@ def line_attention_fusable(layer) -> bool:
             and t.bias is None and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 
 
+# the envelope kernels (matris_env_linear, matris_env_agg_bwd_env_proj, matris_seg_sum_mul_proj)
+# take at most this many basis functions per row
+ENV_BASIS_MAX = 8
+
+
+def _env_ok(layer) -> bool:
+    env = layer.learnable_envelope
+    return env.bias is None and env.in_features <= ENV_BASIS_MAX and env.out_features == D
+
+
 def line_refinement_fusable(layer) -> bool:
-    return (layer.graph_type == "line graph" and _gmlp_fusable(layer.edge_nonlinear_update)
+    return (layer.graph_type == "line graph" and _gmlp_fusable(layer.edge_nonlinear_update) and _env_ok(layer)
             and _ffn_fusable(layer.node_FFN) and _ffn_fusable(layer.edge_FFN)
             and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 
@@ -399,7 +409,7 @@ def atom_attention_fusable(layer) -> bool:
 
 
 def atom_refinement_fusable(layer) -> bool:
-    return (layer.graph_type == "atom graph" and _gmlp_fusable(layer.edge_nonlinear_update)
+    return (layer.graph_type == "atom graph" and _gmlp_fusable(layer.edge_nonlinear_update) and _env_ok(layer)
             and _ffn_fusable(layer.node_FFN) and _ffn_fusable(layer.edge_FFN)
             and _res_ok(layer.node_res_weight) and _res_ok(layer.edge_res_weight))
 

@@ -34,8 +34,9 @@ from torch import Tensor, nn
 
 from ..config import EV_A3_TO_GPA
 from ..graph.converter import GraphConverter
-from . import fused, ops
+from . import basis_generic, direct_head, fused, ops
 from .atomref import AtomRef
+from .basis_generic import FourierExpansion, GaussianExpansion
 from .batch import process_graphs
 
 
@@ -246,25 +247,33 @@ class BesselExpansion(nn.Module):
         self.envelope_func = PolynomialEnvelope(cutoff, envelope_exponent) if envelope_exponent is not None else None
 
     def forward(self, dist, return_smooth_factor=False):
-        """B_n(r) env(r) on the device (matris_bessel_fwd / _bwd); there is no host path."""
-        if self.envelope_func is None or return_smooth_factor:
-            raise NotImplementedError("the MI355X path evaluates the enveloped Bessel basis only")
+        """B_n(r) env(r) on the device (matris_bessel_fwd / _bwd); without an envelope
+        (envelope_exponent=None) the plain basis as torch on the device.  With
+        return_smooth_factor, (basis, env(r) [n, 1]) when there is an envelope."""
         if not dist.is_cuda:
             raise RuntimeError("matris_amd ops run on the ROCm device only (no CPU fallback)")
-        return ops.bessel(dist, self.frequencies, self.envelope_func.cutoff, self.envelope_func.p)
+        if self.envelope_func is None:
+            return basis_generic.bessel_plain(dist, self.frequencies, self.inv_cutoff, self.norm_const)
+        out = ops.bessel(dist, self.frequencies, self.envelope_func.cutoff, self.envelope_func.p)
+        if return_smooth_factor:
+            return out, self.envelope_func(dist[:, None])
+        return out
 
 
 class SphericalExpansion(nn.Module):
     """basis_function.py:222-338: the spherical-Bessel radial table times Legendre Y_l.
-    The basis itself is computed on the device (matris_sbf_fwd / _bwd, which hold the
-    root table); this module carries the reference's buffer so state_dict keys match."""
+    The 4 x 4 basis is computed on the device by matris_sbf_fwd / _bwd (which hold the
+    root table); smaller ones (max_n, max_l <= 4) by basis_generic.spherical_basis."""
 
     def __init__(self, max_n=4, max_l=4, cutoff=6):
         super().__init__()
-        if max_n != 4 or max_l != 4:
-            raise NotImplementedError("the MI355X path implements the 4 x 4 spherical basis (max_n = max_l = 4)")
+        if not (1 <= max_n <= 4 and 1 <= max_l <= 4):
+            raise ValueError("SphericalExpansion: max_n and max_l must be 1..4")
         self.max_n, self.max_l, self.cutoff = max_n, max_l, cutoff
         self.register_buffer("factor", torch.sqrt(torch.tensor(2.0 / (cutoff ** 3))))
+
+    def forward(self, dist, three_body):
+        return basis_generic.spherical_basis(dist, three_body, self.max_n, self.max_l, self.cutoff, self.factor)
 
 
 # ------------------------------------------------------------------------------------
@@ -308,11 +317,15 @@ class EdgeBasisEmbedding(nn.Module):
     def __init__(self, pairwise_cutoff=6, three_body_cutoff=4, num_radial=7, edge_feat_dim=128,
                  envelope_exponent=8, distance_expansion="Bessel", learnable=False):
         super().__init__()
-        if distance_expansion.lower() != "bessel":
-            raise NotImplementedError("only the Bessel distance expansion is on the MI355X path")
         self.distance_expansion = distance_expansion
-        self.pairwise_rbf_expansion = BesselExpansion(num_radial, pairwise_cutoff, envelope_exponent, learnable)
-        self.threebody_rbf_expansion = BesselExpansion(num_radial, three_body_cutoff, envelope_exponent, learnable)
+        if distance_expansion.lower() == "bessel":
+            self.pairwise_rbf_expansion = BesselExpansion(num_radial, pairwise_cutoff, envelope_exponent, learnable)
+            self.threebody_rbf_expansion = BesselExpansion(num_radial, three_body_cutoff, envelope_exponent, learnable)
+        elif distance_expansion.lower() == "gaussian":  # torch on the device (basis_generic)
+            self.pairwise_rbf_expansion = GaussianExpansion(0.0, pairwise_cutoff, num_radial, 2.0)
+            self.threebody_rbf_expansion = GaussianExpansion(0.0, three_body_cutoff, num_radial, 2.0)
+        else:
+            raise NotImplementedError(f"Unknown distance_expansion: {distance_expansion}")
         self.edge_linear1 = nn.Linear(num_radial, edge_feat_dim, bias=False)
         self.edge_linear2 = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
         self.swish_layer = SwishLayer(edge_feat_dim, edge_feat_dim, bias=False)
@@ -322,7 +335,7 @@ class EdgeBasisEmbedding(nn.Module):
     def _fusable(self) -> bool:
         """The configuration matris_edge_embed_fwd implements (MatRIS-10M's)."""
         b6, b4, ln = self.pairwise_rbf_expansion, self.threebody_rbf_expansion, self.edge_init_norm
-        return (b6.envelope_func is not None and b4.envelope_func is not None and b6.num_radial == 7
+        return (isinstance(b6, BesselExpansion) and isinstance(b4, BesselExpansion) and b6.envelope_func is not None and b4.envelope_func is not None and b6.num_radial == 7
                 and b4.num_radial == 7 and b6.envelope_func.p == b4.envelope_func.p
                 and self.edge_linear1.bias is None and tuple(self.edge_linear1.weight.shape) == (128, 7)
                 and self.edge_linear2.bias is None and tuple(self.edge_linear2.weight.shape) == (128, 128)
@@ -345,23 +358,43 @@ class EdgeBasisEmbedding(nn.Module):
 
 
 class ThreebodyEmbedding(nn.Module):
-    """feature_embed.py:151-203 (SH expansion)."""
+    """feature_embed.py:151-203.  The 4 x 4 SH expansion runs on the device kernels
+    (matris_sbf_*, matris_tb_embed_*); a smaller SH basis and the Fourier expansion
+    (three_body_expansion="fourier", num_angular features) as torch on the device."""
 
     def __init__(self, num_angular=7, max_n=4, max_l=4, cutoff=6, three_body_feat_dim=128,
-                 three_body_expansion="sh", learnable=True):
+                 three_body_expansion="fourier", learnable=True):
         super().__init__()
         self.three_body_expansion = three_body_expansion.lower()
-        if self.three_body_expansion != "sh":
-            raise NotImplementedError("only the SH three-body expansion is on the MI355X path")
-        self.expansion = SphericalExpansion(max_n=max_n, max_l=max_l, cutoff=cutoff)
-        self.angle_embedding = nn.Linear(max_n * max_l, three_body_feat_dim, bias=False)
+        if self.three_body_expansion == "fourier":
+            self.expansion = FourierExpansion(max_f=(num_angular - 1) // 2, learnable=learnable)
+            self.angle_embedding = nn.Linear(num_angular, three_body_feat_dim, bias=False)
+        elif self.three_body_expansion == "sh":
+            self.expansion = SphericalExpansion(max_n=max_n, max_l=max_l, cutoff=cutoff)
+            self.angle_embedding = nn.Linear(max_n * max_l, three_body_feat_dim, bias=False)
+        else:
+            raise NotImplementedError(f"Unknown three_body_expansion: {three_body_expansion}")
         self.swish_layer = SwishLayer(three_body_feat_dim, three_body_feat_dim, bias=False)
         self._pack = ops._WeightPack()
+
+    def _generic(self, graphs):
+        """The basis from the angle between each angle's two unit edge vectors (the
+        reference's acos of their dot product times 1 - 1e-6), torch on the device."""
+        lg = graphs["line_graph_dict"]
+        u = graphs["unit_edge_vectors"]
+        v_ij = torch.index_select(u, 0, lg["target_DE_index"])
+        v_jk = torch.index_select(u, 0, lg["source_DE_index"])
+        angle = torch.acos(torch.sum(v_ij * v_jk, dim=1) * (1 - 1e-6))
+        if self.three_body_expansion == "sh":
+            return self.expansion(torch.norm(v_jk, dim=1), angle)
+        return self.expansion(angle)
 
     def forward(self, graphs):
         lg = graphs["line_graph_dict"]
         if not graphs["unit_edge_vectors"].is_cuda:
             raise RuntimeError("matris_amd ops run on the ROCm device only (no CPU fallback)")
+        if self.three_body_expansion != "sh" or self.expansion.max_n != 4 or self.expansion.max_l != 4:
+            return self.swish_layer(self.angle_embedding(self._generic(graphs)))
         basis = ops.spherical_basis(graphs["unit_edge_vectors"], lg["grp_de_t"], lg["grp_de_s"], self.expansion.cutoff)
         lin = self.swish_layer.linear
         if (ops.tb_embed_supported() and self.angle_embedding.bias is None and lin.bias is None
@@ -573,17 +606,37 @@ class MagmomHead(nn.Module):
 
 
 class ForceStressHead(nn.Module):
-    """readout.py:136-224, conservative branch: forces and stress by autograd."""
+    """readout.py:136-252.  Conservative (the default): forces and stress by autograd.
+    Direct (is_conservation=False): an equivariant stress head and an MLP force head
+    (direct_head.py), evaluated in the forward."""
 
-    def __init__(self, is_conservation=True, **_unused):
+    def __init__(self, is_conservation=True, feat_dim=128, hidden_dim=128, output_dim=3, mlp_type="mlp",
+                 activation_type="silu"):
         super().__init__()
-        if not is_conservation:
-            raise NotImplementedError("the MI355X path implements the conservative force/stress head")
         self.is_conservation = is_conservation
+        if not is_conservation:
+            hd = [hidden_dim] if isinstance(hidden_dim, int) else list(hidden_dim)
+            self.stress_head = direct_head.EquivariantHead(feat_dim, lmax=2, use_bias=False,
+                                                           make_activation=lambda: get_activation(activation_type))
+            if mlp_type.lower() == "mlp":
+                self.force_head = MLP(feat_dim, hd, output_dim, activation=activation_type)
+            elif mlp_type.lower() == "gatemlp":  # readout.py:175-184
+                self.force_head = nn.Sequential(GatedMLP(feat_dim, hd, hd[-1], norm_type="layer",
+                                                         activation=activation_type),
+                                                nn.Linear(hd[-1], output_dim))
+            else:
+                raise NotImplementedError(f"Unknown mlp_type: {mlp_type}")
 
     def forward(self, batch_graph, compute_force=True, compute_stress=True, total_energy=None, is_training=False,
-                **_unused):
+                node_feat=None, edge_feat=None):
         pred = {}
+        if not self.is_conservation:
+            if compute_stress:
+                pred["s"] = list(torch.unbind(direct_head.direct_stress(self.stress_head, node_feat, batch_graph), 0))
+            if compute_force:
+                f = direct_head.direct_forces(self.force_head, edge_feat, batch_graph)
+                pred["f"] = torch.split(f, batch_graph["atoms_per_graph"])
+            return pred
         if compute_force and compute_stress:
             gc, gs = torch.autograd.grad(total_energy.sum(),
                                          [batch_graph["batch_cart_coords"], batch_graph["batch_strains"]],
@@ -638,7 +691,8 @@ class MatRIS(nn.Module):
         self.readout_norm = get_normalization(norm_type, dim=node_feat_dim)
         self.energy_head = EnergyHead(node_feat_dim, mlp_hidden_dims, 1, "mlp", activation_type)
         self.magmom_head = MagmomHead(node_feat_dim, 2 * node_feat_dim, 1, "mlp", activation_type)
-        self.force_stress_head = ForceStressHead(is_conservation=is_conservation)
+        self.force_stress_head = ForceStressHead(is_conservation, edge_feat_dim, mlp_hidden_dims, 3, "mlp",
+                                                 activation_type)
         self._readout_pack = ops.ReadoutPack()  # the fused readout's weight layouts (no RNG)
         if verbose:
             print(f"MatRIS initialized with {self.get_params()} parameters")
@@ -726,7 +780,7 @@ class MatRIS(nn.Module):
                                                                    use_reentrant=False, context_fn=_ckpt_contexts)
             else:
                 node, edge, tb = layer(bg, node, edge, tb, smooth)
-        if self._readout_fusable():
+        if self._readout_fusable() and self.force_stress_head.is_conservation:
             # readout_norm, the energy MLP and the magmom MLP in one launch (matris_readout_fwd);
             # the energy's backward in one more (matris_readout_bwd)
             pack = self._readout_pack.get(self.readout_norm, self.energy_head.energy_head,
@@ -742,7 +796,8 @@ class MatRIS(nn.Module):
             node = self.readout_norm(node)
             total = self.energy_head(bg, node)
             pred.update(self.force_stress_head(bg, compute_force="f" in task, compute_stress="s" in task,
-                                               total_energy=total, is_training=is_training))
+                                               total_energy=total, is_training=is_training, node_feat=node,
+                                               edge_feat=edge))
             if "m" in task:
                 pred["m"] = self.magmom_head(bg, node)
         apg = bg["atoms_per_graph32"]  # made with the graph's topology: no host-to-device copy here

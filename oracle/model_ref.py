@@ -15,6 +15,9 @@ Pins (see tests/test_oracle_model.py):
   * the non-default update forms (LayerNorm / BatchNorm GatedMLPs, graph_conv_mlp "MLP"
     with RMSNorm and with LayerNorm): per-tensor state_dict sums and the e/f/s/m of C1 and
     of three batched triclinic cells, from the reference modules (tests/golden/configs.npz);
+  * the other constructor options (Gaussian and Fourier bases, smaller SH bases, no
+    envelope, 9 radial functions, fixed bases, extensive energy, the direct force/stress
+    head) in the same form (tests/golden/options.npz);
   * parameter counts 6,286,736 (defaults) / 10,379,664 (num_layers=10);
   * sum of forces = 0, stress symmetry, rotation equivariance, finite-difference
     forces and stress in fp64.
@@ -192,21 +195,55 @@ class BesselExpansion(nn.Module):
             self.frequencies = nn.Parameter(freq, requires_grad=True)
         else:
             self.register_buffer("frequencies", freq)
-        self.envelope_func = PolynomialEnvelope(cutoff, envelope_exponent)
+        self.envelope_func = PolynomialEnvelope(cutoff, envelope_exponent) if envelope_exponent is not None else None
 
     def forward(self, dist):
         dist = dist[:, None]
         out = self.norm_const * torch.sin(self.frequencies * (dist * self.inv_cutoff)) / dist
-        return self.envelope_func(dist) * out
+        return out if self.envelope_func is None else self.envelope_func(dist) * out
 
 
-def spherical_harmonics_l3(x: Tensor) -> Tensor:
-    """basis_function.py:53-77 with lmax=3 (Y_l(cos theta), m=0)."""
+class GaussianExpansion(nn.Module):
+    """basis_function.py:189-219."""
+
+    def __init__(self, start=0.0, stop=6.0, num_gaussians=7, basis_width_scalar=2.0):
+        super().__init__()
+        offset = torch.linspace(start, stop, num_gaussians)
+        self.coeff = -0.5 / (basis_width_scalar * (offset[1] - offset[0])).item() ** 2
+        self.register_buffer("offset", offset)
+
+    def forward(self, dist):
+        return torch.exp(self.coeff * (dist.view(-1, 1) - self.offset.view(1, -1)) ** 2)
+
+
+class FourierExpansion(nn.Module):
+    """basis_function.py:79-113."""
+
+    def __init__(self, max_f=5, scale=math.pi, learnable=False):
+        super().__init__()
+        self.max_f, self.scale = max_f, math.sqrt(scale)
+        freq = torch.arange(1, max_f + 1, dtype=torch.float)
+        if learnable:
+            self.frequencies = nn.Parameter(freq, requires_grad=True)
+        else:
+            self.register_buffer("frequencies", freq)
+
+    def forward(self, angle):
+        out = angle.new_zeros(angle.shape[0], 1 + 2 * self.max_f)
+        out[:, 0] = 1.0 / math.sqrt(2.0)
+        t = torch.outer(angle, self.frequencies)
+        out[:, 1:self.max_f + 1] = torch.sin(t)
+        out[:, self.max_f + 1:] = torch.cos(t)
+        return out / self.scale
+
+
+def spherical_harmonics_l3(x: Tensor, lmax: int = 3) -> Tensor:
+    """basis_function.py:53-77 (Y_l(cos theta), m=0, l = 0..lmax)."""
     y0 = torch.ones_like(x) * 0.5 * math.sqrt(1.0 / math.pi)
     y1 = math.sqrt(3.0 / (4.0 * math.pi)) * x
     y2 = math.sqrt(5.0 / (16.0 * math.pi)) * (3.0 * x ** 2 - 1.0)
     y3 = math.sqrt(7.0 / (16.0 * math.pi)) * x * (5.0 * x ** 2 - 3.0)
-    return torch.stack([y0, y1, y2, y3], dim=-1)
+    return torch.stack([y0, y1, y2, y3][:lmax + 1], dim=-1)
 
 
 # Coefficient table of the spherical Bessel radial functions, basis_function.py:241-274
@@ -235,11 +272,11 @@ SBF_COEF = {
 
 
 class SphericalExpansion(nn.Module):
-    """basis_function.py:222-338 with max_n = max_l = 4."""
+    """basis_function.py:222-338 (max_n, max_l <= 4)."""
 
     def __init__(self, max_n=4, max_l=4, cutoff=6):
         super().__init__()
-        assert max_n == 4 and max_l == 4, "only the default 4x4 expansion is restated"
+        assert 1 <= max_n <= 4 and 1 <= max_l <= 4
         self.max_n, self.max_l, self.cutoff = max_n, max_l, cutoff
         self.register_buffer("factor", torch.sqrt(torch.tensor(2.0 / (cutoff ** 3))))
         coef = torch.zeros(4, 9, 4)
@@ -253,18 +290,25 @@ class SphericalExpansion(nn.Module):
         c = self.coef
         x = dist / self.cutoff
         rbfs = []
-        for j in range(4):
+        L = range(self.max_l)
+        for j in L:
             rbfs.append(torch.sin(c[0, 0, j] * x) / x)
-        for j in range(4):
-            rbfs.append((c[1, 0, j] * x * torch.cos(c[1, 1, j] * x) + c[1, 2, j] * torch.sin(c[1, 3, j] * x)) / x ** 2)
-        for j in range(4):
-            rbfs.append((c[2, 0, j] * x ** 2 * torch.sin(c[2, 1, j] * x) - c[2, 2, j] * x * torch.cos(c[2, 3, j] * x)
-                         + c[2, 4, j] * torch.sin(c[2, 5, j] * x)) / x ** 3)
-        for j in range(4):
-            rbfs.append((c[3, 0, j] * x ** 3 * torch.cos(c[3, 1, j] * x) - c[3, 2, j] * x ** 2 * torch.sin(c[3, 3, j] * x)
-                         - c[3, 4, j] * x * torch.cos(c[3, 5, j] * x) + c[3, 6, j] * torch.sin(c[3, 7, j] * x)) / x ** 4)
+        if self.max_n > 1:
+            for j in L:
+                rbfs.append((c[1, 0, j] * x * torch.cos(c[1, 1, j] * x) + c[1, 2, j] * torch.sin(c[1, 3, j] * x))
+                            / x ** 2)
+        if self.max_n > 2:
+            for j in L:
+                rbfs.append((c[2, 0, j] * x ** 2 * torch.sin(c[2, 1, j] * x) - c[2, 2, j] * x * torch.cos(c[2, 3, j] * x)
+                             + c[2, 4, j] * torch.sin(c[2, 5, j] * x)) / x ** 3)
+        if self.max_n > 3:
+            for j in L:
+                rbfs.append((c[3, 0, j] * x ** 3 * torch.cos(c[3, 1, j] * x)
+                             - c[3, 2, j] * x ** 2 * torch.sin(c[3, 3, j] * x)
+                             - c[3, 4, j] * x * torch.cos(c[3, 5, j] * x) + c[3, 6, j] * torch.sin(c[3, 7, j] * x))
+                            / x ** 4)
         rbfs = torch.stack(rbfs, dim=-1) * self.factor
-        cbfs = spherical_harmonics_l3(torch.cos(three_body)).repeat_interleave(self.max_n, dim=1)
+        cbfs = spherical_harmonics_l3(torch.cos(three_body), self.max_l - 1).repeat_interleave(self.max_n, dim=1)
         return rbfs * cbfs
 
 
@@ -284,14 +328,18 @@ class AtomTypeEmbedding(nn.Module):
 
 
 class EdgeBasisEmbedding(nn.Module):
-    """feature_embed.py:42-148 (Bessel branch)."""
+    """feature_embed.py:42-148."""
 
     def __init__(self, pairwise_cutoff=6, three_body_cutoff=4, num_radial=7, edge_feat_dim=128,
                  envelope_exponent=8, distance_expansion="Bessel", learnable=False):
         super().__init__()
-        assert distance_expansion.lower() == "bessel"
-        self.pairwise_rbf_expansion = BesselExpansion(num_radial, pairwise_cutoff, envelope_exponent, learnable)
-        self.threebody_rbf_expansion = BesselExpansion(num_radial, three_body_cutoff, envelope_exponent, learnable)
+        if distance_expansion.lower() == "bessel":
+            self.pairwise_rbf_expansion = BesselExpansion(num_radial, pairwise_cutoff, envelope_exponent, learnable)
+            self.threebody_rbf_expansion = BesselExpansion(num_radial, three_body_cutoff, envelope_exponent, learnable)
+        else:
+            assert distance_expansion.lower() == "gaussian"
+            self.pairwise_rbf_expansion = GaussianExpansion(0.0, pairwise_cutoff, num_radial, 2.0)
+            self.threebody_rbf_expansion = GaussianExpansion(0.0, three_body_cutoff, num_radial, 2.0)
         self.edge_linear1 = nn.Linear(num_radial, edge_feat_dim, bias=False)
         self.edge_linear2 = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
         self.swish_layer = SwishLayer(edge_feat_dim, edge_feat_dim, bias=False)
@@ -310,14 +358,19 @@ class EdgeBasisEmbedding(nn.Module):
 
 
 class ThreebodyEmbedding(nn.Module):
-    """feature_embed.py:151-203 (SH branch)."""
+    """feature_embed.py:151-203."""
 
     def __init__(self, num_angular=7, max_n=4, max_l=4, cutoff=6, three_body_feat_dim=128,
                  three_body_expansion="sh", learnable=True):
         super().__init__()
-        assert three_body_expansion.lower() == "sh"
-        self.expansion = SphericalExpansion(max_n, max_l, cutoff)
-        self.angle_embedding = nn.Linear(max_n * max_l, three_body_feat_dim, bias=False)
+        self.sh = three_body_expansion.lower() == "sh"
+        if self.sh:
+            self.expansion = SphericalExpansion(max_n, max_l, cutoff)
+            self.angle_embedding = nn.Linear(max_n * max_l, three_body_feat_dim, bias=False)
+        else:
+            assert three_body_expansion.lower() == "fourier"
+            self.expansion = FourierExpansion((num_angular - 1) // 2, learnable=learnable)
+            self.angle_embedding = nn.Linear(num_angular, three_body_feat_dim, bias=False)
         self.swish_layer = SwishLayer(three_body_feat_dim, three_body_feat_dim, bias=False)
 
     def forward(self, g):
@@ -326,7 +379,7 @@ class ThreebodyEmbedding(nn.Module):
         vjk = torch.index_select(g["unit_edge_vectors"], 0, lg["source_DE_index"])
         cos_t = torch.sum(vij * vjk, dim=1) * (1 - 1e-6)
         angle = torch.acos(cos_t)
-        basis = self.expansion(torch.norm(vjk, dim=1), angle)
+        basis = self.expansion(torch.norm(vjk, dim=1), angle) if self.sh else self.expansion(angle)
         return self.swish_layer(self.angle_embedding(basis))
 
 
@@ -539,10 +592,99 @@ def process_graphs(graphs, compute_stress=True):
 
 
 # --------------------------------------------------------------------------------------
+# direct force / stress head (matris/model/readout.py:136-334, functions.py:368-463)
+# --------------------------------------------------------------------------------------
+# functions.py:368-398: rows map the 9 irrep components (l = 0; l = 1 x3; l = 2 x5) of a
+# rank-2 tensor to its Cartesian entries (xx, xy, xz, yx, yy, yz, zx, zy, zz)
+_S2, _S3, _S6 = 2 ** -0.5, 3 ** -0.5, 6 ** -0.5
+CG_CHANGE_MAT = [[_S3, 0, 0, 0, _S3, 0, 0, 0, _S3],
+                 [0, 0, 0, 0, 0, _S2, 0, -_S2, 0],
+                 [0, 0, -_S2, 0, 0, 0, _S2, 0, 0],
+                 [0, _S2, 0, -_S2, 0, 0, 0, 0, 0],
+                 [0, 0, _S2, 0, 0, 0, _S2, 0, 0],
+                 [0, _S2, 0, _S2, 0, 0, 0, 0, 0],
+                 [-_S6, 0, 0, 0, 2 * _S6, 0, 0, 0, -_S6],
+                 [0, 0, 0, 0, 0, _S2, 0, _S2, 0],
+                 [-_S2, 0, 0, 0, 0, 0, 0, 0, _S2]]
+
+
+def sphere_l2(v):
+    """functions.py:436-463, lmax = 2."""
+    x, y, z = v[:, 0], v[:, 1], v[:, 2]
+    return torch.stack([torch.ones_like(x), x, y, z, math.sqrt(3.0) * x * z, math.sqrt(3.0) * x * y,
+                        y.pow(2) - 0.5 * (x.pow(2) + z.pow(2)), math.sqrt(3.0) * y * z,
+                        math.sqrt(3.0) / 2.0 * (z.pow(2) - x.pow(2))], dim=-1)
+
+
+class GatedEquivariantBlock(nn.Module):
+    """readout.py:255-292."""
+
+    def __init__(self, hidden_channels, out_channels):
+        super().__init__()
+        self.out_channels = out_channels
+        self.vec1_proj = nn.Linear(hidden_channels, hidden_channels, bias=False)
+        self.vec2_proj = nn.Linear(hidden_channels, out_channels, bias=False)
+        self.act = _SiLU()
+        self.update_net = nn.Sequential(nn.Linear(hidden_channels * 2, hidden_channels), self.act,
+                                        nn.Linear(hidden_channels, out_channels * 2))
+
+    def forward(self, feas, vec_feas):
+        vec1 = torch.norm(self.vec1_proj(vec_feas), dim=-2)
+        vec2 = self.vec2_proj(vec_feas)
+        feas, vec_feas = torch.split(self.update_net(torch.cat([feas, vec1], dim=-1)), self.out_channels, dim=-1)
+        return self.act(feas), vec_feas.unsqueeze(1) * vec2
+
+
+class EquivariantHead(nn.Module):
+    """readout.py:295-334 (lmax = 2)."""
+
+    def __init__(self, feas_dim=64):
+        super().__init__()
+        self.feas_wise_linear = nn.Linear(feas_dim, feas_dim, bias=False)
+        self.basis_wise_linear = nn.Linear(1, feas_dim, bias=False)
+        self.equivariant_block = nn.ModuleList([GatedEquivariantBlock(feas_dim, feas_dim // 2),
+                                                GatedEquivariantBlock(feas_dim // 2, 1)])
+
+    def forward(self, feas, vec):
+        vec_feas = self.basis_wise_linear(sphere_l2(vec).unsqueeze(2))
+        feas = self.feas_wise_linear(feas)
+        for layer in self.equivariant_block:
+            feas, vec_feas = layer(feas, vec_feas)
+        return vec_feas.squeeze(-1)
+
+
+class DirectHead(nn.Module):
+    """readout.py:136-252, is_conservation=False (mlp_type "mlp", as model.py:171-178)."""
+
+    def __init__(self, feat_dim, hidden_dims):
+        super().__init__()
+        self.stress_head = EquivariantHead(feat_dim)
+        self.force_head = MLP(feat_dim, hidden_dims, 3)
+
+    def forward(self, g, node_feat, edge_feat, compute_force, compute_stress):
+        pred = {}
+        if compute_stress:
+            c = g["batch_cart_coords"]
+            vec = c / ((torch.norm(c, dim=1) * (1 - 1e-6) + 1e-6).unsqueeze(1))
+            st = aggregate(self.stress_head(node_feat, vec), g["atom_segment"], None, True, None)
+            irreps = st.new_zeros(st.shape[0], 9)
+            irreps[:, 0] = st[:, 0]
+            irreps[:, 4:9] = st[:, 4:9]
+            cart = (irreps @ torch.tensor(CG_CHANGE_MAT, dtype=st.dtype)).view(-1, 3, 3)
+            pred["s"] = list(torch.unbind(cart * (1 / g["volumes"] * 160.21766208), dim=0))
+        if compute_force:
+            w = self.force_head(torch.index_select(edge_feat, 0, g["directed2undirected"])) * g["unit_edge_vectors"]
+            f = aggregate(w, g["atom_graph_dict"]["target_index"], None, False, len(node_feat))
+            pred["f"] = torch.split(f, g["atoms_per_graph"])
+        return pred
+
+
+# --------------------------------------------------------------------------------------
 # model (matris/model/model.py, readout.py)
 # --------------------------------------------------------------------------------------
 class MatRISRef(nn.Module):
-    """model.py:30-250 with the conservative readout (readout.py:18-133,193-224)."""
+    """model.py:30-250 with the conservative readout (readout.py:18-133,193-224), or the
+    direct one (is_conservation=False)."""
 
     def __init__(self, num_layers=6, node_feat_dim=128, edge_feat_dim=128, three_body_feat_dim=128,
                  mlp_hidden_dims=(128, 128), dropout=0.0, use_bias=False, distance_expansion="Bessel",
@@ -551,8 +693,9 @@ class MatRISRef(nn.Module):
                  pairwise_cutoff=6, three_body_cutoff=4, use_smoothed_for_delta_edge=False,
                  learnable_basis=True, is_intensive=True, is_conservation=True, reference_energy=None):
         super().__init__()
-        assert is_conservation and reference_energy is None
+        assert reference_energy is None
         self.is_intensive = is_intensive
+        self.is_conservation = is_conservation
         self.atom_embedding = AtomTypeEmbedding(node_feat_dim)
         self.edge_embedding = EdgeBasisEmbedding(pairwise_cutoff, three_body_cutoff, num_radial, edge_feat_dim,
                                                  envelope_exponent, distance_expansion, learnable_basis)
@@ -569,6 +712,8 @@ class MatRISRef(nn.Module):
         self.energy_head.pooling = GraphPooling(False)
         self.magmom_head = nn.Module()
         self.magmom_head.magmom_head = MLP(node_feat_dim, [2 * node_feat_dim], 1)
+        if not is_conservation:
+            self.force_stress_head = DirectHead(edge_feat_dim, hd)
 
     def forward(self, graphs, task="ef", is_training=False):
         g = process_graphs(graphs, compute_stress="s" in task)
@@ -581,7 +726,9 @@ class MatRISRef(nn.Module):
         e_atoms = self.energy_head.energy_head(node)
         total = self.energy_head.pooling(e_atoms, g["atom_segment"]).view(-1)
         pred = {}
-        if "f" in task and "s" in task:
+        if not self.is_conservation:
+            pred.update(self.force_stress_head(g, node, edge, "f" in task, "s" in task))
+        elif "f" in task and "s" in task:
             gc, gs = torch.autograd.grad(total.sum(), [g["batch_cart_coords"], g["batch_strains"]],
                                          create_graph=is_training, retain_graph=is_training)
             pred["f"] = torch.split(-gc, g["atoms_per_graph"])

@@ -12,7 +12,7 @@ rows whose mean square is small (the symmetric C1 cell, bias-free MLP-then-norm 
 feel the difference (6e-4 of the C1 energy), so every RMSNorm here gets the fp32 constant.
 
     python tests/golden/make_fp64.py [--big]
-    python tests/golden/make_fp64.py --only variants    (the non-default update forms)
+    python tests/golden/make_fp64.py --only variants    (the non-default forms and options)
 """
 from __future__ import annotations
 
@@ -43,9 +43,15 @@ def graph(z, prefix):
 
 EPS32 = float(torch.finfo(torch.float32).eps)
 
-# the non-default update forms of tests/golden/configs.npz (two blocks, seed 0)
+# the non-default update forms of tests/golden/configs.npz and the other constructor
+# options of tests/golden/options.npz (two blocks, seed 0)
 VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
-            "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+            "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer"),
+            "gauss": dict(distance_expansion="Gaussian"), "fourier": dict(three_body_expansion="fourier"),
+            "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
+            "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
+            "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
+            "direct": dict(is_conservation=False)}
 
 
 def model64(cfg):

@@ -36,6 +36,11 @@ Outputs (small .npz / .json files; torch version recorded in meta):
                       interaction_block.py:39-62, 172-184) with RMSNorm and with LayerNorm;
                       per variant the state_dict keys and sums and the efsm of C1 alone and
                       of the three small cells as one batch
+  options.npz         (--only options) the other constructor options at two blocks, seed 0,
+                      in the same form: Gaussian distance expansion, Fourier three-body
+                      expansion, SH bases of 3 x 3 and 2 x 4, no envelope, 9 radial
+                      functions, fixed (non-learnable) bases, extensive energy, and the
+                      direct force/stress head (is_conservation=False)
 
     python tests/golden/make_golden.py --only c4 degenerate graphfile   (those fixtures only)
 """
@@ -265,12 +270,19 @@ CONFIG_VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
                    "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
 
 
-def write_configs():
-    """C1 alone and the small cells batched, for each non-default update form."""
+OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict(three_body_expansion="fourier"),
+                   "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
+                   "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
+                   "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
+                   "direct": dict(is_conservation=False)}
+
+
+def write_configs(variants=None, name_out="configs.npz"):
+    """C1 alone and the small cells batched, for each variant configuration."""
     _, g1 = reference_graph(W.c1_cu4())
     gs = [reference_graph(cr)[1] for cr in small_cells()]
     payload = {}
-    for name, over in CONFIG_VARIANTS.items():
+    for name, over in (variants or CONFIG_VARIANTS).items():
         cfg = dict(DEFAULT_CONFIG, num_layers=2, **over)
         model = make_model(cfg)
         sd = model.state_dict()
@@ -278,13 +290,13 @@ def write_configs():
         payload[f"{name}_sums"] = np.array([float(sd[k].double().sum()) for k in sorted(sd.keys())])
         payload.update({f"{name}_c1_{k}": v for k, v in run_efsm(model, [g1]).items()})
         payload.update({f"{name}_cells_{k}": v for k, v in run_efsm(model, gs).items()})
-    save("configs.npz", **payload)
+    save(name_out, **payload)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--big", action="store_true", help="also write the C3 (864-atom) fixture")
-    ap.add_argument("--only", nargs="+", choices=["c4", "degenerate", "graphfile", "configs"],
+    ap.add_argument("--only", nargs="+", choices=["c4", "degenerate", "graphfile", "configs", "options"],
                     help="write only these fixtures (the base set and C3 are left as they are)")
     args = ap.parse_args()
     torch.set_num_threads(8)
@@ -303,6 +315,8 @@ def main():
             write_c4(model10)
         if "configs" in args.only:
             write_configs()
+        if "options" in args.only:
+            write_configs(OPTION_VARIANTS, "options.npz")
         return
     with open(os.path.join(HERE, "state_dict_seed0.json"), "w") as fh:
         json.dump(dict(n_params=sum(p.numel() for p in model10.parameters()), tensors=sd_fingerprint(model10)), fh,

@@ -447,16 +447,29 @@ def test_f16x3_matches_fp32_mfma_across_activation_scales(golden, scale):
 
 CONFIG_VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
                    "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict(three_body_expansion="fourier"),
+                   "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
+                   "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
+                   "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
+                   "direct": dict(is_conservation=False)}
+VARIANTS = [("configs.npz", n, o) for n, o in CONFIG_VARIANTS.items()] + \
+           [("options.npz", n, o) for n, o in OPTION_VARIANTS.items()]
 
 
-@pytest.mark.parametrize("name", list(CONFIG_VARIANTS))
-def test_non_default_update_forms_vs_reference_golden(golden, name):
-    """LayerNorm / BatchNorm GatedMLPs and graph_conv_mlp "MLP" (MLP then the norm) at two
-    blocks, seed 0, against the reference modules' outputs (tests/golden/configs.npz): C1
-    alone and the three triclinic cells as one batch.  These forms run the generic layer
-    path (device gathers, segment attention / sums, the update as torch layers)."""
-    z, zc, zs = golden("configs.npz"), golden("c1_cu4.npz"), golden("cells_small.npz")
-    model = _model(dict(DEFAULT_CONFIG, num_layers=2, **CONFIG_VARIANTS[name]))
+@pytest.mark.parametrize("fixture,name,over", VARIANTS, ids=[v[1] for v in VARIANTS])
+def test_non_default_update_forms_vs_reference_golden(golden, fixture, name, over):
+    """Every non-default constructor option at two blocks, seed 0, against the reference
+    modules' outputs: C1 alone and the three triclinic cells as one batch.
+
+    configs.npz: LayerNorm / BatchNorm GatedMLPs and graph_conv_mlp "MLP" (MLP then the
+    norm), which run the generic layer path (device gathers, segment attention / sums,
+    the update as torch layers).  options.npz: the Gaussian distance basis, the Fourier
+    three-body basis, 3 x 3 and 2 x 4 SH bases, Bessel without envelope (these four as
+    torch on the device), 9 radial functions (the Bessel kernel; the generic refinement,
+    the envelope kernels taking at most 8), fixed bases, extensive energy and the direct
+    force/stress head (forward only)."""
+    z, zc, zs = golden(fixture), golden("c1_cu4.npz"), golden("cells_small.npz")
+    model = _model(dict(DEFAULT_CONFIG, num_layers=2, **over))
     for tag, graphs in (("c1", [_graph_from_arrays(zc, "g_")]),
                         ("cells", [_graph_from_arrays(zs, f"g{i}_") for i in range(3)])):
         _assert_close(_efsm(model, graphs), {k: z[f"{name}_{tag}_{k}"] for k in "efsm"}, f"{name} {tag}",

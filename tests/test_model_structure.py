@@ -1,6 +1,8 @@
 """Host-side structure of the model (no kernel launches): every layer of the MatRIS-10M
 configuration takes the fused MI355X path, and the large-cell memory policy switches on
 at the sizes it should."""
+import math
+
 import pytest
 import torch
 
@@ -68,3 +70,19 @@ def test_fp16_mlps_are_not_fused():
 def test_unknown_update_form_raises():
     with pytest.raises(NotImplementedError, match="mlp_type"):
         MatRIS(**dict(DEFAULT_CONFIG, num_layers=1, graph_conv_mlp="KAN"))
+
+
+def test_direct_head_change_of_basis():
+    """The direct stress head's irrep -> Cartesian matrix, built from its definition, equals
+    the reference's table as the oracle restates it (functions.py:368-398), is orthonormal,
+    and its l = 2 rows reproduce the l = 2 harmonics as r^T T r (sqrt(2/3) |r|^2 scale)."""
+    import numpy as np
+    from matris_amd.model.direct_head import IRREP_TO_CARTESIAN, sphere_harmonics_l2
+    from oracle.model_ref import CG_CHANGE_MAT
+    m = IRREP_TO_CARTESIAN.double()
+    assert torch.allclose(IRREP_TO_CARTESIAN, torch.tensor(CG_CHANGE_MAT, dtype=torch.float32), atol=0, rtol=0)
+    assert torch.allclose(m @ m.T, torch.eye(9, dtype=torch.float64), atol=1e-7)
+    r = torch.tensor(np.random.default_rng(0).normal(size=(5, 3)))
+    y2 = sphere_harmonics_l2(r)[:, 4:]
+    quad = torch.einsum("ni,kij,nj->nk", r, m[4:].view(5, 3, 3), r)
+    assert torch.allclose(quad * math.sqrt(3.0 / 2.0), y2, atol=1e-6)

@@ -90,32 +90,40 @@ def test_oracle_default_config_matches_reference_golden(golden):
 # with LayerNorm
 CONFIG_VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
                    "mlp": dict(graph_conv_mlp="MLP"), "mlp_ln": dict(graph_conv_mlp="MLP", norm_type="layer")}
+# the other constructor options (tests/golden/options.npz, in the same form)
+OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict(three_body_expansion="fourier"),
+                   "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
+                   "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
+                   "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
+                   "direct": dict(is_conservation=False)}
+VARIANTS = [("configs.npz", n, o) for n, o in CONFIG_VARIANTS.items()] + \
+           [("options.npz", n, o) for n, o in OPTION_VARIANTS.items()]
 
 
-def _variant_cfg(name):
-    return dict(DEFAULT_CONFIG, num_layers=2, **CONFIG_VARIANTS[name])
+def _variant_cfg(over):
+    return dict(DEFAULT_CONFIG, num_layers=2, **over)
 
 
-@pytest.mark.parametrize("name", list(CONFIG_VARIANTS))
-def test_variant_state_dicts_match_reference(golden, name):
+@pytest.mark.parametrize("fixture,name,over", VARIANTS, ids=[v[1] for v in VARIANTS])
+def test_variant_state_dicts_match_reference(golden, fixture, name, over):
     """Oracle and product module trees: the reference's keys, and per tensor the same sum
     (same construction order, so the same draws from the seed)."""
     from matris_amd.model import MatRIS
-    z = golden("configs.npz")
+    z = golden(fixture)
     keys = json.loads(str(z[f"{name}_keys"]))
     for cls in (MatRISRef, MatRIS):
         torch.manual_seed(0)
-        sd = cls(**_variant_cfg(name)).state_dict()
+        sd = cls(**_variant_cfg(over)).state_dict()
         assert sorted(sd) == keys, cls.__name__
         sums = np.array([float(sd[k].double().sum()) for k in keys])
         assert np.array_equal(sums, z[f"{name}_sums"]), cls.__name__
 
 
-@pytest.mark.parametrize("name", list(CONFIG_VARIANTS))
-def test_oracle_variants_match_reference_golden(golden, name):
-    z, zc, zs = golden("configs.npz"), golden("c1_cu4.npz"), golden("cells_small.npz")
+@pytest.mark.parametrize("fixture,name,over", VARIANTS, ids=[v[1] for v in VARIANTS])
+def test_oracle_variants_match_reference_golden(golden, fixture, name, over):
+    z, zc, zs = golden(fixture), golden("c1_cu4.npz"), golden("cells_small.npz")
     torch.manual_seed(0)
-    m = MatRISRef(**_variant_cfg(name)).eval()
+    m = MatRISRef(**_variant_cfg(over)).eval()
     for tag, graphs in (("c1", [_graph(zc, "g_")]), ("cells", [_graph(zs, p) for p in ("g0_", "g1_", "g2_")])):
         e, f, s, mm = _efsm(m, graphs)
         r = {k: z[f"{name}_{tag}_{k}"] for k in "efsm"}
@@ -135,6 +143,29 @@ def test_variant_fixtures_tell_the_forms_apart(golden):
                                                                        task="e")["e"][0].detach())
     es = [e_rms] + [float(z[f"{n}_c1_e"][0]) for n in CONFIG_VARIANTS]
     assert min(abs(a - b) for i, a in enumerate(es) for b in es[i + 1:]) > 1e-2
+
+
+def test_option_fixtures_relations(golden):
+    """Relations among the reference's option outputs (tests/golden/options.npz) and the
+    default form at two blocks: fixed bases (learnable_basis=False) are the same function
+    at initialisation; the extensive energy is the per-atom one times the atom count; the
+    direct head leaves e and m alone and gives other f and s; every other option changes
+    the energy."""
+    z, zc, zs = golden("options.npz"), golden("c1_cu4.npz"), golden("cells_small.npz")
+    torch.manual_seed(0)
+    m = MatRISRef(**_variant_cfg({})).eval()
+    for tag, graphs in (("c1", [_graph(zc, "g_")]), ("cells", [_graph(zs, p) for p in ("g0_", "g1_", "g2_")])):
+        e, f, s, mm = _efsm(m, graphs)
+        n_atoms = np.array([len(g["atomic_number"]) for g in graphs])
+        o = {n: {k: z[f"{n}_{tag}_{k}"] for k in "efsm"} for n in OPTION_VARIANTS}
+        assert np.allclose(o["fixed"]["e"], e, rtol=1e-5) and np.abs(o["fixed"]["f"] - f).max() < 2e-5
+        assert np.allclose(o["extensive"]["e"], o["fixed"]["e"] * n_atoms, rtol=1e-6)
+        assert np.allclose(o["direct"]["e"], e, rtol=1e-5) and np.allclose(o["direct"]["m"], mm, rtol=1e-5)
+        assert np.abs(o["direct"]["s"] - s).max() > 1e-3 * np.abs(s).max()
+        if tag == "cells":  # C1's forces vanish by symmetry under every head
+            assert np.abs(o["direct"]["f"] - f).max() > 1e-3
+        for n in ("gauss", "fourier", "sh33", "sh24", "noenv", "nr9"):
+            assert np.min(np.abs(o[n]["e"] - e)) > 1e-4 * np.max(np.abs(e)), (n, tag)
 
 
 def _model64():
