@@ -54,12 +54,15 @@ def _irrep_to_cartesian() -> Tensor:
 
 
 IRREP_TO_CARTESIAN = _irrep_to_cartesian()
+_IRREP_ON = {}  # device -> its copy (made by the first eager evaluation, not inside a capture)
 
 
 def stress_from_irreps(l0: Tensor, l2: Tensor) -> Tensor:
     """[G, 3, 3] from the l = 0 component l0 [G] and the l = 2 components l2 [G, 5]
     (reshape_stress, functions.py:414-433)."""
-    m = IRREP_TO_CARTESIAN.to(l0.device)
+    m = _IRREP_ON.get(l0.device)
+    if m is None:
+        m = _IRREP_ON[l0.device] = IRREP_TO_CARTESIAN.to(l0.device)
     return (l0[:, None] * m[0] + l2 @ m[4:]).view(-1, 3, 3)
 
 
@@ -128,8 +131,9 @@ def direct_stress(stress_head: EquivariantHead, node_feat: Tensor, bg: dict) -> 
     comp = stress_head(node_feat, direction)  # [N, 9]
     n_graphs = len(bg["atoms_per_graph"])
     rowptr = bg.get("atom_rowptr")  # atoms of a structure are contiguous
-    if rowptr is None:  # one structure
-        rowptr = torch.tensor([0, comp.shape[0]], dtype=torch.int32, device=comp.device)
+    if rowptr is None:  # one structure: [0, N] made on the device (no host copy, capturable)
+        apg = bg["atoms_per_graph32"]
+        rowptr = torch.cat([apg.new_zeros(1), apg])
     sums = ops.seg_sum_narrow_raw(comp, rowptr, n_graphs)
     mean = sums / bg["atoms_per_graph32"].to(sums.dtype)[:, None]
     stress = stress_from_irreps(mean[:, 0], mean[:, 4:9])

@@ -92,3 +92,32 @@ def test_changed_index_arrays_are_refused():
     g.line_graph = g.line_graph.clone()
     with pytest.raises(RuntimeError, match="index arrays changed"):
         cap.replay()
+
+
+@pytest.mark.parametrize("over", [dict(distance_expansion="Gaussian", three_body_expansion="fourier",
+                                       is_conservation=False),
+                                  dict(graph_conv_mlp="MLP", norm_type="layer", max_n=3, max_l=3)],
+                         ids=["gauss_fourier_direct", "mlp_ln_sh33"])
+def test_generic_option_paths_replay(golden, over):
+    """Non-default constructor options (torch layers on the device between the library's
+    kernels) captured and replayed: every replay, with eager evaluations and syncs between
+    the replays, equals the eager evaluation to fp32 rounding (the generic paths' torch
+    scatters add in no fixed order), for one structure and for a batch."""
+    from matris_amd.config import DEFAULT_CONFIG
+    from matris_amd.model import MatRIS
+    zc, zs = golden("c1_cu4.npz"), golden("cells_small.npz")
+    torch.manual_seed(0)
+    model = MatRIS(**dict(DEFAULT_CONFIG, num_layers=2, **over)).to("cuda").eval()
+    import sys, os
+    sys.path.insert(0, os.path.dirname(__file__))
+    from test_gpu_model import _graph_from_arrays
+    for graphs in ([_graph_from_arrays(zc, "g_")], [_graph_from_arrays(zs, f"g{i}_") for i in range(3)]):
+        cap = model.capture(graphs, task="efsm")
+        eager = _np(model(graphs, task="efsm"))
+        for r in range(3):
+            rep = _np(cap.replay())
+            for k in "efsm":
+                scale = max(np.max(np.abs(eager[k])), 1e-30)
+                assert np.max(np.abs(rep[k] - eager[k])) <= 1e-6 * scale + 1e-9, (r, k)
+            torch.cuda.synchronize()
+            model(graphs, task="efsm")
