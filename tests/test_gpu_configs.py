@@ -6,7 +6,9 @@ interaction_block.py:113-134) forward and input gradients, and the angle -> bond
 sums, against an fp64 torch restatement of the reference ops run on the device
 (scatter_reduce amax, exp, index_add_ in float64), on the bench's inputs (N(0,1), seed 1,
 in the order alpha_s, alpha_t, e').  Bar: 1e-5 of the largest magnitude (the fp32
-kernels' rounding; the fp64 reference is exact to ~1e-15).
+kernels' rounding; the fp64 reference is exact to ~1e-15).  The whole C2 efsm evaluation
+too, by invariants (forces summing to zero, symmetric stress, rotation equivariance with
+the index arrays held) and the default arithmetic against plain fp32 MFMA products.
 
 C5 (32,000-atom a-SiO2, seed 4; A ~ 9.0 M): one efs evaluation with the default memory
 mode (the leading blocks checkpointed, the trailing ones keeping their activations),
@@ -135,3 +137,53 @@ def test_c5_efs_32k_auto_split_invariants_and_arithmetic():
     s_rel = np.abs(auto["s"] - ref["s"]).max() / np.abs(ref["s"]).max()
     print(f"C5 f16x3 vs fp32 MFMA: e_rel={e_rel:.2e} f_abs={f_abs:.2e} s_rel={s_rel:.2e}", flush=True)
     assert e_rel <= 1e-5 and f_abs <= 1e-4 and s_rel <= 1e-4
+
+
+def test_c2_efsm_full_size_invariants_and_arithmetic(c2_graph):
+    """The whole efsm evaluation at C2's full size (4,096 atoms, 1.88 M angles), checked by
+    what holds at any size: forces summing to zero, symmetric stress, the default f16x3
+    arithmetic against plain fp32 MFMA products within the north-star tolerances, and
+    rotation equivariance (the lattice rotated with the fractional coordinates and every
+    index array unchanged: e the same, forces and stress rotated)."""
+    from matris_amd.config import MATRIS_10M
+    from matris_amd.graph import RadiusGraph
+    from matris_amd.model import MatRIS, ops
+    torch.manual_seed(0)
+    model = MatRIS(**MATRIS_10M).to(DEV).eval()
+    g = c2_graph
+    out = model([g], task="efsm")
+    e = out["e"].detach().double().cpu().numpy()
+    f = out["f"][0].detach().double().cpu().numpy()
+    s = out["s"][0].detach().double().cpu().numpy()
+    m = out["m"][0].detach().double().cpu().numpy()
+    for k, v in (("e", e), ("f", f), ("s", s), ("m", m)):
+        assert np.all(np.isfinite(v)), k
+    assert np.abs(f.sum(0)).max() <= 1e-5 * np.abs(f).sum(0).max()
+    assert np.abs(s - s.T).max() <= 1e-6 * np.abs(s).max()
+
+    with ops.mma_precision("fp32"):
+        ref = _efs(model, g)
+    e_rel = abs(e[0] - ref["e"][0]) / abs(ref["e"][0])
+    f_abs = np.abs(f - ref["f"]).max()
+    s_rel = np.abs(s - ref["s"]).max() / np.abs(ref["s"]).max()
+    print(f"C2 f16x3 vs fp32 MFMA: e_rel={e_rel:.2e} f_abs={f_abs:.2e} s_rel={s_rel:.2e}", flush=True)
+    assert e_rel <= 1e-5 and f_abs <= 1e-4 and s_rel <= 1e-4
+
+    th, ph = 0.6, 0.35
+    rz = np.array([[np.cos(th), -np.sin(th), 0], [np.sin(th), np.cos(th), 0], [0, 0, 1]])
+    rx = np.array([[1, 0, 0], [0, np.cos(ph), -np.sin(ph)], [0, np.sin(ph), np.cos(ph)]])
+    R = rz @ rx
+    lat = g.lattice.detach().double().cpu().numpy()
+    g_rot = RadiusGraph(graph_id=None, mp_id=None, composition=None, atomic_number=g.atomic_number,
+                        atom_frac_coord=g.atom_frac_coord,
+                        lattice=torch.tensor(lat @ R.T, dtype=torch.float32, device=DEV),
+                        neighbor_image=g.neighbor_image, atom_graph=g.atom_graph,
+                        atom_graph_cutoff=g.atom_graph_cutoff, line_graph=g.line_graph,
+                        line_graph_cutoff=g.line_graph_cutoff, directed2undirected=g.directed2undirected,
+                        undirected2directed=g.undirected2directed)
+    rot = _efs(model, g_rot)
+    e_rot = abs(rot["e"][0] - e[0]) / abs(e[0])
+    f_rot = np.abs(rot["f"] - f @ R.T).max()
+    s_rot = np.abs(rot["s"] - R @ s @ R.T).max() / np.abs(s).max()
+    print(f"C2 rotated: e_rel={e_rot:.2e} f_abs={f_rot:.2e} s_rel={s_rot:.2e}", flush=True)
+    assert e_rot <= 1e-5 and f_rot <= 1e-4 and s_rot <= 1e-4
