@@ -51,10 +51,15 @@ def _f32(v: float) -> float:
     return float(torch.tensor(v, dtype=torch.float32))
 
 
+# the tables as the float32 values the products use
+_ROOTS32 = tuple(tuple(_f32(v) for v in r) for r in SBF_ROOTS)
+_COEFS32 = tuple(tuple(tuple(_f32(v) for v in t) for t in c) for c in SBF_COEFS)
+
+
 def radial_sbf(n: int, j: int, x: Tensor) -> Tensor:
     """The order-n spherical Bessel radial function at its j-th root, at x = d / cutoff."""
-    z = _f32(SBF_ROOTS[n][j])
-    c = [_f32(t[j]) for t in SBF_COEFS[n]]
+    z = _ROOTS32[n][j]
+    c = [t[j] for t in _COEFS32[n]]
     s, co = torch.sin(z * x), torch.cos(z * x)
     if n == 0:
         return s / x

@@ -86,3 +86,27 @@ def test_direct_head_change_of_basis():
     y2 = sphere_harmonics_l2(r)[:, 4:]
     quad = torch.einsum("ni,kij,nj->nk", r, m[4:].view(5, 3, 3), r)
     assert torch.allclose(quad * math.sqrt(3.0 / 2.0), y2, atol=1e-6)
+
+
+def test_generic_bases_match_the_oracle_on_the_cpu():
+    """The torch forms of the non-default bases (basis_generic) against the oracle's
+    restatements of the reference, on the same inputs: SH bases of every size up to 4 x 4,
+    the Gaussian and Fourier expansions and the Bessel basis without envelope."""
+    from matris_amd.model import basis_generic as B
+    from oracle import model_ref as R
+    gen = torch.Generator().manual_seed(0)
+    d = 0.9 + 0.2 * torch.rand(200, generator=gen)
+    ang = 3.1 * torch.rand(200, generator=gen)
+    r = 0.7 + 5.0 * torch.rand(200, generator=gen)
+    for mn in range(1, 5):
+        for ml in range(1, 5):
+            o = R.SphericalExpansion(mn, ml, 6)
+            ref = o(d, ang)
+            assert torch.allclose(B.spherical_basis(d, ang, mn, ml, 6, o.factor), ref, rtol=1e-6,
+                                  atol=1e-6 * float(ref.abs().max())), (mn, ml)
+    assert torch.allclose(B.GaussianExpansion(0.0, 6.0, 7, 2.0)(r), R.GaussianExpansion(0.0, 6.0, 7, 2.0)(r),
+                          rtol=1e-6, atol=1e-7)
+    assert torch.allclose(B.FourierExpansion(3)(ang), R.FourierExpansion(3)(ang), rtol=1e-6, atol=1e-7)
+    ob = R.BesselExpansion(7, 6.0, None)
+    assert torch.allclose(B.bessel_plain(r, ob.frequencies, ob.inv_cutoff, ob.norm_const), ob(r), rtol=1e-6,
+                          atol=1e-7)
