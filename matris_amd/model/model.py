@@ -12,10 +12,17 @@ kernels of libmatris_hip.so:
 
 The two line-graph layers of each block (attention, refinement) run as single autograd
 nodes with an explicit backward (fused.py) so their residual updates and gradient sums
-stay inside the kernels.  The small embedding / envelope / head layers are library
-GEMMs (hipBLASLt through torch) and torch elementwise ops on the device.
-Forces and stress come from torch.autograd.grad exactly as in the reference
-(readout.py:202-217); every custom op supplies its own input-gradient kernel.
+stay inside the kernels; the edge and three-body embeddings, the learnable envelopes
+and the readout heads have kernels of their own as well (matris_edge_embed_*,
+matris_tb_embed_*, matris_env_*, matris_readout_*).  Forces and stress come from
+torch.autograd.grad exactly as in the reference (readout.py:202-217); every custom op
+supplies its own input-gradient kernel.
+
+Constructor options outside the MatRIS-10M form (LayerNorm / BatchNorm GatedMLPs,
+graph_conv_mlp="MLP", fp16 MLPs, Gaussian / Fourier / smaller SH bases, no envelope,
+more than 8 radial functions, the direct force/stress head) build the same module tree
+and run each layer's generic path: the library's gathers and segment kernels with the
+option's own pieces as torch layers on the device (basis_generic.py, direct_head.py).
 
 Reference: matris/model/model.py, interaction_block.py, feature_embed.py, functions.py,
 readout.py, basis_function.py.
