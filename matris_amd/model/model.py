@@ -150,10 +150,14 @@ class GatedMLP(nn.Module):
         self._pack = ops.GmlpPack()
 
     def _fusable(self) -> bool:
+        """The form matris_gmlp_fwd / _bwd compute: RMSNorm, one 128-wide hidden layer with
+        biases, SiLU as the hidden and the core activation (activation_type="silu"), fp32."""
         return (isinstance(self.core_norm, nn.RMSNorm) and len(self.mlp_core.layers) == 4
                 and self.mlp_core.layers[0].bias is not None and self.mlp_core.layers[0].out_features == 128
                 and self.mlp_core.layers[3].out_features == 128 and not self.use_fp16
-                and not self.mlp_core.use_fp16 and not self.mlp_gate.use_fp16)
+                and not self.mlp_core.use_fp16 and not self.mlp_gate.use_fp16
+                and isinstance(self.activation_func, FusedSiLU) and isinstance(self.mlp_core.layers[1], FusedSiLU)
+                and isinstance(self.mlp_gate.layers[1], FusedSiLU))
 
     def forward(self, x):
         core = self.activation_func(self.core_norm(self.mlp_core(x)))

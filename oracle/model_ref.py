@@ -17,7 +17,7 @@ Pins (see tests/test_oracle_model.py):
     of three batched triclinic cells, from the reference modules (tests/golden/configs.npz);
   * the other constructor options (Gaussian and Fourier bases, smaller SH bases, no
     envelope, 9 radial functions, fixed bases, extensive energy, the direct force/stress
-    head) in the same form (tests/golden/options.npz);
+    head, GELU and ReLU activations) in the same form (tests/golden/options.npz);
   * parameter counts 6,286,736 (defaults) / 10,379,664 (num_layers=10);
   * sum of forces = 0, stress symmetry, rotation equivariance, finite-difference
     forces and stress in fp64.
@@ -50,6 +50,13 @@ class _Sigmoid(nn.Module):
 
     def forward(self, x):
         return torch.sigmoid(x)
+
+
+def _act(name: str) -> nn.Module:
+    """functions.py:38-55."""
+    table = {"relu": nn.ReLU, "silu": _SiLU, "gelu": nn.GELU, "softplus": nn.Softplus, "sigmoid": _Sigmoid,
+             "tanh": nn.Tanh}
+    return table[name.lower()]()
 
 
 def _norm(name: str, dim: int) -> nn.Module:
@@ -112,7 +119,7 @@ class MLP(nn.Module):
     def __init__(self, input_dim=128, hidden_dim=(128, 128), output_dim=128,
                  dropout=0.0, activation="silu", bias=True):
         super().__init__()
-        act = _SiLU()
+        act = _act(activation)
         layers: list[nn.Module] = []
         if hidden_dim in (None, 0):
             layers += [nn.Dropout(dropout), nn.Linear(input_dim, output_dim, bias=bias)]
@@ -138,7 +145,7 @@ class GatedMLP(nn.Module):
     def __init__(self, input_dim=128, hidden_dim=(128, 128), output_dim=128, dropout=0.0,
                  activation="silu", norm_type="layer", bias=True):
         super().__init__()
-        self.activation_func = _SiLU()
+        self.activation_func = _act(activation)
         self.activation_gate = _Sigmoid()
         self.gate_norm = _norm(norm_type, output_dim)
         self.core_norm = _norm(norm_type, output_dim)
@@ -386,14 +393,15 @@ class ThreebodyEmbedding(nn.Module):
 # --------------------------------------------------------------------------------------
 # interaction block (matris/model/interaction_block.py)
 # --------------------------------------------------------------------------------------
-def _update(mlp_type, input_dim, hidden_dim, output_dim, norm_type, bias):
+def _update(mlp_type, input_dim, hidden_dim, output_dim, norm_type, bias, activation="silu"):
     """The nonlinear update of an attention / refinement layer: a GatedMLP (its MLPs keep
     their biases), or, for mlp_type "MLP", MLP(bias=use_bias) followed by the norm
     (interaction_block.py:39-74, 172-197)."""
     if mlp_type.lower() == "gatemlp":
-        return GatedMLP(input_dim, hidden_dim, output_dim, norm_type=norm_type)
+        return GatedMLP(input_dim, hidden_dim, output_dim, activation=activation, norm_type=norm_type)
     if mlp_type.lower() == "mlp":
-        return nn.Sequential(MLP(input_dim, hidden_dim, output_dim, bias=bias), _norm(norm_type, output_dim))
+        return nn.Sequential(MLP(input_dim, hidden_dim, output_dim, activation=activation, bias=bias),
+                             _norm(norm_type, output_dim))
     raise NotImplementedError(mlp_type)
 
 
@@ -401,14 +409,14 @@ class GraphAttentionLayer(nn.Module):
     """interaction_block.py:17-143."""
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, norm_type="layer",
-                 mlp_type="GateMLP", use_bias=False):
+                 mlp_type="GateMLP", use_bias=False, activation="silu"):
         super().__init__()
         self.source_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
         self.target_weight_linear = nn.Linear(edge_feat_dim, edge_feat_dim, bias=False)
         self.node_nonlinear_update = _update(mlp_type, edge_feat_dim * 2 + node_feat_dim, hidden_dim, node_feat_dim,
-                                             norm_type, use_bias)
+                                             norm_type, use_bias, activation)
         self.edge_nonlinear_update = _update(mlp_type, node_feat_dim * 2 + edge_feat_dim, hidden_dim, edge_feat_dim,
-                                             norm_type, use_bias)
+                                             norm_type, use_bias, activation)
         self.node_res_weight = nn.Parameter(torch.ones(1, node_feat_dim))
         self.edge_res_weight = nn.Parameter(torch.ones(1, edge_feat_dim))
 
@@ -434,7 +442,7 @@ class Refinement(nn.Module):
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, hidden_dim=128, num_basis=7,
                  norm_type="layer", graph_type="atom graph", atom_feat_dim=128,
-                 use_smoothed_for_delta_edge=False, use_bias=False, mlp_type="GateMLP"):
+                 use_smoothed_for_delta_edge=False, use_bias=False, mlp_type="GateMLP", activation="silu"):
         super().__init__()
         self.graph_type = graph_type
         self.use_smoothed_for_delta_edge = use_smoothed_for_delta_edge
@@ -442,7 +450,8 @@ class Refinement(nn.Module):
             input_dim = 2 * node_feat_dim + edge_feat_dim
         else:
             input_dim = atom_feat_dim + 2 * node_feat_dim + edge_feat_dim
-        self.edge_nonlinear_update = _update(mlp_type, input_dim, hidden_dim, edge_feat_dim, norm_type, use_bias)
+        self.edge_nonlinear_update = _update(mlp_type, input_dim, hidden_dim, edge_feat_dim, norm_type, use_bias,
+                                             activation)
         self.node_FFN = MLP(edge_feat_dim, node_feat_dim, node_feat_dim, bias=use_bias)
         self.edge_FFN = MLP(edge_feat_dim, edge_feat_dim, edge_feat_dim, bias=use_bias)
         self.learnable_envelope = nn.Linear(num_basis, edge_feat_dim, bias=False)
@@ -477,18 +486,18 @@ class InteractionBlock(nn.Module):
 
     def __init__(self, node_feat_dim=128, edge_feat_dim=128, three_body_feat_dim=128, num_radial=7,
                  num_angular=7, use_bias=False, use_smoothed_for_delta_edge=False, norm_type="layer",
-                 mlp_type="GateMLP"):
+                 mlp_type="GateMLP", activation="silu"):
         super().__init__()
         self.attn_block_atom_graph = GraphAttentionLayer(node_feat_dim, edge_feat_dim, node_feat_dim, norm_type,
-                                                         mlp_type, use_bias)
+                                                         mlp_type, use_bias, activation)
         self.attn_block_line_graph = GraphAttentionLayer(edge_feat_dim, three_body_feat_dim, edge_feat_dim, norm_type,
-                                                         mlp_type, use_bias)
+                                                         mlp_type, use_bias, activation)
         self.refine_block_atom_graph = Refinement(node_feat_dim, edge_feat_dim, node_feat_dim, num_radial, norm_type,
                                                   "atom graph", use_smoothed_for_delta_edge=use_smoothed_for_delta_edge,
-                                                  use_bias=use_bias, mlp_type=mlp_type)
+                                                  use_bias=use_bias, mlp_type=mlp_type, activation=activation)
         self.refine_block_line_graph = Refinement(edge_feat_dim, three_body_feat_dim, edge_feat_dim, num_angular,
                                                   norm_type, "line graph", atom_feat_dim=node_feat_dim,
-                                                  use_bias=use_bias, mlp_type=mlp_type)
+                                                  use_bias=use_bias, mlp_type=mlp_type, activation=activation)
 
     def forward(self, g, node_feat, edge_feat, tb_feat, smooth_weight):
         attn_edge, attn_tb = edge_feat, tb_feat
@@ -619,12 +628,12 @@ def sphere_l2(v):
 class GatedEquivariantBlock(nn.Module):
     """readout.py:255-292."""
 
-    def __init__(self, hidden_channels, out_channels):
+    def __init__(self, hidden_channels, out_channels, activation="silu"):
         super().__init__()
         self.out_channels = out_channels
         self.vec1_proj = nn.Linear(hidden_channels, hidden_channels, bias=False)
         self.vec2_proj = nn.Linear(hidden_channels, out_channels, bias=False)
-        self.act = _SiLU()
+        self.act = _act(activation)
         self.update_net = nn.Sequential(nn.Linear(hidden_channels * 2, hidden_channels), self.act,
                                         nn.Linear(hidden_channels, out_channels * 2))
 
@@ -638,12 +647,12 @@ class GatedEquivariantBlock(nn.Module):
 class EquivariantHead(nn.Module):
     """readout.py:295-334 (lmax = 2)."""
 
-    def __init__(self, feas_dim=64):
+    def __init__(self, feas_dim=64, activation="silu"):
         super().__init__()
         self.feas_wise_linear = nn.Linear(feas_dim, feas_dim, bias=False)
         self.basis_wise_linear = nn.Linear(1, feas_dim, bias=False)
-        self.equivariant_block = nn.ModuleList([GatedEquivariantBlock(feas_dim, feas_dim // 2),
-                                                GatedEquivariantBlock(feas_dim // 2, 1)])
+        self.equivariant_block = nn.ModuleList([GatedEquivariantBlock(feas_dim, feas_dim // 2, activation),
+                                                GatedEquivariantBlock(feas_dim // 2, 1, activation)])
 
     def forward(self, feas, vec):
         vec_feas = self.basis_wise_linear(sphere_l2(vec).unsqueeze(2))
@@ -656,10 +665,10 @@ class EquivariantHead(nn.Module):
 class DirectHead(nn.Module):
     """readout.py:136-252, is_conservation=False (mlp_type "mlp", as model.py:171-178)."""
 
-    def __init__(self, feat_dim, hidden_dims):
+    def __init__(self, feat_dim, hidden_dims, activation="silu"):
         super().__init__()
-        self.stress_head = EquivariantHead(feat_dim)
-        self.force_head = MLP(feat_dim, hidden_dims, 3)
+        self.stress_head = EquivariantHead(feat_dim, activation)
+        self.force_head = MLP(feat_dim, hidden_dims, 3, activation=activation)
 
     def forward(self, g, node_feat, edge_feat, compute_force, compute_stress):
         pred = {}
@@ -703,17 +712,17 @@ class MatRISRef(nn.Module):
                                                        three_body_feat_dim, three_body_expansion, learnable_basis)
         self.interaction_block = nn.ModuleList([
             InteractionBlock(node_feat_dim, edge_feat_dim, three_body_feat_dim, num_radial, num_angular,
-                             use_bias, use_smoothed_for_delta_edge, norm_type, graph_conv_mlp)
+                             use_bias, use_smoothed_for_delta_edge, norm_type, graph_conv_mlp, activation_type)
             for _ in range(num_layers)])
         self.readout_norm = _norm(norm_type, node_feat_dim)
         hd = [mlp_hidden_dims] if isinstance(mlp_hidden_dims, int) else list(mlp_hidden_dims)
         self.energy_head = nn.Module()
-        self.energy_head.energy_head = MLP(node_feat_dim, hd, 1)
+        self.energy_head.energy_head = MLP(node_feat_dim, hd, 1, activation=activation_type)
         self.energy_head.pooling = GraphPooling(False)
         self.magmom_head = nn.Module()
-        self.magmom_head.magmom_head = MLP(node_feat_dim, [2 * node_feat_dim], 1)
+        self.magmom_head.magmom_head = MLP(node_feat_dim, [2 * node_feat_dim], 1, activation=activation_type)
         if not is_conservation:
-            self.force_stress_head = DirectHead(edge_feat_dim, hd)
+            self.force_stress_head = DirectHead(edge_feat_dim, hd, activation_type)
 
     def forward(self, graphs, task="ef", is_training=False):
         g = process_graphs(graphs, compute_stress="s" in task)

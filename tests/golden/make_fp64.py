@@ -51,7 +51,8 @@ VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
             "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
             "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
             "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
-            "direct": dict(is_conservation=False)}
+            "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
+            "relu": dict(activation_type="relu")}
 
 
 def model64(cfg):

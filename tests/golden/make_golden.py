@@ -39,8 +39,9 @@ Outputs (small .npz / .json files; torch version recorded in meta):
   options.npz         (--only options) the other constructor options at two blocks, seed 0,
                       in the same form: Gaussian distance expansion, Fourier three-body
                       expansion, SH bases of 3 x 3 and 2 x 4, no envelope, 9 radial
-                      functions, fixed (non-learnable) bases, extensive energy, and the
-                      direct force/stress head (is_conservation=False)
+                      functions, fixed (non-learnable) bases, extensive energy, the
+                      direct force/stress head (is_conservation=False), and the GELU and
+                      ReLU activations (activation_type)
 
     python tests/golden/make_golden.py --only c4 degenerate graphfile   (those fixtures only)
 """
@@ -274,7 +275,8 @@ OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict
                    "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
                    "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
                    "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
-                   "direct": dict(is_conservation=False)}
+                   "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
+                   "relu": dict(activation_type="relu")}
 
 
 def write_configs(variants=None, name_out="configs.npz"):

@@ -451,7 +451,8 @@ OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict
                    "sh33": dict(max_n=3, max_l=3), "sh24": dict(max_n=2, max_l=4),
                    "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
                    "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
-                   "direct": dict(is_conservation=False)}
+                   "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
+                   "relu": dict(activation_type="relu")}
 VARIANTS = [("configs.npz", n, o) for n, o in CONFIG_VARIANTS.items()] + \
            [("options.npz", n, o) for n, o in OPTION_VARIANTS.items()]
 

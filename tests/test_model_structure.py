@@ -110,3 +110,18 @@ def test_generic_bases_match_the_oracle_on_the_cpu():
     ob = R.BesselExpansion(7, 6.0, None)
     assert torch.allclose(B.bessel_plain(r, ob.frequencies, ob.inv_cutoff, ob.norm_const), ob(r), rtol=1e-6,
                           atol=1e-7)
+
+
+@pytest.mark.parametrize("act", ["relu", "gelu", "tanh", "sigmoid", "softplus"])
+def test_other_activations_take_the_generic_gated_mlp_path(act):
+    """The fused GatedMLP kernels compute SiLU: a GatedMLP built with another
+    activation_type runs its module forward, the readout likewise; the Refinement FFNs
+    keep SiLU whatever activation_type is (interaction_block.py:198-210 passes none), so
+    they stay fused."""
+    model = MatRIS(**dict(DEFAULT_CONFIG, num_layers=1, activation_type=act))
+    blk = model.interaction_block[0]
+    assert not blk.attn_block_atom_graph.edge_nonlinear_update._fusable()
+    assert not fused.line_attention_fusable(blk.attn_block_line_graph)
+    assert not fused.line_refinement_fusable(blk.refine_block_line_graph)
+    assert not model._readout_fusable()
+    assert fused._ffn_fusable(blk.refine_block_line_graph.node_FFN)
