@@ -170,7 +170,8 @@ class GatedMLP(nn.Module):
         one 128-wide hidden layer, biases); any other form (LayerNorm or BatchNorm, other
         widths, the fp16 autocast MLPs) runs this module's own forward on the gathered
         concatenation, on the device."""
-        if self._fusable():
+        if (self._fusable() and all(t.dim() == 2 and t.shape[1] == 128 for t, _ in sources)
+                and self.mlp_core.layers[0].in_features == 128 * len(sources)):
             return ops.gated_mlp(self, self._pack, sources)
         return self(gathered_concat(sources))
 

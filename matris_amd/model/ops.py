@@ -559,12 +559,20 @@ class _Gather(torch.autograd.Function):
 
 
 def seg_sum(x, grp: Grouping, scale: float = 1.0):
-    """out[s] = scale * sum of x rows with key s (aggregate(), functions.py:129-160)."""
+    """out[s] = scale * sum of x rows with key s (aggregate(), functions.py:129-160).
+    Rows of another width than 128 (feature widths other than MatRIS-10M's) are summed by
+    torch on the device."""
+    if x.dim() != 2 or x.shape[1] != D:
+        out = torch.zeros(grp.n_seg, *x.shape[1:], dtype=x.dtype, device=x.device)
+        return out.index_add(0, grp.key.long(), x) * scale
     return _SegSum.apply(x, grp, scale)
 
 
 def gather(src, grp: Grouping):
-    """src[grp.key] (torch.index_select), with a deterministic CSR backward."""
+    """src[grp.key] (torch.index_select), with a deterministic CSR backward (rows of
+    another width than 128: torch.index_select itself)."""
+    if src.dim() != 2 or src.shape[1] != D:
+        return torch.index_select(src, 0, grp.key.long())
     return _Gather.apply(src, grp)
 
 
@@ -680,9 +688,27 @@ class _SegAttn(torch.autograd.Function):
         return g_at, g_as, g_e, None, None, None
 
 
+def _dimwise_softmax_torch(a, grp: Grouping):
+    """Dimwise_softmax (functions.py:97-127) by torch on the device: per column, exp of the
+    row minus its segment's maximum over the segment's sum."""
+    key = grp.key.long()
+    mx = torch.full((grp.n_seg, a.shape[1]), float("-inf"), dtype=a.dtype, device=a.device).scatter_reduce(
+        0, key[:, None].expand_as(a), a, "amax", include_self=False)
+    ex = torch.exp(a - mx[key])
+    den = torch.zeros(grp.n_seg, a.shape[1], dtype=a.dtype, device=a.device).index_add(0, key, ex)
+    return ex / den[key]
+
+
 def seg_attention(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: Grouping | None = None):
     """(y_t, y_s): Dimwise_softmax of alpha by target / source segment times e, summed
-    per segment (interaction_block.py:113-134)."""
+    per segment (interaction_block.py:113-134).  Features of another width than 128: the
+    same by torch on the device."""
+    if e.dim() != 2 or e.shape[1] != D or alpha_t.shape[1] != D:
+        if alpha_grp is not None:
+            alpha_t, alpha_s = gather(alpha_t, alpha_grp), gather(alpha_s, alpha_grp)
+        y_t = seg_sum(_dimwise_softmax_torch(alpha_t, tgt) * e, tgt)
+        y_s = seg_sum(_dimwise_softmax_torch(alpha_s, src) * e, src)
+        return y_t, y_s
     return _SegAttn.apply(alpha_t, alpha_s, e, tgt, src, alpha_grp)
 
 

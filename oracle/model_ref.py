@@ -17,7 +17,8 @@ Pins (see tests/test_oracle_model.py):
     of three batched triclinic cells, from the reference modules (tests/golden/configs.npz);
   * the other constructor options (Gaussian and Fourier bases, smaller SH bases, no
     envelope, 9 radial functions, fixed bases, extensive energy, the direct force/stress
-    head, GELU and ReLU activations) in the same form (tests/golden/options.npz);
+    head, GELU and ReLU activations, feature widths of 64 and of 128 / 96 / 64) in the
+    same form (tests/golden/options.npz);
   * parameter counts 6,286,736 (defaults) / 10,379,664 (num_layers=10);
   * sum of forces = 0, stress symmetry, rotation equivariance, finite-difference
     forces and stress in fp64.

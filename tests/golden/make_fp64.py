@@ -52,7 +52,9 @@ VARIANTS = {"ln": dict(norm_type="layer"), "bn": dict(norm_type="batch"),
             "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
             "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
             "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
-            "relu": dict(activation_type="relu")}
+            "relu": dict(activation_type="relu"),
+            "dim64": dict(node_feat_dim=64, edge_feat_dim=64, three_body_feat_dim=64, mlp_hidden_dims=(64, 64)),
+            "mixed": dict(node_feat_dim=128, edge_feat_dim=96, three_body_feat_dim=64)}
 
 
 def model64(cfg):

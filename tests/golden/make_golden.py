@@ -40,8 +40,9 @@ Outputs (small .npz / .json files; torch version recorded in meta):
                       in the same form: Gaussian distance expansion, Fourier three-body
                       expansion, SH bases of 3 x 3 and 2 x 4, no envelope, 9 radial
                       functions, fixed (non-learnable) bases, extensive energy, the
-                      direct force/stress head (is_conservation=False), and the GELU and
-                      ReLU activations (activation_type)
+                      direct force/stress head (is_conservation=False), the GELU and
+                      ReLU activations (activation_type), and feature widths of 64 and
+                      of 128 / 96 / 64 (atoms / bonds / angles)
 
     python tests/golden/make_golden.py --only c4 degenerate graphfile   (those fixtures only)
 """
@@ -276,7 +277,9 @@ OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict
                    "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
                    "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
                    "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
-                   "relu": dict(activation_type="relu")}
+                   "relu": dict(activation_type="relu"),
+                   "dim64": dict(node_feat_dim=64, edge_feat_dim=64, three_body_feat_dim=64, mlp_hidden_dims=(64, 64)),
+                   "mixed": dict(node_feat_dim=128, edge_feat_dim=96, three_body_feat_dim=64)}
 
 
 def write_configs(variants=None, name_out="configs.npz"):

@@ -452,7 +452,9 @@ OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict
                    "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
                    "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
                    "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
-                   "relu": dict(activation_type="relu")}
+                   "relu": dict(activation_type="relu"),
+                   "dim64": dict(node_feat_dim=64, edge_feat_dim=64, three_body_feat_dim=64, mlp_hidden_dims=(64, 64)),
+                   "mixed": dict(node_feat_dim=128, edge_feat_dim=96, three_body_feat_dim=64)}
 VARIANTS = [("configs.npz", n, o) for n, o in CONFIG_VARIANTS.items()] + \
            [("options.npz", n, o) for n, o in OPTION_VARIANTS.items()]
 
@@ -492,5 +494,10 @@ def test_fp16_update_runs_under_autocast():
     err = (out16 - out32).abs().max().item() / out32.abs().max().item()
     print(f"fp16 autocast GatedMLP vs fused fp32: rel {err:.2e}", flush=True)
     assert 0 < err < 1e-2  # fp16 products (11-bit mantissa), not the fp32-grade fused kernel
+    # sources the kernel cannot take (one 384-wide block): fused() runs the module forward,
+    # and the op itself refuses them on the host
+    from matris_amd.model import ops
+    x384 = torch.cat([t for t, _ in xs], dim=1)
+    assert torch.equal(g32.fused([(x384, None)]), g32(x384))
     with pytest.raises(ValueError, match="each source must be"):
-        g32.fused([(torch.randn(1000, 384, device="cuda"), None)])  # one 384-wide source
+        ops.gated_mlp(g32, g32._pack, [(x384, None)])

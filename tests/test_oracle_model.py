@@ -96,7 +96,9 @@ OPTION_VARIANTS = {"gauss": dict(distance_expansion="Gaussian"), "fourier": dict
                    "noenv": dict(envelope_exponent=None), "nr9": dict(num_radial=9, num_angular=9),
                    "fixed": dict(learnable_basis=False), "extensive": dict(is_intensive=False),
                    "direct": dict(is_conservation=False), "gelu": dict(activation_type="gelu"),
-                   "relu": dict(activation_type="relu")}
+                   "relu": dict(activation_type="relu"),
+                   "dim64": dict(node_feat_dim=64, edge_feat_dim=64, three_body_feat_dim=64, mlp_hidden_dims=(64, 64)),
+                   "mixed": dict(node_feat_dim=128, edge_feat_dim=96, three_body_feat_dim=64)}
 VARIANTS = [("configs.npz", n, o) for n, o in CONFIG_VARIANTS.items()] + \
            [("options.npz", n, o) for n, o in OPTION_VARIANTS.items()]
 
@@ -165,7 +167,7 @@ def test_option_fixtures_relations(golden):
         assert np.abs(o["direct"]["s"] - s).max() > 1e-3 * np.abs(s).max()
         if tag == "cells":  # C1's forces vanish by symmetry under every head
             assert np.abs(o["direct"]["f"] - f).max() > 1e-3
-        for n in ("gauss", "fourier", "sh33", "sh24", "noenv", "nr9", "gelu", "relu"):
+        for n in ("gauss", "fourier", "sh33", "sh24", "noenv", "nr9", "gelu", "relu", "dim64", "mixed"):
             assert np.min(np.abs(o[n]["e"] - e)) > 1e-4 * np.max(np.abs(e)), (n, tag)
 
 
