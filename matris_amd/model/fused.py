@@ -152,7 +152,8 @@ def _ffn_fusable(mlp) -> bool:
     L = mlp.layers
     return (len(L) == 4 and L[0].bias is None and L[3].bias is None and tuple(L[0].weight.shape) == (D, D)
             and tuple(L[3].weight.shape) == (D, D) and type(L[1]).__name__ == "FusedSiLU"
-            and not getattr(mlp, "use_fp16", False))
+            and not getattr(mlp, "use_fp16", False)
+            and all(l.p == 0.0 or not l.training for l in L if isinstance(l, torch.nn.Dropout)))
 
 
 def _gmlp_fusable(m) -> bool:

@@ -133,6 +133,12 @@ class MLP(nn.Module):
         return self.layers(x)
 
 
+def dropout_off(mlp) -> bool:
+    """Every Dropout of the MLP is the identity (p = 0, or eval mode): the fused kernels
+    apply none."""
+    return all(l.p == 0.0 or not l.training for l in mlp.layers if isinstance(l, nn.Dropout))
+
+
 class GatedMLP(nn.Module):
     """functions.py:245-311.  `fused(sources)` runs the whole block -- gathers, concat,
     two MLPs, RMSNorm, SiLU, sigmoid, product -- in matris_gmlp_fwd."""
@@ -157,7 +163,8 @@ class GatedMLP(nn.Module):
                 and self.mlp_core.layers[3].out_features == 128 and not self.use_fp16
                 and not self.mlp_core.use_fp16 and not self.mlp_gate.use_fp16
                 and isinstance(self.activation_func, FusedSiLU) and isinstance(self.mlp_core.layers[1], FusedSiLU)
-                and isinstance(self.mlp_gate.layers[1], FusedSiLU))
+                and isinstance(self.mlp_gate.layers[1], FusedSiLU) and dropout_off(self.mlp_core)
+                and dropout_off(self.mlp_gate))
 
     def forward(self, x):
         core = self.activation_func(self.core_norm(self.mlp_core(x)))
@@ -505,7 +512,8 @@ class Refinement(nn.Module):
         """MLP(hidden=int, bias=False) as one fused MFMA kernel (functions.py:198-205)."""
         L = mlp.layers
         if (len(L) == 4 and L[0].bias is None and L[3].bias is None and L[0].weight.shape == (128, 128)
-                and L[3].weight.shape == (128, 128) and isinstance(L[1], FusedSiLU) and not mlp.use_fp16):
+                and L[3].weight.shape == (128, 128) and isinstance(L[1], FusedSiLU) and not mlp.use_fp16
+                and dropout_off(mlp)):
             return ops.ffn(pack.get(L[0].weight, L[3].weight), x)
         return mlp(x)
 

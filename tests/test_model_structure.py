@@ -125,3 +125,26 @@ def test_other_activations_take_the_generic_gated_mlp_path(act):
     assert not fused.line_refinement_fusable(blk.refine_block_line_graph)
     assert not model._readout_fusable()
     assert fused._ffn_fusable(blk.refine_block_line_graph.node_FFN)
+
+
+def test_active_dropout_leaves_the_fused_kernels():
+    """A GatedMLP or FFN with dropout > 0 in training mode runs its module forward (the
+    fused kernels apply no dropout); in eval mode it is fused again.  MatRIS's dropout
+    keyword reaches only the refinement layers' edge updates, as in the reference
+    (interaction_block.py:321-365 passes it to the Refinement layers alone)."""
+    from matris_amd.model.model import MLP, GatedMLP
+    g = GatedMLP(384, 128, 128, dropout=0.1, norm_type="rms").train()
+    f = MLP(128, 128, 128, dropout=0.1, bias=False).train()
+    assert not g._fusable() and not fused._ffn_fusable(f)
+    g.eval(); f.eval()
+    assert g._fusable() and fused._ffn_fusable(f)
+    model = MatRIS(**dict(DEFAULT_CONFIG, num_layers=1, dropout=0.1)).train()
+    active = sorted({n.rsplit(".", 2)[0] for n, l in model.named_modules()
+                     if isinstance(l, torch.nn.Dropout) and l.p > 0})
+    assert active == [f"interaction_block.0.refine_block_{k}_graph.edge_nonlinear_update.{m}"
+                      for k in ("atom", "line") for m in ("mlp_core", "mlp_gate")]
+    blk = model.interaction_block[0]
+    assert not fused.line_refinement_fusable(blk.refine_block_line_graph)
+    assert fused.line_attention_fusable(blk.attn_block_line_graph)
+    model.eval()
+    assert fused.line_refinement_fusable(blk.refine_block_line_graph)
