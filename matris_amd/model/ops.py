@@ -563,6 +563,7 @@ def seg_sum(x, grp: Grouping, scale: float = 1.0):
     Rows of another width than 128 (feature widths other than MatRIS-10M's) are summed by
     torch on the device."""
     if x.dim() != 2 or x.shape[1] != D:
+        _check_dev(x)
         out = torch.zeros(grp.n_seg, *x.shape[1:], dtype=x.dtype, device=x.device)
         return out.index_add(0, grp.key.long(), x) * scale
     return _SegSum.apply(x, grp, scale)
@@ -572,6 +573,7 @@ def gather(src, grp: Grouping):
     """src[grp.key] (torch.index_select), with a deterministic CSR backward (rows of
     another width than 128: torch.index_select itself)."""
     if src.dim() != 2 or src.shape[1] != D:
+        _check_dev(src)
         return torch.index_select(src, 0, grp.key.long())
     return _Gather.apply(src, grp)
 
@@ -704,6 +706,7 @@ def seg_attention(alpha_t, alpha_s, e, tgt: Grouping, src: Grouping, alpha_grp: 
     per segment (interaction_block.py:113-134).  Features of another width than 128: the
     same by torch on the device."""
     if e.dim() != 2 or e.shape[1] != D or alpha_t.shape[1] != D:
+        _check_dev(alpha_t, alpha_s, e)
         if alpha_grp is not None:
             alpha_t, alpha_s = gather(alpha_t, alpha_grp), gather(alpha_s, alpha_grp)
         y_t = seg_sum(_dimwise_softmax_torch(alpha_t, tgt) * e, tgt)

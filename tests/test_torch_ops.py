@@ -71,3 +71,17 @@ def test_cpu_tensors_have_no_kernel():
         torch.ops.matris_hip.seg_sum(x, torch.zeros(3, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), None)
     with pytest.raises(RuntimeError):
         T.fused_silu(x)
+
+
+def test_width_generic_segment_ops_refuse_cpu_tensors():
+    """The torch forms that ops.gather / seg_sum / seg_attention take for rows of another
+    width than 128 run on the device only, like the kernels (no CPU fallback)."""
+    import pytest
+    import torch
+    from matris_amd.model import ops
+    grp = ops.Grouping(torch.zeros(4, dtype=torch.int32), torch.tensor([0, 4], dtype=torch.int32), None, 1)
+    x = torch.zeros(4, 64)
+    for call in (lambda: ops.gather(x, grp), lambda: ops.seg_sum(x, grp),
+                 lambda: ops.seg_attention(x, x, x, grp, grp)):
+        with pytest.raises(RuntimeError, match="ROCm device only"):
+            call()
