@@ -85,6 +85,12 @@ AMU_A2_FS2_EV = 103.642691        # 1 amu * (Angstrom/fs)^2 in eV
 FORCE_TO_ACC = 1.0 / AMU_A2_FS2_EV  # (eV/Angstrom)/amu -> Angstrom/fs^2
 GPA_EV_A3 = 1.0 / 160.21766208    # 1 GPa in eV/A^3
 DEFAULT_BULK_MODULUS_GPA = 2.0    # md.py:207-209
+# The reference's CrystalFeasObserver (base.py:178-198) records results["crystal_fea"] of
+# the calculator, which MatRIS never produces: attaching it (md.py:303-310, relax.py:111-129)
+# fails with a KeyError at the first recorded step.  Here the option is refused up front.
+CRYSTAL_FEAS_UNSUPPORTED = ("crystal feature logging (crystal_feas_logfile / crystal_feas_save_path) is not "
+                            "supported: MatRIS produces no crystal_fea for the observer to record (the reference's "
+                            "observer fails with a KeyError at its first step)")
 
 
 def _detached(v):
@@ -318,6 +324,8 @@ class MolecularDynamics:
                  device: str | None = None, seed: int | None = None, skin: float = 0.0):
         from ..graph.converter import _structure_arrays
         from ..model.model import MatRIS
+        if crystal_feas_logfile:
+            raise NotImplementedError(CRYSTAL_FEAS_UNSUPPORTED)
         self.ensemble, self.thermostat = ensemble.lower(), thermostat
         kind = _kind(ensemble, thermostat)
         if isinstance(model, str):

@@ -175,6 +175,9 @@ class StructOptimizer:
         """Relax `atoms` (ASE Atoms, SimpleAtoms, or a pymatgen Structure when pymatgen is
         installed) until max |f| < fmax or `steps` optimiser steps (relax.py:54-147).
         Returns {"final_structure": relaxed structure, "trajectory": TrajectoryObserver}."""
+        if crystal_feas_save_path:
+            from .md import CRYSTAL_FEAS_UNSUPPORTED
+            raise NotImplementedError(CRYSTAL_FEAS_UNSUPPORTED)
         try:
             import ase.filters as filters  # noqa: F401
             import ase.optimize as ase_optimize

@@ -93,3 +93,15 @@ def test_native_relax_validates_the_cell_filter_name():
         opt.relax(a, ase_filter="StrainFilter", verbose=False)
     with pytest.raises(ValueError, match="Invalid ase_filter"):
         opt.relax(a, ase_filter="NoSuchFilter", verbose=False)
+
+
+def test_crystal_feature_logging_is_refused_with_the_reason():
+    """The reference's CrystalFeasObserver records a crystal_fea the model never produces
+    (its first step raises KeyError): asking for it is refused up front, before a model is
+    touched."""
+    from matris_amd.applications.md import MolecularDynamics
+    from matris_amd.applications.relax import StructOptimizer
+    with pytest.raises(NotImplementedError, match="crystal_fea"):
+        MolecularDynamics(atoms=None, model=None, crystal_feas_logfile="feas.pkl")
+    with pytest.raises(NotImplementedError, match="crystal_fea"):
+        StructOptimizer.relax(object.__new__(StructOptimizer), atoms=None, crystal_feas_save_path="feas.pkl")
