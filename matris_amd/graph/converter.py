@@ -276,7 +276,6 @@ class GraphConverter(nn.Module):
                 "algorithm": self.algorithm}
 
     @classmethod
-    def from_dict(cls, dct) -> "GraphConverter":
-        dct = dict(dct)
-        dct.pop("algorithm", None)
-        return cls(**dct)
+    def from_dict(cls, dict) -> "GraphConverter":  # noqa: A002 (the reference's parameter name)
+        kwargs = {k: v for k, v in dict.items() if k != "algorithm"}
+        return cls(**kwargs)

@@ -29,6 +29,18 @@ class AtomRef(nn.Module):
         for p in self.parameters():
             p.requires_grad = False
 
+    def initialize_from_MPtrj(self) -> None:
+        """reference_energy.py:116-145: the MPtrj table."""
+        self.initialize_from("mptrj")
+
+    def initialize_from_OMat(self) -> None:
+        """reference_energy.py:147-176: the OMat24 table."""
+        self.initialize_from("omat")
+
+    def initialize_from_MPA(self) -> None:
+        """reference_energy.py:178-207: the sAlex + MPtrj table."""
+        self.initialize_from("mpa")
+
     def initialize_from(self, dataset: str) -> None:
         """Load a pre-fitted table: "mptrj" (or "demo"), "omat" or "mpa" (all intensive)."""
         key = dataset.lower()
@@ -50,11 +62,15 @@ class AtomRef(nn.Module):
         feats = torch.stack([self._composition(g.atomic_number) for g in graphs], 0).float()
         return self.fc(feats.to(self.fc.weight.device)).view(-1)
 
-    def fit(self, graphs: Sequence, energies: Sequence[float]) -> None:
-        """Least-squares weights w = pinv(C^T C) C^T e over the given graphs (objects with an
-        `atomic_number` tensor, e.g. RadiusGraph) and their energies."""
-        feats = np.stack([self._composition(torch.as_tensor(g.atomic_number)).float().cpu().numpy()
-                          for g in graphs], 0)
+    def fit(self, structures_or_graphs: Sequence, energies: Sequence[float]) -> None:
+        """Least-squares weights w = pinv(C^T C) C^T e over the given structures or graphs
+        (reference_energy.py:57-101: RadiusGraph objects with an `atomic_number` tensor, or
+        structures with `atomic_numbers`, as pymatgen's Structure) and their energies."""
+        def numbers(x):
+            z = x.atomic_number if hasattr(x, "atomic_number") else x.atomic_numbers
+            return torch.as_tensor(np.asarray(z.cpu() if torch.is_tensor(z) else z, dtype=np.int64))
+
+        feats = np.stack([self._composition(numbers(x)).float().cpu().numpy() for x in structures_or_graphs], 0)
         e = np.asarray(energies, dtype=np.float32)
         w = np.linalg.pinv(feats.T @ feats) @ feats.T @ e
         with torch.no_grad():

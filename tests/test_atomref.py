@@ -65,3 +65,27 @@ def test_model_carries_reference_energy_like_the_reference():
     # without it while their shapes agree
     k = "atom_embedding.embedding.weight"
     assert k in sd0 and sd0[k].shape == sd1[k].shape and not torch.equal(sd0[k], sd1[k])
+
+
+def test_reference_method_names():
+    """The reference's AtomRef methods: initialize_from_MPtrj / _OMat / _MPA load the same
+    tables as initialize_from, and fit takes structures (atomic_numbers, as pymatgen's
+    Structure) as well as graphs, by the reference's keyword."""
+    for meth, key in (("initialize_from_MPtrj", "mptrj"), ("initialize_from_OMat", "omat"),
+                      ("initialize_from_MPA", "mpa")):
+        a, b = AtomRef(None), AtomRef(None)
+        getattr(a, meth)()
+        b.initialize_from(key)
+        assert torch.equal(a.fc.weight, b.fc.weight) and a.fitted
+
+    class _S:  # a structure-like object: a plain sequence of atomic numbers
+        def __init__(self, z):
+            self.atomic_numbers = tuple(int(v) for v in z)
+
+    rng = np.random.default_rng(1)
+    w = rng.normal(size=94).astype(np.float32)
+    zs = [rng.integers(1, 95, size=int(rng.integers(5, 40))) for _ in range(400)]
+    comp = np.stack([np.bincount(z - 1, minlength=94) for z in zs]).astype(np.float64)
+    ref = AtomRef(None, is_intensive=False)
+    ref.fit(structures_or_graphs=[_S(z) for z in zs], energies=comp @ w)
+    np.testing.assert_allclose(ref.fc.weight.view(-1).numpy(), w, rtol=2e-3, atol=2e-3)

@@ -80,3 +80,9 @@ def test_missing_checkpoint_raises(tmp_path):
     from matris_amd.model import MatRIS
     with pytest.raises(FileNotFoundError):
         MatRIS.load(path=str(tmp_path / "absent.pth.tar"), device="cpu")
+
+
+def test_graph_converter_from_dict_takes_the_reference_keyword():
+    from matris_amd.graph.converter import GraphConverter
+    gc = GraphConverter.from_dict(dict={"atom_graph_cutoff": 5.0, "line_graph_cutoff": 3.0, "algorithm": "fast"})
+    assert gc.atom_graph_cutoff == 5.0 and gc.line_graph_cutoff == 3.0
