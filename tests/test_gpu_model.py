@@ -396,7 +396,7 @@ def test_stress_is_the_strain_derivative_of_the_energy_with_the_graph_fixed():
             gg = model.graph_converter(W.Crystal(cr.frac, new, cr.z))
         else:
             gg = RadiusGraph(**{**g.to_dict(), "lattice": torch.as_tensor(new, dtype=torch.float32, device="cuda")})
-        return float(model([gg], task="e")["e"][0]) * n, (len(gg.atom_graph), len(gg.line_graph))
+        return float(model([gg], task="e")["e"][0].detach()) * n, (len(gg.atom_graph), len(gg.line_graph))
 
     h = 1e-3
     for eps, pred in ((np.eye(3) * h, vol * np.trace(s) * h),
