@@ -466,8 +466,8 @@ def main():
     mode_idx, mma_peak, peak_note, dtype = MMA_ROOF[ops.get_mma_precision()]
 
     def gmlp_roof(name, st, n_steps, where):
-        """The GatedMLP family against the MFMA roofline, the bound SURVEY's measurement
-        plan gives the GEMMs (kept fixed): achieved = algorithmic fp32-product FLOPs per
+        """The GatedMLP family against the MFMA roofline, the bound of the dense GEMMs on
+        this path (kept fixed): achieved = algorithmic fp32-product FLOPs per
         launch / mean launch time, against the split-product peak of the arithmetic in use.
         The HBM figure rides along under `hbm`, its bytes the layer's inputs and outputs
         only (the pre-activations the build saves for its backward, p / z and the FFN's,
