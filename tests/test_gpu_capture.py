@@ -96,8 +96,10 @@ def test_changed_index_arrays_are_refused():
 
 @pytest.mark.parametrize("over", [dict(distance_expansion="Gaussian", three_body_expansion="fourier",
                                        is_conservation=False),
-                                  dict(graph_conv_mlp="MLP", norm_type="layer", max_n=3, max_l=3)],
-                         ids=["gauss_fourier_direct", "mlp_ln_sh33"])
+                                  dict(graph_conv_mlp="MLP", norm_type="layer", max_n=3, max_l=3),
+                                  dict(node_feat_dim=64, edge_feat_dim=64, three_body_feat_dim=64,
+                                       mlp_hidden_dims=(64, 64), activation_type="gelu")],
+                         ids=["gauss_fourier_direct", "mlp_ln_sh33", "dim64_gelu"])
 def test_generic_option_paths_replay(golden, over):
     """Non-default constructor options (torch layers on the device between the library's
     kernels) captured and replayed: every replay, with eager evaluations and syncs between
@@ -118,6 +120,9 @@ def test_generic_option_paths_replay(golden, over):
             rep = _np(cap.replay())
             for k in "efsm":
                 scale = max(np.max(np.abs(eager[k])), 1e-30)
-                assert np.max(np.abs(rep[k] - eager[k])) <= 1e-6 * scale + 1e-9, (r, k)
+                # forces: 1e-7 eV/A absolute as well (C1's vanish by symmetry, so both are
+                # rounding noise of ~1e-9 that the unordered scatters place differently)
+                floor = 1e-7 if k == "f" else 1e-9
+                assert np.max(np.abs(rep[k] - eager[k])) <= 1e-6 * scale + floor, (r, k)
             torch.cuda.synchronize()
             model(graphs, task="efsm")
